@@ -1,0 +1,172 @@
+/*
+ * uor_fbs.h - C ABI of the MI355X (gfx950) SpiralCore/FBS integer decode path.
+ *
+ * This is the drop-in boundary for UOR-R4's `lut-stack` FBS step
+ * (`IntegerStackSession::step_native`, crates/uor-r4-integer/src/stack/session.rs:4129-4403)
+ * and for the GPU evaluator that the reference drives through `#[repr(C)]` structs and
+ * `extern "C"` entry points (docs/labs/d11-exporter-float-trunk/instrument/src/lib.rs:14-95,
+ * host_kernel.cpp:8-49, evaluator.cu:8-34, device.rs:93-302).
+ *
+ * Plain C: fixed-width integers, raw pointers and sizes, no C++ or torch types. The host
+ * keeps its own artifact loader (`IntegerStackModel::parse`) and hands the parsed integer
+ * arrays over as a `uor_fbs_model` whose layout equals the reference's `CModel` /
+ * `fbs_model` byte for byte, so an existing binding passes the same struct.
+ *
+ * Ownership: `uor_fbs_model_create` copies every table to the device; the caller may free
+ * its arrays afterwards. Host-buffer entry points copy in and out and synchronise; the
+ * `_async` entry points take device pointers and a HIP stream (as `void *`) and return once
+ * the work is queued. A handle is not thread-safe; separate handles are.
+ *
+ * Status codes: 0 ok, 1 a token outside the vocabulary, 2 a sequence longer than the
+ * context (fbs_core.h:625-628, mapped in lib.rs:269-274); the rest are this library's.
+ */
+#ifndef UOR_FBS_H
+#define UOR_FBS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define UOR_FBS_ABI_VERSION 1u
+
+#define UOR_FBS_OK 0
+#define UOR_FBS_ERR_TOKEN 1       /* token >= vocab (fbs_core.h:627) */
+#define UOR_FBS_ERR_CONTEXT 2     /* position >= context (fbs_core.h:628) */
+#define UOR_FBS_ERR_ARGUMENT 3    /* a null pointer, a zero or inconsistent size */
+#define UOR_FBS_ERR_SHAPE 4       /* a model the reference's loader would refuse */
+#define UOR_FBS_ERR_DEVICE 5      /* a HIP runtime error */
+#define UOR_FBS_ERR_UNSUPPORTED 6 /* a shape this build has no kernel for */
+
+/* One FBS projection (fbs_core.h:43-47, lib.rs:14-21): per output 8-block the input atom and
+ * eight signed-axis codes (`code & 7` the source lane, `code & 8` negate). */
+typedef struct uor_fbs_map {
+  const uint16_t *atoms; /* blocks */
+  const uint8_t *codes;  /* blocks * 8 */
+  uint32_t blocks;
+} uor_fbs_map;
+
+/* One recurrence layer (fbs_core.h:49-57, lib.rs:23-39). */
+typedef struct uor_fbs_layer {
+  const int16_t *rec_gain; /* width grid codes */
+  const int16_t *mlp_gain; /* width grid codes */
+  uor_fbs_map rec_in;      /* width/8 atoms -> 2*width/8 blocks: drive, then output gate */
+  uor_fbs_map rec_gate;    /* width/8 atoms -> (width/4 + width)/8 blocks: decays, rotations */
+  uor_fbs_map rec_out;     /* width/8 atoms -> width/8 blocks */
+  uor_fbs_map mlp_gate;    /* width/8 atoms -> mlp/8 blocks */
+  uor_fbs_map mlp_up;      /* width/8 atoms -> mlp/8 blocks */
+  uor_fbs_map mlp_down;    /* mlp/8 atoms -> width/8 blocks */
+  const int16_t *taps;     /* 4 * width grid codes [tap][channel], tap s = s positions back */
+  const int32_t *conv_bias;    /* width, exponent -16 */
+  const int32_t *gate_bias;    /* width/4 + width, exponent -16 */
+  const int32_t *decay_offset; /* width/4, Q16 */
+} uor_fbs_layer;
+
+/* The model (fbs_core.h:59-73, lib.rs:41-63; filled from `FbsImage`, session.rs:377-446). */
+typedef struct uor_fbs_model {
+  uint32_t vocab, width, mlp, context, kept, layer_count;
+  int64_t eps_mantissa; /* RMSNorm epsilon = eps_mantissa * 2^eps_exp */
+  int32_t eps_exp;
+  const uor_fbs_layer *layers;
+  const int16_t *final_gain;   /* width grid codes */
+  const int16_t *writer_table; /* vocab * width, Q12: input embedding and writer rows */
+  const int32_t *roots_q12;    /* 16 * 8: the Cl(0,6) orbit roots times 4096 */
+  const int8_t *icosian;       /* 120 * 4 * 2: (a + b phi)/2 coefficient pairs */
+  const uint64_t *keep_q31;    /* 16: isqrt(2^62 - 2^(60 - 2 i)) */
+  uint32_t raw_gates;          /* nonzero: Hamilton gates served as unit quaternions */
+  uint32_t raw_transition;     /* nonzero: transition served as lambda * unit quaternion */
+} uor_fbs_model;
+
+/* Extensions beyond the reference's loader limits (no counterpart in the reference). Every
+ * zero/NULL field selects the reference's own rule, so `ext == NULL` is the reference model:
+ *   window 0     -> 3 prior drive rows (CONVOLUTION_WIDTH 4, session.rs:85)
+ *   drawers 0    -> 256 root-pair cells a*16+b scored by the query's first/last 8-blocks
+ *   probes 0     -> model.kept cells kept per position
+ *   keys NULL    -> key of drawer c = (roots_q12[c >> 4], roots_q12[c & 15]) (drawers 256)
+ *   offsets NULL -> drawer of token t = t mod drawers, members ascending
+ *   table_i8 NULL-> the i16 writer table; else row values are (code << table_shift) at Q12
+ *   head 0       -> native writer; 1 -> whole-table L1 nearest (session.rs:4418-4445)     */
+typedef struct uor_fbs_ext {
+  uint32_t window;                 /* W prior rows of the causal window, 1..64 */
+  uint32_t drawers;                /* D drawers, 1..4096 */
+  uint32_t probes;                 /* P drawers kept per position, 1..min(D, 64) */
+  uint32_t head;                   /* 0 writer, 1 nearest */
+  const int16_t *const *wide_taps; /* per layer (W+1)*width grid codes [tap][channel] */
+  const int32_t *drawer_keys;      /* D * 16 Q12 values: first-block key, last-block key */
+  const uint32_t *drawer_offsets;  /* D + 1 CSR offsets into drawer_members */
+  const uint32_t *drawer_members;  /* vocab token ids, each drawer's ascending */
+  const int8_t *table_i8;          /* vocab * width codes */
+  uint32_t table_shift;            /* 0..8 */
+  uint32_t reserved;
+} uor_fbs_ext;
+
+typedef struct uor_fbs_handle uor_fbs_handle;
+
+/* ABI checks, as fbs_host_sizeof_model / fbs_host_sizeof_layer (host_kernel.cpp:8-9). */
+uint32_t uor_fbs_abi_version(void);
+int64_t uor_fbs_sizeof_model(void);
+int64_t uor_fbs_sizeof_layer(void);
+int64_t uor_fbs_sizeof_ext(void);
+
+/* The message of this thread's last failed call ("" if none). */
+const char *uor_fbs_last_error(void);
+
+/* Validate the model (the FBS rules of StackShape::validate, format.rs:616-752, and the route
+ * and grid-code checks of fbs_model, session.rs:640-735), upload it to HIP device `device`
+ * and prepare its lane tables. Replaces DeviceEvaluator::new (device.rs:93-170). */
+int uor_fbs_model_create(const uor_fbs_model *model, const uor_fbs_ext *ext, int32_t device,
+                         uor_fbs_handle **out);
+void uor_fbs_model_destroy(uor_fbs_handle *handle);
+
+/* Per-sequence state sizes for export/import: `state_words` int64 recurrence values
+ * ([layer][width], exponent -32) and `history_words` int32 drive values
+ * ([layer][window][width], row 0 the newest), as `LayerState::Recurrence` (session.rs:1850). */
+uint64_t uor_fbs_state_words(const uor_fbs_handle *handle);
+uint64_t uor_fbs_history_words(const uor_fbs_handle *handle);
+
+/* Teacher-forced sequences from fresh sessions: every position's chosen token, kept drawers
+ * (best first) and Q12 query. Same contract as fbs_host_sequences (host_kernel.cpp:16-29)
+ * and fbs_eval_sequences (evaluator.cu:8-19): outputs S*len, S*len*probes, S*len*width.
+ * Host buffers. Returns the first nonzero sequence status. */
+int uor_fbs_sequences(uor_fbs_handle *handle, const uint32_t *tokens, uint32_t sequences,
+                      uint32_t len, uint32_t *out_tokens, uint32_t *out_kept, int32_t *out_query);
+/* The same on device buffers; `status` holds one int32 per sequence. */
+int uor_fbs_sequences_async(uor_fbs_handle *handle, const uint32_t *tokens, uint32_t sequences,
+                            uint32_t len, uint32_t *out_tokens, uint32_t *out_kept,
+                            int32_t *out_query, int32_t *status, void *stream);
+
+/* Batched greedy decode, the fbs-toks run (fbs-toks.rs:1513-1533) for many sequences: each
+ * sequence steps its `prompt_len` prompt tokens, then `gen` more, each fed the previous
+ * choice. `out_reply` gets gen+1 tokens per sequence: the prompt's last choice, then every
+ * generated choice. Optional state: `in_*` resume a sequence (NULL = fresh session at
+ * position 0), `out_*` export it after the last step (NULL = not wanted). Host buffers. */
+int uor_fbs_decode(uor_fbs_handle *handle, const uint32_t *prompts, uint32_t sequences,
+                   uint32_t prompt_len, uint32_t gen, uint32_t *out_reply,
+                   const int64_t *in_state, const int32_t *in_history,
+                   const uint32_t *in_position, int64_t *out_state, int32_t *out_history,
+                   uint32_t *out_position);
+/* The same on device buffers; `status` holds one int32 per sequence. */
+int uor_fbs_decode_async(uor_fbs_handle *handle, const uint32_t *prompts, uint32_t sequences,
+                         uint32_t prompt_len, uint32_t gen, uint32_t *out_reply,
+                         const int64_t *in_state, const int32_t *in_history,
+                         const uint32_t *in_position, int64_t *out_state,
+                         int32_t *out_history, uint32_t *out_position, int32_t *status,
+                         void *stream);
+
+/* Teacher-forced next-token scoring: for each row of `len` tokens, position t's choice is
+ * compared with row[t+1] (t < len-1); `out_matches` gets the total count of equal pairs.
+ * `out_argmin` (nullable) gets every position's choice, rows*len. Host buffers. */
+int uor_fbs_score(uor_fbs_handle *handle, const uint32_t *rows, uint64_t n_rows, uint32_t len,
+                  uint32_t *out_argmin, uint64_t *out_matches);
+/* The same on device buffers: `matches` is one uint64 the kernel adds into (the caller
+ * zeroes it), `status` one int32 per row. */
+int uor_fbs_score_async(uor_fbs_handle *handle, const uint32_t *rows, uint64_t n_rows,
+                        uint32_t len, uint32_t *out_argmin, uint64_t *matches,
+                        int32_t *status, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* UOR_FBS_H */

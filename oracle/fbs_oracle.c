@@ -1,0 +1,812 @@
+/*
+ * fbs_oracle.c - CPU restatement of UOR-R4's SpiralCore/FBS integer step (TEST INFRASTRUCTURE:
+ * the parity checker and timed CPU baseline; never linked into the product).
+ *
+ * Reference lines are cited per function: RS = crates/uor-r4-integer/src/, TW =
+ * docs/labs/d11-exporter-float-trunk/instrument/src/fbs_core.h (the reference's own C++ twin,
+ * held equal to the Rust session by its tests/parity.rs). Every product is formed modulo 2^64
+ * or 2^128 exactly as the reference's wrapping products; no floating point anywhere.
+ */
+#include "fbs_oracle.h"
+
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+typedef __int128 i128;
+typedef unsigned __int128 u128;
+
+enum {
+  RESIDUAL_EXP = -16,   /* RS stack/kernels.rs:34 */
+  PRODUCT_EXP = -32,    /* RS stack/kernels.rs:37 */
+  STATE_EXP = -32,      /* RS stack/session.rs:72 */
+  NORM_FINE_EXP = -24,  /* RS stack/kernels.rs:566 */
+  Q12_EXP = -12,        /* RS stack/session.rs:475 */
+  GRID_EXP_BIAS = 64,   /* RS stack/kernels.rs:39 */
+  CELLS = 256,          /* session.rs:4069-4121: 16 x 16 root-pair cells */
+  NEAREST_BLOCK = 16    /* RS stack/session.rs:4412 */
+};
+#define PHI_LO 2654435769ull          /* PHI_Q32 - 2^32, RS stack/mod.rs:167 */
+#define ROTATION_EPSILON 4295ull      /* RS stack/session.rs:141 */
+#define GATE_EPSILON 0ull             /* RS stack/session.rs:144 */
+
+/* ------------------------------------------------------------------------------------------
+ * Scalar conventions (RS stack/kernels.rs:41-135, TW 131-220). */
+
+static int64_t sat_add64(int64_t a, int64_t b) {
+  int64_t r;
+  if (__builtin_add_overflow(a, b, &r)) return b > 0 ? INT64_MAX : INT64_MIN;
+  return r;
+}
+static int64_t sat_neg64(int64_t v) { return v == INT64_MIN ? INT64_MAX : -v; }
+static int32_t sat_add32(int32_t a, int32_t b) {
+  int64_t s = (int64_t)a + b;
+  return s > INT32_MAX ? INT32_MAX : s < INT32_MIN ? INT32_MIN : (int32_t)s;
+}
+static int64_t wadd64(int64_t a, int64_t b) { return (int64_t)((uint64_t)a + (uint64_t)b); }
+static i128 wadd128(i128 a, i128 b) { return (i128)((u128)a + (u128)b); }
+static i128 wsub128(i128 a, i128 b) { return (i128)((u128)a - (u128)b); }
+static i128 wmul128(i128 a, i128 b) { return (i128)((u128)a * (u128)b); }
+static uint64_t uabs64(int64_t v) { return v < 0 ? 0ull - (uint64_t)v : (uint64_t)v; }
+static int bitlen64(uint64_t v) { return v ? 64 - __builtin_clzll(v) : 0; }
+
+/* `shift`: round-half-up arithmetic shift right by s (left when negative), saturating to
+ * the i64 range (RS stack/kernels.rs:41-62). */
+static int64_t shift(int64_t v, int32_t s) {
+  if (s > 0) {
+    if (s >= 63) return v < 0 ? -1 : 0;
+    return sat_add64(v, (int64_t)1 << (s - 1)) >> s;
+  }
+  if (s < 0) {
+    uint32_t k = (uint32_t)(-(int64_t)s);
+    if (k > 63) k = 63;
+    int64_t limit = INT64_MAX >> k;
+    if (v > limit) return INT64_MAX;
+    if (v < -limit) return INT64_MIN;
+    return (int64_t)((uint64_t)v << k);
+  }
+  return v;
+}
+
+/* `shift_wide`: round-half-up shift of an i128, clamped to i64 (RS stack/kernels.rs:64-74). */
+static int64_t shift_wide(i128 v, uint32_t s) {
+  i128 r = s == 0 ? v : wadd128(v, (i128)1 << (s - 1)) >> s;
+  if (r > (i128)INT64_MAX) return INT64_MAX;
+  if (r < (i128)INT64_MIN) return INT64_MIN;
+  return (int64_t)r;
+}
+
+/* `to_exp_i32` (RS stack/kernels.rs:76-80). */
+static int32_t to_exp_i32(int64_t v, int32_t from, int32_t to) {
+  int64_t s = shift(v, to - from);
+  return s > INT32_MAX ? INT32_MAX : s < INT32_MIN ? INT32_MIN : (int32_t)s;
+}
+
+/* `grid_apply`: v * (16 + (|c| & 15)) * 2^((|c| >> 4) - 68), rounded half up, sign of c;
+ * the product (16 + m) v wraps modulo 2^64 like `scale_16_plus` (RS stack/kernels.rs:95-135). */
+static int64_t grid_apply(int64_t v, int16_t code) {
+  if (code == 0) return 0;
+  uint32_t c = code < 0 ? (uint32_t)(-(int32_t)code) : (uint32_t)code;
+  int32_t e = (int32_t)(c >> 4) - GRID_EXP_BIAS;
+  int64_t scaled = (int64_t)((uint64_t)v * (uint64_t)(16 + (c & 15)));
+  scaled = shift(scaled, 4 - e);
+  return code < 0 ? sat_neg64(scaled) : scaled;
+}
+
+/* Floor square root of a u128, digit by digit (RS stack/kernels.rs:408-430). */
+static u128 isqrt128(u128 v) {
+  if (v == 0) return 0;
+  int top = 127 - (int)((uint64_t)(v >> 64) ? __builtin_clzll((uint64_t)(v >> 64))
+                                           : 64 + __builtin_clzll((uint64_t)v));
+  u128 bit = (u128)1 << (top & ~1), rem = v, root = 0;
+  while (bit) {
+    if (rem >= root + bit) {
+      rem -= root + bit;
+      root = (root >> 1) + bit;
+    } else {
+      root >>= 1;
+    }
+    bit >>= 2;
+  }
+  return root;
+}
+
+/* Floor division, zero for a zero divisor (RS stack/kernels.rs:345-360). */
+static u128 div128(u128 n, u128 d) { return d == 0 ? 0 : n / d; }
+
+/* ------------------------------------------------------------------------------------------
+ * Vector kernels. */
+
+/* `stack_quantize16`: shared-exponent requantize to +-32767 (RS stack/kernels.rs:545-553,
+ * TW 275-290). Returns the new exponent. */
+static int32_t quantize16(const int64_t *v, uint32_t n, int32_t exp, int16_t *out) {
+  uint64_t max = 0;
+  for (uint32_t i = 0; i < n; i++) {
+    uint64_t a = uabs64(v[i]);
+    if (a > max) max = a;
+  }
+  int32_t s = bitlen64(max) - 15;
+  if (s < 0) s = 0;
+  for (uint32_t i = 0; i < n; i++) {
+    int64_t y = shift(v[i], s);
+    out[i] = (int16_t)(y > 32767 ? 32767 : y < -32767 ? -32767 : y);
+  }
+  return exp + s;
+}
+
+/* `stack_rms_norm_fine` = `rms_norm_into(.., 38, true)`: x / rms(x) at 2^-24, rounded
+ * (RS stack/kernels.rs:569-620, TW 294-330). */
+static void rms_norm_fine(const int32_t *x, uint32_t n, int64_t eps_m, int32_t eps_e,
+                          int64_t *out) {
+  uint32_t max = 0;
+  for (uint32_t i = 0; i < n; i++) {
+    uint32_t a = x[i] < 0 ? 0u - (uint32_t)x[i] : (uint32_t)x[i];
+    if (a > max) max = a;
+  }
+  int32_t sh = bitlen64(max) - 24;
+  if (sh < 0) sh = 0;
+  uint64_t sum = 0;
+  for (uint32_t i = 0; i < n; i++) {
+    int64_t y = shift((int64_t)x[i], sh);
+    out[i] = y;
+    sum += uabs64(y) * uabs64(y);
+  }
+  int64_t mean = (int64_t)(sum / (n ? n : 1));
+  int32_t square_exp = (RESIDUAL_EXP + sh) * 2;
+  int64_t eps_int = shift(eps_m, square_exp - eps_e);
+  if (eps_int < 0) eps_int = 0;
+  int64_t ms = wadd64(mean, eps_int);
+  if (ms < 1) ms = 1;
+  u128 s = isqrt128((u128)(uint64_t)ms << 68);
+  if (s < 1) s = 1;
+  u128 r = div128((u128)1 << 96, s);
+  for (uint32_t i = 0; i < n; i++) {
+    u128 mag = r * (u128)uabs64(out[i]);
+    i128 p = out[i] < 0 ? (i128)(0 - mag) : (i128)mag;
+    i128 y = wadd128(p, (i128)1 << 37) >> 38;
+    out[i] = y > (i128)INT64_MAX ? INT64_MAX : y < (i128)INT64_MIN ? INT64_MIN : (int64_t)y;
+  }
+}
+
+/* `stack_fbs_gather`: block o of the output takes atom atoms[o]'s 8 values, lane code & 7,
+ * negated (saturating) under code & 8, converted from x_exp to -16
+ * (RS stack/session.rs:4033-4053, TW 337-360). */
+static void gather64(const uor_fbs_map *map, const int64_t *x, int32_t x_exp, int32_t *out) {
+  for (uint32_t o = 0; o < map->blocks; o++) {
+    const int64_t *atom = x + 8u * map->atoms[o];
+    for (uint32_t j = 0; j < 8; j++) {
+      uint8_t code = map->codes[8u * o + j];
+      int64_t v = atom[code & 7];
+      if (code & 8) v = sat_neg64(v);
+      out[8u * o + j] = to_exp_i32(v, x_exp, RESIDUAL_EXP);
+    }
+  }
+}
+static void gather16(const uor_fbs_map *map, const int16_t *x, int32_t x_exp, int32_t *out) {
+  for (uint32_t o = 0; o < map->blocks; o++) {
+    const int16_t *atom = x + 8u * map->atoms[o];
+    for (uint32_t j = 0; j < 8; j++) {
+      uint8_t code = map->codes[8u * o + j];
+      int64_t v = atom[code & 7];
+      if (code & 8) v = sat_neg64(v);
+      out[8u * o + j] = to_exp_i32(v, x_exp, RESIDUAL_EXP);
+    }
+  }
+}
+
+/* Hamilton product a (x) b modulo 2^128 (RS stack/kernels.rs:998-1030, TW 363-370). */
+static void hamilton(const int64_t a[4], const int64_t b[4], i128 o[4]) {
+  i128 p[4][4];
+  for (int i = 0; i < 4; i++)
+    for (int j = 0; j < 4; j++) p[i][j] = wmul128((i128)a[i], (i128)b[j]);
+  o[0] = wsub128(wsub128(wsub128(p[0][0], p[1][1]), p[2][2]), p[3][3]);
+  o[1] = wsub128(wadd128(wadd128(p[0][1], p[1][0]), p[2][3]), p[3][2]);
+  o[2] = wadd128(wadd128(wsub128(p[0][2], p[1][3]), p[2][0]), p[3][1]);
+  o[3] = wadd128(wsub128(wadd128(p[0][3], p[1][2]), p[2][1]), p[3][0]);
+}
+
+/* Sign of da + db phi, exactly: 2(da + db phi) = P + db sqrt5 with P = 2 da + db, decided by
+ * P and by P^2 against 5 db^2 (RS stack/kernels.rs:1180-1215, TW 393-408). */
+static int diff_positive(int64_t da, int64_t db) {
+  i128 p = (i128)da * 2 + db;
+  if (db == 0) return p > 0;
+  u128 b2 = (u128)uabs64(db) * uabs64(db) * 5;
+  u128 p2 = (u128)(p < 0 ? -p : p) * (u128)(p < 0 ? -p : p);
+  if (db > 0) return p >= 0 || b2 > p2;
+  return p > 0 && p2 > b2;
+}
+
+/* The icosian root with the largest exact dot product with raw, lowest index on ties: the
+ * 120-root scan that `stack_snap_select`'s candidate tables reproduce
+ * (RS stack/kernels.rs:1420-1474, TW 410-430). Root coordinate c is (a + b phi)/2. */
+static uint32_t snap_select(const int8_t *ico, const int32_t raw[4]) {
+  uint32_t best = 0;
+  int64_t best_a = 0, best_b = 0;
+  for (uint32_t r = 0; r < 120; r++) {
+    int64_t a = 0, b = 0;
+    for (int c = 0; c < 4; c++) {
+      a += (int64_t)raw[c] * ico[8 * r + 2 * c];
+      b += (int64_t)raw[c] * ico[8 * r + 2 * c + 1];
+    }
+    if (r == 0 || diff_positive(a - best_a, b - best_b)) {
+      best = r;
+      best_a = a;
+      best_b = b;
+    }
+  }
+  return best;
+}
+
+/* `stack_snap_rotation`: the chosen root times lambda at Q31, lambda phi rounded at Q31
+ * (RS stack/kernels.rs:1530-1557, TW 435-445). */
+static void snap_rotation(const int8_t *ico, const int32_t raw[4], uint64_t lambda, int64_t o[4]) {
+  uint32_t r = snap_select(ico, raw);
+  uint64_t lambda_phi = lambda + ((lambda * PHI_LO + (1ull << 31)) >> 32);
+  for (int c = 0; c < 4; c++) {
+    int64_t sum = (int64_t)(lambda * (uint64_t)(int64_t)ico[8 * r + 2 * c] +
+                            lambda_phi * (uint64_t)(int64_t)ico[8 * r + 2 * c + 1]);
+    o[c] = shift(sum, 1);
+  }
+}
+
+/* `stack_rotation`: lambda raw/|raw| at Q31; the unit at Q30 by floor division of magnitudes,
+ * signed, then (lambda unit) >> 30 (RS stack/session.rs:5165-5181, TW 459-474). */
+static void rotation(const int32_t raw[4], uint64_t lambda, uint64_t eps, int64_t o[4]) {
+  u128 square = 0;
+  for (int c = 0; c < 4; c++) square += (u128)((int64_t)raw[c] * raw[c]);
+  u128 norm = isqrt128((square + eps) << 32);
+  for (int c = 0; c < 4; c++) {
+    int64_t v = raw[c];
+    i128 mag = (i128)div128((u128)uabs64(v) << 46, norm);
+    i128 unit = v < 0 ? -mag : mag;
+    o[c] = (int64_t)(wmul128((i128)lambda, unit) >> 30);
+  }
+}
+
+static void serve_rotation(const int8_t *ico, uint32_t raw_form, const int32_t raw[4],
+                           uint64_t lambda, uint64_t eps, int64_t o[4]) {
+  if (raw_form)
+    rotation(raw, lambda, eps, o);
+  else
+    snap_rotation(ico, raw, lambda, o);
+}
+
+/* ------------------------------------------------------------------------------------------
+ * The resolved model: the reference image plus the extension's choices. */
+
+typedef struct {
+  const uor_fbs_model *m;
+  uint32_t d, mlp, lanes, g, L, W, D, P, head;
+  int reference_writer; /* 256 root-pair cells, t mod 256, no keys: session.rs:4069-4121 */
+  const int16_t *const *wide_taps;
+  const int32_t *keys;
+  const uint32_t *offsets, *members;
+  const int8_t *t8;
+  uint32_t t8_shift;
+} O;
+
+static void resolve(O *o, const uor_fbs_model *m, const uor_fbs_ext *e) {
+  memset(o, 0, sizeof *o);
+  o->m = m;
+  o->d = m->width;
+  o->mlp = m->mlp;
+  o->lanes = m->width / 4;
+  o->g = o->lanes + m->width;
+  o->L = m->layer_count;
+  o->W = (e && e->window) ? e->window : 3;
+  o->D = (e && e->drawers) ? e->drawers : CELLS;
+  o->P = (e && e->probes) ? e->probes : m->kept;
+  o->head = e ? e->head : 0;
+  o->wide_taps = e ? e->wide_taps : NULL;
+  o->keys = e ? e->drawer_keys : NULL;
+  o->offsets = e ? e->drawer_offsets : NULL;
+  o->members = e ? e->drawer_members : NULL;
+  o->t8 = e ? e->table_i8 : NULL;
+  o->t8_shift = e ? e->table_shift : 0;
+  o->reference_writer = o->D == CELLS && !o->keys && !o->offsets;
+}
+
+/* Writer-table value of token t, channel i, at Q12 (the i16 table, or code << shift). */
+static int32_t row_value(const O *o, uint32_t t, uint32_t i) {
+  uint64_t at = (uint64_t)t * o->d + i;
+  if (o->t8) return (int32_t)((uint32_t)(int32_t)o->t8[at] << o->t8_shift);
+  return o->m->writer_table[at];
+}
+
+static int16_t tap(const O *o, uint32_t l, uint32_t s, uint32_t i) {
+  if (o->wide_taps) return o->wide_taps[l][(uint64_t)s * o->d + i];
+  return o->m->layers[l].taps[(uint64_t)s * o->d + i];
+}
+
+static uint64_t row_l1(const O *o, const int32_t *q, uint32_t t) {
+  uint64_t sum = 0;
+  for (uint32_t i = 0; i < o->d; i++) {
+    int64_t diff = (int64_t)q[i] - row_value(o, t, i);
+    sum += (uint64_t)(diff < 0 ? -diff : diff);
+  }
+  return sum;
+}
+
+/* The native vector writer exactly as the reference states it (RS stack/session.rs:4069-4121,
+ * TW 580-623): ports, 256 cells, kept rounds of first-max, candidates kept + 256 j. */
+static uint32_t writer_reference(const O *o, const int32_t *q, uint32_t *kept, uint64_t *cand) {
+  const uor_fbs_model *m = o->m;
+  int64_t pa[16], pb[16], cells[CELLS];
+  for (int r = 0; r < 16; r++) {
+    int64_t sa = 0, sb = 0;
+    for (int i = 0; i < 8; i++) {
+      int64_t da = (int64_t)q[i] - m->roots_q12[8 * r + i];
+      int64_t db = (int64_t)q[o->d - 8 + i] - m->roots_q12[8 * r + i];
+      sa += da < 0 ? -da : da;
+      sb += db < 0 ? -db : db;
+    }
+    pa[r] = -sa;
+    pb[r] = -sb;
+  }
+  for (int c = 0; c < CELLS; c++) cells[c] = wadd64(pa[c >> 4], pb[c & 15]);
+  for (uint32_t k = 0; k < o->P; k++) {
+    int best = 0;
+    for (int c = 1; c < CELLS; c++)
+      if (cells[c] > cells[best]) best = c;
+    kept[k] = (uint32_t)best;
+    cells[best] = INT64_MIN;
+  }
+  uint32_t token = UINT32_MAX;
+  int64_t token_score = INT64_MIN;
+  for (uint32_t k = 0; k < o->P; k++) {
+    for (uint32_t t = kept[k]; t < m->vocab; t += CELLS) {
+      int64_t score = -(int64_t)row_l1(o, q, t);
+      if (cand) (*cand)++;
+      if (score > token_score || (score == token_score && t < token)) {
+        token = t;
+        token_score = score;
+      }
+    }
+  }
+  return token;
+}
+
+/* The writer over D keyed drawers (extension; reduces to writer_reference for the 256
+ * root-pair keys and t mod 256 membership): drawer score -(L1(q[0..8], keyA) +
+ * L1(q[d-8..d], keyB)); P rounds of first-max (ties to the lower drawer); the lexicographic
+ * minimum (L1, id) over the kept drawers' members. */
+static uint32_t writer_drawers(const O *o, const int32_t *q, uint32_t *kept, uint64_t *cand) {
+  const uor_fbs_model *m = o->m;
+  int64_t *score = (int64_t *)malloc(sizeof(int64_t) * o->D);
+  for (uint32_t c = 0; c < o->D; c++) {
+    int32_t ka[8], kb[8];
+    for (int i = 0; i < 8; i++) {
+      if (o->keys) {
+        ka[i] = o->keys[16ull * c + i];
+        kb[i] = o->keys[16ull * c + 8 + i];
+      } else { /* root pairs: only valid for D = 256 (checked by the caller's image) */
+        ka[i] = m->roots_q12[8 * (c >> 4) + i];
+        kb[i] = m->roots_q12[8 * (c & 15) + i];
+      }
+    }
+    int64_t s = 0;
+    for (int i = 0; i < 8; i++) {
+      int64_t da = (int64_t)q[i] - ka[i], db = (int64_t)q[o->d - 8 + i] - kb[i];
+      s += (da < 0 ? -da : da) + (db < 0 ? -db : db);
+    }
+    score[c] = -s;
+  }
+  for (uint32_t k = 0; k < o->P; k++) {
+    uint32_t best = 0;
+    for (uint32_t c = 1; c < o->D; c++)
+      if (score[c] > score[best]) best = c;
+    kept[k] = best;
+    score[best] = INT64_MIN;
+  }
+  free(score);
+  uint32_t token = UINT32_MAX;
+  uint64_t best_l1 = UINT64_MAX;
+  for (uint32_t k = 0; k < o->P; k++) {
+    uint32_t c = kept[k];
+    if (o->offsets) {
+      for (uint32_t j = o->offsets[c]; j < o->offsets[c + 1]; j++) {
+        uint32_t t = o->members[j];
+        uint64_t l1 = row_l1(o, q, t);
+        if (cand) (*cand)++;
+        if (l1 < best_l1 || (l1 == best_l1 && t < token)) {
+          token = t;
+          best_l1 = l1;
+        }
+      }
+    } else {
+      for (uint32_t t = c; t < m->vocab; t += o->D) {
+        uint64_t l1 = row_l1(o, q, t);
+        if (cand) (*cand)++;
+        if (l1 < best_l1 || (l1 == best_l1 && t < token)) {
+          token = t;
+          best_l1 = l1;
+        }
+      }
+    }
+  }
+  return token;
+}
+
+/* `stack_whole_table_nearest`: L1 argmin over every row, a row left as soon as its partial
+ * sum passes the best after a 16-value block, ties to the smaller id
+ * (RS stack/session.rs:4418-4445). */
+static uint32_t writer_nearest(const O *o, const int32_t *q, uint64_t *cand) {
+  uint32_t token = UINT32_MAX;
+  int64_t best = INT64_MAX;
+  for (uint32_t t = 0; t < o->m->vocab; t++) {
+    int64_t sum = 0;
+    int whole = 1;
+    for (uint32_t i0 = 0; i0 < o->d; i0 += NEAREST_BLOCK) {
+      for (uint32_t i = i0; i < i0 + NEAREST_BLOCK && i < o->d; i++) {
+        int64_t diff = (int64_t)q[i] - row_value(o, t, i);
+        sum += diff < 0 ? -diff : diff;
+      }
+      if (sum > best) {
+        whole = 0;
+        break;
+      }
+    }
+    if (cand) (*cand)++;
+    if (whole && sum < best) {
+      token = t;
+      best = sum;
+    }
+  }
+  return token;
+}
+
+static uint32_t writer(const O *o, const int32_t *q, uint32_t *kept, uint64_t *cand) {
+  if (o->head == 1) {
+    memset(kept, 0, sizeof(uint32_t) * o->P); /* session.rs:4372: no cells kept */
+    return writer_nearest(o, q, cand);
+  }
+  return o->reference_writer ? writer_reference(o, q, kept, cand) : writer_drawers(o, q, kept, cand);
+}
+
+/* ------------------------------------------------------------------------------------------
+ * One sequence's session. */
+
+typedef struct {
+  int32_t *x, *branches, *gate_out, *proj, *gate, *up, *query;
+  int64_t *scratch, *wide;
+  int16_t *act;
+  int64_t *state;   /* L * d */
+  int32_t *history; /* L * W * d, row 0 the newest drive */
+  uint32_t *kept;
+  uint32_t position;
+  uint64_t candidates;
+} S;
+
+static void session_alloc(const O *o, S *s) {
+  uint32_t d = o->d, wide = d > o->mlp ? d : o->mlp;
+  memset(s, 0, sizeof *s);
+  s->x = calloc(d, 4);
+  s->branches = calloc(2 * d, 4);
+  s->gate_out = calloc(o->g, 4);
+  s->proj = calloc(d, 4);
+  s->gate = calloc(o->mlp, 4);
+  s->up = calloc(o->mlp, 4);
+  s->query = calloc(d, 4);
+  s->scratch = calloc(wide, 8);
+  s->wide = calloc(d, 8);
+  s->act = calloc(wide, 2);
+  s->state = calloc((size_t)o->L * d, 8);
+  s->history = calloc((size_t)o->L * o->W * d, 4);
+  s->kept = calloc(o->P ? o->P : 1, 4);
+}
+
+static void session_free(S *s) {
+  free(s->x); free(s->branches); free(s->gate_out); free(s->proj); free(s->gate); free(s->up);
+  free(s->query); free(s->scratch); free(s->wide); free(s->act); free(s->state);
+  free(s->history); free(s->kept);
+}
+
+static void session_reset(const O *o, S *s) {
+  memset(s->state, 0, sizeof(int64_t) * o->L * o->d);
+  memset(s->history, 0, sizeof(int32_t) * o->L * o->W * o->d);
+  s->position = 0;
+}
+
+/* `stack_recurrence_core` with geometric gates, learned rotations and the Hamilton output
+ * gate (RS stack/session.rs:4822-4982, `stack_lanes` :5097-5145, `stack_lane_weights`
+ * :4989-5026; TW 508-561). The causal window reads W prior drive rows (reference W = 3,
+ * `CONVOLUTION_WIDTH` = 4 taps, session.rs:85). Returns the exponent of s->act[..d]. */
+static int32_t recurrence(const O *o, uint32_t l, int64_t *state, int32_t *hist, S *s) {
+  const uor_fbs_model *m = o->m;
+  const uor_fbs_layer *ly = m->layers + l;
+  uint32_t d = o->d, W = o->W;
+  for (uint32_t i = 0; i < o->g; i++) s->gate_out[i] = sat_add32(s->gate_out[i], ly->gate_bias[i]);
+  const int32_t *drive = s->branches, *gate = s->branches + d;
+  for (uint32_t i = 0; i < d; i++) {
+    int64_t c = wadd64(ly->conv_bias[i], grid_apply(drive[i], tap(o, l, 0, i)));
+    for (uint32_t k = 1; k <= W; k++)
+      c = wadd64(c, grid_apply(hist[(uint64_t)(k - 1) * d + i], tap(o, l, k, i)));
+    s->wide[i] = c;
+  }
+  /* Age the history: the oldest row drops off, the drive becomes row 0. */
+  memmove(hist + d, hist, sizeof(int32_t) * (uint64_t)(W - 1) * d);
+  memcpy(hist, drive, sizeof(int32_t) * d);
+  const int32_t *decays = s->gate_out, *rot = s->gate_out + o->lanes;
+  for (uint32_t lane = 0; lane < o->lanes; lane++) {
+    int32_t sq = sat_add32(decays[lane], ly->decay_offset[lane]);
+    if (sq < 0) sq = 0;
+    if (sq > 65536) sq = 65536;
+    uint32_t idx = (uint32_t)sq >> 12;
+    if (idx > 15) idx = 15;
+    uint64_t lambda = 1ull << (30 - idx), keep = m->keep_q31[idx];
+    int64_t t[4];
+    serve_rotation(m->icosian, m->raw_transition, rot + 4 * lane, lambda, ROTATION_EPSILON, t);
+    int64_t *h = state + 4 * lane;
+    int64_t held[4] = {h[0], h[1], h[2], h[3]};
+    i128 moved[4];
+    hamilton(t, held, moved);
+    for (int k = 0; k < 4; k++) {
+      i128 drive_term = wmul128((i128)keep, (i128)s->wide[4 * lane + k]);
+      h[k] = shift_wide(wadd128(moved[k], (i128)((u128)drive_term << 16)), 31);
+    }
+  }
+  for (uint32_t lane = 0; lane < o->lanes; lane++) {
+    int64_t q[4], rhs[4];
+    i128 prod[4];
+    serve_rotation(m->icosian, m->raw_gates, gate + 4 * lane, 1ull << 31, GATE_EPSILON, q);
+    for (int k = 0; k < 4; k++) rhs[k] = shift(state[4 * lane + k], RESIDUAL_EXP - STATE_EXP);
+    hamilton(q, rhs, prod);
+    for (int k = 0; k < 4; k++) s->scratch[4 * lane + k] = shift_wide(prod[k], 15);
+  }
+  return quantize16(s->scratch, d, PRODUCT_EXP, s->act);
+}
+
+/* The Hamilton branch of `stack_swiglu` (RS stack/session.rs:4005-4025, TW 566-578). */
+static void hamilton_gate(const O *o, const int32_t *gate, const int32_t *up, int64_t *out) {
+  const uor_fbs_model *m = o->m;
+  for (uint32_t j = 0; j < o->mlp / 4; j++) {
+    int64_t q[4], rhs[4];
+    i128 prod[4];
+    serve_rotation(m->icosian, m->raw_gates, gate + 4 * j, 1ull << 31, GATE_EPSILON, q);
+    for (int k = 0; k < 4; k++) rhs[k] = up[4 * j + k];
+    hamilton(q, rhs, prod);
+    for (int k = 0; k < 4; k++) out[4 * j + k] = shift_wide(prod[k], 15);
+  }
+}
+
+/* `stack_step_fbs` without the optional Hamming/address/pair/Q31/memory hooks
+ * (RS stack/session.rs:4129-4403, TW 635-675). */
+static int step(const O *o, S *s, uint32_t token, uint32_t *out_token) {
+  const uor_fbs_model *m = o->m;
+  uint32_t d = o->d;
+  if (token >= m->vocab) return UOR_FBS_ERR_TOKEN;
+  if (s->position >= m->context) return UOR_FBS_ERR_CONTEXT;
+  for (uint32_t i = 0; i < d; i++) s->x[i] = to_exp_i32(row_value(o, token, i), Q12_EXP, RESIDUAL_EXP);
+  for (uint32_t l = 0; l < o->L; l++) {
+    const uor_fbs_layer *ly = m->layers + l;
+    int64_t *state = s->state + (uint64_t)l * d;
+    int32_t *hist = s->history + (uint64_t)l * o->W * d;
+    rms_norm_fine(s->x, d, m->eps_mantissa, m->eps_exp, s->scratch);
+    for (uint32_t i = 0; i < d; i++) s->scratch[i] = grid_apply(s->scratch[i], ly->rec_gain[i]);
+    gather64(&ly->rec_in, s->scratch, NORM_FINE_EXP, s->branches);
+    gather64(&ly->rec_gate, s->scratch, NORM_FINE_EXP, s->gate_out);
+    int32_t act_exp = recurrence(o, l, state, hist, s);
+    gather16(&ly->rec_out, s->act, act_exp, s->proj);
+    for (uint32_t i = 0; i < d; i++) s->x[i] = sat_add32(s->x[i], s->proj[i]);
+    rms_norm_fine(s->x, d, m->eps_mantissa, m->eps_exp, s->scratch);
+    for (uint32_t i = 0; i < d; i++) s->scratch[i] = grid_apply(s->scratch[i], ly->mlp_gain[i]);
+    gather64(&ly->mlp_gate, s->scratch, NORM_FINE_EXP, s->gate);
+    gather64(&ly->mlp_up, s->scratch, NORM_FINE_EXP, s->up);
+    hamilton_gate(o, s->gate, s->up, s->scratch);
+    act_exp = quantize16(s->scratch, o->mlp, PRODUCT_EXP, s->act);
+    gather16(&ly->mlp_down, s->act, act_exp, s->proj);
+    for (uint32_t i = 0; i < d; i++) s->x[i] = sat_add32(s->x[i], s->proj[i]);
+  }
+  rms_norm_fine(s->x, d, m->eps_mantissa, m->eps_exp, s->scratch);
+  for (uint32_t i = 0; i < d; i++) {
+    int32_t q = to_exp_i32(grid_apply(s->scratch[i], m->final_gain[i]), NORM_FINE_EXP, Q12_EXP);
+    s->query[i] = q > 32767 ? 32767 : q < -32768 ? -32768 : q;
+  }
+  *out_token = writer(o, s->query, s->kept, &s->candidates);
+  s->position++;
+  return UOR_FBS_OK;
+}
+
+/* ------------------------------------------------------------------------------------------
+ * Batched drivers: sequence i goes to thread i % T. */
+
+
+typedef struct {
+  const O *o;
+  int kind; /* 0 sequences, 1 decode, 2 score */
+  const uint32_t *tokens;
+  uint64_t n;
+  uint32_t len, prompt_len, gen;
+  uint32_t *out_tokens, *out_kept, *out_reply;
+  int32_t *out_query;
+  const int64_t *in_state;
+  const int32_t *in_history;
+  const uint32_t *in_position;
+  int64_t *out_state;
+  int32_t *out_history;
+  uint32_t *out_position;
+  uint64_t *out_candidates;
+  uint64_t matches;
+  int tid, threads, status;
+} Job;
+
+static void *run_job(void *arg) {
+  Job *j = (Job *)arg;
+  const O *o = j->o;
+  uint32_t d = o->d;
+  uint64_t sw = (uint64_t)o->L * d, hw = (uint64_t)o->L * o->W * d;
+  S s;
+  session_alloc(o, &s);
+  for (uint64_t i = (uint64_t)j->tid; i < j->n && j->status == 0; i += (uint64_t)j->threads) {
+    session_reset(o, &s);
+    s.candidates = 0;
+    if (j->kind != 1) {
+      const uint32_t *row = j->tokens + i * j->len;
+      for (uint32_t t = 0; t < j->len; t++) {
+        uint32_t tok;
+        int err = step(o, &s, row[t], &tok);
+        if (err) {
+          j->status = err;
+          break;
+        }
+        uint64_t at = i * j->len + t;
+        if (j->out_tokens) j->out_tokens[at] = tok;
+        if (j->out_kept) memcpy(j->out_kept + at * o->P, s.kept, 4ull * o->P);
+        if (j->out_query) memcpy(j->out_query + at * d, s.query, 4ull * d);
+        if (j->kind == 2 && t + 1 < j->len && tok == row[t + 1]) j->matches++;
+      }
+      continue;
+    }
+    /* Decode: the fbs-toks run (fbs-toks.rs:1513-1533) from an optional saved state. */
+    if (j->in_state) memcpy(s.state, j->in_state + i * sw, 8 * sw);
+    if (j->in_history) memcpy(s.history, j->in_history + i * hw, 4 * hw);
+    if (j->in_position) s.position = j->in_position[i];
+    const uint32_t *prompt = j->tokens + i * j->prompt_len;
+    uint32_t *reply = j->out_reply + i * ((uint64_t)j->gen + 1);
+    uint32_t next = 0;
+    int err = 0;
+    for (uint32_t t = 0; t < j->prompt_len && !err; t++) err = step(o, &s, prompt[t], &next);
+    if (!err) reply[0] = next;
+    for (uint32_t t = 0; t < j->gen && !err; t++) {
+      err = step(o, &s, next, &next);
+      if (!err) reply[t + 1] = next;
+    }
+    if (err) {
+      j->status = err;
+      break;
+    }
+    if (j->out_state) memcpy(j->out_state + i * sw, s.state, 8 * sw);
+    if (j->out_history) memcpy(j->out_history + i * hw, s.history, 4 * hw);
+    if (j->out_position) j->out_position[i] = s.position;
+    if (j->out_candidates) j->out_candidates[i] = s.candidates;
+  }
+  session_free(&s);
+  return NULL;
+}
+
+static int run_jobs(Job *proto, int threads) {
+  if (threads < 1) threads = 1;
+  if ((uint64_t)threads > proto->n) threads = proto->n ? (int)proto->n : 1;
+  Job *jobs = calloc((size_t)threads, sizeof(Job));
+  pthread_t *ids = calloc((size_t)threads, sizeof(pthread_t));
+  for (int t = 0; t < threads; t++) {
+    jobs[t] = *proto;
+    jobs[t].tid = t;
+    jobs[t].threads = threads;
+  }
+  for (int t = 1; t < threads; t++) pthread_create(&ids[t], NULL, run_job, &jobs[t]);
+  run_job(&jobs[0]);
+  for (int t = 1; t < threads; t++) pthread_join(ids[t], NULL);
+  int status = 0;
+  uint64_t matches = 0;
+  for (int t = 0; t < threads; t++) {
+    if (jobs[t].status && !status) status = jobs[t].status;
+    matches += jobs[t].matches;
+  }
+  proto->matches = matches;
+  free(jobs);
+  free(ids);
+  return status;
+}
+
+int fbs_oracle_sequences(const uor_fbs_model *m, const uor_fbs_ext *ext, const uint32_t *tokens,
+                         uint32_t sequences, uint32_t len, uint32_t *out_tokens,
+                         uint32_t *out_kept, int32_t *out_query, int threads) {
+  O o;
+  resolve(&o, m, ext);
+  Job j = {0};
+  j.o = &o;
+  j.kind = 0;
+  j.tokens = tokens;
+  j.n = sequences;
+  j.len = len;
+  j.out_tokens = out_tokens;
+  j.out_kept = out_kept;
+  j.out_query = out_query;
+  return run_jobs(&j, threads);
+}
+
+int fbs_oracle_decode(const uor_fbs_model *m, const uor_fbs_ext *ext, const uint32_t *prompts,
+                      uint32_t sequences, uint32_t prompt_len, uint32_t gen, uint32_t *out_reply,
+                      const int64_t *in_state, const int32_t *in_history,
+                      const uint32_t *in_position, int64_t *out_state, int32_t *out_history,
+                      uint32_t *out_position, uint64_t *out_candidates, int threads) {
+  O o;
+  resolve(&o, m, ext);
+  Job j = {0};
+  j.o = &o;
+  j.kind = 1;
+  j.tokens = prompts;
+  j.n = sequences;
+  j.prompt_len = prompt_len;
+  j.gen = gen;
+  j.out_reply = out_reply;
+  j.in_state = in_state;
+  j.in_history = in_history;
+  j.in_position = in_position;
+  j.out_state = out_state;
+  j.out_history = out_history;
+  j.out_position = out_position;
+  j.out_candidates = out_candidates;
+  return run_jobs(&j, threads);
+}
+
+int fbs_oracle_score(const uor_fbs_model *m, const uor_fbs_ext *ext, const uint32_t *rows,
+                     uint64_t n_rows, uint32_t len, uint32_t *out_argmin,
+                     uint64_t *out_matches, int threads) {
+  O o;
+  resolve(&o, m, ext);
+  Job j = {0};
+  j.o = &o;
+  j.kind = 2;
+  j.tokens = rows;
+  j.n = n_rows;
+  j.len = len;
+  j.out_tokens = out_argmin;
+  int status = run_jobs(&j, threads);
+  if (out_matches) *out_matches = j.matches;
+  return status;
+}
+
+/* ------------------------------------------------------------------------------------------
+ * Exported scalar routines (for the closed-form tests). */
+
+int64_t fbs_oracle_shift(int64_t v, int32_t s) { return shift(v, s); }
+int64_t fbs_oracle_shift_wide(int64_t hi, uint64_t lo, uint32_t s) {
+  return shift_wide((i128)(((u128)(uint64_t)hi << 64) | lo), s);
+}
+int64_t fbs_oracle_grid_apply(int64_t v, int16_t code) { return grid_apply(v, code); }
+void fbs_oracle_isqrt(uint64_t hi, uint64_t lo, uint64_t out[2]) {
+  u128 r = isqrt128(((u128)hi << 64) | lo);
+  out[0] = (uint64_t)(r >> 64);
+  out[1] = (uint64_t)r;
+}
+void fbs_oracle_div_u128(uint64_t nhi, uint64_t nlo, uint64_t dhi, uint64_t dlo, uint64_t out[2]) {
+  u128 r = div128(((u128)nhi << 64) | nlo, ((u128)dhi << 64) | dlo);
+  out[0] = (uint64_t)(r >> 64);
+  out[1] = (uint64_t)r;
+}
+uint32_t fbs_oracle_snap_select(const int8_t *icosian, const int32_t raw[4]) {
+  return snap_select(icosian, raw);
+}
+int fbs_oracle_diff_positive(int64_t da, int64_t db) { return diff_positive(da, db); }
+void fbs_oracle_serve_rotation(const int8_t *icosian, uint32_t raw_form, const int32_t raw[4],
+                               uint64_t lambda, uint64_t epsilon, int64_t out[4]) {
+  serve_rotation(icosian, raw_form, raw, lambda, epsilon, out);
+}
+int32_t fbs_oracle_quantize16(const int64_t *v, uint32_t n, int32_t exp, int16_t *out) {
+  return quantize16(v, n, exp, out);
+}
+void fbs_oracle_rms_norm_fine(const int32_t *x, uint32_t n, int64_t eps_mantissa, int32_t eps_exp,
+                              int64_t *out) {
+  rms_norm_fine(x, n, eps_mantissa, eps_exp, out);
+}
+uint32_t fbs_oracle_writer(const uor_fbs_model *m, const uor_fbs_ext *ext, const int32_t *query,
+                           uint32_t *kept, uint64_t *candidates) {
+  O o;
+  resolve(&o, m, ext);
+  uint64_t c = 0;
+  uint32_t t = writer(&o, query, kept, &c);
+  if (candidates) *candidates = c;
+  return t;
+}

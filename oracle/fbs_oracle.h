@@ -1,0 +1,75 @@
+/*
+ * fbs_oracle.h - CPU restatement of UOR-R4's SpiralCore/FBS integer step, for tests only.
+ *
+ * TEST INFRASTRUCTURE. This is the parity checker of the HIP path and the CPU baseline that
+ * bench.py times beside it. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg may load it; the product (libuor_fbs_hip.so) never links or calls it.
+ *
+ * It follows the Rust session (crates/uor-r4-integer/src/stack/session.rs,
+ * stack/kernels.rs) and the reference's C++ twin
+ * (docs/labs/d11-exporter-float-trunk/instrument/src/fbs_core.h) function by function; each
+ * function in fbs_oracle.c names the lines it restates. It takes the same model image as the
+ * product (include/uor_fbs.h), including the documented extensions (window W, D drawers with
+ * keys and CSR members, int8 table, nearest head), which reduce to the reference's rules at
+ * their defaults.
+ *
+ * Pinning (what checks each part): tests/test_oracle_golden.py compares every position's
+ * token, kept cells and Q12 query with vectors written by the reference's own twin
+ * (oracle/_ref, tests/golden/); tests/test_oracle_math.py checks the scalar routines against
+ * closed forms and brute force (isqrt, floor division, the 120-root snap as an exact argmax,
+ * rounding shifts, grid codes) and the extensions against their reference reductions.
+ */
+#ifndef FBS_ORACLE_H
+#define FBS_ORACLE_H
+
+#include <stdint.h>
+
+#include "../include/uor_fbs.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Teacher-forced sequences from fresh sessions (fbs_core.h:681-695, host_kernel.cpp:16-29):
+ * per position the token, the kept drawers (probes of them) and the width-long Q12 query.
+ * Sequences are spread over `threads` POSIX threads (<= 0: one). */
+int fbs_oracle_sequences(const uor_fbs_model *m, const uor_fbs_ext *ext, const uint32_t *tokens,
+                         uint32_t sequences, uint32_t len, uint32_t *out_tokens,
+                         uint32_t *out_kept, int32_t *out_query, int threads);
+
+/* Greedy decode (fbs-toks.rs:1513-1533) of many sequences, with optional resume state and
+ * export (layouts as uor_fbs_decode). `out_candidates` (nullable) gets, per sequence, the
+ * number of writer candidate rows scored over all its steps. */
+int fbs_oracle_decode(const uor_fbs_model *m, const uor_fbs_ext *ext, const uint32_t *prompts,
+                      uint32_t sequences, uint32_t prompt_len, uint32_t gen, uint32_t *out_reply,
+                      const int64_t *in_state, const int32_t *in_history,
+                      const uint32_t *in_position, int64_t *out_state, int32_t *out_history,
+                      uint32_t *out_position, uint64_t *out_candidates, int threads);
+
+/* Teacher-forced scoring: matches of position t's choice with row[t+1]. */
+int fbs_oracle_score(const uor_fbs_model *m, const uor_fbs_ext *ext, const uint32_t *rows,
+                     uint64_t n_rows, uint32_t len, uint32_t *out_argmin,
+                     uint64_t *out_matches, int threads);
+
+/* Scalar routines, exported so the tests can check them against closed forms. */
+int64_t fbs_oracle_shift(int64_t v, int32_t s);
+int64_t fbs_oracle_shift_wide(int64_t hi, uint64_t lo, uint32_t s);
+int64_t fbs_oracle_grid_apply(int64_t v, int16_t code);
+void fbs_oracle_isqrt(uint64_t hi, uint64_t lo, uint64_t out[2]);
+void fbs_oracle_div_u128(uint64_t nhi, uint64_t nlo, uint64_t dhi, uint64_t dlo, uint64_t out[2]);
+uint32_t fbs_oracle_snap_select(const int8_t *icosian, const int32_t raw[4]);
+int fbs_oracle_diff_positive(int64_t da, int64_t db);
+void fbs_oracle_serve_rotation(const int8_t *icosian, uint32_t raw_form, const int32_t raw[4],
+                               uint64_t lambda, uint64_t epsilon, int64_t out[4]);
+int32_t fbs_oracle_quantize16(const int64_t *v, uint32_t n, int32_t exp, int16_t *out);
+void fbs_oracle_rms_norm_fine(const int32_t *x, uint32_t n, int64_t eps_mantissa, int32_t eps_exp,
+                              int64_t *out);
+/* Writer on a given query: token, kept (probes of them); `candidates` = rows scored. */
+uint32_t fbs_oracle_writer(const uor_fbs_model *m, const uor_fbs_ext *ext, const int32_t *query,
+                           uint32_t *kept, uint64_t *candidates);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

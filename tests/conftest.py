@@ -1,0 +1,28 @@
+"""Shared test setup: import paths, the `gpu` marker, and the built libraries."""
+
+import os
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+for p in (os.path.join(ROOT, "uor-r4_amd"), os.path.join(ROOT, "oracle"), ROOT):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU and the built HIP library")
+    config.addinivalue_line("markers", "slow: a longer CPU test")
+
+
+@pytest.fixture(scope="session", autouse=True)
+def _oracle_built():
+    """The oracle is test infrastructure: build it if a fresh checkout lacks it."""
+    so = os.path.join(ROOT, "oracle", "lib", "libfbs_oracle.so")
+    if not os.path.exists(so):
+        subprocess.run(["make", "-C", os.path.join(ROOT, "oracle")], check=True,
+                       stdout=subprocess.DEVNULL)
