@@ -1,0 +1,231 @@
+"""CPU checks of the product library: it loads, exports every entry point include/uor_fbs.h
+declares, and its structs have the reference's layout; and the kernels' exact integer arithmetic
+(uor-r4_amd/csrc/fbs_int.h, compiled for the host into libuor_fbs_hostprims.so) equals the
+oracle's and Python's exact integers over many inputs."""
+
+import ctypes as C
+import math
+import os
+import random
+import re
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import ROOT
+from uor_fbs import hip, tables
+from uor_fbs.cabi import ExtS, LayerS, ModelS
+
+HP_PATH = os.path.join(ROOT, "uor-r4_amd", "lib", "libuor_fbs_hostprims.so")
+P = C.c_void_p
+U64 = (1 << 64) - 1
+
+
+def declared_symbols():
+    text = open(os.path.join(ROOT, "include", "uor_fbs.h")).read()
+    return set(re.findall(r"\b(uor_fbs_[a-z0-9_]+)\s*\(", text))
+
+
+def test_library_exports_every_declared_entry_point():
+    L = hip.lib()
+    names = declared_symbols()
+    assert names == set(hip.SYMBOLS)
+    for name in names:
+        assert hasattr(L, name), name
+    assert L.uor_fbs_abi_version() == 1
+
+
+def test_struct_layout_matches_the_reference_image():
+    L = hip.lib()
+    assert L.uor_fbs_sizeof_model() == C.sizeof(ModelS)
+    assert L.uor_fbs_sizeof_layer() == C.sizeof(LayerS)
+    assert L.uor_fbs_sizeof_ext() == C.sizeof(ExtS)
+    if oracle.twin_available():  # the reference's own fbs_host_sizeof_* (host_kernel.cpp:8-9)
+        T = oracle.twin()
+        assert T.fbs_host_sizeof_model() == C.sizeof(ModelS)
+        assert T.fbs_host_sizeof_layer() == C.sizeof(LayerS)
+
+
+def test_model_create_refuses_bad_images_without_a_device():
+    """Validation runs before any device call: a bad image fails with a shape error."""
+    from dataclasses import replace
+    from uor_fbs import synth
+    from uor_fbs.cabi import Image
+    art = synth.make_artifact(synth.SMALL, 3)
+    img = Image(art)
+    img.model.width = 40
+    h = P()
+    assert hip.lib().uor_fbs_model_create(C.byref(img.model), None, 0, C.byref(h)) == 4
+    assert b"width" in hip.lib().uor_fbs_last_error()
+    img = Image(art)
+    art.layers[0].rec_gain[3] = -32768  # not a grid code (kernels.rs:116-120)
+    img = Image(art)
+    assert hip.lib().uor_fbs_model_create(C.byref(img.model), None, 0, C.byref(h)) == 4
+    assert b"grid code" in hip.lib().uor_fbs_last_error()
+    art = synth.make_artifact(synth.SMALL, 3)
+    art.layers[1].maps["mlp_up"][0][2] = 4  # atom outside 4 input blocks
+    img = Image(art)
+    assert hip.lib().uor_fbs_model_create(C.byref(img.model), None, 0, C.byref(h)) == 4
+    assert b"atom" in hip.lib().uor_fbs_last_error()
+    art = synth.make_artifact(replace(synth.SMALL, window=5), 3)
+    img = Image(art)
+    img.ext.wide_taps = None
+    assert hip.lib().uor_fbs_model_create(C.byref(img.model), C.byref(img.ext), 0, C.byref(h)) == 4
+
+
+@pytest.fixture(scope="module")
+def hp():
+    if not os.path.exists(HP_PATH):
+        pytest.skip("libuor_fbs_hostprims.so is not built")
+    L = C.CDLL(HP_PATH)
+    L.fbs_hp_isqrt128_many.argtypes = [P, P, P, C.c_uint64]
+    L.fbs_hp_div_many.argtypes = [P, P, P, P, C.c_uint64]
+    L.fbs_hp_rotation_many.argtypes = [P, C.c_uint64, C.c_uint64, P, C.c_uint64]
+    L.fbs_hp_snap_rotation_many.argtypes = [P, P, C.c_uint64, P, C.c_uint64]
+    L.fbs_hp_hamilton_check.argtypes = [P, P, C.c_uint64]
+    L.fbs_hp_hamilton_check.restype = C.c_uint64
+    L.fbs_hp_shift.argtypes = [C.c_int64, C.c_int32]
+    L.fbs_hp_shift.restype = C.c_int64
+    L.fbs_hp_grid_apply.argtypes = [C.c_int64, C.c_int16]
+    L.fbs_hp_grid_apply.restype = C.c_int64
+    L.fbs_hp_rms_norm_fine.argtypes = [P, C.c_uint32, C.c_int64, C.c_int32, P]
+    return L
+
+
+def _u64(vals):
+    return np.array([v & U64 for v in vals], dtype=np.uint64)
+
+
+def test_isqrt128_is_floor_sqrt(hp):
+    rng = random.Random(1)
+    vals = [0, 1, 2, 3, 4, (1 << 128) - 1, 1 << 127, 1 << 126, (1 << 126) - 1]
+    for k in (1, 2, 3, (1 << 32) - 1, 1 << 32, 1 << 63, (1 << 64) - 1, (1 << 48) + 7):
+        vals += [k * k - 1, k * k, min(k * k + 2 * k, (1 << 128) - 1)]
+    vals += [rng.getrandbits(rng.randint(1, 128)) for _ in range(60000)]
+    for _ in range(30000):  # perfect squares and their neighbours at every size
+        k = rng.getrandbits(rng.randint(1, 64))
+        vals += [k * k, max(k * k - 1, 0), min(k * k + 2 * k, (1 << 128) - 1)]
+    hi, lo = _u64([v >> 64 for v in vals]), _u64(vals)
+    out = np.zeros(len(vals), np.uint64)
+    hp.fbs_hp_isqrt128_many(hi.ctypes.data_as(P), lo.ctypes.data_as(P), out.ctypes.data_as(P), len(vals))
+    assert [int(x) for x in out] == [math.isqrt(v) for v in vals]
+
+
+def test_div128_is_floor_division(hp):
+    rng = random.Random(2)
+    ns, ds = [], []
+    for _ in range(60000):
+        d = rng.getrandbits(rng.randint(1, 64)) or 1
+        q = rng.getrandbits(rng.randint(0, 64))
+        ns.append(q * d + rng.randint(0, d - 1))
+        ds.append(d)
+    for d in (1, 2, 3, 1 << 63, (1 << 63) + 1, U64, (1 << 32) - 1, 1 << 32):
+        for q in (0, 1, U64, 1 << 63, 1 << 32):
+            for r in (0, d - 1):
+                ns.append(q * d + r)
+                ds.append(d)
+    ns.append(5), ds.append(0)  # zero divisor -> 0, as the reference's checked_div
+    out = np.zeros(len(ns), np.uint64)
+    hp.fbs_hp_div_many(_u64([n >> 64 for n in ns]).ctypes.data_as(P), _u64(ns).ctypes.data_as(P),
+                       _u64(ds).ctypes.data_as(P), out.ctypes.data_as(P), len(ns))
+    assert [int(x) for x in out] == [n // d if d else 0 for n, d in zip(ns, ds)]
+
+
+def _raw_quaternions(rng, n):
+    raw = []
+    for i in range(n):
+        sh = rng.randint(0, 31)
+        q = [rng.randint(-(1 << 31), (1 << 31) - 1) >> sh for _ in range(4)]
+        if i % 7 == 0:  # one nonzero axis, extremes, zero
+            q = [0, 0, 0, 0]
+            q[rng.randint(0, 3)] = rng.choice([1, -1, (1 << 31) - 1, -(1 << 31), rng.randint(-9, 9)])
+        if i % 11 == 0:
+            q = [rng.choice([-(1 << 31), (1 << 31) - 1]) for _ in range(4)]
+        raw.append(q)
+    return np.array(raw, np.int32)
+
+
+@pytest.mark.parametrize("eps", [0, 4295])
+@pytest.mark.parametrize("lam_exp", [31, 30, 27, 15])
+def test_unit_rotation_equals_oracle(hp, eps, lam_exp):
+    rng = random.Random(eps + lam_exp)
+    raw = _raw_quaternions(rng, 20000)
+    out = np.zeros((len(raw), 4), np.int64)
+    hp.fbs_hp_rotation_many(raw.ctypes.data_as(P), 1 << lam_exp, eps, out.ctypes.data_as(P), len(raw))
+    want = np.zeros(4, np.int64)
+    ico = np.ascontiguousarray(tables.icosian_coefficients())
+    for i in range(0, len(raw), 7):  # the oracle routine, one at a time
+        oracle.lib().fbs_oracle_serve_rotation(ico.ctypes.data_as(P), 1, raw[i].ctypes.data_as(P),
+                                               1 << lam_exp, eps, want.ctypes.data_as(P))
+        assert list(out[i]) == list(want), raw[i]
+    # and all of them against the closed form
+    for i in range(len(raw)):
+        v = [int(x) for x in raw[i]]
+        norm = math.isqrt((sum(x * x for x in v) + eps) << 32)
+        exp = [((1 << lam_exp) * ((-1 if x < 0 else 1) * ((abs(x) << 46) // norm if norm else 0))) >> 30 for x in v]
+        assert list(out[i]) == exp
+
+
+def test_snap_rotation_equals_oracle(hp):
+    rng = random.Random(7)
+    raw = _raw_quaternions(rng, 3000)
+    ico = np.ascontiguousarray(tables.icosian_coefficients())
+    out = np.zeros((len(raw), 4), np.int64)
+    hp.fbs_hp_snap_rotation_many(ico.ctypes.data_as(P), raw.ctypes.data_as(P), 1 << 30,
+                                 out.ctypes.data_as(P), len(raw))
+    want = np.zeros(4, np.int64)
+    for i in range(len(raw)):
+        oracle.lib().fbs_oracle_serve_rotation(ico.ctypes.data_as(P), 0, raw[i].ctypes.data_as(P),
+                                               1 << 30, 0, want.ctypes.data_as(P))
+        assert list(out[i]) == list(want)
+
+
+def test_hamilton32_equals_the_wide_product(hp):
+    """The 32 x 32 partial-product form equals the i64 x i64 -> i128 Hamilton product for left
+    operands of L1 norm <= 2^31 (unit quaternions times lambda), right operands anywhere."""
+    rng = np.random.default_rng(3)
+    n = 40000
+    a = np.zeros((n, 4), np.int64)
+    for i in range(n):
+        v = rng.integers(-(1 << 30), 1 << 30, 4)
+        s = np.abs(v).sum()
+        if s > (1 << 31):
+            v = v * (1 << 31) // s
+        a[i] = v
+    a[::5] = [[1 << 29, -(1 << 29), 1 << 29, -(1 << 29)]]
+    a[1::5] = [[1 << 30, 0, 0, 0]]
+    a = a.astype(np.int32)
+    b = rng.integers(-(1 << 63), (1 << 63) - 1, (n, 4), dtype=np.int64)
+    b[::3] = np.iinfo(np.int64).max
+    b[1::3] = np.iinfo(np.int64).min
+    b[2::7] = rng.integers(-(1 << 31), 1 << 31, (len(b[2::7]), 4))
+    assert hp.fbs_hp_hamilton_check(a.ctypes.data_as(P), b.ctypes.data_as(P), n) == 0
+
+
+def test_shift_and_grid_apply_equal_oracle(hp):
+    rng = random.Random(4)
+    for _ in range(20000):
+        v = rng.randint(-(1 << 63), (1 << 63) - 1) >> rng.randint(0, 63)
+        s = rng.randint(-70, 70)
+        assert hp.fbs_hp_shift(v, s) == oracle.lib().fbs_oracle_shift(v, s)
+        code = rng.choice([0, 1, -1]) * ((rng.randint(1, 127) << 4) | rng.randint(0, 15))
+        assert hp.fbs_hp_grid_apply(v, code) == oracle.lib().fbs_oracle_grid_apply(v, code)
+
+
+def test_rms_norm_fine_equals_oracle(hp):
+    rng = random.Random(11)
+    for trial in range(400):
+        n = rng.choice([32, 64, 96, 256, 512])
+        top = rng.randint(0, 31)
+        x = np.array([rng.randint(-(1 << top), (1 << top)) for _ in range(n)], np.int32)
+        if trial % 9 == 0:
+            x[:] = 0
+        if trial % 13 == 0:
+            x[rng.randint(0, n - 1)] = -(1 << 31)
+        eps_m, eps_e = rng.choice([(2814749767, -48), (0, 0), (1, 40), ((1 << 62), -2), (7, -70)])
+        got = np.zeros(n, np.int64)
+        want = np.zeros(n, np.int64)
+        hp.fbs_hp_rms_norm_fine(x.ctypes.data_as(P), n, eps_m, eps_e, got.ctypes.data_as(P))
+        oracle.lib().fbs_oracle_rms_norm_fine(x.ctypes.data_as(P), n, eps_m, eps_e, want.ctypes.data_as(P))
+        np.testing.assert_array_equal(got, want)

@@ -1,0 +1,601 @@
+// fbs_api.cpp - the C ABI of include/uor_fbs.h: model validation and upload, the per-lane
+// gather programs, device work buffers, and the sequences / decode / score entry points.
+//
+// Replaces the reference's GPU evaluator host side (docs/labs/d11-exporter-float-trunk/
+// instrument/src/device.rs:93-302 `DeviceEvaluator::{new, run}`) and its FFI twin entry
+// (host_kernel.cpp:16-29): the caller passes the parsed model image (`fbs_model` layout), the
+// library validates it as the reference's loader would (session.rs:640-735 `fbs_model`,
+// format.rs:616-752 `StackShape::validate`, kernels.rs:116-120 `grid_valid`) and keeps device
+// copies laid out for the kernels (fbs_device.h).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/uor_fbs.h"
+#include "fbs_device.h"
+#include "fbs_int.h"
+
+namespace fbs {
+hipError_t launch_run(const DevModel &M, const RunArgs &A, uint32_t grid, size_t lds_bytes,
+                      hipStream_t stream);
+}
+
+using namespace fbs;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+  return fail(UOR_FBS_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool grid_valid(int16_t code) {  // kernels.rs:116-120
+  uint32_t field = (uint32_t)(code < 0 ? -(int32_t)code : code) >> 4;
+  return code == 0 || (field >= 1 && field <= 127);
+}
+
+}  // namespace
+
+struct uor_fbs_handle {
+  int device = 0;
+  DevModel M{};
+  std::vector<void *> allocs;
+  size_t lds_bytes = 0;
+  uint32_t max_grid = 0;
+  int32_t *ring = nullptr;
+  size_t ring_blocks = 0;
+
+  ~uor_fbs_handle() {
+    int prev = 0;
+    (void)hipGetDevice(&prev);
+    (void)hipSetDevice(device);
+    for (void *p : allocs) (void)hipFree(p);
+    if (ring) (void)hipFree(ring);
+    (void)hipSetDevice(prev);
+  }
+
+  template <class T>
+  int upload(const T *src, size_t count, const T **dst) {
+    void *p = nullptr;
+    size_t bytes = count * sizeof(T);
+    hipError_t e = hipMalloc(&p, bytes ? bytes : 16);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+    allocs.push_back(p);
+    if (bytes) {
+      e = hipMemcpy(p, src, bytes, hipMemcpyHostToDevice);
+      if (e != hipSuccess) return hip_fail(e, "hipMemcpy");
+    }
+    *dst = (const T *)p;
+    return 0;
+  }
+
+  // The window ring for `blocks` resident sequences (grown, never shrunk).
+  int ensure_ring(size_t blocks) {
+    if (blocks <= ring_blocks) return 0;
+    if (ring) (void)hipFree(ring);
+    ring = nullptr;
+    ring_blocks = 0;
+    size_t bytes = blocks * (size_t)M.L * M.W * M.d * sizeof(int32_t);
+    hipError_t e = hipMalloc((void **)&ring, bytes);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(window ring)");
+    ring_blocks = blocks;
+    return 0;
+  }
+};
+
+extern "C" {
+
+uint32_t uor_fbs_abi_version(void) { return UOR_FBS_ABI_VERSION; }
+int64_t uor_fbs_sizeof_model(void) { return (int64_t)sizeof(uor_fbs_model); }
+int64_t uor_fbs_sizeof_layer(void) { return (int64_t)sizeof(uor_fbs_layer); }
+int64_t uor_fbs_sizeof_ext(void) { return (int64_t)sizeof(uor_fbs_ext); }
+const char *uor_fbs_last_error(void) { return g_last_error.c_str(); }
+
+}  // extern "C"
+
+namespace {
+
+struct Resolved {
+  uint32_t W, D, P, head;
+  bool reference_writer;
+};
+
+int check_map(const uor_fbs_map &mp, uint32_t in_dim, uint32_t out_dim, const char *name,
+              uint32_t layer) {
+  if (mp.blocks != out_dim / 8)
+    return fail(UOR_FBS_ERR_SHAPE, "l%u.%s: %u blocks, expected %u", layer, name, mp.blocks, out_dim / 8);
+  if (!mp.atoms || !mp.codes) return fail(UOR_FBS_ERR_ARGUMENT, "l%u.%s: null table", layer, name);
+  for (uint32_t o = 0; o < mp.blocks; o++) {
+    if (mp.atoms[o] >= in_dim / 8)
+      return fail(UOR_FBS_ERR_SHAPE, "l%u.%s: atom %u outside %u atoms", layer, name,
+                  (unsigned)mp.atoms[o], in_dim / 8);
+    for (int j = 0; j < 8; j++)
+      if (mp.codes[8 * o + j] >= 16)
+        return fail(UOR_FBS_ERR_SHAPE, "l%u.%s: code %u is not a signed axis", layer, name,
+                    (unsigned)mp.codes[8 * o + j]);
+  }
+  return 0;
+}
+
+int check_codes(const int16_t *codes, size_t n, const char *name, uint32_t layer) {
+  if (!codes) return fail(UOR_FBS_ERR_ARGUMENT, "l%u.%s: null table", layer, name);
+  for (size_t i = 0; i < n; i++)
+    if (!grid_valid(codes[i]))
+      return fail(UOR_FBS_ERR_SHAPE, "l%u.%s: %d is not a grid code", layer, name, (int)codes[i]);
+  return 0;
+}
+
+int validate(const uor_fbs_model *m, const uor_fbs_ext *e, Resolved *r) {
+  if (!m) return fail(UOR_FBS_ERR_ARGUMENT, "null model");
+  const uint32_t d = m->width, mlp = m->mlp;
+  if (d < 32 || d > kMaxWidth || d % 32)
+    return fail(UOR_FBS_ERR_SHAPE, "width %u: a multiple of 32 in 32..1024 (format.rs:724-729)", d);
+  if (mlp < 32 || mlp > kMaxMpl * kWave * 4 || mlp % 32)
+    return fail(UOR_FBS_ERR_SHAPE, "mlp %u: a multiple of 32 in 32..1024", mlp);
+  if (m->vocab == 0 || m->vocab >= (1u << 31)) return fail(UOR_FBS_ERR_SHAPE, "vocab %u", m->vocab);
+  if (m->context == 0) return fail(UOR_FBS_ERR_SHAPE, "zero context");
+  if (m->layer_count == 0 || m->layer_count > 64)
+    return fail(UOR_FBS_ERR_SHAPE, "layer count %u: 1..64", m->layer_count);
+  if (m->kept == 0 || m->kept > 16)
+    return fail(UOR_FBS_ERR_SHAPE, "kept cells %u: 1..16 (format.rs:436-439)", m->kept);
+  if (!m->layers || !m->final_gain || !m->writer_table || !m->roots_q12 || !m->icosian || !m->keep_q31)
+    return fail(UOR_FBS_ERR_ARGUMENT, "null model table");
+  r->W = (e && e->window) ? e->window : 3;
+  r->D = (e && e->drawers) ? e->drawers : 256;
+  r->P = (e && e->probes) ? e->probes : m->kept;
+  r->head = e ? e->head : 0;
+  if (r->W > kMaxWindow) return fail(UOR_FBS_ERR_SHAPE, "window %u: 1..%u", r->W, kMaxWindow);
+  if (r->D > kMaxDrawers) return fail(UOR_FBS_ERR_SHAPE, "drawers %u: 1..%u", r->D, kMaxDrawers);
+  if (r->P > kMaxProbes || r->P > r->D)
+    return fail(UOR_FBS_ERR_SHAPE, "probes %u: 1..min(drawers, %u)", r->P, kMaxProbes);
+  if (r->head > 1) return fail(UOR_FBS_ERR_SHAPE, "head %u: 0 writer, 1 nearest", r->head);
+  r->reference_writer = !(e && (e->drawer_keys || e->drawer_offsets)) && r->D == 256;
+  if (r->D != 256 && !(e && e->drawer_keys))
+    return fail(UOR_FBS_ERR_SHAPE, "%u drawers need drawer keys (root pairs make 256)", r->D);
+  if (r->W != 3 && !(e && e->wide_taps))
+    return fail(UOR_FBS_ERR_SHAPE, "window %u needs %u taps per channel (wide_taps)", r->W, r->W + 1);
+  const uint32_t rows = d / 4 + d;
+  for (uint32_t l = 0; l < m->layer_count; l++) {
+    const uor_fbs_layer &ly = m->layers[l];
+    int st;
+    if ((st = check_codes(ly.rec_gain, d, "rec_norm_gain", l))) return st;
+    if ((st = check_codes(ly.mlp_gain, d, "mlp_norm_gain", l))) return st;
+    const int16_t *taps = (e && e->wide_taps) ? e->wide_taps[l] : ly.taps;
+    if ((st = check_codes(taps, (size_t)(r->W + 1) * d, "conv_taps", l))) return st;
+    if (!ly.conv_bias || !ly.gate_bias || !ly.decay_offset)
+      return fail(UOR_FBS_ERR_ARGUMENT, "l%u: null bias table", l);
+    if ((st = check_map(ly.rec_in, d, 2 * d, "rec_in.fbs", l))) return st;
+    if ((st = check_map(ly.rec_gate, d, rows, "rec_gate.fbs", l))) return st;
+    if ((st = check_map(ly.rec_out, d, d, "rec_out.fbs", l))) return st;
+    if ((st = check_map(ly.mlp_gate, d, mlp, "mlp_gate.fbs", l))) return st;
+    if ((st = check_map(ly.mlp_up, d, mlp, "mlp_up.fbs", l))) return st;
+    if ((st = check_map(ly.mlp_down, mlp, d, "mlp_down.fbs", l))) return st;
+  }
+  int st;
+  if ((st = check_codes(m->final_gain, d, "final_norm_gain", 0))) return st;
+  if (e && e->table_i8 && e->table_shift > 8)
+    return fail(UOR_FBS_ERR_SHAPE, "table_shift %u: 0..8", e->table_shift);
+  if (e && e->drawer_keys)
+    for (size_t i = 0; i < (size_t)r->D * 16; i++)
+      if (e->drawer_keys[i] > kMaxKeyQ12 || e->drawer_keys[i] < -kMaxKeyQ12)
+        return fail(UOR_FBS_ERR_UNSUPPORTED, "drawer key %d outside +-%d", e->drawer_keys[i], kMaxKeyQ12);
+  if (e && e->drawer_offsets) {
+    if (!e->drawer_members) return fail(UOR_FBS_ERR_ARGUMENT, "drawer offsets without members");
+    for (uint32_t c = 0; c < r->D; c++)
+      if (e->drawer_offsets[c + 1] < e->drawer_offsets[c])
+        return fail(UOR_FBS_ERR_SHAPE, "drawer offsets decrease at %u", c);
+    for (uint32_t i = e->drawer_offsets[0]; i < e->drawer_offsets[r->D]; i++)
+      if (e->drawer_members[i] >= m->vocab)
+        return fail(UOR_FBS_ERR_SHAPE, "drawer member %u outside the vocabulary", e->drawer_members[i]);
+  }
+  return 0;
+}
+
+// Gather program word of output `o` of `mp` (source words: 2 channel + negate).
+uint16_t prog_word(const uor_fbs_map &mp, uint32_t o) {
+  uint8_t code = mp.codes[o];
+  uint32_t src = 8u * mp.atoms[o / 8] + (code & 7u);
+  return (uint16_t)(2 * src + ((code >> 3) & 1u));
+}
+
+}  // namespace
+
+extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e, int32_t device,
+                                    uor_fbs_handle **out) {
+  if (!out) return fail(UOR_FBS_ERR_ARGUMENT, "null output handle");
+  *out = nullptr;
+  Resolved r;
+  int st = validate(m, e, &r);
+  if (st) return st;
+  int count = 0;
+  hipError_t he = hipGetDeviceCount(&count);
+  if (he != hipSuccess || count == 0) return fail(UOR_FBS_ERR_DEVICE, "no HIP device");
+  if (device < 0 || device >= count) return fail(UOR_FBS_ERR_ARGUMENT, "device %d of %d", device, count);
+  int prev = 0;
+  (void)hipGetDevice(&prev);
+  (void)hipSetDevice(device);
+  uor_fbs_handle *h = new uor_fbs_handle();
+  h->device = device;
+  DevModel &M = h->M;
+  const uint32_t d = m->width, mlp = m->mlp, L = m->layer_count;
+  M.vocab = m->vocab;
+  M.d = d;
+  M.m = mlp;
+  M.L = L;
+  M.W = r.W;
+  M.D = r.D;
+  M.P = r.P;
+  M.head = r.head;
+  M.context = m->context;
+  M.raw_gates = m->raw_gates != 0;
+  M.raw_transition = m->raw_transition != 0;
+  M.nq = d / 4;
+  M.nm = mlp / 4;
+  M.qpl = (M.nq + kWave - 1) / kWave;
+  if (M.qpl == 3) M.qpl = 4;
+  M.mpl = (M.nm + kWave - 1) / kWave;
+  const uint32_t Q = M.qpl, MP = M.mpl;
+  M.s_rec_in = 0;
+  M.s_rec_gate = 8 * Q;
+  M.s_rec_out = 13 * Q;
+  M.s_mlp_gate = 17 * Q;
+  M.s_mlp_up = 17 * Q + 4 * MP;
+  M.s_mlp_down = 17 * Q + 8 * MP;
+  M.nslots = 21 * Q + 8 * MP;
+  M.xbar_words = 2 * (d > mlp ? d : mlp);
+  M.identity_rows = r.head == 1;
+  for (int sh = 0; sh <= 8; sh++) M.eps_int[sh] = norm_eps(m->eps_mantissa, m->eps_exp, sh);
+
+  auto done = [&](int code) {
+    if (code) delete h;
+    else *out = h;
+    (void)hipSetDevice(prev);
+    return code;
+  };
+
+  // Layers: gains, taps, biases and the gather program.
+  std::vector<DevLayer> layers(L);
+  for (uint32_t l = 0; l < L; l++) {
+    const uor_fbs_layer &ly = m->layers[l];
+    DevLayer &dl = layers[l];
+    if ((st = h->upload(ly.rec_gain, d, &dl.rec_gain))) return done(st);
+    if ((st = h->upload(ly.mlp_gain, d, &dl.mlp_gain))) return done(st);
+    const int16_t *taps = (e && e->wide_taps) ? e->wide_taps[l] : ly.taps;
+    if ((st = h->upload(taps, (size_t)(r.W + 1) * d, &dl.taps))) return done(st);
+    if ((st = h->upload(ly.conv_bias, d, &dl.conv_bias))) return done(st);
+    if ((st = h->upload(ly.gate_bias, d / 4 + d, &dl.gate_bias))) return done(st);
+    if ((st = h->upload(ly.decay_offset, d / 4, &dl.decay_offset))) return done(st);
+    std::vector<uint16_t> prog((size_t)M.nslots * kWave, 0);
+    auto put = [&](uint32_t slot, uint32_t lane, uint16_t w) { prog[(size_t)slot * kWave + lane] = w; };
+    for (uint32_t lane = 0; lane < kWave; lane++) {
+      for (uint32_t k = 0; k < Q; k++) {
+        uint32_t q = lane + kWave * k;
+        if (q >= M.nq) continue;
+        for (uint32_t c = 0; c < 4; c++) {
+          put(M.s_rec_in + 4 * k + c, lane, prog_word(ly.rec_in, 4 * q + c));
+          put(M.s_rec_in + 4 * Q + 4 * k + c, lane, prog_word(ly.rec_in, d + 4 * q + c));
+          put(M.s_rec_gate + Q + 4 * k + c, lane, prog_word(ly.rec_gate, M.nq + 4 * q + c));
+          put(M.s_rec_out + 4 * k + c, lane, prog_word(ly.rec_out, 4 * q + c));
+          put(M.s_mlp_down + 4 * k + c, lane, prog_word(ly.mlp_down, 4 * q + c));
+        }
+        put(M.s_rec_gate + k, lane, prog_word(ly.rec_gate, q));
+      }
+      for (uint32_t j = 0; j < MP; j++) {
+        uint32_t mq = lane + kWave * j;
+        if (mq >= M.nm) continue;
+        for (uint32_t c = 0; c < 4; c++) {
+          put(M.s_mlp_gate + 4 * j + c, lane, prog_word(ly.mlp_gate, 4 * mq + c));
+          put(M.s_mlp_up + 4 * j + c, lane, prog_word(ly.mlp_up, 4 * mq + c));
+        }
+      }
+    }
+    if ((st = h->upload(prog.data(), prog.size(), &dl.prog))) return done(st);
+  }
+  if ((st = h->upload(layers.data(), layers.size(), &M.layers))) return done(st);
+  if ((st = h->upload(m->final_gain, d, &M.final_gain))) return done(st);
+
+  // Writer table, biased for the unsigned SAD (row value v stored as v ^ 0x8000).
+  {
+    size_t n = (size_t)m->vocab * d;
+    std::vector<uint16_t> tb(n);
+    if (e && e->table_i8) {
+      for (size_t i = 0; i < n; i++)
+        tb[i] = (uint16_t)((uint16_t)((int32_t)e->table_i8[i] * (1 << e->table_shift)) ^ 0x8000u);
+    } else {
+      for (size_t i = 0; i < n; i++) tb[i] = (uint16_t)((uint16_t)m->writer_table[i] ^ 0x8000u);
+    }
+    if ((st = h->upload(tb.data(), n, &M.table_b))) return done(st);
+  }
+  // Drawer keys: the extension's, or the 256 root pairs (cell c = a * 16 + b scores the first
+  // 8-block against root a and the last against root b, session.rs:4069-4090).
+  {
+    std::vector<int16_t> keys((size_t)r.D * 16);
+    for (uint32_t c = 0; c < r.D; c++)
+      for (int i = 0; i < 8; i++) {
+        int32_t ka, kb;
+        if (e && e->drawer_keys) {
+          ka = e->drawer_keys[16ull * c + i];
+          kb = e->drawer_keys[16ull * c + 8 + i];
+        } else {
+          ka = m->roots_q12[8 * (c >> 4) + i];
+          kb = m->roots_q12[8 * (c & 15) + i];
+          if (ka > kMaxKeyQ12 || ka < -kMaxKeyQ12 || kb > kMaxKeyQ12 || kb < -kMaxKeyQ12)
+            return done(fail(UOR_FBS_ERR_UNSUPPORTED, "root coordinate outside +-%d", kMaxKeyQ12));
+        }
+        keys[16ull * c + i] = (int16_t)ka;
+        keys[16ull * c + 8 + i] = (int16_t)kb;
+      }
+    if ((st = h->upload(keys.data(), keys.size(), &M.keys))) return done(st);
+  }
+  // Drawer membership as CSR: the extension's, or token t in drawer t mod D (ascending).
+  {
+    std::vector<uint32_t> off(r.D + 1), mem;
+    if (e && e->drawer_offsets) {
+      uint32_t b0 = e->drawer_offsets[0];
+      for (uint32_t c = 0; c <= r.D; c++) off[c] = e->drawer_offsets[c] - b0;
+      mem.assign(e->drawer_members + b0, e->drawer_members + e->drawer_offsets[r.D]);
+    } else {
+      mem.reserve(m->vocab);
+      for (uint32_t c = 0; c < r.D; c++) {
+        off[c] = (uint32_t)mem.size();
+        for (uint32_t t = c; t < m->vocab; t += r.D) mem.push_back(t);
+      }
+      off[r.D] = (uint32_t)mem.size();
+    }
+    if (mem.empty()) mem.push_back(0);
+    if ((st = h->upload(off.data(), off.size(), &M.offsets))) return done(st);
+    if ((st = h->upload(mem.data(), mem.size(), &M.members))) return done(st);
+  }
+  if ((st = h->upload(m->icosian, 120 * 8, &M.icosian))) return done(st);
+  if ((st = h->upload(m->keep_q31, 16, &M.keep_q31))) return done(st);
+
+  hipDeviceProp_t prop;
+  he = hipGetDeviceProperties(&prop, device);
+  if (he != hipSuccess) return done(hip_fail(he, "hipGetDeviceProperties"));
+  h->lds_bytes = 4ull * M.xbar_words + 4ull * ((r.D + 3) & ~3u) + 8ull * L * d;
+  if (h->lds_bytes > prop.sharedMemPerBlock)
+    return done(fail(UOR_FBS_ERR_UNSUPPORTED, "%zu bytes of LDS per sequence exceed %zu",
+                     h->lds_bytes, (size_t)prop.sharedMemPerBlock));
+  h->max_grid = (uint32_t)prop.multiProcessorCount * 8;
+  return done(0);
+}
+
+extern "C" void uor_fbs_model_destroy(uor_fbs_handle *h) { delete h; }
+
+extern "C" uint64_t uor_fbs_state_words(const uor_fbs_handle *h) {
+  return h ? (uint64_t)h->M.L * h->M.d : 0;
+}
+extern "C" uint64_t uor_fbs_history_words(const uor_fbs_handle *h) {
+  return h ? (uint64_t)h->M.L * h->M.W * h->M.d : 0;
+}
+
+namespace {
+
+int launch(uor_fbs_handle *h, RunArgs &A, hipStream_t stream) {
+  if (A.n == 0) return 0;
+  uint32_t grid = A.n < h->max_grid ? A.n : h->max_grid;
+  int st = h->ensure_ring(grid);
+  if (st) return st;
+  A.ring = h->ring;
+  hipError_t e = launch_run(h->M, A, grid, h->lds_bytes, stream);
+  if (e != hipSuccess) return hip_fail(e, "kernel launch");
+  return 0;
+}
+
+// Device buffers for the host-buffer entry points.
+struct DevBuf {
+  std::vector<void *> ptrs;
+  ~DevBuf() {
+    for (void *p : ptrs) (void)hipFree(p);
+  }
+  template <class T>
+  int alloc(T **p, size_t count) {
+    *p = nullptr;
+    if (count == 0) return 0;
+    hipError_t e = hipMalloc((void **)p, count * sizeof(T));
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+    ptrs.push_back(*p);
+    return 0;
+  }
+  template <class T>
+  int in(T **p, const T *src, size_t count) {
+    if (!src) {
+      *p = nullptr;
+      return 0;
+    }
+    int st = alloc(p, count);
+    if (st) return st;
+    hipError_t e = hipMemcpy(*p, src, count * sizeof(T), hipMemcpyHostToDevice);
+    return e == hipSuccess ? 0 : hip_fail(e, "hipMemcpy");
+  }
+};
+
+template <class T>
+int copy_out(T *dst, const T *src, size_t count) {
+  if (!dst || !src || count == 0) return 0;
+  hipError_t e = hipMemcpy(dst, src, count * sizeof(T), hipMemcpyDeviceToHost);
+  return e == hipSuccess ? 0 : hip_fail(e, "hipMemcpy");
+}
+
+int first_status(const std::vector<int32_t> &status) {
+  for (int32_t s : status)
+    if (s) return fail(s, "a sequence failed with status %d (1 token, 2 context)", s);
+  return 0;
+}
+
+struct DeviceScope {
+  int prev = 0;
+  explicit DeviceScope(int dev) {
+    (void)hipGetDevice(&prev);
+    (void)hipSetDevice(dev);
+  }
+  ~DeviceScope() { (void)hipSetDevice(prev); }
+};
+
+}  // namespace
+
+extern "C" int uor_fbs_sequences_async(uor_fbs_handle *h, const uint32_t *tokens, uint32_t sequences,
+                                       uint32_t len, uint32_t *out_tokens, uint32_t *out_kept,
+                                       int32_t *out_query, int32_t *status, void *stream) {
+  if (!h || (!tokens && sequences && len) || !status || !out_tokens)
+    return fail(UOR_FBS_ERR_ARGUMENT, "null argument");
+  DeviceScope scope(h->device);
+  RunArgs A{};
+  A.mode = kModeSequences;
+  A.n = sequences;
+  A.len = len;
+  A.tokens = tokens;
+  A.out_tokens = out_tokens;
+  A.out_kept = out_kept;
+  A.out_query = out_query;
+  A.status = status;
+  return launch(h, A, (hipStream_t)stream);
+}
+
+extern "C" int uor_fbs_sequences(uor_fbs_handle *h, const uint32_t *tokens, uint32_t sequences,
+                                 uint32_t len, uint32_t *out_tokens, uint32_t *out_kept,
+                                 int32_t *out_query) {
+  if (!h || !tokens || !out_tokens) return fail(UOR_FBS_ERR_ARGUMENT, "null argument");
+  if (sequences == 0 || len == 0) return 0;
+  DeviceScope scope(h->device);
+  size_t n = (size_t)sequences * len;
+  DevBuf b;
+  uint32_t *dt, *dot, *dk = nullptr;
+  int32_t *dq = nullptr, *ds;
+  int st;
+  if ((st = b.in(&dt, tokens, n)) || (st = b.alloc(&dot, n)) || (st = b.alloc(&ds, sequences)))
+    return st;
+  if (out_kept && (st = b.alloc(&dk, n * h->M.P))) return st;
+  if (out_query && (st = b.alloc(&dq, n * h->M.d))) return st;
+  if ((st = uor_fbs_sequences_async(h, dt, sequences, len, dot, dk, dq, ds, nullptr))) return st;
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_fail(e, "kernel");
+  std::vector<int32_t> status(sequences);
+  if ((st = copy_out(status.data(), ds, sequences)) || (st = copy_out(out_tokens, dot, n)) ||
+      (st = copy_out(out_kept, dk, n * h->M.P)) || (st = copy_out(out_query, dq, n * h->M.d)))
+    return st;
+  return first_status(status);
+}
+
+extern "C" int uor_fbs_decode_async(uor_fbs_handle *h, const uint32_t *prompts, uint32_t sequences,
+                                    uint32_t prompt_len, uint32_t gen, uint32_t *out_reply,
+                                    const int64_t *in_state, const int32_t *in_history,
+                                    const uint32_t *in_position, int64_t *out_state,
+                                    int32_t *out_history, uint32_t *out_position, int32_t *status,
+                                    void *stream) {
+  if (!h || !prompts || !out_reply || !status) return fail(UOR_FBS_ERR_ARGUMENT, "null argument");
+  if (prompt_len == 0) return fail(UOR_FBS_ERR_ARGUMENT, "a decode needs at least one prompt token");
+  DeviceScope scope(h->device);
+  RunArgs A{};
+  A.mode = kModeDecode;
+  A.n = sequences;
+  A.len = prompt_len;
+  A.gen = gen;
+  A.tokens = prompts;
+  A.out_tokens = out_reply;
+  A.in_state = in_state;
+  A.in_history = in_history;
+  A.in_position = in_position;
+  A.out_state = out_state;
+  A.out_history = out_history;
+  A.out_position = out_position;
+  A.status = status;
+  return launch(h, A, (hipStream_t)stream);
+}
+
+extern "C" int uor_fbs_decode(uor_fbs_handle *h, const uint32_t *prompts, uint32_t sequences,
+                              uint32_t prompt_len, uint32_t gen, uint32_t *out_reply,
+                              const int64_t *in_state, const int32_t *in_history,
+                              const uint32_t *in_position, int64_t *out_state,
+                              int32_t *out_history, uint32_t *out_position) {
+  if (!h || !prompts || !out_reply) return fail(UOR_FBS_ERR_ARGUMENT, "null argument");
+  if (prompt_len == 0) return fail(UOR_FBS_ERR_ARGUMENT, "a decode needs at least one prompt token");
+  if (sequences == 0) return 0;
+  DeviceScope scope(h->device);
+  const size_t sw = uor_fbs_state_words(h), hw = uor_fbs_history_words(h);
+  DevBuf b;
+  uint32_t *dp, *dr, *dip = nullptr, *dop = nullptr;
+  int64_t *dis = nullptr, *dos = nullptr;
+  int32_t *dih = nullptr, *doh = nullptr, *ds;
+  int st;
+  if ((st = b.in(&dp, prompts, (size_t)sequences * prompt_len)) ||
+      (st = b.alloc(&dr, (size_t)sequences * (gen + 1))) || (st = b.alloc(&ds, sequences)) ||
+      (st = b.in(&dis, in_state, sequences * sw)) || (st = b.in(&dih, in_history, sequences * hw)) ||
+      (st = b.in(&dip, in_position, sequences)))
+    return st;
+  if (out_state && (st = b.alloc(&dos, sequences * sw))) return st;
+  if (out_history && (st = b.alloc(&doh, sequences * hw))) return st;
+  if (out_position && (st = b.alloc(&dop, sequences))) return st;
+  if ((st = uor_fbs_decode_async(h, dp, sequences, prompt_len, gen, dr, dis, dih, dip, dos, doh,
+                                 dop, ds, nullptr)))
+    return st;
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_fail(e, "kernel");
+  std::vector<int32_t> status(sequences);
+  if ((st = copy_out(status.data(), ds, sequences)) ||
+      (st = copy_out(out_reply, dr, (size_t)sequences * (gen + 1))) ||
+      (st = copy_out(out_state, dos, sequences * sw)) ||
+      (st = copy_out(out_history, doh, sequences * hw)) ||
+      (st = copy_out(out_position, dop, sequences)))
+    return st;
+  return first_status(status);
+}
+
+extern "C" int uor_fbs_score_async(uor_fbs_handle *h, const uint32_t *rows, uint64_t n_rows,
+                                   uint32_t len, uint32_t *out_argmin, uint64_t *matches,
+                                   int32_t *status, void *stream) {
+  if (!h || !rows || !matches || !status) return fail(UOR_FBS_ERR_ARGUMENT, "null argument");
+  if (n_rows >= (1ull << 31)) return fail(UOR_FBS_ERR_ARGUMENT, "%llu rows: below 2^31 per call",
+                                          (unsigned long long)n_rows);
+  DeviceScope scope(h->device);
+  RunArgs A{};
+  A.mode = kModeScore;
+  A.n = (uint32_t)n_rows;
+  A.len = len;
+  A.tokens = rows;
+  A.out_tokens = out_argmin;
+  A.matches = (unsigned long long *)matches;
+  A.status = status;
+  return launch(h, A, (hipStream_t)stream);
+}
+
+extern "C" int uor_fbs_score(uor_fbs_handle *h, const uint32_t *rows, uint64_t n_rows, uint32_t len,
+                             uint32_t *out_argmin, uint64_t *out_matches) {
+  if (!h || !rows || !out_matches) return fail(UOR_FBS_ERR_ARGUMENT, "null argument");
+  *out_matches = 0;
+  if (n_rows == 0 || len == 0) return 0;
+  DeviceScope scope(h->device);
+  size_t n = (size_t)n_rows * len;
+  DevBuf b;
+  uint32_t *dr, *da = nullptr;
+  uint64_t *dm;
+  int32_t *ds;
+  int st;
+  if ((st = b.in(&dr, rows, n)) || (st = b.alloc(&dm, 1)) || (st = b.alloc(&ds, n_rows))) return st;
+  if (out_argmin && (st = b.alloc(&da, n))) return st;
+  hipError_t e = hipMemset(dm, 0, sizeof(uint64_t));
+  if (e != hipSuccess) return hip_fail(e, "hipMemset");
+  if ((st = uor_fbs_score_async(h, dr, n_rows, len, da, dm, ds, nullptr))) return st;
+  e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_fail(e, "kernel");
+  std::vector<int32_t> status(n_rows);
+  if ((st = copy_out(status.data(), ds, n_rows)) || (st = copy_out(out_matches, dm, 1)) ||
+      (st = copy_out(out_argmin, da, n)))
+    return st;
+  return first_status(status);
+}

@@ -1,0 +1,82 @@
+// fbs_device.h - the device image of a SpiralCore/FBS model and the launch arguments, shared by
+// the kernels (fbs_kernel.hip) and the host side that builds them (fbs_api.cpp).
+//
+// Layout in HBM (all tables uploaded once by uor_fbs_model_create, read by every sequence):
+//   per layer: gains (d i16), window taps ((W+1) x d i16, tap s = s positions back),
+//              conv_bias (d i32), gate_bias (d/4 + d i32), decay_offset (d/4 i32), and the
+//              layer's gather program: [slot][64 lanes] u16 LDS word indices that carry out the
+//              six FBS projections (stack_fbs_gather, session.rs:4037-4053) for this lane mapping;
+//   writer: the table as biased u16 rows (v ^ 0x8000, vocab x d), drawer keys (D x 16 i16:
+//           first-block key then last-block key), CSR drawer offsets (D + 1) and members;
+//   per-sequence work (the library's, sized for the resident grid): the causal window ring,
+//           [block][layer][W][d] i32.
+// Lane mapping: one 64-lane wavefront runs one sequence. Lane j owns quaternions j + 64 k
+// (k < QPL) of the recurrence, i.e. channels 4 q .. 4 q + 3, and MLP quaternions j + 64 k
+// (k < mpl).
+#ifndef UOR_FBS_DEVICE_H
+#define UOR_FBS_DEVICE_H
+
+#include <stdint.h>
+
+namespace fbs {
+
+constexpr uint32_t kWave = 64;
+constexpr uint32_t kMaxMpl = 4;        // mlp <= 1024
+constexpr uint32_t kMaxWidth = 1024;   // WRITER_MAX_WIDTH, format.rs:437
+constexpr uint32_t kMaxDrawers = 4096;
+constexpr uint32_t kMaxProbes = 64;
+constexpr uint32_t kMaxWindow = 64;
+constexpr int32_t kMaxKeyQ12 = 16384;  // |drawer key| bound that keeps a drawer score in 20 bits
+
+struct DevLayer {
+  const int16_t *rec_gain;
+  const int16_t *mlp_gain;
+  const int16_t *taps;          // (W + 1) * d, [tap][channel]
+  const int32_t *conv_bias;     // d
+  const int32_t *gate_bias;     // d/4 + d
+  const int32_t *decay_offset;  // d/4
+  const uint16_t *prog;         // nslots * 64
+};
+
+struct DevModel {
+  uint32_t vocab, d, m, L, W, D, P, head, context, raw_gates, raw_transition;
+  uint32_t nq, nm, mpl, qpl;
+  uint32_t nslots, s_rec_in, s_rec_gate, s_rec_out, s_mlp_gate, s_mlp_up, s_mlp_down;
+  uint32_t xbar_words;      // 2 * max(d, m)
+  uint32_t identity_rows;   // the nearest head: one drawer holding every token
+  int64_t eps_int[9];       // RMSNorm epsilon at each pre-shift 0..8
+  const DevLayer *layers;   // L entries
+  const int16_t *final_gain;
+  const uint16_t *table_b;  // vocab * d, biased
+  const int16_t *keys;      // D * 16
+  const uint32_t *offsets;  // D + 1
+  const uint32_t *members;  // offsets[D]
+  const int8_t *icosian;    // 120 * 8
+  const uint64_t *keep_q31; // 16
+};
+
+enum RunMode : uint32_t { kModeSequences = 0, kModeDecode = 1, kModeScore = 2 };
+
+struct RunArgs {
+  uint32_t mode;
+  uint32_t n;          // sequences / rows
+  uint32_t len;        // tokens per sequence (sequences, score) or the prompt length (decode)
+  uint32_t gen;        // decode: generated steps
+  const uint32_t *tokens;
+  uint32_t *out_tokens;   // sequences: n*len; decode: n*(gen+1); score: n*len (nullable)
+  uint32_t *out_kept;     // sequences: n*len*P (nullable)
+  int32_t *out_query;     // sequences: n*len*d (nullable)
+  const int64_t *in_state;
+  const int32_t *in_history;
+  const uint32_t *in_position;
+  int64_t *out_state;
+  int32_t *out_history;
+  uint32_t *out_position;
+  unsigned long long *matches;
+  int32_t *status;        // n
+  int32_t *ring;          // gridDim.x * L * W * d
+};
+
+}  // namespace fbs
+
+#endif

@@ -1,0 +1,75 @@
+// fbs_hostprims.cpp - the device arithmetic of fbs_int.h compiled for the host, exported so the
+// CPU tests can check it against the oracle over millions of inputs (the kernels include the
+// very same header). Not part of the C ABI: a separate test library, libuor_fbs_hostprims.so.
+#include "fbs_int.h"
+
+using namespace fbs;
+
+extern "C" {
+
+uint64_t fbs_hp_isqrt128(uint64_t hi, uint64_t lo) { return isqrt128(((u128)hi << 64) | lo); }
+
+uint64_t fbs_hp_div128_64(uint64_t nhi, uint64_t nlo, uint64_t d) {
+  return div128_64(((u128)nhi << 64) | nlo, d);
+}
+
+// Batched forms for speed: out[i] = isqrt128(hi[i]:lo[i]).
+void fbs_hp_isqrt128_many(const uint64_t *hi, const uint64_t *lo, uint64_t *out, uint64_t n) {
+  for (uint64_t i = 0; i < n; i++) out[i] = isqrt128(((u128)hi[i] << 64) | lo[i]);
+}
+void fbs_hp_div_many(const uint64_t *nhi, const uint64_t *nlo, const uint64_t *d, uint64_t *out,
+                     uint64_t n) {
+  for (uint64_t i = 0; i < n; i++) out[i] = div128_64(((u128)nhi[i] << 64) | nlo[i], d[i]);
+}
+
+uint32_t fbs_hp_rsqrt_q46(uint32_t t) { return rsqrt_q46(t); }
+uint64_t fbs_hp_recip_q63(uint32_t d) { return recip_q63(d); }
+
+int64_t fbs_hp_shift(int64_t v, int32_t s) { return shift(v, s); }
+int64_t fbs_hp_grid_apply(int64_t v, int16_t code) { return grid_apply(v, code); }
+
+// rotation(raw, lambda, eps) for n quaternions: raw n*4 i32, out n*4 i64.
+void fbs_hp_rotation_many(const int32_t *raw, uint64_t lambda, uint64_t eps, int64_t *out,
+                          uint64_t n) {
+  for (uint64_t i = 0; i < n; i++) rotation(raw + 4 * i, lambda, eps, out + 4 * i);
+}
+
+void fbs_hp_snap_rotation_many(const int8_t *ico, const int32_t *raw, uint64_t lambda,
+                               int64_t *out, uint64_t n) {
+  for (uint64_t i = 0; i < n; i++) snap_rotation(ico, raw + 4 * i, lambda, out + 4 * i);
+}
+
+// hamilton32 vs hamilton64 on n pairs: returns the number of mismatching outputs.
+uint64_t fbs_hp_hamilton_check(const int32_t *a, const int64_t *b, uint64_t n) {
+  uint64_t bad = 0;
+  for (uint64_t i = 0; i < n; i++) {
+    int64_t a64[4] = {a[4 * i], a[4 * i + 1], a[4 * i + 2], a[4 * i + 3]};
+    i128 x[4], y[4];
+    hamilton32(a + 4 * i, b + 4 * i, x);
+    hamilton64(a64, b + 4 * i, y);
+    for (int k = 0; k < 4; k++) bad += x[k] != y[k];
+  }
+  return bad;
+}
+
+// RMSNorm on one vector, as the kernel composes it (max, pre-shift, sum, factor, apply).
+void fbs_hp_rms_norm_fine(const int32_t *x, uint32_t n, int64_t eps_m, int32_t eps_e,
+                          int64_t *out) {
+  uint32_t max = 0;
+  for (uint32_t i = 0; i < n; i++) {
+    uint32_t a = uabs32(x[i]);
+    if (a > max) max = a;
+  }
+  int32_t sh = bitlen64(max) - 24;
+  if (sh < 0) sh = 0;
+  uint64_t sum = 0;
+  for (uint32_t i = 0; i < n; i++) {
+    int64_t y = shift(x[i], sh);
+    out[i] = y;
+    sum += uabs64(y) * uabs64(y);
+  }
+  NormFactor f = norm_factor(sum, n, norm_eps(eps_m, eps_e, sh));
+  for (uint32_t i = 0; i < n; i++) out[i] = norm_apply(f, out[i]);
+}
+
+}  // extern "C"

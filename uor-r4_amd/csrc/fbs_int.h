@@ -1,0 +1,449 @@
+// fbs_int.h - exact integer arithmetic of the SpiralCore/FBS step, for gfx950 and the host.
+//
+// Every routine here is bit-exact with the reference's integer kernels
+// (crates/uor-r4-integer/src/stack/kernels.rs, session.rs; its C++ twin
+// docs/labs/d11-exporter-float-trunk/instrument/src/fbs_core.h): round-half-up shifts that
+// saturate, products modulo 2^64 / 2^128, floor square roots and floor quotients. The reference
+// forms its roots digit by digit and its quotients by hardware or restoring division; a GPU has
+// neither, so this file computes them from fixed-point reciprocal estimates (a seed table and
+// Newton steps) and then corrects the estimate with exact integer checks. The correction loops
+// make the result exact for every input whatever the estimate's error; the estimates only
+// decide how many correction steps run (at most one or two for every input class the tests
+// sweep). No floating point is used anywhere.
+//
+// The functions are __host__ __device__ so that the same code is compiled into the kernels and
+// into a host library that the CPU tests check against the oracle.
+#ifndef UOR_FBS_INT_H
+#define UOR_FBS_INT_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define FBS_HD __host__ __device__ __forceinline__
+
+namespace fbs {
+
+typedef __int128 i128;
+typedef unsigned __int128 u128;
+
+constexpr int32_t kResidualExp = -16;  // RS stack/kernels.rs:34
+constexpr int32_t kProductExp = -32;   // RS stack/kernels.rs:37
+constexpr int32_t kStateExp = -32;     // RS stack/session.rs:72
+constexpr int32_t kNormFineExp = -24;  // RS stack/kernels.rs:566
+constexpr int32_t kQ12Exp = -12;       // RS stack/session.rs:475
+constexpr int32_t kGridExpBias = 64;   // RS stack/kernels.rs:39
+constexpr uint64_t kPhiLo = 2654435769ull;   // PHI_Q32 - 2^32, RS stack/mod.rs:167
+constexpr uint64_t kRotationEps = 4295;      // RS stack/session.rs:141
+constexpr uint64_t kGateEps = 0;             // RS stack/session.rs:144
+
+// ---------------------------------------------------------------------------------------------
+// Scalar conventions (RS stack/kernels.rs:41-135).
+
+FBS_HD int64_t sat_add64(int64_t a, int64_t b) {
+  int64_t r;
+  if (__builtin_add_overflow(a, b, &r)) return b > 0 ? INT64_MAX : INT64_MIN;
+  return r;
+}
+FBS_HD int64_t sat_neg64(int64_t v) { return v == INT64_MIN ? INT64_MAX : -v; }
+FBS_HD int32_t sat_add32(int32_t a, int32_t b) {
+  int64_t s = (int64_t)a + b;
+  return s > INT32_MAX ? INT32_MAX : s < INT32_MIN ? INT32_MIN : (int32_t)s;
+}
+FBS_HD int32_t clamp_i32(int64_t v) {
+  return v > INT32_MAX ? INT32_MAX : v < INT32_MIN ? INT32_MIN : (int32_t)v;
+}
+FBS_HD int64_t wadd64(int64_t a, int64_t b) { return (int64_t)((uint64_t)a + (uint64_t)b); }
+FBS_HD uint64_t uabs64(int64_t v) { return v < 0 ? 0ull - (uint64_t)v : (uint64_t)v; }
+FBS_HD uint32_t uabs32(int32_t v) { return v < 0 ? 0u - (uint32_t)v : (uint32_t)v; }
+FBS_HD int clz64(uint64_t v) { return v ? __builtin_clzll(v) : 64; }
+FBS_HD int bitlen64(uint64_t v) { return 64 - clz64(v); }
+FBS_HD int clz128(u128 v) {
+  uint64_t hi = (uint64_t)(v >> 64);
+  return hi ? clz64(hi) : 64 + clz64((uint64_t)v);
+}
+
+// `shift`: round-half-up arithmetic shift right by s, or a saturating shift left for s < 0
+// (RS stack/kernels.rs:41-62).
+FBS_HD int64_t shift(int64_t v, int32_t s) {
+  if (s > 0) {
+    if (s >= 63) return v < 0 ? -1 : 0;
+    return sat_add64(v, (int64_t)1 << (s - 1)) >> s;
+  }
+  if (s < 0) {
+    uint32_t k = (uint32_t)(-(int64_t)s);
+    if (k > 63) k = 63;
+    int64_t limit = INT64_MAX >> k;
+    if (v > limit) return INT64_MAX;
+    if (v < -limit) return INT64_MIN;
+    return (int64_t)((uint64_t)v << k);
+  }
+  return v;
+}
+
+// `shift_wide`: round-half-up shift of an i128 (wrapping add of the half), clamped to i64
+// (RS stack/kernels.rs:64-74). s <= 127.
+FBS_HD int64_t shift_wide(i128 v, uint32_t s) {
+  i128 r = s == 0 ? v : (i128)((u128)v + ((u128)1 << (s - 1))) >> s;
+  if (r > (i128)INT64_MAX) return INT64_MAX;
+  if (r < (i128)INT64_MIN) return INT64_MIN;
+  return (int64_t)r;
+}
+
+// `to_exp_i32` (RS stack/kernels.rs:76-80).
+FBS_HD int32_t to_exp_i32(int64_t v, int32_t from, int32_t to) {
+  return clamp_i32(shift(v, to - from));
+}
+
+// `grid_apply`: v (16 + (|c| & 15)) 2^((|c| >> 4) - 68) rounded half up, then the sign of c;
+// the product wraps modulo 2^64 like `scale_16_plus` (RS stack/kernels.rs:95-135).
+FBS_HD int64_t grid_apply(int64_t v, int16_t code) {
+  if (code == 0) return 0;
+  uint32_t c = code < 0 ? (uint32_t)(-(int32_t)code) : (uint32_t)code;
+  int32_t e = (int32_t)(c >> 4) - kGridExpBias;
+  int64_t scaled = (int64_t)((uint64_t)v * (uint64_t)(16 + (c & 15)));
+  scaled = shift(scaled, 4 - e);
+  return code < 0 ? sat_neg64(scaled) : scaled;
+}
+
+// The same for a 32-bit input, whose product (16 + m) v never wraps.
+FBS_HD int64_t grid_apply32(int32_t v, int16_t code) { return grid_apply((int64_t)v, code); }
+
+// ---------------------------------------------------------------------------------------------
+// Reciprocal and reciprocal-square-root seeds (compile-time tables, no floating point).
+
+constexpr uint64_t ce_isqrt64(uint64_t n) {
+  uint64_t r = 0, b = 1ull << 62;
+  while (b > n) b >>= 2;
+  while (b) {
+    if (n >= r + b) {
+      n -= r + b;
+      r = (r >> 1) + b;
+    } else {
+      r >>= 1;
+    }
+    b >>= 2;
+  }
+  return r;
+}
+
+struct Seed384 {
+  uint32_t v[384];
+};
+struct Seed256 {
+  uint32_t v[256];
+};
+
+// rsqrt seed: bucket i = t >> 23 in [128, 512) of t in [2^30, 2^32); entry ~ 2^46 / sqrt(mid).
+constexpr Seed384 make_rsqrt_seed() {
+  Seed384 s{};
+  for (int i = 0; i < 384; i++) {
+    uint64_t mid = ((uint64_t)(2 * (i + 128) + 1)) << 22;   // bucket middle, < 2^32
+    uint64_t root = ce_isqrt64(mid << 30);                   // sqrt(mid) 2^15
+    s.v[i] = (uint32_t)((1ull << 61) / root);                // 2^46 / sqrt(mid)
+  }
+  return s;
+}
+// reciprocal seed: bucket i = d >> 23 in [256, 512) of d in [2^31, 2^32); entry ~ 2^63 / mid.
+constexpr Seed256 make_recip_seed() {
+  Seed256 s{};
+  for (int i = 0; i < 256; i++) {
+    uint64_t mid = ((uint64_t)(2 * (i + 256) + 1)) << 22;
+    uint64_t v = (1ull << 63) / mid;
+    s.v[i] = v > 0xffffffffull ? 0xffffffffu : (uint32_t)v;
+  }
+  return s;
+}
+
+// y ~ 2^46 / sqrt(t) for t in [2^30, 2^32); y in [2^30, 2^31], relative error below 2^-27.
+FBS_HD uint32_t rsqrt_q46(uint32_t t) {
+  constexpr Seed384 seed = make_rsqrt_seed();
+  uint64_t y = seed.v[(t >> 23) - 128];
+#pragma unroll
+  for (int it = 0; it < 2; it++) {
+    // Newton: y <- y (3 - t y^2 / 2^92) / 2, with p = t y^2 / 2^60 ~ 2^32.
+    uint64_t y2 = y * y;                                   // <= 2^62
+    uint64_t p = (uint64_t)(((u128)t * (y2 >> 28)) >> 32);  // ~ 2^32
+    uint64_t f = ((3ull << 32) - p) >> 1;                   // ~ 2^32
+    y = (y * f) >> 32;
+    if (y > (1ull << 31)) y = 1ull << 31;
+    if (y < (1ull << 30)) y = 1ull << 30;
+  }
+  return (uint32_t)y;
+}
+
+// w ~ 2^63 / d for d in [2^31, 2^32); w in (2^31, 2^32], relative error below 2^-30.
+FBS_HD uint64_t recip_q63(uint32_t d) {
+  constexpr Seed256 seed = make_recip_seed();
+  uint64_t w = seed.v[(d >> 23) - 256];
+#pragma unroll
+  for (int it = 0; it < 2; it++) {
+    // Newton: w <- w + w (2^63 - d w) / 2^63.
+    int64_t e = (int64_t)((1ull << 63) - (uint64_t)d * w);
+    w = (uint64_t)((int64_t)w + (int64_t)(((i128)e * (int64_t)w) >> 63));
+  }
+  return w;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Floor square root of a u128 (RS stack/kernels.rs:408-430 `stack_isqrt`): the result is
+// isqrt(n << z) >> (z / 2) for the even z that puts n's top bit at 126 or 127; the normalised
+// root is estimated from a 32-bit reciprocal square root, refined by two Newton steps on the
+// exact remainder, and corrected to the floor.
+FBS_HD uint64_t isqrt128(u128 n) {
+  if (n == 0) return 0;
+  int z = clz128(n) & ~1;
+  u128 nn = n << z;                                  // [2^126, 2^128)
+  uint32_t t = (uint32_t)(nn >> 96);                 // [2^30, 2^32)
+  uint64_t y = rsqrt_q46(t);                         // 2^46 / sqrt(t)
+  // sqrt(nn) ~ sqrt(t) 2^48 = t y 2^2.
+  u128 s = ((u128)((uint64_t)t * y)) << 2;
+  if (s >= ((u128)1 << 64)) s = ((u128)1 << 64) - 1;
+#pragma unroll
+  for (int it = 0; it < 2; it++) {
+    // s += (nn - s^2) / (2 s), with 1 / (2 s) ~ y / 2^95.
+    i128 diff = (i128)(nn - s * s);                  // small and signed
+    i128 corr = ((diff >> 32) * (i128)y) >> 63;
+    s = (u128)((i128)s + corr);
+    if ((i128)s < 0) s = 0;
+    if (s >= ((u128)1 << 64)) s = ((u128)1 << 64) - 1;
+  }
+  // sqrt(nn) < 2^64, so s + 1 <= 2^64 - 1 whenever the second loop runs.
+  while (s * s > nn) s -= 1;
+  while (s < ((u128)1 << 64) - 1 && (s + 1) * (s + 1) <= nn) s += 1;
+  return (uint64_t)s >> (z >> 1);
+}
+
+// A normalised divisor and its reciprocal, for several quotients by one divisor.
+struct Divisor {
+  uint64_t d;   // the divisor
+  uint64_t dn;  // d << z, in [2^63, 2^64)
+  uint64_t v;   // ~ 2^127 / dn, relative error near 2^-60
+  int z;
+};
+
+FBS_HD Divisor make_divisor(uint64_t d) {
+  Divisor r;
+  r.d = d;
+  if (d == 0) {
+    r.dn = 0;
+    r.v = 0;
+    r.z = 0;
+    return r;
+  }
+  r.z = clz64(d);
+  r.dn = d << r.z;
+  uint64_t w = recip_q63((uint32_t)(r.dn >> 32));    // ~ 2^63 / (dn >> 32) ~ 2^95 / dn
+  // One Newton step at 128 bits: v = w 2^32 + v (2^127 - dn v) / 2^127.
+  u128 v0 = (u128)w << 32;
+  i128 e = (i128)(((u128)1 << 127) - (u128)r.dn * v0);
+  i128 corr = ((e >> 64) * (i128)v0) >> 63;
+  u128 v = (u128)((i128)v0 + corr);
+  if (v >= ((u128)1 << 64)) v = ((u128)1 << 64) - 1;
+  r.v = (uint64_t)v;
+  return r;
+}
+
+// floor(n / d) (RS stack/kernels.rs:345-360), zero for a zero divisor. Requires a quotient
+// below 2^64.
+FBS_HD uint64_t divq(u128 n, const Divisor &dv) {
+  if (dv.d == 0) return 0;
+  u128 nn = n << dv.z;                               // < 2^64 dn, so no bits are lost
+  uint64_t nh = (uint64_t)(nn >> 64);
+  u128 q = ((u128)nh * dv.v) >> 63;                  // under-estimate of nn / dn
+  if (q >= ((u128)1 << 64)) q = ((u128)1 << 64) - 1;
+  // Remainder-based refinement, then the exact floor.
+  i128 rem = (i128)(nn - q * dv.dn);
+  i128 step = ((rem >> 32) * (i128)(dv.v >> 32)) >> 63;
+  q = (u128)((i128)q + step);
+  rem = (i128)(nn - q * dv.dn);
+  while (rem < 0) {
+    q -= 1;
+    rem += (i128)dv.dn;
+  }
+  while (rem >= (i128)dv.dn) {
+    q += 1;
+    rem -= (i128)dv.dn;
+  }
+  return (uint64_t)q;
+}
+
+FBS_HD uint64_t div128_64(u128 n, uint64_t d) { return divq(n, make_divisor(d)); }
+
+// ---------------------------------------------------------------------------------------------
+// Vector kernels, one element at a time.
+
+// RMSNorm's per-vector factor (RS stack/kernels.rs:569-620 `stack_rms_norm_fine`, TW 294-330):
+// from the sum of the squared pre-shifted values, the multiplier r = floor(2^96 / s) with
+// s = isqrt(ms << 68) truncated to 128 bits; `huge` marks s = 1, where r = 2^96.
+struct NormFactor {
+  uint64_t r;
+  bool huge;
+};
+
+FBS_HD NormFactor norm_factor(uint64_t sum, uint32_t n, int64_t eps_int) {
+  uint64_t mean = n == 0 ? 0 : div128_64((u128)sum, n);
+  int64_t ms = wadd64((int64_t)mean, eps_int);
+  if (ms < 1) ms = 1;
+  u128 wide = (u128)(uint64_t)ms << 68;              // truncated to 128 bits as the reference
+  uint64_t s = isqrt128(wide);
+  NormFactor f;
+  if (s <= 1) {
+    f.r = 0;
+    f.huge = true;
+  } else {
+    f.r = div128_64((u128)1 << 96, s);
+    f.huge = false;
+  }
+  return f;
+}
+
+// One normalised value: round(r y / 2^38) with the sign of y, clamped to i64.
+FBS_HD int64_t norm_apply(NormFactor f, int64_t y) {
+  uint64_t u = uabs64(y);
+  u128 mag = f.huge ? ((u128)u << 96) : (u128)f.r * u;
+  i128 p = y < 0 ? (i128)(0 - mag) : (i128)mag;
+  i128 r = (i128)((u128)p + ((u128)1 << 37)) >> 38;
+  if (r > (i128)INT64_MAX) return INT64_MAX;
+  if (r < (i128)INT64_MIN) return INT64_MIN;
+  return (int64_t)r;
+}
+
+// eps at the square exponent of pre-shift sh (kernels.rs:596-602): shift(mantissa,
+// (2 (-16 + sh)) - eps_exp), never negative.
+FBS_HD int64_t norm_eps(int64_t eps_mantissa, int32_t eps_exp, int32_t sh) {
+  int64_t e = shift(eps_mantissa, (kResidualExp + sh) * 2 - eps_exp);
+  return e < 0 ? 0 : e;
+}
+
+// quantize16's element rule: clamp(shift(v, s), +-32767) (RS stack/kernels.rs:545-553).
+FBS_HD int32_t quantize_elem(int64_t v, int32_t s) {
+  int64_t y = shift(v, s);
+  return (int32_t)(y > 32767 ? 32767 : y < -32767 ? -32767 : y);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Quaternions.
+
+// Hamilton product a (x) b modulo 2^128 (RS stack/kernels.rs:998-1030, TW 363-370).
+FBS_HD void hamilton64(const int64_t a[4], const int64_t b[4], i128 o[4]) {
+#define FBS_P(i, j) ((i128)a[i] * (i128)b[j])
+  o[0] = FBS_P(0, 0) - FBS_P(1, 1) - FBS_P(2, 2) - FBS_P(3, 3);
+  o[1] = FBS_P(0, 1) + FBS_P(1, 0) + FBS_P(2, 3) - FBS_P(3, 2);
+  o[2] = FBS_P(0, 2) - FBS_P(1, 3) + FBS_P(2, 0) + FBS_P(3, 1);
+  o[3] = FBS_P(0, 3) + FBS_P(1, 2) - FBS_P(2, 1) + FBS_P(3, 0);
+#undef FBS_P
+}
+
+// a (x) b for a 32-bit left operand: the same sums, from 32 x 32 partial products. b = H 2^32
+// + L with H signed and L read as signed (L - 2^32 [L >= 2^31]); the borrow goes into the high
+// sum. With |a| summing to at most 2^31 + 4 (every unit or snapped quaternion times lambda
+// <= 2^31) neither 64-bit sum can overflow, so the result equals hamilton64's.
+FBS_HD void hamilton32(const int32_t a[4], const int64_t b[4], i128 o[4]) {
+  int32_t hi[4], lo[4], bor[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    hi[j] = (int32_t)(b[j] >> 32);
+    lo[j] = (int32_t)(uint32_t)b[j];
+    bor[j] = lo[j] < 0 ? 1 : 0;
+  }
+  const int sgn[4][4] = {{1, -1, -1, -1}, {1, 1, 1, -1}, {1, -1, 1, 1}, {1, 1, -1, 1}};
+  const int idx[4][4] = {{0, 1, 2, 3}, {1, 0, 3, 2}, {2, 3, 0, 1}, {3, 2, 1, 0}};
+  // Output k sums sgn[k][i] a[i] b[idx[k][i]].
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    int64_t H = 0, L = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      int j = idx[k][i];
+      int64_t ph = (int64_t)a[i] * (int64_t)hi[j] + (bor[j] ? (int64_t)a[i] : 0);
+      int64_t pl = (int64_t)a[i] * (int64_t)lo[j];
+      if (sgn[k][i] > 0) {
+        H += ph;
+        L += pl;
+      } else {
+        H -= ph;
+        L -= pl;
+      }
+    }
+    o[k] = ((i128)H << 32) + (i128)L;
+  }
+}
+
+// Sign of da + db phi, exactly (RS stack/kernels.rs:1180-1215, TW 393-408).
+FBS_HD bool diff_positive(int64_t da, int64_t db) {
+  i128 p = (i128)da * 2 + db;
+  if (db == 0) return p > 0;
+  u128 b2 = (u128)uabs64(db) * uabs64(db) * 5;
+  u128 pa = (u128)(p < 0 ? -p : p);
+  u128 p2 = pa * pa;
+  if (db > 0) return p >= 0 || b2 > p2;
+  return p > 0 && p2 > b2;
+}
+
+// The icosian with the largest exact dot product with raw, the lowest index on ties
+// (RS stack/kernels.rs:1420-1474 `stack_snap_select`). ico: 120 x 4 x (a, b), coordinate
+// (a + b phi) / 2.
+FBS_HD uint32_t snap_select(const int8_t *ico, const int32_t raw[4]) {
+  uint32_t best = 0;
+  int64_t best_a = 0, best_b = 0;
+  for (uint32_t r = 0; r < 120; r++) {
+    int64_t a = 0, b = 0;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      a += (int64_t)raw[c] * ico[8 * r + 2 * c];
+      b += (int64_t)raw[c] * ico[8 * r + 2 * c + 1];
+    }
+    if (r == 0 || diff_positive(a - best_a, b - best_b)) {
+      best = r;
+      best_a = a;
+      best_b = b;
+    }
+  }
+  return best;
+}
+
+// `stack_snap_rotation` (RS stack/kernels.rs:1530-1557, TW 435-445).
+FBS_HD void snap_rotation(const int8_t *ico, const int32_t raw[4], uint64_t lambda, int64_t o[4]) {
+  uint32_t r = snap_select(ico, raw);
+  uint64_t lambda_phi = lambda + ((lambda * kPhiLo + (1ull << 31)) >> 32);
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    int64_t sum = (int64_t)(lambda * (uint64_t)(int64_t)ico[8 * r + 2 * c] +
+                            lambda_phi * (uint64_t)(int64_t)ico[8 * r + 2 * c + 1]);
+    o[c] = shift(sum, 1);
+  }
+}
+
+// The unit quaternion of `stack_rotation` at Q30 before lambda (RS stack/session.rs:5165-5181):
+// u_c = sign(v_c) floor(|v_c| 2^46 / s), s = isqrt((sum v^2 + eps) << 32); all zero for s = 0.
+// |u_c| <= 2^30 and sum u_c^2 <= 2^60.
+FBS_HD void unit_q30(const int32_t raw[4], uint64_t eps, int32_t u[4]) {
+  u128 square = eps;
+#pragma unroll
+  for (int c = 0; c < 4; c++) square += (u128)((uint64_t)((int64_t)raw[c] * raw[c]));
+  uint64_t s = isqrt128(square << 32);
+  Divisor dv = make_divisor(s);
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    uint64_t a = uabs32(raw[c]);
+    uint64_t m = s == 0 ? 0 : divq((u128)a << 46, dv);
+    u[c] = raw[c] < 0 ? -(int32_t)m : (int32_t)m;
+  }
+}
+
+// (lambda u) >> 30 for lambda = 2^p (p <= 31): u << (p - 30) or floor(u / 2^(30 - p)).
+FBS_HD int64_t scale_pow2(int32_t u, uint32_t p) {
+  return p >= 30 ? (int64_t)u << (p - 30) : (int64_t)(u >> (30 - p));
+}
+
+// `stack_rotation` for any lambda (RS stack/session.rs:5165-5181, TW 459-474).
+FBS_HD void rotation(const int32_t raw[4], uint64_t lambda, uint64_t eps, int64_t o[4]) {
+  int32_t u[4];
+  unit_q30(raw, eps, u);
+#pragma unroll
+  for (int c = 0; c < 4; c++) o[c] = (int64_t)(((i128)lambda * (i128)u[c]) >> 30);
+}
+
+}  // namespace fbs
+
+#endif

@@ -1,0 +1,146 @@
+"""ctypes binding of the product library, uor-r4_amd/lib/libuor_fbs_hip.so (include/uor_fbs.h).
+
+The Python face of the boundary the reference's Rust host binds through `extern "C"`
+(docs/labs/d11-exporter-float-trunk/instrument/src/lib.rs:14-95, device.rs:93-302): a model
+handle created from the `fbs_model` image, then teacher-forced `sequences`, greedy `decode`
+with state export/import, and `score`. Errors raise `FbsError` carrying the library's status
+code (1 token outside the vocabulary, 2 context exceeded, as fbs_core.h:625-628) and message.
+There is no fallback: a missing library or device raises.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+from .cabi import Image
+
+PKG = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG, "lib", "libuor_fbs_hip.so")
+
+P = C.c_void_p
+_lib = None
+
+# Every entry point include/uor_fbs.h declares (checked by the CPU tests).
+SYMBOLS = (
+    "uor_fbs_abi_version", "uor_fbs_sizeof_model", "uor_fbs_sizeof_layer", "uor_fbs_sizeof_ext",
+    "uor_fbs_last_error", "uor_fbs_model_create", "uor_fbs_model_destroy", "uor_fbs_state_words",
+    "uor_fbs_history_words", "uor_fbs_sequences", "uor_fbs_sequences_async", "uor_fbs_decode",
+    "uor_fbs_decode_async", "uor_fbs_score", "uor_fbs_score_async",
+)
+
+
+class FbsError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"uor_fbs status {code}: {message}")
+        self.code = code
+
+
+def lib():
+    """The loaded library (raises if it is not built: there is no other implementation)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FileNotFoundError(f"{LIB_PATH} is not built (python -c 'import __graft_entry__ as g; g.build()')")
+        L = C.CDLL(LIB_PATH)
+        L.uor_fbs_abi_version.restype = C.c_uint32
+        L.uor_fbs_sizeof_model.restype = C.c_int64
+        L.uor_fbs_sizeof_layer.restype = C.c_int64
+        L.uor_fbs_sizeof_ext.restype = C.c_int64
+        L.uor_fbs_last_error.restype = C.c_char_p
+        L.uor_fbs_model_create.argtypes = [P, P, C.c_int32, C.POINTER(P)]
+        L.uor_fbs_model_destroy.argtypes = [P]
+        L.uor_fbs_model_destroy.restype = None
+        L.uor_fbs_state_words.argtypes = [P]
+        L.uor_fbs_state_words.restype = C.c_uint64
+        L.uor_fbs_history_words.argtypes = [P]
+        L.uor_fbs_history_words.restype = C.c_uint64
+        L.uor_fbs_sequences.argtypes = [P, P, C.c_uint32, C.c_uint32, P, P, P]
+        L.uor_fbs_sequences_async.argtypes = [P, P, C.c_uint32, C.c_uint32, P, P, P, P, P]
+        L.uor_fbs_decode.argtypes = [P, P, C.c_uint32, C.c_uint32, C.c_uint32, P, P, P, P, P, P, P]
+        L.uor_fbs_decode_async.argtypes = [P, P, C.c_uint32, C.c_uint32, C.c_uint32, P, P, P, P, P,
+                                           P, P, P, P]
+        L.uor_fbs_score.argtypes = [P, P, C.c_uint64, C.c_uint32, P, P]
+        L.uor_fbs_score_async.argtypes = [P, P, C.c_uint64, C.c_uint32, P, P, P, P]
+        _lib = L
+    return _lib
+
+
+def _vp(a):
+    return None if a is None else a.ctypes.data_as(P)
+
+
+def _check(code: int):
+    if code:
+        raise FbsError(code, lib().uor_fbs_last_error().decode())
+
+
+class Model:
+    """A model on one HIP device (IntegerStackModel + DeviceEvaluator in one handle)."""
+
+    def __init__(self, art, device: int = 0, image: Image | None = None):
+        self.art = art
+        self.image = image or Image(art)
+        h = P()
+        ext = C.byref(self.image.ext) if self.image.ext is not None else None
+        _check(lib().uor_fbs_model_create(C.byref(self.image.model), ext, device, C.byref(h)))
+        self.handle = h
+        s = art.spec
+        self.width, self.layers, self.window = s.width, s.layers, s.window
+        self.probes = art.probes
+
+    def close(self):
+        if self.handle:
+            lib().uor_fbs_model_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def state_words(self) -> int:
+        return int(lib().uor_fbs_state_words(self.handle))
+
+    @property
+    def history_words(self) -> int:
+        return int(lib().uor_fbs_history_words(self.handle))
+
+    def sequences(self, tokens, want_kept=True, want_query=True):
+        """Teacher-forced runs from fresh sessions: (tokens [S,len], kept [S,len,P], query [S,len,d])."""
+        tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+        S, n = tokens.shape
+        out_t = np.zeros((S, n), np.uint32)
+        out_k = np.zeros((S, n, self.probes), np.uint32) if want_kept else None
+        out_q = np.zeros((S, n, self.width), np.int32) if want_query else None
+        _check(lib().uor_fbs_sequences(self.handle, _vp(tokens), S, n, _vp(out_t), _vp(out_k), _vp(out_q)))
+        return out_t, out_k, out_q
+
+    def decode(self, prompts, gen: int, in_state=None, in_history=None, in_position=None,
+               want_state: bool = True):
+        """Greedy decode: dict(reply [S, gen+1], state, history, position)."""
+        prompts = np.ascontiguousarray(prompts, dtype=np.uint32)
+        S, plen = prompts.shape
+        reply = np.zeros((S, gen + 1), np.uint32)
+        state = np.zeros((S, self.state_words), np.int64) if want_state else None
+        hist = np.zeros((S, self.history_words), np.int32) if want_state else None
+        pos = np.zeros(S, np.uint32) if want_state else None
+        conv = lambda a, t: None if a is None else np.ascontiguousarray(a, dtype=t)  # noqa: E731
+        in_state, in_history, in_position = conv(in_state, np.int64), conv(in_history, np.int32), conv(in_position, np.uint32)
+        _check(lib().uor_fbs_decode(self.handle, _vp(prompts), S, plen, gen, _vp(reply),
+                                    _vp(in_state), _vp(in_history), _vp(in_position), _vp(state),
+                                    _vp(hist), _vp(pos)))
+        return dict(reply=reply, state=state, history=hist, position=pos)
+
+    def score(self, rows, want_argmin=True):
+        """Teacher-forced scoring: (matches, argmin [n, len] or None)."""
+        rows = np.ascontiguousarray(rows, dtype=np.uint32)
+        n, length = rows.shape
+        argmin = np.zeros((n, length), np.uint32) if want_argmin else None
+        matches = np.zeros(1, np.uint64)
+        _check(lib().uor_fbs_score(self.handle, _vp(rows), n, length, _vp(argmin), _vp(matches)))
+        return int(matches[0]), argmin
