@@ -1,0 +1,220 @@
+#!/usr/bin/env python3
+"""Decoded tokens/s of the integer SpiralCore/FBS decode path on one MI355X.
+
+Workload (BASELINE.json's metric: batch 1,024 at width 256): the width-256 artifact of config 3
+(64 quaternions, 6 layers, mlp 384, vocab 32,768, window 16, 256 Zipf-sized drawers probing 8,
+max 512 members, int32 Q16.16 residual, int64 Q32 state, i16 Q12 writer table), 1,024
+independent sequences, Zipf(1.1) prompts of 1,024 tokens, 1,024 greedy decode steps.
+
+Protocol (the reference's fbs-toks, crates/uor-r4-integer/src/bin/fbs-toks.rs:1510-1533): the
+prompt is prefilled once (untimed setup; its last choice starts the reply), then each timed
+step decodes `gen` greedy tokens for the whole batch from that prefilled state, each step
+feeding back the previous choice. value = batch x gen / step time. Inputs and state are
+resident in HBM before the timed region; the step is one launch of the decode kernel, timed by
+HIP events on its stream.
+
+The same line carries the roofline of that kernel (algorithmic bytes per token x tokens per
+launch / launch time, against MI355X's 8 TB/s) and the CPU baseline: the oracle (a C
+restatement of the reference's step, one sequence per thread) timed on this host over a
+bounded sample of the same decode, whose replies must equal the GPU's.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from dataclasses import replace
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [os.path.join(ROOT, "uor-r4_amd"), os.path.join(ROOT, "oracle")]
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=3)
+    p.add_argument("--warmup", type=int, default=1)
+    p.add_argument("--config", default="c3", choices=["c2", "c3", "c5"])
+    p.add_argument("--batch", type=int, default=1024)
+    p.add_argument("--prompt", type=int, default=1024)
+    p.add_argument("--gen", type=int, default=1024)
+    p.add_argument("--seed", type=int, default=2026120203)
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample time")
+    p.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cores)")
+    p.add_argument("--no-cpu", action="store_true")
+    return p.parse_args()
+
+
+def algorithmic_bytes_per_token(spec, mean_candidates: float) -> float:
+    """Bytes one decoded token moves by the path's definition: its input row, the window read
+    and the new history row per layer, the scored candidate rows, the token id. Shared model
+    tables and on-chip state are excluded."""
+    c = 1 if spec.table == "i8" else 2
+    d, L, W = spec.width, spec.layers, spec.window
+    return c * d + L * (W * d * 4 + d * 4) + c * d * mean_candidates + 4
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py: this path runs on one GPU; --gpus {a.gpus} is not supported "
+              "(sequences are independent: shard the batch across GPUs, see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import oracle
+    from uor_fbs import hip, synth
+
+    spec = replace(synth.CONFIGS[a.config], context=a.prompt + a.gen + 1)
+    art = synth.make_artifact(spec, a.seed)
+    if spec.zipf_drawers:
+        prompts = synth.zipf_prompts(spec.vocab, a.batch, a.prompt, a.seed + 1)
+    else:
+        prompts = synth.uniform_prompts(spec.vocab, a.batch, a.prompt, a.seed + 1)
+    model = hip.Model(art, device=0)
+    L = hip.lib()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    sp = C.c_void_p(stream.cuda_stream)
+    B, G = a.batch, a.gen
+    sw, hw = model.state_words, model.history_words
+
+    def ptr(t):
+        return C.c_void_p(t.data_ptr()) if t is not None else None
+
+    def u32(arr):
+        return torch.from_numpy(np.ascontiguousarray(arr, np.uint32).view(np.int32)).to(dev)
+
+    d_prompts = u32(prompts)
+    state = torch.zeros((B, sw), dtype=torch.int64, device=dev)
+    hist = torch.zeros((B, hw), dtype=torch.int32, device=dev)
+    pos = torch.zeros(B, dtype=torch.int32, device=dev)
+    first = torch.zeros((B, 1), dtype=torch.int32, device=dev)
+    status = torch.zeros(B, dtype=torch.int32, device=dev)
+
+    def check(code):
+        if code:
+            raise hip.FbsError(code, L.uor_fbs_last_error().decode())
+
+    # Prefill (setup): the whole prompt, its last choice is the reply's first token.
+    t0 = time.perf_counter()
+    check(L.uor_fbs_decode_async(model.handle, ptr(d_prompts), B, a.prompt, 0, ptr(first), None,
+                                 None, None, ptr(state), ptr(hist), ptr(pos), ptr(status), sp))
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    assert int(status.abs().sum()) == 0, "prefill failed"
+
+    reply = torch.zeros((B, G), dtype=torch.int32, device=dev)
+
+    def step():
+        # `gen` greedy steps: the first feeds the prefill's choice, each later one the last.
+        check(L.uor_fbs_decode_async(model.handle, ptr(first), B, 1, G - 1, ptr(reply), ptr(state),
+                                     ptr(hist), ptr(pos), None, None, None, ptr(status), sp))
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(a.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(a.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(a.steps):
+        starts[i].record(stream)
+        step()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    assert int(status.abs().sum()) == 0, "decode failed"
+    launch_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    ms_per_step = wall * 1e3 / a.steps
+    tokens = B * G
+    value = tokens / (ms_per_step / 1e3)
+
+    # Candidate rows per decoded token, exactly, from a teacher-forced replay of a sample of
+    # the decoded sequences (the replay reproduces the decode's states and kept drawers).
+    host_reply = reply.cpu().numpy().view(np.uint32)
+    sample = min(B, 32)
+    replay = np.concatenate([prompts[:sample], host_reply[:sample, :-1]], axis=1)
+    _, kept, _ = model.sequences(replay, want_query=False)
+    sizes = art.drawer_sizes()
+    cand = sizes[kept[:, a.prompt:, :].astype(np.int64)].sum(-1)
+    mean_cand = float(cand.mean())
+    bpt = algorithmic_bytes_per_token(spec, mean_cand)
+    mean_launch_s = float(np.mean(launch_ms)) / 1e3
+    achieved = bpt * tokens / mean_launch_s / 1e9
+
+    out = {
+        "metric": "decoded tokens/sec at batch 1024, width 256 (1 GPU)",
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int64",
+        "data": "synthetic (seeded integer artifact and Zipf prompts)",
+        "config": {
+            "workload": f"{a.config} artifact at batch {B}: prefilled {a.prompt}-token prompts, "
+                        f"{G} greedy decode steps per timed step",
+            "width": spec.width, "layers": spec.layers, "mlp": spec.mlp, "vocab": spec.vocab,
+            "window": spec.window, "drawers": art.drawers, "probes": art.probes,
+            "table": spec.table, "batch": B, "prompt": a.prompt, "gen": G,
+            "parallelism": "none (1 GPU)",
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "bytes_per_token": round(bpt, 1), "mean_candidate_rows": round(mean_cand, 1),
+            "kernel": "fbs_run<1>", "launch_ms": [round(x, 3) for x in launch_ms],
+        },
+        "prefill_tokens_per_s": round(B * a.prompt / prefill_s, 1),
+    }
+
+    if not a.no_cpu:
+        threads = a.cpu_threads or min(16, os.cpu_count() or 1)
+        st_np = state.cpu().numpy()
+        hist_np = hist.cpu().numpy()
+        pos_np = pos.cpu().numpy().view(np.uint32)
+        first_np = first.cpu().numpy().view(np.uint32)
+        # Calibrate: a small run, then a sample sized to about --cpu-seconds.
+        n_cal, g_cal = min(B, threads), min(G, 4)
+        t0 = time.perf_counter()
+        oracle.decode(art, first_np[:n_cal], g_cal - 1, threads=threads, in_state=st_np[:n_cal],
+                      in_history=hist_np[:n_cal], in_position=pos_np[:n_cal], want_state=False)
+        per_tok = (time.perf_counter() - t0) / (n_cal * g_cal)
+        g_cpu = min(G, 64)
+        n_cpu = int(max(threads, min(B, a.cpu_seconds / per_tok / g_cpu)))
+        n_cpu = min(B, max(1, (n_cpu // threads) * threads))
+        t0 = time.perf_counter()
+        res = oracle.decode(art, first_np[:n_cpu], g_cpu - 1, threads=threads,
+                            in_state=st_np[:n_cpu], in_history=hist_np[:n_cpu],
+                            in_position=pos_np[:n_cpu], want_state=False)
+        cpu_s = time.perf_counter() - t0
+        assert res["status"] == 0
+        same = np.array_equal(res["reply"], host_reply[:n_cpu, :g_cpu])
+        out["cpu_baseline"] = {
+            "value": round(n_cpu * g_cpu / cpu_s, 1), "unit": "tokens/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{n_cpu} of the {B} prefilled sequences x the first {g_cpu} decode steps "
+                      f"({cpu_s:.1f} s), oracle C restatement, one sequence per thread",
+            "replies_equal_gpu": bool(same),
+        }
+        if not same:
+            print("bench.py: CPU replies differ from the GPU's", file=sys.stderr)
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()
