@@ -22,6 +22,7 @@
 namespace fbs {
 hipError_t launch_run(const DevModel &M, const RunArgs &A, uint32_t grid, size_t lds_bytes,
                       hipStream_t stream);
+size_t lds_bytes(const DevModel &M);
 }
 
 using namespace fbs;
@@ -259,6 +260,7 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
   M.nslots = 21 * Q + 8 * MP;
   M.xbar_words = 2 * (d > mlp ? d : mlp);
   M.identity_rows = r.head == 1;
+  M.taps_fast = 1;
   for (int sh = 0; sh <= 8; sh++) M.eps_int[sh] = norm_eps(m->eps_mantissa, m->eps_exp, sh);
 
   auto done = [&](int code) {
@@ -277,6 +279,20 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
     if ((st = h->upload(ly.mlp_gain, d, &dl.mlp_gain))) return done(st);
     const int16_t *taps = (e && e->wide_taps) ? e->wide_taps[l] : ly.taps;
     if ((st = h->upload(taps, (size_t)(r.W + 1) * d, &dl.taps))) return done(st);
+    {
+      std::vector<uint16_t> td((size_t)(r.W + 1) * d), rg(d), mg(d);
+      for (size_t i = 0; i < td.size(); i++) {
+        td[i] = grid_desc(taps[i]);
+        if (td[i] == kGridDescSlow) M.taps_fast = 0;
+      }
+      for (uint32_t i = 0; i < d; i++) {
+        rg[i] = grid_desc(ly.rec_gain[i]);
+        mg[i] = grid_desc(ly.mlp_gain[i]);
+      }
+      if ((st = h->upload(td.data(), td.size(), &dl.taps_desc))) return done(st);
+      if ((st = h->upload(rg.data(), rg.size(), &dl.rec_gain_desc))) return done(st);
+      if ((st = h->upload(mg.data(), mg.size(), &dl.mlp_gain_desc))) return done(st);
+    }
     if ((st = h->upload(ly.conv_bias, d, &dl.conv_bias))) return done(st);
     if ((st = h->upload(ly.gate_bias, d / 4 + d, &dl.gate_bias))) return done(st);
     if ((st = h->upload(ly.decay_offset, d / 4, &dl.decay_offset))) return done(st);
@@ -308,6 +324,11 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
   }
   if ((st = h->upload(layers.data(), layers.size(), &M.layers))) return done(st);
   if ((st = h->upload(m->final_gain, d, &M.final_gain))) return done(st);
+  {
+    std::vector<uint16_t> fg(d);
+    for (uint32_t i = 0; i < d; i++) fg[i] = grid_desc(m->final_gain[i]);
+    if ((st = h->upload(fg.data(), fg.size(), &M.final_gain_desc))) return done(st);
+  }
 
   // Writer table, biased for the unsigned SAD (row value v stored as v ^ 0x8000).
   {
@@ -367,7 +388,7 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
   hipDeviceProp_t prop;
   he = hipGetDeviceProperties(&prop, device);
   if (he != hipSuccess) return done(hip_fail(he, "hipGetDeviceProperties"));
-  h->lds_bytes = 4ull * M.xbar_words + 4ull * ((r.D + 3) & ~3u) + 8ull * L * d;
+  h->lds_bytes = fbs::lds_bytes(M);
   if (h->lds_bytes > prop.sharedMemPerBlock)
     return done(fail(UOR_FBS_ERR_UNSUPPORTED, "%zu bytes of LDS per sequence exceed %zu",
                      h->lds_bytes, (size_t)prop.sharedMemPerBlock));

@@ -2,7 +2,8 @@
 // the kernels (fbs_kernel.hip) and the host side that builds them (fbs_api.cpp).
 //
 // Layout in HBM (all tables uploaded once by uor_fbs_model_create, read by every sequence):
-//   per layer: gains (d i16), window taps ((W+1) x d i16, tap s = s positions back),
+//   per layer: gains (d i16), window taps ((W+1) x d i16, tap s = s positions back) and the
+//              grid_desc form of both (fbs_int.h),
 //              conv_bias (d i32), gate_bias (d/4 + d i32), decay_offset (d/4 i32), and the
 //              layer's gather program: [slot][64 lanes] u16 LDS word indices that carry out the
 //              six FBS projections (stack_fbs_gather, session.rs:4037-4053) for this lane mapping;
@@ -36,6 +37,9 @@ struct DevLayer {
   const int32_t *gate_bias;     // d/4 + d
   const int32_t *decay_offset;  // d/4
   const uint16_t *prog;         // nslots * 64
+  const uint16_t *taps_desc;    // grid_desc of taps
+  const uint16_t *rec_gain_desc;
+  const uint16_t *mlp_gain_desc;
 };
 
 struct DevModel {
@@ -44,9 +48,11 @@ struct DevModel {
   uint32_t nslots, s_rec_in, s_rec_gate, s_rec_out, s_mlp_gate, s_mlp_up, s_mlp_down;
   uint32_t xbar_words;      // 2 * max(d, m)
   uint32_t identity_rows;   // the nearest head: one drawer holding every token
+  uint32_t taps_fast;       // every window tap has a descriptor (grid_desc != kGridDescSlow)
   int64_t eps_int[9];       // RMSNorm epsilon at each pre-shift 0..8
   const DevLayer *layers;   // L entries
   const int16_t *final_gain;
+  const uint16_t *final_gain_desc;
   const uint16_t *table_b;  // vocab * d, biased
   const int16_t *keys;      // D * 16
   const uint32_t *offsets;  // D + 1

@@ -27,11 +27,41 @@ uint64_t fbs_hp_recip_q63(uint32_t d) { return recip_q63(d); }
 
 int64_t fbs_hp_shift(int64_t v, int32_t s) { return shift(v, s); }
 int64_t fbs_hp_grid_apply(int64_t v, int16_t code) { return grid_apply(v, code); }
+int64_t fbs_hp_grid32_desc(int32_t v, int16_t code) { return grid_apply32_desc(v, grid_desc(code), code); }
+int64_t fbs_hp_grid64_desc(int64_t v, int16_t code) { return grid_apply64_desc(v, grid_desc(code), code); }
+
+// Every valid grid code against n inputs v[]: mismatches of the descriptor forms.
+uint64_t fbs_hp_grid_check(const int64_t *v, uint64_t n) {
+  uint64_t bad = 0;
+  for (int32_t code = -2047; code <= 2047; code++) {
+    uint32_t field = (uint32_t)(code < 0 ? -code : code) >> 4;
+    if (code != 0 && (field < 1 || field > 127)) continue;
+    uint16_t d = grid_desc((int16_t)code);
+    for (uint64_t i = 0; i < n; i++) {
+      bad += grid_apply64_desc(v[i], d, (int16_t)code) != grid_apply(v[i], (int16_t)code);
+      int32_t v32 = (int32_t)v[i];
+      bad += grid_apply32_desc(v32, d, (int16_t)code) != grid_apply((int64_t)v32, (int16_t)code);
+    }
+  }
+  return bad;
+}
 
 // rotation(raw, lambda, eps) for n quaternions: raw n*4 i32, out n*4 i64.
 void fbs_hp_rotation_many(const int32_t *raw, uint64_t lambda, uint64_t eps, int64_t *out,
                           uint64_t n) {
   for (uint64_t i = 0; i < n; i++) rotation(raw + 4 * i, lambda, eps, out + 4 * i);
+}
+
+// unit_q30 (64-bit form) against unit_q30_wide on n quaternions: the number of differing lanes.
+uint64_t fbs_hp_unit_check(const int32_t *raw, uint64_t eps, uint64_t n) {
+  uint64_t bad = 0;
+  for (uint64_t i = 0; i < n; i++) {
+    int32_t a[4], b[4];
+    unit_q30(raw + 4 * i, eps, a);
+    unit_q30_wide(raw + 4 * i, eps, b);
+    for (int c = 0; c < 4; c++) bad += a[c] != b[c];
+  }
+  return bad;
 }
 
 void fbs_hp_snap_rotation_many(const int8_t *ico, const int32_t *raw, uint64_t lambda,
@@ -69,7 +99,7 @@ void fbs_hp_rms_norm_fine(const int32_t *x, uint32_t n, int64_t eps_m, int32_t e
     sum += uabs64(y) * uabs64(y);
   }
   NormFactor f = norm_factor(sum, n, norm_eps(eps_m, eps_e, sh));
-  for (uint32_t i = 0; i < n; i++) out[i] = norm_apply(f, out[i]);
+  for (uint32_t i = 0; i < n; i++) out[i] = norm_apply24(f, out[i]);
 }
 
 }  // extern "C"

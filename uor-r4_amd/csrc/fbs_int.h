@@ -108,6 +108,45 @@ FBS_HD int64_t grid_apply(int64_t v, int16_t code) {
 // The same for a 32-bit input, whose product (16 + m) v never wraps.
 FBS_HD int64_t grid_apply32(int32_t v, int16_t code) { return grid_apply((int64_t)v, code); }
 
+// A grid code prepared for the kernels (16 bits): bits 0-5 the multiplier 16 + m (0 for the zero
+// code), bit 6 the sign, bits 7-12 the right shift sh = 4 - e. With the sign folded in,
+// grid_apply(v, code) = (v (+-(16 + m)) + 2^(sh-1) - [code < 0]) >> sh, because
+// -floor((p + 2^(sh-1)) / 2^sh) = floor((-p + 2^(sh-1) - 1) / 2^sh). The form holds whenever
+// 1 <= sh <= 62 and |v| (16 + m) + 2^(sh-1) < 2^63: always for a 32-bit v, and for a 64-bit v
+// below 2^57 in magnitude. `grid_desc` returns kGridDescSlow for a code outside 1 <= sh <= 62.
+constexpr uint16_t kGridDescSlow = 0xffff;
+
+FBS_HD uint16_t grid_desc(int16_t code) {
+  if (code == 0) return (uint16_t)(1u << 7);  // multiplier 0, shift 1: (0 + 1) >> 1 = 0
+  uint32_t c = code < 0 ? (uint32_t)(-(int32_t)code) : (uint32_t)code;
+  int32_t sh = 4 - ((int32_t)(c >> 4) - kGridExpBias);
+  if (sh < 1 || sh > 62) return kGridDescSlow;
+  return (uint16_t)((16 + (c & 15)) | (code < 0 ? 64u : 0u) | ((uint32_t)sh << 7));
+}
+
+FBS_HD int64_t grid_desc_apply(int64_t v, uint16_t desc) {
+  const int32_t mag = desc & 63, neg = (desc >> 6) & 1;
+  const uint32_t sh = (desc >> 7) & 63;
+  const int32_t mul = (mag ^ -neg) + neg;
+  return (v * mul + (((int64_t)1 << (sh - 1)) - neg)) >> sh;
+}
+
+// grid_apply for a 32-bit input through its descriptor (every valid code has one or is slow).
+FBS_HD int64_t grid_apply32_desc(int32_t v, uint16_t desc, int16_t code) {
+  if (desc == kGridDescSlow) return grid_apply((int64_t)v, code);
+  const int32_t mag = desc & 63, neg = (desc >> 6) & 1;
+  const uint32_t sh = (desc >> 7) & 63;
+  const int32_t mul = (mag ^ -neg) + neg;
+  return ((int64_t)v * (int64_t)mul + (((int64_t)1 << (sh - 1)) - neg)) >> sh;
+}
+
+// grid_apply for a 64-bit input: the descriptor form below 2^57, the reference routine above.
+FBS_HD int64_t grid_apply64_desc(int64_t v, uint16_t desc, int16_t code) {
+  if (desc == kGridDescSlow || v >= ((int64_t)1 << 57) || v <= -((int64_t)1 << 57))
+    return grid_apply(v, code);
+  return grid_desc_apply(v, desc);
+}
+
 // ---------------------------------------------------------------------------------------------
 // Reciprocal and reciprocal-square-root seeds (compile-time tables, no floating point).
 
@@ -161,9 +200,9 @@ FBS_HD uint32_t rsqrt_q46(uint32_t t) {
 #pragma unroll
   for (int it = 0; it < 2; it++) {
     // Newton: y <- y (3 - t y^2 / 2^92) / 2, with p = t y^2 / 2^60 ~ 2^32.
-    uint64_t y2 = y * y;                                   // <= 2^62
-    uint64_t p = (uint64_t)(((u128)t * (y2 >> 28)) >> 32);  // ~ 2^32
-    uint64_t f = ((3ull << 32) - p) >> 1;                   // ~ 2^32
+    uint64_t y2 = (y * y) >> 32;                   // y^2 / 2^32 <= 2^30
+    uint64_t p = ((uint64_t)t * y2) >> 28;         // ~ 2^32
+    uint64_t f = ((3ull << 32) - p) >> 1;          // ~ 2^32
     y = (y * f) >> 32;
     if (y > (1ull << 31)) y = 1ull << 31;
     if (y < (1ull << 30)) y = 1ull << 30;
@@ -179,7 +218,7 @@ FBS_HD uint64_t recip_q63(uint32_t d) {
   for (int it = 0; it < 2; it++) {
     // Newton: w <- w + w (2^63 - d w) / 2^63.
     int64_t e = (int64_t)((1ull << 63) - (uint64_t)d * w);
-    w = (uint64_t)((int64_t)w + (int64_t)(((i128)e * (int64_t)w) >> 63));
+    w = (uint64_t)((int64_t)w + (((e >> 31) * (int64_t)w) >> 32));
   }
   return w;
 }
@@ -308,6 +347,19 @@ FBS_HD int64_t norm_apply(NormFactor f, int64_t y) {
   return (int64_t)r;
 }
 
+// norm_apply for |y| < 2^24 (every pre-shifted norm input) and r < 2^62 (every factor but the
+// huge one): with P = r |y| = A + B 2^32 (A = r_lo |y|, B = r_hi |y|), floor((P + h) / 2^38) =
+// floor((B + floor((A + h) / 2^32)) / 2^6); h = 2^37 for y >= 0, 2^37 - 1 for the negated form
+// (floor((-P + 2^37) / 2^38) = -floor((P + 2^37 - 1) / 2^38)).
+FBS_HD int64_t norm_apply24(NormFactor f, int64_t y) {
+  if (f.huge) return norm_apply(f, y);
+  const uint32_t u = (uint32_t)(y < 0 ? -y : y);
+  const uint64_t A = (uint64_t)(uint32_t)f.r * u, B = (f.r >> 32) * (uint64_t)u;
+  const uint64_t h = y < 0 ? (1ull << 37) - 1 : (1ull << 37);
+  const int64_t mag = (int64_t)((B + ((A + h) >> 32)) >> 6);
+  return y < 0 ? -mag : mag;
+}
+
 // eps at the square exponent of pre-shift sh (kernels.rs:596-602): shift(mantissa,
 // (2 (-16 + sh)) - eps_exp), never negative.
 FBS_HD int64_t norm_eps(int64_t eps_mantissa, int32_t eps_exp, int32_t sh) {
@@ -414,10 +466,10 @@ FBS_HD void snap_rotation(const int8_t *ico, const int32_t raw[4], uint64_t lamb
   }
 }
 
-// The unit quaternion of `stack_rotation` at Q30 before lambda (RS stack/session.rs:5165-5181):
+// The unit quaternion of `stack_rotation` at Q30 before lambda, in 128-bit arithmetic (RS stack/session.rs:5165-5181):
 // u_c = sign(v_c) floor(|v_c| 2^46 / s), s = isqrt((sum v^2 + eps) << 32); all zero for s = 0.
 // |u_c| <= 2^30 and sum u_c^2 <= 2^60.
-FBS_HD void unit_q30(const int32_t raw[4], uint64_t eps, int32_t u[4]) {
+FBS_HD void unit_q30_wide(const int32_t raw[4], uint64_t eps, int32_t u[4]) {
   u128 square = eps;
 #pragma unroll
   for (int c = 0; c < 4; c++) square += (u128)((uint64_t)((int64_t)raw[c] * raw[c]));
@@ -428,6 +480,85 @@ FBS_HD void unit_q30(const int32_t raw[4], uint64_t eps, int32_t u[4]) {
     uint64_t a = uabs32(raw[c]);
     uint64_t m = s == 0 ? 0 : divq((u128)a << 46, dv);
     u[c] = raw[c] < 0 ? -(int32_t)m : (int32_t)m;
+  }
+}
+
+// unit_q30 in 64-bit arithmetic (the kernels' form; equal to unit_q30_wide for every input).
+// X = sum v^2 + eps < 2^65 + 2^13 is normalised to Xn = X 4^k in [2^62, 2^64); r = isqrt(Xn)
+// comes from the 32-bit reciprocal square root and one Newton step on the exact remainder;
+// s = isqrt(X 2^32) = isqrt(Xn 4^(16 - k)) is r shifted, or r 2^j plus the j fractional bits f
+// of the root, estimated from the remainder and checked exactly; each quotient comes from a
+// 32-bit reciprocal of s and is corrected on its exact remainder (small, so its low 64 bits
+// are the remainder).
+FBS_HD void unit_q30(const int32_t raw[4], uint64_t eps, int32_t u[4]) {
+  uint32_t a[4];
+  uint64_t xl = eps;
+  uint32_t xh = 0;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    a[c] = uabs32(raw[c]);
+    uint64_t t = xl + (uint64_t)a[c] * a[c];
+    xh += t < xl;
+    xl = t;
+  }
+  if ((xh | xl) == 0) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) u[c] = 0;
+    return;
+  }
+  int k;
+  uint64_t xn;
+  if (xh) {  // X in [2^64, 2^65 + 2^13): Xn = X / 4 (truncated; only the estimate uses it)
+    xn = ((uint64_t)xh << 62) | (xl >> 2);
+    k = -1;
+  } else {
+    int z = clz64(xl) & ~1;
+    xn = xl << z;
+    k = z >> 1;
+  }
+  uint64_t y = rsqrt_q46((uint32_t)(xn >> 32));      // 2^46 / sqrt(Xn / 2^32)
+  uint64_t r = ((xn >> 32) * y) >> 30;               // ~ sqrt(Xn) < 2^32
+  if (r > 0xffffffffull) r = 0xffffffffull;
+  int64_t diff = (int64_t)(xn - r * r);
+  r = (uint64_t)((int64_t)r + (((diff >> 16) * (int64_t)y) >> 47));
+  if (r > 0xffffffffull) r = 0xffffffffull;
+  if (r < (1ull << 31)) r = 1ull << 31;
+  while (r * r > xn) r--;
+  while (r < 0xffffffffull && (r + 1) * (r + 1) <= xn) r++;
+  uint64_t s;
+  const int j = 16 - k;                               // [-15, 17]
+  if (j <= 0) {
+    s = r >> (-j);
+  } else {
+    // s = r 2^j + f: the largest f < 2^j with f (2^(j+1) r + f) <= N - (r 2^j)^2, where
+    // N - (r 2^j)^2 = rem 4^j (+ (X mod 4) 2^32 when Xn = floor(X / 4), j = 17).
+    uint64_t rem = xn - r * r;                        // [0, 2 r]
+    uint64_t f = (rem * y) >> (63 - j);               // ~ rem 2^(j-1) / r
+    const uint64_t fmax = (1ull << j) - 1;
+    if (f > fmax) f = fmax;
+    const u128 lim = ((u128)rem << (2 * j)) + (xh ? (u128)(xl & 3) << 32 : (u128)0);
+    const uint64_t base = r << (j + 1);
+    while (f > 0 && (u128)f * (base + f) > lim) f--;
+    while (f < fmax && (u128)(f + 1) * (base + f + 1) <= lim) f++;
+    s = (r << j) + f;
+  }
+  // u_c = floor(a_c 2^46 / s), s in [2^16, 2^49].
+  const int zs = clz64(s);
+  const uint64_t w = recip_q63((uint32_t)((s << zs) >> 32));  // ~ 2^95 / (s << zs)
+  const int sh = 49 - zs;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    uint64_t q = ((uint64_t)a[c] * w) >> sh;
+    int64_t rem = (int64_t)(((uint64_t)a[c] << 46) - q * s);
+    while (rem < 0) {
+      q--;
+      rem += (int64_t)s;
+    }
+    while (rem >= (int64_t)s) {
+      q++;
+      rem -= (int64_t)s;
+    }
+    u[c] = raw[c] < 0 ? -(int32_t)q : (int32_t)q;
   }
 }
 

@@ -4,166 +4,96 @@
 // sequences, greedy decode, or scoring). Per step (RS crates/uor-r4-integer/src/stack/
 // session.rs:4129-4403 `stack_step_fbs`; twin fbs_core.h:635-675):
 //   the token's writer row in; per layer the fine RMSNorm and gain, the FBS projections
-//   (gathers through LDS by a precomputed per-lane program), the causal window read from the
-//   sequence's ring in HBM, the quaternion recurrence with its output gate, the shared-exponent
-//   requantize, the residual add, and the same for the Hamilton feed-forward gate; the final
-//   norm, the Q12 query, and the drawer writer (drawer scores, P rounds of lowest (score, drawer),
-//   then the lowest (L1, token) over the kept drawers' CSR members, scanned by lane groups of
-//   d/32 lanes with packed v_sad_u16 on biased rows).
+//   (gathers through LDS by a precomputed per-lane program), the quaternion recurrence with its
+//   output gate and the causal window read from the sequence's ring in HBM, the shared-exponent
+//   requantize and residual add, and the same for the Hamilton feed-forward gate; the final
+//   norm, the Q12 query, and the drawer writer (drawer scores, P rounds of lowest
+//   (score, drawer), then the lowest (L1, token) over the kept drawers' CSR members, scanned by
+//   lane groups of d/32 lanes with packed v_sad_u16 on biased rows).
 // The recurrence state of every layer stays in LDS for the whole run; only the window ring,
-// the table rows and the outputs touch HBM. Every reduction is an exact integer max, sum or
-// lexicographic min, so the outputs do not depend on lane order.
+// the table rows and the outputs touch HBM. Reductions are exact integer max, sum and
+// lexicographic min over DPP lane exchanges, so the outputs do not depend on lane order.
+// A block is one wavefront: lanes hand data to each other through LDS under wavefront-scope
+// fences (LDS operations of a wavefront complete in order), never through a workgroup barrier.
 #include "fbs_device.h"
 #include "fbs_int.h"
 
 namespace fbs {
 
+// ---------------------------------------------------------------------------------------------
+// Wave-level primitives.
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+constexpr int kDppXor1 = 0xb1;        // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4e;        // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within 8
+constexpr int kDppMirror = 0x140;      // lane i <-> 15 - i within 16
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp64(uint64_t v) {
+  uint32_t lo = dpp32<CTRL>((uint32_t)v), hi = dpp32<CTRL>((uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
 __device__ __forceinline__ uint32_t uniform32(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
 }
-__device__ __forceinline__ uint64_t uniform64(uint64_t v) {
-  uint32_t lo = uniform32((uint32_t)v), hi = uniform32((uint32_t)(v >> 32));
-  return ((uint64_t)hi << 32) | lo;
+__device__ __forceinline__ uint32_t lane32(uint32_t v, int l) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, l);
+}
+__device__ __forceinline__ uint64_t lane64(uint64_t v, int l) {
+  return ((uint64_t)lane32((uint32_t)(v >> 32), l) << 32) | lane32((uint32_t)v, l);
 }
 
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    uint32_t w = __shfl_xor(v, o);
-    v = w > v ? w : v;
-  }
-  return uniform32(v);
+struct OpMax {
+  template <class T>
+  __device__ T operator()(T a, T b) const { return a > b ? a : b; }
+};
+struct OpMin {
+  template <class T>
+  __device__ T operator()(T a, T b) const { return a < b ? a : b; }
+};
+struct OpAdd {
+  template <class T>
+  __device__ T operator()(T a, T b) const { return a + b; }
+};
+
+// The op over all 64 lanes, returned uniform: butterflies inside each row of 16, then the four
+// row results read as scalars.
+template <class Op>
+__device__ __forceinline__ uint32_t wave_reduce32(uint32_t v, Op op) {
+  v = op(v, dpp32<kDppXor1>(v));
+  v = op(v, dpp32<kDppXor2>(v));
+  v = op(v, dpp32<kDppHalfMirror>(v));
+  v = op(v, dpp32<kDppMirror>(v));
+  return op(op(lane32(v, 0), lane32(v, 16)), op(lane32(v, 32), lane32(v, 48)));
 }
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    uint32_t w = __shfl_xor(v, o);
-    v = w < v ? w : v;
-  }
-  return uniform32(v);
-}
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    uint64_t w = __shfl_xor((unsigned long long)v, o);
-    v = w > v ? w : v;
-  }
-  return uniform64(v);
-}
-__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    uint64_t w = __shfl_xor((unsigned long long)v, o);
-    v = w < v ? w : v;
-  }
-  return uniform64(v);
-}
-__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += (uint64_t)__shfl_xor((unsigned long long)v, o);
-  return uniform64(v);
+template <class Op>
+__device__ __forceinline__ uint64_t wave_reduce64(uint64_t v, Op op) {
+  v = op(v, dpp64<kDppXor1>(v));
+  v = op(v, dpp64<kDppXor2>(v));
+  v = op(v, dpp64<kDppHalfMirror>(v));
+  v = op(v, dpp64<kDppMirror>(v));
+  return op(op(lane64(v, 0), lane64(v, 16)), op(lane64(v, 32), lane64(v, 48)));
 }
 
-// Fine RMSNorm then the per-channel grid gain, for the lane's channels
-// (RS stack/kernels.rs:569-620, session.rs:4057-4061).
-template <int Q>
-__device__ __forceinline__ void norm_gain(const DevModel &M, const int32_t (&x)[Q][4],
-                                          const bool (&qv)[Q], const uint32_t (&qi)[Q],
-                                          const int16_t *gain, int64_t (&out)[Q][4]) {
-  uint32_t mx = 0;
-#pragma unroll
-  for (int k = 0; k < Q; k++)
-    if (qv[k])
-#pragma unroll
-      for (int c = 0; c < 4; c++) {
-        uint32_t a = uabs32(x[k][c]);
-        mx = a > mx ? a : mx;
-      }
-  mx = wave_max_u32(mx);
-  int32_t sh = bitlen64(mx) - 24;
-  if (sh < 0) sh = 0;
-  uint64_t sum = 0;
-#pragma unroll
-  for (int k = 0; k < Q; k++)
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-      int64_t y = qv[k] ? shift((int64_t)x[k][c], sh) : 0;
-      out[k][c] = y;
-      sum += uabs64(y) * uabs64(y);
-    }
-  sum = wave_sum_u64(sum);
-  NormFactor f = norm_factor(sum, M.d, M.eps_int[sh]);
-  f.r = uniform64(f.r);
-#pragma unroll
-  for (int k = 0; k < Q; k++)
-    if (qv[k]) {
-      short4 g = *(const short4 *)(gain + 4 * qi[k]);
-      int16_t gc[4] = {g.x, g.y, g.z, g.w};
-#pragma unroll
-      for (int c = 0; c < 4; c++) out[k][c] = grid_apply(norm_apply(f, out[k][c]), gc[c]);
-    }
-}
-
-// Publish v (exponent -24) for the FBS gathers: word 2 i + s holds to_exp_i32 of v_i (s = 0)
-// or of its saturating negation (s = 1), at exponent -16 (session.rs:4037-4053: the negation
-// comes before the rounding shift).
-template <int Q>
-__device__ __forceinline__ void publish64(int32_t *xbar, const int64_t (&v)[Q][4],
-                                          const bool (&qv)[Q], const uint32_t (&qi)[Q]) {
-#pragma unroll
-  for (int k = 0; k < Q; k++)
-    if (qv[k]) {
-      int4 p, n;
-      p.x = to_exp_i32(v[k][0], kNormFineExp, kResidualExp);
-      n.x = to_exp_i32(sat_neg64(v[k][0]), kNormFineExp, kResidualExp);
-      p.y = to_exp_i32(v[k][1], kNormFineExp, kResidualExp);
-      n.y = to_exp_i32(sat_neg64(v[k][1]), kNormFineExp, kResidualExp);
-      p.z = to_exp_i32(v[k][2], kNormFineExp, kResidualExp);
-      n.z = to_exp_i32(sat_neg64(v[k][2]), kNormFineExp, kResidualExp);
-      p.w = to_exp_i32(v[k][3], kNormFineExp, kResidualExp);
-      n.w = to_exp_i32(sat_neg64(v[k][3]), kNormFineExp, kResidualExp);
-      int4 *dst = (int4 *)(xbar + 8 * qi[k]);
-      dst[0] = make_int4(p.x, n.x, p.y, n.y);
-      dst[1] = make_int4(p.z, n.z, p.w, n.w);
-    }
-}
-
-// Publish 16-bit activations at exponent `exp` for gather16 (to_exp_i32 of +-a to -16).
-__device__ __forceinline__ void publish16(int32_t *xbar, uint32_t channel0, const int32_t a[4],
-                                          int32_t exp) {
-  int32_t s = kResidualExp - exp;
-  int4 *dst = (int4 *)(xbar + 2 * channel0);
-  dst[0] = make_int4(to_exp_i32(a[0], exp, kResidualExp), to_exp_i32(-(int64_t)a[0], exp, kResidualExp),
-                     to_exp_i32(a[1], exp, kResidualExp), to_exp_i32(-(int64_t)a[1], exp, kResidualExp));
-  dst[1] = make_int4(to_exp_i32(a[2], exp, kResidualExp), to_exp_i32(-(int64_t)a[2], exp, kResidualExp),
-                     to_exp_i32(a[3], exp, kResidualExp), to_exp_i32(-(int64_t)a[3], exp, kResidualExp));
-  (void)s;
-}
-
-__device__ __forceinline__ int32_t gather1(const int32_t *xbar, const uint16_t *prog,
-                                           uint32_t slot, uint32_t lane) {
-  return xbar[prog[slot * kWave + lane]];
-}
-
-// A rotation of the gate kind (lambda 2^31, epsilon 0) applied to rhs: shift_wide(q (x) rhs, 15)
-// (session.rs:4951-4968, :4005-4025). Raw gates use q = 2 u exactly, so the product is formed
-// from u and shifted by 14.
-__device__ __forceinline__ void gate_apply(const DevModel &M, const int32_t raw[4],
-                                           const int64_t rhs[4], int64_t out[4]) {
-  i128 prod[4];
-  if (M.raw_gates) {
-    int32_t u[4];
-    unit_q30(raw, kGateEps, u);
-    hamilton32(u, rhs, prod);
-#pragma unroll
-    for (int c = 0; c < 4; c++) out[c] = shift_wide(prod[c], 14);
-  } else {
-    int64_t q[4];
-    snap_rotation(M.icosian, raw, 1ull << 31, q);
-    hamilton64(q, rhs, prod);
-#pragma unroll
-    for (int c = 0; c < 4; c++) out[c] = shift_wide(prod[c], 15);
-  }
+// Sum over aligned groups of S lanes (S a power of two), every lane of a group getting it.
+__device__ __forceinline__ uint32_t group_sum(uint32_t v, uint32_t S) {
+  if (S >= 2) v += dpp32<kDppXor1>(v);
+  if (S >= 4) v += dpp32<kDppXor2>(v);
+  if (S >= 8) v += dpp32<kDppHalfMirror>(v);
+  if (S >= 16) v += dpp32<kDppMirror>(v);
+  if (S >= 32) v += (uint32_t)__shfl_xor((int)v, 16);
+  if (S >= 64) v += (uint32_t)__shfl_xor((int)v, 32);
+  return v;
 }
 
 // v_sad_u16 on gfx950 sums the absolute differences of both 16-bit halves:
@@ -175,36 +105,192 @@ __device__ __forceinline__ uint32_t sad2_u16(uint32_t a, uint32_t b, uint32_t c)
   return d;
 }
 
-// The candidate scan of the writer over members [beg, end) (or token ids beg..end for the
-// nearest head): lane group g = lane / S scores one row per round, lane sub = lane % S its
-// 32 channels (16 biased pairs against the packed biased query); the group sums its partial
-// L1s and keeps the lowest (L1, token).
-__device__ __forceinline__ uint64_t scan_rows(const DevModel &M, const uint32_t (&qpk)[16],
-                                              uint32_t beg, uint32_t end, uint32_t S,
-                                              uint32_t grp, uint32_t sub, bool seg_ok,
-                                              uint32_t rows, uint64_t best) {
-  const uint32_t d = M.d;
-  for (uint32_t i0 = beg; i0 < end; i0 += rows) {
-    uint32_t i = i0 + grp;
-    bool ok = i < end;
-    uint32_t t = ok ? (M.identity_rows ? i : M.members[i]) : 0u;
-    uint32_t acc = 0;
-    if (seg_ok) {
-      const uint4 *row = (const uint4 *)(M.table_b + (uint64_t)t * d + 32u * sub);
-      uint4 r[4];
+// ---------------------------------------------------------------------------------------------
+// Step pieces.
+
+// Fine RMSNorm then the per-channel grid gain, for the lane's channels
+// (RS stack/kernels.rs:569-620, session.rs:4057-4061). gain: the lane's 4 codes per quaternion.
+template <int Q>
+__device__ __forceinline__ void norm_gain(const DevModel &M, const int32_t (&x)[Q][4],
+                                          const bool (&qv)[Q], const short4 (&gain)[Q],
+                                          const ushort4 (&gdesc)[Q], int64_t (&out)[Q][4]) {
+  uint32_t mx = 0;
 #pragma unroll
-      for (int w = 0; w < 4; w++) r[w] = row[w];
+  for (int k = 0; k < Q; k++)
+    if (qv[k])
 #pragma unroll
-      for (int w = 0; w < 4; w++) {
-        acc = sad2_u16(r[w].x, qpk[4 * w + 0], acc);
-        acc = sad2_u16(r[w].y, qpk[4 * w + 1], acc);
-        acc = sad2_u16(r[w].z, qpk[4 * w + 2], acc);
-        acc = sad2_u16(r[w].w, qpk[4 * w + 3], acc);
+      for (int c = 0; c < 4; c++) {
+        uint32_t a = uabs32(x[k][c]);
+        mx = a > mx ? a : mx;
       }
+  mx = wave_reduce32(mx, OpMax());
+  int32_t sh = bitlen64(mx) - 24;
+  if (sh < 0) sh = 0;
+  uint64_t sum = 0;
+#pragma unroll
+  for (int k = 0; k < Q; k++)
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      int64_t y = qv[k] ? shift((int64_t)x[k][c], sh) : 0;
+      out[k][c] = y;
+      sum += uabs64(y) * uabs64(y);
     }
-    for (uint32_t o = 1; o < S; o <<= 1) acc += __shfl_xor(acc, (int)o);
-    uint64_t cand = ((uint64_t)acc << 32) | t;
-    if (ok && cand < best) best = cand;
+  sum = wave_reduce64(sum, OpAdd());
+  NormFactor f = norm_factor(sum, M.d, M.eps_int[sh]);
+#pragma unroll
+  for (int k = 0; k < Q; k++) {
+    const int16_t gc[4] = {gain[k].x, gain[k].y, gain[k].z, gain[k].w};
+    const uint16_t gd[4] = {gdesc[k].x, gdesc[k].y, gdesc[k].z, gdesc[k].w};
+#pragma unroll
+    for (int c = 0; c < 4; c++) out[k][c] = grid_apply64_desc(norm_apply24(f, out[k][c]), gd[c], gc[c]);
+  }
+}
+
+// Publish v (exponent -24) for the FBS gathers: word 2 i + s holds to_exp_i32 of v_i (s = 0)
+// or of its saturating negation (s = 1), at exponent -16 (session.rs:4037-4053: the negation
+// comes before the rounding shift).
+template <int Q>
+__device__ __forceinline__ void publish64(int32_t *xbar, const int64_t (&v)[Q][4],
+                                          const bool (&qv)[Q], const uint32_t (&qi)[Q]) {
+#pragma unroll
+  for (int k = 0; k < Q; k++)
+    if (qv[k]) {
+      int32_t p[4], n[4];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        p[c] = to_exp_i32(v[k][c], kNormFineExp, kResidualExp);
+        n[c] = to_exp_i32(sat_neg64(v[k][c]), kNormFineExp, kResidualExp);
+      }
+      int4 *dst = (int4 *)(xbar + 8 * qi[k]);
+      dst[0] = make_int4(p[0], n[0], p[1], n[1]);
+      dst[1] = make_int4(p[2], n[2], p[3], n[3]);
+    }
+}
+
+// Publish 16-bit activations at exponent `exp` for gather16 (to_exp_i32 of +-a to -16).
+__device__ __forceinline__ void publish16(int32_t *xbar, uint32_t channel0, const int32_t (&a)[4],
+                                          int32_t exp) {
+  int4 *dst = (int4 *)(xbar + 2 * channel0);
+  dst[0] = make_int4(to_exp_i32(a[0], exp, kResidualExp), to_exp_i32(-(int64_t)a[0], exp, kResidualExp),
+                     to_exp_i32(a[1], exp, kResidualExp), to_exp_i32(-(int64_t)a[1], exp, kResidualExp));
+  dst[1] = make_int4(to_exp_i32(a[2], exp, kResidualExp), to_exp_i32(-(int64_t)a[2], exp, kResidualExp),
+                     to_exp_i32(a[3], exp, kResidualExp), to_exp_i32(-(int64_t)a[3], exp, kResidualExp));
+}
+
+__device__ __forceinline__ uint32_t prog_word(const uint16_t *prog, uint32_t slot, uint32_t lane) {
+  return prog[slot * kWave + lane];
+}
+
+// The snapped transition or gate (RS stack/kernels.rs:1474-1557), out of line: the 120-root
+// scan is long and served only by snapped artifacts.
+__device__ __noinline__ void snap_rotation_dev(const int8_t *ico, int4 raw, uint64_t lambda,
+                                               int64_t *out) {
+  const int32_t r[4] = {raw.x, raw.y, raw.z, raw.w};
+  snap_rotation(ico, r, lambda, out);
+}
+
+// The Hamilton gate on rhs (session.rs:4951-4968, :4005-4025): shift_wide(q (x) rhs, 15) with
+// q the gate's unit quaternion (lambda 2^31, epsilon 0) or its icosian. Raw gates use q = 2 u
+// exactly, so the product is formed from u and shifted by 14.
+__device__ __forceinline__ void gate_apply(const DevModel &M, const int32_t (&raw)[4],
+                                           const int64_t (&rhs)[4], int64_t (&out)[4]) {
+  i128 prod[4];
+  if (M.raw_gates) {
+    int32_t u[4];
+    unit_q30(raw, kGateEps, u);
+    hamilton32(u, rhs, prod);
+#pragma unroll
+    for (int c = 0; c < 4; c++) out[c] = shift_wide(prod[c], 14);
+  } else {
+    int64_t q[4];
+    snap_rotation_dev(M.icosian, make_int4(raw[0], raw[1], raw[2], raw[3]), 1ull << 31, q);
+    hamilton64(q, rhs, prod);
+#pragma unroll
+    for (int c = 0; c < 4; c++) out[c] = shift_wide(prod[c], 15);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// The writer.
+
+constexpr uint32_t kListCap = 2048;  // member ids staged in LDS per scan segment
+constexpr uint32_t kWindowChunk = 8; // window rows in flight per lane
+constexpr int kScanUnroll = 2;       // row groups per pipeline stage
+
+typedef __attribute__((address_space(1))) void global_void;
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Copies n <= 64 words from global src to LDS dst (one per lane) without passing through
+// registers (global_load_lds_dword); complete after wait_lds_dma().
+__device__ __forceinline__ void lds_dma_words(const uint32_t *src, uint32_t *dst, uint32_t n,
+                                              uint32_t lane) {
+  if (lane < n) __builtin_amdgcn_global_load_lds((global_void *)(src + lane), (lds_void *)dst, 4, 0, 0);
+}
+__device__ __forceinline__ void wait_lds_dma() {
+  __builtin_amdgcn_s_waitcnt(0);
+  wave_sync();
+}
+
+struct ScanGeom {
+  uint32_t S, rows, grp, sub;  // lanes per row, rows per round, this lane's row and segment
+  uint32_t mask;               // all ones when the lane's segment lies inside the row
+};
+
+// Loads the rows of U row groups starting at candidate k0 (ids from the LDS list, or base_id + k
+// for the nearest head). Addresses are clamped into range so that every lane loads.
+template <int U>
+__device__ __forceinline__ void scan_load(const DevModel &M, const uint32_t *list, uint32_t fill,
+                                          uint32_t k0, const ScanGeom &g, uint32_t base_id,
+                                          uint4 (&r)[U][4], uint32_t (&t)[U]) {
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    uint32_t k = k0 + u * g.rows + g.grp;
+    k = k < fill ? k : fill - 1;
+    t[u] = list ? list[k] : base_id + k;
+    const uint4 *row = (const uint4 *)(M.table_b + (uint64_t)t[u] * M.d + 32u * g.sub);
+#pragma unroll
+    for (int w = 0; w < 4; w++) r[u][w] = row[w];
+  }
+}
+
+template <int U>
+__device__ __forceinline__ uint64_t scan_score(const uint32_t (&qpk)[16], uint32_t fill,
+                                               uint32_t k0, const ScanGeom &g,
+                                               const uint4 (&r)[U][4], const uint32_t (&t)[U],
+                                               uint64_t best) {
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    uint32_t acc = 0;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+      acc = sad2_u16(r[u][w].x, qpk[4 * w + 0], acc);
+      acc = sad2_u16(r[u][w].y, qpk[4 * w + 1], acc);
+      acc = sad2_u16(r[u][w].z, qpk[4 * w + 2], acc);
+      acc = sad2_u16(r[u][w].w, qpk[4 * w + 3], acc);
+    }
+    acc = group_sum(acc & g.mask, g.S);
+    const uint64_t cand = ((uint64_t)acc << 32) | t[u];
+    const bool ok = k0 + u * g.rows + g.grp < fill;
+    best = ok && cand < best ? cand : best;
+  }
+  return best;
+}
+
+// Lowest (L1, token) over `fill` >= 1 candidates, two stages in flight: the rows of the next U
+// row groups load while the current ones are scored.
+__device__ __forceinline__ uint64_t scan_list(const DevModel &M, const uint32_t (&qpk)[16],
+                                              const uint32_t *list, uint32_t fill,
+                                              uint32_t base_id, const ScanGeom &g, uint64_t best) {
+  constexpr int U = kScanUnroll;
+  const uint32_t chunk = g.rows * U;
+  uint4 ra[U][4], rb[U][4];
+  uint32_t ta[U], tb[U];
+  scan_load<U>(M, list, fill, 0, g, base_id, ra, ta);
+  for (uint32_t k0 = 0; k0 < fill; k0 += 2 * chunk) {
+    scan_load<U>(M, list, fill, k0 + chunk, g, base_id, rb, tb);
+    best = scan_score<U>(qpk, fill, k0, g, ra, ta, best);
+    scan_load<U>(M, list, fill, k0 + 2 * chunk, g, base_id, ra, ta);
+    best = scan_score<U>(qpk, fill, k0 + chunk, g, rb, tb, best);
   }
   return best;
 }
@@ -212,25 +298,36 @@ __device__ __forceinline__ uint64_t scan_rows(const DevModel &M, const uint32_t 
 // The native vector writer (RS stack/session.rs:4069-4121, TW 580-623) over keyed drawers,
 // or the whole-table nearest head (session.rs:4418-4445). `q` holds the query (d words) in
 // LDS. Returns the token (UINT32_MAX when no row was scored); writes the kept drawers in
-// selection order to kept_out (nullable) from lane 0.
-__device__ uint32_t writer(const DevModel &M, const int32_t *q, uint32_t *dscore, uint32_t lane,
-                           uint32_t *kept_out) {
+// selection order to kept_out (nullable).
+__device__ __forceinline__ uint32_t writer(const DevModel &M, const int32_t *q, uint32_t *dscore,
+                                           uint32_t *kept, uint32_t *list, uint32_t lane,
+                                           uint32_t *kept_out) {
   const uint32_t d = M.d, segs = d >> 5;
-  uint32_t S = 1;
-  while (S < segs) S <<= 1;
-  const uint32_t rows = kWave / S, grp = lane / S, sub = lane % S;
-  const bool seg_ok = sub < segs;  // lanes past the row's last 32-channel segment add zero
+  ScanGeom g;
+  g.S = 1;
+  while (g.S < segs) g.S <<= 1;
+  g.rows = kWave / g.S;
+  g.grp = lane / g.S;
+  const uint32_t sub = lane % g.S;
+  // Lanes past the row's last 32-channel segment (widths that are not a power-of-two multiple
+  // of 32) read the last segment again and add zero.
+  g.sub = sub < segs ? sub : segs - 1;
+  g.mask = sub < segs ? 0xffffffffu : 0u;
   uint32_t qpk[16];  // biased query pairs: (q[2i] + 2^15) | (q[2i+1] + 2^15) << 16
 #pragma unroll
   for (int i = 0; i < 16; i++)
-    qpk[i] = seg_ok ? (uint32_t)(q[32 * sub + 2 * i] + 32768) |
-                          ((uint32_t)(q[32 * sub + 2 * i + 1] + 32768) << 16)
-                    : 0u;
+    qpk[i] = (uint32_t)(q[32 * g.sub + 2 * i] + 32768) |
+             ((uint32_t)(q[32 * g.sub + 2 * i + 1] + 32768) << 16);
   uint64_t best = UINT64_MAX;
   if (M.head == 1) {
-    best = scan_rows(M, qpk, 0, M.vocab, S, grp, sub, seg_ok, rows, best);
+    for (uint32_t b = 0; b < M.vocab; b += kListCap) {
+      uint32_t fill = M.vocab - b < kListCap ? M.vocab - b : kListCap;
+      best = scan_list(M, qpk, nullptr, fill, b, g, best);
+    }
     if (kept_out && lane < M.P) kept_out[lane] = 0;
   } else {
+    // Drawer scores: L1 of the query's first and last 8-blocks to the drawer's two keys,
+    // packed with the drawer index so that the minimum is the reference's first maximum.
     int32_t qa[8], qb[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -238,78 +335,136 @@ __device__ uint32_t writer(const DevModel &M, const int32_t *q, uint32_t *dscore
       qb[i] = q[d - 8 + i];
     }
     for (uint32_t c = lane; c < M.D; c += kWave) {
-      const int16_t *key = M.keys + 16u * c;
-      uint32_t s = 0;
+      const int4 *key = (const int4 *)(M.keys + 16u * c);
+      const int4 k4[2] = {key[0], key[1]};
+      const int16_t *kk = (const int16_t *)k4;
+      uint32_t sc = 0;
 #pragma unroll
       for (int i = 0; i < 8; i++) {
-        s += uabs32(qa[i] - (int32_t)key[i]);
-        s += uabs32(qb[i] - (int32_t)key[8 + i]);
+        sc += uabs32(qa[i] - (int32_t)kk[i]);
+        sc += uabs32(qb[i] - (int32_t)kk[8 + i]);
       }
-      dscore[c] = (s << 12) | c;
+      dscore[c] = (sc << 12) | c;
     }
-    __syncthreads();
+    wave_sync();
     for (uint32_t p = 0; p < M.P; p++) {
       uint32_t local = UINT32_MAX;
       for (uint32_t c = lane; c < M.D; c += kWave) local = dscore[c] < local ? dscore[c] : local;
-      uint32_t pick = wave_min_u32(local) & 0xfffu;
-      __syncthreads();
+      const uint32_t pick = wave_reduce32(local, OpMin()) & 0xfffu;
+      wave_sync();
       if ((pick & (kWave - 1)) == lane) dscore[pick] = UINT32_MAX;
-      if (kept_out && lane == 0) kept_out[p] = pick;
-      uint32_t beg = M.offsets[pick], end = M.offsets[pick + 1];
-      best = scan_rows(M, qpk, beg, end, S, grp, sub, seg_ok, rows, best);
-      __syncthreads();
+      if (lane == 0) kept[p] = pick;
+      wave_sync();
+    }
+    if (kept_out && lane < M.P) kept_out[lane] = kept[lane];
+    // Stage the kept drawers' member ids in LDS (at most kListCap per segment) and scan.
+    uint32_t p = 0, done = 0;  // next drawer, members of it already staged
+    while (p < M.P) {
+      uint32_t fill = 0;
+      while (p < M.P && fill < kListCap) {
+        const uint32_t c = uniform32(kept[p]);
+        const uint32_t beg = M.offsets[c] + done, end = M.offsets[c + 1];
+        const uint32_t take = end - beg < kListCap - fill ? end - beg : kListCap - fill;
+        for (uint32_t o = 0; o < take; o += kWave)
+          lds_dma_words(M.members + beg + o, list + fill + o, take - o, lane);
+        fill += take;
+        done += take;
+        if (beg + take == end) {
+          p++;
+          done = 0;
+        }
+      }
+      wait_lds_dma();
+      if (fill) best = scan_list(M, qpk, list, fill, 0, g, best);
+      wave_sync();
     }
   }
-  best = wave_min_u64(best);
+  best = wave_reduce64(best, OpMin());
   return (uint32_t)best;
 }
 
-// One step of the session (RS stack/session.rs:4129-4403, TW 635-675) at position `pos` with
-// ring slot `base`. Returns 0 or the reference's status code; the chosen token goes to *chosen
-// when the writer runs.
+// ---------------------------------------------------------------------------------------------
+// One step of the session (RS stack/session.rs:4129-4403, TW 635-675) at ring slot `base`.
+// Returns 0 or the reference's status code; the chosen token goes to *chosen when the writer
+// runs.
+
+struct Lds {
+  int32_t *xbar;     // gather crossbar, 2 max(d, m) words; also the query
+  int64_t *mlp_out;  // m values
+  uint32_t *dscore;  // D
+  uint32_t *kept;    // kMaxProbes
+  uint32_t *list;    // kListCap
+  int64_t *st;       // L * d recurrence state
+};
+
 template <int Q>
-__device__ int step(const DevModel &M, int32_t *xbar, uint32_t *dscore, int64_t *st,
-                    int32_t *ring, uint32_t base, uint32_t lane, const bool (&qv)[Q],
-                    const uint32_t (&qi)[Q], uint32_t tok, bool want_writer, uint32_t *chosen,
-                    uint32_t *kept_out, int32_t *query_out) {
+__device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ring, uint32_t base, uint32_t lane,
+                    const bool (&qv)[Q], const uint32_t (&qi)[Q], uint32_t tok, bool want_writer,
+                    uint32_t *chosen, uint32_t *kept_out, int32_t *query_out) {
   if (tok >= M.vocab) return 1;
   const uint32_t d = M.d, W = M.W, nq = M.nq;
   int32_t x[Q][4];
 #pragma unroll
   for (int k = 0; k < Q; k++) {
-    if (qv[k]) {
-      uint2 w = *(const uint2 *)(M.table_b + (uint64_t)tok * d + 4 * qi[k]);
-      uint32_t ww[2] = {w.x, w.y};
+    uint2 w = qv[k] ? *(const uint2 *)(M.table_b + (uint64_t)tok * d + 4 * qi[k])
+                    : make_uint2(0x80008000u, 0x80008000u);
+    const uint32_t ww[2] = {w.x, w.y};
 #pragma unroll
-      for (int c = 0; c < 4; c++) {
-        int16_t v = (int16_t)(uint16_t)(((ww[c >> 1] >> (16 * (c & 1))) & 0xffffu) ^ 0x8000u);
-        x[k][c] = (int32_t)v << 4;  // to_exp_i32(v, -12, -16)
-      }
-    } else {
-#pragma unroll
-      for (int c = 0; c < 4; c++) x[k][c] = 0;
+    for (int c = 0; c < 4; c++) {
+      int16_t v = (int16_t)(uint16_t)(((ww[c >> 1] >> (16 * (c & 1))) & 0xffffu) ^ 0x8000u);
+      x[k][c] = (int32_t)v << 4;  // to_exp_i32(v, -12, -16)
     }
   }
   for (uint32_t l = 0; l < M.L; l++) {
     const DevLayer ly = M.layers[l];
-    int64_t v[Q][4];
+    int32_t *ring_l = ring + (uint64_t)l * W * d;
+    // The layer's loads first: gains, biases and the gather program.
+    short4 g_rec[Q], g_mlp[Q], tap0[Q];
+    ushort4 gd_rec[Q], gd_mlp[Q], td0[Q];
+    int4 cbias[Q], rbias[Q];
+    int32_t dbias[Q], doff[Q];
+    uint32_t pw_drive[Q][4], pw_gate[Q][4], pw_rot[Q][4], pw_dec[Q], pw_out[Q][4], pw_down[Q][4];
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      const uint32_t qq = qv[k] ? qi[k] : 0, ch = 4 * qq;
+      g_rec[k] = *(const short4 *)(ly.rec_gain + ch);
+      g_mlp[k] = *(const short4 *)(ly.mlp_gain + ch);
+      tap0[k] = *(const short4 *)(ly.taps + ch);
+      gd_rec[k] = *(const ushort4 *)(ly.rec_gain_desc + ch);
+      gd_mlp[k] = *(const ushort4 *)(ly.mlp_gain_desc + ch);
+      td0[k] = *(const ushort4 *)(ly.taps_desc + ch);
+      cbias[k] = *(const int4 *)(ly.conv_bias + ch);
+      rbias[k] = *(const int4 *)(ly.gate_bias + nq + ch);
+      dbias[k] = ly.gate_bias[qq];
+      doff[k] = ly.decay_offset[qq];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        pw_drive[k][c] = prog_word(ly.prog, M.s_rec_in + 4 * k + c, lane);
+        pw_gate[k][c] = prog_word(ly.prog, M.s_rec_in + 4 * Q + 4 * k + c, lane);
+        pw_rot[k][c] = prog_word(ly.prog, M.s_rec_gate + Q + 4 * k + c, lane);
+        pw_out[k][c] = prog_word(ly.prog, M.s_rec_out + 4 * k + c, lane);
+        pw_down[k][c] = prog_word(ly.prog, M.s_mlp_down + 4 * k + c, lane);
+      }
+      pw_dec[k] = prog_word(ly.prog, M.s_rec_gate + k, lane);
+    }
     // ---- recurrence block
-    norm_gain<Q>(M, x, qv, qi, ly.rec_gain, v);
-    publish64<Q>(xbar, v, qv, qi);
-    __syncthreads();
+    int64_t v[Q][4];
+    norm_gain<Q>(M, x, qv, g_rec, gd_rec, v);
+    publish64<Q>(S.xbar, v, qv, qi);
+    wave_sync();
     int32_t drive[Q][4], gv[Q][4], rot[Q][4], dec[Q];
 #pragma unroll
     for (int k = 0; k < Q; k++) {
+      const int32_t rb[4] = {rbias[k].x, rbias[k].y, rbias[k].z, rbias[k].w};
 #pragma unroll
       for (int c = 0; c < 4; c++) {
-        drive[k][c] = gather1(xbar, ly.prog, M.s_rec_in + 4 * k + c, lane);
-        gv[k][c] = gather1(xbar, ly.prog, M.s_rec_in + 4 * Q + 4 * k + c, lane);
-        rot[k][c] = gather1(xbar, ly.prog, M.s_rec_gate + Q + 4 * k + c, lane);
+        drive[k][c] = S.xbar[pw_drive[k][c]];
+        gv[k][c] = S.xbar[pw_gate[k][c]];
+        rot[k][c] = sat_add32(S.xbar[pw_rot[k][c]], rb[c]);
       }
-      dec[k] = gather1(xbar, ly.prog, M.s_rec_gate + k, lane);
+      dec[k] = sat_add32(S.xbar[pw_dec[k]], dbias[k]);
     }
-    __syncthreads();
-    int32_t *ring_l = ring + (uint64_t)l * W * d;
+    wave_sync();
     int64_t sc[Q][4];
     uint64_t mx = 0;
 #pragma unroll
@@ -319,54 +474,87 @@ __device__ int step(const DevModel &M, int32_t *xbar, uint32_t *dscore, int64_t 
         for (int c = 0; c < 4; c++) sc[k][c] = 0;
         continue;
       }
-      const uint32_t qq = qi[k], ch = 4 * qq;
-      dec[k] = sat_add32(dec[k], ly.gate_bias[qq]);
-#pragma unroll
-      for (int c = 0; c < 4; c++) rot[k][c] = sat_add32(rot[k][c], ly.gate_bias[nq + ch + c]);
-      // The causal window (session.rs:4842-4868): tap 0 on the drive, tap s on the drive s
-      // positions back (ring slot base - s), then the drive enters slot base.
-      int64_t wide[4];
-      {
-        int4 cb = *(const int4 *)(ly.conv_bias + ch);
-        short4 t0 = *(const short4 *)(ly.taps + ch);
-        wide[0] = wadd64(cb.x, grid_apply(drive[k][0], t0.x));
-        wide[1] = wadd64(cb.y, grid_apply(drive[k][1], t0.y));
-        wide[2] = wadd64(cb.z, grid_apply(drive[k][2], t0.z));
-        wide[3] = wadd64(cb.w, grid_apply(drive[k][3], t0.w));
-      }
-      uint32_t slot = base;
-      for (uint32_t s = 1; s <= W; s++) {
-        slot = slot == 0 ? W - 1 : slot - 1;
-        int4 h = *(const int4 *)(ring_l + (uint64_t)slot * d + ch);
-        short4 t = *(const short4 *)(ly.taps + (uint64_t)s * d + ch);
-        wide[0] = wadd64(wide[0], grid_apply(h.x, t.x));
-        wide[1] = wadd64(wide[1], grid_apply(h.y, t.y));
-        wide[2] = wadd64(wide[2], grid_apply(h.z, t.z));
-        wide[3] = wadd64(wide[3], grid_apply(h.w, t.w));
-      }
-      *(int4 *)(ring_l + (uint64_t)base * d + ch) =
-          make_int4(drive[k][0], drive[k][1], drive[k][2], drive[k][3]);
+      const uint32_t ch = 4 * qi[k];
       // Lane weights (session.rs:4989-5026): geometric decay and keep from the 16-step table.
-      int32_t sq = sat_add32(dec[k], ly.decay_offset[qq]);
+      int32_t sq = sat_add32(dec[k], doff[k]);
       sq = sq < 0 ? 0 : sq > 65536 ? 65536 : sq;
       uint32_t idx = (uint32_t)sq >> 12;
       idx = idx > 15 ? 15 : idx;
-      uint64_t lambda = 1ull << (30 - idx), keep = M.keep_q31[idx];
-      // Transport (session.rs:5097-5145): h <- shift_wide(T (x) h + (keep wide) << 16, 31).
-      int64_t *hp = st + (uint64_t)l * d + ch;
-      int64_t h[4] = {hp[0], hp[1], hp[2], hp[3]};
-      i128 moved[4];
+      const uint64_t lambda = 1ull << (30 - idx), keep = M.keep_q31[idx];
+      // The causal window (session.rs:4842-4868): tap 0 on the drive, tap s on the drive s
+      // positions back (ring slot base - s), then the drive enters slot base. Rows and taps
+      // load kWindowChunk at a time; the first chunk is in flight during the rotation.
+      int4 hb[kWindowChunk];
+      ushort4 tb[kWindowChunk];
+      auto load_chunk = [&](uint32_t s0) {
+#pragma unroll
+        for (uint32_t i = 0; i < kWindowChunk; i++) {
+          const uint32_t s = s0 + i;
+          if (s <= W) {
+            const uint32_t sl = base >= s ? base - s : base + W - s;
+            hb[i] = *(const int4 *)(ring_l + (uint64_t)sl * d + ch);
+            tb[i] = *(const ushort4 *)(ly.taps_desc + (uint64_t)s * d + ch);
+          }
+        }
+      };
+      load_chunk(1);
+      // The transition's rotation (session.rs:5097-5145).
+      int32_t T[4];
+      int64_t T64[4];
       if (M.raw_transition) {
-        int32_t u[4], T[4];
+        int32_t u[4];
         unit_q30(rot[k], kRotationEps, u);
 #pragma unroll
         for (int c = 0; c < 4; c++) T[c] = u[c] >> idx;  // (lambda u) >> 30, lambda = 2^(30-idx)
-        hamilton32(T, h, moved);
       } else {
-        int64_t T[4];
-        snap_rotation(M.icosian, rot[k], lambda, T);
-        hamilton64(T, h, moved);
+        snap_rotation_dev(M.icosian, make_int4(rot[k][0], rot[k][1], rot[k][2], rot[k][3]),
+                          lambda, T64);
       }
+      int64_t wide[4];
+      if (M.taps_fast) {
+        const ushort4 t0 = td0[k];
+        wide[0] = wadd64(cbias[k].x, grid_desc_apply(drive[k][0], t0.x));
+        wide[1] = wadd64(cbias[k].y, grid_desc_apply(drive[k][1], t0.y));
+        wide[2] = wadd64(cbias[k].z, grid_desc_apply(drive[k][2], t0.z));
+        wide[3] = wadd64(cbias[k].w, grid_desc_apply(drive[k][3], t0.w));
+        for (uint32_t s0 = 1; s0 <= W; s0 += kWindowChunk) {
+          if (s0 > 1) load_chunk(s0);
+#pragma unroll
+          for (uint32_t i = 0; i < kWindowChunk; i++)
+            if (s0 + i <= W) {
+              wide[0] = wadd64(wide[0], grid_desc_apply(hb[i].x, tb[i].x));
+              wide[1] = wadd64(wide[1], grid_desc_apply(hb[i].y, tb[i].y));
+              wide[2] = wadd64(wide[2], grid_desc_apply(hb[i].z, tb[i].z));
+              wide[3] = wadd64(wide[3], grid_desc_apply(hb[i].w, tb[i].w));
+            }
+        }
+      } else {
+        // A tap outside the descriptor form somewhere in the model: the reference routine.
+        const short4 t0 = tap0[k];
+        wide[0] = wadd64(cbias[k].x, grid_apply(drive[k][0], t0.x));
+        wide[1] = wadd64(cbias[k].y, grid_apply(drive[k][1], t0.y));
+        wide[2] = wadd64(cbias[k].z, grid_apply(drive[k][2], t0.z));
+        wide[3] = wadd64(cbias[k].w, grid_apply(drive[k][3], t0.w));
+        for (uint32_t s = 1; s <= W; s++) {
+          const uint32_t sl = base >= s ? base - s : base + W - s;
+          const int4 hh = *(const int4 *)(ring_l + (uint64_t)sl * d + ch);
+          const short4 t = *(const short4 *)(ly.taps + (uint64_t)s * d + ch);
+          wide[0] = wadd64(wide[0], grid_apply(hh.x, t.x));
+          wide[1] = wadd64(wide[1], grid_apply(hh.y, t.y));
+          wide[2] = wadd64(wide[2], grid_apply(hh.z, t.z));
+          wide[3] = wadd64(wide[3], grid_apply(hh.w, t.w));
+        }
+      }
+      *(int4 *)(ring_l + (uint64_t)base * d + ch) =
+          make_int4(drive[k][0], drive[k][1], drive[k][2], drive[k][3]);
+      // Transport: h <- shift_wide(T (x) h + (keep wide) << 16, 31).
+      int64_t *hp = S.st + (uint64_t)l * d + ch;
+      int64_t h[4] = {hp[0], hp[1], hp[2], hp[3]};
+      i128 moved[4];
+      if (M.raw_transition)
+        hamilton32(T, h, moved);
+      else
+        hamilton64(T64, h, moved);
 #pragma unroll
       for (int c = 0; c < 4; c++) {
         u128 drive_term = (u128)((i128)keep * (i128)wide[c]) << 16;
@@ -386,111 +574,118 @@ __device__ int step(const DevModel &M, int32_t *xbar, uint32_t *dscore, int64_t 
       }
     }
     // quantize16 over the d outputs (kernels.rs:545-553), then gather16 of rec_out.
-    mx = wave_max_u64(mx);
+    mx = wave_reduce64(mx, OpMax());
     int32_t qs = bitlen64(mx) - 15;
     if (qs < 0) qs = 0;
-    const int32_t act_exp = kProductExp + qs;
 #pragma unroll
     for (int k = 0; k < Q; k++)
       if (qv[k]) {
         int32_t a[4];
 #pragma unroll
         for (int c = 0; c < 4; c++) a[c] = quantize_elem(sc[k][c], qs);
-        publish16(xbar, 4 * qi[k], a, act_exp);
+        publish16(S.xbar, 4 * qi[k], a, kProductExp + qs);
       }
-    __syncthreads();
-    int32_t proj[Q][4];
-#pragma unroll
-    for (int k = 0; k < Q; k++)
-#pragma unroll
-      for (int c = 0; c < 4; c++) proj[k][c] = gather1(xbar, ly.prog, M.s_rec_out + 4 * k + c, lane);
-    __syncthreads();
+    wave_sync();
 #pragma unroll
     for (int k = 0; k < Q; k++)
       if (qv[k])
 #pragma unroll
-        for (int c = 0; c < 4; c++) x[k][c] = sat_add32(x[k][c], proj[k][c]);
+        for (int c = 0; c < 4; c++) x[k][c] = sat_add32(x[k][c], S.xbar[pw_out[k][c]]);
+    wave_sync();
     // ---- feed-forward block: the Hamilton gate of mlp_gate on mlp_up (session.rs:4005-4025).
-    norm_gain<Q>(M, x, qv, qi, ly.mlp_gain, v);
-    publish64<Q>(xbar, v, qv, qi);
-    __syncthreads();
-    int64_t mo[kMaxMpl][4];
+    norm_gain<Q>(M, x, qv, g_mlp, gd_mlp, v);
+    publish64<Q>(S.xbar, v, qv, qi);
+    wave_sync();
     uint64_t mmx = 0;
-#pragma unroll
-    for (int j = 0; j < (int)kMaxMpl; j++) {
-      uint32_t mq = lane + kWave * j;
-      if (j < (int)M.mpl && mq < M.nm) {
-        int32_t g[4];
-        int64_t up[4];
+#pragma unroll 1
+    for (uint32_t j = 0; j < M.mpl; j++) {
+      const uint32_t mq = lane + kWave * j;
+      if (mq < M.nm) {
+        int32_t gq[4];
+        int64_t up[4], mo[4];
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-          g[c] = gather1(xbar, ly.prog, M.s_mlp_gate + 4 * j + c, lane);
-          up[c] = gather1(xbar, ly.prog, M.s_mlp_up + 4 * j + c, lane);
+          gq[c] = S.xbar[prog_word(ly.prog, M.s_mlp_gate + 4 * j + c, lane)];
+          up[c] = S.xbar[prog_word(ly.prog, M.s_mlp_up + 4 * j + c, lane)];
         }
-        gate_apply(M, g, up, mo[j]);
+        gate_apply(M, gq, up, mo);
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-          uint64_t a = uabs64(mo[j][c]);
+          S.mlp_out[4 * mq + c] = mo[c];
+          uint64_t a = uabs64(mo[c]);
           mmx = a > mmx ? a : mmx;
         }
       }
     }
-    __syncthreads();
-    mmx = wave_max_u64(mmx);
+    mmx = wave_reduce64(mmx, OpMax());
     qs = bitlen64(mmx) - 15;
     if (qs < 0) qs = 0;
-    const int32_t mlp_exp = kProductExp + qs;
-#pragma unroll
-    for (int j = 0; j < (int)kMaxMpl; j++) {
-      uint32_t mq = lane + kWave * j;
-      if (j < (int)M.mpl && mq < M.nm) {
+    wave_sync();
+#pragma unroll 1
+    for (uint32_t j = 0; j < M.mpl; j++) {
+      const uint32_t mq = lane + kWave * j;
+      if (mq < M.nm) {
         int32_t a[4];
 #pragma unroll
-        for (int c = 0; c < 4; c++) a[c] = quantize_elem(mo[j][c], qs);
-        publish16(xbar, 4 * mq, a, mlp_exp);
+        for (int c = 0; c < 4; c++) a[c] = quantize_elem(S.mlp_out[4 * mq + c], qs);
+        publish16(S.xbar, 4 * mq, a, kProductExp + qs);
       }
     }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < Q; k++)
-#pragma unroll
-      for (int c = 0; c < 4; c++) proj[k][c] = gather1(xbar, ly.prog, M.s_mlp_down + 4 * k + c, lane);
-    __syncthreads();
+    wave_sync();
 #pragma unroll
     for (int k = 0; k < Q; k++)
       if (qv[k])
 #pragma unroll
-        for (int c = 0; c < 4; c++) x[k][c] = sat_add32(x[k][c], proj[k][c]);
+        for (int c = 0; c < 4; c++) x[k][c] = sat_add32(x[k][c], S.xbar[pw_down[k][c]]);
+    wave_sync();
   }
   // Final norm, gain and the Q12 query (session.rs:4294-4295, 4364-4366).
+  short4 g_fin[Q];
+  ushort4 gd_fin[Q];
+#pragma unroll
+  for (int k = 0; k < Q; k++) {
+    g_fin[k] = *(const short4 *)(M.final_gain + 4 * (qv[k] ? qi[k] : 0));
+    gd_fin[k] = *(const ushort4 *)(M.final_gain_desc + 4 * (qv[k] ? qi[k] : 0));
+  }
   int64_t v[Q][4];
-  norm_gain<Q>(M, x, qv, qi, M.final_gain, v);
+  norm_gain<Q>(M, x, qv, g_fin, gd_fin, v);
 #pragma unroll
   for (int k = 0; k < Q; k++)
     if (qv[k]) {
-      int4 qq;
       int32_t qa[4];
 #pragma unroll
       for (int c = 0; c < 4; c++) {
         int32_t y = to_exp_i32(v[k][c], kNormFineExp, kQ12Exp);
         qa[c] = y > 32767 ? 32767 : y < -32768 ? -32768 : y;
       }
-      qq = make_int4(qa[0], qa[1], qa[2], qa[3]);
-      *(int4 *)(xbar + 4 * qi[k]) = qq;
+      int4 qq = make_int4(qa[0], qa[1], qa[2], qa[3]);
+      *(int4 *)(S.xbar + 4 * qi[k]) = qq;
       if (query_out) *(int4 *)(query_out + 4 * qi[k]) = qq;
     }
-  __syncthreads();
-  if (want_writer) *chosen = writer(M, xbar, dscore, lane, kept_out);
-  __syncthreads();
+  wave_sync();
+  if (want_writer) *chosen = writer(M, S.xbar, S.dscore, S.kept, S.list, lane, kept_out);
+  wave_sync();
   return 0;
 }
 
 template <int Q>
 __global__ __launch_bounds__(64) void fbs_run(DevModel M, RunArgs A) {
   extern __shared__ __align__(16) int32_t lds[];
-  int32_t *xbar = lds;
-  uint32_t *dscore = (uint32_t *)(lds + M.xbar_words);
-  int64_t *st = (int64_t *)(lds + M.xbar_words + ((M.D + 3u) & ~3u));
+  Lds S;
+  {
+    uint32_t at = 0;  // words; every region starts 16-byte aligned
+    S.xbar = lds + at;
+    at += M.xbar_words;
+    S.mlp_out = (int64_t *)(lds + at);
+    at += 2 * M.m;
+    S.dscore = (uint32_t *)(lds + at);
+    at += (M.D + 3u) & ~3u;
+    S.kept = (uint32_t *)(lds + at);
+    at += kMaxProbes;
+    S.list = (uint32_t *)(lds + at);
+    at += kListCap;
+    S.st = (int64_t *)(lds + at);
+  }
   const uint32_t lane = threadIdx.x;
   const uint32_t d = M.d, L = M.L, W = M.W;
   int32_t *ring = A.ring + (uint64_t)blockIdx.x * L * W * d;
@@ -513,7 +708,7 @@ __global__ __launch_bounds__(64) void fbs_run(DevModel M, RunArgs A) {
           uint32_t ch = 4 * qi[k];
 #pragma unroll
           for (int c = 0; c < 4; c++)
-            st[(uint64_t)l * d + ch + c] =
+            S.st[(uint64_t)l * d + ch + c] =
                 A.in_state ? A.in_state[((uint64_t)s * L + l) * d + ch + c] : 0;
           for (uint32_t r = 0; r < W; r++) {
             uint32_t slot = (base + 2 * W - 1 - r) % W;
@@ -522,69 +717,62 @@ __global__ __launch_bounds__(64) void fbs_run(DevModel M, RunArgs A) {
             *(int4 *)(ring + ((uint64_t)l * W + slot) * d + ch) = h;
           }
         }
-    __syncthreads();
+    wave_sync();
     int status = 0;
     uint32_t chosen = 0;
-    if (A.mode == kModeDecode) {
-      const uint32_t *prompt = A.tokens + (uint64_t)s * A.len;
-      uint32_t *reply = A.out_tokens + (uint64_t)s * (A.gen + 1);
-      for (uint32_t t = 0; t < A.len + A.gen && status == 0; t++) {
-        uint32_t tok = t < A.len ? prompt[t] : chosen;
-        if (pos >= M.context) {
-          status = 2;
-          break;
+    const bool decode = A.mode == kModeDecode;
+    const uint32_t *toks = A.tokens + (uint64_t)s * A.len;
+    const uint32_t steps = decode ? A.len + A.gen : A.len;
+    unsigned long long hits = 0;
+    for (uint32_t t = 0; t < steps; t++) {
+      if (pos >= M.context) {
+        status = 2;
+        break;
+      }
+      // Decode: the prompt's tokens, then each choice fed back (fbs-toks.rs:1513-1533); the
+      // writer runs at the prompt's last step and every generated one. Sequences and score:
+      // every token of the row, the writer wherever its choice is used.
+      const uint32_t tok = decode && t >= A.len ? chosen : toks[t];
+      const uint64_t at = (uint64_t)s * A.len + t;
+      const bool seq = A.mode == kModeSequences;
+      const bool want = decode ? t + 1 >= A.len : (seq || A.out_tokens || t + 1 < A.len);
+      uint32_t *kept_out = seq && A.out_kept ? A.out_kept + at * M.P : nullptr;
+      int32_t *query_out = seq && A.out_query ? A.out_query + at * d : nullptr;
+      status = step<Q>(M, S, ring, base, lane, qv, qi, tok, want, &chosen, kept_out, query_out);
+      if (status) break;
+      pos++;
+      base = base + 1 == W ? 0 : base + 1;
+      if (lane == 0) {
+        if (decode) {
+          if (want) A.out_tokens[(uint64_t)s * (A.gen + 1) + t + 1 - A.len] = chosen;
+        } else {
+          if (A.out_tokens) A.out_tokens[at] = chosen;
+          if (A.mode == kModeScore && t + 1 < A.len && chosen == toks[t + 1]) hits++;
         }
-        bool want = t + 1 >= A.len;  // the prompt's last step and every generated step
-        status = step<Q>(M, xbar, dscore, st, ring, base, lane, qv, qi, tok, want, &chosen,
-                         nullptr, nullptr);
-        if (status) break;
-        pos++;
-        base = base + 1 == W ? 0 : base + 1;
-        if (want && lane == 0) reply[t + 1 - A.len] = chosen;
       }
-      if (status == 0) {
-        for (uint32_t l = 0; l < L; l++)
+    }
+    if (A.mode == kModeScore && lane == 0 && hits) atomicAdd(A.matches, hits);
+    if (decode && status == 0) {
+      for (uint32_t l = 0; l < L; l++)
 #pragma unroll
-          for (int k = 0; k < Q; k++)
-            if (qv[k]) {
-              uint32_t ch = 4 * qi[k];
-              if (A.out_state)
+        for (int k = 0; k < Q; k++)
+          if (qv[k]) {
+            uint32_t ch = 4 * qi[k];
+            if (A.out_state)
 #pragma unroll
-                for (int c = 0; c < 4; c++)
-                  A.out_state[((uint64_t)s * L + l) * d + ch + c] = st[(uint64_t)l * d + ch + c];
-              if (A.out_history)
-                for (uint32_t r = 0; r < W; r++) {
-                  uint32_t slot = (base + 2 * W - 1 - r) % W;
-                  *(int4 *)(A.out_history + (((uint64_t)s * L + l) * W + r) * d + ch) =
-                      *(const int4 *)(ring + ((uint64_t)l * W + slot) * d + ch);
-                }
-            }
-        if (A.out_position && lane == 0) A.out_position[s] = pos;
-      }
-    } else {
-      const uint32_t *row = A.tokens + (uint64_t)s * A.len;
-      unsigned long long hits = 0;
-      for (uint32_t t = 0; t < A.len; t++) {
-        if (pos >= M.context) {
-          status = 2;
-          break;
-        }
-        uint64_t at = (uint64_t)s * A.len + t;
-        bool want = A.mode == kModeSequences || A.out_tokens || t + 1 < A.len;
-        uint32_t *kept_out = (A.mode == kModeSequences && A.out_kept) ? A.out_kept + at * M.P : nullptr;
-        int32_t *query_out = (A.mode == kModeSequences && A.out_query) ? A.out_query + at * d : nullptr;
-        status = step<Q>(M, xbar, dscore, st, ring, base, lane, qv, qi, row[t], want, &chosen,
-                         kept_out, query_out);
-        if (status) break;
-        pos++;
-        base = base + 1 == W ? 0 : base + 1;
-        if (A.out_tokens && lane == 0) A.out_tokens[at] = chosen;
-        if (A.mode == kModeScore && t + 1 < A.len && chosen == row[t + 1]) hits++;
-      }
-      if (A.mode == kModeScore && lane == 0 && hits) atomicAdd(A.matches, hits);
+              for (int c = 0; c < 4; c++)
+                A.out_state[((uint64_t)s * L + l) * d + ch + c] = S.st[(uint64_t)l * d + ch + c];
+            if (A.out_history)
+              for (uint32_t r = 0; r < W; r++) {
+                uint32_t slot = (base + 2 * W - 1 - r) % W;
+                *(int4 *)(A.out_history + (((uint64_t)s * L + l) * W + r) * d + ch) =
+                    *(const int4 *)(ring + ((uint64_t)l * W + slot) * d + ch);
+              }
+          }
+      if (A.out_position && lane == 0) A.out_position[s] = pos;
     }
     if (lane == 0) A.status[s] = status;
-    __syncthreads();
+    wave_sync();
   }
 }
 
@@ -592,19 +780,25 @@ template __global__ void fbs_run<1>(DevModel, RunArgs);
 template __global__ void fbs_run<2>(DevModel, RunArgs);
 template __global__ void fbs_run<4>(DevModel, RunArgs);
 
+// LDS bytes per block for a model (the layout fbs_run carves).
+size_t lds_bytes(const DevModel &M) {
+  return 4ull * (M.xbar_words + 2 * M.m + ((M.D + 3u) & ~3u) + kMaxProbes + kListCap) +
+         8ull * M.L * M.d;
+}
+
 // Launch entry used by the host side (fbs_api.cpp).
-hipError_t launch_run(const DevModel &M, const RunArgs &A, uint32_t grid, size_t lds_bytes,
+hipError_t launch_run(const DevModel &M, const RunArgs &A, uint32_t grid, size_t lds,
                       hipStream_t stream) {
   dim3 g(grid), b(kWave);
   switch (M.qpl) {
     case 1:
-      hipLaunchKernelGGL(fbs_run<1>, g, b, lds_bytes, stream, M, A);
+      hipLaunchKernelGGL(fbs_run<1>, g, b, lds, stream, M, A);
       break;
     case 2:
-      hipLaunchKernelGGL(fbs_run<2>, g, b, lds_bytes, stream, M, A);
+      hipLaunchKernelGGL(fbs_run<2>, g, b, lds, stream, M, A);
       break;
     default:
-      hipLaunchKernelGGL(fbs_run<4>, g, b, lds_bytes, stream, M, A);
+      hipLaunchKernelGGL(fbs_run<4>, g, b, lds, stream, M, A);
       break;
   }
   return hipGetLastError();
