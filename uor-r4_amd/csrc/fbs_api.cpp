@@ -148,7 +148,8 @@ int validate(const uor_fbs_model *m, const uor_fbs_ext *e, Resolved *r) {
     return fail(UOR_FBS_ERR_SHAPE, "width %u: a multiple of 32 in 32..1024 (format.rs:724-729)", d);
   if (mlp < 32 || mlp > kMaxMpl * kWave * 4 || mlp % 32)
     return fail(UOR_FBS_ERR_SHAPE, "mlp %u: a multiple of 32 in 32..1024", mlp);
-  if (m->vocab == 0 || m->vocab >= (1u << 31)) return fail(UOR_FBS_ERR_SHAPE, "vocab %u", m->vocab);
+  if (m->vocab == 0 || m->vocab >= (1u << 24))
+    return fail(UOR_FBS_ERR_SHAPE, "vocab %u: 1..2^24 - 1", m->vocab);
   if (m->context == 0) return fail(UOR_FBS_ERR_SHAPE, "zero context");
   if (m->layer_count == 0 || m->layer_count > 64)
     return fail(UOR_FBS_ERR_SHAPE, "layer count %u: 1..64", m->layer_count);
@@ -261,6 +262,7 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
   M.xbar_words = 2 * (d > mlp ? d : mlp);
   M.identity_rows = r.head == 1;
   M.taps_fast = 1;
+  M.log2d = (d & (d - 1)) == 0 ? (uint32_t)__builtin_ctz(d) : 0xffu;
   for (int sh = 0; sh <= 8; sh++) M.eps_int[sh] = norm_eps(m->eps_mantissa, m->eps_exp, sh);
 
   auto done = [&](int code) {

@@ -23,6 +23,53 @@ void fbs_hp_div_many(const uint64_t *nhi, const uint64_t *nlo, const uint64_t *d
 }
 
 uint32_t fbs_hp_rsqrt_q46(uint32_t t) { return rsqrt_q46(t); }
+
+// norm_factor_pow2 against norm_factor on n (sum, eps) pairs at 2^log2n: mismatches.
+uint64_t fbs_hp_norm_factor_check(const uint64_t *sum, const int64_t *eps, uint64_t n, uint32_t log2n) {
+  uint64_t bad = 0;
+  for (uint64_t i = 0; i < n; i++) {
+    NormFactor a = norm_factor(sum[i], 1u << log2n, eps[i]);
+    NormFactor b = norm_factor_pow2(sum[i], log2n, eps[i]);
+    bad += a.r != b.r || a.huge != b.huge;
+  }
+  return bad;
+}
+
+// publish16_pair / publish64_pair / quantize_elem against the reference conversions.
+uint64_t fbs_hp_publish_check(const int64_t *v, uint64_t n) {
+  uint64_t bad = 0;
+  for (uint64_t i = 0; i < n; i++) {
+    int32_t p, q;
+    publish64_pair(v[i], &p, &q);
+    bad += p != to_exp_i32(v[i], kNormFineExp, kResidualExp);
+    bad += q != to_exp_i32(sat_neg64(v[i]), kNormFineExp, kResidualExp);
+    for (int32_t s = 0; s <= 49; s++) {
+      int64_t y = shift(v[i], s);
+      int32_t ref = (int32_t)(y > 32767 ? 32767 : y < -32767 ? -32767 : y);
+      int32_t a = quantize_elem(v[i], s);
+      bad += a != ref;
+      int32_t e = kProductExp + s;
+      publish16_pair(a, e, &p, &q);
+      bad += p != to_exp_i32(a, e, kResidualExp);
+      bad += q != to_exp_i32(-(int64_t)a, e, kResidualExp);
+    }
+  }
+  return bad;
+}
+
+// hamilton32x32 then shift_i64(.., 14) against hamilton32 and shift_wide(.., 14).
+uint64_t fbs_hp_hamilton_mlp_check(const int32_t *a, const int32_t *b, uint64_t n) {
+  uint64_t bad = 0;
+  for (uint64_t i = 0; i < n; i++) {
+    int64_t b64[4] = {b[4 * i], b[4 * i + 1], b[4 * i + 2], b[4 * i + 3]};
+    int64_t x[4];
+    i128 y[4];
+    hamilton32x32(a + 4 * i, b + 4 * i, x);
+    hamilton32(a + 4 * i, b64, y);
+    for (int k = 0; k < 4; k++) bad += shift_i64(x[k], 14) != shift_wide(y[k], 14);
+  }
+  return bad;
+}
 uint64_t fbs_hp_recip_q63(uint32_t d) { return recip_q63(d); }
 
 int64_t fbs_hp_shift(int64_t v, int32_t s) { return shift(v, s); }
@@ -99,6 +146,13 @@ void fbs_hp_rms_norm_fine(const int32_t *x, uint32_t n, int64_t eps_m, int32_t e
     sum += uabs64(y) * uabs64(y);
   }
   NormFactor f = norm_factor(sum, n, norm_eps(eps_m, eps_e, sh));
+  if ((n & (n - 1)) == 0) {  // the kernels' form for power-of-two widths must agree
+    NormFactor g = norm_factor_pow2(sum, (uint32_t)__builtin_ctz(n), norm_eps(eps_m, eps_e, sh));
+    if (g.r != f.r || g.huge != f.huge) {
+      for (uint32_t i = 0; i < n; i++) out[i] = INT64_MIN;
+      return;
+    }
+  }
   for (uint32_t i = 0; i < n; i++) out[i] = norm_apply24(f, out[i]);
 }
 

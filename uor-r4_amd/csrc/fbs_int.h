@@ -336,6 +336,91 @@ FBS_HD NormFactor norm_factor(uint64_t sum, uint32_t n, int64_t eps_int) {
   return f;
 }
 
+// floor(2^96 / s) for s in [2^34, 2^64): a 32-bit reciprocal estimate, two refinements on the
+// exact remainder (its high words times the reciprocal), then the exact floor.
+FBS_HD uint64_t div_2p96(uint64_t s) {
+  const int zs = clz64(s);                            // [0, 29]
+  const uint64_t D = s << zs;                         // [2^63, 2^64)
+  const int E = 96 + zs;                              // Q = floor(2^E / D) < 2^62
+  const uint64_t w = recip_q63((uint32_t)(D >> 32));  // ~ 2^95 / D
+  uint64_t q = w << (E - 95);
+  const u128 top = (u128)1 << E;
+#pragma unroll
+  for (int it = 0; it < 2; it++) {
+    const i128 rem = (i128)(top - (u128)q * D);       // small, signed
+    const i128 hi = rem >> 40;                        // rem / 2^40, |.| < 2^63
+    q = (uint64_t)((int64_t)q + (int64_t)(((i128)(int64_t)hi * (int64_t)w) >> 55));
+  }
+  i128 rem = (i128)(top - (u128)q * D);
+  while (rem < 0) {
+    q--;
+    rem += D;
+  }
+  while (rem >= (i128)D) {
+    q++;
+    rem -= D;
+  }
+  return q;
+}
+
+// norm_factor for n = 2^log2n in 64-bit steps (the kernels' form; equal to norm_factor).
+// With m = ms mod 2^60 and M = 16 m < 2^64, s = isqrt(m 2^68) = isqrt(M 2^64) =
+// floor(2^32 sqrt(M)). M is normalised to Mn = M 4^k in [2^62, 2^64); its root t = isqrt(Mn) in
+// [2^31, 2^32) comes from the 32-bit reciprocal square root and is corrected exactly; then
+// s = t 2^J + f with J = 32 - k and f = floor(2^J (sqrt(Mn) - t)) = floor(2^J rem /
+// (t + sqrt(Mn))), rem = Mn - t^2 <= 2 t. The divisor t + sqrt(Mn) lies in [2 t, 2 t + 1) and
+// 2^J rem / (2 t (2 t + 1)) < 1, so f is fh = floor(2^(J-1) rem / t) or fh - 1 (and below
+// 2^J). Writing 2^(J-1) rem = fh t + rho (0 <= rho < t), the exact test
+// f (2^(J+1) t + f) <= rem 4^J for f = fh reads fh^2 <= 2^(J+1) rho.
+FBS_HD NormFactor norm_factor_pow2(uint64_t sum, uint32_t log2n, int64_t eps_int) {
+  NormFactor out;
+  int64_t ms = wadd64((int64_t)(sum >> log2n), eps_int);
+  if (ms < 1) ms = 1;
+  const uint64_t m = (uint64_t)ms & ((1ull << 60) - 1);
+  if (m == 0) {  // isqrt(0) = 0, raised to 1: r = 2^96
+    out.r = 0;
+    out.huge = true;
+    return out;
+  }
+  const uint64_t M = m << 4;
+  const int z = clz64(M) & ~1;
+  const uint64_t mn = M << z;
+  const int J = 32 - (z >> 1);                        // [3, 32]
+  const uint64_t y = rsqrt_q46((uint32_t)(mn >> 32));
+  uint64_t t = ((mn >> 32) * y) >> 30;
+  if (t > 0xffffffffull) t = 0xffffffffull;
+  const int64_t diff = (int64_t)(mn - t * t);
+  t = (uint64_t)((int64_t)t + (((diff >> 16) * (int64_t)y) >> 47));
+  if (t > 0xffffffffull) t = 0xffffffffull;
+  if (t < (1ull << 31)) t = 1ull << 31;
+  while (t * t > mn) t--;
+  while (t < 0xffffffffull && (t + 1) * (t + 1) <= mn) t++;
+  const uint64_t rem = mn - t * t;                    // [0, 2 t] <= 2^33 - 2
+  const uint64_t w = recip_q63((uint32_t)t);          // ~ 2^63 / t
+  const uint64_t num = rem << (J - 1);                // < 2^64
+  uint64_t fh = ((rem >> 1) * w) >> (63 - J);
+  int64_t rho = (int64_t)(num - fh * t);              // small: exact modulo 2^64
+  while (rho < 0) {
+    fh--;
+    rho += (int64_t)t;
+  }
+  while (rho >= (int64_t)t) {
+    fh++;
+    rho -= (int64_t)t;
+  }
+  uint64_t f = fh;
+  if (fh >> J) {
+    f = fh - 1;                                       // f < 2^J
+  } else if (fh) {
+    const bool big = ((uint64_t)rho >> (63 - J)) != 0;  // 2^(J+1) rho >= 2^64 > fh^2
+    if (!big && fh * fh > ((uint64_t)rho << (J + 1))) f = fh - 1;
+  }
+  const uint64_t s = (t << J) + f;                    // >= 2^34
+  out.r = div_2p96(s);
+  out.huge = false;
+  return out;
+}
+
 // One normalised value: round(r y / 2^38) with the sign of y, clamped to i64.
 FBS_HD int64_t norm_apply(NormFactor f, int64_t y) {
   uint64_t u = uabs64(y);
@@ -369,8 +454,36 @@ FBS_HD int64_t norm_eps(int64_t eps_mantissa, int32_t eps_exp, int32_t sh) {
 
 // quantize16's element rule: clamp(shift(v, s), +-32767) (RS stack/kernels.rs:545-553).
 FBS_HD int32_t quantize_elem(int64_t v, int32_t s) {
-  int64_t y = shift(v, s);
+  // shift(v, s) for 0 <= s <= 62: the half is added with saturation, as the reference does.
+  int64_t y = s == 0 ? v : sat_add64(v, (int64_t)1 << (s - 1)) >> s;
   return (int32_t)(y > 32767 ? 32767 : y < -32767 ? -32767 : y);
+}
+
+// to_exp_i32 of a and of -a (|a| <= 32767) from exponent `exp` to -16: a << -k clamped to the
+// i32 range, or rounded half up by k = -16 - exp (zero once k >= 17, as |a| + 2^(k-1) < 2^k).
+FBS_HD void publish16_pair(int32_t a, int32_t exp, int32_t *p, int32_t *n) {
+  const int32_t k = kResidualExp - exp;
+  if (k <= 0) {
+    const int32_t l = -k > 40 ? 40 : -k;
+    *p = clamp_i32((int64_t)a << l);
+    *n = clamp_i32(-(int64_t)a << l);
+  } else if (k <= 16) {
+    const int32_t h = 1 << (k - 1);
+    *p = (a + h) >> k;
+    *n = (-a + h) >> k;
+  } else {
+    *p = 0;
+    *n = 0;
+  }
+}
+
+// to_exp_i32(v, -24, -16) and to_exp_i32(sat_neg64(v), -24, -16): values beyond +-2^40 clamp
+// to the i32 range either way, so v is clamped there first and the shift cannot overflow.
+FBS_HD void publish64_pair(int64_t v, int32_t *p, int32_t *n) {
+  const int64_t lim = (int64_t)1 << 40;
+  const int64_t c = v > lim ? lim : v < -lim ? -lim : v;
+  *p = clamp_i32((c + 128) >> 8);
+  *n = clamp_i32((128 - c) >> 8);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -420,6 +533,20 @@ FBS_HD void hamilton32(const int32_t a[4], const int64_t b[4], i128 o[4]) {
     o[k] = ((i128)H << 32) + (i128)L;
   }
 }
+
+// a (x) b for 32-bit operands: each partial product fits in i64 and, with |a| summing to at
+// most 2^31 + 4, so does each sum of four.
+FBS_HD void hamilton32x32(const int32_t a[4], const int32_t b[4], int64_t o[4]) {
+#define FBS_Q(i, j) ((int64_t)a[i] * (int64_t)b[j])
+  o[0] = FBS_Q(0, 0) - FBS_Q(1, 1) - FBS_Q(2, 2) - FBS_Q(3, 3);
+  o[1] = FBS_Q(0, 1) + FBS_Q(1, 0) + FBS_Q(2, 3) - FBS_Q(3, 2);
+  o[2] = FBS_Q(0, 2) - FBS_Q(1, 3) + FBS_Q(2, 0) + FBS_Q(3, 1);
+  o[3] = FBS_Q(0, 3) + FBS_Q(1, 2) - FBS_Q(2, 1) + FBS_Q(3, 0);
+#undef FBS_Q
+}
+
+// shift_wide of an i64 value (round half up, no clamp needed): s in [1, 62].
+FBS_HD int64_t shift_i64(int64_t v, uint32_t s) { return (v >> s) + ((v >> (s - 1)) & 1); }
 
 // Sign of da + db phi, exactly (RS stack/kernels.rs:1180-1215, TW 393-408).
 FBS_HD bool diff_positive(int64_t da, int64_t db) {

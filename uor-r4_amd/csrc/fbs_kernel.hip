@@ -85,15 +85,35 @@ __device__ __forceinline__ uint64_t wave_reduce64(uint64_t v, Op op) {
   return op(op(lane64(v, 0), lane64(v, 16)), op(lane64(v, 32), lane64(v, 48)));
 }
 
-// Sum over aligned groups of S lanes (S a power of two), every lane of a group getting it.
-__device__ __forceinline__ uint32_t group_sum(uint32_t v, uint32_t S) {
-  if (S >= 2) v += dpp32<kDppXor1>(v);
-  if (S >= 4) v += dpp32<kDppXor2>(v);
-  if (S >= 8) v += dpp32<kDppHalfMirror>(v);
-  if (S >= 16) v += dpp32<kDppMirror>(v);
-  if (S >= 32) v += (uint32_t)__shfl_xor((int)v, 16);
-  if (S >= 64) v += (uint32_t)__shfl_xor((int)v, 32);
-  return v;
+// Sums over aligned groups of S lanes (S a power of two), every lane of a group getting its
+// group's sum, for U independent values at once (each exchange step is applied to all U before
+// the next, so the DPP read-after-write waits are filled with independent work).
+template <int S, int U>
+__device__ __forceinline__ void group_sums(uint32_t (&v)[U]) {
+  if constexpr (S >= 2) {
+#pragma unroll
+    for (int u = 0; u < U; u++) v[u] += dpp32<kDppXor1>(v[u]);
+  }
+  if constexpr (S >= 4) {
+#pragma unroll
+    for (int u = 0; u < U; u++) v[u] += dpp32<kDppXor2>(v[u]);
+  }
+  if constexpr (S >= 8) {
+#pragma unroll
+    for (int u = 0; u < U; u++) v[u] += dpp32<kDppHalfMirror>(v[u]);
+  }
+  if constexpr (S >= 16) {
+#pragma unroll
+    for (int u = 0; u < U; u++) v[u] += dpp32<kDppMirror>(v[u]);
+  }
+  if constexpr (S >= 32) {
+#pragma unroll
+    for (int u = 0; u < U; u++) v[u] += (uint32_t)__shfl_xor((int)v[u], 16);
+  }
+  if constexpr (S >= 64) {
+#pragma unroll
+    for (int u = 0; u < U; u++) v[u] += (uint32_t)__shfl_xor((int)v[u], 32);
+  }
 }
 
 // v_sad_u16 on gfx950 sums the absolute differences of both 16-bit halves:
@@ -136,7 +156,8 @@ __device__ __forceinline__ void norm_gain(const DevModel &M, const int32_t (&x)[
       sum += uabs64(y) * uabs64(y);
     }
   sum = wave_reduce64(sum, OpAdd());
-  NormFactor f = norm_factor(sum, M.d, M.eps_int[sh]);
+  const NormFactor f = M.log2d != 0xffu ? norm_factor_pow2(sum, M.log2d, M.eps_int[sh])
+                                         : norm_factor(sum, M.d, M.eps_int[sh]);
 #pragma unroll
   for (int k = 0; k < Q; k++) {
     const int16_t gc[4] = {gain[k].x, gain[k].y, gain[k].z, gain[k].w};
@@ -157,10 +178,7 @@ __device__ __forceinline__ void publish64(int32_t *xbar, const int64_t (&v)[Q][4
     if (qv[k]) {
       int32_t p[4], n[4];
 #pragma unroll
-      for (int c = 0; c < 4; c++) {
-        p[c] = to_exp_i32(v[k][c], kNormFineExp, kResidualExp);
-        n[c] = to_exp_i32(sat_neg64(v[k][c]), kNormFineExp, kResidualExp);
-      }
+      for (int c = 0; c < 4; c++) publish64_pair(v[k][c], &p[c], &n[c]);
       int4 *dst = (int4 *)(xbar + 8 * qi[k]);
       dst[0] = make_int4(p[0], n[0], p[1], n[1]);
       dst[1] = make_int4(p[2], n[2], p[3], n[3]);
@@ -170,11 +188,12 @@ __device__ __forceinline__ void publish64(int32_t *xbar, const int64_t (&v)[Q][4
 // Publish 16-bit activations at exponent `exp` for gather16 (to_exp_i32 of +-a to -16).
 __device__ __forceinline__ void publish16(int32_t *xbar, uint32_t channel0, const int32_t (&a)[4],
                                           int32_t exp) {
+  int32_t p[4], n[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++) publish16_pair(a[c], exp, &p[c], &n[c]);
   int4 *dst = (int4 *)(xbar + 2 * channel0);
-  dst[0] = make_int4(to_exp_i32(a[0], exp, kResidualExp), to_exp_i32(-(int64_t)a[0], exp, kResidualExp),
-                     to_exp_i32(a[1], exp, kResidualExp), to_exp_i32(-(int64_t)a[1], exp, kResidualExp));
-  dst[1] = make_int4(to_exp_i32(a[2], exp, kResidualExp), to_exp_i32(-(int64_t)a[2], exp, kResidualExp),
-                     to_exp_i32(a[3], exp, kResidualExp), to_exp_i32(-(int64_t)a[3], exp, kResidualExp));
+  dst[0] = make_int4(p[0], n[0], p[1], n[1]);
+  dst[1] = make_int4(p[2], n[2], p[3], n[3]);
 }
 
 __device__ __forceinline__ uint32_t prog_word(const uint16_t *prog, uint32_t slot, uint32_t lane) {
@@ -215,7 +234,7 @@ __device__ __forceinline__ void gate_apply(const DevModel &M, const int32_t (&ra
 
 constexpr uint32_t kListCap = 2048;  // member ids staged in LDS per scan segment
 constexpr uint32_t kWindowChunk = 8; // window rows in flight per lane
-constexpr int kScanUnroll = 2;       // row groups per pipeline stage
+constexpr int kScanUnroll = 4;       // row groups per pipeline stage
 
 typedef __attribute__((address_space(1))) void global_void;
 typedef __attribute__((address_space(3))) void lds_void;
@@ -232,45 +251,54 @@ __device__ __forceinline__ void wait_lds_dma() {
 }
 
 struct ScanGeom {
-  uint32_t S, rows, grp, sub;  // lanes per row, rows per round, this lane's row and segment
-  uint32_t mask;               // all ones when the lane's segment lies inside the row
+  uint32_t grp, sub;  // this lane's row within a round and its 32-channel segment
+  uint32_t mask;      // all ones when the lane's segment lies inside the row
+  uint32_t stride;    // row stride in table words (d)
 };
 
 // Loads the rows of U row groups starting at candidate k0 (ids from the LDS list, or base_id + k
-// for the nearest head). Addresses are clamped into range so that every lane loads.
-template <int U>
+// for the nearest head). Addresses are clamped into range so that every lane loads. Row offsets
+// fit 24-bit products (vocab < 2^24, d <= 1024).
+template <int S, int U>
 __device__ __forceinline__ void scan_load(const DevModel &M, const uint32_t *list, uint32_t fill,
                                           uint32_t k0, const ScanGeom &g, uint32_t base_id,
                                           uint4 (&r)[U][4], uint32_t (&t)[U]) {
+  constexpr uint32_t rows = kWave / S;
 #pragma unroll
   for (int u = 0; u < U; u++) {
-    uint32_t k = k0 + u * g.rows + g.grp;
+    uint32_t k = k0 + u * rows + g.grp;
     k = k < fill ? k : fill - 1;
     t[u] = list ? list[k] : base_id + k;
-    const uint4 *row = (const uint4 *)(M.table_b + (uint64_t)t[u] * M.d + 32u * g.sub);
+    const uint4 *row = (const uint4 *)(M.table_b + __umul24(t[u], g.stride) + 32u * g.sub);
 #pragma unroll
     for (int w = 0; w < 4; w++) r[u][w] = row[w];
   }
 }
 
-template <int U>
+template <int S, int U>
 __device__ __forceinline__ uint64_t scan_score(const uint32_t (&qpk)[16], uint32_t fill,
                                                uint32_t k0, const ScanGeom &g,
                                                const uint4 (&r)[U][4], const uint32_t (&t)[U],
                                                uint64_t best) {
+  constexpr uint32_t rows = kWave / S;
+  uint32_t acc[U];
 #pragma unroll
   for (int u = 0; u < U; u++) {
-    uint32_t acc = 0;
+    acc[u] = 0;
 #pragma unroll
     for (int w = 0; w < 4; w++) {
-      acc = sad2_u16(r[u][w].x, qpk[4 * w + 0], acc);
-      acc = sad2_u16(r[u][w].y, qpk[4 * w + 1], acc);
-      acc = sad2_u16(r[u][w].z, qpk[4 * w + 2], acc);
-      acc = sad2_u16(r[u][w].w, qpk[4 * w + 3], acc);
+      acc[u] = sad2_u16(r[u][w].x, qpk[4 * w + 0], acc[u]);
+      acc[u] = sad2_u16(r[u][w].y, qpk[4 * w + 1], acc[u]);
+      acc[u] = sad2_u16(r[u][w].z, qpk[4 * w + 2], acc[u]);
+      acc[u] = sad2_u16(r[u][w].w, qpk[4 * w + 3], acc[u]);
     }
-    acc = group_sum(acc & g.mask, g.S);
-    const uint64_t cand = ((uint64_t)acc << 32) | t[u];
-    const bool ok = k0 + u * g.rows + g.grp < fill;
+    acc[u] &= g.mask;
+  }
+  group_sums<S, U>(acc);
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const uint64_t cand = ((uint64_t)acc[u] << 32) | t[u];
+    const bool ok = k0 + u * rows + g.grp < fill;
     best = ok && cand < best ? cand : best;
   }
   return best;
@@ -278,19 +306,20 @@ __device__ __forceinline__ uint64_t scan_score(const uint32_t (&qpk)[16], uint32
 
 // Lowest (L1, token) over `fill` >= 1 candidates, two stages in flight: the rows of the next U
 // row groups load while the current ones are scored.
+template <int S>
 __device__ __forceinline__ uint64_t scan_list(const DevModel &M, const uint32_t (&qpk)[16],
                                               const uint32_t *list, uint32_t fill,
                                               uint32_t base_id, const ScanGeom &g, uint64_t best) {
   constexpr int U = kScanUnroll;
-  const uint32_t chunk = g.rows * U;
+  constexpr uint32_t chunk = (kWave / S) * U;
   uint4 ra[U][4], rb[U][4];
   uint32_t ta[U], tb[U];
-  scan_load<U>(M, list, fill, 0, g, base_id, ra, ta);
+  scan_load<S, U>(M, list, fill, 0, g, base_id, ra, ta);
   for (uint32_t k0 = 0; k0 < fill; k0 += 2 * chunk) {
-    scan_load<U>(M, list, fill, k0 + chunk, g, base_id, rb, tb);
-    best = scan_score<U>(qpk, fill, k0, g, ra, ta, best);
-    scan_load<U>(M, list, fill, k0 + 2 * chunk, g, base_id, ra, ta);
-    best = scan_score<U>(qpk, fill, k0 + chunk, g, rb, tb, best);
+    scan_load<S, U>(M, list, fill, k0 + chunk, g, base_id, rb, tb);
+    best = scan_score<S, U>(qpk, fill, k0, g, ra, ta, best);
+    scan_load<S, U>(M, list, fill, k0 + 2 * chunk, g, base_id, ra, ta);
+    best = scan_score<S, U>(qpk, fill, k0 + chunk, g, rb, tb, best);
   }
   return best;
 }
@@ -299,16 +328,15 @@ __device__ __forceinline__ uint64_t scan_list(const DevModel &M, const uint32_t 
 // or the whole-table nearest head (session.rs:4418-4445). `q` holds the query (d words) in
 // LDS. Returns the token (UINT32_MAX when no row was scored); writes the kept drawers in
 // selection order to kept_out (nullable).
+template <int S>
 __device__ __forceinline__ uint32_t writer(const DevModel &M, const int32_t *q, uint32_t *dscore,
                                            uint32_t *kept, uint32_t *list, uint32_t lane,
                                            uint32_t *kept_out) {
-  const uint32_t d = M.d, segs = d >> 5;
+  const uint32_t d = M.d, segs = d >> 5;  // S is the power of two >= segs
   ScanGeom g;
-  g.S = 1;
-  while (g.S < segs) g.S <<= 1;
-  g.rows = kWave / g.S;
-  g.grp = lane / g.S;
-  const uint32_t sub = lane % g.S;
+  g.grp = lane / S;
+  g.stride = d;
+  const uint32_t sub = lane % S;
   // Lanes past the row's last 32-channel segment (widths that are not a power-of-two multiple
   // of 32) read the last segment again and add zero.
   g.sub = sub < segs ? sub : segs - 1;
@@ -322,7 +350,7 @@ __device__ __forceinline__ uint32_t writer(const DevModel &M, const int32_t *q, 
   if (M.head == 1) {
     for (uint32_t b = 0; b < M.vocab; b += kListCap) {
       uint32_t fill = M.vocab - b < kListCap ? M.vocab - b : kListCap;
-      best = scan_list(M, qpk, nullptr, fill, b, g, best);
+      best = scan_list<S>(M, qpk, nullptr, fill, b, g, best);
     }
     if (kept_out && lane < M.P) kept_out[lane] = 0;
   } else {
@@ -357,13 +385,19 @@ __device__ __forceinline__ uint32_t writer(const DevModel &M, const int32_t *q, 
       wave_sync();
     }
     if (kept_out && lane < M.P) kept_out[lane] = kept[lane];
+    // Each drawer's CSR range, loaded by lane p for kept drawer p (all at once).
+    uint32_t my_beg = 0, my_end = 0;
+    if (lane < M.P) {
+      const uint32_t c = kept[lane];
+      my_beg = M.offsets[c];
+      my_end = M.offsets[c + 1];
+    }
     // Stage the kept drawers' member ids in LDS (at most kListCap per segment) and scan.
     uint32_t p = 0, done = 0;  // next drawer, members of it already staged
     while (p < M.P) {
       uint32_t fill = 0;
       while (p < M.P && fill < kListCap) {
-        const uint32_t c = uniform32(kept[p]);
-        const uint32_t beg = M.offsets[c] + done, end = M.offsets[c + 1];
+        const uint32_t beg = lane32(my_beg, (int)p) + done, end = lane32(my_end, (int)p);
         const uint32_t take = end - beg < kListCap - fill ? end - beg : kListCap - fill;
         for (uint32_t o = 0; o < take; o += kWave)
           lds_dma_words(M.members + beg + o, list + fill + o, take - o, lane);
@@ -375,7 +409,7 @@ __device__ __forceinline__ uint32_t writer(const DevModel &M, const int32_t *q, 
         }
       }
       wait_lds_dma();
-      if (fill) best = scan_list(M, qpk, list, fill, 0, g, best);
+      if (fill) best = scan_list<S>(M, qpk, list, fill, 0, g, best);
       wave_sync();
     }
   }
@@ -397,7 +431,7 @@ struct Lds {
   int64_t *st;       // L * d recurrence state
 };
 
-template <int Q>
+template <int Q, int SW>
 __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ring, uint32_t base, uint32_t lane,
                     const bool (&qv)[Q], const uint32_t (&qi)[Q], uint32_t tok, bool want_writer,
                     uint32_t *chosen, uint32_t *kept_out, int32_t *query_out) {
@@ -601,14 +635,25 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
     for (uint32_t j = 0; j < M.mpl; j++) {
       const uint32_t mq = lane + kWave * j;
       if (mq < M.nm) {
-        int32_t gq[4];
-        int64_t up[4], mo[4];
+        int32_t gq[4], up[4];
+        int64_t mo[4];
 #pragma unroll
         for (int c = 0; c < 4; c++) {
           gq[c] = S.xbar[prog_word(ly.prog, M.s_mlp_gate + 4 * j + c, lane)];
           up[c] = S.xbar[prog_word(ly.prog, M.s_mlp_up + 4 * j + c, lane)];
         }
-        gate_apply(M, gq, up, mo);
+        if (M.raw_gates) {
+          // q = 2 u with u the unit quaternion; u (x) up fits in 64 bits.
+          int32_t u[4];
+          int64_t prod[4];
+          unit_q30(gq, kGateEps, u);
+          hamilton32x32(u, up, prod);
+#pragma unroll
+          for (int c = 0; c < 4; c++) mo[c] = shift_i64(prod[c], 14);
+        } else {
+          const int64_t up64[4] = {up[0], up[1], up[2], up[3]};
+          gate_apply(M, gq, up64, mo);
+        }
 #pragma unroll
         for (int c = 0; c < 4; c++) {
           S.mlp_out[4 * mq + c] = mo[c];
@@ -663,12 +708,12 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
       if (query_out) *(int4 *)(query_out + 4 * qi[k]) = qq;
     }
   wave_sync();
-  if (want_writer) *chosen = writer(M, S.xbar, S.dscore, S.kept, S.list, lane, kept_out);
+  if (want_writer) *chosen = writer<SW>(M, S.xbar, S.dscore, S.kept, S.list, lane, kept_out);
   wave_sync();
   return 0;
 }
 
-template <int Q>
+template <int Q, int SW>
 __global__ __launch_bounds__(64) void fbs_run(DevModel M, RunArgs A) {
   extern __shared__ __align__(16) int32_t lds[];
   Lds S;
@@ -738,7 +783,7 @@ __global__ __launch_bounds__(64) void fbs_run(DevModel M, RunArgs A) {
       const bool want = decode ? t + 1 >= A.len : (seq || A.out_tokens || t + 1 < A.len);
       uint32_t *kept_out = seq && A.out_kept ? A.out_kept + at * M.P : nullptr;
       int32_t *query_out = seq && A.out_query ? A.out_query + at * d : nullptr;
-      status = step<Q>(M, S, ring, base, lane, qv, qi, tok, want, &chosen, kept_out, query_out);
+      status = step<Q, SW>(M, S, ring, base, lane, qv, qi, tok, want, &chosen, kept_out, query_out);
       if (status) break;
       pos++;
       base = base + 1 == W ? 0 : base + 1;
@@ -776,9 +821,14 @@ __global__ __launch_bounds__(64) void fbs_run(DevModel M, RunArgs A) {
   }
 }
 
-template __global__ void fbs_run<1>(DevModel, RunArgs);
-template __global__ void fbs_run<2>(DevModel, RunArgs);
-template __global__ void fbs_run<4>(DevModel, RunArgs);
+// The (quaternions per lane, lanes per writer row) pairs widths 32..1024 produce:
+// d <= 256 -> Q 1 with S 1, 2, 4, 8; d <= 512 -> Q 2, S 16; d <= 1024 -> Q 4, S 32.
+template __global__ void fbs_run<1, 1>(DevModel, RunArgs);
+template __global__ void fbs_run<1, 2>(DevModel, RunArgs);
+template __global__ void fbs_run<1, 4>(DevModel, RunArgs);
+template __global__ void fbs_run<1, 8>(DevModel, RunArgs);
+template __global__ void fbs_run<2, 16>(DevModel, RunArgs);
+template __global__ void fbs_run<4, 32>(DevModel, RunArgs);
 
 // LDS bytes per block for a model (the layout fbs_run carves).
 size_t lds_bytes(const DevModel &M) {
@@ -790,17 +840,15 @@ size_t lds_bytes(const DevModel &M) {
 hipError_t launch_run(const DevModel &M, const RunArgs &A, uint32_t grid, size_t lds,
                       hipStream_t stream) {
   dim3 g(grid), b(kWave);
-  switch (M.qpl) {
-    case 1:
-      hipLaunchKernelGGL(fbs_run<1>, g, b, lds, stream, M, A);
-      break;
-    case 2:
-      hipLaunchKernelGGL(fbs_run<2>, g, b, lds, stream, M, A);
-      break;
-    default:
-      hipLaunchKernelGGL(fbs_run<4>, g, b, lds, stream, M, A);
-      break;
-  }
+  uint32_t S = 1;
+  while (S < M.d / 32) S <<= 1;
+  if (M.qpl == 1 && S == 1) hipLaunchKernelGGL((fbs_run<1, 1>), g, b, lds, stream, M, A);
+  else if (M.qpl == 1 && S == 2) hipLaunchKernelGGL((fbs_run<1, 2>), g, b, lds, stream, M, A);
+  else if (M.qpl == 1 && S == 4) hipLaunchKernelGGL((fbs_run<1, 4>), g, b, lds, stream, M, A);
+  else if (M.qpl == 1 && S == 8) hipLaunchKernelGGL((fbs_run<1, 8>), g, b, lds, stream, M, A);
+  else if (M.qpl == 2 && S == 16) hipLaunchKernelGGL((fbs_run<2, 16>), g, b, lds, stream, M, A);
+  else if (M.qpl == 4 && S == 32) hipLaunchKernelGGL((fbs_run<4, 32>), g, b, lds, stream, M, A);
+  else return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
