@@ -193,10 +193,28 @@ constexpr Seed256 make_recip_seed() {
   return s;
 }
 
+// The seed tables, in global (constant) memory; the kernels copy them to LDS and pass that copy.
+FBS_HD const uint32_t *rsqrt_seed_table() {
+  static constexpr Seed384 seed = make_rsqrt_seed();
+  return seed.v;
+}
+FBS_HD const uint32_t *recip_seed_table() {
+  static constexpr Seed256 seed = make_recip_seed();
+  return seed.v;
+}
+constexpr uint32_t kRsqrtSeedWords = 384, kRecipSeedWords = 256;
+
+// The two tables as a pair of pointers (global by default).
+struct Seeds {
+  const uint32_t *rsqrt;
+  const uint32_t *recip;
+  FBS_HD Seeds() : rsqrt(rsqrt_seed_table()), recip(recip_seed_table()) {}
+  FBS_HD Seeds(const uint32_t *r, const uint32_t *q) : rsqrt(r), recip(q) {}
+};
+
 // y ~ 2^46 / sqrt(t) for t in [2^30, 2^32); y in [2^30, 2^31], relative error below 2^-27.
-FBS_HD uint32_t rsqrt_q46(uint32_t t) {
-  constexpr Seed384 seed = make_rsqrt_seed();
-  uint64_t y = seed.v[(t >> 23) - 128];
+FBS_HD uint32_t rsqrt_q46(uint32_t t, const uint32_t *tab) {
+  uint64_t y = tab[(t >> 23) - 128];
 #pragma unroll
   for (int it = 0; it < 2; it++) {
     // Newton: y <- y (3 - t y^2 / 2^92) / 2, with p = t y^2 / 2^60 ~ 2^32.
@@ -209,11 +227,11 @@ FBS_HD uint32_t rsqrt_q46(uint32_t t) {
   }
   return (uint32_t)y;
 }
+FBS_HD uint32_t rsqrt_q46(uint32_t t) { return rsqrt_q46(t, rsqrt_seed_table()); }
 
 // w ~ 2^63 / d for d in [2^31, 2^32); w in (2^31, 2^32], relative error below 2^-30.
-FBS_HD uint64_t recip_q63(uint32_t d) {
-  constexpr Seed256 seed = make_recip_seed();
-  uint64_t w = seed.v[(d >> 23) - 256];
+FBS_HD uint64_t recip_q63(uint32_t d, const uint32_t *tab) {
+  uint64_t w = tab[(d >> 23) - 256];
 #pragma unroll
   for (int it = 0; it < 2; it++) {
     // Newton: w <- w + w (2^63 - d w) / 2^63.
@@ -222,6 +240,7 @@ FBS_HD uint64_t recip_q63(uint32_t d) {
   }
   return w;
 }
+FBS_HD uint64_t recip_q63(uint32_t d) { return recip_q63(d, recip_seed_table()); }
 
 // ---------------------------------------------------------------------------------------------
 // Floor square root of a u128 (RS stack/kernels.rs:408-430 `stack_isqrt`): the result is
@@ -338,11 +357,11 @@ FBS_HD NormFactor norm_factor(uint64_t sum, uint32_t n, int64_t eps_int) {
 
 // floor(2^96 / s) for s in [2^34, 2^64): a 32-bit reciprocal estimate, two refinements on the
 // exact remainder (its high words times the reciprocal), then the exact floor.
-FBS_HD uint64_t div_2p96(uint64_t s) {
+FBS_HD uint64_t div_2p96(uint64_t s, const Seeds &sd = Seeds()) {
   const int zs = clz64(s);                            // [0, 29]
   const uint64_t D = s << zs;                         // [2^63, 2^64)
   const int E = 96 + zs;                              // Q = floor(2^E / D) < 2^62
-  const uint64_t w = recip_q63((uint32_t)(D >> 32));  // ~ 2^95 / D
+  const uint64_t w = recip_q63((uint32_t)(D >> 32), sd.recip);  // ~ 2^95 / D
   uint64_t q = w << (E - 95);
   const u128 top = (u128)1 << E;
 #pragma unroll
@@ -372,7 +391,8 @@ FBS_HD uint64_t div_2p96(uint64_t s) {
 // 2^J rem / (2 t (2 t + 1)) < 1, so f is fh = floor(2^(J-1) rem / t) or fh - 1 (and below
 // 2^J). Writing 2^(J-1) rem = fh t + rho (0 <= rho < t), the exact test
 // f (2^(J+1) t + f) <= rem 4^J for f = fh reads fh^2 <= 2^(J+1) rho.
-FBS_HD NormFactor norm_factor_pow2(uint64_t sum, uint32_t log2n, int64_t eps_int) {
+FBS_HD NormFactor norm_factor_pow2(uint64_t sum, uint32_t log2n, int64_t eps_int,
+                                    const Seeds &sd = Seeds()) {
   NormFactor out;
   int64_t ms = wadd64((int64_t)(sum >> log2n), eps_int);
   if (ms < 1) ms = 1;
@@ -386,7 +406,7 @@ FBS_HD NormFactor norm_factor_pow2(uint64_t sum, uint32_t log2n, int64_t eps_int
   const int z = clz64(M) & ~1;
   const uint64_t mn = M << z;
   const int J = 32 - (z >> 1);                        // [3, 32]
-  const uint64_t y = rsqrt_q46((uint32_t)(mn >> 32));
+  const uint64_t y = rsqrt_q46((uint32_t)(mn >> 32), sd.rsqrt);
   uint64_t t = ((mn >> 32) * y) >> 30;
   if (t > 0xffffffffull) t = 0xffffffffull;
   const int64_t diff = (int64_t)(mn - t * t);
@@ -396,7 +416,7 @@ FBS_HD NormFactor norm_factor_pow2(uint64_t sum, uint32_t log2n, int64_t eps_int
   while (t * t > mn) t--;
   while (t < 0xffffffffull && (t + 1) * (t + 1) <= mn) t++;
   const uint64_t rem = mn - t * t;                    // [0, 2 t] <= 2^33 - 2
-  const uint64_t w = recip_q63((uint32_t)t);          // ~ 2^63 / t
+  const uint64_t w = recip_q63((uint32_t)t, sd.recip); // ~ 2^63 / t
   const uint64_t num = rem << (J - 1);                // < 2^64
   uint64_t fh = ((rem >> 1) * w) >> (63 - J);
   int64_t rho = (int64_t)(num - fh * t);              // small: exact modulo 2^64
@@ -416,7 +436,7 @@ FBS_HD NormFactor norm_factor_pow2(uint64_t sum, uint32_t log2n, int64_t eps_int
     if (!big && fh * fh > ((uint64_t)rho << (J + 1))) f = fh - 1;
   }
   const uint64_t s = (t << J) + f;                    // >= 2^34
-  out.r = div_2p96(s);
+  out.r = div_2p96(s, sd);
   out.huge = false;
   return out;
 }
@@ -617,7 +637,7 @@ FBS_HD void unit_q30_wide(const int32_t raw[4], uint64_t eps, int32_t u[4]) {
 // of the root, estimated from the remainder and checked exactly; each quotient comes from a
 // 32-bit reciprocal of s and is corrected on its exact remainder (small, so its low 64 bits
 // are the remainder).
-FBS_HD void unit_q30(const int32_t raw[4], uint64_t eps, int32_t u[4]) {
+FBS_HD void unit_q30(const int32_t raw[4], uint64_t eps, int32_t u[4], const Seeds &sd = Seeds()) {
   uint32_t a[4];
   uint64_t xl = eps;
   uint32_t xh = 0;
@@ -643,7 +663,7 @@ FBS_HD void unit_q30(const int32_t raw[4], uint64_t eps, int32_t u[4]) {
     xn = xl << z;
     k = z >> 1;
   }
-  uint64_t y = rsqrt_q46((uint32_t)(xn >> 32));      // 2^46 / sqrt(Xn / 2^32)
+  uint64_t y = rsqrt_q46((uint32_t)(xn >> 32), sd.rsqrt);      // 2^46 / sqrt(Xn / 2^32)
   uint64_t r = ((xn >> 32) * y) >> 30;               // ~ sqrt(Xn) < 2^32
   if (r > 0xffffffffull) r = 0xffffffffull;
   int64_t diff = (int64_t)(xn - r * r);
@@ -671,7 +691,7 @@ FBS_HD void unit_q30(const int32_t raw[4], uint64_t eps, int32_t u[4]) {
   }
   // u_c = floor(a_c 2^46 / s), s in [2^16, 2^49].
   const int zs = clz64(s);
-  const uint64_t w = recip_q63((uint32_t)((s << zs) >> 32));  // ~ 2^95 / (s << zs)
+  const uint64_t w = recip_q63((uint32_t)((s << zs) >> 32), sd.recip);  // ~ 2^95 / (s << zs)
   const int sh = 49 - zs;
 #pragma unroll
   for (int c = 0; c < 4; c++) {

@@ -131,9 +131,10 @@ __device__ __forceinline__ uint32_t sad2_u16(uint32_t a, uint32_t b, uint32_t c)
 // Fine RMSNorm then the per-channel grid gain, for the lane's channels
 // (RS stack/kernels.rs:569-620, session.rs:4057-4061). gain: the lane's 4 codes per quaternion.
 template <int Q>
-__device__ __forceinline__ void norm_gain(const DevModel &M, const int32_t (&x)[Q][4],
-                                          const bool (&qv)[Q], const short4 (&gain)[Q],
-                                          const ushort4 (&gdesc)[Q], int64_t (&out)[Q][4]) {
+__device__ __forceinline__ void norm_gain(const DevModel &M, const Seeds &sd,
+                                          const int32_t (&x)[Q][4], const bool (&qv)[Q],
+                                          const short4 (&gain)[Q], const ushort4 (&gdesc)[Q],
+                                          int64_t (&out)[Q][4]) {
   uint32_t mx = 0;
 #pragma unroll
   for (int k = 0; k < Q; k++)
@@ -156,7 +157,7 @@ __device__ __forceinline__ void norm_gain(const DevModel &M, const int32_t (&x)[
       sum += uabs64(y) * uabs64(y);
     }
   sum = wave_reduce64(sum, OpAdd());
-  const NormFactor f = M.log2d != 0xffu ? norm_factor_pow2(sum, M.log2d, M.eps_int[sh])
+  const NormFactor f = M.log2d != 0xffu ? norm_factor_pow2(sum, M.log2d, M.eps_int[sh], sd)
                                          : norm_factor(sum, M.d, M.eps_int[sh]);
 #pragma unroll
   for (int k = 0; k < Q; k++) {
@@ -211,12 +212,13 @@ __device__ __noinline__ void snap_rotation_dev(const int8_t *ico, int4 raw, uint
 // The Hamilton gate on rhs (session.rs:4951-4968, :4005-4025): shift_wide(q (x) rhs, 15) with
 // q the gate's unit quaternion (lambda 2^31, epsilon 0) or its icosian. Raw gates use q = 2 u
 // exactly, so the product is formed from u and shifted by 14.
-__device__ __forceinline__ void gate_apply(const DevModel &M, const int32_t (&raw)[4],
-                                           const int64_t (&rhs)[4], int64_t (&out)[4]) {
+__device__ __forceinline__ void gate_apply(const DevModel &M, const Seeds &sd,
+                                           const int32_t (&raw)[4], const int64_t (&rhs)[4],
+                                           int64_t (&out)[4]) {
   i128 prod[4];
   if (M.raw_gates) {
     int32_t u[4];
-    unit_q30(raw, kGateEps, u);
+    unit_q30(raw, kGateEps, u, sd);
     hamilton32(u, rhs, prod);
 #pragma unroll
     for (int c = 0; c < 4; c++) out[c] = shift_wide(prod[c], 14);
@@ -429,6 +431,7 @@ struct Lds {
   uint32_t *kept;    // kMaxProbes
   uint32_t *list;    // kListCap
   int64_t *st;       // L * d recurrence state
+  Seeds seeds;       // the reciprocal and reciprocal square root seed tables
 };
 
 template <int Q, int SW>
@@ -483,7 +486,7 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
     }
     // ---- recurrence block
     int64_t v[Q][4];
-    norm_gain<Q>(M, x, qv, g_rec, gd_rec, v);
+    norm_gain<Q>(M, S.seeds, x, qv, g_rec, gd_rec, v);
     publish64<Q>(S.xbar, v, qv, qi);
     wave_sync();
     int32_t drive[Q][4], gv[Q][4], rot[Q][4], dec[Q];
@@ -537,7 +540,7 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
       int64_t T64[4];
       if (M.raw_transition) {
         int32_t u[4];
-        unit_q30(rot[k], kRotationEps, u);
+        unit_q30(rot[k], kRotationEps, u, S.seeds);
 #pragma unroll
         for (int c = 0; c < 4; c++) T[c] = u[c] >> idx;  // (lambda u) >> 30, lambda = 2^(30-idx)
       } else {
@@ -599,7 +602,7 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
       int64_t rhs[4], o[4];
 #pragma unroll
       for (int c = 0; c < 4; c++) rhs[c] = shift(h[c], kResidualExp - kStateExp);
-      gate_apply(M, gv[k], rhs, o);
+      gate_apply(M, S.seeds, gv[k], rhs, o);
 #pragma unroll
       for (int c = 0; c < 4; c++) {
         sc[k][c] = o[c];
@@ -627,7 +630,7 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
         for (int c = 0; c < 4; c++) x[k][c] = sat_add32(x[k][c], S.xbar[pw_out[k][c]]);
     wave_sync();
     // ---- feed-forward block: the Hamilton gate of mlp_gate on mlp_up (session.rs:4005-4025).
-    norm_gain<Q>(M, x, qv, g_mlp, gd_mlp, v);
+    norm_gain<Q>(M, S.seeds, x, qv, g_mlp, gd_mlp, v);
     publish64<Q>(S.xbar, v, qv, qi);
     wave_sync();
     uint64_t mmx = 0;
@@ -646,13 +649,13 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
           // q = 2 u with u the unit quaternion; u (x) up fits in 64 bits.
           int32_t u[4];
           int64_t prod[4];
-          unit_q30(gq, kGateEps, u);
+          unit_q30(gq, kGateEps, u, S.seeds);
           hamilton32x32(u, up, prod);
 #pragma unroll
           for (int c = 0; c < 4; c++) mo[c] = shift_i64(prod[c], 14);
         } else {
           const int64_t up64[4] = {up[0], up[1], up[2], up[3]};
-          gate_apply(M, gq, up64, mo);
+          gate_apply(M, S.seeds, gq, up64, mo);
         }
 #pragma unroll
         for (int c = 0; c < 4; c++) {
@@ -693,7 +696,7 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
     gd_fin[k] = *(const ushort4 *)(M.final_gain_desc + 4 * (qv[k] ? qi[k] : 0));
   }
   int64_t v[Q][4];
-  norm_gain<Q>(M, x, qv, g_fin, gd_fin, v);
+  norm_gain<Q>(M, S.seeds, x, qv, g_fin, gd_fin, v);
 #pragma unroll
   for (int k = 0; k < Q; k++)
     if (qv[k]) {
@@ -729,7 +732,14 @@ __global__ __launch_bounds__(64) void fbs_run(DevModel M, RunArgs A) {
     at += kMaxProbes;
     S.list = (uint32_t *)(lds + at);
     at += kListCap;
+    uint32_t *seed_lds = (uint32_t *)(lds + at);
+    at += kRsqrtSeedWords + kRecipSeedWords;
     S.st = (int64_t *)(lds + at);
+    const uint32_t *rs = rsqrt_seed_table(), *rc = recip_seed_table();
+    for (uint32_t i = threadIdx.x; i < kRsqrtSeedWords; i += kWave) seed_lds[i] = rs[i];
+    for (uint32_t i = threadIdx.x; i < kRecipSeedWords; i += kWave) seed_lds[kRsqrtSeedWords + i] = rc[i];
+    S.seeds = Seeds(seed_lds, seed_lds + kRsqrtSeedWords);
+    wave_sync();
   }
   const uint32_t lane = threadIdx.x;
   const uint32_t d = M.d, L = M.L, W = M.W;
@@ -832,7 +842,8 @@ template __global__ void fbs_run<4, 32>(DevModel, RunArgs);
 
 // LDS bytes per block for a model (the layout fbs_run carves).
 size_t lds_bytes(const DevModel &M) {
-  return 4ull * (M.xbar_words + 2 * M.m + ((M.D + 3u) & ~3u) + kMaxProbes + kListCap) +
+  return 4ull * (M.xbar_words + 2 * M.m + ((M.D + 3u) & ~3u) + kMaxProbes + kListCap +
+                 kRsqrtSeedWords + kRecipSeedWords) +
          8ull * M.L * M.d;
 }
 
