@@ -25,6 +25,7 @@ import argparse
 import ctypes as C
 import json
 import os
+import re
 import sys
 import time
 from dataclasses import replace
@@ -35,6 +36,9 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path[:0] = [os.path.join(ROOT, "uor-r4_amd"), os.path.join(ROOT, "oracle")]
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+# Measured HBM bytes per launch of the decode kernel (rocprofv3 FETCH_SIZE and WRITE_SIZE passes,
+# scaled by a copy kernel's reading), for the workload it names.
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fbs_decode_c3_b1024_traffic.md")
 
 
 def parse():
@@ -50,7 +54,43 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample time")
     p.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cores)")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--copy-probe-mib", type=int, default=0,
+                   help="only run one elementwise copy kernel over this many MiB (the reference "
+                        "reading for the FETCH_SIZE / WRITE_SIZE counters) and exit")
     return p.parse_args()
+
+
+def copy_probe(mib: int):
+    """One elementwise kernel that reads and writes mib MiB each (y = ~x over int32)."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    x = torch.arange(n, dtype=torch.int32, device="cuda:0")
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    torch.bitwise_not(x, out=y)
+    torch.cuda.synchronize()
+    assert int(y[-1]) == ~(n - 1)
+    print(json.dumps({"copy_probe": {"read_bytes": n * 4, "write_bytes": n * 4,
+                                     "kernel": "bitwise_not int32"}}))
+
+
+def workload_key(a) -> str:
+    return f"{a.config} batch {a.batch} prompt {a.prompt} gen {a.gen} seed {a.seed}"
+
+
+def measured_traffic(a):
+    """HBM bytes per decode launch from the committed counter summary, if it covers this exact
+    workload; None otherwise."""
+    try:
+        text = open(TRAFFIC_SUMMARY).read()
+    except OSError:
+        return None
+    w = re.search(r"^workload: (.+)$", text, re.M)
+    t = re.search(r"^traffic_bytes_per_launch: (\d+)$", text, re.M)
+    if not w or not t or w.group(1).strip() != workload_key(a):
+        return None
+    return int(t.group(1))
 
 
 def algorithmic_bytes_per_token(spec, mean_candidates: float) -> float:
@@ -69,6 +109,9 @@ def main():
               "(sequences are independent: shard the batch across GPUs, see DESIGN.md)",
               file=sys.stderr)
         sys.exit(2)
+    if a.copy_probe_mib:
+        copy_probe(a.copy_probe_mib)
+        return
     import torch
 
     import oracle
@@ -151,6 +194,11 @@ def main():
     bpt = algorithmic_bytes_per_token(spec, mean_cand)
     mean_launch_s = float(np.mean(launch_ms)) / 1e3
     achieved = bpt * tokens / mean_launch_s / 1e9
+    traffic = measured_traffic(a)
+    S = 1
+    while S < spec.width // 32:
+        S *= 2
+    kernel = f"fbs_decode<{(spec.width // 4 + 63) // 64}, {S}>"
 
     out = {
         "metric": "decoded tokens/sec at batch 1024, width 256 (1 GPU)",
@@ -167,7 +215,7 @@ def main():
         "data": "synthetic (seeded integer artifact and Zipf prompts)",
         "config": {
             "workload": f"{a.config} artifact at batch {B}: prefilled {a.prompt}-token prompts, "
-                        f"{G} greedy decode steps per timed step",
+                        f"{G} greedy decode steps per timed step", "key": workload_key(a),
             "width": spec.width, "layers": spec.layers, "mlp": spec.mlp, "vocab": spec.vocab,
             "window": spec.window, "drawers": art.drawers, "probes": art.probes,
             "table": spec.table, "batch": B, "prompt": a.prompt, "gen": G,
@@ -175,9 +223,10 @@ def main():
         },
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "algorithmic_bytes_per_launch": round(bpt * tokens),
             "bytes_per_token": round(bpt, 1), "mean_candidate_rows": round(mean_cand, 1),
-            "kernel": "fbs_run<1>", "launch_ms": [round(x, 3) for x in launch_ms],
+            "kernel": kernel, "launch_ms": [round(x, 3) for x in launch_ms],
         },
         "prefill_tokens_per_s": round(B * a.prompt / prefill_s, 1),
     }
@@ -188,15 +237,15 @@ def main():
         hist_np = hist.cpu().numpy()
         pos_np = pos.cpu().numpy().view(np.uint32)
         first_np = first.cpu().numpy().view(np.uint32)
-        # Calibrate: a small run, then a sample sized to about --cpu-seconds.
+        # Calibrate: a small run, then a sample sized to about --cpu-seconds: every sequence
+        # (one per thread at a time) for as many leading decode steps as that allows.
         n_cal, g_cal = min(B, threads), min(G, 4)
         t0 = time.perf_counter()
         oracle.decode(art, first_np[:n_cal], g_cal - 1, threads=threads, in_state=st_np[:n_cal],
                       in_history=hist_np[:n_cal], in_position=pos_np[:n_cal], want_state=False)
         per_tok = (time.perf_counter() - t0) / (n_cal * g_cal)
-        g_cpu = min(G, 64)
-        n_cpu = int(max(threads, min(B, a.cpu_seconds / per_tok / g_cpu)))
-        n_cpu = min(B, max(1, (n_cpu // threads) * threads))
+        n_cpu = B if B < threads else (B // threads) * threads
+        g_cpu = int(min(G, max(4, a.cpu_seconds / per_tok / n_cpu)))
         t0 = time.perf_counter()
         res = oracle.decode(art, first_np[:n_cpu], g_cpu - 1, threads=threads,
                             in_state=st_np[:n_cpu], in_history=hist_np[:n_cpu],

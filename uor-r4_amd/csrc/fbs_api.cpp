@@ -20,9 +20,13 @@
 #include "fbs_int.h"
 
 namespace fbs {
-hipError_t launch_run(const DevModel &M, const RunArgs &A, uint32_t grid, size_t lds_bytes,
-                      hipStream_t stream);
-size_t lds_bytes(const DevModel &M);
+// The kernels: fbs_prefill.hip, fbs_decode.hip, fbs_rows.hip.
+hipError_t launch_fbs_prefill(const DevModel &M, const RunArgs &A, uint32_t grid, size_t lds,
+                              hipStream_t stream);
+hipError_t launch_fbs_decode(const DevModel &M, const RunArgs &A, uint32_t grid, size_t lds,
+                             hipStream_t stream);
+hipError_t launch_fbs_rows(const DevModel &M, const RunArgs &A, uint32_t grid, size_t lds,
+                           hipStream_t stream);
 }
 
 using namespace fbs;
@@ -415,7 +419,10 @@ int launch(uor_fbs_handle *h, RunArgs &A, hipStream_t stream) {
   int st = h->ensure_ring(grid);
   if (st) return st;
   A.ring = h->ring;
-  hipError_t e = launch_run(h->M, A, grid, h->lds_bytes, stream);
+  const bool decode = A.mode == kModeDecode;
+  hipError_t e = decode && A.gen == 0 ? launch_fbs_prefill(h->M, A, grid, h->lds_bytes, stream)
+                 : decode             ? launch_fbs_decode(h->M, A, grid, h->lds_bytes, stream)
+                                      : launch_fbs_rows(h->M, A, grid, h->lds_bytes, stream);
   if (e != hipSuccess) return hip_fail(e, "kernel launch");
   return 0;
 }

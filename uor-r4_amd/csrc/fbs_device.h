@@ -1,5 +1,5 @@
 // fbs_device.h - the device image of a SpiralCore/FBS model and the launch arguments, shared by
-// the kernels (fbs_kernel.hip) and the host side that builds them (fbs_api.cpp).
+// the kernels (fbs_run.h) and the host side that builds them (fbs_api.cpp).
 //
 // Layout in HBM (all tables uploaded once by uor_fbs_model_create, read by every sequence):
 //   per layer: gains (d i16), window taps ((W+1) x d i16, tap s = s positions back) and the
@@ -17,6 +17,7 @@
 #ifndef UOR_FBS_DEVICE_H
 #define UOR_FBS_DEVICE_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 namespace fbs {
@@ -28,6 +29,8 @@ constexpr uint32_t kMaxDrawers = 4096;
 constexpr uint32_t kMaxProbes = 64;
 constexpr uint32_t kMaxWindow = 64;
 constexpr int32_t kMaxKeyQ12 = 16384;  // |drawer key| bound that keeps a drawer score in 20 bits
+constexpr uint32_t kListCap = 2048;    // member ids staged in LDS per scan segment
+constexpr uint32_t kSeedWords = 384 + 256;  // the rsqrt and reciprocal seed tables (fbs_int.h)
 
 struct DevLayer {
   const int16_t *rec_gain;
@@ -61,6 +64,14 @@ struct DevModel {
   const int8_t *icosian;    // 120 * 8
   const uint64_t *keep_q31; // 16
 };
+
+// LDS bytes per block (the layout the kernels carve): the gather crossbar, the MLP outputs, the
+// drawer scores, the kept drawers, the staged member list, the seed tables, and every layer's
+// recurrence state (i64).
+inline size_t lds_bytes(const DevModel &M) {
+  return 4ull * (M.xbar_words + 2 * M.m + ((M.D + 3u) & ~3u) + kMaxProbes + kListCap + kSeedWords) +
+         8ull * M.L * M.d;
+}
 
 enum RunMode : uint32_t { kModeSequences = 0, kModeDecode = 1, kModeScore = 2 };
 

@@ -1,4 +1,6 @@
-// fbs_kernel.hip - the SpiralCore/FBS integer decode step for gfx950 (MI355X).
+// fbs_run.h - the SpiralCore/FBS integer decode step for gfx950 (MI355X): the device code of
+// the three kernels (fbs_prefill.hip, fbs_decode.hip, fbs_rows.hip), which differ only in the
+// phase compiled in.
 //
 // One 64-lane wavefront runs one sequence through every step of its run (teacher-forced
 // sequences, greedy decode, or scoring). Per step (RS crates/uor-r4-integer/src/stack/
@@ -15,10 +17,17 @@
 // lexicographic min over DPP lane exchanges, so the outputs do not depend on lane order.
 // A block is one wavefront: lanes hand data to each other through LDS under wavefront-scope
 // fences (LDS operations of a wavefront complete in order), never through a workgroup barrier.
+#ifndef UOR_FBS_RUN_H
+#define UOR_FBS_RUN_H
+
+#include <hip/hip_runtime.h>
+
 #include "fbs_device.h"
 #include "fbs_int.h"
 
 namespace fbs {
+
+static_assert(kRsqrtSeedWords + kRecipSeedWords == kSeedWords, "seed table size");
 
 // ---------------------------------------------------------------------------------------------
 // Wave-level primitives.
@@ -234,7 +243,6 @@ __device__ __forceinline__ void gate_apply(const DevModel &M, const Seeds &sd,
 // ---------------------------------------------------------------------------------------------
 // The writer.
 
-constexpr uint32_t kListCap = 2048;  // member ids staged in LDS per scan segment
 constexpr uint32_t kWindowChunk = 8; // window rows in flight per lane
 constexpr int kScanUnroll = 4;       // row groups per pipeline stage
 
@@ -716,8 +724,13 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
   return 0;
 }
 
-template <int Q, int SW>
-__global__ __launch_bounds__(64) void fbs_run(DevModel M, RunArgs A) {
+// The phase a kernel is compiled for. Prefill: decode launches with no generated step (the
+// prompt, its last choice, the state out). Decode: decode launches that generate. Rows: the
+// teacher-forced modes, sequences and score.
+enum Phase : int { kPhasePrefill = 0, kPhaseDecode = 1, kPhaseRows = 2 };
+
+template <int Q, int SW, int PH>
+__device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
   extern __shared__ __align__(16) int32_t lds[];
   Lds S;
   {
@@ -775,9 +788,9 @@ __global__ __launch_bounds__(64) void fbs_run(DevModel M, RunArgs A) {
     wave_sync();
     int status = 0;
     uint32_t chosen = 0;
-    const bool decode = A.mode == kModeDecode;
+    constexpr bool decode = PH != kPhaseRows;
     const uint32_t *toks = A.tokens + (uint64_t)s * A.len;
-    const uint32_t steps = decode ? A.len + A.gen : A.len;
+    const uint32_t steps = PH == kPhaseDecode ? A.len + A.gen : A.len;
     unsigned long long hits = 0;
     for (uint32_t t = 0; t < steps; t++) {
       if (pos >= M.context) {
@@ -787,9 +800,9 @@ __global__ __launch_bounds__(64) void fbs_run(DevModel M, RunArgs A) {
       // Decode: the prompt's tokens, then each choice fed back (fbs-toks.rs:1513-1533); the
       // writer runs at the prompt's last step and every generated one. Sequences and score:
       // every token of the row, the writer wherever its choice is used.
-      const uint32_t tok = decode && t >= A.len ? chosen : toks[t];
+      const uint32_t tok = PH == kPhaseDecode && t >= A.len ? chosen : toks[t];
       const uint64_t at = (uint64_t)s * A.len + t;
-      const bool seq = A.mode == kModeSequences;
+      const bool seq = !decode && A.mode == kModeSequences;
       const bool want = decode ? t + 1 >= A.len : (seq || A.out_tokens || t + 1 < A.len);
       uint32_t *kept_out = seq && A.out_kept ? A.out_kept + at * M.P : nullptr;
       int32_t *query_out = seq && A.out_query ? A.out_query + at * d : nullptr;
@@ -802,11 +815,11 @@ __global__ __launch_bounds__(64) void fbs_run(DevModel M, RunArgs A) {
           if (want) A.out_tokens[(uint64_t)s * (A.gen + 1) + t + 1 - A.len] = chosen;
         } else {
           if (A.out_tokens) A.out_tokens[at] = chosen;
-          if (A.mode == kModeScore && t + 1 < A.len && chosen == toks[t + 1]) hits++;
+          if (!seq && t + 1 < A.len && chosen == toks[t + 1]) hits++;
         }
       }
     }
-    if (A.mode == kModeScore && lane == 0 && hits) atomicAdd(A.matches, hits);
+    if (!decode && A.mode == kModeScore && lane == 0 && hits) atomicAdd(A.matches, hits);
     if (decode && status == 0) {
       for (uint32_t l = 0; l < L; l++)
 #pragma unroll
@@ -833,34 +846,44 @@ __global__ __launch_bounds__(64) void fbs_run(DevModel M, RunArgs A) {
 
 // The (quaternions per lane, lanes per writer row) pairs widths 32..1024 produce:
 // d <= 256 -> Q 1 with S 1, 2, 4, 8; d <= 512 -> Q 2, S 16; d <= 1024 -> Q 4, S 32.
-template __global__ void fbs_run<1, 1>(DevModel, RunArgs);
-template __global__ void fbs_run<1, 2>(DevModel, RunArgs);
-template __global__ void fbs_run<1, 4>(DevModel, RunArgs);
-template __global__ void fbs_run<1, 8>(DevModel, RunArgs);
-template __global__ void fbs_run<2, 16>(DevModel, RunArgs);
-template __global__ void fbs_run<4, 32>(DevModel, RunArgs);
+using KernelFn = void (*)(DevModel, RunArgs);
+struct KernelSet {
+  KernelFn q1s1, q1s2, q1s4, q1s8, q2s16, q4s32;
+};
 
-// LDS bytes per block for a model (the layout fbs_run carves).
-size_t lds_bytes(const DevModel &M) {
-  return 4ull * (M.xbar_words + 2 * M.m + ((M.D + 3u) & ~3u) + kMaxProbes + kListCap +
-                 kRsqrtSeedWords + kRecipSeedWords) +
-         8ull * M.L * M.d;
-}
-
-// Launch entry used by the host side (fbs_api.cpp).
-hipError_t launch_run(const DevModel &M, const RunArgs &A, uint32_t grid, size_t lds,
-                      hipStream_t stream) {
-  dim3 g(grid), b(kWave);
+// Launches the member of `k` for the model's shape: one 64-lane block per resident sequence.
+inline hipError_t launch_shape(const KernelSet &k, const DevModel &M, const RunArgs &A,
+                               uint32_t grid, size_t lds, hipStream_t stream) {
   uint32_t S = 1;
   while (S < M.d / 32) S <<= 1;
-  if (M.qpl == 1 && S == 1) hipLaunchKernelGGL((fbs_run<1, 1>), g, b, lds, stream, M, A);
-  else if (M.qpl == 1 && S == 2) hipLaunchKernelGGL((fbs_run<1, 2>), g, b, lds, stream, M, A);
-  else if (M.qpl == 1 && S == 4) hipLaunchKernelGGL((fbs_run<1, 4>), g, b, lds, stream, M, A);
-  else if (M.qpl == 1 && S == 8) hipLaunchKernelGGL((fbs_run<1, 8>), g, b, lds, stream, M, A);
-  else if (M.qpl == 2 && S == 16) hipLaunchKernelGGL((fbs_run<2, 16>), g, b, lds, stream, M, A);
-  else if (M.qpl == 4 && S == 32) hipLaunchKernelGGL((fbs_run<4, 32>), g, b, lds, stream, M, A);
-  else return hipErrorInvalidValue;
-  return hipGetLastError();
+  KernelFn f = M.qpl == 1 && S == 1    ? k.q1s1
+               : M.qpl == 1 && S == 2  ? k.q1s2
+               : M.qpl == 1 && S == 4  ? k.q1s4
+               : M.qpl == 1 && S == 8  ? k.q1s8
+               : M.qpl == 2 && S == 16 ? k.q2s16
+               : M.qpl == 4 && S == 32 ? k.q4s32
+                                       : nullptr;
+  if (!f) return hipErrorInvalidValue;
+  DevModel m = M;
+  RunArgs a = A;
+  void *args[] = {&m, &a};
+  hipError_t e = hipLaunchKernel((const void *)f, dim3(grid), dim3(kWave), args, lds, stream);
+  return e != hipSuccess ? e : hipGetLastError();
 }
 
+// The phase's kernels: `NAME<Q, SW>` and `hipError_t launch_NAME(M, A, grid, lds, stream)`.
+#define FBS_PHASE_KERNELS(NAME, PH)                                                          \
+  template <int Q, int SW>                                                                    \
+  __global__ __launch_bounds__(64) void NAME(DevModel M, RunArgs A) {                         \
+    run<Q, SW, PH>(M, A);                                                                     \
+  }                                                                                           \
+  hipError_t launch_##NAME(const DevModel &M, const RunArgs &A, uint32_t grid, size_t lds,    \
+                           hipStream_t stream) {                                              \
+    static const KernelSet k = {NAME<1, 1>, NAME<1, 2>, NAME<1, 4>,                           \
+                                NAME<1, 8>, NAME<2, 16>, NAME<4, 32>};                         \
+    return launch_shape(k, M, A, grid, lds, stream);                                          \
+  }
+
 }  // namespace fbs
+
+#endif
