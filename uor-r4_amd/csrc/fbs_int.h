@@ -630,13 +630,18 @@ FBS_HD void unit_q30_wide(const int32_t raw[4], uint64_t eps, int32_t u[4]) {
   }
 }
 
-// unit_q30 in 64-bit arithmetic (the kernels' form; equal to unit_q30_wide for every input).
-// X = sum v^2 + eps < 2^65 + 2^13 is normalised to Xn = X 4^k in [2^62, 2^64); r = isqrt(Xn)
-// comes from the 32-bit reciprocal square root and one Newton step on the exact remainder;
-// s = isqrt(X 2^32) = isqrt(Xn 4^(16 - k)) is r shifted, or r 2^j plus the j fractional bits f
-// of the root, estimated from the remainder and checked exactly; each quotient comes from a
-// 32-bit reciprocal of s and is corrected on its exact remainder (small, so its low 64 bits
-// are the remainder).
+// unit_q30 in 64-bit arithmetic without data-dependent branches (the kernels' form; equal to
+// unit_q30_wide for every input). With X = sum v^2 + eps < 2^65 + 2^13 and Y = X 2^32:
+//  1. Xn = X 4^k in [2^62, 2^64) (k = -1: Xn = floor(X / 4)); y = rsqrt_q46(Xn / 2^32) ~
+//     2^62 / sqrt(Xn) (relative error within 2^-28.9, checked over every input); r = Xn/2^32
+//     y / 2^30 and one Newton step on the exact remainder give r within 1 of isqrt(Xn).
+//  2. s0 = r 2^j + floor((Xn - r^2) (y / 4) / 2^(61 - j)) for j = 16 - k > 0, or r >> -j, is
+//     within 1 of s = isqrt(Y); the remainder Y - s0^2 is below 2^63 in magnitude, so its
+//     value modulo 2^64 is exact, and one step down and one up give s.
+//  3. w = recip_q63 of the top 32 bits of s normalised (relative error in [-2^-30.4, 0],
+//     checked over every input; truncating s adds at most 2^-31) puts (a 2^46 w) / s within
+//     0.76 of a 2^46 / s <= 2^30 + 2^14, so q0 is within 1 of the floor; one step each way on
+//     the exact remainder a 2^46 - q0 s (small, exact modulo 2^64) gives q.
 FBS_HD void unit_q30(const int32_t raw[4], uint64_t eps, int32_t u[4], const Seeds &sd = Seeds()) {
   uint32_t a[4];
   uint64_t xl = eps;
@@ -644,51 +649,33 @@ FBS_HD void unit_q30(const int32_t raw[4], uint64_t eps, int32_t u[4], const See
 #pragma unroll
   for (int c = 0; c < 4; c++) {
     a[c] = uabs32(raw[c]);
-    uint64_t t = xl + (uint64_t)a[c] * a[c];
+    const uint64_t t = xl + (uint64_t)a[c] * a[c];
     xh += t < xl;
     xl = t;
   }
-  if ((xh | xl) == 0) {
-#pragma unroll
-    for (int c = 0; c < 4; c++) u[c] = 0;
-    return;
-  }
-  int k;
-  uint64_t xn;
-  if (xh) {  // X in [2^64, 2^65 + 2^13): Xn = X / 4 (truncated; only the estimate uses it)
-    xn = ((uint64_t)xh << 62) | (xl >> 2);
-    k = -1;
-  } else {
-    int z = clz64(xl) & ~1;
-    xn = xl << z;
-    k = z >> 1;
-  }
-  uint64_t y = rsqrt_q46((uint32_t)(xn >> 32), sd.rsqrt);      // 2^46 / sqrt(Xn / 2^32)
-  uint64_t r = ((xn >> 32) * y) >> 30;               // ~ sqrt(Xn) < 2^32
-  if (r > 0xffffffffull) r = 0xffffffffull;
-  int64_t diff = (int64_t)(xn - r * r);
+  // X = 0 (all zero, eps 0) gives u = 0 by the same steps on X = 1.
+  xl = (xh == 0 && xl == 0) ? 1 : xl;
+  const int z = clz64(xl) & ~1;
+  const uint64_t xn = xh ? (((uint64_t)xh << 62) | (xl >> 2)) : (xl << z);
+  const int j = xh ? 17 : 16 - (z >> 1);              // [-15, 17]
+  const uint64_t xt = xn >> 32;
+  const uint64_t y = rsqrt_q46((uint32_t)xt, sd.rsqrt);
+  uint64_t r = (xt * y) >> 30;
+  r = r > 0xffffffffull ? 0xffffffffull : r;
+  const int64_t diff = (int64_t)(xn - r * r);
   r = (uint64_t)((int64_t)r + (((diff >> 16) * (int64_t)y) >> 47));
-  if (r > 0xffffffffull) r = 0xffffffffull;
-  if (r < (1ull << 31)) r = 1ull << 31;
-  while (r * r > xn) r--;
-  while (r < 0xffffffffull && (r + 1) * (r + 1) <= xn) r++;
-  uint64_t s;
-  const int j = 16 - k;                               // [-15, 17]
-  if (j <= 0) {
-    s = r >> (-j);
-  } else {
-    // s = r 2^j + f: the largest f < 2^j with f (2^(j+1) r + f) <= N - (r 2^j)^2, where
-    // N - (r 2^j)^2 = rem 4^j (+ (X mod 4) 2^32 when Xn = floor(X / 4), j = 17).
-    uint64_t rem = xn - r * r;                        // [0, 2 r]
-    uint64_t f = (rem * y) >> (63 - j);               // ~ rem 2^(j-1) / r
-    const uint64_t fmax = (1ull << j) - 1;
-    if (f > fmax) f = fmax;
-    const u128 lim = ((u128)rem << (2 * j)) + (xh ? (u128)(xl & 3) << 32 : (u128)0);
-    const uint64_t base = r << (j + 1);
-    while (f > 0 && (u128)f * (base + f) > lim) f--;
-    while (f < fmax && (u128)(f + 1) * (base + f + 1) <= lim) f++;
-    s = (r << j) + f;
-  }
+  r = r > 0xffffffffull ? 0xffffffffull : r < (1ull << 31) ? (1ull << 31) : r;
+  const int64_t rem = (int64_t)(xn - r * r);          // [-2^33, 2^34]
+  const int64_t f = (rem * (int64_t)(y >> 2)) >> (61 - (j > 0 ? j : 0));
+  uint64_t s = j > 0 ? (r << j) + (uint64_t)f : r >> -j;
+  // Y - s^2 modulo 2^64: s < 2^50, so s^2 mod 2^64 = sl^2 + (2 sh sl mod 2^32) 2^32.
+  const uint32_t sl = (uint32_t)s, shi = (uint32_t)(s >> 32);
+  int64_t dy = (int64_t)((xl << 32) - ((uint64_t)sl * sl + ((uint64_t)(2u * shi * sl) << 32)));
+  const bool down = dy < 0;
+  dy = down ? dy + (int64_t)(2 * s - 1) : dy;
+  s = down ? s - 1 : s;
+  const bool up = dy >= (int64_t)(2 * s + 1);
+  s = up ? s + 1 : s;
   // u_c = floor(a_c 2^46 / s), s in [2^16, 2^49].
   const int zs = clz64(s);
   const uint64_t w = recip_q63((uint32_t)((s << zs) >> 32), sd.recip);  // ~ 2^95 / (s << zs)
@@ -696,15 +683,11 @@ FBS_HD void unit_q30(const int32_t raw[4], uint64_t eps, int32_t u[4], const See
 #pragma unroll
   for (int c = 0; c < 4; c++) {
     uint64_t q = ((uint64_t)a[c] * w) >> sh;
-    int64_t rem = (int64_t)(((uint64_t)a[c] << 46) - q * s);
-    while (rem < 0) {
-      q--;
-      rem += (int64_t)s;
-    }
-    while (rem >= (int64_t)s) {
-      q++;
-      rem -= (int64_t)s;
-    }
+    int64_t rq = (int64_t)(((uint64_t)a[c] << 46) - q * s);
+    const bool qd = rq < 0;
+    rq = qd ? rq + (int64_t)s : rq;
+    q = qd ? q - 1 : q;
+    q = rq >= (int64_t)s ? q + 1 : q;
     u[c] = raw[c] < 0 ? -(int32_t)q : (int32_t)q;
   }
 }
