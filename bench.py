@@ -51,7 +51,7 @@ def parse():
     p.add_argument("--prompt", type=int, default=1024)
     p.add_argument("--gen", type=int, default=1024)
     p.add_argument("--seed", type=int, default=2026120203)
-    p.add_argument("--cpu-seconds", type=float, default=12.0, help="target CPU-baseline sample time")
+    p.add_argument("--cpu-seconds", type=float, default=24.0, help="target CPU-baseline sample time")
     p.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cores)")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--copy-probe-mib", type=int, default=0,

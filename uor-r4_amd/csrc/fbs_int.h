@@ -655,8 +655,11 @@ FBS_HD void unit_q30(const int32_t raw[4], uint64_t eps, int32_t u[4], const See
   }
   // X = 0 (all zero, eps 0) gives u = 0 by the same steps on X = 1.
   xl = (xh == 0 && xl == 0) ? 1 : xl;
+  // Both normalisations are formed and one is kept by masks (one basic block, so that the
+  // scheduler can interleave independent rotations).
   const int z = clz64(xl) & ~1;
-  const uint64_t xn = xh ? (((uint64_t)xh << 62) | (xl >> 2)) : (xl << z);
+  const uint64_t big = 0ull - (uint64_t)(xh != 0);
+  const uint64_t xn = ((((uint64_t)xh << 62) | (xl >> 2)) & big) | ((xl << z) & ~big);
   const int j = xh ? 17 : 16 - (z >> 1);              // [-15, 17]
   const uint64_t xt = xn >> 32;
   const uint64_t y = rsqrt_q46((uint32_t)xt, sd.rsqrt);
@@ -666,8 +669,10 @@ FBS_HD void unit_q30(const int32_t raw[4], uint64_t eps, int32_t u[4], const See
   r = (uint64_t)((int64_t)r + (((diff >> 16) * (int64_t)y) >> 47));
   r = r > 0xffffffffull ? 0xffffffffull : r < (1ull << 31) ? (1ull << 31) : r;
   const int64_t rem = (int64_t)(xn - r * r);          // [-2^33, 2^34]
-  const int64_t f = (rem * (int64_t)(y >> 2)) >> (61 - (j > 0 ? j : 0));
-  uint64_t s = j > 0 ? (r << j) + (uint64_t)f : r >> -j;
+  const int jp = j > 0 ? j : 0, jn = j > 0 ? 0 : -j;
+  const int64_t f = (rem * (int64_t)(y >> 2)) >> (61 - jp);
+  const uint64_t frac = 0ull - (uint64_t)(j > 0);
+  uint64_t s = (((r << jp) + (uint64_t)f) & frac) | ((r >> jn) & ~frac);
   // Y - s^2 modulo 2^64: s < 2^50, so s^2 mod 2^64 = sl^2 + (2 sh sl mod 2^32) 2^32.
   const uint32_t sl = (uint32_t)s, shi = (uint32_t)(s >> 32);
   int64_t dy = (int64_t)((xl << 32) - ((uint64_t)sl * sl + ((uint64_t)(2u * shi * sl) << 32)));
