@@ -156,3 +156,21 @@ def test_run_twice_is_identical_and_batch_independent():
         np.testing.assert_array_equal(x, y)
     for x, y in zip(a, one):
         np.testing.assert_array_equal(x[17:18], y)
+
+
+def test_repeated_queries_reuse_the_writer_exactly():
+    # A token fed again and again settles the state, so consecutive queries repeat exactly and
+    # the kernel takes the writer's last result instead of scanning again. Every position's
+    # token, kept drawers and query must still equal the oracle's.
+    spec = reduced("c3", context=96, layers=2)
+    art = synth.make_artifact(spec, 57)
+    rows = np.repeat(np.array([[11], [4703], [9200], [31000]], np.uint32), 96, axis=1)
+    print("repeated tokens c3 layers 2", flush=True)
+    st, want_t, want_k, want_q = oracle.sequences(art, rows, threads=4)
+    assert st == 0
+    tok, kept, query = Model(art).sequences(rows)
+    repeats = (query[:, 1:] == query[:, :-1]).all(-1).sum()
+    assert repeats > 20, repeats  # the reuse path runs
+    np.testing.assert_array_equal(query, want_q)
+    np.testing.assert_array_equal(kept, want_k)
+    np.testing.assert_array_equal(tok, want_t)

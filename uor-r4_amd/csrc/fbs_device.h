@@ -66,10 +66,11 @@ struct DevModel {
 };
 
 // LDS bytes per block (the layout the kernels carve): the gather crossbar, the MLP outputs, the
-// drawer scores, the kept drawers, the staged member list, the seed tables, and every layer's
-// recurrence state (i64).
+// drawer scores, the kept drawers, the staged member list, the writer's last query and token,
+// the seed tables, and every layer's recurrence state (i64).
 inline size_t lds_bytes(const DevModel &M) {
-  return 4ull * (M.xbar_words + 2 * M.m + ((M.D + 3u) & ~3u) + kMaxProbes + kListCap + kSeedWords) +
+  return 4ull * (M.xbar_words + 2 * M.m + ((M.D + 3u) & ~3u) + kMaxProbes + kListCap +
+                 ((M.d + 3u) & ~3u) + 4 + kSeedWords) +
          8ull * M.L * M.d;
 }
 

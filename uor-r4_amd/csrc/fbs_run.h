@@ -439,6 +439,8 @@ struct Lds {
   uint32_t *kept;    // kMaxProbes
   uint32_t *list;    // kListCap
   int64_t *st;       // L * d recurrence state
+  int32_t *wq;       // d: the query of the writer's last run
+  uint32_t *wmeta;   // 4: [0] that run's token, [1] nonzero once wq holds a query
   Seeds seeds;       // the reciprocal and reciprocal square root seed tables
 };
 
@@ -638,6 +640,14 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
         for (int c = 0; c < 4; c++) x[k][c] = sat_add32(x[k][c], S.xbar[pw_out[k][c]]);
     wave_sync();
     // ---- feed-forward block: the Hamilton gate of mlp_gate on mlp_up (session.rs:4005-4025).
+    // The gather words of MLP quaternion group j load one group ahead (the first during the
+    // norm), so that their latency hides behind the previous work.
+    uint32_t pg[4], pu[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      pg[c] = prog_word(ly.prog, M.s_mlp_gate + c, lane);
+      pu[c] = prog_word(ly.prog, M.s_mlp_up + c, lane);
+    }
     norm_gain<Q>(M, S.seeds, x, qv, g_mlp, gd_mlp, v);
     publish64<Q>(S.xbar, v, qv, qi);
     wave_sync();
@@ -645,14 +655,21 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
 #pragma unroll 1
     for (uint32_t j = 0; j < M.mpl; j++) {
       const uint32_t mq = lane + kWave * j;
-      if (mq < M.nm) {
-        int32_t gq[4], up[4];
-        int64_t mo[4];
+      int32_t gq[4], up[4];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        gq[c] = S.xbar[pg[c]];
+        up[c] = S.xbar[pu[c]];
+      }
+      if (j + 1 < M.mpl) {
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-          gq[c] = S.xbar[prog_word(ly.prog, M.s_mlp_gate + 4 * j + c, lane)];
-          up[c] = S.xbar[prog_word(ly.prog, M.s_mlp_up + 4 * j + c, lane)];
+          pg[c] = prog_word(ly.prog, M.s_mlp_gate + 4 * (j + 1) + c, lane);
+          pu[c] = prog_word(ly.prog, M.s_mlp_up + 4 * (j + 1) + c, lane);
         }
+      }
+      if (mq < M.nm) {
+        int64_t mo[4];
         if (M.raw_gates) {
           // q = 2 u with u the unit quaternion; u (x) up fits in 64 bits.
           int32_t u[4];
@@ -705,6 +722,8 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
   }
   int64_t v[Q][4];
   norm_gain<Q>(M, S.seeds, x, qv, g_fin, gd_fin, v);
+  int4 qq[Q];
+  bool same = true;  // this lane's channels equal the query of the writer's last run
 #pragma unroll
   for (int k = 0; k < Q; k++)
     if (qv[k]) {
@@ -714,12 +733,30 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
         int32_t y = to_exp_i32(v[k][c], kNormFineExp, kQ12Exp);
         qa[c] = y > 32767 ? 32767 : y < -32768 ? -32768 : y;
       }
-      int4 qq = make_int4(qa[0], qa[1], qa[2], qa[3]);
-      *(int4 *)(S.xbar + 4 * qi[k]) = qq;
-      if (query_out) *(int4 *)(query_out + 4 * qi[k]) = qq;
+      qq[k] = make_int4(qa[0], qa[1], qa[2], qa[3]);
+      *(int4 *)(S.xbar + 4 * qi[k]) = qq[k];
+      if (query_out) *(int4 *)(query_out + 4 * qi[k]) = qq[k];
+      const int4 old = *(const int4 *)(S.wq + 4 * qi[k]);
+      same = same && old.x == qa[0] && old.y == qa[1] && old.z == qa[2] && old.w == qa[3];
     }
   wave_sync();
-  if (want_writer) *chosen = writer<SW>(M, S.xbar, S.dscore, S.kept, S.list, lane, kept_out);
+  if (want_writer) {
+    // The writer's token and kept drawers are a function of the query alone: a query equal to
+    // the last one the writer ran on (a sequence settled on a fixed point) takes its result.
+    if (S.wmeta[1] != 0 && __all(same)) {
+      *chosen = S.wmeta[0];
+      if (kept_out && lane < M.P) kept_out[lane] = M.head == 1 ? 0u : S.kept[lane];
+    } else {
+      *chosen = writer<SW>(M, S.xbar, S.dscore, S.kept, S.list, lane, kept_out);
+#pragma unroll
+      for (int k = 0; k < Q; k++)
+        if (qv[k]) *(int4 *)(S.wq + 4 * qi[k]) = qq[k];
+      if (lane == 0) {
+        S.wmeta[0] = *chosen;
+        S.wmeta[1] = 1;
+      }
+    }
+  }
   wave_sync();
   return 0;
 }
@@ -745,6 +782,11 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
     at += kMaxProbes;
     S.list = (uint32_t *)(lds + at);
     at += kListCap;
+    S.wq = lds + at;
+    at += (M.d + 3u) & ~3u;
+    S.wmeta = (uint32_t *)(lds + at);
+    at += 4;
+    if (threadIdx.x == 0) S.wmeta[1] = 0;  // no query remembered yet
     uint32_t *seed_lds = (uint32_t *)(lds + at);
     at += kRsqrtSeedWords + kRecipSeedWords;
     S.st = (int64_t *)(lds + at);
