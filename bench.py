@@ -183,17 +183,27 @@ def main():
     value = tokens / (ms_per_step / 1e3)
 
     # Candidate rows per decoded token, exactly, from a teacher-forced replay of a sample of
-    # the decoded sequences (the replay reproduces the decode's states and kept drawers).
+    # the decoded sequences: the prompt, the prefill's choice, then the reply (the replay
+    # reproduces the decode's states, queries and kept drawers at positions prompt ..).
     host_reply = reply.cpu().numpy().view(np.uint32)
-    sample = min(B, 32)
-    replay = np.concatenate([prompts[:sample], host_reply[:sample, :-1]], axis=1)
-    _, kept, _ = model.sequences(replay, want_query=False)
+    host_first = first.cpu().numpy().view(np.uint32)
+    sample = min(B, 64)
+    replay = np.concatenate([prompts[:sample], host_first[:sample], host_reply[:sample, :-1]], axis=1)
+    _, kept, query = model.sequences(replay)
     sizes = art.drawer_sizes()
     cand = sizes[kept[:, a.prompt:, :].astype(np.int64)].sum(-1)
     mean_cand = float(cand.mean())
     bpt = algorithmic_bytes_per_token(spec, mean_cand)
     mean_launch_s = float(np.mean(launch_ms)) / 1e3
     achieved = bpt * tokens / mean_launch_s / 1e9
+    # The writer takes its previous result when a query repeats its last run's exactly (a
+    # sequence settled on a fixed point): those tokens scan no candidate rows. Each launch
+    # starts with nothing remembered, so the first generated token always scans.
+    q = query[:, a.prompt:]
+    reused = np.zeros(q.shape[:2], dtype=bool)
+    reused[:, 1:] = (q[:, 1:] == q[:, :-1]).all(-1)
+    scanned_cand = float(np.where(reused, 0, cand).mean())
+    bpt_scanned = algorithmic_bytes_per_token(spec, scanned_cand)
     traffic = measured_traffic(a)
     S = 1
     while S < spec.width // 32:
@@ -226,6 +236,10 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
             "algorithmic_bytes_per_launch": round(bpt * tokens),
             "bytes_per_token": round(bpt, 1), "mean_candidate_rows": round(mean_cand, 1),
+            "writer_reuse_fraction": round(float(reused.mean()), 4),
+            "bytes_per_token_scanned": round(bpt_scanned, 1),
+            "frac_scanned": round(bpt_scanned * tokens / mean_launch_s / 1e9 / HBM_PEAK_GBS, 4),
+            "replay_sample": sample,
             "kernel": kernel, "launch_ms": [round(x, 3) for x in launch_ms],
         },
         "prefill_tokens_per_s": round(B * a.prompt / prefill_s, 1),
