@@ -229,3 +229,42 @@ def test_rms_norm_fine_equals_oracle(hp):
         hp.fbs_hp_rms_norm_fine(x.ctypes.data_as(P), n, eps_m, eps_e, got.ctypes.data_as(P))
         oracle.lib().fbs_oracle_rms_norm_fine(x.ctypes.data_as(P), n, eps_m, eps_e, want.ctypes.data_as(P))
         np.testing.assert_array_equal(got, want)
+
+
+def _near_square_quaternions(rng, n):
+    """Quaternions whose sum of squares puts X 2^32 next to a perfect square m^2 (from either
+    side), split greedily into four squares: the root and quotient corrections of unit_q30 run
+    on exactly these inputs."""
+    raw = []
+    while len(raw) < n:
+        m = (rng.getrandbits(64) >> rng.randint(0, 47)) | 1
+        if rng.random() < 0.5:
+            m = (m << 17) ^ rng.getrandbits(17)
+        t = (m * m >> 32) + rng.randint(0, 2)
+        if t >> 65:
+            continue
+        q, left = [], t
+        for _ in range(4):
+            v = min(math.isqrt(left), 1 << 31)
+            left -= v * v
+            q.append(-(1 << 31) if v == 1 << 31 else (v if rng.random() < 0.5 else -v))
+        raw.append(q)
+    return np.array(raw, np.int32)
+
+
+@pytest.mark.parametrize("eps", [0, 4295])
+def test_unit_q30_equals_the_128bit_form(hp, eps):
+    # The kernels' branch-free unit quaternion against the 128-bit restoring form (both from
+    # fbs_int.h, compiled for the host): random widths, near-perfect squares, equal components.
+    hp.fbs_hp_unit_check.argtypes = [P, C.c_uint64, C.c_uint64]
+    hp.fbs_hp_unit_check.restype = C.c_uint64
+    rng = random.Random(91 + eps)
+    nprng = np.random.default_rng(92 + eps)
+    wide = (nprng.integers(-(1 << 31), 1 << 31, size=(400000, 4), dtype=np.int64)
+            >> nprng.integers(0, 32, size=(400000, 1))).astype(np.int32)
+    v = (nprng.integers(-(1 << 31), 1 << 31, size=100000, dtype=np.int64)
+         >> nprng.integers(0, 32, size=100000)).astype(np.int32)
+    ties = np.stack([v, v, np.zeros_like(v), np.where(v % 2 == 0, v, 0)], 1)
+    for raw in (wide, ties, _near_square_quaternions(rng, 60000), _raw_quaternions(rng, 20000)):
+        raw = np.ascontiguousarray(raw, np.int32)
+        assert hp.fbs_hp_unit_check(raw.ctypes.data_as(P), eps, len(raw)) == 0
