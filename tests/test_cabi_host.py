@@ -268,3 +268,39 @@ def test_unit_q30_equals_the_128bit_form(hp, eps):
     for raw in (wide, ties, _near_square_quaternions(rng, 60000), _raw_quaternions(rng, 20000)):
         raw = np.ascontiguousarray(raw, np.int32)
         assert hp.fbs_hp_unit_check(raw.ctypes.data_as(P), eps, len(raw)) == 0
+
+
+def test_div_2p96_is_the_exact_floor(hp):
+    # floor(2^96 / s) for s in [2^34, 2^64): random widths, powers of two and their neighbours,
+    # divisors of 2^96 - k for small k (quotients landing on and next to integers).
+    hp.fbs_hp_div_2p96_many.argtypes = [P, P, C.c_uint64]
+    rng = random.Random(97)
+    ss = [rng.getrandbits(64) >> rng.randint(0, 30) for _ in range(200000)]
+    ss += [(1 << e) + dlt for e in range(34, 64) for dlt in (-1, 0, 1) if (1 << e) + dlt >= 1 << 34]
+    ss += [(1 << 64) - 1 - k for k in range(64)]
+    for _ in range(20000):
+        q = rng.randint(1 << 32, (1 << 62)) >> rng.randint(0, 28)
+        s = (1 << 96) // q
+        ss += [x for x in (s - 1, s, s + 1) if (1 << 34) <= x < (1 << 64)]
+    ss = [x for x in ss if (1 << 34) <= x < (1 << 64)]
+    arr = np.array(ss, dtype=np.uint64)
+    out = np.zeros(len(arr), np.uint64)
+    hp.fbs_hp_div_2p96_many(arr.ctypes.data_as(P), out.ctypes.data_as(P), len(arr))
+    assert [int(o) for o in out] == [(1 << 96) // s for s in ss]
+
+
+def test_norm_factor_pow2_equals_the_general_form(hp):
+    # The kernels' RMSNorm factor for power-of-two widths against the general 128-bit form,
+    # including sums whose root extension f sits at its limit and epsilons that wrap.
+    hp.fbs_hp_norm_factor_check.argtypes = [P, P, C.c_uint64, C.c_uint32]
+    hp.fbs_hp_norm_factor_check.restype = C.c_uint64
+    rng = np.random.default_rng(98)
+    n = 300000
+    sums = (rng.integers(0, 2**63, n, dtype=np.uint64)
+            >> rng.integers(0, 64, n).astype(np.uint64)).astype(np.uint64)
+    r = rng.integers(1, 2**32, n // 2, dtype=np.uint64)
+    sums[: n // 2] = (r * r + rng.integers(0, 3, n // 2, dtype=np.uint64)) << rng.integers(0, 8, n // 2).astype(np.uint64)
+    eps = rng.choice(np.array([0, 1, 42950, 2**20, 2**40, 2**59, 2**60, 2**62, 2**63 - 1, -5],
+                              dtype=np.int64), n)
+    for log2n in (5, 8, 10):
+        assert hp.fbs_hp_norm_factor_check(sums.ctypes.data_as(P), eps.ctypes.data_as(P), n, log2n) == 0

@@ -24,6 +24,11 @@ void fbs_hp_div_many(const uint64_t *nhi, const uint64_t *nlo, const uint64_t *d
 
 uint32_t fbs_hp_rsqrt_q46(uint32_t t) { return rsqrt_q46(t); }
 
+// out[i] = div_2p96(s[i]) = floor(2^96 / s[i]) for s[i] in [2^34, 2^64).
+void fbs_hp_div_2p96_many(const uint64_t *s, uint64_t *out, uint64_t n) {
+  for (uint64_t i = 0; i < n; i++) out[i] = div_2p96(s[i]);
+}
+
 // norm_factor_pow2 against norm_factor on n (sum, eps) pairs at 2^log2n: mismatches.
 uint64_t fbs_hp_norm_factor_check(const uint64_t *sum, const int64_t *eps, uint64_t n, uint32_t log2n) {
   uint64_t bad = 0;

@@ -355,42 +355,81 @@ FBS_HD NormFactor norm_factor(uint64_t sum, uint32_t n, int64_t eps_int) {
   return f;
 }
 
-// floor(2^96 / s) for s in [2^34, 2^64): a 32-bit reciprocal estimate, two refinements on the
-// exact remainder (its high words times the reciprocal), then the exact floor.
+// A signed remainder below 2^66 in magnitude as hi 2^64 + lo (hi small and signed).
+struct Rem96 {
+  int64_t hi;
+  uint64_t lo;
+};
+
+// n - q d for a remainder n, q < 2^33 and d < 2^64.
+FBS_HD Rem96 rem_sub_qd(Rem96 n, uint64_t q, uint64_t d) {
+  const uint64_t p1 = q * (d & 0xffffffffull), p2 = q * (d >> 32);  // q d = p2 2^32 + p1
+  const uint64_t pl = p1 + (p2 << 32);
+  const uint64_t ph = (p2 >> 32) + (pl < p1);
+  Rem96 r;
+  r.lo = n.lo - pl;
+  r.hi = n.hi - (int64_t)ph - (int64_t)(n.lo < pl);
+  return r;
+}
+
+// One step each way toward 0 <= r < d: the quotient q and remainder r of a digit whose estimate
+// is within [q - UP, q + 1].
+template <int UP>
+FBS_HD void digit_fix(uint64_t &q, Rem96 &r, uint64_t d) {
+  if (r.hi < 0) {  // q one too large
+    q -= 1;
+    const uint64_t lo = r.lo + d;
+    r.hi += (int64_t)(lo < d);
+    r.lo = lo;
+  }
+#pragma unroll
+  for (int i = 0; i < UP; i++)
+    if (r.hi > 0 || r.lo >= d) {
+      q += 1;
+      r.hi -= (int64_t)(r.lo < d);
+      r.lo -= d;
+    }
+}
+
+// floor(2^96 / s) for s in [2^34, 2^64), as two 31-bit quotient digits of 2^E / D with
+// D = s 2^zs normalised and E = 96 + zs. w = recip_q63(D / 2^32) is 2^95 / D within a relative
+// [-2^-30.4, 2^-31] (the seed error, checked over every input, and the truncation of D), so each
+// digit estimate is within [q - 3, q + 1] and the exact remainder (below 2^66, kept in 96 bits)
+// fixes it in fixed steps.
 FBS_HD uint64_t div_2p96(uint64_t s, const Seeds &sd = Seeds()) {
   const int zs = clz64(s);                            // [0, 29]
   const uint64_t D = s << zs;                         // [2^63, 2^64)
-  const int E = 96 + zs;                              // Q = floor(2^E / D) < 2^62
-  const uint64_t w = recip_q63((uint32_t)(D >> 32), sd.recip);  // ~ 2^95 / D
-  uint64_t q = w << (E - 95);
-  const u128 top = (u128)1 << E;
-#pragma unroll
-  for (int it = 0; it < 2; it++) {
-    const i128 rem = (i128)(top - (u128)q * D);       // small, signed
-    const i128 hi = rem >> 40;                        // rem / 2^40, |.| < 2^63
-    q = (uint64_t)((int64_t)q + (int64_t)(((i128)(int64_t)hi * (int64_t)w) >> 55));
-  }
-  i128 rem = (i128)(top - (u128)q * D);
-  while (rem < 0) {
-    q--;
-    rem += D;
-  }
-  while (rem >= (i128)D) {
-    q++;
-    rem -= D;
-  }
-  return q;
+  const int E = 96 + zs;
+  const uint64_t w = recip_q63((uint32_t)(D >> 32), sd.recip);  // ~ 2^95 / D, <= 2^32
+  // Digit 1: Q1 = floor(2^(E-31) / D) <= 2^31.
+  uint64_t q1 = w >> (126 - E);
+  Rem96 n1;
+  n1.hi = (int64_t)1 << (E - 95);
+  n1.lo = 0;
+  Rem96 r1 = rem_sub_qd(n1, q1, D);
+  digit_fix<2>(q1, r1, D);
+  // Digit 2: Q0 = floor(R1 2^31 / D) < 2^31, R1 in [0, D).
+  const uint64_t R = r1.lo;
+  uint64_t q0 = (((R >> 32) * w) + (((R & 0xffffffffull) * w) >> 32)) >> 32;
+  Rem96 n2;
+  n2.hi = (int64_t)(R >> 33);
+  n2.lo = R << 31;
+  Rem96 r0 = rem_sub_qd(n2, q0, D);
+  digit_fix<3>(q0, r0, D);
+  return (q1 << 31) + q0;
 }
 
 // norm_factor for n = 2^log2n in 64-bit steps (the kernels' form; equal to norm_factor).
 // With m = ms mod 2^60 and M = 16 m < 2^64, s = isqrt(m 2^68) = isqrt(M 2^64) =
 // floor(2^32 sqrt(M)). M is normalised to Mn = M 4^k in [2^62, 2^64); its root t = isqrt(Mn) in
-// [2^31, 2^32) comes from the 32-bit reciprocal square root and is corrected exactly; then
-// s = t 2^J + f with J = 32 - k and f = floor(2^J (sqrt(Mn) - t)) = floor(2^J rem /
-// (t + sqrt(Mn))), rem = Mn - t^2 <= 2 t. The divisor t + sqrt(Mn) lies in [2 t, 2 t + 1) and
-// 2^J rem / (2 t (2 t + 1)) < 1, so f is fh = floor(2^(J-1) rem / t) or fh - 1 (and below
-// 2^J). Writing 2^(J-1) rem = fh t + rho (0 <= rho < t), the exact test
-// f (2^(J+1) t + f) <= rem 4^J for f = fh reads fh^2 <= 2^(J+1) rho.
+// [2^31, 2^32) comes from the 32-bit reciprocal square root within 1 (as in unit_q30) and one
+// step each way; then s = t 2^J + f with J = 32 - k and f = floor(2^J (sqrt(Mn) - t)) =
+// floor(2^J rem / (t + sqrt(Mn))), rem = Mn - t^2 <= 2 t. The divisor t + sqrt(Mn) lies in
+// [2 t, 2 t + 1) and 2^J rem / (2 t (2 t + 1)) < 1, so f is fh = floor(2^(J-1) rem / t) or
+// fh - 1 (and below 2^J). fh comes from the 32-bit reciprocal of t, refined once on the exact
+// remainder (within [fh - 1, fh]) and fixed by one step. Writing 2^(J-1) rem = fh t + rho
+// (0 <= rho < t), the exact test f (2^(J+1) t + f) <= rem 4^J for f = fh reads
+// fh^2 <= 2^(J+1) rho.
 FBS_HD NormFactor norm_factor_pow2(uint64_t sum, uint32_t log2n, int64_t eps_int,
                                     const Seeds &sd = Seeds()) {
   NormFactor out;
@@ -406,34 +445,39 @@ FBS_HD NormFactor norm_factor_pow2(uint64_t sum, uint32_t log2n, int64_t eps_int
   const int z = clz64(M) & ~1;
   const uint64_t mn = M << z;
   const int J = 32 - (z >> 1);                        // [3, 32]
-  const uint64_t y = rsqrt_q46((uint32_t)(mn >> 32), sd.rsqrt);
-  uint64_t t = ((mn >> 32) * y) >> 30;
-  if (t > 0xffffffffull) t = 0xffffffffull;
+  const uint64_t mt = mn >> 32;
+  const uint64_t y = rsqrt_q46((uint32_t)mt, sd.rsqrt);
+  uint64_t t = (mt * y) >> 30;
+  t = t > 0xffffffffull ? 0xffffffffull : t;
   const int64_t diff = (int64_t)(mn - t * t);
   t = (uint64_t)((int64_t)t + (((diff >> 16) * (int64_t)y) >> 47));
-  if (t > 0xffffffffull) t = 0xffffffffull;
-  if (t < (1ull << 31)) t = 1ull << 31;
-  while (t * t > mn) t--;
-  while (t < 0xffffffffull && (t + 1) * (t + 1) <= mn) t++;
-  const uint64_t rem = mn - t * t;                    // [0, 2 t] <= 2^33 - 2
-  const uint64_t w = recip_q63((uint32_t)t, sd.recip); // ~ 2^63 / t
-  const uint64_t num = rem << (J - 1);                // < 2^64
-  uint64_t fh = ((rem >> 1) * w) >> (63 - J);
-  int64_t rho = (int64_t)(num - fh * t);              // small: exact modulo 2^64
-  while (rho < 0) {
-    fh--;
-    rho += (int64_t)t;
+  t = t > 0xffffffffull ? 0xffffffffull : t < (1ull << 31) ? (1ull << 31) : t;
+  uint64_t sq = t * t;
+  if (sq > mn) {
+    t -= 1;
+    sq -= 2 * t + 1;
   }
-  while (rho >= (int64_t)t) {
-    fh++;
-    rho -= (int64_t)t;
+  if (t < 0xffffffffull && sq + 2 * t + 1 <= mn) {
+    sq += 2 * t + 1;
+    t += 1;
+  }
+  const uint64_t rem = mn - sq;                       // [0, 2 t] <= 2^33 - 2
+  const uint64_t num = rem << (J - 1);                // < 2^64
+  const uint64_t w = recip_q63((uint32_t)t, sd.recip); // ~ 2^63 / t
+  uint64_t fh = ((num >> 32) * w) >> 31;              // [q - 9, q]
+  const uint64_t r0 = num - fh * t;                   // [0, 10 t)
+  fh += ((r0 >> 4) * w) >> 59;                        // [q - 1, q]
+  uint64_t rho = num - fh * t;                        // [0, 2 t)
+  if (rho >= t) {
+    fh += 1;
+    rho -= t;
   }
   uint64_t f = fh;
   if (fh >> J) {
     f = fh - 1;                                       // f < 2^J
   } else if (fh) {
-    const bool big = ((uint64_t)rho >> (63 - J)) != 0;  // 2^(J+1) rho >= 2^64 > fh^2
-    if (!big && fh * fh > ((uint64_t)rho << (J + 1))) f = fh - 1;
+    const bool big = (rho >> (63 - J)) != 0;          // 2^(J+1) rho >= 2^64 > fh^2
+    if (!big && fh * fh > (rho << (J + 1))) f = fh - 1;
   }
   const uint64_t s = (t << J) + f;                    // >= 2^34
   out.r = div_2p96(s, sd);
