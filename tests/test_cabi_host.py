@@ -304,3 +304,17 @@ def test_norm_factor_pow2_equals_the_general_form(hp):
                               dtype=np.int64), n)
     for log2n in (5, 8, 10):
         assert hp.fbs_hp_norm_factor_check(sums.ctypes.data_as(P), eps.ctypes.data_as(P), n, log2n) == 0
+
+
+def test_grid_descriptor_forms_equal_grid_apply(hp):
+    # Every valid grid code: the gains' grid_desc forms (32- and 64-bit inputs) and the window
+    # taps' tap_desc form (both halves of a word) against grid_apply, on extremes and random
+    # values of every width.
+    hp.fbs_hp_grid_check.argtypes = [P, C.c_uint64]
+    hp.fbs_hp_grid_check.restype = C.c_uint64
+    rng = np.random.default_rng(99)
+    v = np.concatenate([
+        rng.integers(-2**63, 2**63 - 1, 600, dtype=np.int64) >> rng.integers(0, 63, 600),
+        np.array([0, 1, -1, 2**31 - 1, -2**31, 2**31, -2**31 - 1, 2**57 - 1, -(2**57 - 1), 2**57,
+                  -2**57, 2**63 - 1, -2**63, 127, 128, -128, -129, 255, 256], dtype=np.int64)])
+    assert hp.fbs_hp_grid_check(v.ctypes.data_as(P), len(v)) == 0

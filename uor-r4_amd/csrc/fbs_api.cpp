@@ -288,7 +288,7 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
     {
       std::vector<uint16_t> td((size_t)(r.W + 1) * d), rg(d), mg(d);
       for (size_t i = 0; i < td.size(); i++) {
-        td[i] = grid_desc(taps[i]);
+        td[i] = tap_desc(taps[i]);
         if (td[i] == kGridDescSlow) M.taps_fast = 0;
       }
       for (uint32_t i = 0; i < d; i++) {

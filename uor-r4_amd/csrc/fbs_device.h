@@ -2,8 +2,8 @@
 // the kernels (fbs_run.h) and the host side that builds them (fbs_api.cpp).
 //
 // Layout in HBM (all tables uploaded once by uor_fbs_model_create, read by every sequence):
-//   per layer: gains (d i16), window taps ((W+1) x d i16, tap s = s positions back) and the
-//              grid_desc form of both (fbs_int.h),
+//   per layer: gains (d i16), window taps ((W+1) x d i16, tap s = s positions back) and their
+//              descriptor forms (grid_desc for gains, tap_desc for taps; fbs_int.h),
 //              conv_bias (d i32), gate_bias (d/4 + d i32), decay_offset (d/4 i32), and the
 //              layer's gather program: [slot][64 lanes] u16 LDS word indices that carry out the
 //              six FBS projections (stack_fbs_gather, session.rs:4037-4053) for this lane mapping;
@@ -40,7 +40,7 @@ struct DevLayer {
   const int32_t *gate_bias;     // d/4 + d
   const int32_t *decay_offset;  // d/4
   const uint16_t *prog;         // nslots * 64
-  const uint16_t *taps_desc;    // grid_desc of taps
+  const uint16_t *taps_desc;    // tap_desc of taps
   const uint16_t *rec_gain_desc;
   const uint16_t *mlp_gain_desc;
 };
@@ -51,7 +51,7 @@ struct DevModel {
   uint32_t nslots, s_rec_in, s_rec_gate, s_rec_out, s_mlp_gate, s_mlp_up, s_mlp_down;
   uint32_t xbar_words;      // 2 * max(d, m)
   uint32_t identity_rows;   // the nearest head: one drawer holding every token
-  uint32_t taps_fast;       // every window tap has a descriptor (grid_desc != kGridDescSlow)
+  uint32_t taps_fast;       // every window tap has a descriptor (tap_desc != kGridDescSlow)
   uint32_t log2d;           // log2(d) when d is a power of two, else 0xff
   int64_t eps_int[9];       // RMSNorm epsilon at each pre-shift 0..8
   const DevLayer *layers;   // L entries

@@ -82,17 +82,22 @@ int64_t fbs_hp_grid_apply(int64_t v, int16_t code) { return grid_apply(v, code);
 int64_t fbs_hp_grid32_desc(int32_t v, int16_t code) { return grid_apply32_desc(v, grid_desc(code), code); }
 int64_t fbs_hp_grid64_desc(int64_t v, int16_t code) { return grid_apply64_desc(v, grid_desc(code), code); }
 
-// Every valid grid code against n inputs v[]: mismatches of the descriptor forms.
+// Every valid grid code against n inputs v[]: mismatches of the descriptor forms (the gains'
+// grid_desc forms, and the taps' tap_desc form in both halves of a word).
 uint64_t fbs_hp_grid_check(const int64_t *v, uint64_t n) {
   uint64_t bad = 0;
   for (int32_t code = -2047; code <= 2047; code++) {
     uint32_t field = (uint32_t)(code < 0 ? -code : code) >> 4;
     if (code != 0 && (field < 1 || field > 127)) continue;
     uint16_t d = grid_desc((int16_t)code);
+    uint16_t t = tap_desc((int16_t)code);
+    const uint32_t word0 = 0xa5a50000u | t, word1 = ((uint32_t)t << 16) | 0x5a5au;
     for (uint64_t i = 0; i < n; i++) {
       bad += grid_apply64_desc(v[i], d, (int16_t)code) != grid_apply(v[i], (int16_t)code);
       int32_t v32 = (int32_t)v[i];
-      bad += grid_apply32_desc(v32, d, (int16_t)code) != grid_apply((int64_t)v32, (int16_t)code);
+      const int64_t want = grid_apply((int64_t)v32, (int16_t)code);
+      bad += grid_apply32_desc(v32, d, (int16_t)code) != want;
+      if (t != kGridDescSlow) bad += (tap_desc_apply(v32, word0, 0) != want) + (tap_desc_apply(v32, word1, 1) != want);
     }
   }
   return bad;

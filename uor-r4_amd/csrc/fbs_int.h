@@ -131,6 +131,28 @@ FBS_HD int64_t grid_desc_apply(int64_t v, uint16_t desc) {
   return (v * mul + (((int64_t)1 << (sh - 1)) - neg)) >> sh;
 }
 
+// The window taps' descriptor (16 bits, two per word): bits 0-5 the signed multiplier
+// +-(16 + m) (0 for the zero code), bits 6-11 the shift sh - 1. For a 32-bit v, with
+// p = v mul and neg = [code < 0] (the multiplier's sign bit),
+// grid_apply(v, code) = floor((p - neg + 2^(sh-1)) / 2^sh) = ((p - neg) >> (sh - 1)) + 1) >> 1.
+// Valid for the codes grid_desc serves (1 <= sh <= 62); |p| < 2^36.
+FBS_HD uint16_t tap_desc(int16_t code) {
+  if (code == 0) return 0;  // multiplier 0, shift 1: ((0 >> 0) + 1) >> 1 = 0
+  const uint32_t c = code < 0 ? (uint32_t)(-(int32_t)code) : (uint32_t)code;
+  const int32_t sh = 4 - ((int32_t)(c >> 4) - kGridExpBias);
+  if (sh < 1 || sh > 62) return kGridDescSlow;
+  const int32_t mul = code < 0 ? -(int32_t)(16 + (c & 15)) : (int32_t)(16 + (c & 15));
+  return (uint16_t)(((uint32_t)mul & 63u) | ((uint32_t)(sh - 1) << 6));
+}
+
+// grid_apply(v, code) for the tap descriptor in bits 16 h .. 16 h + 11 of `word`.
+FBS_HD int64_t tap_desc_apply(int32_t v, uint32_t word, int h) {
+  const int32_t mul = (int32_t)(word << (26 - 16 * h)) >> 26;  // sign-extended 6 bits
+  const uint32_t shm1 = (word >> (16 * h + 6)) & 63u;
+  const int64_t p = (int64_t)v * mul + (mul >> 31);            // v mul - neg
+  return ((p >> shm1) + 1) >> 1;
+}
+
 // grid_apply for a 32-bit input through its descriptor (every valid code has one or is slow).
 FBS_HD int64_t grid_apply32_desc(int32_t v, uint16_t desc, int16_t code) {
   if (desc == kGridDescSlow) return grid_apply((int64_t)v, code);

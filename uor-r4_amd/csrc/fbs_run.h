@@ -467,7 +467,8 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
     int32_t *ring_l = ring + (uint64_t)l * W * d;
     // The layer's loads first: gains, biases and the gather program.
     short4 g_rec[Q], g_mlp[Q], tap0[Q];
-    ushort4 gd_rec[Q], gd_mlp[Q], td0[Q];
+    ushort4 gd_rec[Q], gd_mlp[Q];
+    uint2 td0[Q];
     int4 cbias[Q], rbias[Q];
     int32_t dbias[Q], doff[Q];
     uint32_t pw_drive[Q][4], pw_gate[Q][4], pw_rot[Q][4], pw_dec[Q], pw_out[Q][4], pw_down[Q][4];
@@ -479,7 +480,7 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
       tap0[k] = *(const short4 *)(ly.taps + ch);
       gd_rec[k] = *(const ushort4 *)(ly.rec_gain_desc + ch);
       gd_mlp[k] = *(const ushort4 *)(ly.mlp_gain_desc + ch);
-      td0[k] = *(const ushort4 *)(ly.taps_desc + ch);
+      td0[k] = *(const uint2 *)(ly.taps_desc + ch);
       cbias[k] = *(const int4 *)(ly.conv_bias + ch);
       rbias[k] = *(const int4 *)(ly.gate_bias + nq + ch);
       dbias[k] = ly.gate_bias[qq];
@@ -532,7 +533,7 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
       // positions back (ring slot base - s), then the drive enters slot base. Rows and taps
       // load kWindowChunk at a time; the first chunk is in flight during the rotation.
       int4 hb[kWindowChunk];
-      ushort4 tb[kWindowChunk];
+      uint2 tb[kWindowChunk];  // tap_desc pairs: channels 0, 1 in .x, 2, 3 in .y
       auto load_chunk = [&](uint32_t s0) {
 #pragma unroll
         for (uint32_t i = 0; i < kWindowChunk; i++) {
@@ -540,7 +541,7 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
           if (s <= W) {
             const uint32_t sl = base >= s ? base - s : base + W - s;
             hb[i] = *(const int4 *)(ring_l + (uint64_t)sl * d + ch);
-            tb[i] = *(const ushort4 *)(ly.taps_desc + (uint64_t)s * d + ch);
+            tb[i] = *(const uint2 *)(ly.taps_desc + (uint64_t)s * d + ch);
           }
         }
       };
@@ -559,20 +560,20 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
       }
       int64_t wide[4];
       if (M.taps_fast) {
-        const ushort4 t0 = td0[k];
-        wide[0] = wadd64(cbias[k].x, grid_desc_apply(drive[k][0], t0.x));
-        wide[1] = wadd64(cbias[k].y, grid_desc_apply(drive[k][1], t0.y));
-        wide[2] = wadd64(cbias[k].z, grid_desc_apply(drive[k][2], t0.z));
-        wide[3] = wadd64(cbias[k].w, grid_desc_apply(drive[k][3], t0.w));
+        const uint2 t0 = td0[k];
+        wide[0] = wadd64(cbias[k].x, tap_desc_apply(drive[k][0], t0.x, 0));
+        wide[1] = wadd64(cbias[k].y, tap_desc_apply(drive[k][1], t0.x, 1));
+        wide[2] = wadd64(cbias[k].z, tap_desc_apply(drive[k][2], t0.y, 0));
+        wide[3] = wadd64(cbias[k].w, tap_desc_apply(drive[k][3], t0.y, 1));
         for (uint32_t s0 = 1; s0 <= W; s0 += kWindowChunk) {
           if (s0 > 1) load_chunk(s0);
 #pragma unroll
           for (uint32_t i = 0; i < kWindowChunk; i++)
             if (s0 + i <= W) {
-              wide[0] = wadd64(wide[0], grid_desc_apply(hb[i].x, tb[i].x));
-              wide[1] = wadd64(wide[1], grid_desc_apply(hb[i].y, tb[i].y));
-              wide[2] = wadd64(wide[2], grid_desc_apply(hb[i].z, tb[i].z));
-              wide[3] = wadd64(wide[3], grid_desc_apply(hb[i].w, tb[i].w));
+              wide[0] = wadd64(wide[0], tap_desc_apply(hb[i].x, tb[i].x, 0));
+              wide[1] = wadd64(wide[1], tap_desc_apply(hb[i].y, tb[i].x, 1));
+              wide[2] = wadd64(wide[2], tap_desc_apply(hb[i].z, tb[i].y, 0));
+              wide[3] = wadd64(wide[3], tap_desc_apply(hb[i].w, tb[i].y, 1));
             }
         }
       } else {
