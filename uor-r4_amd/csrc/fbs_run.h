@@ -334,10 +334,38 @@ __device__ __forceinline__ uint64_t scan_list(const DevModel &M, const uint32_t 
   return best;
 }
 
+// Drawers per lane held in registers by the writer (models of at most 64 kDrawerRegs drawers);
+// larger drawer counts score through LDS.
+constexpr uint32_t kDrawerRegs = 4;
+
+// A lane's drawers c = lane + 64 i (i < kDrawerRegs): their two 8-value keys and CSR ranges.
+struct DrawerRegs {
+  int4 key[kDrawerRegs][2];
+  uint32_t beg[kDrawerRegs], end[kDrawerRegs];
+};
+
+__device__ __forceinline__ bool drawers_in_regs(const DevModel &M) {
+  return M.head != 1 && M.D <= kWave * kDrawerRegs;
+}
+
+__device__ __forceinline__ void load_drawers(const DevModel &M, uint32_t lane, DrawerRegs &dr) {
+#pragma unroll
+  for (uint32_t i = 0; i < kDrawerRegs; i++) {
+    const uint32_t c = lane + kWave * i;
+    if (c < M.D) {
+      const int4 *key = (const int4 *)(M.keys + 16u * c);
+      dr.key[i][0] = key[0];
+      dr.key[i][1] = key[1];
+      dr.beg[i] = M.offsets[c];
+      dr.end[i] = M.offsets[c + 1];
+    }
+  }
+}
+
 // The native vector writer (RS stack/session.rs:4069-4121, TW 580-623) over keyed drawers,
 // or the whole-table nearest head (session.rs:4418-4445). `q` holds the query (d words) in
 // LDS. Returns the token (UINT32_MAX when no row was scored); writes the kept drawers in
-// selection order to kept_out (nullable).
+// selection order to kept[] and kept_out (nullable).
 template <int S>
 __device__ __forceinline__ uint32_t writer(const DevModel &M, const int32_t *q, uint32_t *dscore,
                                            uint32_t *kept, uint32_t *list, uint32_t lane,
@@ -372,36 +400,81 @@ __device__ __forceinline__ uint32_t writer(const DevModel &M, const int32_t *q, 
       qa[i] = q[i];
       qb[i] = q[d - 8 + i];
     }
-    for (uint32_t c = lane; c < M.D; c += kWave) {
-      const int4 *key = (const int4 *)(M.keys + 16u * c);
-      const int4 k4[2] = {key[0], key[1]};
-      const int16_t *kk = (const int16_t *)k4;
-      uint32_t sc = 0;
+    // Lane p < P ends with kept drawer p's CSR range.
+    uint32_t my_beg = 0, my_end = 0;
+    if (drawers_in_regs(M)) {
+      // Scores and ranges in registers: each round takes the wave's minimum, its owner lane
+      // retires it and hands over its range.
+      DrawerRegs dr;
+      load_drawers(M, lane, dr);
+      uint32_t sc[kDrawerRegs];
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
-        sc += uabs32(qa[i] - (int32_t)kk[i]);
-        sc += uabs32(qb[i] - (int32_t)kk[8 + i]);
+      for (uint32_t i = 0; i < kDrawerRegs; i++) {
+        const int16_t *kk = (const int16_t *)dr.key[i];
+        uint32_t s = 0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          s += uabs32(qa[j] - (int32_t)kk[j]);
+          s += uabs32(qb[j] - (int32_t)kk[8 + j]);
+        }
+        const uint32_t c = lane + kWave * i;
+        sc[i] = c < M.D ? (s << 12) | c : UINT32_MAX;
       }
-      dscore[c] = (sc << 12) | c;
-    }
-    wave_sync();
-    for (uint32_t p = 0; p < M.P; p++) {
-      uint32_t local = UINT32_MAX;
-      for (uint32_t c = lane; c < M.D; c += kWave) local = dscore[c] < local ? dscore[c] : local;
-      const uint32_t pick = wave_reduce32(local, OpMin()) & 0xfffu;
+      for (uint32_t p = 0; p < M.P; p++) {
+        uint32_t local = sc[0];
+#pragma unroll
+        for (uint32_t i = 1; i < kDrawerRegs; i++) local = sc[i] < local ? sc[i] : local;
+        const uint32_t pick = wave_reduce32(local, OpMin()) & 0xfffu;
+        const uint32_t slot = pick / kWave;
+        uint32_t b = dr.beg[0], e = dr.end[0];
+#pragma unroll
+        for (uint32_t i = 1; i < kDrawerRegs; i++)
+          if (slot == i) {
+            b = dr.beg[i];
+            e = dr.end[i];
+          }
+        b = lane32(b, (int)(pick & (kWave - 1)));
+        e = lane32(e, (int)(pick & (kWave - 1)));
+#pragma unroll
+        for (uint32_t i = 0; i < kDrawerRegs; i++) sc[i] = (sc[i] & 0xfffu) == pick ? UINT32_MAX : sc[i];
+        if (lane == p) {
+          my_beg = b;
+          my_end = e;
+        }
+        if (lane == 0) kept[p] = pick;
+      }
       wave_sync();
-      if ((pick & (kWave - 1)) == lane) dscore[pick] = UINT32_MAX;
-      if (lane == 0) kept[p] = pick;
+    } else {
+      for (uint32_t c = lane; c < M.D; c += kWave) {
+        const int4 *key = (const int4 *)(M.keys + 16u * c);
+        const int4 k4[2] = {key[0], key[1]};
+        const int16_t *kk = (const int16_t *)k4;
+        uint32_t sc = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          sc += uabs32(qa[i] - (int32_t)kk[i]);
+          sc += uabs32(qb[i] - (int32_t)kk[8 + i]);
+        }
+        dscore[c] = (sc << 12) | c;
+      }
       wave_sync();
+      for (uint32_t p = 0; p < M.P; p++) {
+        uint32_t local = UINT32_MAX;
+        for (uint32_t c = lane; c < M.D; c += kWave) local = dscore[c] < local ? dscore[c] : local;
+        const uint32_t pick = wave_reduce32(local, OpMin()) & 0xfffu;
+        wave_sync();
+        if ((pick & (kWave - 1)) == lane) dscore[pick] = UINT32_MAX;
+        if (lane == 0) kept[p] = pick;
+        wave_sync();
+      }
+      // Each drawer's CSR range, loaded by lane p for kept drawer p (all at once).
+      if (lane < M.P) {
+        const uint32_t c = kept[lane];
+        my_beg = M.offsets[c];
+        my_end = M.offsets[c + 1];
+      }
     }
     if (kept_out && lane < M.P) kept_out[lane] = kept[lane];
-    // Each drawer's CSR range, loaded by lane p for kept drawer p (all at once).
-    uint32_t my_beg = 0, my_end = 0;
-    if (lane < M.P) {
-      const uint32_t c = kept[lane];
-      my_beg = M.offsets[c];
-      my_end = M.offsets[c + 1];
-    }
     // Stage the kept drawers' member ids in LDS (at most kListCap per segment) and scan.
     uint32_t p = 0, done = 0;  // next drawer, members of it already staged
     while (p < M.P) {
