@@ -410,12 +410,16 @@ __device__ __forceinline__ uint32_t writer(const DevModel &M, const int32_t *q, 
       uint32_t sc[kDrawerRegs];
 #pragma unroll
       for (uint32_t i = 0; i < kDrawerRegs; i++) {
-        const int16_t *kk = (const int16_t *)dr.key[i];
+        // The keys' i16 values, two per word, low half first.
+        const int32_t ka[4] = {dr.key[i][0].x, dr.key[i][0].y, dr.key[i][0].z, dr.key[i][0].w};
+        const int32_t kb[4] = {dr.key[i][1].x, dr.key[i][1].y, dr.key[i][1].z, dr.key[i][1].w};
         uint32_t s = 0;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-          s += uabs32(qa[j] - (int32_t)kk[j]);
-          s += uabs32(qb[j] - (int32_t)kk[8 + j]);
+          const int32_t a = (j & 1) ? ka[j >> 1] >> 16 : (int32_t)(int16_t)ka[j >> 1];
+          const int32_t b = (j & 1) ? kb[j >> 1] >> 16 : (int32_t)(int16_t)kb[j >> 1];
+          s += uabs32(qa[j] - a);
+          s += uabs32(qb[j] - b);
         }
         const uint32_t c = lane + kWave * i;
         sc[i] = c < M.D ? (s << 12) | c : UINT32_MAX;
