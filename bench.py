@@ -79,16 +79,17 @@ def workload_key(a) -> str:
     return f"{a.config} batch {a.batch} prompt {a.prompt} gen {a.gen} seed {a.seed}"
 
 
-def measured_traffic(a):
+def measured_traffic(a, kernel):
     """HBM bytes per decode launch from the committed counter summary, if it covers this exact
-    workload; None otherwise."""
+    workload and kernel; None otherwise."""
     try:
         text = open(TRAFFIC_SUMMARY).read()
     except OSError:
         return None
     w = re.search(r"^workload: (.+)$", text, re.M)
+    k = re.search(r"^kernel: (.+)$", text, re.M)
     t = re.search(r"^traffic_bytes_per_launch: (\d+)$", text, re.M)
-    if not w or not t or w.group(1).strip() != workload_key(a):
+    if not w or not k or not t or w.group(1).strip() != workload_key(a) or k.group(1).strip() != kernel:
         return None
     return int(t.group(1))
 
@@ -204,11 +205,12 @@ def main():
     reused[:, 1:] = (q[:, 1:] == q[:, :-1]).all(-1)
     scanned_cand = float(np.where(reused, 0, cand).mean())
     bpt_scanned = algorithmic_bytes_per_token(spec, scanned_cand)
-    traffic = measured_traffic(a)
     S = 1
     while S < spec.width // 32:
         S *= 2
-    kernel = f"fbs_decode<{(spec.width // 4 + 63) // 64}, {S}>"
+    family = "fbs_decode_pair" if model.block_waves(B) == 2 else "fbs_decode"
+    kernel = f"{family}<{(spec.width // 4 + 63) // 64}, {S}>"
+    traffic = measured_traffic(a, kernel)
 
     out = {
         "metric": "decoded tokens/sec at batch 1024, width 256 (1 GPU)",

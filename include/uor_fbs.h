@@ -125,6 +125,12 @@ void uor_fbs_model_destroy(uor_fbs_handle *handle);
 uint64_t uor_fbs_state_words(const uor_fbs_handle *handle);
 uint64_t uor_fbs_history_words(const uor_fbs_handle *handle);
 
+/* Wavefronts per sequence of the kernels a run of n sequences launches: 2 (paired blocks) when
+ * the run leaves SIMDs without a second wave (n at most the device's SIMD count), else 1;
+ * UOR_FBS_BLOCK_WAVES=1 or 2 in the environment at model creation fixes it. No counterpart in
+ * the reference (its CPU decoder has no launch shape): for profilers and tests. */
+uint32_t uor_fbs_block_waves(const uor_fbs_handle *handle, uint32_t n);
+
 /* Teacher-forced sequences from fresh sessions: every position's chosen token, kept drawers
  * (best first) and Q12 query. Same contract as fbs_host_sequences (host_kernel.cpp:16-29)
  * and fbs_eval_sequences (evaluator.cu:8-19): outputs S*len, S*len*probes, S*len*width.

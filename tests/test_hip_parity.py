@@ -21,7 +21,7 @@ from conftest import GOLDEN
 from uor_fbs import synth
 from uor_fbs.hip import FbsError, Model
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("block_waves")]
 
 MANIFEST = json.load(open(os.path.join(GOLDEN, "manifest.json")))
 
@@ -87,6 +87,14 @@ def test_extended_shapes_match_oracle(name):
     np.testing.assert_array_equal(kept, want_k)
     np.testing.assert_array_equal(tok, want_t)
     assert len(np.unique(tok)) > 4  # the case is not degenerate
+
+
+def test_block_waves_follow_the_setting(block_waves, monkeypatch):
+    art = synth.make_artifact(synth.SMALL, 1)
+    assert Model(art).block_waves(64) == (2 if block_waves == "paired" else 1)
+    monkeypatch.delenv("UOR_FBS_BLOCK_WAVES")
+    model = Model(art)  # the library's choice: paired blocks up to one sequence per SIMD
+    assert model.block_waves(1024) == 2 and model.block_waves(1 << 20) == 1
 
 
 def test_decode_matches_oracle_and_resumes():

@@ -14,7 +14,7 @@ from conftest import GOLDEN
 from uor_fbs import synth, uorlut
 from uor_fbs.hip import Model
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("block_waves")]
 
 TRAINED = os.path.join(GOLDEN, "trained")
 MANIFEST = json.load(open(os.path.join(TRAINED, "manifest.json")))

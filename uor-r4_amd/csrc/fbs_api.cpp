@@ -11,6 +11,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -20,13 +21,13 @@
 #include "fbs_int.h"
 
 namespace fbs {
-// The kernels: fbs_prefill.hip, fbs_decode.hip, fbs_rows.hip.
-hipError_t launch_fbs_prefill(const DevModel &M, const RunArgs &A, uint32_t grid, size_t lds,
-                              hipStream_t stream);
-hipError_t launch_fbs_decode(const DevModel &M, const RunArgs &A, uint32_t grid, size_t lds,
-                             hipStream_t stream);
-hipError_t launch_fbs_rows(const DevModel &M, const RunArgs &A, uint32_t grid, size_t lds,
-                           hipStream_t stream);
+// The kernels: fbs_prefill.hip, fbs_decode.hip, fbs_rows.hip (`waves` wavefronts per sequence).
+hipError_t launch_fbs_prefill(const DevModel &M, const RunArgs &A, uint32_t grid, uint32_t waves,
+                              size_t lds, hipStream_t stream);
+hipError_t launch_fbs_decode(const DevModel &M, const RunArgs &A, uint32_t grid, uint32_t waves,
+                             size_t lds, hipStream_t stream);
+hipError_t launch_fbs_rows(const DevModel &M, const RunArgs &A, uint32_t grid, uint32_t waves,
+                           size_t lds, hipStream_t stream);
 }
 
 using namespace fbs;
@@ -62,7 +63,12 @@ struct uor_fbs_handle {
   std::vector<void *> allocs;
   size_t lds_bytes = 0;
   uint32_t max_grid = 0;
+  // Paired blocks (two wavefronts per sequence) run launches of at most pair_max sequences:
+  // one wave per SIMD would leave half of each SIMD's issue slots unused.
+  size_t pair_lds = 0;
+  uint32_t pair_max = 0;
   int32_t *ring = nullptr;
+  int64_t *hist = nullptr;
   size_t ring_blocks = 0;
 
   ~uor_fbs_handle() {
@@ -71,6 +77,7 @@ struct uor_fbs_handle {
     (void)hipSetDevice(device);
     for (void *p : allocs) (void)hipFree(p);
     if (ring) (void)hipFree(ring);
+    if (hist) (void)hipFree(hist);
     (void)hipSetDevice(prev);
   }
 
@@ -89,15 +96,20 @@ struct uor_fbs_handle {
     return 0;
   }
 
-  // The window ring for `blocks` resident sequences (grown, never shrunk).
+  // The window ring and the paired blocks' window sums for `blocks` resident sequences (grown,
+  // never shrunk).
   int ensure_ring(size_t blocks) {
     if (blocks <= ring_blocks) return 0;
     if (ring) (void)hipFree(ring);
+    if (hist) (void)hipFree(hist);
     ring = nullptr;
+    hist = nullptr;
     ring_blocks = 0;
     size_t bytes = blocks * (size_t)M.L * M.W * M.d * sizeof(int32_t);
     hipError_t e = hipMalloc((void **)&ring, bytes);
     if (e != hipSuccess) return hip_fail(e, "hipMalloc(window ring)");
+    e = hipMalloc((void **)&hist, blocks * (size_t)M.L * M.d * sizeof(int64_t));
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(window sums)");
     ring_blocks = blocks;
     return 0;
   }
@@ -399,6 +411,14 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
     return done(fail(UOR_FBS_ERR_UNSUPPORTED, "%zu bytes of LDS per sequence exceed %zu",
                      h->lds_bytes, (size_t)prop.sharedMemPerBlock));
   h->max_grid = (uint32_t)prop.multiProcessorCount * 8;
+  // UOR_FBS_BLOCK_WAVES=1 or 2 fixes the wavefronts per sequence (default: paired blocks for
+  // launches of at most one sequence per SIMD, four SIMDs per CU).
+  const char *bw = getenv("UOR_FBS_BLOCK_WAVES");
+  const int waves = bw && bw[0] == '1' && !bw[1] ? 1 : bw && bw[0] == '2' && !bw[1] ? 2 : 0;
+  h->pair_lds = fbs::pair_lds_bytes(M);
+  h->pair_max = waves == 1 || h->pair_lds > prop.sharedMemPerBlock ? 0
+                : waves == 2                                     ? UINT32_MAX
+                                                                 : (uint32_t)prop.multiProcessorCount * 4;
   return done(0);
 }
 
@@ -410,6 +430,9 @@ extern "C" uint64_t uor_fbs_state_words(const uor_fbs_handle *h) {
 extern "C" uint64_t uor_fbs_history_words(const uor_fbs_handle *h) {
   return h ? (uint64_t)h->M.L * h->M.W * h->M.d : 0;
 }
+extern "C" uint32_t uor_fbs_block_waves(const uor_fbs_handle *h, uint32_t n) {
+  return h && n <= h->pair_max ? 2u : 1u;
+}
 
 namespace {
 
@@ -419,10 +442,13 @@ int launch(uor_fbs_handle *h, RunArgs &A, hipStream_t stream) {
   int st = h->ensure_ring(grid);
   if (st) return st;
   A.ring = h->ring;
-  const bool decode = A.mode == kModeDecode;
-  hipError_t e = decode && A.gen == 0 ? launch_fbs_prefill(h->M, A, grid, h->lds_bytes, stream)
-                 : decode             ? launch_fbs_decode(h->M, A, grid, h->lds_bytes, stream)
-                                      : launch_fbs_rows(h->M, A, grid, h->lds_bytes, stream);
+  A.hist = h->hist;
+  const bool decode = A.mode == kModeDecode, pair = A.n <= h->pair_max;
+  const uint32_t waves = pair ? 2 : 1;
+  const size_t lds = pair ? h->pair_lds : h->lds_bytes;
+  hipError_t e = decode && A.gen == 0 ? launch_fbs_prefill(h->M, A, grid, waves, lds, stream)
+                 : decode             ? launch_fbs_decode(h->M, A, grid, waves, lds, stream)
+                                      : launch_fbs_rows(h->M, A, grid, waves, lds, stream);
   if (e != hipSuccess) return hip_fail(e, "kernel launch");
   return 0;
 }

@@ -74,6 +74,12 @@ inline size_t lds_bytes(const DevModel &M) {
          8ull * M.L * M.d;
 }
 
+// Paired blocks (two wavefronts per sequence) add the window sums and gate quaternions handed
+// from wave 1 to wave 0 (2 d i64), the kept drawers' ranges and four per-wave results.
+inline size_t pair_lds_bytes(const DevModel &M) {
+  return lds_bytes(M) + 4ull * (4 * M.d + 2 * kMaxProbes + 8);
+}
+
 enum RunMode : uint32_t { kModeSequences = 0, kModeDecode = 1, kModeScore = 2 };
 
 struct RunArgs {
@@ -94,6 +100,7 @@ struct RunArgs {
   unsigned long long *matches;
   int32_t *status;        // n
   int32_t *ring;          // gridDim.x * L * W * d
+  int64_t *hist;          // paired blocks: gridDim.x * L * d, the next step's window sums
 };
 
 }  // namespace fbs

@@ -240,6 +240,51 @@ __device__ __forceinline__ void gate_apply(const DevModel &M, const Seeds &sd,
   }
 }
 
+// One MLP quaternion of the Hamilton feed-forward gate (session.rs:4005-4025): the gate of gq
+// applied to up. Raw gates use q = 2 u, and u (x) up fits in 64 bits.
+__device__ __forceinline__ void mlp_gate(const DevModel &M, const Seeds &sd, const int32_t (&gq)[4],
+                                         const int32_t (&up)[4], int64_t (&mo)[4]) {
+  if (M.raw_gates) {
+    int32_t u[4];
+    int64_t prod[4];
+    unit_q30(gq, kGateEps, u, sd);
+    hamilton32x32(u, up, prod);
+#pragma unroll
+    for (int c = 0; c < 4; c++) mo[c] = shift_i64(prod[c], 14);
+  } else {
+    const int64_t up64[4] = {up[0], up[1], up[2], up[3]};
+    gate_apply(M, sd, gq, up64, mo);
+  }
+}
+
+// gate_apply split in two for paired blocks: gate_quat forms the gate's quaternion (the unit
+// quaternion u of a raw gate, or the snapped gate at lambda 2^31), gate_mul applies it.
+__device__ __forceinline__ void gate_quat(const DevModel &M, const Seeds &sd, const int32_t (&raw)[4],
+                                          int64_t (&g)[4]) {
+  if (M.raw_gates) {
+    int32_t u[4];
+    unit_q30(raw, kGateEps, u, sd);
+#pragma unroll
+    for (int c = 0; c < 4; c++) g[c] = u[c];
+  } else {
+    snap_rotation_dev(M.icosian, make_int4(raw[0], raw[1], raw[2], raw[3]), 1ull << 31, g);
+  }
+}
+__device__ __forceinline__ void gate_mul(const DevModel &M, const int64_t (&g)[4],
+                                         const int64_t (&rhs)[4], int64_t (&out)[4]) {
+  i128 prod[4];
+  if (M.raw_gates) {
+    const int32_t u[4] = {(int32_t)g[0], (int32_t)g[1], (int32_t)g[2], (int32_t)g[3]};
+    hamilton32(u, rhs, prod);
+#pragma unroll
+    for (int c = 0; c < 4; c++) out[c] = shift_wide(prod[c], 14);
+  } else {
+    hamilton64(g, rhs, prod);
+#pragma unroll
+    for (int c = 0; c < 4; c++) out[c] = shift_wide(prod[c], 15);
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 // The writer.
 
@@ -362,6 +407,160 @@ __device__ __forceinline__ void load_drawers(const DevModel &M, uint32_t lane, D
   }
 }
 
+// The scan geometry of this lane (S lanes per row, lane groups of S) and its 32-channel segment
+// of the query as biased pairs: (q[2i] + 2^15) | (q[2i+1] + 2^15) << 16.
+template <int S>
+__device__ __forceinline__ void scan_setup(const DevModel &M, const int32_t *q, uint32_t lane,
+                                           ScanGeom &g, uint32_t (&qpk)[16]) {
+  const uint32_t d = M.d, segs = d >> 5;  // S is the power of two >= segs
+  g.grp = lane / S;
+  g.stride = d;
+  const uint32_t sub = lane % S;
+  // Lanes past the row's last 32-channel segment (widths that are not a power-of-two multiple
+  // of 32) read the last segment again and add zero.
+  g.sub = sub < segs ? sub : segs - 1;
+  g.mask = sub < segs ? 0xffffffffu : 0u;
+#pragma unroll
+  for (int i = 0; i < 16; i++)
+    qpk[i] = (uint32_t)(q[32 * g.sub + 2 * i] + 32768) |
+             ((uint32_t)(q[32 * g.sub + 2 * i + 1] + 32768) << 16);
+}
+
+// The whole-table nearest head over tokens [lo, hi) (session.rs:4418-4445).
+template <int S>
+__device__ __forceinline__ uint64_t scan_nearest(const DevModel &M, const uint32_t (&qpk)[16],
+                                                 uint32_t lo, uint32_t hi, const ScanGeom &g,
+                                                 uint64_t best) {
+  for (uint32_t b = lo; b < hi; b += kListCap) {
+    const uint32_t fill = hi - b < kListCap ? hi - b : kListCap;
+    best = scan_list<S>(M, qpk, nullptr, fill, b, g, best);
+  }
+  return best;
+}
+
+// Drawer selection of the keyed writer (session.rs:4069-4100): scores are the L1 of the query's
+// first and last 8-blocks to each drawer's two keys, packed with the drawer index so that the
+// minimum is the reference's first maximum; P rounds take the lowest. Writes the kept drawers in
+// selection order to kept[]; lane p < P ends with kept drawer p's CSR range.
+__device__ __forceinline__ void writer_select(const DevModel &M, const int32_t *q, uint32_t *dscore,
+                                              uint32_t *kept, uint32_t lane, uint32_t &my_beg,
+                                              uint32_t &my_end) {
+  const uint32_t d = M.d;
+  int32_t qa[8], qb[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    qa[i] = q[i];
+    qb[i] = q[d - 8 + i];
+  }
+  my_beg = 0;
+  my_end = 0;
+  if (drawers_in_regs(M)) {
+    // Scores and ranges in registers: each round takes the wave's minimum, its owner lane
+    // retires it and hands over its range.
+    DrawerRegs dr;
+    load_drawers(M, lane, dr);
+    uint32_t sc[kDrawerRegs];
+#pragma unroll
+    for (uint32_t i = 0; i < kDrawerRegs; i++) {
+      // The keys' i16 values, two per word, low half first.
+      const int32_t ka[4] = {dr.key[i][0].x, dr.key[i][0].y, dr.key[i][0].z, dr.key[i][0].w};
+      const int32_t kb[4] = {dr.key[i][1].x, dr.key[i][1].y, dr.key[i][1].z, dr.key[i][1].w};
+      uint32_t s = 0;
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int32_t a = (j & 1) ? ka[j >> 1] >> 16 : (int32_t)(int16_t)ka[j >> 1];
+        const int32_t b = (j & 1) ? kb[j >> 1] >> 16 : (int32_t)(int16_t)kb[j >> 1];
+        s += uabs32(qa[j] - a);
+        s += uabs32(qb[j] - b);
+      }
+      const uint32_t c = lane + kWave * i;
+      sc[i] = c < M.D ? (s << 12) | c : UINT32_MAX;
+    }
+    for (uint32_t p = 0; p < M.P; p++) {
+      uint32_t local = sc[0];
+#pragma unroll
+      for (uint32_t i = 1; i < kDrawerRegs; i++) local = sc[i] < local ? sc[i] : local;
+      const uint32_t pick = wave_reduce32(local, OpMin()) & 0xfffu;
+      const uint32_t slot = pick / kWave;
+      uint32_t b = dr.beg[0], e = dr.end[0];
+#pragma unroll
+      for (uint32_t i = 1; i < kDrawerRegs; i++)
+        if (slot == i) {
+          b = dr.beg[i];
+          e = dr.end[i];
+        }
+      b = lane32(b, (int)(pick & (kWave - 1)));
+      e = lane32(e, (int)(pick & (kWave - 1)));
+#pragma unroll
+      for (uint32_t i = 0; i < kDrawerRegs; i++) sc[i] = (sc[i] & 0xfffu) == pick ? UINT32_MAX : sc[i];
+      if (lane == p) {
+        my_beg = b;
+        my_end = e;
+      }
+      if (lane == 0) kept[p] = pick;
+    }
+    wave_sync();
+  } else {
+    for (uint32_t c = lane; c < M.D; c += kWave) {
+      const int4 *key = (const int4 *)(M.keys + 16u * c);
+      const int4 k4[2] = {key[0], key[1]};
+      const int16_t *kk = (const int16_t *)k4;
+      uint32_t sc = 0;
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        sc += uabs32(qa[i] - (int32_t)kk[i]);
+        sc += uabs32(qb[i] - (int32_t)kk[8 + i]);
+      }
+      dscore[c] = (sc << 12) | c;
+    }
+    wave_sync();
+    for (uint32_t p = 0; p < M.P; p++) {
+      uint32_t local = UINT32_MAX;
+      for (uint32_t c = lane; c < M.D; c += kWave) local = dscore[c] < local ? dscore[c] : local;
+      const uint32_t pick = wave_reduce32(local, OpMin()) & 0xfffu;
+      wave_sync();
+      if ((pick & (kWave - 1)) == lane) dscore[pick] = UINT32_MAX;
+      if (lane == 0) kept[p] = pick;
+      wave_sync();
+    }
+    // Each drawer's CSR range, loaded by lane p for kept drawer p (all at once).
+    if (lane < M.P) {
+      const uint32_t c = kept[lane];
+      my_beg = M.offsets[c];
+      my_end = M.offsets[c + 1];
+    }
+  }
+}
+
+// The lowest (L1, token) over the members of the ranges lanes 0..P-1 hold (session.rs:4100-4121):
+// member ids are staged in `list` (at most `cap` per segment) and scanned.
+template <int S>
+__device__ __forceinline__ uint64_t scan_members(const DevModel &M, const uint32_t (&qpk)[16],
+                                                 uint32_t *list, uint32_t cap, const ScanGeom &g,
+                                                 uint32_t lane, uint32_t my_beg, uint32_t my_end,
+                                                 uint64_t best) {
+  uint32_t p = 0, done = 0;  // next drawer, members of it already staged
+  while (p < M.P) {
+    uint32_t fill = 0;
+    while (p < M.P && fill < cap) {
+      const uint32_t beg = lane32(my_beg, (int)p) + done, end = lane32(my_end, (int)p);
+      const uint32_t take = end - beg < cap - fill ? end - beg : cap - fill;
+      for (uint32_t o = 0; o < take; o += kWave)
+        lds_dma_words(M.members + beg + o, list + fill + o, take - o, lane);
+      fill += take;
+      done += take;
+      if (beg + take == end) {
+        p++;
+        done = 0;
+      }
+    }
+    wait_lds_dma();
+    if (fill) best = scan_list<S>(M, qpk, list, fill, 0, g, best);
+    wave_sync();
+  }
+  return best;
+}
+
 // The native vector writer (RS stack/session.rs:4069-4121, TW 580-623) over keyed drawers,
 // or the whole-table nearest head (session.rs:4418-4445). `q` holds the query (d words) in
 // LDS. Returns the token (UINT32_MAX when no row was scored); writes the kept drawers in
@@ -370,135 +569,18 @@ template <int S>
 __device__ __forceinline__ uint32_t writer(const DevModel &M, const int32_t *q, uint32_t *dscore,
                                            uint32_t *kept, uint32_t *list, uint32_t lane,
                                            uint32_t *kept_out) {
-  const uint32_t d = M.d, segs = d >> 5;  // S is the power of two >= segs
   ScanGeom g;
-  g.grp = lane / S;
-  g.stride = d;
-  const uint32_t sub = lane % S;
-  // Lanes past the row's last 32-channel segment (widths that are not a power-of-two multiple
-  // of 32) read the last segment again and add zero.
-  g.sub = sub < segs ? sub : segs - 1;
-  g.mask = sub < segs ? 0xffffffffu : 0u;
-  uint32_t qpk[16];  // biased query pairs: (q[2i] + 2^15) | (q[2i+1] + 2^15) << 16
-#pragma unroll
-  for (int i = 0; i < 16; i++)
-    qpk[i] = (uint32_t)(q[32 * g.sub + 2 * i] + 32768) |
-             ((uint32_t)(q[32 * g.sub + 2 * i + 1] + 32768) << 16);
+  uint32_t qpk[16];
+  scan_setup<S>(M, q, lane, g, qpk);
   uint64_t best = UINT64_MAX;
   if (M.head == 1) {
-    for (uint32_t b = 0; b < M.vocab; b += kListCap) {
-      uint32_t fill = M.vocab - b < kListCap ? M.vocab - b : kListCap;
-      best = scan_list<S>(M, qpk, nullptr, fill, b, g, best);
-    }
+    best = scan_nearest<S>(M, qpk, 0, M.vocab, g, best);
     if (kept_out && lane < M.P) kept_out[lane] = 0;
   } else {
-    // Drawer scores: L1 of the query's first and last 8-blocks to the drawer's two keys,
-    // packed with the drawer index so that the minimum is the reference's first maximum.
-    int32_t qa[8], qb[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      qa[i] = q[i];
-      qb[i] = q[d - 8 + i];
-    }
-    // Lane p < P ends with kept drawer p's CSR range.
-    uint32_t my_beg = 0, my_end = 0;
-    if (drawers_in_regs(M)) {
-      // Scores and ranges in registers: each round takes the wave's minimum, its owner lane
-      // retires it and hands over its range.
-      DrawerRegs dr;
-      load_drawers(M, lane, dr);
-      uint32_t sc[kDrawerRegs];
-#pragma unroll
-      for (uint32_t i = 0; i < kDrawerRegs; i++) {
-        // The keys' i16 values, two per word, low half first.
-        const int32_t ka[4] = {dr.key[i][0].x, dr.key[i][0].y, dr.key[i][0].z, dr.key[i][0].w};
-        const int32_t kb[4] = {dr.key[i][1].x, dr.key[i][1].y, dr.key[i][1].z, dr.key[i][1].w};
-        uint32_t s = 0;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-          const int32_t a = (j & 1) ? ka[j >> 1] >> 16 : (int32_t)(int16_t)ka[j >> 1];
-          const int32_t b = (j & 1) ? kb[j >> 1] >> 16 : (int32_t)(int16_t)kb[j >> 1];
-          s += uabs32(qa[j] - a);
-          s += uabs32(qb[j] - b);
-        }
-        const uint32_t c = lane + kWave * i;
-        sc[i] = c < M.D ? (s << 12) | c : UINT32_MAX;
-      }
-      for (uint32_t p = 0; p < M.P; p++) {
-        uint32_t local = sc[0];
-#pragma unroll
-        for (uint32_t i = 1; i < kDrawerRegs; i++) local = sc[i] < local ? sc[i] : local;
-        const uint32_t pick = wave_reduce32(local, OpMin()) & 0xfffu;
-        const uint32_t slot = pick / kWave;
-        uint32_t b = dr.beg[0], e = dr.end[0];
-#pragma unroll
-        for (uint32_t i = 1; i < kDrawerRegs; i++)
-          if (slot == i) {
-            b = dr.beg[i];
-            e = dr.end[i];
-          }
-        b = lane32(b, (int)(pick & (kWave - 1)));
-        e = lane32(e, (int)(pick & (kWave - 1)));
-#pragma unroll
-        for (uint32_t i = 0; i < kDrawerRegs; i++) sc[i] = (sc[i] & 0xfffu) == pick ? UINT32_MAX : sc[i];
-        if (lane == p) {
-          my_beg = b;
-          my_end = e;
-        }
-        if (lane == 0) kept[p] = pick;
-      }
-      wave_sync();
-    } else {
-      for (uint32_t c = lane; c < M.D; c += kWave) {
-        const int4 *key = (const int4 *)(M.keys + 16u * c);
-        const int4 k4[2] = {key[0], key[1]};
-        const int16_t *kk = (const int16_t *)k4;
-        uint32_t sc = 0;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-          sc += uabs32(qa[i] - (int32_t)kk[i]);
-          sc += uabs32(qb[i] - (int32_t)kk[8 + i]);
-        }
-        dscore[c] = (sc << 12) | c;
-      }
-      wave_sync();
-      for (uint32_t p = 0; p < M.P; p++) {
-        uint32_t local = UINT32_MAX;
-        for (uint32_t c = lane; c < M.D; c += kWave) local = dscore[c] < local ? dscore[c] : local;
-        const uint32_t pick = wave_reduce32(local, OpMin()) & 0xfffu;
-        wave_sync();
-        if ((pick & (kWave - 1)) == lane) dscore[pick] = UINT32_MAX;
-        if (lane == 0) kept[p] = pick;
-        wave_sync();
-      }
-      // Each drawer's CSR range, loaded by lane p for kept drawer p (all at once).
-      if (lane < M.P) {
-        const uint32_t c = kept[lane];
-        my_beg = M.offsets[c];
-        my_end = M.offsets[c + 1];
-      }
-    }
+    uint32_t my_beg, my_end;
+    writer_select(M, q, dscore, kept, lane, my_beg, my_end);
     if (kept_out && lane < M.P) kept_out[lane] = kept[lane];
-    // Stage the kept drawers' member ids in LDS (at most kListCap per segment) and scan.
-    uint32_t p = 0, done = 0;  // next drawer, members of it already staged
-    while (p < M.P) {
-      uint32_t fill = 0;
-      while (p < M.P && fill < kListCap) {
-        const uint32_t beg = lane32(my_beg, (int)p) + done, end = lane32(my_end, (int)p);
-        const uint32_t take = end - beg < kListCap - fill ? end - beg : kListCap - fill;
-        for (uint32_t o = 0; o < take; o += kWave)
-          lds_dma_words(M.members + beg + o, list + fill + o, take - o, lane);
-        fill += take;
-        done += take;
-        if (beg + take == end) {
-          p++;
-          done = 0;
-        }
-      }
-      wait_lds_dma();
-      if (fill) best = scan_list<S>(M, qpk, list, fill, 0, g, best);
-      wave_sync();
-    }
+    best = scan_members<S>(M, qpk, list, kListCap, g, lane, my_beg, my_end, best);
   }
   best = wave_reduce64(best, OpMin());
   return (uint32_t)best;
@@ -517,8 +599,14 @@ struct Lds {
   uint32_t *list;    // kListCap
   int64_t *st;       // L * d recurrence state
   int32_t *wq;       // d: the query of the writer's last run
-  uint32_t *wmeta;   // 4: [0] that run's token, [1] nonzero once wq holds a query
+  uint32_t *wmeta;   // 4: [0] that run's token, [1] nonzero once wq holds a query,
+                     //    [2] paired blocks: the step reuses that run's result
   Seeds seeds;       // the reciprocal and reciprocal square root seed tables
+  // Paired blocks only (null otherwise):
+  int64_t *wide;     // d: the window sums, wave 1 -> wave 0
+  int64_t *gq;       // d: the output gates' quaternions, wave 1 -> wave 0
+  uint32_t *rng;     // 2 kMaxProbes: the kept drawers' CSR ranges (begins, then ends)
+  uint64_t *pair;    // 4: each wave's MLP maximum magnitude, then each wave's best candidate
 };
 
 template <int Q, int SW>
@@ -748,18 +836,7 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
       }
       if (mq < M.nm) {
         int64_t mo[4];
-        if (M.raw_gates) {
-          // q = 2 u with u the unit quaternion; u (x) up fits in 64 bits.
-          int32_t u[4];
-          int64_t prod[4];
-          unit_q30(gq, kGateEps, u, S.seeds);
-          hamilton32x32(u, up, prod);
-#pragma unroll
-          for (int c = 0; c < 4; c++) mo[c] = shift_i64(prod[c], 14);
-        } else {
-          const int64_t up64[4] = {up[0], up[1], up[2], up[3]};
-          gate_apply(M, S.seeds, gq, up64, mo);
-        }
+        mlp_gate(M, S.seeds, gq, up, mo);
 #pragma unroll
         for (int c = 0; c < 4; c++) {
           S.mlp_out[4 * mq + c] = mo[c];
@@ -839,12 +916,509 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
   return 0;
 }
 
+// ---------------------------------------------------------------------------------------------
+// Paired blocks: one sequence on the two wavefronts of a 128-lane block, for batches that would
+// leave SIMDs without a second wave. Wave 0 holds the residual stream and the recurrence state:
+// the norms, the transition, transport and output gate product, both requantizes and the
+// writer's drawer selection. Wave 1 owns the window ring: it sums the window over the earlier
+// positions while wave 0 normalises, adds tap 0, writes the drive into the ring, and forms the
+// output gate's quaternion while wave 0 forms the transition. The MLP's quaternion groups
+// alternate between the waves, and each wave scans half of the writer's candidates. The two
+// waves meet at block barriers, numbered alike in step_main and step_window: every path through
+// a step reaches the same barriers in the same order on both waves (the branches between them
+// depend only on values both waves hold: the model, the step's token and want_writer, and the
+// reuse flag read after barrier 5).
+
+// Both waves of the block meet; LDS writes before it are visible to the other wave after it.
+// Global loads in flight stay in flight (LDS-only fences).
+__device__ __forceinline__ void pair_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Clips the ranges that lanes 0..P-1 hold to the positions [lo, hi) of their concatenation.
+__device__ __forceinline__ void clip_ranges(uint32_t P, uint32_t lane, uint32_t lo, uint32_t hi,
+                                            uint32_t &my_beg, uint32_t &my_end) {
+  uint32_t nb = my_beg, ne = my_end, cum = 0;
+  for (uint32_t p = 0; p < P; p++) {
+    const uint32_t b = lane32(my_beg, (int)p), len = lane32(my_end, (int)p) - b;
+    const uint32_t from = lo > cum ? (lo - cum < len ? lo - cum : len) : 0;
+    const uint32_t to = hi > cum ? (hi - cum < len ? hi - cum : len) : 0;
+    if (lane == p) {
+      nb = b + from;
+      ne = b + (to > from ? to : from);
+    }
+    cum += len;
+  }
+  my_beg = nb;
+  my_end = ne;
+}
+
+// MLP quaternion groups j0, j0 + 2, ... of the feed-forward gate (session.rs:4005-4025) into
+// S.mlp_out; pg/pu hold group j0's gather words. Returns the groups' maximum magnitude.
+__device__ __forceinline__ uint64_t pair_mlp(const DevModel &M, const Lds &S, const DevLayer &ly,
+                                             uint32_t lane, uint32_t j0, uint32_t (&pg)[4],
+                                             uint32_t (&pu)[4]) {
+  uint64_t mmx = 0;
+#pragma unroll 1
+  for (uint32_t j = j0; j < M.mpl; j += 2) {
+    const uint32_t mq = lane + kWave * j;
+    int32_t gq[4], up[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      gq[c] = S.xbar[pg[c]];
+      up[c] = S.xbar[pu[c]];
+    }
+    if (j + 2 < M.mpl) {
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        pg[c] = prog_word(ly.prog, M.s_mlp_gate + 4 * (j + 2) + c, lane);
+        pu[c] = prog_word(ly.prog, M.s_mlp_up + 4 * (j + 2) + c, lane);
+      }
+    }
+    if (mq < M.nm) {
+      int64_t mo[4];
+      mlp_gate(M, S.seeds, gq, up, mo);
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        S.mlp_out[4 * mq + c] = mo[c];
+        uint64_t a = uabs64(mo[c]);
+        mmx = a > mmx ? a : mmx;
+      }
+    }
+  }
+  return wave_reduce64(mmx, OpMax());
+}
+
+__device__ __forceinline__ void pair_mlp_words(const DevModel &M, const DevLayer &ly, uint32_t lane,
+                                               uint32_t j, uint32_t (&pg)[4], uint32_t (&pu)[4]) {
+  if (j < M.mpl) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      pg[c] = prog_word(ly.prog, M.s_mlp_gate + 4 * j + c, lane);
+      pu[c] = prog_word(ly.prog, M.s_mlp_up + 4 * j + c, lane);
+    }
+  }
+}
+
+// The writer on both waves, after barrier 5 (the query is in the crossbar, wmeta[2] says whether
+// the step reuses the last result): wave 0 selects the drawers, each wave scans half of the
+// candidates (by position in the kept drawers' concatenated members, or half of the table for
+// the nearest head), and both return the lower (L1, token).
+template <int SW>
+__device__ __forceinline__ uint32_t pair_writer(const DevModel &M, const Lds &S, uint32_t wave,
+                                                uint32_t lane, uint32_t *kept_out) {
+  if (S.wmeta[2]) {
+    if (wave == 0 && kept_out && lane < M.P) kept_out[lane] = M.head == 1 ? 0u : S.kept[lane];
+    return S.wmeta[0];
+  }
+  if (wave == 0 && M.head != 1) {
+    uint32_t b, e;
+    writer_select(M, S.xbar, S.dscore, S.kept, lane, b, e);
+    if (lane < M.P) {
+      S.rng[lane] = b;
+      S.rng[kMaxProbes + lane] = e;
+    }
+  }
+  pair_sync();  // 6: the kept drawers and their ranges
+  ScanGeom g;
+  uint32_t qpk[16];
+  scan_setup<SW>(M, S.xbar, lane, g, qpk);
+  uint64_t best = UINT64_MAX;
+  if (M.head == 1) {
+    const uint32_t half = M.vocab / 2;
+    best = scan_nearest<SW>(M, qpk, wave ? half : 0, wave ? M.vocab : half, g, best);
+    if (wave == 0 && kept_out && lane < M.P) kept_out[lane] = 0;
+  } else {
+    if (wave == 0 && kept_out && lane < M.P) kept_out[lane] = S.kept[lane];
+    uint32_t my_beg = lane < M.P ? S.rng[lane] : 0, my_end = lane < M.P ? S.rng[kMaxProbes + lane] : 0;
+    const uint32_t total = wave_reduce32(my_end - my_beg, OpAdd()), half = (total + 1) / 2;
+    clip_ranges(M.P, lane, wave ? half : 0, wave ? total : half, my_beg, my_end);
+    constexpr uint32_t cap = kListCap / 2;
+    best = scan_members<SW>(M, qpk, S.list + wave * cap, cap, g, lane, my_beg, my_end, best);
+  }
+  best = wave_reduce64(best, OpMin());
+  if (lane == 0) S.pair[2 + wave] = best;
+  pair_sync();  // 7: both waves' best candidates
+  const uint64_t b0 = S.pair[2], b1 = S.pair[3];
+  return (uint32_t)(b0 < b1 ? b0 : b1);
+}
+
+// Wave 0 of a paired block: the step (RS stack/session.rs:4129-4403) but the window, the ring,
+// the output gates' quaternions and the odd MLP groups.
+template <int Q, int SW>
+__device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32_t lane,
+                                         const bool (&qv)[Q], const uint32_t (&qi)[Q], uint32_t tok,
+                                         bool want_writer, uint32_t *chosen, uint32_t *kept_out,
+                                         int32_t *query_out) {
+  if (tok >= M.vocab) return 1;
+  const uint32_t d = M.d, nq = M.nq;
+  int32_t x[Q][4];
+#pragma unroll
+  for (int k = 0; k < Q; k++) {
+    uint2 w = qv[k] ? *(const uint2 *)(M.table_b + (uint64_t)tok * d + 4 * qi[k])
+                    : make_uint2(0x80008000u, 0x80008000u);
+    const uint32_t ww[2] = {w.x, w.y};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      int16_t v = (int16_t)(uint16_t)(((ww[c >> 1] >> (16 * (c & 1))) & 0xffffu) ^ 0x8000u);
+      x[k][c] = (int32_t)v << 4;  // to_exp_i32(v, -12, -16)
+    }
+  }
+  for (uint32_t l = 0; l < M.L; l++) {
+    const DevLayer ly = M.layers[l];
+    short4 g_rec[Q], g_mlp[Q];
+    ushort4 gd_rec[Q], gd_mlp[Q];
+    int4 rbias[Q];
+    int32_t dbias[Q], doff[Q];
+    uint32_t pw_rot[Q][4], pw_dec[Q], pw_out[Q][4], pw_down[Q][4];
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      const uint32_t qq = qv[k] ? qi[k] : 0, ch = 4 * qq;
+      g_rec[k] = *(const short4 *)(ly.rec_gain + ch);
+      g_mlp[k] = *(const short4 *)(ly.mlp_gain + ch);
+      gd_rec[k] = *(const ushort4 *)(ly.rec_gain_desc + ch);
+      gd_mlp[k] = *(const ushort4 *)(ly.mlp_gain_desc + ch);
+      rbias[k] = *(const int4 *)(ly.gate_bias + nq + ch);
+      dbias[k] = ly.gate_bias[qq];
+      doff[k] = ly.decay_offset[qq];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        pw_rot[k][c] = prog_word(ly.prog, M.s_rec_gate + Q + 4 * k + c, lane);
+        pw_out[k][c] = prog_word(ly.prog, M.s_rec_out + 4 * k + c, lane);
+        pw_down[k][c] = prog_word(ly.prog, M.s_mlp_down + 4 * k + c, lane);
+      }
+      pw_dec[k] = prog_word(ly.prog, M.s_rec_gate + k, lane);
+    }
+    int64_t v[Q][4];
+    norm_gain<Q>(M, S.seeds, x, qv, g_rec, gd_rec, v);
+    publish64<Q>(S.xbar, v, qv, qi);
+    pair_sync();  // 1: the normed activations
+    int32_t rot[Q][4], dec[Q];
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      const int32_t rb[4] = {rbias[k].x, rbias[k].y, rbias[k].z, rbias[k].w};
+#pragma unroll
+      for (int c = 0; c < 4; c++) rot[k][c] = sat_add32(S.xbar[pw_rot[k][c]], rb[c]);
+      dec[k] = sat_add32(S.xbar[pw_dec[k]], dbias[k]);
+    }
+    // Lane weights (session.rs:4989-5026), the transition's rotation (session.rs:5097-5145)
+    // and its product with the state, which do not wait for the window.
+    uint64_t keep[Q];
+    i128 moved[Q][4];
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      if (!qv[k]) continue;
+      int32_t sq = sat_add32(dec[k], doff[k]);
+      sq = sq < 0 ? 0 : sq > 65536 ? 65536 : sq;
+      uint32_t idx = (uint32_t)sq >> 12;
+      idx = idx > 15 ? 15 : idx;
+      keep[k] = M.keep_q31[idx];
+      const int64_t *hp = S.st + (uint64_t)l * d + 4 * qi[k];
+      const int64_t h[4] = {hp[0], hp[1], hp[2], hp[3]};
+      if (M.raw_transition) {
+        int32_t u[4], T[4];
+        unit_q30(rot[k], kRotationEps, u, S.seeds);
+#pragma unroll
+        for (int c = 0; c < 4; c++) T[c] = u[c] >> idx;  // (lambda u) >> 30, lambda = 2^(30-idx)
+        hamilton32(T, h, moved[k]);
+      } else {
+        int64_t T64[4];
+        snap_rotation_dev(M.icosian, make_int4(rot[k][0], rot[k][1], rot[k][2], rot[k][3]),
+                          1ull << (30 - idx), T64);
+        hamilton64(T64, h, moved[k]);
+      }
+    }
+    pair_sync();  // 2: the window sums and the output gates' quaternions
+    int64_t sc[Q][4];
+    uint64_t mx = 0;
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      if (!qv[k]) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) sc[k][c] = 0;
+        continue;
+      }
+      const uint32_t ch = 4 * qi[k];
+      // Transport: h <- shift_wide(T (x) h + (keep wide) << 16, 31).
+      int64_t *hp = S.st + (uint64_t)l * d + ch;
+      int64_t h[4], wide[4], gate[4];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        wide[c] = S.wide[ch + c];
+        gate[c] = S.gq[ch + c];
+      }
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        u128 drive_term = (u128)((i128)keep[k] * (i128)wide[c]) << 16;
+        h[c] = shift_wide((i128)((u128)moved[k][c] + drive_term), 31);
+        hp[c] = h[c];
+      }
+      // Output gate on the moved state (session.rs:4951-4968).
+      int64_t rhs[4], o[4];
+#pragma unroll
+      for (int c = 0; c < 4; c++) rhs[c] = shift(h[c], kResidualExp - kStateExp);
+      gate_mul(M, gate, rhs, o);
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        sc[k][c] = o[c];
+        uint64_t a = uabs64(o[c]);
+        mx = a > mx ? a : mx;
+      }
+    }
+    // quantize16 over the d outputs (kernels.rs:545-553), then gather16 of rec_out.
+    mx = wave_reduce64(mx, OpMax());
+    int32_t qs = bitlen64(mx) - 15;
+    if (qs < 0) qs = 0;
+#pragma unroll
+    for (int k = 0; k < Q; k++)
+      if (qv[k]) {
+        int32_t a[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) a[c] = quantize_elem(sc[k][c], qs);
+        publish16(S.xbar, 4 * qi[k], a, kProductExp + qs);
+      }
+    wave_sync();
+#pragma unroll
+    for (int k = 0; k < Q; k++)
+      if (qv[k])
+#pragma unroll
+        for (int c = 0; c < 4; c++) x[k][c] = sat_add32(x[k][c], S.xbar[pw_out[k][c]]);
+    wave_sync();
+    // ---- feed-forward block: wave 0 takes the even quaternion groups.
+    uint32_t pg[4], pu[4];
+    pair_mlp_words(M, ly, lane, 0, pg, pu);
+    norm_gain<Q>(M, S.seeds, x, qv, g_mlp, gd_mlp, v);
+    publish64<Q>(S.xbar, v, qv, qi);
+    pair_sync();  // 3: the normed activations
+    uint64_t mmx = pair_mlp(M, S, ly, lane, 0, pg, pu);
+    if (lane == 0) S.pair[0] = mmx;
+    pair_sync();  // 4: both waves' MLP outputs and maxima
+    mmx = S.pair[0] > S.pair[1] ? S.pair[0] : S.pair[1];
+    qs = bitlen64(mmx) - 15;
+    if (qs < 0) qs = 0;
+#pragma unroll 1
+    for (uint32_t j = 0; j < M.mpl; j++) {
+      const uint32_t mq = lane + kWave * j;
+      if (mq < M.nm) {
+        int32_t a[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) a[c] = quantize_elem(S.mlp_out[4 * mq + c], qs);
+        publish16(S.xbar, 4 * mq, a, kProductExp + qs);
+      }
+    }
+    wave_sync();
+#pragma unroll
+    for (int k = 0; k < Q; k++)
+      if (qv[k])
+#pragma unroll
+        for (int c = 0; c < 4; c++) x[k][c] = sat_add32(x[k][c], S.xbar[pw_down[k][c]]);
+    wave_sync();
+  }
+  if (!want_writer) return 0;
+  // Final norm, gain and the Q12 query (session.rs:4294-4295, 4364-4366).
+  short4 g_fin[Q];
+  ushort4 gd_fin[Q];
+#pragma unroll
+  for (int k = 0; k < Q; k++) {
+    g_fin[k] = *(const short4 *)(M.final_gain + 4 * (qv[k] ? qi[k] : 0));
+    gd_fin[k] = *(const ushort4 *)(M.final_gain_desc + 4 * (qv[k] ? qi[k] : 0));
+  }
+  int64_t v[Q][4];
+  norm_gain<Q>(M, S.seeds, x, qv, g_fin, gd_fin, v);
+  int4 qq[Q];
+  bool same = true;  // this lane's channels equal the query of the writer's last run
+#pragma unroll
+  for (int k = 0; k < Q; k++)
+    if (qv[k]) {
+      int32_t qa[4];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        int32_t y = to_exp_i32(v[k][c], kNormFineExp, kQ12Exp);
+        qa[c] = y > 32767 ? 32767 : y < -32768 ? -32768 : y;
+      }
+      qq[k] = make_int4(qa[0], qa[1], qa[2], qa[3]);
+      *(int4 *)(S.xbar + 4 * qi[k]) = qq[k];
+      if (query_out) *(int4 *)(query_out + 4 * qi[k]) = qq[k];
+      const int4 old = *(const int4 *)(S.wq + 4 * qi[k]);
+      same = same && old.x == qa[0] && old.y == qa[1] && old.z == qa[2] && old.w == qa[3];
+    }
+  // The writer's token and kept drawers are a function of the query alone: a query equal to
+  // the last one the writer ran on (a sequence settled on a fixed point) takes its result.
+  const bool reuse = S.wmeta[1] != 0 && __all(same);
+  if (lane == 0) S.wmeta[2] = reuse;
+  pair_sync();  // 5: the query and the reuse flag
+  *chosen = pair_writer<SW>(M, S, 0, lane, kept_out);
+  if (!reuse) {
+#pragma unroll
+    for (int k = 0; k < Q; k++)
+      if (qv[k]) *(int4 *)(S.wq + 4 * qi[k]) = qq[k];
+    if (lane == 0) {
+      S.wmeta[0] = *chosen;
+      S.wmeta[1] = 1;
+    }
+  }
+  return 0;
+}
+
+// Tap k on the lane's four channels of x: tap_desc words (fast taps) or grid codes.
+__device__ __forceinline__ void tap4(const DevModel &M, const DevLayer &ly, uint32_t k, uint32_t ch,
+                                     const int4 &x, int64_t (&acc)[4]) {
+  if (M.taps_fast) {
+    const uint2 t = *(const uint2 *)(ly.taps_desc + (uint64_t)k * M.d + ch);
+    acc[0] = wadd64(acc[0], tap_desc_apply(x.x, t.x, 0));
+    acc[1] = wadd64(acc[1], tap_desc_apply(x.y, t.x, 1));
+    acc[2] = wadd64(acc[2], tap_desc_apply(x.z, t.y, 0));
+    acc[3] = wadd64(acc[3], tap_desc_apply(x.w, t.y, 1));
+  } else {
+    const short4 t = *(const short4 *)(ly.taps + (uint64_t)k * M.d + ch);
+    acc[0] = wadd64(acc[0], grid_apply(x.x, t.x));
+    acc[1] = wadd64(acc[1], grid_apply(x.y, t.y));
+    acc[2] = wadd64(acc[2], grid_apply(x.z, t.z));
+    acc[3] = wadd64(acc[3], grid_apply(x.w, t.w));
+  }
+}
+
+// The window over earlier positions for a step whose ring slot is `base`: tap s on the drive
+// s positions back (ring slot base - s), for s = s1..W, added to acc (session.rs:4842-4868;
+// wrapping sums, so the order of the terms does not matter). Rows and taps load kWindowChunk at
+// a time.
+__device__ __forceinline__ void window_sum(const DevModel &M, const DevLayer &ly,
+                                           const int32_t *ring_l, uint32_t base, uint32_t s1,
+                                           uint32_t ch, int64_t (&acc)[4]) {
+  const uint32_t d = M.d, W = M.W;
+  if (M.taps_fast) {
+    for (uint32_t s0 = s1; s0 <= W; s0 += kWindowChunk) {
+      int4 hb[kWindowChunk];
+      uint2 tb[kWindowChunk];  // tap_desc pairs: channels 0, 1 in .x, 2, 3 in .y
+#pragma unroll
+      for (uint32_t i = 0; i < kWindowChunk; i++) {
+        const uint32_t s = s0 + i;
+        if (s <= W) {
+          const uint32_t sl = base >= s ? base - s : base + W - s;
+          hb[i] = *(const int4 *)(ring_l + (uint64_t)sl * d + ch);
+          tb[i] = *(const uint2 *)(ly.taps_desc + (uint64_t)s * d + ch);
+        }
+      }
+#pragma unroll
+      for (uint32_t i = 0; i < kWindowChunk; i++)
+        if (s0 + i <= W) {
+          acc[0] = wadd64(acc[0], tap_desc_apply(hb[i].x, tb[i].x, 0));
+          acc[1] = wadd64(acc[1], tap_desc_apply(hb[i].y, tb[i].x, 1));
+          acc[2] = wadd64(acc[2], tap_desc_apply(hb[i].z, tb[i].y, 0));
+          acc[3] = wadd64(acc[3], tap_desc_apply(hb[i].w, tb[i].y, 1));
+        }
+    }
+  } else {
+    // A tap outside the descriptor form somewhere in the model: the reference routine.
+    for (uint32_t s = s1; s <= W; s++) {
+      const uint32_t sl = base >= s ? base - s : base + W - s;
+      tap4(M, ly, s, ch, *(const int4 *)(ring_l + (uint64_t)sl * d + ch), acc);
+    }
+  }
+}
+
+// Wave 1 of a paired block: the causal window (session.rs:4842-4868) read from and written to
+// the sequence's ring, the output gates' quaternions, the odd MLP groups and half of the writer.
+// The window's terms over earlier positions (taps 1..W) do not depend on the step's input, so
+// wave 1 sums them for the next step while wave 0 runs the transport, and keeps them in `hist`
+// (L x d i64 per block); the first step of a launch sums its own (`fresh`).
+template <int Q, int SW>
+__device__ __forceinline__ int step_window(const DevModel &M, const Lds &S, int32_t *ring,
+                                           int64_t *hist, uint32_t base, uint32_t lane,
+                                           const bool (&qv)[Q], const uint32_t (&qi)[Q],
+                                           uint32_t tok, bool want_writer, bool fresh,
+                                           uint32_t *chosen) {
+  if (tok >= M.vocab) return 1;
+  const uint32_t d = M.d, W = M.W;
+  const uint32_t next = base + 1 == W ? 0 : base + 1;  // the next step's ring slot
+  for (uint32_t l = 0; l < M.L; l++) {
+    const DevLayer ly = M.layers[l];
+    int32_t *ring_l = ring + (uint64_t)l * W * d;
+    int64_t *hist_l = hist + (uint64_t)l * d;
+    int4 cbias[Q];
+    uint32_t pw_drive[Q][4], pw_gate[Q][4];
+    int64_t sum[Q][4];  // taps 1..W over the earlier positions
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      const uint32_t ch = 4 * (qv[k] ? qi[k] : 0);
+      cbias[k] = *(const int4 *)(ly.conv_bias + ch);
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        pw_drive[k][c] = prog_word(ly.prog, M.s_rec_in + 4 * k + c, lane);
+        pw_gate[k][c] = prog_word(ly.prog, M.s_rec_in + 4 * Q + 4 * k + c, lane);
+      }
+      if (fresh) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) sum[k][c] = 0;
+        if (qv[k]) window_sum(M, ly, ring_l, base, 1, ch, sum[k]);
+      } else {
+        const longlong2 *hp = (const longlong2 *)(hist_l + ch);
+        const longlong2 a = hp[0], b = hp[1];
+        sum[k][0] = a.x;
+        sum[k][1] = a.y;
+        sum[k][2] = b.x;
+        sum[k][3] = b.y;
+      }
+    }
+    // The first MLP group's gather words, for after barrier 3.
+    uint32_t pg[4], pu[4];
+    pair_mlp_words(M, ly, lane, 1, pg, pu);
+    pair_sync();  // 1: the normed activations
+    int4 drive[Q];
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      if (!qv[k]) continue;
+      const uint32_t ch = 4 * qi[k];
+      int32_t gv[4];
+#pragma unroll
+      for (int c = 0; c < 4; c++) gv[c] = S.xbar[pw_gate[k][c]];
+      drive[k] = make_int4(S.xbar[pw_drive[k][0]], S.xbar[pw_drive[k][1]], S.xbar[pw_drive[k][2]],
+                           S.xbar[pw_drive[k][3]]);
+      // Tap 0 on the drive and the conv bias, then the drive enters ring slot base.
+      int64_t wide[4] = {cbias[k].x, cbias[k].y, cbias[k].z, cbias[k].w};
+      tap4(M, ly, 0, ch, drive[k], wide);
+#pragma unroll
+      for (int c = 0; c < 4; c++) S.wide[ch + c] = wadd64(wide[c], sum[k][c]);
+      *(int4 *)(ring_l + (uint64_t)base * d + ch) = drive[k];
+      int64_t gate[4];
+      gate_quat(M, S.seeds, gv, gate);
+#pragma unroll
+      for (int c = 0; c < 4; c++) S.gq[ch + c] = gate[c];
+    }
+    pair_sync();  // 2: the window sums and the output gates' quaternions
+    // The next step's terms over earlier positions: tap 1 on this step's drive, taps 2..W from
+    // the ring (slots next - s, none of them the slot just written).
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      if (!qv[k]) continue;
+      const uint32_t ch = 4 * qi[k];
+      int64_t acc[4] = {0, 0, 0, 0};
+      tap4(M, ly, 1, ch, drive[k], acc);
+      window_sum(M, ly, ring_l, next, 2, ch, acc);
+      longlong2 *hp = (longlong2 *)(hist_l + ch);
+      hp[0] = make_longlong2(acc[0], acc[1]);
+      hp[1] = make_longlong2(acc[2], acc[3]);
+    }
+    pair_sync();  // 3: the normed activations
+    const uint64_t mmx = pair_mlp(M, S, ly, lane, 1, pg, pu);
+    if (lane == 0) S.pair[1] = mmx;
+    pair_sync();  // 4: both waves' MLP outputs and maxima
+  }
+  if (!want_writer) return 0;
+  pair_sync();  // 5: the query and the reuse flag
+  *chosen = pair_writer<SW>(M, S, 1, lane, nullptr);
+  return 0;
+}
+
 // The phase a kernel is compiled for. Prefill: decode launches with no generated step (the
 // prompt, its last choice, the state out). Decode: decode launches that generate. Rows: the
 // teacher-forced modes, sequences and score.
 enum Phase : int { kPhasePrefill = 0, kPhaseDecode = 1, kPhaseRows = 2 };
 
-template <int Q, int SW, int PH>
+// NW = 1: one wavefront per sequence (step); NW = 2: paired blocks (step_main, step_window).
+template <int Q, int SW, int PH, int NW>
 __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
   extern __shared__ __align__(16) int32_t lds[];
   Lds S;
@@ -868,15 +1442,36 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
     uint32_t *seed_lds = (uint32_t *)(lds + at);
     at += kRsqrtSeedWords + kRecipSeedWords;
     S.st = (int64_t *)(lds + at);
+    at += 2 * M.L * M.d;
+    S.wide = S.gq = nullptr;
+    S.rng = nullptr;
+    S.pair = nullptr;
+    if (NW == 2) {  // pair_lds_bytes
+      S.wide = (int64_t *)(lds + at);
+      at += 2 * M.d;
+      S.gq = (int64_t *)(lds + at);
+      at += 2 * M.d;
+      S.rng = (uint32_t *)(lds + at);
+      at += 2 * kMaxProbes;
+      S.pair = (uint64_t *)(lds + at);
+    }
     const uint32_t *rs = rsqrt_seed_table(), *rc = recip_seed_table();
-    for (uint32_t i = threadIdx.x; i < kRsqrtSeedWords; i += kWave) seed_lds[i] = rs[i];
-    for (uint32_t i = threadIdx.x; i < kRecipSeedWords; i += kWave) seed_lds[kRsqrtSeedWords + i] = rc[i];
+    for (uint32_t i = threadIdx.x; i < kRsqrtSeedWords; i += NW * kWave) seed_lds[i] = rs[i];
+    for (uint32_t i = threadIdx.x; i < kRecipSeedWords; i += NW * kWave) seed_lds[kRsqrtSeedWords + i] = rc[i];
     S.seeds = Seeds(seed_lds, seed_lds + kRsqrtSeedWords);
-    wave_sync();
+    if (NW == 2)
+      pair_sync();
+    else
+      wave_sync();
   }
-  const uint32_t lane = threadIdx.x;
+  // The wave index read as a scalar, so that the compiler treats the role branches as uniform.
+  const uint32_t lane = threadIdx.x % kWave, wave = uniform32(threadIdx.x / kWave);
+  // Paired blocks: wave 0 keeps the recurrence state, wave 1 the window ring.
+  const bool keeps_state = NW == 1 || wave == 0, keeps_ring = NW == 1 || wave == 1;
+  const bool writes_out = wave == 0 && lane == 0;
   const uint32_t d = M.d, L = M.L, W = M.W;
   int32_t *ring = A.ring + (uint64_t)blockIdx.x * L * W * d;
+  int64_t *hist = NW == 2 ? A.hist + (uint64_t)blockIdx.x * L * d : nullptr;
   bool qv[Q];
   uint32_t qi[Q];
 #pragma unroll
@@ -894,18 +1489,23 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
       for (int k = 0; k < Q; k++)
         if (qv[k]) {
           uint32_t ch = 4 * qi[k];
+          if (keeps_state)
 #pragma unroll
-          for (int c = 0; c < 4; c++)
-            S.st[(uint64_t)l * d + ch + c] =
-                A.in_state ? A.in_state[((uint64_t)s * L + l) * d + ch + c] : 0;
-          for (uint32_t r = 0; r < W; r++) {
-            uint32_t slot = (base + 2 * W - 1 - r) % W;
-            int4 h = make_int4(0, 0, 0, 0);
-            if (A.in_history) h = *(const int4 *)(A.in_history + (((uint64_t)s * L + l) * W + r) * d + ch);
-            *(int4 *)(ring + ((uint64_t)l * W + slot) * d + ch) = h;
-          }
+            for (int c = 0; c < 4; c++)
+              S.st[(uint64_t)l * d + ch + c] =
+                  A.in_state ? A.in_state[((uint64_t)s * L + l) * d + ch + c] : 0;
+          if (keeps_ring)
+            for (uint32_t r = 0; r < W; r++) {
+              uint32_t slot = (base + 2 * W - 1 - r) % W;
+              int4 h = make_int4(0, 0, 0, 0);
+              if (A.in_history) h = *(const int4 *)(A.in_history + (((uint64_t)s * L + l) * W + r) * d + ch);
+              *(int4 *)(ring + ((uint64_t)l * W + slot) * d + ch) = h;
+            }
         }
-    wave_sync();
+    if (NW == 2)
+      pair_sync();
+    else
+      wave_sync();
     int status = 0;
     uint32_t chosen = 0;
     constexpr bool decode = PH != kPhaseRows;
@@ -926,11 +1526,16 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
       const bool want = decode ? t + 1 >= A.len : (seq || A.out_tokens || t + 1 < A.len);
       uint32_t *kept_out = seq && A.out_kept ? A.out_kept + at * M.P : nullptr;
       int32_t *query_out = seq && A.out_query ? A.out_query + at * d : nullptr;
-      status = step<Q, SW>(M, S, ring, base, lane, qv, qi, tok, want, &chosen, kept_out, query_out);
+      if (NW == 1)
+        status = step<Q, SW>(M, S, ring, base, lane, qv, qi, tok, want, &chosen, kept_out, query_out);
+      else if (wave == 0)
+        status = step_main<Q, SW>(M, S, lane, qv, qi, tok, want, &chosen, kept_out, query_out);
+      else
+        status = step_window<Q, SW>(M, S, ring, hist, base, lane, qv, qi, tok, want, t == 0, &chosen);
       if (status) break;
       pos++;
       base = base + 1 == W ? 0 : base + 1;
-      if (lane == 0) {
+      if (writes_out) {
         if (decode) {
           if (want) A.out_tokens[(uint64_t)s * (A.gen + 1) + t + 1 - A.len] = chosen;
         } else {
@@ -939,28 +1544,31 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
         }
       }
     }
-    if (!decode && A.mode == kModeScore && lane == 0 && hits) atomicAdd(A.matches, hits);
+    if (!decode && A.mode == kModeScore && writes_out && hits) atomicAdd(A.matches, hits);
     if (decode && status == 0) {
       for (uint32_t l = 0; l < L; l++)
 #pragma unroll
         for (int k = 0; k < Q; k++)
           if (qv[k]) {
             uint32_t ch = 4 * qi[k];
-            if (A.out_state)
+            if (A.out_state && keeps_state)
 #pragma unroll
               for (int c = 0; c < 4; c++)
                 A.out_state[((uint64_t)s * L + l) * d + ch + c] = S.st[(uint64_t)l * d + ch + c];
-            if (A.out_history)
+            if (A.out_history && keeps_ring)
               for (uint32_t r = 0; r < W; r++) {
                 uint32_t slot = (base + 2 * W - 1 - r) % W;
                 *(int4 *)(A.out_history + (((uint64_t)s * L + l) * W + r) * d + ch) =
                     *(const int4 *)(ring + ((uint64_t)l * W + slot) * d + ch);
               }
           }
-      if (A.out_position && lane == 0) A.out_position[s] = pos;
+      if (A.out_position && writes_out) A.out_position[s] = pos;
     }
-    if (lane == 0) A.status[s] = status;
-    wave_sync();
+    if (writes_out) A.status[s] = status;
+    if (NW == 2)
+      pair_sync();
+    else
+      wave_sync();
   }
 }
 
@@ -971,9 +1579,10 @@ struct KernelSet {
   KernelFn q1s1, q1s2, q1s4, q1s8, q2s16, q4s32;
 };
 
-// Launches the member of `k` for the model's shape: one 64-lane block per resident sequence.
+// Launches the member of `k` for the model's shape: one block of `waves` wavefronts per
+// resident sequence.
 inline hipError_t launch_shape(const KernelSet &k, const DevModel &M, const RunArgs &A,
-                               uint32_t grid, size_t lds, hipStream_t stream) {
+                               uint32_t grid, uint32_t waves, size_t lds, hipStream_t stream) {
   uint32_t S = 1;
   while (S < M.d / 32) S <<= 1;
   KernelFn f = M.qpl == 1 && S == 1    ? k.q1s1
@@ -987,21 +1596,29 @@ inline hipError_t launch_shape(const KernelSet &k, const DevModel &M, const RunA
   DevModel m = M;
   RunArgs a = A;
   void *args[] = {&m, &a};
-  hipError_t e = hipLaunchKernel((const void *)f, dim3(grid), dim3(kWave), args, lds, stream);
+  hipError_t e = hipLaunchKernel((const void *)f, dim3(grid), dim3(waves * kWave), args, lds, stream);
   return e != hipSuccess ? e : hipGetLastError();
 }
 
-// The phase's kernels: `NAME<Q, SW>` and `hipError_t launch_NAME(M, A, grid, lds, stream)`.
+// The phase's kernels: `NAME<Q, SW>` (one wavefront per sequence), `NAME_pair<Q, SW>` (paired
+// blocks, at most 256 registers per lane so that two waves share each SIMD) and
+// `hipError_t launch_NAME(M, A, grid, waves, lds, stream)`.
 #define FBS_PHASE_KERNELS(NAME, PH)                                                          \
   template <int Q, int SW>                                                                    \
   __global__ __launch_bounds__(64) void NAME(DevModel M, RunArgs A) {                         \
-    run<Q, SW, PH>(M, A);                                                                     \
+    run<Q, SW, PH, 1>(M, A);                                                                  \
   }                                                                                           \
-  hipError_t launch_##NAME(const DevModel &M, const RunArgs &A, uint32_t grid, size_t lds,    \
-                           hipStream_t stream) {                                              \
-    static const KernelSet k = {NAME<1, 1>, NAME<1, 2>, NAME<1, 4>,                           \
-                                NAME<1, 8>, NAME<2, 16>, NAME<4, 32>};                         \
-    return launch_shape(k, M, A, grid, lds, stream);                                          \
+  template <int Q, int SW>                                                                    \
+  __global__ __launch_bounds__(128, 2) void NAME##_pair(DevModel M, RunArgs A) {              \
+    run<Q, SW, PH, 2>(M, A);                                                                  \
+  }                                                                                           \
+  hipError_t launch_##NAME(const DevModel &M, const RunArgs &A, uint32_t grid, uint32_t waves, \
+                           size_t lds, hipStream_t stream) {                                  \
+    static const KernelSet one = {NAME<1, 1>, NAME<1, 2>, NAME<1, 4>,                         \
+                                  NAME<1, 8>, NAME<2, 16>, NAME<4, 32>};                       \
+    static const KernelSet two = {NAME##_pair<1, 1>, NAME##_pair<1, 2>, NAME##_pair<1, 4>,    \
+                                  NAME##_pair<1, 8>, NAME##_pair<2, 16>, NAME##_pair<4, 32>};  \
+    return launch_shape(waves == 2 ? two : one, M, A, grid, waves, lds, stream);              \
   }
 
 }  // namespace fbs

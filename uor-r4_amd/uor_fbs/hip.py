@@ -28,7 +28,7 @@ SYMBOLS = (
     "uor_fbs_abi_version", "uor_fbs_sizeof_model", "uor_fbs_sizeof_layer", "uor_fbs_sizeof_ext",
     "uor_fbs_last_error", "uor_fbs_model_create", "uor_fbs_model_destroy", "uor_fbs_state_words",
     "uor_fbs_history_words", "uor_fbs_sequences", "uor_fbs_sequences_async", "uor_fbs_decode",
-    "uor_fbs_decode_async", "uor_fbs_score", "uor_fbs_score_async",
+    "uor_fbs_decode_async", "uor_fbs_score", "uor_fbs_score_async", "uor_fbs_block_waves",
 )
 
 
@@ -57,6 +57,8 @@ def lib():
         L.uor_fbs_state_words.restype = C.c_uint64
         L.uor_fbs_history_words.argtypes = [P]
         L.uor_fbs_history_words.restype = C.c_uint64
+        L.uor_fbs_block_waves.argtypes = [P, C.c_uint32]
+        L.uor_fbs_block_waves.restype = C.c_uint32
         L.uor_fbs_sequences.argtypes = [P, P, C.c_uint32, C.c_uint32, P, P, P]
         L.uor_fbs_sequences_async.argtypes = [P, P, C.c_uint32, C.c_uint32, P, P, P, P, P]
         L.uor_fbs_decode.argtypes = [P, P, C.c_uint32, C.c_uint32, C.c_uint32, P, P, P, P, P, P, P]
@@ -109,6 +111,10 @@ class Model:
     @property
     def history_words(self) -> int:
         return int(lib().uor_fbs_history_words(self.handle))
+
+    def block_waves(self, n: int) -> int:
+        """Wavefronts per sequence of the kernels a run of n sequences launches (1 or 2)."""
+        return int(lib().uor_fbs_block_waves(self.handle, n))
 
     def sequences(self, tokens, want_kept=True, want_query=True):
         """Teacher-forced runs from fresh sessions: (tokens [S,len], kept [S,len,P], query [S,len,d])."""
