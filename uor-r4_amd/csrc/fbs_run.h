@@ -919,15 +919,16 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
 // ---------------------------------------------------------------------------------------------
 // Paired blocks: one sequence on the two wavefronts of a 128-lane block, for batches that would
 // leave SIMDs without a second wave. Wave 0 holds the residual stream and the recurrence state:
-// the norms, the transition, transport and output gate product, both requantizes and the
-// writer's drawer selection. Wave 1 owns the window ring: it sums the window over the earlier
-// positions while wave 0 normalises, adds tap 0, writes the drive into the ring, and forms the
-// output gate's quaternion while wave 0 forms the transition. The MLP's quaternion groups
+// the norms, the transition and transport, the output gate's product and its requantize, the
+// final query and the writer's drawer selection. Wave 1 owns the window ring: it adds tap 0 to
+// the window sums it formed during the previous step, writes the drive into the ring and forms
+// the output gate's quaternion while wave 0 forms the transition, then sums the next step's
+// window while wave 0 runs the transport. The MLP's quaternion groups (and their requantize)
 // alternate between the waves, and each wave scans half of the writer's candidates. The two
 // waves meet at block barriers, numbered alike in step_main and step_window: every path through
 // a step reaches the same barriers in the same order on both waves (the branches between them
 // depend only on values both waves hold: the model, the step's token and want_writer, and the
-// reuse flag read after barrier 5).
+// reuse flag read after barrier 6).
 
 // Both waves of the block meet; LDS writes before it are visible to the other wave after it.
 // Global loads in flight stay in flight (LDS-only fences).
@@ -953,6 +954,25 @@ __device__ __forceinline__ void clip_ranges(uint32_t P, uint32_t lane, uint32_t 
   }
   my_beg = nb;
   my_end = ne;
+}
+
+// The MLP's requantize (quantize16, kernels.rs:545-553) for groups j0, j0 + 2, ...: S.mlp_out
+// at the shared shift of both waves' maxima, published for the mlp_down gathers.
+__device__ __forceinline__ void pair_requant(const DevModel &M, const Lds &S, uint32_t lane,
+                                             uint32_t j0) {
+  const uint64_t mmx = S.pair[0] > S.pair[1] ? S.pair[0] : S.pair[1];
+  int32_t qs = bitlen64(mmx) - 15;
+  if (qs < 0) qs = 0;
+#pragma unroll 1
+  for (uint32_t j = j0; j < M.mpl; j += 2) {
+    const uint32_t mq = lane + kWave * j;
+    if (mq < M.nm) {
+      int32_t a[4];
+#pragma unroll
+      for (int c = 0; c < 4; c++) a[c] = quantize_elem(S.mlp_out[4 * mq + c], qs);
+      publish16(S.xbar, 4 * mq, a, kProductExp + qs);
+    }
+  }
 }
 
 // MLP quaternion groups j0, j0 + 2, ... of the feed-forward gate (session.rs:4005-4025) into
@@ -1002,7 +1022,7 @@ __device__ __forceinline__ void pair_mlp_words(const DevModel &M, const DevLayer
   }
 }
 
-// The writer on both waves, after barrier 5 (the query is in the crossbar, wmeta[2] says whether
+// The writer on both waves, after barrier 6 (the query is in the crossbar, wmeta[2] says whether
 // the step reuses the last result): wave 0 selects the drawers, each wave scans half of the
 // candidates (by position in the kept drawers' concatenated members, or half of the table for
 // the nearest head), and both return the lower (L1, token).
@@ -1021,7 +1041,7 @@ __device__ __forceinline__ uint32_t pair_writer(const DevModel &M, const Lds &S,
       S.rng[kMaxProbes + lane] = e;
     }
   }
-  pair_sync();  // 6: the kept drawers and their ranges
+  pair_sync();  // 7: the kept drawers and their ranges
   ScanGeom g;
   uint32_t qpk[16];
   scan_setup<SW>(M, S.xbar, lane, g, qpk);
@@ -1040,13 +1060,13 @@ __device__ __forceinline__ uint32_t pair_writer(const DevModel &M, const Lds &S,
   }
   best = wave_reduce64(best, OpMin());
   if (lane == 0) S.pair[2 + wave] = best;
-  pair_sync();  // 7: both waves' best candidates
+  pair_sync();  // 8: both waves' best candidates
   const uint64_t b0 = S.pair[2], b1 = S.pair[3];
   return (uint32_t)(b0 < b1 ? b0 : b1);
 }
 
-// Wave 0 of a paired block: the step (RS stack/session.rs:4129-4403) but the window, the ring,
-// the output gates' quaternions and the odd MLP groups.
+// Wave 0 of a paired block: the step (RS stack/session.rs:4129-4403) but the window and its
+// ring, the output gates' quaternions and the odd MLP groups.
 template <int Q, int SW>
 __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32_t lane,
                                          const bool (&qv)[Q], const uint32_t (&qi)[Q], uint32_t tok,
@@ -1192,23 +1212,11 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
     norm_gain<Q>(M, S.seeds, x, qv, g_mlp, gd_mlp, v);
     publish64<Q>(S.xbar, v, qv, qi);
     pair_sync();  // 3: the normed activations
-    uint64_t mmx = pair_mlp(M, S, ly, lane, 0, pg, pu);
+    const uint64_t mmx = pair_mlp(M, S, ly, lane, 0, pg, pu);
     if (lane == 0) S.pair[0] = mmx;
     pair_sync();  // 4: both waves' MLP outputs and maxima
-    mmx = S.pair[0] > S.pair[1] ? S.pair[0] : S.pair[1];
-    qs = bitlen64(mmx) - 15;
-    if (qs < 0) qs = 0;
-#pragma unroll 1
-    for (uint32_t j = 0; j < M.mpl; j++) {
-      const uint32_t mq = lane + kWave * j;
-      if (mq < M.nm) {
-        int32_t a[4];
-#pragma unroll
-        for (int c = 0; c < 4; c++) a[c] = quantize_elem(S.mlp_out[4 * mq + c], qs);
-        publish16(S.xbar, 4 * mq, a, kProductExp + qs);
-      }
-    }
-    wave_sync();
+    pair_requant(M, S, lane, 0);
+    pair_sync();  // 5: the requantized MLP outputs
 #pragma unroll
     for (int k = 0; k < Q; k++)
       if (qv[k])
@@ -1248,7 +1256,7 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
   // the last one the writer ran on (a sequence settled on a fixed point) takes its result.
   const bool reuse = S.wmeta[1] != 0 && __all(same);
   if (lane == 0) S.wmeta[2] = reuse;
-  pair_sync();  // 5: the query and the reuse flag
+  pair_sync();  // 6: the query and the reuse flag
   *chosen = pair_writer<SW>(M, S, 0, lane, kept_out);
   if (!reuse) {
 #pragma unroll
@@ -1405,9 +1413,11 @@ __device__ __forceinline__ int step_window(const DevModel &M, const Lds &S, int3
     const uint64_t mmx = pair_mlp(M, S, ly, lane, 1, pg, pu);
     if (lane == 0) S.pair[1] = mmx;
     pair_sync();  // 4: both waves' MLP outputs and maxima
+    pair_requant(M, S, lane, 1);
+    pair_sync();  // 5: the requantized MLP outputs
   }
   if (!want_writer) return 0;
-  pair_sync();  // 5: the query and the reuse flag
+  pair_sync();  // 6: the query and the reuse flag
   *chosen = pair_writer<SW>(M, S, 1, lane, nullptr);
   return 0;
 }
@@ -1526,12 +1536,23 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
       const bool want = decode ? t + 1 >= A.len : (seq || A.out_tokens || t + 1 < A.len);
       uint32_t *kept_out = seq && A.out_kept ? A.out_kept + at * M.P : nullptr;
       int32_t *query_out = seq && A.out_query ? A.out_query + at * d : nullptr;
-      if (NW == 1)
+      if (NW == 1) {
         status = step<Q, SW>(M, S, ring, base, lane, qv, qi, tok, want, &chosen, kept_out, query_out);
-      else if (wave == 0)
-        status = step_main<Q, SW>(M, S, lane, qv, qi, tok, want, &chosen, kept_out, query_out);
-      else
-        status = step_window<Q, SW>(M, S, ring, hist, base, lane, qv, qi, tok, want, t == 0, &chosen);
+      } else {
+        // The lane's indices pass through an empty asm at every step, so that the compiler forms
+        // the lane's addresses inside the loop instead of holding them across the kernel.
+        uint32_t ln = lane, qs[Q];
+        asm volatile("" : "+v"(ln));
+#pragma unroll
+        for (int k = 0; k < Q; k++) {
+          qs[k] = qi[k];
+          asm volatile("" : "+v"(qs[k]));
+        }
+        if (wave == 0)
+          status = step_main<Q, SW>(M, S, ln, qv, qs, tok, want, &chosen, kept_out, query_out);
+        else
+          status = step_window<Q, SW>(M, S, ring, hist, base, ln, qv, qs, tok, want, t == 0, &chosen);
+      }
       if (status) break;
       pos++;
       base = base + 1 == W ? 0 : base + 1;
