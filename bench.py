@@ -38,7 +38,7 @@ sys.path[:0] = [os.path.join(ROOT, "uor-r4_amd"), os.path.join(ROOT, "oracle")]
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 # Measured HBM bytes per launch of the decode kernel (rocprofv3 FETCH_SIZE and WRITE_SIZE passes,
 # scaled by a copy kernel's reading), for the workload it names.
-TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fbs_decode_c3_b1024_traffic.md")
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fbs_decode_pair_c3_b1024_traffic.md")
 
 
 def parse():
