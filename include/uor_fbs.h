@@ -34,7 +34,8 @@ extern "C" {
 #define UOR_FBS_OK 0
 #define UOR_FBS_ERR_TOKEN 1       /* token >= vocab (fbs_core.h:627) */
 #define UOR_FBS_ERR_CONTEXT 2     /* position >= context (fbs_core.h:628) */
-#define UOR_FBS_ERR_ARGUMENT 3    /* a null pointer, a zero or inconsistent size */
+#define UOR_FBS_ERR_ARGUMENT 3    /* a null pointer, a zero or inconsistent size; as a
+                                     per-sequence status: a slot past the capacity */
 #define UOR_FBS_ERR_SHAPE 4       /* a model the reference's loader would refuse */
 #define UOR_FBS_ERR_DEVICE 5      /* a HIP runtime error */
 #define UOR_FBS_ERR_UNSUPPORTED 6 /* a shape this build has no kernel for */
@@ -159,6 +160,24 @@ int uor_fbs_decode_async(uor_fbs_handle *handle, const uint32_t *prompts, uint32
                          const uint32_t *in_position, int64_t *out_state,
                          int32_t *out_history, uint32_t *out_position, int32_t *status,
                          void *stream);
+
+/* Serving sessions held in caller-owned device arrays, one slot per session: `state`
+ * [capacity][state_words] int64, `history` [capacity][history_words] int32 and `position`
+ * [capacity] uint32, updated in place. Sequence i of the call is the session in slot
+ * slots[i] < capacity (distinct within a call); it takes prompts[i*prompt_len ..] from its
+ * slot's state, then `gen` greedy steps, as uor_fbs_decode_async: out_reply gets gen+1 tokens
+ * per sequence. The serving loop of IntegerStackSession for a batch of sessions:
+ * serve_step / step_native (session.rs:3356-3440, the browser's wasm_step,
+ * wasm_serve.rs:140-152) with prompt_len 1 and gen 0, read_step (session.rs:3392) for all
+ * prompt tokens but the last, which one call folds into prompt_len. Optional out_kept [n][P]
+ * and out_query [n][width] receive the last step's kept drawers and Q12 query (step_native's
+ * NativeStep, session.rs:484-493). A sequence whose status is nonzero leaves its slot as it
+ * was (status 3: slots[i] >= capacity, nothing read or written). Device buffers. */
+int uor_fbs_decode_slots_async(uor_fbs_handle *handle, const uint32_t *slots, uint32_t sequences,
+                               uint32_t capacity, const uint32_t *prompts, uint32_t prompt_len,
+                               uint32_t gen, uint32_t *out_reply, int64_t *state,
+                               int32_t *history, uint32_t *position, uint32_t *out_kept,
+                               int32_t *out_query, int32_t *status, void *stream);
 
 /* Teacher-forced next-token scoring: for each row of `len` tokens, position t's choice is
  * compared with row[t+1] (t < len-1); `out_matches` gets the total count of equal pairs.

@@ -1,0 +1,186 @@
+"""Serving sessions on the GPU (uor_fbs/session.py over uor_fbs_decode_slots_async) against the
+batched decode and the oracle: IntegerStackSession's serving calls (stack/session.rs:2703-3440),
+a serving loop that steps whichever sessions have a token, and snapshots that restore into any
+slot and continue bit for bit (session.rs:2777-3290, session_codec.rs)."""
+
+from dataclasses import replace
+
+import numpy as np
+import pytest
+
+import oracle
+from uor_fbs import hip, session_codec, synth
+from uor_fbs.hipmem import DeviceArray
+from uor_fbs.session import NO_CHOICE, Session, SessionError, SessionPool, serve_steps
+
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("block_waves")]
+
+SPEC = replace(synth.CONFIGS["c2"], context=48, layers=3)
+SEED = 71
+
+
+@pytest.fixture(scope="module")
+def art():
+    return synth.make_artifact(SPEC, SEED)
+
+
+def test_serving_loop_equals_batched_decode(art):
+    S, P, G = 6, 10, 24
+    prompts = synth.uniform_prompts(SPEC.vocab, S, P, 73)
+    print(f"serving loop: {S} sessions, prompt {P}, gen {G}", flush=True)
+    model = hip.Model(art)
+    want = model.decode(prompts, gen=G)
+    pool = SessionPool(model, capacity=11)
+    # Slots taken out of order; sessions join the loop at different steps.
+    pool.acquire(), pool.acquire()
+    sessions = [Session(pool) for _ in range(S)]
+    start = [0, 3, 1, 7, 2, 5]
+    nxt = [None] * S
+    got = [[] for _ in range(S)]
+    rng = np.random.default_rng(5)
+    for step in range(max(start) + G + 1):
+        batch, toks = [], []
+        for i in rng.permutation(S):
+            k = step - start[i]
+            if k == 0:
+                nxt[i] = sessions[i].feed(prompts[i]).token     # the prompt in one launch
+                got[i].append(nxt[i])
+            elif 0 < k < G + 1:
+                batch.append(sessions[i])
+                toks.append(nxt[i])
+        if batch:
+            for s, (tok, margin) in zip(batch, serve_steps(batch, toks)):
+                i = sessions.index(s)
+                assert margin == 0
+                nxt[i] = tok
+                got[i].append(tok)
+    # Each session has stepped its prompt and G fed-back choices, as the decode did.
+    for i, s in enumerate(sessions):
+        np.testing.assert_array_equal(np.array(got[i], np.uint32), want["reply"][i])
+        st = s.save_state()
+        np.testing.assert_array_equal(np.concatenate([l.state for l in st.layers]), want["state"][i])
+        np.testing.assert_array_equal(np.concatenate([l.history for l in st.layers]), want["history"][i])
+        assert st.position == want["position"][i] == P + G
+        assert st.tokens == [int(t) for t in prompts[i]] + [int(t) for t in want["reply"][i, :G]]
+
+
+def test_step_native_matches_the_oracle(art):
+    tokens = synth.uniform_prompts(SPEC.vocab, 2, 14, 79)
+    st, want_tok, want_kept, want_query = oracle.sequences(art, tokens, threads=2)
+    assert st == 0
+    print("step_native against the oracle", flush=True)
+    pool = SessionPool(hip.Model(art), capacity=3)
+    for r in range(2):
+        s = Session(pool)
+        for t in range(tokens.shape[1]):
+            nat = s.step_native(int(tokens[r, t]))
+            assert nat.token == want_tok[r, t] == s.last_native_token()
+            np.testing.assert_array_equal(nat.kept_cells, want_kept[r, t])
+            np.testing.assert_array_equal(nat.query_q12, want_query[r, t])
+        # A feed of the same row in one launch ends in the same state and choice.
+        s2 = Session(pool)
+        assert s2.feed(tokens[r]).token == want_tok[r, -1]
+        a, b = s.save_state(), s2.save_state()
+        assert a.layers == b.layers and a.tokens == b.tokens and a.position == b.position
+        s.close(), s2.close()
+
+
+def test_save_restore_continues_bit_for_bit(art, tmp_path):
+    prompts = synth.uniform_prompts(SPEC.vocab, 1, 9, 83)[0]
+    print("save/restore", flush=True)
+    model = hip.Model(art)
+    pool = SessionPool(model, capacity=4)
+    a = Session(pool)
+    tok = a.feed(prompts).token
+    for _ in range(5):
+        tok, _ = a.serve_step(tok)
+    snap = a.save_state()
+    assert snap.position == len(prompts) + 5 and snap.cache_at == snap.position * SPEC.width
+    assert len(snap.logits) == SPEC.vocab and not any(snap.logits)
+    wire = session_codec.encode(snap)
+    assert wire[:8] == b"UR4SESS1"
+    path = tmp_path / "sess" / "a.json"
+    a.save_session_to_file(path)
+    cont = []
+    t = tok
+    for _ in range(12):
+        t, _ = a.serve_step(t)
+        cont.append(t)
+    for how in ("codec", "json", "same-slot"):
+        b = a if how == "same-slot" else Session(pool)
+        if how == "codec":
+            b.restore_state(session_codec.decode(wire))
+        elif how == "json":
+            b.restore_session_from_file(path)
+        else:
+            b.restore_state(snap)
+        assert b.position == snap.position
+        t, again = tok, []
+        for _ in range(12):
+            t, _ = b.serve_step(t)
+            again.append(t)
+        assert again == cont, how
+        if b is not a:
+            b.close()
+
+
+def test_reset_and_refusals_leave_state(art):
+    print("reset and refusals", flush=True)
+    pool = SessionPool(hip.Model(art), capacity=2)
+    s = Session(pool)
+    first = s.feed([1, 2, 3]).token
+    before = s.save_state()
+    with pytest.raises(SessionError) as e:
+        s.step_native(SPEC.vocab)
+    assert e.value.kind == "Token" and s.save_state() == before
+    # A feed stops at the refused token, the tokens before it stepped.
+    with pytest.raises(SessionError):
+        s.feed([4, 5, SPEC.vocab + 7, 6])
+    assert s.position == 5 and s.tokens == [1, 2, 3, 4, 5]
+    s.reset()
+    assert s.position == 0 and s.last_native_token() is None
+    assert s.feed([1, 2, 3]).token == first
+    # The context: exactly `context` tokens step, the next is refused.
+    s.reset()
+    s.feed(list(range(1, SPEC.context)))
+    s.serve_step(1)
+    with pytest.raises(SessionError) as e:
+        s.serve_step(1)
+    assert e.value.kind == "ContextFull" and s.position == SPEC.context
+    # Restores check the serving identity.
+    other = SessionPool(hip.Model(synth.make_artifact(SPEC, SEED + 1)), capacity=1)
+    with pytest.raises(SessionError) as e:
+        Session(other).restore_state(before)
+    assert e.value.kind == "Numerics"
+
+
+def test_nearest_head_read_step_chooses_nothing():
+    spec = replace(synth.NON_SQUARE, head=1, context=12)
+    art = synth.make_artifact(spec, 89)
+    print("nearest head read_step", flush=True)
+    pool = SessionPool(hip.Model(art), capacity=2)
+    a, b = Session(pool), Session(pool)
+    a.read_step(3)
+    assert a.last_native_token() is None and a._native.token == NO_CHOICE
+    b.step_native(3)
+    assert b.last_native_token() is not None
+    assert a.save_state().layers == b.save_state().layers
+
+
+def test_slot_bounds_are_checked_by_the_kernel(art):
+    """A slot at or past the capacity gets status 3 and touches nothing; the others step."""
+    print("slot bounds", flush=True)
+    model = hip.Model(art)
+    pool = SessionPool(model, capacity=2)
+    arr = lambda a: DeviceArray(len(a), np.uint32)  # noqa: E731
+    slots, toks = arr([1, 2, 0]), arr([5, 5, 5])
+    slots.upload(np.array([1, 2, 0], np.uint32))
+    toks.upload(np.array([5, 5, 5], np.uint32))
+    reply, status = DeviceArray(3, np.uint32), DeviceArray(3, np.int32)
+    hip._check(hip.lib().uor_fbs_decode_slots_async(
+        model.handle, slots.ptr, 3, 2, toks.ptr, 1, 0, reply.ptr, pool.state.ptr, pool.history.ptr,
+        pool.position.ptr, None, None, status.ptr, None))
+    assert status.download().tolist() == [0, 3, 0]
+    assert pool.position.download().tolist() == [1, 1]
+    r = reply.download()
+    assert r[0] == r[2]

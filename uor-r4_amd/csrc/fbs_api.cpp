@@ -438,6 +438,7 @@ namespace {
 
 int launch(uor_fbs_handle *h, RunArgs &A, hipStream_t stream) {
   if (A.n == 0) return 0;
+  if (!A.slots) A.capacity = A.n;
   uint32_t grid = A.n < h->max_grid ? A.n : h->max_grid;
   int st = h->ensure_ring(grid);
   if (st) return st;
@@ -490,7 +491,7 @@ int copy_out(T *dst, const T *src, size_t count) {
 
 int first_status(const std::vector<int32_t> &status) {
   for (int32_t s : status)
-    if (s) return fail(s, "a sequence failed with status %d (1 token, 2 context)", s);
+    if (s) return fail(s, "a sequence failed with status %d (1 token, 2 context, 3 slot)", s);
   return 0;
 }
 
@@ -570,6 +571,37 @@ extern "C" int uor_fbs_decode_async(uor_fbs_handle *h, const uint32_t *prompts, 
   A.out_state = out_state;
   A.out_history = out_history;
   A.out_position = out_position;
+  A.status = status;
+  return launch(h, A, (hipStream_t)stream);
+}
+
+extern "C" int uor_fbs_decode_slots_async(uor_fbs_handle *h, const uint32_t *slots,
+                                          uint32_t sequences, uint32_t capacity,
+                                          const uint32_t *prompts, uint32_t prompt_len,
+                                          uint32_t gen, uint32_t *out_reply, int64_t *state,
+                                          int32_t *history, uint32_t *position, uint32_t *out_kept,
+                                          int32_t *out_query, int32_t *status, void *stream) {
+  if (!h || !slots || !prompts || !out_reply || !state || !history || !position || !status)
+    return fail(UOR_FBS_ERR_ARGUMENT, "null argument");
+  if (prompt_len == 0) return fail(UOR_FBS_ERR_ARGUMENT, "a step needs at least one token");
+  DeviceScope scope(h->device);
+  RunArgs A{};
+  A.mode = kModeDecode;
+  A.n = sequences;
+  A.len = prompt_len;
+  A.gen = gen;
+  A.tokens = prompts;
+  A.out_tokens = out_reply;
+  A.in_state = state;
+  A.in_history = history;
+  A.in_position = position;
+  A.out_state = state;
+  A.out_history = history;
+  A.out_position = position;
+  A.out_kept = out_kept;
+  A.out_query = out_query;
+  A.slots = slots;
+  A.capacity = capacity;
   A.status = status;
   return launch(h, A, (hipStream_t)stream);
 }

@@ -82,6 +82,10 @@ inline size_t pair_lds_bytes(const DevModel &M) {
 
 enum RunMode : uint32_t { kModeSequences = 0, kModeDecode = 1, kModeScore = 2 };
 
+// Per-sequence status: 0, or the reference's codes (1 token, 2 context), or a slot past the
+// slot arrays' capacity.
+constexpr int32_t kStatusSlot = 3;
+
 struct RunArgs {
   uint32_t mode;
   uint32_t n;          // sequences / rows
@@ -99,6 +103,11 @@ struct RunArgs {
   uint32_t *out_position;
   unsigned long long *matches;
   int32_t *status;        // n
+  // Session slots: sequence s keeps its state, history and position at index slots[s] of the
+  // in/out arrays (which may be the same arrays, updated in place); null = index s. A slot at
+  // or past `capacity` is refused with status kStatusSlot.
+  const uint32_t *slots;
+  uint32_t capacity;
   int32_t *ring;          // gridDim.x * L * W * d
   int64_t *hist;          // paired blocks: gridDim.x * L * d, the next step's window sums
 };

@@ -1490,9 +1490,14 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
     qv[k] = qi[k] < M.nq;
   }
   for (uint32_t s = blockIdx.x; s < A.n; s += gridDim.x) {
+    const uint32_t sl = A.slots ? A.slots[s] : s;  // the session's index in the state arrays
+    if (sl >= A.capacity) {
+      if (writes_out) A.status[s] = kStatusSlot;
+      continue;
+    }
     // Fresh or resumed session: state, window rows (row r = the drive r + 1 positions back)
     // and position (LayerState::Recurrence, session.rs:1850).
-    uint32_t pos = A.in_position ? A.in_position[s] : 0u;
+    uint32_t pos = A.in_position ? A.in_position[sl] : 0u;
     uint32_t base = pos % W;
     for (uint32_t l = 0; l < L; l++)
 #pragma unroll
@@ -1503,12 +1508,12 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
 #pragma unroll
             for (int c = 0; c < 4; c++)
               S.st[(uint64_t)l * d + ch + c] =
-                  A.in_state ? A.in_state[((uint64_t)s * L + l) * d + ch + c] : 0;
+                  A.in_state ? A.in_state[((uint64_t)sl * L + l) * d + ch + c] : 0;
           if (keeps_ring)
             for (uint32_t r = 0; r < W; r++) {
               uint32_t slot = (base + 2 * W - 1 - r) % W;
               int4 h = make_int4(0, 0, 0, 0);
-              if (A.in_history) h = *(const int4 *)(A.in_history + (((uint64_t)s * L + l) * W + r) * d + ch);
+              if (A.in_history) h = *(const int4 *)(A.in_history + (((uint64_t)sl * L + l) * W + r) * d + ch);
               *(int4 *)(ring + ((uint64_t)l * W + slot) * d + ch) = h;
             }
         }
@@ -1534,8 +1539,16 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
       const uint64_t at = (uint64_t)s * A.len + t;
       const bool seq = !decode && A.mode == kModeSequences;
       const bool want = decode ? t + 1 >= A.len : (seq || A.out_tokens || t + 1 < A.len);
-      uint32_t *kept_out = seq && A.out_kept ? A.out_kept + at * M.P : nullptr;
-      int32_t *query_out = seq && A.out_query ? A.out_query + at * d : nullptr;
+      // Sequences: every position's kept drawers and query; decode: the last step's.
+      const bool last = decode && t + 1 == steps;
+      uint32_t *kept_out = !A.out_kept ? nullptr
+                           : seq       ? A.out_kept + at * M.P
+                           : last      ? A.out_kept + (uint64_t)s * M.P
+                                       : nullptr;
+      int32_t *query_out = !A.out_query ? nullptr
+                           : seq        ? A.out_query + at * d
+                           : last       ? A.out_query + (uint64_t)s * d
+                                        : nullptr;
       if (NW == 1) {
         status = step<Q, SW>(M, S, ring, base, lane, qv, qi, tok, want, &chosen, kept_out, query_out);
       } else {
@@ -1575,15 +1588,15 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
             if (A.out_state && keeps_state)
 #pragma unroll
               for (int c = 0; c < 4; c++)
-                A.out_state[((uint64_t)s * L + l) * d + ch + c] = S.st[(uint64_t)l * d + ch + c];
+                A.out_state[((uint64_t)sl * L + l) * d + ch + c] = S.st[(uint64_t)l * d + ch + c];
             if (A.out_history && keeps_ring)
               for (uint32_t r = 0; r < W; r++) {
                 uint32_t slot = (base + 2 * W - 1 - r) % W;
-                *(int4 *)(A.out_history + (((uint64_t)s * L + l) * W + r) * d + ch) =
+                *(int4 *)(A.out_history + (((uint64_t)sl * L + l) * W + r) * d + ch) =
                     *(const int4 *)(ring + ((uint64_t)l * W + slot) * d + ch);
               }
           }
-      if (A.out_position && writes_out) A.out_position[s] = pos;
+      if (A.out_position && writes_out) A.out_position[sl] = pos;
     }
     if (writes_out) A.status[s] = status;
     if (NW == 2)

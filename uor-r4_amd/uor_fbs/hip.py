@@ -29,6 +29,7 @@ SYMBOLS = (
     "uor_fbs_last_error", "uor_fbs_model_create", "uor_fbs_model_destroy", "uor_fbs_state_words",
     "uor_fbs_history_words", "uor_fbs_sequences", "uor_fbs_sequences_async", "uor_fbs_decode",
     "uor_fbs_decode_async", "uor_fbs_score", "uor_fbs_score_async", "uor_fbs_block_waves",
+    "uor_fbs_decode_slots_async",
 )
 
 
@@ -64,6 +65,8 @@ def lib():
         L.uor_fbs_decode.argtypes = [P, P, C.c_uint32, C.c_uint32, C.c_uint32, P, P, P, P, P, P, P]
         L.uor_fbs_decode_async.argtypes = [P, P, C.c_uint32, C.c_uint32, C.c_uint32, P, P, P, P, P,
                                            P, P, P, P]
+        L.uor_fbs_decode_slots_async.argtypes = [P, P, C.c_uint32, C.c_uint32, P, C.c_uint32,
+                                                 C.c_uint32, P, P, P, P, P, P, P, P]
         L.uor_fbs_score.argtypes = [P, P, C.c_uint64, C.c_uint32, P, P]
         L.uor_fbs_score_async.argtypes = [P, P, C.c_uint64, C.c_uint32, P, P, P, P]
         _lib = L
@@ -89,6 +92,7 @@ class Model:
         ext = C.byref(self.image.ext) if self.image.ext is not None else None
         _check(lib().uor_fbs_model_create(C.byref(self.image.model), ext, device, C.byref(h)))
         self.handle = h
+        self.device = device
         s = art.spec
         self.width, self.layers, self.window = s.width, s.layers, s.window
         self.probes = art.probes

@@ -1,0 +1,405 @@
+"""Serving sessions on the GPU: IntegerStackSession's serving surface for FBS models
+(stack/session.rs:2703-3440: reset, step, step_native, read_step, serve_step, save_state,
+restore_state, save_session_to_file, restore_session_from_file) over a pool of session slots
+held in device memory.
+
+A `SessionPool` owns, per slot, one session's recurrence state, window history and position
+in HBM; `uor_fbs_decode_slots_async` steps any set of slots in one launch and updates them in
+place, so a serving loop batches whichever sessions have a token ready (`serve_steps`)
+without moving state through the host. `Session` is one sequence in a slot with the
+reference's per-call semantics; its snapshots are the reference's `SerializedStackSession`,
+encodable as `UR4SESS1` bytes or the JSON of `save_session_to_file` (`session_codec`).
+
+What the GPU path does not keep (and so refuses to restore, rather than continuing
+differently): snap traces (opt-in diagnostics of snapped transports) and read-layer caches
+(the FBS trunk has none).
+"""
+
+from __future__ import annotations
+
+import hashlib
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import hip
+from .hipmem import DeviceArray
+from .session_codec import (STACK_SESSION_SCHEMA, CodecError, RecurrenceLayer, SerializedStackSession,
+                            from_json, to_json)
+
+NO_CHOICE = 0xFFFFFFFF  # session.rs:4406: a nearest-head read step chose no token
+
+
+class SessionError(ValueError):
+    """A refusal of the reference's session API; `kind` names its `StackError` variant
+    (Schema, Numerics, ContentReadout, ContextFull, SessionState, Token, Shape)."""
+
+    def __init__(self, kind: str, message: str):
+        super().__init__(f"{kind}: {message}")
+        self.kind = kind
+
+
+@dataclass
+class NativeStep:
+    """`NativeStep` (session.rs:484-493): the writer's token, kept drawers and Q12 query."""
+    token: int
+    kept_cells: np.ndarray
+    query_q12: np.ndarray
+
+
+def model_identity(art) -> str:
+    """The session's serving identity: the artifact container's SHA-256 (format.rs:1493,
+    session.rs:1049); a generated artifact has no container, so its identity is the SHA-256 of
+    this build's tag, its spec and its seed."""
+    if art.sha256:
+        return art.sha256
+    tag = f"uor-fbs-synthetic/1\0{art.spec!r}\0{art.seed}".encode()
+    return hashlib.sha256(tag).hexdigest()
+
+
+@dataclass(frozen=True)
+class ModelInfo:
+    """What restore_state checks a snapshot against."""
+    sha256: str
+    vocab: int
+    width: int
+    layers: int
+    window: int
+    context: int
+    heads: int = 1       # every served FBS shape has one head (format.rs:616-752)
+    snapped: bool = False
+
+    @staticmethod
+    def of(art) -> "ModelInfo":
+        s = art.spec
+        return ModelInfo(model_identity(art), s.vocab, s.width, s.layers, s.window, s.context,
+                         1, not s.raw_transition)
+
+    @property
+    def state_words(self) -> int:
+        return self.layers * self.width
+
+    @property
+    def history_words(self) -> int:
+        return self.layers * self.window * self.width
+
+
+def max_serialized_session_bytes(info: ModelInfo) -> int:
+    """The JSON size bound restore_session_from_file enforces (session.rs:2281-2345), for the FBS
+    trunk: every layer a recurrence, no pointer or Hamming payloads; 24 bytes per number."""
+    layer_bytes = info.layers * (info.window + 1) * info.width * 24
+    logits_bytes = info.vocab * 24
+    tokens_bytes = info.context * 24
+    trace_bytes = info.context * (info.width // 4) * info.layers * 24 if info.snapped else 0
+    return layer_bytes + logits_bytes + tokens_bytes + trace_bytes + 131072
+
+
+def validate_restore(info: ModelInfo, saved: SerializedStackSession) -> None:
+    """restore_state's checks (session.rs:2876-3090) for an FBS model, in the reference's order;
+    raises SessionError and changes nothing."""
+    if saved.schema != STACK_SESSION_SCHEMA:
+        raise SessionError("Schema", f"expected {STACK_SESSION_SCHEMA}, found {saved.schema}")
+    if saved.version != 1:
+        raise SessionError("Schema", f"unsupported session version {saved.version}")
+    if saved.artifact_sha256 != info.sha256:
+        raise SessionError("Numerics", f"session serving identity mismatch: session has "
+                                       f"'{saved.artifact_sha256}', model has '{info.sha256}'")
+    if saved.content_readout_sha256 is not None:
+        raise SessionError("ContentReadout", "session content-readout identity differs from the attached sidecar")
+    pos = saved.position
+    if pos > info.context:
+        raise SessionError("ContextFull", f"context {info.context}")
+    if saved.cache_at != pos * info.width or saved.lift_at != pos * info.heads:
+        raise SessionError("SessionState", "cache_at/lift_at do not match the position")
+    if len(saved.layers) != info.layers:
+        raise SessionError("SessionState", f"{len(saved.layers)} layers, the model has {info.layers}")
+    if (pos == 0 and saved.logits) or (pos > 0 and len(saved.logits) != info.vocab):
+        raise SessionError("SessionState", "pending logits of the wrong length")
+    if len(saved.tokens) != pos:
+        raise SessionError("SessionState", "the ingested tokens do not match the position")
+    if saved.pointer_keys or saved.pointer_lifts or saved.mixture:
+        raise SessionError("SessionState", "pointer state for a model without a pointer head")
+    for t in saved.tokens:
+        if not 0 <= t < info.vocab:
+            raise SessionError("Token", f"token {t} outside vocab {info.vocab}")
+    if saved.snap_trace is not None:
+        if not info.snapped:
+            if saved.snap_trace:
+                raise SessionError("SessionState", "a snap trace for a model without snapped transport")
+        else:
+            want = pos * (info.width // 4) * info.layers
+            if len(saved.snap_trace) != want or any(not 0 <= r < 120 for r in saved.snap_trace):
+                raise SessionError("SessionState", "a snap trace of the wrong length or roots")
+            if saved.snap_trace:
+                raise SessionError("Shape", "the GPU path does not record snap traces, so a traced "
+                                            "session cannot continue its trace")
+    for layer in saved.layers:
+        if not isinstance(layer, RecurrenceLayer):
+            raise SessionError("SessionState", "a read layer's cache for a recurrence layer")
+        if len(layer.state) != info.width or len(layer.history) != info.window * info.width:
+            raise SessionError("SessionState", "a layer of the wrong width or window")
+
+
+class SessionPool:
+    """`capacity` session slots of one model in device memory, stepped together."""
+
+    def __init__(self, model: "hip.Model", capacity: int):
+        if capacity <= 0:
+            raise ValueError("a pool needs at least one slot")
+        self.model = model
+        self.info = ModelInfo.of(model.art)
+        self.capacity = capacity
+        dev = model.device
+        self.state = DeviceArray((capacity, model.state_words), np.int64, dev)
+        self.history = DeviceArray((capacity, model.history_words), np.int32, dev)
+        self.position = DeviceArray(capacity, np.uint32, dev)
+        self._free = list(range(capacity - 1, -1, -1))
+
+    def acquire(self) -> int:
+        if not self._free:
+            raise SessionError("Shape", f"all {self.capacity} session slots are in use")
+        slot = self._free.pop()
+        self.clear([slot])
+        return slot
+
+    def release(self, slot: int):
+        if slot in self._free or not 0 <= slot < self.capacity:
+            raise ValueError(f"slot {slot} is not held")
+        self._free.append(slot)
+
+    def clear(self, slots):
+        """A fresh session in each slot (reset, session.rs:2703-2760)."""
+        slots = list(slots)
+        for a in (self.state, self.history, self.position):
+            a.zero(slots)
+
+    def read(self, slot: int):
+        """(state [L*d] i64, history [L*W*d] i32, position) of one slot."""
+        pos = self.position.download()[slot]
+        return self.state.download(slot), self.history.download(slot), int(pos)
+
+    def write(self, slot: int, state, history, position: int):
+        self.state.upload(state, slot)
+        self.history.upload(history, slot)
+        p = self.position.download()
+        p[slot] = position
+        self.position.upload(p)
+
+    def run(self, slots, tokens, gen: int = 0, native: bool = False):
+        """One launch: the sessions in `slots` take tokens [n, len] and `gen` greedy steps.
+        Returns dict(reply [n, gen+1], status [n], kept [n, P], query [n, d]) (kept and query
+        when `native`)."""
+        slots = np.asarray(slots, dtype=np.uint32).reshape(-1)
+        tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+        n = len(slots)
+        if tokens.ndim != 2 or tokens.shape[0] != n or tokens.shape[1] == 0:
+            raise ValueError("tokens must be [sessions, len >= 1]")
+        if len(set(slots.tolist())) != n:
+            raise ValueError("a slot appears twice in one step")
+        if np.any(slots >= self.capacity):
+            raise ValueError("a slot outside the pool")
+        dev = self.model.device
+        d_slots, d_tok = DeviceArray(n, np.uint32, dev), DeviceArray(tokens.size, np.uint32, dev)
+        d_slots.upload(slots)
+        d_tok.upload(tokens.reshape(-1))
+        reply = DeviceArray((n, gen + 1), np.uint32, dev)
+        status = DeviceArray(n, np.int32, dev)
+        kept = DeviceArray((n, self.model.probes), np.uint32, dev) if native else None
+        query = DeviceArray((n, self.model.width), np.int32, dev) if native else None
+        ptr = lambda x: None if x is None else x.ptr  # noqa: E731
+        # The null stream: the runtime's blocking copies below wait for the launch.
+        hip._check(hip.lib().uor_fbs_decode_slots_async(
+            self.model.handle, d_slots.ptr, n, self.capacity, d_tok.ptr, tokens.shape[1], gen,
+            reply.ptr, self.state.ptr, self.history.ptr, self.position.ptr, ptr(kept), ptr(query),
+            status.ptr, None))
+        out = dict(reply=reply.download(), status=status.download())
+        if native:
+            out["kept"] = kept.download()
+            out["query"] = query.download()
+        return out
+
+
+_STATUS = {1: ("Token", "a token lies outside the vocabulary"),
+           2: ("ContextFull", "the session is at its context"),
+           3: ("Shape", "a slot outside the pool")}
+
+
+class Session:
+    """One sequence in a pool slot, with IntegerStackSession's serving calls."""
+
+    def __init__(self, pool: SessionPool, slot: int | None = None):
+        self.pool = pool
+        self.info = pool.info
+        self.slot = pool.acquire() if slot is None else slot
+        self._reset_host()
+
+    def _reset_host(self):
+        self.position = 0
+        self.tokens: list[int] = []
+        self.logits: list[int] | None = None   # pending logits from a restore; zeros otherwise
+        self.hamming_payloads: list = []
+        self._native: NativeStep | None = None
+
+    def close(self):
+        if self.slot is not None:
+            self.pool.release(self.slot)
+            self.slot = None
+
+    def reset(self):
+        """Start a new stream (session.rs:2703-2760)."""
+        self.pool.clear([self.slot])
+        self._reset_host()
+
+    # ---- stepping ----
+    def _admit(self, tokens) -> list[int]:
+        """The prefix of `tokens` the reference would step before refusing one (a token outside
+        the vocabulary, or the context full), and the refusal, if any."""
+        ok = []
+        for tok in tokens:
+            if not 0 <= tok < self.info.vocab:
+                return ok, SessionError("Token", f"token {tok} outside vocab {self.info.vocab}")
+            if self.position + len(ok) >= self.info.context:
+                return ok, SessionError("ContextFull", f"context {self.info.context}")
+            ok.append(int(tok))
+        return ok, None
+
+    def _after(self, fed: list[int], reply, kept, query):
+        self.position += len(fed)
+        self.tokens.extend(fed)
+        self._native = NativeStep(int(reply[-1]), kept, query)
+
+    def feed(self, tokens) -> NativeStep:
+        """The prompt tokens in one launch: read_step for all but the last, then step_native on
+        the last. A refused token stops the feed there, with the tokens before it stepped."""
+        ok, err = self._admit(list(tokens))
+        if ok:
+            out = self.pool.run([self.slot], np.asarray([ok], np.uint32), native=True)
+            st = int(out["status"][0])
+            if st:
+                raise SessionError(*_STATUS.get(st, ("Shape", f"status {st}")))
+            self._after(ok, out["reply"][0], out["kept"][0], out["query"][0])
+        if err:
+            raise err
+        return self._native
+
+    def step_native(self, token: int) -> NativeStep:
+        """Feed one token and return the native writer's choice (session.rs:3356-3371)."""
+        return self.feed([token])
+
+    def step(self, token: int) -> np.ndarray:
+        """Feed one token; an FBS step returns no logits, an empty slice (session.rs:3320-3330)."""
+        self.feed([token])
+        return np.zeros(0, np.int32)
+
+    def read_step(self, token: int) -> None:
+        """A token whose successor the caller holds (session.rs:3392-3397): the state as step
+        leaves it; under the nearest head no token is chosen."""
+        self.feed([token])
+        if self.pool.model.art.spec.head == 1:
+            self._native = NativeStep(NO_CHOICE, self._native.kept_cells, self._native.query_q12)
+
+    def serve_step(self, token: int) -> tuple[int, int]:
+        """The served greedy next token and margin (session.rs:3405-3425): an FBS model's native
+        token, margin 0."""
+        return self.feed([token]).token, 0
+
+    def last_native_token(self) -> int | None:
+        """session.rs:3373-3380: None before any step and after a nearest-head read step."""
+        if self._native is None or self._native.token == NO_CHOICE:
+            return None
+        return self._native.token
+
+    def last_query_q12(self) -> np.ndarray | None:
+        return None if self._native is None else self._native.query_q12
+
+    # ---- snapshots ----
+    def save_state(self) -> SerializedStackSession:
+        """session.rs:2777-2870 for an FBS session: every layer a recurrence."""
+        state, hist, pos = self.pool.read(self.slot)
+        assert pos == self.position, (pos, self.position)
+        i, d, w = self.info, self.info.width, self.info.window
+        layers = [RecurrenceLayer(state[l * d:(l + 1) * d].tolist(),
+                                  hist[l * w * d:(l + 1) * w * d].tolist()) for l in range(i.layers)]
+        logits = [] if pos == 0 else (list(self.logits) if self.logits is not None else [0] * i.vocab)
+        return SerializedStackSession(STACK_SESSION_SCHEMA, 1, i.sha256, pos, pos * d, pos * i.heads,
+                                      0, logits, list(self.tokens), list(self.hamming_payloads),
+                                      None, [], [], [], None, layers)
+
+    def restore_state(self, saved: SerializedStackSession) -> None:
+        """session.rs:2876-3190: validate everything, then replace the slot's state."""
+        validate_restore(self.info, saved)
+        state = np.concatenate([np.asarray(l.state, np.int64) for l in saved.layers])
+        hist = np.concatenate([np.asarray(l.history, np.int64).astype(np.int32) for l in saved.layers])
+        self.pool.write(self.slot, state, hist, saved.position)
+        self.position = saved.position
+        self.tokens = list(saved.tokens)
+        self.logits = list(saved.logits) if saved.position > 0 else None
+        self.hamming_payloads = [list(p) for p in saved.hamming_payloads]
+        self._native = None
+
+    def save_session_to_file(self, path) -> None:
+        """JSON to `path`, atomically and durably (session.rs:3202-3262): an exclusive temporary
+        sibling, flushed and synced, renamed over `path`, then the directory synced."""
+        data = to_json(self.save_state())
+        path = os.fspath(path)
+        parent = os.path.dirname(path) or "."
+        os.makedirs(parent, exist_ok=True)
+        tmp = os.path.join(parent, f".{os.path.basename(path) or 'session'}.tmp-{os.getpid()}-{id(data)}")
+        fd = os.open(tmp, os.O_WRONLY | os.O_CREAT | os.O_EXCL, 0o644)
+        try:
+            with os.fdopen(fd, "wb") as f:
+                f.write(data)
+                f.flush()
+                os.fsync(f.fileno())
+            os.replace(tmp, path)
+        except BaseException:
+            if os.path.exists(tmp):
+                os.remove(tmp)
+            raise
+        dfd = os.open(parent, os.O_RDONLY)
+        try:
+            os.fsync(dfd)
+        finally:
+            os.close(dfd)
+
+    def restore_session_from_file(self, path) -> None:
+        """session.rs:3264-3290: bounded by max_serialized_session_bytes before reading."""
+        bound = max_serialized_session_bytes(self.info)
+        if os.path.getsize(path) > bound:
+            raise SessionError("Numerics", f"session file size {os.path.getsize(path)} exceeds "
+                                           f"maximum expected bound {bound}")
+        with open(path, "rb") as f:
+            data = f.read(bound + 1)
+        if len(data) > bound:
+            raise SessionError("Numerics", f"session file size exceeds maximum expected bound {bound}")
+        try:
+            saved = from_json(data)
+        except CodecError as e:
+            raise SessionError("Numerics", str(e)) from None
+        self.restore_state(saved)
+
+
+def serve_steps(sessions: list[Session], tokens: list[int]) -> list[tuple[int, int]]:
+    """serve_step for many sessions of one pool in one launch: the serving loop's batch. A
+    session whose token is refused raises after the others have stepped."""
+    if not sessions:
+        return []
+    pool = sessions[0].pool
+    if any(s.pool is not pool for s in sessions):
+        raise ValueError("sessions of one pool")
+    go, errs = [], []
+    for s, tok in zip(sessions, tokens):
+        ok, err = s._admit([tok])
+        (go.append((s, ok)) if ok else errs.append(err))
+    if go:
+        out = pool.run([s.slot for s, _ in go], np.asarray([ok for _, ok in go], np.uint32), native=True)
+        for i, (s, ok) in enumerate(go):
+            st = int(out["status"][i])
+            if st:
+                errs.append(SessionError(*_STATUS.get(st, ("Shape", f"status {st}"))))
+                continue
+            s._after(ok, out["reply"][i], out["kept"][i], out["query"][i])
+    if errs:
+        raise errs[0]
+    return [(s._native.token, 0) for s in sessions]

@@ -146,6 +146,9 @@ class Artifact:
     drawer_keys: np.ndarray | None = None
     drawer_offsets: np.ndarray | None = None
     drawer_members: np.ndarray | None = None
+    # SHA-256 (hex) of the container bytes a served artifact was read from (format.rs:1493);
+    # None for a generated one.
+    sha256: str | None = None
 
     @property
     def window(self) -> int:

@@ -25,6 +25,7 @@ executes nothing from the file.
 
 from __future__ import annotations
 
+import hashlib
 import json
 import struct
 
@@ -173,4 +174,5 @@ def load(source) -> Artifact:
                 raw_gates=bool(s.get("raw_gates")), raw_transition=bool(s.get("raw_transition")))
     return Artifact(spec=spec, seed=-1, layers=layers, final_gain=codes("final_norm_gain", d),
                     writer_table=table("writer.table", "i16", V * d).astype(np.int16),
-                    table_i8=None, eps_mantissa=int(eps["mantissa"]), eps_exp=int(eps["exp"]))
+                    table_i8=None, eps_mantissa=int(eps["mantissa"]), eps_exp=int(eps["exp"]),
+                    sha256=hashlib.sha256(data).hexdigest())
