@@ -54,6 +54,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=24.0, help="target CPU-baseline sample time")
     p.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cores)")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--serve-steps", type=int, default=64,
+                   help="serving-loop launches after the decode (0: none); reported beside the metric")
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="only run one elementwise copy kernel over this many MiB (the reference "
                         "reading for the FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -246,6 +248,54 @@ def main():
         },
         "prefill_tokens_per_s": round(B * a.prompt / prefill_s, 1),
     }
+
+    if a.serve_steps:
+        # The serving loop: every sequence is a session in a device slot (a fixed permutation of
+        # the slots), and each launch steps all of them by one token from their slot state,
+        # updated in place (uor_fbs_decode_slots_async, serve_step for the whole batch). From
+        # the same prefilled state, its tokens must equal the decode's replies.
+        K = min(a.serve_steps, G)
+        perm = np.random.default_rng(a.seed).permutation(B).astype(np.uint32)
+        d_slots = u32(perm)
+        s_state, s_hist, s_pos = (torch.empty_like(t) for t in (state, hist, pos))
+        s_state[d_slots.long()] = state  # sequence i lives in slot perm[i]
+        # A slot's history is its window ring: ring row (p - 1 - r) mod W holds history row r.
+        L_, W_, d_ = spec.layers, spec.window, spec.width
+        p0 = int(pos[0].item())
+        assert bool((pos == p0).all())
+        src = torch.from_numpy((p0 - 1 - np.arange(W_)) % W_)
+        ring_rows = torch.empty(W_, dtype=torch.int64)
+        ring_rows[src] = torch.arange(W_)
+        s_hist[d_slots.long()] = hist.view(B, L_, W_, d_)[:, :, ring_rows.to(dev)].reshape(B, -1)
+        s_pos[d_slots.long()] = pos
+        served = torch.zeros((K + 1, B), dtype=torch.int32, device=dev)
+        served[0] = first[:, 0]
+        sv_start = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
+        sv_end = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for k in range(K):
+            sv_start[k].record(stream)
+            check(L.uor_fbs_decode_slots_async(model.handle, ptr(d_slots), B, B, ptr(served[k]), 1, 0,
+                                               ptr(served[k + 1]), ptr(s_state), ptr(s_hist),
+                                               ptr(s_pos), None, None, ptr(status), sp))
+            sv_end[k].record(stream)
+        torch.cuda.synchronize()
+        serve_wall = time.perf_counter() - t0
+        assert int(status.abs().sum()) == 0, "serving loop failed"
+        serve_ms = [s_.elapsed_time(e_) for s_, e_ in zip(sv_start, sv_end)]
+        same_serve = np.array_equal(served[1:].cpu().numpy().view(np.uint32).T, host_reply[:, :K])
+        out["serving"] = {
+            "tokens_per_s": round(B * K / serve_wall, 1),
+            "ms_per_launch": round(float(np.mean(serve_ms)), 4),
+            "launches": K, "sessions": B,
+            "kernel": kernel.replace("fbs_decode", "fbs_prefill"),
+            "workload": f"{B} sessions in permuted device slots, one token each per launch, "
+                        f"{K} launches from the prefilled state",
+            "tokens_equal_decode": bool(same_serve),
+        }
+        if not same_serve:
+            print("bench.py: the serving loop's tokens differ from the decode's", file=sys.stderr)
 
     if not a.no_cpu:
         threads = a.cpu_threads or min(16, os.cpu_count() or 1)

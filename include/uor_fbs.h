@@ -163,7 +163,10 @@ int uor_fbs_decode_async(uor_fbs_handle *handle, const uint32_t *prompts, uint32
 
 /* Serving sessions held in caller-owned device arrays, one slot per session: `state`
  * [capacity][state_words] int64, `history` [capacity][history_words] int32 and `position`
- * [capacity] uint32, updated in place. Sequence i of the call is the session in slot
+ * [capacity] uint32, updated in place. A slot's history is its window ring, [layer][window]
+ * [width] with row p mod window holding the drive of position p (exported row r, the drive
+ * r + 1 positions back, is ring row (position - 1 - r) mod window), so no launch copies it.
+ * Sequence i of the call is the session in slot
  * slots[i] < capacity (distinct within a call); it takes prompts[i*prompt_len ..] from its
  * slot's state, then `gen` greedy steps, as uor_fbs_decode_async: out_reply gets gen+1 tokens
  * per sequence. The serving loop of IntegerStackSession for a batch of sessions:
@@ -171,8 +174,9 @@ int uor_fbs_decode_async(uor_fbs_handle *handle, const uint32_t *prompts, uint32
  * wasm_serve.rs:140-152) with prompt_len 1 and gen 0, read_step (session.rs:3392) for all
  * prompt tokens but the last, which one call folds into prompt_len. Optional out_kept [n][P]
  * and out_query [n][width] receive the last step's kept drawers and Q12 query (step_native's
- * NativeStep, session.rs:484-493). A sequence whose status is nonzero leaves its slot as it
- * was (status 3: slots[i] >= capacity, nothing read or written). Device buffers. */
+ * NativeStep, session.rs:484-493). A sequence refused with status 1 or 2 leaves its slot
+ * holding the tokens stepped before the refused one, as the reference's session after its
+ * error; status 3 (slots[i] >= capacity): nothing read or written. Device buffers. */
 int uor_fbs_decode_slots_async(uor_fbs_handle *handle, const uint32_t *slots, uint32_t sequences,
                                uint32_t capacity, const uint32_t *prompts, uint32_t prompt_len,
                                uint32_t gen, uint32_t *out_reply, int64_t *state,

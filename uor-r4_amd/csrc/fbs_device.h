@@ -103,9 +103,13 @@ struct RunArgs {
   uint32_t *out_position;
   unsigned long long *matches;
   int32_t *status;        // n
-  // Session slots: sequence s keeps its state, history and position at index slots[s] of the
-  // in/out arrays (which may be the same arrays, updated in place); null = index s. A slot at
-  // or past `capacity` is refused with status kStatusSlot.
+  // Session slots: sequence s keeps its state and position at index slots[s] of the in/out
+  // arrays (the same arrays, updated in place), and out_history's entry of that slot is the
+  // sequence's window ring itself ([layer][W][d], row p mod W holding the drive of position
+  // p), so nothing is copied between launches; null = index s, the rows exported newest first
+  // through the block's own ring. A slot at or past `capacity` is refused with status
+  // kStatusSlot. Slot sequences export their state and position also when a step is refused:
+  // the session then holds the tokens stepped before it.
   const uint32_t *slots;
   uint32_t capacity;
   int32_t *ring;          // gridDim.x * L * W * d

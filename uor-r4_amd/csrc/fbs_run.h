@@ -1480,7 +1480,7 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
   const bool keeps_state = NW == 1 || wave == 0, keeps_ring = NW == 1 || wave == 1;
   const bool writes_out = wave == 0 && lane == 0;
   const uint32_t d = M.d, L = M.L, W = M.W;
-  int32_t *ring = A.ring + (uint64_t)blockIdx.x * L * W * d;
+  int32_t *const block_ring = A.ring + (uint64_t)blockIdx.x * L * W * d;
   int64_t *hist = NW == 2 ? A.hist + (uint64_t)blockIdx.x * L * d : nullptr;
   bool qv[Q];
   uint32_t qi[Q];
@@ -1499,6 +1499,8 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
     // and position (LayerState::Recurrence, session.rs:1850).
     uint32_t pos = A.in_position ? A.in_position[sl] : 0u;
     uint32_t base = pos % W;
+    // A slot's history is its ring; otherwise the block's ring takes the rows.
+    int32_t *ring = A.slots ? A.out_history + (uint64_t)sl * L * W * d : block_ring;
     for (uint32_t l = 0; l < L; l++)
 #pragma unroll
       for (int k = 0; k < Q; k++)
@@ -1509,7 +1511,7 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
             for (int c = 0; c < 4; c++)
               S.st[(uint64_t)l * d + ch + c] =
                   A.in_state ? A.in_state[((uint64_t)sl * L + l) * d + ch + c] : 0;
-          if (keeps_ring)
+          if (keeps_ring && !A.slots)
             for (uint32_t r = 0; r < W; r++) {
               uint32_t slot = (base + 2 * W - 1 - r) % W;
               int4 h = make_int4(0, 0, 0, 0);
@@ -1579,7 +1581,7 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
       }
     }
     if (!decode && A.mode == kModeScore && writes_out && hits) atomicAdd(A.matches, hits);
-    if (decode && status == 0) {
+    if (decode && (status == 0 || A.slots)) {
       for (uint32_t l = 0; l < L; l++)
 #pragma unroll
         for (int k = 0; k < Q; k++)
@@ -1589,7 +1591,7 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
 #pragma unroll
               for (int c = 0; c < 4; c++)
                 A.out_state[((uint64_t)sl * L + l) * d + ch + c] = S.st[(uint64_t)l * d + ch + c];
-            if (A.out_history && keeps_ring)
+            if (A.out_history && keeps_ring && !A.slots)
               for (uint32_t r = 0; r < W; r++) {
                 uint32_t slot = (base + 2 * W - 1 - r) % W;
                 *(int4 *)(A.out_history + (((uint64_t)sl * L + l) * W + r) * d + ch) =

@@ -174,14 +174,26 @@ class SessionPool:
         for a in (self.state, self.history, self.position):
             a.zero(slots)
 
+    def _ring_rows(self, position: int) -> np.ndarray:
+        """Ring row holding history row r (the drive r + 1 positions back) at `position`."""
+        w = self.info.window
+        return (position - 1 - np.arange(w)) % w
+
     def read(self, slot: int):
-        """(state [L*d] i64, history [L*W*d] i32, position) of one slot."""
-        pos = self.position.download()[slot]
-        return self.state.download(slot), self.history.download(slot), int(pos)
+        """(state [L*d] i64, history [L*W*d] i32 newest row first, position) of one slot; the
+        device holds the history as the kernel's ring (row p mod W = the drive of position p)."""
+        pos = int(self.position.download()[slot])
+        i = self.info
+        ring = self.history.download(slot).reshape(i.layers, i.window, i.width)
+        return self.state.download(slot), ring[:, self._ring_rows(pos)].reshape(-1), pos
 
     def write(self, slot: int, state, history, position: int):
+        i = self.info
+        rows = np.asarray(history, np.int32).reshape(i.layers, i.window, i.width)
+        ring = np.empty_like(rows)
+        ring[:, self._ring_rows(position)] = rows
         self.state.upload(state, slot)
-        self.history.upload(history, slot)
+        self.history.upload(ring.reshape(-1), slot)
         p = self.position.download()
         p[slot] = position
         self.position.upload(p)
