@@ -126,10 +126,12 @@ void uor_fbs_model_destroy(uor_fbs_handle *handle);
 uint64_t uor_fbs_state_words(const uor_fbs_handle *handle);
 uint64_t uor_fbs_history_words(const uor_fbs_handle *handle);
 
-/* Wavefronts per sequence of the kernels a run of n sequences launches: 2 (paired blocks) when
- * the run leaves SIMDs without a second wave (n at most the device's SIMD count), else 1;
- * UOR_FBS_BLOCK_WAVES=1 or 2 in the environment at model creation fixes it. No counterpart in
- * the reference (its CPU decoder has no launch shape): for profilers and tests. */
+/* Wavefronts per sequence of the kernels a run of n sequences launches: 2 (paired blocks, at
+ * most one block per SIMD, each stepping its share of the sequences) unless
+ * UOR_FBS_BLOCK_WAVES=1 was set at model creation or the model's paired LDS does not fit, then
+ * 1 (one wavefront per sequence). The same for every n today; n is kept for a policy that
+ * depends on the batch. No counterpart in the reference (its CPU decoder has no launch shape):
+ * for profilers and tests. */
 uint32_t uor_fbs_block_waves(const uor_fbs_handle *handle, uint32_t n);
 
 /* Teacher-forced sequences from fresh sessions: every position's chosen token, kept drawers

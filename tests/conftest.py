@@ -22,8 +22,8 @@ def pytest_configure(config):
 @pytest.fixture(params=["one-wave", "paired"])
 def block_waves(request, monkeypatch):
     """Both kernel families: one wavefront per sequence, and paired blocks (two wavefronts per
-    sequence, the library's choice for launches of at most one sequence per SIMD). The library
-    reads UOR_FBS_BLOCK_WAVES when a model is created."""
+    sequence, the library's default). The library reads UOR_FBS_BLOCK_WAVES when a model is
+    created."""
     monkeypatch.setenv("UOR_FBS_BLOCK_WAVES", "1" if request.param == "one-wave" else "2")
     return request.param
 

@@ -93,8 +93,8 @@ def test_block_waves_follow_the_setting(block_waves, monkeypatch):
     art = synth.make_artifact(synth.SMALL, 1)
     assert Model(art).block_waves(64) == (2 if block_waves == "paired" else 1)
     monkeypatch.delenv("UOR_FBS_BLOCK_WAVES")
-    model = Model(art)  # the library's choice: paired blocks up to one sequence per SIMD
-    assert model.block_waves(1024) == 2 and model.block_waves(1 << 20) == 1
+    model = Model(art)  # the library's choice: paired blocks at every batch size
+    assert model.block_waves(1024) == 2 and model.block_waves(1 << 20) == 2
 
 
 def test_decode_matches_oracle_and_resumes():

@@ -63,10 +63,14 @@ struct uor_fbs_handle {
   std::vector<void *> allocs;
   size_t lds_bytes = 0;
   uint32_t max_grid = 0;
-  // Paired blocks (two wavefronts per sequence) run launches of at most pair_max sequences:
-  // one wave per SIMD would leave half of each SIMD's issue slots unused.
+  // Paired blocks (two wavefronts per sequence, two waves on every SIMD) run every launch unless
+  // the environment asks for one wave or their LDS does not fit; their grid is at most one
+  // block per SIMD, each block stepping its share of the batch's sequences in turn, so that
+  // every block is resident from the start and each SIMD keeps wave 0 of one block beside
+  // wave 1 of another.
+  bool pair = false;
   size_t pair_lds = 0;
-  uint32_t pair_max = 0;
+  uint32_t pair_grid = 0;
   int32_t *ring = nullptr;
   int64_t *hist = nullptr;
   size_t ring_blocks = 0;
@@ -411,14 +415,11 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
     return done(fail(UOR_FBS_ERR_UNSUPPORTED, "%zu bytes of LDS per sequence exceed %zu",
                      h->lds_bytes, (size_t)prop.sharedMemPerBlock));
   h->max_grid = (uint32_t)prop.multiProcessorCount * 8;
-  // UOR_FBS_BLOCK_WAVES=1 or 2 fixes the wavefronts per sequence (default: paired blocks for
-  // launches of at most one sequence per SIMD, four SIMDs per CU).
+  // UOR_FBS_BLOCK_WAVES=1 fixes one wavefront per sequence (default: paired blocks).
   const char *bw = getenv("UOR_FBS_BLOCK_WAVES");
-  const int waves = bw && bw[0] == '1' && !bw[1] ? 1 : bw && bw[0] == '2' && !bw[1] ? 2 : 0;
   h->pair_lds = fbs::pair_lds_bytes(M);
-  h->pair_max = waves == 1 || h->pair_lds > prop.sharedMemPerBlock ? 0
-                : waves == 2                                     ? UINT32_MAX
-                                                                 : (uint32_t)prop.multiProcessorCount * 4;
+  h->pair = !(bw && bw[0] == '1' && !bw[1]) && h->pair_lds <= prop.sharedMemPerBlock;
+  h->pair_grid = (uint32_t)prop.multiProcessorCount * 4;  // four SIMDs per CU
   return done(0);
 }
 
@@ -431,7 +432,8 @@ extern "C" uint64_t uor_fbs_history_words(const uor_fbs_handle *h) {
   return h ? (uint64_t)h->M.L * h->M.W * h->M.d : 0;
 }
 extern "C" uint32_t uor_fbs_block_waves(const uor_fbs_handle *h, uint32_t n) {
-  return h && n <= h->pair_max ? 2u : 1u;
+  (void)n;
+  return h && h->pair ? 2u : 1u;
 }
 
 namespace {
@@ -439,12 +441,14 @@ namespace {
 int launch(uor_fbs_handle *h, RunArgs &A, hipStream_t stream) {
   if (A.n == 0) return 0;
   if (!A.slots) A.capacity = A.n;
-  uint32_t grid = A.n < h->max_grid ? A.n : h->max_grid;
+  const bool pair = h->pair;
+  const uint32_t cap = pair ? h->pair_grid : h->max_grid;
+  const uint32_t grid = A.n < cap ? A.n : cap;
   int st = h->ensure_ring(grid);
   if (st) return st;
   A.ring = h->ring;
   A.hist = h->hist;
-  const bool decode = A.mode == kModeDecode, pair = A.n <= h->pair_max;
+  const bool decode = A.mode == kModeDecode;
   const uint32_t waves = pair ? 2 : 1;
   const size_t lds = pair ? h->pair_lds : h->lds_bytes;
   hipError_t e = decode && A.gen == 0 ? launch_fbs_prefill(h->M, A, grid, waves, lds, stream)
