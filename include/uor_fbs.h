@@ -196,6 +196,74 @@ int uor_fbs_score_async(uor_fbs_handle *handle, const uint32_t *rows, uint64_t n
                         uint32_t len, uint32_t *out_argmin, uint64_t *matches,
                         int32_t *status, void *stream);
 
+/* ---- The 256-cell CSR drawer index (the reference's uor_inverted_file API,
+ * projects/uor-cuda-inverted-file/include/uor_inverted_file.hpp:41-50, which its CUDA
+ * kernels uor_if_build/update/probe/full_scan, src/kernels.cu:139-243, serve; the discrete
+ * crate's bucket build/update entries, crates/uor-r4-discrete/src/bucket_source.rs:1-12).
+ *
+ * table [count][width] int32 (16-byte aligned, width a multiple of 4 in 16..MAX_WIDTH; the
+ * reference's Token is width 32: four 8-value blocks), roots [16][8] int32 (the reference's
+ * codebook, src/codebook.cpp:5-14). A token's cell is r0*16 + r1 when its first 8 values equal
+ * root r0 and its last 8 equal root r1 (first match), else ABSENT (0xffffffff). The index:
+ * offsets [257], members [count] (offsets[256] of them used: each cell's tokens ascending),
+ * cells [count], absent_count [1]. All device buffers; every call is asynchronous on `stream`
+ * and writes one int32 `status` word, a uor_inverted_file::Status (hpp:29-37): 0 Ok,
+ * 1 InvalidArgument, 2 NonRootBlock, 3 CsrInvariant. The return value is UOR_FBS_ERR_ARGUMENT
+ * (nothing launched) for null pointers, count 0 or above MAX_TOKENS, a bad width or
+ * alignment, k outside 1..16; UOR_FBS_ERR_DEVICE for a launch error. `workspace` holds
+ * uor_fbs_index_workspace_bytes(count) bytes of device memory, needs no initialisation and
+ * serialises the calls that share it (one stream). */
+#define UOR_FBS_INDEX_ABSENT 0xffffffffu
+#define UOR_FBS_INDEX_MAX_WIDTH 256u
+#define UOR_FBS_INDEX_MAX_TOKENS (1u << 30)
+
+uint64_t uor_fbs_index_workspace_bytes(uint32_t count);
+/* build (inverted_file.cpp:112-138, 173-175): status 2 when a token has no cell and
+ * allow_absent is 0 (the buffers then hold no valid index). */
+int uor_fbs_index_build_async(const int32_t *table, uint32_t count, uint32_t width,
+                              const int32_t *roots, uint32_t allow_absent, uint32_t *offsets,
+                              uint32_t *members, uint32_t *cells, uint32_t *absent_count,
+                              void *workspace, int32_t *status, void *stream);
+/* update (inverted_file.cpp:182-236): token `moved`'s row changed; the index is checked first
+ * (status 3, unchanged), then the token moves to its new cell (status 2 and unchanged when
+ * the new row has no cell), and the whole index is validated against the table after a
+ * move, as the reference returns validate(table, index). */
+int uor_fbs_index_update_async(const int32_t *table, uint32_t count, uint32_t width,
+                               const int32_t *roots, uint32_t moved, uint32_t *offsets,
+                               uint32_t *members, uint32_t *cells, uint32_t *absent_count,
+                               void *workspace, int32_t *status, void *stream);
+/* remove_token (inverted_file.cpp:238-249): token `moved` leaves its cell for ABSENT. A stored
+ * cell above 255, which the reference would index out of range, is refused with status 3. */
+int uor_fbs_index_remove_async(uint32_t count, uint32_t moved, uint32_t *offsets,
+                               uint32_t *members, uint32_t *cells, uint32_t *absent_count,
+                               void *workspace, int32_t *status, void *stream);
+/* validate (inverted_file.cpp:164-176) with a table, validate_structure (:141-162) when
+ * `table` is null (roots and width then unused). */
+int uor_fbs_index_validate_async(const int32_t *table, uint32_t count, uint32_t width,
+                                 const int32_t *roots, const uint32_t *offsets,
+                                 const uint32_t *members, const uint32_t *cells,
+                                 const uint32_t *absent_count, void *workspace, int32_t *status,
+                                 void *stream);
+/* probe (inverted_file.cpp:250-258) for `rows` queries [rows][width]: admitted [rows][16]
+ * (the k nearest non-empty cells by endpoint L1, ties to the lower cell, ABSENT-padded),
+ * top8 [rows][8] (the admitted cells' members by row L1, ties to the lower token),
+ * predictions [rows] = top8[0], status [rows]: 0, 1 when nothing was admitted, 3 when the
+ * index pointed outside the table. The index is not validated (validate once per change; the
+ * reference's probe validates on every call). */
+int uor_fbs_index_probe_async(const int32_t *table, uint32_t count, uint32_t width,
+                              const int32_t *roots, const int32_t *queries, uint32_t rows,
+                              uint32_t k, const uint32_t *offsets, const uint32_t *members,
+                              uint32_t *predictions, uint32_t *admitted, uint32_t *top8,
+                              int32_t *status, void *stream);
+/* full_scan (inverted_file.cpp:260-270): cells admitted from `offsets` of an index of the
+ * same table built with allow_absent 1, then every token of the table in an admitted cell
+ * ranked; outputs as the probe's. */
+int uor_fbs_index_full_scan_async(const int32_t *table, uint32_t count, uint32_t width,
+                                  const int32_t *roots, const int32_t *queries, uint32_t rows,
+                                  uint32_t k, const uint32_t *offsets, uint32_t *predictions,
+                                  uint32_t *admitted, uint32_t *top8, int32_t *status,
+                                  void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -68,6 +68,36 @@ void fbs_oracle_rms_norm_fine(const int32_t *x, uint32_t n, int64_t eps_mantissa
 uint32_t fbs_oracle_writer(const uor_fbs_model *m, const uor_fbs_ext *ext, const int32_t *query,
                            uint32_t *kept, uint64_t *candidates);
 
+/* The 256-cell CSR drawer index (fbs_index_oracle.c; projects/uor-cuda-inverted-file/src/
+ * inverted_file.cpp): table [count][width] int32, roots [16][8] int32, offsets[257],
+ * members (offsets[256] used), cells[count]. Status 0 ok, 1 invalid argument, 2 non-root
+ * block, 3 CSR invariant. */
+uint32_t fbs_oracle_index_cell(const int32_t *row, uint32_t width, const int32_t *roots);
+int fbs_oracle_index_build(const int32_t *table, uint32_t count, uint32_t width,
+                           const int32_t *roots, int allow_absent, uint32_t *offsets,
+                           uint32_t *members, uint32_t *cells, uint32_t *absent_count);
+int fbs_oracle_index_update(const int32_t *table, uint32_t count, uint32_t width,
+                            const int32_t *roots, uint32_t moved, uint32_t *offsets,
+                            uint32_t *members, uint32_t *cells, uint32_t *absent_count);
+int fbs_oracle_index_remove(uint32_t count, uint32_t moved, uint32_t *offsets, uint32_t *members,
+                            uint32_t *cells, uint32_t *absent_count);
+int fbs_oracle_index_validate_structure(const uint32_t *offsets, const uint32_t *members,
+                                        const uint32_t *cells, uint32_t count,
+                                        uint32_t absent_count);
+int fbs_oracle_index_validate(const int32_t *table, uint32_t count, uint32_t width,
+                              const int32_t *roots, const uint32_t *offsets,
+                              const uint32_t *members, const uint32_t *cells,
+                              uint32_t absent_count);
+/* Probe and full scan of one query row [width]: admitted[16], top8[8], *prediction. */
+int fbs_oracle_index_probe(const int32_t *table, uint32_t count, uint32_t width,
+                           const int32_t *roots, const int32_t *query, uint32_t k,
+                           const uint32_t *offsets, const uint32_t *members,
+                           const uint32_t *cells, uint32_t absent_count, uint32_t *admitted,
+                           uint32_t *top8, uint32_t *prediction);
+int fbs_oracle_index_full_scan(const int32_t *table, uint32_t count, uint32_t width,
+                               const int32_t *roots, const int32_t *query, uint32_t k,
+                               uint32_t *admitted, uint32_t *top8, uint32_t *prediction);
+
 #ifdef __cplusplus
 }
 #endif

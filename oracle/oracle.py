@@ -134,3 +134,203 @@ def twin_sequences(art, tokens: np.ndarray):
     st = twin().fbs_host_sequences(C.addressof(img.model), _vp(tokens), S, n, _vp(out_t),
                                    _vp(out_k), _vp(out_q))
     return st, out_t, out_k, out_q
+
+
+# ---- the CSR drawer index (fbs_index_oracle.c) and the reference's own inverted file
+# (oracle/_ref/libif_ref.so over projects/uor-cuda-inverted-file/src/inverted_file.cpp)
+
+IF_REF_SO = os.path.join(HERE, "_ref", "libif_ref.so")
+_if_ref = None
+
+
+def _index_lib():
+    L = lib()
+    if not hasattr(L, "_index_bound"):
+        u32 = C.c_uint32
+        L.fbs_oracle_index_cell.argtypes = [P, u32, P]
+        L.fbs_oracle_index_cell.restype = u32
+        L.fbs_oracle_index_build.argtypes = [P, u32, u32, P, C.c_int, P, P, P, P]
+        L.fbs_oracle_index_update.argtypes = [P, u32, u32, P, u32, P, P, P, P]
+        L.fbs_oracle_index_remove.argtypes = [u32, u32, P, P, P, P]
+        L.fbs_oracle_index_validate_structure.argtypes = [P, P, P, u32, u32]
+        L.fbs_oracle_index_validate.argtypes = [P, u32, u32, P, P, P, P, u32]
+        L.fbs_oracle_index_probe.argtypes = [P, u32, u32, P, P, u32, P, P, P, u32, P, P, P]
+        L.fbs_oracle_index_full_scan.argtypes = [P, u32, u32, P, P, u32, P, P, P]
+        L._index_bound = True
+    return L
+
+
+def if_ref_available() -> bool:
+    return os.path.exists(IF_REF_SO)
+
+
+def if_ref():
+    global _if_ref
+    if _if_ref is None:
+        R = C.CDLL(IF_REF_SO)
+        u32 = C.c_uint32
+        R.if_ref_codebook.argtypes = [P]
+        R.if_ref_build.argtypes = [P, u32, C.c_int, P, P, P, P]
+        R.if_ref_update.argtypes = [P, u32, u32, P, P, P, P]
+        R.if_ref_remove.argtypes = [P, u32, u32, P, P, P, P]
+        R.if_ref_validate.argtypes = [P, u32, P, P, P, u32]
+        R.if_ref_validate_structure.argtypes = [P, P, P, u32, u32]
+        R.if_ref_probe.argtypes = [P, u32, P, u32, P, P, P, u32, P, P, P]
+        R.if_ref_full_scan.argtypes = [P, u32, P, u32, P, P, P]
+        _if_ref = R
+    return _if_ref
+
+
+def _flat(idx, count):
+    """A HostIndex as the flat buffers both libraries take (members with room for count)."""
+    off = np.ascontiguousarray(idx.offsets, dtype=np.uint32).copy()
+    mem = np.zeros(max(count, 1), np.uint32)
+    n = min(len(idx.members), count)
+    mem[:n] = idx.members[:n]
+    cells = np.ascontiguousarray(idx.cells, dtype=np.uint32).copy()
+    return off, mem, cells, C.c_uint32(int(idx.absent_count))
+
+
+def _host(off, mem, cells, absent, count):
+    from uor_fbs.index import HostIndex
+    return HostIndex(off, mem[:min(int(off[256]), count)].copy(), cells, int(absent.value))
+
+
+def _table(table):
+    t = np.ascontiguousarray(table, dtype=np.int32)
+    return t, t.shape[0], t.shape[1]
+
+
+def index_cell(row, roots) -> int:
+    row = np.ascontiguousarray(row, dtype=np.int32)
+    return int(_index_lib().fbs_oracle_index_cell(_vp(row), row.size,
+                                                  _vp(np.ascontiguousarray(roots, np.int32))))
+
+
+def index_build(table, roots, allow_absent=False):
+    """(status, HostIndex) of build (inverted_file.cpp:112-138)."""
+    t, count, width = _table(table)
+    roots = np.ascontiguousarray(roots, np.int32)
+    off, mem, cells = np.zeros(257, np.uint32), np.zeros(max(count, 1), np.uint32), np.zeros(max(count, 1), np.uint32)
+    absent = C.c_uint32()
+    st = _index_lib().fbs_oracle_index_build(_vp(t), count, width, _vp(roots), int(allow_absent),
+                                             _vp(off), _vp(mem), _vp(cells), C.byref(absent))
+    return st, _host(off, mem, cells[:count], absent, count)
+
+
+def index_update(table, roots, moved, idx):
+    """(status, HostIndex after) of update (inverted_file.cpp:182-236)."""
+    t, count, width = _table(table)
+    off, mem, cells, absent = _flat(idx, count)
+    st = _index_lib().fbs_oracle_index_update(_vp(t), count, width,
+                                              _vp(np.ascontiguousarray(roots, np.int32)), moved,
+                                              _vp(off), _vp(mem), _vp(cells), C.byref(absent))
+    return st, _host(off, mem, cells, absent, count)
+
+
+def index_remove(count, moved, idx):
+    """(status, HostIndex after) of remove_token (inverted_file.cpp:238-249)."""
+    off, mem, cells, absent = _flat(idx, count)
+    st = _index_lib().fbs_oracle_index_remove(count, moved, _vp(off), _vp(mem), _vp(cells),
+                                              C.byref(absent))
+    return st, _host(off, mem, cells, absent, count)
+
+
+def index_validate(table, roots, idx) -> int:
+    t, count, width = _table(table)
+    off, mem, cells, absent = _flat(idx, count)
+    return _index_lib().fbs_oracle_index_validate(
+        _vp(t), count, width, _vp(np.ascontiguousarray(roots, np.int32)), _vp(off), _vp(mem),
+        _vp(cells), absent.value)
+
+
+def index_validate_structure(idx) -> int:
+    count = len(idx.cells)
+    off, mem, cells, absent = _flat(idx, count)
+    return _index_lib().fbs_oracle_index_validate_structure(_vp(off), _vp(mem), _vp(cells), count,
+                                                            absent.value)
+
+
+def _scan_out():
+    return np.zeros(16, np.uint32), np.zeros(8, np.uint32), C.c_uint32()
+
+
+def index_probe(table, roots, query, k, idx):
+    """(status, admitted [16], top8 [8], prediction) of probe (inverted_file.cpp:250-258)."""
+    t, count, width = _table(table)
+    q = np.ascontiguousarray(query, np.int32).reshape(width)
+    off, mem, cells, absent = _flat(idx, count)
+    adm, top, pred = _scan_out()
+    st = _index_lib().fbs_oracle_index_probe(
+        _vp(t), count, width, _vp(np.ascontiguousarray(roots, np.int32)), _vp(q), k, _vp(off),
+        _vp(mem), _vp(cells), absent.value, _vp(adm), _vp(top), C.byref(pred))
+    return st, adm, top, pred.value
+
+
+def index_full_scan(table, roots, query, k):
+    """(status, admitted, top8, prediction) of full_scan (inverted_file.cpp:260-270)."""
+    t, count, width = _table(table)
+    q = np.ascontiguousarray(query, np.int32).reshape(width)
+    adm, top, pred = _scan_out()
+    st = _index_lib().fbs_oracle_index_full_scan(
+        _vp(t), count, width, _vp(np.ascontiguousarray(roots, np.int32)), _vp(q), k, _vp(adm),
+        _vp(top), C.byref(pred))
+    return st, adm, top, pred.value
+
+
+# The reference library's calls (width-32 tables, its own codebook).
+
+def ref_codebook() -> np.ndarray:
+    roots = np.zeros((16, 8), np.int32)
+    if_ref().if_ref_codebook(_vp(roots))
+    return roots
+
+
+def ref_build(table, allow_absent=False):
+    t, count, width = _table(table)
+    assert width == 32
+    off, mem, cells = np.zeros(257, np.uint32), np.zeros(max(count, 1), np.uint32), np.zeros(max(count, 1), np.uint32)
+    absent = C.c_uint32()
+    st = if_ref().if_ref_build(_vp(t), count, int(allow_absent), _vp(off), _vp(mem), _vp(cells),
+                               C.byref(absent))
+    return st, _host(off, mem, cells[:count], absent, count)
+
+
+def ref_update(table, moved, idx):
+    t, count, _ = _table(table)
+    off, mem, cells, absent = _flat(idx, count)
+    st = if_ref().if_ref_update(_vp(t), count, moved, _vp(off), _vp(mem), _vp(cells),
+                                C.byref(absent))
+    return st, _host(off, mem, cells, absent, count)
+
+
+def ref_remove(table, moved, idx):
+    t, count, _ = _table(table)
+    off, mem, cells, absent = _flat(idx, count)
+    st = if_ref().if_ref_remove(_vp(t), count, moved, _vp(off), _vp(mem), _vp(cells),
+                                C.byref(absent))
+    return st, _host(off, mem, cells, absent, count)
+
+
+def ref_validate(table, idx) -> int:
+    t, count, _ = _table(table)
+    off, mem, cells, absent = _flat(idx, count)
+    return if_ref().if_ref_validate(_vp(t), count, _vp(off), _vp(mem), _vp(cells), absent.value)
+
+
+def ref_probe(table, query, k, idx):
+    t, count, _ = _table(table)
+    q = np.ascontiguousarray(query, np.int32).reshape(32)
+    off, mem, cells, absent = _flat(idx, count)
+    adm, top, pred = _scan_out()
+    st = if_ref().if_ref_probe(_vp(t), count, _vp(q), k, _vp(off), _vp(mem), _vp(cells),
+                               absent.value, _vp(adm), _vp(top), C.byref(pred))
+    return st, adm, top, pred.value
+
+
+def ref_full_scan(table, query, k):
+    t, count, _ = _table(table)
+    q = np.ascontiguousarray(query, np.int32).reshape(32)
+    adm, top, pred = _scan_out()
+    st = if_ref().if_ref_full_scan(_vp(t), count, _vp(q), k, _vp(adm), _vp(top), C.byref(pred))
+    return st, adm, top, pred.value

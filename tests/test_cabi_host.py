@@ -74,6 +74,40 @@ def test_model_create_refuses_bad_images_without_a_device():
     assert hip.lib().uor_fbs_model_create(C.byref(img.model), C.byref(img.ext), 0, C.byref(h)) == 4
 
 
+def test_index_entry_points_refuse_bad_arguments_before_any_launch():
+    """The CSR index's entry points check pointers, sizes, widths, alignment and k on the host
+    and return UOR_FBS_ERR_ARGUMENT (3) without a launch; the workspace size is 16 header words
+    plus 257 words per tile of 2,048 tokens and 257 totals."""
+    L = hip.lib()
+    fake = P(4096)  # never dereferenced: every call below is refused first
+    odd = P(4100)   # a table pointer that is not 16-byte aligned
+    mx = 1 << 30
+    assert L.uor_fbs_index_workspace_bytes(1) == 4 * (16 + 257 * 2)
+    assert L.uor_fbs_index_workspace_bytes(2049) == 4 * (16 + 257 * 3)
+    build = L.uor_fbs_index_build_async
+    assert build(None, 10, 32, fake, 0, fake, fake, fake, fake, fake, fake, None) == 3
+    assert build(fake, 0, 32, fake, 0, fake, fake, fake, fake, fake, fake, None) == 3
+    assert build(fake, mx + 1, 32, fake, 0, fake, fake, fake, fake, fake, fake, None) == 3
+    for width in (8, 12, 30, 260):
+        assert build(fake, 10, width, fake, 0, fake, fake, fake, fake, fake, fake, None) == 3
+    assert build(odd, 10, 32, fake, 0, fake, fake, fake, fake, fake, fake, None) == 3
+    assert build(fake, 10, 32, fake, 0, fake, fake, fake, fake, None, fake, None) == 3
+    assert L.uor_fbs_index_update_async(fake, 10, 32, None, 0, fake, fake, fake, fake, fake, fake,
+                                        None) == 3
+    assert L.uor_fbs_index_remove_async(0, 0, fake, fake, fake, fake, fake, fake, None) == 3
+    assert L.uor_fbs_index_remove_async(10, 0, fake, None, fake, fake, fake, fake, None) == 3
+    assert L.uor_fbs_index_validate_async(fake, 10, 18, fake, fake, fake, fake, fake, fake, fake,
+                                          None) == 3
+    probe = L.uor_fbs_index_probe_async
+    for k in (0, 17):
+        assert probe(fake, 10, 32, fake, fake, 1, k, fake, fake, fake, fake, fake, fake, None) == 3
+    assert probe(fake, 10, 32, fake, fake, 0, 8, fake, fake, fake, fake, fake, fake, None) == 3
+    assert probe(fake, 10, 32, fake, fake, 1, 8, fake, None, fake, fake, fake, fake, None) == 3
+    scan = L.uor_fbs_index_full_scan_async
+    assert scan(fake, 10, 32, fake, fake, 1, 17, fake, fake, fake, fake, fake, None) == 3
+    assert scan(fake, 10, 32, fake, None, 1, 8, fake, fake, fake, fake, fake, None) == 3
+
+
 @pytest.fixture(scope="module")
 def hp():
     if not os.path.exists(HP_PATH):

@@ -29,7 +29,9 @@ SYMBOLS = (
     "uor_fbs_last_error", "uor_fbs_model_create", "uor_fbs_model_destroy", "uor_fbs_state_words",
     "uor_fbs_history_words", "uor_fbs_sequences", "uor_fbs_sequences_async", "uor_fbs_decode",
     "uor_fbs_decode_async", "uor_fbs_score", "uor_fbs_score_async", "uor_fbs_block_waves",
-    "uor_fbs_decode_slots_async",
+    "uor_fbs_decode_slots_async", "uor_fbs_index_workspace_bytes", "uor_fbs_index_build_async",
+    "uor_fbs_index_update_async", "uor_fbs_index_remove_async", "uor_fbs_index_validate_async",
+    "uor_fbs_index_probe_async", "uor_fbs_index_full_scan_async",
 )
 
 
@@ -69,6 +71,16 @@ def lib():
                                                  C.c_uint32, P, P, P, P, P, P, P, P]
         L.uor_fbs_score.argtypes = [P, P, C.c_uint64, C.c_uint32, P, P]
         L.uor_fbs_score_async.argtypes = [P, P, C.c_uint64, C.c_uint32, P, P, P, P]
+        u32 = C.c_uint32
+        L.uor_fbs_index_workspace_bytes.argtypes = [u32]
+        L.uor_fbs_index_workspace_bytes.restype = C.c_uint64
+        L.uor_fbs_index_build_async.argtypes = [P, u32, u32, P, u32, P, P, P, P, P, P, P]
+        L.uor_fbs_index_update_async.argtypes = [P, u32, u32, P, u32, P, P, P, P, P, P, P]
+        L.uor_fbs_index_remove_async.argtypes = [u32, u32, P, P, P, P, P, P, P]
+        L.uor_fbs_index_validate_async.argtypes = [P, u32, u32, P, P, P, P, P, P, P, P]
+        L.uor_fbs_index_probe_async.argtypes = [P, u32, u32, P, P, u32, u32, P, P, P, P, P, P, P]
+        L.uor_fbs_index_full_scan_async.argtypes = [P, u32, u32, P, P, u32, u32, P, P, P, P, P,
+                                                    P]
         _lib = L
     return _lib
 
