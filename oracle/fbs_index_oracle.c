@@ -141,6 +141,9 @@ int fbs_oracle_index_remove(uint32_t count, uint32_t moved, uint32_t *offsets, u
   if (fbs_oracle_index_validate_structure(offsets, members, cells, count, *absent_count)) return 3;
   const uint32_t old_cell = cells[moved];
   if (old_cell == ABSENT) return 0;
+  /* The reference reads offsets[old_cell] unchecked here (remove_from_bucket, :84-100); a
+   * stored cell past 255 has no range, and is refused as a CSR invariant. */
+  if (old_cell > 255) return 3;
   uint32_t remove_pos = ABSENT;
   for (uint32_t p = offsets[old_cell]; p < offsets[old_cell + 1]; p++)
     if (members[p] == moved) {
