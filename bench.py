@@ -17,6 +17,11 @@ The same line carries the roofline of that kernel (algorithmic bytes per token x
 launch / launch time, against MI355X's 8 TB/s) and the CPU baseline: the oracle (a C
 restatement of the reference's step, one sequence per thread) timed on this host over a
 bounded sample of the same decode, whose replies must equal the GPU's.
+
+Beside the metric, `drawer_index` measures the 256-cell CSR drawer index (uor_fbs_index_*):
+builds at C5's vocabulary and at --index-large tokens (checked against torch's stable sort),
+single-token updates, batched probes (checked against the full scan), and the reference's
+single-query protocol with its published RTX 5090 medians beside ours.
 """
 
 from __future__ import annotations
@@ -56,6 +61,10 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--serve-steps", type=int, default=64,
                    help="serving-loop launches after the decode (0: none); reported beside the metric")
+    p.add_argument("--no-index", action="store_true",
+                   help="skip the CSR drawer index measurements (build, update, probe)")
+    p.add_argument("--index-large", type=int, default=1 << 24,
+                   help="tokens of the large index build (width 32)")
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="only run one elementwise copy kernel over this many MiB (the reference "
                         "reading for the FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -103,6 +112,179 @@ def algorithmic_bytes_per_token(spec, mean_candidates: float) -> float:
     c = 1 if spec.table == "i8" else 2
     d, L, W = spec.width, spec.layers, spec.window
     return c * d + L * (W * d * 4 + d * 4) + c * d * mean_candidates + 4
+
+
+# Bytes one token moves in an index build by the path's definition: its two 8-value endpoint
+# blocks read, its cell written and read back by the scatter, its member entry written.
+INDEX_BUILD_BYTES_PER_TOKEN = 64 + 4 + 4 + 4
+# Measured HBM bytes of one 16,777,216-token build (rocprofv3 FETCH_SIZE and WRITE_SIZE passes).
+INDEX_TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fbs_index_build_16m_traffic.md")
+# The reference's published single-card kernel medians (RTX 5090, 120 launches per operation
+# over V in {64, 256, 1024, 4096} x K in {1, 8, 16}, one query each;
+# projects/uor-cuda-inverted-file/RESULTS.md).
+INDEX_REFERENCE_MS = {"probe": 0.160144, "full_scan": 0.109856}
+
+
+def index_section(torch, dev, stream, sp, large: int) -> dict:
+    """The CSR drawer index on the device: builds (at C5's vocabulary and at `large` tokens),
+    single-token updates, batched probes, and the reference's single-query protocol. Results
+    are checked on the device against torch's stable sort and against the full scan."""
+    from uor_fbs import hip
+    from uor_fbs import index as ix
+
+    L = hip.lib()
+    roots = torch.from_numpy(ix.CODEBOOK).to(dev)
+    out: dict = {"build": [], "probe": []}
+
+    def ptr(t):
+        return C.c_void_p(t.data_ptr())
+
+    def check(code):
+        if code:
+            raise hip.FbsError(code, L.uor_fbs_last_error().decode())
+
+    def timed(fn, reps, warm=2):
+        for _ in range(warm):
+            fn()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(reps)]
+        for s_, e_ in ev:
+            s_.record(stream)
+            fn()
+            e_.record(stream)
+        torch.cuda.synchronize()
+        return [s_.elapsed_time(e_) for s_, e_ in ev]
+
+    def random_table(count, seed):
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        t = torch.randint(-(1 << 31), (1 << 31) - 1, (count, 32), dtype=torch.int32, device=dev,
+                          generator=g)
+        cells = torch.randint(0, 256, (count,), device=dev, generator=g)
+        t[:, :8] = roots[cells // 16]
+        t[:, 24:] = roots[cells % 16]
+        return t, cells
+
+    class Buffers:
+        def __init__(self, count):
+            z = lambda n: torch.zeros(n, dtype=torch.int32, device=dev)  # noqa: E731
+            self.count = count
+            self.off, self.mem, self.cells, self.absent = z(257), z(count), z(count), z(1)
+            self.ws = z(int(L.uor_fbs_index_workspace_bytes(count)) // 4)
+            self.status = z(1)
+
+        def build(self, table):
+            check(L.uor_fbs_index_build_async(ptr(table), self.count, 32, ptr(roots), 0,
+                                              ptr(self.off), ptr(self.mem), ptr(self.cells),
+                                              ptr(self.absent), ptr(self.ws), ptr(self.status), sp))
+
+        def update(self, table, moved):
+            check(L.uor_fbs_index_update_async(ptr(table), self.count, 32, ptr(roots), moved,
+                                               ptr(self.off), ptr(self.mem), ptr(self.cells),
+                                               ptr(self.absent), ptr(self.ws), ptr(self.status),
+                                               sp))
+
+    def same_as_sort(b, cells):
+        order = torch.sort(cells, stable=True).indices.to(torch.int32)
+        offsets = torch.zeros(257, dtype=torch.int64, device=dev)
+        offsets[1:] = torch.cumsum(torch.bincount(cells, minlength=256), 0)
+        return (int(b.status.item()) == 0 and bool(torch.equal(b.mem, order))
+                and bool(torch.equal(b.cells.long(), cells))
+                and bool(torch.equal(b.off.long(), offsets)) and int(b.absent.item()) == 0)
+
+    keep = {}
+    for count in (65536, large):
+        table, cells = random_table(count, count)
+        b = Buffers(count)
+        ms = timed(lambda: b.build(table), reps=10)
+        ok = same_as_sort(b, cells)
+        achieved = INDEX_BUILD_BYTES_PER_TOKEN * count / (np.mean(ms) / 1e3) / 1e9
+        traffic = None
+        if count == 1 << 24 and os.path.exists(INDEX_TRAFFIC_SUMMARY):
+            m = re.search(r"^traffic_bytes_per_launch: (\d+)$", open(INDEX_TRAFFIC_SUMMARY).read(),
+                          re.M)
+            traffic = int(m.group(1)) if m else None
+        out["build"].append({
+            "tokens": count, "width": 32, "ms": round(float(np.mean(ms)), 4),
+            "tokens_per_s": round(count / (np.mean(ms) / 1e3), 1), "equal_stable_sort": ok,
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                         "traffic": traffic, "bytes_per_token": INDEX_BUILD_BYTES_PER_TOKEN}})
+        if count == 65536:
+            keep["c5"] = (table, cells, b)
+        del table, cells
+    # Updates at C5's vocabulary: 64 tokens move to other cells, one call each (the row edit is
+    # the caller's and stays outside the timing); the result must equal a fresh build.
+    table, cells, b = keep["c5"]
+    rng = np.random.default_rng(5)
+    upd_ms = []
+    for _ in range(64):
+        moved, c = int(rng.integers(0, 65536)), int(rng.integers(0, 256))
+        table[moved, :8], table[moved, 24:] = roots[c // 16], roots[c % 16]
+        cells[moved] = c
+        upd_ms += timed(lambda: b.update(table, moved), reps=1, warm=0)
+        assert int(b.status.item()) == 0, "index update failed"
+    out["update"] = {"tokens": 65536, "moves": 64, "ms_per_update": round(float(np.mean(upd_ms)), 4),
+                     "launches_per_update": 4, "equal_fresh_build": same_as_sort(b, cells)}
+    # Batched probes: 65,536 query rows (root endpoints, random middles) against tables of the
+    # reference's size and of C5's vocabulary.
+    rows = 65536
+    queries, _ = random_table(rows, 77)
+    z = lambda n: torch.zeros(n, dtype=torch.int32, device=dev)  # noqa: E731
+    pred, adm, top, st = z(rows), z(rows * 16), z(rows * 8), z(rows)
+    for count in (4096, 65536):
+        if count == 65536:
+            tb, bb = table, b
+        else:
+            tb, _ = random_table(count, 4096)
+            bb = Buffers(count)
+            bb.build(tb)
+        for k in (8, 16):
+            def probe():
+                check(L.uor_fbs_index_probe_async(ptr(tb), count, 32, ptr(roots), ptr(queries),
+                                                  rows, k, ptr(bb.off), ptr(bb.mem), ptr(pred),
+                                                  ptr(adm), ptr(top), ptr(st), sp))
+            ms = timed(probe, reps=10)
+            ok = int(st.abs().sum().item()) == 0
+            # Cross-check: the full scan (every token of the table) on the first 512 rows.
+            n = 512
+            fp, fa, ft, fs = z(n), z(n * 16), z(n * 8), z(n)
+            check(L.uor_fbs_index_full_scan_async(ptr(tb), count, 32, ptr(roots), ptr(queries), n,
+                                                  k, ptr(bb.off), ptr(fp), ptr(fa), ptr(ft),
+                                                  ptr(fs), sp))
+            torch.cuda.synchronize()
+            ok = ok and bool(torch.equal(ft, top[:n * 8])) and bool(torch.equal(fa, adm[:n * 16]))
+            out["probe"].append({"tokens": count, "k": k, "rows": rows,
+                                 "ms_per_launch": round(float(np.mean(ms)), 4),
+                                 "rows_per_s": round(rows / (np.mean(ms) / 1e3), 1),
+                                 "equal_full_scan_first_512": ok})
+    # For the CPU leg: the C5 table, its index and the last probe's (k 16) first 64 rows.
+    keep["probe_check"] = (queries[:64].cpu().numpy(), table.cpu().numpy(),
+                           [b.off.cpu().numpy(), b.mem.cpu().numpy(), b.cells.cpu().numpy()],
+                           top[:64 * 8].cpu().numpy().reshape(64, 8))
+    # The reference's protocol: one query (its query_at(7)) per launch on its seeded tables.
+    single = {"probe": [], "full_scan": []}
+    q1 = torch.from_numpy(ix.seeded_query(7)).to(dev)
+    o1 = [z(1), z(16), z(8), z(1)]
+    for count in (64, 256, 1024, 4096):
+        tb = torch.from_numpy(ix.seeded_table(count)).to(dev)
+        bb = Buffers(count)
+        bb.build(tb)
+        for k in (1, 8, 16):
+            single["probe"] += timed(lambda: check(L.uor_fbs_index_probe_async(
+                ptr(tb), count, 32, ptr(roots), ptr(q1), 1, k, ptr(bb.off), ptr(bb.mem),
+                *[ptr(x) for x in o1], sp)), reps=10, warm=3)
+            single["full_scan"] += timed(lambda: check(L.uor_fbs_index_full_scan_async(
+                ptr(tb), count, 32, ptr(roots), ptr(q1), 1, k, ptr(bb.off),
+                *[ptr(x) for x in o1], sp)), reps=10, warm=3)
+    out["single_query_ms"] = {
+        op: {"median": round(float(np.median(v)), 5), "launches": len(v),
+             "reference_rtx5090_median": INDEX_REFERENCE_MS[op]} for op, v in single.items()}
+    out["single_query_protocol"] = ("one query (query_at(7)) per launch on the reference tests' "
+                                    "seeded tables, V in {64, 256, 1024, 4096} x K in {1, 8, 16}, "
+                                    "3 warm-up + 10 timed launches each, HIP events")
+    out["_keep"] = keep
+    return out
 
 
 def main():
@@ -297,6 +479,8 @@ def main():
         if not same_serve:
             print("bench.py: the serving loop's tokens differ from the decode's", file=sys.stderr)
 
+    index = None if a.no_index else index_section(torch, dev, stream, sp, a.index_large)
+
     if not a.no_cpu:
         threads = a.cpu_threads or min(16, os.cpu_count() or 1)
         st_np = state.cpu().numpy()
@@ -328,7 +512,37 @@ def main():
         }
         if not same:
             print("bench.py: CPU replies differ from the GPU's", file=sys.stderr)
+        if index is not None:
+            index["cpu_baseline"] = index_cpu_baseline(oracle, index)
+    if index is not None:
+        index.pop("_keep", None)
+        out["drawer_index"] = index
     print(json.dumps(out))
+
+
+def index_cpu_baseline(oracle, index) -> dict:
+    """The oracle's index build on this host at C5's vocabulary (one thread), timed, and its
+    index and probes compared with the device's."""
+    from uor_fbs import index as ix
+    keep = index["_keep"]
+    queries, table, (off, mem, cells), top = keep["probe_check"]
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        st, host = oracle.index_build(table, ix.CODEBOOK)
+        reps += 1
+        if time.perf_counter() - t0 > 2.0:
+            break
+    cpu_s = (time.perf_counter() - t0) / reps
+    same = (st == 0 and np.array_equal(host.offsets, off.view(np.uint32))
+            and np.array_equal(host.members, mem.view(np.uint32))
+            and np.array_equal(host.cells, cells.view(np.uint32)))
+    probes_same = True
+    for r in range(len(queries)):
+        pst, _, ptop, _ = oracle.index_probe(table, ix.CODEBOOK, queries[r], 16, host)
+        probes_same &= pst == 0 and np.array_equal(ptop, top[r].view(np.uint32))
+    return {"build_tokens_per_s": round(len(table) / cpu_s, 1), "cores": 1, "kind": "port",
+            "sample": f"oracle build of the {len(table)}-token index x {reps}",
+            "index_equal_gpu": bool(same), "probes_equal_gpu_first_64": bool(probes_same)}
 
 
 if __name__ == "__main__":

@@ -77,13 +77,15 @@ def test_model_create_refuses_bad_images_without_a_device():
 def test_index_entry_points_refuse_bad_arguments_before_any_launch():
     """The CSR index's entry points check pointers, sizes, widths, alignment and k on the host
     and return UOR_FBS_ERR_ARGUMENT (3) without a launch; the workspace size is 16 header words
-    plus 257 words per tile of 2,048 tokens and 257 totals."""
+    plus 257 words per build tile and 257 totals; a tile is 512 tokens times the largest
+    power of two up to 16 that leaves about 256 tiles."""
     L = hip.lib()
     fake = P(4096)  # never dereferenced: every call below is refused first
     odd = P(4100)   # a table pointer that is not 16-byte aligned
     mx = 1 << 30
-    assert L.uor_fbs_index_workspace_bytes(1) == 4 * (16 + 257 * 2)
-    assert L.uor_fbs_index_workspace_bytes(2049) == 4 * (16 + 257 * 3)
+    for count, tiles in ((1, 1), (512, 1), (513, 2), (65536, 128), (262144, 256),
+                         (1 << 20, 256), (1 << 24, 2048), ((1 << 24) + 1, 2049)):
+        assert L.uor_fbs_index_workspace_bytes(count) == 4 * (16 + 257 * (tiles + 1)), count
     build = L.uor_fbs_index_build_async
     assert build(None, 10, 32, fake, 0, fake, fake, fake, fake, fake, fake, None) == 3
     assert build(fake, 0, 32, fake, 0, fake, fake, fake, fake, fake, fake, None) == 3

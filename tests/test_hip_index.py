@@ -40,9 +40,9 @@ def check_scan(res: ix.ScanResult, table, queries, k, host_index=None):
         assert res.prediction[r] == want[3], r
 
 
-@pytest.mark.parametrize("count,width", [(1, 32), (64, 32), (256, 32), (2047, 32), (2048, 32),
-                                         (2049, 16), (4096, 32), (65536, 32), (300001, 64),
-                                         (5000, 256)])
+@pytest.mark.parametrize("count,width", [(1, 32), (64, 32), (511, 32), (512, 32), (513, 16),
+                                         (4096, 32), (65536, 32), (300001, 64), (5000, 256),
+                                         ((1 << 20) + 1, 32), ((1 << 22) + 3, 16)])
 def test_build_matches_oracle(count, width):
     rng = np.random.default_rng(count)
     table = table_of(count) if width == 32 and count <= 4096 else random_table(rng, count, width)

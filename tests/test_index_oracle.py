@@ -51,6 +51,15 @@ def test_codebook_fixture_is_the_reference_codebook():
     np.testing.assert_array_equal(oracle.ref_codebook(), R)
 
 
+def test_inputs_match_the_package_generators():
+    """The package's codebook and seeded generators (bench.py's inputs) are these inputs."""
+    from uor_fbs import index as ix
+    np.testing.assert_array_equal(ix.CODEBOOK, R)
+    np.testing.assert_array_equal(ix.seeded_table(300), table_of(300))
+    for s in range(40):
+        np.testing.assert_array_equal(ix.seeded_query(s), query_at(s))
+
+
 @pytest.mark.parametrize("v", [1, 64, 256, 4096])
 def test_build_matches_numpy_and_construction(v):
     t = table_of(v)

@@ -12,9 +12,11 @@
 // (include/uor_inverted_file.hpp:29-37): 0 ok, 1 invalid argument, 2 non-root block,
 // 3 CSR invariant.
 //
-// Build (three launches): cells and one histogram per tile of 2,048 tokens; one block per cell
+// Build (three launches): cells and one histogram per tile (512 to 8,192 tokens: the largest
+// that leaves about 256 tiles); one block per cell
 // scanning that cell's tile counts; a stable scatter in which a token's place is its cell's
-// offset + its tile's start in the cell + the earlier tokens of the tile in the same cell.
+// offset + its tile's start in the cell + the earlier tokens of the tile in the same cell, the
+// tile sorted in LDS first so that each cell's run is written contiguously.
 // Update / remove (four launches): the structure check the reference runs first, spread over
 // many blocks; one block moving the token with the reference's shifts (the members between
 // the old and the new place move by one, in chunks that read before they write); then the
@@ -37,10 +39,12 @@ namespace fbs_index {
 constexpr uint32_t kAbsent = 0xffffffffu;
 constexpr uint32_t kCells = 256;
 constexpr uint32_t kSlots = kCells + 1;  // cells, then the absent tokens
-constexpr uint32_t kThreads = 256;       // build, scan, verify and full-scan blocks
+constexpr uint32_t kThreads = 256;       // scan, verify and full-scan blocks
 constexpr uint32_t kWaves = kThreads / 64;
-constexpr uint32_t kPerThread = 8;
-constexpr uint32_t kTile = kThreads * kPerThread;  // tokens per build block
+constexpr uint32_t kBuildThreads = 512;  // cells and scatter blocks
+constexpr uint32_t kBuildWaves = kBuildThreads / 64;
+constexpr uint32_t kMaxPer = 16;  // rounds of kBuildThreads tokens per build tile
+constexpr uint32_t kMaxTile = kBuildThreads * kMaxPer;
 constexpr uint32_t kMoveThreads = 1024;
 constexpr uint32_t kShiftPer = 4;  // members per thread per shift chunk
 constexpr uint32_t kMaxVerifyBlocks = 2048;
@@ -50,9 +54,18 @@ constexpr int64_t kFar = INT64_MAX;
 // Workspace words ahead of the build's tile counts.
 constexpr uint32_t kBad = 0, kDone = 1, kTally = 2, kPost = 3, kHeader = 16;
 static_assert(kThreads == kCells, "one thread per cell in the scans");
+static_assert(kBuildThreads >= kCells, "a build block has a thread per cell");
 
+// Rounds per build tile: the most (longer runs per cell, so the scatter's writes coalesce)
+// that still leave about 256 tiles (one per CU) to spread the work.
+__host__ __device__ inline uint32_t rounds_of(uint32_t count) {
+  uint32_t per = 1;
+  while (per < kMaxPer && (uint64_t)count >= (uint64_t)2 * per * kBuildThreads * 256) per *= 2;
+  return per;
+}
 __host__ __device__ inline uint32_t tiles_of(uint32_t count) {
-  return (count + kTile - 1) / kTile;
+  const uint32_t tile = rounds_of(count) * kBuildThreads;
+  return (count + tile - 1) / tile;
 }
 
 // ---- cells
@@ -81,12 +94,13 @@ __device__ __forceinline__ uint32_t token_cell(const int32_t *row, uint32_t widt
   return a == kAbsent || b == kAbsent ? kAbsent : a * 16 + b;
 }
 
-// Inclusive scan over the block's 256 threads (buf: 256 words of LDS); every thread may read
-// buf[255], the block's total, on return.
+// Inclusive scan over the block's N threads (buf: N words of LDS); every thread may read
+// buf[N - 1], the block's total, on return.
+template <uint32_t N>
 __device__ uint32_t block_scan(uint32_t v, uint32_t *buf) {
   buf[threadIdx.x] = v;
   __syncthreads();
-  for (uint32_t off = 1; off < kThreads; off *= 2) {
+  for (uint32_t off = 1; off < N; off *= 2) {
     const uint32_t add = threadIdx.x >= off ? buf[threadIdx.x - off] : 0;
     __syncthreads();
     buf[threadIdx.x] += add;
@@ -95,41 +109,58 @@ __device__ uint32_t block_scan(uint32_t v, uint32_t *buf) {
   return buf[threadIdx.x];
 }
 
+// The cell holding position p of a CSR run list: the c with start[c] <= p < start[c + 1]
+// (start non-decreasing, start[0] <= p < start[256]).
+__device__ __forceinline__ uint32_t cell_at(const uint32_t *start, uint32_t p) {
+  uint32_t lo = 0, hi = kCells;
+  while (hi - lo > 1) {
+    const uint32_t mid = (lo + hi) / 2;
+    if (start[mid] <= p) lo = mid; else hi = mid;
+  }
+  return lo;
+}
+
 // ---- build
 
 // Cells, and each tile's count of every cell (slot 256: absent tokens) as counts[slot][tile].
-__global__ __launch_bounds__(kThreads) void index_cells(const int32_t *__restrict__ table,
-                                                        uint32_t count, uint32_t width,
-                                                        const int32_t *__restrict__ roots,
-                                                        uint32_t tiles,
-                                                        uint32_t *__restrict__ cells,
-                                                        uint32_t *__restrict__ counts) {
+// Token t of a tile is t = tile * per * kBuildThreads + r * kBuildThreads + thread, r < per,
+// in passes of up to 8 rows per thread (16 loads in flight each).
+__global__ __launch_bounds__(kBuildThreads) void index_cells(const int32_t *__restrict__ table,
+                                                             uint32_t count, uint32_t width,
+                                                             const int32_t *__restrict__ roots,
+                                                             uint32_t per, uint32_t tiles,
+                                                             uint32_t *__restrict__ cells,
+                                                             uint32_t *__restrict__ counts) {
   __shared__ __align__(16) int32_t sroots[128];
   __shared__ uint32_t hist[kSlots];
   load_roots(roots, sroots);
-  for (uint32_t i = threadIdx.x; i < kSlots; i += kThreads) hist[i] = 0;
+  for (uint32_t i = threadIdx.x; i < kSlots; i += kBuildThreads) hist[i] = 0;
   __syncthreads();
-  const uint32_t first = blockIdx.x * kTile + threadIdx.x;
-  uint32_t c[kPerThread];
+  const uint32_t first = blockIdx.x * per * kBuildThreads + threadIdx.x;
+  for (uint32_t pass = 0; pass < per; pass += 8) {
+    uint32_t c[8];
 #pragma unroll
-  for (uint32_t r = 0; r < kPerThread; r++) {
-    const uint32_t t = first + r * kThreads;
-    c[r] = t < count ? token_cell(table + (uint64_t)t * width, width, sroots) : kAbsent;
-  }
+    for (uint32_t r = 0; r < 8; r++) {
+      const uint32_t t = first + (pass + r) * kBuildThreads;
+      c[r] = pass + r < per && t < count ? token_cell(table + (uint64_t)t * width, width, sroots)
+                                         : kAbsent;
+    }
 #pragma unroll
-  for (uint32_t r = 0; r < kPerThread; r++) {
-    const uint32_t t = first + r * kThreads;
-    if (t < count) {
-      cells[t] = c[r];
-      atomicAdd(&hist[c[r] == kAbsent ? kCells : c[r]], 1u);
+    for (uint32_t r = 0; r < 8; r++) {
+      const uint32_t t = first + (pass + r) * kBuildThreads;
+      if (pass + r < per && t < count) {
+        cells[t] = c[r];
+        atomicAdd(&hist[c[r] == kAbsent ? kCells : c[r]], 1u);
+      }
     }
   }
   __syncthreads();
-  for (uint32_t i = threadIdx.x; i < kSlots; i += kThreads)
+  for (uint32_t i = threadIdx.x; i < kSlots; i += kBuildThreads)
     counts[(uint64_t)i * tiles + blockIdx.x] = hist[i];
 }
 
-// One block per slot: the exclusive scan of the slot's tile counts (in place) and its total.
+// One block per slot: the exclusive scan of the slot's tile counts (in place: each tile's
+// start within the slot) and the slot's total.
 __global__ __launch_bounds__(kThreads) void index_scan_tiles(uint32_t *counts, uint32_t tiles,
                                                              uint32_t *totals) {
   __shared__ uint32_t buf[kThreads];
@@ -138,7 +169,7 @@ __global__ __launch_bounds__(kThreads) void index_scan_tiles(uint32_t *counts, u
   for (uint32_t base = 0; base < tiles; base += kThreads) {
     const uint32_t i = base + threadIdx.x;
     const uint32_t v = i < tiles ? row[i] : 0;
-    const uint32_t incl = block_scan(v, buf);
+    const uint32_t incl = block_scan<kThreads>(v, buf);
     if (i < tiles) row[i] = carry + incl - v;
     carry += buf[kThreads - 1];
     __syncthreads();
@@ -146,53 +177,87 @@ __global__ __launch_bounds__(kThreads) void index_scan_tiles(uint32_t *counts, u
   if (threadIdx.x == 0) totals[blockIdx.x] = carry;
 }
 
-// Stable scatter of each tile's tokens; block 0 also writes offsets, the absent count and the
-// status.
-__global__ __launch_bounds__(kThreads) void index_scatter(
-    const uint32_t *__restrict__ cells, uint32_t count, const uint32_t *__restrict__ starts,
-    uint32_t tiles, const uint32_t *__restrict__ totals, uint32_t allow_absent,
+// Stable scatter of one tile: its tokens are ordered by (cell, token) in LDS, then each cell's
+// run is written to members contiguously (runs of tile/256 members on average, so the writes
+// coalesce). A token's place in its cell's run: the run's earlier rounds, the earlier waves of
+// its round (per-wave counts) and the earlier lanes of its wave with the same cell (a match of
+// the cell's 8 bits over ballots). Block 0 also writes offsets, the absent count and status.
+__global__ __launch_bounds__(kBuildThreads) void index_scatter(
+    const uint32_t *__restrict__ cells, uint32_t count, uint32_t per,
+    const uint32_t *__restrict__ starts, uint32_t tiles, const uint32_t *__restrict__ totals,
+    uint32_t allow_absent,
     uint32_t *__restrict__ offsets, uint32_t *__restrict__ members,
     uint32_t *__restrict__ absent_count, int32_t *__restrict__ status) {
-  __shared__ uint32_t buf[kThreads];
+  __shared__ uint32_t sorted[kMaxTile];
+  __shared__ uint32_t buf[kBuildThreads];
+  __shared__ uint32_t lstart[kSlots];  // each cell's run within the tile's sorted tokens
+  __shared__ uint32_t gbase[kCells];   // each cell's run within members
   __shared__ uint32_t cursor[kCells];
-  __shared__ uint32_t wave_hist[kWaves][kCells];
-  const uint32_t tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
-  const uint32_t v = totals[tid];
-  const uint32_t incl = block_scan(v, buf);
-  if (blockIdx.x == 0) {
-    offsets[tid] = incl - v;
-    if (tid == kThreads - 1) {
+  __shared__ uint32_t wave_cnt[kBuildWaves][kCells];
+  const uint32_t tid = threadIdx.x, lane = tid % 64, wave = tid / 64, tile = blockIdx.x;
+  const bool is_cell = tid < kCells;
+  // Cell offsets: the exclusive scan of the cells' totals.
+  const uint32_t total = is_cell ? totals[tid] : 0;
+  const uint32_t incl = block_scan<kBuildThreads>(total, buf);
+  const uint32_t cell_base = incl - total;
+  if (tile == 0 && is_cell) {
+    offsets[tid] = cell_base;
+    if (tid == kCells - 1) {
       offsets[kCells] = incl;
       const uint32_t absent = totals[kCells];
       *absent_count = absent;
       *status = absent && !allow_absent ? kNonRoot : kOk;
     }
   }
-  cursor[tid] = incl - v + starts[(uint64_t)tid * tiles + blockIdx.x];
-  for (uint32_t w = 0; w < kWaves; w++) wave_hist[w][tid] = 0;
+  // This tile's count of each cell, from its start and the next tile's.
+  uint32_t here = 0;
+  if (is_cell) {
+    const uint32_t start = starts[(uint64_t)tid * tiles + tile];
+    const uint32_t next = tile + 1 < tiles ? starts[(uint64_t)tid * tiles + tile + 1] : total;
+    here = next - start;
+    gbase[tid] = cell_base + start;
+    cursor[tid] = 0;
+  }
+  __syncthreads();  // buf is reused by the next scan
+  const uint32_t lincl = block_scan<kBuildThreads>(here, buf);
+  if (is_cell) lstart[tid] = lincl - here;
+  if (tid == kCells - 1) lstart[kCells] = lincl;
+  for (uint32_t i = tid; i < kBuildWaves * kCells; i += kBuildThreads) (&wave_cnt[0][0])[i] = 0;
   __syncthreads();
-  const uint32_t first = blockIdx.x * kTile + tid;
-  for (uint32_t r = 0; r < kPerThread; r++) {
-    const uint32_t t = first + r * kThreads;
+  const uint64_t below = (1ull << lane) - 1;
+  for (uint32_t r = 0; r < per; r++) {
+    const uint32_t t = (tile * per + r) * kBuildThreads + tid;
     const uint32_t c = t < count ? cells[t] : kAbsent;
-    if (c != kAbsent) atomicAdd(&wave_hist[wave][c], 1u);
-    // Earlier lanes of this wave with the same cell.
-    uint32_t rank = 0;
-    for (uint32_t j = 0; j < 64; j++)
-      rank += j < lane && (uint32_t)__builtin_amdgcn_readlane((int)c, (int)j) == c;
+    const bool valid = c != kAbsent;
+    uint64_t peers = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 8; b++) {
+      const bool bit = (c >> b) & 1;
+      const uint64_t m = __ballot(bit);
+      peers &= bit ? m : ~m;
+    }
+    if (valid && (peers & below) == 0) wave_cnt[wave][c] = __popcll(peers);
     __syncthreads();
-    if (c != kAbsent) {
-      for (uint32_t w = 0; w < wave; w++) rank += wave_hist[w][c];
-      members[cursor[c] + rank] = t;
+    if (valid) {
+      uint32_t rank = cursor[c] + __popcll(peers & below);
+      for (uint32_t w = 0; w < wave; w++) rank += wave_cnt[w][c];
+      sorted[lstart[c] + rank] = t;
     }
     __syncthreads();
-    uint32_t add = 0;
-    for (uint32_t w = 0; w < kWaves; w++) {
-      add += wave_hist[w][tid];
-      wave_hist[w][tid] = 0;
+    if (is_cell) {
+      uint32_t add = 0;
+      for (uint32_t w = 0; w < kBuildWaves; w++) {
+        add += wave_cnt[w][tid];
+        wave_cnt[w][tid] = 0;
+      }
+      cursor[tid] += add;
     }
-    cursor[tid] += add;
     __syncthreads();
+  }
+  const uint32_t n = lstart[kCells];
+  for (uint32_t i = tid; i < n; i += kBuildThreads) {
+    const uint32_t c = cell_at(lstart, i);
+    members[gbase[c] + (i - lstart[c])] = sorted[i];
   }
 }
 
@@ -230,12 +295,7 @@ __global__ __launch_bounds__(kThreads) void index_verify(
   if (!bad) {
     for (uint32_t p = blockIdx.x * kThreads + tid; p < size; p += stride) {
       const uint32_t m = members[p];
-      uint32_t lo = 0, hi = kCells;  // the cell holding p: soff[lo] <= p < soff[lo + 1]
-      while (hi - lo > 1) {
-        const uint32_t mid = (lo + hi) / 2;
-        if (soff[mid] <= p) lo = mid; else hi = mid;
-      }
-      if (m >= count || (p > soff[lo] && members[p - 1] >= m)) bad = 1;
+      if (m >= count || (p > soff[cell_at(soff, p)] && members[p - 1] >= m)) bad = 1;
     }
   }
   if (what == 2) {
@@ -671,15 +731,15 @@ extern "C" int uor_fbs_index_build_async(const int32_t *table, uint32_t count, u
       !workspace || !status || count == 0 || count > UOR_FBS_INDEX_MAX_TOKENS)
     return UOR_FBS_ERR_ARGUMENT;
   hipStream_t s = (hipStream_t)stream;
-  const uint32_t tiles = tiles_of(count);
+  const uint32_t per = rounds_of(count), tiles = tiles_of(count);
   uint32_t *counts = (uint32_t *)workspace + kHeader;
   uint32_t *totals = counts + (uint64_t)kSlots * tiles;
-  hipLaunchKernelGGL(index_cells, dim3(tiles), dim3(kThreads), 0, s, table, count, width, roots,
-                     tiles, cells, counts);
+  hipLaunchKernelGGL(index_cells, dim3(tiles), dim3(kBuildThreads), 0, s, table, count, width, roots,
+                     per, tiles, cells, counts);
   hipLaunchKernelGGL(index_scan_tiles, dim3(kSlots), dim3(kThreads), 0, s, counts, tiles,
                      totals);
-  hipLaunchKernelGGL(index_scatter, dim3(tiles), dim3(kThreads), 0, s, cells, count, counts,
-                     tiles, totals, allow_absent, offsets, members, absent_count, status);
+  hipLaunchKernelGGL(index_scatter, dim3(tiles), dim3(kBuildThreads), 0, s, cells, count, per,
+                     counts, tiles, totals, allow_absent, offsets, members, absent_count, status);
   return launched();
 }
 

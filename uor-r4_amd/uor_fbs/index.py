@@ -32,6 +32,41 @@ MAX_WIDTH = 256
 MAX_TOKENS = 1 << 30
 
 
+# The reference's 16 roots (src/codebook.cpp:5-14), the table its inverted file and tests use.
+CODEBOOK = np.array([
+    [2, 2, 0, 0, 0, 0, 0, 0], [-2, -2, 0, 0, 0, 0, 0, 0], [-2, 2, 0, 0, 0, 0, 0, 0],
+    [0, 0, -2, 0, -2, 0, 0, 0], [0, 0, -2, 0, 2, 0, 0, 0], [0, 0, 0, -2, 0, 0, 0, -2],
+    [0, 0, 0, -2, 0, 0, 0, 2], [0, 0, 0, 0, 0, -2, -2, 0], [0, 0, 0, 0, 0, -2, 2, 0],
+    [0, 0, 0, 0, 0, 2, -2, 0], [0, 0, 0, 0, 0, 2, 2, 0], [0, 0, 0, 2, 0, 0, 0, -2],
+    [0, 0, 0, 2, 0, 0, 0, 2], [0, 0, 2, 0, -2, 0, 0, 0], [0, 0, 2, 0, 2, 0, 0, 0],
+    [2, -2, 0, 0, 0, 0, 0, 0]], dtype=np.int32)
+
+
+def seeded_table(count: int) -> np.ndarray:
+    """The reference tests' seeded width-32 table (tests/inverted_file_test.cpp:39-53,
+    token_at / table_of): token i's endpoints are roots (7i+1) mod 16 and (11i+3) mod 16, its
+    middle blocks (29i+7d) mod 37 - 18 and (13i+5d) mod 41 - 20."""
+    i = np.arange(count, dtype=np.int64)[:, None]
+    d = np.arange(8, dtype=np.int64)[None, :]
+    t = np.empty((count, 4, 8), np.int32)
+    t[:, 0] = CODEBOOK[(i[:, 0] * 7 + 1) % 16]
+    t[:, 1] = (i * 29 + d * 7) % 37 - 18
+    t[:, 2] = (i * 13 + d * 5) % 41 - 20
+    t[:, 3] = CODEBOOK[(i[:, 0] * 11 + 3) % 16]
+    return t.reshape(count, 32)
+
+
+def seeded_query(seed: int) -> np.ndarray:
+    """The reference tests' query (tests/inverted_file_test.cpp:63-71, query_at)."""
+    d = np.arange(8, dtype=np.int64)
+    q = np.empty((4, 8), np.int32)
+    q[0] = CODEBOOK[seed % 16]
+    q[1] = (seed * 11 + d * 3) % 23 - 11
+    q[2] = (seed * 17 + d * 2) % 19 - 9
+    q[3] = CODEBOOK[(seed * 5 + 1) % 16]
+    return q.reshape(32)
+
+
 class Status(enum.IntEnum):
     """uor_inverted_file::Status (hpp:29-37); the CUDA and telemetry values have no use here."""
     Ok = 0
@@ -244,5 +279,5 @@ def full_scan(table: Table, queries, k: int, index: Index | None = None) -> Scan
     return _scan(hip.lib().uor_fbs_index_full_scan_async, table, queries, k, index.offsets, None)
 
 
-__all__ = ["ABSENT", "Status", "HostIndex", "ScanResult", "Table", "Index", "build", "update",
+__all__ = ["ABSENT", "CODEBOOK", "seeded_table", "seeded_query", "Status", "HostIndex", "ScanResult", "Table", "Index", "build", "update",
            "remove_token", "validate", "validate_structure", "probe", "full_scan"]
