@@ -305,16 +305,21 @@ __device__ __forceinline__ void wait_lds_dma() {
   wave_sync();
 }
 
+// A row of d channels is 4 (d / 32) pieces of 16 bytes (8 channels). The S lanes of a row
+// group take pieces sub + S w (w < 4), so each of the four loads reads S consecutive pieces of
+// every row (whole 128-byte spans for S = 8) rather than one piece of each 64-byte segment.
 struct ScanGeom {
-  uint32_t grp, sub;  // this lane's row within a round and its 32-channel segment
-  uint32_t mask;      // all ones when the lane's segment lies inside the row
+  uint32_t grp, sub;  // this lane's row within a round and its first piece
   uint32_t stride;    // row stride in table words (d)
+  uint32_t last;      // the row's last piece
+  uint32_t valid;     // bit w: piece sub + S w lies inside the row
+  bool full;          // every lane's four pieces lie inside the row (d = 32 S)
 };
 
 // Loads the rows of U row groups starting at candidate k0 (ids from the LDS list, or base_id + k
 // for the nearest head). Addresses are clamped into range so that every lane loads. Row offsets
 // fit 24-bit products (vocab < 2^24, d <= 1024).
-template <int S, int U>
+template <int S, int U, bool Full>
 __device__ __forceinline__ void scan_load(const DevModel &M, const uint32_t *list, uint32_t fill,
                                           uint32_t k0, const ScanGeom &g, uint32_t base_id,
                                           uint4 (&r)[U][4], uint32_t (&t)[U]) {
@@ -324,30 +329,52 @@ __device__ __forceinline__ void scan_load(const DevModel &M, const uint32_t *lis
     uint32_t k = k0 + u * rows + g.grp;
     k = k < fill ? k : fill - 1;
     t[u] = list ? list[k] : base_id + k;
-    const uint4 *row = (const uint4 *)(M.table_b + __umul24(t[u], g.stride) + 32u * g.sub);
+    const uint4 *row = (const uint4 *)(M.table_b + __umul24(t[u], g.stride));
+    if (Full) {
 #pragma unroll
-    for (int w = 0; w < 4; w++) r[u][w] = row[w];
+      for (int w = 0; w < 4; w++) r[u][w] = row[g.sub + S * w];
+    } else {
+#pragma unroll
+      for (int w = 0; w < 4; w++) {
+        const uint32_t piece = g.sub + S * w;
+        r[u][w] = row[piece <= g.last ? piece : g.last];
+      }
+    }
   }
 }
 
-template <int S, int U>
+template <int S, int U, bool Full>
 __device__ __forceinline__ uint64_t scan_score(const uint32_t (&qpk)[16], uint32_t fill,
                                                uint32_t k0, const ScanGeom &g,
                                                const uint4 (&r)[U][4], const uint32_t (&t)[U],
                                                uint64_t best) {
   constexpr uint32_t rows = kWave / S;
   uint32_t acc[U];
+  if (Full) {
 #pragma unroll
-  for (int u = 0; u < U; u++) {
-    acc[u] = 0;
+    for (int u = 0; u < U; u++) {
+      acc[u] = 0;
 #pragma unroll
-    for (int w = 0; w < 4; w++) {
-      acc[u] = sad2_u16(r[u][w].x, qpk[4 * w + 0], acc[u]);
-      acc[u] = sad2_u16(r[u][w].y, qpk[4 * w + 1], acc[u]);
-      acc[u] = sad2_u16(r[u][w].z, qpk[4 * w + 2], acc[u]);
-      acc[u] = sad2_u16(r[u][w].w, qpk[4 * w + 3], acc[u]);
+      for (int w = 0; w < 4; w++) {
+        acc[u] = sad2_u16(r[u][w].x, qpk[4 * w + 0], acc[u]);
+        acc[u] = sad2_u16(r[u][w].y, qpk[4 * w + 1], acc[u]);
+        acc[u] = sad2_u16(r[u][w].z, qpk[4 * w + 2], acc[u]);
+        acc[u] = sad2_u16(r[u][w].w, qpk[4 * w + 3], acc[u]);
+      }
     }
-    acc[u] &= g.mask;
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      acc[u] = 0;
+#pragma unroll
+      for (int w = 0; w < 4; w++) {
+        uint32_t a = sad2_u16(r[u][w].x, qpk[4 * w + 0], 0);
+        a = sad2_u16(r[u][w].y, qpk[4 * w + 1], a);
+        a = sad2_u16(r[u][w].z, qpk[4 * w + 2], a);
+        a = sad2_u16(r[u][w].w, qpk[4 * w + 3], a);
+        acc[u] += (g.valid >> w) & 1 ? a : 0;  // a piece past the row's end adds nothing
+      }
+    }
   }
   group_sums<S, U>(acc);
 #pragma unroll
@@ -360,23 +387,32 @@ __device__ __forceinline__ uint64_t scan_score(const uint32_t (&qpk)[16], uint32
 }
 
 // Lowest (L1, token) over `fill` >= 1 candidates, two stages in flight: the rows of the next U
-// row groups load while the current ones are scored.
-template <int S>
-__device__ __forceinline__ uint64_t scan_list(const DevModel &M, const uint32_t (&qpk)[16],
+// row groups load while the current ones are scored. Full: every piece of every lane lies
+// inside the row (compiled apart, so that the common widths carry no clamps or masks).
+template <int S, bool Full>
+__device__ __forceinline__ uint64_t scan_rows(const DevModel &M, const uint32_t (&qpk)[16],
                                               const uint32_t *list, uint32_t fill,
                                               uint32_t base_id, const ScanGeom &g, uint64_t best) {
   constexpr int U = kScanUnroll;
   constexpr uint32_t chunk = (kWave / S) * U;
   uint4 ra[U][4], rb[U][4];
   uint32_t ta[U], tb[U];
-  scan_load<S, U>(M, list, fill, 0, g, base_id, ra, ta);
+  scan_load<S, U, Full>(M, list, fill, 0, g, base_id, ra, ta);
   for (uint32_t k0 = 0; k0 < fill; k0 += 2 * chunk) {
-    scan_load<S, U>(M, list, fill, k0 + chunk, g, base_id, rb, tb);
-    best = scan_score<S, U>(qpk, fill, k0, g, ra, ta, best);
-    scan_load<S, U>(M, list, fill, k0 + 2 * chunk, g, base_id, ra, ta);
-    best = scan_score<S, U>(qpk, fill, k0 + chunk, g, rb, tb, best);
+    scan_load<S, U, Full>(M, list, fill, k0 + chunk, g, base_id, rb, tb);
+    best = scan_score<S, U, Full>(qpk, fill, k0, g, ra, ta, best);
+    scan_load<S, U, Full>(M, list, fill, k0 + 2 * chunk, g, base_id, ra, ta);
+    best = scan_score<S, U, Full>(qpk, fill, k0 + chunk, g, rb, tb, best);
   }
   return best;
+}
+
+template <int S>
+__device__ __forceinline__ uint64_t scan_list(const DevModel &M, const uint32_t (&qpk)[16],
+                                              const uint32_t *list, uint32_t fill,
+                                              uint32_t base_id, const ScanGeom &g, uint64_t best) {
+  return g.full ? scan_rows<S, true>(M, qpk, list, fill, base_id, g, best)
+                : scan_rows<S, false>(M, qpk, list, fill, base_id, g, best);
 }
 
 // Drawers per lane held in registers by the writer (models of at most 64 kDrawerRegs drawers);
@@ -407,23 +443,29 @@ __device__ __forceinline__ void load_drawers(const DevModel &M, uint32_t lane, D
   }
 }
 
-// The scan geometry of this lane (S lanes per row, lane groups of S) and its 32-channel segment
-// of the query as biased pairs: (q[2i] + 2^15) | (q[2i+1] + 2^15) << 16.
+// The scan geometry of this lane (S lanes per row, lane groups of S) and its four pieces of
+// the query as biased pairs: qpk[4 w + j] = (q[c] + 2^15) | (q[c + 1] + 2^15) << 16 with
+// c = 8 (sub + S w) + 2 j.
 template <int S>
 __device__ __forceinline__ void scan_setup(const DevModel &M, const int32_t *q, uint32_t lane,
                                            ScanGeom &g, uint32_t (&qpk)[16]) {
-  const uint32_t d = M.d, segs = d >> 5;  // S is the power of two >= segs
+  const uint32_t d = M.d, pieces = d >> 3;  // S is the power of two >= d / 32
   g.grp = lane / S;
   g.stride = d;
-  const uint32_t sub = lane % S;
-  // Lanes past the row's last 32-channel segment (widths that are not a power-of-two multiple
-  // of 32) read the last segment again and add zero.
-  g.sub = sub < segs ? sub : segs - 1;
-  g.mask = sub < segs ? 0xffffffffu : 0u;
+  g.sub = lane % S;
+  g.last = pieces - 1;
+  g.full = uniform32(pieces == 4 * S);
+  g.valid = 0;
 #pragma unroll
-  for (int i = 0; i < 16; i++)
-    qpk[i] = (uint32_t)(q[32 * g.sub + 2 * i] + 32768) |
-             ((uint32_t)(q[32 * g.sub + 2 * i + 1] + 32768) << 16);
+  for (int w = 0; w < 4; w++) {
+    const uint32_t piece = g.sub + S * w;
+    const bool in = piece < pieces;
+    g.valid |= (uint32_t)in << w;
+    const uint32_t c = 8 * (in ? piece : 0);
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      qpk[4 * w + j] = (uint32_t)(q[c + 2 * j] + 32768) | ((uint32_t)(q[c + 2 * j + 1] + 32768) << 16);
+  }
 }
 
 // The whole-table nearest head over tokens [lo, hi) (session.rs:4418-4445).
