@@ -497,6 +497,7 @@ struct Top8 {
     for (int i = 0; i < 8; i++) d[i] = kFar, t[i] = kAbsent;
   }
   __device__ void add(int64_t x, uint32_t y) {
+    if (!before(x, y, d[7], t[7])) return;  // most candidates, once the list is full
     // From the bottom up: entry i takes entry i - 1 when the new pair sorts before that too,
     // else the new pair when it sorts before entry i.
 #pragma unroll
@@ -537,16 +538,23 @@ __device__ __forceinline__ int64_t l1_8(const int32_t *q, const int32_t *r) {
   return s;
 }
 
-// L1 between the query (LDS) and a table row, 16-byte loads.
+// |a - b| of two int32 values, exact in 32 unsigned bits.
+__device__ __forceinline__ uint32_t absdiff32(int32_t a, int32_t b) {
+  return a > b ? (uint32_t)a - (uint32_t)b : (uint32_t)b - (uint32_t)a;
+}
+
+// L1 between the query (LDS) and a table row, 16-byte loads; each difference in 32 bits, the
+// sum in 64.
 __device__ __forceinline__ int64_t row_l1(const int32_t *q, const int32_t *row, uint32_t width) {
-  int64_t s = 0;
+  uint64_t s = 0;
   for (uint32_t i = 0; i < width; i += 4) {
     const int4 a = *(const int4 *)(row + i), b = *(const int4 *)(q + i);
-    const int64_t x = (int64_t)b.x - a.x, y = (int64_t)b.y - a.y, z = (int64_t)b.z - a.z,
-                  w = (int64_t)b.w - a.w;
-    s += (x < 0 ? -x : x) + (y < 0 ? -y : y) + (z < 0 ? -z : z) + (w < 0 ? -w : w);
+    s += absdiff32(b.x, a.x);
+    s += absdiff32(b.y, a.y);
+    s += absdiff32(b.z, a.z);
+    s += absdiff32(b.w, a.w);
   }
-  return s;
+  return (int64_t)s;
 }
 
 // fill_admitted (inverted_file.cpp:83-96) on one wave: the k nearest non-empty cells by
