@@ -44,6 +44,25 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 # Measured HBM bytes per launch of the decode kernel (rocprofv3 FETCH_SIZE and WRITE_SIZE passes,
 # scaled by a copy kernel's reading), for the workload it names.
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fbs_decode_pair_c3_b1024_traffic.md")
+# BASELINE.json's configs at their full shapes: (sequences, prompt, decode steps); c4 is
+# teacher-forced scoring of (rows, row length).
+CONFIG_SHAPES = {"c1": (1, 256, 256), "c2": (1024, 512, 512), "c3": (1024, 1024, 1024),
+                 "c4": (1 << 20, 128, 0), "c5": (16384, 4096, 4096)}
+
+
+def log(msg: str):
+    """A progress line on stderr (stdout carries only the JSON line)."""
+    print(f"bench.py: {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def parse():
@@ -51,10 +70,11 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=3)
     p.add_argument("--warmup", type=int, default=1)
-    p.add_argument("--config", default="c3", choices=["c2", "c3", "c5"])
-    p.add_argument("--batch", type=int, default=1024)
-    p.add_argument("--prompt", type=int, default=1024)
-    p.add_argument("--gen", type=int, default=1024)
+    p.add_argument("--config", default="c3", choices=sorted(CONFIG_SHAPES),
+                   help="BASELINE's configs: c3 (default) is the metric's; c4 scores rows")
+    p.add_argument("--batch", type=int, default=None, help="sequences (c4: rows); config's default")
+    p.add_argument("--prompt", type=int, default=None, help="prompt tokens (c4: row length)")
+    p.add_argument("--gen", type=int, default=None, help="decode steps per timed step")
     p.add_argument("--seed", type=int, default=2026120203)
     p.add_argument("--cpu-seconds", type=float, default=24.0, help="target CPU-baseline sample time")
     p.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cores)")
@@ -68,7 +88,12 @@ def parse():
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="only run one elementwise copy kernel over this many MiB (the reference "
                         "reading for the FETCH_SIZE / WRITE_SIZE counters) and exit")
-    return p.parse_args()
+    a = p.parse_args()
+    batch, prompt, gen = CONFIG_SHAPES[a.config]
+    a.batch = batch if a.batch is None else a.batch
+    a.prompt = prompt if a.prompt is None else a.prompt
+    a.gen = gen if a.gen is None else a.gen
+    return a
 
 
 def copy_probe(mib: int):
@@ -287,6 +312,93 @@ def index_section(torch, dev, stream, sp, large: int) -> dict:
     return out
 
 
+def score_main(a, torch, oracle, art, model, rows, dev, stream, sp) -> dict:
+    """C4: teacher-forced scoring of `batch` rows of `prompt` tokens; a step is one score launch
+    over every row (each position's choice compared with the next token, the matches summed)."""
+    from uor_fbs import hip
+    L = hip.lib()
+    spec = art.spec
+    R, n = a.batch, a.prompt
+    d_rows = torch.from_numpy(np.ascontiguousarray(rows, np.uint32).view(np.int32)).to(dev)
+    matches = torch.zeros(1, dtype=torch.int64, device=dev)
+    status = torch.zeros(R, dtype=torch.int32, device=dev)
+
+    def step():
+        matches.zero_()
+        code = L.uor_fbs_score_async(model.handle, C.c_void_p(d_rows.data_ptr()), R, n, None,
+                                     C.c_void_p(matches.data_ptr()),
+                                     C.c_void_p(status.data_ptr()), sp)
+        if code:
+            raise hip.FbsError(code, L.uor_fbs_last_error().decode())
+
+    log(f"c4: scoring {R} rows x {n}")
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(a.steps)]
+    t0 = time.perf_counter()
+    for s_, e_ in ev:
+        s_.record(stream)
+        step()
+        e_.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    assert int(status.abs().sum()) == 0, "scoring failed"
+    launch_ms = [s_.elapsed_time(e_) for s_, e_ in ev]
+    ms_per_step = wall * 1e3 / a.steps
+    positions = R * n
+    sample = min(R, 64)
+    _, kept, _ = model.sequences(rows[:sample])
+    cand = art.drawer_sizes()[kept.astype(np.int64)].sum(-1)
+    mean_cand = float(cand.mean())
+    bpt = algorithmic_bytes_per_token(spec, mean_cand) + 4  # plus each position's input id
+    achieved = bpt * positions / (float(np.mean(launch_ms)) / 1e3) / 1e9
+    S = 1
+    while S < spec.width // 32:
+        S *= 2
+    family = "fbs_rows_pair" if model.block_waves(R) == 2 else "fbs_rows"
+    out = {
+        "metric": f"teacher-forced scored positions/sec, {R} rows x {n}, width {spec.width} (1 GPU)",
+        "value": round(positions / (ms_per_step / 1e3), 1), "unit": "positions/s", "n_gpus": 1,
+        "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int64",
+        "data": "synthetic (seeded integer artifact and Zipf rows)",
+        "config": {"workload": f"c4 artifact: {R} Zipf(1.1) rows of {n} tokens scored per timed "
+                               f"step", "key": workload_key(a), "width": spec.width,
+                   "layers": spec.layers, "vocab": spec.vocab, "window": spec.window,
+                   "drawers": art.drawers, "probes": art.probes, "rows": R, "row_length": n,
+                   "parallelism": "none (1 GPU)"},
+        "matches": int(matches.item()),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_position": round(bpt, 1), "mean_candidate_rows": round(mean_cand, 1),
+                     "kernel": f"{family}<{(spec.width // 4 + 63) // 64}, {S}>",
+                     "launch_ms": [round(x, 3) for x in launch_ms]},
+    }
+    if not a.no_cpu:
+        log("c4: CPU baseline")
+        threads = a.cpu_threads or min(16, os.cpu_count() or 1)
+        t0 = time.perf_counter()
+        oracle.score(art, rows[:threads], threads=threads)
+        per_row = (time.perf_counter() - t0) / threads
+        n_cpu = int(min(R, max(threads, a.cpu_seconds / per_row)))
+        n_cpu -= n_cpu % threads if n_cpu > threads else 0
+        t0 = time.perf_counter()
+        st, cpu_matches, cpu_argmin = oracle.score(art, rows[:n_cpu], threads=threads)
+        cpu_s = time.perf_counter() - t0
+        gpu_matches, gpu_argmin = model.score(rows[:n_cpu])
+        same = st == 0 and cpu_matches == gpu_matches and np.array_equal(cpu_argmin, gpu_argmin)
+        out["cpu_baseline"] = {
+            "value": round(n_cpu * n / cpu_s, 1), "unit": "positions/s",
+            "cores": min(threads, n_cpu), "cpu_model": cpu_model(), "kind": "port",
+            "sample": f"the first {n_cpu} of the {R} rows ({cpu_s:.1f} s), oracle C restatement, "
+                      f"one row per thread", "choices_equal_gpu": bool(same)}
+        if not same:
+            print("bench.py: CPU scoring differs from the GPU's", file=sys.stderr)
+    return out
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -309,10 +421,14 @@ def main():
     else:
         prompts = synth.uniform_prompts(spec.vocab, a.batch, a.prompt, a.seed + 1)
     model = hip.Model(art, device=0)
+    log(f"{a.config}: artifact and inputs ready")
     L = hip.lib()
     dev = torch.device("cuda:0")
     stream = torch.cuda.current_stream(dev)
     sp = C.c_void_p(stream.cuda_stream)
+    if a.config == "c4":
+        print(json.dumps(score_main(a, torch, oracle, art, model, prompts, dev, stream, sp)))
+        return
     B, G = a.batch, a.gen
     sw, hw = model.state_words, model.history_words
 
@@ -340,6 +456,7 @@ def main():
     torch.cuda.synchronize()
     prefill_s = time.perf_counter() - t0
     assert int(status.abs().sum()) == 0, "prefill failed"
+    log(f"{a.config}: prefill {prefill_s:.1f} s")
 
     reply = torch.zeros((B, G), dtype=torch.int32, device=dev)
 
@@ -362,6 +479,7 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     assert int(status.abs().sum()) == 0, "decode failed"
+    log(f"{a.config}: {a.steps} timed steps, {wall:.1f} s")
     launch_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
     ms_per_step = wall * 1e3 / a.steps
     tokens = B * G
@@ -397,7 +515,7 @@ def main():
     traffic = measured_traffic(a, kernel)
 
     out = {
-        "metric": "decoded tokens/sec at batch 1024, width 256 (1 GPU)",
+        "metric": f"decoded tokens/sec at batch {B}, width {spec.width} (1 GPU)",
         "value": round(value, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -430,6 +548,8 @@ def main():
         },
         "prefill_tokens_per_s": round(B * a.prompt / prefill_s, 1),
     }
+    if B == 1:  # a latency: one sequence (the config's CPU-runnable case)
+        out["ms_per_token"] = round(ms_per_step / G, 5)
 
     if a.serve_steps:
         # The serving loop: every sequence is a session in a device slot (a fixed permutation of
@@ -479,9 +599,11 @@ def main():
         if not same_serve:
             print("bench.py: the serving loop's tokens differ from the decode's", file=sys.stderr)
 
-    index = None if a.no_index else index_section(torch, dev, stream, sp, a.index_large)
+    index = None if a.no_index or a.config != "c3" else index_section(torch, dev, stream, sp,
+                                                                          a.index_large)
 
     if not a.no_cpu:
+        log(f"{a.config}: CPU baseline")
         threads = a.cpu_threads or min(16, os.cpu_count() or 1)
         st_np = state.cpu().numpy()
         hist_np = hist.cpu().numpy()
@@ -504,8 +626,8 @@ def main():
         assert res["status"] == 0
         same = np.array_equal(res["reply"], host_reply[:n_cpu, :g_cpu])
         out["cpu_baseline"] = {
-            "value": round(n_cpu * g_cpu / cpu_s, 1), "unit": "tokens/s", "cores": threads,
-            "kind": "port",
+            "value": round(n_cpu * g_cpu / cpu_s, 1), "unit": "tokens/s",
+            "cores": min(threads, n_cpu), "cpu_model": cpu_model(), "kind": "port",
             "sample": f"{n_cpu} of the {B} prefilled sequences x the first {g_cpu} decode steps "
                       f"({cpu_s:.1f} s), oracle C restatement, one sequence per thread",
             "replies_equal_gpu": bool(same),
