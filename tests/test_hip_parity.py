@@ -166,6 +166,24 @@ def test_run_twice_is_identical_and_batch_independent():
         np.testing.assert_array_equal(x[17:18], y)
 
 
+def test_decode_batch_above_the_grid_matches_oracle():
+    # More sequences than resident blocks (at most one paired block per SIMD, 1,024 on MI355X):
+    # each block decodes several sequences in turn, each from its own fresh session. Sequences
+    # on both sides of the block boundaries must equal the oracle's, state and window included.
+    spec = reduced("c2", context=24, layers=2)
+    art = synth.make_artifact(spec, 58)
+    prompts = synth.uniform_prompts(spec.vocab, 2600, 8, 68)
+    model = Model(art)
+    out = model.decode(prompts, gen=12)
+    pick = np.array([0, 1, 1023, 1024, 1025, 2047, 2048, 2049, 2599])
+    ref = oracle.decode(art, prompts[pick], 12, threads=4)
+    assert ref["status"] == 0
+    np.testing.assert_array_equal(out["reply"][pick], ref["reply"])
+    np.testing.assert_array_equal(out["state"][pick], ref["state"])
+    np.testing.assert_array_equal(out["history"][pick], ref["history"])
+    np.testing.assert_array_equal(out["position"][pick], ref["position"])
+
+
 def test_repeated_queries_reuse_the_writer_exactly():
     # A token fed again and again settles the state, so consecutive queries repeat exactly and
     # the kernel takes the writer's last result instead of scanning again. Every position's
