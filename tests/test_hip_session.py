@@ -64,6 +64,27 @@ def test_serving_loop_equals_batched_decode(art):
         assert st.tokens == [int(t) for t in prompts[i]] + [int(t) for t in want["reply"][i, :G]]
 
 
+def test_pool_larger_than_the_grid(art):
+    # More live sessions than resident blocks (1,024 paired blocks on MI355X): one launch steps
+    # 2,600 sessions held in scrambled slots of a 3,000-slot pool, blocks looping over them.
+    # Each session's prompt feed and following steps must equal the batched decode's.
+    S, P, G = 2600, 6, 4
+    prompts = synth.uniform_prompts(SPEC.vocab, S, P, 83)
+    model = hip.Model(art)
+    want = model.decode(prompts, gen=G)
+    pool = SessionPool(model, capacity=3000)
+    slots = np.random.default_rng(9).permutation(3000)[:S].astype(np.uint32)
+    print(f"pool of {pool.capacity}: {S} sessions", flush=True)
+    out = pool.run(slots, prompts, gen=G)
+    assert (out["status"] == 0).all()
+    np.testing.assert_array_equal(out["reply"], want["reply"])
+    for i in (0, 1023, 1024, 2047, 2048, S - 1):
+        state, history, position = pool.read(int(slots[i]))
+        np.testing.assert_array_equal(state, want["state"][i])
+        np.testing.assert_array_equal(history, want["history"][i])
+        assert position == P + G
+
+
 def test_step_native_matches_the_oracle(art):
     tokens = synth.uniform_prompts(SPEC.vocab, 2, 14, 79)
     st, want_tok, want_kept, want_query = oracle.sequences(art, tokens, threads=2)
