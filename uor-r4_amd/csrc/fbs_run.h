@@ -416,8 +416,10 @@ __device__ __forceinline__ uint64_t scan_list(const DevModel &M, const uint32_t 
 }
 
 // Drawers per lane held in registers by the writer (models of at most 64 kDrawerRegs drawers);
-// larger drawer counts score through LDS.
+// up to 64 kScoreRegs drawers keep only their scores in registers; larger drawer counts score
+// through LDS.
 constexpr uint32_t kDrawerRegs = 4;
+constexpr uint32_t kScoreRegs = 16;
 
 // A lane's drawers c = lane + 64 i (i < kDrawerRegs): their two 8-value keys and CSR ranges.
 struct DrawerRegs {
@@ -542,6 +544,43 @@ __device__ __forceinline__ void writer_select(const DevModel &M, const int32_t *
       if (lane == 0) kept[p] = pick;
     }
     wave_sync();
+  } else if (M.head != 1 && M.D <= kWave * kScoreRegs) {
+    // Scores in registers (drawer c = lane + 64 i), keys read once; each round takes the
+    // wave's minimum and its owner lane retires it. Ranges load after the rounds.
+    uint32_t sc[kScoreRegs];
+#pragma unroll
+    for (uint32_t i = 0; i < kScoreRegs; i++) {
+      const uint32_t c = lane + kWave * i;
+      uint32_t s = UINT32_MAX;
+      if (c < M.D) {
+        const int4 *key = (const int4 *)(M.keys + 16u * c);
+        const int4 k4[2] = {key[0], key[1]};
+        const int16_t *kk = (const int16_t *)k4;
+        uint32_t v = 0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          v += uabs32(qa[j] - (int32_t)kk[j]);
+          v += uabs32(qb[j] - (int32_t)kk[8 + j]);
+        }
+        s = (v << 12) | c;
+      }
+      sc[i] = s;
+    }
+    for (uint32_t p = 0; p < M.P; p++) {
+      uint32_t local = sc[0];
+#pragma unroll
+      for (uint32_t i = 1; i < kScoreRegs; i++) local = sc[i] < local ? sc[i] : local;
+      const uint32_t pick = wave_reduce32(local, OpMin()) & 0xfffu;
+#pragma unroll
+      for (uint32_t i = 0; i < kScoreRegs; i++) sc[i] = (sc[i] & 0xfffu) == pick ? UINT32_MAX : sc[i];
+      if (lane == 0) kept[p] = pick;
+    }
+    wave_sync();
+    if (lane < M.P) {
+      const uint32_t c = kept[lane];
+      my_beg = M.offsets[c];
+      my_end = M.offsets[c + 1];
+    }
   } else {
     for (uint32_t c = lane; c < M.D; c += kWave) {
       const int4 *key = (const int4 *)(M.keys + 16u * c);
