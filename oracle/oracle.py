@@ -334,3 +334,55 @@ def ref_full_scan(table, query, k):
     adm, top, pred = _scan_out()
     st = if_ref().if_ref_full_scan(_vp(t), count, _vp(q), k, _vp(adm), _vp(top), C.byref(pred))
     return st, adm, top, pred.value
+
+
+# ---------------------------------------------------------------------------------------------
+# The discrete M1 evaluator (oracle/lib/libd11_oracle.so, d11_oracle.c).
+
+D11_SO = os.path.join(HERE, "lib", "libd11_oracle.so")
+_d11 = None
+
+
+def d11_lib():
+    global _d11
+    if _d11 is None:
+        if not os.path.exists(D11_SO):
+            raise FileNotFoundError(f"{D11_SO} is not built (make -C oracle)")
+        L = C.CDLL(D11_SO)
+        L.d11_oracle_score_rows.argtypes = [P, P, P, P, C.c_uint32, C.c_uint32, P, C.c_int]
+        L.d11_oracle_row_relation.argtypes = [P, P, C.c_int32, C.c_uint32, P, P]
+        L.d11_oracle_plan.argtypes = [C.c_int32, P, P]
+        _d11 = L
+    return _d11
+
+
+def d11_score_rows(art, prefixes, lengths, targets, threads=8):
+    """One uor_d11_row_out record per row (uor_fbs.d11.ROW_DTYPE), as the HIP scorer writes."""
+    from uor_fbs import d11
+    m, keep = d11.c_model(art)
+    prefixes = np.ascontiguousarray(prefixes, np.uint32)
+    rows, stride = prefixes.shape
+    lengths = np.ascontiguousarray(lengths, np.int32)
+    targets = np.ascontiguousarray(targets, np.uint32)
+    out = np.zeros(rows, d11.ROW_DTYPE)
+    d11_lib().d11_oracle_score_rows(C.byref(m), prefixes.ctypes.data, lengths.ctypes.data,
+                                    targets.ctypes.data, rows, stride, out.ctypes.data, threads)
+    return out
+
+
+def d11_row_relation(art, prefix, target=0):
+    """(record, relation scores (blocks, nodes)) of one row."""
+    from uor_fbs import d11
+    m, keep = d11.c_model(art)
+    prefix = np.ascontiguousarray(prefix, np.uint32)
+    out = np.zeros(1, d11.ROW_DTYPE)
+    rel = np.zeros(art.shape.blocks * 512, np.int32)
+    n = d11_lib().d11_oracle_row_relation(C.byref(m), prefix.ctypes.data, len(prefix), target,
+                                          out.ctypes.data, rel.ctypes.data)
+    return out[0], rel[:art.shape.blocks * n].reshape(art.shape.blocks, n)
+
+
+def d11_plan(length):
+    nodes, frontier = C.c_int32(), C.c_int32()
+    st = d11_lib().d11_oracle_plan(length, C.byref(nodes), C.byref(frontier))
+    return None if st else (nodes.value, frontier.value)

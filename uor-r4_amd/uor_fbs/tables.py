@@ -13,6 +13,14 @@ kept here as data (not code) and checked by closed-form tests:
   ``(a + b phi) / 2`` per coordinate, in the order built by
   ``historical_root_coefficients`` (crates/uor-r4-integer/src/h4_classifier.rs:20-76):
   8 axis roots, 16 half roots, then 12 even permutations x 8 sign choices.
+- ``BFS``: for orbit roots ``s`` and ``d``, the route state ``BFS[16 s + d]`` that carries root
+  ``s`` to root ``d`` (discrete_d11.rs:246-258, read by ``cl06_bfs`` :916-918); of the several
+  states that do, the table's own choice, so it is data.
+- ``BRANCH``: the three successor roots of each root on the discrete route's later stages
+  (discrete_d11.rs:259-276).
+- ``compose_table()``: the 64 x 64 product of route states, ``compose(a, b)`` the state acting
+  as ``a`` after ``b`` (the relation the reference's ``COMPOSE`` table holds,
+  discrete_d11.rs:57-226), derived here from ``AXES``.
 - ``keep_q31()``: ``isqrt(2^62 - 2^(60 - 2 i))``, the geometric drive weights
   (stack/session.rs:87-108).
 """
@@ -61,6 +69,22 @@ ROOTS = np.array([
     (2, -2, 0, 0, 0, 0, 0, 0),
 ], dtype=np.int32)
 
+BFS = np.array([
+    0, 16, 7, 42, 3, 8, 9, 27, 5, 24, 4, 47, 2, 12, 1, 34, 16, 0, 34, 1, 12, 2, 47, 4, 24, 5, 27, 9, 8, 3, 42, 7,
+    34, 7, 0, 26, 11, 9, 14, 10, 6, 4, 5, 2, 47, 1, 3, 16, 1, 42, 3, 0, 15, 4, 5, 8, 13, 9, 2, 10, 27, 7, 16, 48,
+    12, 3, 1, 7, 0, 5, 6, 9, 2, 41, 13, 4, 35, 16, 15, 11, 2, 8, 47, 27, 24, 0, 7, 1, 3, 12, 42, 34, 16, 5, 4, 9,
+    47, 9, 2, 10, 4, 34, 0, 3, 11, 1, 26, 16, 7, 6, 5, 14, 4, 27, 5, 2, 13, 42, 48, 0, 7, 15, 16, 3, 1, 9, 8, 10,
+    35, 5, 4, 9, 41, 12, 1, 15, 0, 16, 7, 11, 3, 2, 13, 6, 5, 35, 6, 13, 2, 3, 11, 7, 16, 0, 15, 1, 12, 41, 9, 4,
+    27, 4, 10, 8, 9, 1, 3, 16, 15, 7, 0, 48, 42, 13, 2, 5, 9, 47, 14, 5, 6, 7, 16, 26, 1, 11, 3, 0, 34, 4, 10, 2,
+    8, 2, 9, 4, 5, 16, 34, 42, 12, 3, 1, 7, 0, 24, 27, 47, 3, 12, 11, 15, 16, 35, 4, 13, 41, 2, 9, 6, 5, 0, 7, 1,
+    42, 1, 48, 16, 7, 27, 10, 2, 9, 13, 8, 5, 4, 15, 0, 3, 7, 34, 16, 3, 1, 47, 2, 5, 4, 6, 10, 14, 9, 11, 26, 0,
+], dtype=np.uint8)
+
+BRANCH = np.array([
+    0, 14, 3, 1, 3, 14, 2, 13, 4, 3, 0, 1, 4, 2, 15, 5, 7, 10, 6, 9, 8, 7, 12, 5,
+    8, 6, 11, 9, 11, 6, 10, 5, 12, 11, 8, 9, 12, 10, 7, 13, 15, 2, 14, 1, 0, 15, 4, 13,
+], dtype=np.uint8).reshape(16, 3)
+
 # Output axis -> base coordinate for the 12 even permutations of four axes
 # (h4_classifier.rs:23-36); base coordinates 1, 2, 3 carry the signs s1, s2, s3.
 EVEN_PERMUTATIONS = (
@@ -107,3 +131,28 @@ def roots_q12() -> np.ndarray:
 def axes_codes(state: int) -> np.ndarray:
     """The eight signed-axis codes of Cl(0,6) state ``state`` (< 64)."""
     return AXES[8 * state: 8 * state + 8]
+
+
+def act(state: int, x) -> np.ndarray:
+    """Route state ``state`` applied to an 8-vector: out[d] = +-x[code & 7] (code & 8 negates)."""
+    state = int(state)
+    codes = AXES[8 * state: 8 * state + 8]
+    x = np.asarray(x)
+    return np.where(codes & 8, -x[codes & 7], x[codes & 7])
+
+
+def compose_table() -> np.ndarray:
+    """(64, 64) uint8: entry (a, b) is the state c with act(c, x) == act(a, act(b, x))."""
+    probe = np.arange(1, 9)
+    index = {tuple(act(c, probe)): c for c in range(64)}
+    out = np.zeros((64, 64), np.uint8)
+    for a in range(64):
+        for b in range(64):
+            out[a, b] = index[tuple(act(a, act(b, probe)))]
+    return out
+
+
+def root_id(x) -> int:
+    """The orbit root equal to ``x``, or -1."""
+    hit = np.nonzero((ROOTS == np.asarray(x)).all(axis=1))[0]
+    return int(hit[0]) if len(hit) else -1
