@@ -354,3 +354,39 @@ def test_grid_descriptor_forms_equal_grid_apply(hp):
         np.array([0, 1, -1, 2**31 - 1, -2**31, 2**31, -2**31 - 1, 2**57 - 1, -(2**57 - 1), 2**57,
                   -2**57, 2**63 - 1, -2**63, 127, 128, -128, -129, 255, 256], dtype=np.int64)])
     assert hp.fbs_hp_grid_check(v.ctypes.data_as(P), len(v)) == 0
+
+
+def test_d11_library_exports_and_layout():
+    """include/uor_d11.h: every declared entry point is exported; the model image and the row
+    record have the layout the Python face writes and reads."""
+    from uor_fbs import d11
+    text = open(os.path.join(ROOT, "include", "uor_d11.h")).read()
+    names = set(re.findall(r"\b(uor_d11_[a-z0-9_]+)\s*\(", text))
+    assert names == set(d11.SYMBOLS)
+    L = d11.lib()
+    for name in names:
+        assert hasattr(L, name), name
+    assert L.uor_d11_abi_version() == 1
+    assert L.uor_d11_sizeof_row_out() == d11.ROW_DTYPE.itemsize == 656
+
+
+@pytest.mark.parametrize("edit,msg", [
+    (lambda a: setattr(a.shape, "stages", a.shape.stages + 1), b"shape"),
+    (lambda a: a.routes.__setitem__(0, 64), b"routes"),
+    (lambda a: a.gates.__setitem__(1, 2), b"gates"),
+    (lambda a: a.cells.__setitem__(3, a.cells[3] ^ 1), b"cells"),
+    (lambda a: a.table.__setitem__((2, 1, 0), 1), b"orbit"),
+    (lambda a: a.trunk.step_candidates.__setitem__(5, 16), b"step_candidates"),
+    (lambda a: a.trunk.sparse["query_table"].__setitem__((0, 2), 0), b"zero count"),
+])
+def test_d11_model_create_refuses_without_a_device(edit, msg):
+    """The library repeats the loader's checks before any device call."""
+    from uor_fbs import d11
+    art = d11.synthetic(vocabulary=64, context=12, seed=5, trunk_entries=50)
+    art.table, art.cells, art.routes, art.gates = (art.table.copy(), art.cells.copy(),
+                                                   art.routes.copy(), art.gates.copy())
+    edit(art)
+    m, keep = d11.c_model(art)
+    h = P()
+    assert d11.lib().uor_d11_model_create(C.byref(m), 0, C.byref(h)) == -1
+    assert msg in d11.lib().uor_d11_last_error()
