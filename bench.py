@@ -48,6 +48,17 @@ TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fbs_decode_pair_c3_b1024_traff
 # teacher-forced scoring of (rows, row length).
 CONFIG_SHAPES = {"c1": (1, 256, 256), "c2": (1024, 512, 512), "c3": (1024, 1024, 1024),
                  "c4": (1 << 20, 128, 0), "c5": (16384, 4096, 4096)}
+# The discrete M1 panel scorer (uor_d11_score_rows): the reference's ft/dev panel size, the M1
+# container's shape (vocabulary 4,096, 4 blocks, context 192, 8 kept cells, relation read
+# keeping 8 with 1 sweep, 19-table trunk), rows of 186-192 tokens (the published run's mean
+# context is 34,625,934 / 183,206 = 189 tokens per row).
+D11_ROWS = 14287
+D11_PUBLISHED = {
+    "value": 183206, "unit": "response tokens/s", "context_tokens_per_s": 34625934,
+    "hardware": "1x RTX 5090 (compute_120)", "rows": 14287,
+    "timing": "wall time of DeviceScorer::score (device.rs:120-210): host-to-device copies of "
+              "the rows, scratch allocation, launches and device-to-host copies of the records",
+    "source": "docs/loop/tasks/m1-close-saved-model/antigravity-110/REPORT.md:32, STATE.md:43"}
 
 
 def log(msg: str):
@@ -70,7 +81,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=3)
     p.add_argument("--warmup", type=int, default=1)
-    p.add_argument("--config", default="c3", choices=sorted(CONFIG_SHAPES),
+    p.add_argument("--config", default="c3", choices=sorted(CONFIG_SHAPES) + ["m1"],
                    help="BASELINE's configs: c3 (default) is the metric's; c4 scores rows")
     p.add_argument("--batch", type=int, default=None, help="sequences (c4: rows); config's default")
     p.add_argument("--prompt", type=int, default=None, help="prompt tokens (c4: row length)")
@@ -88,8 +99,10 @@ def parse():
     p.add_argument("--copy-probe-mib", type=int, default=0,
                    help="only run one elementwise copy kernel over this many MiB (the reference "
                         "reading for the FETCH_SIZE / WRITE_SIZE counters) and exit")
+    p.add_argument("--d11-trunk-entries", type=int, default=600_000,
+                   help="m1: (key, token) entries in each of the six trunk tables it reads")
     a = p.parse_args()
-    batch, prompt, gen = CONFIG_SHAPES[a.config]
+    batch, prompt, gen = CONFIG_SHAPES.get(a.config, (D11_ROWS, 192, 0))
     a.batch = batch if a.batch is None else a.batch
     a.prompt = prompt if a.prompt is None else a.prompt
     a.gen = gen if a.gen is None else a.gen
@@ -399,6 +412,106 @@ def score_main(a, torch, oracle, art, model, rows, dev, stream, sp) -> dict:
     return out
 
 
+def d11_main(a, torch, oracle) -> dict:
+    """The discrete M1 panel: a step is one uor_d11_score_rows launch over every row (each row's
+    read, admitted cells, top 8, hinges and losses)."""
+    from uor_fbs import d11
+    L = d11.lib()
+    art = d11.synthetic(seed=a.seed, trunk_entries=a.d11_trunk_entries)
+    R = a.batch
+    pre, lens, tg = d11.panel_rows(art, R, a.seed + 1, min_len=186)
+    ctx = art.shape.context
+    model = d11.IntegerDiscreteModel(art)
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    sp = C.c_void_p(stream.cuda_stream)
+    d_pre = torch.from_numpy(pre.view(np.int32)).to(dev)
+    d_len = torch.from_numpy(lens).to(dev)
+    d_tg = torch.from_numpy(tg.view(np.int32)).to(dev)
+    d_out = torch.zeros(R * d11.ROW_DTYPE.itemsize, dtype=torch.uint8, device=dev)
+    log(f"m1: {R} rows, {int(lens.sum())} context tokens, trunk tables of "
+        f"{a.d11_trunk_entries} entries")
+
+    def step():
+        code = L.uor_d11_score_rows_async(model.handle, C.c_void_p(d_pre.data_ptr()),
+                                          C.c_void_p(d_len.data_ptr()),
+                                          C.c_void_p(d_tg.data_ptr()), R, ctx,
+                                          C.c_void_p(d_out.data_ptr()), sp)
+        if code:
+            raise d11.DiscreteError(L.uor_d11_last_error().decode())
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(a.steps)]
+    t0 = time.perf_counter()
+    for s_, e_ in ev:
+        s_.record(stream)
+        step()
+        e_.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    launch_ms = [s_.elapsed_time(e_) for s_, e_ in ev]
+    recs = d_out.cpu().numpy().view(d11.ROW_DTYPE)
+    assert (recs["status"] == 0).all(), "rows failed"
+    ms_per_step = wall * 1e3 / a.steps
+    # The reference's timing includes the host copies: the same over host buffers.
+    host_ms = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        host = model.score_rows(pre, lens, tg)
+        host_ms.append((time.perf_counter() - t0) * 1e3)
+    assert np.array_equal(host.view(np.uint32), recs.view(np.uint32)), "host path differs"
+    host_best = min(host_ms)
+    bytes_per_row = 4 * float(lens.mean()) + 8 + d11.ROW_DTYPE.itemsize
+    achieved = bytes_per_row * R / (float(np.mean(launch_ms)) / 1e3) / 1e9
+    ctx_tokens = int(lens.sum())
+    out = {
+        "metric": f"scored response tokens/sec, discrete M1 panel of {R} rows (1 GPU)",
+        "value": round(R / (ms_per_step / 1e3), 1), "unit": "response tokens/s", "n_gpus": 1,
+        "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int32",
+        "data": "synthetic (seeded discrete container of the M1 shape, uniform rows)",
+        "config": {"workload": f"m1: {R} (prefix, target) rows of 186-192 tokens scored per timed "
+                               "step", "vocabulary": art.shape.vocabulary,
+                   "blocks": art.shape.blocks, "context": ctx, "kept_cells": art.shape.kept_cells,
+                   "read": f"{art.shape.read_mode} kept {art.shape.read_kept} sweeps "
+                           f"{art.shape.read_sweeps}", "trunk_entries_per_table": a.d11_trunk_entries,
+                   "parallelism": "none (1 GPU)"},
+        "context_tokens_per_s": round(ctx_tokens / (ms_per_step / 1e3), 1),
+        "host_inclusive": {"ms": round(host_best, 3), "response_tokens_per_s": round(R / (host_best / 1e3), 1),
+                           "what": "uor_d11_score_rows over host buffers: allocation, copies to "
+                                   "and from the device, the launch"},
+        "reference_published": D11_PUBLISHED,
+        "vs_published_host_inclusive": round(R / (host_best / 1e3) / D11_PUBLISHED["value"], 2),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
+                     "bytes_per_row": round(bytes_per_row, 1), "kernel": "d11_score_rows",
+                     "launch_ms": [round(x, 3) for x in launch_ms]},
+    }
+    if not a.no_cpu:
+        threads = a.cpu_threads or min(16, os.cpu_count() or 1)
+        t0 = time.perf_counter()
+        oracle.d11_score_rows(art, pre[:threads * 4], lens[:threads * 4], tg[:threads * 4],
+                              threads=threads)
+        per_row = (time.perf_counter() - t0) / (threads * 4)
+        n_cpu = int(min(R, max(threads, a.cpu_seconds / per_row)))
+        t0 = time.perf_counter()
+        cpu = oracle.d11_score_rows(art, pre[:n_cpu], lens[:n_cpu], tg[:n_cpu], threads=threads)
+        cpu_s = time.perf_counter() - t0
+        same = np.array_equal(cpu.view(np.uint32), recs[:n_cpu].view(np.uint32))
+        out["cpu_baseline"] = {
+            "value": round(n_cpu / cpu_s, 1), "unit": "response tokens/s",
+            "cores": min(threads, n_cpu), "cpu_model": cpu_model(), "kind": "port",
+            "sample": f"the first {n_cpu} of the {R} rows ({cpu_s:.1f} s), oracle C restatement, "
+                      "one row per thread", "records_equal_gpu": bool(same)}
+        if not same:
+            print("bench.py: CPU records differ from the GPU's", file=sys.stderr)
+    model.close()
+    return out
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -414,6 +527,9 @@ def main():
     import oracle
     from uor_fbs import hip, synth
 
+    if a.config == "m1":
+        print(json.dumps(d11_main(a, torch, oracle)))
+        return
     spec = replace(synth.CONFIGS[a.config], context=a.prompt + a.gen + 1)
     art = synth.make_artifact(spec, a.seed)
     if spec.zipf_drawers:

@@ -33,7 +33,7 @@
 
 namespace d11 {
 
-constexpr int kWaves = 4;  // rows per block
+constexpr int kWaves = 8;  // rows per block
 constexpr int kThreads = 64 * kWaves;
 constexpr int kMaxNodes = 512;
 constexpr int kMaxLevels = 8;
@@ -110,31 +110,47 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-__device__ __forceinline__ uint32_t wave_min32(uint32_t v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, m, 64));
-  return v;
+// Wave-wide reductions: butterflies inside each row of 16 lanes through DPP, then the four rows'
+// results read as scalars (uniform). Every lane must be active.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
 }
-
-__device__ __forceinline__ uint32_t wave_max32(uint32_t v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, m, 64));
-  return v;
+__device__ __forceinline__ uint32_t lane32(uint32_t v, int l) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, l);
 }
+constexpr int kXor1 = 0xb1, kXor2 = 0x4e, kHalfMirror = 0x141, kMirror = 0x140;
 
-__device__ __forceinline__ uint64_t wave_max64(uint64_t v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    const uint64_t o = __shfl_xor(v, m, 64);
-    v = o > v ? o : v;
+#define D11_WAVE_REDUCE32(NAME, OP)                                                   \
+  __device__ __forceinline__ uint32_t NAME(uint32_t v) {                              \
+    v = OP(v, dpp32<kXor1>(v));                                                       \
+    v = OP(v, dpp32<kXor2>(v));                                                       \
+    v = OP(v, dpp32<kHalfMirror>(v));                                                 \
+    v = OP(v, dpp32<kMirror>(v));                                                     \
+    return OP(OP(lane32(v, 0), lane32(v, 16)), OP(lane32(v, 32), lane32(v, 48)));    \
   }
-  return v;
-}
+__device__ __forceinline__ uint32_t op_min(uint32_t a, uint32_t b) { return a < b ? a : b; }
+__device__ __forceinline__ uint32_t op_max(uint32_t a, uint32_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint32_t op_add(uint32_t a, uint32_t b) { return a + b; }
+D11_WAVE_REDUCE32(wave_min32, op_min)
+D11_WAVE_REDUCE32(wave_max32, op_max)
+D11_WAVE_REDUCE32(wave_sum32, op_add)
+#undef D11_WAVE_REDUCE32
 
-__device__ __forceinline__ uint32_t wave_sum32(uint32_t v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += (uint32_t)__shfl_xor((int)v, m, 64);
-  return v;
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp64(uint64_t v) {
+  return (uint64_t)dpp32<CTRL>((uint32_t)(v >> 32)) << 32 | dpp32<CTRL>((uint32_t)v);
+}
+__device__ __forceinline__ uint64_t max64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint64_t lane64(uint64_t v, int l) {
+  return (uint64_t)lane32((uint32_t)(v >> 32), l) << 32 | lane32((uint32_t)v, l);
+}
+__device__ __forceinline__ uint64_t wave_max64(uint64_t v) {
+  v = max64(v, dpp64<kXor1>(v));
+  v = max64(v, dpp64<kXor2>(v));
+  v = max64(v, dpp64<kHalfMirror>(v));
+  v = max64(v, dpp64<kMirror>(v));
+  return max64(max64(lane64(v, 0), lane64(v, 16)), max64(lane64(v, 32), lane64(v, 48)));
 }
 
 // snap(x, n) (discrete_d11.rs:755-778) over the wave: lane r < 16 scores root r; the least
@@ -180,14 +196,6 @@ __device__ __forceinline__ uint64_t lower_bound64(const uint64_t *a, uint64_t n,
     else hi = mid;
   }
   return lo;
-}
-
-// DiscreteSparseCountTable::get (discrete_d11.rs:451-456).
-__device__ __forceinline__ uint32_t sparse_get(const DevModel &M, int t, uint32_t key,
-                                               uint32_t tok) {
-  const uint64_t want = (uint64_t)key << 32 | tok;
-  const uint64_t i = lower_bound64(M.pairs[t], M.rows[t], want);
-  return i < M.rows[t] && M.pairs[t][i] == want ? M.counts[t][i] : 0u;
 }
 
 __device__ void write_error(uor_d11_row_out *o, int status, int lane) {
@@ -269,26 +277,34 @@ __device__ int flock_block(const DevModel &M, const Geo &g, const Plan &P, WaveL
       w.prev[i] = 8 - (int32_t)g.dist[qf][w.frame[i]];
       w.rel[i] = 0;
     }
-    // Previous node of the same level with the same frame (edge type 4), chunk by chunk.
-    for (int l = 0; l < kMaxLevels && P.level_start[l] < P.level_start[l + 1]; l++) {
-      int lastf = -1;  // lane v < 16: the level's last node so far with frame v
+    // Previous node of the same level with the same frame (edge type 4, only on levels whose
+    // gate uses it), 64 nodes at a time: per frame value a ballot finds each lane's nearest
+    // lower lane with that frame; the level's last node per frame carries across chunks.
+    for (int l = 0; l < S && P.level_start[l] < P.level_start[l + 1]; l++) {
+      if (rg[l * 5 + 4] == 0) continue;
+      int seen[16];
+#pragma unroll
+      for (int v = 0; v < 16; v++) seen[v] = -1;
       for (int c = P.level_start[l]; c < P.level_start[l + 1]; c += 64) {
         const int k = c + lane;
         const bool valid = k < P.level_start[l + 1];
         const int i = valid ? P.order[k] : 0;
         const int fr = valid ? w.frame[i] : 0xff;
-        int res = -1;
+        int src = -1, res = -1;
+#pragma unroll
         for (int v = 0; v < 16; v++) {
           const uint64_t m = __ballot(fr == v);
-          if (!m) continue;
-          const int seen = __shfl(lastf, v, 64);
-          if (fr == v) {
-            const uint64_t below = m & ((1ull << lane) - 1);
-            res = below ? P.order[c + 63 - __clzll(below)] : seen;
+          if (m) {
+            if (fr == v) {
+              const uint64_t below = m & ((1ull << lane) - 1);
+              if (below) src = 63 - __clzll(below);
+              else res = seen[v];
+            }
+            seen[v] = __builtin_amdgcn_readlane(i, 63 - __clzll(m));
           }
-          if (lane == v) lastf = P.order[c + 63 - __clzll(m)];
         }
-        if (valid) w.samef[i] = (int16_t)res;
+        const int from = __shfl(i, src < 0 ? lane : src, 64);
+        if (valid) w.samef[i] = (int16_t)(src >= 0 ? from : res);
       }
     }
     wave_sync();
@@ -444,33 +460,51 @@ __device__ void trunk_gate(const DevModel &M, const Geo &g, WaveLds &w, int len,
   const bool has_ptr = pm >= 0;
   const uint32_t ptr = has_ptr ? w.tok[pm + 1] : 0u;
   // select_level3_joint_pointer_global (:546-599): the candidates are the entries under the
-  // query, read and recurrence keys, and the pointer successor.
+  // query, read and recurrence keys, and the pointer successor. Each table is read under one key
+  // per row, so lanes 0..11 first find the six keys' ranges; every count is then a search
+  // within its key's range.
   const uint32_t qtok = w.tok[last];
-  const uint32_t keys[3] = {qtok, read_code, rec_code};
-  const int src[3] = {S_QUERY, S_READ, S_REC};
-  uint64_t beg[3], n[3];
+  uint32_t key_of[kSparse];
+  key_of[S_QUERY] = qtok;
+  key_of[S_QUERY_READ] = qtok << 16 | read_code;
+  key_of[S_READ] = read_code;
+  key_of[S_QUERY_REC] = qtok << 16 | rec_code;
+  key_of[S_READ_REC] = read_code << 16 | rec_code;
+  key_of[S_REC] = rec_code;
+  uint64_t bound = 0;
 #pragma unroll
-  for (int k = 0; k < 3; k++) {
-    const int t = src[k];
-    beg[k] = lower_bound64(M.pairs[t], M.rows[t], (uint64_t)keys[k] << 32);
-    n[k] = lower_bound64(M.pairs[t], M.rows[t], ((uint64_t)keys[k] + 1) << 32) - beg[k];
+  for (int t = 0; t < kSparse; t++)
+    if (lane == t || lane == t + kSparse) {
+      const uint64_t x = ((uint64_t)key_of[t] + (lane >= kSparse ? 1 : 0)) << 32;
+      bound = lower_bound64(M.pairs[t], M.rows[t], x);
+    }
+  uint64_t beg[kSparse], end[kSparse];
+#pragma unroll
+  for (int t = 0; t < kSparse; t++) {
+    beg[t] = lane64(bound, t);
+    end[t] = lane64(bound, t + kSparse);
   }
-  const uint64_t total = n[0] + n[1] + n[2] + (has_ptr ? 1 : 0);
+  const uint64_t n0 = end[S_QUERY] - beg[S_QUERY], n1 = end[S_READ] - beg[S_READ];
+  const uint64_t n2 = end[S_REC] - beg[S_REC];
+  const uint64_t total = n0 + n1 + n2 + (has_ptr ? 1 : 0);
   uint64_t best_s = 0;
   uint32_t best_u = 0, best_t = 0xffffffffu;
   for (uint64_t c = lane; c < total; c += 64) {
     uint32_t tok;
-    if (c < n[0]) tok = (uint32_t)M.pairs[src[0]][beg[0] + c];
-    else if (c < n[0] + n[1]) tok = (uint32_t)M.pairs[src[1]][beg[1] + c - n[0]];
-    else if (c < n[0] + n[1] + n[2]) tok = (uint32_t)M.pairs[src[2]][beg[2] + c - n[0] - n[1]];
+    if (c < n0) tok = (uint32_t)M.pairs[S_QUERY][beg[S_QUERY] + c];
+    else if (c < n0 + n1) tok = (uint32_t)M.pairs[S_READ][beg[S_READ] + c - n0];
+    else if (c < n0 + n1 + n2) tok = (uint32_t)M.pairs[S_REC][beg[S_REC] + c - n0 - n1];
     else tok = ptr;
     if (tok >= M.vocab) continue;
-    const uint64_t c_q = sparse_get(M, S_QUERY, qtok, tok);
-    const uint64_t c_qr = sparse_get(M, S_QUERY_READ, qtok << 16 | read_code, tok);
-    const uint64_t c_r = sparse_get(M, S_READ, read_code, tok);
-    const uint64_t c_qc = sparse_get(M, S_QUERY_REC, qtok << 16 | rec_code, tok);
-    const uint64_t c_rr = sparse_get(M, S_READ_REC, read_code << 16 | rec_code, tok);
-    const uint64_t s = (c_qr << 6) + (c_qc << 5) + (c_rr << 3) + (c_r << 1) + c_q +
+    uint64_t cnt[5];
+#pragma unroll
+    for (int t = 0; t < 5; t++) {
+      const uint64_t want = (uint64_t)key_of[t] << 32 | tok;
+      const uint64_t i = beg[t] + lower_bound64(M.pairs[t] + beg[t], end[t] - beg[t], want);
+      cnt[t] = i < end[t] && M.pairs[t][i] == want ? M.counts[t][i] : 0u;
+    }
+    const uint64_t s = (cnt[S_QUERY_READ] << 6) + (cnt[S_QUERY_REC] << 5) +
+                       (cnt[S_READ_REC] << 3) + (cnt[S_READ] << 1) + cnt[S_QUERY] +
                        (has_ptr && ptr == tok ? 256u : 0u);
     const uint32_t uc = M.unigram[tok];
     if (s > 0 && (s > best_s || (s == best_s && (uc > best_u || (uc == best_u && tok < best_t))))) {
