@@ -89,8 +89,13 @@ struct DevModel {
   const uint8_t *norm;       // [4]
   const uint64_t *pairs[kSparse];  // key << 32 | token, ascending
   const uint32_t *counts[kSparse];
+  const uint32_t *bucket[kSparse];  // [65537]: first entry whose key >> shift is >= b
   uint64_t rows[kSparse];
 };
+// Bucket shift per table: the 16-bit keys (token, read code, recurrence code) index their
+// buckets directly; the composite keys bucket by their high half.
+constexpr int kBucketShift[kSparse] = {0, 16, 0, 16, 16, 0};
+constexpr uint32_t kBuckets = 65536;
 
 struct WaveLds {
   uint16_t tok[256];
@@ -102,7 +107,18 @@ struct WaveLds {
   int16_t samef[kMaxNodes];  // previous node of the level with the same frame, -1 none
   uint32_t rec[kRecWords];   // the record: admitted cells and top 8 are kept here as found
   uint8_t qroot[UOR_D11_MAX_BLOCKS];  // the read, one root per block
+  int16_t lastf[16];                  // a level's last node so far, per frame
+  uint64_t tokbits[4][14];            // per 64 positions: the tokens' 13 bit planes, then valid
 };
+
+// Lanes whose value equals this lane's, from the bit-plane ballots of a 64-lane group.
+template <int BITS>
+__device__ __forceinline__ uint64_t same_as(uint32_t v, const uint64_t *planes, uint64_t valid) {
+  uint64_t m = valid;
+#pragma unroll
+  for (int k = 0; k < BITS; k++) m &= (v >> k & 1) ? planes[k] : ~planes[k];
+  return m;
+}
 
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -278,33 +294,31 @@ __device__ int flock_block(const DevModel &M, const Geo &g, const Plan &P, WaveL
       w.rel[i] = 0;
     }
     // Previous node of the same level with the same frame (edge type 4, only on levels whose
-    // gate uses it), 64 nodes at a time: per frame value a ballot finds each lane's nearest
-    // lower lane with that frame; the level's last node per frame carries across chunks.
+    // gate uses it), 64 nodes at a time: the frame's four bit planes as ballots give each lane
+    // the lanes holding its frame; the nearest lower one, else the level's last node with that
+    // frame in earlier chunks (kept per frame in LDS).
+    const uint64_t lt = (1ull << lane) - 1, gt_mask = ~lt & ~(1ull << lane);
     for (int l = 0; l < S && P.level_start[l] < P.level_start[l + 1]; l++) {
       if (rg[l * 5 + 4] == 0) continue;
-      int seen[16];
-#pragma unroll
-      for (int v = 0; v < 16; v++) seen[v] = -1;
+      if (lane < 16) w.lastf[lane] = -1;
+      wave_sync();
       for (int c = P.level_start[l]; c < P.level_start[l + 1]; c += 64) {
         const int k = c + lane;
         const bool valid = k < P.level_start[l + 1];
         const int i = valid ? P.order[k] : 0;
-        const int fr = valid ? w.frame[i] : 0xff;
-        int src = -1, res = -1;
+        const uint32_t fr = valid ? w.frame[i] : 0u;
+        uint64_t planes[4];
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-          const uint64_t m = __ballot(fr == v);
-          if (m) {
-            if (fr == v) {
-              const uint64_t below = m & ((1ull << lane) - 1);
-              if (below) src = 63 - __clzll(below);
-              else res = seen[v];
-            }
-            seen[v] = __builtin_amdgcn_readlane(i, 63 - __clzll(m));
-          }
-        }
-        const int from = __shfl(i, src < 0 ? lane : src, 64);
-        if (valid) w.samef[i] = (int16_t)(src >= 0 ? from : res);
+        for (int bit = 0; bit < 4; bit++) planes[bit] = __ballot(fr >> bit & 1);
+        const uint64_t same = same_as<4>(fr, planes, __ballot(valid));
+        const uint64_t below = same & lt;
+        const int src = below ? 63 - __clzll(below) : lane;
+        const int from = __shfl(i, src, 64);
+        const int seen = valid ? w.lastf[fr] : -1;
+        if (valid) w.samef[i] = (int16_t)(below ? from : seen);
+        wave_sync();
+        if (valid && !(same & gt_mask)) w.lastf[fr] = (int16_t)i;
+        wave_sync();
       }
     }
     wave_sync();
@@ -379,7 +393,26 @@ __device__ int flock_block(const DevModel &M, const Geo &g, const Plan &P, WaveL
     }
     int32_t sum[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     int found = 0;
-    for (int r = 0; r < kept; r++) {
+    // Only the kept set enters the sum: when the eligible nodes fit, take them all.
+    uint32_t mine = 0;
+#pragma unroll
+    for (int j = 0; j < kPerLane; j++) mine += mk[j] != 0;
+    const uint32_t eligible = wave_sum32(mine);
+    if ((int)eligible <= kept) {
+#pragma unroll
+      for (int j = 0; j < kPerLane; j++) {
+        if (mk[j]) {
+          const int node = (int)(kNone - (uint32_t)(mk[j] & kNone));
+          const int cr = g.act[g.bfs[(w.frame[node] << 4) + qf]][w.payload[node]];
+#pragma unroll
+          for (int d = 0; d < 8; d++) sum[d] += g.roots[cr][d];
+        }
+      }
+#pragma unroll
+      for (int d = 0; d < 8; d++) sum[d] = (int32_t)wave_sum32((uint32_t)sum[d]);
+      found = (int)eligible;
+    }
+    for (int r = 0; (int)eligible > kept && r < kept; r++) {
       uint64_t loc = 0;
 #pragma unroll
       for (int j = 0; j < kPerLane; j++) loc = mk[j] > loc ? mk[j] : loc;
@@ -475,8 +508,14 @@ __device__ void trunk_gate(const DevModel &M, const Geo &g, WaveLds &w, int len,
 #pragma unroll
   for (int t = 0; t < kSparse; t++)
     if (lane == t || lane == t + kSparse) {
-      const uint64_t x = ((uint64_t)key_of[t] + (lane >= kSparse ? 1 : 0)) << 32;
-      bound = lower_bound64(M.pairs[t], M.rows[t], x);
+      const uint32_t b = key_of[t] >> kBucketShift[t];
+      const uint64_t lo = M.bucket[t][b], hi = M.bucket[t][b + 1];
+      if (kBucketShift[t] == 0) {
+        bound = lane >= kSparse ? hi : lo;
+      } else {
+        const uint64_t x = ((uint64_t)key_of[t] + (lane >= kSparse ? 1 : 0)) << 32;
+        bound = lo + lower_bound64(M.pairs[t] + lo, hi - lo, x);
+      }
     }
   uint64_t beg[kSparse], end[kSparse];
 #pragma unroll
@@ -561,13 +600,32 @@ __device__ void score_row(const DevModel &M, const Geo &g, WaveLds &w, const uin
   const Plan &P = M.plans[len - 1];
   const bool relation = M.read_mode == UOR_D11_READ_RELATION;
   if (relation && M.gates[B * M.stages + 3] != 0) {
-    // Edge type 3 (level 0 only): each atom's previous position holding the same token.
-    for (int a = lane; a < len; a += 64) {
-      const uint16_t t = w.tok[a];
+    // Edge type 3 (level 0 only): each atom's previous position holding the same token. Each
+    // group of 64 positions keeps its tokens' 13 bit planes as ballots; a position's match in
+    // group g is the AND of the planes its bits select, taken below its own lane in its group.
+    const int groups = (len + 63) >> 6;
+    for (int gi = 0; gi < groups; gi++) {
+      const int a = gi * 64 + lane;
+      const uint32_t t = a < len ? w.tok[a] : 0u;
+#pragma unroll
+      for (int bit = 0; bit < 13; bit++) {
+        const uint64_t m = __ballot(t >> bit & 1);
+        if (lane == 0) w.tokbits[gi][bit] = m;
+      }
+      const uint64_t vm = __ballot(a < len);
+      if (lane == 0) w.tokbits[gi][13] = vm;
+    }
+    wave_sync();
+    for (int gi = 0; gi < groups; gi++) {
+      const int a = gi * 64 + lane;
+      const uint32_t t = a < len ? w.tok[a] : 0u;
       int j = -1;
-      for (int p = 0; p < a; p++)
-        if (w.tok[p] == t) j = p;
-      w.prevocc[a] = (int16_t)(j < 0 ? -1 : P.order[P.level_start[0] + j]);
+      for (int h = gi; h >= 0 && j < 0; h--) {
+        uint64_t m = same_as<13>(t, w.tokbits[h], w.tokbits[h][13]);
+        if (h == gi) m &= (1ull << lane) - 1;
+        if (m) j = h * 64 + 63 - __clzll(m);
+      }
+      if (a < len) w.prevocc[a] = (int16_t)(j < 0 ? -1 : P.order[P.level_start[0] + j]);
     }
     wave_sync();
   }
@@ -965,7 +1023,7 @@ extern "C" int uor_d11_model_create(const uor_d11_model *m, int32_t device, void
   std::vector<uint8_t> step(64, 0), norm(4, 0);
   std::vector<uint32_t> unigram(V, 0);
   std::vector<uint64_t> pairs[kSparse];
-  std::vector<uint32_t> counts[kSparse];
+  std::vector<uint32_t> counts[kSparse], bucket[kSparse];
   uint32_t unigram_best = 0;
   if (tr) {
     if (B != 4) return fail(-1, "the trunk requires 4 blocks");
@@ -1032,8 +1090,23 @@ extern "C" int uor_d11_model_create(const uor_d11_model *m, int32_t device, void
             (d.routes = h->upload(routes)) && (d.gates = h->upload(gates)) &&
             (d.plans = h->upload(plans)) && (d.unigram = h->upload(unigram)) &&
             (d.code4 = h->upload(code4)) && (d.step = h->upload(step)) && (d.norm = h->upload(norm));
+  for (int s = 0; s < kSparse; s++) {
+    bucket[s].assign(kBuckets + 1, 0);
+    uint32_t i = 0;
+    for (uint32_t b = 0; b < kBuckets; b++) {
+      const uint64_t first = (uint64_t)b << (32 + kBucketShift[s]);  // below 2^64 for b < 2^16
+      while (i < pairs[s].size() && pairs[s][i] < first) i++;
+      bucket[s][b] = i;
+    }
+    if (kBucketShift[s] == 0)  // keys of 2^16 and above lie beyond every bucket
+      while (i < pairs[s].size() && pairs[s][i] < ((uint64_t)kBuckets << 32)) i++;
+    else
+      i = (uint32_t)pairs[s].size();
+    bucket[s][kBuckets] = i;
+  }
   for (int s = 0; ok && s < kSparse; s++) {
-    ok = (d.pairs[s] = h->upload(pairs[s])) && (d.counts[s] = h->upload(counts[s]));
+    ok = (d.pairs[s] = h->upload(pairs[s])) && (d.counts[s] = h->upload(counts[s])) &&
+         (d.bucket[s] = h->upload(bucket[s]));
     d.rows[s] = pairs[s].size();
   }
   (void)hipSetDevice(prev);
