@@ -44,6 +44,7 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 # Measured HBM bytes per launch of the decode kernel (rocprofv3 FETCH_SIZE and WRITE_SIZE passes,
 # scaled by a copy kernel's reading), for the workload it names.
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fbs_decode_pair_c3_b1024_traffic.md")
+D11_TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "d11_score_rows_m1_traffic.md")
 # BASELINE.json's configs at their full shapes: (sequences, prompt, decode steps); c4 is
 # teacher-forced scoring of (rows, row length).
 CONFIG_SHAPES = {"c1": (1, 256, 256), "c2": (1024, 512, 512), "c3": (1024, 1024, 1024),
@@ -465,6 +466,11 @@ def d11_main(a, torch, oracle) -> dict:
     assert np.array_equal(host.view(np.uint32), recs.view(np.uint32)), "host path differs"
     host_best = min(host_ms)
     bytes_per_row = 4 * float(lens.mean()) + 8 + d11.ROW_DTYPE.itemsize
+    traffic = None  # the committed counter summary, for the workload it was measured on
+    if (R, a.d11_trunk_entries, a.seed) == (D11_ROWS, 600_000, 2026120203) and \
+            os.path.exists(D11_TRAFFIC_SUMMARY):
+        m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", open(D11_TRAFFIC_SUMMARY).read())
+        traffic = int(m.group(1)) if m else None
     achieved = bytes_per_row * R / (float(np.mean(launch_ms)) / 1e3) / 1e9
     ctx_tokens = int(lens.sum())
     out = {
@@ -486,20 +492,22 @@ def d11_main(a, torch, oracle) -> dict:
         "reference_published": D11_PUBLISHED,
         "vs_published_host_inclusive": round(R / (host_best / 1e3) / D11_PUBLISHED["value"], 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5), "traffic": traffic,
                      "bytes_per_row": round(bytes_per_row, 1), "kernel": "d11_score_rows",
                      "launch_ms": [round(x, 3) for x in launch_ms]},
     }
     if not a.no_cpu:
         threads = a.cpu_threads or min(16, os.cpu_count() or 1)
+        cpu_model_ = oracle.D11Oracle(art)  # loaded once, as the reference's from_bytes
+        n_cal = threads * 8
         t0 = time.perf_counter()
-        oracle.d11_score_rows(art, pre[:threads * 4], lens[:threads * 4], tg[:threads * 4],
-                              threads=threads)
-        per_row = (time.perf_counter() - t0) / (threads * 4)
+        cpu_model_.score_rows(pre[:n_cal], lens[:n_cal], tg[:n_cal], threads=threads)
+        per_row = (time.perf_counter() - t0) / n_cal
         n_cpu = int(min(R, max(threads, a.cpu_seconds / per_row)))
         t0 = time.perf_counter()
-        cpu = oracle.d11_score_rows(art, pre[:n_cpu], lens[:n_cpu], tg[:n_cpu], threads=threads)
+        cpu = cpu_model_.score_rows(pre[:n_cpu], lens[:n_cpu], tg[:n_cpu], threads=threads)
         cpu_s = time.perf_counter() - t0
+        cpu_model_.close()
         same = np.array_equal(cpu.view(np.uint32), recs[:n_cpu].view(np.uint32))
         out["cpu_baseline"] = {
             "value": round(n_cpu / cpu_s, 1), "unit": "response tokens/s",

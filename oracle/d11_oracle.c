@@ -729,6 +729,36 @@ int d11_oracle_score_rows(const uor_d11_model *m, const uint32_t *prefixes, cons
   return 0;
 }
 
+/* A loaded oracle (the model and its sorted trunk tables, as from_bytes builds them once), so
+ * that timing covers the rows alone. */
+void *d11_oracle_open(const uor_d11_model *m) {
+  Oracle *o = (Oracle *)malloc(sizeof(Oracle));
+  oracle_init(o, m);
+  return o;
+}
+
+void d11_oracle_close(void *h) {
+  oracle_free((Oracle *)h);
+  free(h);
+}
+
+int d11_oracle_score_open(void *h, const uint32_t *prefixes, const int32_t *lengths,
+                          const uint32_t *targets, uint32_t rows, uint32_t stride,
+                          uor_d11_row_out *out, int threads) {
+  if (threads < 1) threads = 1;
+  if (threads > 64) threads = 64;
+  pthread_t th[64];
+  Job jobs[64];
+  for (int t = 0; t < threads; t++) {
+    jobs[t] = (Job){(const Oracle *)h, prefixes, lengths, targets, rows, stride, (uint32_t)t,
+                    (uint32_t)threads, out};
+    if (t > 0) pthread_create(&th[t], NULL, run_job, &jobs[t]);
+  }
+  run_job(&jobs[0]);
+  for (int t = 1; t < threads; t++) pthread_join(th[t], NULL);
+  return 0;
+}
+
 /* One row with its relation scores (blocks x node count of the row's plan), as
  * DiscretePrefixEvaluation::relation_scores (:386-388). Returns the node count. */
 int d11_oracle_row_relation(const uor_d11_model *m, const uint32_t *prefix, int32_t length,

@@ -352,6 +352,11 @@ def d11_lib():
         L.d11_oracle_score_rows.argtypes = [P, P, P, P, C.c_uint32, C.c_uint32, P, C.c_int]
         L.d11_oracle_row_relation.argtypes = [P, P, C.c_int32, C.c_uint32, P, P]
         L.d11_oracle_plan.argtypes = [C.c_int32, P, P]
+        L.d11_oracle_open.argtypes = [P]
+        L.d11_oracle_open.restype = P
+        L.d11_oracle_close.argtypes = [P]
+        L.d11_oracle_close.restype = None
+        L.d11_oracle_score_open.argtypes = [P, P, P, P, C.c_uint32, C.c_uint32, P, C.c_int]
         _d11 = L
     return _d11
 
@@ -386,3 +391,28 @@ def d11_plan(length):
     nodes, frontier = C.c_int32(), C.c_int32()
     st = d11_lib().d11_oracle_plan(length, C.byref(nodes), C.byref(frontier))
     return None if st else (nodes.value, frontier.value)
+
+
+class D11Oracle:
+    """The oracle with its model loaded once (timing covers the rows alone)."""
+
+    def __init__(self, art):
+        from uor_fbs import d11
+        self.m, self.keep = d11.c_model(art)
+        self.h = d11_lib().d11_oracle_open(C.byref(self.m))
+
+    def score_rows(self, prefixes, lengths, targets, threads=8):
+        from uor_fbs import d11
+        prefixes = np.ascontiguousarray(prefixes, np.uint32)
+        rows, stride = prefixes.shape
+        lengths = np.ascontiguousarray(lengths, np.int32)
+        targets = np.ascontiguousarray(targets, np.uint32)
+        out = np.zeros(rows, d11.ROW_DTYPE)
+        d11_lib().d11_oracle_score_open(self.h, prefixes.ctypes.data, lengths.ctypes.data,
+                                        targets.ctypes.data, rows, stride, out.ctypes.data, threads)
+        return out
+
+    def close(self):
+        if self.h:
+            d11_lib().d11_oracle_close(self.h)
+            self.h = None
