@@ -416,3 +416,31 @@ class D11Oracle:
         if self.h:
             d11_lib().d11_oracle_close(self.h)
             self.h = None
+
+
+# ---------------------------------------------------------------------------------------------
+# The copy heads' Hamming read (oracle/lib/libcopy_oracle.so, copy_oracle.c).
+
+COPY_SO = os.path.join(HERE, "lib", "libcopy_oracle.so")
+_copy = None
+
+
+def copy_mean_rows(heads, tokens, lengths, opening=None):
+    """(out, found, chosen) as uor_copy_mean_rows writes them."""
+    global _copy
+    if _copy is None:
+        _copy = C.CDLL(COPY_SO)
+        _copy.copy_oracle_mean_rows.argtypes = [P, P, P, P, C.c_uint32, C.c_uint32, P, P, P]
+    s, keep = heads.c_struct()
+    tokens = np.ascontiguousarray(tokens, np.uint32)
+    rows, stride = tokens.shape
+    lengths = np.ascontiguousarray(lengths, np.int32)
+    op = None if opening is None else np.ascontiguousarray(opening, np.uint8)
+    width, copy = heads.table.shape[1], heads.codes.shape[1]
+    out = np.zeros((rows, width), np.int64)
+    found = np.zeros(rows, np.uint8)
+    chosen = np.zeros((rows, copy, heads.kept), np.int32)
+    _copy.copy_oracle_mean_rows(C.byref(s), tokens.ctypes.data, lengths.ctypes.data,
+                                None if op is None else op.ctypes.data, rows, stride,
+                                out.ctypes.data, found.ctypes.data, chosen.ctypes.data)
+    return out, found.astype(bool), chosen

@@ -390,3 +390,26 @@ def test_d11_model_create_refuses_without_a_device(edit, msg):
     h = P()
     assert d11.lib().uor_d11_model_create(C.byref(m), 0, C.byref(h)) == -1
     assert msg in d11.lib().uor_d11_last_error()
+
+
+def test_copy_library_exports_and_refusals():
+    """include/uor_copy.h: every declared entry point is exported; create refuses shapes
+    outside its limits before any device call."""
+    from uor_fbs import copy as cp
+    text = open(os.path.join(ROOT, "include", "uor_copy.h")).read()
+    names = set(re.findall(r"\b(uor_copy_[a-z0-9_]+)\s*\(", text))
+    assert names == set(cp.SYMBOLS)
+    L = cp.lib()
+    for name in names:
+        assert hasattr(L, name), name
+    assert L.uor_copy_abi_version() == 1
+    import copy_cases as K
+    for kw in ({"kept": 33}, {"kept": 0}):
+        heads = K.heads(kw["kept"], "mean")
+        s, keep = heads.c_struct()
+        h = P()
+        assert L.uor_copy_create(C.byref(s), 0, C.byref(h)) == -1
+    heads = K.heads(4, "longest-after-opening", marker=(9, 1))
+    s, keep = heads.c_struct()
+    assert L.uor_copy_create(C.byref(s), 0, C.byref(P())) == -1
+    assert b"marker" in L.uor_copy_last_error()

@@ -1,0 +1,49 @@
+"""The HIP copy heads' Hamming read (uor_copy_mean_rows) against the reference's copy-rule
+tests (hamming.rs:705-1058, literal positions and means) and against the oracle, stream for
+stream and bit for bit: every rule, copy key 1 and 2 heads, reply markers and the caller's
+opening flags, streams from empty to the 4,096-token stride."""
+
+import numpy as np
+import pytest
+
+import copy_cases as K
+import oracle
+from uor_fbs.copy import RULES, CopyHeads
+
+pytestmark = pytest.mark.gpu
+
+
+def test_the_reference_copy_rule_tests_on_the_gpu():
+    print("copy rule tests", flush=True)
+    made = []
+
+    def make(kept, rule, **kw):
+        h = CopyHeads(K.heads(kept, rule, **kw))
+        made.append(h)
+        return h
+    try:
+        K.check_rust_tests(make)
+    finally:
+        for h in made:
+            h.close()
+
+
+@pytest.mark.parametrize("rule", sorted(RULES))
+@pytest.mark.parametrize("shape", [(300, 96, 4, 8, 40, 200), (5000, 512, 8, 32, 4096, 64),
+                                   (64, 1024, 16, 1, 300, 40)])
+def test_random_streams_match_the_oracle(rule, shape):
+    vocab, width, copy, kept, stride, rows = shape
+    heads = K.random_heads(RULES[rule] * 7 + width, vocab=vocab, width=width, copy=copy,
+                           kept=kept, rule=rule)
+    tok, lens, opening = K.random_streams(RULES[rule] + width, vocab, rows, stride)
+    print(f"copy {rule} {shape}", flush=True)
+    gpu = CopyHeads(heads)
+    try:
+        out, found, chosen = gpu.mean_rows(tok, lens, opening)
+    finally:
+        gpu.close()
+    w_out, w_found, w_chosen = oracle.copy_mean_rows(heads, tok, lens, opening)
+    np.testing.assert_array_equal(chosen, w_chosen)
+    np.testing.assert_array_equal(found, w_found)
+    np.testing.assert_array_equal(out, w_out)
+    assert found.sum() > rows // 4
