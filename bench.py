@@ -82,7 +82,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=3)
     p.add_argument("--warmup", type=int, default=1)
-    p.add_argument("--config", default="c3", choices=sorted(CONFIG_SHAPES) + ["m1"],
+    p.add_argument("--config", default="c3", choices=sorted(CONFIG_SHAPES) + ["m1", "copy"],
                    help="BASELINE's configs: c3 (default) is the metric's; c4 scores rows")
     p.add_argument("--batch", type=int, default=None, help="sequences (c4: rows); config's default")
     p.add_argument("--prompt", type=int, default=None, help="prompt tokens (c4: row length)")
@@ -103,7 +103,8 @@ def parse():
     p.add_argument("--d11-trunk-entries", type=int, default=600_000,
                    help="m1: (key, token) entries in each of the six trunk tables it reads")
     a = p.parse_args()
-    batch, prompt, gen = CONFIG_SHAPES.get(a.config, (D11_ROWS, 192, 0))
+    batch, prompt, gen = CONFIG_SHAPES.get(a.config, (D11_ROWS, 192, 0) if a.config == "m1"
+                                           else (4096, 1024, 0))
     a.batch = batch if a.batch is None else a.batch
     a.prompt = prompt if a.prompt is None else a.prompt
     a.gen = gen if a.gen is None else a.gen
@@ -520,6 +521,87 @@ def d11_main(a, torch, oracle) -> dict:
     return out
 
 
+def copy_main(a, torch, oracle) -> dict:
+    """The copy heads' Hamming read: a step is one uor_copy_mean_rows launch reading the last row
+    of every stream (C3's width and vocabulary, 4 copy heads keeping 16 positions each)."""
+    from uor_fbs import copy as cp
+    L = cp.lib()
+    heads = cp.synthetic(seed=a.seed)
+    R, n = a.batch, a.prompt
+    rng = np.random.default_rng(a.seed + 1)
+    tok = rng.integers(0, heads.codes.shape[0], (R, n)).astype(np.uint32)
+    lens = np.full(R, n, np.int32)
+    gpu = cp.CopyHeads(heads)
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    sp = C.c_void_p(stream.cuda_stream)
+    d_tok = torch.from_numpy(tok.view(np.int32)).to(dev)
+    d_len = torch.from_numpy(lens).to(dev)
+    d_out = torch.zeros((R, heads.table.shape[1]), dtype=torch.int64, device=dev)
+    d_found = torch.zeros(R, dtype=torch.uint8, device=dev)
+    log(f"copy: {R} streams of {n} tokens")
+
+    def step():
+        code = L.uor_copy_mean_rows_async(gpu.handle, C.c_void_p(d_tok.data_ptr()),
+                                          C.c_void_p(d_len.data_ptr()), None, R, n,
+                                          C.c_void_p(d_out.data_ptr()),
+                                          C.c_void_p(d_found.data_ptr()), None, sp)
+        if code:
+            raise cp.CopyError(L.uor_copy_last_error().decode())
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(a.steps)]
+    t0 = time.perf_counter()
+    for s_, e_ in ev:
+        s_.record(stream)
+        step()
+        e_.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    launch_ms = [s_.elapsed_time(e_) for s_, e_ in ev]
+    ms_per_step = wall * 1e3 / a.steps
+    copy, kept, width = heads.codes.shape[1], heads.kept, heads.table.shape[1]
+    bytes_per_read = 4 * n + copy * kept * width * 2 + width * 8 + 1
+    achieved = bytes_per_read * R / (float(np.mean(launch_ms)) / 1e3) / 1e9
+    out = {
+        "metric": f"copy-head reads/sec, {R} streams of {n} tokens, width {width} (1 GPU)",
+        "value": round(R / (ms_per_step / 1e3), 1), "unit": "reads/s", "n_gpus": 1,
+        "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int64",
+        "data": "synthetic (random 64-bit head codes, uniform streams)",
+        "config": {"workload": f"copy: the read at the last row of {R} streams of {n} tokens",
+                   "vocab": int(heads.codes.shape[0]), "width": width, "copy_heads": copy,
+                   "kept": kept, "rule": heads.rule, "parallelism": "none (1 GPU)"},
+        "context_tokens_per_s": round(R * n / (ms_per_step / 1e3), 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_read": bytes_per_read, "kernel": "copy_mean_rows",
+                     "launch_ms": [round(x, 3) for x in launch_ms]},
+    }
+    got_out = d_out.cpu().numpy()
+    got_found = d_found.cpu().numpy().astype(bool)
+    if not a.no_cpu:
+        threads = 1  # the oracle is single-threaded
+        t0 = time.perf_counter()
+        oracle.copy_mean_rows(heads, tok[:8], lens[:8])
+        per = (time.perf_counter() - t0) / 8
+        n_cpu = int(min(R, max(8, a.cpu_seconds / per)))
+        t0 = time.perf_counter()
+        w_out, w_found, _ = oracle.copy_mean_rows(heads, tok[:n_cpu], lens[:n_cpu])
+        cpu_s = time.perf_counter() - t0
+        same = np.array_equal(w_out, got_out[:n_cpu]) and np.array_equal(w_found, got_found[:n_cpu])
+        out["cpu_baseline"] = {"value": round(n_cpu / cpu_s, 1), "unit": "reads/s",
+                               "cores": threads, "cpu_model": cpu_model(), "kind": "port",
+                               "sample": f"the first {n_cpu} of the {R} streams ({cpu_s:.1f} s), "
+                                         "oracle C restatement, one thread",
+                               "reads_equal_gpu": bool(same)}
+    gpu.close()
+    return out
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -537,6 +619,9 @@ def main():
 
     if a.config == "m1":
         print(json.dumps(d11_main(a, torch, oracle)))
+        return
+    if a.config == "copy":
+        print(json.dumps(copy_main(a, torch, oracle)))
         return
     spec = replace(synth.CONFIGS[a.config], context=a.prompt + a.gen + 1)
     art = synth.make_artifact(spec, a.seed)

@@ -150,3 +150,14 @@ class CopyHeads:
         tok, lens = pack_rows([list(tokens)])
         _, _, chosen = self.mean_rows(tok, lens, [int(opening)])
         return [(int(v) & 0xffffff, int(v) >> 24) for v in chosen[0, h] if v >= 0]
+
+
+def synthetic(vocab=32768, width=256, copy=4, kept=16, rule="mean", seed=1, margin_bits=28):
+    """Random heads: 64-bit codes per token and head, margins of `margin_bits` bits, copy key 2
+    on odd heads (first half the low 32 bits), a Q12-range table."""
+    rng = np.random.default_rng(seed)
+    codes = rng.integers(0, 1 << 63, (vocab, copy), dtype=np.int64).astype(np.uint64)
+    codes ^= rng.integers(0, 2, (vocab, copy)).astype(np.uint64) << np.uint64(63)
+    pair = np.array([0 if h % 2 == 0 else (1 << 32) - 1 for h in range(copy)], np.uint64)
+    table = rng.integers(-4096, 4097, (vocab, width)).astype(np.int16)
+    return Heads(codes, np.full(copy, margin_bits << 16, np.int32), table, kept, rule, pair)
