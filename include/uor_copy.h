@@ -56,6 +56,16 @@ const char *uor_copy_last_error(void);
 int uor_copy_create(const uor_copy_heads *heads, int32_t device, void **handle);
 void uor_copy_destroy(void *handle);
 
+/* The heads' codes (`vocab_codes`, hamming.rs:541-582): for copy head h < copy of heads_total
+ * heads over width / heads_total coordinates (at most 64), entry v's code is the sign word of
+ * its table point through the head's key rotation, bit c set when coordinate c of
+ * unit(key_rotation quaternion) (x) point is at or above 0, the unit at Q31 as `stack_rotation`
+ * normalizes raw gates (epsilon 0). key_rotation holds width raw i32 values; codes receives
+ * vocab x copy words. Host buffers; computed on `device`. */
+int uor_copy_vocab_codes(const int32_t *key_rotation, const int16_t *table, uint32_t vocab,
+                         uint32_t width, uint32_t heads_total, uint32_t copy, int32_t device,
+                         uint64_t *codes);
+
 /* For each of `rows` streams (tokens: rows x stride, row r's first lengths[r] tokens; opening:
  * one flag per row, the caller's reply mark, or NULL for none): the copy mean of its last row
  * into out[r][width] and found[r] = 1, or zeros and found[r] = 0 when no head kept a position

@@ -444,3 +444,35 @@ def copy_mean_rows(heads, tokens, lengths, opening=None):
                                 None if op is None else op.ctypes.data, rows, stride,
                                 out.ctypes.data, found.ctypes.data, chosen.ctypes.data)
     return out, found.astype(bool), chosen
+
+
+def copy_vocab_codes(key_rotation, table, heads_total, copy):
+    """vocab_codes (hamming.rs:541-582) restated: units from the oracle's stack_rotation (raw
+    form, lambda 2^31, epsilon 0), then each head's sign word of stack_hamilton(unit, point)."""
+    rot = np.ascontiguousarray(key_rotation, np.int32)
+    table = np.asarray(table, np.int64)
+    vocab, width = table.shape
+    units = []
+    for q in range(width // 4):
+        out = np.zeros(4, np.int64)
+        lib().fbs_oracle_serve_rotation(None, 1, rot[4 * q:4 * q + 4].ctypes.data, 1 << 31, 0,
+                                        out.ctypes.data)
+        units.append([int(x) for x in out])
+    hw = width // heads_total
+    codes = np.zeros((vocab, copy), np.uint64)
+    for v in range(vocab):
+        p = [int(x) for x in table[v]]
+        for h in range(copy):
+            word = 0
+            for c in range(0, hw, 4):
+                at = h * hw + c
+                a, b = units[at // 4], p[at:at + 4]
+                r = [a[0] * b[0] - a[1] * b[1] - a[2] * b[2] - a[3] * b[3],
+                     a[0] * b[1] + a[1] * b[0] + a[2] * b[3] - a[3] * b[2],
+                     a[0] * b[2] - a[1] * b[3] + a[2] * b[0] + a[3] * b[1],
+                     a[0] * b[3] + a[1] * b[2] - a[2] * b[1] + a[3] * b[0]]
+                for i, x in enumerate(r):
+                    if x >= 0:
+                        word |= 1 << (c + i)
+            codes[v, h] = word
+    return codes

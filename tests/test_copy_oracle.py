@@ -103,3 +103,23 @@ def test_rules_against_brute_force(rule):
         want = brute(heads, [int(x) for x in tok[r, :lens[r]]], bool(opening[r]))
         got = out[r].tolist() if found[r] else None
         assert got == want, r
+
+
+def test_vocab_codes_restatement_closed_form():
+    # The identity rotation (raw [1, 0, 0, 0]: unit 2^31) leaves each point, so a code's bits are
+    # the signs of the table row (bit c set at or above 0); a half turn about the first axis
+    # (raw [0, 1, 0, 0]) maps (a, b, c, d) to (-b, a, -d, c).
+    rng = np.random.default_rng(3)
+    table = rng.integers(-5, 6, (40, 32)).astype(np.int16)
+    ident = np.tile(np.array([1, 0, 0, 0], np.int32), 8)
+    codes = oracle.copy_vocab_codes(ident, table, 2, 2)
+    for v in range(40):
+        for h in range(2):
+            want = sum(1 << c for c in range(16) if table[v, 16 * h + c] >= 0)
+            assert int(codes[v, h]) == want
+    turn = np.tile(np.array([0, 1, 0, 0], np.int32), 8)
+    codes = oracle.copy_vocab_codes(turn, table, 2, 1)
+    for v in range(40):
+        q = table[v, :16].reshape(4, 4).astype(int)
+        rot = np.stack([-q[:, 1], q[:, 0], -q[:, 3], q[:, 2]], 1).reshape(-1)
+        assert int(codes[v, 0]) == sum(1 << c for c in range(16) if rot[c] >= 0)

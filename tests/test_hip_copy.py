@@ -47,3 +47,18 @@ def test_random_streams_match_the_oracle(rule, shape):
     np.testing.assert_array_equal(found, w_found)
     np.testing.assert_array_equal(out, w_out)
     assert found.sum() > rows // 4
+
+
+def test_vocab_codes_match_the_restatement():
+    from uor_fbs.copy import vocab_codes
+    rng = np.random.default_rng(8)
+    table = rng.integers(-32768, 32768, (500, 256)).astype(np.int16)
+    table[:5] = 0                                   # points on the sign boundary
+    rot = rng.integers(-(1 << 31), 1 << 31, 256, dtype=np.int64).astype(np.int32)
+    rot[:4] = 0                                     # a zero quaternion: the unit of nothing
+    print("copy vocab codes", flush=True)
+    got = vocab_codes(rot, table, 8, 4)
+    want = oracle.copy_vocab_codes(rot, table, 8, 4)
+    np.testing.assert_array_equal(got, want)
+    got2 = vocab_codes(rot[:128], table[:, :128], 2, 1)
+    np.testing.assert_array_equal(got2, oracle.copy_vocab_codes(rot[:128], table[:, :128], 2, 1))

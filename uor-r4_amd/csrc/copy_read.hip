@@ -17,8 +17,10 @@
 #include <stdint.h>
 
 #include <string>
+#include <vector>
 
 #include "../../include/uor_copy.h"
+#include "fbs_int.h"
 
 namespace copyread {
 
@@ -196,6 +198,32 @@ __global__ __launch_bounds__(kThreads) void copy_mean_rows(Dev D, const uint32_t
   if (lane == 0) found[row] = heads_found > 0;
 }
 
+// vocab_codes (hamming.rs:566-582): one thread per (token, copy head); the sign word of the
+// token's table point through the head's unit rotations (stack_hamilton, the unit on the left;
+// the products are exact: |unit| <= 2^31, |point| <= 2^15).
+__global__ void copy_vocab_codes(const int64_t *units, const int16_t *table, uint32_t vocab,
+                                 uint32_t width, uint32_t head_width, uint32_t copy,
+                                 uint64_t *codes) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (uint64_t)vocab * copy) return;
+  const uint32_t v = (uint32_t)(i / copy), h = (uint32_t)(i % copy);
+  const int16_t *row = table + (uint64_t)v * width;
+  uint64_t word = 0;
+  for (uint32_t c = 0; c < head_width; c += 4) {
+    const uint32_t at = h * head_width + c;
+    const int64_t *a = units + at;  // the quaternion at / 4
+    const int64_t b0 = row[at], b1 = row[at + 1], b2 = row[at + 2], b3 = row[at + 3];
+    const int64_t r[4] = {a[0] * b0 - a[1] * b1 - a[2] * b2 - a[3] * b3,
+                          a[0] * b1 + a[1] * b0 + a[2] * b3 - a[3] * b2,
+                          a[0] * b2 - a[1] * b3 + a[2] * b0 + a[3] * b1,
+                          a[0] * b3 + a[1] * b2 - a[2] * b1 + a[3] * b0};
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+      if (r[k] >= 0) word |= 1ull << (c + k);
+  }
+  codes[i] = word;
+}
+
 thread_local std::string g_error;
 int fail(int code, const std::string &m) {
   g_error = m;
@@ -324,6 +352,44 @@ extern "C" int uor_copy_mean_rows(void *handle, const uint32_t *tokens, const in
                       hipMemcpy(found, b + of, nf, hipMemcpyDeviceToHost) != hipSuccess ||
                       (chosen && hipMemcpy(chosen, b + och, nch, hipMemcpyDeviceToHost) != hipSuccess)))
         rc = fail(-2, "the read failed on the device");
+    }
+    (void)hipFree(b);
+  }
+  (void)hipSetDevice(prev);
+  return rc;
+}
+
+extern "C" int uor_copy_vocab_codes(const int32_t *key_rotation, const int16_t *table,
+                                    uint32_t vocab, uint32_t width, uint32_t heads_total,
+                                    uint32_t copy, int32_t device, uint64_t *codes) {
+  if (!key_rotation || !table || !codes) return fail(-1, "null buffer");
+  if (vocab < 1 || width < 4 || width % 4 || heads_total < 1 || width % heads_total ||
+      (width / heads_total) % 4 || width / heads_total > 64 || copy < 1 || copy > heads_total)
+    return fail(-1, "codes need width / heads_total a multiple of 4 and at most 64");
+  // The unit rotations g / |g| at Q31 (stack_rotation with lambda 2^31 and epsilon 0).
+  std::vector<int64_t> units(width);
+  for (uint32_t q = 0; q < width / 4; q++) fbs::rotation(key_rotation + 4 * q, 1ull << 31, 0, &units[4 * q]);
+  const size_t nu = (size_t)width * 8, nt = (size_t)vocab * width * 2, nc = (size_t)vocab * copy * 8;
+  const size_t ot = (nu + 255) & ~(size_t)255, oc = (ot + nt + 255) & ~(size_t)255;
+  int prev = 0;
+  (void)hipGetDevice(&prev);
+  if (hipSetDevice(device) != hipSuccess) return fail(-2, "hipSetDevice failed");
+  char *b = nullptr;
+  int rc = 0;
+  if (hipMalloc((void **)&b, oc + nc) != hipSuccess) {
+    rc = fail(-2, "device allocation failed");
+  } else {
+    const uint64_t n = (uint64_t)vocab * copy;
+    if (hipMemcpy(b, units.data(), nu, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(b + ot, table, nt, hipMemcpyHostToDevice) != hipSuccess) {
+      rc = fail(-2, "copy to the device failed");
+    } else {
+      hipLaunchKernelGGL(copy_vocab_codes, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, nullptr,
+                         (const int64_t *)b, (const int16_t *)(b + ot), vocab, width,
+                         width / heads_total, copy, (uint64_t *)(b + oc));
+      if (hipGetLastError() != hipSuccess || hipDeviceSynchronize() != hipSuccess ||
+          hipMemcpy(codes, b + oc, nc, hipMemcpyDeviceToHost) != hipSuccess)
+        rc = fail(-2, "the codes failed on the device");
     }
     (void)hipFree(b);
   }

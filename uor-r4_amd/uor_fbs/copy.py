@@ -17,7 +17,7 @@ import numpy as np
 RULES = {"mean": 0, "latest-exact": 1, "latest-nearest": 2, "longest-exact": 3,
          "longest-after-opening": 4}
 SYMBOLS = ("uor_copy_abi_version", "uor_copy_last_error", "uor_copy_create", "uor_copy_destroy",
-           "uor_copy_mean_rows", "uor_copy_mean_rows_async")
+           "uor_copy_mean_rows", "uor_copy_mean_rows_async", "uor_copy_vocab_codes")
 MAX_KEPT = 32
 
 
@@ -79,6 +79,8 @@ def lib():
         L.uor_copy_destroy.restype = None
         L.uor_copy_mean_rows.argtypes = [P, P, P, P, C.c_uint32, C.c_uint32, P, P, P]
         L.uor_copy_mean_rows_async.argtypes = [P, P, P, P, C.c_uint32, C.c_uint32, P, P, P, P]
+        L.uor_copy_vocab_codes.argtypes = [P, P, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
+                                           C.c_int32, P]
         _lib = L
     return _lib
 
@@ -86,6 +88,17 @@ def lib():
 def _check(code):
     if code:
         raise CopyError(f"uor_copy status {code}: {lib().uor_copy_last_error().decode()}")
+
+
+def vocab_codes(key_rotation, table, heads_total, copy, device=0):
+    """(vocab, copy) uint64: every entry's code per copy head (hamming.rs:566-582), on the GPU."""
+    rot = np.ascontiguousarray(key_rotation, np.int32)
+    table = np.ascontiguousarray(table, np.int16)
+    vocab, width = table.shape
+    codes = np.zeros((vocab, copy), np.uint64)
+    _check(lib().uor_copy_vocab_codes(rot.ctypes.data, table.ctypes.data, vocab, width,
+                                      heads_total, copy, device, codes.ctypes.data))
+    return codes
 
 
 def pack_rows(streams, stride=None):
