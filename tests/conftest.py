@@ -31,7 +31,7 @@ def block_waves(request, monkeypatch):
 @pytest.fixture(scope="session", autouse=True)
 def _oracle_built():
     """The oracle is test infrastructure: build it if a fresh checkout lacks it."""
-    libs = [os.path.join(ROOT, "oracle", "lib", n) for n in ("libfbs_oracle.so", "libd11_oracle.so")]
+    libs = [os.path.join(ROOT, "oracle", "lib", n) for n in ("libfbs_oracle.so", "libd11_oracle.so", "libcopy_oracle.so")]
     if not all(os.path.exists(so) for so in libs):
         subprocess.run(["make", "-C", os.path.join(ROOT, "oracle")], check=True,
                        stdout=subprocess.DEVNULL)

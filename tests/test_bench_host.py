@@ -61,3 +61,20 @@ def test_more_than_one_gpu_is_refused():
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stderr and r.stdout == ""
+
+
+def test_extra_configs_parse_to_their_workloads(monkeypatch):
+    monkeypatch.setattr(sys, "argv", ["bench.py", "--config", "m1"])
+    a = bench.parse()
+    assert (a.batch, a.prompt) == (bench.D11_ROWS, 192) == (14287, 192)
+    monkeypatch.setattr(sys, "argv", ["bench.py", "--config", "copy"])
+    a = bench.parse()
+    assert (a.batch, a.prompt) == (4096, 1024)
+
+
+def test_d11_traffic_summary_has_its_figure():
+    import re
+    text = open(bench.D11_TRAFFIC_SUMMARY).read()
+    m = re.search(r"traffic_bytes_per_launch:\s*(\d+)", text)
+    assert m and int(m.group(1)) > 14287 * 656  # at least the records written
+    assert bench.D11_PUBLISHED["value"] == 183206
