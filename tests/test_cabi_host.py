@@ -413,3 +413,20 @@ def test_copy_library_exports_and_refusals():
     s, keep = heads.c_struct()
     assert L.uor_copy_create(C.byref(s), 0, C.byref(P())) == -1
     assert b"marker" in L.uor_copy_last_error()
+
+
+def test_norm_factor_pow2_at_its_edges(hp):
+    # The factor's double estimates at the ends of their ranges: mean squares of 1 (s = 2^34,
+    # r = 2^62), at the 60-bit mask's top, on and one off perfect squares and powers of two,
+    # each entered as epsilon over a zero sum.
+    hp.fbs_hp_norm_factor_check.argtypes = [P, P, C.c_uint64, C.c_uint32]
+    hp.fbs_hp_norm_factor_check.restype = C.c_uint64
+    vals = [1, 2, 3, 15, 16, 17, 2**60 - 1, 2**60 - 2, 2**60 - 17, 2**59, 2**59 - 1, 2**59 + 1]
+    for k in range(1, 31):
+        for v in (k * k, (2**k) ** 2, (2**k - 1) ** 2, 3**k):
+            vals += [v - 1, v, v + 1]
+    for k in range(1, 61):
+        vals += [2**k - 1, 2**k, 2**k + 1]
+    eps = np.array([v for v in vals if 0 < v < 2**63], dtype=np.int64)
+    sums = np.zeros(len(eps), np.uint64)
+    assert hp.fbs_hp_norm_factor_check(sums.ctypes.data_as(P), eps.ctypes.data_as(P), len(eps), 5) == 0

@@ -454,6 +454,7 @@ FBS_HD uint64_t div_2p96(uint64_t s, const Seeds &sd = Seeds()) {
 // fh^2 <= 2^(J+1) rho.
 FBS_HD NormFactor norm_factor_pow2(uint64_t sum, uint32_t log2n, int64_t eps_int,
                                     const Seeds &sd = Seeds()) {
+  (void)sd;
   NormFactor out;
   int64_t ms = wadd64((int64_t)(sum >> log2n), eps_int);
   if (ms < 1) ms = 1;
@@ -463,46 +464,34 @@ FBS_HD NormFactor norm_factor_pow2(uint64_t sum, uint32_t log2n, int64_t eps_int
     out.huge = true;
     return out;
   }
+  // s = isqrt(M 2^64), M = 16 m in [16, 2^64): a double estimate within 2^12 + 1, one Newton
+  // step on the exact 128-bit residual (its excess over sqrt(M 2^64) is below 2^-9, the
+  // residual's conversion to double moves it by less than 2^-10), then one exact step each way.
   const uint64_t M = m << 4;
-  const int z = clz64(M) & ~1;
-  const uint64_t mn = M << z;
-  const int J = 32 - (z >> 1);                        // [3, 32]
-  const uint64_t mt = mn >> 32;
-  const uint64_t y = rsqrt_q46((uint32_t)mt, sd.rsqrt);
-  uint64_t t = (mt * y) >> 30;
-  t = t > 0xffffffffull ? 0xffffffffull : t;
-  const int64_t diff = (int64_t)(mn - t * t);
-  t = (uint64_t)((int64_t)t + (((diff >> 16) * (int64_t)y) >> 47));
-  t = t > 0xffffffffull ? 0xffffffffull : t < (1ull << 31) ? (1ull << 31) : t;
-  uint64_t sq = t * t;
-  if (sq > mn) {
-    t -= 1;
-    sq -= 2 * t + 1;
+  const u128 N = (u128)M << 64;
+  const double sx = sqrt((double)M) * 4294967296.0;
+  const uint64_t s0 = sx >= 18446744073709551615.0 ? ~0ull : (uint64_t)sx;
+  const i128 e = (i128)(N - (u128)s0 * s0);  // |e| < 2^78: exact as a signed value
+  const double ed = (double)(int64_t)(e >> 64) * 18446744073709551616.0 + (double)(uint64_t)e;
+  const double cd = floor(ed / (2.0 * (double)s0));
+  uint64_t s = s0 + (uint64_t)(int64_t)cd;  // |cd| < 2^14
+  u128 sq = (u128)s * s;
+  if (sq > N) {
+    s -= 1;
+  } else if (s < ~0ull && sq + 2 * (u128)s + 1 <= N) {
+    s += 1;
   }
-  if (t < 0xffffffffull && sq + 2 * t + 1 <= mn) {
-    sq += 2 * t + 1;
-    t += 1;
-  }
-  const uint64_t rem = mn - sq;                       // [0, 2 t] <= 2^33 - 2
-  const uint64_t num = rem << (J - 1);                // < 2^64
-  const uint64_t w = recip_q63((uint32_t)t, sd.recip); // ~ 2^63 / t
-  uint64_t fh = ((num >> 32) * w) >> 31;              // [q - 9, q]
-  const uint64_t r0 = num - fh * t;                   // [0, 10 t)
-  fh += ((r0 >> 4) * w) >> 59;                        // [q - 1, q]
-  uint64_t rho = num - fh * t;                        // [0, 2 t)
-  if (rho >= t) {
-    fh += 1;
-    rho -= t;
-  }
-  uint64_t f = fh;
-  if (fh >> J) {
-    f = fh - 1;                                       // f < 2^J
-  } else if (fh) {
-    const bool big = (rho >> (63 - J)) != 0;          // 2^(J+1) rho >= 2^64 > fh^2
-    if (!big && fh * fh > (rho << (J + 1))) f = fh - 1;
-  }
-  const uint64_t s = (t << J) + f;                    // >= 2^34
-  out.r = div_2p96(s, sd);
+  // r = floor(2^96 / s), s in [2^34, 2^64): a double estimate within 2^11, one correction from
+  // the exact 128-bit remainder (within 1), then one exact step each way.
+  const u128 P96 = (u128)1 << 96;
+  const uint64_t r0 = (uint64_t)(79228162514264337593543950336.0 / (double)s);
+  const i128 rem0 = (i128)(P96 - (u128)r0 * s);  // |rem0| < 2^12 s
+  const double rd = (double)(int64_t)(rem0 >> 64) * 18446744073709551616.0 + (double)(uint64_t)rem0;
+  uint64_t r = (uint64_t)((int64_t)r0 + (int64_t)floor(rd / (double)s));
+  const i128 rem = (i128)(P96 - (u128)r * s);
+  if (rem < 0) r -= 1;
+  else if (rem >= (i128)s) r += 1;
+  out.r = r;
   out.huge = false;
   return out;
 }
