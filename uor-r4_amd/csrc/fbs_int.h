@@ -710,24 +710,11 @@ FBS_HD void unit_q30(const int32_t raw[4], uint64_t eps, int32_t u[4], const See
   }
   // X = 0 (all zero, eps 0) gives u = 0 by the same steps on X = 1.
   xl = (xh == 0 && xl == 0) ? 1 : xl;
-  // Both normalisations are formed and one is kept by masks (one basic block, so that the
-  // scheduler can interleave independent rotations).
-  const int z = clz64(xl) & ~1;
-  const uint64_t big = 0ull - (uint64_t)(xh != 0);
-  const uint64_t xn = ((((uint64_t)xh << 62) | (xl >> 2)) & big) | ((xl << z) & ~big);
-  const int j = xh ? 17 : 16 - (z >> 1);              // [-15, 17]
-  const uint64_t xt = xn >> 32;
-  const uint64_t y = rsqrt_q46((uint32_t)xt, sd.rsqrt);
-  uint64_t r = (xt * y) >> 30;
-  r = r > 0xffffffffull ? 0xffffffffull : r;
-  const int64_t diff = (int64_t)(xn - r * r);
-  r = (uint64_t)((int64_t)r + (((diff >> 16) * (int64_t)y) >> 47));
-  r = r > 0xffffffffull ? 0xffffffffull : r < (1ull << 31) ? (1ull << 31) : r;
-  const int64_t rem = (int64_t)(xn - r * r);          // [-2^33, 2^34]
-  const int jp = j > 0 ? j : 0, jn = j > 0 ? 0 : -j;
-  const int64_t f = (rem * (int64_t)(y >> 2)) >> (61 - jp);
-  const uint64_t frac = 0ull - (uint64_t)(j > 0);
-  uint64_t s = (((r << jp) + (uint64_t)f) & frac) | ((r >> jn) & ~frac);
+  // s0 = floor(sqrt(X) 2^16) from a double: X rounds to 53 bits and the root adds one rounding,
+  // so s0 is within 2^-4 of the real root's floor argument, hence within 1 of s = isqrt(Y).
+  (void)sd;
+  const double xd = (double)xh * 18446744073709551616.0 + (double)xl;
+  uint64_t s = (uint64_t)(sqrt(xd) * 65536.0);
   // Y - s^2 modulo 2^64: s < 2^50, so s^2 mod 2^64 = sl^2 + (2 sh sl mod 2^32) 2^32.
   const uint32_t sl = (uint32_t)s, shi = (uint32_t)(s >> 32);
   int64_t dy = (int64_t)((xl << 32) - ((uint64_t)sl * sl + ((uint64_t)(2u * shi * sl) << 32)));
@@ -736,13 +723,13 @@ FBS_HD void unit_q30(const int32_t raw[4], uint64_t eps, int32_t u[4], const See
   s = down ? s - 1 : s;
   const bool up = dy >= (int64_t)(2 * s + 1);
   s = up ? s + 1 : s;
-  // u_c = floor(a_c 2^46 / s), s in [2^16, 2^49].
-  const int zs = clz64(s);
-  const uint64_t w = recip_q63((uint32_t)((s << zs) >> 32), sd.recip);  // ~ 2^95 / (s << zs)
-  const int sh = 49 - zs;
+  // u_c = floor(a_c 2^46 / s), s in [2^16, 2^49]: a_c 2^46 times the double reciprocal of s is
+  // within 2^-21 of the quotient (at most 2^30 + 2^14), so q0 is within 1 of the floor; one step
+  // each way on the exact remainder a_c 2^46 - q0 s (small, exact modulo 2^64) gives q.
+  const double inv = 1.0 / (double)s;
 #pragma unroll
   for (int c = 0; c < 4; c++) {
-    uint64_t q = ((uint64_t)a[c] * w) >> sh;
+    uint64_t q = (uint64_t)((double)a[c] * 70368744177664.0 * inv);
     int64_t rq = (int64_t)(((uint64_t)a[c] << 46) - q * s);
     const bool qd = rq < 0;
     rq = qd ? rq + (int64_t)s : rq;
@@ -751,7 +738,6 @@ FBS_HD void unit_q30(const int32_t raw[4], uint64_t eps, int32_t u[4], const See
     u[c] = raw[c] < 0 ? -(int32_t)q : (int32_t)q;
   }
 }
-
 // (lambda u) >> 30 for lambda = 2^p (p <= 31): u << (p - 30) or floor(u / 2^(30 - p)).
 FBS_HD int64_t scale_pow2(int32_t u, uint32_t p) {
   return p >= 30 ? (int64_t)u << (p - 30) : (int64_t)(u >> (30 - p));
