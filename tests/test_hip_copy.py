@@ -62,3 +62,33 @@ def test_vocab_codes_match_the_restatement():
     np.testing.assert_array_equal(got, want)
     got2 = vocab_codes(rot[:128], table[:, :128], 2, 1)
     np.testing.assert_array_equal(got2, oracle.copy_vocab_codes(rot[:128], table[:, :128], 2, 1))
+
+
+def test_device_buffers_and_a_stream_outside_the_vocabulary_reads_nothing():
+    # uor_copy_mean_rows_async over device arrays on the default stream: a stream holding a
+    # token outside the vocabulary (the host call refuses it) reads nothing; the others equal
+    # the oracle. The same for lengths outside 0..stride.
+    from uor_fbs import copy as cp
+    from uor_fbs.hipmem import DeviceArray
+    heads = K.random_heads(5, vocab=100, width=64, copy=2, kept=4)
+    tok, lens, _ = K.random_streams(6, 100, 12, 30)
+    tok[3, 2] = 100
+    lens[3] = max(lens[3], 5)
+    lens[4] = 31                                    # longer than the stride
+    print("copy device buffers", flush=True)
+    gpu = CopyHeads(heads)
+    try:
+        dt, dl = DeviceArray(tok.shape, np.uint32), DeviceArray(lens.shape, np.int32)
+        do, df = DeviceArray((12, 64), np.int64), DeviceArray(12, np.uint8)
+        dt.upload(tok)
+        dl.upload(lens)
+        assert cp.lib().uor_copy_mean_rows_async(gpu.handle, dt.ptr, dl.ptr, None, 12, 30,
+                                                 do.ptr, df.ptr, None, None) == 0
+        out, found = do.download(), df.download().astype(bool)
+    finally:
+        gpu.close()
+    assert not found[3] and not found[4] and not out[3].any() and not out[4].any()
+    keep = [r for r in range(12) if r not in (3, 4)]
+    w_out, w_found, _ = oracle.copy_mean_rows(heads, tok[keep], lens[keep])
+    np.testing.assert_array_equal(out[keep], w_out)
+    np.testing.assert_array_equal(found[keep], w_found)
