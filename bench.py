@@ -47,6 +47,8 @@ TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fbs_decode_pair_c3_b1024_traff
 D11_TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "d11_score_rows_m1_traffic.md")
 # BASELINE.json's configs at their full shapes: (sequences, prompt, decode steps); c4 is
 # teacher-forced scoring of (rows, row length).
+# Query bytes a candidate-statistics replay may move (the whole batch at C2/C3).
+REPLAY_BYTES = 6 << 30
 CONFIG_SHAPES = {"c1": (1, 256, 256), "c2": (1024, 512, 512), "c3": (1024, 1024, 1024),
                  "c4": (1 << 20, 128, 0), "c5": (16384, 4096, 4096)}
 # The discrete M1 panel scorer (uor_d11_score_rows): the reference's ft/dev panel size, the M1
@@ -77,6 +79,44 @@ def cpu_model() -> str:
     return "unknown"
 
 
+def cpu_threads(a) -> tuple[int, dict]:
+    """Threads for the CPU baseline and what they are: every core this process may run on
+    (its affinity), capped at the CPU share the GPU box grants one GPU, which it states in
+    OMP_NUM_THREADS (16 there); --cpu-threads overrides."""
+    affinity = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS")
+    share = int(omp) if omp and omp.isdigit() and int(omp) > 0 else affinity
+    threads = a.cpu_threads or max(1, min(affinity, share))
+    return threads, {"affinity_cores": affinity, "cpu_count": os.cpu_count(),
+                     "omp_num_threads": omp, "cpu_model": cpu_model()}
+
+
+def cpu_protocol(run, units: int, runs: int, warmup: int = 1, same=None) -> dict:
+    """The reference's CPU timing protocol (src/bin/fbs-toks.rs:1513-1610): `warmup` untimed
+    runs, then `runs` timed ones that must all give the same result; integer nanoseconds, the
+    median (integer mean of the middle two for an even count), the nearest-rank p95, and
+    integer units per second at each. Returns the summary and the first timed result."""
+    for _ in range(warmup):
+        run()
+    raw, first = [], None
+    for _ in range(runs):
+        t0 = time.perf_counter_ns()
+        r = run()
+        raw.append(time.perf_counter_ns() - t0)
+        if first is None:
+            first = r
+        elif same is not None and not same(first, r):
+            raise RuntimeError("timed CPU runs gave different results")
+    srt = sorted(raw)
+    n = len(srt)
+    med = srt[n // 2] if n % 2 else (srt[n // 2 - 1] + srt[n // 2]) // 2
+    p95 = srt[max(1, -(-n * 95 // 100)) - 1]
+    per_s = lambda ns: units * 1_000_000_000 // max(ns, 1)  # noqa: E731
+    return {"warmup_runs": warmup, "timed_runs": runs, "units_per_run": units, "raw_ns": raw,
+            "median_ns": med, "p95_ns": p95, "median_per_s": per_s(med),
+            "p95_per_s": per_s(p95)}, first
+
+
 def parse():
     p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -89,7 +129,13 @@ def parse():
     p.add_argument("--gen", type=int, default=None, help="decode steps per timed step")
     p.add_argument("--seed", type=int, default=2026120203)
     p.add_argument("--cpu-seconds", type=float, default=24.0, help="target CPU-baseline sample time")
-    p.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, cores)")
+    p.add_argument("--cpu-threads", type=int, default=0,
+                   help="0: the host cores this process may run on, capped at the CPU share the "
+                        "box grants one GPU (OMP_NUM_THREADS where set)")
+    p.add_argument("--cpu-runs", type=int, default=20,
+                   help="timed CPU-baseline runs after one warm-up (fbs-toks' protocol)")
+    p.add_argument("--no-writer-memory-pass", action="store_true",
+                   help="skip the extra timed pass with the writer's memory of its last query off")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--serve-steps", type=int, default=64,
                    help="serving-loop launches after the decode (0: none); reported beside the metric")
@@ -393,22 +439,31 @@ def score_main(a, torch, oracle, art, model, rows, dev, stream, sp) -> dict:
     }
     if not a.no_cpu:
         log("c4: CPU baseline")
-        threads = a.cpu_threads or min(16, os.cpu_count() or 1)
+        threads, host = cpu_threads(a)
         t0 = time.perf_counter()
         oracle.score(art, rows[:threads], threads=threads)
         per_row = (time.perf_counter() - t0) / threads
-        n_cpu = int(min(R, max(threads, a.cpu_seconds / per_row)))
+        per_run = a.cpu_seconds / (a.cpu_runs + 1)
+        n_cpu = int(min(R, max(threads, per_run / per_row)))
         n_cpu -= n_cpu % threads if n_cpu > threads else 0
-        t0 = time.perf_counter()
-        st, cpu_matches, cpu_argmin = oracle.score(art, rows[:n_cpu], threads=threads)
-        cpu_s = time.perf_counter() - t0
+
+        def cpu_run():
+            st_, m_, arg_ = oracle.score(art, rows[:n_cpu], threads=threads)
+            assert st_ == 0
+            return m_, arg_
+
+        proto, (cpu_matches, cpu_argmin) = cpu_protocol(
+            cpu_run, n_cpu * n, a.cpu_runs,
+            same=lambda x, y: x[0] == y[0] and np.array_equal(x[1], y[1]))
         gpu_matches, gpu_argmin = model.score(rows[:n_cpu])
-        same = st == 0 and cpu_matches == gpu_matches and np.array_equal(cpu_argmin, gpu_argmin)
+        same = cpu_matches == gpu_matches and np.array_equal(cpu_argmin, gpu_argmin)
         out["cpu_baseline"] = {
-            "value": round(n_cpu * n / cpu_s, 1), "unit": "positions/s",
-            "cores": min(threads, n_cpu), "cpu_model": cpu_model(), "kind": "port",
-            "sample": f"the first {n_cpu} of the {R} rows ({cpu_s:.1f} s), oracle C restatement, "
-                      f"one row per thread", "choices_equal_gpu": bool(same)}
+            "value": proto["median_per_s"], "unit": "positions/s",
+            "cores": min(threads, n_cpu), **host, "kind": "port",
+            "sample": f"the first {n_cpu} of the {R} rows per run, oracle C restatement, one row "
+                      f"per thread; value = integer median over {a.cpu_runs} timed runs after "
+                      f"one warm-up", "p95_positions_per_s": proto["p95_per_s"],
+            "protocol": proto, "choices_equal_gpu": bool(same)}
         if not same:
             print("bench.py: CPU scoring differs from the GPU's", file=sys.stderr)
     return out
@@ -498,23 +553,25 @@ def d11_main(a, torch, oracle) -> dict:
                      "launch_ms": [round(x, 3) for x in launch_ms]},
     }
     if not a.no_cpu:
-        threads = a.cpu_threads or min(16, os.cpu_count() or 1)
+        threads, host = cpu_threads(a)
         cpu_model_ = oracle.D11Oracle(art)  # loaded once, as the reference's from_bytes
         n_cal = threads * 8
         t0 = time.perf_counter()
         cpu_model_.score_rows(pre[:n_cal], lens[:n_cal], tg[:n_cal], threads=threads)
         per_row = (time.perf_counter() - t0) / n_cal
-        n_cpu = int(min(R, max(threads, a.cpu_seconds / per_row)))
-        t0 = time.perf_counter()
-        cpu = cpu_model_.score_rows(pre[:n_cpu], lens[:n_cpu], tg[:n_cpu], threads=threads)
-        cpu_s = time.perf_counter() - t0
+        n_cpu = int(min(R, max(threads, a.cpu_seconds / (a.cpu_runs + 1) / per_row)))
+        proto, cpu = cpu_protocol(
+            lambda: cpu_model_.score_rows(pre[:n_cpu], lens[:n_cpu], tg[:n_cpu], threads=threads),
+            n_cpu, a.cpu_runs, same=lambda x, y: np.array_equal(x.view(np.uint32), y.view(np.uint32)))
         cpu_model_.close()
         same = np.array_equal(cpu.view(np.uint32), recs[:n_cpu].view(np.uint32))
         out["cpu_baseline"] = {
-            "value": round(n_cpu / cpu_s, 1), "unit": "response tokens/s",
-            "cores": min(threads, n_cpu), "cpu_model": cpu_model(), "kind": "port",
-            "sample": f"the first {n_cpu} of the {R} rows ({cpu_s:.1f} s), oracle C restatement, "
-                      "one row per thread", "records_equal_gpu": bool(same)}
+            "value": proto["median_per_s"], "unit": "response tokens/s",
+            "cores": min(threads, n_cpu), **host, "kind": "port",
+            "sample": f"the first {n_cpu} of the {R} rows per run, oracle C restatement, one row "
+                      f"per thread; value = integer median over {a.cpu_runs} timed runs after "
+                      f"one warm-up", "p95_response_tokens_per_s": proto["p95_per_s"],
+            "protocol": proto, "records_equal_gpu": bool(same)}
         if not same:
             print("bench.py: CPU records differ from the GPU's", file=sys.stderr)
     model.close()
@@ -584,19 +641,21 @@ def copy_main(a, torch, oracle) -> dict:
     got_out = d_out.cpu().numpy()
     got_found = d_found.cpu().numpy().astype(bool)
     if not a.no_cpu:
-        threads = 1  # the oracle is single-threaded
+        _, host = cpu_threads(a)
         t0 = time.perf_counter()
         oracle.copy_mean_rows(heads, tok[:8], lens[:8])
         per = (time.perf_counter() - t0) / 8
-        n_cpu = int(min(R, max(8, a.cpu_seconds / per)))
-        t0 = time.perf_counter()
-        w_out, w_found, _ = oracle.copy_mean_rows(heads, tok[:n_cpu], lens[:n_cpu])
-        cpu_s = time.perf_counter() - t0
+        n_cpu = int(min(R, max(8, a.cpu_seconds / (a.cpu_runs + 1) / per)))
+        proto, (w_out, w_found, _) = cpu_protocol(
+            lambda: oracle.copy_mean_rows(heads, tok[:n_cpu], lens[:n_cpu]), n_cpu, a.cpu_runs,
+            same=lambda x, y: np.array_equal(x[0], y[0]) and np.array_equal(x[1], y[1]))
         same = np.array_equal(w_out, got_out[:n_cpu]) and np.array_equal(w_found, got_found[:n_cpu])
-        out["cpu_baseline"] = {"value": round(n_cpu / cpu_s, 1), "unit": "reads/s",
-                               "cores": threads, "cpu_model": cpu_model(), "kind": "port",
-                               "sample": f"the first {n_cpu} of the {R} streams ({cpu_s:.1f} s), "
-                                         "oracle C restatement, one thread",
+        out["cpu_baseline"] = {"value": proto["median_per_s"], "unit": "reads/s",
+                               "cores": 1, **host, "kind": "port",
+                               "sample": f"the first {n_cpu} of the {R} streams per run, oracle "
+                                         f"C restatement on one thread (it has no threaded form); "
+                                         f"value = integer median over {a.cpu_runs} timed runs "
+                                         f"after one warm-up", "protocol": proto,
                                "reads_equal_gpu": bool(same)}
     gpu.close()
     return out
@@ -694,28 +753,81 @@ def main():
     tokens = B * G
     value = tokens / (ms_per_step / 1e3)
 
-    # Candidate rows per decoded token, exactly, from a teacher-forced replay of a sample of
-    # the decoded sequences: the prompt, the prefill's choice, then the reply (the replay
-    # reproduces the decode's states, queries and kept drawers at positions prompt ..).
+    # Candidate rows per decoded token, exactly, from a teacher-forced replay of the decoded
+    # sequences (every one, unless their queries would exceed REPLAY_BYTES: then evenly spaced
+    # ones): the prompt, the prefill's choice, then the reply; the replay reproduces the
+    # decode's states, queries and kept drawers at positions prompt .. .
     host_reply = reply.cpu().numpy().view(np.uint32)
     host_first = first.cpu().numpy().view(np.uint32)
-    sample = min(B, 64)
-    replay = np.concatenate([prompts[:sample], host_first[:sample], host_reply[:sample, :-1]], axis=1)
-    _, kept, query = model.sequences(replay)
+    per_seq = (a.prompt + G) * spec.width * 4
+    n_rep = int(min(B, max(1, REPLAY_BYTES // per_seq)))
+    rep_ids = np.linspace(0, B - 1, n_rep).astype(np.int64) if n_rep < B else np.arange(B)
     sizes = art.drawer_sizes()
-    cand = sizes[kept[:, a.prompt:, :].astype(np.int64)].sum(-1)
-    mean_cand = float(cand.mean())
+    cand_sum = scanned_sum = reused_n = 0
+    chunk = max(1, min(256, (1 << 29) // per_seq))
+    for c0 in range(0, n_rep, chunk):
+        ids = rep_ids[c0:c0 + chunk]
+        replay = np.concatenate([prompts[ids], host_first[ids], host_reply[ids, :-1]], axis=1)
+        _, kept, query = model.sequences(replay)
+        cand = sizes[kept[:, a.prompt:, :].astype(np.int64)].sum(-1)
+        # The writer takes its previous result when a query repeats its last run's exactly (a
+        # sequence settled on a fixed point): those tokens scan no candidate rows. Each launch
+        # starts with nothing remembered, so the first generated token always scans.
+        q = query[:, a.prompt:]
+        reused = np.zeros(q.shape[:2], dtype=bool)
+        reused[:, 1:] = (q[:, 1:] == q[:, :-1]).all(-1)
+        cand_sum += int(cand.sum())
+        scanned_sum += int(np.where(reused, 0, cand).sum())
+        reused_n += int(reused.sum())
+        del kept, query, q
+    n_tok = n_rep * G
+    mean_cand = cand_sum / n_tok
+    scanned_cand = scanned_sum / n_tok
     bpt = algorithmic_bytes_per_token(spec, mean_cand)
     mean_launch_s = float(np.mean(launch_ms)) / 1e3
     achieved = bpt * tokens / mean_launch_s / 1e9
-    # The writer takes its previous result when a query repeats its last run's exactly (a
-    # sequence settled on a fixed point): those tokens scan no candidate rows. Each launch
-    # starts with nothing remembered, so the first generated token always scans.
-    q = query[:, a.prompt:]
-    reused = np.zeros(q.shape[:2], dtype=bool)
-    reused[:, 1:] = (q[:, 1:] == q[:, :-1]).all(-1)
-    scanned_cand = float(np.where(reused, 0, cand).mean())
     bpt_scanned = algorithmic_bytes_per_token(spec, scanned_cand)
+
+    # The same launches with the writer's memory of its last query off: every decoded token
+    # then scans its candidates, so every token moves the algorithmic bytes.
+    no_memory = None
+    if not a.no_writer_memory_pass:
+        os.environ["UOR_FBS_WRITER_MEMORY"] = "0"
+        try:
+            model_nm = hip.Model(art, device=0)
+        finally:
+            del os.environ["UOR_FBS_WRITER_MEMORY"]
+        reply_nm = torch.zeros_like(reply)
+
+        def step_nm():
+            check(L.uor_fbs_decode_async(model_nm.handle, ptr(first), B, 1, G - 1, ptr(reply_nm),
+                                         ptr(state), ptr(hist), ptr(pos), None, None, None,
+                                         ptr(status), sp))
+
+        step_nm()
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(a.steps)]
+        t0 = time.perf_counter()
+        for s_, e_ in ev:
+            s_.record(stream)
+            step_nm()
+            e_.record(stream)
+        torch.cuda.synchronize()
+        wall_nm = time.perf_counter() - t0
+        assert int(status.abs().sum()) == 0, "decode without the writer memory failed"
+        ms_nm = [s_.elapsed_time(e_) for s_, e_ in ev]
+        mean_nm = float(np.mean(ms_nm)) / 1e3
+        no_memory = {
+            "value": round(tokens / (wall_nm / a.steps), 1),
+            "ms_per_step": round(wall_nm * 1e3 / a.steps, 3),
+            "frac": round(bpt * tokens / mean_nm / 1e9 / HBM_PEAK_GBS, 4),
+            "launch_ms": [round(x, 3) for x in ms_nm],
+            "replies_equal": bool(torch.equal(reply_nm, reply)),
+            "what": "UOR_FBS_WRITER_MEMORY=0 at model creation: no step takes the writer's "
+                    "previous result",
+        }
+        del model_nm
     S = 1
     while S < spec.width // 32:
         S *= 2
@@ -749,10 +861,11 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
             "algorithmic_bytes_per_launch": round(bpt * tokens),
             "bytes_per_token": round(bpt, 1), "mean_candidate_rows": round(mean_cand, 1),
-            "writer_reuse_fraction": round(float(reused.mean()), 4),
+            "writer_reuse_fraction": round(reused_n / n_tok, 4),
             "bytes_per_token_scanned": round(bpt_scanned, 1),
             "frac_scanned": round(bpt_scanned * tokens / mean_launch_s / 1e9 / HBM_PEAK_GBS, 4),
-            "replay_sample": sample,
+            "replay_sequences": n_rep,
+            "without_writer_memory": no_memory,
             "kernel": kernel, "launch_ms": [round(x, 3) for x in launch_ms],
         },
         "prefill_tokens_per_s": round(B * a.prompt / prefill_s, 1),
@@ -813,32 +926,42 @@ def main():
 
     if not a.no_cpu:
         log(f"{a.config}: CPU baseline")
-        threads = a.cpu_threads or min(16, os.cpu_count() or 1)
+        threads, host = cpu_threads(a)
         st_np = state.cpu().numpy()
         hist_np = hist.cpu().numpy()
         pos_np = pos.cpu().numpy().view(np.uint32)
         first_np = first.cpu().numpy().view(np.uint32)
-        # Calibrate: a small run, then a sample sized to about --cpu-seconds: every sequence
-        # (one per thread at a time) for as many leading decode steps as that allows.
+        # Calibrate: a small run, then a sample sized so that a warm-up and --cpu-runs timed
+        # runs take about --cpu-seconds: sequences (one per thread at a time) for as many
+        # leading decode steps as that allows, fewer sequences where two steps of all are long.
         n_cal, g_cal = min(B, threads), min(G, 4)
         t0 = time.perf_counter()
         oracle.decode(art, first_np[:n_cal], g_cal - 1, threads=threads, in_state=st_np[:n_cal],
                       in_history=hist_np[:n_cal], in_position=pos_np[:n_cal], want_state=False)
         per_tok = (time.perf_counter() - t0) / (n_cal * g_cal)
+        per_run = a.cpu_seconds / (a.cpu_runs + 1)
         n_cpu = B if B < threads else (B // threads) * threads
-        g_cpu = int(min(G, max(4, a.cpu_seconds / per_tok / n_cpu)))
-        t0 = time.perf_counter()
-        res = oracle.decode(art, first_np[:n_cpu], g_cpu - 1, threads=threads,
-                            in_state=st_np[:n_cpu], in_history=hist_np[:n_cpu],
-                            in_position=pos_np[:n_cpu], want_state=False)
-        cpu_s = time.perf_counter() - t0
-        assert res["status"] == 0
-        same = np.array_equal(res["reply"], host_reply[:n_cpu, :g_cpu])
+        g_cpu = int(min(G, max(2, per_run / per_tok / n_cpu)))
+        if n_cpu > threads and n_cpu * g_cpu * per_tok > 1.5 * per_run:
+            n_cpu = max(threads, int(per_run / per_tok / g_cpu) // threads * threads)
+
+        def cpu_run():
+            r = oracle.decode(art, first_np[:n_cpu], g_cpu - 1, threads=threads,
+                              in_state=st_np[:n_cpu], in_history=hist_np[:n_cpu],
+                              in_position=pos_np[:n_cpu], want_state=False)
+            assert r["status"] == 0
+            return r["reply"]
+
+        proto, cpu_reply = cpu_protocol(cpu_run, n_cpu * g_cpu, a.cpu_runs,
+                                        same=np.array_equal)
+        same = np.array_equal(cpu_reply, host_reply[:n_cpu, :g_cpu])
         out["cpu_baseline"] = {
-            "value": round(n_cpu * g_cpu / cpu_s, 1), "unit": "tokens/s",
-            "cores": min(threads, n_cpu), "cpu_model": cpu_model(), "kind": "port",
+            "value": proto["median_per_s"], "unit": "tokens/s",
+            "cores": min(threads, n_cpu), **host, "kind": "port",
             "sample": f"{n_cpu} of the {B} prefilled sequences x the first {g_cpu} decode steps "
-                      f"({cpu_s:.1f} s), oracle C restatement, one sequence per thread",
+                      f"per run, oracle C restatement, one sequence per thread; value = integer "
+                      f"median over {a.cpu_runs} timed runs after one warm-up",
+            "p95_tokens_per_s": proto["p95_per_s"], "protocol": proto,
             "replies_equal_gpu": bool(same),
         }
         if not same:

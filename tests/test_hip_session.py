@@ -205,3 +205,25 @@ def test_slot_bounds_are_checked_by_the_kernel(art):
     assert pool.position.download().tolist() == [1, 1]
     r = reply.download()
     assert r[0] == r[2]
+
+
+def test_session_slots_are_checked_on_the_host(art):
+    """A caller-chosen slot must lie in the pool and be free; it is then held like an acquired
+    one. Device rows are bounds-checked before any copy."""
+    print("session slot checks", flush=True)
+    pool = SessionPool(hip.Model(art), capacity=3)
+    with pytest.raises(ValueError):
+        Session(pool, slot=3)
+    a = Session(pool, slot=1)
+    with pytest.raises(ValueError):
+        Session(pool, slot=1)
+    b, c = Session(pool), Session(pool)
+    assert sorted([a.slot, b.slot, c.slot]) == [0, 1, 2]
+    with pytest.raises(SessionError):
+        Session(pool)
+    a.close()
+    assert Session(pool, slot=1).slot == 1
+    with pytest.raises(IndexError):
+        pool.position.zero([3])
+    with pytest.raises(IndexError):
+        pool.position.download(row=3)

@@ -80,11 +80,19 @@ __device__ __forceinline__ uint64_t joined(const Dev &D, uint32_t near, uint32_t
   return first ? (c & first) | (code(D, far, h) & ~first) : c;
 }
 
+// n / k rounded toward zero (Rust's i128 division), for k >= 1, in the integer division of
+// fbs_int.h: the kernels divide by no variable with the compiler's `/`, whose expansion goes
+// through a float reciprocal estimate.
+__device__ __forceinline__ int64_t div_trunc(int64_t n, uint32_t k) {
+  const uint64_t q = fbs::div128_64(fbs::uabs64(n), k);
+  return n < 0 ? -(int64_t)q : (int64_t)q;
+}
+
 // copy_weight_q31 (:243-252)
 __device__ __forceinline__ uint64_t weight_q31(int32_t margin, uint32_t d) {
   const int64_t over = (int64_t)margin - ((int64_t)d << 16);
   if (over <= 0) return 0;
-  return ((uint64_t)over << 31) / (uint64_t)(margin > (1 << 16) ? margin : (1 << 16));
+  return fbs::div128_64((fbs::u128)((uint64_t)over << 31), (uint64_t)(margin > (1 << 16) ? margin : (1 << 16)));
 }
 
 __global__ __launch_bounds__(kThreads) void copy_mean_rows(Dev D, const uint32_t *tokens,
@@ -186,14 +194,14 @@ __global__ __launch_bounds__(kThreads) void copy_mean_rows(Dev D, const uint32_t
     if (count) {
       heads_found++;
 #pragma unroll
-      for (int j = 0; j < kPerLane; j++) sum[j] += head[j] / count;
+      for (int j = 0; j < kPerLane; j++) sum[j] += div_trunc(head[j], count);
     }
     wave_sync();
   }
 #pragma unroll
   for (int j = 0; j < kPerLane; j++) {
     const uint32_t c = (uint32_t)lane + 64u * j;
-    if (c < D.width) out[(uint64_t)row * D.width + c] = heads_found ? sum[j] / heads_found : 0;
+    if (c < D.width) out[(uint64_t)row * D.width + c] = heads_found ? div_trunc(sum[j], heads_found) : 0;
   }
   if (lane == 0) found[row] = heads_found > 0;
 }
@@ -206,7 +214,7 @@ __global__ void copy_vocab_codes(const int64_t *units, const int16_t *table, uin
                                  uint64_t *codes) {
   const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (uint64_t)vocab * copy) return;
-  const uint32_t v = (uint32_t)(i / copy), h = (uint32_t)(i % copy);
+  const uint32_t v = (uint32_t)fbs::div128_64(i, copy), h = (uint32_t)(i - (uint64_t)v * copy);
   const int16_t *row = table + (uint64_t)v * width;
   uint64_t word = 0;
   for (uint32_t c = 0; c < head_width; c += 4) {

@@ -436,6 +436,19 @@ __device__ int flock_block(const DevModel &M, const Geo &g, const Plan &P, WaveL
   return snap_wave(g, u, terms, lane);
 }
 
+// p / c for 0 <= p < 256 and 1 <= c <= 16 by restoring subtraction: the kernels divide by no
+// variable with the compiler's `/`, whose expansion goes through a float reciprocal estimate.
+__device__ __forceinline__ int div_small(int p, int c) {
+  int q = 0;
+#pragma unroll
+  for (int k = 7; k >= 0; k--)
+    if (p >= (c << k)) {
+      p -= c << k;
+      q |= 1 << k;
+    }
+  return q;
+}
+
 // The trunk's joint-pointer gate (discrete_d11.rs:463-685): the recurrence code from the
 // products of step states over the prefix, the causal pointer successor, the best token of the
 // sparse counts, and each read block carried to that token's root.
@@ -465,9 +478,9 @@ __device__ void trunk_gate(const DevModel &M, const Geo &g, WaveLds &w, int len,
   }
   int excl = __shfl_up(incl, 1, 16);
   if (sl == 0) excl = 0;
-  const int a_prev = __shfl(g.compose[part_prev][excl], (seg << 4) + pprev / ch, 64);
-  const int a_mid = __shfl(g.compose[part_mid][excl], (seg << 4) + pmid / ch, 64);
-  const int f_last = __shfl(g.compose[part_last][excl], (seg << 4) + last / ch, 64);
+  const int a_prev = __shfl(g.compose[part_prev][excl], (seg << 4) + div_small(pprev, ch), 64);
+  const int a_mid = __shfl(g.compose[part_mid][excl], (seg << 4) + div_small(pmid, ch), 64);
+  const int f_last = __shfl(g.compose[part_last][excl], (seg << 4) + div_small(last, ch), 64);
   const int inv_prev = g.compose[a_prev][g.compose[a_prev][a_prev]];
   const int inv_mid = g.compose[a_mid][g.compose[a_mid][a_mid]];
   const int h_prev = g.compose[f_last][inv_prev], h_mid = g.compose[f_last][inv_mid];

@@ -283,6 +283,10 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
   M.identity_rows = r.head == 1;
   M.taps_fast = 1;
   M.log2d = (d & (d - 1)) == 0 ? (uint32_t)__builtin_ctz(d) : 0xffu;
+  // UOR_FBS_WRITER_MEMORY=0 turns the writer's memory of its last query off (for measurement:
+  // every step then scans its candidates; the results are the same either way).
+  const char *wm = getenv("UOR_FBS_WRITER_MEMORY");
+  M.writer_memory = (wm && wm[0] == '0' && !wm[1]) ? 0u : 1u;
   for (int sh = 0; sh <= 8; sh++) M.eps_int[sh] = norm_eps(m->eps_mantissa, m->eps_exp, sh);
 
   auto done = [&](int code) {

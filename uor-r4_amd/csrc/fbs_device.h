@@ -53,6 +53,7 @@ struct DevModel {
   uint32_t identity_rows;   // the nearest head: one drawer holding every token
   uint32_t taps_fast;       // every window tap has a descriptor (tap_desc != kGridDescSlow)
   uint32_t log2d;           // log2(d) when d is a power of two, else 0xff
+  uint32_t writer_memory;   // 1: a query equal to the writer's last one takes its result
   int64_t eps_int[9];       // RMSNorm epsilon at each pre-shift 0..8
   const DevLayer *layers;   // L entries
   const int16_t *final_gain;

@@ -228,10 +228,10 @@ constexpr uint32_t kRsqrtSeedWords = 384, kRecipSeedWords = 256;
 
 // The two tables as a pair of pointers (global by default).
 struct Seeds {
-  const uint32_t *rsqrt;
-  const uint32_t *recip;
-  FBS_HD Seeds() : rsqrt(rsqrt_seed_table()), recip(recip_seed_table()) {}
-  FBS_HD Seeds(const uint32_t *r, const uint32_t *q) : rsqrt(r), recip(q) {}
+  const uint32_t *rsq_seed;
+  const uint32_t *rcp_seed;
+  FBS_HD Seeds() : rsq_seed(rsqrt_seed_table()), rcp_seed(recip_seed_table()) {}
+  FBS_HD Seeds(const uint32_t *r, const uint32_t *q) : rsq_seed(r), rcp_seed(q) {}
 };
 
 // y ~ 2^46 / sqrt(t) for t in [2^30, 2^32); y in [2^30, 2^31], relative error below 2^-27.
@@ -422,7 +422,7 @@ FBS_HD uint64_t div_2p96(uint64_t s, const Seeds &sd = Seeds()) {
   const int zs = clz64(s);                            // [0, 29]
   const uint64_t D = s << zs;                         // [2^63, 2^64)
   const int E = 96 + zs;
-  const uint64_t w = recip_q63((uint32_t)(D >> 32), sd.recip);  // ~ 2^95 / D, <= 2^32
+  const uint64_t w = recip_q63((uint32_t)(D >> 32), sd.rcp_seed);  // ~ 2^95 / D, <= 2^32
   // Digit 1: Q1 = floor(2^(E-31) / D) <= 2^31.
   uint64_t q1 = w >> (126 - E);
   Rem96 n1;
@@ -454,7 +454,6 @@ FBS_HD uint64_t div_2p96(uint64_t s, const Seeds &sd = Seeds()) {
 // fh^2 <= 2^(J+1) rho.
 FBS_HD NormFactor norm_factor_pow2(uint64_t sum, uint32_t log2n, int64_t eps_int,
                                     const Seeds &sd = Seeds()) {
-  (void)sd;
   NormFactor out;
   int64_t ms = wadd64((int64_t)(sum >> log2n), eps_int);
   if (ms < 1) ms = 1;
@@ -464,34 +463,46 @@ FBS_HD NormFactor norm_factor_pow2(uint64_t sum, uint32_t log2n, int64_t eps_int
     out.huge = true;
     return out;
   }
-  // s = isqrt(M 2^64), M = 16 m in [16, 2^64): a double estimate within 2^12 + 1, one Newton
-  // step on the exact 128-bit residual (its excess over sqrt(M 2^64) is below 2^-9, the
-  // residual's conversion to double moves it by less than 2^-10), then one exact step each way.
   const uint64_t M = m << 4;
-  const u128 N = (u128)M << 64;
-  const double sx = sqrt((double)M) * 4294967296.0;
-  const uint64_t s0 = sx >= 18446744073709551615.0 ? ~0ull : (uint64_t)sx;
-  const i128 e = (i128)(N - (u128)s0 * s0);  // |e| < 2^78: exact as a signed value
-  const double ed = (double)(int64_t)(e >> 64) * 18446744073709551616.0 + (double)(uint64_t)e;
-  const double cd = floor(ed / (2.0 * (double)s0));
-  uint64_t s = s0 + (uint64_t)(int64_t)cd;  // |cd| < 2^14
-  u128 sq = (u128)s * s;
-  if (sq > N) {
-    s -= 1;
-  } else if (s < ~0ull && sq + 2 * (u128)s + 1 <= N) {
-    s += 1;
+  const int z = clz64(M) & ~1;
+  const uint64_t mn = M << z;
+  const int J = 32 - (z >> 1);                        // [3, 32]
+  const uint64_t mt = mn >> 32;
+  const uint64_t y = rsqrt_q46((uint32_t)mt, sd.rsq_seed);
+  uint64_t t = (mt * y) >> 30;
+  t = t > 0xffffffffull ? 0xffffffffull : t;
+  const int64_t diff = (int64_t)(mn - t * t);
+  t = (uint64_t)((int64_t)t + (((diff >> 16) * (int64_t)y) >> 47));
+  t = t > 0xffffffffull ? 0xffffffffull : t < (1ull << 31) ? (1ull << 31) : t;
+  uint64_t sq = t * t;
+  if (sq > mn) {
+    t -= 1;
+    sq -= 2 * t + 1;
   }
-  // r = floor(2^96 / s), s in [2^34, 2^64): a double estimate within 2^11, one correction from
-  // the exact 128-bit remainder (within 1), then one exact step each way.
-  const u128 P96 = (u128)1 << 96;
-  const uint64_t r0 = (uint64_t)(79228162514264337593543950336.0 / (double)s);
-  const i128 rem0 = (i128)(P96 - (u128)r0 * s);  // |rem0| < 2^12 s
-  const double rd = (double)(int64_t)(rem0 >> 64) * 18446744073709551616.0 + (double)(uint64_t)rem0;
-  uint64_t r = (uint64_t)((int64_t)r0 + (int64_t)floor(rd / (double)s));
-  const i128 rem = (i128)(P96 - (u128)r * s);
-  if (rem < 0) r -= 1;
-  else if (rem >= (i128)s) r += 1;
-  out.r = r;
+  if (t < 0xffffffffull && sq + 2 * t + 1 <= mn) {
+    sq += 2 * t + 1;
+    t += 1;
+  }
+  const uint64_t rem = mn - sq;                       // [0, 2 t] <= 2^33 - 2
+  const uint64_t num = rem << (J - 1);                // < 2^64
+  const uint64_t w = recip_q63((uint32_t)t, sd.rcp_seed); // ~ 2^63 / t
+  uint64_t fh = ((num >> 32) * w) >> 31;              // [q - 9, q]
+  const uint64_t r0 = num - fh * t;                   // [0, 10 t)
+  fh += ((r0 >> 4) * w) >> 59;                        // [q - 1, q]
+  uint64_t rho = num - fh * t;                        // [0, 2 t)
+  if (rho >= t) {
+    fh += 1;
+    rho -= t;
+  }
+  uint64_t f = fh;
+  if (fh >> J) {
+    f = fh - 1;                                       // f < 2^J
+  } else if (fh) {
+    const bool big = (rho >> (63 - J)) != 0;          // 2^(J+1) rho >= 2^64 > fh^2
+    if (!big && fh * fh > (rho << (J + 1))) f = fh - 1;
+  }
+  const uint64_t s = (t << J) + f;                    // >= 2^34
+  out.r = div_2p96(s, sd);
   out.huge = false;
   return out;
 }
@@ -710,11 +721,24 @@ FBS_HD void unit_q30(const int32_t raw[4], uint64_t eps, int32_t u[4], const See
   }
   // X = 0 (all zero, eps 0) gives u = 0 by the same steps on X = 1.
   xl = (xh == 0 && xl == 0) ? 1 : xl;
-  // s0 = floor(sqrt(X) 2^16) from a double: X rounds to 53 bits and the root adds one rounding,
-  // so s0 is within 2^-4 of the real root's floor argument, hence within 1 of s = isqrt(Y).
-  (void)sd;
-  const double xd = (double)xh * 18446744073709551616.0 + (double)xl;
-  uint64_t s = (uint64_t)(sqrt(xd) * 65536.0);
+  // Both normalisations are formed and one is kept by masks (one basic block, so that the
+  // scheduler can interleave independent rotations).
+  const int z = clz64(xl) & ~1;
+  const uint64_t big = 0ull - (uint64_t)(xh != 0);
+  const uint64_t xn = ((((uint64_t)xh << 62) | (xl >> 2)) & big) | ((xl << z) & ~big);
+  const int j = xh ? 17 : 16 - (z >> 1);              // [-15, 17]
+  const uint64_t xt = xn >> 32;
+  const uint64_t y = rsqrt_q46((uint32_t)xt, sd.rsq_seed);
+  uint64_t r = (xt * y) >> 30;
+  r = r > 0xffffffffull ? 0xffffffffull : r;
+  const int64_t diff = (int64_t)(xn - r * r);
+  r = (uint64_t)((int64_t)r + (((diff >> 16) * (int64_t)y) >> 47));
+  r = r > 0xffffffffull ? 0xffffffffull : r < (1ull << 31) ? (1ull << 31) : r;
+  const int64_t rem = (int64_t)(xn - r * r);          // [-2^33, 2^34]
+  const int jp = j > 0 ? j : 0, jn = j > 0 ? 0 : -j;
+  const int64_t f = (rem * (int64_t)(y >> 2)) >> (61 - jp);
+  const uint64_t frac = 0ull - (uint64_t)(j > 0);
+  uint64_t s = (((r << jp) + (uint64_t)f) & frac) | ((r >> jn) & ~frac);
   // Y - s^2 modulo 2^64: s < 2^50, so s^2 mod 2^64 = sl^2 + (2 sh sl mod 2^32) 2^32.
   const uint32_t sl = (uint32_t)s, shi = (uint32_t)(s >> 32);
   int64_t dy = (int64_t)((xl << 32) - ((uint64_t)sl * sl + ((uint64_t)(2u * shi * sl) << 32)));
@@ -723,13 +747,13 @@ FBS_HD void unit_q30(const int32_t raw[4], uint64_t eps, int32_t u[4], const See
   s = down ? s - 1 : s;
   const bool up = dy >= (int64_t)(2 * s + 1);
   s = up ? s + 1 : s;
-  // u_c = floor(a_c 2^46 / s), s in [2^16, 2^49]: a_c 2^46 times the double reciprocal of s is
-  // within 2^-21 of the quotient (at most 2^30 + 2^14), so q0 is within 1 of the floor; one step
-  // each way on the exact remainder a_c 2^46 - q0 s (small, exact modulo 2^64) gives q.
-  const double inv = 1.0 / (double)s;
+  // u_c = floor(a_c 2^46 / s), s in [2^16, 2^49].
+  const int zs = clz64(s);
+  const uint64_t w = recip_q63((uint32_t)((s << zs) >> 32), sd.rcp_seed);  // ~ 2^95 / (s << zs)
+  const int sh = 49 - zs;
 #pragma unroll
   for (int c = 0; c < 4; c++) {
-    uint64_t q = (uint64_t)((double)a[c] * 70368744177664.0 * inv);
+    uint64_t q = ((uint64_t)a[c] * w) >> sh;
     int64_t rq = (int64_t)(((uint64_t)a[c] << 46) - q * s);
     const bool qd = rq < 0;
     rq = qd ? rq + (int64_t)s : rq;
@@ -738,6 +762,7 @@ FBS_HD void unit_q30(const int32_t raw[4], uint64_t eps, int32_t u[4], const See
     u[c] = raw[c] < 0 ? -(int32_t)q : (int32_t)q;
   }
 }
+
 // (lambda u) >> 30 for lambda = 2^p (p <= 31): u << (p - 30) or floor(u / 2^(30 - p)).
 FBS_HD int64_t scale_pow2(int32_t u, uint32_t p) {
   return p >= 30 ? (int64_t)u << (p - 30) : (int64_t)(u >> (30 - p));

@@ -134,6 +134,18 @@ __device__ __forceinline__ uint32_t sad2_u16(uint32_t a, uint32_t b, uint32_t c)
   return d;
 }
 
+// x mod w for 1 <= w <= kMaxWindow by restoring subtraction of w 2^k. The kernels divide by no
+// variable: the compiler's expansion of an integer % goes through a float reciprocal estimate,
+// and the served path carries no floating-point instruction.
+__device__ __forceinline__ uint32_t mod_window(uint32_t x, uint32_t w) {
+#pragma unroll
+  for (int k = 31; k >= 0; k--) {
+    const uint64_t t = (uint64_t)w << k;
+    x = x >= t ? (uint32_t)(x - t) : x;
+  }
+  return x;
+}
+
 // ---------------------------------------------------------------------------------------------
 // Step pieces.
 
@@ -989,7 +1001,7 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
         if (qv[k]) *(int4 *)(S.wq + 4 * qi[k]) = qq[k];
       if (lane == 0) {
         S.wmeta[0] = *chosen;
-        S.wmeta[1] = 1;
+        S.wmeta[1] = M.writer_memory;
       }
     }
   }
@@ -1345,7 +1357,7 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
       if (qv[k]) *(int4 *)(S.wq + 4 * qi[k]) = qq[k];
     if (lane == 0) {
       S.wmeta[0] = *chosen;
-      S.wmeta[1] = 1;
+      S.wmeta[1] = M.writer_memory;
     }
   }
   return 0;
@@ -1579,7 +1591,7 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
     // Fresh or resumed session: state, window rows (row r = the drive r + 1 positions back)
     // and position (LayerState::Recurrence, session.rs:1850).
     uint32_t pos = A.in_position ? A.in_position[sl] : 0u;
-    uint32_t base = pos % W;
+    uint32_t base = mod_window(pos, W);
     // A slot's history is its ring; otherwise the block's ring takes the rows.
     int32_t *ring = A.slots ? A.out_history + (uint64_t)sl * L * W * d : block_ring;
     for (uint32_t l = 0; l < L; l++)
@@ -1594,7 +1606,8 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
                   A.in_state ? A.in_state[((uint64_t)sl * L + l) * d + ch + c] : 0;
           if (keeps_ring && !A.slots)
             for (uint32_t r = 0; r < W; r++) {
-              uint32_t slot = (base + 2 * W - 1 - r) % W;
+              uint32_t slot = base + W - 1 - r;  // (base - 1 - r) mod W, from [0, 2 W - 1)
+              slot = slot >= W ? slot - W : slot;
               int4 h = make_int4(0, 0, 0, 0);
               if (A.in_history) h = *(const int4 *)(A.in_history + (((uint64_t)sl * L + l) * W + r) * d + ch);
               *(int4 *)(ring + ((uint64_t)l * W + slot) * d + ch) = h;
@@ -1674,7 +1687,8 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
                 A.out_state[((uint64_t)sl * L + l) * d + ch + c] = S.st[(uint64_t)l * d + ch + c];
             if (A.out_history && keeps_ring && !A.slots)
               for (uint32_t r = 0; r < W; r++) {
-                uint32_t slot = (base + 2 * W - 1 - r) % W;
+                uint32_t slot = base + W - 1 - r;  // (base - 1 - r) mod W, from [0, 2 W - 1)
+                slot = slot >= W ? slot - W : slot;
                 *(int4 *)(A.out_history + (((uint64_t)sl * L + l) * W + r) * d + ch) =
                     *(const int4 *)(ring + ((uint64_t)l * W + slot) * d + ch);
               }

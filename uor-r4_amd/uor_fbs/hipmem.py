@@ -66,6 +66,10 @@ class DeviceArray:
         return self._p
 
     def _at(self, index: int, row_bytes: int) -> C.c_void_p:
+        """The address of row `index` of the first axis (checked against the allocation)."""
+        index = int(index)
+        if not 0 <= index < self.shape[0]:
+            raise IndexError(f"row {index} outside the array's {self.shape[0]}")
         return C.c_void_p(self._p.value + index * row_bytes)
 
     def zero(self, rows=None):

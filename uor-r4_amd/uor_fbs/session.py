@@ -156,10 +156,19 @@ class SessionPool:
         self.position = DeviceArray(capacity, np.uint32, dev)
         self._free = list(range(capacity - 1, -1, -1))
 
-    def acquire(self) -> int:
-        if not self._free:
-            raise SessionError("Shape", f"all {self.capacity} session slots are in use")
-        slot = self._free.pop()
+    def acquire(self, slot: int | None = None) -> int:
+        """A free slot holding a fresh session: the next free one, or `slot` if it is free."""
+        if slot is None:
+            if not self._free:
+                raise SessionError("Shape", f"all {self.capacity} session slots are in use")
+            slot = self._free.pop()
+        else:
+            slot = int(slot)
+            if not 0 <= slot < self.capacity:
+                raise ValueError(f"slot {slot} outside the pool's {self.capacity}")
+            if slot not in self._free:
+                raise ValueError(f"slot {slot} is held by another session")
+            self._free.remove(slot)
         self.clear([slot])
         return slot
 
@@ -243,7 +252,7 @@ class Session:
     def __init__(self, pool: SessionPool, slot: int | None = None):
         self.pool = pool
         self.info = pool.info
-        self.slot = pool.acquire() if slot is None else slot
+        self.slot = pool.acquire(slot)
         self._reset_host()
 
     def _reset_host(self):
