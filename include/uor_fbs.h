@@ -163,6 +163,25 @@ int uor_fbs_decode_async(uor_fbs_handle *handle, const uint32_t *prompts, uint32
                          int32_t *out_history, uint32_t *out_position, int32_t *status,
                          void *stream);
 
+/* uor_fbs_decode_async without allocating: no hipMalloc, hipFree or allocating library call,
+ * for callers that cannot allocate (code under HIP graph capture, tight serving loops, hosts
+ * that forbid allocation on their path). No counterpart in the reference. Same arguments,
+ * outputs and statuses as uor_fbs_decode_async; the caller still passes every input and output
+ * buffer. The window rings and window sums live in a device array of
+ * UOR_FBS_NOALLOC_SCRATCH_BYTES inside the library, one per GPU, held until the process ends:
+ * the launch uses as many resident blocks as that holds (sequences loop within them; results do
+ * not depend on the grid), and a model whose one sequence needs more is refused with
+ * UOR_FBS_ERR_UNSUPPORTED. Every call on a GPU shares that GPU's array, and nothing in it needs
+ * to start at zero: calls that overlap on one GPU (other streams, other threads, other handles)
+ * race on it and must be serialised by the caller. */
+#define UOR_FBS_NOALLOC_SCRATCH_BYTES (128u << 20)
+int uor_fbs_decode_noalloc_async(uor_fbs_handle *handle, const uint32_t *prompts,
+                                 uint32_t sequences, uint32_t prompt_len, uint32_t gen,
+                                 uint32_t *out_reply, const int64_t *in_state,
+                                 const int32_t *in_history, const uint32_t *in_position,
+                                 int64_t *out_state, int32_t *out_history,
+                                 uint32_t *out_position, int32_t *status, void *stream);
+
 /* Serving sessions held in caller-owned device arrays, one slot per session: `state`
  * [capacity][state_words] int64, `history` [capacity][history_words] int32 and `position`
  * [capacity] uint32, updated in place. A slot's history is its window ring, [layer][window]

@@ -13,6 +13,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -74,6 +75,9 @@ struct uor_fbs_handle {
   int32_t *ring = nullptr;
   int64_t *hist = nullptr;
   size_t ring_blocks = 0;
+  // This device's copy of the allocation-free decode's scratch array (null if its address could
+  // not be read; that entry point then refuses).
+  unsigned char *scratch = nullptr;
 
   ~uor_fbs_handle() {
     int prev = 0;
@@ -118,6 +122,36 @@ struct uor_fbs_handle {
     return 0;
   }
 };
+
+// The allocation-free decode (uor_fbs_decode_noalloc_async) keeps its window rings and window
+// sums in this file-scope device array instead of memory from hipMalloc. Every GPU the library
+// loads on holds its own copy, at its own address, until the process ends. In host code the
+// array's name is not a device address: kernels and copies take the per-device address that
+// hipGetSymbolAddress returns (scratch_address), read once per device at model creation.
+static __device__ __align__(256) unsigned char scratch[UOR_FBS_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+unsigned char *g_scratch_ptr[kScratchDevices];
+bool g_scratch_read[kScratchDevices];
+
+// The scratch array's address on `device`, which must be current; read once per device.
+unsigned char *scratch_address(int device) {
+  if (device < 0 || device >= kScratchDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_read[device]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_ptr[device] = e == hipSuccess ? (unsigned char *)p : nullptr;
+    g_scratch_read[device] = true;
+    if (e != hipSuccess) (void)hipGetLastError();  // the entry point reports it when called
+  }
+  return g_scratch_ptr[device];
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -253,6 +287,7 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
   (void)hipSetDevice(device);
   uor_fbs_handle *h = new uor_fbs_handle();
   h->device = device;
+  h->scratch = scratch_address(device);
   DevModel &M = h->M;
   const uint32_t d = m->width, mlp = m->mlp, L = m->layer_count;
   M.vocab = m->vocab;
@@ -442,16 +477,33 @@ extern "C" uint32_t uor_fbs_block_waves(const uor_fbs_handle *h, uint32_t n) {
 
 namespace {
 
-int launch(uor_fbs_handle *h, RunArgs &A, hipStream_t stream) {
+// `noalloc`: the window rings and sums come from the device's scratch array, whose size bounds
+// the grid (sequences loop within the blocks), and nothing is allocated.
+int launch(uor_fbs_handle *h, RunArgs &A, hipStream_t stream, bool noalloc = false) {
   if (A.n == 0) return 0;
   if (!A.slots) A.capacity = A.n;
   const bool pair = h->pair;
   const uint32_t cap = pair ? h->pair_grid : h->max_grid;
-  const uint32_t grid = A.n < cap ? A.n : cap;
-  int st = h->ensure_ring(grid);
-  if (st) return st;
-  A.ring = h->ring;
-  A.hist = h->hist;
+  uint32_t grid = A.n < cap ? A.n : cap;
+  if (noalloc) {
+    if (!h->scratch)
+      return fail(UOR_FBS_ERR_DEVICE, "the scratch array's device address could not be read");
+    const size_t ring = (size_t)h->M.L * h->M.W * h->M.d * sizeof(int32_t);
+    const size_t sums = pair ? (size_t)h->M.L * h->M.d * sizeof(int64_t) : 0;
+    const size_t fit = (UOR_FBS_NOALLOC_SCRATCH_BYTES - 256) / (ring + sums);
+    if (fit == 0)
+      return fail(UOR_FBS_ERR_UNSUPPORTED,
+                  "one sequence's window ring and sums (%zu bytes) exceed the %zu-byte scratch",
+                  ring + sums, (size_t)UOR_FBS_NOALLOC_SCRATCH_BYTES);
+    grid = grid < fit ? grid : (uint32_t)fit;
+    A.ring = (int32_t *)h->scratch;
+    A.hist = (int64_t *)(h->scratch + ((grid * ring + 255) & ~(size_t)255));
+  } else {
+    int st = h->ensure_ring(grid);
+    if (st) return st;
+    A.ring = h->ring;
+    A.hist = h->hist;
+  }
   const bool decode = A.mode == kModeDecode;
   const uint32_t waves = pair ? 2 : 1;
   const size_t lds = pair ? h->pair_lds : h->lds_bytes;
@@ -581,6 +633,32 @@ extern "C" int uor_fbs_decode_async(uor_fbs_handle *h, const uint32_t *prompts, 
   A.out_position = out_position;
   A.status = status;
   return launch(h, A, (hipStream_t)stream);
+}
+
+extern "C" int uor_fbs_decode_noalloc_async(uor_fbs_handle *h, const uint32_t *prompts,
+                                            uint32_t sequences, uint32_t prompt_len, uint32_t gen,
+                                            uint32_t *out_reply, const int64_t *in_state,
+                                            const int32_t *in_history, const uint32_t *in_position,
+                                            int64_t *out_state, int32_t *out_history,
+                                            uint32_t *out_position, int32_t *status, void *stream) {
+  if (!h || !prompts || !out_reply || !status) return fail(UOR_FBS_ERR_ARGUMENT, "null argument");
+  if (prompt_len == 0) return fail(UOR_FBS_ERR_ARGUMENT, "a decode needs at least one prompt token");
+  DeviceScope scope(h->device);
+  RunArgs A{};
+  A.mode = kModeDecode;
+  A.n = sequences;
+  A.len = prompt_len;
+  A.gen = gen;
+  A.tokens = prompts;
+  A.out_tokens = out_reply;
+  A.in_state = in_state;
+  A.in_history = in_history;
+  A.in_position = in_position;
+  A.out_state = out_state;
+  A.out_history = out_history;
+  A.out_position = out_position;
+  A.status = status;
+  return launch(h, A, (hipStream_t)stream, true);
 }
 
 extern "C" int uor_fbs_decode_slots_async(uor_fbs_handle *h, const uint32_t *slots,

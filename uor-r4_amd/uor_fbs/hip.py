@@ -28,7 +28,8 @@ SYMBOLS = (
     "uor_fbs_abi_version", "uor_fbs_sizeof_model", "uor_fbs_sizeof_layer", "uor_fbs_sizeof_ext",
     "uor_fbs_last_error", "uor_fbs_model_create", "uor_fbs_model_destroy", "uor_fbs_state_words",
     "uor_fbs_history_words", "uor_fbs_sequences", "uor_fbs_sequences_async", "uor_fbs_decode",
-    "uor_fbs_decode_async", "uor_fbs_score", "uor_fbs_score_async", "uor_fbs_block_waves",
+    "uor_fbs_decode_async", "uor_fbs_decode_noalloc_async", "uor_fbs_score",
+    "uor_fbs_score_async", "uor_fbs_block_waves",
     "uor_fbs_decode_slots_async", "uor_fbs_index_workspace_bytes", "uor_fbs_index_build_async",
     "uor_fbs_index_update_async", "uor_fbs_index_remove_async", "uor_fbs_index_validate_async",
     "uor_fbs_index_probe_async", "uor_fbs_index_full_scan_async",
@@ -67,6 +68,7 @@ def lib():
         L.uor_fbs_decode.argtypes = [P, P, C.c_uint32, C.c_uint32, C.c_uint32, P, P, P, P, P, P, P]
         L.uor_fbs_decode_async.argtypes = [P, P, C.c_uint32, C.c_uint32, C.c_uint32, P, P, P, P, P,
                                            P, P, P, P]
+        L.uor_fbs_decode_noalloc_async.argtypes = L.uor_fbs_decode_async.argtypes
         L.uor_fbs_decode_slots_async.argtypes = [P, P, C.c_uint32, C.c_uint32, P, C.c_uint32,
                                                  C.c_uint32, P, P, P, P, P, P, P, P]
         L.uor_fbs_score.argtypes = [P, P, C.c_uint64, C.c_uint32, P, P]
