@@ -19,7 +19,10 @@ sys.path.insert(0, os.path.join(ROOT, "uor-r4_amd"))
 
 from uor_fbs.cabi import Image, ptr  # noqa: E402
 
-ORACLE_SO = os.path.join(HERE, "lib", "libfbs_oracle.so")
+# UOR_ORACLE_LIB_DIR=oracle/lib_san selects the AddressSanitizer + UBSan build of the oracle
+# libraries (make -C oracle sanitize; tests/test_sanitized_cpu.py).
+LIB_DIR = os.environ.get("UOR_ORACLE_LIB_DIR") or os.path.join(HERE, "lib")
+ORACLE_SO = os.path.join(LIB_DIR, "libfbs_oracle.so")
 TWIN_SO = os.path.join(HERE, "_ref", "libfbs_twin.so")
 
 _lib = None
@@ -339,7 +342,7 @@ def ref_full_scan(table, query, k):
 # ---------------------------------------------------------------------------------------------
 # The discrete M1 evaluator (oracle/lib/libd11_oracle.so, d11_oracle.c).
 
-D11_SO = os.path.join(HERE, "lib", "libd11_oracle.so")
+D11_SO = os.path.join(LIB_DIR, "libd11_oracle.so")
 _d11 = None
 
 
@@ -421,7 +424,7 @@ class D11Oracle:
 # ---------------------------------------------------------------------------------------------
 # The copy heads' Hamming read (oracle/lib/libcopy_oracle.so, copy_oracle.c).
 
-COPY_SO = os.path.join(HERE, "lib", "libcopy_oracle.so")
+COPY_SO = os.path.join(LIB_DIR, "libcopy_oracle.so")
 _copy = None
 
 

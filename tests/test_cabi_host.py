@@ -17,7 +17,10 @@ from conftest import ROOT
 from uor_fbs import hip, tables
 from uor_fbs.cabi import ExtS, LayerS, ModelS
 
-HP_PATH = os.path.join(ROOT, "uor-r4_amd", "lib", "libuor_fbs_hostprims.so")
+# UOR_HOSTPRIMS_LIB selects another build of the host arithmetic (the sanitizer build,
+# tests/test_sanitized_cpu.py).
+HP_PATH = os.environ.get("UOR_HOSTPRIMS_LIB") or os.path.join(ROOT, "uor-r4_amd", "lib",
+                                                              "libuor_fbs_hostprims.so")
 P = C.c_void_p
 U64 = (1 << 64) - 1
 

@@ -723,7 +723,9 @@ FBS_HD void unit_q30(const int32_t raw[4], uint64_t eps, int32_t u[4], const See
   xl = (xh == 0 && xl == 0) ? 1 : xl;
   // Both normalisations are formed and one is kept by masks (one basic block, so that the
   // scheduler can interleave independent rotations).
-  const int z = clz64(xl) & ~1;
+  // z is taken mod 64 so that the unused form stays a defined shift when xl = 0 (then xh != 0
+  // and the mask keeps the other form).
+  const int z = clz64(xl) & 62;
   const uint64_t big = 0ull - (uint64_t)(xh != 0);
   const uint64_t xn = ((((uint64_t)xh << 62) | (xl >> 2)) & big) | ((xl << z) & ~big);
   const int j = xh ? 17 : 16 - (z >> 1);              // [-15, 17]
