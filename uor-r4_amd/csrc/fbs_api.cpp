@@ -322,7 +322,9 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
   // every step then scans its candidates; the results are the same either way).
   const char *wm = getenv("UOR_FBS_WRITER_MEMORY");
   M.writer_memory = (wm && wm[0] == '0' && !wm[1]) ? 0u : 1u;
-  for (int sh = 0; sh <= 8; sh++) M.eps_int[sh] = norm_eps(m->eps_mantissa, m->eps_exp, sh);
+  M.w_recip = (1ull << 32) / M.W;
+  int64_t eps_int[9];
+  for (int sh = 0; sh <= 8; sh++) eps_int[sh] = norm_eps(m->eps_mantissa, m->eps_exp, sh);
 
   auto done = [&](int code) {
     if (code) delete h;
@@ -445,6 +447,7 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
   }
   if ((st = h->upload(m->icosian, 120 * 8, &M.icosian))) return done(st);
   if ((st = h->upload(m->keep_q31, 16, &M.keep_q31))) return done(st);
+  if ((st = h->upload(eps_int, 9, &M.eps_int))) return done(st);
 
   hipDeviceProp_t prop;
   he = hipGetDeviceProperties(&prop, device);

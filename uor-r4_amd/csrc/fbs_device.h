@@ -54,7 +54,7 @@ struct DevModel {
   uint32_t taps_fast;       // every window tap has a descriptor (tap_desc != kGridDescSlow)
   uint32_t log2d;           // log2(d) when d is a power of two, else 0xff
   uint32_t writer_memory;   // 1: a query equal to the writer's last one takes its result
-  int64_t eps_int[9];       // RMSNorm epsilon at each pre-shift 0..8
+  uint64_t w_recip;         // floor(2^32 / W): the ring slot of a position without division
   const DevLayer *layers;   // L entries
   const int16_t *final_gain;
   const uint16_t *final_gain_desc;
@@ -64,6 +64,7 @@ struct DevModel {
   const uint32_t *members;  // offsets[D]
   const int8_t *icosian;    // 120 * 8
   const uint64_t *keep_q31; // 16
+  const int64_t *eps_int;   // 9: the RMSNorm epsilon at each pre-shift 0..8
 };
 
 // LDS bytes per block (the layout the kernels carve): the gather crossbar, the MLP outputs, the

@@ -234,35 +234,41 @@ struct Seeds {
   FBS_HD Seeds(const uint32_t *r, const uint32_t *q) : rsq_seed(r), rcp_seed(q) {}
 };
 
+// The high 32 bits of a 32 x 32 product.
+FBS_HD uint32_t mulhi32(uint32_t a, uint32_t b) { return (uint32_t)(((uint64_t)a * b) >> 32); }
+
 // y ~ 2^46 / sqrt(t) for t in [2^30, 2^32); y in [2^30, 2^31], relative error below 2^-27.
+// Every product is 32 x 32 bits: y stays below 2^31 before the clamp and f = (3 2^32 - p) / 2
+// below 2^33 (both checked over every input), so y f / 2^32 = y [f >= 2^32] + mulhi(y, f mod 2^32).
 FBS_HD uint32_t rsqrt_q46(uint32_t t, const uint32_t *tab) {
-  uint64_t y = tab[(t >> 23) - 128];
+  uint32_t y = tab[(t >> 23) - 128];
 #pragma unroll
   for (int it = 0; it < 2; it++) {
     // Newton: y <- y (3 - t y^2 / 2^92) / 2, with p = t y^2 / 2^60 ~ 2^32.
-    uint64_t y2 = (y * y) >> 32;                   // y^2 / 2^32 <= 2^30
-    uint64_t p = ((uint64_t)t * y2) >> 28;         // ~ 2^32
-    uint64_t f = ((3ull << 32) - p) >> 1;          // ~ 2^32
-    y = (y * f) >> 32;
-    if (y > (1ull << 31)) y = 1ull << 31;
-    if (y < (1ull << 30)) y = 1ull << 30;
+    const uint32_t y2 = mulhi32(y, y);                        // y^2 / 2^32 <= 2^30
+    const uint64_t p = ((uint64_t)t * y2) >> 28;              // ~ 2^32
+    const uint64_t f = ((3ull << 32) - p) >> 1;               // ~ 2^32, < 2^33
+    y = mulhi32(y, (uint32_t)f) + ((f >> 32) ? y : 0u);
+    y = y > (1u << 31) ? 1u << 31 : y < (1u << 30) ? 1u << 30 : y;
   }
-  return (uint32_t)y;
+  return y;
 }
 FBS_HD uint32_t rsqrt_q46(uint32_t t) { return rsqrt_q46(t, rsqrt_seed_table()); }
 
-// w ~ 2^63 / d for d in [2^31, 2^32); w in (2^31, 2^32], relative error below 2^-30.
-FBS_HD uint64_t recip_q63(uint32_t d, const uint32_t *tab) {
-  uint64_t w = tab[(d >> 23) - 256];
+// w ~ 2^63 / d for d in [2^31, 2^32); w in (2^31, 2^32), relative error below 2^-30. w stays
+// below 2^32 and (2^63 - d w) / 2^31 inside +-2^23.1 at every step (checked over every input),
+// so each product is 32 x 32 bits.
+FBS_HD uint32_t recip_q63(uint32_t d, const uint32_t *tab) {
+  uint32_t w = tab[(d >> 23) - 256];
 #pragma unroll
   for (int it = 0; it < 2; it++) {
     // Newton: w <- w + w (2^63 - d w) / 2^63.
-    int64_t e = (int64_t)((1ull << 63) - (uint64_t)d * w);
-    w = (uint64_t)((int64_t)w + (((e >> 31) * (int64_t)w) >> 32));
+    const int32_t es = (int32_t)((int64_t)((1ull << 63) - (uint64_t)d * w) >> 31);
+    w = (uint32_t)((int64_t)w + (((int64_t)es * (int64_t)(uint64_t)w) >> 32));
   }
   return w;
 }
-FBS_HD uint64_t recip_q63(uint32_t d) { return recip_q63(d, recip_seed_table()); }
+FBS_HD uint32_t recip_q63(uint32_t d) { return recip_q63(d, recip_seed_table()); }
 
 // ---------------------------------------------------------------------------------------------
 // Floor square root of a u128 (RS stack/kernels.rs:408-430 `stack_isqrt`): the result is
@@ -383,9 +389,9 @@ struct Rem96 {
   uint64_t lo;
 };
 
-// n - q d for a remainder n, q < 2^33 and d < 2^64.
-FBS_HD Rem96 rem_sub_qd(Rem96 n, uint64_t q, uint64_t d) {
-  const uint64_t p1 = q * (d & 0xffffffffull), p2 = q * (d >> 32);  // q d = p2 2^32 + p1
+// n - q d for a remainder n, q < 2^32 and d < 2^64.
+FBS_HD Rem96 rem_sub_qd(Rem96 n, uint32_t q, uint64_t d) {
+  const uint64_t p1 = (uint64_t)q * (uint32_t)d, p2 = (uint64_t)q * (uint32_t)(d >> 32);  // q d = p2 2^32 + p1
   const uint64_t pl = p1 + (p2 << 32);
   const uint64_t ph = (p2 >> 32) + (pl < p1);
   Rem96 r;
@@ -418,27 +424,32 @@ FBS_HD void digit_fix(uint64_t &q, Rem96 &r, uint64_t d) {
 // [-2^-30.4, 2^-31] (the seed error, checked over every input, and the truncation of D), so each
 // digit estimate is within [q - 3, q + 1] and the exact remainder (below 2^66, kept in 96 bits)
 // fixes it in fixed steps.
-FBS_HD uint64_t div_2p96(uint64_t s, const Seeds &sd = Seeds()) {
+// div_2p96_w takes w = recip_q63(D / 2^32) from the caller, which may hold it already.
+FBS_HD uint64_t div_2p96_w(uint64_t s, uint32_t w) {
   const int zs = clz64(s);                            // [0, 29]
   const uint64_t D = s << zs;                         // [2^63, 2^64)
   const int E = 96 + zs;
-  const uint64_t w = recip_q63((uint32_t)(D >> 32), sd.rcp_seed);  // ~ 2^95 / D, <= 2^32
   // Digit 1: Q1 = floor(2^(E-31) / D) <= 2^31.
   uint64_t q1 = w >> (126 - E);
   Rem96 n1;
   n1.hi = (int64_t)1 << (E - 95);
   n1.lo = 0;
-  Rem96 r1 = rem_sub_qd(n1, q1, D);
+  Rem96 r1 = rem_sub_qd(n1, (uint32_t)q1, D);
   digit_fix<2>(q1, r1, D);
   // Digit 2: Q0 = floor(R1 2^31 / D) < 2^31, R1 in [0, D).
   const uint64_t R = r1.lo;
-  uint64_t q0 = (((R >> 32) * w) + (((R & 0xffffffffull) * w) >> 32)) >> 32;
+  uint64_t q0 = ((uint64_t)(uint32_t)(R >> 32) * w + mulhi32((uint32_t)R, w)) >> 32;
   Rem96 n2;
   n2.hi = (int64_t)(R >> 33);
   n2.lo = R << 31;
-  Rem96 r0 = rem_sub_qd(n2, q0, D);
+  Rem96 r0 = rem_sub_qd(n2, (uint32_t)q0, D);
   digit_fix<3>(q0, r0, D);
   return (q1 << 31) + q0;
+}
+
+FBS_HD uint64_t div_2p96(uint64_t s, const Seeds &sd = Seeds()) {
+  const uint64_t top = (s << clz64(s)) >> 32;         // D / 2^32
+  return div_2p96_w(s, recip_q63((uint32_t)top, sd.rcp_seed));
 }
 
 // norm_factor for n = 2^log2n in 64-bit steps (the kernels' form; equal to norm_factor).
@@ -467,14 +478,16 @@ FBS_HD NormFactor norm_factor_pow2(uint64_t sum, uint32_t log2n, int64_t eps_int
   const int z = clz64(M) & ~1;
   const uint64_t mn = M << z;
   const int J = 32 - (z >> 1);                        // [3, 32]
-  const uint64_t mt = mn >> 32;
-  const uint64_t y = rsqrt_q46((uint32_t)mt, sd.rsq_seed);
-  uint64_t t = (mt * y) >> 30;
+  // Every product below has 32-bit factors: mt, y and t are below 2^32, |diff| / 2^16 below
+  // 2^31 (t is within 2^6 of the root before its Newton step).
+  const uint32_t mt = (uint32_t)(mn >> 32);
+  const uint32_t y = rsqrt_q46(mt, sd.rsq_seed);
+  uint64_t t = ((uint64_t)mt * y) >> 30;
   t = t > 0xffffffffull ? 0xffffffffull : t;
-  const int64_t diff = (int64_t)(mn - t * t);
-  t = (uint64_t)((int64_t)t + (((diff >> 16) * (int64_t)y) >> 47));
+  const int64_t diff = (int64_t)(mn - (uint64_t)(uint32_t)t * (uint32_t)t);
+  t = (uint64_t)((int64_t)t + (((int64_t)(int32_t)(diff >> 16) * (int64_t)(uint64_t)y) >> 47));
   t = t > 0xffffffffull ? 0xffffffffull : t < (1ull << 31) ? (1ull << 31) : t;
-  uint64_t sq = t * t;
+  uint64_t sq = (uint64_t)(uint32_t)t * (uint32_t)t;
   if (sq > mn) {
     t -= 1;
     sq -= 2 * t + 1;
@@ -485,10 +498,10 @@ FBS_HD NormFactor norm_factor_pow2(uint64_t sum, uint32_t log2n, int64_t eps_int
   }
   const uint64_t rem = mn - sq;                       // [0, 2 t] <= 2^33 - 2
   const uint64_t num = rem << (J - 1);                // < 2^64
-  const uint64_t w = recip_q63((uint32_t)t, sd.rcp_seed); // ~ 2^63 / t
-  uint64_t fh = ((num >> 32) * w) >> 31;              // [q - 9, q]
+  const uint32_t w = recip_q63((uint32_t)t, sd.rcp_seed); // ~ 2^63 / t
+  uint64_t fh = ((uint64_t)(uint32_t)(num >> 32) * w) >> 31;  // [q - 9, q]
   const uint64_t r0 = num - fh * t;                   // [0, 10 t)
-  fh += ((r0 >> 4) * w) >> 59;                        // [q - 1, q]
+  fh += ((uint64_t)(uint32_t)(r0 >> 4) * w) >> 59;    // [q - 1, q]
   uint64_t rho = num - fh * t;                        // [0, 2 t)
   if (rho >= t) {
     fh += 1;
@@ -499,10 +512,12 @@ FBS_HD NormFactor norm_factor_pow2(uint64_t sum, uint32_t log2n, int64_t eps_int
     f = fh - 1;                                       // f < 2^J
   } else if (fh) {
     const bool big = (rho >> (63 - J)) != 0;          // 2^(J+1) rho >= 2^64 > fh^2
-    if (!big && fh * fh > (rho << (J + 1))) f = fh - 1;
+    if (!big && (uint64_t)(uint32_t)fh * (uint32_t)fh > (rho << (J + 1))) f = fh - 1;  // fh < 2^J
   }
   const uint64_t s = (t << J) + f;                    // >= 2^34
-  out.r = div_2p96(s, sd);
+  // s = t 2^J + f with t in [2^31, 2^32) and f < 2^J, so s normalised to [2^63, 2^64) is
+  // t 2^32 + f 2^(32-J): its top 32 bits are t, whose reciprocal w is at hand.
+  out.r = div_2p96_w(s, w);
   out.huge = false;
   return out;
 }
@@ -729,14 +744,15 @@ FBS_HD void unit_q30(const int32_t raw[4], uint64_t eps, int32_t u[4], const See
   const uint64_t big = 0ull - (uint64_t)(xh != 0);
   const uint64_t xn = ((((uint64_t)xh << 62) | (xl >> 2)) & big) | ((xl << z) & ~big);
   const int j = xh ? 17 : 16 - (z >> 1);              // [-15, 17]
-  const uint64_t xt = xn >> 32;
-  const uint64_t y = rsqrt_q46((uint32_t)xt, sd.rsq_seed);
-  uint64_t r = (xt * y) >> 30;
+  // As in norm_factor_pow2, every product but the fraction's has 32-bit factors.
+  const uint32_t xt = (uint32_t)(xn >> 32);
+  const uint32_t y = rsqrt_q46(xt, sd.rsq_seed);
+  uint64_t r = ((uint64_t)xt * y) >> 30;
   r = r > 0xffffffffull ? 0xffffffffull : r;
-  const int64_t diff = (int64_t)(xn - r * r);
-  r = (uint64_t)((int64_t)r + (((diff >> 16) * (int64_t)y) >> 47));
+  const int64_t diff = (int64_t)(xn - (uint64_t)(uint32_t)r * (uint32_t)r);
+  r = (uint64_t)((int64_t)r + (((int64_t)(int32_t)(diff >> 16) * (int64_t)(uint64_t)y) >> 47));
   r = r > 0xffffffffull ? 0xffffffffull : r < (1ull << 31) ? (1ull << 31) : r;
-  const int64_t rem = (int64_t)(xn - r * r);          // [-2^33, 2^34]
+  const int64_t rem = (int64_t)(xn - (uint64_t)(uint32_t)r * (uint32_t)r);  // [-2^33, 2^34]
   const int jp = j > 0 ? j : 0, jn = j > 0 ? 0 : -j;
   const int64_t f = (rem * (int64_t)(y >> 2)) >> (61 - jp);
   const uint64_t frac = 0ull - (uint64_t)(j > 0);
@@ -751,12 +767,12 @@ FBS_HD void unit_q30(const int32_t raw[4], uint64_t eps, int32_t u[4], const See
   s = up ? s + 1 : s;
   // u_c = floor(a_c 2^46 / s), s in [2^16, 2^49].
   const int zs = clz64(s);
-  const uint64_t w = recip_q63((uint32_t)((s << zs) >> 32), sd.rcp_seed);  // ~ 2^95 / (s << zs)
+  const uint32_t w = recip_q63((uint32_t)((s << zs) >> 32), sd.rcp_seed);  // ~ 2^95 / (s << zs)
   const int sh = 49 - zs;
 #pragma unroll
   for (int c = 0; c < 4; c++) {
-    uint64_t q = ((uint64_t)a[c] * w) >> sh;
-    int64_t rq = (int64_t)(((uint64_t)a[c] << 46) - q * s);
+    uint64_t q = ((uint64_t)a[c] * w) >> sh;        // below 2^31
+    int64_t rq = (int64_t)(((uint64_t)a[c] << 46) - (uint64_t)(uint32_t)q * s);
     const bool qd = rq < 0;
     rq = qd ? rq + (int64_t)s : rq;
     q = qd ? q - 1 : q;

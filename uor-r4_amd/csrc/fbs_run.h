@@ -134,16 +134,14 @@ __device__ __forceinline__ uint32_t sad2_u16(uint32_t a, uint32_t b, uint32_t c)
   return d;
 }
 
-// x mod w for 1 <= w <= kMaxWindow by restoring subtraction of w 2^k. The kernels divide by no
-// variable: the compiler's expansion of an integer % goes through a float reciprocal estimate,
-// and the served path carries no floating-point instruction.
-__device__ __forceinline__ uint32_t mod_window(uint32_t x, uint32_t w) {
-#pragma unroll
-  for (int k = 31; k >= 0; k--) {
-    const uint64_t t = (uint64_t)w << k;
-    x = x >= t ? (uint32_t)(x - t) : x;
-  }
-  return x;
+// x mod W for the model's window W through its reciprocal M.w_recip = floor(2^32 / W), which the
+// host forms: q = floor(x w_recip / 2^32) is floor(x / W) or one less (x < 2^32), so the remainder
+// x - q W lies in [0, 2 W) and one step fixes it. The kernels divide by no variable with the
+// compiler's `%`, whose expansion goes through a float reciprocal estimate.
+__device__ __forceinline__ uint32_t mod_window(const DevModel &M, uint32_t x) {
+  const uint32_t q = (uint32_t)(((uint64_t)x * M.w_recip) >> 32);
+  const uint32_t r = x - q * M.W;
+  return r >= M.W ? r - M.W : r;
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -223,11 +221,22 @@ __device__ __forceinline__ uint32_t prog_word(const uint16_t *prog, uint32_t slo
 }
 
 // The snapped transition or gate (RS stack/kernels.rs:1474-1557), out of line: the 120-root
-// scan is long and served only by snapped artifacts.
-__device__ __noinline__ void snap_rotation_dev(const int8_t *ico, int4 raw, uint64_t lambda,
-                                               int64_t *out) {
+// scan is long and served only by snapped artifacts. The quaternion comes back by value (in
+// registers), so no caller array lives in private memory.
+struct Quat64 {
+  int64_t v[4];
+};
+__device__ __noinline__ Quat64 snap_rotation_dev(const int8_t *ico, int4 raw, uint64_t lambda) {
   const int32_t r[4] = {raw.x, raw.y, raw.z, raw.w};
-  snap_rotation(ico, r, lambda, out);
+  Quat64 q;
+  snap_rotation(ico, r, lambda, q.v);
+  return q;
+}
+__device__ __forceinline__ void snap_rotation_to(const int8_t *ico, int4 raw, uint64_t lambda,
+                                                 int64_t (&out)[4]) {
+  const Quat64 q = snap_rotation_dev(ico, raw, lambda);
+#pragma unroll
+  for (int c = 0; c < 4; c++) out[c] = q.v[c];
 }
 
 // The Hamilton gate on rhs (session.rs:4951-4968, :4005-4025): shift_wide(q (x) rhs, 15) with
@@ -245,7 +254,7 @@ __device__ __forceinline__ void gate_apply(const DevModel &M, const Seeds &sd,
     for (int c = 0; c < 4; c++) out[c] = shift_wide(prod[c], 14);
   } else {
     int64_t q[4];
-    snap_rotation_dev(M.icosian, make_int4(raw[0], raw[1], raw[2], raw[3]), 1ull << 31, q);
+    snap_rotation_to(M.icosian, make_int4(raw[0], raw[1], raw[2], raw[3]), 1ull << 31, q);
     hamilton64(q, rhs, prod);
 #pragma unroll
     for (int c = 0; c < 4; c++) out[c] = shift_wide(prod[c], 15);
@@ -279,7 +288,7 @@ __device__ __forceinline__ void gate_quat(const DevModel &M, const Seeds &sd, co
 #pragma unroll
     for (int c = 0; c < 4; c++) g[c] = u[c];
   } else {
-    snap_rotation_dev(M.icosian, make_int4(raw[0], raw[1], raw[2], raw[3]), 1ull << 31, g);
+    snap_rotation_to(M.icosian, make_int4(raw[0], raw[1], raw[2], raw[3]), 1ull << 31, g);
   }
 }
 __device__ __forceinline__ void gate_mul(const DevModel &M, const int64_t (&g)[4],
@@ -813,7 +822,7 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
 #pragma unroll
         for (int c = 0; c < 4; c++) T[c] = u[c] >> idx;  // (lambda u) >> 30, lambda = 2^(30-idx)
       } else {
-        snap_rotation_dev(M.icosian, make_int4(rot[k][0], rot[k][1], rot[k][2], rot[k][3]),
+        snap_rotation_to(M.icosian, make_int4(rot[k][0], rot[k][1], rot[k][2], rot[k][3]),
                           lambda, T64);
       }
       int64_t wide[4];
@@ -1238,7 +1247,7 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
         hamilton32(T, h, moved[k]);
       } else {
         int64_t T64[4];
-        snap_rotation_dev(M.icosian, make_int4(rot[k][0], rot[k][1], rot[k][2], rot[k][3]),
+        snap_rotation_to(M.icosian, make_int4(rot[k][0], rot[k][1], rot[k][2], rot[k][3]),
                           1ull << (30 - idx), T64);
         hamilton64(T64, h, moved[k]);
       }
@@ -1591,7 +1600,7 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
     // Fresh or resumed session: state, window rows (row r = the drive r + 1 positions back)
     // and position (LayerState::Recurrence, session.rs:1850).
     uint32_t pos = A.in_position ? A.in_position[sl] : 0u;
-    uint32_t base = mod_window(pos, W);
+    uint32_t base = mod_window(M, pos);
     // A slot's history is its ring; otherwise the block's ring takes the rows.
     int32_t *ring = A.slots ? A.out_history + (uint64_t)sl * L * W * d : block_ring;
     for (uint32_t l = 0; l < L; l++)
