@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define UOR_FBS_ABI_VERSION 1u
+#define UOR_FBS_ABI_VERSION 2u
 
 #define UOR_FBS_OK 0
 #define UOR_FBS_ERR_TOKEN 1       /* token >= vocab (fbs_core.h:627) */
@@ -88,6 +88,44 @@ typedef struct uor_fbs_model {
  *   offsets NULL -> drawer of token t = t mod drawers, members ascending
  *   table_i8 NULL-> the i16 writer table; else row values are (code << table_shift) at Q12
  *   head 0       -> native writer; 1 -> whole-table L1 nearest (session.rs:4418-4445)     */
+/* The Hamming reads of a `uor-r4.lut-stack/6` stack (the `hamming` record, StackHamming,
+ * stack/format.rs:229-292, and one HammingReadImage per read, stack/hamming.rs:25-40, from the
+ * sections `hamming.d{depth}.*`), served inside the step as the reference session serves them
+ * (ServedHamming::stream after `depth` layers and ServedHamming::readout on the final norm's
+ * output, session.rs:4252-4276, 4296-4320; hamming.rs:1551-1960). The place read
+ * (`hamming.place`) is not served by this build: a record with one is refused. */
+#define UOR_FBS_COPY_ARTIFACT 0xffffffffu /* serve the artifact's own copy rule */
+#define UOR_FBS_COPY_MEAN 0u              /* CopyRule::Mean (hamming.rs:180-201) */
+#define UOR_FBS_COPY_LATEST_EXACT 1u
+#define UOR_FBS_COPY_LATEST_NEAREST 2u
+#define UOR_FBS_COPY_LONGEST_EXACT 3u
+#define UOR_FBS_COPY_LONGEST_AFTER_OPENING 4u
+
+typedef struct uor_fbs_hamming_read {
+  uint32_t depth;                /* after this many layers; the layer count: the readout read */
+  uint32_t carry_rows;           /* the readout read's question carry reach h (0: none) */
+  const int32_t *query_rotation; /* width raw values at 2^-24: the type heads' query */
+  const int32_t *key_rotation;   /* width: the copy heads' and the type heads' keys */
+  const int32_t *value_rotation; /* width: the type heads' payloads */
+  const int32_t *margin;         /* heads margins in bits at Q16, each positive */
+  const int32_t *weight;         /* 2 * width at 2^-24: the copy weights w_c, then w_y */
+  const int16_t *ask;            /* vocab * width Q12 question table; NULL: the read does not ask */
+  const int32_t *carry;          /* vocab carry gains at Q16 (with carry_rows), else NULL */
+} uor_fbs_hamming_read;
+
+typedef struct uor_fbs_hamming {
+  uint32_t heads;               /* per read: heads/2 copy heads, then the type (or ask) heads */
+  uint32_t kept;                /* earlier positions each head keeps, >= 1 */
+  uint32_t copy_key;            /* tokens a copy head's key names: 1 or 2 */
+  uint32_t copy_latest;         /* nonzero: the copy heads read their latest exact match */
+  const uint32_t *copy_keys;    /* heads/2 entries of 1 or 2 when they differ, else NULL */
+  uint32_t copy_longest;        /* nonzero: the longest rule after the reply marker below */
+  uint32_t marker[2];           /* the two ids before a reply's first token (copy_longest) */
+  uint32_t rule;                /* the copy rule served: UOR_FBS_COPY_ARTIFACT or a rule */
+  uint32_t read_count;
+  const uor_fbs_hamming_read *reads; /* read_count reads, depths strictly increasing */
+} uor_fbs_hamming;
+
 typedef struct uor_fbs_ext {
   uint32_t window;                 /* W prior rows of the causal window, 1..64 */
   uint32_t drawers;                /* D drawers, 1..4096 */
@@ -100,6 +138,7 @@ typedef struct uor_fbs_ext {
   const int8_t *table_i8;          /* vocab * width codes */
   uint32_t table_shift;            /* 0..8 */
   uint32_t reserved;
+  const uor_fbs_hamming *hamming;  /* NULL: no Hamming reads (every schema but lut-stack/6) */
 } uor_fbs_ext;
 
 typedef struct uor_fbs_handle uor_fbs_handle;
@@ -203,6 +242,41 @@ int uor_fbs_decode_slots_async(uor_fbs_handle *handle, const uint32_t *slots, ui
                                uint32_t gen, uint32_t *out_reply, int64_t *state,
                                int32_t *history, uint32_t *position, uint32_t *out_kept,
                                int32_t *out_query, int32_t *status, void *stream);
+
+/* ---- Hamming models (an ext with `hamming`): the session's token stream and payloads.
+ * A Hamming read at row t reads the session's tokens x_0..x_t (IntegerStackSession::tokens) and,
+ * for a read whose type heads bring back payloads, the payload it kept at every earlier row
+ * (`hamming_payloads`, session.rs:1755-1759, 2232; ServedHamming::payload_caches,
+ * hamming.rs:1680-1685), so a resumed session needs both besides its state. `stream_words`:
+ * tokens a session keeps, the context (0 without Hamming reads); `payload_words`: int64 payload
+ * values, [typed read][context][width] (0 without such reads). The other decode entry points
+ * decode a Hamming model from fresh sessions and refuse `in_position` (resuming) on one with
+ * UOR_FBS_ERR_UNSUPPORTED, as the reference refuses a saved session without its payloads
+ * (session.rs:2885-2910); the slot and allocation-free entry points refuse Hamming models. */
+uint64_t uor_fbs_stream_words(const uor_fbs_handle *handle);
+uint64_t uor_fbs_payload_words(const uor_fbs_handle *handle);
+
+/* uor_fbs_decode_async with the stream: `in_stream` [n][stream_words] (entries below the
+ * position read) and `in_payloads` [n][payload_words] (rows below the position read) resume,
+ * both required with `in_position` on a Hamming model; `out_stream` and `out_payloads` receive
+ * them after the last step (rows at and past the position are left as found). `out_payloads`
+ * may equal `in_payloads` (updated in place). On a model without Hamming reads the stream
+ * arguments are ignored. Device buffers. */
+int uor_fbs_decode_stream_async(uor_fbs_handle *handle, const uint32_t *prompts,
+                                uint32_t sequences, uint32_t prompt_len, uint32_t gen,
+                                uint32_t *out_reply, const int64_t *in_state,
+                                const int32_t *in_history, const uint32_t *in_position,
+                                const uint32_t *in_stream, const int64_t *in_payloads,
+                                int64_t *out_state, int32_t *out_history, uint32_t *out_position,
+                                uint32_t *out_stream, int64_t *out_payloads, int32_t *status,
+                                void *stream);
+/* The same on host buffers. */
+int uor_fbs_decode_stream(uor_fbs_handle *handle, const uint32_t *prompts, uint32_t sequences,
+                          uint32_t prompt_len, uint32_t gen, uint32_t *out_reply,
+                          const int64_t *in_state, const int32_t *in_history,
+                          const uint32_t *in_position, const uint32_t *in_stream,
+                          const int64_t *in_payloads, int64_t *out_state, int32_t *out_history,
+                          uint32_t *out_position, uint32_t *out_stream, int64_t *out_payloads);
 
 /* Teacher-forced next-token scoring: for each row of `len` tokens, position t's choice is
  * compared with row[t+1] (t < len-1); `out_matches` gets the total count of equal pairs.

@@ -283,7 +283,12 @@ typedef struct {
   const uint32_t *offsets, *members;
   const int8_t *t8;
   uint32_t t8_shift;
+  struct Ham *ham; /* the Hamming reads, or NULL */
 } O;
+
+struct Ham;
+static struct Ham *ham_build(const O *o, const uor_fbs_hamming *hm);
+static void ham_free(struct Ham *h);
 
 static void resolve(O *o, const uor_fbs_model *m, const uor_fbs_ext *e) {
   memset(o, 0, sizeof *o);
@@ -304,6 +309,12 @@ static void resolve(O *o, const uor_fbs_model *m, const uor_fbs_ext *e) {
   o->t8 = e ? e->table_i8 : NULL;
   o->t8_shift = e ? e->table_shift : 0;
   o->reference_writer = o->D == CELLS && !o->keys && !o->offsets;
+  o->ham = (e && e->hamming) ? ham_build(o, e->hamming) : NULL;
+}
+
+static void unresolve(O *o) {
+  ham_free(o->ham);
+  o->ham = NULL;
 }
 
 /* Writer-table value of token t, channel i, at Q12 (the i16 table, or code << shift). */
@@ -463,6 +474,400 @@ static uint32_t writer(const O *o, const int32_t *q, uint32_t *kept, uint64_t *c
   return o->reference_writer ? writer_reference(o, q, kept, cand) : writer_drawers(o, q, kept, cand);
 }
 
+
+/* ------------------------------------------------------------------------------------------
+ * The Hamming reads of a lut-stack/6 stack (RS stack/hamming.rs): at the stream read after
+ * `depth` layers the residual becomes x + w_c (.) c + w_y (.) y, on the readout the final norm's
+ * output n + w_c (.) (c - n) + w_y (.) y (or (y - n) for a read that asks), c the copy heads'
+ * mean and y the type heads' (ServedHamming::stream/readout :1831-1913, stream_sum :1918-1925,
+ * readout_sum :1933-1940, readout_ask_sum :1946-1953). */
+
+#define COPY_MEAN_EXP (-43)     /* RS stack/hamming.rs:175 */
+#define HAMMING_WEIGHT_EXP (-24) /* RS stack/format.rs:59 */
+#define TYPE_MEAN_SHIFT 31u     /* RS stack/hamming.rs:1364 */
+#define STREAM_SHIFT ((uint32_t)(RESIDUAL_EXP - HAMMING_WEIGHT_EXP - COPY_MEAN_EXP))
+#define NORM_RAISE ((uint32_t)(NORM_FINE_EXP - COPY_MEAN_EXP))
+#define READOUT_SHIFT ((uint32_t)(NORM_FINE_EXP - HAMMING_WEIGHT_EXP - COPY_MEAN_EXP))
+#define STREAM_COPY_RAISE ((uint32_t)(COPY_MEAN_EXP - RESIDUAL_EXP + (int)TYPE_MEAN_SHIFT))
+#define READOUT_TYPE_DROP ((uint32_t)(COPY_MEAN_EXP - NORM_FINE_EXP + (int)TYPE_MEAN_SHIFT))
+
+typedef struct {
+  const uor_fbs_hamming_read *r;
+  int64_t *qu, *ku, *vu; /* width/4 unit quaternions at Q31 (`units`, :541-548) */
+  int typed;             /* type heads served: some w_y is not zero (:1574-1599) */
+  int asks;              /* its type heads ask from the question table (:1147) */
+  int slot;              /* its payload cache, for a typed read that does not ask; else -1 */
+  uint64_t *codes;       /* vocab * heads: every entry's code through the key rotation
+                            (`vocab_codes` :566-582), copy heads first, then type heads */
+  uint32_t heads;
+} HR;
+
+typedef struct Ham {
+  uint32_t heads, copy, hw, kept, rule, has_marker, marker[2], n, slots;
+  uint64_t *pair;  /* per copy head: the first half's bits under copy key 2, else 0 */
+  HR *reads;
+  int *at;         /* layers + 1: the read at each depth, -1 none */
+} Ham;
+
+typedef struct {
+  size_t s;
+  uint32_t d;
+} Pick;
+
+static i128 shl128(i128 v, uint32_t s) { return (i128)((u128)v << s); }
+
+/* `round_shift` (:1353-1360): v / 2^s rounded half away from zero. */
+static i128 round_shift(i128 v, uint32_t s) {
+  i128 half = (i128)1 << (s - 1);
+  return v >= 0 ? (v + half) >> s : -((half - v) >> s);
+}
+
+static int64_t clamp64(i128 v) {
+  return v > (i128)INT64_MAX ? INT64_MAX : v < (i128)INT64_MIN ? INT64_MIN : (int64_t)v;
+}
+
+/* `stream_sum` (:1918-1925). */
+static int32_t stream_sum(int32_t x, int32_t w_c, i128 c, int32_t w_y, i128 y) {
+  uint32_t sh = STREAM_SHIFT + STREAM_COPY_RAISE;
+  i128 sum = shl128(x, sh) + shl128(wmul128(w_c, c), STREAM_COPY_RAISE) + wmul128(w_y, y);
+  i128 r = round_shift(sum, sh);
+  return r > INT32_MAX ? INT32_MAX : r < INT32_MIN ? INT32_MIN : (int32_t)r;
+}
+
+/* `readout_sum` (:1933-1940): c present where a copy head matched. */
+static int64_t readout_sum(int64_t n, int32_t w_c, const i128 *c, int32_t w_y, i128 y) {
+  i128 moved = c ? wmul128(w_c, *c - shl128(n, NORM_RAISE)) : 0;
+  i128 typed = round_shift(wmul128(w_y, y), READOUT_TYPE_DROP);
+  return clamp64(round_shift(shl128(n, READOUT_SHIFT) + moved + typed, READOUT_SHIFT));
+}
+
+/* `readout_ask_sum` (:1946-1953): each move present where a head of its kind matched. */
+static int64_t readout_ask_sum(int64_t n, int32_t w_c, const i128 *c, int32_t w_y, const i128 *y) {
+  i128 raised = shl128(n, NORM_RAISE);
+  i128 copied = c ? wmul128(w_c, *c - raised) : 0;
+  i128 asked = y ? wmul128(w_y, *y - raised) : 0;
+  return clamp64(round_shift(shl128(n, READOUT_SHIFT) + copied + asked, READOUT_SHIFT));
+}
+
+/* `copy_weight_q31` (:243-252). */
+static uint64_t ham_weight(int32_t margin_q16, uint32_t distance) {
+  int64_t margin = margin_q16, over = margin - ((int64_t)distance << 16);
+  if (over <= 0) return 0;
+  return ((uint64_t)over << 31) / (uint64_t)(margin > (1 << 16) ? margin : (1 << 16));
+}
+
+/* `head_code` (:550-564): head h's sign word of `point` through `units`, the unit on the left. */
+static uint64_t head_code(const int64_t *units, const int64_t *point, uint32_t h, uint32_t hw) {
+  uint64_t word = 0;
+  for (uint32_t c = 0; c < hw; c += 4) {
+    uint32_t at = h * hw + c;
+    i128 o[4];
+    hamilton(units + at, point + at, o);
+    for (int i = 0; i < 4; i++)
+      if (o[i] >= 0) word |= 1ull << (c + i);
+  }
+  return word;
+}
+
+static int cmp_pick(const void *a, const void *b) {
+  const Pick *x = (const Pick *)a, *y = (const Pick *)b;
+  if (x->d != y->d) return x->d < y->d ? -1 : 1;
+  return x->s < y->s ? -1 : x->s > y->s;
+}
+
+static uint64_t ham_code(const HR *r, uint32_t token, uint32_t head) {
+  return r->codes[(size_t)token * r->heads + head];
+}
+/* `joined` (:379-385), `query_at` (:389-391), `key_at` (:395-397). */
+static uint64_t ham_joined(const Ham *h, const HR *r, uint32_t near, uint32_t far, uint32_t head) {
+  uint64_t c = ham_code(r, near, head), first = h->pair[head];
+  return first ? (c & first) | (ham_code(r, far, head) & ~first) : c;
+}
+
+/* `nearest` (:690-701): the min(kept, t - 1) positions 1 <= s < t nearest by popcount, ties to
+ * the earlier position; `key[s]` is position s's code. */
+static size_t ham_nearest(uint64_t query, size_t t, uint32_t kept, const uint64_t *key, Pick *out) {
+  if (t < 2) return 0;
+  Pick *all = malloc(sizeof(Pick) * t);
+  size_t n = 0;
+  for (size_t s = 1; s < t; s++) all[n++] = (Pick){s, (uint32_t)__builtin_popcountll(query ^ key[s])};
+  qsort(all, n, sizeof(Pick), cmp_pick);
+  if (n > kept) n = kept;
+  memcpy(out, all, n * sizeof(Pick));
+  free(all);
+  return n;
+}
+
+/* Copy head `head`'s positions at the last row of tok[0..=t] under the rule in force
+ * (`choose_ruled` :356-371, `latest_of` :584-598, `longest_of` :601-615, `longer_at` :349-352);
+ * `opening` is the caller's reply mark (this build passes none). */
+static size_t ham_copy_choose(const Ham *h, const HR *r, uint32_t head, const uint32_t *tok,
+                              size_t t, int opening, uint64_t *key, Pick *out) {
+  uint32_t rule = h->rule;
+  if (rule == UOR_FBS_COPY_LONGEST_AFTER_OPENING) {
+    int opens = h->has_marker ? (t >= 1 && tok[t - 1] == h->marker[0] && tok[t] == h->marker[1])
+                              : opening;
+    rule = opens ? UOR_FBS_COPY_LATEST_EXACT : UOR_FBS_COPY_LONGEST_EXACT;
+  }
+  uint64_t q = ham_joined(h, r, tok[t], tok[t ? t - 1 : 0], head);
+  for (size_t s = 1; s < t; s++) key[s] = ham_joined(h, r, tok[s - 1], tok[s >= 2 ? s - 2 : 0], head);
+  if (rule == UOR_FBS_COPY_MEAN) return ham_nearest(q, t, h->kept, key, out);
+  if (rule == UOR_FBS_COPY_LATEST_EXACT || rule == UOR_FBS_COPY_LATEST_NEAREST) {
+    size_t best = 0;
+    uint32_t least = 0;
+    for (size_t s = 1; s < t; s++) {
+      uint32_t d = (uint32_t)__builtin_popcountll(q ^ key[s]);
+      if (rule == UOR_FBS_COPY_LATEST_EXACT && d != 0) continue;
+      if (!best || d <= least) {
+        best = s;
+        least = d;
+      }
+    }
+    if (!best) return 0;
+    out[0] = (Pick){best, least};
+    return 1;
+  }
+  /* longest exact: the latest exact match whose token before the key also agrees by the head's
+   * code, else the latest exact match. */
+  size_t kd = h->pair[head] ? 2 : 1, ex = 0, lg = 0;
+  for (size_t s = 1; s < t; s++) {
+    if (key[s] != q) continue;
+    ex = s;
+    if (s > kd && ham_code(r, tok[s - 1 - kd], head) == ham_code(r, tok[t - kd], head)) lg = s;
+  }
+  size_t pick = lg ? lg : ex;
+  if (!pick) return 0;
+  out[0] = (Pick){pick, 0};
+  return 1;
+}
+
+/* One head's weighted sum over its picks into acc (width), `point(s, i)` the value brought back
+ * from position s; returns the count of positions inside the margin (`mean_by` :506-538,
+ * TypeHeads::mean_by :1282-1334). */
+typedef struct {
+  const O *o;
+  const uint32_t *tok;
+  const int64_t *payloads; /* NULL: table points of each position's own token */
+} Brought;
+
+static i128 brought(const Brought *b, size_t s, uint32_t i) {
+  if (b->payloads) return b->payloads[s * b->o->d + i];
+  return row_value(b->o, b->tok[s], i);
+}
+
+static uint32_t ham_head_sum(const Brought *b, const Pick *picks, size_t n, int32_t margin,
+                             i128 *acc) {
+  uint32_t d = b->o->d, count = 0;
+  for (uint32_t i = 0; i < d; i++) acc[i] = 0;
+  for (size_t k = 0; k < n; k++) {
+    uint64_t w = ham_weight(margin, picks[k].d);
+    if (!w) continue;
+    count++;
+    for (uint32_t i = 0; i < d; i++) acc[i] += brought(b, picks[k].s, i) * (i128)w;
+  }
+  return count;
+}
+
+/* The copy heads' mean at row t (`CopyHeads::mean_at` :482-504): returns 0 when no head found a
+ * position inside its margin. */
+static int ham_copy_mean(const O *o, const HR *r, const uint32_t *tok, size_t t, i128 *c) {
+  const Ham *h = o->ham;
+  uint32_t d = o->d, found = 0;
+  i128 *head = malloc(sizeof(i128) * d);
+  uint64_t *key = malloc(sizeof(uint64_t) * (t + 1));
+  Pick *picks = malloc(sizeof(Pick) * (h->kept + 1));
+  for (uint32_t i = 0; i < d; i++) c[i] = 0;
+  Brought b = {o, tok, NULL};
+  for (uint32_t k = 0; k < h->copy; k++) {
+    size_t n = ham_copy_choose(h, r, k, tok, t, 0, key, picks);
+    uint32_t count = ham_head_sum(&b, picks, n, r->r->margin[k], head);
+    if (!count) continue;
+    found++;
+    for (uint32_t i = 0; i < d; i++) c[i] += head[i] / (i128)count;
+  }
+  if (found)
+    for (uint32_t i = 0; i < d; i++) c[i] /= (i128)found;
+  free(head);
+  free(key);
+  free(picks);
+  return found > 0;
+}
+
+/* `TypeHeads::asked_point` (:1161-1181): (table + a)[x_t] at Q28 plus the carried rows. */
+static void ham_asked_point(const O *o, const HR *r, const uint32_t *tok, size_t t, int64_t *p) {
+  uint32_t d = o->d;
+  const int16_t *a = r->r->ask;
+  for (uint32_t i = 0; i < d; i++)
+    p[i] = (int64_t)(row_value(o, tok[t], i) + a[(size_t)tok[t] * d + i]) * 65536;
+  if (r->r->carry && r->r->carry_rows) {
+    size_t reach = r->r->carry_rows < t ? r->r->carry_rows : t;
+    for (size_t s = 1; s <= reach; s++) {
+      uint32_t v = tok[t - s];
+      int64_t gain = r->r->carry[v];
+      for (uint32_t i = 0; i < d; i++)
+        p[i] += gain * (int64_t)(row_value(o, v, i) + a[(size_t)v * d + i]);
+    }
+  }
+}
+
+/* The type heads' mean at row t (`ServedHamming::type_mean` :1750-1783, TypeHeads::mean and
+ * ask_mean :1254-1280): for a read that asks, the question codes of the asked point through the
+ * key rotation and the kept tokens' table points (at COPY_MEAN_EXP); otherwise `point`'s payload
+ * is kept at row t first, the query codes are `point`'s through the query rotation and the kept
+ * positions' payloads come back (at the point's exponent minus 31). */
+static int ham_type_mean(const O *o, const HR *r, const uint32_t *tok, size_t t,
+                         const int64_t *point, int64_t *payloads, i128 *y) {
+  const Ham *h = o->ham;
+  uint32_t d = o->d, found = 0, types = h->heads - h->copy;
+  int64_t *asked = NULL;
+  if (r->asks) {
+    asked = malloc(sizeof(int64_t) * d);
+    ham_asked_point(o, r, tok, t, asked);
+  } else {
+    for (uint32_t q = 0; q < d / 4; q++) {
+      i128 rot[4];
+      hamilton(r->vu + 4 * q, point + 4 * q, rot);
+      for (int k = 0; k < 4; k++) payloads[t * d + 4 * q + k] = clamp64(round_shift(rot[k], 31));
+    }
+  }
+  i128 *head = malloc(sizeof(i128) * d);
+  uint64_t *key = malloc(sizeof(uint64_t) * (t + 1));
+  Pick *picks = malloc(sizeof(Pick) * (h->kept + 1));
+  for (uint32_t i = 0; i < d; i++) y[i] = 0;
+  Brought b = {o, tok, r->asks ? NULL : payloads};
+  for (uint32_t j = 0; j < types; j++) {
+    uint64_t query = r->asks ? head_code(r->ku, asked, h->copy + j, h->hw)
+                             : head_code(r->qu, point, h->copy + j, h->hw);
+    for (size_t s = 1; s < t; s++) key[s] = ham_code(r, tok[s - 1], h->copy + j);
+    size_t n = ham_nearest(query, t, h->kept, key, picks);
+    uint32_t count = ham_head_sum(&b, picks, n, r->r->margin[h->copy + j], head);
+    if (!count) continue;
+    found++;
+    for (uint32_t i = 0; i < d; i++) y[i] += head[i] / (i128)count;
+  }
+  if (found)
+    for (uint32_t i = 0; i < d; i++) y[i] /= (i128)found;
+  free(asked);
+  free(head);
+  free(key);
+  free(picks);
+  return found > 0;
+}
+
+/* The stream read after `depth` layers on the residual x (ServedHamming::stream :1831-1866). */
+static void ham_stream(const O *o, uint32_t depth, const uint32_t *tok, size_t t, int32_t *x,
+                       int64_t *payloads) {
+  const Ham *h = o->ham;
+  if (depth == o->L || h->at[depth] < 0) return;
+  const HR *r = &h->reads[h->at[depth]];
+  uint32_t d = o->d;
+  i128 *c = malloc(sizeof(i128) * d), *y = malloc(sizeof(i128) * d);
+  int has_c = h->copy ? ham_copy_mean(o, r, tok, t, c) : 0, has_y = 0;
+  if (r->typed) {
+    int64_t *point = malloc(sizeof(int64_t) * d);
+    for (uint32_t i = 0; i < d; i++) point[i] = x[i];
+    has_y = ham_type_mean(o, r, tok, t, point,
+                          r->slot >= 0 ? payloads + (size_t)r->slot * o->m->context * d : NULL, y);
+    free(point);
+    if (has_y && r->asks)
+      for (uint32_t i = 0; i < d; i++) y[i] = shl128(y[i], STREAM_COPY_RAISE);
+  }
+  if (has_c || has_y)
+    for (uint32_t i = 0; i < d; i++)
+      x[i] = stream_sum(x[i], r->r->weight[i], has_c ? c[i] : 0, r->r->weight[d + i], has_y ? y[i] : 0);
+  free(c);
+  free(y);
+}
+
+/* The readout read on the final norm's output n (ServedHamming::readout :1883-1913); no place
+ * read, so no offer. */
+static void ham_readout(const O *o, const uint32_t *tok, size_t t, int64_t *n, int64_t *payloads) {
+  const Ham *h = o->ham;
+  if (h->at[o->L] < 0) return;
+  const HR *r = &h->reads[h->at[o->L]];
+  uint32_t d = o->d;
+  i128 *c = malloc(sizeof(i128) * d), *y = malloc(sizeof(i128) * d);
+  int has_c = h->copy ? ham_copy_mean(o, r, tok, t, c) : 0, has_y = 0;
+  if (r->typed)
+    has_y = ham_type_mean(o, r, tok, t, n,
+                          r->slot >= 0 ? payloads + (size_t)r->slot * o->m->context * d : NULL, y);
+  if (has_c || has_y)
+    for (uint32_t i = 0; i < d; i++) {
+      const i128 *ci = has_c ? &c[i] : NULL;
+      n[i] = r->asks ? readout_ask_sum(n[i], r->r->weight[i], ci, r->r->weight[d + i], has_y ? &y[i] : NULL)
+                     : readout_sum(n[i], r->r->weight[i], ci, r->r->weight[d + i], has_y ? y[i] : 0);
+    }
+  free(c);
+  free(y);
+}
+
+/* Builds the served reads (ServedHamming::new :1571-1609 with CopyHeads::new :287-313 and
+ * TypeHeads::new :1130-1145): units of the three rotations, every vocabulary entry's key code
+ * per head, the copy heads' pair masks and rule. */
+static Ham *ham_build(const O *o, const uor_fbs_hamming *hm) {
+  Ham *h = calloc(1, sizeof(Ham));
+  uint32_t d = o->d, V = o->m->vocab;
+  h->heads = hm->heads;
+  h->copy = hm->heads / 2;
+  h->hw = d / hm->heads;
+  h->kept = hm->kept;
+  h->n = hm->read_count;
+  h->has_marker = hm->copy_longest != 0;
+  h->marker[0] = hm->marker[0];
+  h->marker[1] = hm->marker[1];
+  h->rule = hm->rule != UOR_FBS_COPY_ARTIFACT ? hm->rule
+            : hm->copy_longest          ? UOR_FBS_COPY_LONGEST_AFTER_OPENING
+            : hm->copy_latest           ? UOR_FBS_COPY_LATEST_EXACT
+                                        : UOR_FBS_COPY_MEAN;
+  h->pair = calloc(h->copy ? h->copy : 1, sizeof(uint64_t));
+  for (uint32_t k = 0; k < h->copy; k++) {
+    uint32_t key = hm->copy_keys ? hm->copy_keys[k] : hm->copy_key;
+    h->pair[k] = key == 2 ? (1ull << (h->hw / 2)) - 1 : 0;
+  }
+  h->at = malloc(sizeof(int) * (o->L + 1));
+  for (uint32_t l = 0; l <= o->L; l++) h->at[l] = -1;
+  h->reads = calloc(h->n, sizeof(HR));
+  for (uint32_t i = 0; i < h->n; i++) {
+    HR *r = &h->reads[i];
+    r->r = &hm->reads[i];
+    h->at[r->r->depth] = (int)i;
+    int64_t **u[3] = {&r->qu, &r->ku, &r->vu};
+    const int32_t *raw[3] = {r->r->query_rotation, r->r->key_rotation, r->r->value_rotation};
+    for (int k = 0; k < 3; k++) {
+      *u[k] = malloc(sizeof(int64_t) * d);
+      for (uint32_t q = 0; q < d / 4; q++) rotation(raw[k] + 4 * q, 1ull << 31, GATE_EPSILON, *u[k] + 4 * q);
+    }
+    r->typed = 0;
+    for (uint32_t c = 0; c < d; c++) r->typed |= r->r->weight[d + c] != 0;
+    r->asks = r->r->ask != NULL;
+    r->slot = (r->typed && !r->asks) ? (int)h->slots++ : -1;
+    r->heads = h->heads;
+    r->codes = malloc(sizeof(uint64_t) * (size_t)V * h->heads);
+    int64_t *point = malloc(sizeof(int64_t) * d);
+    for (uint32_t v = 0; v < V; v++) {
+      for (uint32_t c = 0; c < d; c++) point[c] = row_value(o, v, c);
+      for (uint32_t k = 0; k < h->heads; k++)
+        r->codes[(size_t)v * h->heads + k] = head_code(r->ku, point, k, h->hw);
+    }
+    free(point);
+  }
+  return h;
+}
+
+static void ham_free(Ham *h) {
+  if (!h) return;
+  for (uint32_t i = 0; i < h->n; i++) {
+    free(h->reads[i].qu);
+    free(h->reads[i].ku);
+    free(h->reads[i].vu);
+    free(h->reads[i].codes);
+  }
+  free(h->reads);
+  free(h->pair);
+  free(h->at);
+  free(h);
+}
+
 /* ------------------------------------------------------------------------------------------
  * One sequence's session. */
 
@@ -475,6 +880,9 @@ typedef struct {
   uint32_t *kept;
   uint32_t position;
   uint64_t candidates;
+  uint32_t *tokens;  /* the session's tokens x_0..x_{position-1} (IntegerStackSession::tokens) */
+  int64_t *payloads; /* [typed read][context][width]: the type heads' payloads (hamming_payloads) */
+  int64_t *normed;   /* width: the final norm's output (the readout read's input) */
 } S;
 
 static void session_alloc(const O *o, S *s) {
@@ -493,18 +901,23 @@ static void session_alloc(const O *o, S *s) {
   s->state = calloc((size_t)o->L * d, 8);
   s->history = calloc((size_t)o->L * o->W * d, 4);
   s->kept = calloc(o->P ? o->P : 1, 4);
+  s->tokens = calloc(o->m->context ? o->m->context : 1, 4);
+  s->payloads = calloc(o->ham && o->ham->slots ? (size_t)o->ham->slots * o->m->context * d : 1, 8);
+  s->normed = calloc(d, 8);
 }
 
 static void session_free(S *s) {
   free(s->x); free(s->branches); free(s->gate_out); free(s->proj); free(s->gate); free(s->up);
   free(s->query); free(s->scratch); free(s->wide); free(s->act); free(s->state);
-  free(s->history); free(s->kept);
+  free(s->history); free(s->kept); free(s->tokens); free(s->payloads); free(s->normed);
 }
 
 static void session_reset(const O *o, S *s) {
   memset(s->state, 0, sizeof(int64_t) * o->L * o->d);
   memset(s->history, 0, sizeof(int32_t) * o->L * o->W * o->d);
   s->position = 0;
+  memset(s->tokens, 0, 4ull * o->m->context);
+  if (o->ham && o->ham->slots) memset(s->payloads, 0, 8ull * o->ham->slots * o->m->context * o->d);
 }
 
 /* `stack_recurrence_core` with geometric gates, learned rotations and the Hamilton output
@@ -569,13 +982,17 @@ static void hamilton_gate(const O *o, const int32_t *gate, const int32_t *up, in
   }
 }
 
-/* `stack_step_fbs` without the optional Hamming/address/pair/Q31/memory hooks
- * (RS stack/session.rs:4129-4403, TW 635-675). */
+/* `stack_step_fbs` with the Hamming reads and without the address/pair/Q31/memory hooks
+ * (RS stack/session.rs:4129-4403, TW 635-675): the token joins the session's tokens first, the
+ * stream read follows a layer at its depth (:4252-4276), the readout read moves the final norm's
+ * output before the query (:4296-4320). */
 static int step(const O *o, S *s, uint32_t token, uint32_t *out_token) {
   const uor_fbs_model *m = o->m;
   uint32_t d = o->d;
   if (token >= m->vocab) return UOR_FBS_ERR_TOKEN;
   if (s->position >= m->context) return UOR_FBS_ERR_CONTEXT;
+  s->tokens[s->position] = token;
+  const size_t t = s->position;
   for (uint32_t i = 0; i < d; i++) s->x[i] = to_exp_i32(row_value(o, token, i), Q12_EXP, RESIDUAL_EXP);
   for (uint32_t l = 0; l < o->L; l++) {
     const uor_fbs_layer *ly = m->layers + l;
@@ -596,10 +1013,13 @@ static int step(const O *o, S *s, uint32_t token, uint32_t *out_token) {
     act_exp = quantize16(s->scratch, o->mlp, PRODUCT_EXP, s->act);
     gather16(&ly->mlp_down, s->act, act_exp, s->proj);
     for (uint32_t i = 0; i < d; i++) s->x[i] = sat_add32(s->x[i], s->proj[i]);
+    if (o->ham) ham_stream(o, l + 1, s->tokens, t, s->x, s->payloads);
   }
   rms_norm_fine(s->x, d, m->eps_mantissa, m->eps_exp, s->scratch);
+  for (uint32_t i = 0; i < d; i++) s->normed[i] = grid_apply(s->scratch[i], m->final_gain[i]);
+  if (o->ham) ham_readout(o, s->tokens, t, s->normed, s->payloads);
   for (uint32_t i = 0; i < d; i++) {
-    int32_t q = to_exp_i32(grid_apply(s->scratch[i], m->final_gain[i]), NORM_FINE_EXP, Q12_EXP);
+    int32_t q = to_exp_i32(s->normed[i], NORM_FINE_EXP, Q12_EXP);
     s->query[i] = q > 32767 ? 32767 : q < -32768 ? -32768 : q;
   }
   *out_token = writer(o, s->query, s->kept, &s->candidates);
@@ -626,6 +1046,10 @@ typedef struct {
   int32_t *out_history;
   uint32_t *out_position;
   uint64_t *out_candidates;
+  const uint32_t *in_tokens;   /* [n][context], the session's tokens (Hamming reads) */
+  uint32_t *out_tokens_ctx;
+  const int64_t *in_payloads;  /* [n][typed reads][context][width] */
+  int64_t *out_payloads;
   uint64_t matches;
   int tid, threads, status;
 } Job;
@@ -661,6 +1085,9 @@ static void *run_job(void *arg) {
     if (j->in_state) memcpy(s.state, j->in_state + i * sw, 8 * sw);
     if (j->in_history) memcpy(s.history, j->in_history + i * hw, 4 * hw);
     if (j->in_position) s.position = j->in_position[i];
+    const uint64_t ctx = o->m->context, pw = o->ham ? (uint64_t)o->ham->slots * ctx * d : 0;
+    if (j->in_tokens) memcpy(s.tokens, j->in_tokens + i * ctx, 4 * ctx);
+    if (j->in_payloads && pw) memcpy(s.payloads, j->in_payloads + i * pw, 8 * pw);
     const uint32_t *prompt = j->tokens + i * j->prompt_len;
     uint32_t *reply = j->out_reply + i * ((uint64_t)j->gen + 1);
     uint32_t next = 0;
@@ -679,6 +1106,8 @@ static void *run_job(void *arg) {
     if (j->out_history) memcpy(j->out_history + i * hw, s.history, 4 * hw);
     if (j->out_position) j->out_position[i] = s.position;
     if (j->out_candidates) j->out_candidates[i] = s.candidates;
+    if (j->out_tokens_ctx) memcpy(j->out_tokens_ctx + i * ctx, s.tokens, 4 * ctx);
+    if (j->out_payloads && pw) memcpy(j->out_payloads + i * pw, s.payloads, 8 * pw);
   }
   session_free(&s);
   return NULL;
@@ -723,7 +1152,9 @@ int fbs_oracle_sequences(const uor_fbs_model *m, const uor_fbs_ext *ext, const u
   j.out_tokens = out_tokens;
   j.out_kept = out_kept;
   j.out_query = out_query;
-  return run_jobs(&j, threads);
+  int status = run_jobs(&j, threads);
+  unresolve(&o);
+  return status;
 }
 
 int fbs_oracle_decode(const uor_fbs_model *m, const uor_fbs_ext *ext, const uint32_t *prompts,
@@ -748,7 +1179,93 @@ int fbs_oracle_decode(const uor_fbs_model *m, const uor_fbs_ext *ext, const uint
   j.out_history = out_history;
   j.out_position = out_position;
   j.out_candidates = out_candidates;
-  return run_jobs(&j, threads);
+  int status = run_jobs(&j, threads);
+  unresolve(&o);
+  return status;
+}
+
+int fbs_oracle_decode_stream(const uor_fbs_model *m, const uor_fbs_ext *ext,
+                             const uint32_t *prompts, uint32_t sequences, uint32_t prompt_len,
+                             uint32_t gen, uint32_t *out_reply, const int64_t *in_state,
+                             const int32_t *in_history, const uint32_t *in_position,
+                             const uint32_t *in_tokens, const int64_t *in_payloads,
+                             int64_t *out_state, int32_t *out_history, uint32_t *out_position,
+                             uint32_t *out_tokens, int64_t *out_payloads, int threads) {
+  O o;
+  resolve(&o, m, ext);
+  Job j = {0};
+  j.o = &o;
+  j.kind = 1;
+  j.tokens = prompts;
+  j.n = sequences;
+  j.prompt_len = prompt_len;
+  j.gen = gen;
+  j.out_reply = out_reply;
+  j.in_state = in_state;
+  j.in_history = in_history;
+  j.in_position = in_position;
+  j.out_state = out_state;
+  j.out_history = out_history;
+  j.out_position = out_position;
+  j.in_tokens = in_tokens;
+  j.out_tokens_ctx = out_tokens;
+  j.in_payloads = in_payloads;
+  j.out_payloads = out_payloads;
+  int status = run_jobs(&j, threads);
+  unresolve(&o);
+  return status;
+}
+
+uint32_t fbs_oracle_hamming_typed(const uor_fbs_model *m, const uor_fbs_ext *ext) {
+  O o;
+  resolve(&o, m, ext);
+  uint32_t n = o.ham ? o.ham->slots : 0;
+  unresolve(&o);
+  return n;
+}
+
+/* The read at one row, as the reference's hook tests drive it (tests.rs:5579-5623, 8380-8470):
+ * tok[0..=t] the window, `x` (width, the stream read at `depth` < layers) or `n` (width, the
+ * readout read at depth = layers) read in place, `payloads` the typed reads' caches. */
+int fbs_oracle_hamming_row(const uor_fbs_model *m, const uor_fbs_ext *ext, uint32_t depth,
+                           const uint32_t *tok, uint32_t t, int32_t *x, int64_t *n,
+                           int64_t *payloads) {
+  O o;
+  resolve(&o, m, ext);
+  if (!o.ham) return UOR_FBS_ERR_ARGUMENT;
+  if (depth < o.L)
+    ham_stream(&o, depth, tok, t, x, payloads);
+  else
+    ham_readout(&o, tok, t, n, payloads);
+  unresolve(&o);
+  return 0;
+}
+
+/* Every vocabulary entry's code per head through read r's key rotation (vocab * heads). */
+int fbs_oracle_hamming_codes(const uor_fbs_model *m, const uor_fbs_ext *ext, uint32_t r,
+                             uint64_t *out) {
+  O o;
+  resolve(&o, m, ext);
+  if (!o.ham || r >= o.ham->n) return UOR_FBS_ERR_ARGUMENT;
+  memcpy(out, o.ham->reads[r].codes, sizeof(uint64_t) * (size_t)m->vocab * o.ham->heads);
+  unresolve(&o);
+  return 0;
+}
+
+int32_t fbs_oracle_stream_sum(int32_t x, int32_t w_c, int64_t c_hi, uint64_t c_lo, int32_t w_y,
+                              int64_t y_hi, uint64_t y_lo) {
+  return stream_sum(x, w_c, (i128)(((u128)(uint64_t)c_hi << 64) | c_lo), w_y,
+                    (i128)(((u128)(uint64_t)y_hi << 64) | y_lo));
+}
+int64_t fbs_oracle_readout_sum(int64_t n, int32_t w_c, int has_c, int64_t c_hi, uint64_t c_lo,
+                               int32_t w_y, int64_t y_hi, uint64_t y_lo) {
+  i128 c = (i128)(((u128)(uint64_t)c_hi << 64) | c_lo);
+  return readout_sum(n, w_c, has_c ? &c : NULL, w_y, (i128)(((u128)(uint64_t)y_hi << 64) | y_lo));
+}
+int64_t fbs_oracle_readout_ask_sum(int64_t n, int32_t w_c, int has_c, int64_t c_hi, uint64_t c_lo,
+                                   int32_t w_y, int has_y, int64_t y_hi, uint64_t y_lo) {
+  i128 c = (i128)(((u128)(uint64_t)c_hi << 64) | c_lo), y = (i128)(((u128)(uint64_t)y_hi << 64) | y_lo);
+  return readout_ask_sum(n, w_c, has_c ? &c : NULL, w_y, has_y ? &y : NULL);
 }
 
 int fbs_oracle_score(const uor_fbs_model *m, const uor_fbs_ext *ext, const uint32_t *rows,
@@ -765,6 +1282,7 @@ int fbs_oracle_score(const uor_fbs_model *m, const uor_fbs_ext *ext, const uint3
   j.out_tokens = out_argmin;
   int status = run_jobs(&j, threads);
   if (out_matches) *out_matches = j.matches;
+  unresolve(&o);
   return status;
 }
 
@@ -808,5 +1326,6 @@ uint32_t fbs_oracle_writer(const uor_fbs_model *m, const uor_fbs_ext *ext, const
   uint64_t c = 0;
   uint32_t t = writer(&o, query, kept, &c);
   if (candidates) *candidates = c;
+  unresolve(&o);
   return t;
 }

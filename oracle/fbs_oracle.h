@@ -51,6 +51,32 @@ int fbs_oracle_score(const uor_fbs_model *m, const uor_fbs_ext *ext, const uint3
                      uint64_t n_rows, uint32_t len, uint32_t *out_argmin,
                      uint64_t *out_matches, int threads);
 
+/* Greedy decode with the Hamming reads' session stream: the session's tokens ([n][context],
+ * the first position of them valid) and the typed reads' payload caches
+ * ([n][typed][context][width], typed = fbs_oracle_hamming_typed), resumed and exported beside the
+ * state as IntegerStackSession keeps them (session.rs:2232-2252). */
+int fbs_oracle_decode_stream(const uor_fbs_model *m, const uor_fbs_ext *ext,
+                             const uint32_t *prompts, uint32_t sequences, uint32_t prompt_len,
+                             uint32_t gen, uint32_t *out_reply, const int64_t *in_state,
+                             const int32_t *in_history, const uint32_t *in_position,
+                             const uint32_t *in_tokens, const int64_t *in_payloads,
+                             int64_t *out_state, int32_t *out_history, uint32_t *out_position,
+                             uint32_t *out_tokens, int64_t *out_payloads, int threads);
+uint32_t fbs_oracle_hamming_typed(const uor_fbs_model *m, const uor_fbs_ext *ext);
+/* One read at row t of tok (the stream read at depth < layers on x, the readout read on n). */
+int fbs_oracle_hamming_row(const uor_fbs_model *m, const uor_fbs_ext *ext, uint32_t depth,
+                           const uint32_t *tok, uint32_t t, int32_t *x, int64_t *n,
+                           int64_t *payloads);
+int fbs_oracle_hamming_codes(const uor_fbs_model *m, const uor_fbs_ext *ext, uint32_t r,
+                             uint64_t *out);
+/* stream_sum / readout_sum / readout_ask_sum (hamming.rs:1918-1953), 128-bit means as hi:lo. */
+int32_t fbs_oracle_stream_sum(int32_t x, int32_t w_c, int64_t c_hi, uint64_t c_lo, int32_t w_y,
+                              int64_t y_hi, uint64_t y_lo);
+int64_t fbs_oracle_readout_sum(int64_t n, int32_t w_c, int has_c, int64_t c_hi, uint64_t c_lo,
+                               int32_t w_y, int64_t y_hi, uint64_t y_lo);
+int64_t fbs_oracle_readout_ask_sum(int64_t n, int32_t w_c, int has_c, int64_t c_hi, uint64_t c_lo,
+                                   int32_t w_y, int has_y, int64_t y_hi, uint64_t y_lo);
+
 /* Scalar routines, exported so the tests can check them against closed forms. */
 int64_t fbs_oracle_shift(int64_t v, int32_t s);
 int64_t fbs_oracle_shift_wide(int64_t hi, uint64_t lo, uint32_t s);

@@ -58,6 +58,20 @@ def lib():
         L.fbs_oracle_rms_norm_fine.argtypes = [P, C.c_uint32, C.c_int64, C.c_int32, P]
         L.fbs_oracle_writer.argtypes = [P, P, P, P, P]
         L.fbs_oracle_writer.restype = C.c_uint32
+        u32, i32, i64, u64 = C.c_uint32, C.c_int32, C.c_int64, C.c_uint64
+        L.fbs_oracle_decode_stream.argtypes = [P, P, P, u32, u32, u32, P, P, P, P, P, P, P, P, P,
+                                               P, P, C.c_int]
+        L.fbs_oracle_hamming_typed.argtypes = [P, P]
+        L.fbs_oracle_hamming_typed.restype = u32
+        L.fbs_oracle_hamming_row.argtypes = [P, P, u32, P, u32, P, P, P]
+        L.fbs_oracle_hamming_codes.argtypes = [P, P, u32, P]
+        L.fbs_oracle_stream_sum.argtypes = [i32, i32, i64, u64, i32, i64, u64]
+        L.fbs_oracle_stream_sum.restype = i32
+        L.fbs_oracle_readout_sum.argtypes = [i64, i32, C.c_int, i64, u64, i32, i64, u64]
+        L.fbs_oracle_readout_sum.restype = i64
+        L.fbs_oracle_readout_ask_sum.argtypes = [i64, i32, C.c_int, i64, u64, i32, C.c_int, i64,
+                                                 u64]
+        L.fbs_oracle_readout_ask_sum.restype = i64
         _lib = L
     return _lib
 
@@ -112,6 +126,88 @@ def decode(art, prompts: np.ndarray, gen: int, threads: int = 1, image: Image | 
                                  _vp(in_history), _vp(in_position), _vp(state), _vp(hist),
                                  _vp(pos), _vp(cand), threads)
     return dict(status=st, reply=reply, state=state, history=hist, position=pos, candidates=cand)
+
+
+def _ext(img):
+    return img.ext_ptr() and C.addressof(img.ext)
+
+
+def hamming_typed(art, image: Image | None = None) -> int:
+    """Typed reads whose payloads a session keeps (ServedHamming::payload_caches)."""
+    img = image or Image(art)
+    return int(lib().fbs_oracle_hamming_typed(C.addressof(img.model), _ext(img)))
+
+
+def decode_stream(art, prompts: np.ndarray, gen: int, threads: int = 1, image: Image | None = None,
+                  resume: dict | None = None):
+    """Oracle greedy decode with the Hamming reads' session stream: dict(status, reply, state,
+    history, position, tokens [S, context], payloads [S, typed, context, width]); `resume` is
+    a dict of the same arrays to continue from."""
+    img = image or Image(art)
+    prompts = np.ascontiguousarray(prompts, dtype=np.uint32)
+    S, plen = prompts.shape
+    s = art.spec
+    typed = hamming_typed(art, img)
+    out = dict(reply=np.zeros((S, gen + 1), np.uint32),
+               state=np.zeros((S, s.layers * s.width), np.int64),
+               history=np.zeros((S, s.layers * s.window * s.width), np.int32),
+               position=np.zeros(S, np.uint32), tokens=np.zeros((S, s.context), np.uint32),
+               payloads=np.zeros((S, typed, s.context, s.width), np.int64))
+    r = resume or {}
+    conv = lambda k, t: None if k not in r else np.ascontiguousarray(r[k], t)  # noqa: E731
+    ins = [conv("state", np.int64), conv("history", np.int32), conv("position", np.uint32),
+           conv("tokens", np.uint32), conv("payloads", np.int64)]
+    st = lib().fbs_oracle_decode_stream(
+        C.addressof(img.model), _ext(img), _vp(prompts), S, plen, gen, _vp(out["reply"]),
+        *[_vp(a) for a in ins], _vp(out["state"]), _vp(out["history"]), _vp(out["position"]),
+        _vp(out["tokens"]), _vp(out["payloads"]), threads)
+    out["status"] = st
+    return out
+
+
+def hamming_row(art, depth: int, tokens, x=None, n=None, payloads=None, image: Image | None = None):
+    """One Hamming read at the last row of `tokens` (the stream read on x at depth < layers, the
+    readout read on n at the layer count), in place; returns (x or n, payloads)."""
+    img = image or Image(art)
+    tok = np.ascontiguousarray(tokens, dtype=np.uint32)
+    s = art.spec
+    typed = hamming_typed(art, img)
+    pay = (np.zeros((typed, s.context, s.width), np.int64) if payloads is None
+           else np.ascontiguousarray(payloads, np.int64))
+    xa = None if x is None else np.ascontiguousarray(x, np.int32).copy()
+    na = None if n is None else np.ascontiguousarray(n, np.int64).copy()
+    st = lib().fbs_oracle_hamming_row(C.addressof(img.model), _ext(img), depth, _vp(tok),
+                                      len(tok) - 1, _vp(xa), _vp(na), _vp(pay))
+    assert st == 0
+    return (xa if x is not None else na), pay
+
+
+def hamming_codes(art, read: int, image: Image | None = None) -> np.ndarray:
+    """Every vocabulary entry's code per head through read `read`'s key rotation."""
+    img = image or Image(art)
+    out = np.zeros((art.spec.vocab, art.hamming.heads), np.uint64)
+    assert lib().fbs_oracle_hamming_codes(C.addressof(img.model), _ext(img), read, _vp(out)) == 0
+    return out
+
+
+def _split128(v: int):
+    v &= (1 << 128) - 1
+    hi = v >> 64
+    return (hi - (1 << 64) if hi >= 1 << 63 else hi), v & ((1 << 64) - 1)
+
+
+def stream_sum(x, w_c, c, w_y, y) -> int:
+    return int(lib().fbs_oracle_stream_sum(x, w_c, *_split128(c), w_y, *_split128(y)))
+
+
+def readout_sum(n, w_c, c, w_y, y) -> int:
+    return int(lib().fbs_oracle_readout_sum(n, w_c, int(c is not None), *_split128(c or 0), w_y,
+                                            *_split128(y)))
+
+
+def readout_ask_sum(n, w_c, c, w_y, y) -> int:
+    return int(lib().fbs_oracle_readout_ask_sum(n, w_c, int(c is not None), *_split128(c or 0),
+                                                w_y, int(y is not None), *_split128(y or 0)))
 
 
 def score(art, rows: np.ndarray, threads: int = 1, image: Image | None = None, want_argmin=True):

@@ -1,0 +1,145 @@
+"""The Hamming reads inside the served step on the GPU (fbs_hamming.h through the C ABI) against
+the oracle, bit for bit: greedy decode replies, exported state and window, teacher-forced
+choices, kept drawers and queries, and a decode split and resumed through the session stream
+(tokens and payload caches, uor_fbs_decode_stream). Cases cover every kernel width (Q = 1, 2, 4
+quaternions a lane), copy, type and ask heads with the question carry, every copy rule with mixed
+copy keys and the reply marker, and a trained artifact with seeded reads added; then the
+refusals of what this build does not serve.
+"""
+
+from dataclasses import replace
+
+import numpy as np
+import pytest
+
+import oracle
+from test_uorlut import HAM, MANIFEST, fixture
+from uor_fbs import synth, uorlut
+from uor_fbs.hip import FbsError, Model
+
+pytestmark = pytest.mark.gpu
+
+H = synth.HammingSpec
+CASES = {
+    # Copy and type heads at a stream read and at the readout.
+    "w64_copy_type": (synth.Spec(vocab=256, width=64, mlp=64, layers=3, context=64, kept=8),
+                      H(heads=4, depths=(1, 3), kept=8), 3, 24, 30),
+    # Ask heads on the readout with the question carry; latest-exact copy heads; 8-wide heads.
+    "w64_ask_carry": (synth.Spec(vocab=256, width=64, mlp=96, layers=3, context=64, kept=8),
+                      H(heads=8, depths=(2, 3), kept=8, asks=(False, True), carry_rows=3,
+                        copy_latest=True), 3, 20, 36),
+    # Width 128, window 8, keyed drawers; mixed copy keys under latest-nearest; three reads.
+    "w128_rules": (replace(synth.CONFIGS["c2"], layers=3, context=64),
+                   H(heads=8, depths=(1, 2, 3), kept=16, copy_keys=(1, 2, 1, 2), rule=2), 4, 24, 32),
+    # Width 256 (C3's shape, Zipf drawers): the longest rule after the reply marker.
+    "w256_marker": (replace(synth.CONFIGS["c3"], layers=2, context=64),
+                    H(heads=8, depths=(1, 2), kept=16, copy_latest=True, copy_longest=(3, 5)),
+                    3, 24, 30),
+    # Width 512 (two quaternions a lane), int8 table, asking stream read and typed readout.
+    "w512": (replace(synth.CONFIGS["c5"], layers=2, context=48, vocab=4096),
+             H(heads=16, depths=(1, 2), kept=8, asks=(True, False)), 2, 16, 24),
+    # Width 1024 (four quaternions a lane), 64-coordinate heads, longest-exact.
+    "w1024": (synth.Spec(vocab=512, width=1024, mlp=256, layers=2, context=40, kept=8),
+              H(heads=16, depths=(1, 2), kept=12, rule=3), 2, 12, 20),
+}
+
+
+def build(name):
+    spec, ham, n, plen, gen = CASES[name]
+    art = synth.make_artifact(replace(spec, hamming=ham), 500 + list(CASES).index(name))
+    prompts = synth.uniform_prompts(spec.vocab, n, plen, 77) % 16  # repeats for the heads
+    if name == "w256_marker":
+        prompts[:, 6:8] = (3, 5)
+    return art, prompts.astype(np.uint32), gen
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_decode_matches_the_oracle(name):
+    art, prompts, gen = build(name)
+    print(f"case {name} prompts {prompts.shape} gen {gen}", flush=True)
+    model = Model(art)
+    assert model.block_waves(len(prompts)) == 1
+    got = model.decode(prompts, gen)
+    want = oracle.decode(art, prompts, gen, threads=4)
+    assert want["status"] == 0
+    for k in ("reply", "state", "history", "position"):
+        np.testing.assert_array_equal(got[k], want[k], err_msg=f"{name} {k}")
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_sequences_match_the_oracle(name):
+    art, prompts, gen = build(name)
+    rows = np.concatenate([prompts, prompts[:, ::-1]], 1)[:, : art.spec.context]
+    print(f"case {name} rows {rows.shape}", flush=True)
+    tok, kept, query = Model(art).sequences(rows)
+    st, t2, k2, q2 = oracle.sequences(art, rows, threads=4)
+    assert st == 0
+    np.testing.assert_array_equal(tok, t2)
+    np.testing.assert_array_equal(kept, k2)
+    np.testing.assert_array_equal(query, q2)
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_a_resumed_stream_matches_the_oracle(name):
+    art, prompts, gen = build(name)
+    print(f"case {name} stream", flush=True)
+    model = Model(art)
+    first = model.decode_stream(prompts, gen // 2)
+    want = oracle.decode_stream(art, prompts, gen // 2, threads=4)
+    pos = int(want["position"][0])
+    np.testing.assert_array_equal(first["reply"], want["reply"])
+    np.testing.assert_array_equal(first["tokens"][:, :pos], want["tokens"][:, :pos])
+    np.testing.assert_array_equal(first["payloads"][:, :, :pos], want["payloads"][:, :, :pos])
+    again = model.decode_stream(first["reply"][:, -1:], gen - gen // 2 - 1, resume=first)
+    want2 = oracle.decode_stream(art, want["reply"][:, -1:], gen - gen // 2 - 1, threads=4,
+                                 resume=want)
+    whole = oracle.decode(art, prompts, gen, threads=4)
+    np.testing.assert_array_equal(again["reply"], want2["reply"])
+    np.testing.assert_array_equal(again["reply"], whole["reply"][:, gen // 2 + 1:])
+    for k in ("state", "history", "position"):
+        np.testing.assert_array_equal(again[k], whole[k], err_msg=k)
+    pos = int(whole["position"][0])
+    np.testing.assert_array_equal(again["tokens"][:, :pos], want2["tokens"][:, :pos])
+    np.testing.assert_array_equal(again["payloads"][:, :, :pos], want2["payloads"][:, :, :pos])
+
+
+def test_a_trained_artifact_with_reads_matches_the_oracle():
+    _, data, _ = fixture(sorted(MANIFEST)[0])
+    reads = synth.hamming_reads(uorlut.load(data).spec, HAM, 7)
+    art = uorlut.load(uorlut.add_hamming(data, HAM, reads))
+    prompts = ((np.arange(2 * 40, dtype=np.uint32).reshape(2, 40) * 37) % 60).astype(np.uint32)
+    print("case trained+hamming", flush=True)
+    got = Model(art).decode(prompts, 40)
+    want = oracle.decode(art, prompts, 40, threads=4)
+    for k in ("reply", "state", "history", "position"):
+        np.testing.assert_array_equal(got[k], want[k], err_msg=k)
+
+
+def test_refusals():
+    art, prompts, gen = build("w64_copy_type")
+    model = Model(art)
+    first = model.decode(prompts, 2)
+    with pytest.raises(FbsError) as e:  # resuming without the stream
+        model.decode(prompts[:, :1], 2, in_state=first["state"], in_history=first["history"],
+                     in_position=first["position"])
+    assert e.value.code == 6
+    bad = synth.make_artifact(replace(CASES["w64_copy_type"][0], hamming=H(heads=4, depths=(1, 3), kept=65)), 1)
+    with pytest.raises(FbsError) as e:
+        Model(bad)
+    assert e.value.code == 6
+    bad.hamming_reads[0].margin[1] = 0
+    bad.hamming = replace(bad.hamming, kept=8)
+    with pytest.raises(FbsError) as e:
+        Model(bad)
+    assert e.value.code == 4
+
+
+def test_a_resumed_token_outside_the_vocabulary_is_refused():
+    art, prompts, _ = build("w64_copy_type")
+    model = Model(art)
+    first = model.decode_stream(prompts, 3)
+    bad = dict(first, tokens=first["tokens"].copy())
+    bad["tokens"][1, 2] = art.spec.vocab
+    with pytest.raises(FbsError) as e:
+        model.decode_stream(first["reply"][:, -1:], 2, resume=bad)
+    assert e.value.code == 1

@@ -14,7 +14,7 @@ import pytest
 
 import oracle
 from conftest import GOLDEN
-from uor_fbs import uorlut
+from uor_fbs import synth, uorlut
 
 TRAINED = os.path.join(GOLDEN, "trained")
 MANIFEST = json.load(open(os.path.join(TRAINED, "manifest.json")))
@@ -128,3 +128,107 @@ def test_every_trained_artifact_in_the_reference_loads():
     for f in files:
         art = uorlut.load(f)
         assert art.spec.width == 256 and art.spec.layers == 6
+
+
+# ---- Hamming reads (lut-stack/6, and /7 or /8 with a `hamming` record) ---------------------
+# No container the reference holds has Hamming reads, so they are added to a trained fixture
+# (uorlut.add_hamming, as the reference's section adders append, format.rs:2730-2783) with
+# seeded reads; the reader's refusals follow StackHamming::check (format.rs:336-430) and
+# hamming_image (hamming.rs:58-110).
+
+HAM = synth.HammingSpec(heads=8, depths=(2, 6), kept=16, asks=(False, True), carry_rows=4)
+
+
+def hamming_fixture(h=HAM):
+    _, data, _ = fixture(sorted(MANIFEST)[0])
+    reads = synth.hamming_reads(uorlut.load(data).spec, h, 7)
+    return data, uorlut.add_hamming(data, h, reads), reads
+
+
+def test_hamming_reads_load_as_added():
+    data, added, reads = hamming_fixture()
+    art = uorlut.load(added)
+    assert json.loads(added[16:16 + struct.unpack("<Q", added[8:16])[0]])["schema"] == "uor-r4.lut-stack/7"
+    h = art.hamming
+    assert (h.heads, h.depths, h.kept, h.asks, h.carry_rows, h.copy_key) == (8, (2, 6), 16, (False, True), 4, 1)
+    for a, b in zip(art.hamming_reads, reads):
+        assert a.depth == b.depth
+        for part in ("query_rotation", "key_rotation", "value_rotation", "margin", "weight", "ask", "carry"):
+            x, y = getattr(a, part), getattr(b, part)
+            assert (x is None) == (y is None) and (x is None or np.array_equal(x, y)), part
+    # The reads change what the model decodes (the oracle, a few steps).
+    plain = uorlut.load(data)
+    prompts = (np.arange(24, dtype=np.uint32).reshape(2, 12) * 37) % 50
+    assert not np.array_equal(oracle.decode(art, prompts, 6)["reply"], oracle.decode(plain, prompts, 6)["reply"])
+
+
+def test_a_stack_without_memory_names_schema_6():
+    _, data, _ = fixture(sorted(MANIFEST)[0])
+    header, body = _split(data)
+    del header["memory"]
+    header["schema"] = "uor-r4.lut-stack/5"
+    plain = _build(header, body)
+    uorlut.load(plain)
+    reads = synth.hamming_reads(uorlut.load(plain).spec, HAM, 3)
+    added = uorlut.add_hamming(plain, HAM, reads)
+    assert _split(added)[0]["schema"] == "uor-r4.lut-stack/6"
+    assert uorlut.load(added).hamming.depths == (2, 6)
+
+
+@pytest.mark.parametrize("case", [
+    "place", "unknown", "missing_field", "exponent", "depth_zero", "depth_order", "depth_past",
+    "odd_heads", "wide_heads", "copy_keys_equal", "longest_without_latest", "kept_zero",
+    "asks_all_off", "carry_without_ask", "carry_reach", "ask_unnamed", "ask_missing",
+    "margin_zero", "section_length", "schema_6_with_memory"])
+def test_refuses_malformed_hamming_reads(case):
+    _, added, _ = hamming_fixture()
+
+    def edit(h, body):
+        r = h["hamming"]
+        if case == "place":
+            r["place"] = {"stop": [1], "arm": [2], "open": [3]}
+        elif case == "unknown":
+            r["bogus"] = 1
+        elif case == "missing_field":
+            del r["kept"]
+        elif case == "exponent":
+            r["margin_exp"] = -15
+        elif case == "depth_zero":
+            r["depths"] = [0, 6]
+        elif case == "depth_order":
+            r["depths"] = [6, 2]
+        elif case == "depth_past":
+            r["depths"] = [2, 7]
+        elif case == "odd_heads":
+            r["heads"] = 7
+        elif case == "wide_heads":
+            r["heads"] = 2  # 128 coordinates a head
+        elif case == "copy_keys_equal":
+            r["copy_keys"] = [1, 1, 1, 1]
+        elif case == "longest_without_latest":
+            r["copy_longest"] = [1, 2]
+        elif case == "kept_zero":
+            r["kept"] = 0
+        elif case == "asks_all_off":
+            r["asks"] = [False, False]
+            del r["carry_rows"]
+        elif case == "carry_without_ask":
+            r["asks"] = [True, False]
+        elif case == "carry_reach":
+            r["carry_rows"] = 4097
+        elif case == "ask_unnamed":
+            del r["asks"]
+            del r["carry_rows"]
+        elif case == "ask_missing":
+            h["tables"] = [t for t in h["tables"] if t["name"] != "hamming.d6.ask"]
+        elif case == "margin_zero":
+            off = _table(h, "hamming.d2.margin")["span"]["offset"]
+            body[off:off + 4] = struct.pack("<i", 0)
+        elif case == "section_length":
+            t = _table(h, "hamming.d2.weight")
+            t["len"] -= 1
+            t["span"]["bytes"] -= 4
+        elif case == "schema_6_with_memory":
+            h["schema"] = "uor-r4.lut-stack/6"
+    with pytest.raises(uorlut.UorlutError):
+        uorlut.load(_mutant(added, edit))

@@ -75,6 +75,9 @@ struct uor_fbs_handle {
   int32_t *ring = nullptr;
   int64_t *hist = nullptr;
   size_t ring_blocks = 0;
+  // Hamming models: the type heads' payload caches of sequences whose caller takes none out.
+  int64_t *pay = nullptr;
+  size_t pay_blocks = 0;
   // This device's copy of the allocation-free decode's scratch array (null if its address could
   // not be read; that entry point then refuses).
   unsigned char *scratch = nullptr;
@@ -86,7 +89,22 @@ struct uor_fbs_handle {
     for (void *p : allocs) (void)hipFree(p);
     if (ring) (void)hipFree(ring);
     if (hist) (void)hipFree(hist);
+    if (pay) (void)hipFree(pay);
     (void)hipSetDevice(prev);
+  }
+
+  // Payload words (i64) one session keeps: slots x context x d.
+  size_t payload_words() const { return (size_t)M.ham.slots * M.context * M.d; }
+
+  int ensure_pay(size_t blocks) {
+    if (blocks <= pay_blocks) return 0;
+    if (pay) (void)hipFree(pay);
+    pay = nullptr;
+    pay_blocks = 0;
+    hipError_t e = hipMalloc((void **)&pay, blocks * payload_words() * sizeof(int64_t));
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(payload caches)");
+    pay_blocks = blocks;
+    return 0;
   }
 
   template <class T>
@@ -195,6 +213,73 @@ int check_codes(const int16_t *codes, size_t n, const char *name, uint32_t layer
   return 0;
 }
 
+// The Hamming record and its reads, as the reference's loader refuses them
+// (StackHamming::check, format.rs:336-430; hamming_image and AskImage::checked, hamming.rs:58-110,
+// 1069-1095; check_payload_cache :1538-1549), and this build's own limits: a head keeps at most
+// kMaxHamKept positions and positions fit 24 bits.
+int check_hamming(const uor_fbs_model *m, const uor_fbs_hamming &hm) {
+  const uint32_t d = m->width, heads = hm.heads;
+  if (heads < 2 || heads % 2 || d % heads)
+    return fail(UOR_FBS_ERR_SHAPE, "hamming: %u heads: an even count of at least 2 dividing the width", heads);
+  const uint32_t hw = d / heads;
+  if (hw % 4 || hw > 64)
+    return fail(UOR_FBS_ERR_SHAPE, "hamming: heads of %u coordinates: whole 4-lane blocks, at most 64", hw);
+  if (hm.copy_key != 1 && hm.copy_key != 2)
+    return fail(UOR_FBS_ERR_SHAPE, "hamming: copy key %u names 1 or 2 tokens", hm.copy_key);
+  bool any2 = hm.copy_key == 2, all_one = hm.copy_key == 1;
+  if (hm.copy_keys) {
+    bool differ = false;
+    for (uint32_t k = 0; k < heads / 2; k++) {
+      const uint32_t key = hm.copy_keys[k];
+      if (key != 1 && key != 2) return fail(UOR_FBS_ERR_SHAPE, "hamming: copy key %u names 1 or 2 tokens", key);
+      differ |= key != hm.copy_keys[0];
+      any2 |= key == 2;
+      all_one &= key == 1;
+    }
+    if (hm.copy_key != 1 || !differ)
+      return fail(UOR_FBS_ERR_SHAPE, "hamming: mixed copy keys differ and leave copy_key at 1");
+  }
+  if (any2 && hw % 8)
+    return fail(UOR_FBS_ERR_SHAPE, "hamming: copy key 2 needs heads of whole 8-coordinate blocks");
+  if (hm.copy_longest && (!hm.copy_latest || !all_one || hm.marker[0] >= m->vocab || hm.marker[1] >= m->vocab))
+    return fail(UOR_FBS_ERR_SHAPE,
+                "hamming: the longest rule needs the latest exact rule, one-token copy keys and a "
+                "marker of two vocabulary ids");
+  if (hm.rule != UOR_FBS_COPY_ARTIFACT && hm.rule > UOR_FBS_COPY_LONGEST_AFTER_OPENING)
+    return fail(UOR_FBS_ERR_ARGUMENT, "hamming: copy rule %u", hm.rule);
+  if (hm.kept == 0) return fail(UOR_FBS_ERR_SHAPE, "hamming: a read keeps at least one position");
+  if (hm.kept > kMaxHamKept)
+    return fail(UOR_FBS_ERR_UNSUPPORTED, "hamming: %u kept positions (this build keeps at most %u)", hm.kept,
+                kMaxHamKept);
+  if (m->context >= (1u << kHamPosBits))
+    return fail(UOR_FBS_ERR_UNSUPPORTED, "hamming: context %u past 2^24 - 1", m->context);
+  if (hm.read_count == 0 || !hm.reads) return fail(UOR_FBS_ERR_SHAPE, "hamming: no reads");
+  uint64_t typed = 0;
+  for (uint32_t i = 0; i < hm.read_count; i++) {
+    const uor_fbs_hamming_read &r = hm.reads[i];
+    if (r.depth < 1 || r.depth > m->layer_count || (i && r.depth <= hm.reads[i - 1].depth))
+      return fail(UOR_FBS_ERR_SHAPE, "hamming: read depths strictly increase from 1 to the layer count");
+    if (!r.query_rotation || !r.key_rotation || !r.value_rotation || !r.margin || !r.weight)
+      return fail(UOR_FBS_ERR_ARGUMENT, "hamming.d%u: null table", r.depth);
+    for (uint32_t k = 0; k < heads; k++)
+      if (r.margin[k] <= 0) return fail(UOR_FBS_ERR_SHAPE, "hamming.d%u.margin: a margin is not positive", r.depth);
+    const bool last = i + 1 == hm.read_count;
+    if (r.carry_rows || r.carry) {
+      if (!last || r.depth != m->layer_count)
+        return fail(UOR_FBS_ERR_SHAPE, "hamming: a question carry is served on the readout read only");
+      if (!r.ask) return fail(UOR_FBS_ERR_SHAPE, "hamming: a question carry needs its read to ask");
+      if (!r.carry || r.carry_rows == 0 || r.carry_rows > (1u << 12))
+        return fail(UOR_FBS_ERR_SHAPE, "hamming: a question carry reaches 1 to 4096 rows with its gains");
+    }
+    bool ty = false;
+    for (uint32_t c = 0; c < d; c++) ty |= r.weight[d + c] != 0;
+    typed += ty && !r.ask;
+  }
+  if (typed * m->context * d * 8 > (1ull << 32))
+    return fail(UOR_FBS_ERR_SHAPE, "hamming: the payload caches exceed 4 GiB a session");
+  return 0;
+}
+
 int validate(const uor_fbs_model *m, const uor_fbs_ext *e, Resolved *r) {
   if (!m) return fail(UOR_FBS_ERR_ARGUMENT, "null model");
   const uint32_t d = m->width, mlp = m->mlp;
@@ -259,6 +344,7 @@ int validate(const uor_fbs_model *m, const uor_fbs_ext *e, Resolved *r) {
       if (e->drawer_members[i] >= m->vocab)
         return fail(UOR_FBS_ERR_SHAPE, "drawer member %u outside the vocabulary", e->drawer_members[i]);
   }
+  if (e && e->hamming && (st = check_hamming(m, *e->hamming))) return st;
   return 0;
 }
 
@@ -267,6 +353,87 @@ uint16_t prog_word(const uor_fbs_map &mp, uint32_t o) {
   uint8_t code = mp.codes[o];
   uint32_t src = 8u * mp.atoms[o / 8] + (code & 7u);
   return (uint16_t)(2 * src + ((code >> 3) & 1u));
+}
+
+}  // namespace
+
+namespace {
+
+// The served reads (ServedHamming::new, hamming.rs:1571-1609, with CopyHeads::new :287-313 and
+// TypeHeads::new :1130-1145): each read's three rotations as unit quaternions at Q31 (`units`
+// :541-548, stack_rotation at lambda 2^31 and epsilon 0), every vocabulary entry's key code per
+// head through the key rotation (`head_code`, `vocab_codes` :550-582), the copy heads' pair masks
+// and rule, and the payload cache slot of each typed read that does not ask.
+int upload_hamming(uor_fbs_handle *h, const uor_fbs_model *m, const uor_fbs_ext &e,
+                   const uor_fbs_hamming &hm) {
+  DevModel &M = h->M;
+  DevHam &H = M.ham;
+  const uint32_t d = m->width, V = m->vocab, heads = hm.heads, hw = d / heads;
+  H.heads = heads;
+  H.copy = heads / 2;
+  H.hw = hw;
+  H.kept = hm.kept;
+  H.rule = hm.rule != UOR_FBS_COPY_ARTIFACT ? hm.rule
+           : hm.copy_longest                ? UOR_FBS_COPY_LONGEST_AFTER_OPENING
+           : hm.copy_latest                 ? UOR_FBS_COPY_LATEST_EXACT
+                                            : UOR_FBS_COPY_MEAN;
+  H.has_marker = hm.copy_longest != 0;
+  H.m0 = hm.marker[0];
+  H.m1 = hm.marker[1];
+  std::vector<uint64_t> pair(H.copy);
+  for (uint32_t k = 0; k < H.copy; k++) {
+    const uint32_t key = hm.copy_keys ? hm.copy_keys[k] : hm.copy_key;
+    pair[k] = key == 2 ? (1ull << (hw / 2)) - 1 : 0;
+  }
+  std::vector<int32_t> at(M.L + 1, -1);
+  std::vector<DevHamRead> reads(hm.read_count);
+  // The writer table's value of token v, channel c, at Q12: what the reads see.
+  auto row_q12 = [&](uint32_t v, uint32_t c) -> int64_t {
+    const size_t i = (size_t)v * d + c;
+    return e.table_i8 ? (int64_t)e.table_i8[i] * (1 << e.table_shift) : m->writer_table[i];
+  };
+  int st;
+  for (uint32_t i = 0; i < hm.read_count; i++) {
+    const uor_fbs_hamming_read &r = hm.reads[i];
+    DevHamRead &R = reads[i];
+    at[r.depth] = (int32_t)i;
+    std::vector<int64_t> units[3];
+    const int32_t *raw[3] = {r.query_rotation, r.key_rotation, r.value_rotation};
+    for (int k = 0; k < 3; k++) {
+      units[k].resize(d);
+      for (uint32_t q = 0; q < d / 4; q++) rotation(raw[k] + 4 * q, 1ull << 31, kGateEps, units[k].data() + 4 * q);
+    }
+    const int64_t **dst[3] = {&R.qu, &R.ku, &R.vu};
+    for (int k = 0; k < 3; k++)
+      if ((st = h->upload(units[k].data(), d, dst[k]))) return st;
+    std::vector<uint64_t> codes((size_t)V * heads, 0);
+    for (uint32_t v = 0; v < V; v++)
+      for (uint32_t q = 0; q < d / 4; q++) {
+        int64_t p[4];
+        for (int c = 0; c < 4; c++) p[c] = row_q12(v, 4 * q + c);
+        i128 o[4];
+        hamilton64(units[1].data() + 4 * q, p, o);
+        const uint32_t head = 4 * q / hw, bit = 4 * q % hw;
+        for (int c = 0; c < 4; c++)
+          if (o[c] >= 0) codes[(size_t)v * heads + head] |= 1ull << (bit + c);
+      }
+    if ((st = h->upload(codes.data(), codes.size(), &R.codes))) return st;
+    if ((st = h->upload(r.margin, heads, &R.margin))) return st;
+    if ((st = h->upload(r.weight, 2 * (size_t)d, &R.w))) return st;
+    R.ask = nullptr;
+    R.carry = nullptr;
+    if (r.ask && (st = h->upload(r.ask, (size_t)V * d, &R.ask))) return st;
+    if (r.carry && (st = h->upload(r.carry, V, &R.carry))) return st;
+    R.carry_rows = r.carry ? r.carry_rows : 0;
+    R.typed = 0;
+    for (uint32_t c = 0; c < d; c++) R.typed |= r.weight[d + c] != 0;
+    R.slot = R.typed && !r.ask ? H.slots++ : kHamNoSlot;
+    R.pad = 0;
+  }
+  if ((st = h->upload(pair.data(), pair.size(), &H.pair))) return st;
+  if ((st = h->upload(at.data(), at.size(), &H.at))) return st;
+  if ((st = h->upload(reads.data(), reads.size(), &H.reads))) return st;
+  return 0;
 }
 
 }  // namespace
@@ -449,10 +616,12 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
   if ((st = h->upload(m->keep_q31, 16, &M.keep_q31))) return done(st);
   if ((st = h->upload(eps_int, 9, &M.eps_int))) return done(st);
 
+  if (e && e->hamming && (st = upload_hamming(h, m, *e, *e->hamming))) return done(st);
+
   hipDeviceProp_t prop;
   he = hipGetDeviceProperties(&prop, device);
   if (he != hipSuccess) return done(hip_fail(he, "hipGetDeviceProperties"));
-  h->lds_bytes = fbs::lds_bytes(M);
+  h->lds_bytes = fbs::lds_bytes(M) + fbs::ham_lds_bytes(M);
   if (h->lds_bytes > prop.sharedMemPerBlock)
     return done(fail(UOR_FBS_ERR_UNSUPPORTED, "%zu bytes of LDS per sequence exceed %zu",
                      h->lds_bytes, (size_t)prop.sharedMemPerBlock));
@@ -460,7 +629,7 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
   // UOR_FBS_BLOCK_WAVES=1 fixes one wavefront per sequence (default: paired blocks).
   const char *bw = getenv("UOR_FBS_BLOCK_WAVES");
   h->pair_lds = fbs::pair_lds_bytes(M);
-  h->pair = !(bw && bw[0] == '1' && !bw[1]) && h->pair_lds <= prop.sharedMemPerBlock;
+  h->pair = !(bw && bw[0] == '1' && !bw[1]) && h->pair_lds <= prop.sharedMemPerBlock && !M.ham.heads;
   h->pair_grid = (uint32_t)prop.multiProcessorCount * 4;  // four SIMDs per CU
   return done(0);
 }
@@ -488,6 +657,20 @@ int launch(uor_fbs_handle *h, RunArgs &A, hipStream_t stream, bool noalloc = fal
   const bool pair = h->pair;
   const uint32_t cap = pair ? h->pair_grid : h->max_grid;
   uint32_t grid = A.n < cap ? A.n : cap;
+  if (noalloc && h->M.ham.heads)
+    return fail(UOR_FBS_ERR_UNSUPPORTED,
+                "the allocation-free decode serves no Hamming reads (their token streams and payload "
+                "caches are the caller's: uor_fbs_decode_stream_async)");
+  if (h->M.ham.slots && !A.out_payloads) {
+    // The library's payload caches, one per resident block, within 16 GiB (blocks loop over
+    // their sequences).
+    const size_t per = h->payload_words() * sizeof(int64_t), fit = ((size_t)16 << 30) / per;
+    if (fit == 0) return fail(UOR_FBS_ERR_UNSUPPORTED, "one session's payload caches exceed 16 GiB");
+    grid = grid < fit ? grid : (uint32_t)fit;
+    int st = h->ensure_pay(grid);
+    if (st) return st;
+    A.pay = h->pay;
+  }
   if (noalloc) {
     if (!h->scratch)
       return fail(UOR_FBS_ERR_DEVICE, "the scratch array's device address could not be read");
@@ -558,6 +741,13 @@ int first_status(const std::vector<int32_t> &status) {
   return 0;
 }
 
+// A Hamming model's session reads its earlier tokens (and payloads): resuming one needs them.
+int refuse_streamless() {
+  return fail(UOR_FBS_ERR_UNSUPPORTED,
+              "a Hamming model resumes a session only with its token stream "
+              "(uor_fbs_decode_stream_async)");
+}
+
 struct DeviceScope {
   int prev = 0;
   explicit DeviceScope(int dev) {
@@ -620,6 +810,7 @@ extern "C" int uor_fbs_decode_async(uor_fbs_handle *h, const uint32_t *prompts, 
                                     void *stream) {
   if (!h || !prompts || !out_reply || !status) return fail(UOR_FBS_ERR_ARGUMENT, "null argument");
   if (prompt_len == 0) return fail(UOR_FBS_ERR_ARGUMENT, "a decode needs at least one prompt token");
+  if (in_position && h->M.ham.heads) return refuse_streamless();
   DeviceScope scope(h->device);
   RunArgs A{};
   A.mode = kModeDecode;
@@ -646,6 +837,7 @@ extern "C" int uor_fbs_decode_noalloc_async(uor_fbs_handle *h, const uint32_t *p
                                             uint32_t *out_position, int32_t *status, void *stream) {
   if (!h || !prompts || !out_reply || !status) return fail(UOR_FBS_ERR_ARGUMENT, "null argument");
   if (prompt_len == 0) return fail(UOR_FBS_ERR_ARGUMENT, "a decode needs at least one prompt token");
+  if (in_position && h->M.ham.heads) return refuse_streamless();
   DeviceScope scope(h->device);
   RunArgs A{};
   A.mode = kModeDecode;
@@ -673,6 +865,9 @@ extern "C" int uor_fbs_decode_slots_async(uor_fbs_handle *h, const uint32_t *slo
   if (!h || !slots || !prompts || !out_reply || !state || !history || !position || !status)
     return fail(UOR_FBS_ERR_ARGUMENT, "null argument");
   if (prompt_len == 0) return fail(UOR_FBS_ERR_ARGUMENT, "a step needs at least one token");
+  if (h->M.ham.heads)
+    return fail(UOR_FBS_ERR_UNSUPPORTED,
+                "session slots serve no Hamming reads yet (uor_fbs_decode_stream_async resumes them)");
   DeviceScope scope(h->device);
   RunArgs A{};
   A.mode = kModeDecode;
@@ -729,6 +924,95 @@ extern "C" int uor_fbs_decode(uor_fbs_handle *h, const uint32_t *prompts, uint32
       (st = copy_out(out_state, dos, sequences * sw)) ||
       (st = copy_out(out_history, doh, sequences * hw)) ||
       (st = copy_out(out_position, dop, sequences)))
+    return st;
+  return first_status(status);
+}
+
+extern "C" uint64_t uor_fbs_stream_words(const uor_fbs_handle *h) {
+  return h && h->M.ham.heads ? h->M.context : 0;
+}
+extern "C" uint64_t uor_fbs_payload_words(const uor_fbs_handle *h) {
+  return h && h->M.ham.heads ? h->payload_words() : 0;
+}
+
+extern "C" int uor_fbs_decode_stream_async(
+    uor_fbs_handle *h, const uint32_t *prompts, uint32_t sequences, uint32_t prompt_len,
+    uint32_t gen, uint32_t *out_reply, const int64_t *in_state, const int32_t *in_history,
+    const uint32_t *in_position, const uint32_t *in_stream, const int64_t *in_payloads,
+    int64_t *out_state, int32_t *out_history, uint32_t *out_position, uint32_t *out_stream,
+    int64_t *out_payloads, int32_t *status, void *stream) {
+  if (!h || !prompts || !out_reply || !status) return fail(UOR_FBS_ERR_ARGUMENT, "null argument");
+  if (prompt_len == 0) return fail(UOR_FBS_ERR_ARGUMENT, "a decode needs at least one prompt token");
+  if (in_position && h->M.ham.heads && (!in_stream || (h->M.ham.slots && !in_payloads)))
+    return fail(UOR_FBS_ERR_ARGUMENT, "a resumed session needs its token stream%s",
+                h->M.ham.slots ? " and payload caches" : "");
+  DeviceScope scope(h->device);
+  RunArgs A{};
+  A.mode = kModeDecode;
+  A.n = sequences;
+  A.len = prompt_len;
+  A.gen = gen;
+  A.tokens = prompts;
+  A.out_tokens = out_reply;
+  A.in_state = in_state;
+  A.in_history = in_history;
+  A.in_position = in_position;
+  A.out_state = out_state;
+  A.out_history = out_history;
+  A.out_position = out_position;
+  A.status = status;
+  if (h->M.ham.heads) {
+    A.in_stream = in_stream;
+    A.out_stream = out_stream;
+    A.in_payloads = h->M.ham.slots ? in_payloads : nullptr;
+    A.out_payloads = h->M.ham.slots ? out_payloads : nullptr;
+  }
+  return launch(h, A, (hipStream_t)stream);
+}
+
+extern "C" int uor_fbs_decode_stream(uor_fbs_handle *h, const uint32_t *prompts, uint32_t sequences,
+                                     uint32_t prompt_len, uint32_t gen, uint32_t *out_reply,
+                                     const int64_t *in_state, const int32_t *in_history,
+                                     const uint32_t *in_position, const uint32_t *in_stream,
+                                     const int64_t *in_payloads, int64_t *out_state,
+                                     int32_t *out_history, uint32_t *out_position,
+                                     uint32_t *out_stream, int64_t *out_payloads) {
+  if (!h || !prompts || !out_reply) return fail(UOR_FBS_ERR_ARGUMENT, "null argument");
+  if (prompt_len == 0) return fail(UOR_FBS_ERR_ARGUMENT, "a decode needs at least one prompt token");
+  if (sequences == 0) return 0;
+  DeviceScope scope(h->device);
+  const size_t sw = uor_fbs_state_words(h), hw = uor_fbs_history_words(h);
+  const size_t tw = uor_fbs_stream_words(h), pw = uor_fbs_payload_words(h);
+  DevBuf b;
+  uint32_t *dp, *dr, *dip = nullptr, *dop = nullptr, *dit = nullptr, *dot = nullptr;
+  int64_t *dis = nullptr, *dos = nullptr, *dipl = nullptr, *dopl = nullptr;
+  int32_t *dih = nullptr, *doh = nullptr, *ds;
+  int st;
+  if ((st = b.in(&dp, prompts, (size_t)sequences * prompt_len)) ||
+      (st = b.alloc(&dr, (size_t)sequences * (gen + 1))) || (st = b.alloc(&ds, sequences)) ||
+      (st = b.in(&dis, in_state, sequences * sw)) || (st = b.in(&dih, in_history, sequences * hw)) ||
+      (st = b.in(&dip, in_position, sequences)) ||
+      (tw && (st = b.in(&dit, in_stream, sequences * tw))) ||
+      (pw && (st = b.in(&dipl, in_payloads, sequences * pw))))
+    return st;
+  if (out_state && (st = b.alloc(&dos, sequences * sw))) return st;
+  if (out_history && (st = b.alloc(&doh, sequences * hw))) return st;
+  if (out_position && (st = b.alloc(&dop, sequences))) return st;
+  if (out_stream && tw && (st = b.alloc(&dot, sequences * tw))) return st;
+  if (out_payloads && pw && (st = b.alloc(&dopl, sequences * pw))) return st;
+  if ((st = uor_fbs_decode_stream_async(h, dp, sequences, prompt_len, gen, dr, dis, dih, dip, dit,
+                                        dipl, dos, doh, dop, dot, dopl, ds, nullptr)))
+    return st;
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_fail(e, "kernel");
+  std::vector<int32_t> status(sequences);
+  if ((st = copy_out(status.data(), ds, sequences)) ||
+      (st = copy_out(out_reply, dr, (size_t)sequences * (gen + 1))) ||
+      (st = copy_out(out_state, dos, sequences * sw)) ||
+      (st = copy_out(out_history, doh, sequences * hw)) ||
+      (st = copy_out(out_position, dop, sequences)) ||
+      (st = copy_out(out_stream, dot, sequences * tw)) ||
+      (st = copy_out(out_payloads, dopl, sequences * pw)))
     return st;
   return first_status(status);
 }

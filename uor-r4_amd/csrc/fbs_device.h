@@ -45,6 +45,38 @@ struct DevLayer {
   const uint16_t *mlp_gain_desc;
 };
 
+// The Hamming reads of a lut-stack/6 stack (fbs_hamming.h), one entry per read. Every table is
+// the host's: the three rotations' unit quaternions at Q31 (`units`, hamming.rs:541-548) and
+// each vocabulary entry's key code per head (`vocab_codes`, :566-582), copy heads first.
+constexpr uint32_t kMaxHamKept = 64;        // positions a head keeps
+constexpr uint32_t kHamPosBits = 24;        // positions below 2^24 (a pick packs its distance above)
+constexpr uint32_t kHamNoSlot = 0xffffffffu;
+
+struct DevHamRead {
+  const int64_t *qu, *ku, *vu;  // d each: query, key and value units
+  const uint64_t *codes;        // vocab * heads
+  const int32_t *margin;        // heads, bits at Q16
+  const int32_t *w;             // 2 d at 2^-24: w_c, then w_y
+  const int16_t *ask;           // vocab * d question table (Q12), or null: the read does not ask
+  const int32_t *carry;         // vocab carry gains (Q16), or null
+  uint32_t carry_rows;          // the carry's reach
+  uint32_t typed;               // type heads served (some w_y is not zero)
+  uint32_t slot;                // payload cache of a typed read that does not ask, else kHamNoSlot
+  uint32_t pad;
+};
+
+struct DevHam {
+  uint32_t heads;               // 0: the model has no Hamming reads
+  uint32_t copy, hw, kept;      // heads / 2 copy heads, d / heads coordinates a head
+  uint32_t rule;                // the copy rule served (UOR_FBS_COPY_*, resolved)
+  uint32_t has_marker, m0, m1;  // the longest rule's reply marker
+  uint32_t slots;               // payload caches a session keeps
+  uint32_t pad;
+  const uint64_t *pair;         // copy: a copy key 2 head's first-half mask, else 0
+  const int32_t *at;            // L + 1: the read index at each depth, or -1
+  const DevHamRead *reads;
+};
+
 struct DevModel {
   uint32_t vocab, d, m, L, W, D, P, head, context, raw_gates, raw_transition;
   uint32_t nq, nm, mpl, qpl;
@@ -65,6 +97,7 @@ struct DevModel {
   const int8_t *icosian;    // 120 * 8
   const uint64_t *keep_q31; // 16
   const int64_t *eps_int;   // 9: the RMSNorm epsilon at each pre-shift 0..8
+  DevHam ham;
 };
 
 // LDS bytes per block (the layout the kernels carve): the gather crossbar, the MLP outputs, the
@@ -80,6 +113,13 @@ inline size_t lds_bytes(const DevModel &M) {
 // from wave 1 to wave 0 (2 d i64), the kept drawers' ranges and four per-wave results.
 inline size_t pair_lds_bytes(const DevModel &M) {
   return lds_bytes(M) + 4ull * (4 * M.d + 2 * kMaxProbes + 8);
+}
+
+// A Hamming model's kernels add the session's tokens (context u32), the distances (context
+// bytes), one head's picks and weights (2 kMaxHamKept u32) and the sign nibbles (d / 4 u32).
+inline size_t ham_lds_bytes(const DevModel &M) {
+  if (!M.ham.heads) return 0;
+  return 4ull * M.context + ((M.context + 15ull) & ~15ull) + 8ull * kMaxHamKept + 4ull * (M.d / 4);
 }
 
 enum RunMode : uint32_t { kModeSequences = 0, kModeDecode = 1, kModeScore = 2 };
@@ -116,6 +156,14 @@ struct RunArgs {
   uint32_t capacity;
   int32_t *ring;          // gridDim.x * L * W * d
   int64_t *hist;          // paired blocks: gridDim.x * L * d, the next step's window sums
+  // Hamming models: the session's token stream ([n][context]: x_0..x_{position-1}) and its type
+  // heads' payload caches ([n][slots][context][d]) in and out (null: a fresh stream, none
+  // exported); `pay` the library's caches for sequences with no out_payloads, [gridDim.x][...].
+  const uint32_t *in_stream;
+  uint32_t *out_stream;
+  const int64_t *in_payloads;
+  int64_t *out_payloads;
+  int64_t *pay;
 };
 
 }  // namespace fbs

@@ -1,0 +1,432 @@
+// fbs_hamming.h - the Hamming reads of a lut-stack/6 stack inside the FBS step (gfx950): the
+// copy heads, the type heads (payloads of the hook's input) and the ask heads (a question table
+// with its carry), at the stream read after `depth` layers and on the readout
+// (RS crates/uor-r4-integer/src/stack/hamming.rs: ServedHamming::stream :1831-1866 and
+// readout :1883-1913; session.rs:4252-4276, 4296-4320). Included by fbs_run.h.
+//
+// One 64-lane wavefront runs a read; the session's tokens x_0..x_t sit in LDS. Each head in turn
+// chooses its positions 1 <= s < t by the popcount distance between the row's query code and
+// position s's key code (x_{s-1}'s code through the read's key rotation, precomputed per
+// vocabulary entry at model creation): `nearest` (:690-701) as successive wave minima of
+// (distance, position) over the distances staged in LDS, the latest and longest rules
+// (:584-615) as one wave minimum or maximum. The chosen positions and their Q31 margin weights
+// (`copy_weight_q31` :243-252) go to LDS, uniform for the wave; then every lane sums, for its
+// own channels, the weighted values the positions bring back (the table point of the position's
+// own token, or the payload kept at the position, which the same lane wrote), divides by the
+// head's count, and after the last head by the number of heads that found a position, both
+// quotients truncating toward zero (`mean_by` :506-538, :1282-1334). The sums at the hooks are
+// formed exactly in 128 bits and rounded once (stream_sum, readout_sum, readout_ask_sum
+// :1918-1953). Integer only: the quotients go through fbs_int.h's integer division.
+#ifndef UOR_FBS_HAMMING_H
+#define UOR_FBS_HAMMING_H
+
+namespace fbs {
+
+constexpr int32_t kCopyMeanExp = -43;       // COPY_MEAN_EXP, hamming.rs:175
+constexpr int32_t kHammingWeightExp = -24;  // HAMMING_WEIGHT_EXP, format.rs:59
+constexpr uint32_t kTypeMeanShift = 31;     // TYPE_MEAN_SHIFT, hamming.rs:1364
+constexpr uint32_t kStreamShift = (uint32_t)(kResidualExp - kHammingWeightExp - kCopyMeanExp);
+constexpr uint32_t kNormRaise = (uint32_t)(kNormFineExp - kCopyMeanExp);
+constexpr uint32_t kReadoutShift = (uint32_t)(kNormFineExp - kHammingWeightExp - kCopyMeanExp);
+constexpr uint32_t kStreamCopyRaise =
+    (uint32_t)(kCopyMeanExp - kResidualExp + (int32_t)kTypeMeanShift);
+constexpr uint32_t kReadoutTypeDrop =
+    (uint32_t)(kCopyMeanExp - kNormFineExp + (int32_t)kTypeMeanShift);
+constexpr uint32_t kPosBits = kHamPosBits;  // a packed pick: distance << 24 | position
+constexpr uint32_t kPosMask = (1u << kPosBits) - 1;
+
+FBS_HD i128 shl128(i128 v, uint32_t s) { return (i128)((u128)v << s); }
+
+// `round_shift` (:1353-1360): v / 2^s rounded half away from zero, 1 <= s <= 126.
+FBS_HD i128 round_shift128(i128 v, uint32_t s) {
+  const i128 half = (i128)1 << (s - 1);
+  return v >= 0 ? (v + half) >> s : -((half - v) >> s);
+}
+
+FBS_HD int64_t clamp_i64(i128 v) {
+  return v > (i128)INT64_MAX ? INT64_MAX : v < (i128)INT64_MIN ? INT64_MIN : (int64_t)v;
+}
+
+// v / k rounded toward zero (Rust's integer division) by a prepared divisor k >= 1.
+FBS_HD int64_t div_trunc64(int64_t v, const Divisor &k) {
+  const uint64_t a = v < 0 ? 0 - (uint64_t)v : (uint64_t)v;
+  const uint64_t q = divq((u128)a, k);
+  return v < 0 ? (int64_t)(0 - q) : (int64_t)q;
+}
+FBS_HD i128 div_trunc128(i128 v, const Divisor &k) {
+  const u128 a = v < 0 ? (u128)0 - (u128)v : (u128)v;
+  const uint64_t hi = (uint64_t)(a >> 64), lo = (uint64_t)a;
+  const uint64_t qh = divq((u128)hi, k), rh = hi - qh * k.d;
+  const uint64_t ql = divq(((u128)rh << 64) | lo, k);  // rh < k, so the quotient fits
+  const u128 q = ((u128)qh << 64) | ql;
+  return v < 0 ? (i128)((u128)0 - q) : (i128)q;
+}
+
+// `stream_sum` (:1918-1925): x + w_c c + w_y y at Q16, formed exactly, rounded once.
+FBS_HD int32_t ham_stream_sum(int32_t x, int32_t w_c, i128 c, int32_t w_y, i128 y) {
+  constexpr uint32_t sh = kStreamShift + kStreamCopyRaise;
+  const i128 sum = shl128(x, sh) + shl128((i128)w_c * c, kStreamCopyRaise) + (i128)w_y * y;
+  const i128 r = round_shift128(sum, sh);
+  return r > INT32_MAX ? INT32_MAX : r < INT32_MIN ? INT32_MIN : (int32_t)r;
+}
+
+// `readout_sum` (:1933-1940): n + [copy matched] w_c (c - n) + w_y y, the type term pre-rounded.
+FBS_HD int64_t ham_readout_sum(int64_t n, int32_t w_c, bool has_c, i128 c, int32_t w_y, i128 y) {
+  const i128 moved = has_c ? (i128)w_c * (c - shl128(n, kNormRaise)) : 0;
+  const i128 typed = round_shift128((i128)w_y * y, kReadoutTypeDrop);
+  return clamp_i64(round_shift128(shl128(n, kReadoutShift) + moved + typed, kReadoutShift));
+}
+
+// `readout_ask_sum` (:1946-1953): n + [copy matched] w_c (c - n) + [ask matched] w_y (y - n).
+FBS_HD int64_t ham_readout_ask_sum(int64_t n, int32_t w_c, bool has_c, i128 c, int32_t w_y,
+                                   bool has_y, i128 y) {
+  const i128 raised = shl128(n, kNormRaise);
+  const i128 copied = has_c ? (i128)w_c * (c - raised) : 0;
+  const i128 asked = has_y ? (i128)w_y * (y - raised) : 0;
+  return clamp_i64(round_shift128(shl128(n, kReadoutShift) + copied + asked, kReadoutShift));
+}
+
+// `copy_weight_q31` (:243-252): max(0, m - d) / max(m, 1) at Q31, the margin in bits at Q16.
+FBS_HD uint32_t ham_weight(int32_t margin_q16, uint32_t distance) {
+  const int64_t over = (int64_t)margin_q16 - ((int64_t)distance << 16);
+  if (over <= 0) return 0;
+  const uint64_t m = (uint64_t)(margin_q16 > (1 << 16) ? margin_q16 : (1 << 16));
+  return (uint32_t)div128_64((u128)((uint64_t)over << 31), m);
+}
+
+// The sign nibble of unit (x) p (the unit on the left, `head_code` :550-564): bit i is 1 where
+// coordinate i is at or above 0.
+FBS_HD uint32_t ham_nibble(const int64_t *unit, const int64_t (&p)[4]) {
+  const int64_t u[4] = {unit[0], unit[1], unit[2], unit[3]};
+  i128 o[4];
+  hamilton64(u, p, o);
+  return (uint32_t)(o[0] >= 0) | (uint32_t)(o[1] >= 0) << 1 | (uint32_t)(o[2] >= 0) << 2 |
+         (uint32_t)(o[3] >= 0) << 3;
+}
+
+// Head j's code word from the sign nibbles of its hw / 4 quaternions in LDS (uniform).
+__device__ __forceinline__ uint64_t ham_word(const uint32_t *nib, uint32_t j, uint32_t hw) {
+  uint64_t word = 0;
+  for (uint32_t c = 0; c < hw; c += 4) word |= (uint64_t)nib[(j * hw + c) >> 2] << c;
+  return word;
+}
+
+__device__ __forceinline__ uint64_t ham_code(const DevHamRead &R, uint32_t heads, uint32_t token,
+                                             uint32_t head) {
+  return R.codes[(uint64_t)token * heads + head];
+}
+
+// One token's Q12 table value on the lane's four channels of quaternion q.
+__device__ __forceinline__ void ham_point(const DevModel &M, uint32_t token, uint32_t q,
+                                          int64_t (&v)[4]) {
+  const uint2 w = *(const uint2 *)(M.table_b + (uint64_t)token * M.d + 4 * q);
+  v[0] = (int16_t)(uint16_t)((w.x & 0xffffu) ^ 0x8000u);
+  v[1] = (int16_t)(uint16_t)((w.x >> 16) ^ 0x8000u);
+  v[2] = (int16_t)(uint16_t)((w.y & 0xffffu) ^ 0x8000u);
+  v[3] = (int16_t)(uint16_t)((w.y >> 16) ^ 0x8000u);
+}
+
+// A head's positions at row t under `rule` (0 the mean's `nearest`, 1 latest exact, 2 latest
+// nearest, 3 longest exact), position s's key from keyf(s), into S.hpick (position) and S.hwgt
+// (Q31 weight) in ascending distance, then ascending position: only the positions inside the
+// margin (weights fall with distance, so they lead). Returns their count, uniform. For the
+// longest rule, longer(s) says whether one token more matches.
+template <class KeyF, class LongerF>
+__device__ __forceinline__ uint32_t ham_choose(const Lds &S, uint32_t rule, uint64_t q, uint32_t t,
+                                               uint32_t kept, int32_t margin, uint32_t lane,
+                                               KeyF keyf, LongerF longer) {
+  if (t < 2) return 0;
+  uint32_t n = 0;
+  if (rule == 0) {
+    for (uint32_t s = 1 + lane; s < t; s += kWave) S.hdist[s] = (uint8_t)__popcll(q ^ keyf(s));
+    wave_sync();
+    uint32_t last = 0;  // every packed pick exceeds 0: positions start at 1
+    for (uint32_t r = 0; r < kept; r++) {
+      uint32_t loc = UINT32_MAX;
+      for (uint32_t s = 1 + lane; s < t; s += kWave) {
+        const uint32_t k = (uint32_t)S.hdist[s] << kPosBits | s;
+        loc = k > last && k < loc ? k : loc;
+      }
+      const uint32_t m = wave_reduce32(loc, OpMin());
+      if (m == UINT32_MAX) break;
+      const uint32_t w = ham_weight(margin, m >> kPosBits);
+      if (!w) break;  // this and every later pick lie outside the margin
+      if (lane == 0) {
+        S.hpick[n] = m & kPosMask;
+        S.hwgt[n] = w;
+      }
+      n++;
+      last = m;
+    }
+  } else if (rule <= 2) {
+    uint32_t best = UINT32_MAX;
+    for (uint32_t s = 1 + lane; s < t; s += kWave) {
+      const uint32_t dd = (uint32_t)__popcll(q ^ keyf(s));
+      if (rule == 1 && dd != 0) continue;
+      const uint32_t k = dd << kPosBits | (kPosMask - s);
+      best = k < best ? k : best;
+    }
+    const uint32_t m = wave_reduce32(best, OpMin());
+    const uint32_t w = m == UINT32_MAX ? 0 : ham_weight(margin, m >> kPosBits);
+    if (w) {
+      if (lane == 0) {
+        S.hpick[0] = kPosMask - (m & kPosMask);
+        S.hwgt[0] = w;
+      }
+      n = 1;
+    }
+  } else {
+    uint32_t ex = 0, lg = 0;
+    for (uint32_t s = 1 + lane; s < t; s += kWave) {
+      if (keyf(s) != q) continue;
+      ex = s > ex ? s : ex;
+      if (longer(s)) lg = s > lg ? s : lg;
+    }
+    ex = wave_reduce32(ex, OpMax());
+    lg = wave_reduce32(lg, OpMax());
+    const uint32_t pick = lg ? lg : ex;
+    const uint32_t w = pick ? ham_weight(margin, 0) : 0;
+    if (w) {
+      if (lane == 0) {
+        S.hpick[0] = pick;
+        S.hwgt[0] = w;
+      }
+      n = 1;
+    }
+  }
+  wave_sync();
+  return n;
+}
+
+// The copy heads' mean at row t (`CopyHeads::mean_at` :482-504) on the lane's channels into cm
+// (at 2^-43; |cm| < 2^53, so 64 bits hold it). Returns whether a head found a position.
+template <int Q>
+__device__ __forceinline__ bool ham_copy_mean(const DevModel &M, const DevHamRead &R, const Lds &S,
+                                              uint32_t t, uint32_t lane, const bool (&qv)[Q],
+                                              const uint32_t (&qi)[Q], int64_t (&cm)[Q][4]) {
+  const DevHam &H = M.ham;
+  const uint32_t *tk = S.tok;
+#pragma unroll
+  for (int k = 0; k < Q; k++)
+#pragma unroll
+    for (int c = 0; c < 4; c++) cm[k][c] = 0;
+  uint32_t rule = H.rule;
+  if (rule == 4)  // longest after opening: the opening row is found from the marker
+    rule = H.has_marker && t >= 1 && tk[t - 1] == H.m0 && tk[t] == H.m1 ? 1u : 3u;
+  uint32_t found = 0;
+  for (uint32_t h = 0; h < H.copy; h++) {
+    const uint64_t first = H.pair[h];
+    auto joined = [&](uint32_t near, uint32_t far) -> uint64_t {
+      const uint64_t code = ham_code(R, H.heads, near, h);
+      return first ? (code & first) | (ham_code(R, H.heads, far, h) & ~first) : code;
+    };
+    const uint64_t q = joined(tk[t], tk[t ? t - 1 : 0]);
+    const uint32_t kd = first ? 2 : 1;
+    const uint64_t before = t >= kd ? ham_code(R, H.heads, tk[t - kd], h) : 0;
+    const uint32_t n = ham_choose(
+        S, rule, q, t, H.kept, R.margin[h], lane,
+        [&](uint32_t s) { return joined(tk[s - 1], tk[s >= 2 ? s - 2 : 0]); },
+        [&](uint32_t s) { return s > kd && ham_code(R, H.heads, tk[s - 1 - kd], h) == before; });
+    if (!n) continue;
+    found++;
+    const Divisor dv = make_divisor(n);
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      if (!qv[k]) continue;
+      int64_t acc[4] = {0, 0, 0, 0};
+      for (uint32_t i = 0; i < n; i++) {
+        int64_t v[4];
+        ham_point(M, tk[S.hpick[i]], qi[k], v);
+        const int64_t w = S.hwgt[i];
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc[c] += v[c] * w;
+      }
+#pragma unroll
+      for (int c = 0; c < 4; c++) cm[k][c] += div_trunc64(acc[c], dv);
+    }
+    wave_sync();  // the picks are read before the next head writes them
+  }
+  if (!found) return false;
+  const Divisor dv = make_divisor(found);
+#pragma unroll
+  for (int k = 0; k < Q; k++)
+#pragma unroll
+    for (int c = 0; c < 4; c++) cm[k][c] = div_trunc64(cm[k][c], dv);
+  return true;
+}
+
+// The type heads' mean at row t (`ServedHamming::type_mean` :1750-1783) into ym. A read that
+// asks (`asked_point` :1161-1181, `ask_queries` :1185-1190) asks with the sign codes of
+// (table + a)[x_t] 2^16 + sum_{s <= min(h, t)} c[x_{t-s}] (table + a)[x_{t-s}] through the key
+// rotation and brings back the kept tokens' table points (ym at 2^-43); otherwise `point`'s
+// payload (`payload` :1204-1215) is kept at row t of `pay` first, the query codes are `point`'s
+// through the query rotation and the kept positions' payloads come back (ym at the point's
+// exponent minus 31). Returns whether a head found a position.
+template <int Q>
+__device__ __forceinline__ bool ham_type_mean(const DevModel &M, const DevHamRead &R, const Lds &S,
+                                              uint32_t t, uint32_t lane, const bool (&qv)[Q],
+                                              const uint32_t (&qi)[Q], const int64_t (&point)[Q][4],
+                                              int64_t *pay, i128 (&ym)[Q][4]) {
+  const DevHam &H = M.ham;
+  const uint32_t d = M.d, *tk = S.tok;
+  const bool asks = R.ask != nullptr;
+#pragma unroll
+  for (int k = 0; k < Q; k++) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) ym[k][c] = 0;
+    if (!qv[k]) continue;
+    const uint32_t q = qi[k];
+    if (asks) {
+      auto asked = [&](uint32_t v, int64_t (&o)[4]) {
+        ham_point(M, v, q, o);
+        const short4 a = *(const short4 *)(R.ask + (uint64_t)v * d + 4 * q);
+        o[0] += a.x;
+        o[1] += a.y;
+        o[2] += a.z;
+        o[3] += a.w;
+      };
+      int64_t p[4];
+      asked(tk[t], p);
+#pragma unroll
+      for (int c = 0; c < 4; c++) p[c] *= 65536;
+      if (R.carry) {
+        const uint32_t reach = R.carry_rows < t ? R.carry_rows : t;
+        for (uint32_t s = 1; s <= reach; s++) {
+          const uint32_t v = tk[t - s];
+          const int64_t gain = R.carry[v];
+          int64_t o[4];
+          asked(v, o);
+#pragma unroll
+          for (int c = 0; c < 4; c++) p[c] += gain * o[c];
+        }
+      }
+      S.hnib[q] = ham_nibble(R.ku + 4 * q, p);
+    } else {
+      i128 o[4];
+      const int64_t u[4] = {R.vu[4 * q], R.vu[4 * q + 1], R.vu[4 * q + 2], R.vu[4 * q + 3]};
+      hamilton64(u, point[k], o);
+      int64_t *dst = pay + (uint64_t)t * d + 4 * q;
+      *(longlong2 *)dst = make_longlong2(clamp_i64(round_shift128(o[0], 31)),
+                                         clamp_i64(round_shift128(o[1], 31)));
+      *(longlong2 *)(dst + 2) = make_longlong2(clamp_i64(round_shift128(o[2], 31)),
+                                               clamp_i64(round_shift128(o[3], 31)));
+      S.hnib[q] = ham_nibble(R.qu + 4 * q, point[k]);
+    }
+  }
+  wave_sync();
+  uint32_t found = 0;
+  for (uint32_t j = H.copy; j < H.heads; j++) {
+    const uint64_t q = ham_word(S.hnib, j, H.hw);
+    const uint32_t n = ham_choose(
+        S, 0, q, t, H.kept, R.margin[j], lane,
+        [&](uint32_t s) { return ham_code(R, H.heads, tk[s - 1], j); },
+        [&](uint32_t) { return false; });
+    if (!n) continue;
+    found++;
+    const Divisor dv = make_divisor(n);
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      if (!qv[k]) continue;
+      i128 acc[4] = {0, 0, 0, 0};
+      for (uint32_t i = 0; i < n; i++) {
+        const uint32_t s = S.hpick[i];
+        const int64_t w = S.hwgt[i];
+        int64_t v[4];
+        if (asks) {
+          ham_point(M, tk[s], qi[k], v);
+        } else {
+          const longlong2 *src = (const longlong2 *)(pay + (uint64_t)s * d + 4 * qi[k]);
+          const longlong2 a = src[0], b = src[1];
+          v[0] = a.x;
+          v[1] = a.y;
+          v[2] = b.x;
+          v[3] = b.y;
+        }
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc[c] += (i128)v[c] * w;
+      }
+#pragma unroll
+      for (int c = 0; c < 4; c++) ym[k][c] += div_trunc128(acc[c], dv);
+    }
+    wave_sync();
+  }
+  if (!found) return false;
+  const Divisor dv = make_divisor(found);
+#pragma unroll
+  for (int k = 0; k < Q; k++)
+#pragma unroll
+    for (int c = 0; c < 4; c++) ym[k][c] = div_trunc128(ym[k][c], dv);
+  return true;
+}
+
+// The stream read after `depth` layers (< the layer count) on the residual x, in place. `pay`:
+// the sequence's payload caches, [slot][context][d].
+template <int Q>
+__device__ __forceinline__ void ham_stream(const DevModel &M, const DevHamRead &R, const Lds &S,
+                                           uint32_t t, int64_t *pay, uint32_t lane,
+                                           const bool (&qv)[Q], const uint32_t (&qi)[Q],
+                                           int32_t (&x)[Q][4]) {
+  int64_t cm[Q][4];
+  i128 ym[Q][4];
+  const bool has_c = ham_copy_mean<Q>(M, R, S, t, lane, qv, qi, cm);
+  bool has_y = false;
+  if (R.typed) {
+    int64_t point[Q][4];
+#pragma unroll
+    for (int k = 0; k < Q; k++)
+#pragma unroll
+      for (int c = 0; c < 4; c++) point[k][c] = x[k][c];
+    int64_t *cache = R.ask ? nullptr : pay + (uint64_t)R.slot * M.context * M.d;
+    has_y = ham_type_mean<Q>(M, R, S, t, lane, qv, qi, point, cache, ym);
+    if (has_y && R.ask)
+#pragma unroll
+      for (int k = 0; k < Q; k++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) ym[k][c] = shl128(ym[k][c], kStreamCopyRaise);
+  }
+  if (!has_c && !has_y) return;
+#pragma unroll
+  for (int k = 0; k < Q; k++)
+    if (qv[k]) {
+      const int4 wc = *(const int4 *)(R.w + 4 * qi[k]);
+      const int4 wy = *(const int4 *)(R.w + M.d + 4 * qi[k]);
+      const int32_t a[4] = {wc.x, wc.y, wc.z, wc.w}, b[4] = {wy.x, wy.y, wy.z, wy.w};
+#pragma unroll
+      for (int c = 0; c < 4; c++)
+        x[k][c] = ham_stream_sum(x[k][c], a[c], has_c ? (i128)cm[k][c] : 0, b[c],
+                                 has_y ? ym[k][c] : 0);
+    }
+}
+
+// The readout read on the final norm's output n (at 2^-24), in place.
+template <int Q>
+__device__ __forceinline__ void ham_readout(const DevModel &M, const DevHamRead &R, const Lds &S,
+                                            uint32_t t, int64_t *pay, uint32_t lane,
+                                            const bool (&qv)[Q], const uint32_t (&qi)[Q],
+                                            int64_t (&n)[Q][4]) {
+  int64_t cm[Q][4];
+  i128 ym[Q][4];
+  const bool has_c = ham_copy_mean<Q>(M, R, S, t, lane, qv, qi, cm);
+  bool has_y = false;
+  if (R.typed) {
+    int64_t *cache = R.ask ? nullptr : pay + (uint64_t)R.slot * M.context * M.d;
+    has_y = ham_type_mean<Q>(M, R, S, t, lane, qv, qi, n, cache, ym);
+  }
+  if (!has_c && !has_y) return;
+#pragma unroll
+  for (int k = 0; k < Q; k++)
+    if (qv[k]) {
+      const int4 wc = *(const int4 *)(R.w + 4 * qi[k]);
+      const int4 wy = *(const int4 *)(R.w + M.d + 4 * qi[k]);
+      const int32_t a[4] = {wc.x, wc.y, wc.z, wc.w}, b[4] = {wy.x, wy.y, wy.z, wy.w};
+#pragma unroll
+      for (int c = 0; c < 4; c++)
+        n[k][c] = R.ask ? ham_readout_ask_sum(n[k][c], a[c], has_c, cm[k][c], b[c], has_y, ym[k][c])
+                        : ham_readout_sum(n[k][c], a[c], has_c, cm[k][c], b[c],
+                                          has_y ? ym[k][c] : 0);
+    }
+}
+
+}  // namespace fbs
+
+#endif

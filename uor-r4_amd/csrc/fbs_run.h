@@ -709,14 +709,33 @@ struct Lds {
   int64_t *gq;       // d: the output gates' quaternions, wave 1 -> wave 0
   uint32_t *rng;     // 2 kMaxProbes: the kept drawers' CSR ranges (begins, then ends)
   uint64_t *pair;    // 4: each wave's MLP maximum magnitude, then each wave's best candidate
+  // Hamming models only (null otherwise):
+  uint32_t *tok;     // context: the session's tokens x_0..x_t
+  uint8_t *hdist;    // context: one head's distances at the row
+  uint32_t *hpick;   // kMaxHamKept: one head's chosen positions
+  uint32_t *hwgt;    // kMaxHamKept: their Q31 weights
+  uint32_t *hnib;    // d / 4: the sign nibbles of the row's point
 };
 
-template <int Q, int SW>
+}  // namespace fbs
+
+#include "fbs_hamming.h"
+
+namespace fbs {
+
+// HM: the model's Hamming reads run at their hooks (row t of the session, `pay` its payload
+// caches).
+template <int Q, int SW, bool HM>
 __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ring, uint32_t base, uint32_t lane,
                     const bool (&qv)[Q], const uint32_t (&qi)[Q], uint32_t tok, bool want_writer,
-                    uint32_t *chosen, uint32_t *kept_out, int32_t *query_out) {
+                    uint32_t *chosen, uint32_t *kept_out, int32_t *query_out, uint32_t t,
+                    int64_t *pay) {
   if (tok >= M.vocab) return 1;
   const uint32_t d = M.d, W = M.W, nq = M.nq;
+  if (HM) {  // the read at this row needs x_0..=x_t (session.rs:4149-4152)
+    if (lane == 0) S.tok[t] = tok;
+    wave_sync();
+  }
   int32_t x[Q][4];
 #pragma unroll
   for (int k = 0; k < Q; k++) {
@@ -968,6 +987,10 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
 #pragma unroll
         for (int c = 0; c < 4; c++) x[k][c] = sat_add32(x[k][c], S.xbar[pw_down[k][c]]);
     wave_sync();
+    if (HM) {  // the stream read after l + 1 layers (session.rs:4252-4276)
+      const int32_t r = M.ham.at[l + 1];
+      if (r >= 0 && l + 1 < M.L) ham_stream<Q>(M, M.ham.reads[r], S, t, pay, lane, qv, qi, x);
+    }
   }
   // Final norm, gain and the Q12 query (session.rs:4294-4295, 4364-4366).
   short4 g_fin[Q];
@@ -979,6 +1002,10 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
   }
   int64_t v[Q][4];
   norm_gain<Q>(M, S.seeds, x, qv, g_fin, gd_fin, v);
+  if (HM) {  // the readout read on the final norm's output (session.rs:4296-4320)
+    const int32_t r = M.ham.at[M.L];
+    if (r >= 0) ham_readout<Q>(M, M.ham.reads[r], S, t, pay, lane, qv, qi, v);
+  }
   int4 qq[Q];
   bool same = true;  // this lane's channels equal the query of the writer's last run
 #pragma unroll
@@ -1530,8 +1557,10 @@ __device__ __forceinline__ int step_window(const DevModel &M, const Lds &S, int3
 enum Phase : int { kPhasePrefill = 0, kPhaseDecode = 1, kPhaseRows = 2 };
 
 // NW = 1: one wavefront per sequence (step); NW = 2: paired blocks (step_main, step_window).
-template <int Q, int SW, int PH, int NW>
+// HM: a model with Hamming reads (one wavefront per sequence).
+template <int Q, int SW, int PH, int NW, bool HM = false>
 __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
+  static_assert(!HM || NW == 1, "the Hamming reads run on one wavefront per sequence");
   extern __shared__ __align__(16) int32_t lds[];
   Lds S;
   {
@@ -1566,6 +1595,20 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
       S.rng = (uint32_t *)(lds + at);
       at += 2 * kMaxProbes;
       S.pair = (uint64_t *)(lds + at);
+    }
+    S.tok = nullptr;
+    S.hdist = nullptr;
+    S.hpick = S.hwgt = S.hnib = nullptr;
+    if (HM) {  // ham_lds_bytes
+      S.tok = (uint32_t *)(lds + at);
+      at += M.context;
+      S.hdist = (uint8_t *)(lds + at);
+      at += ((M.context + 15u) & ~15u) / 4u;
+      S.hpick = (uint32_t *)(lds + at);
+      at += kMaxHamKept;
+      S.hwgt = (uint32_t *)(lds + at);
+      at += kMaxHamKept;
+      S.hnib = (uint32_t *)(lds + at);
     }
     const uint32_t *rs = rsqrt_seed_table(), *rc = recip_seed_table();
     for (uint32_t i = threadIdx.x; i < kRsqrtSeedWords; i += NW * kWave) seed_lds[i] = rs[i];
@@ -1622,15 +1665,44 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
               *(int4 *)(ring + ((uint64_t)l * W + slot) * d + ch) = h;
             }
         }
+    // Hamming models: the session's tokens into LDS, and its payload caches: the caller's
+    // out_payloads (the resumed rows copied in first, each lane its own channels) or the block's.
+    // A resumed token outside the vocabulary refuses the sequence (status 1) before any read
+    // indexes a table by it.
+    int64_t *pay = nullptr;
+    bool bad_stream = false;
+    if (HM) {
+      uint32_t bad = 0;
+      for (uint32_t i = lane; i < M.context; i += kWave) {
+        const uint32_t v = A.in_stream && i < pos ? A.in_stream[(uint64_t)sl * M.context + i] : 0u;
+        bad |= v >= M.vocab ? 1u : 0u;
+        S.tok[i] = v;
+      }
+      bad_stream = wave_reduce32(bad, OpMax()) != 0;
+      const uint64_t stride = (uint64_t)M.ham.slots * M.context * d;
+      pay = A.out_payloads ? A.out_payloads + (uint64_t)sl * stride : A.pay + (uint64_t)blockIdx.x * stride;
+      if (A.in_payloads && A.in_payloads != A.out_payloads)
+        for (uint32_t c = 0; c < M.ham.slots; c++)
+          for (uint32_t r = 0; r < pos; r++)
+#pragma unroll
+            for (int k = 0; k < Q; k++)
+              if (qv[k]) {
+                const uint64_t o = ((uint64_t)c * M.context + r) * d + 4 * qi[k];
+                const longlong2 *src = (const longlong2 *)(A.in_payloads + (uint64_t)sl * stride + o);
+                longlong2 *dst = (longlong2 *)(pay + o);
+                dst[0] = src[0];
+                dst[1] = src[1];
+              }
+    }
     if (NW == 2)
       pair_sync();
     else
       wave_sync();
-    int status = 0;
+    int status = bad_stream ? 1 : 0;
     uint32_t chosen = 0;
     constexpr bool decode = PH != kPhaseRows;
     const uint32_t *toks = A.tokens + (uint64_t)s * A.len;
-    const uint32_t steps = PH == kPhaseDecode ? A.len + A.gen : A.len;
+    const uint32_t steps = bad_stream ? 0u : PH == kPhaseDecode ? A.len + A.gen : A.len;
     unsigned long long hits = 0;
     for (uint32_t t = 0; t < steps; t++) {
       if (pos >= M.context) {
@@ -1655,7 +1727,8 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
                            : last       ? A.out_query + (uint64_t)s * d
                                         : nullptr;
       if (NW == 1) {
-        status = step<Q, SW>(M, S, ring, base, lane, qv, qi, tok, want, &chosen, kept_out, query_out);
+        status = step<Q, SW, HM>(M, S, ring, base, lane, qv, qi, tok, want, &chosen, kept_out,
+                                 query_out, pos, pay);
       } else {
         // The lane's indices pass through an empty asm at every step, so that the compiler forms
         // the lane's addresses inside the loop instead of holding them across the kernel.
@@ -1703,6 +1776,9 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
               }
           }
       if (A.out_position && writes_out) A.out_position[sl] = pos;
+      if (HM && A.out_stream)
+        for (uint32_t i = lane; i < M.context; i += kWave)
+          A.out_stream[(uint64_t)sl * M.context + i] = S.tok[i];
     }
     if (writes_out) A.status[s] = status;
     if (NW == 2)
@@ -1752,13 +1828,21 @@ inline hipError_t launch_shape(const KernelSet &k, const DevModel &M, const RunA
   __global__ __launch_bounds__(128, 2) void NAME##_pair(DevModel M, RunArgs A) {              \
     run<Q, SW, PH, 2>(M, A);                                                                  \
   }                                                                                           \
+  template <int Q, int SW>                                                                    \
+  __global__ __launch_bounds__(64) void NAME##_ham(DevModel M, RunArgs A) {                   \
+    run<Q, SW, PH, 1, true>(M, A);                                                            \
+  }                                                                                           \
   hipError_t launch_##NAME(const DevModel &M, const RunArgs &A, uint32_t grid, uint32_t waves, \
                            size_t lds, hipStream_t stream) {                                  \
     static const KernelSet one = {NAME<1, 1>, NAME<1, 2>, NAME<1, 4>,                         \
                                   NAME<1, 8>, NAME<2, 16>, NAME<4, 32>};                       \
     static const KernelSet two = {NAME##_pair<1, 1>, NAME##_pair<1, 2>, NAME##_pair<1, 4>,    \
                                   NAME##_pair<1, 8>, NAME##_pair<2, 16>, NAME##_pair<4, 32>};  \
-    return launch_shape(waves == 2 ? two : one, M, A, grid, waves, lds, stream);              \
+    static const KernelSet ham = {NAME##_ham<1, 1>, NAME##_ham<1, 2>, NAME##_ham<1, 4>,       \
+                                  NAME##_ham<1, 8>, NAME##_ham<2, 16>, NAME##_ham<4, 32>};     \
+    if (M.ham.heads && waves != 1) return hipErrorInvalidValue;                               \
+    return launch_shape(M.ham.heads ? ham : waves == 2 ? two : one, M, A, grid, waves, lds,   \
+                        stream);                                                              \
   }
 
 }  // namespace fbs

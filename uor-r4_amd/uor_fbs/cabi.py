@@ -35,12 +35,28 @@ class ModelS(C.Structure):
                 ("raw_gates", C.c_uint32), ("raw_transition", C.c_uint32)]
 
 
+class HammingReadS(C.Structure):
+    _fields_ = [("depth", C.c_uint32), ("carry_rows", C.c_uint32),
+                ("query_rotation", C.POINTER(C.c_int32)), ("key_rotation", C.POINTER(C.c_int32)),
+                ("value_rotation", C.POINTER(C.c_int32)), ("margin", C.POINTER(C.c_int32)),
+                ("weight", C.POINTER(C.c_int32)), ("ask", C.POINTER(C.c_int16)),
+                ("carry", C.POINTER(C.c_int32))]
+
+
+class HammingS(C.Structure):
+    _fields_ = [("heads", C.c_uint32), ("kept", C.c_uint32), ("copy_key", C.c_uint32),
+                ("copy_latest", C.c_uint32), ("copy_keys", C.POINTER(C.c_uint32)),
+                ("copy_longest", C.c_uint32), ("marker", C.c_uint32 * 2), ("rule", C.c_uint32),
+                ("read_count", C.c_uint32), ("reads", C.POINTER(HammingReadS))]
+
+
 class ExtS(C.Structure):
     _fields_ = [("window", C.c_uint32), ("drawers", C.c_uint32), ("probes", C.c_uint32),
                 ("head", C.c_uint32), ("wide_taps", C.POINTER(C.POINTER(C.c_int16))),
                 ("drawer_keys", C.POINTER(C.c_int32)), ("drawer_offsets", C.POINTER(C.c_uint32)),
                 ("drawer_members", C.POINTER(C.c_uint32)), ("table_i8", C.POINTER(C.c_int8)),
-                ("table_shift", C.c_uint32), ("reserved", C.c_uint32)]
+                ("table_shift", C.c_uint32), ("reserved", C.c_uint32),
+                ("hamming", C.POINTER(HammingS))]
 
 
 _CT = {np.dtype(np.int8): C.c_int8, np.dtype(np.uint8): C.c_uint8, np.dtype(np.int16): C.c_int16,
@@ -95,7 +111,9 @@ class Image:
         m.keep_q31 = ptr(arr(art.keep_q31, np.uint64))
         m.raw_gates, m.raw_transition = int(s.raw_gates), int(s.raw_transition)
         self.model = m
-        needs_ext = not s.reference_shape or s.head != 0 or art.drawer_keys is not None
+        ham = getattr(art, "hamming", None)
+        needs_ext = (not s.reference_shape or s.head != 0 or art.drawer_keys is not None
+                     or ham is not None)
         if with_ext is None:
             with_ext = needs_ext
         self.ext = None
@@ -120,6 +138,32 @@ class Image:
                                    else arr(art.drawer_members, np.uint32), C.c_uint32)
             e.table_i8 = ptr(None if art.table_i8 is None else arr(art.table_i8, np.int8), C.c_int8)
             e.table_shift = s.table_shift if art.table_i8 is not None else 0
+            if ham is not None:
+                reads = (HammingReadS * len(art.hamming_reads))()
+                for i, r in enumerate(art.hamming_reads):
+                    R = reads[i]
+                    R.depth, R.carry_rows = r.depth, (ham.carry_rows if r.carry is not None else 0)
+                    R.query_rotation = ptr(arr(r.query_rotation, np.int32))
+                    R.key_rotation = ptr(arr(r.key_rotation, np.int32))
+                    R.value_rotation = ptr(arr(r.value_rotation, np.int32))
+                    R.margin = ptr(arr(r.margin, np.int32))
+                    R.weight = ptr(arr(r.weight, np.int32))
+                    R.ask = ptr(None if r.ask is None else arr(r.ask, np.int16), C.c_int16)
+                    R.carry = ptr(None if r.carry is None else arr(r.carry, np.int32), C.c_int32)
+                keep.append(reads)
+                H = HammingS()
+                H.heads, H.kept, H.copy_key = ham.heads, ham.kept, ham.copy_key
+                H.copy_latest = int(ham.copy_latest)
+                H.copy_keys = ptr(None if ham.copy_keys is None
+                                  else arr(np.array(ham.copy_keys), np.uint32), C.c_uint32)
+                H.copy_longest = int(ham.copy_longest is not None)
+                if ham.copy_longest is not None:
+                    H.marker[0], H.marker[1] = ham.copy_longest
+                H.rule = ham.rule
+                H.read_count = len(art.hamming_reads)
+                H.reads = C.cast(reads, C.POINTER(HammingReadS))
+                keep.append(H)
+                e.hamming = C.pointer(H)
             self.ext = e
         self._keep = keep
 

@@ -32,7 +32,8 @@ SYMBOLS = (
     "uor_fbs_score_async", "uor_fbs_block_waves",
     "uor_fbs_decode_slots_async", "uor_fbs_index_workspace_bytes", "uor_fbs_index_build_async",
     "uor_fbs_index_update_async", "uor_fbs_index_remove_async", "uor_fbs_index_validate_async",
-    "uor_fbs_index_probe_async", "uor_fbs_index_full_scan_async",
+    "uor_fbs_index_probe_async", "uor_fbs_index_full_scan_async", "uor_fbs_stream_words",
+    "uor_fbs_payload_words", "uor_fbs_decode_stream", "uor_fbs_decode_stream_async",
 )
 
 
@@ -69,6 +70,13 @@ def lib():
         L.uor_fbs_decode_async.argtypes = [P, P, C.c_uint32, C.c_uint32, C.c_uint32, P, P, P, P, P,
                                            P, P, P, P]
         L.uor_fbs_decode_noalloc_async.argtypes = L.uor_fbs_decode_async.argtypes
+        L.uor_fbs_stream_words.argtypes = [P]
+        L.uor_fbs_stream_words.restype = C.c_uint64
+        L.uor_fbs_payload_words.argtypes = [P]
+        L.uor_fbs_payload_words.restype = C.c_uint64
+        L.uor_fbs_decode_stream.argtypes = [P, P, C.c_uint32, C.c_uint32, C.c_uint32] + [P] * 11
+        L.uor_fbs_decode_stream_async.argtypes = ([P, P, C.c_uint32, C.c_uint32, C.c_uint32]
+                                                  + [P] * 13)
         L.uor_fbs_decode_slots_async.argtypes = [P, P, C.c_uint32, C.c_uint32, P, C.c_uint32,
                                                  C.c_uint32, P, P, P, P, P, P, P, P]
         L.uor_fbs_score.argtypes = [P, P, C.c_uint64, C.c_uint32, P, P]
@@ -159,6 +167,39 @@ class Model:
                                     _vp(in_state), _vp(in_history), _vp(in_position), _vp(state),
                                     _vp(hist), _vp(pos)))
         return dict(reply=reply, state=state, history=hist, position=pos)
+
+    @property
+    def stream_words(self) -> int:
+        """Tokens a session of a Hamming model keeps (the context), else 0."""
+        return int(lib().uor_fbs_stream_words(self.handle))
+
+    @property
+    def payload_words(self) -> int:
+        """int64 payload values a session of a Hamming model keeps, [typed read][context][width]."""
+        return int(lib().uor_fbs_payload_words(self.handle))
+
+    def decode_stream(self, prompts, gen: int, resume: dict | None = None):
+        """Greedy decode with the Hamming reads' session stream: dict(reply, state, history,
+        position, tokens [S, context], payloads [S, typed, context, width]); `resume` holds the
+        same arrays (state, history, position, tokens, payloads) to continue from."""
+        prompts = np.ascontiguousarray(prompts, dtype=np.uint32)
+        S, _ = prompts.shape
+        tw, pw = self.stream_words, self.payload_words
+        typed = pw // max(1, self.width * max(tw, 1))
+        out = dict(reply=np.zeros((S, gen + 1), np.uint32),
+                   state=np.zeros((S, self.state_words), np.int64),
+                   history=np.zeros((S, self.history_words), np.int32),
+                   position=np.zeros(S, np.uint32), tokens=np.zeros((S, tw), np.uint32),
+                   payloads=np.zeros((S, typed, tw, self.width), np.int64))
+        r = resume or {}
+        conv = lambda k, t: None if k not in r else np.ascontiguousarray(r[k], t)  # noqa: E731
+        ins = [conv("state", np.int64), conv("history", np.int32), conv("position", np.uint32),
+               conv("tokens", np.uint32), conv("payloads", np.int64)]
+        _check(lib().uor_fbs_decode_stream(
+            self.handle, _vp(prompts), S, prompts.shape[1], gen, _vp(out["reply"]),
+            *[_vp(a) for a in ins], _vp(out["state"]), _vp(out["history"]), _vp(out["position"]),
+            _vp(out["tokens"]) if tw else None, _vp(out["payloads"]) if pw else None))
+        return out
 
     def score(self, rows, want_argmin=True):
         """Teacher-forced scoring: (matches, argmin [n, len] or None)."""

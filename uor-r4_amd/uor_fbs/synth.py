@@ -89,6 +89,24 @@ def lcg(seed: int) -> Lcg:
 
 
 @dataclass(frozen=True)
+class HammingSpec:
+    """Seeded Hamming reads of a lut-stack/6 stack (StackHamming, stack/format.rs:229-292)."""
+
+    heads: int = 4
+    depths: tuple = (1,)          # after these many layers; the layer count is the readout read
+    kept: int = 16                # HAMMING_KEPT (format.rs:61)
+    copy_key: int = 1
+    copy_keys: tuple | None = None
+    copy_latest: bool = False
+    copy_longest: tuple | None = None   # the reply marker (two ids)
+    asks: tuple | None = None     # one flag per read
+    carry_rows: int = 0           # the readout read's question carry reach
+    typed: bool = True            # nonzero type weights w_y (type heads served)
+    margin_bits: tuple = (2, 12)  # margins drawn in this many bits (at Q16)
+    rule: int = 0xFFFFFFFF        # the copy rule served (UOR_FBS_COPY_*; default: the artifact's)
+
+
+@dataclass(frozen=True)
 class Spec:
     """Shape of a synthetic artifact. Zero extension fields mean the reference's rule."""
 
@@ -111,11 +129,26 @@ class Spec:
     gain_fields: tuple = (63, 64)
     tap_fields: tuple = (59, 62)
     bias_range: int = 1 << 14
+    hamming: HammingSpec | None = None
 
     @property
     def reference_shape(self) -> bool:
         return (self.window == 3 and self.drawers in (0, 256) and self.zipf_drawers == 0
                 and self.table == "i16" and self.probes in (0, self.kept))
+
+
+@dataclass
+class HammingRead:
+    """One read's integers (HammingReadImage, stack/hamming.rs:25-40)."""
+
+    depth: int
+    query_rotation: np.ndarray  # width i32 at 2^-24
+    key_rotation: np.ndarray
+    value_rotation: np.ndarray
+    margin: np.ndarray          # heads i32 at Q16, positive
+    weight: np.ndarray          # 2 * width i32 at 2^-24: w_c then w_y
+    ask: np.ndarray | None = None    # vocab * width i16 Q12
+    carry: np.ndarray | None = None  # vocab i32 Q16
 
 
 @dataclass
@@ -149,6 +182,9 @@ class Artifact:
     # SHA-256 (hex) of the container bytes a served artifact was read from (format.rs:1493);
     # None for a generated one.
     sha256: str | None = None
+    # The Hamming reads (lut-stack/6): the record's fields and one HammingRead per depth.
+    hamming: HammingSpec | None = None
+    hamming_reads: list | None = None
 
     @property
     def window(self) -> int:
@@ -278,7 +314,41 @@ def make_artifact(spec: Spec, seed: int) -> Artifact:
         for c in range(D):
             members[offsets[c]:offsets[c + 1]] = np.sort(perm[offsets[c]:offsets[c + 1]])
         art.drawer_offsets, art.drawer_members = offsets, members
+    if spec.hamming is not None:
+        art.hamming, art.hamming_reads = spec.hamming, _hamming_reads(g, spec)
     return art
+
+
+def _hamming_reads(g: Lcg, spec: Spec) -> list:
+    """Seeded reads for spec.hamming, drawn after every other table (so an artifact without reads
+    is unchanged): raw rotations in +-2^24 (about +-1 at 2^-24), margins between the record's
+    bit bounds at Q16, weights in +-2^24, and ask tables in +-2^12 at Q12 with carry gains in
+    +-2^16 at Q16."""
+    h, d, V = spec.hamming, spec.width, spec.vocab
+    if h.heads < 2 or h.heads % 2 or d % h.heads or (d // h.heads) % 4 or d // h.heads > 64:
+        raise ValueError("heads: even, at least 2, dividing the width into 4..64-coordinate heads")
+    reads = []
+    lo, hi = h.margin_bits
+    for r, depth in enumerate(h.depths):
+        rot = [_uniform_i32(g, d, 1 << 24) for _ in range(3)]
+        margin = (((g.take(h.heads) % np.uint64((hi - lo) * 65536 + 1)).astype(np.int64)
+                   + lo * 65536)).astype(np.int32)
+        margin = np.maximum(margin, 1)
+        weight = _uniform_i32(g, 2 * d, 1 << 24)
+        if not h.typed:
+            weight[d:] = 0
+        asks = h.asks is not None and h.asks[r]
+        ask = _uniform_i32(g, V * d, 1 << 12).astype(np.int16) if asks else None
+        last = r + 1 == len(h.depths)
+        carry = _uniform_i32(g, V, 1 << 16) if (asks and last and h.carry_rows) else None
+        reads.append(HammingRead(depth, rot[0], rot[1], rot[2], margin, weight, ask, carry))
+    return reads
+
+
+def hamming_reads(spec: Spec, hamming: HammingSpec, seed: int) -> list:
+    """Seeded reads for `hamming` over `spec`'s shape, drawn on their own (to add to an artifact
+    read from a container, uorlut.add_hamming)."""
+    return _hamming_reads(lcg(seed), replace(spec, hamming=hamming))
 
 
 def uniform_prompts(vocab: int, count: int, length: int, seed: int) -> np.ndarray:

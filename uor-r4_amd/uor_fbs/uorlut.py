@@ -12,12 +12,14 @@ route words (atom in the low 16 bits, axis state in the high 16 bits, codes = `c
 discrete_d11.rs:857-913), `rec_norm_gain`, `mlp_norm_gain`, `conv_taps` (4 x width grid codes),
 `conv_bias`, `gate_bias`, `decay_offset`; then `final_norm_gain` and `writer.table`.
 
-Served schemas: `uor-r4.lut-stack/4` and `/5` (FBS, snapped or raw gates/transition), and the
-turn-memory `/7` and point-key `/8` stacks, whose extra records `step_native` does not apply
-(session.rs:4327-4392 applies them only after `mark_reply_start`); the reference's loader
-accepts them for the plain step, and so does this one. Hamming reads, memory chains, bound
-contracts, address tables, Q31 records and pair rows are refused by schema, as a reader that
-does not serve them must.
+Served schemas: `uor-r4.lut-stack/4` and `/5` (FBS, snapped or raw gates/transition), `/6`
+(FBS with Hamming reads: the `hamming` record and its `hamming.d{depth}.*` sections,
+StackHamming, format.rs:229-430, read as hamming_image does, hamming.rs:58-110), and the
+turn-memory `/7` and point-key `/8` stacks (with or without Hamming reads), whose turn memory
+`step_native` does not apply (session.rs:4327-4392 applies it only after `mark_reply_start`);
+the reference's loader accepts them for the plain step, and so does this one. The Hamming place
+read (`hamming.place`), memory chains, bound contracts, address tables, Q31 records and pair
+rows are refused, as a reader that does not serve them must.
 
 Loading is host code outside the served path: it reads JSON and raw little-endian arrays and
 executes nothing from the file.
@@ -32,7 +34,7 @@ import struct
 import numpy as np
 
 from . import tables
-from .synth import Artifact, Layer, Spec
+from .synth import Artifact, HammingRead, HammingSpec, Layer, Spec
 
 MAGIC = b"UORLUT01"
 ALIGN = 64                 # format.rs:443
@@ -42,10 +44,18 @@ KINDS = {"i16": np.dtype("<i2"), "i32": np.dtype("<i4"), "u32": np.dtype("<u4")}
 SERVED = {
     "uor-r4.lut-stack/4",  # FBS, snapped gates and transition
     "uor-r4.lut-stack/5",  # FBS with raw gates or transition
+    "uor-r4.lut-stack/6",  # FBS with Hamming reads
     "uor-r4.lut-stack/7",  # + turn memory (not applied by step_native)
     "uor-r4.lut-stack/8",  # + point key (not applied by step_native)
 }
-REFUSED_RECORDS = ("hamming", "memory_chain", "address", "pair_rows", "q31", "q31_lanes", "q31_read")
+REFUSED_RECORDS = ("memory_chain", "address", "pair_rows", "q31", "q31_lanes", "q31_read")
+# The Hamming record's fields (StackHamming, format.rs:229-292, deny_unknown_fields) and the
+# exponents this engine reads (format.rs:55-59).
+HAMMING_FIELDS = {"heads", "depths", "kept", "rotation_exp", "margin_exp", "weight_exp", "copy_key",
+                  "copy_keys", "copy_latest", "copy_longest", "asks", "carry_rows", "place"}
+HAMMING_EXPS = {"rotation_exp": -24, "margin_exp": -16, "weight_exp": -24}
+ASK_CARRY_MAX = 1 << 12            # hamming.rs:1052
+MAX_READ_CACHE_BYTES = 1 << 32     # format.rs:456
 
 
 class UorlutError(ValueError):
@@ -100,7 +110,9 @@ def _check_shape(header: dict) -> dict:
     s = header["shape"]
     raw = bool(s.get("raw_gates")) or bool(s.get("raw_transition"))
     memory, point = header.get("memory") is not None, header.get("point") is not None
+    hamming = header.get("hamming") is not None
     expected = ("uor-r4.lut-stack/8" if point else "uor-r4.lut-stack/7" if memory
+                else "uor-r4.lut-stack/6" if hamming
                 else "uor-r4.lut-stack/5" if raw else "uor-r4.lut-stack/4")
     if schema != expected:
         raise UorlutError(f"schema {schema} does not match its records (expected {expected})")
@@ -123,6 +135,159 @@ def _check_shape(header: dict) -> dict:
         if not snap or snap.get("name") != "icosian" or snap.get("roots") != 120:
             raise UorlutError("a snapped transition needs transport_snap=icosian with 120 roots")
     return s
+
+
+def _check_hamming(rec: dict, s: dict) -> HammingSpec:
+    """`StackHamming::check` (format.rs:336-430) on the header's record; the place read is not
+    served by this path."""
+    if not isinstance(rec, dict) or set(rec) - HAMMING_FIELDS:
+        raise UorlutError(f"hamming: unknown fields {sorted(set(rec) - HAMMING_FIELDS)}")
+    if rec.get("place") is not None:
+        raise UorlutError("the Hamming place read (hamming.place) is not served by this path")
+    missing = {"heads", "depths", "kept", *HAMMING_EXPS} - set(rec)
+    if missing:
+        raise UorlutError(f"hamming: missing fields {sorted(missing)}")
+    d, V, L = int(s["width"]), int(s["vocab"]), len(s["pattern"])
+    heads, depths, kept = int(rec["heads"]), [int(x) for x in rec["depths"]], int(rec["kept"])
+    if heads < 2 or heads % 2 or d % heads:
+        raise UorlutError("a Hamming read needs an even head count of at least 2 that divides the width")
+    hw = d // heads
+    if hw % 4 or hw > 64:
+        raise UorlutError("a Hamming head needs whole 4-lane blocks and at most 64 coordinates")
+    copy_key = int(rec.get("copy_key", 1))
+    if copy_key not in (1, 2):
+        raise UorlutError("a Hamming copy key names 1 or 2 tokens")
+    keys = rec.get("copy_keys")
+    if keys is not None:
+        keys = [int(k) for k in keys]
+        if (copy_key != 1 or len(keys) != heads // 2 or any(k not in (1, 2) for k in keys)
+                or all(k == keys[0] for k in keys)):
+            raise UorlutError("mixed Hamming copy keys name 1 or 2 tokens for each copy head, differ, "
+                              "and leave copy_key at 1")
+    per_head = keys or [copy_key] * (heads // 2)
+    if 2 in per_head and hw % 8:
+        raise UorlutError("copy key 2 needs heads of whole 8-coordinate blocks")
+    latest, longest = bool(rec.get("copy_latest", False)), rec.get("copy_longest")
+    if longest is not None:
+        longest = tuple(int(x) for x in longest)
+        if not latest or any(k != 1 for k in per_head) or len(longest) != 2 or max(longest) >= V:
+            raise UorlutError("the longest rule needs the latest exact rule, one-token copy keys and "
+                              "a marker of two vocabulary ids")
+    if not depths or any(b <= a for a, b in zip(depths, depths[1:])) or not all(1 <= x <= L for x in depths):
+        raise UorlutError("Hamming read depths must be strictly increasing, from 1 to the layer count")
+    if kept == 0:
+        raise UorlutError("a Hamming read keeps at least one position")
+    asks = rec.get("asks")
+    if asks is not None:
+        asks = tuple(bool(a) for a in asks)
+        if len(asks) != len(depths) or not any(asks):
+            raise UorlutError("Hamming ask heads name one flag per read, not all off")
+    reach = rec.get("carry_rows")
+    if reach is not None:
+        reach = int(reach)
+        if depths[-1] != L:
+            raise UorlutError("a Hamming question carry is served on the readout read only")
+        if not (asks and asks[-1]):
+            raise UorlutError("a Hamming question carry needs its read to ask")
+        if not 1 <= reach <= ASK_CARRY_MAX:
+            raise UorlutError("a Hamming question carry reaches from 1 to ASK_CARRY_MAX rows")
+    for k, v in HAMMING_EXPS.items():
+        if rec.get(k) != v:
+            raise UorlutError("the Hamming read's exponents are not this engine's")
+    return HammingSpec(heads=heads, depths=tuple(depths), kept=kept, copy_key=copy_key,
+                       copy_keys=None if keys is None else tuple(keys), copy_latest=latest,
+                       copy_longest=longest, asks=asks, carry_rows=reach or 0)
+
+
+def _hamming_reads(h: HammingSpec, tabs: dict, V: int, d: int, context: int) -> list:
+    """Every read's sections at the lengths its record implies (hamming_image, hamming.rs:58-110;
+    AskImage::checked :1069-1095), margins positive, and the payload caches within the session
+    read cache (check_payload_cache :1538-1549)."""
+    reads, typed = [], 0
+    for r, depth in enumerate(h.depths):
+        def section(part, kind, n, present=True):
+            name = f"hamming.d{depth}.{part}"
+            if name not in tabs:
+                if present:
+                    raise UorlutError(f"missing section {name}")
+                return None
+            if not present:
+                raise UorlutError(f"{name}: present, but the record does not name it")
+            t = tabs[name]
+            if t.dtype != KINDS[kind] or len(t) != n:
+                raise UorlutError(f"{name}: {len(t)} {t.dtype} values, expected {n} {kind}")
+            return t
+        margin = section("margin", "i32", h.heads).astype(np.int32)
+        if np.any(margin <= 0):
+            raise UorlutError(f"hamming.d{depth}.margin: a margin is not positive")
+        asks = bool(h.asks and h.asks[r])
+        carries = bool(h.carry_rows) and r + 1 == len(h.depths)
+        ask = section("ask", "i16", V * d, asks)
+        carry = section("carry", "i32", V, carries)
+        weight = section("weight", "i32", 2 * d).astype(np.int32)
+        typed += int(not asks and np.any(weight[d:] != 0))
+        reads.append(HammingRead(
+            depth=depth, query_rotation=section("query_rotation", "i32", d).astype(np.int32),
+            key_rotation=section("key_rotation", "i32", d).astype(np.int32),
+            value_rotation=section("value_rotation", "i32", d).astype(np.int32), margin=margin,
+            weight=weight, ask=None if ask is None else ask.astype(np.int16),
+            carry=None if carry is None else carry.astype(np.int32)))
+    if typed * context * d * 8 > MAX_READ_CACHE_BYTES:
+        raise UorlutError("the Hamming type heads' payload cache exceeds the session read cache's 4 GiB")
+    return reads
+
+
+def add_hamming(source, h: HammingSpec, reads: list) -> bytes:
+    """A container with Hamming reads added: every section of `source` byte for byte, each read's
+    `hamming.d{depth}.*` sections appended, the header's `hamming` record written and its schema
+    moved to `/6` when it has no turn memory (as the reference's exporter names a Hamming stack,
+    format.rs:2595-2607, and its section adders append, :2730-2783). The result is read back."""
+    data = bytes(source if isinstance(source, (bytes, bytearray)) else open(source, "rb").read())
+    header, _ = parse(data)
+    if header.get("hamming") is not None:
+        raise UorlutError("the container already has Hamming reads")
+    (declared,) = struct.unpack("<Q", data[8:16])
+    end = 16 + declared
+    body = bytearray(data[end + (ALIGN - end % ALIGN) % ALIGN:])
+    tables_ = list(header["tables"])
+
+    def push(name, arr, kind):
+        nonlocal body
+        body += b"\0" * ((ALIGN - len(body) % ALIGN) % ALIGN)
+        raw = np.ascontiguousarray(arr, KINDS[kind]).tobytes()
+        tables_.append({"name": name, "kind": kind, "len": int(np.asarray(arr).size),
+                        "span": {"offset": len(body), "bytes": len(raw)}})
+        body += raw
+
+    for r in reads:
+        p = f"hamming.d{r.depth}."
+        for part in ("query_rotation", "key_rotation", "value_rotation", "margin", "weight"):
+            push(p + part, getattr(r, part), "i32")
+        if r.ask is not None:
+            push(p + "ask", r.ask, "i16")
+        if r.carry is not None:
+            push(p + "carry", r.carry, "i32")
+    rec = {"heads": h.heads, "depths": list(h.depths), "kept": h.kept, **HAMMING_EXPS}
+    if h.copy_key != 1:
+        rec["copy_key"] = h.copy_key
+    if h.copy_keys is not None:
+        rec["copy_keys"] = list(h.copy_keys)
+    if h.copy_latest:
+        rec["copy_latest"] = True
+    if h.copy_longest is not None:
+        rec["copy_longest"] = list(h.copy_longest)
+    if h.asks is not None:
+        rec["asks"] = list(h.asks)
+    if h.carry_rows:
+        rec["carry_rows"] = h.carry_rows
+    header = dict(header, tables=tables_, hamming=rec)
+    if header.get("memory") is None and header.get("point") is None:
+        header["schema"] = "uor-r4.lut-stack/6"
+    hb = json.dumps(header).encode()
+    out = MAGIC + struct.pack("<Q", len(hb)) + hb
+    out += b"\0" * ((ALIGN - len(out) % ALIGN) % ALIGN) + bytes(body)
+    load(out)
+    return out
 
 
 def load(source) -> Artifact:
@@ -172,7 +337,11 @@ def load(source) -> Artifact:
     spec = Spec(vocab=V, width=d, mlp=m, layers=L, context=int(s["context"]),
                 kept=int(s["kept_cells"]), head=1 if s["head"] == "native_vector_nearest" else 0,
                 raw_gates=bool(s.get("raw_gates")), raw_transition=bool(s.get("raw_transition")))
-    return Artifact(spec=spec, seed=-1, layers=layers, final_gain=codes("final_norm_gain", d),
-                    writer_table=table("writer.table", "i16", V * d).astype(np.int16),
-                    table_i8=None, eps_mantissa=int(eps["mantissa"]), eps_exp=int(eps["exp"]),
-                    sha256=hashlib.sha256(data).hexdigest())
+    art = Artifact(spec=spec, seed=-1, layers=layers, final_gain=codes("final_norm_gain", d),
+                   writer_table=table("writer.table", "i16", V * d).astype(np.int16),
+                   table_i8=None, eps_mantissa=int(eps["mantissa"]), eps_exp=int(eps["exp"]),
+                   sha256=hashlib.sha256(data).hexdigest())
+    if header.get("hamming") is not None:
+        art.hamming = _check_hamming(header["hamming"], s)
+        art.hamming_reads = _hamming_reads(art.hamming, tabs, V, d, int(s["context"]))
+    return art
