@@ -51,6 +51,11 @@ D11_TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "d11_score_rows_m1_traffic.
 REPLAY_BYTES = 6 << 30
 CONFIG_SHAPES = {"c1": (1, 256, 256), "c2": (1024, 512, 512), "c3": (1024, 1024, 1024),
                  "c4": (1 << 20, 128, 0), "c5": (16384, 4096, 4096)}
+# The Hamming reads in the served step (--config hamming): C3's artifact with a typed stream read
+# after layer 3 and a typed readout read, 8 heads (4 copy, 4 type) keeping 16 positions each;
+# (sequences, prompt, decode steps) as C3.
+HAMMING_READS = dict(heads=8, depths=(3, 6), kept=16)
+HAMMING_SHAPE = (1024, 1024, 1024)
 # The discrete M1 panel scorer (uor_d11_score_rows): the reference's ft/dev panel size, the M1
 # container's shape (vocabulary 4,096, 4 blocks, context 192, 8 kept cells, relation read
 # keeping 8 with 1 sweep, 19-table trunk), rows of 186-192 tokens (the published run's mean
@@ -122,7 +127,8 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=3)
     p.add_argument("--warmup", type=int, default=1)
-    p.add_argument("--config", default="c3", choices=sorted(CONFIG_SHAPES) + ["m1", "copy"],
+    p.add_argument("--config", default="c3",
+                   choices=sorted(CONFIG_SHAPES) + ["m1", "copy", "hamming"],
                    help="BASELINE's configs: c3 (default) is the metric's; c4 scores rows")
     p.add_argument("--batch", type=int, default=None, help="sequences (c4: rows); config's default")
     p.add_argument("--prompt", type=int, default=None, help="prompt tokens (c4: row length)")
@@ -150,6 +156,7 @@ def parse():
                    help="m1: (key, token) entries in each of the six trunk tables it reads")
     a = p.parse_args()
     batch, prompt, gen = CONFIG_SHAPES.get(a.config, (D11_ROWS, 192, 0) if a.config == "m1"
+                                           else HAMMING_SHAPE if a.config == "hamming"
                                            else (4096, 1024, 0))
     a.batch = batch if a.batch is None else a.batch
     a.prompt = prompt if a.prompt is None else a.prompt
@@ -661,6 +668,136 @@ def copy_main(a, torch, oracle) -> dict:
     return out
 
 
+def hamming_bytes_per_token(spec, ham, mean_candidates: float, t_mean: float) -> dict:
+    """HBM bytes one decoded token moves with the Hamming reads, by definition: the base path's
+    (algorithmic_bytes_per_token) plus, per read, the kept positions' table rows (copy heads,
+    2 B a channel) and payloads (type heads, 8 B a channel: read, and this row's written), and
+    the session's token ids (4 B a position). The key codes of the earlier positions are
+    gathered from a per-read table of vocab x heads words that stays in the L2 caches (2 MiB at
+    C3): counted apart, as `code_bytes`."""
+    d, copy, types, kept = spec.width, ham.heads // 2, ham.heads - ham.heads // 2, ham.kept
+    reads = len(ham.depths)
+    per_read = copy * kept * d * 2 + types * kept * d * 8 + d * 8 + 4 * t_mean
+    return {"base": algorithmic_bytes_per_token(spec, mean_candidates),
+            "reads": reads * per_read, "code_bytes": reads * ham.heads * 8 * t_mean}
+
+
+def hamming_main(a, torch, oracle) -> dict:
+    """The Hamming reads inside the served step: C3's artifact with HAMMING_READS; a step is
+    `gen` greedy steps of every sequence resumed from its prefilled session (state, window ring,
+    token stream and payload caches; uor_fbs_decode_stream_async with the payloads updated in
+    place)."""
+    from uor_fbs import hip, synth
+    spec = replace(synth.CONFIGS["c3"], context=a.prompt + a.gen + 1,
+                   hamming=synth.HammingSpec(**HAMMING_READS))
+    art = synth.make_artifact(spec, a.seed)
+    prompts = synth.zipf_prompts(spec.vocab, a.batch, a.prompt, a.seed + 1)
+    model = hip.Model(art, device=0)
+    L = hip.lib()
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream(dev)
+    sp = C.c_void_p(stream.cuda_stream)
+    B, G = a.batch, a.gen
+    ptr = lambda t: None if t is None else C.c_void_p(t.data_ptr())  # noqa: E731
+
+    def check(code):
+        if code:
+            raise hip.FbsError(code, L.uor_fbs_last_error().decode())
+
+    d_prompts = torch.from_numpy(prompts.view(np.int32)).to(dev)
+    state = torch.zeros((B, model.state_words), dtype=torch.int64, device=dev)
+    hist = torch.zeros((B, model.history_words), dtype=torch.int32, device=dev)
+    pos = torch.zeros(B, dtype=torch.int32, device=dev)
+    tok = torch.zeros((B, model.stream_words), dtype=torch.int32, device=dev)
+    pay = torch.zeros((B, model.payload_words), dtype=torch.int64, device=dev)
+    first = torch.zeros((B, 1), dtype=torch.int32, device=dev)
+    status = torch.zeros(B, dtype=torch.int32, device=dev)
+    log(f"hamming: {B} sequences, payload caches {pay.numel() * 8 / 2**30:.1f} GiB")
+    t0 = time.perf_counter()
+    check(L.uor_fbs_decode_stream_async(model.handle, ptr(d_prompts), B, a.prompt, 0, ptr(first),
+                                        None, None, None, None, None, ptr(state), ptr(hist),
+                                        ptr(pos), ptr(tok), ptr(pay), ptr(status), sp))
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    assert int(status.abs().sum()) == 0, "prefill failed"
+    log(f"hamming: prefill {prefill_s:.1f} s")
+    reply = torch.zeros((B, G), dtype=torch.int32, device=dev)
+
+    def step():
+        check(L.uor_fbs_decode_stream_async(model.handle, ptr(first), B, 1, G - 1, ptr(reply),
+                                            ptr(state), ptr(hist), ptr(pos), ptr(tok), ptr(pay),
+                                            None, None, None, None, ptr(pay), ptr(status), sp))
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(a.steps)]
+    t0 = time.perf_counter()
+    for s_, e_ in ev:
+        s_.record(stream)
+        step()
+        e_.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    assert int(status.abs().sum()) == 0, "decode failed"
+    launch_ms = [s_.elapsed_time(e_) for s_, e_ in ev]
+    ms_per_step = wall * 1e3 / a.steps
+    tokens = B * G
+    # Candidate rows per token from a teacher-forced replay of evenly spaced sequences.
+    host_reply = reply.cpu().numpy().view(np.uint32)
+    host_first = first.cpu().numpy().view(np.uint32)
+    ids = np.linspace(0, B - 1, min(B, 64)).astype(np.int64)
+    replay = np.concatenate([prompts[ids], host_first[ids], host_reply[ids, :-1]], axis=1)
+    _, kept, _ = model.sequences(replay, want_query=False)
+    mean_cand = float(art.drawer_sizes()[kept[:, a.prompt:, :].astype(np.int64)].sum(-1).mean())
+    bpt = hamming_bytes_per_token(spec, spec.hamming, mean_cand, a.prompt + G / 2)
+    total = bpt["base"] + bpt["reads"]
+    achieved = total * tokens / (float(np.mean(launch_ms)) / 1e3) / 1e9
+    Q = (spec.width // 4 + 63) // 64
+    Sw = 1
+    while Sw < spec.width // 32:
+        Sw *= 2
+    out = {
+        "metric": f"decoded tokens/sec at batch {B}, width {spec.width}, with Hamming reads (1 GPU)",
+        "value": round(tokens / (ms_per_step / 1e3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int64",
+        "data": "synthetic (seeded integer artifact and Hamming reads, Zipf prompts)",
+        "config": {"workload": f"hamming: c3 artifact with reads {HAMMING_READS} at batch {B}: "
+                               f"prefilled {a.prompt}-token prompts, {G} greedy decode steps per "
+                               "timed step", "batch": B, "prompt": a.prompt, "gen": G,
+                   "width": spec.width, "layers": spec.layers, "vocab": spec.vocab,
+                   "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_token": {k: round(v, 1) for k, v in bpt.items()},
+                     "mean_candidate_rows": round(mean_cand, 1),
+                     "kernel": f"fbs_decode_ham<{Q}, {Sw}>",
+                     "launch_ms": [round(x, 3) for x in launch_ms]},
+        "prefill_tokens_per_s": round(B * a.prompt / prefill_s, 1),
+    }
+    if not a.no_cpu:
+        _, host = cpu_threads(a)
+        n_cpu = 2
+        t0 = time.perf_counter()
+        want = oracle.decode(art, prompts[:n_cpu], 8, threads=1)
+        per_tok = (time.perf_counter() - t0) / (n_cpu * (a.prompt + 8))
+        proto, w = cpu_protocol(lambda: oracle.decode(art, prompts[:n_cpu], 8, threads=n_cpu),
+                                n_cpu * (a.prompt + 8), min(a.cpu_runs, 3),
+                                same=lambda x, y: np.array_equal(x["reply"], y["reply"]))
+        same = np.array_equal(w["reply"][:, 1:], host_reply[:n_cpu, :8]) and \
+            np.array_equal(w["reply"][:, :1], host_first[:n_cpu])
+        out["cpu_baseline"] = {"value": proto["median_per_s"], "unit": "tokens/s",
+                               "cores": n_cpu, **host, "kind": "port",
+                               "sample": f"{n_cpu} sequences: the prompt and 8 decode steps, oracle "
+                                         f"C restatement on {n_cpu} threads; value = integer median "
+                                         f"over {min(a.cpu_runs, 3)} timed runs after one warm-up "
+                                         f"({per_tok * 1e3:.2f} ms a token on one thread)",
+                               "protocol": proto, "tokens_equal_gpu": bool(same)}
+    return out
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -681,6 +818,9 @@ def main():
         return
     if a.config == "copy":
         print(json.dumps(copy_main(a, torch, oracle)))
+        return
+    if a.config == "hamming":
+        print(json.dumps(hamming_main(a, torch, oracle)))
         return
     spec = replace(synth.CONFIGS[a.config], context=a.prompt + a.gen + 1)
     art = synth.make_artifact(spec, a.seed)
@@ -876,8 +1016,9 @@ def main():
     if a.serve_steps:
         # The serving loop: every sequence is a session in a device slot (a fixed permutation of
         # the slots), and each launch steps all of them by one token from their slot state,
-        # updated in place (uor_fbs_decode_slots_async, serve_step for the whole batch). From
-        # the same prefilled state, its tokens must equal the decode's replies.
+        # updated in place with each slot's serving cache (uor_fbs_serve_slots_async, serve_step
+        # for the whole batch; the cache starts empty). From the same prefilled state, its tokens
+        # must equal the decode's replies. The same launches without the cache are timed beside.
         K = min(a.serve_steps, G)
         perm = np.random.default_rng(a.seed).permutation(B).astype(np.uint32)
         d_slots = u32(perm)
@@ -892,23 +1033,34 @@ def main():
         ring_rows[src] = torch.arange(W_)
         s_hist[d_slots.long()] = hist.view(B, L_, W_, d_)[:, :, ring_rows.to(dev)].reshape(B, -1)
         s_pos[d_slots.long()] = pos
-        served = torch.zeros((K + 1, B), dtype=torch.int32, device=dev)
-        served[0] = first[:, 0]
-        sv_start = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
-        sv_end = [torch.cuda.Event(enable_timing=True) for _ in range(K)]
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for k in range(K):
-            sv_start[k].record(stream)
-            check(L.uor_fbs_decode_slots_async(model.handle, ptr(d_slots), B, B, ptr(served[k]), 1, 0,
-                                               ptr(served[k + 1]), ptr(s_state), ptr(s_hist),
-                                               ptr(s_pos), None, None, ptr(status), sp))
-            sv_end[k].record(stream)
-        torch.cuda.synchronize()
-        serve_wall = time.perf_counter() - t0
-        assert int(status.abs().sum()) == 0, "serving loop failed"
-        serve_ms = [s_.elapsed_time(e_) for s_, e_ in zip(sv_start, sv_end)]
-        same_serve = np.array_equal(served[1:].cpu().numpy().view(np.uint32).T, host_reply[:, :K])
+        saved = [t.clone() for t in (s_state, s_hist, s_pos)]
+        cache = torch.zeros((B, int(L.uor_fbs_slot_cache_bytes(model.handle))), dtype=torch.uint8,
+                            device=dev)
+
+        def serve_loop(cached: bool):
+            for t, v in zip((s_state, s_hist, s_pos), saved):
+                t.copy_(v)
+            served = torch.zeros((K + 1, B), dtype=torch.int32, device=dev)
+            served[0] = first[:, 0]
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(K)]
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for k in range(K):
+                ev[k][0].record(stream)
+                check(L.uor_fbs_serve_slots_async(
+                    model.handle, ptr(d_slots), B, B, ptr(served[k]), 1, 0, ptr(served[k + 1]),
+                    ptr(s_state), ptr(s_hist), ptr(s_pos), ptr(cache) if cached else None, None,
+                    None, None, ptr(status), sp))
+                ev[k][1].record(stream)
+            torch.cuda.synchronize()
+            wall_ = time.perf_counter() - t0
+            assert int(status.abs().sum()) == 0, "serving loop failed"
+            same_ = np.array_equal(served[1:].cpu().numpy().view(np.uint32).T, host_reply[:, :K])
+            return wall_, [s_.elapsed_time(e_) for s_, e_ in ev], same_
+
+        bare_wall, bare_ms, bare_same = serve_loop(False)
+        serve_wall, serve_ms, same_serve = serve_loop(True)
         out["serving"] = {
             "tokens_per_s": round(B * K / serve_wall, 1),
             "ms_per_launch": round(float(np.mean(serve_ms)), 4),
@@ -917,6 +1069,11 @@ def main():
             "workload": f"{B} sessions in permuted device slots, one token each per launch, "
                         f"{K} launches from the prefilled state",
             "tokens_equal_decode": bool(same_serve),
+            "cache": "each slot's window sums for its next step and the writer's memory, kept "
+                     "between launches (empty at the first)",
+            "without_cache": {"tokens_per_s": round(B * K / bare_wall, 1),
+                              "ms_per_launch": round(float(np.mean(bare_ms)), 4),
+                              "tokens_equal_decode": bool(bare_same)},
         }
         if not same_serve:
             print("bench.py: the serving loop's tokens differ from the decode's", file=sys.stderr)

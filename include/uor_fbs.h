@@ -278,6 +278,32 @@ int uor_fbs_decode_stream(uor_fbs_handle *handle, const uint32_t *prompts, uint3
                           const int64_t *in_payloads, int64_t *out_state, int32_t *out_history,
                           uint32_t *out_position, uint32_t *out_stream, int64_t *out_payloads);
 
+/* ---- The serving loop with per-slot caches and the context slide.
+ * uor_fbs_decode_slots_async's slots, plus two things a serving loop keeps between launches:
+ * - `cache`: capacity * uor_fbs_slot_cache_bytes(handle) device bytes, zero-filled by the caller
+ *   before its first use (a zero entry holds nothing). Each slot's entry keeps the window sums
+ *   its last launch formed for the slot's next step, tagged with the position they hold for, so
+ *   a launch that starts there does not sum the window again, and the writer's memory of its
+ *   last query, which depends on the model alone. A caller that writes a slot's state, history
+ *   or position itself (restoring or resetting a session) zeroes the slot's entry first (its
+ *   first 4 bytes suffice). An entry belongs to this handle's model. NULL: no cache (as
+ *   uor_fbs_decode_slots_async).
+ * - `slide`: capacity bytes, nonzero for a slot whose session continues past a full context
+ *   (IntegerStackSession::set_context_slide, session.rs:2391-2402, :4143-4151: the step does not
+ *   refuse at the context, and the position keeps counting; nothing else in the step reads it
+ *   beyond the window ring's slot). NULL: no slot slides. The reference refuses the slide for a
+ *   model with Hamming reads or a turn memory; this entry refuses Hamming models and the caller
+ *   (uor_fbs/session.py) the rest.
+ * No counterpart beyond those: the reference's sessions keep their window sums implicitly (a CPU
+ * session steps one token at a time). Device buffers. */
+uint64_t uor_fbs_slot_cache_bytes(const uor_fbs_handle *handle);
+int uor_fbs_serve_slots_async(uor_fbs_handle *handle, const uint32_t *slots, uint32_t sequences,
+                              uint32_t capacity, const uint32_t *prompts, uint32_t prompt_len,
+                              uint32_t gen, uint32_t *out_reply, int64_t *state, int32_t *history,
+                              uint32_t *position, void *cache, const uint8_t *slide,
+                              uint32_t *out_kept, int32_t *out_query, int32_t *status,
+                              void *stream);
+
 /* Teacher-forced next-token scoring: for each row of `len` tokens, position t's choice is
  * compared with row[t+1] (t < len-1); `out_matches` gets the total count of equal pairs.
  * `out_argmin` (nullable) gets every position's choice, rows*len. Host buffers. */

@@ -883,6 +883,7 @@ typedef struct {
   uint32_t *tokens;  /* the session's tokens x_0..x_{position-1} (IntegerStackSession::tokens) */
   int64_t *payloads; /* [typed read][context][width]: the type heads' payloads (hamming_payloads) */
   int64_t *normed;   /* width: the final norm's output (the readout read's input) */
+  int slide;         /* a full context continues (set_context_slide, session.rs:2391-2402) */
 } S;
 
 static void session_alloc(const O *o, S *s) {
@@ -990,8 +991,10 @@ static int step(const O *o, S *s, uint32_t token, uint32_t *out_token) {
   const uor_fbs_model *m = o->m;
   uint32_t d = o->d;
   if (token >= m->vocab) return UOR_FBS_ERR_TOKEN;
-  if (s->position >= m->context) return UOR_FBS_ERR_CONTEXT;
-  s->tokens[s->position] = token;
+  /* A session with the slide on steps past its context (session.rs:4143-4151); a model with
+   * Hamming reads refuses the slide (can_slide_tokens, :1146-1151), so its tokens stay inside. */
+  if (s->position >= m->context && !s->slide) return UOR_FBS_ERR_CONTEXT;
+  if (o->ham) s->tokens[s->position] = token;
   const size_t t = s->position;
   for (uint32_t i = 0; i < d; i++) s->x[i] = to_exp_i32(row_value(o, token, i), Q12_EXP, RESIDUAL_EXP);
   for (uint32_t l = 0; l < o->L; l++) {
@@ -1051,6 +1054,7 @@ typedef struct {
   const int64_t *in_payloads;  /* [n][typed reads][context][width] */
   int64_t *out_payloads;
   uint64_t matches;
+  int slide;
   int tid, threads, status;
 } Job;
 
@@ -1061,6 +1065,7 @@ static void *run_job(void *arg) {
   uint64_t sw = (uint64_t)o->L * d, hw = (uint64_t)o->L * o->W * d;
   S s;
   session_alloc(o, &s);
+  s.slide = j->slide;
   for (uint64_t i = (uint64_t)j->tid; i < j->n && j->status == 0; i += (uint64_t)j->threads) {
     session_reset(o, &s);
     s.candidates = 0;
@@ -1179,6 +1184,39 @@ int fbs_oracle_decode(const uor_fbs_model *m, const uor_fbs_ext *ext, const uint
   j.out_history = out_history;
   j.out_position = out_position;
   j.out_candidates = out_candidates;
+  int status = run_jobs(&j, threads);
+  unresolve(&o);
+  return status;
+}
+
+/* fbs_oracle_decode with every session's context slide on (set_context_slide,
+ * session.rs:2391-2402): a full context continues; refused for a model with Hamming reads. */
+int fbs_oracle_decode_slide(const uor_fbs_model *m, const uor_fbs_ext *ext, const uint32_t *prompts,
+                            uint32_t sequences, uint32_t prompt_len, uint32_t gen,
+                            uint32_t *out_reply, const int64_t *in_state, const int32_t *in_history,
+                            const uint32_t *in_position, int64_t *out_state, int32_t *out_history,
+                            uint32_t *out_position, int threads) {
+  O o;
+  resolve(&o, m, ext);
+  if (o.ham) {
+    unresolve(&o);
+    return UOR_FBS_ERR_SHAPE;
+  }
+  Job j = {0};
+  j.o = &o;
+  j.kind = 1;
+  j.slide = 1;
+  j.tokens = prompts;
+  j.n = sequences;
+  j.prompt_len = prompt_len;
+  j.gen = gen;
+  j.out_reply = out_reply;
+  j.in_state = in_state;
+  j.in_history = in_history;
+  j.in_position = in_position;
+  j.out_state = out_state;
+  j.out_history = out_history;
+  j.out_position = out_position;
   int status = run_jobs(&j, threads);
   unresolve(&o);
   return status;

@@ -55,6 +55,13 @@ int fbs_oracle_score(const uor_fbs_model *m, const uor_fbs_ext *ext, const uint3
  * the first position of them valid) and the typed reads' payload caches
  * ([n][typed][context][width], typed = fbs_oracle_hamming_typed), resumed and exported beside the
  * state as IntegerStackSession keeps them (session.rs:2232-2252). */
+/* fbs_oracle_decode with the context slide on for every session (session.rs:2391-2402); a model
+ * with Hamming reads is refused (UOR_FBS_ERR_SHAPE). */
+int fbs_oracle_decode_slide(const uor_fbs_model *m, const uor_fbs_ext *ext, const uint32_t *prompts,
+                            uint32_t sequences, uint32_t prompt_len, uint32_t gen,
+                            uint32_t *out_reply, const int64_t *in_state, const int32_t *in_history,
+                            const uint32_t *in_position, int64_t *out_state, int32_t *out_history,
+                            uint32_t *out_position, int threads);
 int fbs_oracle_decode_stream(const uor_fbs_model *m, const uor_fbs_ext *ext,
                              const uint32_t *prompts, uint32_t sequences, uint32_t prompt_len,
                              uint32_t gen, uint32_t *out_reply, const int64_t *in_state,

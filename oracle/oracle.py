@@ -59,6 +59,7 @@ def lib():
         L.fbs_oracle_writer.argtypes = [P, P, P, P, P]
         L.fbs_oracle_writer.restype = C.c_uint32
         u32, i32, i64, u64 = C.c_uint32, C.c_int32, C.c_int64, C.c_uint64
+        L.fbs_oracle_decode_slide.argtypes = [P, P, P, u32, u32, u32, P, P, P, P, P, P, P, C.c_int]
         L.fbs_oracle_decode_stream.argtypes = [P, P, P, u32, u32, u32, P, P, P, P, P, P, P, P, P,
                                                P, P, C.c_int]
         L.fbs_oracle_hamming_typed.argtypes = [P, P]
@@ -110,8 +111,10 @@ def sequences(art, tokens: np.ndarray, threads: int = 1, image: Image | None = N
 
 
 def decode(art, prompts: np.ndarray, gen: int, threads: int = 1, image: Image | None = None,
-           in_state=None, in_history=None, in_position=None, want_state: bool = True):
-    """Oracle greedy decode: dict(status, reply [S, gen+1], state, history, position, candidates)."""
+           in_state=None, in_history=None, in_position=None, want_state: bool = True,
+           slide: bool = False):
+    """Oracle greedy decode: dict(status, reply [S, gen+1], state, history, position, candidates);
+    `slide`: every session's context slide on (a full context continues)."""
     img = image or Image(art)
     prompts = np.ascontiguousarray(prompts, dtype=np.uint32)
     S, plen = prompts.shape
@@ -121,6 +124,15 @@ def decode(art, prompts: np.ndarray, gen: int, threads: int = 1, image: Image | 
     hist = np.zeros((S, s.layers * s.window * s.width), np.int32) if want_state else None
     pos = np.zeros(S, np.uint32) if want_state else None
     cand = np.zeros(S, np.uint64)
+    conv = lambda a, t: None if a is None else np.ascontiguousarray(a, t)  # noqa: E731
+    in_state, in_history = conv(in_state, np.int64), conv(in_history, np.int32)
+    in_position = conv(in_position, np.uint32)
+    if slide:
+        st = lib().fbs_oracle_decode_slide(
+            C.addressof(img.model), img.ext_ptr() and C.addressof(img.ext), _vp(prompts), S, plen,
+            gen, _vp(reply), _vp(in_state), _vp(in_history), _vp(in_position), _vp(state),
+            _vp(hist), _vp(pos), threads)
+        return dict(status=st, reply=reply, state=state, history=hist, position=pos, candidates=None)
     st = lib().fbs_oracle_decode(C.addressof(img.model), img.ext_ptr() and C.addressof(img.ext),
                                  _vp(prompts), S, plen, gen, _vp(reply), _vp(in_state),
                                  _vp(in_history), _vp(in_position), _vp(state), _vp(hist),

@@ -319,3 +319,23 @@ def test_the_reads_move_the_decode_and_a_resumed_stream_continues_it(case):
     st, tok, _, _ = oracle.sequences(art, rows)
     assert st == 0
     assert np.array_equal(tok[:, 9:], whole["reply"])
+
+
+def test_the_context_slide_continues_as_an_unbounded_context():
+    """set_context_slide (session.rs:2391-2402, :4143-4151): a full context continues; nothing
+    else in the step reads the position past its ring slot, so the slid decode equals the decode
+    of the same weights with a context that never fills. Without the slide the step refuses at
+    the bound (status 2), and a model with Hamming reads refuses the slide (can_slide_tokens,
+    :1146-1151)."""
+    small = synth.make_artifact(replace(BASE, context=16, window=5), 61)
+    big = replace(small, spec=replace(small.spec, context=200))
+    prompts = synth.uniform_prompts(BASE.vocab, 3, 9, 62)
+    slid = oracle.decode(small, prompts, 40, slide=True)
+    assert slid["status"] == 0
+    want = oracle.decode(big, prompts, 40)
+    for k in ("reply", "state", "history", "position"):
+        assert np.array_equal(slid[k], want[k]), k
+    assert int(slid["position"][0]) == 9 + 40 > 16
+    assert oracle.decode(small, prompts, 40)["status"] == 2
+    ham = make(BASE, 63, heads=4, depths=(1,), kept=4)
+    assert oracle.decode(ham, prompts, 4, slide=True)["status"] == 4

@@ -227,3 +227,91 @@ def test_session_slots_are_checked_on_the_host(art):
         pool.position.zero([3])
     with pytest.raises(IndexError):
         pool.position.download(row=3)
+
+
+def test_a_slid_session_equals_the_oracle(art):
+    """set_context_slide (session.rs:2391-2402): a session at its context continues; its tokens,
+    state, window and position equal the oracle's sliding decode, one token per launch through
+    the pool's serving cache."""
+    small = replace(art, spec=replace(art.spec, context=16))
+    prompts = synth.uniform_prompts(SPEC.vocab, 2, 10, 91)
+    G = 30
+    want = oracle.decode(small, prompts, G, slide=True)
+    assert want["status"] == 0
+    model = hip.Model(small)
+    pool = SessionPool(model, capacity=4)
+    plain = Session(pool)
+    plain.feed(prompts[0])
+    with pytest.raises(SessionError) as e:
+        for _ in range(G):
+            plain.serve_step(int(prompts[0, 0]))
+    assert e.value.kind == "ContextFull" and plain.position == 16
+    for i in range(2):
+        s = Session(pool)
+        s.set_context_slide(True)
+        got = [s.feed(prompts[i]).token]
+        for _ in range(G):
+            got.append(s.serve_step(got[-1])[0])
+        np.testing.assert_array_equal(np.array(got, np.uint32), want["reply"][i])
+        st = s.save_state()
+        np.testing.assert_array_equal(np.concatenate([l.state for l in st.layers]), want["state"][i])
+        np.testing.assert_array_equal(np.concatenate([l.history for l in st.layers]), want["history"][i])
+        assert st.position == want["position"][i] == 10 + G
+        assert len(st.tokens) == 16
+        s.reset()
+        assert s.slide  # reset keeps the caller's setting
+        s.close()
+
+
+def test_the_slide_is_refused_where_the_reference_refuses_it(art):
+    ham = synth.make_artifact(replace(SPEC, hamming=synth.HammingSpec(heads=4, depths=(1,), kept=4)), 3)
+    s = Session(SessionPool(hip.Model(ham), capacity=1))
+    with pytest.raises(SessionError):
+        s.set_context_slide(True)
+    mem = replace(art, turn_memory=True)
+    s = Session(SessionPool(hip.Model(mem), capacity=1))
+    with pytest.raises(SessionError):
+        s.set_context_slide(True)
+
+
+def test_the_serving_cache_equals_launches_without_it(art):
+    """uor_fbs_serve_slots_async with each slot's cache (window sums for the next step, writer
+    memory) against the same entry without one, one token a launch for 12 launches over
+    scrambled slots, and both against the batched decode. (Slots rewritten by the caller, whose
+    cache entries SessionPool.write zeroes, continue bit for bit in the snapshot tests above.)"""
+    n, cap, P, K = 5, 9, 8, 12
+    model = hip.Model(art)
+    L = hip.lib()
+    prompts = synth.uniform_prompts(SPEC.vocab, n, P, 95)
+    want = model.decode(prompts, gen=K)
+    slots = np.array([7, 2, 5, 0, 8], np.uint32)
+    pools = []
+    for cached in (True, False):
+        st = DeviceArray((cap, model.state_words), np.int64)
+        hi = DeviceArray((cap, model.history_words), np.int32)
+        po = DeviceArray(cap, np.uint32)
+        ca = DeviceArray((cap, int(L.uor_fbs_slot_cache_bytes(model.handle))), np.uint8)
+        for a in (st, hi, po, ca):
+            a.zero()
+        pools.append((st, hi, po, ca if cached else None))
+    d_slots = DeviceArray(n, np.uint32)
+    d_slots.upload(slots)
+    status = DeviceArray(n, np.int32)
+    outs = []
+    for st, hi, po, ca in pools:
+        toks = prompts
+        got = []
+        for k in range(K + 1):
+            d_tok = DeviceArray(toks.size, np.uint32)
+            d_tok.upload(np.ascontiguousarray(toks, np.uint32).reshape(-1))
+            reply = DeviceArray((n, 1), np.uint32)
+            hip._check(L.uor_fbs_serve_slots_async(
+                model.handle, d_slots.ptr, n, cap, d_tok.ptr, toks.shape[1], 0, reply.ptr, st.ptr,
+                hi.ptr, po.ptr, None if ca is None else ca.ptr, None, None, None, status.ptr, None))
+            assert (status.download() == 0).all()
+            r = reply.download()
+            got.append(r[:, 0])
+            toks = r
+        outs.append(np.stack(got, 1))
+    np.testing.assert_array_equal(outs[0], outs[1])
+    np.testing.assert_array_equal(outs[0], want["reply"])

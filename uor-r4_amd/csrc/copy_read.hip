@@ -88,11 +88,9 @@ __device__ __forceinline__ int64_t div_trunc(int64_t n, uint32_t k) {
   return n < 0 ? -(int64_t)q : (int64_t)q;
 }
 
-// copy_weight_q31 (:243-252)
+// copy_weight_q31 (:243-252), shared with the served step's reads.
 __device__ __forceinline__ uint64_t weight_q31(int32_t margin, uint32_t d) {
-  const int64_t over = (int64_t)margin - ((int64_t)d << 16);
-  if (over <= 0) return 0;
-  return fbs::div128_64((fbs::u128)((uint64_t)over << 31), (uint64_t)(margin > (1 << 16) ? margin : (1 << 16)));
+  return fbs::copy_weight_q31(margin, d);
 }
 
 __global__ __launch_bounds__(kThreads) void copy_mean_rows(Dev D, const uint32_t *tokens,

@@ -419,6 +419,10 @@ int upload_hamming(uor_fbs_handle *h, const uor_fbs_model *m, const uor_fbs_ext 
       }
     if ((st = h->upload(codes.data(), codes.size(), &R.codes))) return st;
     if ((st = h->upload(r.margin, heads, &R.margin))) return st;
+    std::vector<uint32_t> wd((size_t)heads * kHamBins, 0);
+    for (uint32_t k = 0; k < heads; k++)
+      for (uint32_t dd = 0; dd <= 64; dd++) wd[(size_t)k * kHamBins + dd] = copy_weight_q31(r.margin[k], dd);
+    if ((st = h->upload(wd.data(), wd.size(), &R.wd))) return st;
     if ((st = h->upload(r.weight, 2 * (size_t)d, &R.w))) return st;
     R.ask = nullptr;
     R.carry = nullptr;
@@ -887,6 +891,48 @@ extern "C" int uor_fbs_decode_slots_async(uor_fbs_handle *h, const uint32_t *slo
   A.slots = slots;
   A.capacity = capacity;
   A.status = status;
+  return launch(h, A, (hipStream_t)stream);
+}
+
+extern "C" uint64_t uor_fbs_slot_cache_bytes(const uor_fbs_handle *h) {
+  return h ? slot_cache_layout(h->M).bytes : 0;
+}
+
+extern "C" int uor_fbs_serve_slots_async(uor_fbs_handle *h, const uint32_t *slots,
+                                         uint32_t sequences, uint32_t capacity,
+                                         const uint32_t *prompts, uint32_t prompt_len, uint32_t gen,
+                                         uint32_t *out_reply, int64_t *state, int32_t *history,
+                                         uint32_t *position, void *cache, const uint8_t *slide,
+                                         uint32_t *out_kept, int32_t *out_query, int32_t *status,
+                                         void *stream) {
+  if (!h || !slots || !prompts || !out_reply || !state || !history || !position || !status)
+    return fail(UOR_FBS_ERR_ARGUMENT, "null argument");
+  if (prompt_len == 0) return fail(UOR_FBS_ERR_ARGUMENT, "a step needs at least one token");
+  if (h->M.ham.heads)
+    return fail(UOR_FBS_ERR_UNSUPPORTED,
+                "session slots serve no Hamming reads yet (uor_fbs_decode_stream_async resumes them)");
+  DeviceScope scope(h->device);
+  RunArgs A{};
+  A.mode = kModeDecode;
+  A.n = sequences;
+  A.len = prompt_len;
+  A.gen = gen;
+  A.tokens = prompts;
+  A.out_tokens = out_reply;
+  A.in_state = state;
+  A.in_history = history;
+  A.in_position = position;
+  A.out_state = state;
+  A.out_history = history;
+  A.out_position = position;
+  A.out_kept = out_kept;
+  A.out_query = out_query;
+  A.slots = slots;
+  A.capacity = capacity;
+  A.status = status;
+  A.cache = (uint8_t *)cache;
+  A.cache_stride = slot_cache_layout(h->M).bytes;
+  A.slide = slide;
   return launch(h, A, (hipStream_t)stream);
 }
 

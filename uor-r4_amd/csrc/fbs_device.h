@@ -50,12 +50,14 @@ struct DevLayer {
 // each vocabulary entry's key code per head (`vocab_codes`, :566-582), copy heads first.
 constexpr uint32_t kMaxHamKept = 64;        // positions a head keeps
 constexpr uint32_t kHamPosBits = 24;        // positions below 2^24 (a pick packs its distance above)
+constexpr uint32_t kHamBins = 68;            // distances 0..64 (a word per distance), padded
 constexpr uint32_t kHamNoSlot = 0xffffffffu;
 
 struct DevHamRead {
   const int64_t *qu, *ku, *vu;  // d each: query, key and value units
   const uint64_t *codes;        // vocab * heads
   const int32_t *margin;        // heads, bits at Q16
+  const uint32_t *wd;           // heads * kHamBins: each distance's Q31 weight (copy_weight_q31)
   const int32_t *w;             // 2 d at 2^-24: w_c, then w_y
   const int16_t *ask;           // vocab * d question table (Q12), or null: the read does not ask
   const int32_t *carry;         // vocab carry gains (Q16), or null
@@ -116,10 +118,28 @@ inline size_t pair_lds_bytes(const DevModel &M) {
 }
 
 // A Hamming model's kernels add the session's tokens (context u32), the distances (context
-// bytes), one head's picks and weights (2 kMaxHamKept u32) and the sign nibbles (d / 4 u32).
+// bytes), one head's picks and weights (2 kMaxHamKept u32), its distance histogram and the
+// weight of each distance (2 kHamBins u32) and the sign nibbles (d / 4 u32).
 inline size_t ham_lds_bytes(const DevModel &M) {
   if (!M.ham.heads) return 0;
-  return 4ull * M.context + ((M.context + 15ull) & ~15ull) + 8ull * kMaxHamKept + 4ull * (M.d / 4);
+  return 4ull * M.context + ((M.context + 15ull) & ~15ull) + 8ull * kMaxHamKept + 8ull * kHamBins +
+         4ull * (M.d / 4);
+}
+
+// One serving slot's cache (uor_fbs_serve_slots_async), bytes from the entry's start: a u32 tag
+// (the position + 1 the window sums hold for; 0: none), a u32 flag (the writer memory below
+// holds a query), the memory's token, then its query (d i32), its kept drawers (kMaxProbes
+// u32) and, for paired blocks, the slot's window sums for its next step (L d i64).
+struct SlotCacheLayout {
+  uint32_t query, kept, sums, bytes;
+};
+__host__ __device__ inline SlotCacheLayout slot_cache_layout(const DevModel &M) {
+  SlotCacheLayout c;
+  c.query = 16;
+  c.kept = c.query + 4 * ((M.d + 3u) & ~3u);
+  c.sums = (c.kept + 4 * kMaxProbes + 15u) & ~15u;
+  c.bytes = (c.sums + 8 * M.L * M.d + 255u) & ~255u;
+  return c;
 }
 
 enum RunMode : uint32_t { kModeSequences = 0, kModeDecode = 1, kModeScore = 2 };
@@ -164,6 +184,12 @@ struct RunArgs {
   const int64_t *in_payloads;
   int64_t *out_payloads;
   int64_t *pay;
+  // Serving slots: each slot's cache (SlotCacheLayout, `cache_stride` bytes a slot; null: none)
+  // and context slide flags (nonzero: the slot's session continues past a full context; null:
+  // none slides).
+  uint8_t *cache;
+  uint32_t cache_stride;
+  const uint8_t *slide;
 };
 
 }  // namespace fbs

@@ -7,9 +7,10 @@
 // One 64-lane wavefront runs a read; the session's tokens x_0..x_t sit in LDS. Each head in turn
 // chooses its positions 1 <= s < t by the popcount distance between the row's query code and
 // position s's key code (x_{s-1}'s code through the read's key rotation, precomputed per
-// vocabulary entry at model creation): `nearest` (:690-701) as successive wave minima of
-// (distance, position) over the distances staged in LDS, the latest and longest rules
-// (:584-615) as one wave minimum or maximum. The chosen positions and their Q31 margin weights
+// vocabulary entry at model creation): `nearest` (:690-701) from a histogram of the distances
+// (staged in LDS with them) and one pass that keeps every position nearer than the threshold
+// distance and the earliest ones at it, the latest and longest rules (:584-615) as one wave
+// minimum or maximum. The chosen positions and their Q31 margin weights
 // (`copy_weight_q31` :243-252) go to LDS, uniform for the wave; then every lane sums, for its
 // own channels, the weighted values the positions bring back (the table point of the position's
 // own token, or the payload kept at the position, which the same lane wrote), divides by the
@@ -86,14 +87,6 @@ FBS_HD int64_t ham_readout_ask_sum(int64_t n, int32_t w_c, bool has_c, i128 c, i
   return clamp_i64(round_shift128(shl128(n, kReadoutShift) + copied + asked, kReadoutShift));
 }
 
-// `copy_weight_q31` (:243-252): max(0, m - d) / max(m, 1) at Q31, the margin in bits at Q16.
-FBS_HD uint32_t ham_weight(int32_t margin_q16, uint32_t distance) {
-  const int64_t over = (int64_t)margin_q16 - ((int64_t)distance << 16);
-  if (over <= 0) return 0;
-  const uint64_t m = (uint64_t)(margin_q16 > (1 << 16) ? margin_q16 : (1 << 16));
-  return (uint32_t)div128_64((u128)((uint64_t)over << 31), m);
-}
-
 // The sign nibble of unit (x) p (the unit on the left, `head_code` :550-564): bit i is 1 where
 // coordinate i is at or above 0.
 FBS_HD uint32_t ham_nibble(const int64_t *unit, const int64_t (&p)[4]) {
@@ -128,35 +121,62 @@ __device__ __forceinline__ void ham_point(const DevModel &M, uint32_t token, uin
 
 // A head's positions at row t under `rule` (0 the mean's `nearest`, 1 latest exact, 2 latest
 // nearest, 3 longest exact), position s's key from keyf(s), into S.hpick (position) and S.hwgt
-// (Q31 weight) in ascending distance, then ascending position: only the positions inside the
-// margin (weights fall with distance, so they lead). Returns their count, uniform. For the
-// longest rule, longer(s) says whether one token more matches.
+// (Q31 weight): only the positions inside the margin (under the mean rule the `kept` nearest by
+// (distance, position), in ascending position). `wd`: the head's weight of each distance
+// 0..64 (`copy_weight_q31` of its margin, formed by the host), positive exactly below the
+// margin. Returns their count, uniform. For the longest rule, longer(s) says whether one token
+// more matches.
 template <class KeyF, class LongerF>
 __device__ __forceinline__ uint32_t ham_choose(const Lds &S, uint32_t rule, uint64_t q, uint32_t t,
-                                               uint32_t kept, int32_t margin, uint32_t lane,
-                                               KeyF keyf, LongerF longer) {
+                                               uint32_t kept, int32_t margin, const uint32_t *wd,
+                                               uint32_t lane, KeyF keyf, LongerF longer) {
   if (t < 2) return 0;
   uint32_t n = 0;
   if (rule == 0) {
-    for (uint32_t s = 1 + lane; s < t; s += kWave) S.hdist[s] = (uint8_t)__popcll(q ^ keyf(s));
+    // Distances inside the margin are those below dlim; the histogram and each distance's
+    // weight go to LDS.
+    const int64_t lim = ((int64_t)margin + 65535) >> 16;
+    const uint32_t dlim = lim < 65 ? (uint32_t)lim : 65u;
+    for (uint32_t i = lane; i < kHamBins; i += kWave) {
+      S.hhist[i] = 0;
+      S.hwd[i] = wd[i];
+    }
     wave_sync();
-    uint32_t last = 0;  // every packed pick exceeds 0: positions start at 1
-    for (uint32_t r = 0; r < kept; r++) {
-      uint32_t loc = UINT32_MAX;
-      for (uint32_t s = 1 + lane; s < t; s += kWave) {
-        const uint32_t k = (uint32_t)S.hdist[s] << kPosBits | s;
-        loc = k > last && k < loc ? k : loc;
+    for (uint32_t s = 1 + lane; s < t; s += kWave) {
+      const uint32_t dd = (uint32_t)__popcll(q ^ keyf(s));
+      S.hdist[s] = (uint8_t)dd;
+      if (dd < dlim) atomicAdd(&S.hhist[dd], 1u);
+    }
+    wave_sync();
+    // The threshold: the least distance th at which the positions nearer or equal reach `kept`
+    // (then `need` positions at th are taken, the earliest first), else every position inside
+    // the margin (th = dlim).
+    uint32_t th = dlim, need = 0, cum = 0;
+    for (uint32_t dd = 0; dd < dlim; dd++) {
+      const uint32_t h = S.hhist[dd];
+      if (cum + h >= kept) {
+        th = dd;
+        need = kept - cum;
+        break;
       }
-      const uint32_t m = wave_reduce32(loc, OpMin());
-      if (m == UINT32_MAX) break;
-      const uint32_t w = ham_weight(margin, m >> kPosBits);
-      if (!w) break;  // this and every later pick lie outside the margin
-      if (lane == 0) {
-        S.hpick[n] = m & kPosMask;
-        S.hwgt[n] = w;
+      cum += h;
+    }
+    // One pass in ascending position: positions nearer than th, and the first `need` at th.
+    const uint64_t below = __lanemask_lt();
+    uint32_t at = 0;
+    for (uint32_t s0 = 1; s0 < t; s0 += kWave) {
+      const uint32_t s = s0 + lane;
+      const uint32_t dd = s < t ? S.hdist[s] : 255u;
+      const uint64_t eq = __ballot(dd == th);
+      const bool take = dd < th || (dd == th && at + (uint32_t)__popcll(eq & below) < need);
+      const uint64_t tk = __ballot(take);
+      if (take) {
+        const uint32_t i = n + (uint32_t)__popcll(tk & below);
+        S.hpick[i] = s;
+        S.hwgt[i] = S.hwd[dd];
       }
-      n++;
-      last = m;
+      n += (uint32_t)__popcll(tk);
+      at += (uint32_t)__popcll(eq);
     }
   } else if (rule <= 2) {
     uint32_t best = UINT32_MAX;
@@ -167,7 +187,7 @@ __device__ __forceinline__ uint32_t ham_choose(const Lds &S, uint32_t rule, uint
       best = k < best ? k : best;
     }
     const uint32_t m = wave_reduce32(best, OpMin());
-    const uint32_t w = m == UINT32_MAX ? 0 : ham_weight(margin, m >> kPosBits);
+    const uint32_t w = m == UINT32_MAX ? 0 : wd[m >> kPosBits];
     if (w) {
       if (lane == 0) {
         S.hpick[0] = kPosMask - (m & kPosMask);
@@ -185,7 +205,7 @@ __device__ __forceinline__ uint32_t ham_choose(const Lds &S, uint32_t rule, uint
     ex = wave_reduce32(ex, OpMax());
     lg = wave_reduce32(lg, OpMax());
     const uint32_t pick = lg ? lg : ex;
-    const uint32_t w = pick ? ham_weight(margin, 0) : 0;
+    const uint32_t w = pick ? wd[0] : 0;
     if (w) {
       if (lane == 0) {
         S.hpick[0] = pick;
@@ -224,7 +244,7 @@ __device__ __forceinline__ bool ham_copy_mean(const DevModel &M, const DevHamRea
     const uint32_t kd = first ? 2 : 1;
     const uint64_t before = t >= kd ? ham_code(R, H.heads, tk[t - kd], h) : 0;
     const uint32_t n = ham_choose(
-        S, rule, q, t, H.kept, R.margin[h], lane,
+        S, rule, q, t, H.kept, R.margin[h], R.wd + h * kHamBins, lane,
         [&](uint32_t s) { return joined(tk[s - 1], tk[s >= 2 ? s - 2 : 0]); },
         [&](uint32_t s) { return s > kd && ham_code(R, H.heads, tk[s - 1 - kd], h) == before; });
     if (!n) continue;
@@ -318,7 +338,7 @@ __device__ __forceinline__ bool ham_type_mean(const DevModel &M, const DevHamRea
   for (uint32_t j = H.copy; j < H.heads; j++) {
     const uint64_t q = ham_word(S.hnib, j, H.hw);
     const uint32_t n = ham_choose(
-        S, 0, q, t, H.kept, R.margin[j], lane,
+        S, 0, q, t, H.kept, R.margin[j], R.wd + j * kHamBins, lane,
         [&](uint32_t s) { return ham_code(R, H.heads, tk[s - 1], j); },
         [&](uint32_t) { return false; });
     if (!n) continue;

@@ -355,6 +355,16 @@ FBS_HD uint64_t divq(u128 n, const Divisor &dv) {
 
 FBS_HD uint64_t div128_64(u128 n, uint64_t d) { return divq(n, make_divisor(d)); }
 
+// A Hamming candidate's weight at `distance` bits under a head's margin (bits at Q16), at Q31:
+// max(0, m - d) / max(m, 1), floored (RS stack/hamming.rs:243-252 `copy_weight_q31`). At most
+// 2^31, so it fits 32 bits.
+FBS_HD uint32_t copy_weight_q31(int32_t margin_q16, uint32_t distance) {
+  const int64_t over = (int64_t)margin_q16 - ((int64_t)distance << 16);
+  if (over <= 0) return 0;
+  const uint64_t m = (uint64_t)(margin_q16 > (1 << 16) ? margin_q16 : (1 << 16));
+  return (uint32_t)div128_64((u128)((uint64_t)over << 31), m);
+}
+
 // ---------------------------------------------------------------------------------------------
 // Vector kernels, one element at a time.
 

@@ -714,6 +714,8 @@ struct Lds {
   uint8_t *hdist;    // context: one head's distances at the row
   uint32_t *hpick;   // kMaxHamKept: one head's chosen positions
   uint32_t *hwgt;    // kMaxHamKept: their Q31 weights
+  uint32_t *hhist;   // kHamBins: one head's distance histogram
+  uint32_t *hwd;     // kHamBins: the Q31 weight of each distance under the head's margin
   uint32_t *hnib;    // d / 4: the sign nibbles of the row's point
 };
 
@@ -1598,7 +1600,7 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
     }
     S.tok = nullptr;
     S.hdist = nullptr;
-    S.hpick = S.hwgt = S.hnib = nullptr;
+    S.hpick = S.hwgt = S.hhist = S.hwd = S.hnib = nullptr;
     if (HM) {  // ham_lds_bytes
       S.tok = (uint32_t *)(lds + at);
       at += M.context;
@@ -1608,6 +1610,10 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
       at += kMaxHamKept;
       S.hwgt = (uint32_t *)(lds + at);
       at += kMaxHamKept;
+      S.hhist = (uint32_t *)(lds + at);
+      at += kHamBins;
+      S.hwd = (uint32_t *)(lds + at);
+      at += kHamBins;
       S.hnib = (uint32_t *)(lds + at);
     }
     const uint32_t *rs = rsqrt_seed_table(), *rc = recip_seed_table();
@@ -1646,6 +1652,27 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
     uint32_t base = mod_window(M, pos);
     // A slot's history is its ring; otherwise the block's ring takes the rows.
     int32_t *ring = A.slots ? A.out_history + (uint64_t)sl * L * W * d : block_ring;
+    // A serving slot's cache: the window sums its last launch formed for this position (paired
+    // blocks take them in place of summing the window at the first step) and the writer's memory
+    // of its last query, which depends on the model alone, so it is taken whenever it holds one.
+    uint8_t *const ce = A.cache ? A.cache + (uint64_t)sl * A.cache_stride : nullptr;
+    bool fresh = true;
+    if (ce) {
+      const SlotCacheLayout cl = slot_cache_layout(M);
+      const uint32_t *head = (const uint32_t *)ce;
+      if (NW == 2) {
+        hist = (int64_t *)(ce + cl.sums);
+        fresh = head[0] != pos + 1;
+      }
+      if (wave == 0 && head[1] && M.writer_memory) {
+        for (uint32_t i = lane; i < d; i += kWave) S.wq[i] = ((const int32_t *)(ce + cl.query))[i];
+        if (lane < kMaxProbes) S.kept[lane] = ((const uint32_t *)(ce + cl.kept))[lane];
+        if (lane == 0) {
+          S.wmeta[0] = head[2];
+          S.wmeta[1] = 1;
+        }
+      }
+    }
     for (uint32_t l = 0; l < L; l++)
 #pragma unroll
       for (int k = 0; k < Q; k++)
@@ -1704,8 +1731,9 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
     const uint32_t *toks = A.tokens + (uint64_t)s * A.len;
     const uint32_t steps = bad_stream ? 0u : PH == kPhaseDecode ? A.len + A.gen : A.len;
     unsigned long long hits = 0;
+    uint32_t done = 0;  // steps run
     for (uint32_t t = 0; t < steps; t++) {
-      if (pos >= M.context) {
+      if (pos >= M.context && !(A.slide && A.slide[sl])) {  // set_context_slide: continue
         status = 2;
         break;
       }
@@ -1742,9 +1770,11 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
         if (wave == 0)
           status = step_main<Q, SW>(M, S, ln, qv, qs, tok, want, &chosen, kept_out, query_out);
         else
-          status = step_window<Q, SW>(M, S, ring, hist, base, ln, qv, qs, tok, want, t == 0, &chosen);
+          status = step_window<Q, SW>(M, S, ring, hist, base, ln, qv, qs, tok, want,
+                                      t == 0 && fresh, &chosen);
       }
       if (status) break;
+      done++;
       pos++;
       base = base + 1 == W ? 0 : base + 1;
       if (writes_out) {
@@ -1785,6 +1815,20 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
       pair_sync();
     else
       wave_sync();
+    if (ce && wave == 0) {
+      // The slot's cache for its next launch: the sums the last step formed (paired blocks) hold
+      // for the slot's position, and the writer's memory as the block holds it.
+      const SlotCacheLayout cl = slot_cache_layout(M);
+      uint32_t *head = (uint32_t *)ce;
+      for (uint32_t i = lane; i < d; i += kWave) ((int32_t *)(ce + cl.query))[i] = S.wq[i];
+      if (lane < kMaxProbes) ((uint32_t *)(ce + cl.kept))[lane] = S.kept[lane];
+      if (lane == 0) {
+        head[0] = NW == 2 && (done > 0 || !fresh) ? pos + 1 : 0u;
+        head[1] = S.wmeta[1] != 0;
+        head[2] = S.wmeta[0];
+      }
+      wave_sync();
+    }
   }
 }
 

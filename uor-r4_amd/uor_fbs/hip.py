@@ -34,6 +34,7 @@ SYMBOLS = (
     "uor_fbs_index_update_async", "uor_fbs_index_remove_async", "uor_fbs_index_validate_async",
     "uor_fbs_index_probe_async", "uor_fbs_index_full_scan_async", "uor_fbs_stream_words",
     "uor_fbs_payload_words", "uor_fbs_decode_stream", "uor_fbs_decode_stream_async",
+    "uor_fbs_slot_cache_bytes", "uor_fbs_serve_slots_async",
 )
 
 
@@ -79,6 +80,10 @@ def lib():
                                                   + [P] * 13)
         L.uor_fbs_decode_slots_async.argtypes = [P, P, C.c_uint32, C.c_uint32, P, C.c_uint32,
                                                  C.c_uint32, P, P, P, P, P, P, P, P]
+        L.uor_fbs_slot_cache_bytes.argtypes = [P]
+        L.uor_fbs_slot_cache_bytes.restype = C.c_uint64
+        L.uor_fbs_serve_slots_async.argtypes = [P, P, C.c_uint32, C.c_uint32, P, C.c_uint32,
+                                                C.c_uint32, P, P, P, P, P, P, P, P, P, P]
         L.uor_fbs_score.argtypes = [P, P, C.c_uint64, C.c_uint32, P, P]
         L.uor_fbs_score_async.argtypes = [P, P, C.c_uint64, C.c_uint32, P, P, P, P]
         u32 = C.c_uint32

@@ -4,9 +4,10 @@ restore_state, save_session_to_file, restore_session_from_file) over a pool of s
 held in device memory.
 
 A `SessionPool` owns, per slot, one session's recurrence state, window history and position
-in HBM; `uor_fbs_decode_slots_async` steps any set of slots in one launch and updates them in
-place, so a serving loop batches whichever sessions have a token ready (`serve_steps`)
-without moving state through the host. `Session` is one sequence in a slot with the
+in HBM, a serving cache (the window sums formed for the slot's next step and the writer's
+memory of its last query) and a context-slide flag; `uor_fbs_serve_slots_async` steps any set
+of slots in one launch and updates them in place, so a serving loop batches whichever sessions
+have a token ready (`serve_steps`) without moving state through the host. `Session` is one sequence in a slot with the
 reference's per-call semantics; its snapshots are the reference's `SerializedStackSession`,
 encodable as `UR4SESS1` bytes or the JSON of `save_session_to_file` (`session_codec`).
 
@@ -154,6 +155,12 @@ class SessionPool:
         self.state = DeviceArray((capacity, model.state_words), np.int64, dev)
         self.history = DeviceArray((capacity, model.history_words), np.int32, dev)
         self.position = DeviceArray(capacity, np.uint32, dev)
+        # Each slot's serving cache (zero: holds nothing) and context-slide flag.
+        self.cache_bytes = int(hip.lib().uor_fbs_slot_cache_bytes(model.handle))
+        self.cache = DeviceArray((capacity, self.cache_bytes), np.uint8, dev)
+        self.cache.zero()
+        self.slide = DeviceArray(capacity, np.uint8, dev)
+        self.slide.zero()
         self._free = list(range(capacity - 1, -1, -1))
 
     def acquire(self, slot: int | None = None) -> int:
@@ -178,10 +185,16 @@ class SessionPool:
         self._free.append(slot)
 
     def clear(self, slots):
-        """A fresh session in each slot (reset, session.rs:2703-2760)."""
+        """A fresh session in each slot (reset, session.rs:2703-2760); the slide setting stays,
+        as reset keeps it."""
         slots = list(slots)
-        for a in (self.state, self.history, self.position):
+        for a in (self.state, self.history, self.position, self.cache):
             a.zero(slots)
+
+    def set_slide(self, slot: int, on: bool):
+        flags = self.slide.download()
+        flags[slot] = 1 if on else 0
+        self.slide.upload(flags)
 
     def _ring_rows(self, position: int) -> np.ndarray:
         """Ring row holding history row r (the drive r + 1 positions back) at `position`."""
@@ -206,6 +219,7 @@ class SessionPool:
         p = self.position.download()
         p[slot] = position
         self.position.upload(p)
+        self.cache.zero([slot])  # its window sums were formed for the state it held
 
     def run(self, slots, tokens, gen: int = 0, native: bool = False):
         """One launch: the sessions in `slots` take tokens [n, len] and `gen` greedy steps.
@@ -230,10 +244,10 @@ class SessionPool:
         query = DeviceArray((n, self.model.width), np.int32, dev) if native else None
         ptr = lambda x: None if x is None else x.ptr  # noqa: E731
         # The null stream: the runtime's blocking copies below wait for the launch.
-        hip._check(hip.lib().uor_fbs_decode_slots_async(
+        hip._check(hip.lib().uor_fbs_serve_slots_async(
             self.model.handle, d_slots.ptr, n, self.capacity, d_tok.ptr, tokens.shape[1], gen,
-            reply.ptr, self.state.ptr, self.history.ptr, self.position.ptr, ptr(kept), ptr(query),
-            status.ptr, None))
+            reply.ptr, self.state.ptr, self.history.ptr, self.position.ptr, self.cache.ptr,
+            self.slide.ptr, ptr(kept), ptr(query), status.ptr, None))
         out = dict(reply=reply.download(), status=status.download())
         if native:
             out["kept"] = kept.download()
@@ -253,9 +267,12 @@ class Session:
         self.pool = pool
         self.info = pool.info
         self.slot = pool.acquire(slot)
+        self.slide = False
+        pool.set_slide(self.slot, False)
         self._reset_host()
 
     def _reset_host(self):
+        self.slide = getattr(self, "slide", False)  # a caller's setting: reset keeps it
         self.position = 0
         self.tokens: list[int] = []
         self.logits: list[int] | None = None   # pending logits from a restore; zeros otherwise
@@ -272,6 +289,17 @@ class Session:
         self.pool.clear([self.slot])
         self._reset_host()
 
+    def set_context_slide(self, on: bool) -> None:
+        """Let a full context continue instead of refusing (session.rs:2391-2402): refused for a
+        model whose reads name token positions (Hamming reads) or that has a turn memory
+        (can_slide_tokens, :1146-1151)."""
+        art = self.pool.model.art
+        if on and (getattr(art, "hamming", None) is not None or getattr(art, "turn_memory", False)):
+            raise SessionError("Shape", "a context slide needs a model whose reads do not use "
+                                        "token positions")
+        self.slide = bool(on)
+        self.pool.set_slide(self.slot, self.slide)
+
     # ---- stepping ----
     def _admit(self, tokens) -> list[int]:
         """The prefix of `tokens` the reference would step before refusing one (a token outside
@@ -280,7 +308,7 @@ class Session:
         for tok in tokens:
             if not 0 <= tok < self.info.vocab:
                 return ok, SessionError("Token", f"token {tok} outside vocab {self.info.vocab}")
-            if self.position + len(ok) >= self.info.context:
+            if self.position + len(ok) >= self.info.context and not self.slide:
                 return ok, SessionError("ContextFull", f"context {self.info.context}")
             ok.append(int(tok))
         return ok, None
@@ -288,6 +316,8 @@ class Session:
     def _after(self, fed: list[int], reply, kept, query):
         self.position += len(fed)
         self.tokens.extend(fed)
+        # A sliding session keeps its last `context` tokens (session.rs:4149-4151).
+        del self.tokens[:max(0, len(self.tokens) - self.info.context)]
         self._native = NativeStep(int(reply[-1]), kept, query)
 
     def feed(self, tokens) -> NativeStep:

@@ -182,6 +182,9 @@ class Artifact:
     # SHA-256 (hex) of the container bytes a served artifact was read from (format.rs:1493);
     # None for a generated one.
     sha256: str | None = None
+    # A container with a turn memory (`memory` record, lut-stack/7 and /8): the plain step does not
+    # apply it, but it rules out the context slide (session.rs:1146-1151).
+    turn_memory: bool = False
     # The Hamming reads (lut-stack/6): the record's fields and one HammingRead per depth.
     hamming: HammingSpec | None = None
     hamming_reads: list | None = None

@@ -340,7 +340,8 @@ def load(source) -> Artifact:
     art = Artifact(spec=spec, seed=-1, layers=layers, final_gain=codes("final_norm_gain", d),
                    writer_table=table("writer.table", "i16", V * d).astype(np.int16),
                    table_i8=None, eps_mantissa=int(eps["mantissa"]), eps_exp=int(eps["exp"]),
-                   sha256=hashlib.sha256(data).hexdigest())
+                   sha256=hashlib.sha256(data).hexdigest(),
+                   turn_memory=header.get("memory") is not None)
     if header.get("hamming") is not None:
         art.hamming = _check_hamming(header["hamming"], s)
         art.hamming_reads = _hamming_reads(art.hamming, tabs, V, d, int(s["context"]))
