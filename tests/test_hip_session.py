@@ -1,4 +1,4 @@
-"""Serving sessions on the GPU (uor_fbs/session.py over uor_fbs_decode_slots_async) against the
+"""Serving sessions on the GPU (uor_fbs/session.py over uor_fbs_serve_slots_async) against the
 batched decode and the oracle: IntegerStackSession's serving calls (stack/session.rs:2703-3440),
 a serving loop that steps whichever sessions have a token, and snapshots that restore into any
 slot and continue bit for bit (session.rs:2777-3290, session_codec.rs)."""
