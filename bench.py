@@ -41,9 +41,12 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path[:0] = [os.path.join(ROOT, "uor-r4_amd"), os.path.join(ROOT, "oracle")]
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
-# Measured HBM bytes per launch of the decode kernel (rocprofv3 FETCH_SIZE and WRITE_SIZE passes,
-# scaled by a copy kernel's reading), for the workload it names.
-TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fbs_decode_pair_c3_b1024_traffic.md")
+# Measured HBM bytes per launch of each config's timed kernel (rocprofv3 FETCH_SIZE and WRITE_SIZE
+# passes, scaled by a copy kernel's reading), for the workload each summary names.
+TRAFFIC_SUMMARIES = {
+    "c2": "fbs_decode_pair_c2_b1024_traffic.md", "c3": "fbs_decode_pair_c3_b1024_traffic.md",
+    "c4": "fbs_rows_pair_c4_r1048576_traffic.md", "c5": "fbs_decode_pair_c5_b16384_traffic.md",
+    "hamming": "fbs_decode_ham_c3_b1024_traffic.md"}
 D11_TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "d11_score_rows_m1_traffic.md")
 # BASELINE.json's configs at their full shapes: (sequences, prompt, decode steps); c4 is
 # teacher-forced scoring of (rows, row length).
@@ -184,11 +187,11 @@ def workload_key(a) -> str:
 
 
 def measured_traffic(a, kernel):
-    """HBM bytes per decode launch from the committed counter summary, if it covers this exact
-    workload and kernel; None otherwise."""
+    """HBM bytes per timed launch from the config's committed counter summary, if it covers this
+    exact workload and kernel; None otherwise."""
     try:
-        text = open(TRAFFIC_SUMMARY).read()
-    except OSError:
+        text = open(os.path.join(ROOT, "profiles", TRAFFIC_SUMMARIES[a.config])).read()
+    except (KeyError, OSError):
         return None
     w = re.search(r"^workload: (.+)$", text, re.M)
     k = re.search(r"^kernel: (.+)$", text, re.M)
@@ -439,7 +442,8 @@ def score_main(a, torch, oracle, art, model, rows, dev, stream, sp) -> dict:
                    "parallelism": "none (1 GPU)"},
         "matches": int(matches.item()),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(a, f"{family}<{(spec.width // 4 + 63) // 64}, {S}>"),
                      "bytes_per_position": round(bpt, 1), "mean_candidate_rows": round(mean_cand, 1),
                      "kernel": f"{family}<{(spec.width // 4 + 63) // 64}, {S}>",
                      "launch_ms": [round(x, 3) for x in launch_ms]},
@@ -766,11 +770,12 @@ def hamming_main(a, torch, oracle) -> dict:
         "data": "synthetic (seeded integer artifact and Hamming reads, Zipf prompts)",
         "config": {"workload": f"hamming: c3 artifact with reads {HAMMING_READS} at batch {B}: "
                                f"prefilled {a.prompt}-token prompts, {G} greedy decode steps per "
-                               "timed step", "batch": B, "prompt": a.prompt, "gen": G,
-                   "width": spec.width, "layers": spec.layers, "vocab": spec.vocab,
-                   "parallelism": "none (1 GPU)"},
+                               "timed step", "key": workload_key(a), "batch": B,
+                   "prompt": a.prompt, "gen": G, "width": spec.width, "layers": spec.layers,
+                   "vocab": spec.vocab, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(a, f"fbs_decode_ham<{Q}, {Sw}>"),
                      "bytes_per_token": {k: round(v, 1) for k, v in bpt.items()},
                      "mean_candidate_rows": round(mean_cand, 1),
                      "kernel": f"fbs_decode_ham<{Q}, {Sw}>",
