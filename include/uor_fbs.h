@@ -184,6 +184,23 @@ int uor_fbs_sequences_async(uor_fbs_handle *handle, const uint32_t *tokens, uint
                             uint32_t len, uint32_t *out_tokens, uint32_t *out_kept,
                             int32_t *out_query, int32_t *status, void *stream);
 
+/* The snap trace (fbs_core.h:488-501, claude-134): uor_fbs_sequences with every position's trace,
+ * `uor_fbs_trace_stride(handle)` bytes a position: per layer, the transition's chosen icosian root
+ * per lane (width/4 bytes), the output gate's per lane, then the feed-forward gate's per 4 MLP
+ * channels (mlp/4 bytes); 255 where a site is served unsnapped (raw gates or transition) or its
+ * raw quaternion is zero. Same contract as fbs_trace_sequences (evaluator.cu:21-33) and
+ * fbs_host_trace_sequences (host_kernel.cpp:31-49); the other outputs are those of
+ * uor_fbs_sequences. Runs the one-wavefront kernels. Host buffers; `_async`: device buffers and
+ * one int32 status per sequence. */
+uint64_t uor_fbs_trace_stride(const uor_fbs_handle *handle);
+int uor_fbs_trace_sequences(uor_fbs_handle *handle, const uint32_t *tokens, uint32_t sequences,
+                            uint32_t len, uint32_t *out_tokens, uint32_t *out_kept,
+                            int32_t *out_query, uint8_t *out_trace);
+int uor_fbs_trace_sequences_async(uor_fbs_handle *handle, const uint32_t *tokens,
+                                  uint32_t sequences, uint32_t len, uint32_t *out_tokens,
+                                  uint32_t *out_kept, int32_t *out_query, uint8_t *out_trace,
+                                  int32_t *status, void *stream);
+
 /* Batched greedy decode, the fbs-toks run (fbs-toks.rs:1513-1533) for many sequences: each
  * sequence steps its `prompt_len` prompt tokens, then `gen` more, each fed the previous
  * choice. `out_reply` gets gen+1 tokens per sequence: the prompt's last choice, then every

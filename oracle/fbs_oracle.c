@@ -238,8 +238,8 @@ static uint32_t snap_select(const int8_t *ico, const int32_t raw[4]) {
 }
 
 /* `stack_snap_rotation`: the chosen root times lambda at Q31, lambda phi rounded at Q31
- * (RS stack/kernels.rs:1530-1557, TW 435-445). */
-static void snap_rotation(const int8_t *ico, const int32_t raw[4], uint64_t lambda, int64_t o[4]) {
+ * (RS stack/kernels.rs:1530-1557, TW 435-445). Returns the root's index (the snap trace's). */
+static uint32_t snap_rotation(const int8_t *ico, const int32_t raw[4], uint64_t lambda, int64_t o[4]) {
   uint32_t r = snap_select(ico, raw);
   uint64_t lambda_phi = lambda + ((lambda * PHI_LO + (1ull << 31)) >> 32);
   for (int c = 0; c < 4; c++) {
@@ -247,6 +247,7 @@ static void snap_rotation(const int8_t *ico, const int32_t raw[4], uint64_t lamb
                             lambda_phi * (uint64_t)(int64_t)ico[8 * r + 2 * c + 1]);
     o[c] = shift(sum, 1);
   }
+  return r;
 }
 
 /* `stack_rotation`: lambda raw/|raw| at Q31; the unit at Q30 by floor division of magnitudes,
@@ -263,12 +264,18 @@ static void rotation(const int32_t raw[4], uint64_t lambda, uint64_t eps, int64_
   }
 }
 
-static void serve_rotation(const int8_t *ico, uint32_t raw_form, const int32_t raw[4],
-                           uint64_t lambda, uint64_t eps, int64_t o[4]) {
+/* A quaternion as the artifact serves it, returning its snap trace byte (TW 476-502, claude-134):
+ * the chosen root's index, or 255 where none was chosen (served unsnapped) or the raw
+ * quaternion is zero (its tie selects root 0). */
+#define TRACE_NONE 255u
+static uint32_t serve_rotation(const int8_t *ico, uint32_t raw_form, const int32_t raw[4],
+                               uint64_t lambda, uint64_t eps, int64_t o[4]) {
+  uint32_t chosen = TRACE_NONE;
   if (raw_form)
     rotation(raw, lambda, eps, o);
   else
-    snap_rotation(ico, raw, lambda, o);
+    chosen = snap_rotation(ico, raw, lambda, o);
+  return (raw[0] | raw[1] | raw[2] | raw[3]) == 0 ? TRACE_NONE : chosen;
 }
 
 /* ------------------------------------------------------------------------------------------
@@ -884,6 +891,7 @@ typedef struct {
   int64_t *payloads; /* [typed read][context][width]: the type heads' payloads (hamming_payloads) */
   int64_t *normed;   /* width: the final norm's output (the readout read's input) */
   int slide;         /* a full context continues (set_context_slide, session.rs:2391-2402) */
+  uint8_t *trace;    /* this step's snap trace (layers * (2 lanes + mlp / 4) bytes), or NULL */
 } S;
 
 static void session_alloc(const O *o, S *s) {
@@ -925,7 +933,8 @@ static void session_reset(const O *o, S *s) {
  * gate (RS stack/session.rs:4822-4982, `stack_lanes` :5097-5145, `stack_lane_weights`
  * :4989-5026; TW 508-561). The causal window reads W prior drive rows (reference W = 3,
  * `CONVOLUTION_WIDTH` = 4 taps, session.rs:85). Returns the exponent of s->act[..d]. */
-static int32_t recurrence(const O *o, uint32_t l, int64_t *state, int32_t *hist, S *s) {
+static int32_t recurrence(const O *o, uint32_t l, int64_t *state, int32_t *hist, S *s,
+                          uint8_t *trace) {
   const uor_fbs_model *m = o->m;
   const uor_fbs_layer *ly = m->layers + l;
   uint32_t d = o->d, W = o->W;
@@ -949,7 +958,8 @@ static int32_t recurrence(const O *o, uint32_t l, int64_t *state, int32_t *hist,
     if (idx > 15) idx = 15;
     uint64_t lambda = 1ull << (30 - idx), keep = m->keep_q31[idx];
     int64_t t[4];
-    serve_rotation(m->icosian, m->raw_transition, rot + 4 * lane, lambda, ROTATION_EPSILON, t);
+    uint32_t root = serve_rotation(m->icosian, m->raw_transition, rot + 4 * lane, lambda, ROTATION_EPSILON, t);
+    if (trace) trace[lane] = (uint8_t)root;
     int64_t *h = state + 4 * lane;
     int64_t held[4] = {h[0], h[1], h[2], h[3]};
     i128 moved[4];
@@ -962,7 +972,8 @@ static int32_t recurrence(const O *o, uint32_t l, int64_t *state, int32_t *hist,
   for (uint32_t lane = 0; lane < o->lanes; lane++) {
     int64_t q[4], rhs[4];
     i128 prod[4];
-    serve_rotation(m->icosian, m->raw_gates, gate + 4 * lane, 1ull << 31, GATE_EPSILON, q);
+    uint32_t root = serve_rotation(m->icosian, m->raw_gates, gate + 4 * lane, 1ull << 31, GATE_EPSILON, q);
+    if (trace) trace[o->lanes + lane] = (uint8_t)root;
     for (int k = 0; k < 4; k++) rhs[k] = shift(state[4 * lane + k], RESIDUAL_EXP - STATE_EXP);
     hamilton(q, rhs, prod);
     for (int k = 0; k < 4; k++) s->scratch[4 * lane + k] = shift_wide(prod[k], 15);
@@ -971,12 +982,14 @@ static int32_t recurrence(const O *o, uint32_t l, int64_t *state, int32_t *hist,
 }
 
 /* The Hamilton branch of `stack_swiglu` (RS stack/session.rs:4005-4025, TW 566-578). */
-static void hamilton_gate(const O *o, const int32_t *gate, const int32_t *up, int64_t *out) {
+static void hamilton_gate(const O *o, const int32_t *gate, const int32_t *up, int64_t *out,
+                          uint8_t *trace) {
   const uor_fbs_model *m = o->m;
   for (uint32_t j = 0; j < o->mlp / 4; j++) {
     int64_t q[4], rhs[4];
     i128 prod[4];
-    serve_rotation(m->icosian, m->raw_gates, gate + 4 * j, 1ull << 31, GATE_EPSILON, q);
+    uint32_t root = serve_rotation(m->icosian, m->raw_gates, gate + 4 * j, 1ull << 31, GATE_EPSILON, q);
+    if (trace) trace[j] = (uint8_t)root;
     for (int k = 0; k < 4; k++) rhs[k] = up[4 * j + k];
     hamilton(q, rhs, prod);
     for (int k = 0; k < 4; k++) out[4 * j + k] = shift_wide(prod[k], 15);
@@ -1005,14 +1018,17 @@ static int step(const O *o, S *s, uint32_t token, uint32_t *out_token) {
     for (uint32_t i = 0; i < d; i++) s->scratch[i] = grid_apply(s->scratch[i], ly->rec_gain[i]);
     gather64(&ly->rec_in, s->scratch, NORM_FINE_EXP, s->branches);
     gather64(&ly->rec_gate, s->scratch, NORM_FINE_EXP, s->gate_out);
-    int32_t act_exp = recurrence(o, l, state, hist, s);
+    /* The position's snap trace, per layer: the transition's root per lane, the output gate's,
+     * then the feed-forward gate's per 4 MLP channels (TW 488-496). */
+    uint8_t *lt = s->trace ? s->trace + (uint64_t)l * (2 * o->lanes + o->mlp / 4) : NULL;
+    int32_t act_exp = recurrence(o, l, state, hist, s, lt);
     gather16(&ly->rec_out, s->act, act_exp, s->proj);
     for (uint32_t i = 0; i < d; i++) s->x[i] = sat_add32(s->x[i], s->proj[i]);
     rms_norm_fine(s->x, d, m->eps_mantissa, m->eps_exp, s->scratch);
     for (uint32_t i = 0; i < d; i++) s->scratch[i] = grid_apply(s->scratch[i], ly->mlp_gain[i]);
     gather64(&ly->mlp_gate, s->scratch, NORM_FINE_EXP, s->gate);
     gather64(&ly->mlp_up, s->scratch, NORM_FINE_EXP, s->up);
-    hamilton_gate(o, s->gate, s->up, s->scratch);
+    hamilton_gate(o, s->gate, s->up, s->scratch, lt ? lt + 2 * o->lanes : NULL);
     act_exp = quantize16(s->scratch, o->mlp, PRODUCT_EXP, s->act);
     gather16(&ly->mlp_down, s->act, act_exp, s->proj);
     for (uint32_t i = 0; i < d; i++) s->x[i] = sat_add32(s->x[i], s->proj[i]);
@@ -1054,6 +1070,7 @@ typedef struct {
   const int64_t *in_payloads;  /* [n][typed reads][context][width] */
   int64_t *out_payloads;
   uint64_t matches;
+  uint8_t *out_trace; /* sequences: every position's snap trace */
   int slide;
   int tid, threads, status;
 } Job;
@@ -1066,6 +1083,8 @@ static void *run_job(void *arg) {
   S s;
   session_alloc(o, &s);
   s.slide = j->slide;
+  s.trace = NULL;
+  const uint64_t stride = (uint64_t)o->L * (2 * o->lanes + o->mlp / 4);
   for (uint64_t i = (uint64_t)j->tid; i < j->n && j->status == 0; i += (uint64_t)j->threads) {
     session_reset(o, &s);
     s.candidates = 0;
@@ -1073,6 +1092,7 @@ static void *run_job(void *arg) {
       const uint32_t *row = j->tokens + i * j->len;
       for (uint32_t t = 0; t < j->len; t++) {
         uint32_t tok;
+        s.trace = j->out_trace ? j->out_trace + (i * j->len + t) * stride : NULL;
         int err = step(o, &s, row[t], &tok);
         if (err) {
           j->status = err;
@@ -1157,6 +1177,33 @@ int fbs_oracle_sequences(const uor_fbs_model *m, const uor_fbs_ext *ext, const u
   j.out_tokens = out_tokens;
   j.out_kept = out_kept;
   j.out_query = out_query;
+  int status = run_jobs(&j, threads);
+  unresolve(&o);
+  return status;
+}
+
+/* fbs_host_trace_sequences (TW host_kernel.cpp:31-49): the sequences with every position's snap
+ * trace, fbs_oracle_trace_stride bytes a position. */
+uint64_t fbs_oracle_trace_stride(const uor_fbs_model *m) {
+  return (uint64_t)m->layer_count * (2 * (m->width / 4) + m->mlp / 4);
+}
+
+int fbs_oracle_trace_sequences(const uor_fbs_model *m, const uor_fbs_ext *ext, const uint32_t *tokens,
+                               uint32_t sequences, uint32_t len, uint32_t *out_tokens,
+                               uint32_t *out_kept, int32_t *out_query, uint8_t *out_trace,
+                               int threads) {
+  O o;
+  resolve(&o, m, ext);
+  Job j = {0};
+  j.o = &o;
+  j.kind = 0;
+  j.tokens = tokens;
+  j.n = sequences;
+  j.len = len;
+  j.out_tokens = out_tokens;
+  j.out_kept = out_kept;
+  j.out_query = out_query;
+  j.out_trace = out_trace;
   int status = run_jobs(&j, threads);
   unresolve(&o);
   return status;

@@ -55,6 +55,14 @@ int fbs_oracle_score(const uor_fbs_model *m, const uor_fbs_ext *ext, const uint3
  * the first position of them valid) and the typed reads' payload caches
  * ([n][typed][context][width], typed = fbs_oracle_hamming_typed), resumed and exported beside the
  * state as IntegerStackSession keeps them (session.rs:2232-2252). */
+/* The sequences with every position's snap trace (fbs_host_trace_sequences, TW
+ * host_kernel.cpp:31-49): per position and layer, the transition's root per lane, the output
+ * gate's per lane, the feed-forward gate's per 4 MLP channels; 255 where none was chosen. */
+uint64_t fbs_oracle_trace_stride(const uor_fbs_model *m);
+int fbs_oracle_trace_sequences(const uor_fbs_model *m, const uor_fbs_ext *ext, const uint32_t *tokens,
+                               uint32_t sequences, uint32_t len, uint32_t *out_tokens,
+                               uint32_t *out_kept, int32_t *out_query, uint8_t *out_trace,
+                               int threads);
 /* fbs_oracle_decode with the context slide on for every session (session.rs:2391-2402); a model
  * with Hamming reads is refused (UOR_FBS_ERR_SHAPE). */
 int fbs_oracle_decode_slide(const uor_fbs_model *m, const uor_fbs_ext *ext, const uint32_t *prompts,

@@ -59,6 +59,9 @@ def lib():
         L.fbs_oracle_writer.argtypes = [P, P, P, P, P]
         L.fbs_oracle_writer.restype = C.c_uint32
         u32, i32, i64, u64 = C.c_uint32, C.c_int32, C.c_int64, C.c_uint64
+        L.fbs_oracle_trace_stride.argtypes = [P]
+        L.fbs_oracle_trace_stride.restype = u64
+        L.fbs_oracle_trace_sequences.argtypes = [P, P, P, u32, u32, P, P, P, P, C.c_int]
         L.fbs_oracle_decode_slide.argtypes = [P, P, P, u32, u32, u32, P, P, P, P, P, P, P, C.c_int]
         L.fbs_oracle_decode_stream.argtypes = [P, P, P, u32, u32, u32, P, P, P, P, P, P, P, P, P,
                                                P, P, C.c_int]
@@ -86,6 +89,9 @@ def twin():
     if _twin is None:
         T = C.CDLL(TWIN_SO)
         T.fbs_host_sequences.argtypes = [P, P, C.c_uint32, C.c_uint32, P, P, P]
+        T.fbs_host_trace_sequences.argtypes = [P, P, C.c_uint32, C.c_uint32, P, P, P, P]
+        T.fbs_host_trace_stride.argtypes = [P]
+        T.fbs_host_trace_stride.restype = C.c_uint64
         T.fbs_host_sizeof_model.restype = C.c_int64
         T.fbs_host_sizeof_layer.restype = C.c_int64
         _twin = T
@@ -231,6 +237,38 @@ def score(art, rows: np.ndarray, threads: int = 1, image: Image | None = None, w
     st = lib().fbs_oracle_score(C.addressof(img.model), img.ext_ptr() and C.addressof(img.ext),
                                 _vp(rows), n, length, _vp(argmin), _vp(matches), threads)
     return st, int(matches[0]), argmin
+
+
+def trace_sequences(art, tokens: np.ndarray, threads: int = 1, image: Image | None = None):
+    """Oracle teacher-forced outputs with every position's snap trace:
+    (status, tokens, kept, query, trace [S, len, stride] u8)."""
+    img = image or Image(art)
+    tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+    S, n = tokens.shape
+    stride = int(lib().fbs_oracle_trace_stride(C.addressof(img.model)))
+    out_t = np.zeros((S, n), np.uint32)
+    out_k = np.zeros((S, n, art.probes), np.uint32)
+    out_q = np.zeros((S, n, art.spec.width), np.int32)
+    out_tr = np.full((S, n, stride), 0xEE, np.uint8)
+    st = lib().fbs_oracle_trace_sequences(C.addressof(img.model), _ext(img), _vp(tokens), S, n,
+                                          _vp(out_t), _vp(out_k), _vp(out_q), _vp(out_tr), threads)
+    return st, out_t, out_k, out_q, out_tr
+
+
+def twin_trace_sequences(art, tokens: np.ndarray):
+    """The reference twin's fbs_host_trace_sequences (reference shapes only)."""
+    assert art.spec.reference_shape and art.spec.head == 0
+    img = Image(art, with_ext=False)
+    tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+    S, n = tokens.shape
+    stride = int(twin().fbs_host_trace_stride(C.addressof(img.model)))
+    out_t = np.zeros((S, n), np.uint32)
+    out_k = np.zeros((S, n, art.spec.kept), np.uint32)
+    out_q = np.zeros((S, n, art.spec.width), np.int32)
+    out_tr = np.full((S, n, stride), 0xEE, np.uint8)
+    st = twin().fbs_host_trace_sequences(C.addressof(img.model), _vp(tokens), S, n, _vp(out_t),
+                                         _vp(out_k), _vp(out_q), _vp(out_tr))
+    return st, out_t, out_k, out_q, out_tr
 
 
 def twin_sequences(art, tokens: np.ndarray):

@@ -200,3 +200,23 @@ def test_repeated_queries_reuse_the_writer_exactly():
     np.testing.assert_array_equal(query, want_q)
     np.testing.assert_array_equal(kept, want_k)
     np.testing.assert_array_equal(tok, want_t)
+
+
+TRACE = json.load(open(os.path.join(GOLDEN, "trace", "manifest.json")))
+
+
+@pytest.mark.parametrize("name", sorted(TRACE))
+def test_snap_trace_matches_the_golden_twin(name):
+    """uor_fbs_trace_sequences against the twin's fbs_host_trace_sequences (host_kernel.cpp:31-49,
+    tests/golden/make_golden_trace.py): every position's roots, and the outputs beside them."""
+    entry, art, data = load_case(name)
+    rec = TRACE[name]
+    print(f"trace {name} tokens {data['tokens'].shape}", flush=True)
+    tok, kept, query, trace = Model(art).trace_sequences(data["tokens"])
+    np.testing.assert_array_equal(tok, data["out_tokens"])
+    np.testing.assert_array_equal(kept, data["out_kept"])
+    assert trace.shape[-1] == rec["stride"]
+    if "trace_sha256" in rec:
+        assert [hashlib.sha256(t.tobytes()).hexdigest() for t in trace] == rec["trace_sha256"]
+    else:
+        np.testing.assert_array_equal(trace, np.load(os.path.join(GOLDEN, "trace", f"{name}.npz"))["trace"])

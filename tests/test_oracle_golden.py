@@ -58,3 +58,25 @@ def test_golden_cases_are_not_degenerate():
         outs = [np.load(os.path.join(GOLDEN, f"{base}_{s}_seq.npz"))["out_tokens"]
                 for s in ("g1t1", "g0t0", "g1t0", "g0t1")]
         assert not np.array_equal(outs[0], outs[1])
+
+
+TRACE = json.load(open(os.path.join(GOLDEN, "trace", "manifest.json")))
+
+
+@pytest.mark.parametrize("name", sorted(TRACE))
+def test_oracle_snap_trace_matches_twin_golden(name):
+    """The snap trace (fbs_host_trace_sequences, host_kernel.cpp:31-49, written by
+    tests/golden/make_golden_trace.py): every position's roots per layer, 255 where a site is
+    served unsnapped or its raw quaternion is zero; the outputs beside it are the golden ones."""
+    entry, art, data = load_case(name)
+    rec = TRACE[name]
+    st, tok, kept, query, trace = oracle.trace_sequences(art, data["tokens"], threads=4)
+    assert st == 0 and trace.shape[-1] == rec["stride"]
+    check_outputs(entry, data, tok, kept, query)
+    if "trace_sha256" in rec:
+        assert [hashlib.sha256(t.tobytes()).hexdigest() for t in trace] == rec["trace_sha256"]
+    else:
+        np.testing.assert_array_equal(trace, np.load(os.path.join(GOLDEN, "trace", f"{name}.npz"))["trace"])
+    if oracle.twin_available():
+        t2 = oracle.twin_trace_sequences(art, data["tokens"])[4]
+        np.testing.assert_array_equal(trace, t2)

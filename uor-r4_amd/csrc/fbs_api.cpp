@@ -22,13 +22,26 @@
 #include "fbs_int.h"
 
 namespace fbs {
-// The kernels: fbs_prefill.hip, fbs_decode.hip, fbs_rows.hip (`waves` wavefronts per sequence).
-hipError_t launch_fbs_prefill(const DevModel &M, const RunArgs &A, uint32_t grid, uint32_t waves,
-                              size_t lds, hipStream_t stream);
-hipError_t launch_fbs_decode(const DevModel &M, const RunArgs &A, uint32_t grid, uint32_t waves,
-                             size_t lds, hipStream_t stream);
-hipError_t launch_fbs_rows(const DevModel &M, const RunArgs &A, uint32_t grid, uint32_t waves,
-                           size_t lds, hipStream_t stream);
+// The kernels: fbs_{prefill,decode,rows}{,_pair,_ham}.hip (phase x family).
+#define FBS_LAUNCHER(NAME)                                                                     \
+  hipError_t launch_##NAME(const DevModel &M, const RunArgs &A, uint32_t grid, size_t lds,    \
+                           hipStream_t stream);
+FBS_LAUNCHER(fbs_prefill)
+FBS_LAUNCHER(fbs_prefill_pair)
+FBS_LAUNCHER(fbs_prefill_ham)
+FBS_LAUNCHER(fbs_decode)
+FBS_LAUNCHER(fbs_decode_pair)
+FBS_LAUNCHER(fbs_decode_ham)
+FBS_LAUNCHER(fbs_rows)
+FBS_LAUNCHER(fbs_rows_pair)
+FBS_LAUNCHER(fbs_rows_ham)
+FBS_LAUNCHER(fbs_prefill_8)
+FBS_LAUNCHER(fbs_prefill_pair8)
+FBS_LAUNCHER(fbs_decode_8)
+FBS_LAUNCHER(fbs_decode_pair8)
+FBS_LAUNCHER(fbs_rows_8)
+FBS_LAUNCHER(fbs_rows_pair8)
+#undef FBS_LAUNCHER
 }
 
 using namespace fbs;
@@ -575,6 +588,14 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
       for (size_t i = 0; i < n; i++) tb[i] = (uint16_t)((uint16_t)m->writer_table[i] ^ 0x8000u);
     }
     if ((st = h->upload(tb.data(), n, &M.table_b))) return done(st);
+    M.table8 = nullptr;
+    M.t8_shift = 0;
+    if (e && e->table_i8) {  // the writer's scan reads the codes themselves, biased
+      std::vector<uint8_t> t8(n);
+      for (size_t i = 0; i < n; i++) t8[i] = (uint8_t)((int32_t)e->table_i8[i] + 128);
+      if ((st = h->upload(t8.data(), n, &M.table8))) return done(st);
+      M.t8_shift = e->table_shift;
+    }
   }
   // Drawer keys: the extension's, or the 256 root pairs (cell c = a * 16 + b scores the first
   // 8-block against root a and the last against root b, session.rs:4069-4090).
@@ -654,11 +675,13 @@ extern "C" uint32_t uor_fbs_block_waves(const uor_fbs_handle *h, uint32_t n) {
 namespace {
 
 // `noalloc`: the window rings and sums come from the device's scratch array, whose size bounds
-// the grid (sequences loop within the blocks), and nothing is allocated.
-int launch(uor_fbs_handle *h, RunArgs &A, hipStream_t stream, bool noalloc = false) {
+// the grid (sequences loop within the blocks), and nothing is allocated. `one_wave`: the
+// one-wavefront kernels whatever the model's default (the snap trace is recorded there).
+int launch(uor_fbs_handle *h, RunArgs &A, hipStream_t stream, bool noalloc = false,
+           bool one_wave = false) {
   if (A.n == 0) return 0;
   if (!A.slots) A.capacity = A.n;
-  const bool pair = h->pair;
+  const bool pair = h->pair && !one_wave;
   const uint32_t cap = pair ? h->pair_grid : h->max_grid;
   uint32_t grid = A.n < cap ? A.n : cap;
   if (noalloc && h->M.ham.heads)
@@ -697,9 +720,18 @@ int launch(uor_fbs_handle *h, RunArgs &A, hipStream_t stream, bool noalloc = fal
   const bool decode = A.mode == kModeDecode;
   const uint32_t waves = pair ? 2 : 1;
   const size_t lds = pair ? h->pair_lds : h->lds_bytes;
-  hipError_t e = decode && A.gen == 0 ? launch_fbs_prefill(h->M, A, grid, waves, lds, stream)
-                 : decode             ? launch_fbs_decode(h->M, A, grid, waves, lds, stream)
-                                      : launch_fbs_rows(h->M, A, grid, waves, lds, stream);
+  using Launcher = hipError_t (*)(const DevModel &, const RunArgs &, uint32_t, size_t, hipStream_t);
+  // Families: one wavefront, paired, Hamming reads, then the first two for an int8 table.
+  static const Launcher table[3][5] = {
+      {launch_fbs_prefill, launch_fbs_prefill_pair, launch_fbs_prefill_ham, launch_fbs_prefill_8,
+       launch_fbs_prefill_pair8},
+      {launch_fbs_decode, launch_fbs_decode_pair, launch_fbs_decode_ham, launch_fbs_decode_8,
+       launch_fbs_decode_pair8},
+      {launch_fbs_rows, launch_fbs_rows_pair, launch_fbs_rows_ham, launch_fbs_rows_8,
+       launch_fbs_rows_pair8}};
+  const int phase = decode && A.gen == 0 ? 0 : decode ? 1 : 2;
+  const int family = h->M.ham.heads ? 2 : (waves == 2 ? 1 : 0) + (h->M.table8 ? 3 : 0);
+  hipError_t e = table[phase][family](h->M, A, grid, lds, stream);
   if (e != hipSuccess) return hip_fail(e, "kernel launch");
   return 0;
 }
@@ -779,6 +811,60 @@ extern "C" int uor_fbs_sequences_async(uor_fbs_handle *h, const uint32_t *tokens
   A.out_query = out_query;
   A.status = status;
   return launch(h, A, (hipStream_t)stream);
+}
+
+extern "C" uint64_t uor_fbs_trace_stride(const uor_fbs_handle *h) {
+  return h ? (uint64_t)h->M.L * (2 * h->M.nq + h->M.nm) : 0;
+}
+
+extern "C" int uor_fbs_trace_sequences_async(uor_fbs_handle *h, const uint32_t *tokens,
+                                             uint32_t sequences, uint32_t len, uint32_t *out_tokens,
+                                             uint32_t *out_kept, int32_t *out_query,
+                                             uint8_t *out_trace, int32_t *status, void *stream) {
+  if (!h || (!tokens && sequences && len) || !status || !out_tokens || !out_trace)
+    return fail(UOR_FBS_ERR_ARGUMENT, "null argument");
+  DeviceScope scope(h->device);
+  RunArgs A{};
+  A.mode = kModeSequences;
+  A.n = sequences;
+  A.len = len;
+  A.tokens = tokens;
+  A.out_tokens = out_tokens;
+  A.out_kept = out_kept;
+  A.out_query = out_query;
+  A.out_trace = out_trace;
+  A.status = status;
+  return launch(h, A, (hipStream_t)stream, false, true);
+}
+
+extern "C" int uor_fbs_trace_sequences(uor_fbs_handle *h, const uint32_t *tokens,
+                                       uint32_t sequences, uint32_t len, uint32_t *out_tokens,
+                                       uint32_t *out_kept, int32_t *out_query,
+                                       uint8_t *out_trace) {
+  if (!h || !tokens || !out_tokens || !out_trace) return fail(UOR_FBS_ERR_ARGUMENT, "null argument");
+  if (sequences == 0 || len == 0) return 0;
+  DeviceScope scope(h->device);
+  const size_t n = (size_t)sequences * len, stride = uor_fbs_trace_stride(h);
+  DevBuf b;
+  uint32_t *dt, *dot, *dk = nullptr;
+  int32_t *dq = nullptr, *ds;
+  uint8_t *dtr;
+  int st;
+  if ((st = b.in(&dt, tokens, n)) || (st = b.alloc(&dot, n)) || (st = b.alloc(&ds, sequences)) ||
+      (st = b.alloc(&dtr, n * stride)))
+    return st;
+  if (out_kept && (st = b.alloc(&dk, n * h->M.P))) return st;
+  if (out_query && (st = b.alloc(&dq, n * h->M.d))) return st;
+  if ((st = uor_fbs_trace_sequences_async(h, dt, sequences, len, dot, dk, dq, dtr, ds, nullptr)))
+    return st;
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_fail(e, "kernel");
+  std::vector<int32_t> status(sequences);
+  if ((st = copy_out(status.data(), ds, sequences)) || (st = copy_out(out_tokens, dot, n)) ||
+      (st = copy_out(out_kept, dk, n * h->M.P)) || (st = copy_out(out_query, dq, n * h->M.d)) ||
+      (st = copy_out(out_trace, dtr, n * stride)))
+    return st;
+  return first_status(status);
 }
 
 extern "C" int uor_fbs_sequences(uor_fbs_handle *h, const uint32_t *tokens, uint32_t sequences,

@@ -93,6 +93,11 @@ struct DevModel {
   const int16_t *final_gain;
   const uint16_t *final_gain_desc;
   const uint16_t *table_b;  // vocab * d, biased
+  // An int8 table (uor_fbs_ext.table_i8): its codes biased, code + 128, vocab * d bytes, which
+  // the writer's scan reads in place of table_b (half the bytes a candidate row moves); null
+  // for an i16 table.
+  const uint8_t *table8;
+  uint32_t t8_shift;        // the int8 table's shift to Q12
   const int16_t *keys;      // D * 16
   const uint32_t *offsets;  // D + 1
   const uint32_t *members;  // offsets[D]
@@ -190,6 +195,9 @@ struct RunArgs {
   uint8_t *cache;
   uint32_t cache_stride;
   const uint8_t *slide;
+  // Sequences on one wavefront a sequence: every position's snap trace, L (2 d/4 + m/4) bytes
+  // a position (null: none).
+  uint8_t *out_trace;
 };
 
 }  // namespace fbs

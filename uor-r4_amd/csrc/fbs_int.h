@@ -693,7 +693,7 @@ FBS_HD uint32_t snap_select(const int8_t *ico, const int32_t raw[4]) {
 }
 
 // `stack_snap_rotation` (RS stack/kernels.rs:1530-1557, TW 435-445).
-FBS_HD void snap_rotation(const int8_t *ico, const int32_t raw[4], uint64_t lambda, int64_t o[4]) {
+FBS_HD uint32_t snap_rotation(const int8_t *ico, const int32_t raw[4], uint64_t lambda, int64_t o[4]) {
   uint32_t r = snap_select(ico, raw);
   uint64_t lambda_phi = lambda + ((lambda * kPhiLo + (1ull << 31)) >> 32);
 #pragma unroll
@@ -702,6 +702,7 @@ FBS_HD void snap_rotation(const int8_t *ico, const int32_t raw[4], uint64_t lamb
                             lambda_phi * (uint64_t)(int64_t)ico[8 * r + 2 * c + 1]);
     o[c] = shift(sum, 1);
   }
+  return r;
 }
 
 // The unit quaternion of `stack_rotation` at Q30 before lambda, in 128-bit arithmetic (RS stack/session.rs:5165-5181):

@@ -1,9 +1,8 @@
-// fbs_prefill.hip - the prefill kernels: decode launches that generate nothing: the prompt, the choice at its last
-// position, and the exported session (the serving prefill).
+// fbs_prefill.hip - the prefill kernels: decode launches with no generated step (the prompt, its last choice, the state out); one wavefront per sequence.
 #include "fbs_run.h"
 
 namespace fbs {
 
-FBS_PHASE_KERNELS(fbs_prefill, kPhasePrefill)
+FBS_ONE_KERNELS(fbs_prefill, kPhasePrefill)
 
 }  // namespace fbs

@@ -1,9 +1,8 @@
-// fbs_rows.hip - the rows kernels: the teacher-forced modes: every position of each row, with its choice,
-// kept drawers and query (sequences) or the count of next-token matches (score).
+// fbs_rows.hip - the teacher-forced kernels: sequences and scoring; one wavefront per sequence.
 #include "fbs_run.h"
 
 namespace fbs {
 
-FBS_PHASE_KERNELS(fbs_rows, kPhaseRows)
+FBS_ONE_KERNELS(fbs_rows, kPhaseRows)
 
 }  // namespace fbs

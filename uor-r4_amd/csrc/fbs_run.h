@@ -225,26 +225,35 @@ __device__ __forceinline__ uint32_t prog_word(const uint16_t *prog, uint32_t slo
 // registers), so no caller array lives in private memory.
 struct Quat64 {
   int64_t v[4];
+  uint32_t root;  // the chosen root's index
 };
 __device__ __noinline__ Quat64 snap_rotation_dev(const int8_t *ico, int4 raw, uint64_t lambda) {
   const int32_t r[4] = {raw.x, raw.y, raw.z, raw.w};
   Quat64 q;
-  snap_rotation(ico, r, lambda, q.v);
+  q.root = snap_rotation(ico, r, lambda, q.v);
   return q;
 }
-__device__ __forceinline__ void snap_rotation_to(const int8_t *ico, int4 raw, uint64_t lambda,
-                                                 int64_t (&out)[4]) {
+// The snap trace's byte of a site (fbs_core.h:488-501, claude-134): the chosen root, or 255 where
+// none was chosen (served unsnapped) or the raw quaternion is zero.
+constexpr uint32_t kTraceNone = 255;
+__device__ __forceinline__ uint32_t trace_root(const int32_t (&raw)[4], uint32_t root) {
+  return (raw[0] | raw[1] | raw[2] | raw[3]) == 0 ? kTraceNone : root;
+}
+__device__ __forceinline__ uint32_t snap_rotation_to(const int8_t *ico, int4 raw, uint64_t lambda,
+                                                     int64_t (&out)[4]) {
   const Quat64 q = snap_rotation_dev(ico, raw, lambda);
 #pragma unroll
   for (int c = 0; c < 4; c++) out[c] = q.v[c];
+  return q.root;
 }
 
 // The Hamilton gate on rhs (session.rs:4951-4968, :4005-4025): shift_wide(q (x) rhs, 15) with
 // q the gate's unit quaternion (lambda 2^31, epsilon 0) or its icosian. Raw gates use q = 2 u
 // exactly, so the product is formed from u and shifted by 14.
-__device__ __forceinline__ void gate_apply(const DevModel &M, const Seeds &sd,
-                                           const int32_t (&raw)[4], const int64_t (&rhs)[4],
-                                           int64_t (&out)[4]) {
+// Returns the gate's snap trace byte.
+__device__ __forceinline__ uint32_t gate_apply(const DevModel &M, const Seeds &sd,
+                                               const int32_t (&raw)[4], const int64_t (&rhs)[4],
+                                               int64_t (&out)[4]) {
   i128 prod[4];
   if (M.raw_gates) {
     int32_t u[4];
@@ -252,19 +261,22 @@ __device__ __forceinline__ void gate_apply(const DevModel &M, const Seeds &sd,
     hamilton32(u, rhs, prod);
 #pragma unroll
     for (int c = 0; c < 4; c++) out[c] = shift_wide(prod[c], 14);
-  } else {
-    int64_t q[4];
-    snap_rotation_to(M.icosian, make_int4(raw[0], raw[1], raw[2], raw[3]), 1ull << 31, q);
-    hamilton64(q, rhs, prod);
-#pragma unroll
-    for (int c = 0; c < 4; c++) out[c] = shift_wide(prod[c], 15);
+    return kTraceNone;
   }
+  int64_t q[4];
+  const uint32_t root =
+      snap_rotation_to(M.icosian, make_int4(raw[0], raw[1], raw[2], raw[3]), 1ull << 31, q);
+  hamilton64(q, rhs, prod);
+#pragma unroll
+  for (int c = 0; c < 4; c++) out[c] = shift_wide(prod[c], 15);
+  return trace_root(raw, root);
 }
 
 // One MLP quaternion of the Hamilton feed-forward gate (session.rs:4005-4025): the gate of gq
 // applied to up. Raw gates use q = 2 u, and u (x) up fits in 64 bits.
-__device__ __forceinline__ void mlp_gate(const DevModel &M, const Seeds &sd, const int32_t (&gq)[4],
-                                         const int32_t (&up)[4], int64_t (&mo)[4]) {
+__device__ __forceinline__ uint32_t mlp_gate(const DevModel &M, const Seeds &sd,
+                                             const int32_t (&gq)[4], const int32_t (&up)[4],
+                                             int64_t (&mo)[4]) {
   if (M.raw_gates) {
     int32_t u[4];
     int64_t prod[4];
@@ -272,10 +284,10 @@ __device__ __forceinline__ void mlp_gate(const DevModel &M, const Seeds &sd, con
     hamilton32x32(u, up, prod);
 #pragma unroll
     for (int c = 0; c < 4; c++) mo[c] = shift_i64(prod[c], 14);
-  } else {
-    const int64_t up64[4] = {up[0], up[1], up[2], up[3]};
-    gate_apply(M, sd, gq, up64, mo);
+    return kTraceNone;
   }
+  const int64_t up64[4] = {up[0], up[1], up[2], up[3]};
+  return gate_apply(M, sd, gq, up64, mo);
 }
 
 // gate_apply split in two for paired blocks: gate_quat forms the gate's quaternion (the unit
@@ -339,8 +351,9 @@ struct ScanGeom {
 
 // Loads the rows of U row groups starting at candidate k0 (ids from the LDS list, or base_id + k
 // for the nearest head). Addresses are clamped into range so that every lane loads. Row offsets
-// fit 24-bit products (vocab < 2^24, d <= 1024).
-template <int S, int U, bool Full>
+// fit 24-bit products (vocab < 2^24, d <= 1024). T8: the int8 table's rows (8 bytes a piece,
+// into .x and .y, widened by scan_rows).
+template <int S, int U, bool Full, bool T8>
 __device__ __forceinline__ void scan_load(const DevModel &M, const uint32_t *list, uint32_t fill,
                                           uint32_t k0, const ScanGeom &g, uint32_t base_id,
                                           uint4 (&r)[U][4], uint32_t (&t)[U]) {
@@ -350,18 +363,38 @@ __device__ __forceinline__ void scan_load(const DevModel &M, const uint32_t *lis
     uint32_t k = k0 + u * rows + g.grp;
     k = k < fill ? k : fill - 1;
     t[u] = list ? list[k] : base_id + k;
-    const uint4 *row = (const uint4 *)(M.table_b + __umul24(t[u], g.stride));
-    if (Full) {
-#pragma unroll
-      for (int w = 0; w < 4; w++) r[u][w] = row[g.sub + S * w];
-    } else {
+    const uint32_t off = __umul24(t[u], g.stride);
+    if (T8) {
+      const uint2 *row = (const uint2 *)(M.table8 + off);
 #pragma unroll
       for (int w = 0; w < 4; w++) {
         const uint32_t piece = g.sub + S * w;
-        r[u][w] = row[piece <= g.last ? piece : g.last];
+        const uint2 b = row[Full || piece <= g.last ? piece : g.last];
+        r[u][w].x = b.x;
+        r[u][w].y = b.y;
+      }
+    } else {
+      const uint4 *row = (const uint4 *)(M.table_b + off);
+#pragma unroll
+      for (int w = 0; w < 4; w++) {
+        const uint32_t piece = g.sub + S * w;
+        r[u][w] = row[Full || piece <= g.last ? piece : g.last];
       }
     }
   }
+}
+
+// Four biased bytes (code + 128) of `x` as two words of 16-bit halves, each (code + 128) << s:
+// a byte permute places bytes 0, 1 (lo) and 2, 3 (hi) in the halves' low bytes, and a packed
+// 16-bit shift raises them.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void widen8(uint32_t x, u16x2 sh, uint32_t &lo, uint32_t &hi) {
+  const uint32_t a = __builtin_amdgcn_perm(0u, x, 0x0C010C00u);
+  const uint32_t b = __builtin_amdgcn_perm(0u, x, 0x0C030C02u);
+  u16x2 va = __builtin_bit_cast(u16x2, a) << sh;
+  u16x2 vb = __builtin_bit_cast(u16x2, b) << sh;
+  lo = __builtin_bit_cast(uint32_t, va);
+  hi = __builtin_bit_cast(uint32_t, vb);
 }
 
 template <int S, int U, bool Full>
@@ -409,31 +442,48 @@ __device__ __forceinline__ uint64_t scan_score(const uint32_t (&qpk)[16], uint32
 
 // Lowest (L1, token) over `fill` >= 1 candidates, two stages in flight: the rows of the next U
 // row groups load while the current ones are scored. Full: every piece of every lane lies
-// inside the row (compiled apart, so that the common widths carry no clamps or masks).
-template <int S, bool Full>
+// inside the row (compiled apart, so that the common widths carry no clamps or masks). T8: an
+// int8 table, whose rows load as bytes and widen in registers before the same scoring (kernels
+// of their own, so that neither form carries the other's registers).
+template <int S, bool Full, bool T8>
 __device__ __forceinline__ uint64_t scan_rows(const DevModel &M, const uint32_t (&qpk)[16],
                                               const uint32_t *list, uint32_t fill,
                                               uint32_t base_id, const ScanGeom &g, uint64_t best) {
   constexpr int U = kScanUnroll;
   constexpr uint32_t chunk = (kWave / S) * U;
+  const u16x2 sh = {(unsigned short)M.t8_shift, (unsigned short)M.t8_shift};
   uint4 ra[U][4], rb[U][4];
   uint32_t ta[U], tb[U];
-  scan_load<S, U, Full>(M, list, fill, 0, g, base_id, ra, ta);
+  auto widen = [&](uint4 (&r)[U][4]) {
+    if (T8) {
+#pragma unroll
+      for (int u = 0; u < U; u++)
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+          const uint32_t x = r[u][w].x, y = r[u][w].y;
+          widen8(x, sh, r[u][w].x, r[u][w].y);
+          widen8(y, sh, r[u][w].z, r[u][w].w);
+        }
+    }
+  };
+  scan_load<S, U, Full, T8>(M, list, fill, 0, g, base_id, ra, ta);
   for (uint32_t k0 = 0; k0 < fill; k0 += 2 * chunk) {
-    scan_load<S, U, Full>(M, list, fill, k0 + chunk, g, base_id, rb, tb);
+    scan_load<S, U, Full, T8>(M, list, fill, k0 + chunk, g, base_id, rb, tb);
+    widen(ra);
     best = scan_score<S, U, Full>(qpk, fill, k0, g, ra, ta, best);
-    scan_load<S, U, Full>(M, list, fill, k0 + 2 * chunk, g, base_id, ra, ta);
+    scan_load<S, U, Full, T8>(M, list, fill, k0 + 2 * chunk, g, base_id, ra, ta);
+    widen(rb);
     best = scan_score<S, U, Full>(qpk, fill, k0 + chunk, g, rb, tb, best);
   }
   return best;
 }
 
-template <int S>
+template <int S, bool T8>
 __device__ __forceinline__ uint64_t scan_list(const DevModel &M, const uint32_t (&qpk)[16],
                                               const uint32_t *list, uint32_t fill,
                                               uint32_t base_id, const ScanGeom &g, uint64_t best) {
-  return g.full ? scan_rows<S, true>(M, qpk, list, fill, base_id, g, best)
-                : scan_rows<S, false>(M, qpk, list, fill, base_id, g, best);
+  return g.full ? scan_rows<S, true, T8>(M, qpk, list, fill, base_id, g, best)
+                : scan_rows<S, false, T8>(M, qpk, list, fill, base_id, g, best);
 }
 
 // Drawers per lane held in registers by the writer (models of at most 64 kDrawerRegs drawers);
@@ -468,8 +518,8 @@ __device__ __forceinline__ void load_drawers(const DevModel &M, uint32_t lane, D
 
 // The scan geometry of this lane (S lanes per row, lane groups of S) and its four pieces of
 // the query as biased pairs: qpk[4 w + j] = (q[c] + 2^15) | (q[c + 1] + 2^15) << 16 with
-// c = 8 (sub + S w) + 2 j.
-template <int S>
+// c = 8 (sub + S w) + 2 j; T8: packed for the int8 table's widened rows instead.
+template <int S, bool T8>
 __device__ __forceinline__ void scan_setup(const DevModel &M, const int32_t *q, uint32_t lane,
                                            ScanGeom &g, uint32_t (&qpk)[16]) {
   const uint32_t d = M.d, pieces = d >> 3;  // S is the power of two >= d / 32
@@ -485,20 +535,33 @@ __device__ __forceinline__ void scan_setup(const DevModel &M, const int32_t *q, 
     const bool in = piece < pieces;
     g.valid |= (uint32_t)in << w;
     const uint32_t c = 8 * (in ? piece : 0);
+    if (T8) {
+      // Against (code + 128) << s: the query offset by 128 << s and clamped to the table's range
+      // [0, 255 << s], which adds the same amount to every candidate's L1 on the channel (the
+      // clamped-off distance), so the lowest (L1, token) is unchanged.
+      const int32_t off = 128 << M.t8_shift, top = 255 << M.t8_shift;
+      auto b = [&](int32_t v) -> uint32_t {
+        const int32_t x = v + off;
+        return (uint32_t)(x < 0 ? 0 : x > top ? top : x);
+      };
 #pragma unroll
-    for (int j = 0; j < 4; j++)
-      qpk[4 * w + j] = (uint32_t)(q[c + 2 * j] + 32768) | ((uint32_t)(q[c + 2 * j + 1] + 32768) << 16);
+      for (int j = 0; j < 4; j++) qpk[4 * w + j] = b(q[c + 2 * j]) | (b(q[c + 2 * j + 1]) << 16);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        qpk[4 * w + j] = (uint32_t)(q[c + 2 * j] + 32768) | ((uint32_t)(q[c + 2 * j + 1] + 32768) << 16);
+    }
   }
 }
 
 // The whole-table nearest head over tokens [lo, hi) (session.rs:4418-4445).
-template <int S>
+template <int S, bool T8>
 __device__ __forceinline__ uint64_t scan_nearest(const DevModel &M, const uint32_t (&qpk)[16],
                                                  uint32_t lo, uint32_t hi, const ScanGeom &g,
                                                  uint64_t best) {
   for (uint32_t b = lo; b < hi; b += kListCap) {
     const uint32_t fill = hi - b < kListCap ? hi - b : kListCap;
-    best = scan_list<S>(M, qpk, nullptr, fill, b, g, best);
+    best = scan_list<S, T8>(M, qpk, nullptr, fill, b, g, best);
   }
   return best;
 }
@@ -636,7 +699,7 @@ __device__ __forceinline__ void writer_select(const DevModel &M, const int32_t *
 
 // The lowest (L1, token) over the members of the ranges lanes 0..P-1 hold (session.rs:4100-4121):
 // member ids are staged in `list` (at most `cap` per segment) and scanned.
-template <int S>
+template <int S, bool T8>
 __device__ __forceinline__ uint64_t scan_members(const DevModel &M, const uint32_t (&qpk)[16],
                                                  uint32_t *list, uint32_t cap, const ScanGeom &g,
                                                  uint32_t lane, uint32_t my_beg, uint32_t my_end,
@@ -657,7 +720,7 @@ __device__ __forceinline__ uint64_t scan_members(const DevModel &M, const uint32
       }
     }
     wait_lds_dma();
-    if (fill) best = scan_list<S>(M, qpk, list, fill, 0, g, best);
+    if (fill) best = scan_list<S, T8>(M, qpk, list, fill, 0, g, best);
     wave_sync();
   }
   return best;
@@ -667,22 +730,22 @@ __device__ __forceinline__ uint64_t scan_members(const DevModel &M, const uint32
 // or the whole-table nearest head (session.rs:4418-4445). `q` holds the query (d words) in
 // LDS. Returns the token (UINT32_MAX when no row was scored); writes the kept drawers in
 // selection order to kept[] and kept_out (nullable).
-template <int S>
+template <int S, bool T8>
 __device__ __forceinline__ uint32_t writer(const DevModel &M, const int32_t *q, uint32_t *dscore,
                                            uint32_t *kept, uint32_t *list, uint32_t lane,
                                            uint32_t *kept_out) {
   ScanGeom g;
   uint32_t qpk[16];
-  scan_setup<S>(M, q, lane, g, qpk);
+  scan_setup<S, T8>(M, q, lane, g, qpk);
   uint64_t best = UINT64_MAX;
   if (M.head == 1) {
-    best = scan_nearest<S>(M, qpk, 0, M.vocab, g, best);
+    best = scan_nearest<S, T8>(M, qpk, 0, M.vocab, g, best);
     if (kept_out && lane < M.P) kept_out[lane] = 0;
   } else {
     uint32_t my_beg, my_end;
     writer_select(M, q, dscore, kept, lane, my_beg, my_end);
     if (kept_out && lane < M.P) kept_out[lane] = kept[lane];
-    best = scan_members<S>(M, qpk, list, kListCap, g, lane, my_beg, my_end, best);
+    best = scan_members<S, T8>(M, qpk, list, kListCap, g, lane, my_beg, my_end, best);
   }
   best = wave_reduce64(best, OpMin());
   return (uint32_t)best;
@@ -726,12 +789,14 @@ struct Lds {
 namespace fbs {
 
 // HM: the model's Hamming reads run at their hooks (row t of the session, `pay` its payload
-// caches).
-template <int Q, int SW, bool HM>
+// caches). `trace` (nullable): the position's snap trace, per layer the transition's root per
+// lane, the output gate's per lane, then the feed-forward gate's per MLP quaternion
+// (fbs_core.h:488-501).
+template <int Q, int SW, bool HM, bool T8>
 __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ring, uint32_t base, uint32_t lane,
                     const bool (&qv)[Q], const uint32_t (&qi)[Q], uint32_t tok, bool want_writer,
                     uint32_t *chosen, uint32_t *kept_out, int32_t *query_out, uint32_t t,
-                    int64_t *pay) {
+                    int64_t *pay, uint8_t *trace) {
   if (tok >= M.vocab) return 1;
   const uint32_t d = M.d, W = M.W, nq = M.nq;
   if (HM) {  // the read at this row needs x_0..=x_t (session.rs:4149-4152)
@@ -837,15 +902,19 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
       // The transition's rotation (session.rs:5097-5145).
       int32_t T[4];
       int64_t T64[4];
+      uint32_t root = kTraceNone;
       if (M.raw_transition) {
         int32_t u[4];
         unit_q30(rot[k], kRotationEps, u, S.seeds);
 #pragma unroll
         for (int c = 0; c < 4; c++) T[c] = u[c] >> idx;  // (lambda u) >> 30, lambda = 2^(30-idx)
       } else {
-        snap_rotation_to(M.icosian, make_int4(rot[k][0], rot[k][1], rot[k][2], rot[k][3]),
-                          lambda, T64);
+        root = trace_root(rot[k], snap_rotation_to(M.icosian, make_int4(rot[k][0], rot[k][1],
+                                                                         rot[k][2], rot[k][3]),
+                                                    lambda, T64));
       }
+      uint8_t *lt = trace ? trace + (uint64_t)l * (2 * nq + M.nm) : nullptr;
+      if (lt) lt[qi[k]] = (uint8_t)root;
       int64_t wide[4];
       if (M.taps_fast) {
         const uint2 t0 = td0[k];
@@ -901,7 +970,8 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
       int64_t rhs[4], o[4];
 #pragma unroll
       for (int c = 0; c < 4; c++) rhs[c] = shift(h[c], kResidualExp - kStateExp);
-      gate_apply(M, S.seeds, gv[k], rhs, o);
+      const uint32_t groot = gate_apply(M, S.seeds, gv[k], rhs, o);
+      if (lt) lt[nq + qi[k]] = (uint8_t)groot;
 #pragma unroll
       for (int c = 0; c < 4; c++) {
         sc[k][c] = o[c];
@@ -959,7 +1029,8 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
       }
       if (mq < M.nm) {
         int64_t mo[4];
-        mlp_gate(M, S.seeds, gq, up, mo);
+        const uint32_t mroot = mlp_gate(M, S.seeds, gq, up, mo);
+        if (trace) trace[(uint64_t)l * (2 * nq + M.nm) + 2 * nq + mq] = (uint8_t)mroot;
 #pragma unroll
         for (int c = 0; c < 4; c++) {
           S.mlp_out[4 * mq + c] = mo[c];
@@ -1033,7 +1104,7 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
       *chosen = S.wmeta[0];
       if (kept_out && lane < M.P) kept_out[lane] = M.head == 1 ? 0u : S.kept[lane];
     } else {
-      *chosen = writer<SW>(M, S.xbar, S.dscore, S.kept, S.list, lane, kept_out);
+      *chosen = writer<SW, T8>(M, S.xbar, S.dscore, S.kept, S.list, lane, kept_out);
 #pragma unroll
       for (int k = 0; k < Q; k++)
         if (qv[k]) *(int4 *)(S.wq + 4 * qi[k]) = qq[k];
@@ -1157,7 +1228,7 @@ __device__ __forceinline__ void pair_mlp_words(const DevModel &M, const DevLayer
 // the step reuses the last result): wave 0 selects the drawers, each wave scans half of the
 // candidates (by position in the kept drawers' concatenated members, or half of the table for
 // the nearest head), and both return the lower (L1, token).
-template <int SW>
+template <int SW, bool T8>
 __device__ __forceinline__ uint32_t pair_writer(const DevModel &M, const Lds &S, uint32_t wave,
                                                 uint32_t lane, uint32_t *kept_out) {
   if (S.wmeta[2]) {
@@ -1175,11 +1246,11 @@ __device__ __forceinline__ uint32_t pair_writer(const DevModel &M, const Lds &S,
   pair_sync();  // 7: the kept drawers and their ranges
   ScanGeom g;
   uint32_t qpk[16];
-  scan_setup<SW>(M, S.xbar, lane, g, qpk);
+  scan_setup<SW, T8>(M, S.xbar, lane, g, qpk);
   uint64_t best = UINT64_MAX;
   if (M.head == 1) {
     const uint32_t half = M.vocab / 2;
-    best = scan_nearest<SW>(M, qpk, wave ? half : 0, wave ? M.vocab : half, g, best);
+    best = scan_nearest<SW, T8>(M, qpk, wave ? half : 0, wave ? M.vocab : half, g, best);
     if (wave == 0 && kept_out && lane < M.P) kept_out[lane] = 0;
   } else {
     if (wave == 0 && kept_out && lane < M.P) kept_out[lane] = S.kept[lane];
@@ -1187,7 +1258,7 @@ __device__ __forceinline__ uint32_t pair_writer(const DevModel &M, const Lds &S,
     const uint32_t total = wave_reduce32(my_end - my_beg, OpAdd()), half = (total + 1) / 2;
     clip_ranges(M.P, lane, wave ? half : 0, wave ? total : half, my_beg, my_end);
     constexpr uint32_t cap = kListCap / 2;
-    best = scan_members<SW>(M, qpk, S.list + wave * cap, cap, g, lane, my_beg, my_end, best);
+    best = scan_members<SW, T8>(M, qpk, S.list + wave * cap, cap, g, lane, my_beg, my_end, best);
   }
   best = wave_reduce64(best, OpMin());
   if (lane == 0) S.pair[2 + wave] = best;
@@ -1198,7 +1269,7 @@ __device__ __forceinline__ uint32_t pair_writer(const DevModel &M, const Lds &S,
 
 // Wave 0 of a paired block: the step (RS stack/session.rs:4129-4403) but the window and its
 // ring, the output gates' quaternions and the odd MLP groups.
-template <int Q, int SW>
+template <int Q, int SW, bool T8>
 __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32_t lane,
                                          const bool (&qv)[Q], const uint32_t (&qi)[Q], uint32_t tok,
                                          bool want_writer, uint32_t *chosen, uint32_t *kept_out,
@@ -1388,7 +1459,7 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
   const bool reuse = S.wmeta[1] != 0 && __all(same);
   if (lane == 0) S.wmeta[2] = reuse;
   pair_sync();  // 6: the query and the reuse flag
-  *chosen = pair_writer<SW>(M, S, 0, lane, kept_out);
+  *chosen = pair_writer<SW, T8>(M, S, 0, lane, kept_out);
   if (!reuse) {
 #pragma unroll
     for (int k = 0; k < Q; k++)
@@ -1463,7 +1534,7 @@ __device__ __forceinline__ void window_sum(const DevModel &M, const DevLayer &ly
 // The window's terms over earlier positions (taps 1..W) do not depend on the step's input, so
 // wave 1 sums them for the next step while wave 0 runs the transport, and keeps them in `hist`
 // (L x d i64 per block); the first step of a launch sums its own (`fresh`).
-template <int Q, int SW>
+template <int Q, int SW, bool T8>
 __device__ __forceinline__ int step_window(const DevModel &M, const Lds &S, int32_t *ring,
                                            int64_t *hist, uint32_t base, uint32_t lane,
                                            const bool (&qv)[Q], const uint32_t (&qi)[Q],
@@ -1549,7 +1620,7 @@ __device__ __forceinline__ int step_window(const DevModel &M, const Lds &S, int3
   }
   if (!want_writer) return 0;
   pair_sync();  // 6: the query and the reuse flag
-  *chosen = pair_writer<SW>(M, S, 1, lane, nullptr);
+  *chosen = pair_writer<SW, T8>(M, S, 1, lane, nullptr);
   return 0;
 }
 
@@ -1559,8 +1630,9 @@ __device__ __forceinline__ int step_window(const DevModel &M, const Lds &S, int3
 enum Phase : int { kPhasePrefill = 0, kPhaseDecode = 1, kPhaseRows = 2 };
 
 // NW = 1: one wavefront per sequence (step); NW = 2: paired blocks (step_main, step_window).
-// HM: a model with Hamming reads (one wavefront per sequence).
-template <int Q, int SW, int PH, int NW, bool HM = false>
+// HM: a model with Hamming reads (one wavefront per sequence); T8: a model with an int8 table,
+// whose writer scans its bytes.
+template <int Q, int SW, int PH, int NW, bool HM = false, bool T8 = false>
 __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
   static_assert(!HM || NW == 1, "the Hamming reads run on one wavefront per sequence");
   extern __shared__ __align__(16) int32_t lds[];
@@ -1755,8 +1827,10 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
                            : last       ? A.out_query + (uint64_t)s * d
                                         : nullptr;
       if (NW == 1) {
-        status = step<Q, SW, HM>(M, S, ring, base, lane, qv, qi, tok, want, &chosen, kept_out,
-                                 query_out, pos, pay);
+        uint8_t *trace = A.out_trace && seq ? A.out_trace + at * (uint64_t)M.L * (2 * M.nq + M.nm)
+                                            : nullptr;
+        status = step<Q, SW, HM, T8>(M, S, ring, base, lane, qv, qi, tok, want, &chosen, kept_out,
+                                 query_out, pos, pay, trace);
       } else {
         // The lane's indices pass through an empty asm at every step, so that the compiler forms
         // the lane's addresses inside the loop instead of holding them across the kernel.
@@ -1768,9 +1842,9 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
           asm volatile("" : "+v"(qs[k]));
         }
         if (wave == 0)
-          status = step_main<Q, SW>(M, S, ln, qv, qs, tok, want, &chosen, kept_out, query_out);
+          status = step_main<Q, SW, T8>(M, S, ln, qv, qs, tok, want, &chosen, kept_out, query_out);
         else
-          status = step_window<Q, SW>(M, S, ring, hist, base, ln, qv, qs, tok, want,
+          status = step_window<Q, SW, T8>(M, S, ring, hist, base, ln, qv, qs, tok, want,
                                       t == 0 && fresh, &chosen);
       }
       if (status) break;
@@ -1860,33 +1934,67 @@ inline hipError_t launch_shape(const KernelSet &k, const DevModel &M, const RunA
   return e != hipSuccess ? e : hipGetLastError();
 }
 
-// The phase's kernels: `NAME<Q, SW>` (one wavefront per sequence), `NAME_pair<Q, SW>` (paired
-// blocks, at most 256 registers per lane so that two waves share each SIMD) and
-// `hipError_t launch_NAME(M, A, grid, waves, lds, stream)`.
-#define FBS_PHASE_KERNELS(NAME, PH)                                                          \
+// The phase's kernels, one family per translation unit (so that the units compile in parallel):
+// FBS_ONE_KERNELS: `NAME<Q, SW>` (one wavefront per sequence); FBS_PAIR_KERNELS: `NAME_pair<Q, SW>`
+// (paired blocks, at most 256 registers per lane so that two waves share each SIMD);
+// FBS_HAM_KERNELS: `NAME_ham<Q, SW>` (one wavefront per sequence with the Hamming reads; their
+// writer scans the 16-bit table); FBS_ONE8_KERNELS / FBS_PAIR8_KERNELS: `NAME_8`, `NAME_pair8`,
+// the first two for an int8 table. Each defines `hipError_t launch_NAME[_pair|_ham|_8|_pair8](M,
+// A, grid, lds, stream)`.
+#define FBS_ONE_KERNELS(NAME, PH)                                                            \
   template <int Q, int SW>                                                                    \
   __global__ __launch_bounds__(64) void NAME(DevModel M, RunArgs A) {                         \
     run<Q, SW, PH, 1>(M, A);                                                                  \
   }                                                                                           \
+  hipError_t launch_##NAME(const DevModel &M, const RunArgs &A, uint32_t grid, size_t lds,    \
+                           hipStream_t stream) {                                              \
+    static const KernelSet k = {NAME<1, 1>, NAME<1, 2>, NAME<1, 4>,                           \
+                                NAME<1, 8>, NAME<2, 16>, NAME<4, 32>};                         \
+    return launch_shape(k, M, A, grid, 1, lds, stream);                                       \
+  }
+#define FBS_ONE8_KERNELS(NAME, PH)                                                           \
+  template <int Q, int SW>                                                                    \
+  __global__ __launch_bounds__(64) void NAME##_8(DevModel M, RunArgs A) {                     \
+    run<Q, SW, PH, 1, false, true>(M, A);                                                     \
+  }                                                                                           \
+  hipError_t launch_##NAME##_8(const DevModel &M, const RunArgs &A, uint32_t grid, size_t lds, \
+                               hipStream_t stream) {                                          \
+    static const KernelSet k = {NAME##_8<1, 1>, NAME##_8<1, 2>, NAME##_8<1, 4>,               \
+                                NAME##_8<1, 8>, NAME##_8<2, 16>, NAME##_8<4, 32>};             \
+    return launch_shape(k, M, A, grid, 1, lds, stream);                                       \
+  }
+#define FBS_PAIR8_KERNELS(NAME, PH)                                                          \
+  template <int Q, int SW>                                                                    \
+  __global__ __launch_bounds__(128, 2) void NAME##_pair8(DevModel M, RunArgs A) {             \
+    run<Q, SW, PH, 2, false, true>(M, A);                                                     \
+  }                                                                                           \
+  hipError_t launch_##NAME##_pair8(const DevModel &M, const RunArgs &A, uint32_t grid,        \
+                                   size_t lds, hipStream_t stream) {                          \
+    static const KernelSet k = {NAME##_pair8<1, 1>, NAME##_pair8<1, 2>, NAME##_pair8<1, 4>,   \
+                                NAME##_pair8<1, 8>, NAME##_pair8<2, 16>, NAME##_pair8<4, 32>}; \
+    return launch_shape(k, M, A, grid, 2, lds, stream);                                       \
+  }
+#define FBS_PAIR_KERNELS(NAME, PH)                                                           \
   template <int Q, int SW>                                                                    \
   __global__ __launch_bounds__(128, 2) void NAME##_pair(DevModel M, RunArgs A) {              \
     run<Q, SW, PH, 2>(M, A);                                                                  \
   }                                                                                           \
+  hipError_t launch_##NAME##_pair(const DevModel &M, const RunArgs &A, uint32_t grid,         \
+                                  size_t lds, hipStream_t stream) {                           \
+    static const KernelSet k = {NAME##_pair<1, 1>, NAME##_pair<1, 2>, NAME##_pair<1, 4>,      \
+                                NAME##_pair<1, 8>, NAME##_pair<2, 16>, NAME##_pair<4, 32>};    \
+    return launch_shape(k, M, A, grid, 2, lds, stream);                                       \
+  }
+#define FBS_HAM_KERNELS(NAME, PH)                                                            \
   template <int Q, int SW>                                                                    \
   __global__ __launch_bounds__(64) void NAME##_ham(DevModel M, RunArgs A) {                   \
     run<Q, SW, PH, 1, true>(M, A);                                                            \
   }                                                                                           \
-  hipError_t launch_##NAME(const DevModel &M, const RunArgs &A, uint32_t grid, uint32_t waves, \
-                           size_t lds, hipStream_t stream) {                                  \
-    static const KernelSet one = {NAME<1, 1>, NAME<1, 2>, NAME<1, 4>,                         \
-                                  NAME<1, 8>, NAME<2, 16>, NAME<4, 32>};                       \
-    static const KernelSet two = {NAME##_pair<1, 1>, NAME##_pair<1, 2>, NAME##_pair<1, 4>,    \
-                                  NAME##_pair<1, 8>, NAME##_pair<2, 16>, NAME##_pair<4, 32>};  \
-    static const KernelSet ham = {NAME##_ham<1, 1>, NAME##_ham<1, 2>, NAME##_ham<1, 4>,       \
-                                  NAME##_ham<1, 8>, NAME##_ham<2, 16>, NAME##_ham<4, 32>};     \
-    if (M.ham.heads && waves != 1) return hipErrorInvalidValue;                               \
-    return launch_shape(M.ham.heads ? ham : waves == 2 ? two : one, M, A, grid, waves, lds,   \
-                        stream);                                                              \
+  hipError_t launch_##NAME##_ham(const DevModel &M, const RunArgs &A, uint32_t grid,          \
+                                 size_t lds, hipStream_t stream) {                            \
+    static const KernelSet k = {NAME##_ham<1, 1>, NAME##_ham<1, 2>, NAME##_ham<1, 4>,         \
+                                NAME##_ham<1, 8>, NAME##_ham<2, 16>, NAME##_ham<4, 32>};       \
+    return launch_shape(k, M, A, grid, 1, lds, stream);                                       \
   }
 
 }  // namespace fbs

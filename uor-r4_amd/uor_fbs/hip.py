@@ -34,7 +34,8 @@ SYMBOLS = (
     "uor_fbs_index_update_async", "uor_fbs_index_remove_async", "uor_fbs_index_validate_async",
     "uor_fbs_index_probe_async", "uor_fbs_index_full_scan_async", "uor_fbs_stream_words",
     "uor_fbs_payload_words", "uor_fbs_decode_stream", "uor_fbs_decode_stream_async",
-    "uor_fbs_slot_cache_bytes", "uor_fbs_serve_slots_async",
+    "uor_fbs_slot_cache_bytes", "uor_fbs_serve_slots_async", "uor_fbs_trace_stride",
+    "uor_fbs_trace_sequences", "uor_fbs_trace_sequences_async",
 )
 
 
@@ -80,6 +81,10 @@ def lib():
                                                   + [P] * 13)
         L.uor_fbs_decode_slots_async.argtypes = [P, P, C.c_uint32, C.c_uint32, P, C.c_uint32,
                                                  C.c_uint32, P, P, P, P, P, P, P, P]
+        L.uor_fbs_trace_stride.argtypes = [P]
+        L.uor_fbs_trace_stride.restype = C.c_uint64
+        L.uor_fbs_trace_sequences.argtypes = [P, P, C.c_uint32, C.c_uint32, P, P, P, P]
+        L.uor_fbs_trace_sequences_async.argtypes = [P, P, C.c_uint32, C.c_uint32, P, P, P, P, P, P]
         L.uor_fbs_slot_cache_bytes.argtypes = [P]
         L.uor_fbs_slot_cache_bytes.restype = C.c_uint64
         L.uor_fbs_serve_slots_async.argtypes = [P, P, C.c_uint32, C.c_uint32, P, C.c_uint32,
@@ -205,6 +210,20 @@ class Model:
             *[_vp(a) for a in ins], _vp(out["state"]), _vp(out["history"]), _vp(out["position"]),
             _vp(out["tokens"]) if tw else None, _vp(out["payloads"]) if pw else None))
         return out
+
+    def trace_sequences(self, tokens):
+        """Teacher-forced runs with every position's snap trace: (tokens [S,len], kept
+        [S,len,P], query [S,len,d], trace [S,len,stride] u8)."""
+        tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+        S, n = tokens.shape
+        stride = int(lib().uor_fbs_trace_stride(self.handle))
+        out_t = np.zeros((S, n), np.uint32)
+        out_k = np.zeros((S, n, self.probes), np.uint32)
+        out_q = np.zeros((S, n, self.width), np.int32)
+        out_tr = np.zeros((S, n, stride), np.uint8)
+        _check(lib().uor_fbs_trace_sequences(self.handle, _vp(tokens), S, n, _vp(out_t), _vp(out_k),
+                                             _vp(out_q), _vp(out_tr)))
+        return out_t, out_k, out_q, out_tr
 
     def score(self, rows, want_argmin=True):
         """Teacher-forced scoring: (matches, argmin [n, len] or None)."""
