@@ -45,7 +45,7 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 # passes, scaled by a copy kernel's reading), for the workload each summary names.
 TRAFFIC_SUMMARIES = {
     "c2": "fbs_decode_pair_c2_b1024_traffic.md", "c3": "fbs_decode_pair_c3_b1024_traffic.md",
-    "c4": "fbs_rows_pair_c4_r1048576_traffic.md", "c5": "fbs_decode_pair_c5_b16384_traffic.md",
+    "c4": "fbs_rows_pair_c4_r1048576_traffic.md", "c5": "fbs_decode_pair8_c5_b16384_traffic.md",
     "hamming": "fbs_decode_ham_c3_b1024_traffic.md"}
 D11_TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "d11_score_rows_m1_traffic.md")
 # BASELINE.json's configs at their full shapes: (sequences, prompt, decode steps); c4 is
@@ -429,6 +429,8 @@ def score_main(a, torch, oracle, art, model, rows, dev, stream, sp) -> dict:
     while S < spec.width // 32:
         S *= 2
     family = "fbs_rows_pair" if model.block_waves(R) == 2 else "fbs_rows"
+    if spec.table == "i8":  # the int8 table's own kernels (fbs_rows_pair8, fbs_rows_8)
+        family += "8" if family.endswith("pair") else "_8"
     out = {
         "metric": f"teacher-forced scored positions/sec, {R} rows x {n}, width {spec.width} (1 GPU)",
         "value": round(positions / (ms_per_step / 1e3), 1), "unit": "positions/s", "n_gpus": 1,
@@ -977,6 +979,8 @@ def main():
     while S < spec.width // 32:
         S *= 2
     family = "fbs_decode_pair" if model.block_waves(B) == 2 else "fbs_decode"
+    if spec.table == "i8":  # the int8 table's own kernels (fbs_decode_pair8, fbs_decode_8)
+        family += "8" if family.endswith("pair") else "_8"
     kernel = f"{family}<{(spec.width // 4 + 63) // 64}, {S}>"
     traffic = measured_traffic(a, kernel)
 

@@ -93,11 +93,6 @@ struct DevModel {
   const int16_t *final_gain;
   const uint16_t *final_gain_desc;
   const uint16_t *table_b;  // vocab * d, biased
-  // An int8 table (uor_fbs_ext.table_i8): its codes biased, code + 128, vocab * d bytes, which
-  // the writer's scan reads in place of table_b (half the bytes a candidate row moves); null
-  // for an i16 table.
-  const uint8_t *table8;
-  uint32_t t8_shift;        // the int8 table's shift to Q12
   const int16_t *keys;      // D * 16
   const uint32_t *offsets;  // D + 1
   const uint32_t *members;  // offsets[D]
@@ -105,6 +100,11 @@ struct DevModel {
   const uint64_t *keep_q31; // 16
   const int64_t *eps_int;   // 9: the RMSNorm epsilon at each pre-shift 0..8
   DevHam ham;
+  // An int8 table (uor_fbs_ext.table_i8): its codes biased, code + 128, vocab * d bytes, which
+  // the writer's scan reads in place of table_b (half the bytes a candidate row moves); null
+  // for an i16 table. Last, so that the other fields keep their kernel-argument offsets.
+  const uint8_t *table8;
+  uint32_t t8_shift;        // the int8 table's shift to Q12
 };
 
 // LDS bytes per block (the layout the kernels carve): the gather crossbar, the MLP outputs, the

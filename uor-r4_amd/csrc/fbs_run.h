@@ -363,9 +363,8 @@ __device__ __forceinline__ void scan_load(const DevModel &M, const uint32_t *lis
     uint32_t k = k0 + u * rows + g.grp;
     k = k < fill ? k : fill - 1;
     t[u] = list ? list[k] : base_id + k;
-    const uint32_t off = __umul24(t[u], g.stride);
     if (T8) {
-      const uint2 *row = (const uint2 *)(M.table8 + off);
+      const uint2 *row = (const uint2 *)(M.table8 + __umul24(t[u], g.stride));
 #pragma unroll
       for (int w = 0; w < 4; w++) {
         const uint32_t piece = g.sub + S * w;
@@ -374,11 +373,16 @@ __device__ __forceinline__ void scan_load(const DevModel &M, const uint32_t *lis
         r[u][w].y = b.y;
       }
     } else {
-      const uint4 *row = (const uint4 *)(M.table_b + off);
+      const uint4 *row = (const uint4 *)(M.table_b + __umul24(t[u], g.stride));
+      if (Full) {
 #pragma unroll
-      for (int w = 0; w < 4; w++) {
-        const uint32_t piece = g.sub + S * w;
-        r[u][w] = row[Full || piece <= g.last ? piece : g.last];
+        for (int w = 0; w < 4; w++) r[u][w] = row[g.sub + S * w];
+      } else {
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+          const uint32_t piece = g.sub + S * w;
+          r[u][w] = row[piece <= g.last ? piece : g.last];
+        }
       }
     }
   }
