@@ -1060,7 +1060,7 @@ def main():
                 check(L.uor_fbs_serve_slots_async(
                     model.handle, ptr(d_slots), B, B, ptr(served[k]), 1, 0, ptr(served[k + 1]),
                     ptr(s_state), ptr(s_hist), ptr(s_pos), ptr(cache) if cached else None, None,
-                    None, None, ptr(status), sp))
+                    None, None, None, ptr(status), sp))
                 ev[k][1].record(stream)
             torch.cuda.synchronize()
             wall_ = time.perf_counter() - t0

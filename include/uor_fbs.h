@@ -311,6 +311,13 @@ int uor_fbs_decode_stream(uor_fbs_handle *handle, const uint32_t *prompts, uint3
  *   beyond the window ring's slot). NULL: no slot slides. The reference refuses the slide for a
  *   model with Hamming reads or a turn memory; this entry refuses Hamming models and the caller
  *   (uor_fbs/session.py) the rest.
+ * - `out_trace`: the snap trace of every step, sequences * (prompt_len + gen) *
+ *   uor_fbs_trace_stride(handle) bytes, laid out as uor_fbs_trace_sequences' (per step, per
+ *   layer: transition roots per lane, output gate roots, feed-forward gate roots). A session's
+ *   opt-in snap trace (IntegerStackSession::enable_snap_trace, session.rs:2570-2620) records the
+ *   transition roots (stack_lanes, session.rs:5097-5150); a zero raw quaternion, 255 here,
+ *   selects root 0 there. Rows of steps a slot did not run are left as they were. NULL: no
+ *   trace; otherwise the launch runs the one-wavefront kernels.
  * No counterpart beyond those: the reference's sessions keep their window sums implicitly (a CPU
  * session steps one token at a time). Device buffers. */
 uint64_t uor_fbs_slot_cache_bytes(const uor_fbs_handle *handle);
@@ -318,8 +325,8 @@ int uor_fbs_serve_slots_async(uor_fbs_handle *handle, const uint32_t *slots, uin
                               uint32_t capacity, const uint32_t *prompts, uint32_t prompt_len,
                               uint32_t gen, uint32_t *out_reply, int64_t *state, int32_t *history,
                               uint32_t *position, void *cache, const uint8_t *slide,
-                              uint32_t *out_kept, int32_t *out_query, int32_t *status,
-                              void *stream);
+                              uint32_t *out_kept, int32_t *out_query, uint8_t *out_trace,
+                              int32_t *status, void *stream);
 
 /* Teacher-forced next-token scoring: for each row of `len` tokens, position t's choice is
  * compared with row[t+1] (t < len-1); `out_matches` gets the total count of equal pairs.

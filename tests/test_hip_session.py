@@ -307,7 +307,8 @@ def test_the_serving_cache_equals_launches_without_it(art):
             reply = DeviceArray((n, 1), np.uint32)
             hip._check(L.uor_fbs_serve_slots_async(
                 model.handle, d_slots.ptr, n, cap, d_tok.ptr, toks.shape[1], 0, reply.ptr, st.ptr,
-                hi.ptr, po.ptr, None if ca is None else ca.ptr, None, None, None, status.ptr, None))
+                hi.ptr, po.ptr, None if ca is None else ca.ptr, None, None, None, None, status.ptr,
+                None))
             assert (status.download() == 0).all()
             r = reply.download()
             got.append(r[:, 0])
@@ -315,3 +316,44 @@ def test_the_serving_cache_equals_launches_without_it(art):
         outs.append(np.stack(got, 1))
     np.testing.assert_array_equal(outs[0], outs[1])
     np.testing.assert_array_equal(outs[0], want["reply"])
+
+
+def test_snap_trace_follows_the_oracle():
+    """enable_snap_trace on the device path: each step's transition roots (stack_lanes,
+    session.rs:5117-5124) from the traced slot launch equal the oracle's teacher-forced trace;
+    a traced snapshot continues its trace in another slot; the served tokens are unchanged."""
+    from uor_fbs.session import transition_roots
+    spec = replace(SPEC, raw_transition=False, raw_gates=False)
+    art = synth.make_artifact(spec, 89)
+    tokens = synth.uniform_prompts(spec.vocab, 1, 24, 97)[0]
+    st, want_tok, _, _, tr = oracle.trace_sequences(art, tokens[None], threads=2)
+    assert st == 0
+    lanes = spec.width // 4
+    per = spec.layers * lanes
+    want = transition_roots(tr[0], spec.layers, lanes)
+    print(f"snap trace: width {spec.width}, {spec.layers} layers, {len(tokens)} tokens", flush=True)
+    pool = SessionPool(hip.Model(art), capacity=5)
+    a, b, c = Session(pool), Session(pool), Session(pool)
+    a.feed(tokens[:3])
+    a.enable_snap_trace()
+    assert a.feed(tokens[3:9]).token == want_tok[0, 8]
+    for k in range(9, 14):
+        assert a.serve_step(int(tokens[k]))[0] == want_tok[0, k]
+    got = a.snap_trace()
+    assert [e.root for e in got] == want[3 * per:14 * per].tolist()
+    assert (got[0].position, got[-1].position) == (3, 13)
+    assert a.save_state().snap_trace is None
+    b.enable_snap_trace()
+    b.feed(tokens[:10])
+    snap = b.save_state()
+    assert snap.snap_trace == want[:10 * per].tolist()
+    c.restore_state(session_codec.decode(session_codec.encode(snap)))
+    replies = serve_steps([c, a], [int(tokens[10]), int(tokens[14])])
+    assert (replies[0][0], replies[1][0]) == (want_tok[0, 10], want_tok[0, 14])
+    for t in tokens[11:]:
+        c.serve_step(int(t))
+    assert c.save_state().snap_trace == want.tolist()
+    assert [e.root for e in a.snap_trace()] == want[3 * per:15 * per].tolist()
+    b.reset()
+    b.feed(tokens[:5])
+    assert b.save_state().snap_trace == want[:5 * per].tolist()

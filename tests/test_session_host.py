@@ -6,11 +6,13 @@ import dataclasses
 import hashlib
 import os
 
+import numpy as np
 import pytest
 
 from conftest import GOLDEN
 from uor_fbs import synth, uorlut
-from uor_fbs.session import (ModelInfo, SessionError, max_serialized_session_bytes, model_identity,
+from uor_fbs.session import (TRACE_UNSET, ModelInfo, SessionError, SnapTrace,
+                             max_serialized_session_bytes, model_identity, transition_roots,
                              validate_restore)
 from uor_fbs.session_codec import (STACK_SESSION_SCHEMA, ReadLayer, RecurrenceLayer,
                                    SerializedStackSession)
@@ -69,10 +71,7 @@ def test_snapped_traces():
     with pytest.raises(SessionError) as e:  # the wrong length
         validate_restore(info, ok)
     assert e.value.kind == "SessionState"
-    full = saved(snap_trace=[7] * (3 * lanes * info.layers))
-    with pytest.raises(SessionError) as e:  # right, but the GPU path keeps no trace
-        validate_restore(info, full)
-    assert e.value.kind == "Shape"
+    validate_restore(info, saved(snap_trace=[7] * (3 * lanes * info.layers)))
     with pytest.raises(SessionError) as e:
         validate_restore(info, saved(snap_trace=[120] * (3 * lanes * info.layers)))
     assert e.value.kind == "SessionState"
@@ -96,3 +95,27 @@ def test_serving_identity():
     b = synth.make_artifact(synth.SMALL, 2)
     assert model_identity(a) == model_identity(synth.make_artifact(synth.SMALL, 1))
     assert model_identity(a) != model_identity(b) and len(model_identity(a)) == 64
+
+
+def test_snap_trace_buffer():
+    """SnapTrace::record (session.rs:2050-2058): stores in order while room is left, and keeps
+    counting past the end; clear (session.rs:2728-2737) starts over with every entry unset."""
+    t = SnapTrace(5, 2)
+    t.record([3, 4])
+    t.record([5, 6, 7, 8])
+    assert t.selected.tolist() == [3, 4, 5, 6, 7] and t.written == 6 and t.origin_position == 2
+    t.clear(7)
+    assert t.selected.tolist() == [TRACE_UNSET] * 7 and t.written == 0 and t.origin_position == 0
+
+
+def test_transition_roots_from_trace_bytes():
+    """Per step, per layer, the first width/4 bytes (the transition's roots) of the layer's
+    2 width/4 + mlp/4; the zero-quaternion byte reads as root 0."""
+    layers, lanes, mlp4 = 2, 3, 2
+    per_layer = 2 * lanes + mlp4
+    tr = np.arange(3 * layers * per_layer, dtype=np.uint8).reshape(3, layers * per_layer) % 119
+    tr[1, per_layer + 2] = 255
+    got = transition_roots(tr, layers, lanes)
+    want = [int(tr[s, l * per_layer + k]) for s in range(3) for l in range(layers) for k in range(lanes)]
+    want[(1 * layers + 1) * lanes + 2] = 0
+    assert got.tolist() == want

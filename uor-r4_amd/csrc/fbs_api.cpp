@@ -989,8 +989,8 @@ extern "C" int uor_fbs_serve_slots_async(uor_fbs_handle *h, const uint32_t *slot
                                          const uint32_t *prompts, uint32_t prompt_len, uint32_t gen,
                                          uint32_t *out_reply, int64_t *state, int32_t *history,
                                          uint32_t *position, void *cache, const uint8_t *slide,
-                                         uint32_t *out_kept, int32_t *out_query, int32_t *status,
-                                         void *stream) {
+                                         uint32_t *out_kept, int32_t *out_query, uint8_t *out_trace,
+                                         int32_t *status, void *stream) {
   if (!h || !slots || !prompts || !out_reply || !state || !history || !position || !status)
     return fail(UOR_FBS_ERR_ARGUMENT, "null argument");
   if (prompt_len == 0) return fail(UOR_FBS_ERR_ARGUMENT, "a step needs at least one token");
@@ -1019,7 +1019,9 @@ extern "C" int uor_fbs_serve_slots_async(uor_fbs_handle *h, const uint32_t *slot
   A.cache = (uint8_t *)cache;
   A.cache_stride = slot_cache_layout(h->M).bytes;
   A.slide = slide;
-  return launch(h, A, (hipStream_t)stream);
+  A.out_trace = out_trace;
+  // The trace is recorded by the one-wavefront kernels.
+  return launch(h, A, (hipStream_t)stream, false, out_trace != nullptr);
 }
 
 extern "C" int uor_fbs_decode(uor_fbs_handle *h, const uint32_t *prompts, uint32_t sequences,

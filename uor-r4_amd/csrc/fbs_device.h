@@ -195,8 +195,8 @@ struct RunArgs {
   uint8_t *cache;
   uint32_t cache_stride;
   const uint8_t *slide;
-  // Sequences on one wavefront a sequence: every position's snap trace, L (2 d/4 + m/4) bytes
-  // a position (null: none).
+  // One wavefront a sequence only: the snap trace, L (2 d/4 + m/4) bytes a position, of every
+  // position (sequences) or of every step, len + gen a sequence (decode) (null: none).
   uint8_t *out_trace;
 };
 

@@ -1831,8 +1831,11 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
                            : last       ? A.out_query + (uint64_t)s * d
                                         : nullptr;
       if (NW == 1) {
-        uint8_t *trace = A.out_trace && seq ? A.out_trace + at * (uint64_t)M.L * (2 * M.nq + M.nm)
-                                            : nullptr;
+        // Sequences: every position's trace; decode: every step's, len + gen a sequence (not
+        // with Hamming reads, whose serving slots are refused).
+        uint8_t *trace = !A.out_trace || (HM && decode) ? nullptr
+                         : A.out_trace + (decode ? (uint64_t)s * (A.len + A.gen) + t : at) *
+                                             ((uint64_t)M.L * (2 * M.nq + M.nm));
         status = step<Q, SW, HM, T8>(M, S, ring, base, lane, qv, qi, tok, want, &chosen, kept_out,
                                  query_out, pos, pay, trace);
       } else {

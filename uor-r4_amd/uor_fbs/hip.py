@@ -88,7 +88,7 @@ def lib():
         L.uor_fbs_slot_cache_bytes.argtypes = [P]
         L.uor_fbs_slot_cache_bytes.restype = C.c_uint64
         L.uor_fbs_serve_slots_async.argtypes = [P, P, C.c_uint32, C.c_uint32, P, C.c_uint32,
-                                                C.c_uint32, P, P, P, P, P, P, P, P, P, P]
+                                                C.c_uint32, P, P, P, P, P, P, P, P, P, P, P]
         L.uor_fbs_score.argtypes = [P, P, C.c_uint64, C.c_uint32, P, P]
         L.uor_fbs_score_async.argtypes = [P, P, C.c_uint64, C.c_uint32, P, P, P, P]
         u32 = C.c_uint32

@@ -11,9 +11,9 @@ have a token ready (`serve_steps`) without moving state through the host. `Sessi
 reference's per-call semantics; its snapshots are the reference's `SerializedStackSession`,
 encodable as `UR4SESS1` bytes or the JSON of `save_session_to_file` (`session_codec`).
 
-What the GPU path does not keep (and so refuses to restore, rather than continuing
-differently): snap traces (opt-in diagnostics of snapped transports) and read-layer caches
-(the FBS trunk has none).
+A session's opt-in snap trace (`enable_snap_trace`) records each step's transition roots from
+the launch's trace output. What the GPU path does not keep (and so refuses to restore, rather
+than continuing differently): read-layer caches (the FBS trunk has none).
 """
 
 from __future__ import annotations
@@ -30,6 +30,8 @@ from .session_codec import (STACK_SESSION_SCHEMA, CodecError, RecurrenceLayer, S
                             from_json, to_json)
 
 NO_CHOICE = 0xFFFFFFFF  # session.rs:4406: a nearest-head read step chose no token
+TRACE_UNSET = 0xFFFFFFFF  # a snap trace entry no step has written (session.rs:2580-2584)
+TRACE_ZERO = 255  # the launch's trace byte for a zero raw quaternion, whose selection is root 0
 
 
 class SessionError(ValueError):
@@ -60,6 +62,53 @@ def model_identity(art) -> str:
 
 
 @dataclass(frozen=True)
+class SnapTraceEntry:
+    """`SnapTraceEntry` (session.rs:2021-2034): the root the snapped transition chose at one
+    (layer, position, lane)."""
+    layer: int
+    position: int
+    lane: int
+    root: int
+
+
+class SnapTrace:
+    """The opt-in trace buffer (session.rs:2040-2058): one root index per (position, layer,
+    lane) in step order, `context * layers * lanes` entries allocated once; `written` keeps
+    counting past the end (a sliding session), where nothing more is stored."""
+
+    def __init__(self, entries: int, origin_position: int):
+        self.origin_position = origin_position
+        self.selected = np.full(entries, TRACE_UNSET, np.uint32)
+        self.written = 0
+
+    def record(self, roots) -> None:
+        """`SnapTrace::record` for each of `roots` in order."""
+        roots = np.asarray(roots, np.uint32).reshape(-1)
+        lo = min(self.written, len(self.selected))
+        hi = min(self.written + len(roots), len(self.selected))
+        self.selected[lo:hi] = roots[:hi - lo]
+        self.written += len(roots)
+
+    def clear(self, entries: int) -> None:
+        """reset's handling (session.rs:2728-2737): origin 0, nothing written, every entry unset."""
+        self.origin_position = 0
+        self.written = 0
+        if len(self.selected) < entries:
+            self.selected = np.full(entries, TRACE_UNSET, np.uint32)
+        self.selected.fill(TRACE_UNSET)
+
+
+def transition_roots(trace: np.ndarray, layers: int, lanes: int) -> np.ndarray:
+    """The roots a session's snap trace records from the launch's trace bytes of some steps
+    ([steps, trace stride]): per step, per layer, the transition's root per lane (stack_lanes,
+    session.rs:5117-5124); the byte for a zero raw quaternion reads as root 0, the index
+    stack_snap_select (stack/kernels.rs:1474-1528) gives it (every root scores 0; the lowest
+    index wins the tie)."""
+    t = np.asarray(trace, np.uint8).reshape(len(trace), layers, -1)[:, :, :lanes]
+    return np.where(t == TRACE_ZERO, 0, t).astype(np.uint32).reshape(-1)
+
+
+@dataclass(frozen=True)
 class ModelInfo:
     """What restore_state checks a snapshot against."""
     sha256: str
@@ -84,6 +133,15 @@ class ModelInfo:
     @property
     def history_words(self) -> int:
         return self.layers * self.window * self.width
+
+    @property
+    def lanes(self) -> int:
+        return self.width // 4
+
+    @property
+    def trace_entries(self) -> int:
+        """A full context's snap trace entries (session.rs:2578-2580): every layer recurs."""
+        return self.context * self.layers * self.lanes
 
 
 def max_serialized_session_bytes(info: ModelInfo) -> int:
@@ -132,9 +190,6 @@ def validate_restore(info: ModelInfo, saved: SerializedStackSession) -> None:
             want = pos * (info.width // 4) * info.layers
             if len(saved.snap_trace) != want or any(not 0 <= r < 120 for r in saved.snap_trace):
                 raise SessionError("SessionState", "a snap trace of the wrong length or roots")
-            if saved.snap_trace:
-                raise SessionError("Shape", "the GPU path does not record snap traces, so a traced "
-                                            "session cannot continue its trace")
     for layer in saved.layers:
         if not isinstance(layer, RecurrenceLayer):
             raise SessionError("SessionState", "a read layer's cache for a recurrence layer")
@@ -221,10 +276,10 @@ class SessionPool:
         self.position.upload(p)
         self.cache.zero([slot])  # its window sums were formed for the state it held
 
-    def run(self, slots, tokens, gen: int = 0, native: bool = False):
+    def run(self, slots, tokens, gen: int = 0, native: bool = False, trace: bool = False):
         """One launch: the sessions in `slots` take tokens [n, len] and `gen` greedy steps.
-        Returns dict(reply [n, gen+1], status [n], kept [n, P], query [n, d]) (kept and query
-        when `native`)."""
+        Returns dict(reply [n, gen+1], status [n], kept [n, P], query [n, d], trace [n, len + gen,
+        trace stride]) (kept and query when `native`, trace when `trace`)."""
         slots = np.asarray(slots, dtype=np.uint32).reshape(-1)
         tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
         n = len(slots)
@@ -242,16 +297,21 @@ class SessionPool:
         status = DeviceArray(n, np.int32, dev)
         kept = DeviceArray((n, self.model.probes), np.uint32, dev) if native else None
         query = DeviceArray((n, self.model.width), np.int32, dev) if native else None
+        steps = tokens.shape[1] + gen
+        stride = int(hip.lib().uor_fbs_trace_stride(self.model.handle))
+        snap = DeviceArray((n, steps, stride), np.uint8, dev) if trace else None
         ptr = lambda x: None if x is None else x.ptr  # noqa: E731
         # The null stream: the runtime's blocking copies below wait for the launch.
         hip._check(hip.lib().uor_fbs_serve_slots_async(
             self.model.handle, d_slots.ptr, n, self.capacity, d_tok.ptr, tokens.shape[1], gen,
             reply.ptr, self.state.ptr, self.history.ptr, self.position.ptr, self.cache.ptr,
-            self.slide.ptr, ptr(kept), ptr(query), status.ptr, None))
+            self.slide.ptr, ptr(kept), ptr(query), ptr(snap), status.ptr, None))
         out = dict(reply=reply.download(), status=status.download())
         if native:
             out["kept"] = kept.download()
             out["query"] = query.download()
+        if trace:
+            out["trace"] = snap.download()
         return out
 
 
@@ -269,6 +329,7 @@ class Session:
         self.slot = pool.acquire(slot)
         self.slide = False
         pool.set_slide(self.slot, False)
+        self.trace: SnapTrace | None = None  # off by default (session.rs:2570-2576)
         self._reset_host()
 
     def _reset_host(self):
@@ -285,9 +346,28 @@ class Session:
             self.slot = None
 
     def reset(self):
-        """Start a new stream (session.rs:2703-2760)."""
+        """Start a new stream (session.rs:2703-2760); a snap trace stays enabled and starts over."""
         self.pool.clear([self.slot])
         self._reset_host()
+        if self.trace is not None:
+            self.trace.clear(self.info.trace_entries)
+
+    def enable_snap_trace(self) -> None:
+        """Record the root each step's snapped transition selects at every (layer, lane)
+        (session.rs:2570-2585): the buffer is allocated here, once, for a full context; from the
+        session's current position. A model without a snap records nothing."""
+        self.trace = SnapTrace(self.info.trace_entries, self.position)
+
+    def snap_trace(self) -> list[SnapTraceEntry] | None:
+        """The recorded trace as (layer, position, lane, root) entries in step order, or None
+        when tracing is off (session.rs:2587-2620)."""
+        if self.trace is None:
+            return None
+        lanes, per = self.info.lanes, self.info.layers * self.info.lanes
+        written = min(self.trace.written, len(self.trace.selected))
+        return [SnapTraceEntry(rem // lanes, self.trace.origin_position + k // per, rem % lanes,
+                               int(self.trace.selected[k]))
+                for k in range(written) for rem in (k % per,)]
 
     def set_context_slide(self, on: bool) -> None:
         """Let a full context continue instead of refusing (session.rs:2391-2402): refused for a
@@ -313,7 +393,9 @@ class Session:
             ok.append(int(tok))
         return ok, None
 
-    def _after(self, fed: list[int], reply, kept, query):
+    def _after(self, fed: list[int], reply, kept, query, trace=None):
+        if self.trace is not None and trace is not None:
+            self.trace.record(transition_roots(trace[:len(fed)], self.info.layers, self.info.lanes))
         self.position += len(fed)
         self.tokens.extend(fed)
         # A sliding session keeps its last `context` tokens (session.rs:4149-4151).
@@ -325,11 +407,13 @@ class Session:
         the last. A refused token stops the feed there, with the tokens before it stepped."""
         ok, err = self._admit(list(tokens))
         if ok:
-            out = self.pool.run([self.slot], np.asarray([ok], np.uint32), native=True)
+            traced = self.trace is not None and self.info.snapped  # unsnapped: nothing recorded
+            out = self.pool.run([self.slot], np.asarray([ok], np.uint32), native=True, trace=traced)
             st = int(out["status"][0])
             if st:
                 raise SessionError(*_STATUS.get(st, ("Shape", f"status {st}")))
-            self._after(ok, out["reply"][0], out["kept"][0], out["query"][0])
+            self._after(ok, out["reply"][0], out["kept"][0], out["query"][0],
+                        out["trace"][0] if traced else None)
         if err:
             raise err
         return self._native
@@ -373,9 +457,16 @@ class Session:
         layers = [RecurrenceLayer(state[l * d:(l + 1) * d].tolist(),
                                   hist[l * w * d:(l + 1) * w * d].tolist()) for l in range(i.layers)]
         logits = [] if pos == 0 else (list(self.logits) if self.logits is not None else [0] * i.vocab)
+        # The trace travels when it covers every step from position 0 (session.rs:2827-2845).
+        snap = None
+        if i.snapped and self.trace is not None:
+            want = pos * i.lanes * i.layers
+            t = self.trace
+            if t.origin_position == 0 and t.written == want and want <= len(t.selected):
+                snap = t.selected[:want].tolist()
         return SerializedStackSession(STACK_SESSION_SCHEMA, 1, i.sha256, pos, pos * d, pos * i.heads,
                                       0, logits, list(self.tokens), list(self.hamming_payloads),
-                                      None, [], [], [], None, layers)
+                                      snap, [], [], [], None, layers)
 
     def restore_state(self, saved: SerializedStackSession) -> None:
         """session.rs:2876-3190: validate everything, then replace the slot's state."""
@@ -388,6 +479,12 @@ class Session:
         self.logits = list(saved.logits) if saved.position > 0 else None
         self.hamming_payloads = [list(p) for p in saved.hamming_payloads]
         self._native = None
+        # The trace continues from a traced snapshot; an untraced one turns tracing off, so no
+        # partial root history carries over (session.rs:3172-3190).
+        self.trace = None
+        if saved.snap_trace is not None and self.info.snapped:
+            self.trace = SnapTrace(self.info.trace_entries, 0)
+            self.trace.record(saved.snap_trace)
 
     def save_session_to_file(self, path) -> None:
         """JSON to `path`, atomically and durably (session.rs:3202-3262): an exclusive temporary
@@ -444,13 +541,16 @@ def serve_steps(sessions: list[Session], tokens: list[int]) -> list[tuple[int, i
         ok, err = s._admit([tok])
         (go.append((s, ok)) if ok else errs.append(err))
     if go:
-        out = pool.run([s.slot for s, _ in go], np.asarray([ok for _, ok in go], np.uint32), native=True)
+        traced = any(s.trace is not None for s, _ in go) and pool.info.snapped
+        out = pool.run([s.slot for s, _ in go], np.asarray([ok for _, ok in go], np.uint32),
+                       native=True, trace=traced)
         for i, (s, ok) in enumerate(go):
             st = int(out["status"][i])
             if st:
                 errs.append(SessionError(*_STATUS.get(st, ("Shape", f"status {st}"))))
                 continue
-            s._after(ok, out["reply"][i], out["kept"][i], out["query"][i])
+            s._after(ok, out["reply"][i], out["kept"][i], out["query"][i],
+                     out["trace"][i] if traced else None)
     if errs:
         raise errs[0]
     return [(s._native.token, 0) for s in sessions]
