@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define UOR_D11_ABI_VERSION 1u
+#define UOR_D11_ABI_VERSION 2u
 
 #define UOR_D11_MAX_CONTEXT 243u
 #define UOR_D11_MAX_BLOCKS 16u
@@ -41,6 +41,30 @@ extern "C" {
 #define UOR_D11_READ_ROUTE 0u
 #define UOR_D11_READ_FLOCK 1u
 #define UOR_D11_READ_RELATION 2u
+
+/* The model's flags. STATE_TRANSPORT_KNOCKOUT: evaluate with_state_transport_knockout's copy
+ * (discrete_d11.rs:1283-1304): the library (and the oracle) set every route to the identity
+ * state 0 and zero the level and relation gates in their own copies of the tables; the route
+ * read then returns the last token's blocks untransported (:1346-1361), and the trunk's pointer
+ * gate is not applied (:1810-1814). */
+#define UOR_D11_FLAG_STATE_TRANSPORT_KNOCKOUT 1u
+
+/* Trace words of evaluate_prefix_traced (discrete_d11.rs:293-297, :1768-1770), per block of
+ * the read, in block order:
+ * - route read: a header (frontier length, the resolved root, stages taken, the atom) and per
+ *   stage (route state, root before the stage, best port, goal root, composed state, next
+ *   node) (:1369-1442);
+ * - flock and relation reads: a header (query frame root, the block's output root, terms, the
+ *   query payload's root) and per level (gate + 1, kept nodes found, their snapped root,
+ *   eligible nodes, then 8 kept nodes best first, 8 route states carrying them into the query
+ *   frame, 8 carried roots) (:1480-1738).
+ * Words no step writes hold 0xffffffff. Relation reads also give each block's relation scores
+ * (as u32) padded with 0xffffffff to the node count of a full context's plan (:1474-1478,
+ * :1640-1644). */
+#define UOR_D11_ROUTE_TRACE_HEADER_WORDS 4u
+#define UOR_D11_ROUTE_TRACE_STAGE_WORDS 6u
+#define UOR_D11_ACTIVE_TRACE_HEADER_WORDS 4u
+#define UOR_D11_ACTIVE_TRACE_LEVEL_WORDS 28u
 
 /* objective_policy (discrete_d11.rs:301-304): which loss `selected_loss` carries */
 #define UOR_D11_POLICY_NEAREST_ADDRESS_MARGIN 0u /* loss_ta */
@@ -78,7 +102,7 @@ typedef struct {
   uint32_t vocabulary, blocks, context, kept_cells, stages;
   uint32_t read_mode, read_kept, read_sweeps;
   uint32_t objective_policy;
-  uint32_t reserved;
+  uint32_t flags; /* UOR_D11_FLAG_* */
   const int32_t *table;
   const uint32_t *cells;
   const uint32_t *routes;
@@ -127,6 +151,22 @@ int uor_d11_score_rows(void *handle, const uint32_t *prefixes, const int32_t *le
 int uor_d11_score_rows_async(void *handle, const uint32_t *d_prefixes, const int32_t *d_lengths,
                              const uint32_t *d_targets, uint32_t rows, uint32_t stride,
                              uor_d11_row_out *d_out, void *stream);
+
+/* evaluate_prefix_traced (discrete_d11.rs:1768-1770, DiscreteTracedPrefixEvaluation :391-400)
+ * for every row: the records as uor_d11_score_rows writes them, plus each row's trace words
+ * (uor_d11_trace_words(handle, NULL) a row, the layout above) in `trace` and, for a relation
+ * read, its relation words (`*relation_words` a row) in `relation_trace` (required then; ignored
+ * otherwise). The reference's CPU evaluator returns these for one prefix; here they come from the
+ * same kernels' traced instance. A row whose status is not 0 has unspecified trace words (the
+ * reference returns an error and no trace). */
+uint32_t uor_d11_trace_words(void *handle, uint32_t *relation_words);
+int uor_d11_score_rows_traced(void *handle, const uint32_t *prefixes, const int32_t *lengths,
+                              const uint32_t *targets, uint32_t rows, uint32_t stride,
+                              uor_d11_row_out *out, uint32_t *trace, uint32_t *relation_trace);
+int uor_d11_score_rows_traced_async(void *handle, const uint32_t *d_prefixes,
+                                    const int32_t *d_lengths, const uint32_t *d_targets,
+                                    uint32_t rows, uint32_t stride, uor_d11_row_out *d_out,
+                                    uint32_t *d_trace, uint32_t *d_relation_trace, void *stream);
 
 #ifdef __cplusplus
 }

@@ -156,6 +156,11 @@ typedef struct {
   int trunk;
   Sparse sp[12];
   uint8_t (*roots4)[4]; /* [vocab][4] codebook roots */
+  /* with_state_transport_knockout (:1283-1304): the model with identity routes and zero gates */
+  int knockout;
+  uor_d11_model km;
+  uint32_t *kroutes;
+  int32_t *kgates;
 } Oracle;
 
 static int cmp_u64_idx(const void *a, const void *b, void *ctx) {
@@ -220,15 +225,36 @@ static const int32_t *token_block(const uor_d11_model *m, uint32_t tok, int b) {
 }
 
 /* ---------------------------------------------------------------------------------------- */
-/* route_read (:1337-1451). Returns a row status. */
+/* route_read (:1337-1451). Returns a row status. `trace` (NULL: none): the row's trace words,
+ * filled with UINT32_MAX by the caller; `knockout`: the knocked-out read (:1346-1361). */
 static int route_read(const uor_d11_model *m, const uint32_t *prefix, int length, const Plan *p,
-                      Vec8 *out) {
+                      Vec8 *out, int knockout, uint32_t *trace) {
   const uint32_t last_token = prefix[length - 1];
+  const uint32_t tstride = UOR_D11_ROUTE_TRACE_HEADER_WORDS + m->stages * UOR_D11_ROUTE_TRACE_STAGE_WORDS;
+  if (knockout) {
+    for (uint32_t b = 0; b < m->blocks; b++) {
+      memcpy(out[b].x, token_block(m, last_token, b), sizeof out[b].x);
+      if (trace) {
+        uint32_t *w = trace + b * tstride;
+        int r = root_id(out[b].x);
+        w[0] = (uint32_t)p->frontier_len;
+        w[1] = r < 0 ? UINT32_MAX : (uint32_t)r;
+        w[2] = 0;
+      }
+    }
+    return UOR_D11_ROW_OK;
+  }
   for (uint32_t b = 0; b < m->blocks; b++) {
     const int32_t *query = token_block(m, last_token, b);
+    uint32_t *w = trace ? trace + b * tstride : NULL;
     int node = 0, root = 0, total = 0, resolved = 0;
     for (uint32_t stage = 0; stage < m->stages; stage++) {
       int frame = (int)m->routes[b * m->stages + stage];
+      uint32_t *ws = w ? w + UOR_D11_ROUTE_TRACE_HEADER_WORDS + stage * UOR_D11_ROUTE_TRACE_STAGE_WORDS : NULL;
+      if (ws) {
+        ws[0] = (uint32_t)frame;
+        ws[1] = (uint32_t)root;
+      }
       Vec8 q = action(frame, query);
       int count = stage == 0 ? p->frontier_len : 3;
       int best = 0, goal = 0;
@@ -253,22 +279,43 @@ static int route_read(const uor_d11_model *m, const uint32_t *prefix, int length
         if (p->nodes[node].atom >= 0) return UOR_D11_ROW_ROUTE; /* stepped past a leaf */
         next = p->nodes[node].child[best];
       }
+      if (ws) {
+        ws[2] = (uint32_t)best;
+        ws[3] = (uint32_t)goal;
+        ws[4] = (uint32_t)total;
+        ws[5] = (uint32_t)next;
+      }
       if (p->nodes[next].atom >= 0) {
         out[b] = action(total, token_block(m, prefix[p->nodes[next].atom], b));
         resolved = 1;
+        if (w) {
+          w[0] = (uint32_t)p->frontier_len;
+          w[2] = stage + 1;
+          w[3] = (uint32_t)p->nodes[next].atom;
+        }
         break;
       }
       node = next;
     }
     if (!resolved) return UOR_D11_ROW_ROUTE;
+    if (w) {
+      int r = root_id(out[b].x);
+      if (r < 0) return UOR_D11_ROW_ORBIT;
+      w[1] = (uint32_t)r;
+    }
   }
   return UOR_D11_ROW_OK;
 }
 
-/* flock_or_relation_read (:1453-1741). rel_out (blocks x count) receives the relation scores. */
+/* flock_or_relation_read (:1453-1741). rel_out (blocks x count) receives the relation scores.
+ * `trace` (NULL: none): the row's trace words, filled with UINT32_MAX by the caller; then every
+ * level is visited, gated or not, as the traced read does (:1649-1652). `rel_trace` (relation
+ * reads; NULL: none): blocks x `rel_stride` words, filled likewise. */
 static int flock_or_relation_read(const uor_d11_model *m, const uint32_t *prefix, int length,
                                   const Plan *p, int kept, int sweeps, int relation, Vec8 *out,
-                                  int32_t *rel_out) {
+                                  int32_t *rel_out, uint32_t *trace, uint32_t *rel_trace,
+                                  int rel_stride) {
+  const uint32_t tstride = UOR_D11_ACTIVE_TRACE_HEADER_WORDS + m->stages * UOR_D11_ACTIVE_TRACE_LEVEL_WORDS;
   const int blocks = (int)m->blocks, stages = (int)m->stages, nodes = p->count;
   const uint32_t last_token = prefix[length - 1];
   const int32_t *rgates = m->gates + blocks * stages;
@@ -282,6 +329,11 @@ static int flock_or_relation_read(const uor_d11_model *m, const uint32_t *prefix
     memcpy(u.x, token_block(m, last_token, b), sizeof u.x);
     int fq = root_id(query_frame);
     if (fq < 0 || root_id(u.x) < 0) return UOR_D11_ROW_ORBIT;
+    uint32_t *w = trace ? trace + b * tstride : NULL;
+    if (w) {
+      w[0] = (uint32_t)fq;
+      w[3] = (uint32_t)root_id(u.x);
+    }
     for (int i = 0; i < nodes; i++) {
       const Node *n = &p->nodes[i];
       if (n->atom >= 0) {
@@ -365,17 +417,20 @@ static int flock_or_relation_read(const uor_d11_model *m, const uint32_t *prefix
         memcpy(prev, rel, sizeof(int32_t) * nodes);
       }
       if (rel_out) memcpy(rel_out + (size_t)b * nodes, rel, sizeof(int32_t) * nodes);
+      if (rel_trace)
+        for (int i = 0; i < nodes; i++) rel_trace[(size_t)b * rel_stride + i] = (uint32_t)rel[i];
     }
     int terms = 1;
     for (int l = 0; l < stages; l++) {
       int gate = m->gates[b * stages + l];
-      if (gate == 0) continue;
-      int top[8], found = 0;
+      if (gate == 0 && !w) continue;
+      int top[8], found = 0, eligible = 0;
       int32_t kr[8];
       uint32_t kd[8], kh[8];
       for (int node = 0; node < nodes; node++) {
         const Node *n = &p->nodes[node];
         if (n->level != l || n->last + 1 >= length) continue;
+        eligible++;
         uint32_t dist, ham;
         root_cost(query_frame, frame[node], &dist, &ham);
         int32_t rs = rel[node];
@@ -407,6 +462,12 @@ static int flock_or_relation_read(const uor_d11_model *m, const uint32_t *prefix
           if (found < kept) found++;
         }
       }
+      uint32_t *wl = w ? w + UOR_D11_ACTIVE_TRACE_HEADER_WORDS + l * UOR_D11_ACTIVE_TRACE_LEVEL_WORDS : NULL;
+      if (wl) {
+        wl[0] = (uint32_t)(gate + 1);
+        wl[1] = (uint32_t)found;
+        wl[3] = (uint32_t)eligible;
+      }
       if (found == 0) continue;
       int32_t sum[8] = {0};
       for (int k = 0; k < found; k++) {
@@ -414,10 +475,27 @@ static int flock_or_relation_read(const uor_d11_model *m, const uint32_t *prefix
         for (int d = 0; d < 8; d++) sum[d] += carried.x[d];
       }
       int mroot = snap(sum, found);
+      if (wl) {
+        wl[2] = (uint32_t)mroot;
+        for (int k = 0; k < found; k++) {
+          int act = kD11Bfs[(frame[top[k]] << 4) + fq];
+          Vec8 carried = action(act, payload[top[k]].x);
+          int cr = root_id(carried.x);
+          if (cr < 0) return UOR_D11_ROW_ORBIT;
+          wl[4 + k] = (uint32_t)top[k];
+          wl[12 + k] = (uint32_t)act;
+          wl[20 + k] = (uint32_t)cr;
+        }
+      }
+      if (gate == 0) continue;
       for (int d = 0; d < 8; d++) u.x[d] += gate > 0 ? kD11Roots[mroot][d] : -kD11Roots[mroot][d];
       terms++;
     }
     out[b] = root_vec(snap(u.x, terms));
+    if (w) {
+      w[1] = (uint32_t)root_id(out[b].x);
+      w[2] = (uint32_t)terms;
+    }
   }
   return UOR_D11_ROW_OK;
 }
@@ -547,11 +625,30 @@ static uint32_t token_distance(const uor_d11_model *m, const Vec8 *q, uint32_t t
 /* checked_scaled_add (:780-795) on the u32 range the records carry. */
 static uint32_t scaled(uint32_t v, uint32_t times) { return v * times; }
 
-/* evaluate_prefix_internal (:1772-1890) and observe_target (:1892-1993) of one row. */
+/* The words of one row's trace and of its relation trace (0 unless a relation read): the
+ * traced evaluation's layout (:293-297, :1474-1478). */
+static uint32_t trace_words(const uor_d11_model *m) {
+  return m->blocks * (m->read_mode == UOR_D11_READ_ROUTE
+                          ? UOR_D11_ROUTE_TRACE_HEADER_WORDS + m->stages * UOR_D11_ROUTE_TRACE_STAGE_WORDS
+                          : UOR_D11_ACTIVE_TRACE_HEADER_WORDS + m->stages * UOR_D11_ACTIVE_TRACE_LEVEL_WORDS);
+}
+
+static int max_nodes(const uor_d11_model *m) {
+  static __thread Plan p;
+  return build_row_plan((int)m->context, &p) == 0 ? p.count : 0;
+}
+
+/* evaluate_prefix_internal (:1772-1890) and observe_target (:1892-1993) of one row; with
+ * `trace`, evaluate_prefix_traced's words (rel_trace: blocks x rel_stride). */
 static void score_row(const Oracle *o, const uint32_t *prefix, int length, uint32_t target,
-                      uor_d11_row_out *out, int32_t *rel_out) {
+                      uor_d11_row_out *out, int32_t *rel_out, uint32_t *trace, uint32_t *rel_trace,
+                      int rel_stride) {
   const uor_d11_model *m = o->m;
   memset(out, 0, sizeof *out);
+  if (trace)
+    for (uint32_t i = 0; i < trace_words(m); i++) trace[i] = UINT32_MAX;
+  if (rel_trace)
+    for (uint32_t i = 0; i < m->blocks * (uint32_t)rel_stride; i++) rel_trace[i] = UINT32_MAX;
   if (length < 1 || length > (int)m->context) {
     out->status = UOR_D11_ROW_PREFIX_LENGTH;
     return;
@@ -568,12 +665,13 @@ static void score_row(const Oracle *o, const uint32_t *prefix, int length, uint3
   static __thread Plan plan;
   build_row_plan(length, &plan);
   Vec8 q[UOR_D11_MAX_BLOCKS];
+  const int relation = m->read_mode == UOR_D11_READ_RELATION;
   int st = m->read_mode == UOR_D11_READ_ROUTE
-               ? route_read(m, prefix, length, &plan, q)
+               ? route_read(m, prefix, length, &plan, q, o->knockout, trace)
                : flock_or_relation_read(m, prefix, length, &plan, (int)m->read_kept,
-                                        m->read_mode == UOR_D11_READ_RELATION ? (int)m->read_sweeps : 0,
-                                        m->read_mode == UOR_D11_READ_RELATION, q, rel_out);
-  if (st == UOR_D11_ROW_OK && o->trunk) st = trunk_gate(o, prefix, length, q);
+                                        relation ? (int)m->read_sweeps : 0, relation, q, rel_out,
+                                        trace, relation ? rel_trace : NULL, rel_stride);
+  if (st == UOR_D11_ROW_OK && o->trunk && !o->knockout) st = trunk_gate(o, prefix, length, q);
   if (st != UOR_D11_ROW_OK) {
     out->status = st;
     return;
@@ -674,6 +772,17 @@ static void oracle_init(Oracle *o, const uor_d11_model *m) {
   memset(o, 0, sizeof *o);
   o->m = m;
   o->trunk = m->trunk != NULL;
+  o->knockout = (m->flags & UOR_D11_FLAG_STATE_TRANSPORT_KNOCKOUT) != 0;
+  if (o->knockout) {
+    size_t nr = (size_t)m->blocks * m->stages;
+    size_t ng = nr + (m->read_mode == UOR_D11_READ_RELATION ? (size_t)m->stages * EDGE_TYPES : 0);
+    o->kroutes = (uint32_t *)calloc(nr ? nr : 1, sizeof(uint32_t)); /* IDENTITY = 0 (:278) */
+    o->kgates = (int32_t *)calloc(ng ? ng : 1, sizeof(int32_t));
+    o->km = *m;
+    o->km.routes = o->kroutes;
+    o->km.gates = o->kgates;
+    o->m = &o->km;
+  }
   if (o->trunk) {
     for (int i = 0; i < 12; i++) sparse_build(&o->sp[i], m->trunk->sparse[i], m->trunk->sparse_rows[i]);
     o->roots4 = (uint8_t(*)[4])malloc((size_t)m->vocabulary * 4);
@@ -683,6 +792,8 @@ static void oracle_init(Oracle *o, const uor_d11_model *m) {
 }
 
 static void oracle_free(Oracle *o) {
+  free(o->kroutes);
+  free(o->kgates);
   if (o->trunk) {
     for (int i = 0; i < 12; i++) {
       free(o->sp[i].pairs);
@@ -699,13 +810,18 @@ typedef struct {
   const uint32_t *targets;
   uint32_t rows, stride, start, step;
   uor_d11_row_out *out;
+  uint32_t *trace, *rel_trace; /* NULL: untraced */
+  uint32_t trace_words;
+  int rel_stride;
 } Job;
 
 static void *run_job(void *arg) {
   Job *j = (Job *)arg;
+  const uint32_t B = j->o->m->blocks;
   for (uint32_t r = j->start; r < j->rows; r += j->step)
     score_row(j->o, j->prefixes + (size_t)r * j->stride, j->lengths[r], j->targets[r], j->out + r,
-              NULL);
+              NULL, j->trace ? j->trace + (size_t)r * j->trace_words : NULL,
+              j->rel_trace ? j->rel_trace + (size_t)r * B * j->rel_stride : NULL, j->rel_stride);
   return NULL;
 }
 
@@ -720,7 +836,8 @@ int d11_oracle_score_rows(const uor_d11_model *m, const uint32_t *prefixes, cons
   pthread_t th[64];
   Job jobs[64];
   for (int t = 0; t < threads; t++) {
-    jobs[t] = (Job){&o, prefixes, lengths, targets, rows, stride, (uint32_t)t, (uint32_t)threads, out};
+    jobs[t] = (Job){&o, prefixes, lengths, targets, rows, stride, (uint32_t)t, (uint32_t)threads, out,
+                    NULL, NULL, 0, 0};
     if (t > 0) pthread_create(&th[t], NULL, run_job, &jobs[t]);
   }
   run_job(&jobs[0]);
@@ -751,7 +868,7 @@ int d11_oracle_score_open(void *h, const uint32_t *prefixes, const int32_t *leng
   Job jobs[64];
   for (int t = 0; t < threads; t++) {
     jobs[t] = (Job){(const Oracle *)h, prefixes, lengths, targets, rows, stride, (uint32_t)t,
-                    (uint32_t)threads, out};
+                    (uint32_t)threads, out, NULL, NULL, 0, 0};
     if (t > 0) pthread_create(&th[t], NULL, run_job, &jobs[t]);
   }
   run_job(&jobs[0]);
@@ -765,7 +882,7 @@ int d11_oracle_row_relation(const uor_d11_model *m, const uint32_t *prefix, int3
                             uint32_t target, uor_d11_row_out *out, int32_t *relation_scores) {
   Oracle o;
   oracle_init(&o, m);
-  score_row(&o, prefix, length, target, out, relation_scores);
+  score_row(&o, prefix, length, target, out, relation_scores, NULL, NULL, 0);
   oracle_free(&o);
   Plan p;
   return build_row_plan(length, &p) == 0 ? p.count : 0;
@@ -777,5 +894,38 @@ int d11_oracle_plan(int32_t length, int32_t *nodes, int32_t *frontier) {
   if (build_row_plan(length, &p)) return -1;
   *nodes = p.count;
   *frontier = p.frontier_len;
+  return 0;
+}
+
+/* The words of one row's trace and, in `*relation_words`, of its relation trace (blocks x a
+ * full context's node count; 0 unless a relation read). */
+uint32_t d11_oracle_trace_words(const uor_d11_model *m, uint32_t *relation_words) {
+  *relation_words = m->read_mode == UOR_D11_READ_RELATION ? m->blocks * (uint32_t)max_nodes(m) : 0;
+  return trace_words(m);
+}
+
+/* evaluate_prefix_traced (:1768-1770) and observe_target for every row: the records, `trace`
+ * rows x d11_oracle_trace_words words and, for a relation read, `relation_trace` rows x its
+ * relation words (NULL: not wanted). A row whose status is not 0 has no trace (the reference
+ * returns an error); its words are unspecified. */
+int d11_oracle_score_rows_traced(const uor_d11_model *m, const uint32_t *prefixes,
+                                 const int32_t *lengths, const uint32_t *targets, uint32_t rows,
+                                 uint32_t stride, uor_d11_row_out *out, uint32_t *trace,
+                                 uint32_t *relation_trace, int threads) {
+  Oracle o;
+  oracle_init(&o, m);
+  if (threads < 1) threads = 1;
+  if (threads > 64) threads = 64;
+  pthread_t th[64];
+  Job jobs[64];
+  const int rel_stride = m->read_mode == UOR_D11_READ_RELATION ? max_nodes(m) : 0;
+  for (int t = 0; t < threads; t++) {
+    jobs[t] = (Job){&o, prefixes, lengths, targets, rows, stride, (uint32_t)t, (uint32_t)threads, out,
+                    trace, rel_stride ? relation_trace : NULL, trace_words(m), rel_stride};
+    if (t > 0) pthread_create(&th[t], NULL, run_job, &jobs[t]);
+  }
+  run_job(&jobs[0]);
+  for (int t = 1; t < threads; t++) pthread_join(th[t], NULL);
+  oracle_free(&o);
   return 0;
 }

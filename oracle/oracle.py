@@ -506,6 +506,10 @@ def d11_lib():
         L.d11_oracle_close.argtypes = [P]
         L.d11_oracle_close.restype = None
         L.d11_oracle_score_open.argtypes = [P, P, P, P, C.c_uint32, C.c_uint32, P, C.c_int]
+        L.d11_oracle_trace_words.argtypes = [P, P]
+        L.d11_oracle_trace_words.restype = C.c_uint32
+        L.d11_oracle_score_rows_traced.argtypes = [P, P, P, P, C.c_uint32, C.c_uint32, P, P, P,
+                                                   C.c_int]
         _d11 = L
     return _d11
 
@@ -522,6 +526,30 @@ def d11_score_rows(art, prefixes, lengths, targets, threads=8):
     d11_lib().d11_oracle_score_rows(C.byref(m), prefixes.ctypes.data, lengths.ctypes.data,
                                     targets.ctypes.data, rows, stride, out.ctypes.data, threads)
     return out
+
+
+def d11_score_rows_traced(art, prefixes, lengths, targets, knockout=False, threads=8):
+    """evaluate_prefix_traced for every row: (records, trace words [rows, words], relation
+    trace words [rows, blocks, a full context's node count] or None), of the model or of its
+    state-transport knockout."""
+    from uor_fbs import d11
+    m, keep = d11.c_model(art, knockout=knockout)
+    prefixes = np.ascontiguousarray(prefixes, np.uint32)
+    rows, stride = prefixes.shape
+    lengths = np.ascontiguousarray(lengths, np.int32)
+    targets = np.ascontiguousarray(targets, np.uint32)
+    rw = C.c_uint32()
+    words = d11_lib().d11_oracle_trace_words(C.byref(m), C.byref(rw))
+    out = np.zeros(rows, d11.ROW_DTYPE)
+    trace = np.zeros((rows, words), np.uint32)
+    rel = np.zeros((rows, rw.value), np.uint32) if rw.value else None
+    d11_lib().d11_oracle_score_rows_traced(C.byref(m), prefixes.ctypes.data, lengths.ctypes.data,
+                                           targets.ctypes.data, rows, stride, out.ctypes.data,
+                                           trace.ctypes.data, None if rel is None else rel.ctypes.data,
+                                           threads)
+    if rel is not None:
+        rel = rel.reshape(rows, art.shape.blocks, -1)
+    return out, trace, rel
 
 
 def d11_row_relation(art, prefix, target=0):

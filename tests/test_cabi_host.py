@@ -369,7 +369,7 @@ def test_d11_library_exports_and_layout():
     L = d11.lib()
     for name in names:
         assert hasattr(L, name), name
-    assert L.uor_d11_abi_version() == 1
+    assert L.uor_d11_abi_version() == 2
     assert L.uor_d11_sizeof_row_out() == d11.ROW_DTYPE.itemsize == 656
 
 

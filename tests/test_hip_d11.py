@@ -115,3 +115,62 @@ def test_m1_panel_beyond_one_launch_of_resident_waves():
     assert_same(got[pick], want)
     assert (got["status"] == 0).all()
     assert len(np.unique(got["prediction"])) > 100
+
+
+TRACE_CASES = [c for c in CASES if c[3] <= 192] + [("relation", 4, 8192, 243, 16, 8, 5, True, 18)]
+
+
+@pytest.mark.parametrize("knockout", [False, True], ids=["model", "knockout"])
+@pytest.mark.parametrize("case", TRACE_CASES, ids=[f"{c[0]}-b{c[1]}-ctx{c[3]}-s{c[6]}-t{int(c[7])}" for c in TRACE_CASES])
+def test_traced_rows_match_the_oracle(case, knockout):
+    """uor_d11_score_rows_traced (evaluate_prefix_traced, discrete_d11.rs:1768) and the
+    state-transport knockout (:1283-1304) against the oracle: records, trace words and relation
+    words, word for word."""
+    mode, blocks, V, ctx, kc, kept, sweeps, trunk, seed = case
+    art = d11.synthetic(vocabulary=V, blocks=blocks, context=ctx, kept_cells=kc, read_mode=mode,
+                        read_kept=kept, read_sweeps=sweeps, seed=seed, trunk=trunk,
+                        trunk_entries=20000)
+    pre, lens, tg = d11.panel_rows(art, 200, seed + 200)
+    lens[:3] = [1, 2, ctx]
+    print(f"d11 traced {case} knockout={knockout}", flush=True)
+    model = d11.IntegerDiscreteModel(art, knockout=knockout)
+    try:
+        got, tr, rel = model.score_rows_traced(pre, lens, tg)
+        plain = model.score_rows(pre, lens, tg)
+    finally:
+        model.close()
+    want, wtr, wrel = oracle.d11_score_rows_traced(art, pre, lens, tg, knockout=knockout, threads=8)
+    assert (want["status"] == 0).all()
+    assert_same(got, want)
+    assert_same(plain, want)
+    np.testing.assert_array_equal(tr, wtr)
+    assert (rel is None) == (wrel is None)
+    if rel is not None:
+        np.testing.assert_array_equal(rel, wrel)
+
+
+def test_traced_evaluation_api():
+    """evaluate_prefix_traced, a relation read's relation_scores from evaluate_prefix, and
+    with_state_transport_knockout through the Python face, against the oracle."""
+    art = d11.synthetic(vocabulary=1500, context=100, read_mode="relation", read_kept=8,
+                        read_sweeps=2, seed=41, trunk_entries=5000)
+    prefix = d11.panel_rows(art, 1, 42, min_len=60)[0][0][:77]
+    print("d11 traced api", flush=True)
+    model = d11.IntegerDiscreteModel(art)
+    ko = model.with_state_transport_knockout()
+    try:
+        assert ko.is_state_transport_knocked_out() and not model.is_state_transport_knocked_out()
+        t = model.evaluate_prefix_traced(prefix)
+        _, wtr, wrel = oracle.d11_score_rows_traced(art, prefix[None], [77], [0])
+        assert t.trace_words == wtr[0].tolist()
+        assert t.relation_trace_words == wrel[0].reshape(-1).tolist()
+        _, rel = oracle.d11_row_relation(art, prefix, 0)
+        assert t.evaluation.relation_scores == rel.reshape(-1).tolist()
+        assert model.evaluate_prefix(prefix).relation_scores == rel.reshape(-1).tolist()
+        k = ko.evaluate_prefix(prefix)
+        want, _, _ = oracle.d11_score_rows_traced(art, prefix[None], [77], [0], knockout=True)
+        assert k.read_vector == want[0]["read_vector"][:32].tolist()
+        assert k.read_vector == art.table.reshape(1500, 4, 8)[prefix[-1]].reshape(-1).tolist()
+    finally:
+        ko.close()
+        model.close()

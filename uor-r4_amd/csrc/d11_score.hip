@@ -74,6 +74,9 @@ constexpr int kSparseSource[kSparse] = {7, 8, 0, 9, 2, 1};  // index in the cont
 struct DevModel {
   uint32_t vocab, blocks, context, kept_cells, stages, read_mode, read_kept, read_sweeps, policy;
   uint32_t trunk, unigram_best;
+  uint32_t knockout;    // with_state_transport_knockout: routes and gates already zeroed
+  uint32_t trace_block;  // trace words per block of the read
+  uint32_t rel_stride;   // relation trace words per block: a full context's node count
   uint32_t occupied[8];
   const Geo *geo;
   const uint8_t *troot;      // [vocab][blocks] root ids
@@ -219,11 +222,19 @@ __device__ void write_error(uor_d11_row_out *o, int status, int lane) {
   for (int i = lane; i < kRecWords; i += 64) w[i] = i == 0 ? (uint32_t)status : 0u;
 }
 
-// route_read (discrete_d11.rs:1337-1451) of block b; -1 when the route ends off a leaf.
+// route_read (discrete_d11.rs:1337-1451) of block b; -1 when the route ends off a leaf. TR:
+// the block's trace words at `tw` (header, then 6 words a stage, discrete_d11.rs:1369-1442).
+template <bool TR>
 __device__ int route_block(const DevModel &M, const Geo &g, const Plan &P, const WaveLds &w,
-                           int len, int b, int lane) {
+                           int len, int b, int lane, uint32_t *tw) {
   const int B = (int)M.blocks, S = (int)M.stages;
   const int qr0 = M.troot[(uint32_t)w.tok[len - 1] * B + b];
+  if (M.knockout) {  // the last token's block, untransported (:1346-1361)
+    if (TR)
+      for (int i = lane; i < 4 + 6 * S; i += 64)
+        tw[i] = i == 0 ? (uint32_t)P.frontier_len : i == 1 ? (uint32_t)qr0 : i == 2 ? 0u : 0xffffffffu;
+    return qr0;
+  }
   int node = 0, root = 0, total = 0;
   for (int stage = 0; stage < S; stage++) {
     const int frame = M.routes[b * S + stage];
@@ -236,6 +247,7 @@ __device__ int route_block(const DevModel &M, const Geo &g, const Plan &P, const
     }
     const int best = (int)(wave_min32(key) & 0xff);
     const int goal = stage == 0 ? best : g.branch[root][best];
+    const int from = root;
     total = g.compose[g.bfs[(root << 4) + goal]][total];
     root = goal;
     int next;
@@ -246,19 +258,40 @@ __device__ int route_block(const DevModel &M, const Geo &g, const Plan &P, const
       if (!(nd >> 30 & 1)) return -1;  // stepped past an atom leaf
       next = (int)(nd >> (9 * best) & kNone);
     }
+    if (TR && lane < 6) {
+      const uint32_t v[6] = {(uint32_t)frame, (uint32_t)from, (uint32_t)best, (uint32_t)goal,
+                             (uint32_t)total, (uint32_t)next};
+      uint32_t x = v[0];
+#pragma unroll
+      for (int k = 1; k < 6; k++) x = lane == k ? v[k] : x;
+      tw[4 + 6 * stage + lane] = x;
+    }
     const uint32_t nn = P.node[next];
     if (!(nn >> 30 & 1)) {
       const int carrier = M.troot[(uint32_t)w.tok[nn & kNone] * B + b];
-      return g.act[total][carrier];
+      const int r = g.act[total][carrier];
+      if (TR) {
+        // The header, and the stages not taken.
+        for (int i = lane; i < 6 * (S - stage - 1); i += 64) tw[4 + 6 * (stage + 1) + i] = 0xffffffffu;
+        if (lane < 4)
+          tw[lane] = lane == 0   ? (uint32_t)P.frontier_len
+                     : lane == 1 ? (uint32_t)r
+                     : lane == 2 ? (uint32_t)(stage + 1)
+                                 : (nn & kNone);
+      }
+      return r;
     }
     node = next;
   }
   return -1;
 }
 
-// flock_or_relation_read (discrete_d11.rs:1453-1741) of block b.
+// flock_or_relation_read (discrete_d11.rs:1453-1741) of block b. TR: the block's trace words
+// at `tw` (header, then 28 words a level, every level visited whatever its gate, :1480-1738)
+// and, for the relation read, its scores at `rw` padded to M.rel_stride (:1640-1644).
+template <bool TR>
 __device__ int flock_block(const DevModel &M, const Geo &g, const Plan &P, WaveLds &w, int len,
-                           int b, bool relation, int lane) {
+                           int b, bool relation, int lane, uint32_t *tw, uint32_t *rw) {
   const int B = (int)M.blocks, S = (int)M.stages;
   const int f = b == 0 ? B - 1 : 0;
   const uint32_t last = w.tok[len - 1];
@@ -363,6 +396,8 @@ __device__ int flock_block(const DevModel &M, const Geo &g, const Plan &P, WaveL
       for (int i = lane; i < count; i += 64) w.prev[i] = w.rel[i];
       wave_sync();
     }
+    if (TR)
+      for (int i = lane; i < (int)M.rel_stride; i += 64) rw[i] = i < count ? (uint32_t)w.rel[i] : 0xffffffffu;
   }
   // Per level with a gate: the kept nodes (best first) carried into the query frame.
   int32_t u[8];
@@ -373,7 +408,7 @@ __device__ int flock_block(const DevModel &M, const Geo &g, const Plan &P, WaveL
   const int kept = (int)M.read_kept;
   for (int l = 0; l < S; l++) {
     const int gate = M.gates[b * S + l];
-    if (gate == 0) continue;
+    if (!TR && gate == 0) continue;
     uint64_t mk[kPerLane];
 #pragma unroll
     for (int j = 0; j < kPerLane; j++) {
@@ -398,7 +433,10 @@ __device__ int flock_block(const DevModel &M, const Geo &g, const Plan &P, WaveL
 #pragma unroll
     for (int j = 0; j < kPerLane; j++) mine += mk[j] != 0;
     const uint32_t eligible = wave_sum32(mine);
-    if ((int)eligible <= kept) {
+    // The level's trace word this lane writes: kept nodes at 4 + k, their route states at 12 + k,
+    // the carried roots at 20 + k, in selection order (the ordered selection always runs).
+    uint32_t tv = 0xffffffffu;
+    if (!TR && (int)eligible <= kept) {
 #pragma unroll
       for (int j = 0; j < kPerLane; j++) {
         if (mk[j]) {
@@ -412,7 +450,7 @@ __device__ int flock_block(const DevModel &M, const Geo &g, const Plan &P, WaveL
       for (int d = 0; d < 8; d++) sum[d] = (int32_t)wave_sum32((uint32_t)sum[d]);
       found = (int)eligible;
     }
-    for (int r = 0; (int)eligible > kept && r < kept; r++) {
+    for (int r = 0; (TR || (int)eligible > kept) && r < kept; r++) {
       uint64_t loc = 0;
 #pragma unroll
       for (int j = 0; j < kPerLane; j++) loc = mk[j] > loc ? mk[j] : loc;
@@ -422,18 +460,30 @@ __device__ int flock_block(const DevModel &M, const Geo &g, const Plan &P, WaveL
       for (int j = 0; j < kPerLane; j++)
         if (mk[j] == m) mk[j] = 0;
       const int node = (int)(kNone - (uint32_t)(m & kNone));
-      const int cr = g.act[g.bfs[(w.frame[node] << 4) + qf]][w.payload[node]];
+      const int act = g.bfs[(w.frame[node] << 4) + qf];
+      const int cr = g.act[act][w.payload[node]];
+      if (TR) tv = lane == 4 + r ? (uint32_t)node : lane == 12 + r ? (uint32_t)act : lane == 20 + r ? (uint32_t)cr : tv;
 #pragma unroll
       for (int d = 0; d < 8; d++) sum[d] += g.roots[cr][d];
       found++;
     }
-    if (found == 0) continue;
+    if (TR && lane < 28 && lane != 2)
+      tw[4 + 28 * l + lane] = lane == 0 ? (uint32_t)(gate + 1) : lane == 1 ? (uint32_t)found
+                              : lane == 3 ? eligible : tv;
+    if (found == 0) {
+      if (TR && lane == 2) tw[4 + 28 * l + 2] = 0xffffffffu;
+      continue;
+    }
     const int mroot = snap_wave(g, sum, found, lane);
+    if (TR && lane == 2) tw[4 + 28 * l + 2] = (uint32_t)mroot;
+    if (TR && gate == 0) continue;
 #pragma unroll
     for (int d = 0; d < 8; d++) u[d] += gate > 0 ? g.roots[mroot][d] : -g.roots[mroot][d];
     terms++;
   }
-  return snap_wave(g, u, terms, lane);
+  const int out = snap_wave(g, u, terms, lane);
+  if (TR && lane < 4) tw[lane] = lane == 0 ? (uint32_t)qf : lane == 1 ? (uint32_t)out : lane == 2 ? (uint32_t)terms : (uint32_t)u0;
+  return out;
 }
 
 // p / c for 0 <= p < 256 and 1 <= c <= 16 by restoring subtraction: the kernels divide by no
@@ -588,9 +638,13 @@ __device__ void trunk_gate(const DevModel &M, const Geo &g, WaveLds &w, int len,
   wave_sync();
 }
 
+// TR: evaluate_prefix_traced's words at `tw` (M.trace_block a block) and, for the relation
+// read, the relation words at `rw` (M.rel_stride a block); unspecified for a row whose status
+// is not 0 (the reference returns an error).
+template <bool TR>
 __device__ void score_row(const DevModel &M, const Geo &g, WaveLds &w, const uint32_t *prefix,
                           int len, uint32_t target, uint32_t stride, uor_d11_row_out *o,
-                          int lane) {
+                          int lane, uint32_t *tw, uint32_t *rw) {
   const int B = (int)M.blocks;
   int status = 0;
   if (len < 1 || len > (int)M.context || len > (int)stride) {
@@ -644,8 +698,11 @@ __device__ void score_row(const DevModel &M, const Geo &g, WaveLds &w, const uin
   }
   uint8_t *qroot = w.qroot;
   for (int b = 0; b < B; b++) {
-    const int r = M.read_mode == UOR_D11_READ_ROUTE ? route_block(M, g, P, w, len, b, lane)
-                                                     : flock_block(M, g, P, w, len, b, relation, lane);
+    uint32_t *tb = TR ? tw + (uint64_t)b * M.trace_block : nullptr;
+    uint32_t *rb = TR && relation ? rw + (uint64_t)b * M.rel_stride : nullptr;
+    const int r = M.read_mode == UOR_D11_READ_ROUTE
+                      ? route_block<TR>(M, g, P, w, len, b, lane, tb)
+                      : flock_block<TR>(M, g, P, w, len, b, relation, lane, tb, rb);
     if (r < 0) {
       write_error(o, UOR_D11_ROW_ROUTE, lane);
       return;
@@ -653,7 +710,7 @@ __device__ void score_row(const DevModel &M, const Geo &g, WaveLds &w, const uin
     if (lane == 0) qroot[b] = (uint8_t)r;
     wave_sync();
   }
-  if (M.trunk) trunk_gate(M, g, w, len, lane);
+  if (M.trunk && !M.knockout) trunk_gate(M, g, w, len, lane);  // not for a knockout (:1810-1814)
   // The writer (:1843-1888): admitted cells by (address distance, cell), then the top 8 of
   // their tokens by (token distance, token).
   const int q0 = qroot[0], ql = qroot[B - 1];
@@ -778,10 +835,11 @@ __device__ void score_row(const DevModel &M, const Geo &g, WaveLds &w, const uin
   for (int i = lane; i < kRecWords; i += 64) dst[i] = w.rec[i];
 }
 
-__global__ __launch_bounds__(kThreads) void d11_score_rows(DevModel M, const uint32_t *prefixes,
-                                                           const int32_t *lengths,
-                                                           const uint32_t *targets, uint32_t rows,
-                                                           uint32_t stride, uor_d11_row_out *out) {
+template <bool TR>
+__device__ __forceinline__ void score_block(const DevModel &M, const uint32_t *prefixes,
+                                            const int32_t *lengths, const uint32_t *targets,
+                                            uint32_t rows, uint32_t stride, uor_d11_row_out *out,
+                                            uint32_t *trace, uint32_t *rel_trace) {
   __shared__ Geo g;
   __shared__ WaveLds lds[kWaves];
   {
@@ -793,8 +851,24 @@ __global__ __launch_bounds__(kThreads) void d11_score_rows(DevModel M, const uin
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const uint32_t row = blockIdx.x * kWaves + wave;
   if (row >= rows) return;
-  score_row(M, g, lds[wave], prefixes + (uint64_t)row * stride, lengths[row], targets[row], stride,
-            out + row, lane);
+  score_row<TR>(M, g, lds[wave], prefixes + (uint64_t)row * stride, lengths[row], targets[row],
+                stride, out + row, lane,
+                TR ? trace + (uint64_t)row * M.blocks * M.trace_block : nullptr,
+                TR && rel_trace ? rel_trace + (uint64_t)row * M.blocks * M.rel_stride : nullptr);
+}
+
+__global__ __launch_bounds__(kThreads) void d11_score_rows(DevModel M, const uint32_t *prefixes,
+                                                           const int32_t *lengths,
+                                                           const uint32_t *targets, uint32_t rows,
+                                                           uint32_t stride, uor_d11_row_out *out) {
+  score_block<false>(M, prefixes, lengths, targets, rows, stride, out, nullptr, nullptr);
+}
+
+// evaluate_prefix_traced for every row (discrete_d11.rs:1768-1770).
+__global__ __launch_bounds__(kThreads) void d11_score_rows_traced(
+    DevModel M, const uint32_t *prefixes, const int32_t *lengths, const uint32_t *targets,
+    uint32_t rows, uint32_t stride, uor_d11_row_out *out, uint32_t *trace, uint32_t *rel_trace) {
+  score_block<true>(M, prefixes, lengths, targets, rows, stride, out, trace, rel_trace);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -993,6 +1067,8 @@ extern "C" int uor_d11_model_create(const uor_d11_model *m, int32_t device, void
        m->read_sweeps <= UOR_D11_MAX_SWEEPS);
   if (!ok_mode) return fail(-1, "unsupported discrete read mode or parameters");
   if (m->objective_policy > 1) return fail(-1, "unsupported discrete objective policy");
+  if (m->flags & ~UOR_D11_FLAG_STATE_TRANSPORT_KNOCKOUT) return fail(-1, "unknown model flags");
+  const bool knockout = (m->flags & UOR_D11_FLAG_STATE_TRANSPORT_KNOCKOUT) != 0;
   if (!m->table || !m->cells || !m->routes || !m->gates) return fail(-1, "null section");
   const uint32_t ngates = B * S + (m->read_mode == UOR_D11_READ_RELATION ? 5 * S : 0);
   for (uint32_t i = 0; i < B * S; i++)
@@ -1024,10 +1100,12 @@ extern "C" int uor_d11_model_create(const uor_d11_model *m, int32_t device, void
     std::vector<uint32_t> fill(cell_off.begin(), cell_off.end() - 1);
     for (uint32_t t = 0; t < V; t++) cell_tok[fill[cell[t]]++] = (uint16_t)t;
   }
+  // with_state_transport_knockout (discrete_d11.rs:1283-1304): identity routes (state 0), zero
+  // level and relation gates.
   std::vector<uint8_t> routes(B * S);
-  for (uint32_t i = 0; i < B * S; i++) routes[i] = (uint8_t)m->routes[i];
+  for (uint32_t i = 0; i < B * S; i++) routes[i] = knockout ? 0 : (uint8_t)m->routes[i];
   std::vector<int8_t> gates(ngates);
-  for (uint32_t i = 0; i < ngates; i++) gates[i] = (int8_t)m->gates[i];
+  for (uint32_t i = 0; i < ngates; i++) gates[i] = knockout ? 0 : (int8_t)m->gates[i];
   std::vector<Plan> plans(m->context);
   for (uint32_t n = 1; n <= m->context; n++)
     if (!make_plan((int)n, plans[n - 1])) return fail(-1, "row plan outside the kernel's limits");
@@ -1096,6 +1174,11 @@ extern "C" int uor_d11_model_create(const uor_d11_model *m, int32_t device, void
   d.policy = m->objective_policy;
   d.trunk = tr != nullptr;
   d.unigram_best = unigram_best;
+  d.knockout = knockout;
+  d.trace_block = m->read_mode == UOR_D11_READ_ROUTE
+                      ? UOR_D11_ROUTE_TRACE_HEADER_WORDS + S * UOR_D11_ROUTE_TRACE_STAGE_WORDS
+                      : UOR_D11_ACTIVE_TRACE_HEADER_WORDS + S * UOR_D11_ACTIVE_TRACE_LEVEL_WORDS;
+  d.rel_stride = m->read_mode == UOR_D11_READ_RELATION ? plans[m->context - 1].count : 0;
   for (int i = 0; i < 8; i++) d.occupied[i] = occupied[i];
   const std::vector<Geo> geo(1, make_geo());
   bool ok = (d.geo = h->upload(geo)) && (d.troot = h->upload(troot)) && (d.cell = h->upload(cell)) &&
@@ -1153,9 +1236,40 @@ extern "C" int uor_d11_score_rows_async(void *handle, const uint32_t *d_prefixes
   return e == hipSuccess ? 0 : fail(-2, std::string("launch: ") + hipGetErrorString(e));
 }
 
-extern "C" int uor_d11_score_rows(void *handle, const uint32_t *prefixes, const int32_t *lengths,
-                                  const uint32_t *targets, uint32_t rows, uint32_t stride,
-                                  uor_d11_row_out *out) {
+extern "C" uint32_t uor_d11_trace_words(void *handle, uint32_t *relation_words) {
+  if (!handle) return 0;
+  const DevModel &d = ((Handle *)handle)->dm;
+  if (relation_words) *relation_words = d.blocks * d.rel_stride;
+  return d.blocks * d.trace_block;
+}
+
+extern "C" int uor_d11_score_rows_traced_async(void *handle, const uint32_t *d_prefixes,
+                                               const int32_t *d_lengths, const uint32_t *d_targets,
+                                               uint32_t rows, uint32_t stride, uor_d11_row_out *d_out,
+                                               uint32_t *d_trace, uint32_t *d_relation_trace,
+                                               void *stream) {
+  if (!handle) return fail(-1, "null handle");
+  if (rows == 0) return 0;
+  Handle *h = (Handle *)handle;
+  if (!d_prefixes || !d_lengths || !d_targets || !d_out || !d_trace || stride == 0 ||
+      (h->dm.rel_stride && !d_relation_trace))
+    return fail(-1, "null buffer or zero stride");
+  int prev = 0;
+  (void)hipGetDevice(&prev);
+  (void)hipSetDevice(h->device);
+  const uint32_t grid = (rows + kWaves - 1) / kWaves;
+  hipLaunchKernelGGL(d11_score_rows_traced, dim3(grid), dim3(kThreads), 0, (hipStream_t)stream,
+                     h->dm, d_prefixes, d_lengths, d_targets, rows, stride, d_out, d_trace,
+                     h->dm.rel_stride ? d_relation_trace : nullptr);
+  const hipError_t e = hipGetLastError();
+  (void)hipSetDevice(prev);
+  return e == hipSuccess ? 0 : fail(-2, std::string("launch: ") + hipGetErrorString(e));
+}
+
+// The host-buffer form of either launch: copies in, one launch, copies out.
+static int score_host(void *handle, const uint32_t *prefixes, const int32_t *lengths,
+                      const uint32_t *targets, uint32_t rows, uint32_t stride, uor_d11_row_out *out,
+                      uint32_t *trace, uint32_t *relation_trace) {
   if (!handle) return fail(-1, "null handle");
   if (rows == 0) return 0;
   if (!prefixes || !lengths || !targets || !out || stride == 0)
@@ -1163,31 +1277,56 @@ extern "C" int uor_d11_score_rows(void *handle, const uint32_t *prefixes, const 
   for (uint32_t r = 0; r < rows; r++)
     if (lengths[r] < 0 || (uint32_t)lengths[r] > stride) return fail(-1, "a length exceeds the row stride");
   Handle *h = (Handle *)handle;
+  uint32_t rel_words = 0;
+  const uint32_t words = uor_d11_trace_words(handle, &rel_words);
+  if (trace && rel_words && !relation_trace) return fail(-1, "a relation read needs the relation trace");
   int prev = 0;
   (void)hipGetDevice(&prev);
   (void)hipSetDevice(h->device);
   const size_t np = (size_t)rows * stride * 4, nr = (size_t)rows * 4, no = (size_t)rows * sizeof(uor_d11_row_out);
+  const size_t nt = trace ? (size_t)rows * words * 4 : 0, nrel = trace ? (size_t)rows * rel_words * 4 : 0;
+  const size_t at_out = (np + 2 * nr + 15) & ~(size_t)15, at_tr = (at_out + no + 15) & ~(size_t)15;
+  const size_t at_rel = (at_tr + nt + 15) & ~(size_t)15;
   char *buf = nullptr;
   int rc = 0;
-  if (hipMalloc((void **)&buf, np + 2 * nr + no + 64) != hipSuccess) {
+  if (hipMalloc((void **)&buf, at_rel + nrel + 64) != hipSuccess) {
     rc = fail(-2, "device allocation failed");
   } else {
     uint32_t *dp = (uint32_t *)buf;
     int32_t *dl = (int32_t *)(buf + np);
     uint32_t *dt = (uint32_t *)(buf + np + nr);
-    uor_d11_row_out *dout = (uor_d11_row_out *)(buf + ((np + 2 * nr + 15) & ~(size_t)15));
+    uor_d11_row_out *dout = (uor_d11_row_out *)(buf + at_out);
+    uint32_t *dtr = (uint32_t *)(buf + at_tr), *drel = (uint32_t *)(buf + at_rel);
     if (hipMemcpy(dp, prefixes, np, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(dl, lengths, nr, hipMemcpyHostToDevice) != hipSuccess ||
         hipMemcpy(dt, targets, nr, hipMemcpyHostToDevice) != hipSuccess) {
       rc = fail(-2, "copy to the device failed");
     } else {
-      rc = uor_d11_score_rows_async(handle, dp, dl, dt, rows, stride, dout, nullptr);
+      rc = trace ? uor_d11_score_rows_traced_async(handle, dp, dl, dt, rows, stride, dout, dtr,
+                                                   drel, nullptr)
+                 : uor_d11_score_rows_async(handle, dp, dl, dt, rows, stride, dout, nullptr);
       if (rc == 0 && (hipDeviceSynchronize() != hipSuccess ||
-                      hipMemcpy(out, dout, no, hipMemcpyDeviceToHost) != hipSuccess))
+                      hipMemcpy(out, dout, no, hipMemcpyDeviceToHost) != hipSuccess ||
+                      (nt && hipMemcpy(trace, dtr, nt, hipMemcpyDeviceToHost) != hipSuccess) ||
+                      (nrel && hipMemcpy(relation_trace, drel, nrel, hipMemcpyDeviceToHost) != hipSuccess)))
         rc = fail(-2, "scoring failed on the device");
     }
     (void)hipFree(buf);
   }
   (void)hipSetDevice(prev);
   return rc;
+}
+
+extern "C" int uor_d11_score_rows(void *handle, const uint32_t *prefixes, const int32_t *lengths,
+                                  const uint32_t *targets, uint32_t rows, uint32_t stride,
+                                  uor_d11_row_out *out) {
+  return score_host(handle, prefixes, lengths, targets, rows, stride, out, nullptr, nullptr);
+}
+
+extern "C" int uor_d11_score_rows_traced(void *handle, const uint32_t *prefixes,
+                                         const int32_t *lengths, const uint32_t *targets,
+                                         uint32_t rows, uint32_t stride, uor_d11_row_out *out,
+                                         uint32_t *trace, uint32_t *relation_trace) {
+  if (!trace) return fail(-1, "null trace buffer");
+  return score_host(handle, prefixes, lengths, targets, rows, stride, out, trace, relation_trace);
 }

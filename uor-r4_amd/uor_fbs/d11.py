@@ -105,6 +105,19 @@ def expected_stages(context: int) -> int | None:
     return stages
 
 
+def plan_nodes(length: int) -> int:
+    """build_row_plan's node count (discrete_d11.rs:813-884): every atom, and a node for each
+    merge of the frontier's last three nodes while they share a level."""
+    levels, count = [], 0
+    for _ in range(length):
+        levels.append(0)
+        count += 1
+        while len(levels) >= 3 and levels[-1] == levels[-2] == levels[-3]:
+            levels[-3:] = [levels[-1] + 1]
+            count += 1
+    return count
+
+
 def root_ids(table: np.ndarray) -> np.ndarray:
     """Orbit root of every 8-block (-1 where a block is none of the 16)."""
     t = np.asarray(table, np.int64).reshape(-1, 8)
@@ -369,7 +382,8 @@ def tables_header_arrays() -> dict:
 
 SYMBOLS = ("uor_d11_abi_version", "uor_d11_sizeof_model", "uor_d11_sizeof_row_out",
            "uor_d11_last_error", "uor_d11_model_create", "uor_d11_model_destroy",
-           "uor_d11_score_rows", "uor_d11_score_rows_async")
+           "uor_d11_score_rows", "uor_d11_score_rows_async", "uor_d11_trace_words",
+           "uor_d11_score_rows_traced", "uor_d11_score_rows_traced_async")
 
 MAX_BLOCKS = 16
 MAX_KEPT_CELLS = 16
@@ -385,7 +399,7 @@ class CModel(C.Structure):
     _fields_ = [("vocabulary", C.c_uint32), ("blocks", C.c_uint32), ("context", C.c_uint32),
                 ("kept_cells", C.c_uint32), ("stages", C.c_uint32), ("read_mode", C.c_uint32),
                 ("read_kept", C.c_uint32), ("read_sweeps", C.c_uint32),
-                ("objective_policy", C.c_uint32), ("reserved", C.c_uint32),
+                ("objective_policy", C.c_uint32), ("flags", C.c_uint32),
                 ("table", C.c_void_p), ("cells", C.c_void_p), ("routes", C.c_void_p),
                 ("gates", C.c_void_p), ("trunk", C.POINTER(CTrunk))]
 
@@ -409,13 +423,18 @@ ROW_DTYPE = np.dtype([("status", "<i4"), ("admitted_count", "<i4"), ("top8_count
 assert ROW_DTYPE.itemsize == C.sizeof(CRowOut)
 
 
-def c_model(art: Artifact):
-    """The ``uor_d11_model`` image of an artifact and the arrays it points into (keep both)."""
+FLAG_STATE_TRANSPORT_KNOCKOUT = 1
+
+
+def c_model(art: Artifact, knockout: bool = False):
+    """The ``uor_d11_model`` image of an artifact and the arrays it points into (keep both);
+    `knockout`: its state-transport knockout (the flag; the library zeroes the tables itself)."""
     s = art.shape
     keep = [np.ascontiguousarray(art.table, np.int32), np.ascontiguousarray(art.cells, np.uint32),
             np.ascontiguousarray(art.routes, np.uint32), np.ascontiguousarray(art.gates, np.int32)]
     m = CModel(s.vocabulary, s.blocks, s.context, s.kept_cells, s.stages, READ_MODES[s.read_mode],
-               s.read_kept, s.read_sweeps, POLICIES[s.objective_policy], 0,
+               s.read_kept, s.read_sweeps, POLICIES[s.objective_policy],
+               FLAG_STATE_TRANSPORT_KNOCKOUT if knockout else 0,
                *(a.ctypes.data for a in keep), None)
     if art.trunk is not None:
         t = CTrunk()
@@ -452,6 +471,11 @@ def lib():
         L.uor_d11_model_destroy.restype = None
         L.uor_d11_score_rows.argtypes = [P, P, P, P, C.c_uint32, C.c_uint32, P]
         L.uor_d11_score_rows_async.argtypes = [P, P, P, P, C.c_uint32, C.c_uint32, P, P]
+        L.uor_d11_trace_words.argtypes = [P, P]
+        L.uor_d11_trace_words.restype = C.c_uint32
+        L.uor_d11_score_rows_traced.argtypes = [P, P, P, P, C.c_uint32, C.c_uint32, P, P, P]
+        L.uor_d11_score_rows_traced_async.argtypes = [P, P, P, P, C.c_uint32, C.c_uint32, P, P, P,
+                                                      P]
         assert L.uor_d11_sizeof_row_out() == ROW_DTYPE.itemsize
         assert L.uor_d11_sizeof_model() == C.sizeof(CModel)
         _lib = L
@@ -478,18 +502,40 @@ class Evaluation:
     loss_ta: int = 0
     loss_tr: int = 0
     selected_loss: int = 0
+    relation_scores: list | None = None  # blocks * nodes of the row's plan (relation reads)
+
+
+@dataclass
+class TracedEvaluation:
+    """``DiscreteTracedPrefixEvaluation`` (discrete_d11.rs:391-400): the evaluation and the read's
+    decision words (layout in include/uor_d11.h), the relation scores padded to a full context's
+    node count with 0xffffffff (relation reads)."""
+    evaluation: Evaluation
+    trace_words: list
+    relation_trace_words: list | None
 
 
 class IntegerDiscreteModel:
     """A discrete model resident on one GPU (the reference's API names)."""
 
-    def __init__(self, art: Artifact, device: int = 0):
+    def __init__(self, art: Artifact, device: int = 0, knockout: bool = False):
         self.art = art
         self.shape = art.shape
-        m, keep = c_model(art)
+        self.device = device
+        self.knockout = knockout
+        m, keep = c_model(art, knockout=knockout)
         h = C.c_void_p()
         _check(lib().uor_d11_model_create(C.byref(m), device, C.byref(h)))
         self.handle = h
+
+    def with_state_transport_knockout(self) -> "IntegerDiscreteModel":
+        """``with_state_transport_knockout`` (discrete_d11.rs:1283-1304): a model whose binder
+        routes are the identity state and whose level and relation gates are zero; its route read
+        returns the last token's blocks untransported and the trunk's pointer gate is skipped."""
+        return IntegerDiscreteModel(self.art, self.device, knockout=True)
+
+    def is_state_transport_knocked_out(self) -> bool:
+        return self.knockout
 
     @classmethod
     def from_bytes(cls, data: bytes, device: int = 0):
@@ -527,22 +573,62 @@ class IntegerDiscreteModel:
                                             targets.ctypes.data, rows, stride, out.ctypes.data))
         return out
 
-    def _one(self, prefix, target):
+    def trace_words(self) -> tuple[int, int]:
+        """(trace words, relation trace words) of one row."""
+        rw = C.c_uint32()
+        return int(lib().uor_d11_trace_words(self.handle, C.byref(rw))), rw.value
+
+    def score_rows_traced(self, prefixes, lengths, targets):
+        """``score_rows`` with every row's trace: (records, trace [rows, words], relation trace
+        [rows, blocks, a full context's node count] or None)."""
+        prefixes = np.ascontiguousarray(prefixes, np.uint32)
+        if prefixes.ndim != 2:
+            raise ValueError("prefixes must be (rows, stride)")
+        rows, stride = prefixes.shape
+        lengths = np.ascontiguousarray(lengths, np.int32)
+        targets = np.ascontiguousarray(targets, np.uint32)
+        if lengths.shape != (rows,) or targets.shape != (rows,):
+            raise ValueError("lengths and targets need one entry per row")
+        if rows and ((lengths < 0) | (lengths > stride)).any():
+            raise ValueError("a length exceeds the row stride")
+        words, rwords = self.trace_words()
+        out = np.zeros(rows, ROW_DTYPE)
+        trace = np.zeros((rows, words), np.uint32)
+        rel = np.zeros((rows, rwords), np.uint32) if rwords else None
+        if rows:
+            _check(lib().uor_d11_score_rows_traced(
+                self.handle, prefixes.ctypes.data, lengths.ctypes.data, targets.ctypes.data, rows,
+                stride, out.ctypes.data, trace.ctypes.data, None if rel is None else rel.ctypes.data))
+        if rel is not None:
+            rel = rel.reshape(rows, self.shape.blocks, -1)
+        return out, trace, rel
+
+    def _one(self, prefix, target, traced=False):
         prefix = np.asarray(prefix, np.uint32).reshape(-1)
         if len(prefix) == 0 or len(prefix) > self.shape.context:
             raise DiscreteError("prefix length must be in 1..=context")
         if (prefix >= self.shape.vocabulary).any():
             raise DiscreteError("prefix token ID outside vocabulary")
-        row = self.score_rows(prefix[None, :], [len(prefix)], [target])[0]
+        if traced:
+            out, trace, rel = self.score_rows_traced(prefix[None, :], [len(prefix)], [target])
+            row, trace, rel = out[0], trace[0], None if rel is None else rel[0]
+        else:
+            row = self.score_rows(prefix[None, :], [len(prefix)], [target])[0]
         if row["status"] != 0:
             raise DiscreteError(STATUS.get(int(row["status"]), str(row["status"])))
-        return row
+        return (row, trace, rel) if traced else row
 
-    def _evaluation(self, row, observed: bool) -> Evaluation:
+    def _relation(self) -> bool:
+        return READ_MODES[self.shape.read_mode] == 2
+
+    def _evaluation(self, row, observed: bool, rel=None, length=0) -> Evaluation:
         B = self.shape.blocks
         ev = Evaluation(row["read_vector"][:8 * B].tolist(),
                         row["admitted"][:row["admitted_count"]].tolist(),
                         row["top8"][:row["top8_count"]].tolist(), int(row["prediction"]))
+        if rel is not None:  # the row plan's nodes of each block, as i32 (:386-388)
+            n = plan_nodes(length)
+            ev.relation_scores = rel[:, :n].view(np.int32).reshape(-1).tolist()
         if observed:
             for k in ("token_rivals", "address_rivals", "token_hinge", "address_hinge",
                       "rank_hinge", "loss_ta", "loss_tr", "selected_loss"):
@@ -550,11 +636,25 @@ class IntegerDiscreteModel:
         return ev
 
     def evaluate_prefix(self, prefix) -> Evaluation:
-        """``evaluate_prefix`` (discrete_d11.rs:1761): the read, admitted cells and top 8."""
+        """``evaluate_prefix`` (discrete_d11.rs:1761): the read, admitted cells and top 8, and a
+        relation read's scores (taken from the traced launch)."""
+        if self._relation():
+            return self.evaluate_prefix_traced(prefix).evaluation
         return self._evaluation(self._one(prefix, 0), False)
+
+    def evaluate_prefix_traced(self, prefix) -> TracedEvaluation:
+        """``evaluate_prefix_traced`` (discrete_d11.rs:1768): the evaluation with the read's
+        decision words."""
+        row, trace, rel = self._one(prefix, 0, traced=True)
+        n = len(np.asarray(prefix).reshape(-1))
+        return TracedEvaluation(self._evaluation(row, False, rel, n), trace.tolist(),
+                                None if rel is None else rel.reshape(-1).tolist())
 
     def observe_target(self, prefix, target: int) -> Evaluation:
         """``observe_target`` (discrete_d11.rs:1892): the evaluation plus hinges and losses."""
         if not 0 <= int(target) < self.shape.vocabulary:
             raise DiscreteError("target token ID outside vocabulary")
+        if self._relation():
+            row, _, rel = self._one(prefix, int(target), traced=True)
+            return self._evaluation(row, True, rel, len(np.asarray(prefix).reshape(-1)))
         return self._evaluation(self._one(prefix, int(target)), True)
