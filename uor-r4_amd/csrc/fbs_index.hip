@@ -45,6 +45,7 @@ constexpr uint32_t kBuildThreads = 512;  // cells and scatter blocks
 constexpr uint32_t kBuildWaves = kBuildThreads / 64;
 constexpr uint32_t kMaxPer = 16;  // rounds of kBuildThreads tokens per build tile
 constexpr uint32_t kMaxTile = kBuildThreads * kMaxPer;
+static_assert(kMaxTile <= 65536, "a token's place in its tile fits 16 bits");
 constexpr uint32_t kMoveThreads = 1024;
 constexpr uint32_t kShiftPer = 4;  // members per thread per shift chunk
 constexpr uint32_t kMaxVerifyBlocks = 2048;
@@ -136,21 +137,41 @@ __global__ __launch_bounds__(kBuildThreads) void index_cells(const int32_t *__re
   load_roots(roots, sroots);
   for (uint32_t i = threadIdx.x; i < kSlots; i += kBuildThreads) hist[i] = 0;
   __syncthreads();
-  const uint32_t first = blockIdx.x * per * kBuildThreads + threadIdx.x;
-  for (uint32_t pass = 0; pass < per; pass += 8) {
-    uint32_t c[8];
+  // Four lanes a row, each loading one 16-byte piece of an endpoint block (the first block's
+  // two, then the last block's two), so one load instruction covers 16 rows' endpoints instead
+  // of one piece of 64 rows. Each lane matches its piece against its half of every root (a bit
+  // per root); a lane pair's AND is the block's match, its lowest bit the first equal root.
+  const uint32_t which = threadIdx.x & 3, half = which & 1;
+  const uint32_t piece = which < 2 ? which : width / 4 - 4 + which;
+  int4 R[16];
 #pragma unroll
-    for (uint32_t r = 0; r < 8; r++) {
-      const uint32_t t = first + (pass + r) * kBuildThreads;
-      c[r] = pass + r < per && t < count ? token_cell(table + (uint64_t)t * width, width, sroots)
-                                         : kAbsent;
+  for (int r = 0; r < 16; r++) R[r] = *(const int4 *)(sroots + 8 * r + 4 * half);
+  constexpr uint32_t kRows = kBuildThreads / 4;  // rows a block reads per round
+  const uint32_t rounds = per * 4, first = blockIdx.x * per * kBuildThreads + (threadIdx.x >> 2);
+  for (uint32_t round = 0; round < rounds; round += 8) {
+    int4 v[8];
+#pragma unroll
+    for (uint32_t u = 0; u < 8; u++) {
+      const uint32_t t = first + (round + u) * kRows;
+      v[u] = round + u < rounds && t < count
+                 ? *(const int4 *)(table + (uint64_t)t * width + 4 * piece)
+                 : make_int4(0, 0, 0, 0);
     }
 #pragma unroll
-    for (uint32_t r = 0; r < 8; r++) {
-      const uint32_t t = first + (pass + r) * kBuildThreads;
-      if (pass + r < per && t < count) {
-        cells[t] = c[r];
-        atomicAdd(&hist[c[r] == kAbsent ? kCells : c[r]], 1u);
+    for (uint32_t u = 0; u < 8; u++) {
+      uint32_t m = 0;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int d = (v[u].x ^ R[r].x) | (v[u].y ^ R[r].y) | (v[u].z ^ R[r].z) | (v[u].w ^ R[r].w);
+        m |= (uint32_t)(d == 0) << r;
+      }
+      m &= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0xB1, 0xf, 0xf, false);  // lane ^ 1
+      const uint32_t b = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x4E, 0xf, 0xf, false);
+      const uint32_t t = first + (round + u) * kRows;
+      if (which == 0 && round + u < rounds && t < count) {
+        const uint32_t c = m && b ? (uint32_t)__builtin_ctz(m) * 16 + (uint32_t)__builtin_ctz(b) : kAbsent;
+        cells[t] = c;
+        atomicAdd(&hist[c == kAbsent ? kCells : c], 1u);
       }
     }
   }
@@ -177,23 +198,43 @@ __global__ __launch_bounds__(kThreads) void index_scan_tiles(uint32_t *counts, u
   if (threadIdx.x == 0) totals[blockIdx.x] = carry;
 }
 
+// The lanes of this wave holding the same cell as this lane (a match of the cell's 8 bits over
+// ballots), among the valid ones.
+__device__ __forceinline__ uint64_t same_cell(uint32_t c, bool valid) {
+  uint64_t peers = __ballot(valid);
+#pragma unroll
+  for (int b = 0; b < 8; b++) {
+    const bool bit = (c >> b) & 1;
+    const uint64_t m = __ballot(bit);
+    peers &= bit ? m : ~m;
+  }
+  return peers;
+}
+
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Stable scatter of one tile: its tokens are ordered by (cell, token) in LDS, then each cell's
 // run is written to members contiguously (runs of tile/256 members on average, so the writes
-// coalesce). A token's place in its cell's run: the run's earlier rounds, the earlier waves of
-// its round (per-wave counts) and the earlier lanes of its wave with the same cell (a match of
-// the cell's 8 bits over ballots). Block 0 also writes offsets, the absent count and status.
+// coalesce). Each wave takes a contiguous chunk of the tile: it counts its chunk's cells, one
+// pass over the cells turns the counts into each wave's first place in every cell's run, and
+// the wave walks its chunk again, a token's place being its wave's cursor for the cell plus the
+// earlier lanes with the same cell; so the block meets three barriers a tile. Block 0 also
+// writes offsets, the absent count and status.
 __global__ __launch_bounds__(kBuildThreads) void index_scatter(
     const uint32_t *__restrict__ cells, uint32_t count, uint32_t per,
     const uint32_t *__restrict__ starts, uint32_t tiles, const uint32_t *__restrict__ totals,
     uint32_t allow_absent,
     uint32_t *__restrict__ offsets, uint32_t *__restrict__ members,
     uint32_t *__restrict__ absent_count, int32_t *__restrict__ status) {
-  __shared__ uint32_t sorted[kMaxTile];
+  __shared__ uint32_t sorted[kMaxTile];  // cell << 16 | the token's place in the tile
   __shared__ uint32_t buf[kBuildThreads];
   __shared__ uint32_t lstart[kSlots];  // each cell's run within the tile's sorted tokens
   __shared__ uint32_t gbase[kCells];   // each cell's run within members
-  __shared__ uint32_t cursor[kCells];
-  __shared__ uint32_t wave_cnt[kBuildWaves][kCells];
+  __shared__ uint32_t wave_cnt[kBuildWaves][kCells];  // counts, then each wave's cursors
   const uint32_t tid = threadIdx.x, lane = tid % 64, wave = tid / 64, tile = blockIdx.x;
   const bool is_cell = tid < kCells;
   // Cell offsets: the exclusive scan of the cells' totals.
@@ -216,7 +257,6 @@ __global__ __launch_bounds__(kBuildThreads) void index_scatter(
     const uint32_t next = tile + 1 < tiles ? starts[(uint64_t)tid * tiles + tile + 1] : total;
     here = next - start;
     gbase[tid] = cell_base + start;
-    cursor[tid] = 0;
   }
   __syncthreads();  // buf is reused by the next scan
   const uint32_t lincl = block_scan<kBuildThreads>(here, buf);
@@ -225,39 +265,50 @@ __global__ __launch_bounds__(kBuildThreads) void index_scatter(
   for (uint32_t i = tid; i < kBuildWaves * kCells; i += kBuildThreads) (&wave_cnt[0][0])[i] = 0;
   __syncthreads();
   const uint64_t below = (1ull << lane) - 1;
-  for (uint32_t r = 0; r < per; r++) {
-    const uint32_t t = (tile * per + r) * kBuildThreads + tid;
-    const uint32_t c = t < count ? cells[t] : kAbsent;
-    const bool valid = c != kAbsent;
-    uint64_t peers = __ballot(valid);
+  // This wave's chunk: per rounds of 64 consecutive tokens, its cells loaded at once.
+  const uint32_t local = wave * per * 64 + lane, tile_base = tile * per * kBuildThreads;
+  uint32_t cv[kMaxPer];
 #pragma unroll
-    for (int b = 0; b < 8; b++) {
-      const bool bit = (c >> b) & 1;
-      const uint64_t m = __ballot(bit);
-      peers &= bit ? m : ~m;
-    }
-    if (valid && (peers & below) == 0) wave_cnt[wave][c] = __popcll(peers);
-    __syncthreads();
-    if (valid) {
-      uint32_t rank = cursor[c] + __popcll(peers & below);
-      for (uint32_t w = 0; w < wave; w++) rank += wave_cnt[w][c];
-      sorted[lstart[c] + rank] = t;
-    }
-    __syncthreads();
-    if (is_cell) {
-      uint32_t add = 0;
-      for (uint32_t w = 0; w < kBuildWaves; w++) {
-        add += wave_cnt[w][tid];
-        wave_cnt[w][tid] = 0;
-      }
-      cursor[tid] += add;
-    }
-    __syncthreads();
+  for (uint32_t r = 0; r < kMaxPer; r++) {
+    const uint32_t t = tile_base + local + r * 64;
+    cv[r] = r < per && t < count ? cells[t] : kAbsent;
   }
+#pragma unroll
+  for (uint32_t r = 0; r < kMaxPer; r++) {
+    if (r >= per) break;
+    const uint32_t c = cv[r];
+    const bool valid = c != kAbsent;
+    const uint64_t peers = same_cell(c, valid);
+    if (valid && (peers & below) == 0) wave_cnt[wave][c] += __popcll(peers);
+    wave_sync();
+  }
+  __syncthreads();
+  // Each wave's first place in each cell's run: the run's start and the earlier waves' counts.
+  if (is_cell) {
+    uint32_t at = lstart[tid];
+    for (uint32_t w = 0; w < kBuildWaves; w++) {
+      const uint32_t n = wave_cnt[w][tid];
+      wave_cnt[w][tid] = at;
+      at += n;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (uint32_t r = 0; r < kMaxPer; r++) {
+    if (r >= per) break;
+    const uint32_t c = cv[r];
+    const bool valid = c != kAbsent;
+    const uint64_t peers = same_cell(c, valid);
+    if (valid) sorted[wave_cnt[wave][c] + __popcll(peers & below)] = c << 16 | (local + r * 64);
+    wave_sync();
+    if (valid && (peers & below) == 0) wave_cnt[wave][c] += __popcll(peers);
+    wave_sync();
+  }
+  __syncthreads();
   const uint32_t n = lstart[kCells];
   for (uint32_t i = tid; i < n; i += kBuildThreads) {
-    const uint32_t c = cell_at(lstart, i);
-    members[gbase[c] + (i - lstart[c])] = sorted[i];
+    const uint32_t e = sorted[i], c = e >> 16;
+    members[gbase[c] + (i - lstart[c])] = tile_base + (e & 0xffff);
   }
 }
 
