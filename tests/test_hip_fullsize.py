@@ -9,7 +9,8 @@ oracle on whole sequences drawn from the same batch.
   its own reply through the rows kernel (decode = step_native fed its choices,
   fbs-toks.rs:1513-1533), and equals the oracle's decode (reply, state, window, position) on
   sampled sequences.
-- C4 teacher-forced scoring rows (128 tokens, Zipf prompts): the match count is additive over
+- C4 teacher-forced scoring at BASELINE's 1,048,576 rows of 128 tokens (Zipf prompts): the
+  match count is additive over
   any split of the rows, equals the count recomputed from the per-position choices, and the
   choices equal the oracle's on sampled rows.
 - C5 (width 512, int8 codes, window 32, 1,024 drawers probing 16) decode at its per-sequence
@@ -88,9 +89,10 @@ def test_c5_decode_full_length():
 
 
 def test_c4_scoring_rows():
+    # BASELINE's C4 shape: 1,048,576 Zipf rows of 128 tokens (about 13 s a pass on MI355X).
     spec = synth.CONFIGS["c4"]
     art = synth.make_artifact(spec, 2026120204)
-    n = 131072
+    n = 1 << 20
     rows = synth.zipf_prompts(spec.vocab, n, 128, 2026120205)
     print(f"c4: {n} rows x 128", flush=True)
     model = Model(art)
@@ -104,7 +106,7 @@ def test_c4_scoring_rows():
     assert a + b == total
     np.testing.assert_array_equal(arg_a, argmin[: n // 3])
     # The oracle on sampled rows.
-    pick = np.linspace(0, n - 1, 512).astype(np.int64)
+    pick = np.concatenate([np.linspace(0, n - 1, 510).astype(np.int64), [131071, 131072]])
     st, want_matches, want_argmin = oracle.score(art, rows[pick], threads=16)
     assert st == 0
     np.testing.assert_array_equal(argmin[pick], want_argmin)
