@@ -388,17 +388,12 @@ __device__ __forceinline__ void scan_load(const DevModel &M, const uint32_t *lis
   }
 }
 
-// Four biased bytes (code + 128) of `x` as two words of 16-bit halves, each (code + 128) << s:
-// a byte permute places bytes 0, 1 (lo) and 2, 3 (hi) in the halves' low bytes, and a packed
-// 16-bit shift raises them.
-typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ void widen8(uint32_t x, u16x2 sh, uint32_t &lo, uint32_t &hi) {
-  const uint32_t a = __builtin_amdgcn_perm(0u, x, 0x0C010C00u);
-  const uint32_t b = __builtin_amdgcn_perm(0u, x, 0x0C030C02u);
-  u16x2 va = __builtin_bit_cast(u16x2, a) << sh;
-  u16x2 vb = __builtin_bit_cast(u16x2, b) << sh;
-  lo = __builtin_bit_cast(uint32_t, va);
-  hi = __builtin_bit_cast(uint32_t, vb);
+// Four biased bytes (code + 128) of `x` as two words of 16-bit halves, each (code + 128) << 8:
+// a byte permute places bytes 0, 1 (lo) and 2, 3 (hi) in the halves' high bytes (the query is
+// scaled to match, scan_setup).
+__device__ __forceinline__ void widen8(uint32_t x, uint32_t &lo, uint32_t &hi) {
+  lo = __builtin_amdgcn_perm(0u, x, 0x010C000Cu);  // bytes 0, 1 as the high bytes of two u16
+  hi = __builtin_amdgcn_perm(0u, x, 0x030C020Cu);  // bytes 2, 3
 }
 
 template <int S, int U, bool Full>
@@ -455,7 +450,6 @@ __device__ __forceinline__ uint64_t scan_rows(const DevModel &M, const uint32_t 
                                               uint32_t base_id, const ScanGeom &g, uint64_t best) {
   constexpr int U = kScanUnroll;
   constexpr uint32_t chunk = (kWave / S) * U;
-  const u16x2 sh = {(unsigned short)M.t8_shift, (unsigned short)M.t8_shift};
   uint4 ra[U][4], rb[U][4];
   uint32_t ta[U], tb[U];
   auto widen = [&](uint4 (&r)[U][4]) {
@@ -465,8 +459,8 @@ __device__ __forceinline__ uint64_t scan_rows(const DevModel &M, const uint32_t 
 #pragma unroll
         for (int w = 0; w < 4; w++) {
           const uint32_t x = r[u][w].x, y = r[u][w].y;
-          widen8(x, sh, r[u][w].x, r[u][w].y);
-          widen8(y, sh, r[u][w].z, r[u][w].w);
+          widen8(x, r[u][w].x, r[u][w].y);
+          widen8(y, r[u][w].z, r[u][w].w);
         }
     }
   };
@@ -542,11 +536,15 @@ __device__ __forceinline__ void scan_setup(const DevModel &M, const int32_t *q, 
     if (T8) {
       // Against (code + 128) << s: the query offset by 128 << s and clamped to the table's range
       // [0, 255 << s], which adds the same amount to every candidate's L1 on the channel (the
-      // clamped-off distance), so the lowest (L1, token) is unchanged.
-      const int32_t off = 128 << M.t8_shift, top = 255 << M.t8_shift;
+      // clamped-off distance), so the lowest (L1, token) is unchanged. Both sides are then
+      // scaled by 2^(8 - s) (s <= 8), so a row's byte is the high byte of its u16 as loaded:
+      // every candidate's L1 is multiplied by the same power of two, which keeps the order and
+      // the ties, and stays below 2^26 for d <= 1024.
+      const int32_t lo = -(128 << M.t8_shift), hi = 127 << M.t8_shift;
+      const uint32_t up = 8 - M.t8_shift;
       auto b = [&](int32_t v) -> uint32_t {
-        const int32_t x = v + off;
-        return (uint32_t)(x < 0 ? 0 : x > top ? top : x);
+        const int32_t x = v < lo ? lo : v > hi ? hi : v;
+        return (uint32_t)(x - lo) << up;
       };
 #pragma unroll
       for (int j = 0; j < 4; j++) qpk[4 * w + j] = b(q[c + 2 * j]) | (b(q[c + 2 * j + 1]) << 16);
