@@ -109,10 +109,20 @@ __device__ __forceinline__ uint64_t ham_code(const DevHamRead &R, uint32_t heads
   return R.codes[(uint64_t)token * heads + head];
 }
 
-// One token's Q12 table value on the lane's four channels of quaternion q.
+// One token's biased table words on the lane's four channels of quaternion q, and their Q12
+// values.
+__device__ __forceinline__ uint2 ham_point_raw(const DevModel &M, uint32_t token, uint32_t q) {
+  return *(const uint2 *)(M.table_b + (uint64_t)token * M.d + 4 * q);
+}
+__device__ __forceinline__ void ham_point_of(uint2 w, int64_t (&v)[4]) {
+  v[0] = (int16_t)(uint16_t)((w.x & 0xffffu) ^ 0x8000u);
+  v[1] = (int16_t)(uint16_t)((w.x >> 16) ^ 0x8000u);
+  v[2] = (int16_t)(uint16_t)((w.y & 0xffffu) ^ 0x8000u);
+  v[3] = (int16_t)(uint16_t)((w.y >> 16) ^ 0x8000u);
+}
 __device__ __forceinline__ void ham_point(const DevModel &M, uint32_t token, uint32_t q,
                                           int64_t (&v)[4]) {
-  const uint2 w = *(const uint2 *)(M.table_b + (uint64_t)token * M.d + 4 * q);
+  const uint2 w = ham_point_raw(M, token, q);
   v[0] = (int16_t)(uint16_t)((w.x & 0xffffu) ^ 0x8000u);
   v[1] = (int16_t)(uint16_t)((w.x >> 16) ^ 0x8000u);
   v[2] = (int16_t)(uint16_t)((w.y & 0xffffu) ^ 0x8000u);
@@ -126,6 +136,11 @@ __device__ __forceinline__ void ham_point(const DevModel &M, uint32_t token, uin
 // 0..64 (`copy_weight_q31` of its margin, formed by the host), positive exactly below the
 // margin. Returns their count, uniform. For the longest rule, longer(s) says whether one token
 // more matches.
+// The positions a lane visits are taken kHamBatch at a time, their keys (a token from LDS, then
+// a code from the read's table) loaded together before any is used, so that a lane waits for one
+// round trip per batch rather than one per position.
+constexpr uint32_t kHamBatch = 8;
+
 template <class KeyF, class LongerF>
 __device__ __forceinline__ uint32_t ham_choose(const Lds &S, uint32_t rule, uint64_t q, uint32_t t,
                                                uint32_t kept, int32_t margin, const uint32_t *wd,
@@ -142,49 +157,88 @@ __device__ __forceinline__ uint32_t ham_choose(const Lds &S, uint32_t rule, uint
       S.hwd[i] = wd[i];
     }
     wave_sync();
-    for (uint32_t s = 1 + lane; s < t; s += kWave) {
-      const uint32_t dd = (uint32_t)__popcll(q ^ keyf(s));
-      S.hdist[s] = (uint8_t)dd;
-      if (dd < dlim) atomicAdd(&S.hhist[dd], 1u);
+    for (uint32_t s0 = 1 + lane; s0 < t; s0 += kHamBatch * kWave) {
+      uint64_t key[kHamBatch];
+#pragma unroll
+      for (uint32_t u = 0; u < kHamBatch; u++) {
+        const uint32_t s = s0 + u * kWave;
+        key[u] = s < t ? keyf(s) : 0;
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < kHamBatch; u++) {
+        const uint32_t s = s0 + u * kWave;
+        if (s >= t) break;
+        const uint32_t dd = (uint32_t)__popcll(q ^ key[u]);
+        S.hdist[s] = (uint8_t)dd;
+        if (dd < dlim) atomicAdd(&S.hhist[dd], 1u);
+      }
     }
     wave_sync();
     // The threshold: the least distance th at which the positions nearer or equal reach `kept`
     // (then `need` positions at th are taken, the earliest first), else every position inside
-    // the margin (th = dlim).
-    uint32_t th = dlim, need = 0, cum = 0;
-    for (uint32_t dd = 0; dd < dlim; dd++) {
-      const uint32_t h = S.hhist[dd];
-      if (cum + h >= kept) {
-        th = dd;
-        need = kept - cum;
-        break;
+    // the margin (th = dlim). Lane l holds distance l's count; a wave prefix sum of the counts
+    // and a ballot of the lanes whose running count reaches `kept` find th at once, distance 64
+    // (a lane short) after them.
+    const uint32_t h = lane < dlim ? S.hhist[lane] : 0u;
+    uint32_t cum = h;
+#pragma unroll
+    for (uint32_t off = 1; off < kWave; off <<= 1) {
+      const uint32_t y = (uint32_t)__shfl_up((int)cum, off, kWave);
+      cum += lane >= off ? y : 0u;
+    }
+    const uint64_t reach = __ballot(lane < dlim && cum >= kept);
+    uint32_t th = dlim, need = 0;
+    if (reach) {
+      th = (uint32_t)__builtin_ctzll(reach);
+      need = kept - ((uint32_t)__shfl((int)cum, (int)th, kWave) - (uint32_t)__shfl((int)h, (int)th, kWave));
+    } else if (dlim > kWave) {
+      const uint32_t below64 = (uint32_t)__shfl((int)cum, kWave - 1, kWave);
+      if (below64 + S.hhist[kWave] >= kept) {
+        th = kWave;
+        need = kept - below64;
       }
-      cum += h;
     }
     // One pass in ascending position: positions nearer than th, and the first `need` at th.
     const uint64_t below = __lanemask_lt();
     uint32_t at = 0;
-    for (uint32_t s0 = 1; s0 < t; s0 += kWave) {
-      const uint32_t s = s0 + lane;
-      const uint32_t dd = s < t ? S.hdist[s] : 255u;
-      const uint64_t eq = __ballot(dd == th);
-      const bool take = dd < th || (dd == th && at + (uint32_t)__popcll(eq & below) < need);
-      const uint64_t tk = __ballot(take);
-      if (take) {
-        const uint32_t i = n + (uint32_t)__popcll(tk & below);
-        S.hpick[i] = s;
-        S.hwgt[i] = S.hwd[dd];
+    for (uint32_t s1 = 1; s1 < t; s1 += 4 * kWave) {  // four rounds' distances read together
+      uint32_t dv[4];
+#pragma unroll
+      for (uint32_t u = 0; u < 4; u++) {
+        const uint32_t s = s1 + u * kWave + lane;
+        dv[u] = s < t ? S.hdist[s] : 255u;
       }
-      n += (uint32_t)__popcll(tk);
-      at += (uint32_t)__popcll(eq);
+#pragma unroll
+      for (uint32_t u = 0; u < 4; u++) {
+        const uint32_t s = s1 + u * kWave + lane, dd = dv[u];
+        const uint64_t eq = __ballot(dd == th);
+        const bool take = dd < th || (dd == th && at + (uint32_t)__popcll(eq & below) < need);
+        const uint64_t tk = __ballot(take);
+        if (take) {
+          const uint32_t i = n + (uint32_t)__popcll(tk & below);
+          S.hpick[i] = s;
+          S.hwgt[i] = S.hwd[dd];
+        }
+        n += (uint32_t)__popcll(tk);
+        at += (uint32_t)__popcll(eq);
+      }
     }
   } else if (rule <= 2) {
     uint32_t best = UINT32_MAX;
-    for (uint32_t s = 1 + lane; s < t; s += kWave) {
-      const uint32_t dd = (uint32_t)__popcll(q ^ keyf(s));
-      if (rule == 1 && dd != 0) continue;
-      const uint32_t k = dd << kPosBits | (kPosMask - s);
-      best = k < best ? k : best;
+    for (uint32_t s0 = 1 + lane; s0 < t; s0 += kHamBatch * kWave) {
+      uint64_t key[kHamBatch];
+#pragma unroll
+      for (uint32_t u = 0; u < kHamBatch; u++) {
+        const uint32_t s = s0 + u * kWave;
+        key[u] = s < t ? keyf(s) : 0;
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < kHamBatch; u++) {
+        const uint32_t s = s0 + u * kWave;
+        const uint32_t dd = (uint32_t)__popcll(q ^ key[u]);
+        const uint32_t k = dd << kPosBits | (kPosMask - s);
+        best = s < t && (rule != 1 || dd == 0) && k < best ? k : best;
+      }
     }
     const uint32_t m = wave_reduce32(best, OpMin());
     const uint32_t w = m == UINT32_MAX ? 0 : wd[m >> kPosBits];
@@ -197,10 +251,20 @@ __device__ __forceinline__ uint32_t ham_choose(const Lds &S, uint32_t rule, uint
     }
   } else {
     uint32_t ex = 0, lg = 0;
-    for (uint32_t s = 1 + lane; s < t; s += kWave) {
-      if (keyf(s) != q) continue;
-      ex = s > ex ? s : ex;
-      if (longer(s)) lg = s > lg ? s : lg;
+    for (uint32_t s0 = 1 + lane; s0 < t; s0 += kHamBatch * kWave) {
+      uint64_t key[kHamBatch];
+#pragma unroll
+      for (uint32_t u = 0; u < kHamBatch; u++) {
+        const uint32_t s = s0 + u * kWave;
+        key[u] = s < t ? keyf(s) : ~q;
+      }
+#pragma unroll
+      for (uint32_t u = 0; u < kHamBatch; u++) {
+        const uint32_t s = s0 + u * kWave;
+        if (s >= t || key[u] != q) continue;
+        ex = s > ex ? s : ex;
+        if (longer(s)) lg = s > lg ? s : lg;
+      }
     }
     ex = wave_reduce32(ex, OpMax());
     lg = wave_reduce32(lg, OpMax());
@@ -254,12 +318,22 @@ __device__ __forceinline__ bool ham_copy_mean(const DevModel &M, const DevHamRea
     for (int k = 0; k < Q; k++) {
       if (!qv[k]) continue;
       int64_t acc[4] = {0, 0, 0, 0};
-      for (uint32_t i = 0; i < n; i++) {
-        int64_t v[4];
-        ham_point(M, tk[S.hpick[i]], qi[k], v);
-        const int64_t w = S.hwgt[i];
+      for (uint32_t i0 = 0; i0 < n; i0 += 16) {  // sixteen positions' points loaded together
+        uint2 raw[16];
 #pragma unroll
-        for (int c = 0; c < 4; c++) acc[c] += v[c] * w;
+        for (uint32_t u = 0; u < 16; u++) {
+          const uint32_t i = i0 + u;
+          raw[u] = i < n ? ham_point_raw(M, tk[S.hpick[i]], qi[k]) : make_uint2(0x80008000u, 0x80008000u);
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < 16; u++) {
+          const uint32_t i = i0 + u;
+          const int64_t w = i < n ? S.hwgt[i] : 0;
+          int64_t v[4];
+          ham_point_of(raw[u], v);
+#pragma unroll
+          for (int c = 0; c < 4; c++) acc[c] += v[c] * w;
+        }
       }
 #pragma unroll
       for (int c = 0; c < 4; c++) cm[k][c] += div_trunc64(acc[c], dv);
@@ -348,22 +422,30 @@ __device__ __forceinline__ bool ham_type_mean(const DevModel &M, const DevHamRea
     for (int k = 0; k < Q; k++) {
       if (!qv[k]) continue;
       i128 acc[4] = {0, 0, 0, 0};
-      for (uint32_t i = 0; i < n; i++) {
-        const uint32_t s = S.hpick[i];
-        const int64_t w = S.hwgt[i];
-        int64_t v[4];
-        if (asks) {
-          ham_point(M, tk[s], qi[k], v);
-        } else {
-          const longlong2 *src = (const longlong2 *)(pay + (uint64_t)s * d + 4 * qi[k]);
-          const longlong2 a = src[0], b = src[1];
-          v[0] = a.x;
-          v[1] = a.y;
-          v[2] = b.x;
-          v[3] = b.y;
+      for (uint32_t i0 = 0; i0 < n; i0 += 4) {  // four positions' values loaded together
+        int64_t v[4][4], w[4];
+#pragma unroll
+        for (uint32_t u = 0; u < 4; u++) {
+          const uint32_t i = i0 + u;
+          w[u] = i < n ? S.hwgt[i] : 0;
+          v[u][0] = v[u][1] = v[u][2] = v[u][3] = 0;
+          if (i >= n) continue;
+          const uint32_t s = S.hpick[i];
+          if (asks) {
+            ham_point(M, tk[s], qi[k], v[u]);
+          } else {
+            const longlong2 *src = (const longlong2 *)(pay + (uint64_t)s * d + 4 * qi[k]);
+            const longlong2 a = src[0], b = src[1];
+            v[u][0] = a.x;
+            v[u][1] = a.y;
+            v[u][2] = b.x;
+            v[u][3] = b.y;
+          }
         }
 #pragma unroll
-        for (int c = 0; c < 4; c++) acc[c] += (i128)v[c] * w;
+        for (uint32_t u = 0; u < 4; u++)
+#pragma unroll
+          for (int c = 0; c < 4; c++) acc[c] += (i128)v[u][c] * w[u];
       }
 #pragma unroll
       for (int c = 0; c < 4; c++) ym[k][c] += div_trunc128(acc[c], dv);
