@@ -263,3 +263,19 @@ def test_knockout(mode):
                 assert (rel[r][:, :n] == 0).all()
     # The knockout is the flag's alone: the model's own evaluation is unchanged.
     assert oracle.d11_score_rows(art, *rows, threads=2).tobytes() == plain.tobytes()
+
+
+def test_m1_shape_reads_hold_to_the_trace_checks():
+    """At the M1 panel's shape (vocabulary 4,096, 4 blocks, context 192, relation read keeping 8
+    with one sweep), the oracle's reads on rows of 186-192 tokens satisfy every check above: the
+    kept nodes by brute-force sort, each level's snapped root and the block's read recomputed
+    from the words. (The trunk's pointer gate comes after the read; the model is taken without it.)"""
+    art = d11.synthetic(vocabulary=4096, blocks=4, context=192, kept_cells=8, read_mode="relation",
+                        read_kept=8, read_sweeps=1, seed=44, trunk=False)
+    pre, lens, tg = d11.panel_rows(art, 6, 45, min_len=186)
+    out, tr, rel = traced(art, (pre, lens, tg))
+    assert (out["status"] == 0).all()
+    for r in range(6):
+        prefix = pre[r, :lens[r]]
+        _, want = oracle.d11_row_relation(art, prefix, int(tg[r]))
+        check_active(art, prefix, out[r], tr[r], want)
