@@ -396,7 +396,27 @@ __device__ __forceinline__ void widen8(uint32_t x, uint32_t &lo, uint32_t &hi) {
   hi = __builtin_amdgcn_perm(0u, x, 0x030C020Cu);  // bytes 2, 3
 }
 
-template <int S, int U, bool Full>
+// One row piece's L1 against the query: eight 16-bit channels (i16 table), or T8 the piece's
+// eight int8 codes (x, y) widened at the SAD, so that a stage in flight holds the raw bytes.
+template <bool T8>
+__device__ __forceinline__ uint32_t piece_sad(const uint4 &p, const uint32_t (&qpk)[16], int w,
+                                              uint32_t acc) {
+  if (T8) {
+    uint32_t lo, hi;
+    widen8(p.x, lo, hi);
+    acc = sad2_u16(lo, qpk[4 * w + 0], acc);
+    acc = sad2_u16(hi, qpk[4 * w + 1], acc);
+    widen8(p.y, lo, hi);
+    acc = sad2_u16(lo, qpk[4 * w + 2], acc);
+    return sad2_u16(hi, qpk[4 * w + 3], acc);
+  }
+  acc = sad2_u16(p.x, qpk[4 * w + 0], acc);
+  acc = sad2_u16(p.y, qpk[4 * w + 1], acc);
+  acc = sad2_u16(p.z, qpk[4 * w + 2], acc);
+  return sad2_u16(p.w, qpk[4 * w + 3], acc);
+}
+
+template <int S, int U, bool Full, bool T8>
 __device__ __forceinline__ uint64_t scan_score(const uint32_t (&qpk)[16], uint32_t fill,
                                                uint32_t k0, const ScanGeom &g,
                                                const uint4 (&r)[U][4], const uint32_t (&t)[U],
@@ -408,12 +428,7 @@ __device__ __forceinline__ uint64_t scan_score(const uint32_t (&qpk)[16], uint32
     for (int u = 0; u < U; u++) {
       acc[u] = 0;
 #pragma unroll
-      for (int w = 0; w < 4; w++) {
-        acc[u] = sad2_u16(r[u][w].x, qpk[4 * w + 0], acc[u]);
-        acc[u] = sad2_u16(r[u][w].y, qpk[4 * w + 1], acc[u]);
-        acc[u] = sad2_u16(r[u][w].z, qpk[4 * w + 2], acc[u]);
-        acc[u] = sad2_u16(r[u][w].w, qpk[4 * w + 3], acc[u]);
-      }
+      for (int w = 0; w < 4; w++) acc[u] = piece_sad<T8>(r[u][w], qpk, w, acc[u]);
     }
   } else {
 #pragma unroll
@@ -421,10 +436,7 @@ __device__ __forceinline__ uint64_t scan_score(const uint32_t (&qpk)[16], uint32
       acc[u] = 0;
 #pragma unroll
       for (int w = 0; w < 4; w++) {
-        uint32_t a = sad2_u16(r[u][w].x, qpk[4 * w + 0], 0);
-        a = sad2_u16(r[u][w].y, qpk[4 * w + 1], a);
-        a = sad2_u16(r[u][w].z, qpk[4 * w + 2], a);
-        a = sad2_u16(r[u][w].w, qpk[4 * w + 3], a);
+        const uint32_t a = piece_sad<T8>(r[u][w], qpk, w, 0u);
         acc[u] += (g.valid >> w) & 1 ? a : 0;  // a piece past the row's end adds nothing
       }
     }
@@ -452,26 +464,12 @@ __device__ __forceinline__ uint64_t scan_rows(const DevModel &M, const uint32_t 
   constexpr uint32_t chunk = (kWave / S) * U;
   uint4 ra[U][4], rb[U][4];
   uint32_t ta[U], tb[U];
-  auto widen = [&](uint4 (&r)[U][4]) {
-    if (T8) {
-#pragma unroll
-      for (int u = 0; u < U; u++)
-#pragma unroll
-        for (int w = 0; w < 4; w++) {
-          const uint32_t x = r[u][w].x, y = r[u][w].y;
-          widen8(x, r[u][w].x, r[u][w].y);
-          widen8(y, r[u][w].z, r[u][w].w);
-        }
-    }
-  };
   scan_load<S, U, Full, T8>(M, list, fill, 0, g, base_id, ra, ta);
   for (uint32_t k0 = 0; k0 < fill; k0 += 2 * chunk) {
     scan_load<S, U, Full, T8>(M, list, fill, k0 + chunk, g, base_id, rb, tb);
-    widen(ra);
-    best = scan_score<S, U, Full>(qpk, fill, k0, g, ra, ta, best);
+    best = scan_score<S, U, Full, T8>(qpk, fill, k0, g, ra, ta, best);
     scan_load<S, U, Full, T8>(M, list, fill, k0 + 2 * chunk, g, base_id, ra, ta);
-    widen(rb);
-    best = scan_score<S, U, Full>(qpk, fill, k0 + chunk, g, rb, tb, best);
+    best = scan_score<S, U, Full, T8>(qpk, fill, k0 + chunk, g, rb, tb, best);
   }
   return best;
 }
