@@ -1702,6 +1702,10 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
   // Paired blocks: wave 0 keeps the recurrence state, wave 1 the window ring.
   const bool keeps_state = NW == 1 || wave == 0, keeps_ring = NW == 1 || wave == 1;
   const bool writes_out = wave == 0 && lane == 0;
+  // The recurrence wave is the step's critical path (its instructions issue one after another,
+  // each waiting for the last), while the ring wave's window sums and candidate scan have slack:
+  // the recurrence wave takes the issue slots first wherever the two compete.
+  if (NW == 2 && wave == 0) __builtin_amdgcn_s_setprio(3);
   const uint32_t d = M.d, L = M.L, W = M.W;
   int32_t *const block_ring = A.ring + (uint64_t)blockIdx.x * L * W * d;
   int64_t *hist = NW == 2 ? A.hist + (uint64_t)blockIdx.x * L * d : nullptr;
