@@ -93,6 +93,11 @@ __device__ __forceinline__ uint64_t wave_reduce64(uint64_t v, Op op) {
   v = op(v, dpp64<kDppMirror>(v));
   return op(op(lane64(v, 0), lane64(v, 16)), op(lane64(v, 32), lane64(v, 48)));
 }
+// The bit length of the wave's largest magnitude from each lane's largest: the bit length of a
+// maximum is the maximum of the bit lengths, so a 32-bit reduction takes the place of a 64-bit one.
+__device__ __forceinline__ int32_t wave_bitlen_max(uint64_t v) {
+  return (int32_t)wave_reduce32((uint32_t)bitlen64(v), OpMax());
+}
 
 // Sums over aligned groups of S lanes (S a power of two), every lane of a group getting its
 // group's sum, for U independent values at once (each exchange step is applied to all U before
@@ -173,7 +178,8 @@ __device__ __forceinline__ void norm_gain(const DevModel &M, const Seeds &sd,
     for (int c = 0; c < 4; c++) {
       int64_t y = qv[k] ? shift((int64_t)x[k][c], sh) : 0;
       out[k][c] = y;
-      sum += uabs64(y) * uabs64(y);
+      const uint32_t a = (uint32_t)uabs64(y);  // |y| <= 2^24: the shift leaves 24 bits
+      sum += (uint64_t)a * a;
     }
   sum = wave_reduce64(sum, OpAdd());
   const NormFactor f = M.log2d != 0xffu ? norm_factor_pow2(sum, M.log2d, M.eps_int[sh], sd)
@@ -980,8 +986,7 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
       }
     }
     // quantize16 over the d outputs (kernels.rs:545-553), then gather16 of rec_out.
-    mx = wave_reduce64(mx, OpMax());
-    int32_t qs = bitlen64(mx) - 15;
+    int32_t qs = wave_bitlen_max(mx) - 15;
     if (qs < 0) qs = 0;
 #pragma unroll
     for (int k = 0; k < Q; k++)
@@ -1039,8 +1044,7 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
         }
       }
     }
-    mmx = wave_reduce64(mmx, OpMax());
-    qs = bitlen64(mmx) - 15;
+    qs = wave_bitlen_max(mmx) - 15;
     if (qs < 0) qs = 0;
     wave_sync();
 #pragma unroll 1
@@ -1162,8 +1166,8 @@ __device__ __forceinline__ void clip_ranges(uint32_t P, uint32_t lane, uint32_t 
 // at the shared shift of both waves' maxima, published for the mlp_down gathers.
 __device__ __forceinline__ void pair_requant(const DevModel &M, const Lds &S, uint32_t lane,
                                              uint32_t j0) {
-  const uint64_t mmx = S.pair[0] > S.pair[1] ? S.pair[0] : S.pair[1];
-  int32_t qs = bitlen64(mmx) - 15;
+  const uint64_t bl = S.pair[0] > S.pair[1] ? S.pair[0] : S.pair[1];  // bit lengths
+  int32_t qs = (int32_t)bl - 15;
   if (qs < 0) qs = 0;
 #pragma unroll 1
   for (uint32_t j = j0; j < M.mpl; j += 2) {
@@ -1178,7 +1182,8 @@ __device__ __forceinline__ void pair_requant(const DevModel &M, const Lds &S, ui
 }
 
 // MLP quaternion groups j0, j0 + 2, ... of the feed-forward gate (session.rs:4005-4025) into
-// S.mlp_out; pg/pu hold group j0's gather words. Returns the groups' maximum magnitude.
+// S.mlp_out; pg/pu hold group j0's gather words. Returns the bit length of the groups' largest
+// magnitude.
 __device__ __forceinline__ uint64_t pair_mlp(const DevModel &M, const Lds &S, const DevLayer &ly,
                                              uint32_t lane, uint32_t j0, uint32_t (&pg)[4],
                                              uint32_t (&pu)[4]) {
@@ -1210,7 +1215,7 @@ __device__ __forceinline__ uint64_t pair_mlp(const DevModel &M, const Lds &S, co
       }
     }
   }
-  return wave_reduce64(mmx, OpMax());
+  return (uint64_t)wave_bitlen_max(mmx);
 }
 
 __device__ __forceinline__ void pair_mlp_words(const DevModel &M, const DevLayer &ly, uint32_t lane,
@@ -1390,8 +1395,7 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
       }
     }
     // quantize16 over the d outputs (kernels.rs:545-553), then gather16 of rec_out.
-    mx = wave_reduce64(mx, OpMax());
-    int32_t qs = bitlen64(mx) - 15;
+    int32_t qs = wave_bitlen_max(mx) - 15;
     if (qs < 0) qs = 0;
 #pragma unroll
     for (int k = 0; k < Q; k++)
@@ -1414,8 +1418,8 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
     norm_gain<Q>(M, S.seeds, x, qv, g_mlp, gd_mlp, v);
     publish64<Q>(S.xbar, v, qv, qi);
     pair_sync();  // 3: the normed activations
-    const uint64_t mmx = pair_mlp(M, S, ly, lane, 0, pg, pu);
-    if (lane == 0) S.pair[0] = mmx;
+    const uint64_t mbl = pair_mlp(M, S, ly, lane, 0, pg, pu);
+    if (lane == 0) S.pair[0] = mbl;
     pair_sync();  // 4: both waves' MLP outputs and maxima
     pair_requant(M, S, lane, 0);
     pair_sync();  // 5: the requantized MLP outputs
@@ -1612,8 +1616,8 @@ __device__ __forceinline__ int step_window(const DevModel &M, const Lds &S, int3
       hp[1] = make_longlong2(acc[2], acc[3]);
     }
     pair_sync();  // 3: the normed activations
-    const uint64_t mmx = pair_mlp(M, S, ly, lane, 1, pg, pu);
-    if (lane == 0) S.pair[1] = mmx;
+    const uint64_t mbl = pair_mlp(M, S, ly, lane, 1, pg, pu);
+    if (lane == 0) S.pair[1] = mbl;
     pair_sync();  // 4: both waves' MLP outputs and maxima
     pair_requant(M, S, lane, 1);
     pair_sync();  // 5: the requantized MLP outputs
