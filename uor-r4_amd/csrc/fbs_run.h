@@ -1707,8 +1707,8 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
   const bool keeps_state = NW == 1 || wave == 0, keeps_ring = NW == 1 || wave == 1;
   const bool writes_out = wave == 0 && lane == 0;
   // The recurrence wave is the step's critical path (its instructions issue one after another,
-  // each waiting for the last), while the ring wave's window sums and candidate scan have slack:
-  // the recurrence wave takes the issue slots first wherever the two compete.
+  // each waiting for the last), while the ring wave's window sums have slack: the recurrence
+  // wave takes the issue slots first wherever waves on its SIMD compete for them.
   if (NW == 2 && wave == 0) __builtin_amdgcn_s_setprio(3);
   const uint32_t d = M.d, L = M.L, W = M.W;
   int32_t *const block_ring = A.ring + (uint64_t)blockIdx.x * L * W * d;
