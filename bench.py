@@ -146,6 +146,9 @@ def parse():
     p.add_argument("--no-writer-memory-pass", action="store_true",
                    help="skip the extra timed pass with the writer's memory of its last query off")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-parts", action="store_true",
+                   help="skip the part clocks' launch (the step's phases in cycles, after the "
+                        "timed launches)")
     p.add_argument("--serve-steps", type=int, default=64,
                    help="serving-loop launches after the decode (0: none); reported beside the metric")
     p.add_argument("--no-index", action="store_true",
@@ -934,6 +937,7 @@ def main():
     mean_launch_s = float(np.mean(launch_ms)) / 1e3
     achieved = bpt * tokens / mean_launch_s / 1e9
     bpt_scanned = algorithmic_bytes_per_token(spec, scanned_cand)
+    achieved_scanned = bpt_scanned * tokens / mean_launch_s / 1e9
 
     # The same launches with the writer's memory of its last query off: every decoded token
     # then scans its candidates, so every token moves the algorithmic bytes.
@@ -1005,14 +1009,20 @@ def main():
             "table": spec.table, "batch": B, "prompt": a.prompt, "gen": G,
             "parallelism": "none (1 GPU)",
         },
+        # achieved/frac charge each decoded token the bytes it moves: a token that takes the
+        # writer's remembered result scans no candidate rows. The figure that charges every
+        # token its kept drawers' rows is beside it (_full_scan), and the launch with the
+        # memory off in without_writer_memory.
         "roofline": {
-            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "algorithmic_bytes_per_launch": round(bpt * tokens),
-            "bytes_per_token": round(bpt, 1), "mean_candidate_rows": round(mean_cand, 1),
+            "bound": "hbm", "achieved": round(achieved_scanned, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(achieved_scanned / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "algorithmic_bytes_per_launch": round(bpt_scanned * tokens),
+            "bytes_per_token": round(bpt_scanned, 1),
+            "scanned_candidate_rows": round(scanned_cand, 1),
             "writer_reuse_fraction": round(reused_n / n_tok, 4),
-            "bytes_per_token_scanned": round(bpt_scanned, 1),
-            "frac_scanned": round(bpt_scanned * tokens / mean_launch_s / 1e9 / HBM_PEAK_GBS, 4),
+            "bytes_per_token_full_scan": round(bpt, 1), "mean_candidate_rows": round(mean_cand, 1),
+            "achieved_full_scan": round(achieved, 1),
+            "frac_full_scan": round(achieved / HBM_PEAK_GBS, 4),
             "replay_sequences": n_rep,
             "without_writer_memory": no_memory,
             "kernel": kernel, "launch_ms": [round(x, 3) for x in launch_ms],
@@ -1021,6 +1031,39 @@ def main():
     }
     if B == 1:  # a latency: one sequence (the config's CPU-runnable case)
         out["ms_per_token"] = round(ms_per_step / G, 5)
+
+    if not a.no_parts and model.block_waves(B) == 2:
+        # The part clocks (measure_fbs_step_parts): the same launch from the same state on the
+        # instrumented kernel, outside the timed region; its replies must equal the decode's.
+        names = hip.part_names()
+        n_part = len(names)
+        parts = torch.zeros((B, 2 * n_part + 2), dtype=torch.int64, device=dev)
+        reply_p = torch.zeros_like(reply)
+        ev_p = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+        ev_p[0].record(stream)
+        check(L.uor_fbs_decode_parts_async(model.handle, ptr(first), B, 1, G - 1, ptr(reply_p),
+                                           ptr(state), ptr(hist), ptr(pos), None, None, None,
+                                           ptr(status), ptr(parts), sp))
+        ev_p[1].record(stream)
+        torch.cuda.synchronize()
+        assert int(status.abs().sum()) == 0, "the part clocks' decode failed"
+        raw = parts.cpu().numpy().view(np.uint64)
+        steps_run = float(raw[:, 2 * n_part].sum())
+        cyc = raw[:, :2 * n_part].reshape(B, 2, n_part).sum(0).astype(np.float64) / steps_run
+        total0 = float(cyc[0].sum())
+        mhz = float(raw[:, :n_part].sum()) / float(raw[:, 2 * n_part + 1].sum()) * 100.0
+        out["parts"] = {
+            "what": "cycles per decoded token in each phase of the paired step, wave 0 (the "
+                    "recurrence chain) and wave 1 (the window ring), summed over layers; syncN "
+                    "is the wait at barrier N; from one launch of the instrumented kernel "
+                    "(uor_fbs_decode_parts_async) at this workload",
+            "wave0": {n: round(float(c), 1) for n, c in zip(names, cyc[0])},
+            "wave1": {n: round(float(c), 1) for n, c in zip(names, cyc[1])},
+            "cycles_per_token": round(total0, 1),
+            "shader_mhz": round(mhz, 1),
+            "launch_ms": round(ev_p[0].elapsed_time(ev_p[1]), 3),
+            "replies_equal_decode": bool(torch.equal(reply_p, reply)),
+        }
 
     if a.serve_steps:
         # The serving loop: every sequence is a session in a device slot (a fixed permutation of

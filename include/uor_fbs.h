@@ -219,6 +219,24 @@ int uor_fbs_decode_async(uor_fbs_handle *handle, const uint32_t *prompts, uint32
                          int32_t *out_history, uint32_t *out_position, int32_t *status,
                          void *stream);
 
+/* Part clocks, after measure_fbs_step_parts (session.rs:4721-4779, stack_step_fbs_timed :4456)
+ * and `fbs-toks --parts`: uor_fbs_decode_async (gen > 0, a model the paired kernels serve) on an
+ * instrumented copy of its kernel that reads the shader clock between the step's phases.
+ * Outputs, state and statuses are the decode's. `out_parts` (device) gets per sequence
+ * 2 * uor_fbs_part_count() + 2 uint64 words: for wave 0 (the recurrence chain) and then wave 1
+ * (the window ring) the cycles spent in each part, summed over the sequence's steps and layers
+ * (uor_fbs_part_name: the reference's parts of a step, the barriers between the two waves as
+ * parts of their own), then the steps run, then the sequence's time in ticks of the 100 MHz
+ * real-time counter. The clock reads cost time of their own: compare a plain decode's. */
+uint32_t uor_fbs_part_count(void);
+const char *uor_fbs_part_name(uint32_t part);
+int uor_fbs_decode_parts_async(uor_fbs_handle *handle, const uint32_t *prompts,
+                               uint32_t sequences, uint32_t prompt_len, uint32_t gen,
+                               uint32_t *out_reply, const int64_t *in_state,
+                               const int32_t *in_history, const uint32_t *in_position,
+                               int64_t *out_state, int32_t *out_history, uint32_t *out_position,
+                               int32_t *status, uint64_t *out_parts, void *stream);
+
 /* uor_fbs_decode_async without allocating: no hipMalloc, hipFree or allocating library call,
  * for callers that cannot allocate (code under HIP graph capture, tight serving loops, hosts
  * that forbid allocation on their path). No counterpart in the reference. Same arguments,

@@ -41,6 +41,7 @@ FBS_LAUNCHER(fbs_decode_8)
 FBS_LAUNCHER(fbs_decode_pair8)
 FBS_LAUNCHER(fbs_rows_8)
 FBS_LAUNCHER(fbs_rows_pair8)
+FBS_LAUNCHER(fbs_decode_pair_clk)
 #undef FBS_LAUNCHER
 }
 
@@ -85,6 +86,7 @@ struct uor_fbs_handle {
   bool pair = false;
   size_t pair_lds = 0;
   uint32_t pair_grid = 0;
+  size_t lds_limit = 0;  // LDS bytes a block may take
   int32_t *ring = nullptr;
   int64_t *hist = nullptr;
   size_t ring_blocks = 0;
@@ -656,6 +658,7 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
   h->pair_lds = fbs::pair_lds_bytes(M);
   h->pair = !(bw && bw[0] == '1' && !bw[1]) && h->pair_lds <= prop.sharedMemPerBlock && !M.ham.heads;
   h->pair_grid = (uint32_t)prop.multiProcessorCount * 4;  // four SIMDs per CU
+  h->lds_limit = prop.sharedMemPerBlock;
   return done(0);
 }
 
@@ -680,6 +683,11 @@ namespace {
 int launch(uor_fbs_handle *h, RunArgs &A, hipStream_t stream, bool noalloc = false,
            bool one_wave = false) {
   if (A.n == 0) return 0;
+  const bool clocks = A.out_parts != nullptr;
+  if (clocks && (!h->pair || one_wave || noalloc || h->M.ham.heads || A.mode != kModeDecode ||
+                 A.gen == 0 || A.slots))
+    return fail(UOR_FBS_ERR_UNSUPPORTED,
+                "the part clocks time the paired decode kernels (a model they serve, gen > 0)");
   if (!A.slots) A.capacity = A.n;
   const bool pair = h->pair && !one_wave;
   const uint32_t cap = pair ? h->pair_grid : h->max_grid;
@@ -719,7 +727,13 @@ int launch(uor_fbs_handle *h, RunArgs &A, hipStream_t stream, bool noalloc = fal
   }
   const bool decode = A.mode == kModeDecode;
   const uint32_t waves = pair ? 2 : 1;
-  const size_t lds = pair ? h->pair_lds : h->lds_bytes;
+  const size_t lds = pair ? h->pair_lds + (clocks ? clock_lds_bytes() : 0) : h->lds_bytes;
+  if (clocks) {
+    if (lds > h->lds_limit)
+      return fail(UOR_FBS_ERR_UNSUPPORTED, "the part clocks' LDS (%zu bytes) does not fit", lds);
+    hipError_t e = launch_fbs_decode_pair_clk(h->M, A, grid, lds, stream);
+    return e != hipSuccess ? hip_fail(e, "kernel launch") : 0;
+  }
   using Launcher = hipError_t (*)(const DevModel &, const RunArgs &, uint32_t, size_t, hipStream_t);
   // Families: one wavefront, paired, Hamming reads, then the first two for an int8 table.
   static const Launcher table[3][5] = {
@@ -916,6 +930,47 @@ extern "C" int uor_fbs_decode_async(uor_fbs_handle *h, const uint32_t *prompts, 
   A.out_history = out_history;
   A.out_position = out_position;
   A.status = status;
+  return launch(h, A, (hipStream_t)stream);
+}
+
+extern "C" uint32_t uor_fbs_part_count(void) { return kParts; }
+
+extern "C" const char *uor_fbs_part_name(uint32_t part) {
+  static const char *const names[kParts] = {
+      "embed",        "loads",          "norm_rec",     "sync1",          "transition",
+      "sync2",        "transport",      "requant_rec",  "residual_rec",   "norm_mlp",
+      "sync3",        "mlp",            "sync4",        "requant_mlp",    "sync5",
+      "residual_mlp", "final",          "sync6",        "select",         "sync7",
+      "scan",         "sync8",          "step"};
+  return part < kParts ? names[part] : nullptr;
+}
+
+extern "C" int uor_fbs_decode_parts_async(uor_fbs_handle *h, const uint32_t *prompts,
+                                          uint32_t sequences, uint32_t prompt_len, uint32_t gen,
+                                          uint32_t *out_reply, const int64_t *in_state,
+                                          const int32_t *in_history, const uint32_t *in_position,
+                                          int64_t *out_state, int32_t *out_history,
+                                          uint32_t *out_position, int32_t *status,
+                                          uint64_t *out_parts, void *stream) {
+  if (!h || !prompts || !out_reply || !status || !out_parts)
+    return fail(UOR_FBS_ERR_ARGUMENT, "null argument");
+  if (prompt_len == 0) return fail(UOR_FBS_ERR_ARGUMENT, "a decode needs at least one prompt token");
+  DeviceScope scope(h->device);
+  RunArgs A{};
+  A.mode = kModeDecode;
+  A.n = sequences;
+  A.len = prompt_len;
+  A.gen = gen;
+  A.tokens = prompts;
+  A.out_tokens = out_reply;
+  A.in_state = in_state;
+  A.in_history = in_history;
+  A.in_position = in_position;
+  A.out_state = out_state;
+  A.out_history = out_history;
+  A.out_position = out_position;
+  A.status = status;
+  A.out_parts = out_parts;
   return launch(h, A, (hipStream_t)stream);
 }
 

@@ -198,7 +198,49 @@ struct RunArgs {
   // One wavefront a sequence only: the snap trace, L (2 d/4 + m/4) bytes a position, of every
   // position (sequences) or of every step, len + gen a sequence (decode) (null: none).
   uint8_t *out_trace;
+  // The part clocks' kernels only: kPartWords u64 a sequence (Part).
+  uint64_t *out_parts;
 };
+
+// The part clocks (uor_fbs_decode_parts_async, after the reference's measure_fbs_step_parts,
+// session.rs:4753): the phases of a paired block's step in the order they run, each wave's
+// shader-clock cycles summed over a sequence's steps and layers. Wave 0 (the recurrence) and
+// wave 1 (the window ring) share the numbering; a phase one wave does not run stays 0, and a
+// barrier's entry is the time the wave waited there.
+enum Part : uint32_t {
+  kPartEmbed = 0,     // wave 0: the token's table row
+  kPartLoads,         // the layer's parameters and gather words issued (wave 1: the window sums)
+  kPartNormRec,       // wave 0: the recurrence block's norm, gain and publish
+  kPartSync1,
+  kPartTransition,    // wave 0: gathers, lane weights, the transition and its product with the
+                      // state; wave 1: drive and gate gathers, tap 0, the ring write, the gates'
+                      // quaternions
+  kPartSync2,
+  kPartTransport,     // wave 0: the transport and the output gate's product; wave 1: the next
+                      // step's window sums
+  kPartRequantRec,    // wave 0: quantize16 of the gate outputs and their publish
+  kPartResidualRec,   // wave 0: the rec_out gathers and the residual add
+  kPartNormMlp,       // wave 0: the feed-forward block's norm, gain and publish
+  kPartSync3,
+  kPartMlp,           // both: the waves' MLP quaternion groups
+  kPartSync4,
+  kPartRequantMlp,    // both: quantize16 of the waves' MLP groups
+  kPartSync5,
+  kPartResidualMlp,   // wave 0: the mlp_down gathers and the residual add
+  kPartFinal,         // wave 0: the final norm, gain, Q12 query and the writer-memory check
+  kPartSync6,
+  kPartSelect,        // wave 0: drawer scores and the P kept drawers (or the remembered result)
+  kPartSync7,
+  kPartScan,          // both: the wave's half of the candidate rows
+  kPartSync8,
+  kPartStep,          // between steps: the token written out, the position advanced
+  kParts
+};
+// Per sequence: cycles [wave][kParts], then the steps run and the sequence's wall time in ticks
+// of the 100 MHz real-time counter (wave 0).
+constexpr uint32_t kPartWords = 2 * kParts + 2;
+// The part clocks' kernels add each wave's counters to the paired blocks' LDS (2 kParts u64).
+inline size_t clock_lds_bytes() { return 16ull * kParts; }
 
 }  // namespace fbs
 

@@ -786,6 +786,8 @@ struct Lds {
   uint32_t *hhist;   // kHamBins: one head's distance histogram
   uint32_t *hwd;     // kHamBins: the Q31 weight of each distance under the head's margin
   uint32_t *hnib;    // d / 4: the sign nibbles of the row's point
+  // The part clocks' kernels only: [wave][kParts] cycle counters.
+  uint64_t *clk;
 };
 
 }  // namespace fbs
@@ -1144,6 +1146,32 @@ __device__ __forceinline__ void pair_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// The part clocks (Part): with ON, lap(p) adds the shader-clock cycles since the last lap to the
+// wave's counter p in LDS (lane 0 writes it); without, every call compiles to nothing, so the
+// served kernels carry no clock code. The clock read waits for the wave's LDS operations, not for
+// its global loads.
+template <bool ON>
+struct PartClock {
+  uint64_t t = 0;
+  uint64_t *acc = nullptr;  // LDS: this wave's kParts counters
+  __device__ __forceinline__ void start() {
+    if constexpr (ON) t = __builtin_amdgcn_s_memtime();
+  }
+  __device__ __forceinline__ void lap(uint32_t part) {
+    if constexpr (ON) {
+      const uint64_t now = __builtin_amdgcn_s_memtime();
+      if (threadIdx.x % kWave == 0) acc[part] += now - t;
+      t = now;
+    }
+  }
+  // A barrier timed as its own part (the wait), the work before it as `before`.
+  __device__ __forceinline__ void sync(uint32_t before, uint32_t barrier) {
+    lap(before);
+    pair_sync();
+    lap(barrier);
+  }
+};
+
 // Clips the ranges that lanes 0..P-1 hold to the positions [lo, hi) of their concatenation.
 __device__ __forceinline__ void clip_ranges(uint32_t P, uint32_t lane, uint32_t lo, uint32_t hi,
                                             uint32_t &my_beg, uint32_t &my_end) {
@@ -1233,11 +1261,13 @@ __device__ __forceinline__ void pair_mlp_words(const DevModel &M, const DevLayer
 // the step reuses the last result): wave 0 selects the drawers, each wave scans half of the
 // candidates (by position in the kept drawers' concatenated members, or half of the table for
 // the nearest head), and both return the lower (L1, token).
-template <int SW, bool T8>
+template <int SW, bool T8, bool CLK>
 __device__ __forceinline__ uint32_t pair_writer(const DevModel &M, const Lds &S, uint32_t wave,
-                                                uint32_t lane, uint32_t *kept_out) {
+                                                uint32_t lane, uint32_t *kept_out,
+                                                PartClock<CLK> &clk) {
   if (S.wmeta[2]) {
     if (wave == 0 && kept_out && lane < M.P) kept_out[lane] = M.head == 1 ? 0u : S.kept[lane];
+    clk.lap(kPartSelect);
     return S.wmeta[0];
   }
   if (wave == 0 && M.head != 1) {
@@ -1248,7 +1278,7 @@ __device__ __forceinline__ uint32_t pair_writer(const DevModel &M, const Lds &S,
       S.rng[kMaxProbes + lane] = e;
     }
   }
-  pair_sync();  // 7: the kept drawers and their ranges
+  clk.sync(kPartSelect, kPartSync7);  // 7: the kept drawers and their ranges
   ScanGeom g;
   uint32_t qpk[16];
   scan_setup<SW, T8>(M, S.xbar, lane, g, qpk);
@@ -1267,18 +1297,18 @@ __device__ __forceinline__ uint32_t pair_writer(const DevModel &M, const Lds &S,
   }
   best = wave_reduce64(best, OpMin());
   if (lane == 0) S.pair[2 + wave] = best;
-  pair_sync();  // 8: both waves' best candidates
+  clk.sync(kPartScan, kPartSync8);  // 8: both waves' best candidates
   const uint64_t b0 = S.pair[2], b1 = S.pair[3];
   return (uint32_t)(b0 < b1 ? b0 : b1);
 }
 
 // Wave 0 of a paired block: the step (RS stack/session.rs:4129-4403) but the window and its
 // ring, the output gates' quaternions and the odd MLP groups.
-template <int Q, int SW, bool T8>
+template <int Q, int SW, bool T8, bool CLK>
 __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32_t lane,
                                          const bool (&qv)[Q], const uint32_t (&qi)[Q], uint32_t tok,
                                          bool want_writer, uint32_t *chosen, uint32_t *kept_out,
-                                         int32_t *query_out) {
+                                         int32_t *query_out, PartClock<CLK> &clk) {
   if (tok >= M.vocab) return 1;
   const uint32_t d = M.d, nq = M.nq;
   int32_t x[Q][4];
@@ -1293,6 +1323,7 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
       x[k][c] = (int32_t)v << 4;  // to_exp_i32(v, -12, -16)
     }
   }
+  clk.lap(kPartEmbed);
   for (uint32_t l = 0; l < M.L; l++) {
     const DevLayer ly = M.layers[l];
     short4 g_rec[Q], g_mlp[Q];
@@ -1318,10 +1349,11 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
       }
       pw_dec[k] = prog_word(ly.prog, M.s_rec_gate + k, lane);
     }
+    clk.lap(kPartLoads);
     int64_t v[Q][4];
     norm_gain<Q>(M, S.seeds, x, qv, g_rec, gd_rec, v);
     publish64<Q>(S.xbar, v, qv, qi);
-    pair_sync();  // 1: the normed activations
+    clk.sync(kPartNormRec, kPartSync1);  // 1: the normed activations
     int32_t rot[Q][4], dec[Q];
 #pragma unroll
     for (int k = 0; k < Q; k++) {
@@ -1357,7 +1389,7 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
         hamilton64(T64, h, moved[k]);
       }
     }
-    pair_sync();  // 2: the window sums and the output gates' quaternions
+    clk.sync(kPartTransition, kPartSync2);  // 2: the window sums and the output gates' quaternions
     int64_t sc[Q][4];
     uint64_t mx = 0;
 #pragma unroll
@@ -1394,6 +1426,7 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
         mx = a > mx ? a : mx;
       }
     }
+    clk.lap(kPartTransport);
     // quantize16 over the d outputs (kernels.rs:545-553), then gather16 of rec_out.
     int32_t qs = wave_bitlen_max(mx) - 15;
     if (qs < 0) qs = 0;
@@ -1406,29 +1439,32 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
         publish16(S.xbar, 4 * qi[k], a, kProductExp + qs);
       }
     wave_sync();
+    clk.lap(kPartRequantRec);
 #pragma unroll
     for (int k = 0; k < Q; k++)
       if (qv[k])
 #pragma unroll
         for (int c = 0; c < 4; c++) x[k][c] = sat_add32(x[k][c], S.xbar[pw_out[k][c]]);
     wave_sync();
+    clk.lap(kPartResidualRec);
     // ---- feed-forward block: wave 0 takes the even quaternion groups.
     uint32_t pg[4], pu[4];
     pair_mlp_words(M, ly, lane, 0, pg, pu);
     norm_gain<Q>(M, S.seeds, x, qv, g_mlp, gd_mlp, v);
     publish64<Q>(S.xbar, v, qv, qi);
-    pair_sync();  // 3: the normed activations
+    clk.sync(kPartNormMlp, kPartSync3);  // 3: the normed activations
     const uint64_t mbl = pair_mlp(M, S, ly, lane, 0, pg, pu);
     if (lane == 0) S.pair[0] = mbl;
-    pair_sync();  // 4: both waves' MLP outputs and maxima
+    clk.sync(kPartMlp, kPartSync4);  // 4: both waves' MLP outputs and maxima
     pair_requant(M, S, lane, 0);
-    pair_sync();  // 5: the requantized MLP outputs
+    clk.sync(kPartRequantMlp, kPartSync5);  // 5: the requantized MLP outputs
 #pragma unroll
     for (int k = 0; k < Q; k++)
       if (qv[k])
 #pragma unroll
         for (int c = 0; c < 4; c++) x[k][c] = sat_add32(x[k][c], S.xbar[pw_down[k][c]]);
     wave_sync();
+    clk.lap(kPartResidualMlp);
   }
   if (!want_writer) return 0;
   // Final norm, gain and the Q12 query (session.rs:4294-4295, 4364-4366).
@@ -1462,8 +1498,8 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
   // the last one the writer ran on (a sequence settled on a fixed point) takes its result.
   const bool reuse = S.wmeta[1] != 0 && __all(same);
   if (lane == 0) S.wmeta[2] = reuse;
-  pair_sync();  // 6: the query and the reuse flag
-  *chosen = pair_writer<SW, T8>(M, S, 0, lane, kept_out);
+  clk.sync(kPartFinal, kPartSync6);  // 6: the query and the reuse flag
+  *chosen = pair_writer<SW, T8, CLK>(M, S, 0, lane, kept_out, clk);
   if (!reuse) {
 #pragma unroll
     for (int k = 0; k < Q; k++)
@@ -1538,12 +1574,12 @@ __device__ __forceinline__ void window_sum(const DevModel &M, const DevLayer &ly
 // The window's terms over earlier positions (taps 1..W) do not depend on the step's input, so
 // wave 1 sums them for the next step while wave 0 runs the transport, and keeps them in `hist`
 // (L x d i64 per block); the first step of a launch sums its own (`fresh`).
-template <int Q, int SW, bool T8>
+template <int Q, int SW, bool T8, bool CLK>
 __device__ __forceinline__ int step_window(const DevModel &M, const Lds &S, int32_t *ring,
                                            int64_t *hist, uint32_t base, uint32_t lane,
                                            const bool (&qv)[Q], const uint32_t (&qi)[Q],
                                            uint32_t tok, bool want_writer, bool fresh,
-                                           uint32_t *chosen) {
+                                           uint32_t *chosen, PartClock<CLK> &clk) {
   if (tok >= M.vocab) return 1;
   const uint32_t d = M.d, W = M.W;
   const uint32_t next = base + 1 == W ? 0 : base + 1;  // the next step's ring slot
@@ -1579,7 +1615,7 @@ __device__ __forceinline__ int step_window(const DevModel &M, const Lds &S, int3
     // The first MLP group's gather words, for after barrier 3.
     uint32_t pg[4], pu[4];
     pair_mlp_words(M, ly, lane, 1, pg, pu);
-    pair_sync();  // 1: the normed activations
+    clk.sync(kPartLoads, kPartSync1);  // 1: the normed activations
     int4 drive[Q];
 #pragma unroll
     for (int k = 0; k < Q; k++) {
@@ -1601,7 +1637,7 @@ __device__ __forceinline__ int step_window(const DevModel &M, const Lds &S, int3
 #pragma unroll
       for (int c = 0; c < 4; c++) S.gq[ch + c] = gate[c];
     }
-    pair_sync();  // 2: the window sums and the output gates' quaternions
+    clk.sync(kPartTransition, kPartSync2);  // 2: the window sums and the output gates' quaternions
     // The next step's terms over earlier positions: tap 1 on this step's drive, taps 2..W from
     // the ring (slots next - s, none of them the slot just written).
 #pragma unroll
@@ -1615,16 +1651,16 @@ __device__ __forceinline__ int step_window(const DevModel &M, const Lds &S, int3
       hp[0] = make_longlong2(acc[0], acc[1]);
       hp[1] = make_longlong2(acc[2], acc[3]);
     }
-    pair_sync();  // 3: the normed activations
+    clk.sync(kPartTransport, kPartSync3);  // 3: the normed activations
     const uint64_t mbl = pair_mlp(M, S, ly, lane, 1, pg, pu);
     if (lane == 0) S.pair[1] = mbl;
-    pair_sync();  // 4: both waves' MLP outputs and maxima
+    clk.sync(kPartMlp, kPartSync4);  // 4: both waves' MLP outputs and maxima
     pair_requant(M, S, lane, 1);
-    pair_sync();  // 5: the requantized MLP outputs
+    clk.sync(kPartRequantMlp, kPartSync5);  // 5: the requantized MLP outputs
   }
   if (!want_writer) return 0;
-  pair_sync();  // 6: the query and the reuse flag
-  *chosen = pair_writer<SW, T8>(M, S, 1, lane, nullptr);
+  clk.sync(kPartFinal, kPartSync6);  // 6: the query and the reuse flag
+  *chosen = pair_writer<SW, T8, CLK>(M, S, 1, lane, nullptr, clk);
   return 0;
 }
 
@@ -1636,9 +1672,11 @@ enum Phase : int { kPhasePrefill = 0, kPhaseDecode = 1, kPhaseRows = 2 };
 // NW = 1: one wavefront per sequence (step); NW = 2: paired blocks (step_main, step_window).
 // HM: a model with Hamming reads (one wavefront per sequence); T8: a model with an int8 table,
 // whose writer scans its bytes.
-template <int Q, int SW, int PH, int NW, bool HM = false, bool T8 = false>
+// CLK: the part clocks (paired decode only), each sequence's counters to A.out_parts.
+template <int Q, int SW, int PH, int NW, bool HM = false, bool T8 = false, bool CLK = false>
 __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
   static_assert(!HM || NW == 1, "the Hamming reads run on one wavefront per sequence");
+  static_assert(!CLK || NW == 2, "the part clocks time paired blocks");
   extern __shared__ __align__(16) int32_t lds[];
   Lds S;
   {
@@ -1673,6 +1711,7 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
       S.rng = (uint32_t *)(lds + at);
       at += 2 * kMaxProbes;
       S.pair = (uint64_t *)(lds + at);
+      at += 8;
     }
     S.tok = nullptr;
     S.hdist = nullptr;
@@ -1692,6 +1731,11 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
       at += kHamBins;
       S.hnib = (uint32_t *)(lds + at);
     }
+    S.clk = nullptr;
+    if (CLK) {  // clock_lds_bytes
+      S.clk = (uint64_t *)(lds + at);
+      at += 4 * kParts;
+    }
     const uint32_t *rs = rsqrt_seed_table(), *rc = recip_seed_table();
     for (uint32_t i = threadIdx.x; i < kRsqrtSeedWords; i += NW * kWave) seed_lds[i] = rs[i];
     for (uint32_t i = threadIdx.x; i < kRecipSeedWords; i += NW * kWave) seed_lds[kRsqrtSeedWords + i] = rc[i];
@@ -1706,6 +1750,8 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
   // Paired blocks: wave 0 keeps the recurrence state, wave 1 the window ring.
   const bool keeps_state = NW == 1 || wave == 0, keeps_ring = NW == 1 || wave == 1;
   const bool writes_out = wave == 0 && lane == 0;
+  PartClock<CLK> clk;
+  if constexpr (CLK) clk.acc = S.clk + wave * kParts;
   // The recurrence wave is the step's critical path (its instructions issue one after another,
   // each waiting for the last), while the ring wave's window sums have slack: the recurrence
   // wave takes the issue slots first wherever waves on its SIMD compete for them.
@@ -1801,10 +1847,16 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
                 dst[1] = src[1];
               }
     }
+    uint64_t t_real = 0;
+    if constexpr (CLK) {
+      for (uint32_t i = lane; i < kParts; i += kWave) clk.acc[i] = 0;
+      t_real = __builtin_amdgcn_s_memrealtime();
+    }
     if (NW == 2)
       pair_sync();
     else
       wave_sync();
+    clk.start();
     int status = bad_stream ? 1 : 0;
     uint32_t chosen = 0;
     constexpr bool decode = PH != kPhaseRows;
@@ -1853,10 +1905,11 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
           asm volatile("" : "+v"(qs[k]));
         }
         if (wave == 0)
-          status = step_main<Q, SW, T8>(M, S, ln, qv, qs, tok, want, &chosen, kept_out, query_out);
+          status = step_main<Q, SW, T8, CLK>(M, S, ln, qv, qs, tok, want, &chosen, kept_out,
+                                             query_out, clk);
         else
-          status = step_window<Q, SW, T8>(M, S, ring, hist, base, ln, qv, qs, tok, want,
-                                      t == 0 && fresh, &chosen);
+          status = step_window<Q, SW, T8, CLK>(M, S, ring, hist, base, ln, qv, qs, tok, want,
+                                               t == 0 && fresh, &chosen, clk);
       }
       if (status) break;
       done++;
@@ -1869,6 +1922,17 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
           if (A.out_tokens) A.out_tokens[at] = chosen;
           if (!seq && t + 1 < A.len && chosen == toks[t + 1]) hits++;
         }
+      }
+      clk.lap(kPartStep);
+    }
+    if constexpr (CLK) {
+      const uint64_t real = __builtin_amdgcn_s_memrealtime() - t_real;
+      pair_sync();  // both waves' counters
+      uint64_t *o = A.out_parts + (uint64_t)s * kPartWords;
+      for (uint32_t i = threadIdx.x; i < 2 * kParts; i += 2 * kWave) o[i] = S.clk[i];
+      if (writes_out) {
+        o[2 * kParts] = done;
+        o[2 * kParts + 1] = real;
       }
     }
     if (!decode && A.mode == kModeScore && writes_out && hits) atomicAdd(A.matches, hits);
@@ -1995,6 +2059,27 @@ inline hipError_t launch_shape(const KernelSet &k, const DevModel &M, const RunA
     static const KernelSet k = {NAME##_pair<1, 1>, NAME##_pair<1, 2>, NAME##_pair<1, 4>,      \
                                 NAME##_pair<1, 8>, NAME##_pair<2, 16>, NAME##_pair<4, 32>};    \
     return launch_shape(k, M, A, grid, 2, lds, stream);                                       \
+  }
+// FBS_PAIR_CLK_KERNELS: `NAME_pair_clk<Q, SW>` and `NAME_pair8_clk<Q, SW>`, the paired kernels
+// with the part clocks; `launch_NAME_pair_clk(M, A, grid, lds, stream)` picks by the table.
+#define FBS_PAIR_CLK_KERNELS(NAME, PH)                                                       \
+  template <int Q, int SW>                                                                    \
+  __global__ __launch_bounds__(128, 2) void NAME##_pair_clk(DevModel M, RunArgs A) {          \
+    run<Q, SW, PH, 2, false, false, true>(M, A);                                              \
+  }                                                                                           \
+  template <int Q, int SW>                                                                    \
+  __global__ __launch_bounds__(128, 2) void NAME##_pair8_clk(DevModel M, RunArgs A) {         \
+    run<Q, SW, PH, 2, false, true, true>(M, A);                                               \
+  }                                                                                           \
+  hipError_t launch_##NAME##_pair_clk(const DevModel &M, const RunArgs &A, uint32_t grid,     \
+                                      size_t lds, hipStream_t stream) {                       \
+    static const KernelSet k16 = {NAME##_pair_clk<1, 1>, NAME##_pair_clk<1, 2>,               \
+                                  NAME##_pair_clk<1, 4>, NAME##_pair_clk<1, 8>,               \
+                                  NAME##_pair_clk<2, 16>, NAME##_pair_clk<4, 32>};            \
+    static const KernelSet k8 = {NAME##_pair8_clk<1, 1>, NAME##_pair8_clk<1, 2>,              \
+                                 NAME##_pair8_clk<1, 4>, NAME##_pair8_clk<1, 8>,              \
+                                 NAME##_pair8_clk<2, 16>, NAME##_pair8_clk<4, 32>};           \
+    return launch_shape(M.table8 ? k8 : k16, M, A, grid, 2, lds, stream);                     \
   }
 #define FBS_HAM_KERNELS(NAME, PH)                                                            \
   template <int Q, int SW>                                                                    \

@@ -35,7 +35,8 @@ SYMBOLS = (
     "uor_fbs_index_probe_async", "uor_fbs_index_full_scan_async", "uor_fbs_stream_words",
     "uor_fbs_payload_words", "uor_fbs_decode_stream", "uor_fbs_decode_stream_async",
     "uor_fbs_slot_cache_bytes", "uor_fbs_serve_slots_async", "uor_fbs_trace_stride",
-    "uor_fbs_trace_sequences", "uor_fbs_trace_sequences_async",
+    "uor_fbs_trace_sequences", "uor_fbs_trace_sequences_async", "uor_fbs_part_count",
+    "uor_fbs_part_name", "uor_fbs_decode_parts_async",
 )
 
 
@@ -72,6 +73,10 @@ def lib():
         L.uor_fbs_decode_async.argtypes = [P, P, C.c_uint32, C.c_uint32, C.c_uint32, P, P, P, P, P,
                                            P, P, P, P]
         L.uor_fbs_decode_noalloc_async.argtypes = L.uor_fbs_decode_async.argtypes
+        L.uor_fbs_part_count.restype = C.c_uint32
+        L.uor_fbs_part_name.argtypes = [C.c_uint32]
+        L.uor_fbs_part_name.restype = C.c_char_p
+        L.uor_fbs_decode_parts_async.argtypes = L.uor_fbs_decode_async.argtypes[:-1] + [P, P]
         L.uor_fbs_stream_words.argtypes = [P]
         L.uor_fbs_stream_words.restype = C.c_uint64
         L.uor_fbs_payload_words.argtypes = [P]
@@ -112,6 +117,12 @@ def _vp(a):
 def _check(code: int):
     if code:
         raise FbsError(code, lib().uor_fbs_last_error().decode())
+
+
+def part_names() -> list[str]:
+    """The part clocks' phases in their order (uor_fbs_part_name)."""
+    L = lib()
+    return [L.uor_fbs_part_name(i).decode() for i in range(int(L.uor_fbs_part_count()))]
 
 
 class Model:
@@ -177,6 +188,43 @@ class Model:
                                     _vp(in_state), _vp(in_history), _vp(in_position), _vp(state),
                                     _vp(hist), _vp(pos)))
         return dict(reply=reply, state=state, history=hist, position=pos)
+
+    def decode_parts(self, prompts, gen: int, in_state=None, in_history=None, in_position=None):
+        """decode() on the part clocks' kernels (uor_fbs_decode_parts_async, device buffers):
+        dict(reply, state, history, position, parts [S, 2, part_count()] cycles of each wave in
+        each part over the sequence's steps, steps [S], ticks [S] of the 100 MHz clock)."""
+        from .hipmem import DeviceArray, runtime
+        prompts = np.ascontiguousarray(prompts, dtype=np.uint32)
+        S, plen = prompts.shape
+        npart = int(lib().uor_fbs_part_count())
+
+        def dev(a, t):
+            if a is None:
+                return None
+            d = DeviceArray(np.shape(a), t, self.device)
+            d.upload(np.ascontiguousarray(a, t))
+            return d
+
+        d_prompts = dev(prompts, np.uint32)
+        d_in = [dev(in_state, np.int64), dev(in_history, np.int32), dev(in_position, np.uint32)]
+        reply = DeviceArray((S, gen + 1), np.uint32, self.device)
+        state = DeviceArray((S, self.state_words), np.int64, self.device)
+        hist = DeviceArray((S, self.history_words), np.int32, self.device)
+        pos = DeviceArray(S, np.uint32, self.device)
+        status = DeviceArray(S, np.int32, self.device)
+        parts = DeviceArray((S, 2 * npart + 2), np.uint64, self.device)
+        ptr = lambda d: None if d is None else d.ptr  # noqa: E731
+        _check(lib().uor_fbs_decode_parts_async(
+            self.handle, d_prompts.ptr, S, plen, gen, reply.ptr, *[ptr(d) for d in d_in],
+            state.ptr, hist.ptr, pos.ptr, status.ptr, parts.ptr, None))
+        runtime().hipDeviceSynchronize()
+        st = status.download()
+        if st.any():
+            raise FbsError(int(st[st != 0][0]), "a sequence failed in the part clocks' decode")
+        raw = parts.download()
+        return dict(reply=reply.download(), state=state.download(), history=hist.download(),
+                    position=pos.download(), parts=raw[:, :2 * npart].reshape(S, 2, npart),
+                    steps=raw[:, 2 * npart], ticks=raw[:, 2 * npart + 1])
 
     @property
     def stream_words(self) -> int:
