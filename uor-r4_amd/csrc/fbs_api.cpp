@@ -503,6 +503,7 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
   M.xbar_words = 2 * (d > mlp ? d : mlp);
   M.identity_rows = r.head == 1;
   M.taps_fast = 1;
+  M.gains_fast = 1;
   M.log2d = (d & (d - 1)) == 0 ? (uint32_t)__builtin_ctz(d) : 0xffu;
   // UOR_FBS_WRITER_MEMORY=0 turns the writer's memory of its last query off (for measurement:
   // every step then scans its candidates; the results are the same either way).
@@ -537,6 +538,7 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
       for (uint32_t i = 0; i < d; i++) {
         rg[i] = grid_desc(ly.rec_gain[i]);
         mg[i] = grid_desc(ly.mlp_gain[i]);
+        if (rg[i] == kGridDescSlow || mg[i] == kGridDescSlow) M.gains_fast = 0;
       }
       if ((st = h->upload(td.data(), td.size(), &dl.taps_desc))) return done(st);
       if ((st = h->upload(rg.data(), rg.size(), &dl.rec_gain_desc))) return done(st);
@@ -575,7 +577,10 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
   if ((st = h->upload(m->final_gain, d, &M.final_gain))) return done(st);
   {
     std::vector<uint16_t> fg(d);
-    for (uint32_t i = 0; i < d; i++) fg[i] = grid_desc(m->final_gain[i]);
+    for (uint32_t i = 0; i < d; i++) {
+      fg[i] = grid_desc(m->final_gain[i]);
+      if (fg[i] == kGridDescSlow) M.gains_fast = 0;
+    }
     if ((st = h->upload(fg.data(), fg.size(), &M.final_gain_desc))) return done(st);
   }
 

@@ -86,6 +86,7 @@ struct DevModel {
   uint32_t xbar_words;      // 2 * max(d, m)
   uint32_t identity_rows;   // the nearest head: one drawer holding every token
   uint32_t taps_fast;       // every window tap has a descriptor (tap_desc != kGridDescSlow)
+  uint32_t gains_fast;      // every norm gain (rec, mlp, final) has a descriptor (grid_desc)
   uint32_t log2d;           // log2(d) when d is a power of two, else 0xff
   uint32_t writer_memory;   // 1: a query equal to the writer's last one takes its result
   uint64_t w_recip;         // floor(2^32 / W): the ring slot of a position without division

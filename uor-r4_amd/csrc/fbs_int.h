@@ -547,6 +547,13 @@ FBS_HD int64_t norm_apply(NormFactor f, int64_t y) {
 // huge one): with P = r |y| = A + B 2^32 (A = r_lo |y|, B = r_hi |y|), floor((P + h) / 2^38) =
 // floor((B + floor((A + h) / 2^32)) / 2^6); h = 2^37 for y >= 0, 2^37 - 1 for the negated form
 // (floor((-P + 2^37) / 2^38) = -floor((P + 2^37 - 1) / 2^38)).
+FBS_HD int64_t norm_apply24_fast(NormFactor f, int64_t y) {
+  const uint32_t u = (uint32_t)(y < 0 ? -y : y);
+  const uint64_t A = (uint64_t)(uint32_t)f.r * u, B = (f.r >> 32) * (uint64_t)u;
+  const uint64_t h = y < 0 ? (1ull << 37) - 1 : (1ull << 37);
+  const int64_t mag = (int64_t)((B + ((A + h) >> 32)) >> 6);
+  return y < 0 ? -mag : mag;
+}
 FBS_HD int64_t norm_apply24(NormFactor f, int64_t y) {
   if (f.huge) return norm_apply(f, y);
   const uint32_t u = (uint32_t)(y < 0 ? -y : y);
@@ -614,7 +621,7 @@ FBS_HD void hamilton64(const int64_t a[4], const int64_t b[4], i128 o[4]) {
 // + L with H signed and L read as signed (L - 2^32 [L >= 2^31]); the borrow goes into the high
 // sum. With |a| summing to at most 2^31 + 4 (every unit or snapped quaternion times lambda
 // <= 2^31) neither 64-bit sum can overflow, so the result equals hamilton64's.
-FBS_HD void hamilton32(const int32_t a[4], const int64_t b[4], i128 o[4]) {
+FBS_HD void hamilton32_hl(const int32_t a[4], const int64_t b[4], int64_t Ho[4], int64_t Lo[4]) {
   int32_t hi[4], lo[4], bor[4];
 #pragma unroll
   for (int j = 0; j < 4; j++) {
@@ -641,8 +648,41 @@ FBS_HD void hamilton32(const int32_t a[4], const int64_t b[4], i128 o[4]) {
         L -= pl;
       }
     }
-    o[k] = ((i128)H << 32) + (i128)L;
+    Ho[k] = H;
+    Lo[k] = L;
   }
+}
+FBS_HD void hamilton32(const int32_t a[4], const int64_t b[4], i128 o[4]) {
+  int64_t H[4], L[4];
+  hamilton32_hl(a, b, H, L);
+#pragma unroll
+  for (int k = 0; k < 4; k++) o[k] = ((i128)H[k] << 32) + (i128)L[k];
+}
+
+// shift_wide(H 2^32 + L, 14) (the raw output gate's product, session.rs:4951-4968) for |H| < 2^44:
+// H 2^18 + floor((L + 2^13) / 2^14). |L| <= (2^31 + 4) 2^31 (hamilton32's bound), so nothing
+// wraps, and the sum stays below 2^63 in magnitude: shift_wide's clamp never acts.
+FBS_HD int64_t gate_shift14_fast(int64_t H, int64_t L) {
+  return H * (1ll << 18) + ((L + (1ll << 13)) >> 14);
+}
+
+// The transport (session.rs:5097-5145): shift_wide(H 2^32 + L + keep wide 2^16, 31) for
+// |H| < 2^59, keep <= 2^31 and -2^45 <= wide < 2^45. With wide = wh 2^32 + wl (wl < 2^32) and
+// K = keep wl < 2^63 = (K >> 15) 2^15 + (K mod 2^15), the sum is 2^31 (2 H + keep wh 2^17 + (K >> 15))
+// + Z with Z = L + (K mod 2^15) 2^16, so the shift is that bracket plus floor((Z + 2^30) / 2^31).
+// The terms are below 2^60, 2^61, 2^48 and 2^32 in magnitude: nothing wraps and the clamp never
+// acts.
+FBS_HD int64_t transport_fast(int64_t H, int64_t L, uint64_t keep, int64_t wide) {
+  const int64_t wh = wide >> 32;
+  const uint64_t K = keep * (uint64_t)(uint32_t)wide;
+  const int64_t Z = L + (int64_t)((K & 0x7fffu) << 16);
+  return 2 * H + (int64_t)keep * wh * (1ll << 17) + (int64_t)(K >> 15) + ((Z + (1ll << 30)) >> 31);
+}
+// The fast forms' ranges.
+FBS_HD bool gate_fast_ok(int64_t H) { return (uint64_t)(H + (1ll << 44)) < (1ull << 45); }
+FBS_HD bool transport_fast_ok(int64_t H, int64_t wide, uint64_t keep) {
+  return (uint64_t)(H + (1ll << 59)) < (1ull << 60) && (uint64_t)(wide + (1ll << 45)) < (1ull << 46) &&
+         keep <= (1ull << 31);
 }
 
 // a (x) b for 32-bit operands: each partial product fits in i64 and, with |a| summing to at

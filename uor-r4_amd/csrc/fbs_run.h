@@ -152,6 +152,38 @@ __device__ __forceinline__ uint32_t mod_window(const DevModel &M, uint32_t x) {
 // ---------------------------------------------------------------------------------------------
 // Step pieces.
 
+// Out of line: the step's rare forms (wide sums, slow grid codes, widths that are not powers of
+// two), so that the served loop's hot code stays compact in the instruction cache.
+__device__ __noinline__ NormFactor norm_factor_slow(uint64_t sum, uint32_t n, int64_t eps) {
+  return norm_factor(sum, n, eps);
+}
+// norm_factor_pow2 as one shared copy for the kernel's norms: the seed tables lie at the start
+// of the block's LDS (run()).
+__device__ __noinline__ NormFactor norm_factor_lds(uint64_t sum, uint32_t log2n, int64_t eps) {
+  extern __shared__ __align__(16) int32_t lds[];
+  const uint32_t *seeds = (const uint32_t *)lds;
+  return norm_factor_pow2(sum, log2n, eps, Seeds(seeds, seeds + kRsqrtSeedWords));
+}
+__device__ __noinline__ int64_t norm_gain_slow(uint64_t r, uint32_t huge, int64_t y, uint32_t desc,
+                                               int32_t code) {
+  NormFactor f;
+  f.r = r;
+  f.huge = huge != 0;
+  return grid_apply64_desc(norm_apply24(f, y), (uint16_t)desc, (int16_t)code);
+}
+// shift_wide(mh 2^32 + ml + (keep wide) << 16, 31) (raw: the split form of hamilton32_hl) or of
+// (mh 2^64 + ml) + (keep wide) << 16 (a snapped transition's i128).
+__device__ __noinline__ int64_t transport_wide(int64_t mh, int64_t ml, uint64_t keep, int64_t wide,
+                                               uint32_t raw) {
+  const i128 moved = raw ? ((i128)mh << 32) + (i128)ml
+                         : (i128)(((u128)(uint64_t)mh << 64) | (u128)(uint64_t)ml);
+  const u128 drive_term = (u128)((i128)keep * (i128)wide) << 16;
+  return shift_wide((i128)((u128)moved + drive_term), 31);
+}
+__device__ __noinline__ int64_t gate_wide14(int64_t gh, int64_t gl) {
+  return shift_wide(((i128)gh << 32) + (i128)gl, 14);
+}
+
 // Fine RMSNorm then the per-channel grid gain, for the lane's channels
 // (RS stack/kernels.rs:569-620, session.rs:4057-4061). gain: the lane's 4 codes per quaternion.
 template <int Q>
@@ -182,14 +214,26 @@ __device__ __forceinline__ void norm_gain(const DevModel &M, const Seeds &sd,
       sum += (uint64_t)a * a;
     }
   sum = wave_reduce64(sum, OpAdd());
-  const NormFactor f = M.log2d != 0xffu ? norm_factor_pow2(sum, M.log2d, M.eps_int[sh], sd)
-                                         : norm_factor(sum, M.d, M.eps_int[sh]);
+  (void)sd;
+  const NormFactor f = M.log2d != 0xffu ? norm_factor_lds(sum, M.log2d, M.eps_int[sh])
+                                         : norm_factor_slow(sum, M.d, M.eps_int[sh]);
+  if (!f.huge && M.gains_fast) {
+    // The common case, one uniform branch: r < 2^62 and |y| <= 2^24 keep every normed value
+    // below 2^48 in magnitude, where each gain's descriptor form is exact.
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      const uint16_t gd[4] = {gdesc[k].x, gdesc[k].y, gdesc[k].z, gdesc[k].w};
+#pragma unroll
+      for (int c = 0; c < 4; c++) out[k][c] = grid_desc_apply(norm_apply24_fast(f, out[k][c]), gd[c]);
+    }
+    return;
+  }
 #pragma unroll
   for (int k = 0; k < Q; k++) {
     const int16_t gc[4] = {gain[k].x, gain[k].y, gain[k].z, gain[k].w};
     const uint16_t gd[4] = {gdesc[k].x, gdesc[k].y, gdesc[k].z, gdesc[k].w};
 #pragma unroll
-    for (int c = 0; c < 4; c++) out[k][c] = grid_apply64_desc(norm_apply24(f, out[k][c]), gd[c], gc[c]);
+    for (int c = 0; c < 4; c++) out[k][c] = norm_gain_slow(f.r, f.huge, out[k][c], gd[c], gc[c]);
   }
 }
 
@@ -239,6 +283,37 @@ __device__ __noinline__ Quat64 snap_rotation_dev(const int8_t *ico, int4 raw, ui
   q.root = snap_rotation(ico, r, lambda, q.v);
   return q;
 }
+// The snapped gates' and transitions' 128-bit Hamilton products, out of line (snapped artifacts
+// only): shift_wide(q (x) r, sh) by value, or the product's high and low 64 bits.
+__device__ __noinline__ Quat64 hamilton64_shift(int64_t q0, int64_t q1, int64_t q2, int64_t q3,
+                                                int64_t r0, int64_t r1, int64_t r2, int64_t r3,
+                                                uint32_t sh) {
+  const int64_t q[4] = {q0, q1, q2, q3}, r[4] = {r0, r1, r2, r3};
+  i128 prod[4];
+  hamilton64(q, r, prod);
+  Quat64 o;
+#pragma unroll
+  for (int c = 0; c < 4; c++) o.v[c] = shift_wide(prod[c], sh);
+  o.root = 0;
+  return o;
+}
+struct Wide4 {
+  int64_t hi[4], lo[4];
+};
+__device__ __noinline__ Wide4 hamilton64_wide(int64_t q0, int64_t q1, int64_t q2, int64_t q3,
+                                              int64_t r0, int64_t r1, int64_t r2, int64_t r3) {
+  const int64_t q[4] = {q0, q1, q2, q3}, r[4] = {r0, r1, r2, r3};
+  i128 prod[4];
+  hamilton64(q, r, prod);
+  Wide4 o;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    o.hi[c] = (int64_t)(prod[c] >> 64);
+    o.lo[c] = (int64_t)(uint64_t)prod[c];
+  }
+  return o;
+}
+
 // The snap trace's byte of a site (fbs_core.h:488-501, claude-134): the chosen root, or 255 where
 // none was chosen (served unsnapped) or the raw quaternion is zero.
 constexpr uint32_t kTraceNone = 255;
@@ -272,9 +347,9 @@ __device__ __forceinline__ uint32_t gate_apply(const DevModel &M, const Seeds &s
   int64_t q[4];
   const uint32_t root =
       snap_rotation_to(M.icosian, make_int4(raw[0], raw[1], raw[2], raw[3]), 1ull << 31, q);
-  hamilton64(q, rhs, prod);
+  const Quat64 p = hamilton64_shift(q[0], q[1], q[2], q[3], rhs[0], rhs[1], rhs[2], rhs[3], 15);
 #pragma unroll
-  for (int c = 0; c < 4; c++) out[c] = shift_wide(prod[c], 15);
+  for (int c = 0; c < 4; c++) out[c] = p.v[c];
   return trace_root(raw, root);
 }
 
@@ -318,9 +393,9 @@ __device__ __forceinline__ void gate_mul(const DevModel &M, const int64_t (&g)[4
 #pragma unroll
     for (int c = 0; c < 4; c++) out[c] = shift_wide(prod[c], 14);
   } else {
-    hamilton64(g, rhs, prod);
+    const Quat64 p = hamilton64_shift(g[0], g[1], g[2], g[3], rhs[0], rhs[1], rhs[2], rhs[3], 15);
 #pragma unroll
-    for (int c = 0; c < 4; c++) out[c] = shift_wide(prod[c], 15);
+    for (int c = 0; c < 4; c++) out[c] = p.v[c];
   }
 }
 
@@ -1364,11 +1439,18 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
     }
     // Lane weights (session.rs:4989-5026), the transition's rotation (session.rs:5097-5145)
     // and its product with the state, which do not wait for the window.
+    // T (x) h: a raw transition's as mh 2^32 + ml (hamilton32_hl), a snapped one's i128 as its
+    // high and low 64 bits.
     uint64_t keep[Q];
-    i128 moved[Q][4];
+    int64_t mh[Q][4], ml[Q][4];
 #pragma unroll
     for (int k = 0; k < Q; k++) {
-      if (!qv[k]) continue;
+      if (!qv[k]) {
+        keep[k] = 0;
+#pragma unroll
+        for (int c = 0; c < 4; c++) mh[k][c] = ml[k][c] = 0;
+        continue;
+      }
       int32_t sq = sat_add32(dec[k], doff[k]);
       sq = sq < 0 ? 0 : sq > 65536 ? 65536 : sq;
       uint32_t idx = (uint32_t)sq >> 12;
@@ -1381,50 +1463,98 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
         unit_q30(rot[k], kRotationEps, u, S.seeds);
 #pragma unroll
         for (int c = 0; c < 4; c++) T[c] = u[c] >> idx;  // (lambda u) >> 30, lambda = 2^(30-idx)
-        hamilton32(T, h, moved[k]);
+        hamilton32_hl(T, h, mh[k], ml[k]);
       } else {
         int64_t T64[4];
         snap_rotation_to(M.icosian, make_int4(rot[k][0], rot[k][1], rot[k][2], rot[k][3]),
                           1ull << (30 - idx), T64);
-        hamilton64(T64, h, moved[k]);
+        const Wide4 mv = hamilton64_wide(T64[0], T64[1], T64[2], T64[3], h[0], h[1], h[2], h[3]);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          mh[k][c] = mv.hi[c];
+          ml[k][c] = mv.lo[c];
+        }
       }
     }
     clk.sync(kPartTransition, kPartSync2);  // 2: the window sums and the output gates' quaternions
+    // Transport: h <- shift_wide(T (x) h + (keep wide) << 16, 31). A raw transition whose sums
+    // lie in transport_fast's ranges on every lane takes its 64-bit form (one uniform branch).
+    int64_t h[Q][4];
+    {
+      bool fast = M.raw_transition != 0;
+      int64_t wide[Q][4];
+#pragma unroll
+      for (int k = 0; k < Q; k++) {
+        const uint32_t ch = 4 * (qv[k] ? qi[k] : 0);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          wide[k][c] = S.wide[ch + c];
+          fast = fast && (!qv[k] || transport_fast_ok(mh[k][c], wide[k][c], keep[k]));
+        }
+      }
+      if (__all(fast)) {
+#pragma unroll
+        for (int k = 0; k < Q; k++)
+#pragma unroll
+          for (int c = 0; c < 4; c++) h[k][c] = transport_fast(mh[k][c], ml[k][c], keep[k], wide[k][c]);
+      } else {
+#pragma unroll
+        for (int k = 0; k < Q; k++)
+#pragma unroll
+          for (int c = 0; c < 4; c++)
+            h[k][c] = transport_wide(mh[k][c], ml[k][c], keep[k], wide[k][c], M.raw_transition);
+      }
+    }
+    // Output gate on the moved state (session.rs:4951-4968): a raw gate's product in its 64-bit
+    // form where every lane's sums allow it (gate_shift14_fast).
     int64_t sc[Q][4];
     uint64_t mx = 0;
+    {
+      int64_t gh[Q][4], gl[Q][4];
+      bool fast = M.raw_gates != 0;
 #pragma unroll
-    for (int k = 0; k < Q; k++) {
-      if (!qv[k]) {
+      for (int k = 0; k < Q; k++) {
+        const uint32_t ch = 4 * (qv[k] ? qi[k] : 0);
+        if (qv[k]) {
+          int64_t *hp = S.st + (uint64_t)l * d + ch;
 #pragma unroll
-        for (int c = 0; c < 4; c++) sc[k][c] = 0;
-        continue;
+          for (int c = 0; c < 4; c++) hp[c] = h[k][c];
+        }
+        int64_t rhs[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) rhs[c] = shift(h[k][c], kResidualExp - kStateExp);
+        if (M.raw_gates) {
+          const int32_t u[4] = {(int32_t)S.gq[ch], (int32_t)S.gq[ch + 1], (int32_t)S.gq[ch + 2],
+                                (int32_t)S.gq[ch + 3]};
+          hamilton32_hl(u, rhs, gh[k], gl[k]);
+#pragma unroll
+          for (int c = 0; c < 4; c++) fast = fast && (!qv[k] || gate_fast_ok(gh[k][c]));
+        } else {
+          const int64_t g[4] = {S.gq[ch], S.gq[ch + 1], S.gq[ch + 2], S.gq[ch + 3]};
+          gate_mul(M, g, rhs, sc[k]);
+        }
       }
-      const uint32_t ch = 4 * qi[k];
-      // Transport: h <- shift_wide(T (x) h + (keep wide) << 16, 31).
-      int64_t *hp = S.st + (uint64_t)l * d + ch;
-      int64_t h[4], wide[4], gate[4];
+      if (M.raw_gates) {
+        if (__all(fast)) {
 #pragma unroll
-      for (int c = 0; c < 4; c++) {
-        wide[c] = S.wide[ch + c];
-        gate[c] = S.gq[ch + c];
+          for (int k = 0; k < Q; k++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) sc[k][c] = gate_shift14_fast(gh[k][c], gl[k][c]);
+        } else {
+#pragma unroll
+          for (int k = 0; k < Q; k++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) sc[k][c] = gate_wide14(gh[k][c], gl[k][c]);
+        }
       }
 #pragma unroll
-      for (int c = 0; c < 4; c++) {
-        u128 drive_term = (u128)((i128)keep[k] * (i128)wide[c]) << 16;
-        h[c] = shift_wide((i128)((u128)moved[k][c] + drive_term), 31);
-        hp[c] = h[c];
-      }
-      // Output gate on the moved state (session.rs:4951-4968).
-      int64_t rhs[4], o[4];
+      for (int k = 0; k < Q; k++)
 #pragma unroll
-      for (int c = 0; c < 4; c++) rhs[c] = shift(h[c], kResidualExp - kStateExp);
-      gate_mul(M, gate, rhs, o);
-#pragma unroll
-      for (int c = 0; c < 4; c++) {
-        sc[k][c] = o[c];
-        uint64_t a = uabs64(o[c]);
-        mx = a > mx ? a : mx;
-      }
+        for (int c = 0; c < 4; c++) {
+          if (!qv[k]) sc[k][c] = 0;
+          const uint64_t a = uabs64(sc[k][c]);
+          mx = a > mx ? a : mx;
+        }
     }
     clk.lap(kPartTransport);
     // quantize16 over the d outputs (kernels.rs:545-553), then gather16 of rec_out.
@@ -1681,6 +1811,9 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
   Lds S;
   {
     uint32_t at = 0;  // words; every region starts 16-byte aligned
+    // The seed tables first: norm_factor_lds reads them at offset 0.
+    uint32_t *seed_lds = (uint32_t *)(lds + at);
+    at += kRsqrtSeedWords + kRecipSeedWords;
     S.xbar = lds + at;
     at += M.xbar_words;
     S.mlp_out = (int64_t *)(lds + at);
@@ -1696,8 +1829,6 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
     S.wmeta = (uint32_t *)(lds + at);
     at += 4;
     if (threadIdx.x == 0) S.wmeta[1] = 0;  // no query remembered yet
-    uint32_t *seed_lds = (uint32_t *)(lds + at);
-    at += kRsqrtSeedWords + kRecipSeedWords;
     S.st = (int64_t *)(lds + at);
     at += 2 * M.L * M.d;
     S.wide = S.gq = nullptr;
