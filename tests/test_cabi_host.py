@@ -418,6 +418,45 @@ def test_copy_library_exports_and_refusals():
     assert b"marker" in L.uor_copy_last_error()
 
 
+def test_norm_factor_wave_equals_the_general_form(hp):
+    # The lane-parallel factor (three windows of 64 candidates, each the last that passes its
+    # exact test; the host runs the 64 tests in turn) against the general 128-bit form: random
+    # and near-square sums, wrapping epsilons, every mean square below 2^20 (quotients up to
+    # 2^62), the edges of the ranges, and the kernels' usual range. None is sent to the fallback.
+    f = hp.fbs_hp_norm_factor_wave_check
+    f.argtypes = [P, P, C.c_uint64, C.c_uint32, P]
+    f.restype = C.c_uint64
+
+    def check(sums, eps, log2n):
+        refused = np.zeros(1, np.uint64)
+        bad = f(sums.ctypes.data_as(P), eps.ctypes.data_as(P), len(eps), log2n,
+                refused.ctypes.data_as(P))
+        assert (bad, int(refused[0])) == (0, 0)
+
+    rng = np.random.default_rng(99)
+    n = 200000
+    sums = (rng.integers(0, 2**63, n, dtype=np.uint64)
+            >> rng.integers(0, 64, n).astype(np.uint64)).astype(np.uint64)
+    r = rng.integers(1, 2**32, n // 2, dtype=np.uint64)
+    sums[: n // 2] = (r * r + rng.integers(0, 3, n // 2, dtype=np.uint64)) << rng.integers(0, 8, n // 2).astype(np.uint64)
+    eps = rng.choice(np.array([0, 1, 42950, 2**20, 2**40, 2**59, 2**60, 2**62, 2**63 - 1, -5],
+                              dtype=np.int64), n)
+    for log2n in (5, 8, 10):
+        check(sums, eps, log2n)
+    small = np.arange(1, 2**20, dtype=np.int64)
+    check(np.zeros(len(small), np.uint64), small, 5)
+    vals = [1, 2, 3, 15, 16, 17, 2**60 - 1, 2**60 - 2, 2**60 - 17, 2**59, 2**59 - 1, 2**59 + 1]
+    for k in range(1, 31):
+        for v in (k * k, (2**k) ** 2, (2**k - 1) ** 2, 3**k):
+            vals += [v - 1, v, v + 1]
+    for k in range(1, 61):
+        vals += [2**k - 1, 2**k, 2**k + 1]
+    edge = np.array([v for v in vals if 0 < v < 2**63], dtype=np.int64)
+    check(np.zeros(len(edge), np.uint64), edge, 5)
+    usual = rng.integers(2**30, 2**50, 500000, dtype=np.uint64) << np.uint64(8)
+    check(usual, np.full(len(usual), 42950, np.int64), 8)
+
+
 def test_norm_factor_pow2_at_its_edges(hp):
     # The factor's double estimates at the ends of their ranges: mean squares of 1 (s = 2^34,
     # r = 2^62), at the 60-bit mask's top, on and one off perfect squares and powers of two,

@@ -29,6 +29,25 @@ void fbs_hp_div_2p96_many(const uint64_t *s, uint64_t *out, uint64_t n) {
   for (uint64_t i = 0; i < n; i++) out[i] = div_2p96(s[i]);
 }
 
+// norm_factor_wave against norm_factor on n (sum, eps) pairs at 2^log2n: mismatches among the
+// inputs it accepts (ok), and in *refused the inputs it sends to the fallback.
+uint64_t fbs_hp_norm_factor_wave_check(const uint64_t *sum, const int64_t *eps, uint64_t n,
+                                       uint32_t log2n, uint64_t *refused) {
+  uint64_t bad = 0, no = 0;
+  for (uint64_t i = 0; i < n; i++) {
+    NormFactor a = norm_factor(sum[i], 1u << log2n, eps[i]);
+    bool ok;
+    NormFactor b = norm_factor_wave(sum[i], log2n, eps[i], Seeds(), ok);
+    if (!ok) {
+      no++;
+      continue;
+    }
+    if (a.huge != b.huge || (!a.huge && a.r != b.r)) bad++;
+  }
+  *refused = no;
+  return bad;
+}
+
 // norm_factor_pow2 against norm_factor on n (sum, eps) pairs at 2^log2n: mismatches.
 uint64_t fbs_hp_norm_factor_check(const uint64_t *sum, const int64_t *eps, uint64_t n, uint32_t log2n) {
   uint64_t bad = 0;

@@ -532,6 +532,94 @@ FBS_HD NormFactor norm_factor_pow2(uint64_t sum, uint32_t log2n, int64_t eps_int
   return out;
 }
 
+// The largest k in [0, 64) with ok(k), for an ok that holds up to some k and fails after it, or
+// -1 when ok(0) fails. In device code every lane of the wave (all 64 active) tests its own k and
+// one ballot gives the answer; on the host the same 64 tests run in turn.
+template <class F>
+FBS_HD int last_ok64(F ok) {
+#ifdef __HIP_DEVICE_COMPILE__
+  const uint64_t m = (uint64_t)__ballot(ok((int)(threadIdx.x & 63u)));
+  return m ? 63 - __builtin_clzll(m) : -1;
+#else
+  int k = -1;
+  for (int i = 0; i < 64; i++)
+    if (ok(i)) k = i;
+  return k;
+#endif
+}
+
+// norm_factor_pow2 with its corrections made in parallel: each exact quantity (the root t, its
+// extension f, the quotient r) is estimated to within 32 and then found as the last of 64
+// consecutive candidates that passes its exact test, one candidate per lane of the wave.
+// The estimates come from one reciprocal square root y ~ 2^46 / sqrt(mt) (mt the top 32 bits of
+// the normalised mean square, relative error below 2^-28.9):
+//   t  = isqrt(mn):                       t0 = mt y / 2^30, within 12 of t;
+//   f  = floor(2^J (sqrt(mn) - t)):        f0 = rem 2^(J-1) y / 2^62, within 12 of f;
+//   r  = floor(2^96 / s), s = t 2^J + f:  r0 = y 2^(34-J) refined by one Newton step on the exact
+//                                          2^96 - r0 s, within 32 of r wherever r < 2^61.
+// `ok` is false where a candidate window does not hold its answer strictly inside (an input
+// beyond the estimates' ranges); the caller then takes norm_factor_pow2.
+FBS_HD NormFactor norm_factor_wave(uint64_t sum, uint32_t log2n, int64_t eps_int, const Seeds &sd,
+                                   bool &ok) {
+  NormFactor out;
+  ok = true;
+  int64_t ms = wadd64((int64_t)(sum >> log2n), eps_int);
+  if (ms < 1) ms = 1;
+  const uint64_t m = (uint64_t)ms & ((1ull << 60) - 1);
+  if (m == 0) {  // isqrt(0) = 0, raised to 1: r = 2^96
+    out.r = 0;
+    out.huge = true;
+    return out;
+  }
+  out.huge = false;
+  const uint64_t M = m << 4;
+  const int z = clz64(M) & ~1;
+  const uint64_t mn = M << z;                         // [2^62, 2^64)
+  const int J = 32 - (z >> 1);                        // [3, 32]
+  const uint32_t mt = (uint32_t)(mn >> 32);
+  const uint32_t y = rsqrt_q46(mt, sd.rsq_seed);
+  // t: candidates tb + k, tested t^2 <= mn (t < 2^32, so t^2 < 2^64).
+  const uint64_t tb = (((uint64_t)mt * y) >> 30) - 32;
+  // (The tests combine their conditions without branching: every lane evaluates all of them.)
+  const int kt = last_ok64([&](int k) {
+    const uint64_t c = tb + (uint64_t)k;
+    return (c <= 0xffffffffull) & (c * c <= mn);
+  });
+  const uint64_t t = tb + (uint64_t)(kt < 0 ? 0 : kt);
+  const uint64_t rem = mn - t * t;                    // [0, 2 t]
+  const uint64_t num = rem << (J - 1);                // rem 2^(J-1) < 2^64
+  // f: candidates fb + k below 2^J, tested f (2^(J+1) t + f) <= rem 4^J, that is
+  // f^2 <= 2^(J+1) (num - f t).
+  const uint64_t f0 = (((num >> 32) * y) + ((((uint64_t)(uint32_t)num) * y) >> 32)) >> 30;
+  const uint64_t fb = f0 > 32 ? f0 - 32 : 0;
+  const uint64_t flim = 1ull << J;
+  const int kf = last_ok64([&](int k) {
+    const uint64_t c = fb + (uint64_t)k;
+    const uint64_t ct = c * t;                        // c < 2^32 where it counts, t < 2^32
+    const uint64_t rho = num - ct;
+    // 2^(J+1) rho >= 2^64 > c^2 where rho >> (63 - J) is not zero.
+    return (c < flim) & (ct <= num) & (((rho >> (63 - J)) != 0) | (c * c <= (rho << (J + 1))));
+  });
+  const uint64_t f = fb + (uint64_t)(kf < 0 ? 0 : kf);
+  const uint64_t sv = (t << J) + f;                   // [2^34, 2^64)
+  // r: candidates rb + k, tested r s <= 2^96.
+  const uint64_t r0 = (uint64_t)y << (34 - J);
+  const u128 p0 = (u128)r0 * sv;
+  const i128 e = (i128)(((u128)1 << 96) - p0);        // |e| < 2^69
+  const i128 corr = ((e >> 32) * (i128)r0) >> 64;
+  const int64_t r1 = (int64_t)((i128)r0 + corr);
+  const uint64_t rb = (uint64_t)(r1 - 32);
+  const int kr = last_ok64([&](int k) {
+    const uint64_t c = rb + (uint64_t)k;
+    return (u128)c * sv <= ((u128)1 << 96);
+  });
+  out.r = rb + (uint64_t)(kr < 0 ? 0 : kr);
+  // Each answer must lie strictly inside its window (or at the end of f's range).
+  ok = kt > 0 && kt < 63 && (kf > 0 || fb == 0) && (kf < 63 || fb + 63 >= flim - 1) && kr > 0 &&
+       kr < 63 && r1 > 32;
+  return out;
+}
+
 // One normalised value: round(r y / 2^38) with the sign of y, clamped to i64.
 FBS_HD int64_t norm_apply(NormFactor f, int64_t y) {
   uint64_t u = uabs64(y);

@@ -157,12 +157,18 @@ __device__ __forceinline__ uint32_t mod_window(const DevModel &M, uint32_t x) {
 __device__ __noinline__ NormFactor norm_factor_slow(uint64_t sum, uint32_t n, int64_t eps) {
   return norm_factor(sum, n, eps);
 }
-// norm_factor_pow2 as one shared copy for the kernel's norms: the seed tables lie at the start
-// of the block's LDS (run()).
-__device__ __noinline__ NormFactor norm_factor_lds(uint64_t sum, uint32_t log2n, int64_t eps) {
-  extern __shared__ __align__(16) int32_t lds[];
-  const uint32_t *seeds = (const uint32_t *)lds;
-  return norm_factor_pow2(sum, log2n, eps, Seeds(seeds, seeds + kRsqrtSeedWords));
+// The power-of-two widths' RMSNorm factor as one shared copy for the kernel's norms: the
+// lane-parallel form (norm_factor_wave, every lane of the wave active), or norm_factor_pow2 for
+// an input outside its estimates' ranges. `seed_lds`: the block's seed tables in LDS.
+typedef __attribute__((address_space(3))) const uint32_t lds_u32;
+__device__ __noinline__ NormFactor norm_factor_lds(uint64_t sum, uint32_t log2n, int64_t eps,
+                                                   lds_u32 *seed_lds) {
+  const uint32_t *seeds = (const uint32_t *)seed_lds;
+  const Seeds sd(seeds, seeds + kRsqrtSeedWords);
+  bool ok;
+  NormFactor f = norm_factor_wave(sum, log2n, eps, sd, ok);
+  if (!ok) f = norm_factor_pow2(sum, log2n, eps, sd);
+  return f;
 }
 __device__ __noinline__ int64_t norm_gain_slow(uint64_t r, uint32_t huge, int64_t y, uint32_t desc,
                                                int32_t code) {
@@ -215,7 +221,8 @@ __device__ __forceinline__ void norm_gain(const DevModel &M, const Seeds &sd,
     }
   sum = wave_reduce64(sum, OpAdd());
   (void)sd;
-  const NormFactor f = M.log2d != 0xffu ? norm_factor_lds(sum, M.log2d, M.eps_int[sh])
+  const NormFactor f = M.log2d != 0xffu ? norm_factor_lds(sum, M.log2d, M.eps_int[sh],
+                                                          (lds_u32 *)sd.rsq_seed)
                                          : norm_factor_slow(sum, M.d, M.eps_int[sh]);
   if (!f.huge && M.gains_fast) {
     // The common case, one uniform branch: r < 2^62 and |y| <= 2^24 keep every normed value
@@ -1811,7 +1818,7 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
   Lds S;
   {
     uint32_t at = 0;  // words; every region starts 16-byte aligned
-    // The seed tables first: norm_factor_lds reads them at offset 0.
+    // The seed tables (rsqrt, then reciprocal) at the start.
     uint32_t *seed_lds = (uint32_t *)(lds + at);
     at += kRsqrtSeedWords + kRecipSeedWords;
     S.xbar = lds + at;
