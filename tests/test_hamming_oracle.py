@@ -11,7 +11,15 @@ without retyping them:
 - the ask heads and their carry against an f64 reference, as
   an_asking_read_brings_back_the_kept_tokens_points (tests.rs:8380-8470), within 0.6 of a step;
 - zero weights reduce the model to the read-free one, and a decode split and resumed through the
-  session stream equals the decode in one call.
+  session stream equals the decode in one call;
+- the type and ask heads' integers exactly, on cases whose answers the quaternion units' table
+  and the definitions fix: payloads under the units 1, -1, i, j, k equal the point permuted and
+  negated, and under the half unit each signed sum halved with odd negative sums rounded away
+  from zero; one head keeping one position moves the stream by its weight times the payload; a
+  head's halving by its count and the heads' halving by their number truncate toward zero (sums
+  built to land half a step from a rounding boundary of the hook's output); an ask head brings
+  back the kept position's own token's row, raised 4 bits. Each of these fails on the oracle
+  with a planted mistake (payload rounding half up, either halving floored).
 """
 
 from dataclasses import replace
@@ -339,3 +347,231 @@ def test_the_context_slide_continues_as_an_unbounded_context():
     assert oracle.decode(small, prompts, 40)["status"] == 2
     ham = make(BASE, 63, heads=4, depths=(1,), kept=4)
     assert oracle.decode(ham, prompts, 4, slide=True)["status"] == 4
+
+
+# ---- exact cases of the type and ask heads (hamming.rs:1204-1334) ---------------------------
+#
+# Rotations whose unit quaternions are exact at Q31 (stack_rotation of (c, 0, 0, 0) is the
+# identity 2^31, of (0, c, 0, 0) the unit i, of (c, c, c, c) 2^30 on every coordinate), key and
+# query rotations that leave a point's sign code as the signs of its coordinates, and table rows
+# whose codes sit at chosen distances: every quantity below follows from the quaternion units'
+# multiplication table and the definitions of the weight, the means and the rounding.
+
+ONE = 1 << 24  # a raw rotation coordinate of 1.0 at 2^-24
+HW = BASE.width // 4  # coordinates a head covers (4 heads)
+
+
+def exact_read(seed, kept, margins, value_raw=(ONE, 0, 0, 0), asks=None):
+    art = make(BASE, seed, heads=4, depths=(1,), kept=kept, asks=asks)
+    read = art.hamming_reads[0]
+    d = BASE.width
+    ident = np.tile(np.array([ONE, 0, 0, 0], np.int32), d // 4)
+    read.key_rotation[:] = ident
+    read.query_rotation[:] = ident
+    read.value_rotation[:] = np.tile(np.asarray(value_raw, np.int32), d // 4)
+    read.weight[:d] = 0          # no copy term: the hook moves by the type (or ask) mean alone
+    read.weight[d:] = ONE
+    read.margin[:] = margins
+    if read.ask is not None:
+        read.ask[:] = 0
+    return art, read
+
+
+def weight_q31(margin, dist):
+    """copy_weight_q31 (hamming.rs:243-251) by its definition."""
+    over = margin - (dist << 16)
+    return 0 if over <= 0 else (over << 31) // max(margin, 1 << 16)
+
+
+def half_away(n, shift):
+    """round_shift (hamming.rs:1354-1361): n / 2^shift rounded half away from zero."""
+    q = (abs(n) + (1 << (shift - 1))) >> shift
+    return q if n >= 0 else -q
+
+
+def trunc_div(a, b):
+    q = abs(a) // abs(b)
+    return q if (a >= 0) == (b > 0) else -q
+
+
+def set_row(art, token, signs):
+    """Table row of `token`: magnitude 1000 with the given signs (64 of them)."""
+    table = art.writer_table.reshape(BASE.vocab, BASE.width)
+    table[token] = np.where(np.asarray(signs) >= 0, 1000, -1000).astype(table.dtype)
+
+
+def head_signs(pattern2, pattern3):
+    """Signs for a row or point: copy heads' coordinates positive, type heads' as given."""
+    s = np.ones(BASE.width, np.int64)
+    s[2 * HW:3 * HW] = pattern2
+    s[3 * HW:] = pattern3
+    return s
+
+
+PERMUTED = {
+    # u (x) (a, b, c, d) for the units 1, -1, i, j, k (the Hamilton product's table)
+    "identity": ((ONE, 0, 0, 0), lambda a, b, c, d: (a, b, c, d)),
+    "minus": ((-ONE, 0, 0, 0), lambda a, b, c, d: (-a, -b, -c, -d)),
+    "i": ((0, ONE, 0, 0), lambda a, b, c, d: (-b, a, -d, c)),
+    "j": ((0, 0, ONE, 0), lambda a, b, c, d: (-c, d, a, -b)),
+    "k": ((0, 0, 0, ONE), lambda a, b, c, d: (-d, -c, b, a)),
+}
+
+
+@pytest.mark.parametrize("name", sorted(PERMUTED) + ["half"])
+def test_type_payloads_under_exact_rotations(name):
+    # TypeHeads::payload (hamming.rs:1204-1218): round_shift(u (x) p, 31). Under 1, -1, i, j, k
+    # the payload is the point permuted and negated exactly; under the half unit (2^30 on each
+    # coordinate) it is each signed sum of the four coordinates halved, an odd one rounded away
+    # from zero (a negative odd sum fixes the direction against rounding half up).
+    raw = (ONE, ONE, ONE, ONE) if name == "half" else PERMUTED[name][0]
+    art, read = exact_read(7, 4, [1 << 16] * 4, value_raw=raw)
+    rng = np.random.default_rng(11)
+    rows = 24
+    tokens = rng.integers(0, 12, rows).astype(np.uint32)
+    points = rng.integers(-(1 << 20), 1 << 20, (rows, BASE.width)).astype(np.int32)
+    pay = None
+    odd_negative = 0
+    for t in range(rows):
+        _, pay = oracle.hamming_row(art, 1, tokens[: t + 1], x=points[t], payloads=pay)
+        p = points[t].astype(np.int64).reshape(-1, 4)
+        if name == "half":
+            a, b, c, d = p.T
+            sums = [a - b - c - d, a + b - c + d, a + b + c - d, a - b + c + d]
+            want = np.stack([[half_away(int(v) << 30, 31) for v in s] for s in sums], 1)
+            odd_negative += sum(int(((s < 0) & (s % 2 != 0)).sum()) for s in sums)
+        else:
+            want = np.stack(PERMUTED[name][1](*p.T), 1)
+        assert np.array_equal(pay[0, t].reshape(-1, 4), want), (name, t)
+    if name == "half":
+        assert odd_negative > 100
+
+
+def run_exact(art, read, tokens, point):
+    """The hook's output at the last row of `tokens` for the stream input `point`, with every
+    earlier row's payload formed by the oracle at its own row (points: the rows' inputs)."""
+    pay = None
+    for t in range(len(tokens)):
+        got, pay = oracle.hamming_row(art, 1, tokens[: t + 1], x=point[t], payloads=pay)
+    return got
+
+
+def test_one_type_head_keeping_one_position_moves_by_its_weighted_payload():
+    # One type head finds one position (kept 1) at distance 1 inside a margin with a fraction,
+    # the other finds none (distance 8 against a margin of 2 bits): the mean is w v exactly, and
+    # the stream moves by it through stream_sum (pinned by the reference's literal answers).
+    A, B = 3, 4
+    m2 = (3 << 16) + 12345
+    art, read = exact_read(8, 1, [1 << 16, 1 << 16, m2, 2 << 16])
+    one_off = np.ones(HW, np.int64)
+    one_off[5] = -1
+    set_row(art, A, head_signs(one_off, np.ones(HW)))      # head 2 code: one bit off all-ones
+    set_row(art, B, head_signs(-np.ones(HW), -np.ones(HW)))
+    tokens = np.array([A, B, B, B, A, B], np.uint32)       # position 1's key is A's row
+    rng = np.random.default_rng(12)
+    pts = rng.integers(-(1 << 20), 1 << 20, (len(tokens), BASE.width)).astype(np.int64)
+    mixed = np.array([1, -1] * (HW // 2))
+    last = head_signs(np.ones(HW), mixed) * np.abs(pts[-1]) + head_signs(np.ones(HW), mixed)
+    pts[-1] = last
+    got = run_exact(art, read, tokens, pts.astype(np.int32))
+    # positions 1..4: keys A, B, B, B -> distances 1, 16, 16, 16 for head 2; the query of head 3
+    # (alternating signs) is 8 from both A's and B's codes.
+    w = weight_q31(m2, 1)
+    assert 0 < w < 1 << 31
+    y = [w * int(v) for v in pts[1]]                        # payload of position 1 = its point
+    want = [oracle.stream_sum(int(last[k]), 0, 0, ONE, y[k]) for k in range(BASE.width)]
+    assert list(map(int, got)) == want
+
+
+def half_step_pair(w2, k=3):
+    """Payload values v1, v2 with 2^31 v1 + w2 v2 = -(2 k + 1) 2^31 + 1 (w2 odd): the sum is odd
+    and negative, and half of it lies a half step inside -(k + 1/2) 2^31, so the two ways of
+    rounding the halving (toward zero, or down) move the hook's Q16 output differently."""
+    m = 1 << 31
+    v2 = pow(w2, -1, m)                       # w2 v2 = 1 + j 2^31
+    j = (w2 * v2 - 1) >> 31
+    v1 = -(2 * k + 1) - j
+    assert 2**31 * v1 + w2 * v2 == -(2 * k + 1) * 2**31 + 1 and abs(v1) < 2**31 and v2 < 2**31
+    return v1, v2
+
+
+def odd_weight_margin(dist):
+    for m in range((4 << 16) + 1, (5 << 16)):
+        if weight_q31(m, dist) % 2 == 1:
+            return m
+    raise AssertionError
+
+
+@pytest.mark.parametrize("split", ["within_a_head", "across_heads"])
+def test_type_means_truncate_toward_zero(split):
+    # TypeHeads::mean_by (hamming.rs:1282-1334) halves twice: a head's sum by its count of kept
+    # positions, and the heads' total by the heads that found one, both truncating toward zero.
+    # Either the head with two kept positions (distances 0 and 1) or two heads each keeping one
+    # carry the sum 2^31 v1 + w v2 = -(2 k + 1) 2^31 + 1 on coordinate 0, whose half rounds to
+    # the hook's output one way if truncated and another if floored.
+    A, C2, B = 3, 5, 4
+    m = odd_weight_margin(1)
+    w0, w1 = weight_q31(m, 0), weight_q31(m, 1)
+    assert w0 == 1 << 31 and w1 % 2 == 1
+    mixed = np.array([1, -1] * (HW // 2))
+    off1 = np.ones(HW, np.int64)
+    off1[2] = -1
+    if split == "within_a_head":
+        kept, margins = 2, [1 << 16, 1 << 16, m, 2 << 16]   # head 3 finds nothing
+        row_a = head_signs(np.ones(HW), np.ones(HW))         # head 2: distance 0
+        row_c = head_signs(off1, np.ones(HW))                # head 2: distance 1
+        last = head_signs(np.ones(HW), mixed)
+    else:
+        kept, margins = 1, [1 << 16, 1 << 16, m, m]
+        row_a = head_signs(np.ones(HW), -np.ones(HW))        # head 2: 0, head 3: 16 (far)
+        row_c = head_signs(-np.ones(HW), off1)               # head 2: 16, head 3: 1
+        last = head_signs(np.ones(HW), np.ones(HW))
+    art, read = exact_read(9, kept, margins)
+    set_row(art, A, row_a)
+    set_row(art, C2, row_c)
+    set_row(art, B, head_signs(-np.ones(HW), -np.ones(HW)))  # 8 or 16 from every query
+    tokens = np.array([A, C2, B, B, B, B, A], np.uint32)   # keys of positions 1, 2: A, C2
+    rng = np.random.default_rng(13)
+    pts = rng.integers(-(1 << 20), 1 << 20, (len(tokens), BASE.width)).astype(np.int64)
+    v1, v2 = half_step_pair(w1)
+    pts[1][0], pts[2][0] = v1, v2
+    pts[-1] = last * (np.abs(pts[-1]) + 1)
+    pts[-1][0] = -5          # a negative sum: its rounding goes away from zero (down)
+    got = run_exact(art, read, tokens, pts.astype(np.int32))
+    total = [w0 * int(pts[1][k]) + w1 * int(pts[2][k]) for k in range(BASE.width)]
+    # One head with two positions: total / 2, then / 1; two heads with one position each:
+    # (v / 1 + v' / 1) / 2. Either way the halving of the total.
+    y = [trunc_div(v, 2) for v in total]
+    want = [oracle.stream_sum(int(pts[-1][k]), 0, 0, ONE, y[k]) for k in range(BASE.width)]
+    floored = oracle.stream_sum(int(pts[-1][0]), 0, 0, ONE, total[0] // 2)
+    assert floored != want[0]                               # the case tells the two apart
+    assert list(map(int, got)) == want
+
+
+def test_an_ask_head_brings_back_the_kept_token_point_exactly():
+    # An asking read (hamming.rs:1149-1181, mean_by over Brought::Points): the question is the
+    # code of (table + a)[x_t] (a = 0, no carry) through the key rotation; one ask head keeps
+    # the position whose key (the row before it) is one bit off, and brings back the table row
+    # of that position's own token times the weight; the stream raises it by 4 bits to the type
+    # term's exponent (hamming.rs:1849-1855).
+    A, B, P = 3, 4, 6
+    m2 = (3 << 16) + 4321
+    art, read = exact_read(10, 1, [1 << 16, 1 << 16, m2, 2 << 16], asks=(True,))
+    assert read.ask is not None
+    one_off = np.ones(HW, np.int64)
+    one_off[7] = -1
+    mixed = np.array([1, -1] * (HW // 2))
+    set_row(art, A, head_signs(one_off, np.ones(HW)))
+    set_row(art, B, head_signs(-np.ones(HW), -np.ones(HW)))
+    set_row(art, P, head_signs(np.ones(HW), mixed))       # the asking token: head 2 all ones
+    table = art.writer_table.reshape(BASE.vocab, BASE.width)
+    rng = np.random.default_rng(14)
+    table[B] = (table[B] * rng.integers(1, 30, BASE.width)).astype(table.dtype)  # varied values
+    tokens = np.array([A, B, B, B, P], np.uint32)          # position 1 (key A) holds token B
+    x = rng.integers(-(1 << 20), 1 << 20, BASE.width).astype(np.int32)
+    got, pay = oracle.hamming_row(art, 1, tokens, x=x)
+    assert pay.size == 0
+    w = weight_q31(m2, 1)
+    y = [(w * int(v)) << 4 for v in table[B]]
+    want = [oracle.stream_sum(int(x[k]), 0, 0, ONE, y[k]) for k in range(BASE.width)]
+    assert list(map(int, got)) == want
