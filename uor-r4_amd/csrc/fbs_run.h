@@ -1413,13 +1413,24 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
     int4 rbias[Q];
     int32_t dbias[Q], doff[Q];
     uint32_t pw_rot[Q][4], pw_dec[Q], pw_out[Q][4], pw_down[Q][4];
+    // The feed-forward block's gains and gather words: loaded here for one quaternion a lane,
+    // where registers allow their latency to hide behind the recurrence block, and at the
+    // feed-forward block for more (their registers would spill to scratch across the block).
+    auto load_ffn = [&]() {
+#pragma unroll
+      for (int k = 0; k < Q; k++) {
+        const uint32_t ch = 4 * (qv[k] ? qi[k] : 0);
+        g_mlp[k] = *(const short4 *)(ly.mlp_gain + ch);
+        gd_mlp[k] = *(const ushort4 *)(ly.mlp_gain_desc + ch);
+#pragma unroll
+        for (int c = 0; c < 4; c++) pw_down[k][c] = prog_word(ly.prog, M.s_mlp_down + 4 * k + c, lane);
+      }
+    };
 #pragma unroll
     for (int k = 0; k < Q; k++) {
       const uint32_t qq = qv[k] ? qi[k] : 0, ch = 4 * qq;
       g_rec[k] = *(const short4 *)(ly.rec_gain + ch);
-      g_mlp[k] = *(const short4 *)(ly.mlp_gain + ch);
       gd_rec[k] = *(const ushort4 *)(ly.rec_gain_desc + ch);
-      gd_mlp[k] = *(const ushort4 *)(ly.mlp_gain_desc + ch);
       rbias[k] = *(const int4 *)(ly.gate_bias + nq + ch);
       dbias[k] = ly.gate_bias[qq];
       doff[k] = ly.decay_offset[qq];
@@ -1427,10 +1438,10 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
       for (int c = 0; c < 4; c++) {
         pw_rot[k][c] = prog_word(ly.prog, M.s_rec_gate + Q + 4 * k + c, lane);
         pw_out[k][c] = prog_word(ly.prog, M.s_rec_out + 4 * k + c, lane);
-        pw_down[k][c] = prog_word(ly.prog, M.s_mlp_down + 4 * k + c, lane);
       }
       pw_dec[k] = prog_word(ly.prog, M.s_rec_gate + k, lane);
     }
+    if constexpr (Q == 1) load_ffn();
     clk.lap(kPartLoads);
     int64_t v[Q][4];
     norm_gain<Q>(M, S.seeds, x, qv, g_rec, gd_rec, v);
@@ -1585,6 +1596,7 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
     wave_sync();
     clk.lap(kPartResidualRec);
     // ---- feed-forward block: wave 0 takes the even quaternion groups.
+    if constexpr (Q != 1) load_ffn();
     uint32_t pg[4], pu[4];
     pair_mlp_words(M, ly, lane, 0, pg, pu);
     norm_gain<Q>(M, S.seeds, x, qv, g_mlp, gd_mlp, v);
@@ -1673,8 +1685,8 @@ __device__ __forceinline__ void tap4(const DevModel &M, const DevLayer &ly, uint
 // a time.
 __device__ __forceinline__ void window_sum(const DevModel &M, const DevLayer &ly,
                                            const int32_t *ring_l, uint32_t base, uint32_t s1,
-                                           uint32_t ch, int64_t (&acc)[4]) {
-  const uint32_t d = M.d, W = M.W;
+                                           uint32_t ch, int64_t (&acc)[4], uint32_t s2 = 0) {
+  const uint32_t d = M.d, W = s2 ? s2 : M.W;  // taps s1..W (the last tap s2 when given)
   if (M.taps_fast) {
     for (uint32_t s0 = s1; s0 <= W; s0 += kWindowChunk) {
       int4 hb[kWindowChunk];
@@ -1683,7 +1695,7 @@ __device__ __forceinline__ void window_sum(const DevModel &M, const DevLayer &ly
       for (uint32_t i = 0; i < kWindowChunk; i++) {
         const uint32_t s = s0 + i;
         if (s <= W) {
-          const uint32_t sl = base >= s ? base - s : base + W - s;
+          const uint32_t sl = base >= s ? base - s : base + M.W - s;
           hb[i] = *(const int4 *)(ring_l + (uint64_t)sl * d + ch);
           tb[i] = *(const uint2 *)(ly.taps_desc + (uint64_t)s * d + ch);
         }
@@ -1700,7 +1712,7 @@ __device__ __forceinline__ void window_sum(const DevModel &M, const DevLayer &ly
   } else {
     // A tap outside the descriptor form somewhere in the model: the reference routine.
     for (uint32_t s = s1; s <= W; s++) {
-      const uint32_t sl = base >= s ? base - s : base + W - s;
+      const uint32_t sl = base >= s ? base - s : base + M.W - s;
       tap4(M, ly, s, ch, *(const int4 *)(ring_l + (uint64_t)sl * d + ch), acc);
     }
   }
@@ -1720,13 +1732,19 @@ __device__ __forceinline__ int step_window(const DevModel &M, const Lds &S, int3
   if (tok >= M.vocab) return 1;
   const uint32_t d = M.d, W = M.W;
   const uint32_t next = base + 1 == W ? 0 : base + 1;  // the next step's ring slot
+  // Windows of more than 16 rows: the next step's taps 2..split (about a quarter) are summed
+  // before barrier 1, where this wave waits for the norm, and taps split+1..W after barrier 2
+  // (none of their ring rows is the one this step writes); shorter windows sum every tap after
+  // barrier 2. (C5, W = 32: taps 2..8 first; a half first, or 3/8, measured slower.)
+  const uint32_t split = W > 16 ? 1 + (W - 1) / 4 : 1;
   for (uint32_t l = 0; l < M.L; l++) {
     const DevLayer ly = M.layers[l];
     int32_t *ring_l = ring + (uint64_t)l * W * d;
     int64_t *hist_l = hist + (uint64_t)l * d;
     int4 cbias[Q];
     uint32_t pw_drive[Q][4], pw_gate[Q][4];
-    int64_t sum[Q][4];  // taps 1..W over the earlier positions
+    int64_t sum[Q][4];   // taps 1..W over the earlier positions
+    int64_t part[Q][4];  // the next step's taps 2..split
 #pragma unroll
     for (int k = 0; k < Q; k++) {
       const uint32_t ch = 4 * (qv[k] ? qi[k] : 0);
@@ -1748,6 +1766,12 @@ __device__ __forceinline__ int step_window(const DevModel &M, const Lds &S, int3
         sum[k][2] = b.x;
         sum[k][3] = b.y;
       }
+    }
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+#pragma unroll
+      for (int c = 0; c < 4; c++) part[k][c] = 0;
+      if (qv[k]) window_sum(M, ly, ring_l, next, 2, 4 * qi[k], part[k], split);
     }
     // The first MLP group's gather words, for after barrier 3.
     uint32_t pg[4], pu[4];
@@ -1775,15 +1799,16 @@ __device__ __forceinline__ int step_window(const DevModel &M, const Lds &S, int3
       for (int c = 0; c < 4; c++) S.gq[ch + c] = gate[c];
     }
     clk.sync(kPartTransition, kPartSync2);  // 2: the window sums and the output gates' quaternions
-    // The next step's terms over earlier positions: tap 1 on this step's drive, taps 2..W from
-    // the ring (slots next - s, none of them the slot just written).
+    // The next step's terms over earlier positions: tap 1 on this step's drive, taps
+    // split+1..W from the ring (slots next - s, none of them the slot just written), added to
+    // taps 2..split.
 #pragma unroll
     for (int k = 0; k < Q; k++) {
       if (!qv[k]) continue;
       const uint32_t ch = 4 * qi[k];
-      int64_t acc[4] = {0, 0, 0, 0};
+      int64_t acc[4] = {part[k][0], part[k][1], part[k][2], part[k][3]};
       tap4(M, ly, 1, ch, drive[k], acc);
-      window_sum(M, ly, ring_l, next, 2, ch, acc);
+      if (split < W) window_sum(M, ly, ring_l, next, split + 1, ch, acc);
       longlong2 *hp = (longlong2 *)(hist_l + ch);
       hp[0] = make_longlong2(acc[0], acc[1]);
       hp[1] = make_longlong2(acc[2], acc[3]);
