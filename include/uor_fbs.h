@@ -319,10 +319,12 @@ int uor_fbs_decode_stream(uor_fbs_handle *handle, const uint32_t *prompts, uint3
  *   before its first use (a zero entry holds nothing). Each slot's entry keeps the window sums
  *   its last launch formed for the slot's next step, tagged with the position they hold for, so
  *   a launch that starts there does not sum the window again, and the writer's memory of its
- *   last query, which depends on the model alone. A caller that writes a slot's state, history
- *   or position itself (restoring or resetting a session) zeroes the slot's entry first (its
- *   first 4 bytes suffice). An entry belongs to this handle's model. NULL: no cache (as
- *   uor_fbs_decode_slots_async).
+ *   last query, which depends on the model alone. The sums are also tagged with a fingerprint of
+ *   the slot's state as that launch left it: a launch that finds another state in the slot (a
+ *   caller restored a session there at the same position) sums the window afresh. A caller
+ *   that rewrites a slot's history alone, leaving its state and position, zeroes the slot's entry
+ *   first (its first 4 bytes suffice); zeroing it on every write of a slot is always right. An
+ *   entry belongs to this handle's model. NULL: no cache (as uor_fbs_decode_slots_async).
  * - `slide`: capacity bytes, nonzero for a slot whose session continues past a full context
  *   (IntegerStackSession::set_context_slide, session.rs:2391-2402, :4143-4151: the step does not
  *   refuse at the context, and the position keeps counting; nothing else in the step reads it

@@ -15,7 +15,9 @@ oracle on whole sequences drawn from the same batch.
   choices equal the oracle's on sampled rows.
 - C5 (width 512, int8 codes, window 32, 1,024 drawers probing 16) decode at its per-sequence
   length (4,096 + 4,096) over 2,048 sequences (more than the 1,024 resident blocks, so blocks
-  take a second sequence), with the same properties and two whole sequences against the oracle.
+  take a second sequence), with the same properties and two whole sequences against the oracle;
+  and at BASELINE's batch of 16,384 (16 sequences a block), five whole replies against the
+  oracle.
 - C3 and C5 oracle samples sit on both sides of every block boundary a launch has.
 Every comparison is exact equality.
 """
@@ -86,6 +88,24 @@ def test_c2_decode_full_size():
 def test_c5_decode_full_length():
     _decode_properties("c5", synth.CONFIGS["c5"], 2026120205, batch=2048, prompt=4096, gen=4096,
                        zipf=False, replay=8, picks=[0, 2047])
+
+
+@pytest.mark.timeout(900)
+def test_c5_decode_full_batch():
+    # BASELINE's C5 batch: 16,384 sequences of 4,096 + 4,096 (16 a resident block), replies only;
+    # the oracle on sequences at both ends and on both sides of the first block boundary.
+    spec = replace(synth.CONFIGS["c5"], context=4096 + 4096 + 1)
+    art = synth.make_artifact(spec, 2026120205)
+    batch = 16384
+    prompts = synth.uniform_prompts(spec.vocab, batch, 4096, 2026120206)
+    print(f"c5: batch {batch} prompt 4096 gen 4096", flush=True)
+    full = Model(art).decode(prompts, gen=4096, want_state=False)
+    assert len(np.unique(full["reply"])) > 16
+    pick = np.array([0, 1023, 1024, 8191, 16383], np.int64)
+    print(f"c5: oracle on sequences {list(pick)}", flush=True)
+    want = oracle.decode(art, prompts[pick], 4096, threads=len(pick), want_state=False)
+    assert want["status"] == 0
+    np.testing.assert_array_equal(full["reply"][pick], want["reply"])
 
 
 def test_c4_scoring_rows():

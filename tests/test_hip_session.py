@@ -357,3 +357,55 @@ def test_snap_trace_follows_the_oracle():
     b.reset()
     b.feed(tokens[:5])
     assert b.save_state().snap_trace == want[:5 * per].tolist()
+
+
+def test_a_slot_rewritten_in_place_sums_its_window_afresh(art):
+    """A caller that writes another session's state, history and position into a slot at the
+    position the slot's cache entry was formed for, without clearing the entry (the C ABI does
+    not require it to): the entry's sums were formed beside the slot's old state, whose
+    fingerprint no longer matches, so the launch sums the window afresh and the slot continues as
+    the session it now holds."""
+    cap, P, K = 4, 10, 6
+    A, B = 1, 2
+    model = hip.Model(art)
+    L = hip.lib()
+    pa, pb = (synth.uniform_prompts(SPEC.vocab, 1, P, s) for s in (301, 302))
+    st = DeviceArray((cap, model.state_words), np.int64)
+    hi = DeviceArray((cap, model.history_words), np.int32)
+    po = DeviceArray(cap, np.uint32)
+    ca = DeviceArray((cap, int(L.uor_fbs_slot_cache_bytes(model.handle))), np.uint8)
+    for a in (st, hi, po, ca):
+        a.zero()
+    status = DeviceArray(2, np.int32)
+
+    def serve(slots, toks):
+        d_slots = DeviceArray(len(slots), np.uint32)
+        d_slots.upload(np.asarray(slots, np.uint32))
+        toks = np.ascontiguousarray(toks, np.uint32)
+        d_tok = DeviceArray(toks.size, np.uint32)
+        d_tok.upload(toks.reshape(-1))
+        reply = DeviceArray((len(slots), 1), np.uint32)
+        hip._check(L.uor_fbs_serve_slots_async(
+            model.handle, d_slots.ptr, len(slots), cap, d_tok.ptr, toks.shape[1], 0, reply.ptr,
+            st.ptr, hi.ptr, po.ptr, ca.ptr, None, None, None, None, status.ptr, None))
+        assert (status.download()[: len(slots)] == 0).all()
+        return reply.download()[:, 0]
+
+    first = serve([A, B], np.concatenate([pa, pb]))   # both slots at position P, entries cached
+    rows = [a.download() for a in (st, hi, po)]
+    assert not np.array_equal(rows[1][A], rows[1][B])
+    for a, r in zip((st, hi, po), rows):
+        r[A] = r[B]
+        a.upload(r)
+    want = model.decode(pb, gen=K)["reply"][0]
+    tok_a = tok_b = first[1]
+    got_a, got_b = [first[1]], [first[1]]
+    for _ in range(K):
+        tok_a, tok_b = serve([A, B], np.array([[tok_a], [tok_b]], np.uint32))
+        got_a.append(tok_a)
+        got_b.append(tok_b)
+    np.testing.assert_array_equal(got_b, want)
+    np.testing.assert_array_equal(got_a, want)
+    end = [a.download() for a in (st, hi, po)]
+    for r in end:                                     # the whole session, not only its tokens
+        np.testing.assert_array_equal(r[A], r[B])

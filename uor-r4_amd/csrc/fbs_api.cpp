@@ -170,16 +170,20 @@ std::mutex g_scratch_mu;
 unsigned char *g_scratch_ptr[kScratchDevices];
 bool g_scratch_read[kScratchDevices];
 
-// The scratch array's address on `device`, which must be current; read once per device.
+// The scratch array's address on `device`, which must be current; read once per device (a
+// failed read is not kept, so a later model creation on the device reads it again).
 unsigned char *scratch_address(int device) {
   if (device < 0 || device >= kScratchDevices) return nullptr;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_read[device]) {
     void *p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    g_scratch_ptr[device] = e == hipSuccess ? (unsigned char *)p : nullptr;
-    g_scratch_read[device] = true;
-    if (e != hipSuccess) (void)hipGetLastError();  // the entry point reports it when called
+    if (e == hipSuccess) {
+      g_scratch_ptr[device] = (unsigned char *)p;
+      g_scratch_read[device] = true;
+    } else {
+      (void)hipGetLastError();  // the entry point reports the missing address when called
+    }
   }
   return g_scratch_ptr[device];
 }

@@ -134,8 +134,10 @@ inline size_t ham_lds_bytes(const DevModel &M) {
 
 // One serving slot's cache (uor_fbs_serve_slots_async), bytes from the entry's start: a u32 tag
 // (the position + 1 the window sums hold for; 0: none), a u32 flag (the writer memory below
-// holds a query), the memory's token, then its query (d i32), its kept drawers (kMaxProbes
-// u32) and, for paired blocks, the slot's window sums for its next step (L d i64).
+// holds a query), the memory's token, a u32 fingerprint of the slot's state the sums were formed
+// beside (a launch that finds another state there sums the window afresh), then its query
+// (d i32), its kept drawers (kMaxProbes u32) and, for paired blocks, the slot's window sums for
+// its next step (L d i64).
 struct SlotCacheLayout {
   uint32_t query, kept, sums, bytes;
 };

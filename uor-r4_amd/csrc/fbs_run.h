@@ -149,6 +149,14 @@ __device__ __forceinline__ uint32_t mod_window(const DevModel &M, uint32_t x) {
   return r >= M.W ? r - M.W : r;
 }
 
+// One state word's share of a slot state's fingerprint: the word and its index mixed by
+// multiplication (splitmix64's constants), summed over the state's words modulo 2^32.
+__device__ __forceinline__ uint32_t state_fp_word(int64_t v, uint32_t index) {
+  const uint64_t u = (uint64_t)v ^ ((uint64_t)index * 0x9E3779B97F4A7C15ull);
+  const uint64_t m = (u ^ (u >> 31)) * 0xBF58476D1CE4E5B9ull;
+  return (uint32_t)(m >> 32) ^ (uint32_t)m;
+}
+
 // ---------------------------------------------------------------------------------------------
 // Step pieces.
 
@@ -853,7 +861,8 @@ struct Lds {
   int64_t *st;       // L * d recurrence state
   int32_t *wq;       // d: the query of the writer's last run
   uint32_t *wmeta;   // 4: [0] that run's token, [1] nonzero once wq holds a query,
-                     //    [2] paired blocks: the step reuses that run's result
+                     //    [2] paired blocks: the step reuses that run's result, [3] a serving
+                     //    slot's state fingerprint as loaded
   Seeds seeds;       // the reciprocal and reciprocal square root seed tables
   // Paired blocks only (null otherwise):
   int64_t *wide;     // d: the window sums, wave 1 -> wave 0
@@ -1946,12 +1955,14 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
     // of its last query, which depends on the model alone, so it is taken whenever it holds one.
     uint8_t *const ce = A.cache ? A.cache + (uint64_t)sl * A.cache_stride : nullptr;
     bool fresh = true;
+    uint32_t fp_tag = 0;  // the fingerprint of the state the cached sums were formed beside
     if (ce) {
       const SlotCacheLayout cl = slot_cache_layout(M);
       const uint32_t *head = (const uint32_t *)ce;
       if (NW == 2) {
         hist = (int64_t *)(ce + cl.sums);
         fresh = head[0] != pos + 1;
+        fp_tag = head[3];
       }
       if (wave == 0 && head[1] && M.writer_memory) {
         for (uint32_t i = lane; i < d; i += kWave) S.wq[i] = ((const int32_t *)(ce + cl.query))[i];
@@ -1962,6 +1973,7 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
         }
       }
     }
+    uint32_t fp_acc = 0;
     for (uint32_t l = 0; l < L; l++)
 #pragma unroll
       for (int k = 0; k < Q; k++)
@@ -1969,9 +1981,12 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
           uint32_t ch = 4 * qi[k];
           if (keeps_state)
 #pragma unroll
-            for (int c = 0; c < 4; c++)
-              S.st[(uint64_t)l * d + ch + c] =
-                  A.in_state ? A.in_state[((uint64_t)sl * L + l) * d + ch + c] : 0;
+            for (int c = 0; c < 4; c++) {
+              const uint64_t at = (uint64_t)l * d + ch + c;
+              const int64_t v = A.in_state ? A.in_state[((uint64_t)sl * L + l) * d + ch + c] : 0;
+              S.st[at] = v;
+              if (NW == 2 && ce) fp_acc += state_fp_word(v, (uint32_t)at);
+            }
           if (keeps_ring && !A.slots)
             for (uint32_t r = 0; r < W; r++) {
               uint32_t slot = base + W - 1 - r;  // (base - 1 - r) mod W, from [0, 2 W - 1)
@@ -2010,6 +2025,12 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
                 dst[1] = src[1];
               }
     }
+    // A serving slot's cached sums hold only beside the state they were formed with: a slot
+    // whose state the host rewrote at the same position (a restore) sums its window afresh.
+    if (NW == 2 && ce && wave == 0) {
+      const uint32_t fp = wave_reduce32(fp_acc, OpAdd());
+      if (lane == 0) S.wmeta[3] = fp;
+    }
     uint64_t t_real = 0;
     if constexpr (CLK) {
       for (uint32_t i = lane; i < kParts; i += kWave) clk.acc[i] = 0;
@@ -2020,6 +2041,7 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
     else
       wave_sync();
     clk.start();
+    if (NW == 2 && ce) fresh = fresh || S.wmeta[3] != fp_tag;
     int status = bad_stream ? 1 : 0;
     uint32_t chosen = 0;
     constexpr bool decode = PH != kPhaseRows;
@@ -2134,10 +2156,25 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
       uint32_t *head = (uint32_t *)ce;
       for (uint32_t i = lane; i < d; i += kWave) ((int32_t *)(ce + cl.query))[i] = S.wq[i];
       if (lane < kMaxProbes) ((uint32_t *)(ce + cl.kept))[lane] = S.kept[lane];
+      uint32_t fp = 0;
+      if (NW == 2) {
+        uint32_t acc = 0;
+        for (uint32_t l = 0; l < L; l++)
+#pragma unroll
+          for (int k = 0; k < Q; k++)
+            if (qv[k])
+#pragma unroll
+              for (int c = 0; c < 4; c++) {
+                const uint64_t at = (uint64_t)l * d + 4 * qi[k] + c;
+                acc += state_fp_word(S.st[at], (uint32_t)at);
+              }
+        fp = wave_reduce32(acc, OpAdd());
+      }
       if (lane == 0) {
         head[0] = NW == 2 && (done > 0 || !fresh) ? pos + 1 : 0u;
         head[1] = S.wmeta[1] != 0;
         head[2] = S.wmeta[0];
+        head[3] = fp;
       }
       wave_sync();
     }
