@@ -348,6 +348,27 @@ int uor_fbs_serve_slots_async(uor_fbs_handle *handle, const uint32_t *slots, uin
                               uint32_t *out_kept, int32_t *out_query, uint8_t *out_trace,
                               int32_t *status, void *stream);
 
+/* The serving loop for a model with Hamming reads (lut-stack/6): IntegerStackSession's
+ * serve_step/step_native (session.rs:3356-3440) on sessions whose reads look back over their own
+ * tokens and payloads (session.rs:4149-4152, 4252-4276, 4296-4320). uor_fbs_serve_slots_async's
+ * slots, plus each slot's token stream and payload caches, updated in place:
+ * - `stream`: capacity * uor_fbs_stream_words(handle) u32, the slot's tokens x_0..x_{position-1}
+ *   (entries at and past the position are ignored and rewritten);
+ * - `payloads`: capacity * uor_fbs_payload_words(handle) i64, each typed read's payload of every
+ *   position, [typed read][context][width] (NULL for a model with none).
+ * A fresh slot has position 0 (its stream and payloads are then not read). `cache` as
+ * uor_fbs_serve_slots_async's (the writer's memory; these kernels keep no window sums there).
+ * No context slide (the reference refuses it for Hamming reads) and no snap trace. A model
+ * without Hamming reads is served as by uor_fbs_serve_slots_async (stream and payloads unused).
+ * Device buffers. */
+int uor_fbs_serve_slots_stream_async(uor_fbs_handle *handle, const uint32_t *slots,
+                                     uint32_t sequences, uint32_t capacity,
+                                     const uint32_t *prompts, uint32_t prompt_len, uint32_t gen,
+                                     uint32_t *out_reply, int64_t *state, int32_t *history,
+                                     uint32_t *position, uint32_t *stream, int64_t *payloads,
+                                     void *cache, uint32_t *out_kept, int32_t *out_query,
+                                     int32_t *status, void *hip_stream);
+
 /* Teacher-forced next-token scoring: for each row of `len` tokens, position t's choice is
  * compared with row[t+1] (t < len-1); `out_matches` gets the total count of equal pairs.
  * `out_argmin` (nullable) gets every position's choice, rows*len. Host buffers. */

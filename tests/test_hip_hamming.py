@@ -4,7 +4,9 @@ choices, kept drawers and queries, and a decode split and resumed through the se
 (tokens and payload caches, uor_fbs_decode_stream). Cases cover every kernel width (Q = 1, 2, 4
 quaternions a lane), copy, type and ask heads with the question carry, every copy rule with mixed
 copy keys and the reply marker, and a trained artifact with seeded reads added; then the
-refusals of what this build does not serve.
+refusals of what this build does not serve. Sessions of these models served from pool slots
+(uor_fbs_serve_slots_stream_async: serve_step and snapshots, stack/session.rs:2777-3440) equal
+the oracle's stream decode.
 """
 
 from dataclasses import replace
@@ -14,8 +16,9 @@ import pytest
 
 import oracle
 from test_uorlut import HAM, MANIFEST, fixture
-from uor_fbs import synth, uorlut
+from uor_fbs import session_codec, synth, uorlut
 from uor_fbs.hip import FbsError, Model
+from uor_fbs.session import Session, SessionError, SessionPool, serve_steps
 
 pytestmark = pytest.mark.gpu
 
@@ -143,3 +146,103 @@ def test_a_resumed_token_outside_the_vocabulary_is_refused():
     with pytest.raises(FbsError) as e:
         model.decode_stream(first["reply"][:, -1:], 2, resume=bad)
     assert e.value.code == 1
+
+
+def served_payloads(snap, art):
+    """A snapshot's payload caches as [typed, context, width] (the reads that keep one)."""
+    d, n = art.spec.width, art.spec.context
+    return np.array([np.reshape(p, (n, d)) for p in snap.hamming_payloads if p],
+                    np.int64).reshape(-1, n, d)
+
+
+@pytest.mark.parametrize("name", ["w64_copy_type", "w64_ask_carry", "w256_marker", "w512"])
+def test_a_serving_loop_of_sessions_matches_the_oracle(name):
+    # Sessions in scrambled slots join the loop at different steps; each launch steps whichever
+    # sessions have a token, in a shuffled order. Replies, state, window, token stream and
+    # payload caches must equal the oracle's stream decode of the same prompts.
+    art, prompts, gen = build(name)
+    n = len(prompts)
+    print(f"case {name} serving loop: {n} sessions, gen {gen}", flush=True)
+    model = Model(art)
+    want = oracle.decode_stream(art, prompts, gen, threads=4)
+    assert want["status"] == 0
+    pool = SessionPool(model, capacity=2 * n + 3)
+    pool.acquire(1), pool.acquire(4)
+    sessions = [Session(pool) for _ in range(n)]
+    start = [0, 2, 1, 3][:n]
+    nxt, got = [None] * n, [[] for _ in range(n)]
+    rng = np.random.default_rng(11)
+    for step in range(max(start) + gen + 1):
+        batch, toks = [], []
+        for i in rng.permutation(n):
+            k = step - start[i]
+            if k == 0:
+                half = prompts.shape[1] // 2  # the prompt in two launches
+                sessions[i].feed(prompts[i, :half])
+                nxt[i] = sessions[i].feed(prompts[i, half:]).token
+                got[i].append(nxt[i])
+            elif 0 < k <= gen:
+                batch.append(sessions[i])
+                toks.append(nxt[i])
+        if batch:
+            for s, (tok, _) in zip(batch, serve_steps(batch, toks)):
+                i = sessions.index(s)
+                nxt[i] = tok
+                got[i].append(tok)
+    for i, s in enumerate(sessions):
+        np.testing.assert_array_equal(np.array(got[i], np.uint32), want["reply"][i], err_msg=str(i))
+        snap = s.save_state()
+        pos = int(want["position"][i])
+        assert snap.position == pos
+        np.testing.assert_array_equal(np.concatenate([l.state for l in snap.layers]), want["state"][i])
+        np.testing.assert_array_equal(np.concatenate([l.history for l in snap.layers]),
+                                      want["history"][i])
+        assert snap.tokens == want["tokens"][i, :pos].tolist()
+        pay = served_payloads(snap, art)
+        assert pay.shape[0] == want["payloads"].shape[1]
+        np.testing.assert_array_equal(pay[:, :pos], want["payloads"][i, :, :pos])
+
+
+@pytest.mark.parametrize("name", ["w64_copy_type", "w512"])
+def test_a_restored_session_continues_bit_for_bit(name, tmp_path):
+    # A Hamming session saved mid-stream (tokens and payloads in the snapshot) and restored into
+    # another slot, through the codec, JSON and in place, continues as the original did and as
+    # the oracle's resumed stream decode does.
+    art, prompts, gen = build(name)
+    print(f"case {name} save/restore", flush=True)
+    pool = SessionPool(Model(art), capacity=5)
+    a = Session(pool, 2)
+    tok = a.feed(prompts[0]).token
+    for _ in range(4):
+        tok, _ = a.serve_step(tok)
+    snap = a.save_state()
+    wire = session_codec.encode(snap)
+    path = tmp_path / "h.json"
+    a.save_session_to_file(path)
+    cont, t = [], tok
+    for _ in range(gen - 5):
+        t, _ = a.serve_step(t)
+        cont.append(t)
+    want = oracle.decode_stream(art, prompts[:1], gen, threads=4)
+    np.testing.assert_array_equal(np.array(cont, np.uint32), want["reply"][0, 5:gen])
+    for how in ("codec", "json", "same-slot"):
+        b = a if how == "same-slot" else Session(pool)
+        if how == "codec":
+            b.restore_state(session_codec.decode(wire))
+        elif how == "json":
+            b.restore_session_from_file(path)
+        else:
+            b.restore_state(snap)
+        t, again = tok, []
+        for _ in range(gen - 5):
+            t, _ = b.serve_step(t)
+            again.append(t)
+        assert again == cont, how
+        if b is not a:
+            b.close()
+    # A snapshot without its payloads is refused where the model keeps them.
+    if served_payloads(snap, art).shape[0]:
+        bare = session_codec.decode(wire)
+        bare.hamming_payloads = []
+        with pytest.raises(SessionError):
+            Session(pool).restore_state(bare)

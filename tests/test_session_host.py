@@ -85,6 +85,32 @@ def test_size_bound():
     assert max_serialized_session_bytes(snapped) - max_serialized_session_bytes(INFO) == 16 * 8 * 2 * 24
 
 
+def test_hamming_payload_caches():
+    # One cache per read with payload-bringing type heads (an asking read and a read without
+    # type weights keep none, hamming.rs:1678-1685); a type-head snapshot without them, or with
+    # caches of other lengths, is refused (session.rs:2894-2910); the size bound counts them.
+    spec = dataclasses.replace(synth.SMALL, context=16,
+                               hamming=synth.HammingSpec(heads=2, depths=(1, 2), kept=4,
+                                                         asks=(False, True)))
+    art = synth.make_artifact(spec, 3)
+    info = ModelInfo.of(art)
+    d = spec.width
+    assert info.hamming and info.payload_reads == (True, False) and info.payload_slots == 1
+    assert [len(p) for p in info.payload_caches()] == [16 * d, 0]
+    art.hamming_reads[0].weight[d:] = 0  # no type weights: no cache
+    assert ModelInfo.of(art).payload_reads == (False, False)
+    ok = dataclasses.replace(saved(), artifact_sha256=info.sha256)
+    ok = dataclasses.replace(ok, layers=[RecurrenceLayer([0] * d, [0] * (info.window * d))] * info.layers,
+                             logits=[0] * info.vocab, tokens=[1, 2, 3])
+    validate_restore(info, dataclasses.replace(ok, hamming_payloads=info.payload_caches()))
+    for bad in ([], [[0] * (16 * d)], [[0] * (16 * d - 1), []]):
+        with pytest.raises(SessionError) as e:
+            validate_restore(info, dataclasses.replace(ok, hamming_payloads=bad))
+        assert e.value.kind == "Shape"
+    plain = dataclasses.replace(info, payload_reads=(False, False))
+    assert max_serialized_session_bytes(info) - max_serialized_session_bytes(plain) == 16 * d * 24
+
+
 def test_serving_identity():
     path = os.path.join(GOLDEN, "trained", "content_seed1_s7.uorlut")
     art = uorlut.load(path)

@@ -1088,6 +1088,48 @@ extern "C" int uor_fbs_serve_slots_async(uor_fbs_handle *h, const uint32_t *slot
   return launch(h, A, (hipStream_t)stream, false, out_trace != nullptr);
 }
 
+extern "C" int uor_fbs_serve_slots_stream_async(
+    uor_fbs_handle *h, const uint32_t *slots, uint32_t sequences, uint32_t capacity,
+    const uint32_t *prompts, uint32_t prompt_len, uint32_t gen, uint32_t *out_reply, int64_t *state,
+    int32_t *history, uint32_t *position, uint32_t *stream, int64_t *payloads, void *cache,
+    uint32_t *out_kept, int32_t *out_query, int32_t *status, void *hip_stream) {
+  if (!h || !slots || !prompts || !out_reply || !state || !history || !position || !status)
+    return fail(UOR_FBS_ERR_ARGUMENT, "null argument");
+  if (prompt_len == 0) return fail(UOR_FBS_ERR_ARGUMENT, "a step needs at least one token");
+  if (h->M.ham.heads && !stream)
+    return fail(UOR_FBS_ERR_ARGUMENT, "a Hamming model's slots need their token streams");
+  if (h->M.ham.slots && !payloads)
+    return fail(UOR_FBS_ERR_ARGUMENT, "a Hamming model's typed reads need their payload caches");
+  DeviceScope scope(h->device);
+  RunArgs A{};
+  A.mode = kModeDecode;
+  A.n = sequences;
+  A.len = prompt_len;
+  A.gen = gen;
+  A.tokens = prompts;
+  A.out_tokens = out_reply;
+  A.in_state = state;
+  A.in_history = history;
+  A.in_position = position;
+  A.out_state = state;
+  A.out_history = history;
+  A.out_position = position;
+  A.out_kept = out_kept;
+  A.out_query = out_query;
+  A.slots = slots;
+  A.capacity = capacity;
+  A.status = status;
+  A.cache = (uint8_t *)cache;
+  A.cache_stride = slot_cache_layout(h->M).bytes;
+  if (h->M.ham.heads) {
+    A.in_stream = stream;
+    A.out_stream = stream;
+    A.in_payloads = payloads;
+    A.out_payloads = payloads;
+  }
+  return launch(h, A, (hipStream_t)hip_stream);
+}
+
 extern "C" int uor_fbs_decode(uor_fbs_handle *h, const uint32_t *prompts, uint32_t sequences,
                               uint32_t prompt_len, uint32_t gen, uint32_t *out_reply,
                               const int64_t *in_state, const int32_t *in_history,

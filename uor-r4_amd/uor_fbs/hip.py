@@ -36,7 +36,7 @@ SYMBOLS = (
     "uor_fbs_payload_words", "uor_fbs_decode_stream", "uor_fbs_decode_stream_async",
     "uor_fbs_slot_cache_bytes", "uor_fbs_serve_slots_async", "uor_fbs_trace_stride",
     "uor_fbs_trace_sequences", "uor_fbs_trace_sequences_async", "uor_fbs_part_count",
-    "uor_fbs_part_name", "uor_fbs_decode_parts_async",
+    "uor_fbs_part_name", "uor_fbs_decode_parts_async", "uor_fbs_serve_slots_stream_async",
 )
 
 
@@ -73,6 +73,8 @@ def lib():
         L.uor_fbs_decode_async.argtypes = [P, P, C.c_uint32, C.c_uint32, C.c_uint32, P, P, P, P, P,
                                            P, P, P, P]
         L.uor_fbs_decode_noalloc_async.argtypes = L.uor_fbs_decode_async.argtypes
+        L.uor_fbs_serve_slots_stream_async.argtypes = [P, P, C.c_uint32, C.c_uint32, P, C.c_uint32,
+                                                       C.c_uint32] + [P] * 11
         L.uor_fbs_part_count.restype = C.c_uint32
         L.uor_fbs_part_name.argtypes = [C.c_uint32]
         L.uor_fbs_part_name.restype = C.c_char_p

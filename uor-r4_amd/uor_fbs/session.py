@@ -11,6 +11,10 @@ have a token ready (`serve_steps`) without moving state through the host. `Sessi
 reference's per-call semantics; its snapshots are the reference's `SerializedStackSession`,
 encodable as `UR4SESS1` bytes or the JSON of `save_session_to_file` (`session_codec`).
 
+A model with Hamming reads also keeps each slot's token stream and the typed reads' payloads
+of every position in HBM (`uor_fbs_serve_slots_stream_async`); its snapshots carry them as the
+reference's `tokens` and `hamming_payloads`.
+
 A session's opt-in snap trace (`enable_snap_trace`) records each step's transition roots from
 the launch's trace output. What the GPU path does not keep (and so refuses to restore, rather
 than continuing differently): read-layer caches (the FBS trunk has none).
@@ -119,12 +123,29 @@ class ModelInfo:
     context: int
     heads: int = 1       # every served FBS shape has one head (format.rs:616-752)
     snapped: bool = False
+    hamming: bool = False
+    # Per Hamming read: whether it keeps a payload cache (type heads that bring a payload back,
+    # payload_caches, hamming.rs:1678-1685).
+    payload_reads: tuple = ()
 
     @staticmethod
     def of(art) -> "ModelInfo":
         s = art.spec
+        reads = getattr(art, "hamming_reads", None) or []
+        d = s.width
+        cached = tuple(bool(r.ask is None and np.any(np.asarray(r.weight)[d:] != 0)) for r in reads)
         return ModelInfo(model_identity(art), s.vocab, s.width, s.layers, s.window, s.context,
-                         1, not s.raw_transition)
+                         1, not s.raw_transition, getattr(art, "hamming", None) is not None, cached)
+
+    @property
+    def payload_slots(self) -> int:
+        return sum(self.payload_reads)
+
+    def payload_caches(self) -> list:
+        """A fresh session's hamming_payloads: `context * width` zeros per read that keeps one,
+        an empty list per other read, none without Hamming reads (hamming.rs:1678-1685)."""
+        n = self.context * self.width
+        return [[0] * n if c else [] for c in self.payload_reads]
 
     @property
     def state_words(self) -> int:
@@ -146,12 +167,14 @@ class ModelInfo:
 
 def max_serialized_session_bytes(info: ModelInfo) -> int:
     """The JSON size bound restore_session_from_file enforces (session.rs:2281-2345), for the FBS
-    trunk: every layer a recurrence, no pointer or Hamming payloads; 24 bytes per number."""
+    trunk: every layer a recurrence, no pointer; a Hamming read's payloads `context * width`
+    numbers per read that keeps them; 24 bytes per number."""
     layer_bytes = info.layers * (info.window + 1) * info.width * 24
     logits_bytes = info.vocab * 24
     tokens_bytes = info.context * 24
     trace_bytes = info.context * (info.width // 4) * info.layers * 24 if info.snapped else 0
-    return layer_bytes + logits_bytes + tokens_bytes + trace_bytes + 131072
+    payload_bytes = info.payload_slots * info.context * info.width * 24
+    return layer_bytes + logits_bytes + tokens_bytes + trace_bytes + payload_bytes + 131072
 
 
 def validate_restore(info: ModelInfo, saved: SerializedStackSession) -> None:
@@ -190,6 +213,13 @@ def validate_restore(info: ModelInfo, saved: SerializedStackSession) -> None:
             want = pos * (info.width // 4) * info.layers
             if len(saved.snap_trace) != want or any(not 0 <= r < 120 for r in saved.snap_trace):
                 raise SessionError("SessionState", "a snap trace of the wrong length or roots")
+    # A type-head session's payloads travel with it (session.rs:2894-2910); a snapshot without
+    # them, or with caches of other lengths, is refused.
+    if info.payload_slots:
+        want = [len(p) for p in info.payload_caches()]
+        if [len(p) for p in saved.hamming_payloads] != want:
+            raise SessionError("Shape", "a type-head session needs its per-position payloads, "
+                                        "which this snapshot does not carry")
     for layer in saved.layers:
         if not isinstance(layer, RecurrenceLayer):
             raise SessionError("SessionState", "a read layer's cache for a recurrence layer")
@@ -216,6 +246,14 @@ class SessionPool:
         self.cache.zero()
         self.slide = DeviceArray(capacity, np.uint8, dev)
         self.slide.zero()
+        # A Hamming model's sessions also keep their token stream and the typed reads' payloads
+        # of every position, which the reads look back over.
+        tw, pw = model.stream_words, model.payload_words
+        self.stream = DeviceArray((capacity, tw), np.uint32, dev) if self.info.hamming else None
+        self.payloads = DeviceArray((capacity, pw), np.int64, dev) if pw else None
+        for a in (self.stream, self.payloads):
+            if a is not None:
+                a.zero()
         self._free = list(range(capacity - 1, -1, -1))
 
     def acquire(self, slot: int | None = None) -> int:
@@ -243,8 +281,9 @@ class SessionPool:
         """A fresh session in each slot (reset, session.rs:2703-2760); the slide setting stays,
         as reset keeps it."""
         slots = list(slots)
-        for a in (self.state, self.history, self.position, self.cache):
-            a.zero(slots)
+        for a in (self.state, self.history, self.position, self.cache, self.stream, self.payloads):
+            if a is not None:
+                a.zero(slots)
 
     def set_slide(self, slot: int, on: bool):
         flags = self.slide.download()
@@ -276,6 +315,22 @@ class SessionPool:
         self.position.upload(p)
         self.cache.zero([slot])  # its window sums were formed for the state it held
 
+    def read_stream(self, slot: int, position: int):
+        """(tokens [position], payloads [payload reads, context, width]) of a Hamming slot."""
+        i = self.info
+        tokens = self.stream.download(slot)[:position]
+        pay = (self.payloads.download(slot) if self.payloads is not None
+               else np.zeros(0, np.int64)).reshape(i.payload_slots, i.context, i.width)
+        return tokens, pay
+
+    def write_stream(self, slot: int, tokens, payloads):
+        """A Hamming slot's token stream (the first len(tokens) entries) and payload caches."""
+        row = np.zeros(self.stream.shape[1], np.uint32)
+        row[:len(tokens)] = np.asarray(tokens, np.uint32)
+        self.stream.upload(row, slot)
+        if self.payloads is not None:
+            self.payloads.upload(np.asarray(payloads, np.int64).reshape(-1), slot)
+
     def run(self, slots, tokens, gen: int = 0, native: bool = False, trace: bool = False):
         """One launch: the sessions in `slots` take tokens [n, len] and `gen` greedy steps.
         Returns dict(reply [n, gen+1], status [n], kept [n, P], query [n, d], trace [n, len + gen,
@@ -302,10 +357,18 @@ class SessionPool:
         snap = DeviceArray((n, steps, stride), np.uint8, dev) if trace else None
         ptr = lambda x: None if x is None else x.ptr  # noqa: E731
         # The null stream: the runtime's blocking copies below wait for the launch.
-        hip._check(hip.lib().uor_fbs_serve_slots_async(
-            self.model.handle, d_slots.ptr, n, self.capacity, d_tok.ptr, tokens.shape[1], gen,
-            reply.ptr, self.state.ptr, self.history.ptr, self.position.ptr, self.cache.ptr,
-            self.slide.ptr, ptr(kept), ptr(query), ptr(snap), status.ptr, None))
+        if self.stream is not None:
+            if trace:
+                raise SessionError("Shape", "the snap trace is not served with Hamming reads")
+            hip._check(hip.lib().uor_fbs_serve_slots_stream_async(
+                self.model.handle, d_slots.ptr, n, self.capacity, d_tok.ptr, tokens.shape[1], gen,
+                reply.ptr, self.state.ptr, self.history.ptr, self.position.ptr, self.stream.ptr,
+                ptr(self.payloads), self.cache.ptr, ptr(kept), ptr(query), status.ptr, None))
+        else:
+            hip._check(hip.lib().uor_fbs_serve_slots_async(
+                self.model.handle, d_slots.ptr, n, self.capacity, d_tok.ptr, tokens.shape[1], gen,
+                reply.ptr, self.state.ptr, self.history.ptr, self.position.ptr, self.cache.ptr,
+                self.slide.ptr, ptr(kept), ptr(query), ptr(snap), status.ptr, None))
         out = dict(reply=reply.download(), status=status.download())
         if native:
             out["kept"] = kept.download()
@@ -337,7 +400,7 @@ class Session:
         self.position = 0
         self.tokens: list[int] = []
         self.logits: list[int] | None = None   # pending logits from a restore; zeros otherwise
-        self.hamming_payloads: list = []
+        self.hamming_payloads: list = self.info.payload_caches()
         self._native: NativeStep | None = None
 
     def close(self):
@@ -464,20 +527,32 @@ class Session:
             t = self.trace
             if t.origin_position == 0 and t.written == want and want <= len(t.selected):
                 snap = t.selected[:want].tolist()
+        payloads = []
+        if i.hamming:
+            tokens, pay = self.pool.read_stream(self.slot, pos)
+            assert tokens.tolist() == self.tokens, "the slot's stream and the session's tokens"
+            it = iter(pay)
+            payloads = [next(it).reshape(-1).tolist() if c else [] for c in i.payload_reads]
         return SerializedStackSession(STACK_SESSION_SCHEMA, 1, i.sha256, pos, pos * d, pos * i.heads,
-                                      0, logits, list(self.tokens), list(self.hamming_payloads),
-                                      snap, [], [], [], None, layers)
+                                      0, logits, list(self.tokens), payloads, snap, [], [], [],
+                                      None, layers)
 
     def restore_state(self, saved: SerializedStackSession) -> None:
         """session.rs:2876-3190: validate everything, then replace the slot's state."""
         validate_restore(self.info, saved)
         state = np.concatenate([np.asarray(l.state, np.int64) for l in saved.layers])
         hist = np.concatenate([np.asarray(l.history, np.int64).astype(np.int32) for l in saved.layers])
+        if self.info.hamming:
+            caches = saved.hamming_payloads if self.info.payload_slots else []
+            pay = [np.asarray(p, np.int64) for p, c in zip(caches, self.info.payload_reads) if c]
+            self.pool.write_stream(self.slot, saved.tokens,
+                                   np.concatenate(pay) if pay else np.zeros(0, np.int64))
         self.pool.write(self.slot, state, hist, saved.position)
         self.position = saved.position
         self.tokens = list(saved.tokens)
         self.logits = list(saved.logits) if saved.position > 0 else None
-        self.hamming_payloads = [list(p) for p in saved.hamming_payloads]
+        self.hamming_payloads = ([list(p) for p in saved.hamming_payloads] if saved.hamming_payloads
+                                 else self.info.payload_caches())
         self._native = None
         # The trace continues from a traced snapshot; an untraced one turns tracing off, so no
         # partial root history carries over (session.rs:3172-3190).
