@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define UOR_FBS_ABI_VERSION 2u
+#define UOR_FBS_ABI_VERSION 3u
 
 #define UOR_FBS_OK 0
 #define UOR_FBS_ERR_TOKEN 1       /* token >= vocab (fbs_core.h:627) */
@@ -92,8 +92,8 @@ typedef struct uor_fbs_model {
  * stack/format.rs:229-292, and one HammingReadImage per read, stack/hamming.rs:25-40, from the
  * sections `hamming.d{depth}.*`), served inside the step as the reference session serves them
  * (ServedHamming::stream after `depth` layers and ServedHamming::readout on the final norm's
- * output, session.rs:4252-4276, 4296-4320; hamming.rs:1551-1960). The place read
- * (`hamming.place`) is not served by this build: a record with one is refused. */
+ * output, session.rs:4252-4276, 4296-4320; hamming.rs:1551-1960), with the readout read's place
+ * read when the record carries one (`hamming.place`, below). */
 #define UOR_FBS_COPY_ARTIFACT 0xffffffffu /* serve the artifact's own copy rule */
 #define UOR_FBS_COPY_MEAN 0u              /* CopyRule::Mean (hamming.rs:180-201) */
 #define UOR_FBS_COPY_LATEST_EXACT 1u
@@ -113,6 +113,28 @@ typedef struct uor_fbs_hamming_read {
   const int32_t *carry;          /* vocab carry gains at Q16 (with carry_rows), else NULL */
 } uor_fbs_hamming_read;
 
+/* The readout read's place read (the record's `place` marks, PlaceMarks, fbs_snapshot.rs:2725-
+ * 2762, and the `hamming.d{depth}.place` class table, PlaceImage, :2772-2795): the ids that frame
+ * a conversation and each vocabulary entry's class. The readout read's ask heads then find a
+ * place in the session's finished user turns and bring nothing back themselves; a reply row the
+ * register opens reads the token at the place in place of the copy heads' mean
+ * (ServedHamming::place_advance and readout, hamming.rs:1510-1533, 1625-1634, 1883-1913;
+ * PlaceState::advance, fbs_snapshot.rs:2893-3090). The caller's asks table (set_place_asks,
+ * hamming.rs:1639) is not served. Each marker list holds at most UOR_FBS_PLACE_MARK_MAX ids. */
+#define UOR_FBS_PLACE_STOP 1
+#define UOR_FBS_PLACE_ARM 2
+#define UOR_FBS_PLACE_OPEN 4
+#define UOR_FBS_PLACE_MARK_MAX 16u
+typedef struct uor_fbs_place {
+  uint32_t bos, eos;               /* the document's start and end marks */
+  uint32_t sep_len, system_len, user_len, assistant_len;
+  const uint32_t *sep;             /* the turn separator, sep_len >= 1 ids */
+  const uint32_t *system;          /* the role markers (system may be empty) */
+  const uint32_t *user;
+  const uint32_t *assistant;
+  const int16_t *class_table;      /* vocab classes: STOP | ARM | OPEN bits */
+} uor_fbs_place;
+
 typedef struct uor_fbs_hamming {
   uint32_t heads;               /* per read: heads/2 copy heads, then the type (or ask) heads */
   uint32_t kept;                /* earlier positions each head keeps, >= 1 */
@@ -124,6 +146,7 @@ typedef struct uor_fbs_hamming {
   uint32_t rule;                /* the copy rule served: UOR_FBS_COPY_ARTIFACT or a rule */
   uint32_t read_count;
   const uor_fbs_hamming_read *reads; /* read_count reads, depths strictly increasing */
+  const uor_fbs_place *place;        /* NULL: no place read */
 } uor_fbs_hamming;
 
 typedef struct uor_fbs_ext {

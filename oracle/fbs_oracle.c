@@ -514,6 +514,7 @@ typedef struct Ham {
   uint64_t *pair;  /* per copy head: the first half's bits under copy key 2, else 0 */
   HR *reads;
   int *at;         /* layers + 1: the read at each depth, -1 none */
+  const uor_fbs_place *place; /* the readout read's place read, or NULL */
 } Ham;
 
 typedef struct {
@@ -786,15 +787,24 @@ static void ham_stream(const O *o, uint32_t depth, const uint32_t *tok, size_t t
   free(y);
 }
 
-/* The readout read on the final norm's output n (ServedHamming::readout :1883-1913); no place
- * read, so no offer. */
-static void ham_readout(const O *o, const uint32_t *tok, size_t t, int64_t *n, int64_t *payloads) {
+/* The readout read on the final norm's output n (ServedHamming::readout :1883-1913). At a row the
+ * place read opens, `offer` (>= 0) is the place: the table's point of the token there, at
+ * 2^COPY_MEAN_EXP (a Q12 point at a Q31 weight of one), is the copy term in place of the copy
+ * heads' mean (:1895-1899). */
+static void ham_readout(const O *o, const uint32_t *tok, size_t t, int64_t *n, int64_t *payloads,
+                        long offer) {
   const Ham *h = o->ham;
   if (h->at[o->L] < 0) return;
   const HR *r = &h->reads[h->at[o->L]];
   uint32_t d = o->d;
   i128 *c = malloc(sizeof(i128) * d), *y = malloc(sizeof(i128) * d);
-  int has_c = h->copy ? ham_copy_mean(o, r, tok, t, c) : 0, has_y = 0;
+  int has_c = 0, has_y = 0;
+  if (offer >= 0) {
+    for (uint32_t i = 0; i < d; i++) c[i] = shl128((i128)row_value(o, tok[offer], i), 31);
+    has_c = 1;
+  } else if (h->copy) {
+    has_c = ham_copy_mean(o, r, tok, t, c);
+  }
   if (r->typed)
     has_y = ham_type_mean(o, r, tok, t, n,
                           r->slot >= 0 ? payloads + (size_t)r->slot * o->m->context * d : NULL, y);
@@ -833,6 +843,7 @@ static Ham *ham_build(const O *o, const uor_fbs_hamming *hm) {
   }
   h->at = malloc(sizeof(int) * (o->L + 1));
   for (uint32_t l = 0; l <= o->L; l++) h->at[l] = -1;
+  h->place = hm->place;
   h->reads = calloc(h->n, sizeof(HR));
   for (uint32_t i = 0; i < h->n; i++) {
     HR *r = &h->reads[i];
@@ -847,6 +858,9 @@ static Ham *ham_build(const O *o, const uor_fbs_hamming *hm) {
     r->typed = 0;
     for (uint32_t c = 0; c < d; c++) r->typed |= r->r->weight[d + c] != 0;
     r->asks = r->r->ask != NULL;
+    /* The place read's ask heads find a place and bring nothing back: the readout read then
+     * serves no type heads (`typed = places.is_none() && ...`, :1580-1590). */
+    if (hm->place && r->r->depth == o->L) r->typed = r->asks = 0;
     r->slot = (r->typed && !r->asks) ? (int)h->slots++ : -1;
     r->heads = h->heads;
     r->codes = malloc(sizeof(uint64_t) * (size_t)V * h->heads);
@@ -859,6 +873,243 @@ static Ham *ham_build(const O *o, const uor_fbs_hamming *hm) {
     free(point);
   }
   return h;
+}
+
+/* ------------------------------------------------------------------------------------------
+ * The place read (fbs_snapshot.rs:2716-3135, served by hamming.rs:1510-1533 and 1625-1634): a
+ * register over the session's tokens, every step an integer compare or an index. */
+
+typedef struct {
+  int role;               /* the turn being read: 0 none, 1 system, 2 user, 3 assistant */
+  size_t start;           /* its first content row */
+  size_t nu, *ua, *ub;    /* the contents [ua, ub) of the document's finished user turns */
+  size_t nf, *fat, *fpos; /* the finds of the user turn being read: (row, place) */
+  int has_place;          /* the register: a place and the end of its turn's content */
+  size_t place, pend;
+  long offer;             /* the place offered at the row read last, or -1 */
+  int over, answered;
+} Place;
+
+/* What the register did at one row (PlaceRow, :2860-2877): -1 for none. */
+typedef struct {
+  long held, offer;
+  int stepped;
+  long asked_a, asked_b;   /* at a reply's start: the user turn it answers */
+  size_t nfound;           /* its finds, and the last of them */
+  long found_at, found_pos;
+} PlaceRowOut;
+
+static void place_alloc(Place *pl, size_t context) {
+  memset(pl, 0, sizeof *pl);
+  size_t n = context + 1;
+  pl->ua = calloc(n, sizeof(size_t));
+  pl->ub = calloc(n, sizeof(size_t));
+  pl->fat = calloc(n, sizeof(size_t));
+  pl->fpos = calloc(n, sizeof(size_t));
+  pl->offer = -1;
+}
+
+static void place_free(Place *pl) {
+  free(pl->ua); free(pl->ub); free(pl->fat); free(pl->fpos);
+}
+
+static void place_reset(Place *pl) {
+  pl->role = 0;
+  pl->start = pl->nu = pl->nf = pl->place = pl->pend = 0;
+  pl->has_place = pl->over = pl->answered = 0;
+  pl->offer = -1;
+}
+
+static int ends_with(const uint32_t *tok, size_t len, const uint32_t *m, uint32_t ml) {
+  if (ml > len) return 0;
+  for (uint32_t i = 0; i < ml; i++)
+    if (tok[len - ml + i] != m[i]) return 0;
+  return 1;
+}
+
+static int place_has(const uor_fbs_place *pm, uint32_t vocab, uint32_t token, int bit) {
+  return token < vocab && (pm->class_table[token] & bit) != 0;
+}
+
+/* PlaceTurns::push (:2801-2837): the role whose marker ends at the last token, 0 for none. */
+static int place_turns_push(const uor_fbs_place *pm, Place *pl, const uint32_t *tok, size_t len) {
+  if (!len) return 0;
+  if (tok[len - 1] == pm->bos) {
+    pl->role = 0;
+    pl->start = 0;
+    pl->nu = 0;
+    return 0;
+  }
+  const uint32_t *mk[3] = {pm->system, pm->user, pm->assistant};
+  const uint32_t ml[3] = {pm->system_len, pm->user_len, pm->assistant_len};
+  for (int r = 0; r < 3; r++) {
+    if (!ml[r] || !ends_with(tok, len, mk[r], ml[r])) continue;
+    const size_t m = len - ml[r];
+    const int after_sep = ends_with(tok, m, pm->sep, pm->sep_len);
+    if (pl->role == 0) {
+      if (!(m > 0 && (tok[m - 1] == pm->bos || after_sep))) continue;
+    } else {
+      const size_t a = pl->start;
+      if (!(after_sep && m >= a + pm->sep_len)) continue;
+      size_t b = m - pm->sep_len;
+      if (b > a && tok[b - 1] == pm->eos) b--;
+      if (pl->role == 2) {
+        pl->ua[pl->nu] = a;
+        pl->ub[pl->nu] = b;
+        pl->nu++;
+      }
+    }
+    pl->role = r + 1;
+    pl->start = len;
+    return r + 1;
+  }
+  return 0;
+}
+
+typedef long (*PlaceFind)(const void *ctx, const Place *pl, const uint32_t *tok, size_t t);
+
+/* PlaceState::advance / read (:2937-3090) without the caller's asks: the last token of
+ * tok[0..len) read, every earlier one read before it. `find` answers a row of a user turn's
+ * content with the place its question finds among the finished user turns, or -1. */
+static void place_read(const uor_fbs_place *pm, uint32_t vocab, Place *pl, const uint32_t *tok,
+                       size_t len, PlaceFind find, const void *ctx, PlaceRowOut *row) {
+  row->held = row->offer = row->asked_a = row->asked_b = row->found_at = row->found_pos = -1;
+  row->stepped = 0;
+  row->nfound = 0;
+  if (!len) return;
+  const size_t t = len - 1;
+  const uint32_t token = tok[t];
+  /* The step: the row before was offered the token at the place, and this token is it. */
+  const long at = pl->offer;
+  pl->offer = -1;
+  if (at >= 0 && pl->has_place && (size_t)at == pl->place && token == tok[pl->place]) {
+    const size_t next = pl->place + 1;
+    if (next >= pl->pend || place_has(pm, vocab, tok[next], UOR_FBS_PLACE_STOP)) {
+      pl->has_place = 0;
+    } else {
+      pl->place = next;
+      row->stepped = 1;
+    }
+  }
+  if (token == pm->bos) {
+    pl->nf = 0;
+    pl->has_place = 0;
+    pl->answered = 0;
+  }
+  const int role = place_turns_push(pm, pl, tok, len);
+  if (role == 2) {
+    pl->nf = 0;
+    pl->has_place = 0;
+    pl->answered = 0;
+  } else if (role == 3) {
+    pl->over = 0;
+    pl->has_place = 0;
+    const int asked = pl->nu > 0 && !pl->answered;
+    pl->answered = 1;
+    if (asked) {
+      const size_t ca = pl->ua[pl->nu - 1], cb = pl->ub[pl->nu - 1];
+      long armed = -1;
+      for (size_t i = 0; i < pl->nf; i++) {
+        if (pl->fat[i] < ca || pl->fat[i] >= cb) continue;
+        row->found_at = (long)pl->fat[i];
+        row->found_pos = (long)pl->fpos[i];
+        row->nfound++;
+        if (place_has(pm, vocab, tok[pl->fat[i]], UOR_FBS_PLACE_ARM)) armed = (long)pl->fpos[i];
+      }
+      pl->nf = 0;
+      for (size_t u = 0; armed >= 0 && u + 1 < pl->nu; u++)
+        if ((size_t)armed >= pl->ua[u] && (size_t)armed < pl->ub[u]) {
+          pl->has_place = 1;
+          pl->place = (size_t)armed;
+          pl->pend = pl->ub[u];
+          break;
+        }
+      row->asked_a = (long)ca;
+      row->asked_b = (long)cb;
+    }
+  }
+  if (pl->role == 2 && t >= pl->start && pl->nu > 0) {
+    const long pos = find(ctx, pl, tok, t);
+    if (pos >= 0) {
+      pl->fat[pl->nf] = t;
+      pl->fpos[pl->nf] = (size_t)pos;
+      pl->nf++;
+    }
+  } else if (pl->role == 3) {
+    const size_t a = pl->start;
+    if (token == pm->eos && t >= a) {
+      pl->over = 1;
+      pl->has_place = 0;
+    }
+    if (t + 1 >= a && !pl->over) {
+      row->held = pl->has_place ? (long)pl->place : -1;
+      const int open = place_has(pm, vocab, token, UOR_FBS_PLACE_OPEN);
+      if (row->held >= 0 && (row->stepped || open)) row->offer = row->held;
+    }
+  }
+  pl->offer = row->offer;
+}
+
+/* place_pick (:3117-3135): per head the nearest key over the candidate positions (>= 2), the
+ * later on ties, kept inside the head's margin (m > d 2^16); then the later of the heads'. */
+typedef uint64_t (*PlaceKey)(const void *ctx, uint32_t head, size_t s);
+static long place_pick(const uint64_t *queries, const int32_t *margins, uint32_t heads,
+                       const size_t *ra, const size_t *rb, size_t nr, PlaceKey key, const void *ctx) {
+  long found = -1;
+  for (uint32_t j = 0; j < heads; j++) {
+    long best = -1;
+    uint32_t least = 0;
+    for (size_t u = 0; u < nr; u++)
+      for (size_t s = ra[u] < 2 ? 2 : ra[u]; s < rb[u]; s++) {
+        const uint32_t dd = (uint32_t)__builtin_popcountll(queries[j] ^ key(ctx, j, s));
+        if (best < 0 || dd <= least) {
+          best = (long)s;
+          least = dd;
+        }
+      }
+    if (best >= 0 && (int64_t)margins[j] > ((int64_t)least << 16) && best > found) found = best;
+  }
+  return found;
+}
+
+typedef struct {
+  const O *o;
+  const HR *r;
+  const uint32_t *tok;
+  uint64_t first;
+} PlaceFindCtx;
+
+static uint64_t place_joined(uint64_t near, uint64_t far, uint64_t first) {
+  return (near & first) | (far & ~first);
+}
+
+static uint64_t place_key(const void *ctx, uint32_t j, size_t s) {
+  const PlaceFindCtx *c = ctx;
+  const uint32_t head = c->o->ham->copy + j;
+  return place_joined(ham_code(c->r, c->tok[s - 1], head), ham_code(c->r, c->tok[s - 2], head), c->first);
+}
+
+/* ServedPlace::find (hamming.rs:1525-1533) with place_find (fbs_snapshot.rs:3093-3108): head j
+ * asks with its question code for x_t (the ask point's code through the key rotation, window
+ * from row 0) in the first half of its bits and x_{t-1}'s key code in the rest; its key at s
+ * is x_{s-1}'s key code in the first half and x_{s-2}'s in the rest. */
+static long place_find_row(const void *ctx, const Place *pl, const uint32_t *tok, size_t t) {
+  const O *o = ctx;
+  const Ham *h = o->ham;
+  if (t < 1) return -1;
+  const HR *r = &h->reads[h->at[o->L]];
+  const uint32_t d = o->d, types = h->heads - h->copy;
+  const uint64_t first = (1ull << (h->hw / 2)) - 1;
+  int64_t *p = malloc(sizeof(int64_t) * d);
+  ham_asked_point(o, r, tok, t, p);
+  uint64_t *q = malloc(sizeof(uint64_t) * types);
+  for (uint32_t j = 0; j < types; j++)
+    q[j] = place_joined(head_code(r->ku, p, h->copy + j, h->hw), ham_code(r, tok[t - 1], h->copy + j), first);
+  PlaceFindCtx c = {o, r, tok, first};
+  const long found = place_pick(q, r->r->margin + h->copy, types, pl->ua, pl->ub, pl->nu, place_key, &c);
+  free(p);
+  free(q);
+  return found;
 }
 
 static void ham_free(Ham *h) {
@@ -892,6 +1143,8 @@ typedef struct {
   int64_t *normed;   /* width: the final norm's output (the readout read's input) */
   int slide;         /* a full context continues (set_context_slide, session.rs:2391-2402) */
   uint8_t *trace;    /* this step's snap trace (layers * (2 lanes + mlp / 4) bytes), or NULL */
+  Place place;       /* the place read's register and turns (session.rs:2239-2241) */
+  long held, offer;  /* the register after the last step (last_place, session.rs:2626-2631) */
 } S;
 
 static void session_alloc(const O *o, S *s) {
@@ -913,12 +1166,15 @@ static void session_alloc(const O *o, S *s) {
   s->tokens = calloc(o->m->context ? o->m->context : 1, 4);
   s->payloads = calloc(o->ham && o->ham->slots ? (size_t)o->ham->slots * o->m->context * d : 1, 8);
   s->normed = calloc(d, 8);
+  place_alloc(&s->place, o->m->context);
+  s->held = s->offer = -1;
 }
 
 static void session_free(S *s) {
   free(s->x); free(s->branches); free(s->gate_out); free(s->proj); free(s->gate); free(s->up);
   free(s->query); free(s->scratch); free(s->wide); free(s->act); free(s->state);
   free(s->history); free(s->kept); free(s->tokens); free(s->payloads); free(s->normed);
+  place_free(&s->place);
 }
 
 static void session_reset(const O *o, S *s) {
@@ -927,6 +1183,21 @@ static void session_reset(const O *o, S *s) {
   s->position = 0;
   memset(s->tokens, 0, 4ull * o->m->context);
   if (o->ham && o->ham->slots) memset(s->payloads, 0, 8ull * o->ham->slots * o->m->context * o->d);
+  place_reset(&s->place);
+  s->held = s->offer = -1;
+}
+
+/* The place register over a resumed session's tokens x_0..x_{position-1}: the state it holds
+ * after stepping them (the register depends on the tokens and the model alone). */
+static void place_replay(const O *o, S *s) {
+  if (!o->ham || !o->ham->place) return;
+  place_reset(&s->place);
+  PlaceRowOut row;
+  for (size_t t = 0; t < s->position; t++) {
+    place_read(o->ham->place, o->m->vocab, &s->place, s->tokens, t + 1, place_find_row, o, &row);
+    s->held = row.held;
+    s->offer = row.offer;
+  }
 }
 
 /* `stack_recurrence_core` with geometric gates, learned rotations and the Hamilton output
@@ -1009,6 +1280,13 @@ static int step(const O *o, S *s, uint32_t token, uint32_t *out_token) {
   if (s->position >= m->context && !s->slide) return UOR_FBS_ERR_CONTEXT;
   if (o->ham) s->tokens[s->position] = token;
   const size_t t = s->position;
+  /* The place read's register moves on this token, before the row's readout (:4154-4162). */
+  if (o->ham && o->ham->place) {
+    PlaceRowOut row;
+    place_read(o->ham->place, m->vocab, &s->place, s->tokens, t + 1, place_find_row, o, &row);
+    s->held = row.held;
+    s->offer = row.offer;
+  }
   for (uint32_t i = 0; i < d; i++) s->x[i] = to_exp_i32(row_value(o, token, i), Q12_EXP, RESIDUAL_EXP);
   for (uint32_t l = 0; l < o->L; l++) {
     const uor_fbs_layer *ly = m->layers + l;
@@ -1036,7 +1314,7 @@ static int step(const O *o, S *s, uint32_t token, uint32_t *out_token) {
   }
   rms_norm_fine(s->x, d, m->eps_mantissa, m->eps_exp, s->scratch);
   for (uint32_t i = 0; i < d; i++) s->normed[i] = grid_apply(s->scratch[i], m->final_gain[i]);
-  if (o->ham) ham_readout(o, s->tokens, t, s->normed, s->payloads);
+  if (o->ham) ham_readout(o, s->tokens, t, s->normed, s->payloads, o->ham->place ? s->offer : -1);
   for (uint32_t i = 0; i < d; i++) {
     int32_t q = to_exp_i32(s->normed[i], NORM_FINE_EXP, Q12_EXP);
     s->query[i] = q > 32767 ? 32767 : q < -32768 ? -32768 : q;
@@ -1071,6 +1349,7 @@ typedef struct {
   int64_t *out_payloads;
   uint64_t matches;
   uint8_t *out_trace; /* sequences: every position's snap trace */
+  int64_t *out_place; /* sequences: every position's (held, offered) place, -1 for none */
   int slide;
   int tid, threads, status;
 } Job;
@@ -1102,6 +1381,10 @@ static void *run_job(void *arg) {
         if (j->out_tokens) j->out_tokens[at] = tok;
         if (j->out_kept) memcpy(j->out_kept + at * o->P, s.kept, 4ull * o->P);
         if (j->out_query) memcpy(j->out_query + at * d, s.query, 4ull * d);
+        if (j->out_place) {
+          j->out_place[2 * at] = s.held;
+          j->out_place[2 * at + 1] = s.offer;
+        }
         if (j->kind == 2 && t + 1 < j->len && tok == row[t + 1]) j->matches++;
       }
       continue;
@@ -1113,6 +1396,7 @@ static void *run_job(void *arg) {
     const uint64_t ctx = o->m->context, pw = o->ham ? (uint64_t)o->ham->slots * ctx * d : 0;
     if (j->in_tokens) memcpy(s.tokens, j->in_tokens + i * ctx, 4 * ctx);
     if (j->in_payloads && pw) memcpy(s.payloads, j->in_payloads + i * pw, 8 * pw);
+    if (j->in_tokens) place_replay(o, &s);
     const uint32_t *prompt = j->tokens + i * j->prompt_len;
     uint32_t *reply = j->out_reply + i * ((uint64_t)j->gen + 1);
     uint32_t next = 0;
@@ -1321,7 +1605,7 @@ int fbs_oracle_hamming_row(const uor_fbs_model *m, const uor_fbs_ext *ext, uint3
   if (depth < o.L)
     ham_stream(&o, depth, tok, t, x, payloads);
   else
-    ham_readout(&o, tok, t, n, payloads);
+    ham_readout(&o, tok, t, n, payloads, -1);
   unresolve(&o);
   return 0;
 }
@@ -1413,4 +1697,95 @@ uint32_t fbs_oracle_writer(const uor_fbs_model *m, const uor_fbs_ext *ext, const
   if (candidates) *candidates = c;
   unresolve(&o);
   return t;
+}
+
+/* ------------------------------------------------------------------------------------------
+ * The place read's pieces, for the tests that pin them (the reference's place_tests,
+ * fbs_snapshot.rs:3136-3370, and a_session_serves_the_place_read, stack/tests.rs:8882-8930). */
+
+/* Teacher-forced sequences with every position's place register after the step (last_place:
+ * held, offered; -1 for none), besides fbs_oracle_sequences' outputs. */
+int fbs_oracle_place_sequences(const uor_fbs_model *m, const uor_fbs_ext *ext,
+                               const uint32_t *tokens, uint32_t sequences, uint32_t len,
+                               uint32_t *out_tokens, int32_t *out_query, int64_t *out_place,
+                               int threads) {
+  O o;
+  resolve(&o, m, ext);
+  Job j = {0};
+  j.o = &o;
+  j.kind = 0;
+  j.tokens = tokens;
+  j.n = sequences;
+  j.len = len;
+  j.out_tokens = out_tokens;
+  j.out_query = out_query;
+  j.out_place = out_place;
+  int status = run_jobs(&j, threads);
+  unresolve(&o);
+  return status;
+}
+
+typedef struct {
+  const int64_t *finds; /* (row, place) pairs */
+  uint32_t n;
+} InjectedFinds;
+
+static long injected_find(const void *ctx, const Place *pl, const uint32_t *tok, size_t t) {
+  (void)pl;
+  (void)tok;
+  const InjectedFinds *f = ctx;
+  for (uint32_t i = 0; i < f->n; i++)
+    if (f->finds[2 * i] == (int64_t)t) return (long)f->finds[2 * i + 1];
+  return -1;
+}
+
+/* The register over tokens[0..n) from a fresh state, the question at each row finds[2i] finding
+ * finds[2i+1] and every other row nothing (the tests' `rows`, fbs_snapshot.rs:3161-3165). Per row,
+ * 8 values: held, offer, stepped, asked content start and end, the asked finds' count and the
+ * last of them (row, place); -1 for none. */
+int fbs_oracle_place_rows(const uor_fbs_place *pm, uint32_t vocab, const uint32_t *tokens,
+                          uint64_t n, const int64_t *finds, uint32_t nfinds, int64_t *out) {
+  Place pl;
+  place_alloc(&pl, n);
+  InjectedFinds f = {finds, nfinds};
+  for (uint64_t t = 0; t < n; t++) {
+    PlaceRowOut row;
+    place_read(pm, vocab, &pl, tokens, t + 1, injected_find, &f, &row);
+    int64_t *o = out + 8 * t;
+    o[0] = row.held;
+    o[1] = row.offer;
+    o[2] = row.stepped;
+    o[3] = row.asked_a;
+    o[4] = row.asked_b;
+    o[5] = (int64_t)row.nfound;
+    o[6] = row.found_at;
+    o[7] = row.found_pos;
+  }
+  place_free(&pl);
+  return 0;
+}
+
+typedef struct {
+  const uint64_t *keys;
+} PickKeys;
+
+static uint64_t pick_key(const void *ctx, uint32_t j, size_t s) {
+  (void)j;
+  return ((const PickKeys *)ctx)->keys[s];
+}
+
+/* place_pick over candidate ranges [ranges[2u], ranges[2u+1]), every head's key at position s
+ * keys[s] (the tests' key closure). Returns the position, or -1. */
+int64_t fbs_oracle_place_pick(const uint64_t *queries, const int32_t *margins, uint32_t heads,
+                              const uint64_t *ranges, uint32_t nranges, const uint64_t *keys) {
+  size_t *ra = calloc(nranges + 1, sizeof(size_t)), *rb = calloc(nranges + 1, sizeof(size_t));
+  for (uint32_t u = 0; u < nranges; u++) {
+    ra[u] = ranges[2 * u];
+    rb[u] = ranges[2 * u + 1];
+  }
+  PickKeys k = {keys};
+  const long found = place_pick(queries, margins, heads, ra, rb, nranges, pick_key, &k);
+  free(ra);
+  free(rb);
+  return found;
 }

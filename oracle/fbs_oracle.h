@@ -84,6 +84,17 @@ int fbs_oracle_hamming_row(const uor_fbs_model *m, const uor_fbs_ext *ext, uint3
                            int64_t *payloads);
 int fbs_oracle_hamming_codes(const uor_fbs_model *m, const uor_fbs_ext *ext, uint32_t r,
                              uint64_t *out);
+/* The place read: teacher-forced sequences with every position's register after the step
+ * (held, offered place; -1 for none), the register over a token stream with injected finds,
+ * and the place pick over candidate ranges with per-position keys. */
+int fbs_oracle_place_sequences(const uor_fbs_model *m, const uor_fbs_ext *ext,
+                               const uint32_t *tokens, uint32_t sequences, uint32_t len,
+                               uint32_t *out_tokens, int32_t *out_query, int64_t *out_place,
+                               int threads);
+int fbs_oracle_place_rows(const uor_fbs_place *pm, uint32_t vocab, const uint32_t *tokens,
+                          uint64_t n, const int64_t *finds, uint32_t nfinds, int64_t *out);
+int64_t fbs_oracle_place_pick(const uint64_t *queries, const int32_t *margins, uint32_t heads,
+                              const uint64_t *ranges, uint32_t nranges, const uint64_t *keys);
 /* stream_sum / readout_sum / readout_ask_sum (hamming.rs:1918-1953), 128-bit means as hi:lo. */
 int32_t fbs_oracle_stream_sum(int32_t x, int32_t w_c, int64_t c_hi, uint64_t c_lo, int32_t w_y,
                               int64_t y_hi, uint64_t y_lo);

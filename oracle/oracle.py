@@ -76,6 +76,10 @@ def lib():
         L.fbs_oracle_readout_ask_sum.argtypes = [i64, i32, C.c_int, i64, u64, i32, C.c_int, i64,
                                                  u64]
         L.fbs_oracle_readout_ask_sum.restype = i64
+        L.fbs_oracle_place_sequences.argtypes = [P, P, P, u32, u32, P, P, P, C.c_int]
+        L.fbs_oracle_place_rows.argtypes = [P, u32, P, u64, P, u32, P]
+        L.fbs_oracle_place_pick.argtypes = [P, P, u32, P, u32, P]
+        L.fbs_oracle_place_pick.restype = i64
         _lib = L
     return _lib
 
@@ -114,6 +118,59 @@ def sequences(art, tokens: np.ndarray, threads: int = 1, image: Image | None = N
     st = lib().fbs_oracle_sequences(C.addressof(img.model), img.ext_ptr() and C.addressof(img.ext),
                                     _vp(tokens), S, n, _vp(out_t), _vp(out_k), _vp(out_q), threads)
     return st, out_t, out_k, out_q
+
+
+def place_sequences(art, tokens: np.ndarray, threads: int = 1, image: Image | None = None):
+    """Teacher-forced outputs with the place register after every step: (status, tokens [S,len],
+    query [S,len,d], place [S,len,2] as (held, offered), -1 for none)."""
+    img = image or Image(art)
+    tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+    S, n = tokens.shape
+    out_t = np.zeros((S, n), np.uint32)
+    out_q = np.zeros((S, n, art.spec.width), np.int32)
+    out_p = np.zeros((S, n, 2), np.int64)
+    st = lib().fbs_oracle_place_sequences(C.addressof(img.model), img.ext_ptr() and C.addressof(img.ext),
+                                          _vp(tokens), S, n, _vp(out_t), _vp(out_q), _vp(out_p), threads)
+    return st, out_t, out_q, out_p
+
+
+def place_rows(marks, classes, tokens, finds) -> np.ndarray:
+    """The place register over `tokens` from a fresh state, the question at each row `at` of
+    `finds` [(at, pos), ...] finding `pos` (every other row nothing): per row (held, offer,
+    stepped, asked start, asked end, finds in the asked turn, the last find's row and place), -1
+    for none."""
+    from uor_fbs.cabi import PlaceS
+    keep = []
+
+    def ids(v):
+        a = np.ascontiguousarray(v, np.uint32)
+        keep.append(a)
+        return ptr(a, C.c_uint32) if len(a) else ptr(None, C.c_uint32)
+
+    pm = PlaceS()
+    pm.bos, pm.eos = marks.bos, marks.eos
+    for name in ("sep", "system", "user", "assistant"):
+        setattr(pm, name + "_len", len(getattr(marks, name)))
+        setattr(pm, name, ids(getattr(marks, name)))
+    cls = np.ascontiguousarray(classes, np.int16)
+    pm.class_table = ptr(cls, C.c_int16)
+    tok = np.ascontiguousarray(tokens, np.uint32)
+    out = np.zeros((len(tok), 8), np.int64)
+    f = np.ascontiguousarray(np.asarray(finds, np.int64).reshape(-1), np.int64)
+    lib().fbs_oracle_place_rows(C.addressof(pm), len(cls), _vp(tok), len(tok),
+                                _vp(f) if f.size else None, f.size // 2, _vp(out))
+    return out
+
+
+def place_pick(queries, margins, ranges, keys) -> int | None:
+    """place_pick with every head's key at position s keys[s]; None when nothing is found."""
+    q = np.ascontiguousarray(queries, np.uint64)
+    m = np.ascontiguousarray(margins, np.int32)
+    r = np.ascontiguousarray(np.asarray(ranges, np.uint64).reshape(-1), np.uint64)
+    k = np.ascontiguousarray(keys, np.uint64)
+    got = lib().fbs_oracle_place_pick(_vp(q), _vp(m), len(q), _vp(r) if r.size else None,
+                                      r.size // 2, _vp(k))
+    return None if got < 0 else int(got)
 
 
 def decode(art, prompts: np.ndarray, gen: int, threads: int = 1, image: Image | None = None,

@@ -36,7 +36,7 @@ def test_library_exports_every_declared_entry_point():
     assert names == set(hip.SYMBOLS)
     for name in names:
         assert hasattr(L, name), name
-    assert L.uor_fbs_abi_version() == 2
+    assert L.uor_fbs_abi_version() == 3
 
 
 def test_struct_layout_matches_the_reference_image():

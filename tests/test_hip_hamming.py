@@ -246,3 +246,124 @@ def test_a_restored_session_continues_bit_for_bit(name, tmp_path):
         bare.hamming_payloads = []
         with pytest.raises(SessionError):
             Session(pool).restore_state(bare)
+
+
+# ---- The place read (hamming.rs:1510-1533, 1625-1634, 1883-1913; fbs_snapshot.rs:2716-3135) ----
+# The oracle's register is pinned by the reference's own place tests (test_place_oracle.py); here
+# the GPU path is held to it, bit for bit, on the reference's talk and on seeded conversations
+# whose words stop, arm and open at random, at every kernel width.
+
+from test_place_oracle import P_ASK, P_BOS, P_EOS, P_MODEL, P_SEP, P_TALK, P_USER, place_trunk
+
+PLACE_CASES = {  # shape, heads, the teacher-forced conversations' seed
+    "w64": (synth.Spec(vocab=512, width=64, mlp=64, layers=3, context=64, kept=8), 4, 7),
+    "w512": (synth.Spec(vocab=1024, width=512, mlp=128, layers=2, context=48, kept=8), 16, 7),
+    "w1024": (synth.Spec(vocab=768, width=1024, mlp=128, layers=2, context=40, kept=8), 16, 14),
+}
+
+
+def place_case(name, seed=91):
+    spec, heads, _ = PLACE_CASES[name]
+    _, placed = place_trunk(spec, seed, heads=heads, margin_bits=(6, 24))
+    rng = np.random.default_rng(seed)
+    cls = placed.hamming_place.copy()
+    words = np.arange(20, 40)
+    cls[words] = (np.where(rng.random(20) < 0.15, 1, 0) | np.where(rng.random(20) < 0.35, 2, 0)
+                  | np.where(rng.random(20) < 0.35, 4, 0))
+    placed.hamming_place = cls
+    return placed
+
+
+def conversations(n, length, seed, end_in_reply=False):
+    """Seeded conversations over the marks and a small alphabet (words repeat, so finds land)."""
+    rng = np.random.default_rng(seed)
+    rows = []
+    for _ in range(n):
+        toks = [P_BOS]
+        while len(toks) < length:
+            role = rng.choice([P_USER, P_MODEL, 503], p=[0.45, 0.45, 0.1])
+            toks += [role] if len(toks) == 1 else [P_SEP, role]
+            toks += [int(w) for w in rng.integers(20, 40, size=int(rng.integers(2, 9)))]
+            if rng.random() < 0.3:
+                toks.append(P_ASK)
+            if rng.random() < 0.5:
+                toks.append(P_EOS)
+        toks = toks[:length]
+        if end_in_reply:
+            toks[-2:] = [P_SEP, P_MODEL]
+        rows.append(toks)
+    return np.asarray(rows, np.uint32)
+
+
+@pytest.mark.parametrize("name", sorted(PLACE_CASES))
+def test_the_place_read_matches_the_oracle_teacher_forced(name):
+    art = place_case(name)
+    rows = conversations(8, art.spec.context, PLACE_CASES[name][2])
+    print(f"place {name} rows {rows.shape}", flush=True)
+    st, tok, query, place = oracle.place_sequences(art, rows, threads=4)
+    assert st == 0
+    assert (place[..., 1] >= 0).sum() >= 3, "the register opens rows in these conversations"
+    got_t, got_k, got_q = Model(art).sequences(rows)
+    np.testing.assert_array_equal(got_t, tok)
+    np.testing.assert_array_equal(got_q, query)
+    _, _, k2, _ = oracle.sequences(art, rows, threads=4)
+    np.testing.assert_array_equal(got_k, k2)
+
+
+@pytest.mark.parametrize("name", sorted(PLACE_CASES))
+def test_the_place_read_decodes_and_resumes_as_the_oracle(name):
+    art = place_case(name)
+    ctx = art.spec.context
+    prompts = conversations(4, ctx // 2, 8, end_in_reply=True)
+    gen = ctx - prompts.shape[1] - 1
+    print(f"place {name} decode prompts {prompts.shape} gen {gen}", flush=True)
+    model = Model(art)
+    want = oracle.decode(art, prompts, gen, threads=4)
+    assert want["status"] == 0
+    got = model.decode(prompts, gen)
+    for k in ("reply", "state", "history", "position"):
+        np.testing.assert_array_equal(got[k], want[k], err_msg=f"{name} {k}")
+    # Split and resumed through the session stream: the register is rebuilt from the tokens.
+    half = gen // 2
+    first = model.decode_stream(prompts, half)
+    again = model.decode_stream(first["reply"][:, -1:], gen - half - 1, resume=first)
+    np.testing.assert_array_equal(again["reply"], want["reply"][:, half + 1:])
+    for k in ("state", "history", "position"):
+        np.testing.assert_array_equal(again[k], want[k], err_msg=f"{name} resumed {k}")
+
+
+def test_the_reference_talk_is_offered_its_place_on_the_gpu():
+    # The reference's own session case (stack/tests.rs:8882-8930) through the GPU: with the copy
+    # weights at one, an open row's query is the table point of the token at the place.
+    asked, placed = place_trunk()
+    d = placed.spec.width
+    table = placed.writer_table.reshape(-1, d)
+    rows = np.asarray([P_TALK], np.uint32)
+    tok, _, query = Model(placed).sequences(rows)
+    st, t2, q2, place = oracle.place_sequences(placed, rows)
+    assert st == 0
+    np.testing.assert_array_equal(tok, t2)
+    np.testing.assert_array_equal(query, q2)
+    np.testing.assert_array_equal(query[0, 18], table[P_TALK[4]])
+    np.testing.assert_array_equal(query[0, 19], table[P_TALK[5]])
+    _, _, free = Model(asked).sequences(rows)
+    moved = [t for t in range(len(P_TALK)) if not np.array_equal(query[0, t], free[0, t])]
+    assert moved == [18, 19]
+
+
+def test_place_sessions_served_from_slots_match_the_oracle():
+    art = place_case("w64")
+    prompts = conversations(3, 20, 9, end_in_reply=True)
+    gen = 24
+    print("place sessions from slots", flush=True)
+    want = oracle.decode_stream(art, prompts, gen, threads=4)
+    pool = SessionPool(Model(art), capacity=5)
+    sessions = [Session(pool, s) for s in (3, 0, 4)]
+    nxt = [s.feed(p[:7]).token for s, p in zip(sessions, prompts)]
+    nxt = [s.feed(p[7:]).token for s, p in zip(sessions, prompts)]
+    got = [[t] for t in nxt]
+    for _ in range(gen):
+        for i, (tok, _) in enumerate(serve_steps(sessions, nxt)):
+            got[i].append(tok)
+            nxt[i] = tok
+    np.testing.assert_array_equal(np.asarray(got, np.uint32), want["reply"])

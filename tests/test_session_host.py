@@ -111,6 +111,15 @@ def test_hamming_payload_caches():
     assert max_serialized_session_bytes(info) - max_serialized_session_bytes(plain) == 16 * d * 24
 
 
+def test_a_place_read_session_is_not_restored():
+    # The reference saves neither the place register nor the turns, and refuses the restore by
+    # name (session.rs:2911-2919).
+    info = dataclasses.replace(INFO, hamming=True, place=True)
+    with pytest.raises(SessionError, match="place read") as e:
+        validate_restore(info, saved())
+    assert e.value.kind == "Shape"
+
+
 def test_serving_identity():
     path = os.path.join(GOLDEN, "trained", "content_seed1_s7.uorlut")
     art = uorlut.load(path)

@@ -296,6 +296,45 @@ int check_hamming(const uor_fbs_model *m, const uor_fbs_hamming &hm) {
   }
   if (typed * m->context * d * 8 > (1ull << 32))
     return fail(UOR_FBS_ERR_SHAPE, "hamming: the payload caches exceed 4 GiB a session");
+  if (hm.place) {
+    // StackHamming::check's place rules (format.rs:415-427) and PlaceImage::checked
+    // (fbs_snapshot.rs:2779-2790, PlaceMarks::check :2741-2761).
+    const uor_fbs_place &p = *hm.place;
+    const uor_fbs_hamming_read &last = hm.reads[hm.read_count - 1];
+    if (last.depth != m->layer_count || !last.ask)
+      return fail(UOR_FBS_ERR_SHAPE, "hamming: a place read is served on a readout read that asks");
+    if (hw % 8)
+      return fail(UOR_FBS_ERR_SHAPE,
+                  "hamming: a place read needs heads of whole 8-coordinate blocks, so each half is whole lanes");
+    const uint32_t *lists[4] = {p.sep, p.system, p.user, p.assistant};
+    const uint32_t lens[4] = {p.sep_len, p.system_len, p.user_len, p.assistant_len};
+    for (int k = 0; k < 4; k++) {
+      if (lens[k] > UOR_FBS_PLACE_MARK_MAX)
+        return fail(UOR_FBS_ERR_UNSUPPORTED, "hamming: a place read's marker of %u ids (this build reads at most %u)",
+                    lens[k], UOR_FBS_PLACE_MARK_MAX);
+      if (lens[k] && !lists[k]) return fail(UOR_FBS_ERR_ARGUMENT, "hamming: a place read's null marker");
+    }
+    if (!p.class_table) return fail(UOR_FBS_ERR_ARGUMENT, "hamming: a place read's null class table");
+    bool outside = p.bos >= m->vocab || p.eos >= m->vocab;
+    for (int k = 0; k < 4; k++)
+      for (uint32_t i = 0; i < lens[k]; i++) outside |= lists[k][i] >= m->vocab;
+    if (outside) return fail(UOR_FBS_ERR_SHAPE, "hamming: a place read's mark is outside the vocabulary");
+    if (!p.sep_len || !p.user_len || !p.assistant_len)
+      return fail(UOR_FBS_ERR_SHAPE, "hamming: a place read needs a separator, a user marker and an assistant marker");
+    if (p.bos == p.eos) return fail(UOR_FBS_ERR_SHAPE, "hamming: a place read's start mark and end mark are one token");
+    for (int i = 1; i < 4; i++)
+      for (int j = 1; j < 4; j++) {
+        if (i == j || !lens[j] || lens[i] < lens[j]) continue;
+        bool ends = true;
+        for (uint32_t k = 0; k < lens[j]; k++) ends &= lists[i][lens[i] - lens[j] + k] == lists[j][k];
+        if (ends) return fail(UOR_FBS_ERR_SHAPE, "hamming: one of a place read's role markers ends with another");
+      }
+    for (uint32_t v = 0; v < m->vocab; v++)
+      if (p.class_table[v] & ~(UOR_FBS_PLACE_STOP | UOR_FBS_PLACE_ARM | UOR_FBS_PLACE_OPEN))
+        return fail(UOR_FBS_ERR_SHAPE, "hamming: the place read's class table has a bit outside stop, arm and open");
+    if (m->context > 0xffffu)
+      return fail(UOR_FBS_ERR_UNSUPPORTED, "hamming: a place read over a context past 65535 positions");
+  }
   return 0;
 }
 
@@ -452,6 +491,36 @@ int upload_hamming(uor_fbs_handle *h, const uor_fbs_model *m, const uor_fbs_ext 
     for (uint32_t c = 0; c < d; c++) R.typed |= r.weight[d + c] != 0;
     R.slot = R.typed && !r.ask ? H.slots++ : kHamNoSlot;
     R.pad = 0;
+  }
+  H.place = 0;
+  if (hm.place) {
+    // The place read's ask heads find a place and bring nothing back: its read serves no type
+    // heads and reads as a read that does not ask (`typed = places.is_none() && ...`,
+    // hamming.rs:1580-1600); the question table and carry serve the find.
+    const uor_fbs_place &p = *hm.place;
+    H.place = 1;
+    H.p_read = hm.read_count - 1;
+    H.p_bos = p.bos;
+    H.p_eos = p.eos;
+    const uint32_t *lists[4] = {p.sep, p.system, p.user, p.assistant};
+    const uint32_t lens[4] = {p.sep_len, p.system_len, p.user_len, p.assistant_len};
+    std::vector<uint32_t> marks(4 * kPlaceMarkMax, 0);
+    for (int k = 0; k < 4; k++) {
+      H.p_len[k] = lens[k];
+      for (uint32_t i = 0; i < lens[k]; i++) marks[k * kPlaceMarkMax + i] = lists[k][i];
+    }
+    if ((st = h->upload(marks.data(), marks.size(), &H.p_marks))) return st;
+    std::vector<uint8_t> cls(V);
+    for (uint32_t v = 0; v < V; v++) cls[v] = (uint8_t)p.class_table[v];
+    if ((st = h->upload(cls.data(), cls.size(), &H.p_class))) return st;
+    DevHamRead &R = reads[H.p_read];
+    H.p_ask = R.ask;
+    H.p_carry = R.carry;
+    H.p_carry_rows = R.carry_rows;
+    R.ask = nullptr;
+    R.carry = nullptr;
+    R.carry_rows = 0;
+    R.typed = 0;
   }
   if ((st = h->upload(pair.data(), pair.size(), &H.pair))) return st;
   if ((st = h->upload(at.data(), at.size(), &H.at))) return st;

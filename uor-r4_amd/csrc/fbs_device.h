@@ -67,16 +67,30 @@ struct DevHamRead {
   uint32_t pad;
 };
 
+// The readout read's place read (fbs_hamming.h's place register): the marks and the classes.
+constexpr uint32_t kPlaceMarkMax = 16;     // ids a marker list holds (UOR_FBS_PLACE_MARK_MAX)
+constexpr uint32_t kPlaceWords = 16;       // the register's scalars in LDS
+constexpr uint32_t kPlaceNone = 0xffffffffu;
+constexpr uint32_t kPlaceStop = 1, kPlaceArm = 2, kPlaceOpen = 4;  // the class bits
+
 struct DevHam {
   uint32_t heads;               // 0: the model has no Hamming reads
   uint32_t copy, hw, kept;      // heads / 2 copy heads, d / heads coordinates a head
   uint32_t rule;                // the copy rule served (UOR_FBS_COPY_*, resolved)
   uint32_t has_marker, m0, m1;  // the longest rule's reply marker
   uint32_t slots;               // payload caches a session keeps
-  uint32_t pad;
+  uint32_t place;               // 1: the readout read's place read
+  uint32_t p_read;              // the place read's index (the readout read)
+  uint32_t p_bos, p_eos;        // the document's start and end marks
+  uint32_t p_len[4];            // the separator's and the system, user, assistant markers' lengths
+  uint32_t p_carry_rows;        // the place read's question carry reach
   const uint64_t *pair;         // copy: a copy key 2 head's first-half mask, else 0
   const int32_t *at;            // L + 1: the read index at each depth, or -1
   const DevHamRead *reads;
+  const uint32_t *p_marks;      // 4 * kPlaceMarkMax: the separator, then the role markers
+  const uint8_t *p_class;       // vocab: UOR_FBS_PLACE_STOP | _ARM | _OPEN
+  const int16_t *p_ask;         // the place read's question table (vocab * d, Q12)
+  const int32_t *p_carry;       // its carry gains (Q16), or null
 };
 
 struct DevModel {
@@ -126,10 +140,16 @@ inline size_t pair_lds_bytes(const DevModel &M) {
 // A Hamming model's kernels add the session's tokens (context u32), the distances (context
 // bytes), one head's picks and weights (2 kMaxHamKept u32), its distance histogram and the
 // weight of each distance (2 kHamBins u32) and the sign nibbles (d / 4 u32).
+inline size_t place_lds_bytes(const DevModel &M) {
+  // The register's scalars, then per position the end of its finished user turn (u16) and an
+  // arming row's find + 1 (u16).
+  return M.ham.place ? 4ull * kPlaceWords + 2 * ((2ull * M.context + 15ull) & ~15ull) : 0;
+}
+
 inline size_t ham_lds_bytes(const DevModel &M) {
   if (!M.ham.heads) return 0;
   return 4ull * M.context + ((M.context + 15ull) & ~15ull) + 8ull * kMaxHamKept + 8ull * kHamBins +
-         4ull * (M.d / 4);
+         4ull * (M.d / 4) + place_lds_bytes(M);
 }
 
 // One serving slot's cache (uor_fbs_serve_slots_async), bytes from the entry's start: a u32 tag

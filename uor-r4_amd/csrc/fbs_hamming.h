@@ -461,6 +461,226 @@ __device__ __forceinline__ bool ham_type_mean(const DevModel &M, const DevHamRea
   return true;
 }
 
+// ---- The place read (fbs_snapshot.rs:2716-3135, served by hamming.rs:1510-1533 and 1625-1634) --
+// The readout read's ask heads find a place in the session's finished user turns; the register
+// over the session's tokens holds it from the reply's start, and a reply row it opens reads the
+// token at the place (ham_readout). The sequence's register sits in LDS: kPlaceWords scalars
+// (below), per position the end of the finished user turn that holds it (`uend`, 0 for none) and,
+// at a row of a user turn's content whose token arms, the place its question found + 1 (`farm`;
+// only an arming row's find can set the register, so no other row's is kept). Every lane runs the
+// register's scalar program on the same values; lane 0 writes them back.
+enum : uint32_t {
+  kPlRole = 0,   // the turn being read: 0 none, 1 system, 2 user, 3 assistant
+  kPlStart,      // its first content row
+  kPlUsers,      // the document's finished user turns
+  kPlLastA,      // the last of them: its content [a, b)
+  kPlLastB,
+  kPlDoc,        // the document's first row (positions before it belong to a forgotten one)
+  kPlHas,        // the register is set: a place and the end of its turn's content
+  kPlPlace,
+  kPlEnd,
+  kPlOffer,      // the place offered at the row read last, or kPlaceNone
+  kPlOver,       // the reply being read reached its end mark
+  kPlAnswered,   // a reply started since the last user turn did
+};
+
+// A fresh register (PlaceState::default) and empty per-position tables.
+__device__ __forceinline__ void place_init(const DevModel &M, const Lds &S, uint32_t lane) {
+  for (uint32_t i = lane; i < kPlaceWords; i += kWave) S.pst[i] = i == kPlOffer ? kPlaceNone : 0u;
+  for (uint32_t i = lane; i < M.context; i += kWave) {
+    S.uend[i] = 0;
+    S.farm[i] = 0;
+  }
+  wave_sync();
+}
+
+// The find of the question at row t (ServedPlace::find, hamming.rs:1525-1533; place_find and
+// place_pick, fbs_snapshot.rs:3093-3135): head j (a type head of the readout read) asks with the
+// sign code of the ask point of x_t (the question table and carry, window from row 0) through
+// the key rotation in the first half of its bits and x_{t-1}'s key code in the rest; its key at
+// position s is x_{s-1}'s key code in the first half and x_{s-2}'s in the rest. Over the
+// positions s >= 2 of the document's finished user turns, the nearest key (the later on ties)
+// inside the head's margin (m > d 2^16); then the later of the heads' positions. Returns the
+// place + 1, or 0. Uniform.
+template <int Q>
+__device__ __forceinline__ uint32_t place_find(const DevModel &M, const Lds &S, uint32_t t,
+                                               uint32_t doc, uint32_t lane, const bool (&qv)[Q],
+                                               const uint32_t (&qi)[Q]) {
+  const DevHam &H = M.ham;
+  const DevHamRead &R = H.reads[H.p_read];
+  const uint32_t d = M.d, *tk = S.tok;
+  if (t < 1) return 0;
+#pragma unroll
+  for (int k = 0; k < Q; k++) {
+    if (!qv[k]) continue;
+    const uint32_t q = qi[k];
+    auto asked = [&](uint32_t v, int64_t (&o)[4]) {
+      ham_point(M, v, q, o);
+      const short4 a = *(const short4 *)(H.p_ask + (uint64_t)v * d + 4 * q);
+      o[0] += a.x;
+      o[1] += a.y;
+      o[2] += a.z;
+      o[3] += a.w;
+    };
+    int64_t p[4];
+    asked(tk[t], p);
+#pragma unroll
+    for (int c = 0; c < 4; c++) p[c] *= 65536;
+    if (H.p_carry) {
+      const uint32_t reach = H.p_carry_rows < t ? H.p_carry_rows : t;
+      for (uint32_t s = 1; s <= reach; s++) {
+        const uint32_t v = tk[t - s];
+        const int64_t gain = H.p_carry[v];
+        int64_t o[4];
+        asked(v, o);
+#pragma unroll
+        for (int c = 0; c < 4; c++) p[c] += gain * o[c];
+      }
+    }
+    S.hnib[q] = ham_nibble(R.ku + 4 * q, p);
+  }
+  wave_sync();
+  const uint64_t first = (1ull << (H.hw / 2)) - 1;
+  const uint32_t s0 = doc > 2 ? doc : 2u;
+  uint32_t found = 0;
+  for (uint32_t j = H.copy; j < H.heads; j++) {
+    const uint64_t q = (ham_word(S.hnib, j, H.hw) & first) | (ham_code(R, H.heads, tk[t - 1], j) & ~first);
+    uint32_t best = UINT32_MAX;
+    for (uint32_t s = s0 + lane; s < t; s += kWave) {
+      if (!S.uend[s]) continue;
+      const uint64_t key = (ham_code(R, H.heads, tk[s - 1], j) & first) |
+                           (ham_code(R, H.heads, tk[s - 2], j) & ~first);
+      const uint32_t k = (uint32_t)__popcll(q ^ key) << kPosBits | (kPosMask - s);
+      best = k < best ? k : best;
+    }
+    const uint32_t m = wave_reduce32(best, OpMin());
+    if (m != UINT32_MAX && (int64_t)R.margin[j] > ((int64_t)(m >> kPosBits) << 16)) {
+      const uint32_t s = kPosMask - (m & kPosMask);
+      found = s + 1 > found ? s + 1 : found;
+    }
+  }
+  return found;
+}
+
+// The register's step at row t (PlaceState::advance without a caller's asks,
+// fbs_snapshot.rs:2937-3090, with PlaceTurns::push :2801-2837): the step of the place held by
+// the row before, the turns, the arm at a reply's start, the find at an arming row of a user
+// turn's content, the stop at the reply's end mark, and the offer of an open reply row.
+template <int Q>
+__device__ __forceinline__ void place_advance(const DevModel &M, const Lds &S, uint32_t t,
+                                              uint32_t lane, const bool (&qv)[Q],
+                                              const uint32_t (&qi)[Q]) {
+  const DevHam &H = M.ham;
+  const uint32_t *tk = S.tok;
+  uint32_t *ps = S.pst;
+  uint32_t role = ps[kPlRole], start = ps[kPlStart], users = ps[kPlUsers];
+  uint32_t la = ps[kPlLastA], lb = ps[kPlLastB], doc = ps[kPlDoc];
+  uint32_t place = ps[kPlPlace], pend = ps[kPlEnd];
+  bool has = ps[kPlHas] != 0, over = ps[kPlOver] != 0, answered = ps[kPlAnswered] != 0;
+  const uint32_t at = ps[kPlOffer], token = tk[t], len = t + 1;
+  auto cls = [&](uint32_t v) -> uint32_t { return v < M.vocab ? (uint32_t)H.p_class[v] : 0u; };
+  // The step: the row before was offered the token at the place, and this token is it.
+  bool stepped = false;
+  if (at != kPlaceNone && has && at == place && token == tk[place]) {
+    const uint32_t next = place + 1;
+    if (next >= pend || (cls(tk[next]) & kPlaceStop)) {
+      has = false;
+    } else {
+      place = next;
+      stepped = true;
+    }
+  }
+  uint32_t pushed = 0;
+  if (token == H.p_bos) {  // the start mark forgets the document
+    has = false;
+    answered = false;
+    role = start = users = 0;
+    doc = len;
+  } else {
+    const uint32_t sl = H.p_len[0];
+    for (uint32_t r = 1; r <= 3 && !pushed; r++) {
+      const uint32_t ml = H.p_len[r];
+      if (!ml || ml > len) continue;
+      const uint32_t *mk = H.p_marks + r * kPlaceMarkMax;
+      bool ends = true;
+      for (uint32_t i = 0; i < ml; i++) ends = ends && tk[len - ml + i] == mk[i];
+      if (!ends) continue;
+      const uint32_t m = len - ml;
+      bool after = m >= sl;
+      for (uint32_t i = 0; i < sl && after; i++) after = tk[m - sl + i] == H.p_marks[i];
+      if (role == 0) {
+        if (!(m > 0 && (tk[m - 1] == H.p_bos || after))) continue;
+      } else {
+        if (!(after && m >= start + sl)) continue;
+        uint32_t b = m - sl;
+        if (b > start && tk[b - 1] == H.p_eos) b--;
+        if (role == 2) {
+          for (uint32_t s = start + lane; s < b; s += kWave) S.uend[s] = (uint16_t)b;
+          users++;
+          la = start;
+          lb = b;
+        }
+      }
+      role = r;
+      start = len;
+      pushed = r;
+    }
+  }
+  wave_sync();
+  if (pushed == 2) {  // a user turn's start clears the register
+    has = false;
+    answered = false;
+  } else if (pushed == 3) {  // a reply's start: the arm, once per user turn
+    over = false;
+    has = false;
+    const bool asked = users > 0 && !answered;
+    answered = true;
+    if (asked) {
+      uint32_t last = 0;  // the last arming row of the answered turn's content + 1
+      for (uint32_t r = la + lane; r < lb; r += kWave)
+        if (S.farm[r]) last = r + 1;
+      last = wave_reduce32(last, OpMax());
+      if (last) {
+        const uint32_t pos = (uint32_t)S.farm[last - 1] - 1u;
+        const uint32_t e = pos >= doc && pos < la ? (uint32_t)S.uend[pos] : 0u;
+        if (e) {
+          has = true;
+          place = pos;
+          pend = e;
+        }
+      }
+    }
+  }
+  uint32_t offer = kPlaceNone;
+  if (role == 2 && t >= start && users > 0) {
+    if (cls(token) & kPlaceArm) {
+      const uint32_t f = place_find<Q>(M, S, t, doc, lane, qv, qi);
+      if (f && lane == 0) S.farm[t] = (uint16_t)f;
+    }
+  } else if (role == 3) {
+    if (token == H.p_eos && t >= start) {
+      over = true;
+      has = false;
+    }
+    if (t + 1 >= start && !over && has && (stepped || (cls(token) & kPlaceOpen))) offer = place;
+  }
+  if (lane == 0) {
+    ps[kPlRole] = role;
+    ps[kPlStart] = start;
+    ps[kPlUsers] = users;
+    ps[kPlLastA] = la;
+    ps[kPlLastB] = lb;
+    ps[kPlDoc] = doc;
+    ps[kPlHas] = has;
+    ps[kPlPlace] = place;
+    ps[kPlEnd] = pend;
+    ps[kPlOffer] = offer;
+    ps[kPlOver] = over;
+    ps[kPlAnswered] = answered;
+  }
+  wave_sync();
+}
+
 // The stream read after `depth` layers (< the layer count) on the residual x, in place. `pay`:
 // the sequence's payload caches, [slot][context][d].
 template <int Q>
@@ -508,7 +728,23 @@ __device__ __forceinline__ void ham_readout(const DevModel &M, const DevHamRead 
                                             int64_t (&n)[Q][4]) {
   int64_t cm[Q][4];
   i128 ym[Q][4];
-  const bool has_c = ham_copy_mean<Q>(M, R, S, t, lane, qv, qi, cm);
+  // At a row the place read opens, the table's point of the token at the place, at
+  // 2^COPY_MEAN_EXP (a Q12 point at a Q31 weight of one), in place of the copy heads' mean
+  // (hamming.rs:1895-1899).
+  const uint32_t offer = M.ham.place ? S.pst[kPlOffer] : kPlaceNone;
+  bool has_c;
+  if (offer != kPlaceNone) {
+#pragma unroll
+    for (int k = 0; k < Q; k++) {
+      int64_t v[4] = {0, 0, 0, 0};
+      if (qv[k]) ham_point(M, S.tok[offer], qi[k], v);
+#pragma unroll
+      for (int c = 0; c < 4; c++) cm[k][c] = v[c] * ((int64_t)1 << 31);
+    }
+    has_c = true;
+  } else {
+    has_c = ham_copy_mean<Q>(M, R, S, t, lane, qv, qi, cm);
+  }
   bool has_y = false;
   if (R.typed) {
     int64_t *cache = R.ask ? nullptr : pay + (uint64_t)R.slot * M.context * M.d;

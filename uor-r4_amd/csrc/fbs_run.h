@@ -877,6 +877,10 @@ struct Lds {
   uint32_t *hhist;   // kHamBins: one head's distance histogram
   uint32_t *hwd;     // kHamBins: the Q31 weight of each distance under the head's margin
   uint32_t *hnib;    // d / 4: the sign nibbles of the row's point
+  // A model with a place read only (null otherwise): its register (fbs_hamming.h).
+  uint32_t *pst;     // kPlaceWords: the register's scalars
+  uint16_t *uend;    // context: the end of the finished user turn holding the position, or 0
+  uint16_t *farm;    // context: at a row whose token arms, the place its question found + 1
   // The part clocks' kernels only: [wave][kParts] cycle counters.
   uint64_t *clk;
 };
@@ -901,6 +905,8 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
   if (HM) {  // the read at this row needs x_0..=x_t (session.rs:4149-4152)
     if (lane == 0) S.tok[t] = tok;
     wave_sync();
+    // The place read's register moves on this token, before the row's readout (:4154-4162).
+    if (M.ham.place) place_advance<Q>(M, S, t, lane, qv, qi);
   }
   int32_t x[Q][4];
 #pragma unroll
@@ -1888,6 +1894,8 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
     S.tok = nullptr;
     S.hdist = nullptr;
     S.hpick = S.hwgt = S.hhist = S.hwd = S.hnib = nullptr;
+    S.pst = nullptr;
+    S.uend = S.farm = nullptr;
     if (HM) {  // ham_lds_bytes
       S.tok = (uint32_t *)(lds + at);
       at += M.context;
@@ -1902,6 +1910,16 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
       S.hwd = (uint32_t *)(lds + at);
       at += kHamBins;
       S.hnib = (uint32_t *)(lds + at);
+      at += M.d / 4;
+      if (M.ham.place) {  // place_lds_bytes
+        const uint32_t words = ((2u * M.context + 15u) & ~15u) / 4u;
+        S.pst = (uint32_t *)(lds + at);
+        at += kPlaceWords;
+        S.uend = (uint16_t *)(lds + at);
+        at += words;
+        S.farm = (uint16_t *)(lds + at);
+        at += words;
+      }
     }
     S.clk = nullptr;
     if (CLK) {  // clock_lds_bytes
@@ -2010,6 +2028,13 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
         S.tok[i] = v;
       }
       bad_stream = wave_reduce32(bad, OpMax()) != 0;
+      // The place read's register over the resumed tokens: the state their steps left (it
+      // depends on the tokens and the model alone).
+      if (M.ham.place) {
+        place_init(M, S, lane);
+        if (!bad_stream)
+          for (uint32_t r = 0; r < pos; r++) place_advance<Q>(M, S, r, lane, qv, qi);
+      }
       const uint64_t stride = (uint64_t)M.ham.slots * M.context * d;
       pay = A.out_payloads ? A.out_payloads + (uint64_t)sl * stride : A.pay + (uint64_t)blockIdx.x * stride;
       if (A.in_payloads && A.in_payloads != A.out_payloads)

@@ -43,11 +43,20 @@ class HammingReadS(C.Structure):
                 ("carry", C.POINTER(C.c_int32))]
 
 
+class PlaceS(C.Structure):
+    _fields_ = [("bos", C.c_uint32), ("eos", C.c_uint32), ("sep_len", C.c_uint32),
+                ("system_len", C.c_uint32), ("user_len", C.c_uint32), ("assistant_len", C.c_uint32),
+                ("sep", C.POINTER(C.c_uint32)), ("system", C.POINTER(C.c_uint32)),
+                ("user", C.POINTER(C.c_uint32)), ("assistant", C.POINTER(C.c_uint32)),
+                ("class_table", C.POINTER(C.c_int16))]
+
+
 class HammingS(C.Structure):
     _fields_ = [("heads", C.c_uint32), ("kept", C.c_uint32), ("copy_key", C.c_uint32),
                 ("copy_latest", C.c_uint32), ("copy_keys", C.POINTER(C.c_uint32)),
                 ("copy_longest", C.c_uint32), ("marker", C.c_uint32 * 2), ("rule", C.c_uint32),
-                ("read_count", C.c_uint32), ("reads", C.POINTER(HammingReadS))]
+                ("read_count", C.c_uint32), ("reads", C.POINTER(HammingReadS)),
+                ("place", C.POINTER(PlaceS))]
 
 
 class ExtS(C.Structure):
@@ -162,6 +171,16 @@ class Image:
                 H.rule = ham.rule
                 H.read_count = len(art.hamming_reads)
                 H.reads = C.cast(reads, C.POINTER(HammingReadS))
+                if ham.place is not None:
+                    pm, P = ham.place, PlaceS()
+                    P.bos, P.eos = pm.bos, pm.eos
+                    for name in ("sep", "system", "user", "assistant"):
+                        ids = np.asarray(getattr(pm, name), np.uint32)
+                        setattr(P, name + "_len", len(ids))
+                        setattr(P, name, ptr(arr(ids, np.uint32) if len(ids) else None, C.c_uint32))
+                    P.class_table = ptr(arr(art.hamming_place, np.int16), C.c_int16)
+                    keep.append(P)
+                    H.place = C.pointer(P)
                 keep.append(H)
                 e.hamming = C.pointer(H)
             self.ext = e

@@ -127,6 +127,7 @@ class ModelInfo:
     # Per Hamming read: whether it keeps a payload cache (type heads that bring a payload back,
     # payload_caches, hamming.rs:1678-1685).
     payload_reads: tuple = ()
+    place: bool = False  # a place read, whose register and turns a snapshot does not carry
 
     @staticmethod
     def of(art) -> "ModelInfo":
@@ -134,8 +135,10 @@ class ModelInfo:
         reads = getattr(art, "hamming_reads", None) or []
         d = s.width
         cached = tuple(bool(r.ask is None and np.any(np.asarray(r.weight)[d:] != 0)) for r in reads)
+        ham = getattr(art, "hamming", None)
         return ModelInfo(model_identity(art), s.vocab, s.width, s.layers, s.window, s.context,
-                         1, not s.raw_transition, getattr(art, "hamming", None) is not None, cached)
+                         1, not s.raw_transition, ham is not None, cached,
+                         ham is not None and ham.place is not None)
 
     @property
     def payload_slots(self) -> int:
@@ -180,6 +183,16 @@ def max_serialized_session_bytes(info: ModelInfo) -> int:
 def validate_restore(info: ModelInfo, saved: SerializedStackSession) -> None:
     """restore_state's checks (session.rs:2876-3090) for an FBS model, in the reference's order;
     raises SessionError and changes nothing."""
+    # A type-head session's payloads travel with it (session.rs:2894-2910); a snapshot without
+    # them, or with caches of other lengths, is refused.
+    if info.payload_slots:
+        want = [len(p) for p in info.payload_caches()]
+        if [len(p) for p in saved.hamming_payloads] != want:
+            raise SessionError("Shape", "a type-head session needs its per-position payloads, "
+                                        "which this snapshot does not carry")
+    if info.place:  # session.rs:2911-2919
+        raise SessionError("Shape", "a session of a place read cannot be restored yet: its register "
+                                    "and turns are not saved")
     if saved.schema != STACK_SESSION_SCHEMA:
         raise SessionError("Schema", f"expected {STACK_SESSION_SCHEMA}, found {saved.schema}")
     if saved.version != 1:
@@ -213,13 +226,6 @@ def validate_restore(info: ModelInfo, saved: SerializedStackSession) -> None:
             want = pos * (info.width // 4) * info.layers
             if len(saved.snap_trace) != want or any(not 0 <= r < 120 for r in saved.snap_trace):
                 raise SessionError("SessionState", "a snap trace of the wrong length or roots")
-    # A type-head session's payloads travel with it (session.rs:2894-2910); a snapshot without
-    # them, or with caches of other lengths, is refused.
-    if info.payload_slots:
-        want = [len(p) for p in info.payload_caches()]
-        if [len(p) for p in saved.hamming_payloads] != want:
-            raise SessionError("Shape", "a type-head session needs its per-position payloads, "
-                                        "which this snapshot does not carry")
     for layer in saved.layers:
         if not isinstance(layer, RecurrenceLayer):
             raise SessionError("SessionState", "a read layer's cache for a recurrence layer")

@@ -88,6 +88,47 @@ def lcg(seed: int) -> Lcg:
     return g
 
 
+PLACE_STOP, PLACE_ARM, PLACE_OPEN = 1, 2, 4  # fbs_snapshot.rs:2762-2766
+PLACE_MARK_MAX = 16  # ids a marker list may hold on this build
+
+
+@dataclass(frozen=True)
+class PlaceMarks:
+    """The ids that frame a conversation for the place read (PlaceMarks, fbs_snapshot.rs:2725-
+    2732): the document's start and end marks, the turn separator and the three role markers."""
+
+    bos: int
+    eos: int
+    sep: tuple
+    system: tuple
+    user: tuple
+    assistant: tuple
+
+    def check(self, vocab: int) -> str | None:
+        """PlaceMarks::check (fbs_snapshot.rs:2741-2761): the reason marks are refused, or None.
+        This build also refuses a marker list over PLACE_MARK_MAX ids."""
+        lists = (self.sep, self.system, self.user, self.assistant)
+        if any(not 0 <= int(i) < vocab for i in (self.bos, self.eos, *[x for l in lists for x in l])):
+            return "a place read's mark is outside the vocabulary"
+        if not self.sep or not self.user or not self.assistant:
+            return "a place read needs a separator, a user marker and an assistant marker"
+        if self.bos == self.eos:
+            return "a place read's start mark and end mark are one token"
+        roles = (tuple(self.system), tuple(self.user), tuple(self.assistant))
+        for i, a in enumerate(roles):
+            for j, b in enumerate(roles):
+                if i != j and b and len(a) >= len(b) and a[len(a) - len(b):] == b:
+                    return "one of a place read's role markers ends with another"
+        if any(len(l) > PLACE_MARK_MAX for l in lists):
+            return f"a place read's marker list holds more than {PLACE_MARK_MAX} ids on this build"
+        return None
+
+    def to_json(self) -> dict:
+        return dict(bos=int(self.bos), eos=int(self.eos), sep=[int(x) for x in self.sep],
+                    system=[int(x) for x in self.system], user=[int(x) for x in self.user],
+                    assistant=[int(x) for x in self.assistant])
+
+
 @dataclass(frozen=True)
 class HammingSpec:
     """Seeded Hamming reads of a lut-stack/6 stack (StackHamming, stack/format.rs:229-292)."""
@@ -104,6 +145,7 @@ class HammingSpec:
     typed: bool = True            # nonzero type weights w_y (type heads served)
     margin_bits: tuple = (2, 12)  # margins drawn in this many bits (at Q16)
     rule: int = 0xFFFFFFFF        # the copy rule served (UOR_FBS_COPY_*; default: the artifact's)
+    place: PlaceMarks | None = None  # the readout read's place read (its read must ask)
 
 
 @dataclass(frozen=True)
@@ -188,6 +230,9 @@ class Artifact:
     # The Hamming reads (lut-stack/6): the record's fields and one HammingRead per depth.
     hamming: HammingSpec | None = None
     hamming_reads: list | None = None
+    # The place read's class table (vocab i16: PLACE_STOP | PLACE_ARM | PLACE_OPEN), with
+    # hamming.place.
+    hamming_place: np.ndarray | None = None
 
     @property
     def window(self) -> int:
@@ -319,7 +364,20 @@ def make_artifact(spec: Spec, seed: int) -> Artifact:
         art.drawer_offsets, art.drawer_members = offsets, members
     if spec.hamming is not None:
         art.hamming, art.hamming_reads = spec.hamming, _hamming_reads(g, spec)
+        if spec.hamming.place is not None:
+            art.hamming_place = place_classes(g, spec.vocab, spec.hamming.place)
     return art
+
+
+def place_classes(g: Lcg, vocab: int, marks: PlaceMarks) -> np.ndarray:
+    """A seeded class table: each entry stops with probability 1/8, arms with 1/16 and opens
+    with 1/8 (independently); the marks themselves have no class."""
+    r = g.take(vocab)
+    cls = (np.where(r % np.uint64(8) == 0, PLACE_STOP, 0) | np.where((r >> np.uint64(3)) % np.uint64(16) == 0, PLACE_ARM, 0)
+           | np.where((r >> np.uint64(7)) % np.uint64(8) == 0, PLACE_OPEN, 0)).astype(np.int16)
+    for i in (marks.bos, marks.eos, *marks.sep, *marks.system, *marks.user, *marks.assistant):
+        cls[int(i)] = 0
+    return cls
 
 
 def _hamming_reads(g: Lcg, spec: Spec) -> list:

@@ -34,7 +34,8 @@ import struct
 import numpy as np
 
 from . import tables
-from .synth import Artifact, HammingRead, HammingSpec, Layer, Spec
+from .synth import (PLACE_ARM, PLACE_OPEN, PLACE_STOP, Artifact, HammingRead, HammingSpec, Layer,
+                    PlaceMarks, Spec)
 
 MAGIC = b"UORLUT01"
 ALIGN = 64                 # format.rs:443
@@ -137,13 +138,22 @@ def _check_shape(header: dict) -> dict:
     return s
 
 
+def _place_marks(rec) -> PlaceMarks:
+    """The record's `place` marks (PlaceMarks, fbs_snapshot.rs:2725-2732, deny_unknown_fields)."""
+    fields = {"bos", "eos", "sep", "system", "user", "assistant"}
+    if not isinstance(rec, dict) or set(rec) != fields:
+        raise UorlutError(f"hamming.place: the fields are {sorted(fields)}")
+    try:
+        lists = {k: tuple(int(x) for x in rec[k]) for k in ("sep", "system", "user", "assistant")}
+        return PlaceMarks(bos=int(rec["bos"]), eos=int(rec["eos"]), **lists)
+    except (TypeError, ValueError):
+        raise UorlutError("hamming.place: marks are vocabulary ids") from None
+
+
 def _check_hamming(rec: dict, s: dict) -> HammingSpec:
-    """`StackHamming::check` (format.rs:336-430) on the header's record; the place read is not
-    served by this path."""
+    """`StackHamming::check` (format.rs:336-430) on the header's record."""
     if not isinstance(rec, dict) or set(rec) - HAMMING_FIELDS:
         raise UorlutError(f"hamming: unknown fields {sorted(set(rec) - HAMMING_FIELDS)}")
-    if rec.get("place") is not None:
-        raise UorlutError("the Hamming place read (hamming.place) is not served by this path")
     missing = {"heads", "depths", "kept", *HAMMING_EXPS} - set(rec)
     if missing:
         raise UorlutError(f"hamming: missing fields {sorted(missing)}")
@@ -191,12 +201,45 @@ def _check_hamming(rec: dict, s: dict) -> HammingSpec:
             raise UorlutError("a Hamming question carry needs its read to ask")
         if not 1 <= reach <= ASK_CARRY_MAX:
             raise UorlutError("a Hamming question carry reaches from 1 to ASK_CARRY_MAX rows")
+    place = rec.get("place")
+    if place is not None:
+        place = _place_marks(place)
+        if depths[-1] != L or not (asks and asks[-1]):
+            raise UorlutError("a Hamming place read is served on a readout read that asks")
+        if hw % 8:
+            raise UorlutError("a Hamming place read needs heads of whole 8-coordinate blocks, so "
+                              "each half is whole lanes")
+        why = place.check(V)
+        if why:
+            raise UorlutError(why)
     for k, v in HAMMING_EXPS.items():
         if rec.get(k) != v:
             raise UorlutError("the Hamming read's exponents are not this engine's")
     return HammingSpec(heads=heads, depths=tuple(depths), kept=kept, copy_key=copy_key,
                        copy_keys=None if keys is None else tuple(keys), copy_latest=latest,
-                       copy_longest=longest, asks=asks, carry_rows=reach or 0)
+                       copy_longest=longest, asks=asks, carry_rows=reach or 0, place=place)
+
+
+def _place_classes(h: HammingSpec, tabs: dict, V: int) -> np.ndarray | None:
+    """The readout read's `hamming.d{depth}.place` class table (PlaceImage::checked,
+    fbs_snapshot.rs:2779-2790), present exactly when the record carries the marks
+    (hamming.rs:113-122)."""
+    name = f"hamming.d{h.depths[-1]}.place"
+    if h.place is None:
+        if name in tabs:
+            raise UorlutError(f"{name}: present, but the record names no place read")
+        return None
+    if name not in tabs:
+        raise UorlutError(f"missing section {name}")
+    t = tabs[name]
+    if t.dtype != KINDS["i16"]:
+        raise UorlutError(f"{name}: {t.dtype} values, expected i16")
+    if len(t) != V:
+        raise UorlutError(f"the place read's class table has {len(t)} entries for a vocabulary of {V}")
+    cls = np.asarray(t, np.int16)
+    if np.any(cls & ~np.int16(PLACE_STOP | PLACE_ARM | PLACE_OPEN)):
+        raise UorlutError("the place read's class table has a bit outside stop, arm and open")
+    return cls
 
 
 def _hamming_reads(h: HammingSpec, tabs: dict, V: int, d: int, context: int) -> list:
@@ -246,6 +289,8 @@ def add_hamming(source, h: HammingSpec, reads: list) -> bytes:
     header, _ = parse(data)
     if header.get("hamming") is not None:
         raise UorlutError("the container already has Hamming reads")
+    if h.place is not None:
+        raise UorlutError("a place read is added after the reads (add_hamming_place)")
     (declared,) = struct.unpack("<Q", data[8:16])
     end = 16 + declared
     body = bytearray(data[end + (ALIGN - end % ALIGN) % ALIGN:])
@@ -345,4 +390,45 @@ def load(source) -> Artifact:
     if header.get("hamming") is not None:
         art.hamming = _check_hamming(header["hamming"], s)
         art.hamming_reads = _hamming_reads(art.hamming, tabs, V, d, int(s["context"]))
+        art.hamming_place = _place_classes(art.hamming, tabs, V)
     return art
+
+
+def add_hamming_place(source, marks: PlaceMarks, classes) -> bytes:
+    """A Hamming stack whose readout read asks, with the place read added
+    (add_hamming_place_uorlut01, format.rs:2780-2819): every section byte for byte, then
+    `hamming.d{depth}.place` (i16 classes of the vocabulary) on the readout read, the record's
+    `place` carrying the marks. Refused: a stack without Hamming reads or with a place read
+    already, marks or classes PlaceImage::checked refuses, and a readout read that does not ask.
+    The result is read back."""
+    data = bytes(source if isinstance(source, (bytes, bytearray)) else open(source, "rb").read())
+    header, _ = parse(data)
+    rec = header.get("hamming")
+    if rec is None:
+        raise UorlutError("a place read is added to a stack with Hamming reads")
+    if rec.get("place") is not None:
+        raise UorlutError("a place read is added to a stack without one")
+    V = int(header["shape"]["vocab"])
+    cls = np.asarray(classes, np.int16)
+    why = marks.check(V)
+    if why:
+        raise UorlutError(why)
+    if len(cls) != V:
+        raise UorlutError(f"the place read's class table has {len(cls)} entries for a vocabulary of {V}")
+    if np.any(cls & ~np.int16(PLACE_STOP | PLACE_ARM | PLACE_OPEN)):
+        raise UorlutError("the place read's class table has a bit outside stop, arm and open")
+    (declared,) = struct.unpack("<Q", data[8:16])
+    end = 16 + declared
+    body = bytearray(data[end + (ALIGN - end % ALIGN) % ALIGN:])
+    body += b"\0" * ((ALIGN - len(body) % ALIGN) % ALIGN)
+    raw = cls.tobytes()
+    name = f"hamming.d{int(rec['depths'][-1])}.place"
+    tables_ = list(header["tables"]) + [{"name": name, "kind": "i16", "len": int(cls.size),
+                                         "span": {"offset": len(body), "bytes": len(raw)}}]
+    body += raw
+    header = dict(header, tables=tables_, hamming=dict(rec, place=marks.to_json()))
+    hb = json.dumps(header).encode()
+    out = MAGIC + struct.pack("<Q", len(hb)) + hb
+    out += b"\0" * ((ALIGN - len(out) % ALIGN) % ALIGN) + bytes(body)
+    load(out)
+    return out
