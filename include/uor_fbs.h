@@ -392,6 +392,33 @@ int uor_fbs_serve_slots_stream_async(uor_fbs_handle *handle, const uint32_t *slo
                                      void *cache, uint32_t *out_kept, int32_t *out_query,
                                      int32_t *status, void *hip_stream);
 
+/* The Hamming trace and Q5's decision trace with the forced replay, teacher-forced from fresh
+ * sessions: set_hamming_trace / take_hamming_trace (session.rs:2361-2370, HammingStepRead
+ * hamming.rs:1378-1395, `record` :1787-1814) and set_decision_trace / take_decision_trace
+ * (session.rs:2438-2515, DecisionStep fbs_snapshot.rs:643-703, ForcedBucket / ForcedCode
+ * :754-797, BucketTrace::decide session.rs:2192-2215), as `fbs-toks --forced --decision-trace`
+ * runs windows. Every position of `sequences` rows of `len` tokens gets a record of
+ * uor_fbs_decision_stride(handle, decisions) bytes in `out_trace`:
+ * - with `decisions`: each layer's rate scores clamp(decay + offset, 0, 2^16) (i32 [layer][lane],
+ *   lane = width / 4) and the entries used (u8 [layer][lane]), padded to 8 bytes;
+ * - then each Hamming read in depth order, each head it serves (the copy heads, then the type
+ *   heads where the read serves them): the query code (u64), the key code at the row (u64, 0 at
+ *   row 0), the kept count (u32) and the kept positions (u32 each, `kept` of them; the nearest by
+ *   distance then position, or the rule's one position), padded to 8 bytes.
+ * The forced replay (NULL: nothing forced): `force_buckets` [sequence][step][layer][lane] (255:
+ * the score's own entry, else 0..15; needs `decisions`), `force_codes` [sequence][step][read]
+ * [head][2] (the query, the key) with `force_mask` [sequence][step][read][head] (bit 0: the
+ * query is forced at that step, bit 1: the key, which every later row reads for that candidate).
+ * Refused as the reference refuses them: the decision trace on a snapped artifact or one whose
+ * head is not the nearest; a forced bucket entry past 15; a forced code on a model without
+ * Hamming reads, on a head its read does not serve, a key at step 0, or with a place read.
+ * `out_tokens` and `out_query` (NULL: not wanted) as uor_fbs_sequences'. Host buffers. */
+uint64_t uor_fbs_decision_stride(const uor_fbs_handle *handle, uint32_t decisions);
+int uor_fbs_decision_sequences(uor_fbs_handle *handle, const uint32_t *tokens, uint32_t sequences,
+                               uint32_t len, uint32_t decisions, const uint8_t *force_buckets,
+                               const uint64_t *force_codes, const uint8_t *force_mask,
+                               uint32_t *out_tokens, int32_t *out_query, uint8_t *out_trace);
+
 /* Teacher-forced next-token scoring: for each row of `len` tokens, position t's choice is
  * compared with row[t+1] (t < len-1); `out_matches` gets the total count of equal pairs.
  * `out_argmin` (nullable) gets every position's choice, rows*len. Host buffers. */

@@ -522,6 +522,44 @@ typedef struct {
   uint32_t d;
 } Pick;
 
+/* The Hamming trace and Q5's forced replay at one step (session.rs:2361-2370, 2438-2520;
+ * hamming.rs:1378-1421, 1686-1740, 1787-1814): the sequence's forced codes and this position's
+ * trace record. NULL members: nothing forced, nothing recorded. */
+typedef struct {
+  const uint64_t *codes;  /* [len][reads][heads][2]: the forced query and key of each head */
+  const uint8_t *mask;    /* [len][reads][heads]: bit 0 the query is forced, bit 1 the key */
+  uint32_t reads, heads;
+  uint8_t *rec;           /* this position's record (fbs_oracle_decision_stride bytes) */
+  size_t reads_at;        /* the reads' part of the record */
+  const uint8_t *buckets; /* this position's forced rate buckets [L][lanes], 255: none */
+  int decisions;          /* record the rate buckets */
+} Tr;
+
+static size_t tr_head_bytes(uint32_t kept) { return (20 + 4 * (size_t)kept + 7) & ~(size_t)7; }
+
+static int tr_forced(const Tr *tr, uint32_t ri, uint32_t head, size_t step, int role, uint64_t *code) {
+  if (!tr || !tr->mask) return 0;
+  size_t at = ((size_t)step * tr->reads + ri) * tr->heads + head;
+  if (!(tr->mask[at] & (1u << role))) return 0;
+  *code = tr->codes[2 * at + (size_t)role];
+  return 1;
+}
+
+/* Head record: query u64, key u64, the kept count u32 and the kept positions u32 (the order
+ * `nearest` and the rules keep them). */
+static void tr_record(const Tr *tr, size_t off, uint64_t query, uint64_t key, const Pick *picks,
+                      size_t n) {
+  uint8_t *p = tr->rec + off;
+  memcpy(p, &query, 8);
+  memcpy(p + 8, &key, 8);
+  uint32_t c = (uint32_t)n;
+  memcpy(p + 16, &c, 4);
+  for (size_t k = 0; k < n; k++) {
+    uint32_t v = (uint32_t)picks[k].s;
+    memcpy(p + 20 + 4 * k, &v, 4);
+  }
+}
+
 static i128 shl128(i128 v, uint32_t s) { return (i128)((u128)v << s); }
 
 /* `round_shift` (:1353-1360): v / 2^s rounded half away from zero. */
@@ -610,15 +648,22 @@ static size_t ham_nearest(uint64_t query, size_t t, uint32_t kept, const uint64_
  * (`choose_ruled` :356-371, `latest_of` :584-598, `longest_of` :601-615, `longer_at` :349-352);
  * `opening` is the caller's reply mark (this build passes none). */
 static size_t ham_copy_choose(const Ham *h, const HR *r, uint32_t head, const uint32_t *tok,
-                              size_t t, int opening, uint64_t *key, Pick *out) {
+                              size_t t, int opening, uint64_t *key, Pick *out, const Tr *tr,
+                              uint32_t ri, uint64_t *query_used) {
   uint32_t rule = h->rule;
   if (rule == UOR_FBS_COPY_LONGEST_AFTER_OPENING) {
     int opens = h->has_marker ? (t >= 1 && tok[t - 1] == h->marker[0] && tok[t] == h->marker[1])
                               : opening;
     rule = opens ? UOR_FBS_COPY_LATEST_EXACT : UOR_FBS_COPY_LONGEST_EXACT;
   }
+  /* `choose_forced` (:450-466): a forced query replaces the row's, a forced key candidate s's. */
   uint64_t q = ham_joined(h, r, tok[t], tok[t ? t - 1 : 0], head);
-  for (size_t s = 1; s < t; s++) key[s] = ham_joined(h, r, tok[s - 1], tok[s >= 2 ? s - 2 : 0], head);
+  tr_forced(tr, ri, head, t, 0, &q);
+  *query_used = q;
+  for (size_t s = 1; s < t; s++) {
+    key[s] = ham_joined(h, r, tok[s - 1], tok[s >= 2 ? s - 2 : 0], head);
+    tr_forced(tr, ri, head, s, 1, &key[s]);
+  }
   if (rule == UOR_FBS_COPY_MEAN) return ham_nearest(q, t, h->kept, key, out);
   if (rule == UOR_FBS_COPY_LATEST_EXACT || rule == UOR_FBS_COPY_LATEST_NEAREST) {
     size_t best = 0;
@@ -678,16 +723,27 @@ static uint32_t ham_head_sum(const Brought *b, const Pick *picks, size_t n, int3
 
 /* The copy heads' mean at row t (`CopyHeads::mean_at` :482-504): returns 0 when no head found a
  * position inside its margin. */
-static int ham_copy_mean(const O *o, const HR *r, const uint32_t *tok, size_t t, i128 *c) {
+static int ham_copy_mean(const O *o, const HR *r, const uint32_t *tok, size_t t, i128 *c,
+                         const Tr *tr, uint32_t ri, size_t rec_at) {
   const Ham *h = o->ham;
   uint32_t d = o->d, found = 0;
   i128 *head = malloc(sizeof(i128) * d);
-  uint64_t *key = malloc(sizeof(uint64_t) * (t + 1));
+  uint64_t *key = malloc(sizeof(uint64_t) * (t + 2));
   Pick *picks = malloc(sizeof(Pick) * (h->kept + 1));
   for (uint32_t i = 0; i < d; i++) c[i] = 0;
   Brought b = {o, tok, NULL};
   for (uint32_t k = 0; k < h->copy; k++) {
-    size_t n = ham_copy_choose(h, r, k, tok, t, 0, key, picks);
+    uint64_t q;
+    size_t n = ham_copy_choose(h, r, k, tok, t, 0, key, picks, tr, ri, &q);
+    if (tr && tr->rec) {
+      /* The record (`record` :1787-1814): the key at t is x_{t-1}'s code (0 at row 0). */
+      uint64_t kt = 0;
+      if (t > 0) {
+        kt = ham_joined(h, r, tok[t - 1], tok[t >= 2 ? t - 2 : 0], k);
+        tr_forced(tr, ri, k, t, 1, &kt);
+      }
+      tr_record(tr, rec_at + k * tr_head_bytes(h->kept), q, kt, picks, n);
+    }
     uint32_t count = ham_head_sum(&b, picks, n, r->r->margin[k], head);
     if (!count) continue;
     found++;
@@ -724,9 +780,11 @@ static void ham_asked_point(const O *o, const HR *r, const uint32_t *tok, size_t
  * is kept at row t first, the query codes are `point`'s through the query rotation and the kept
  * positions' payloads come back (at the point's exponent minus 31). */
 static int ham_type_mean(const O *o, const HR *r, const uint32_t *tok, size_t t,
-                         const int64_t *point, int64_t *payloads, i128 *y) {
+                         const int64_t *point, int64_t *payloads, i128 *y, const Tr *tr,
+                         size_t rec_at) {
   const Ham *h = o->ham;
   uint32_t d = o->d, found = 0, types = h->heads - h->copy;
+  const uint32_t ri = (uint32_t)(r - h->reads);
   int64_t *asked = NULL;
   if (r->asks) {
     asked = malloc(sizeof(int64_t) * d);
@@ -739,15 +797,27 @@ static int ham_type_mean(const O *o, const HR *r, const uint32_t *tok, size_t t,
     }
   }
   i128 *head = malloc(sizeof(i128) * d);
-  uint64_t *key = malloc(sizeof(uint64_t) * (t + 1));
+  uint64_t *key = malloc(sizeof(uint64_t) * (t + 2));
   Pick *picks = malloc(sizeof(Pick) * (h->kept + 1));
   for (uint32_t i = 0; i < d; i++) y[i] = 0;
   Brought b = {o, tok, r->asks ? NULL : payloads};
   for (uint32_t j = 0; j < types; j++) {
     uint64_t query = r->asks ? head_code(r->ku, asked, h->copy + j, h->hw)
                              : head_code(r->qu, point, h->copy + j, h->hw);
-    for (size_t s = 1; s < t; s++) key[s] = ham_code(r, tok[s - 1], h->copy + j);
+    tr_forced(tr, ri, h->copy + j, t, 0, &query);
+    for (size_t s = 1; s < t; s++) {
+      key[s] = ham_code(r, tok[s - 1], h->copy + j);
+      tr_forced(tr, ri, h->copy + j, s, 1, &key[s]);
+    }
     size_t n = ham_nearest(query, t, h->kept, key, picks);
+    if (tr && tr->rec) {
+      uint64_t kt = 0;
+      if (t > 0) {
+        kt = ham_code(r, tok[t - 1], h->copy + j);
+        tr_forced(tr, ri, h->copy + j, t, 1, &kt);
+      }
+      tr_record(tr, rec_at + (h->copy + j) * tr_head_bytes(h->kept), query, kt, picks, n);
+    }
     uint32_t count = ham_head_sum(&b, picks, n, r->r->margin[h->copy + j], head);
     if (!count) continue;
     found++;
@@ -763,19 +833,31 @@ static int ham_type_mean(const O *o, const HR *r, const uint32_t *tok, size_t t,
 }
 
 /* The stream read after `depth` layers on the residual x (ServedHamming::stream :1831-1866). */
+/* The record offset of read ri's heads: after the buckets, each earlier read's served heads. */
+static size_t tr_read_at(const O *o, const Tr *tr, uint32_t ri) {
+  const Ham *h = o->ham;
+  size_t at = tr->reads_at;
+  for (uint32_t i = 0; i < ri; i++)
+    at += (h->copy + (h->reads[i].typed ? h->heads - h->copy : 0)) * tr_head_bytes(h->kept);
+  return at;
+}
+
 static void ham_stream(const O *o, uint32_t depth, const uint32_t *tok, size_t t, int32_t *x,
-                       int64_t *payloads) {
+                       int64_t *payloads, const Tr *tr) {
   const Ham *h = o->ham;
   if (depth == o->L || h->at[depth] < 0) return;
-  const HR *r = &h->reads[h->at[depth]];
+  const uint32_t ri = (uint32_t)h->at[depth];
+  const HR *r = &h->reads[ri];
+  const size_t rec_at = tr && tr->rec ? tr_read_at(o, tr, ri) : 0;
   uint32_t d = o->d;
   i128 *c = malloc(sizeof(i128) * d), *y = malloc(sizeof(i128) * d);
-  int has_c = h->copy ? ham_copy_mean(o, r, tok, t, c) : 0, has_y = 0;
+  int has_c = h->copy ? ham_copy_mean(o, r, tok, t, c, tr, ri, rec_at) : 0, has_y = 0;
   if (r->typed) {
     int64_t *point = malloc(sizeof(int64_t) * d);
     for (uint32_t i = 0; i < d; i++) point[i] = x[i];
     has_y = ham_type_mean(o, r, tok, t, point,
-                          r->slot >= 0 ? payloads + (size_t)r->slot * o->m->context * d : NULL, y);
+                          r->slot >= 0 ? payloads + (size_t)r->slot * o->m->context * d : NULL, y,
+                          tr, rec_at);
     free(point);
     if (has_y && r->asks)
       for (uint32_t i = 0; i < d; i++) y[i] = shl128(y[i], STREAM_COPY_RAISE);
@@ -792,22 +874,27 @@ static void ham_stream(const O *o, uint32_t depth, const uint32_t *tok, size_t t
  * 2^COPY_MEAN_EXP (a Q12 point at a Q31 weight of one), is the copy term in place of the copy
  * heads' mean (:1895-1899). */
 static void ham_readout(const O *o, const uint32_t *tok, size_t t, int64_t *n, int64_t *payloads,
-                        long offer) {
+                        long offer, const Tr *tr) {
   const Ham *h = o->ham;
   if (h->at[o->L] < 0) return;
-  const HR *r = &h->reads[h->at[o->L]];
+  const uint32_t ri = (uint32_t)h->at[o->L];
+  const HR *r = &h->reads[ri];
+  const size_t rec_at = tr && tr->rec ? tr_read_at(o, tr, ri) : 0;
   uint32_t d = o->d;
   i128 *c = malloc(sizeof(i128) * d), *y = malloc(sizeof(i128) * d);
   int has_c = 0, has_y = 0;
   if (offer >= 0) {
+    /* The trace records the copy heads' choices at an open row too (`record` runs first). */
+    if (tr && tr->rec && h->copy) ham_copy_mean(o, r, tok, t, c, tr, ri, rec_at);
     for (uint32_t i = 0; i < d; i++) c[i] = shl128((i128)row_value(o, tok[offer], i), 31);
     has_c = 1;
   } else if (h->copy) {
-    has_c = ham_copy_mean(o, r, tok, t, c);
+    has_c = ham_copy_mean(o, r, tok, t, c, tr, ri, rec_at);
   }
   if (r->typed)
     has_y = ham_type_mean(o, r, tok, t, n,
-                          r->slot >= 0 ? payloads + (size_t)r->slot * o->m->context * d : NULL, y);
+                          r->slot >= 0 ? payloads + (size_t)r->slot * o->m->context * d : NULL, y,
+                          tr, rec_at);
   if (has_c || has_y)
     for (uint32_t i = 0; i < d; i++) {
       const i128 *ci = has_c ? &c[i] : NULL;
@@ -1145,6 +1232,7 @@ typedef struct {
   uint8_t *trace;    /* this step's snap trace (layers * (2 lanes + mlp / 4) bytes), or NULL */
   Place place;       /* the place read's register and turns (session.rs:2239-2241) */
   long held, offer;  /* the register after the last step (last_place, session.rs:2626-2631) */
+  Tr *tr;            /* the traces and forced replay of this step, or NULL */
 } S;
 
 static void session_alloc(const O *o, S *s) {
@@ -1227,6 +1315,15 @@ static int32_t recurrence(const O *o, uint32_t l, int64_t *state, int32_t *hist,
     if (sq > 65536) sq = 65536;
     uint32_t idx = (uint32_t)sq >> 12;
     if (idx > 15) idx = 15;
+    /* Q5's decision trace (BucketTrace::decide, session.rs:2192-2215): a forced entry replaces
+     * the score's; the score and the entry used are recorded. */
+    if (s->tr && s->tr->decisions) {
+      const size_t at = (size_t)l * o->lanes + lane;
+      if (s->tr->buckets && s->tr->buckets[at] != 255) idx = s->tr->buckets[at];
+      int32_t score = sq;
+      memcpy(s->tr->rec + 4 * at, &score, 4);
+      s->tr->rec[(size_t)4 * o->L * o->lanes + at] = (uint8_t)idx;
+    }
     uint64_t lambda = 1ull << (30 - idx), keep = m->keep_q31[idx];
     int64_t t[4];
     uint32_t root = serve_rotation(m->icosian, m->raw_transition, rot + 4 * lane, lambda, ROTATION_EPSILON, t);
@@ -1310,11 +1407,12 @@ static int step(const O *o, S *s, uint32_t token, uint32_t *out_token) {
     act_exp = quantize16(s->scratch, o->mlp, PRODUCT_EXP, s->act);
     gather16(&ly->mlp_down, s->act, act_exp, s->proj);
     for (uint32_t i = 0; i < d; i++) s->x[i] = sat_add32(s->x[i], s->proj[i]);
-    if (o->ham) ham_stream(o, l + 1, s->tokens, t, s->x, s->payloads);
+    if (o->ham) ham_stream(o, l + 1, s->tokens, t, s->x, s->payloads, s->tr);
   }
   rms_norm_fine(s->x, d, m->eps_mantissa, m->eps_exp, s->scratch);
   for (uint32_t i = 0; i < d; i++) s->normed[i] = grid_apply(s->scratch[i], m->final_gain[i]);
-  if (o->ham) ham_readout(o, s->tokens, t, s->normed, s->payloads, o->ham->place ? s->offer : -1);
+  if (o->ham)
+    ham_readout(o, s->tokens, t, s->normed, s->payloads, o->ham->place ? s->offer : -1, s->tr);
   for (uint32_t i = 0; i < d; i++) {
     int32_t q = to_exp_i32(s->normed[i], NORM_FINE_EXP, Q12_EXP);
     s->query[i] = q > 32767 ? 32767 : q < -32768 ? -32768 : q;
@@ -1350,6 +1448,12 @@ typedef struct {
   uint64_t matches;
   uint8_t *out_trace; /* sequences: every position's snap trace */
   int64_t *out_place; /* sequences: every position's (held, offered) place, -1 for none */
+  uint8_t *out_dtrace;          /* sequences: every position's decision / Hamming trace record */
+  size_t dstride;               /* its bytes a position */
+  int decisions;                /* record the rate buckets */
+  const uint8_t *force_buckets; /* [n][len][L][lanes], 255: not forced */
+  const uint64_t *force_codes;  /* [n][len][reads][heads][2] */
+  const uint8_t *force_mask;    /* [n][len][reads][heads] */
   int slide;
   int tid, threads, status;
 } Job;
@@ -1372,6 +1476,21 @@ static void *run_job(void *arg) {
       for (uint32_t t = 0; t < j->len; t++) {
         uint32_t tok;
         s.trace = j->out_trace ? j->out_trace + (i * j->len + t) * stride : NULL;
+        Tr tr;
+        s.tr = NULL;
+        if (j->out_dtrace) {
+          const uint32_t nr = o->ham ? o->ham->n : 0, nh = o->ham ? o->ham->heads : 0;
+          const size_t lanes = (size_t)o->L * o->lanes;
+          tr.codes = j->force_codes ? j->force_codes + i * j->len * nr * nh * 2 : NULL;
+          tr.mask = j->force_mask ? j->force_mask + i * j->len * nr * nh : NULL;
+          tr.reads = nr;
+          tr.heads = nh;
+          tr.rec = j->out_dtrace + (i * j->len + t) * j->dstride;
+          tr.reads_at = j->decisions ? (5 * lanes + 7) & ~(size_t)7 : 0;
+          tr.buckets = j->force_buckets ? j->force_buckets + (i * j->len + t) * lanes : NULL;
+          tr.decisions = j->decisions;
+          s.tr = &tr;
+        }
         int err = step(o, &s, row[t], &tok);
         if (err) {
           j->status = err;
@@ -1603,9 +1722,9 @@ int fbs_oracle_hamming_row(const uor_fbs_model *m, const uor_fbs_ext *ext, uint3
   resolve(&o, m, ext);
   if (!o.ham) return UOR_FBS_ERR_ARGUMENT;
   if (depth < o.L)
-    ham_stream(&o, depth, tok, t, x, payloads);
+    ham_stream(&o, depth, tok, t, x, payloads, NULL);
   else
-    ham_readout(&o, tok, t, n, payloads, -1);
+    ham_readout(&o, tok, t, n, payloads, -1, NULL);
   unresolve(&o);
   return 0;
 }
@@ -1788,4 +1907,51 @@ int64_t fbs_oracle_place_pick(const uint64_t *queries, const int32_t *margins, u
   free(ra);
   free(rb);
   return found;
+}
+
+/* ------------------------------------------------------------------------------------------
+ * The Hamming trace and Q5's decision trace with forced replay (session.rs:2361-2370,
+ * 2438-2520), teacher-forced from fresh sessions. A position's record: with `decisions`, each
+ * layer's rate scores (i32, [L][lanes]) and entries used (u8, [L][lanes]), padded to 8 bytes;
+ * then each read in depth order, each served head (the copy heads, then the type heads where the
+ * read serves them): the query (u64), the key at the row (u64, 0 at row 0), the kept count (u32)
+ * and the kept positions (u32 each, `kept` of them), padded to 8 bytes. */
+uint64_t fbs_oracle_decision_stride(const uor_fbs_model *m, const uor_fbs_ext *ext, int decisions) {
+  O o;
+  resolve(&o, m, ext);
+  size_t at = decisions ? (5 * (size_t)o.L * o.lanes + 7) & ~(size_t)7 : 0;
+  if (o.ham)
+    for (uint32_t i = 0; i < o.ham->n; i++)
+      at += (o.ham->copy + (o.ham->reads[i].typed ? o.ham->heads - o.ham->copy : 0)) *
+            tr_head_bytes(o.ham->kept);
+  unresolve(&o);
+  return at;
+}
+
+int fbs_oracle_decision_sequences(const uor_fbs_model *m, const uor_fbs_ext *ext,
+                                  const uint32_t *tokens, uint32_t sequences, uint32_t len,
+                                  int decisions, const uint8_t *force_buckets,
+                                  const uint64_t *force_codes, const uint8_t *force_mask,
+                                  uint32_t *out_tokens, int32_t *out_query, uint8_t *out_trace,
+                                  int threads) {
+  const uint64_t stride = fbs_oracle_decision_stride(m, ext, decisions);
+  O o;
+  resolve(&o, m, ext);
+  Job j = {0};
+  j.o = &o;
+  j.kind = 0;
+  j.tokens = tokens;
+  j.n = sequences;
+  j.len = len;
+  j.out_tokens = out_tokens;
+  j.out_query = out_query;
+  j.out_dtrace = out_trace;
+  j.dstride = stride;
+  j.decisions = decisions;
+  j.force_buckets = force_buckets;
+  j.force_codes = force_codes;
+  j.force_mask = force_mask;
+  int status = run_jobs(&j, threads);
+  unresolve(&o);
+  return status;
 }

@@ -95,6 +95,15 @@ int fbs_oracle_place_rows(const uor_fbs_place *pm, uint32_t vocab, const uint32_
                           uint64_t n, const int64_t *finds, uint32_t nfinds, int64_t *out);
 int64_t fbs_oracle_place_pick(const uint64_t *queries, const int32_t *margins, uint32_t heads,
                               const uint64_t *ranges, uint32_t nranges, const uint64_t *keys);
+/* The Hamming trace and the decision trace with forced replay, teacher-forced from fresh
+ * sessions: fbs_oracle_decision_stride bytes a position (layout in fbs_oracle.c). */
+uint64_t fbs_oracle_decision_stride(const uor_fbs_model *m, const uor_fbs_ext *ext, int decisions);
+int fbs_oracle_decision_sequences(const uor_fbs_model *m, const uor_fbs_ext *ext,
+                                  const uint32_t *tokens, uint32_t sequences, uint32_t len,
+                                  int decisions, const uint8_t *force_buckets,
+                                  const uint64_t *force_codes, const uint8_t *force_mask,
+                                  uint32_t *out_tokens, int32_t *out_query, uint8_t *out_trace,
+                                  int threads);
 /* stream_sum / readout_sum / readout_ask_sum (hamming.rs:1918-1953), 128-bit means as hi:lo. */
 int32_t fbs_oracle_stream_sum(int32_t x, int32_t w_c, int64_t c_hi, uint64_t c_lo, int32_t w_y,
                               int64_t y_hi, uint64_t y_lo);

@@ -80,6 +80,10 @@ def lib():
         L.fbs_oracle_place_rows.argtypes = [P, u32, P, u64, P, u32, P]
         L.fbs_oracle_place_pick.argtypes = [P, P, u32, P, u32, P]
         L.fbs_oracle_place_pick.restype = i64
+        L.fbs_oracle_decision_stride.argtypes = [P, P, C.c_int]
+        L.fbs_oracle_decision_stride.restype = u64
+        L.fbs_oracle_decision_sequences.argtypes = [P, P, P, u32, u32, C.c_int, P, P, P, P, P, P,
+                                                    C.c_int]
         _lib = L
     return _lib
 
@@ -132,6 +136,31 @@ def place_sequences(art, tokens: np.ndarray, threads: int = 1, image: Image | No
     st = lib().fbs_oracle_place_sequences(C.addressof(img.model), img.ext_ptr() and C.addressof(img.ext),
                                           _vp(tokens), S, n, _vp(out_t), _vp(out_q), _vp(out_p), threads)
     return st, out_t, out_q, out_p
+
+
+def decision_sequences(art, tokens: np.ndarray, decisions: bool = True, force=None,
+                       threads: int = 1, image: Image | None = None):
+    """The oracle's traced teacher-forced windows: (status, tokens, query, raw records
+    [S, len, stride]), the records laid out as uor_fbs_decision_sequences writes them; `force` as
+    hip.Model.decision_trace's."""
+    from uor_fbs import trace as tr
+    img = image or Image(art)
+    tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+    S, n = tokens.shape
+    layout = tr.TraceLayout.of(art, decisions)
+    if not isinstance(force, (list, tuple)):
+        force = [force] * S
+    fb, fc, fm = layout.force_arrays(force, S, n)
+    ext = img.ext_ptr() and C.addressof(img.ext)
+    stride = int(lib().fbs_oracle_decision_stride(C.addressof(img.model), ext, int(decisions)))
+    assert stride == layout.stride, (stride, layout.stride)
+    out_t = np.zeros((S, n), np.uint32)
+    out_q = np.zeros((S, n, art.spec.width), np.int32)
+    raw = np.zeros((S, n, max(stride, 1)), np.uint8)
+    st = lib().fbs_oracle_decision_sequences(C.addressof(img.model), ext, _vp(tokens), S, n,
+                                             int(decisions), _vp(fb), _vp(fc), _vp(fm),
+                                             _vp(out_t), _vp(out_q), _vp(raw), threads)
+    return st, out_t, out_q, raw
 
 
 def place_rows(marks, classes, tokens, finds) -> np.ndarray:

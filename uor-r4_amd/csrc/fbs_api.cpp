@@ -42,6 +42,7 @@ FBS_LAUNCHER(fbs_decode_pair8)
 FBS_LAUNCHER(fbs_rows_8)
 FBS_LAUNCHER(fbs_rows_pair8)
 FBS_LAUNCHER(fbs_decode_pair_clk)
+FBS_LAUNCHER(fbs_rows_dt)
 #undef FBS_LAUNCHER
 }
 
@@ -75,6 +76,7 @@ bool grid_valid(int16_t code) {  // kernels.rs:116-120
 struct uor_fbs_handle {
   int device = 0;
   DevModel M{};
+  std::vector<bool> ham_read_typed;  // per Hamming read: its type heads are served
   std::vector<void *> allocs;
   size_t lds_bytes = 0;
   uint32_t max_grid = 0;
@@ -490,7 +492,6 @@ int upload_hamming(uor_fbs_handle *h, const uor_fbs_model *m, const uor_fbs_ext 
     R.typed = 0;
     for (uint32_t c = 0; c < d; c++) R.typed |= r.weight[d + c] != 0;
     R.slot = R.typed && !r.ask ? H.slots++ : kHamNoSlot;
-    R.pad = 0;
   }
   H.place = 0;
   if (hm.place) {
@@ -522,6 +523,17 @@ int upload_hamming(uor_fbs_handle *h, const uor_fbs_model *m, const uor_fbs_ext 
     R.carry_rows = 0;
     R.typed = 0;
   }
+  // A trace record's heads: each read's copy heads, then its type heads where it serves them.
+  uint32_t before = 0;
+  h->ham_read_typed.clear();
+  for (DevHamRead &R : reads) {
+    R.heads_before = before;
+    before += H.copy + (R.typed ? heads - H.copy : 0);
+    h->ham_read_typed.push_back(R.typed != 0);
+  }
+  H.nreads = hm.read_count;
+  std::vector<uint32_t> ones(kHamBins, 1);
+  if ((st = h->upload(ones.data(), ones.size(), &H.ones))) return st;
   if ((st = h->upload(pair.data(), pair.size(), &H.pair))) return st;
   if ((st = h->upload(at.data(), at.size(), &H.at))) return st;
   if ((st = h->upload(reads.data(), reads.size(), &H.reads))) return st;
@@ -812,6 +824,12 @@ int launch(uor_fbs_handle *h, RunArgs &A, hipStream_t stream, bool noalloc = fal
     hipError_t e = launch_fbs_decode_pair_clk(h->M, A, grid, lds, stream);
     return e != hipSuccess ? hip_fail(e, "kernel launch") : 0;
   }
+  if (A.out_dtrace) {  // the traced teacher-forced kernels (one wavefront a sequence)
+    if (pair || A.mode != kModeSequences)
+      return fail(UOR_FBS_ERR_UNSUPPORTED, "the traces run teacher-forced on one wavefront");
+    hipError_t e = launch_fbs_rows_dt(h->M, A, grid, lds, stream);
+    return e != hipSuccess ? hip_fail(e, "kernel launch") : 0;
+  }
   using Launcher = hipError_t (*)(const DevModel &, const RunArgs &, uint32_t, size_t, hipStream_t);
   // Families: one wavefront, paired, Hamming reads, then the first two for an int8 table.
   static const Launcher table[3][5] = {
@@ -955,6 +973,101 @@ extern "C" int uor_fbs_trace_sequences(uor_fbs_handle *h, const uint32_t *tokens
   if ((st = copy_out(status.data(), ds, sequences)) || (st = copy_out(out_tokens, dot, n)) ||
       (st = copy_out(out_kept, dk, n * h->M.P)) || (st = copy_out(out_query, dq, n * h->M.d)) ||
       (st = copy_out(out_trace, dtr, n * stride)))
+    return st;
+  return first_status(status);
+}
+
+extern "C" uint64_t uor_fbs_decision_stride(const uor_fbs_handle *h, uint32_t decisions) {
+  if (!h) return 0;
+  const DevModel &M = h->M;
+  uint64_t at = decisions ? decision_bucket_bytes(M.L, M.nq) : 0;
+  if (M.ham.heads) {
+    uint32_t heads = 0;
+    const uint32_t copy = M.ham.heads / 2;
+    for (uint32_t i = 0; i < h->ham_read_typed.size(); i++)
+      heads += copy + (h->ham_read_typed[i] ? M.ham.heads - copy : 0);
+    at += (uint64_t)heads * decision_head_bytes(M.ham.kept);
+  }
+  return at;
+}
+
+extern "C" int uor_fbs_decision_sequences(uor_fbs_handle *h, const uint32_t *tokens,
+                                          uint32_t sequences, uint32_t len, uint32_t decisions,
+                                          const uint8_t *force_buckets, const uint64_t *force_codes,
+                                          const uint8_t *force_mask, uint32_t *out_tokens,
+                                          int32_t *out_query, uint8_t *out_trace) {
+  if (!h || !tokens || !out_tokens || !out_trace) return fail(UOR_FBS_ERR_ARGUMENT, "null argument");
+  if (sequences == 0 || len == 0) return 0;
+  const DevModel &M = h->M;
+  // set_decision_trace's refusals (session.rs:2438-2500).
+  if (decisions && (!M.raw_gates || !M.raw_transition))
+    return fail(UOR_FBS_ERR_SHAPE,
+                "the decision trace reads an unsnapped artifact: the snap is not a decision it records");
+  if (decisions && M.head != 1)
+    return fail(UOR_FBS_ERR_SHAPE,
+                "the decision trace reads the Hamilton gate and the nearest head, with no point key");
+  if (force_buckets && !decisions)
+    return fail(UOR_FBS_ERR_ARGUMENT, "forced buckets need the decision trace");
+  if (!force_codes != !force_mask) return fail(UOR_FBS_ERR_ARGUMENT, "forced codes come with their mask");
+  if (len > M.context) return fail(UOR_FBS_ERR_SHAPE, "a window past the context");
+  const size_t n = (size_t)sequences * len, lanes = (size_t)M.L * M.nq;
+  if (force_buckets)
+    for (size_t i = 0; i < n * lanes; i++)
+      if (force_buckets[i] != 255 && force_buckets[i] > 15)
+        return fail(UOR_FBS_ERR_SHAPE, "a forced bucket names a step, layer, lane or entry outside the model");
+  const uint32_t R = M.ham.heads ? M.ham.nreads : 0, H = M.ham.heads, copy = H / 2;
+  if (force_mask) {
+    if (!M.ham.heads) return fail(UOR_FBS_ERR_SHAPE, "a forced code names a read the model does not have");
+    bool any = false;
+    for (size_t i = 0; i < n * R * H; i++) {
+      const uint8_t f = force_mask[i];
+      if (!f) continue;
+      any = true;
+      const size_t head = i % H, r = (i / H) % R, step = (i / H / R) % len;
+      if (f & ~3u) return fail(UOR_FBS_ERR_ARGUMENT, "a forced code's mask holds bits 0 and 1");
+      if (head >= copy && !h->ham_read_typed[r])
+        return fail(UOR_FBS_ERR_SHAPE, "a forced code names a head its read does not serve");
+      if ((f & 2u) && step == 0) return fail(UOR_FBS_ERR_SHAPE, "a forced key at step 0 names no candidate");
+    }
+    if (any && M.ham.place) return fail(UOR_FBS_ERR_SHAPE, "forced codes are not served with a place read");
+  }
+  DeviceScope scope(h->device);
+  const uint64_t stride = uor_fbs_decision_stride(h, decisions);
+  DevBuf b;
+  uint32_t *dt, *dot;
+  int32_t *dq = nullptr, *ds;
+  uint8_t *dtr, *dfb = nullptr, *dfm = nullptr;
+  uint64_t *dfc = nullptr;
+  int st;
+  if ((st = b.in(&dt, tokens, n)) || (st = b.alloc(&dot, n)) || (st = b.alloc(&ds, sequences)) ||
+      (st = b.alloc(&dtr, n * stride)) || (st = b.in(&dfb, force_buckets, n * lanes)) ||
+      (st = b.in(&dfc, force_codes, n * R * H * 2)) || (st = b.in(&dfm, force_mask, n * R * H)))
+    return st;
+  if (out_query && (st = b.alloc(&dq, n * M.d))) return st;
+  if (stride) {
+    hipError_t e = hipMemset(dtr, 0, n * stride);
+    if (e != hipSuccess) return hip_fail(e, "hipMemset");
+  }
+  RunArgs A{};
+  A.mode = kModeSequences;
+  A.n = sequences;
+  A.len = len;
+  A.tokens = dt;
+  A.out_tokens = dot;
+  A.out_query = dq;
+  A.status = ds;
+  A.out_dtrace = dtr;
+  A.dstride = (uint32_t)stride;
+  A.decisions = decisions ? 1u : 0u;
+  A.force_buckets = dfb;
+  A.force_codes = dfc;
+  A.force_mask = dfm;
+  if ((st = launch(h, A, nullptr, false, true))) return st;
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_fail(e, "kernel");
+  std::vector<int32_t> status(sequences);
+  if ((st = copy_out(status.data(), ds, sequences)) || (st = copy_out(out_tokens, dot, n)) ||
+      (st = copy_out(out_query, dq, n * M.d)) || (st = copy_out(out_trace, dtr, n * stride)))
     return st;
   return first_status(status);
 }

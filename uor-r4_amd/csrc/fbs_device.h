@@ -64,7 +64,7 @@ struct DevHamRead {
   uint32_t carry_rows;          // the carry's reach
   uint32_t typed;               // type heads served (some w_y is not zero)
   uint32_t slot;                // payload cache of a typed read that does not ask, else kHamNoSlot
-  uint32_t pad;
+  uint32_t heads_before;        // the served heads of the earlier reads (a trace record's place)
 };
 
 // The readout read's place read (fbs_hamming.h's place register): the marks and the classes.
@@ -84,6 +84,7 @@ struct DevHam {
   uint32_t p_bos, p_eos;        // the document's start and end marks
   uint32_t p_len[4];            // the separator's and the system, user, assistant markers' lengths
   uint32_t p_carry_rows;        // the place read's question carry reach
+  uint32_t nreads;              // the reads
   const uint64_t *pair;         // copy: a copy key 2 head's first-half mask, else 0
   const int32_t *at;            // L + 1: the read index at each depth, or -1
   const DevHamRead *reads;
@@ -91,6 +92,7 @@ struct DevHam {
   const uint8_t *p_class;       // vocab: UOR_FBS_PLACE_STOP | _ARM | _OPEN
   const int16_t *p_ask;         // the place read's question table (vocab * d, Q12)
   const int32_t *p_carry;       // its carry gains (Q16), or null
+  const uint32_t *ones;         // kHamBins ones: every distance kept (the trace's nearest)
 };
 
 struct DevModel {
@@ -223,7 +225,24 @@ struct RunArgs {
   uint8_t *out_trace;
   // The part clocks' kernels only: kPartWords u64 a sequence (Part).
   uint64_t *out_parts;
+  // The traced kernels only (uor_fbs_decision_sequences): every position's record, `dstride`
+  // bytes (decision_layout), and the forced replay: rate buckets [n][len][L][d/4] (255: none),
+  // codes [n][len][reads][heads][2] (query, key) with their mask [n][len][reads][heads] (bit 0
+  // the query, bit 1 the key); null: nothing forced. `decisions`: the record holds the buckets.
+  uint8_t *out_dtrace;
+  uint32_t dstride, decisions;
+  const uint8_t *force_buckets;
+  const uint64_t *force_codes;
+  const uint8_t *force_mask;
 };
+
+// A traced position's record (uor_fbs_decision_sequences): with the decisions, each layer's rate
+// scores (i32, [L][d/4]) then the entries used (u8, [L][d/4]), padded to 8 bytes; then each read
+// in depth order, each served head (the copy heads, then the type heads where the read serves
+// them): the query (u64), the key at the row (u64), the kept count (u32) and kept positions (u32,
+// `kept` of them), padded to 8 bytes.
+constexpr uint32_t decision_head_bytes(uint32_t kept) { return (20u + 4u * kept + 7u) & ~7u; }
+constexpr uint32_t decision_bucket_bytes(uint32_t L, uint32_t lanes) { return (5u * L * lanes + 7u) & ~7u; }
 
 // The part clocks (uor_fbs_decode_parts_async, after the reference's measure_fbs_step_parts,
 // session.rs:4753): the phases of a paired block's step in the order they run, each wave's

@@ -282,12 +282,56 @@ __device__ __forceinline__ uint32_t ham_choose(const Lds &S, uint32_t rule, uint
   return n;
 }
 
+// The forced replay (Q5's, claude-249; HeadForce and `forcing`, :1397-1421, 1686-1740): head
+// `head` of read `ri`'s forced query at step `step` (role 0) or candidate key (role 1), if any.
+__device__ __forceinline__ bool dt_forced(const DtCtx *dc, const DevHam &H, uint32_t ri,
+                                          uint32_t head, uint32_t step, uint32_t role,
+                                          uint64_t &code) {
+  if (!dc->mask) return false;
+  const uint64_t at = ((uint64_t)step * H.nreads + ri) * H.heads + head;
+  if (!((dc->mask[at] >> role) & 1u)) return false;
+  code = dc->codes[2 * at + role];
+  return true;
+}
+
+// One head's trace record at row t (`record`, :1787-1814): the query, the key at the row, and
+// the kept positions as `nearest` keeps them (the kept nearest by (distance, position), every
+// distance counted; :690-701) or the rule's one position (`latest_of`, `longest_of`), whatever
+// the margin then weighs them. Run before the served choice, which overwrites the picks.
+template <class KeyF, class LongerF>
+__device__ __forceinline__ void ham_trace_head(const Lds &S, const DevHam &H, uint32_t rule,
+                                               uint64_t q, uint64_t kt, uint32_t t, uint32_t lane,
+                                               KeyF keyf, LongerF longer, uint8_t *rec) {
+  const uint32_t n = ham_choose(S, rule, q, t, H.kept, INT32_MAX, H.ones, lane, keyf, longer);
+  uint32_t *kept = (uint32_t *)(rec + 20);
+  if (rule == 0) {
+    for (uint32_t i = lane; i < n; i += kWave) {
+      const uint32_t si = S.hpick[i], di = S.hdist[si];
+      uint32_t rank = 0;
+      for (uint32_t j = 0; j < n; j++) {
+        const uint32_t sj = S.hpick[j], dj = S.hdist[sj];
+        rank += dj < di || (dj == di && sj < si) ? 1u : 0u;
+      }
+      kept[rank] = si;
+    }
+  } else if (lane == 0 && n) {
+    kept[0] = S.hpick[0];
+  }
+  if (lane == 0) {
+    *(uint64_t *)rec = q;
+    *(uint64_t *)(rec + 8) = kt;
+    *(uint32_t *)(rec + 16) = n;
+  }
+  wave_sync();
+}
+
 // The copy heads' mean at row t (`CopyHeads::mean_at` :482-504) on the lane's channels into cm
 // (at 2^-43; |cm| < 2^53, so 64 bits hold it). Returns whether a head found a position.
-template <int Q>
-__device__ __forceinline__ bool ham_copy_mean(const DevModel &M, const DevHamRead &R, const Lds &S,
-                                              uint32_t t, uint32_t lane, const bool (&qv)[Q],
-                                              const uint32_t (&qi)[Q], int64_t (&cm)[Q][4]) {
+template <int Q, bool DT = false>
+__device__ __forceinline__ bool ham_copy_mean(const DevModel &M, const DevHamRead &R, uint32_t ri,
+                                              const Lds &S, uint32_t t, uint32_t lane,
+                                              const bool (&qv)[Q], const uint32_t (&qi)[Q],
+                                              int64_t (&cm)[Q][4], const DtCtx *dc = nullptr) {
   const DevHam &H = M.ham;
   const uint32_t *tk = S.tok;
 #pragma unroll
@@ -304,13 +348,24 @@ __device__ __forceinline__ bool ham_copy_mean(const DevModel &M, const DevHamRea
       const uint64_t code = ham_code(R, H.heads, near, h);
       return first ? (code & first) | (ham_code(R, H.heads, far, h) & ~first) : code;
     };
-    const uint64_t q = joined(tk[t], tk[t ? t - 1 : 0]);
+    uint64_t q = joined(tk[t], tk[t ? t - 1 : 0]);
+    if (DT) dt_forced(dc, H, ri, h, t, 0, q);
     const uint32_t kd = first ? 2 : 1;
     const uint64_t before = t >= kd ? ham_code(R, H.heads, tk[t - kd], h) : 0;
-    const uint32_t n = ham_choose(
-        S, rule, q, t, H.kept, R.margin[h], R.wd + h * kHamBins, lane,
-        [&](uint32_t s) { return joined(tk[s - 1], tk[s >= 2 ? s - 2 : 0]); },
-        [&](uint32_t s) { return s > kd && ham_code(R, H.heads, tk[s - 1 - kd], h) == before; });
+    auto keyf = [&](uint32_t s) {
+      uint64_t k = joined(tk[s - 1], tk[s >= 2 ? s - 2 : 0]);
+      if (DT) dt_forced(dc, H, ri, h, s, 1, k);
+      return k;
+    };
+    // The longer test reads the tokens, which a replay does not force.
+    auto longer = [&](uint32_t s) { return s > kd && ham_code(R, H.heads, tk[s - 1 - kd], h) == before; };
+    if (DT && dc->rec) {
+      const uint64_t kt = t ? keyf(t) : 0;
+      ham_trace_head(S, H, rule, q, kt, t, lane, keyf, longer,
+                     dc->rec + dc->reads_at + (R.heads_before + h) * decision_head_bytes(H.kept));
+    }
+    const uint32_t n = ham_choose(S, rule, q, t, H.kept, R.margin[h], R.wd + h * kHamBins, lane,
+                                  keyf, longer);
     if (!n) continue;
     found++;
     const Divisor dv = make_divisor(n);
@@ -356,11 +411,12 @@ __device__ __forceinline__ bool ham_copy_mean(const DevModel &M, const DevHamRea
 // payload (`payload` :1204-1215) is kept at row t of `pay` first, the query codes are `point`'s
 // through the query rotation and the kept positions' payloads come back (ym at the point's
 // exponent minus 31). Returns whether a head found a position.
-template <int Q>
-__device__ __forceinline__ bool ham_type_mean(const DevModel &M, const DevHamRead &R, const Lds &S,
-                                              uint32_t t, uint32_t lane, const bool (&qv)[Q],
-                                              const uint32_t (&qi)[Q], const int64_t (&point)[Q][4],
-                                              int64_t *pay, i128 (&ym)[Q][4]) {
+template <int Q, bool DT = false>
+__device__ __forceinline__ bool ham_type_mean(const DevModel &M, const DevHamRead &R, uint32_t ri,
+                                              const Lds &S, uint32_t t, uint32_t lane,
+                                              const bool (&qv)[Q], const uint32_t (&qi)[Q],
+                                              const int64_t (&point)[Q][4], int64_t *pay,
+                                              i128 (&ym)[Q][4], const DtCtx *dc = nullptr) {
   const DevHam &H = M.ham;
   const uint32_t d = M.d, *tk = S.tok;
   const bool asks = R.ask != nullptr;
@@ -410,11 +466,21 @@ __device__ __forceinline__ bool ham_type_mean(const DevModel &M, const DevHamRea
   wave_sync();
   uint32_t found = 0;
   for (uint32_t j = H.copy; j < H.heads; j++) {
-    const uint64_t q = ham_word(S.hnib, j, H.hw);
-    const uint32_t n = ham_choose(
-        S, 0, q, t, H.kept, R.margin[j], R.wd + j * kHamBins, lane,
-        [&](uint32_t s) { return ham_code(R, H.heads, tk[s - 1], j); },
-        [&](uint32_t) { return false; });
+    uint64_t q = ham_word(S.hnib, j, H.hw);
+    if (DT) dt_forced(dc, H, ri, j, t, 0, q);
+    auto keyf = [&](uint32_t s) {
+      uint64_t k = ham_code(R, H.heads, tk[s - 1], j);
+      if (DT) dt_forced(dc, H, ri, j, s, 1, k);
+      return k;
+    };
+    auto never = [&](uint32_t) { return false; };
+    if (DT && dc->rec) {
+      const uint64_t kt = t ? keyf(t) : 0;
+      ham_trace_head(S, H, 0, q, kt, t, lane, keyf, never,
+                     dc->rec + dc->reads_at + (R.heads_before + j) * decision_head_bytes(H.kept));
+    }
+    const uint32_t n = ham_choose(S, 0, q, t, H.kept, R.margin[j], R.wd + j * kHamBins, lane,
+                                  keyf, never);
     if (!n) continue;
     found++;
     const Divisor dv = make_divisor(n);
@@ -683,14 +749,14 @@ __device__ __forceinline__ void place_advance(const DevModel &M, const Lds &S, u
 
 // The stream read after `depth` layers (< the layer count) on the residual x, in place. `pay`:
 // the sequence's payload caches, [slot][context][d].
-template <int Q>
-__device__ __forceinline__ void ham_stream(const DevModel &M, const DevHamRead &R, const Lds &S,
-                                           uint32_t t, int64_t *pay, uint32_t lane,
+template <int Q, bool DT = false>
+__device__ __forceinline__ void ham_stream(const DevModel &M, const DevHamRead &R, uint32_t ri,
+                                           const Lds &S, uint32_t t, int64_t *pay, uint32_t lane,
                                            const bool (&qv)[Q], const uint32_t (&qi)[Q],
-                                           int32_t (&x)[Q][4]) {
+                                           int32_t (&x)[Q][4], const DtCtx *dc = nullptr) {
   int64_t cm[Q][4];
   i128 ym[Q][4];
-  const bool has_c = ham_copy_mean<Q>(M, R, S, t, lane, qv, qi, cm);
+  const bool has_c = ham_copy_mean<Q, DT>(M, R, ri, S, t, lane, qv, qi, cm, dc);
   bool has_y = false;
   if (R.typed) {
     int64_t point[Q][4];
@@ -699,7 +765,7 @@ __device__ __forceinline__ void ham_stream(const DevModel &M, const DevHamRead &
 #pragma unroll
       for (int c = 0; c < 4; c++) point[k][c] = x[k][c];
     int64_t *cache = R.ask ? nullptr : pay + (uint64_t)R.slot * M.context * M.d;
-    has_y = ham_type_mean<Q>(M, R, S, t, lane, qv, qi, point, cache, ym);
+    has_y = ham_type_mean<Q, DT>(M, R, ri, S, t, lane, qv, qi, point, cache, ym, dc);
     if (has_y && R.ask)
 #pragma unroll
       for (int k = 0; k < Q; k++)
@@ -721,11 +787,11 @@ __device__ __forceinline__ void ham_stream(const DevModel &M, const DevHamRead &
 }
 
 // The readout read on the final norm's output n (at 2^-24), in place.
-template <int Q>
-__device__ __forceinline__ void ham_readout(const DevModel &M, const DevHamRead &R, const Lds &S,
-                                            uint32_t t, int64_t *pay, uint32_t lane,
+template <int Q, bool DT = false>
+__device__ __forceinline__ void ham_readout(const DevModel &M, const DevHamRead &R, uint32_t ri,
+                                            const Lds &S, uint32_t t, int64_t *pay, uint32_t lane,
                                             const bool (&qv)[Q], const uint32_t (&qi)[Q],
-                                            int64_t (&n)[Q][4]) {
+                                            int64_t (&n)[Q][4], const DtCtx *dc = nullptr) {
   int64_t cm[Q][4];
   i128 ym[Q][4];
   // At a row the place read opens, the table's point of the token at the place, at
@@ -734,6 +800,8 @@ __device__ __forceinline__ void ham_readout(const DevModel &M, const DevHamRead 
   const uint32_t offer = M.ham.place ? S.pst[kPlOffer] : kPlaceNone;
   bool has_c;
   if (offer != kPlaceNone) {
+    // The trace records the copy heads' choices at an open row too (`record` runs first).
+    if (DT && dc->rec && M.ham.copy) ham_copy_mean<Q, DT>(M, R, ri, S, t, lane, qv, qi, cm, dc);
 #pragma unroll
     for (int k = 0; k < Q; k++) {
       int64_t v[4] = {0, 0, 0, 0};
@@ -743,12 +811,12 @@ __device__ __forceinline__ void ham_readout(const DevModel &M, const DevHamRead 
     }
     has_c = true;
   } else {
-    has_c = ham_copy_mean<Q>(M, R, S, t, lane, qv, qi, cm);
+    has_c = ham_copy_mean<Q, DT>(M, R, ri, S, t, lane, qv, qi, cm, dc);
   }
   bool has_y = false;
   if (R.typed) {
     int64_t *cache = R.ask ? nullptr : pay + (uint64_t)R.slot * M.context * M.d;
-    has_y = ham_type_mean<Q>(M, R, S, t, lane, qv, qi, n, cache, ym);
+    has_y = ham_type_mean<Q, DT>(M, R, ri, S, t, lane, qv, qi, n, cache, ym, dc);
   }
   if (!has_c && !has_y) return;
 #pragma unroll

@@ -885,6 +885,16 @@ struct Lds {
   uint64_t *clk;
 };
 
+// A traced position (the traced kernels, DT): its record and the forced replay's inputs.
+struct DtCtx {
+  uint8_t *rec;          // this position's record (decision_layout), or null
+  uint32_t reads_at;     // the reads' part of the record
+  uint32_t decisions;    // the record holds the rate buckets
+  const uint8_t *fb;     // this position's forced buckets [L][d/4] (255: none), or null
+  const uint64_t *codes; // the sequence's forced codes [len][reads][heads][2], or null
+  const uint8_t *mask;   // [len][reads][heads]: bit 0 the query is forced, bit 1 the key
+};
+
 }  // namespace fbs
 
 #include "fbs_hamming.h"
@@ -895,11 +905,11 @@ namespace fbs {
 // caches). `trace` (nullable): the position's snap trace, per layer the transition's root per
 // lane, the output gate's per lane, then the feed-forward gate's per MLP quaternion
 // (fbs_core.h:488-501).
-template <int Q, int SW, bool HM, bool T8>
+template <int Q, int SW, bool HM, bool T8, bool DT = false>
 __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ring, uint32_t base, uint32_t lane,
                     const bool (&qv)[Q], const uint32_t (&qi)[Q], uint32_t tok, bool want_writer,
                     uint32_t *chosen, uint32_t *kept_out, int32_t *query_out, uint32_t t,
-                    int64_t *pay, uint8_t *trace) {
+                    int64_t *pay, uint8_t *trace, const DtCtx *dc = nullptr) {
   if (tok >= M.vocab) return 1;
   const uint32_t d = M.d, W = M.W, nq = M.nq;
   if (HM) {  // the read at this row needs x_0..=x_t (session.rs:4149-4152)
@@ -986,6 +996,14 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
       sq = sq < 0 ? 0 : sq > 65536 ? 65536 : sq;
       uint32_t idx = (uint32_t)sq >> 12;
       idx = idx > 15 ? 15 : idx;
+      if (DT && dc->decisions) {
+        // Q5's decision trace (BucketTrace::decide, session.rs:2192-2215): a forced entry
+        // replaces the score's; the score and the entry used are recorded.
+        const uint32_t at = l * nq + qi[k];
+        if (dc->fb && dc->fb[at] != 255) idx = dc->fb[at];
+        *(int32_t *)(dc->rec + 4u * at) = sq;
+        dc->rec[4u * M.L * nq + at] = (uint8_t)idx;
+      }
       const uint64_t lambda = 1ull << (30 - idx), keep = M.keep_q31[idx];
       // The causal window (session.rs:4842-4868): tap 0 on the drive, tap s on the drive s
       // positions back (ring slot base - s), then the drive enters slot base. Rows and taps
@@ -1165,7 +1183,7 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
     wave_sync();
     if (HM) {  // the stream read after l + 1 layers (session.rs:4252-4276)
       const int32_t r = M.ham.at[l + 1];
-      if (r >= 0 && l + 1 < M.L) ham_stream<Q>(M, M.ham.reads[r], S, t, pay, lane, qv, qi, x);
+      if (r >= 0 && l + 1 < M.L) ham_stream<Q, DT>(M, M.ham.reads[r], (uint32_t)r, S, t, pay, lane, qv, qi, x, dc);
     }
   }
   // Final norm, gain and the Q12 query (session.rs:4294-4295, 4364-4366).
@@ -1180,7 +1198,7 @@ __device__ __forceinline__ int step(const DevModel &M, const Lds &S, int32_t *ri
   norm_gain<Q>(M, S.seeds, x, qv, g_fin, gd_fin, v);
   if (HM) {  // the readout read on the final norm's output (session.rs:4296-4320)
     const int32_t r = M.ham.at[M.L];
-    if (r >= 0) ham_readout<Q>(M, M.ham.reads[r], S, t, pay, lane, qv, qi, v);
+    if (r >= 0) ham_readout<Q, DT>(M, M.ham.reads[r], (uint32_t)r, S, t, pay, lane, qv, qi, v, dc);
   }
   int4 qq[Q];
   bool same = true;  // this lane's channels equal the query of the writer's last run
@@ -1850,7 +1868,8 @@ enum Phase : int { kPhasePrefill = 0, kPhaseDecode = 1, kPhaseRows = 2 };
 // HM: a model with Hamming reads (one wavefront per sequence); T8: a model with an int8 table,
 // whose writer scans its bytes.
 // CLK: the part clocks (paired decode only), each sequence's counters to A.out_parts.
-template <int Q, int SW, int PH, int NW, bool HM = false, bool T8 = false, bool CLK = false>
+template <int Q, int SW, int PH, int NW, bool HM = false, bool T8 = false, bool CLK = false,
+          bool DT = false>
 __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
   static_assert(!HM || NW == 1, "the Hamming reads run on one wavefront per sequence");
   static_assert(!CLK || NW == 2, "the part clocks time paired blocks");
@@ -2102,8 +2121,22 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
         uint8_t *trace = !A.out_trace || (HM && decode) ? nullptr
                          : A.out_trace + (decode ? (uint64_t)s * (A.len + A.gen) + t : at) *
                                              ((uint64_t)M.L * (2 * M.nq + M.nm));
-        status = step<Q, SW, HM, T8>(M, S, ring, base, lane, qv, qi, tok, want, &chosen, kept_out,
-                                 query_out, pos, pay, trace);
+        if (DT) {
+          // The traced kernels: every position's record (sequences), and the forced replay.
+          const uint32_t R = HM ? M.ham.nreads : 0u, H = HM ? M.ham.heads : 0u;
+          DtCtx dc;
+          dc.rec = A.out_dtrace + at * A.dstride;
+          dc.decisions = A.decisions;
+          dc.reads_at = A.decisions ? decision_bucket_bytes(M.L, M.nq) : 0u;
+          dc.fb = A.force_buckets ? A.force_buckets + at * ((uint64_t)M.L * M.nq) : nullptr;
+          dc.codes = A.force_codes ? A.force_codes + (uint64_t)s * A.len * R * H * 2 : nullptr;
+          dc.mask = A.force_mask ? A.force_mask + (uint64_t)s * A.len * R * H : nullptr;
+          status = step<Q, SW, HM, T8, true>(M, S, ring, base, lane, qv, qi, tok, want, &chosen,
+                                             kept_out, query_out, pos, pay, trace, &dc);
+        } else {
+          status = step<Q, SW, HM, T8>(M, S, ring, base, lane, qv, qi, tok, want, &chosen, kept_out,
+                                       query_out, pos, pay, trace);
+        }
       } else {
         // The lane's indices pass through an empty asm at every step, so that the compiler forms
         // the lane's addresses inside the loop instead of holding them across the kernel.
@@ -2284,6 +2317,33 @@ inline hipError_t launch_shape(const KernelSet &k, const DevModel &M, const RunA
     static const KernelSet k = {NAME##_pair<1, 1>, NAME##_pair<1, 2>, NAME##_pair<1, 4>,      \
                                 NAME##_pair<1, 8>, NAME##_pair<2, 16>, NAME##_pair<4, 32>};    \
     return launch_shape(k, M, A, grid, 2, lds, stream);                                       \
+  }
+// FBS_DT_KERNELS: `NAME_dt<Q, SW>`, `NAME_dt8<Q, SW>` and `NAME_dt_ham<Q, SW>`, the traced
+// one-wavefront kernels (the decision and Hamming traces with the forced replay) of a 16-bit
+// table, an int8 table and a model with Hamming reads; `launch_NAME_dt(M, A, grid, lds, stream)`
+// picks by the model.
+#define FBS_DT_KERNELS(NAME, PH)                                                             \
+  template <int Q, int SW>                                                                    \
+  __global__ __launch_bounds__(64) void NAME##_dt(DevModel M, RunArgs A) {                    \
+    run<Q, SW, PH, 1, false, false, false, true>(M, A);                                       \
+  }                                                                                           \
+  template <int Q, int SW>                                                                    \
+  __global__ __launch_bounds__(64) void NAME##_dt8(DevModel M, RunArgs A) {                   \
+    run<Q, SW, PH, 1, false, true, false, true>(M, A);                                        \
+  }                                                                                           \
+  template <int Q, int SW>                                                                    \
+  __global__ __launch_bounds__(64) void NAME##_dt_ham(DevModel M, RunArgs A) {                \
+    run<Q, SW, PH, 1, true, false, false, true>(M, A);                                        \
+  }                                                                                           \
+  hipError_t launch_##NAME##_dt(const DevModel &M, const RunArgs &A, uint32_t grid,           \
+                                size_t lds, hipStream_t stream) {                             \
+    static const KernelSet a = {NAME##_dt<1, 1>, NAME##_dt<1, 2>, NAME##_dt<1, 4>,            \
+                                NAME##_dt<1, 8>, NAME##_dt<2, 16>, NAME##_dt<4, 32>};          \
+    static const KernelSet b = {NAME##_dt8<1, 1>, NAME##_dt8<1, 2>, NAME##_dt8<1, 4>,         \
+                                NAME##_dt8<1, 8>, NAME##_dt8<2, 16>, NAME##_dt8<4, 32>};       \
+    static const KernelSet c = {NAME##_dt_ham<1, 1>, NAME##_dt_ham<1, 2>, NAME##_dt_ham<1, 4>, \
+                                NAME##_dt_ham<1, 8>, NAME##_dt_ham<2, 16>, NAME##_dt_ham<4, 32>}; \
+    return launch_shape(M.ham.heads ? c : M.table8 ? b : a, M, A, grid, 1, lds, stream);        \
   }
 // FBS_PAIR_CLK_KERNELS: `NAME_pair_clk<Q, SW>` and `NAME_pair8_clk<Q, SW>`, the paired kernels
 // with the part clocks; `launch_NAME_pair_clk(M, A, grid, lds, stream)` picks by the table.

@@ -37,6 +37,7 @@ SYMBOLS = (
     "uor_fbs_slot_cache_bytes", "uor_fbs_serve_slots_async", "uor_fbs_trace_stride",
     "uor_fbs_trace_sequences", "uor_fbs_trace_sequences_async", "uor_fbs_part_count",
     "uor_fbs_part_name", "uor_fbs_decode_parts_async", "uor_fbs_serve_slots_stream_async",
+    "uor_fbs_decision_stride", "uor_fbs_decision_sequences",
 )
 
 
@@ -75,6 +76,10 @@ def lib():
         L.uor_fbs_decode_noalloc_async.argtypes = L.uor_fbs_decode_async.argtypes
         L.uor_fbs_serve_slots_stream_async.argtypes = [P, P, C.c_uint32, C.c_uint32, P, C.c_uint32,
                                                        C.c_uint32] + [P] * 11
+        L.uor_fbs_decision_stride.argtypes = [P, C.c_uint32]
+        L.uor_fbs_decision_stride.restype = C.c_uint64
+        L.uor_fbs_decision_sequences.argtypes = [P, P, C.c_uint32, C.c_uint32, C.c_uint32, P, P, P,
+                                                 P, P, P]
         L.uor_fbs_part_count.restype = C.c_uint32
         L.uor_fbs_part_name.argtypes = [C.c_uint32]
         L.uor_fbs_part_name.restype = C.c_char_p
@@ -260,6 +265,42 @@ class Model:
             *[_vp(a) for a in ins], _vp(out["state"]), _vp(out["history"]), _vp(out["position"]),
             _vp(out["tokens"]) if tw else None, _vp(out["payloads"]) if pw else None))
         return out
+
+    def decision_trace(self, tokens, decisions: bool = True, force=None):
+        """Teacher-forced windows from fresh sessions with every position's trace record
+        (uor_fbs_decision_sequences): the decision trace (`decisions`, each step a
+        trace.DecisionStep with the nearest added from its query) or the Hamming trace alone
+        (each step a list of trace.HammingStepRead). `force`: a trace.DecisionForceWindow per
+        row (or one for every row), None for none. Returns dict(tokens, query, steps)."""
+        from . import trace as tr
+        tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+        S, n = tokens.shape
+        layout = tr.TraceLayout.of(self.art, decisions)
+        if not isinstance(force, (list, tuple)):
+            force = [force] * S
+        fb, fc, fm = layout.force_arrays(force, S, n)
+        stride = int(lib().uor_fbs_decision_stride(self.handle, int(decisions)))
+        assert stride == layout.stride, (stride, layout.stride)
+        out_t = np.zeros((S, n), np.uint32)
+        out_q = np.zeros((S, n, self.width), np.int32)
+        raw = np.zeros((S, n, max(stride, 1)), np.uint8)
+        _check(lib().uor_fbs_decision_sequences(
+            self.handle, _vp(tokens), S, n, int(decisions), _vp(fb), _vp(fc), _vp(fm),
+            _vp(out_t), _vp(out_q), _vp(raw)))
+        table = self.art.writer_table.reshape(-1, self.width)
+        steps = []
+        for i in range(S):
+            rows = []
+            for t in range(n):
+                rec = raw[i, t].tobytes()
+                if decisions:
+                    step = layout.step(rec)
+                    step.nearest = tr.nearest(out_q[i, t], table)
+                    rows.append(step)
+                else:
+                    rows.append(layout.reads(rec))
+            steps.append(rows)
+        return dict(tokens=out_t, query=out_q, steps=steps, raw=raw)
 
     def trace_sequences(self, tokens):
         """Teacher-forced runs with every position's snap trace: (tokens [S,len], kept

@@ -399,6 +399,8 @@ class Session:
         self.slide = False
         pool.set_slide(self.slot, False)
         self.trace: SnapTrace | None = None  # off by default (session.rs:2570-2576)
+        self.hamming_trace: list | None = None   # off by default (session.rs:2361-2370)
+        self.decision: dict | None = None        # off by default (session.rs:2438-2515)
         self._reset_host()
 
     def _reset_host(self):
@@ -470,6 +472,71 @@ class Session:
         # A sliding session keeps its last `context` tokens (session.rs:4149-4151).
         del self.tokens[:max(0, len(self.tokens) - self.info.context)]
         self._native = NativeStep(int(reply[-1]), kept, query)
+        self._record_traces(len(fed))
+
+    # ---- the Hamming and decision traces (session.rs:2361-2370, 2438-2515) ----
+    def _record_traces(self, fed: int) -> None:
+        """The fed steps' records: the session's tokens run again from position 0 through the
+        traced teacher-forced kernels. Neither trace changes a step, and a position's decisions
+        are a function of the tokens up to it, so the records are the served steps' own."""
+        if self.hamming_trace is None and self.decision is None:
+            return
+        decisions = self.decision is not None
+        got = self.pool.model.decision_trace(np.asarray([self.tokens], np.uint32), decisions)
+        new = got["steps"][0][len(self.tokens) - fed:]
+        if decisions:
+            for step in new:
+                step.nearest = None  # the caller's to add, from the step's query
+            self.decision["steps"].extend(new)
+        else:
+            for reads in new:
+                self.hamming_trace.extend(reads)
+
+    def set_hamming_trace(self, on: bool) -> None:
+        """Record each Hamming read's choices from the next step on, or stop and drop them
+        (session.rs:2361-2363)."""
+        self.hamming_trace = [] if on else None
+
+    def take_hamming_trace(self):
+        """The reads recorded since the trace was turned on, in step order, each step's stream
+        reads in depth order and then its readout read (trace.HammingStepRead); the trace stays
+        on, empty. None while it is off (session.rs:2365-2370)."""
+        if self.hamming_trace is None:
+            return None
+        out, self.hamming_trace = self.hamming_trace, []
+        return out
+
+    def set_decision_trace(self, force=None) -> None:
+        """Record every step's decisions from the next step on (session.rs:2438-2510): each
+        layer's rate buckets and the stream read after it, and the readout read; the nearest is
+        the caller's to add from the step's query. It turns the Hamming trace off. Refused as the
+        reference refuses it: a snapped artifact, a head other than the nearest, a session that
+        has stepped. A forced set that forces something runs as teacher-forced windows
+        (hip.Model.decision_trace): a live session's steps are the served ones."""
+        art = self.pool.model.art
+        if not art.spec.raw_gates or not art.spec.raw_transition:
+            raise SessionError("Shape", "the decision trace reads an unsnapped artifact: the snap is "
+                                        "not a decision it records")
+        if art.spec.head != 1:
+            raise SessionError("Shape", "the decision trace reads the Hamilton gate and the nearest "
+                                        "head, with no point key")
+        if self.position != 0:
+            raise SessionError("Shape", "the decision trace starts in a fresh session")
+        if force is not None and (force.buckets or force.codes):
+            raise SessionError("Shape", "a forced replay runs as teacher-forced windows "
+                                        "(Model.decision_trace), not on a served session")
+        if self.slide:
+            raise SessionError("Shape", "a sliding session's decisions are not replayed")
+        self.hamming_trace = None
+        self.decision = dict(force=force, steps=[])
+
+    def take_decision_trace(self):
+        """The decisions recorded since set_decision_trace (trace.DecisionStep), one a step, and
+        the trace turned off; None while it is off (session.rs:2512-2515)."""
+        if self.decision is None:
+            return None
+        steps, self.decision = self.decision["steps"], None
+        return steps
 
     def feed(self, tokens) -> NativeStep:
         """The prompt tokens in one launch: read_step for all but the last, then step_native on
