@@ -738,6 +738,7 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
   hipDeviceProp_t prop;
   he = hipGetDeviceProperties(&prop, device);
   if (he != hipSuccess) return done(hip_fail(he, "hipGetDeviceProperties"));
+  M.list_cap = M.ham.heads ? kListCap / 2 : kListCap;  // the paired kernels split kListCap
   h->lds_bytes = fbs::lds_bytes(M) + fbs::ham_lds_bytes(M);
   if (h->lds_bytes > prop.sharedMemPerBlock)
     return done(fail(UOR_FBS_ERR_UNSUPPORTED, "%zu bytes of LDS per sequence exceed %zu",

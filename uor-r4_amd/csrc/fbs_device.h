@@ -122,13 +122,16 @@ struct DevModel {
   // for an i16 table. Last, so that the other fields keep their kernel-argument offsets.
   const uint8_t *table8;
   uint32_t t8_shift;        // the int8 table's shift to Q12
+  // Member ids the one-wavefront writer stages in LDS per scan segment: kListCap, or half of it
+  // for a model with Hamming reads, so that four of their blocks share a CU's LDS at C3's shape.
+  uint32_t list_cap;
 };
 
 // LDS bytes per block (the layout the kernels carve): the gather crossbar, the MLP outputs, the
 // drawer scores, the kept drawers, the staged member list, the writer's last query and token,
 // the seed tables, and every layer's recurrence state (i64).
 inline size_t lds_bytes(const DevModel &M) {
-  return 4ull * (M.xbar_words + 2 * M.m + ((M.D + 3u) & ~3u) + kMaxProbes + kListCap +
+  return 4ull * (M.xbar_words + 2 * M.m + ((M.D + 3u) & ~3u) + kMaxProbes + M.list_cap +
                  ((M.d + 3u) & ~3u) + 4 + kSeedWords) +
          8ull * M.L * M.d;
 }

@@ -841,7 +841,7 @@ __device__ __forceinline__ uint32_t writer(const DevModel &M, const int32_t *q, 
     uint32_t my_beg, my_end;
     writer_select(M, q, dscore, kept, lane, my_beg, my_end);
     if (kept_out && lane < M.P) kept_out[lane] = kept[lane];
-    best = scan_members<S, T8>(M, qpk, list, kListCap, g, lane, my_beg, my_end, best);
+    best = scan_members<S, T8>(M, qpk, list, M.list_cap, g, lane, my_beg, my_end, best);
   }
   best = wave_reduce64(best, OpMin());
   return (uint32_t)best;
@@ -1889,7 +1889,7 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
     S.kept = (uint32_t *)(lds + at);
     at += kMaxProbes;
     S.list = (uint32_t *)(lds + at);
-    at += kListCap;
+    at += M.list_cap;
     S.wq = lds + at;
     at += (M.d + 3u) & ~3u;
     S.wmeta = (uint32_t *)(lds + at);
