@@ -264,7 +264,7 @@ int uor_fbs_decode_parts_async(uor_fbs_handle *handle, const uint32_t *prompts,
  * for callers that cannot allocate (code under HIP graph capture, tight serving loops, hosts
  * that forbid allocation on their path). No counterpart in the reference. Same arguments,
  * outputs and statuses as uor_fbs_decode_async; the caller still passes every input and output
- * buffer. The window rings and window sums live in a device array of
+ * buffer. The window rings, window sums and (paired blocks) recurrence states live in a device array of
  * UOR_FBS_NOALLOC_SCRATCH_BYTES inside the library, one per GPU, held until the process ends:
  * the launch uses as many resident blocks as that holds (sequences loop within them; results do
  * not depend on the grid), and a model whose one sequence needs more is refused with

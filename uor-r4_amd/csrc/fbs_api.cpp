@@ -139,7 +139,8 @@ struct uor_fbs_handle {
     return 0;
   }
 
-  // The window ring and the paired blocks' window sums for `blocks` resident sequences (grown,
+  // The window ring and the paired blocks' window sums, then their recurrence states (read by
+  // the kernels of two or more quaternions a lane), for `blocks` resident sequences (grown,
   // never shrunk).
   int ensure_ring(size_t blocks) {
     if (blocks <= ring_blocks) return 0;
@@ -151,7 +152,7 @@ struct uor_fbs_handle {
     size_t bytes = blocks * (size_t)M.L * M.W * M.d * sizeof(int32_t);
     hipError_t e = hipMalloc((void **)&ring, bytes);
     if (e != hipSuccess) return hip_fail(e, "hipMalloc(window ring)");
-    e = hipMalloc((void **)&hist, blocks * (size_t)M.L * M.d * sizeof(int64_t));
+    e = hipMalloc((void **)&hist, 2 * blocks * (size_t)M.L * M.d * sizeof(int64_t));
     if (e != hipSuccess) return hip_fail(e, "hipMalloc(window sums)");
     ring_blocks = blocks;
     return 0;
@@ -801,11 +802,11 @@ int launch(uor_fbs_handle *h, RunArgs &A, hipStream_t stream, bool noalloc = fal
     if (!h->scratch)
       return fail(UOR_FBS_ERR_DEVICE, "the scratch array's device address could not be read");
     const size_t ring = (size_t)h->M.L * h->M.W * h->M.d * sizeof(int32_t);
-    const size_t sums = pair ? (size_t)h->M.L * h->M.d * sizeof(int64_t) : 0;
+    const size_t sums = pair ? 2 * (size_t)h->M.L * h->M.d * sizeof(int64_t) : 0;  // and states
     const size_t fit = (UOR_FBS_NOALLOC_SCRATCH_BYTES - 256) / (ring + sums);
     if (fit == 0)
       return fail(UOR_FBS_ERR_UNSUPPORTED,
-                  "one sequence's window ring and sums (%zu bytes) exceed the %zu-byte scratch",
+                  "one sequence's window ring, sums and state (%zu bytes) exceed the %zu-byte scratch",
                   ring + sums, (size_t)UOR_FBS_NOALLOC_SCRATCH_BYTES);
     grid = grid < fit ? grid : (uint32_t)fit;
     A.ring = (int32_t *)h->scratch;

@@ -138,8 +138,9 @@ inline size_t lds_bytes(const DevModel &M) {
 
 // Paired blocks (two wavefronts per sequence) add the window sums and gate quaternions handed
 // from wave 1 to wave 0 (2 d i64), the kept drawers' ranges and four per-wave results.
+// With two or more quaternions a lane the state lives in global memory (kPairStateGlobal).
 inline size_t pair_lds_bytes(const DevModel &M) {
-  return lds_bytes(M) + 4ull * (4 * M.d + 2 * kMaxProbes + 8);
+  return lds_bytes(M) + 4ull * (4 * M.d + 2 * kMaxProbes + 8) - (M.qpl >= 2 ? 8ull * M.L * M.d : 0);
 }
 
 // A Hamming model's kernels add the session's tokens (context u32), the distances (context

@@ -32,6 +32,11 @@ static_assert(kRsqrtSeedWords + kRecipSeedWords == kSeedWords, "seed table size"
 // ---------------------------------------------------------------------------------------------
 // Wave-level primitives.
 
+// Paired blocks of two or more quaternions a lane keep the recurrence state in a per-block global
+// buffer (beside the window sums) instead of LDS, so that four of their blocks share a CU's LDS.
+template <int Q>
+constexpr bool kPairStateGlobal = Q >= 2;
+
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -1423,7 +1428,8 @@ template <int Q, int SW, bool T8, bool CLK>
 __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32_t lane,
                                          const bool (&qv)[Q], const uint32_t (&qi)[Q], uint32_t tok,
                                          bool want_writer, uint32_t *chosen, uint32_t *kept_out,
-                                         int32_t *query_out, PartClock<CLK> &clk) {
+                                         int32_t *query_out, PartClock<CLK> &clk,
+                                         int64_t *gst) {
   if (tok >= M.vocab) return 1;
   const uint32_t d = M.d, nq = M.nq;
   int32_t x[Q][4];
@@ -1479,6 +1485,20 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
     int64_t v[Q][4];
     norm_gain<Q>(M, S.seeds, x, qv, g_rec, gd_rec, v);
     publish64<Q>(S.xbar, v, qv, qi);
+    // Two or more quaternions a lane keep the state in the block's global buffer (each lane its
+    // own channels): its loads are issued here, to land during the barrier's wait.
+    int64_t hg[Q][4];
+    if constexpr (kPairStateGlobal<Q>) {
+#pragma unroll
+      for (int k = 0; k < Q; k++) {
+        const longlong2 *src = (const longlong2 *)(gst + (uint64_t)l * d + 4 * (qv[k] ? qi[k] : 0));
+        const longlong2 a = src[0], b = src[1];
+        hg[k][0] = a.x;
+        hg[k][1] = a.y;
+        hg[k][2] = b.x;
+        hg[k][3] = b.y;
+      }
+    }
     clk.sync(kPartNormRec, kPartSync1);  // 1: the normed activations
     int32_t rot[Q][4], dec[Q];
 #pragma unroll
@@ -1507,8 +1527,15 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
       uint32_t idx = (uint32_t)sq >> 12;
       idx = idx > 15 ? 15 : idx;
       keep[k] = M.keep_q31[idx];
-      const int64_t *hp = S.st + (uint64_t)l * d + 4 * qi[k];
-      const int64_t h[4] = {hp[0], hp[1], hp[2], hp[3]};
+      int64_t h[4];
+      if constexpr (kPairStateGlobal<Q>) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) h[c] = hg[k][c];
+      } else {
+        const int64_t *hp = S.st + (uint64_t)l * d + 4 * qi[k];
+#pragma unroll
+        for (int c = 0; c < 4; c++) h[c] = hp[c];
+      }
       if (M.raw_transition) {
         int32_t u[4], T[4];
         unit_q30(rot[k], kRotationEps, u, S.seeds);
@@ -1567,9 +1594,15 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
       for (int k = 0; k < Q; k++) {
         const uint32_t ch = 4 * (qv[k] ? qi[k] : 0);
         if (qv[k]) {
-          int64_t *hp = S.st + (uint64_t)l * d + ch;
+          if constexpr (kPairStateGlobal<Q>) {
+            longlong2 *dst = (longlong2 *)(gst + (uint64_t)l * d + ch);
+            dst[0] = make_longlong2(h[k][0], h[k][1]);
+            dst[1] = make_longlong2(h[k][2], h[k][3]);
+          } else {
+            int64_t *hp = S.st + (uint64_t)l * d + ch;
 #pragma unroll
-          for (int c = 0; c < 4; c++) hp[c] = h[k][c];
+            for (int c = 0; c < 4; c++) hp[c] = h[k][c];
+          }
         }
         int64_t rhs[4];
 #pragma unroll
@@ -1895,8 +1928,11 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
     S.wmeta = (uint32_t *)(lds + at);
     at += 4;
     if (threadIdx.x == 0) S.wmeta[1] = 0;  // no query remembered yet
-    S.st = (int64_t *)(lds + at);
-    at += 2 * M.L * M.d;
+    S.st = nullptr;
+    if (!(NW == 2 && kPairStateGlobal<Q>)) {  // lds_bytes' state
+      S.st = (int64_t *)(lds + at);
+      at += 2 * M.L * M.d;
+    }
     S.wide = S.gq = nullptr;
     S.rng = nullptr;
     S.pair = nullptr;
@@ -1968,6 +2004,11 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
   const uint32_t d = M.d, L = M.L, W = M.W;
   int32_t *const block_ring = A.ring + (uint64_t)blockIdx.x * L * W * d;
   int64_t *hist = NW == 2 ? A.hist + (uint64_t)blockIdx.x * L * d : nullptr;
+  // The recurrence state: LDS, or for paired blocks of two or more quaternions a lane the
+  // block's global buffer after every block's window sums.
+  int64_t *const stb = NW == 2 && kPairStateGlobal<Q>
+                           ? A.hist + ((uint64_t)gridDim.x + blockIdx.x) * L * d
+                           : S.st;
   bool qv[Q];
   uint32_t qi[Q];
 #pragma unroll
@@ -2021,7 +2062,7 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
             for (int c = 0; c < 4; c++) {
               const uint64_t at = (uint64_t)l * d + ch + c;
               const int64_t v = A.in_state ? A.in_state[((uint64_t)sl * L + l) * d + ch + c] : 0;
-              S.st[at] = v;
+              stb[at] = v;
               if (NW == 2 && ce) fp_acc += state_fp_word(v, (uint32_t)at);
             }
           if (keeps_ring && !A.slots)
@@ -2149,7 +2190,7 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
         }
         if (wave == 0)
           status = step_main<Q, SW, T8, CLK>(M, S, ln, qv, qs, tok, want, &chosen, kept_out,
-                                             query_out, clk);
+                                             query_out, clk, stb);
         else
           status = step_window<Q, SW, T8, CLK>(M, S, ring, hist, base, ln, qv, qs, tok, want,
                                                t == 0 && fresh, &chosen, clk);
@@ -2188,7 +2229,7 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
             if (A.out_state && keeps_state)
 #pragma unroll
               for (int c = 0; c < 4; c++)
-                A.out_state[((uint64_t)sl * L + l) * d + ch + c] = S.st[(uint64_t)l * d + ch + c];
+                A.out_state[((uint64_t)sl * L + l) * d + ch + c] = stb[(uint64_t)l * d + ch + c];
             if (A.out_history && keeps_ring && !A.slots)
               for (uint32_t r = 0; r < W; r++) {
                 uint32_t slot = base + W - 1 - r;  // (base - 1 - r) mod W, from [0, 2 W - 1)
@@ -2224,7 +2265,7 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
 #pragma unroll
               for (int c = 0; c < 4; c++) {
                 const uint64_t at = (uint64_t)l * d + 4 * qi[k] + c;
-                acc += state_fp_word(S.st[at], (uint32_t)at);
+                acc += state_fp_word(stb[at], (uint32_t)at);
               }
         fp = wave_reduce32(acc, OpAdd());
       }
