@@ -61,7 +61,8 @@ def test_decode_matches_the_oracle(name):
     art, prompts, gen = build(name)
     print(f"case {name} prompts {prompts.shape} gen {gen}", flush=True)
     model = Model(art)
-    assert model.block_waves(len(prompts)) == 1
+    # Paired at one quaternion a lane (widths up to 256), one wavefront wider.
+    assert model.block_waves(len(prompts)) == (2 if art.spec.width <= 256 else 1)
     got = model.decode(prompts, gen)
     want = oracle.decode(art, prompts, gen, threads=4)
     assert want["status"] == 0
@@ -367,3 +368,34 @@ def test_place_sessions_served_from_slots_match_the_oracle():
             got[i].append(tok)
             nxt[i] = tok
     np.testing.assert_array_equal(np.asarray(got, np.uint32), want["reply"])
+
+
+@pytest.mark.parametrize("name", ["w64_copy_type", "w64_ask_carry", "w128_rules", "w256_marker"])
+@pytest.mark.parametrize("waves", ["1", "2"])
+def test_paired_and_one_wavefront_reads_are_the_oracles(name, waves, monkeypatch):
+    # The paired kernels share each read's heads between the waves (wave 0 the even heads of each
+    # kind, wave 1 the odd, partial sums added before the divisions); one wavefront takes them
+    # all. Both bit for bit the oracle's: decode through the stream, resumed, and teacher-forced.
+    monkeypatch.setenv("UOR_FBS_BLOCK_WAVES", waves)
+    art, prompts, gen = build(name)
+    print(f"case {name} on {waves} wavefront(s)", flush=True)
+    model = Model(art)
+    assert model.block_waves(len(prompts)) == int(waves)
+    want = oracle.decode_stream(art, prompts, gen // 2, threads=4)
+    first = model.decode_stream(prompts, gen // 2)
+    for k in ("reply", "state", "history", "position"):
+        np.testing.assert_array_equal(first[k], want[k], err_msg=f"{name} {k}")
+    pos = int(want["position"][0])
+    np.testing.assert_array_equal(first["tokens"][:, :pos], want["tokens"][:, :pos])
+    np.testing.assert_array_equal(first["payloads"][:, :, :pos], want["payloads"][:, :, :pos])
+    again = model.decode_stream(first["reply"][:, -1:], gen - gen // 2 - 1, resume=first)
+    whole = oracle.decode(art, prompts, gen, threads=4)
+    np.testing.assert_array_equal(again["reply"], whole["reply"][:, gen // 2 + 1:])
+    for k in ("state", "history", "position"):
+        np.testing.assert_array_equal(again[k], whole[k], err_msg=f"{name} resumed {k}")
+    rows = np.concatenate([prompts, prompts[:, ::-1]], 1)[:, : art.spec.context]
+    tok, kept, query = model.sequences(rows)
+    st, t2, k2, q2 = oracle.sequences(art, rows, threads=4)
+    np.testing.assert_array_equal(tok, t2)
+    np.testing.assert_array_equal(kept, k2)
+    np.testing.assert_array_equal(query, q2)

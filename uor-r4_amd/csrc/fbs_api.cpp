@@ -43,6 +43,9 @@ FBS_LAUNCHER(fbs_rows_8)
 FBS_LAUNCHER(fbs_rows_pair8)
 FBS_LAUNCHER(fbs_decode_pair_clk)
 FBS_LAUNCHER(fbs_rows_dt)
+FBS_LAUNCHER(fbs_prefill_pair_ham)
+FBS_LAUNCHER(fbs_decode_pair_ham)
+FBS_LAUNCHER(fbs_rows_pair_ham)
 #undef FBS_LAUNCHER
 }
 
@@ -747,8 +750,12 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
   h->max_grid = (uint32_t)prop.multiProcessorCount * 8;
   // UOR_FBS_BLOCK_WAVES=1 fixes one wavefront per sequence (default: paired blocks).
   const char *bw = getenv("UOR_FBS_BLOCK_WAVES");
-  h->pair_lds = fbs::pair_lds_bytes(M);
-  h->pair = !(bw && bw[0] == '1' && !bw[1]) && h->pair_lds <= prop.sharedMemPerBlock && !M.ham.heads;
+  // A model with Hamming reads pairs at one quaternion a lane (wider, the paired reads spill
+  // their registers) where wave 1's read scratch fits the LDS a read leaves unused
+  // (ham_pair_fits); its blocks add the reads' LDS to the paired layout.
+  h->pair_lds = fbs::pair_lds_bytes(M) + fbs::ham_lds_bytes(M);
+  h->pair = !(bw && bw[0] == '1' && !bw[1]) && h->pair_lds <= prop.sharedMemPerBlock &&
+            (!M.ham.heads || (M.qpl == 1 && fbs::ham_pair_fits(M)));
   h->pair_grid = (uint32_t)prop.multiProcessorCount * 4;  // four SIMDs per CU
   h->lds_limit = prop.sharedMemPerBlock;
   return done(0);
@@ -833,16 +840,17 @@ int launch(uor_fbs_handle *h, RunArgs &A, hipStream_t stream, bool noalloc = fal
     return e != hipSuccess ? hip_fail(e, "kernel launch") : 0;
   }
   using Launcher = hipError_t (*)(const DevModel &, const RunArgs &, uint32_t, size_t, hipStream_t);
-  // Families: one wavefront, paired, Hamming reads, then the first two for an int8 table.
-  static const Launcher table[3][5] = {
+  // Families: one wavefront, paired, Hamming reads, then the first two for an int8 table, then
+  // the paired Hamming reads.
+  static const Launcher table[3][6] = {
       {launch_fbs_prefill, launch_fbs_prefill_pair, launch_fbs_prefill_ham, launch_fbs_prefill_8,
-       launch_fbs_prefill_pair8},
+       launch_fbs_prefill_pair8, launch_fbs_prefill_pair_ham},
       {launch_fbs_decode, launch_fbs_decode_pair, launch_fbs_decode_ham, launch_fbs_decode_8,
-       launch_fbs_decode_pair8},
+       launch_fbs_decode_pair8, launch_fbs_decode_pair_ham},
       {launch_fbs_rows, launch_fbs_rows_pair, launch_fbs_rows_ham, launch_fbs_rows_8,
-       launch_fbs_rows_pair8}};
+       launch_fbs_rows_pair8, launch_fbs_rows_pair_ham}};
   const int phase = decode && A.gen == 0 ? 0 : decode ? 1 : 2;
-  const int family = h->M.ham.heads ? 2 : (waves == 2 ? 1 : 0) + (h->M.table8 ? 3 : 0);
+  const int family = h->M.ham.heads ? (waves == 2 ? 5 : 2) : (waves == 2 ? 1 : 0) + (h->M.table8 ? 3 : 0);
   hipError_t e = table[phase][family](h->M, A, grid, lds, stream);
   if (e != hipSuccess) return hip_fail(e, "kernel launch");
   return 0;

@@ -52,6 +52,7 @@ constexpr uint32_t kMaxHamKept = 64;        // positions a head keeps
 constexpr uint32_t kHamPosBits = 24;        // positions below 2^24 (a pick packs its distance above)
 constexpr uint32_t kHamBins = 68;            // distances 0..64 (a word per distance), padded
 constexpr uint32_t kHamNoSlot = 0xffffffffu;
+constexpr uint32_t kHamReqWords = 8;         // a read's request to a paired block's second wave
 
 struct DevHamRead {
   const int64_t *qu, *ku, *vu;  // d each: query, key and value units
@@ -138,9 +139,11 @@ inline size_t lds_bytes(const DevModel &M) {
 
 // Paired blocks (two wavefronts per sequence) add the window sums and gate quaternions handed
 // from wave 1 to wave 0 (2 d i64), the kept drawers' ranges and four per-wave results.
-// With two or more quaternions a lane the state lives in global memory (kPairStateGlobal).
+// With two or more quaternions a lane, or Hamming reads, the state lives in global memory
+// (kPairStateGlobal, pair_state_global).
 inline size_t pair_lds_bytes(const DevModel &M) {
-  return lds_bytes(M) + 4ull * (4 * M.d + 2 * kMaxProbes + 8) - (M.qpl >= 2 ? 8ull * M.L * M.d : 0);
+  return lds_bytes(M) + 4ull * (4 * M.d + 2 * kMaxProbes + 8) -
+         (M.qpl >= 2 || M.ham.heads ? 8ull * M.L * M.d : 0);
 }
 
 // A Hamming model's kernels add the session's tokens (context u32), the distances (context
@@ -155,7 +158,17 @@ inline size_t place_lds_bytes(const DevModel &M) {
 inline size_t ham_lds_bytes(const DevModel &M) {
   if (!M.ham.heads) return 0;
   return 4ull * M.context + ((M.context + 15ull) & ~15ull) + 8ull * kMaxHamKept + 8ull * kHamBins +
-         4ull * (M.d / 4) + place_lds_bytes(M);
+         4ull * (M.d / 4) + 4ull * kHamReqWords + place_lds_bytes(M);
+}
+
+// The paired Hamming kernels' second wavefront keeps its read scratch where a read leaves LDS
+// unused (ham_help_lds): its distances, picks, weights, histogram and nibbles in the writer's
+// staging list, the point and partial sums (3 d i64) over the gather crossbar, the MLP outputs
+// and the drawer scores.
+inline bool ham_pair_fits(const DevModel &M) {
+  const uint64_t scratch = ((M.context + 15ull) & ~15ull) / 4 + 2ull * kMaxHamKept + 2ull * kHamBins + M.d / 4;
+  const uint64_t pool = (uint64_t)M.xbar_words + 2ull * M.m + ((M.D + 3u) & ~3u);
+  return scratch <= M.list_cap && pool >= 6ull * M.d;
 }
 
 // One serving slot's cache (uor_fbs_serve_slots_async), bytes from the entry's start: a u32 tag

@@ -327,11 +327,15 @@ __device__ __forceinline__ void ham_trace_head(const Lds &S, const DevHam &H, ui
 
 // The copy heads' mean at row t (`CopyHeads::mean_at` :482-504) on the lane's channels into cm
 // (at 2^-43; |cm| < 2^53, so 64 bits hold it). Returns whether a head found a position.
+// The copy heads h0, h0 + hs, ... below the copy count: each head that finds a position adds its
+// mean (truncating toward zero) into cm; returns how many did. ham_copy_mean divides the sum by
+// the count once every head has added (the sum of exact integers does not depend on the order).
 template <int Q, bool DT = false>
-__device__ __forceinline__ bool ham_copy_mean(const DevModel &M, const DevHamRead &R, uint32_t ri,
-                                              const Lds &S, uint32_t t, uint32_t lane,
-                                              const bool (&qv)[Q], const uint32_t (&qi)[Q],
-                                              int64_t (&cm)[Q][4], const DtCtx *dc = nullptr) {
+__device__ __forceinline__ uint32_t ham_copy_part(const DevModel &M, const DevHamRead &R, uint32_t ri,
+                                                  const Lds &S, uint32_t t, uint32_t lane,
+                                                  const bool (&qv)[Q], const uint32_t (&qi)[Q],
+                                                  int64_t (&cm)[Q][4], const DtCtx *dc,
+                                                  uint32_t h0, uint32_t hs) {
   const DevHam &H = M.ham;
   const uint32_t *tk = S.tok;
 #pragma unroll
@@ -342,7 +346,7 @@ __device__ __forceinline__ bool ham_copy_mean(const DevModel &M, const DevHamRea
   if (rule == 4)  // longest after opening: the opening row is found from the marker
     rule = H.has_marker && t >= 1 && tk[t - 1] == H.m0 && tk[t] == H.m1 ? 1u : 3u;
   uint32_t found = 0;
-  for (uint32_t h = 0; h < H.copy; h++) {
+  for (uint32_t h = h0; h < H.copy; h += hs) {
     const uint64_t first = H.pair[h];
     auto joined = [&](uint32_t near, uint32_t far) -> uint64_t {
       const uint64_t code = ham_code(R, H.heads, near, h);
@@ -395,12 +399,35 @@ __device__ __forceinline__ bool ham_copy_mean(const DevModel &M, const DevHamRea
     }
     wave_sync();  // the picks are read before the next head writes them
   }
-  if (!found) return false;
+  return found;
+}
+
+template <int Q>
+__device__ __forceinline__ void ham_finish64(int64_t (&cm)[Q][4], uint32_t found) {
   const Divisor dv = make_divisor(found);
 #pragma unroll
   for (int k = 0; k < Q; k++)
 #pragma unroll
     for (int c = 0; c < 4; c++) cm[k][c] = div_trunc64(cm[k][c], dv);
+}
+
+template <int Q>
+__device__ __forceinline__ void ham_finish128(i128 (&ym)[Q][4], uint32_t found) {
+  const Divisor dv = make_divisor(found);
+#pragma unroll
+  for (int k = 0; k < Q; k++)
+#pragma unroll
+    for (int c = 0; c < 4; c++) ym[k][c] = div_trunc128(ym[k][c], dv);
+}
+
+template <int Q, bool DT = false>
+__device__ __forceinline__ bool ham_copy_mean(const DevModel &M, const DevHamRead &R, uint32_t ri,
+                                              const Lds &S, uint32_t t, uint32_t lane,
+                                              const bool (&qv)[Q], const uint32_t (&qi)[Q],
+                                              int64_t (&cm)[Q][4], const DtCtx *dc = nullptr) {
+  const uint32_t found = ham_copy_part<Q, DT>(M, R, ri, S, t, lane, qv, qi, cm, dc, 0, 1);
+  if (!found) return false;
+  ham_finish64<Q>(cm, found);
   return true;
 }
 
@@ -411,12 +438,15 @@ __device__ __forceinline__ bool ham_copy_mean(const DevModel &M, const DevHamRea
 // payload (`payload` :1204-1215) is kept at row t of `pay` first, the query codes are `point`'s
 // through the query rotation and the kept positions' payloads come back (ym at the point's
 // exponent minus 31). Returns whether a head found a position.
+// The type heads j0, j0 + js, ... below the head count (as ham_copy_part): the point's payload
+// is kept at row t first where `write_pay` (one wavefront of a block writes it).
 template <int Q, bool DT = false>
-__device__ __forceinline__ bool ham_type_mean(const DevModel &M, const DevHamRead &R, uint32_t ri,
-                                              const Lds &S, uint32_t t, uint32_t lane,
-                                              const bool (&qv)[Q], const uint32_t (&qi)[Q],
-                                              const int64_t (&point)[Q][4], int64_t *pay,
-                                              i128 (&ym)[Q][4], const DtCtx *dc = nullptr) {
+__device__ __forceinline__ uint32_t ham_type_part(const DevModel &M, const DevHamRead &R, uint32_t ri,
+                                                  const Lds &S, uint32_t t, uint32_t lane,
+                                                  const bool (&qv)[Q], const uint32_t (&qi)[Q],
+                                                  const int64_t (&point)[Q][4], int64_t *pay,
+                                                  i128 (&ym)[Q][4], const DtCtx *dc, uint32_t j0,
+                                                  uint32_t js, bool write_pay) {
   const DevHam &H = M.ham;
   const uint32_t d = M.d, *tk = S.tok;
   const bool asks = R.ask != nullptr;
@@ -455,17 +485,19 @@ __device__ __forceinline__ bool ham_type_mean(const DevModel &M, const DevHamRea
       i128 o[4];
       const int64_t u[4] = {R.vu[4 * q], R.vu[4 * q + 1], R.vu[4 * q + 2], R.vu[4 * q + 3]};
       hamilton64(u, point[k], o);
-      int64_t *dst = pay + (uint64_t)t * d + 4 * q;
-      *(longlong2 *)dst = make_longlong2(clamp_i64(round_shift128(o[0], 31)),
-                                         clamp_i64(round_shift128(o[1], 31)));
-      *(longlong2 *)(dst + 2) = make_longlong2(clamp_i64(round_shift128(o[2], 31)),
-                                               clamp_i64(round_shift128(o[3], 31)));
+      if (write_pay) {
+        int64_t *dst = pay + (uint64_t)t * d + 4 * q;
+        *(longlong2 *)dst = make_longlong2(clamp_i64(round_shift128(o[0], 31)),
+                                           clamp_i64(round_shift128(o[1], 31)));
+        *(longlong2 *)(dst + 2) = make_longlong2(clamp_i64(round_shift128(o[2], 31)),
+                                                 clamp_i64(round_shift128(o[3], 31)));
+      }
       S.hnib[q] = ham_nibble(R.qu + 4 * q, point[k]);
     }
   }
   wave_sync();
   uint32_t found = 0;
-  for (uint32_t j = H.copy; j < H.heads; j++) {
+  for (uint32_t j = j0; j < H.heads; j += js) {
     uint64_t q = ham_word(S.hnib, j, H.hw);
     if (DT) dt_forced(dc, H, ri, j, t, 0, q);
     auto keyf = [&](uint32_t s) {
@@ -518,12 +550,19 @@ __device__ __forceinline__ bool ham_type_mean(const DevModel &M, const DevHamRea
     }
     wave_sync();
   }
+  return found;
+}
+
+template <int Q, bool DT = false>
+__device__ __forceinline__ bool ham_type_mean(const DevModel &M, const DevHamRead &R, uint32_t ri,
+                                              const Lds &S, uint32_t t, uint32_t lane,
+                                              const bool (&qv)[Q], const uint32_t (&qi)[Q],
+                                              const int64_t (&point)[Q][4], int64_t *pay,
+                                              i128 (&ym)[Q][4], const DtCtx *dc = nullptr) {
+  const uint32_t found = ham_type_part<Q, DT>(M, R, ri, S, t, lane, qv, qi, point, pay, ym, dc,
+                                              M.ham.copy, 1, true);
   if (!found) return false;
-  const Divisor dv = make_divisor(found);
-#pragma unroll
-  for (int k = 0; k < Q; k++)
-#pragma unroll
-    for (int c = 0; c < 4; c++) ym[k][c] = div_trunc128(ym[k][c], dv);
+  ham_finish128<Q>(ym, found);
   return true;
 }
 
@@ -747,31 +786,182 @@ __device__ __forceinline__ void place_advance(const DevModel &M, const Lds &S, u
   wave_sync();
 }
 
+// Both wavefronts of a paired block meet at a read: their LDS and global writes before it (the
+// point, the partial sums, the payloads) are visible to the other after it.
+__device__ __forceinline__ void hook_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// Where a paired block's second wavefront reads and writes during a read (the LDS a read leaves
+// unused): its distances, picks, weights, histogram and nibbles in the writer's staging list;
+// the point it reads and the partial sums it returns (d i64, then d i128 as low and high i64
+// halves) over the gather crossbar, the MLP outputs and the drawer scores, which lie contiguous
+// (ham_pair_fits on the host).
+__device__ __forceinline__ Lds ham_help_lds(const DevModel &M, const Lds &S0) {
+  Lds S = S0;
+  uint8_t *base = (uint8_t *)S0.list;
+  S.hdist = base;
+  base += (M.context + 15u) & ~15u;
+  S.hpick = (uint32_t *)base;
+  S.hwgt = S.hpick + kMaxHamKept;
+  S.hhist = S.hwgt + kMaxHamKept;
+  S.hwd = S.hhist + kHamBins;
+  S.hnib = S.hwd + kHamBins;
+  return S;
+}
+
+// A read's two means at row t (the copy heads' unless `skip_copy`, the type heads' where the read
+// serves them; `point` the hook's input): on one wavefront, or (PAIR) with the paired block's
+// second wavefront (ham_help), which takes the odd heads of each kind: the first publishes the
+// request and the point, takes the even heads, and adds the second's partial sums and counts
+// before the divisions; the sums are of exact integers, so the heads' order does not change them.
+template <int Q, bool DT, bool PAIR>
+__device__ __forceinline__ void ham_read_means(const DevModel &M, const DevHamRead &R, uint32_t ri,
+                                               const Lds &S, uint32_t t, int64_t *pay,
+                                               uint32_t lane, const bool (&qv)[Q],
+                                               const uint32_t (&qi)[Q],
+                                               const int64_t (&point)[Q][4], bool skip_copy,
+                                               int64_t (&cm)[Q][4], i128 (&ym)[Q][4],
+                                               bool &has_c, bool &has_y, const DtCtx *dc) {
+  int64_t *cache = R.typed && !R.ask ? pay + (uint64_t)R.slot * M.context * M.d : nullptr;
+  if constexpr (PAIR) {
+    static_assert(!DT, "the traced kernels run on one wavefront");
+    int64_t *pc = (int64_t *)S.xbar;
+#pragma unroll
+    for (int k = 0; k < Q; k++)
+      if (qv[k])
+#pragma unroll
+        for (int c = 0; c < 4; c++) pc[4 * qi[k] + c] = point[k][c];
+    if (lane == 0) {
+      S.hreq[0] = ri;
+      S.hreq[1] = t;
+      S.hreq[2] = skip_copy;
+    }
+    hook_sync();  // the request and the point
+    uint32_t fc = 0, fy = 0;
+    if (!skip_copy) {
+      fc = ham_copy_part<Q>(M, R, ri, S, t, lane, qv, qi, cm, nullptr, 0, 2);
+    } else {
+#pragma unroll
+      for (int k = 0; k < Q; k++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) cm[k][c] = 0;
+    }
+    if (R.typed) {
+      fy = ham_type_part<Q>(M, R, ri, S, t, lane, qv, qi, point, cache, ym, nullptr, M.ham.copy, 2, true);
+    } else {
+#pragma unroll
+      for (int k = 0; k < Q; k++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) ym[k][c] = 0;
+    }
+    hook_sync();  // the second wavefront's partial sums and counts
+    const int64_t *py = pc + M.d;
+#pragma unroll
+    for (int k = 0; k < Q; k++)
+      if (qv[k])
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          const uint32_t ch = 4 * qi[k] + c;
+          cm[k][c] += pc[ch];
+          ym[k][c] += (i128)(((u128)(uint64_t)py[M.d + ch] << 64) | (u128)(uint64_t)py[ch]);
+        }
+    fc += S.hreq[6];
+    fy += S.hreq[7];
+    has_c = fc != 0;
+    has_y = fy != 0;
+    if (has_c) ham_finish64<Q>(cm, fc);
+    if (has_y) ham_finish128<Q>(ym, fy);
+  } else {
+    has_c = false;
+    if (!skip_copy) {
+      has_c = ham_copy_mean<Q, DT>(M, R, ri, S, t, lane, qv, qi, cm, dc);
+    } else if (DT && dc->rec && M.ham.copy) {
+      // The trace records the copy heads' choices at an open row too (`record` runs first).
+      ham_copy_mean<Q, DT>(M, R, ri, S, t, lane, qv, qi, cm, dc);
+    }
+    has_y = R.typed && ham_type_mean<Q, DT>(M, R, ri, S, t, lane, qv, qi, point, cache, ym, dc);
+  }
+}
+
+// The paired block's second wavefront at a read the first requests (ham_read_means): the odd
+// copy and type heads over its own scratch (ham_help_lds), then its partial sums over the point it
+// read and its counts in the request. Two hook barriers, as the first wavefront's.
+template <int Q>
+__device__ __forceinline__ void ham_help(const DevModel &M, const Lds &S0, int64_t *pay,
+                                         uint32_t lane, const bool (&qv)[Q],
+                                         const uint32_t (&qi)[Q]) {
+  hook_sync();  // the request and the point
+  const Lds S = ham_help_lds(M, S0);
+  const uint32_t ri = S0.hreq[0], t = S0.hreq[1];
+  const bool skip_copy = S0.hreq[2] != 0;
+  const DevHamRead &R = M.ham.reads[ri];
+  int64_t *pc = (int64_t *)S0.xbar, *py = pc + M.d;
+  int64_t point[Q][4];
+#pragma unroll
+  for (int k = 0; k < Q; k++)
+#pragma unroll
+    for (int c = 0; c < 4; c++) point[k][c] = qv[k] ? pc[4 * qi[k] + c] : 0;
+  int64_t cm[Q][4];
+  i128 ym[Q][4];
+  uint32_t fc = 0, fy = 0;
+  if (!skip_copy) {
+    fc = ham_copy_part<Q>(M, R, ri, S, t, lane, qv, qi, cm, nullptr, 1, 2);
+  } else {
+#pragma unroll
+    for (int k = 0; k < Q; k++)
+#pragma unroll
+      for (int c = 0; c < 4; c++) cm[k][c] = 0;
+  }
+  if (R.typed) {
+    int64_t *cache = R.ask ? nullptr : pay + (uint64_t)R.slot * M.context * M.d;
+    fy = ham_type_part<Q>(M, R, ri, S, t, lane, qv, qi, point, cache, ym, nullptr, M.ham.copy + 1, 2,
+                          false);
+  } else {
+#pragma unroll
+    for (int k = 0; k < Q; k++)
+#pragma unroll
+      for (int c = 0; c < 4; c++) ym[k][c] = 0;
+  }
+#pragma unroll
+  for (int k = 0; k < Q; k++)
+    if (qv[k])
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const uint32_t ch = 4 * qi[k] + c;
+        pc[ch] = cm[k][c];
+        py[ch] = (int64_t)(uint64_t)(u128)ym[k][c];
+        py[M.d + ch] = (int64_t)(uint64_t)((u128)ym[k][c] >> 64);
+      }
+  if (lane == 0) {
+    S0.hreq[6] = fc;
+    S0.hreq[7] = fy;
+  }
+  hook_sync();  // the partial sums and counts
+}
+
 // The stream read after `depth` layers (< the layer count) on the residual x, in place. `pay`:
 // the sequence's payload caches, [slot][context][d].
-template <int Q, bool DT = false>
+template <int Q, bool DT = false, bool PAIR = false>
 __device__ __forceinline__ void ham_stream(const DevModel &M, const DevHamRead &R, uint32_t ri,
                                            const Lds &S, uint32_t t, int64_t *pay, uint32_t lane,
                                            const bool (&qv)[Q], const uint32_t (&qi)[Q],
                                            int32_t (&x)[Q][4], const DtCtx *dc = nullptr) {
-  int64_t cm[Q][4];
+  int64_t cm[Q][4], point[Q][4];
   i128 ym[Q][4];
-  const bool has_c = ham_copy_mean<Q, DT>(M, R, ri, S, t, lane, qv, qi, cm, dc);
-  bool has_y = false;
-  if (R.typed) {
-    int64_t point[Q][4];
+#pragma unroll
+  for (int k = 0; k < Q; k++)
+#pragma unroll
+    for (int c = 0; c < 4; c++) point[k][c] = x[k][c];
+  bool has_c, has_y;
+  ham_read_means<Q, DT, PAIR>(M, R, ri, S, t, pay, lane, qv, qi, point, false, cm, ym, has_c, has_y, dc);
+  if (has_y && R.ask)
 #pragma unroll
     for (int k = 0; k < Q; k++)
 #pragma unroll
-      for (int c = 0; c < 4; c++) point[k][c] = x[k][c];
-    int64_t *cache = R.ask ? nullptr : pay + (uint64_t)R.slot * M.context * M.d;
-    has_y = ham_type_mean<Q, DT>(M, R, ri, S, t, lane, qv, qi, point, cache, ym, dc);
-    if (has_y && R.ask)
-#pragma unroll
-      for (int k = 0; k < Q; k++)
-#pragma unroll
-        for (int c = 0; c < 4; c++) ym[k][c] = shl128(ym[k][c], kStreamCopyRaise);
-  }
+      for (int c = 0; c < 4; c++) ym[k][c] = shl128(ym[k][c], kStreamCopyRaise);
   if (!has_c && !has_y) return;
 #pragma unroll
   for (int k = 0; k < Q; k++)
@@ -787,7 +977,7 @@ __device__ __forceinline__ void ham_stream(const DevModel &M, const DevHamRead &
 }
 
 // The readout read on the final norm's output n (at 2^-24), in place.
-template <int Q, bool DT = false>
+template <int Q, bool DT = false, bool PAIR = false>
 __device__ __forceinline__ void ham_readout(const DevModel &M, const DevHamRead &R, uint32_t ri,
                                             const Lds &S, uint32_t t, int64_t *pay, uint32_t lane,
                                             const bool (&qv)[Q], const uint32_t (&qi)[Q],
@@ -798,10 +988,10 @@ __device__ __forceinline__ void ham_readout(const DevModel &M, const DevHamRead 
   // 2^COPY_MEAN_EXP (a Q12 point at a Q31 weight of one), in place of the copy heads' mean
   // (hamming.rs:1895-1899).
   const uint32_t offer = M.ham.place ? S.pst[kPlOffer] : kPlaceNone;
-  bool has_c;
+  bool has_c, has_y;
+  ham_read_means<Q, DT, PAIR>(M, R, ri, S, t, pay, lane, qv, qi, n, offer != kPlaceNone, cm, ym,
+                              has_c, has_y, dc);
   if (offer != kPlaceNone) {
-    // The trace records the copy heads' choices at an open row too (`record` runs first).
-    if (DT && dc->rec && M.ham.copy) ham_copy_mean<Q, DT>(M, R, ri, S, t, lane, qv, qi, cm, dc);
 #pragma unroll
     for (int k = 0; k < Q; k++) {
       int64_t v[4] = {0, 0, 0, 0};
@@ -810,13 +1000,6 @@ __device__ __forceinline__ void ham_readout(const DevModel &M, const DevHamRead 
       for (int c = 0; c < 4; c++) cm[k][c] = v[c] * ((int64_t)1 << 31);
     }
     has_c = true;
-  } else {
-    has_c = ham_copy_mean<Q, DT>(M, R, ri, S, t, lane, qv, qi, cm, dc);
-  }
-  bool has_y = false;
-  if (R.typed) {
-    int64_t *cache = R.ask ? nullptr : pay + (uint64_t)R.slot * M.context * M.d;
-    has_y = ham_type_mean<Q, DT>(M, R, ri, S, t, lane, qv, qi, n, cache, ym, dc);
   }
   if (!has_c && !has_y) return;
 #pragma unroll

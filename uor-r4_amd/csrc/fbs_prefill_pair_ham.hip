@@ -1,0 +1,9 @@
+// fbs_prefill_pair_ham.hip - the prefill phase's paired kernels with the Hamming reads: wave 0 the
+// recurrence chain and the reads' even heads, wave 1 the window ring and the odd heads.
+#include "fbs_run.h"
+
+namespace fbs {
+
+FBS_PAIR_HAM_KERNELS(fbs_prefill, kPhasePrefill)
+
+}  // namespace fbs

@@ -32,10 +32,11 @@ static_assert(kRsqrtSeedWords + kRecipSeedWords == kSeedWords, "seed table size"
 // ---------------------------------------------------------------------------------------------
 // Wave-level primitives.
 
-// Paired blocks of two or more quaternions a lane keep the recurrence state in a per-block global
-// buffer (beside the window sums) instead of LDS, so that four of their blocks share a CU's LDS.
-template <int Q>
-constexpr bool kPairStateGlobal = Q >= 2;
+// Paired blocks of two or more quaternions a lane, or with Hamming reads, keep the recurrence
+// state in a per-block global buffer (beside the window sums) instead of LDS, so that four of
+// their blocks share a CU's LDS.
+template <int Q, bool HM = false>
+constexpr bool kPairStateGlobal = Q >= 2 || HM;
 
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -882,6 +883,7 @@ struct Lds {
   uint32_t *hhist;   // kHamBins: one head's distance histogram
   uint32_t *hwd;     // kHamBins: the Q31 weight of each distance under the head's margin
   uint32_t *hnib;    // d / 4: the sign nibbles of the row's point
+  uint32_t *hreq;    // kHamReqWords: paired blocks, a read's request to wave 1 and its counts
   // A model with a place read only (null otherwise): its register (fbs_hamming.h).
   uint32_t *pst;     // kPlaceWords: the register's scalars
   uint16_t *uend;    // context: the end of the finished user turn holding the position, or 0
@@ -1412,7 +1414,7 @@ __device__ __forceinline__ uint32_t pair_writer(const DevModel &M, const Lds &S,
     uint32_t my_beg = lane < M.P ? S.rng[lane] : 0, my_end = lane < M.P ? S.rng[kMaxProbes + lane] : 0;
     const uint32_t total = wave_reduce32(my_end - my_beg, OpAdd()), half = (total + 1) / 2;
     clip_ranges(M.P, lane, wave ? half : 0, wave ? total : half, my_beg, my_end);
-    constexpr uint32_t cap = kListCap / 2;
+    const uint32_t cap = M.list_cap / 2;  // each wave its half of the staging list
     best = scan_members<SW, T8>(M, qpk, S.list + wave * cap, cap, g, lane, my_beg, my_end, best);
   }
   best = wave_reduce64(best, OpMin());
@@ -1424,13 +1426,19 @@ __device__ __forceinline__ uint32_t pair_writer(const DevModel &M, const Lds &S,
 
 // Wave 0 of a paired block: the step (RS stack/session.rs:4129-4403) but the window and its
 // ring, the output gates' quaternions and the odd MLP groups.
-template <int Q, int SW, bool T8, bool CLK>
+template <int Q, int SW, bool T8, bool CLK, bool HM = false>
 __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32_t lane,
                                          const bool (&qv)[Q], const uint32_t (&qi)[Q], uint32_t tok,
                                          bool want_writer, uint32_t *chosen, uint32_t *kept_out,
                                          int32_t *query_out, PartClock<CLK> &clk,
-                                         int64_t *gst) {
+                                         int64_t *gst, uint32_t t = 0, int64_t *pay = nullptr) {
   if (tok >= M.vocab) return 1;
+  if constexpr (HM) {  // the read at this row needs x_0..=x_t (session.rs:4149-4152)
+    if (lane == 0) S.tok[t] = tok;
+    wave_sync();
+    // The place read's register moves on this token, before the row's readout (:4154-4162).
+    if (M.ham.place) place_advance<Q>(M, S, t, lane, qv, qi);
+  }
   const uint32_t d = M.d, nq = M.nq;
   int32_t x[Q][4];
 #pragma unroll
@@ -1488,7 +1496,7 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
     // Two or more quaternions a lane keep the state in the block's global buffer (each lane its
     // own channels): its loads are issued here, to land during the barrier's wait.
     int64_t hg[Q][4];
-    if constexpr (kPairStateGlobal<Q>) {
+    if constexpr (kPairStateGlobal<Q, HM>) {
 #pragma unroll
       for (int k = 0; k < Q; k++) {
         const longlong2 *src = (const longlong2 *)(gst + (uint64_t)l * d + 4 * (qv[k] ? qi[k] : 0));
@@ -1528,7 +1536,7 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
       idx = idx > 15 ? 15 : idx;
       keep[k] = M.keep_q31[idx];
       int64_t h[4];
-      if constexpr (kPairStateGlobal<Q>) {
+      if constexpr (kPairStateGlobal<Q, HM>) {
 #pragma unroll
         for (int c = 0; c < 4; c++) h[c] = hg[k][c];
       } else {
@@ -1594,7 +1602,7 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
       for (int k = 0; k < Q; k++) {
         const uint32_t ch = 4 * (qv[k] ? qi[k] : 0);
         if (qv[k]) {
-          if constexpr (kPairStateGlobal<Q>) {
+          if constexpr (kPairStateGlobal<Q, HM>) {
             longlong2 *dst = (longlong2 *)(gst + (uint64_t)l * d + ch);
             dst[0] = make_longlong2(h[k][0], h[k][1]);
             dst[1] = make_longlong2(h[k][2], h[k][3]);
@@ -1680,8 +1688,15 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
         for (int c = 0; c < 4; c++) x[k][c] = sat_add32(x[k][c], S.xbar[pw_down[k][c]]);
     wave_sync();
     clk.lap(kPartResidualMlp);
+    if constexpr (HM) {  // the stream read after l + 1 layers (session.rs:4252-4276)
+      const int32_t r = M.ham.at[l + 1];
+      if (r >= 0 && l + 1 < M.L)
+        ham_stream<Q, false, true>(M, M.ham.reads[r], (uint32_t)r, S, t, pay, lane, qv, qi, x);
+    }
   }
-  if (!want_writer) return 0;
+  // A model with a readout read runs it at every row: a typed one keeps the row's payload.
+  const bool readout = HM && M.ham.at[M.L] >= 0;
+  if (!want_writer && !readout) return 0;
   // Final norm, gain and the Q12 query (session.rs:4294-4295, 4364-4366).
   short4 g_fin[Q];
   ushort4 gd_fin[Q];
@@ -1692,6 +1707,13 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
   }
   int64_t v[Q][4];
   norm_gain<Q>(M, S.seeds, x, qv, g_fin, gd_fin, v);
+  if constexpr (HM) {  // the readout read on the final norm's output (session.rs:4296-4320)
+    if (readout) {
+      const uint32_t r = (uint32_t)M.ham.at[M.L];
+      ham_readout<Q, false, true>(M, M.ham.reads[r], r, S, t, pay, lane, qv, qi, v);
+    }
+    if (!want_writer) return 0;
+  }
   int4 qq[Q];
   bool same = true;  // this lane's channels equal the query of the writer's last run
 #pragma unroll
@@ -1789,12 +1811,13 @@ __device__ __forceinline__ void window_sum(const DevModel &M, const DevLayer &ly
 // The window's terms over earlier positions (taps 1..W) do not depend on the step's input, so
 // wave 1 sums them for the next step while wave 0 runs the transport, and keeps them in `hist`
 // (L x d i64 per block); the first step of a launch sums its own (`fresh`).
-template <int Q, int SW, bool T8, bool CLK>
+template <int Q, int SW, bool T8, bool CLK, bool HM = false>
 __device__ __forceinline__ int step_window(const DevModel &M, const Lds &S, int32_t *ring,
                                            int64_t *hist, uint32_t base, uint32_t lane,
                                            const bool (&qv)[Q], const uint32_t (&qi)[Q],
                                            uint32_t tok, bool want_writer, bool fresh,
-                                           uint32_t *chosen, PartClock<CLK> &clk) {
+                                           uint32_t *chosen, PartClock<CLK> &clk,
+                                           int64_t *pay = nullptr) {
   if (tok >= M.vocab) return 1;
   const uint32_t d = M.d, W = M.W;
   const uint32_t next = base + 1 == W ? 0 : base + 1;  // the next step's ring slot
@@ -1885,6 +1908,13 @@ __device__ __forceinline__ int step_window(const DevModel &M, const Lds &S, int3
     clk.sync(kPartMlp, kPartSync4);  // 4: both waves' MLP outputs and maxima
     pair_requant(M, S, lane, 1);
     clk.sync(kPartRequantMlp, kPartSync5);  // 5: the requantized MLP outputs
+    if constexpr (HM) {  // the stream read's odd heads (ham_help), as step_main requests it
+      const int32_t r = M.ham.at[l + 1];
+      if (r >= 0 && l + 1 < M.L) ham_help<Q>(M, S, pay, lane, qv, qi);
+    }
+  }
+  if constexpr (HM) {  // the readout read's odd heads, at every row (step_main)
+    if (M.ham.at[M.L] >= 0) ham_help<Q>(M, S, pay, lane, qv, qi);
   }
   if (!want_writer) return 0;
   clk.sync(kPartFinal, kPartSync6);  // 6: the query and the reuse flag
@@ -1904,7 +1934,7 @@ enum Phase : int { kPhasePrefill = 0, kPhaseDecode = 1, kPhaseRows = 2 };
 template <int Q, int SW, int PH, int NW, bool HM = false, bool T8 = false, bool CLK = false,
           bool DT = false>
 __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
-  static_assert(!HM || NW == 1, "the Hamming reads run on one wavefront per sequence");
+  static_assert(!HM || !T8, "the Hamming kernels' writer scans the 16-bit table");
   static_assert(!CLK || NW == 2, "the part clocks time paired blocks");
   extern __shared__ __align__(16) int32_t lds[];
   Lds S;
@@ -1929,7 +1959,7 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
     at += 4;
     if (threadIdx.x == 0) S.wmeta[1] = 0;  // no query remembered yet
     S.st = nullptr;
-    if (!(NW == 2 && kPairStateGlobal<Q>)) {  // lds_bytes' state
+    if (!(NW == 2 && kPairStateGlobal<Q, HM>)) {  // lds_bytes' state
       S.st = (int64_t *)(lds + at);
       at += 2 * M.L * M.d;
     }
@@ -1948,7 +1978,7 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
     }
     S.tok = nullptr;
     S.hdist = nullptr;
-    S.hpick = S.hwgt = S.hhist = S.hwd = S.hnib = nullptr;
+    S.hpick = S.hwgt = S.hhist = S.hwd = S.hnib = S.hreq = nullptr;
     S.pst = nullptr;
     S.uend = S.farm = nullptr;
     if (HM) {  // ham_lds_bytes
@@ -1966,6 +1996,8 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
       at += kHamBins;
       S.hnib = (uint32_t *)(lds + at);
       at += M.d / 4;
+      S.hreq = (uint32_t *)(lds + at);
+      at += kHamReqWords;
       if (M.ham.place) {  // place_lds_bytes
         const uint32_t words = ((2u * M.context + 15u) & ~15u) / 4u;
         S.pst = (uint32_t *)(lds + at);
@@ -2006,7 +2038,7 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
   int64_t *hist = NW == 2 ? A.hist + (uint64_t)blockIdx.x * L * d : nullptr;
   // The recurrence state: LDS, or for paired blocks of two or more quaternions a lane the
   // block's global buffer after every block's window sums.
-  int64_t *const stb = NW == 2 && kPairStateGlobal<Q>
+  int64_t *const stb = NW == 2 && kPairStateGlobal<Q, HM>
                            ? A.hist + ((uint64_t)gridDim.x + blockIdx.x) * L * d
                            : S.st;
   bool qv[Q];
@@ -2090,14 +2122,14 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
       bad_stream = wave_reduce32(bad, OpMax()) != 0;
       // The place read's register over the resumed tokens: the state their steps left (it
       // depends on the tokens and the model alone).
-      if (M.ham.place) {
+      if (M.ham.place && keeps_state) {  // paired blocks: wave 0 keeps the register
         place_init(M, S, lane);
         if (!bad_stream)
           for (uint32_t r = 0; r < pos; r++) place_advance<Q>(M, S, r, lane, qv, qi);
       }
       const uint64_t stride = (uint64_t)M.ham.slots * M.context * d;
       pay = A.out_payloads ? A.out_payloads + (uint64_t)sl * stride : A.pay + (uint64_t)blockIdx.x * stride;
-      if (A.in_payloads && A.in_payloads != A.out_payloads)
+      if (A.in_payloads && A.in_payloads != A.out_payloads && keeps_state)
         for (uint32_t c = 0; c < M.ham.slots; c++)
           for (uint32_t r = 0; r < pos; r++)
 #pragma unroll
@@ -2189,11 +2221,11 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
           asm volatile("" : "+v"(qs[k]));
         }
         if (wave == 0)
-          status = step_main<Q, SW, T8, CLK>(M, S, ln, qv, qs, tok, want, &chosen, kept_out,
-                                             query_out, clk, stb);
+          status = step_main<Q, SW, T8, CLK, HM>(M, S, ln, qv, qs, tok, want, &chosen, kept_out,
+                                                 query_out, clk, stb, pos, pay);
         else
-          status = step_window<Q, SW, T8, CLK>(M, S, ring, hist, base, ln, qv, qs, tok, want,
-                                               t == 0 && fresh, &chosen, clk);
+          status = step_window<Q, SW, T8, CLK, HM>(M, S, ring, hist, base, ln, qv, qs, tok, want,
+                                                   t == 0 && fresh, &chosen, clk, pay);
       }
       if (status) break;
       done++;
@@ -2357,6 +2389,21 @@ inline hipError_t launch_shape(const KernelSet &k, const DevModel &M, const RunA
                                   size_t lds, hipStream_t stream) {                           \
     static const KernelSet k = {NAME##_pair<1, 1>, NAME##_pair<1, 2>, NAME##_pair<1, 4>,      \
                                 NAME##_pair<1, 8>, NAME##_pair<2, 16>, NAME##_pair<4, 32>};    \
+    return launch_shape(k, M, A, grid, 2, lds, stream);                                       \
+  }
+// FBS_PAIR_HAM_KERNELS: `NAME_pair_ham<Q, SW>`, the paired kernels with the Hamming reads (each
+// read's heads shared between the waves, ham_help); `launch_NAME_pair_ham(M, A, grid, lds,
+// stream)`.
+#define FBS_PAIR_HAM_KERNELS(NAME, PH)                                                       \
+  template <int Q, int SW>                                                                    \
+  __global__ __launch_bounds__(128, 2) void NAME##_pair_ham(DevModel M, RunArgs A) {          \
+    run<Q, SW, PH, 2, true>(M, A);                                                            \
+  }                                                                                           \
+  hipError_t launch_##NAME##_pair_ham(const DevModel &M, const RunArgs &A, uint32_t grid,     \
+                                      size_t lds, hipStream_t stream) {                       \
+    static const KernelSet k = {NAME##_pair_ham<1, 1>, NAME##_pair_ham<1, 2>,                 \
+                                NAME##_pair_ham<1, 4>, NAME##_pair_ham<1, 8>,                 \
+                                NAME##_pair_ham<2, 16>, NAME##_pair_ham<4, 32>};              \
     return launch_shape(k, M, A, grid, 2, lds, stream);                                       \
   }
 // FBS_DT_KERNELS: `NAME_dt<Q, SW>`, `NAME_dt8<Q, SW>` and `NAME_dt_ham<Q, SW>`, the traced
