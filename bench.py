@@ -1089,35 +1089,55 @@ def main():
         cache = torch.zeros((B, int(L.uor_fbs_slot_cache_bytes(model.handle))), dtype=torch.uint8,
                             device=dev)
 
-        def serve_loop(cached: bool):
+        def serve_loop(cached: bool, handle=model.handle):
             for t, v in zip((s_state, s_hist, s_pos), saved):
                 t.copy_(v)
             served = torch.zeros((K + 1, B), dtype=torch.int32, device=dev)
             served[0] = first[:, 0]
-            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                  for _ in range(K)]
+            # Each launch's arguments formed before the loop, so that the host enqueues the
+            # launches back to back (a caller's serving loop in compiled code issues them with a
+            # few microseconds between calls); one event pair brackets the K launches.
+            args = [(handle, ptr(d_slots), B, B, ptr(served[k]), 1, 0, ptr(served[k + 1]),
+                     ptr(s_state), ptr(s_hist), ptr(s_pos), ptr(cache) if cached else None, None,
+                     None, None, None, ptr(status), sp) for k in range(K)]
+            fn = L.uor_fbs_serve_slots_async
+            ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             torch.cuda.synchronize()
             t0 = time.perf_counter()
+            ev[0].record(stream)
             for k in range(K):
-                ev[k][0].record(stream)
-                check(L.uor_fbs_serve_slots_async(
-                    model.handle, ptr(d_slots), B, B, ptr(served[k]), 1, 0, ptr(served[k + 1]),
-                    ptr(s_state), ptr(s_hist), ptr(s_pos), ptr(cache) if cached else None, None,
-                    None, None, None, ptr(status), sp))
-                ev[k][1].record(stream)
+                check(fn(*args[k]))
+            ev[1].record(stream)
             torch.cuda.synchronize()
             wall_ = time.perf_counter() - t0
             assert int(status.abs().sum()) == 0, "serving loop failed"
             same_ = np.array_equal(served[1:].cpu().numpy().view(np.uint32).T, host_reply[:, :K])
-            return wall_, [s_.elapsed_time(e_) for s_, e_ in ev], same_
+            return wall_, [ev[0].elapsed_time(ev[1]) / K], same_
 
         bare_wall, bare_ms, bare_same = serve_loop(False)
         serve_wall, serve_ms, same_serve = serve_loop(True)
+        # The same launches with the writer inside the step (UOR_FBS_SERVE_SCAN=fused at model
+        # creation), for comparison with the drawer-major scan of the default.
+        fused_out = None
+        if model.block_waves(B) == 2:
+            os.environ["UOR_FBS_SERVE_SCAN"] = "fused"
+            try:
+                model_f = hip.Model(art, device=0)
+            finally:
+                del os.environ["UOR_FBS_SERVE_SCAN"]
+            f_wall, f_ms, f_same = serve_loop(True, model_f.handle)
+            fused_out = {"tokens_per_s": round(B * K / f_wall, 1),
+                         "ms_per_launch": round(float(np.mean(f_ms)), 4),
+                         "tokens_equal_decode": bool(f_same),
+                         "what": "the writer inside the step (one kernel a launch)"}
+            del model_f
         out["serving"] = {
             "tokens_per_s": round(B * K / serve_wall, 1),
             "ms_per_launch": round(float(np.mean(serve_ms)), 4),
             "launches": K, "sessions": B,
-            "kernel": kernel.replace("fbs_decode", "fbs_prefill"),
+            "kernel": (kernel.replace("fbs_decode", "fbs_prefill") +
+                       (" + fbs_serve_plan + fbs_serve_scan + fbs_serve_finish"
+                        if fused_out is not None and spec.table == "i16" else "")),
             "workload": f"{B} sessions in permuted device slots, one token each per launch, "
                         f"{K} launches from the prefilled state",
             "tokens_equal_decode": bool(same_serve),
@@ -1126,6 +1146,7 @@ def main():
             "without_cache": {"tokens_per_s": round(B * K / bare_wall, 1),
                               "ms_per_launch": round(float(np.mean(bare_ms)), 4),
                               "tokens_equal_decode": bool(bare_same)},
+            "fused_writer": fused_out,
         }
         if not same_serve:
             print("bench.py: the serving loop's tokens differ from the decode's", file=sys.stderr)

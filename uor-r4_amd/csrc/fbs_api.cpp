@@ -47,6 +47,11 @@ FBS_LAUNCHER(fbs_prefill_pair_ham)
 FBS_LAUNCHER(fbs_decode_pair_ham)
 FBS_LAUNCHER(fbs_rows_pair_ham)
 #undef FBS_LAUNCHER
+// The deferred writer's drawer-major scan and hand-out (fbs_serve.hip).
+hipError_t launch_fbs_serve_scan(const DevModel &M, const ServeScan &J, uint32_t blocks,
+                                 hipStream_t stream);
+hipError_t launch_fbs_serve_finish(const DevModel &M, const ServeScan &J, hipStream_t stream);
+hipError_t launch_fbs_fill_u32(uint32_t *p, uint64_t n, uint32_t v, hipStream_t stream);
 }
 
 using namespace fbs;
@@ -91,6 +96,7 @@ struct uor_fbs_handle {
   bool pair = false;
   size_t pair_lds = 0;
   uint32_t pair_grid = 0;
+  uint32_t cus = 0;      // the device's compute units
   size_t lds_limit = 0;  // LDS bytes a block may take
   int32_t *ring = nullptr;
   int64_t *hist = nullptr;
@@ -101,6 +107,17 @@ struct uor_fbs_handle {
   // This device's copy of the allocation-free decode's scratch array (null if its address could
   // not be read; that entry point then refuses).
   unsigned char *scratch = nullptr;
+  // The deferred writer of one-token serving launches (fbs_serve.hip): the (drawer, first
+  // member) chunks of 64 members, and the job buffers for `jobs_cap` sequences (grown, never
+  // shrunk). UOR_FBS_SERVE_SCAN=fused at model creation keeps the writer in the step.
+  bool serve_drawer_major = true;
+  const uint2 *serve_chunks = nullptr;
+  uint32_t serve_nchunks = 0, serve_max_chunks = 0;  // chunks, and the most of one drawer
+  uint32_t jobs_cap = 0, item_cap = 0;
+  uint32_t *job_query = nullptr, *job_flag = nullptr, *drawer_count = nullptr,
+           *drawer_list = nullptr, *item_count = nullptr;
+  uint4 *items = nullptr;
+  unsigned long long *job_best = nullptr;
 
   ~uor_fbs_handle() {
     int prev = 0;
@@ -110,7 +127,50 @@ struct uor_fbs_handle {
     if (ring) (void)hipFree(ring);
     if (hist) (void)hipFree(hist);
     if (pay) (void)hipFree(pay);
+    free_jobs();
     (void)hipSetDevice(prev);
+  }
+
+  void free_jobs() {
+    for (void *p : {(void *)job_query, (void *)job_flag, (void *)drawer_count, (void *)drawer_list,
+                    (void *)job_best, (void *)items, (void *)item_count})
+      if (p) (void)hipFree(p);
+    job_query = job_flag = drawer_count = drawer_list = item_count = nullptr;
+    items = nullptr;
+    job_best = nullptr;
+    jobs_cap = item_cap = 0;
+  }
+
+  // The deferred writer's job buffers for n sequences: flags and drawer counts start at zero
+  // (a fill kernel on `stream`; the hand-out kernel clears what a launch set).
+  int ensure_jobs(uint32_t n, hipStream_t stream) {
+    if (n <= jobs_cap) return 0;
+    free_jobs();
+    const size_t words = M.d / 2;
+    // Items: a chunk's slices are at most its drawer's sessions / 16 + 1, and the sessions of all
+    // drawers together n P.
+    const uint64_t cap = serve_nchunks + (uint64_t)serve_max_chunks *
+                                             (((uint64_t)n * M.P + kServeSessions - 1) / kServeSessions);
+    if (cap > 0xffffffffull) return fail(UOR_FBS_ERR_UNSUPPORTED, "too many serving sessions");
+    hipError_t e = hipMalloc((void **)&job_query, (size_t)n * words * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc((void **)&job_flag, (size_t)n * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc((void **)&job_best, (size_t)n * sizeof(unsigned long long));
+    if (e == hipSuccess) e = hipMalloc((void **)&drawer_count, (size_t)M.D * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc((void **)&drawer_list, (size_t)M.D * n * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc((void **)&items, (size_t)cap * sizeof(uint4));
+    if (e == hipSuccess) e = hipMalloc((void **)&item_count, sizeof(uint32_t));
+    if (e != hipSuccess) {
+      free_jobs();
+      return hip_fail(e, "hipMalloc(serving jobs)");
+    }
+    if ((e = launch_fbs_fill_u32(job_flag, n, 0, stream)) != hipSuccess ||
+        (e = launch_fbs_fill_u32(drawer_count, M.D, 0, stream)) != hipSuccess) {
+      free_jobs();
+      return hip_fail(e, "kernel launch");
+    }
+    jobs_cap = n;
+    item_cap = (uint32_t)cap;
+    return 0;
   }
 
   // Payload words (i64) one session keeps: slots x context x d.
@@ -598,6 +658,10 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
   // every step then scans its candidates; the results are the same either way).
   const char *wm = getenv("UOR_FBS_WRITER_MEMORY");
   M.writer_memory = (wm && wm[0] == '0' && !wm[1]) ? 0u : 1u;
+  // UOR_FBS_SERVE_SCAN=fused keeps the writer inside one-token serving launches (for
+  // measurement: the drawer-major scan is the default; the results are the same either way).
+  const char *ss = getenv("UOR_FBS_SERVE_SCAN");
+  h->serve_drawer_major = !(ss && std::strcmp(ss, "fused") == 0);
   M.w_recip = (1ull << 32) / M.W;
   int64_t eps_int[9];
   for (int sh = 0; sh <= 8; sh++) eps_int[sh] = norm_eps(m->eps_mantissa, m->eps_exp, sh);
@@ -732,6 +796,15 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
     if (mem.empty()) mem.push_back(0);
     if ((st = h->upload(off.data(), off.size(), &M.offsets))) return done(st);
     if ((st = h->upload(mem.data(), mem.size(), &M.members))) return done(st);
+    // The deferred writer's scan chunks: each drawer's members, 64 at a time.
+    std::vector<uint2> chunks;
+    for (uint32_t c = 0; c < r.D; c++) {
+      const uint32_t size = off[c + 1] - off[c], nch = (size + kServeRows - 1) / kServeRows;
+      for (uint32_t k0 = 0; k0 < size; k0 += kServeRows) chunks.push_back(make_uint2(c, k0));
+      h->serve_max_chunks = nch > h->serve_max_chunks ? nch : h->serve_max_chunks;
+    }
+    h->serve_nchunks = (uint32_t)chunks.size();
+    if ((st = h->upload(chunks.data(), chunks.size(), &h->serve_chunks))) return done(st);
   }
   if ((st = h->upload(m->icosian, 120 * 8, &M.icosian))) return done(st);
   if ((st = h->upload(m->keep_q31, 16, &M.keep_q31))) return done(st);
@@ -757,6 +830,7 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
   h->pair = !(bw && bw[0] == '1' && !bw[1]) && h->pair_lds <= prop.sharedMemPerBlock &&
             (!M.ham.heads || (M.qpl == 1 && fbs::ham_pair_fits(M)));
   h->pair_grid = (uint32_t)prop.multiProcessorCount * 4;  // four SIMDs per CU
+  h->cus = (uint32_t)prop.multiProcessorCount;
   h->lds_limit = prop.sharedMemPerBlock;
   return done(0);
 }
@@ -1276,8 +1350,49 @@ extern "C" int uor_fbs_serve_slots_async(uor_fbs_handle *h, const uint32_t *slot
   A.cache_stride = slot_cache_layout(h->M).bytes;
   A.slide = slide;
   A.out_trace = out_trace;
+  // One token a session on the paired kernels of a 16-bit table with keyed drawers: the step
+  // stops at the drawer selection and the drawer-major scan (fbs_serve.hip) chooses the tokens.
+  const bool deferred = h->serve_drawer_major && h->pair && !h->M.ham.heads && !h->M.table8 &&
+                        h->M.head != 1 && h->M.d % 32 == 0 && prompt_len == 1 && gen == 0 &&
+                        !out_trace && sequences > 0;
+  hipStream_t st = (hipStream_t)stream;
+  if (deferred) {
+    int e = h->ensure_jobs(sequences, st);
+    if (e) return e;
+    A.job_query = h->job_query;
+    A.job_flag = h->job_flag;
+    A.job_best = h->job_best;
+    A.drawer_count = h->drawer_count;
+    A.drawer_list = h->drawer_list;
+    A.list_stride = h->jobs_cap;
+  }
   // The trace is recorded by the one-wavefront kernels.
-  return launch(h, A, (hipStream_t)stream, false, out_trace != nullptr);
+  int rc = launch(h, A, st, false, out_trace != nullptr);
+  if (rc || !deferred) return rc;
+  ServeScan J{};
+  J.chunks = h->serve_chunks;
+  J.nchunks = h->serve_nchunks;
+  J.items = h->items;
+  J.item_count = h->item_count;
+  J.item_cap = h->item_cap;
+  J.n = sequences;
+  J.gen = gen;
+  J.job_query = h->job_query;
+  J.job_flag = h->job_flag;
+  J.job_best = h->job_best;
+  J.drawer_count = h->drawer_count;
+  J.drawer_list = h->drawer_list;
+  J.list_stride = h->jobs_cap;
+  J.out_tokens = out_reply;
+  J.slots = slots;
+  J.cache = (uint8_t *)cache;
+  J.cache_stride = A.cache_stride;
+  // The scan's wavefronts take the planned items in turn: two a SIMD, or one an item.
+  const uint32_t blocks = h->item_cap < 8 * h->cus ? h->item_cap : 8 * h->cus;
+  hipError_t e = hipSuccess;
+  if (h->serve_nchunks) e = launch_fbs_serve_scan(h->M, J, blocks, st);
+  if (e == hipSuccess) e = launch_fbs_serve_finish(h->M, J, st);
+  return e != hipSuccess ? hip_fail(e, "kernel launch") : 0;
 }
 
 extern "C" int uor_fbs_serve_slots_stream_async(

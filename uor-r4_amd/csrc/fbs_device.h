@@ -251,6 +251,49 @@ struct RunArgs {
   const uint8_t *force_buckets;
   const uint64_t *force_codes;
   const uint8_t *force_mask;
+  // The deferred writer (one-token serving launches of the paired prefill kernels, i16 table,
+  // keyed drawers; null job_flag: the writer runs in the step). A step that does not take the
+  // writer's remembered result ends at its drawer selection: sequence s's query goes to
+  // job_query (d / 2 words of biased 16-bit pairs), each kept drawer c lists s in
+  // drawer_list[c][.] (drawer_count[c] entries, list_stride a drawer), job_best[s] starts at
+  // the largest (L1, token) and job_flag[s] at 1; fbs_serve_scan and fbs_serve_finish finish it.
+  uint32_t *job_query;
+  uint32_t *job_flag;
+  unsigned long long *job_best;
+  uint32_t *drawer_count;
+  uint32_t *drawer_list;
+  uint32_t list_stride;
+};
+
+// The drawer-major scan of the deferred writer's jobs (fbs_serve.hip): fbs_serve_plan lists the
+// launch's work items, one per (drawer, 64 members) chunk and slice of 16 sessions that kept the
+// drawer; fbs_serve_scan's blocks take the items in turn, score every member row against the
+// queries of the slice's sessions and combine each session's lowest (L1 << 32 | token) by a
+// 64-bit atomic minimum. Then fbs_serve_finish hands each job's token out (and to the slot
+// cache's writer memory) and clears the drawer counts and job flags.
+constexpr uint32_t kServeRows = 64;       // member rows a scan block holds, one per lane
+constexpr uint32_t kServeSessions = 16;   // sessions a scan block scores at once
+struct ServeScan {
+  const uint2 *chunks;                    // (drawer, first member) per chunk
+  uint32_t nchunks;
+  // The launch's work items, (first member index, rows, first drawer-list index, sessions)
+  // each, laid out by fbs_serve_plan from the drawer counts: item_count[0] of them (at most
+  // item_cap).
+  uint4 *items;
+  uint32_t *item_count;
+  uint32_t item_cap;
+  uint32_t n;                             // sequences of the launch
+  uint32_t gen;                           // the launch's generated steps (the out_tokens stride)
+  const uint32_t *job_query;
+  uint32_t *job_flag;
+  unsigned long long *job_best;
+  uint32_t *drawer_count;
+  const uint32_t *drawer_list;
+  uint32_t list_stride;
+  uint32_t *out_tokens;
+  const uint32_t *slots;
+  uint8_t *cache;                         // nullable
+  uint32_t cache_stride;
 };
 
 // A traced position's record (uor_fbs_decision_sequences): with the decisions, each layer's rate

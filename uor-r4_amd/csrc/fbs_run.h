@@ -1431,7 +1431,8 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
                                          const bool (&qv)[Q], const uint32_t (&qi)[Q], uint32_t tok,
                                          bool want_writer, uint32_t *chosen, uint32_t *kept_out,
                                          int32_t *query_out, PartClock<CLK> &clk,
-                                         int64_t *gst, uint32_t t = 0, int64_t *pay = nullptr) {
+                                         int64_t *gst, uint32_t t = 0, int64_t *pay = nullptr,
+                                         bool defer = false) {
   if (tok >= M.vocab) return 1;
   if constexpr (HM) {  // the read at this row needs x_0..=x_t (session.rs:4149-4152)
     if (lane == 0) S.tok[t] = tok;
@@ -1735,6 +1736,28 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
   // the last one the writer ran on (a sequence settled on a fixed point) takes its result.
   const bool reuse = S.wmeta[1] != 0 && __all(same);
   if (lane == 0) S.wmeta[2] = reuse;
+  if (defer) {
+    // The deferred writer: the remembered result, or the drawer selection alone (wmeta[2] = 2:
+    // a job for the drawer-major scan, whose token the memory takes once it is known).
+    if (reuse) {
+      if (kept_out && lane < M.P) kept_out[lane] = S.kept[lane];
+      *chosen = S.wmeta[0];
+      return 0;
+    }
+    wave_sync();
+    uint32_t b, e;
+    writer_select(M, S.xbar, S.dscore, S.kept, lane, b, e);
+    if (kept_out && lane < M.P) kept_out[lane] = S.kept[lane];
+#pragma unroll
+    for (int k = 0; k < Q; k++)
+      if (qv[k]) *(int4 *)(S.wq + 4 * qi[k]) = qq[k];
+    if (lane == 0) {
+      S.wmeta[1] = 0;
+      S.wmeta[2] = 2;
+    }
+    *chosen = UINT32_MAX;
+    return 0;
+  }
   clk.sync(kPartFinal, kPartSync6);  // 6: the query and the reuse flag
   *chosen = pair_writer<SW, T8, CLK>(M, S, 0, lane, kept_out, clk);
   if (!reuse) {
@@ -1817,7 +1840,7 @@ __device__ __forceinline__ int step_window(const DevModel &M, const Lds &S, int3
                                            const bool (&qv)[Q], const uint32_t (&qi)[Q],
                                            uint32_t tok, bool want_writer, bool fresh,
                                            uint32_t *chosen, PartClock<CLK> &clk,
-                                           int64_t *pay = nullptr) {
+                                           int64_t *pay = nullptr, bool defer = false) {
   if (tok >= M.vocab) return 1;
   const uint32_t d = M.d, W = M.W;
   const uint32_t next = base + 1 == W ? 0 : base + 1;  // the next step's ring slot
@@ -1916,7 +1939,7 @@ __device__ __forceinline__ int step_window(const DevModel &M, const Lds &S, int3
   if constexpr (HM) {  // the readout read's odd heads, at every row (step_main)
     if (M.ham.at[M.L] >= 0) ham_help<Q>(M, S, pay, lane, qv, qi);
   }
-  if (!want_writer) return 0;
+  if (!want_writer || defer) return 0;  // the deferred writer runs on wave 0 alone
   clk.sync(kPartFinal, kPartSync6);  // 6: the query and the reuse flag
   *chosen = pair_writer<SW, T8, CLK>(M, S, 1, lane, nullptr, clk);
   return 0;
@@ -2026,6 +2049,10 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
   const uint32_t lane = threadIdx.x % kWave, wave = uniform32(threadIdx.x / kWave);
   // Paired blocks: wave 0 keeps the recurrence state, wave 1 the window ring.
   const bool keeps_state = NW == 1 || wave == 0, keeps_ring = NW == 1 || wave == 1;
+  // The deferred writer (RunArgs::job_flag): compiled into the paired prefill kernels of a
+  // 16-bit table only, the one-token serving launches' family.
+  constexpr bool kDefer = PH == kPhasePrefill && NW == 2 && !HM && !T8 && !CLK && !DT;
+  const bool defer = kDefer && A.job_flag != nullptr;
   const bool writes_out = wave == 0 && lane == 0;
   PartClock<CLK> clk;
   if constexpr (CLK) clk.acc = S.clk + wave * kParts;
@@ -2222,10 +2249,37 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
         }
         if (wave == 0)
           status = step_main<Q, SW, T8, CLK, HM>(M, S, ln, qv, qs, tok, want, &chosen, kept_out,
-                                                 query_out, clk, stb, pos, pay);
+                                                 query_out, clk, stb, pos, pay, defer);
         else
           status = step_window<Q, SW, T8, CLK, HM>(M, S, ring, hist, base, ln, qv, qs, tok, want,
-                                                   t == 0 && fresh, &chosen, clk, pay);
+                                                   t == 0 && fresh, &chosen, clk, pay, defer);
+        if constexpr (kDefer) {
+          // A deferred writer's job: the query as biased pairs, the session in each kept
+          // drawer's list, its best reset (the scan kernel's atomic minimum starts there).
+          if (defer && wave == 0 && status == 0) {
+            wave_sync();
+            if (S.wmeta[2] == 2) {
+              uint32_t *jq = A.job_query + (uint64_t)s * (d / 2);
+#pragma unroll
+              for (int k = 0; k < Q; k++)
+                if (qv[k]) {
+                  const int4 q = *(const int4 *)(S.xbar + 4 * qi[k]);
+                  *(uint2 *)(jq + 2 * qi[k]) =
+                      make_uint2((uint32_t)(q.x + 32768) | ((uint32_t)(q.y + 32768) << 16),
+                                 (uint32_t)(q.z + 32768) | ((uint32_t)(q.w + 32768) << 16));
+                }
+              if (lane < M.P) {
+                const uint32_t c = S.kept[lane];
+                const uint32_t at = atomicAdd(A.drawer_count + c, 1u);
+                if (at < A.list_stride) A.drawer_list[(uint64_t)c * A.list_stride + at] = s;
+              }
+              if (lane == 0) {
+                A.job_best[s] = ~0ull;
+                A.job_flag[s] = 1u;
+              }
+            }
+          }
+        }
       }
       if (status) break;
       done++;

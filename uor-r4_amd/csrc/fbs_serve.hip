@@ -1,0 +1,193 @@
+// fbs_serve.hip - the deferred writer of one-token serving launches: the drawer-major scan of
+// every session's kept drawers, then the hand-out of each session's token.
+//
+// A serving launch steps every session by one token (serve_step, RS stack/session.rs:3405): the
+// paired prefill kernel runs the step up to the writer's drawer selection and leaves a job per
+// session (RunArgs::job_flag). The writer's choice is the lowest (L1, token) over the members of
+// the session's kept drawers (session.rs:4100-4121, twin fbs_core.h:606-623); sessions that
+// keep the same drawer read the same member rows, so the scan here is laid out by drawer: a
+// block holds 64 member rows of one drawer in registers, one row a lane, and scores them against
+// the queries of up to 16 sessions that kept the drawer at a time (staged in LDS and read as
+// broadcasts), each (row, session) L1 by packed v_sad_u16 over biased pairs. Each session's
+// lowest (L1 << 32 | token) over a block's rows goes to its job by a 64-bit atomic minimum:
+// the minimum of the packed pairs is the lexicographic one (the reference's lower token on equal
+// L1), whatever order the blocks run in. A row is read once per 16 sessions instead of once per
+// session, so the launch's candidate bytes shrink by the sessions a drawer serves.
+#include <hip/hip_runtime.h>
+
+#include "fbs_run.h"
+
+namespace fbs {
+
+// The launch's work items from the drawer counts: chunk i = (drawer c, members k0 ..) gets
+// ceil(n_c / 16) items, one per slice of 16 sessions of c's list, listed in chunk order at the
+// exclusive prefix sum of the counts (one block; each thread takes a run of consecutive chunks).
+// An item is (first member index, rows, first list index, sessions): what its scan loads first.
+__global__ __launch_bounds__(1024) void fbs_serve_plan(DevModel M, ServeScan J) {
+  __shared__ uint32_t part[1024];
+  const uint32_t t = threadIdx.x, T = blockDim.x;
+  const uint32_t per = (J.nchunks + T - 1) / T, c0 = t * per;
+  const uint32_t c1 = c0 + per < J.nchunks ? c0 + per : J.nchunks;
+  uint32_t mine = 0;
+  for (uint32_t i = c0; i < c1; i++) {
+    uint32_t nc = J.drawer_count[J.chunks[i].x];
+    nc = nc < J.list_stride ? nc : J.list_stride;
+    mine += (nc + kServeSessions - 1) / kServeSessions;
+  }
+  part[t] = mine;
+  __syncthreads();
+  for (uint32_t o = 1; o < T; o <<= 1) {  // inclusive prefix sums (Hillis-Steele)
+    const uint32_t v = t >= o ? part[t - o] : 0u;
+    __syncthreads();
+    part[t] += v;
+    __syncthreads();
+  }
+  uint32_t at = part[t] - mine;
+  for (uint32_t i = c0; i < c1; i++) {
+    const uint2 ch = J.chunks[i];
+    uint32_t nc = J.drawer_count[ch.x];
+    nc = nc < J.list_stride ? nc : J.list_stride;
+    const uint32_t beg = M.offsets[ch.x] + ch.y, end = M.offsets[ch.x + 1];
+    const uint32_t rows = end - beg < kServeRows ? end - beg : kServeRows;
+    for (uint32_t g = 0; g < nc; g += kServeSessions, at++) {
+      const uint32_t ns = nc - g < kServeSessions ? nc - g : kServeSessions;
+      if (at < J.item_cap)
+        J.items[at] = make_uint4(beg, rows, ch.x * J.list_stride + g, ns);
+    }
+  }
+  if (t == T - 1) J.item_count[0] = part[t] < J.item_cap ? part[t] : J.item_cap;
+}
+
+// The blocks (a wavefront each) take the planned items in turn: an item scores `rows` member
+// rows from its first member index (one a lane, in registers) against `ns` sessions of its
+// drawer's list, whose query words are staged in LDS and read as broadcasts (every lane reads
+// the same words), four sessions at a time. RW: the row words (biased 16-bit pairs) a lane holds
+// at once; rows of more words are scored in segments of RW, the sessions' sums carried across.
+// (Query words read as scalars straight from memory measured slower: each scalar load's wait
+// lands on the sums' path.)
+template <int RW>
+__global__ __launch_bounds__(64) void fbs_serve_scan(DevModel M, ServeScan J) {
+  __shared__ __align__(16) uint32_t qs[kServeSessions * RW];
+  const uint32_t lane = threadIdx.x;
+  const uint32_t total = uniform32(J.item_count[0]);
+  const uint32_t words = M.d / 2;
+  for (uint32_t it = blockIdx.x; it < total; it += gridDim.x) {
+    const uint4 item = J.items[it];
+    const uint32_t beg = uniform32(item.x), rows = uniform32(item.y);
+    const uint32_t lbeg = uniform32(item.z), ns = uniform32(item.w);
+    const bool valid = lane < rows;
+    const uint32_t tok = valid ? M.members[beg + lane] : 0u;
+    const uint4 *row = (const uint4 *)((const uint32_t *)M.table_b + (uint64_t)tok * words);
+    const uint32_t *list = J.drawer_list + lbeg;
+    uint32_t sid[kServeSessions];
+#pragma unroll
+    for (uint32_t i = 0; i < kServeSessions; i++) sid[i] = i < ns ? uniform32(list[i]) : 0u;
+    uint32_t acc[kServeSessions];
+#pragma unroll
+    for (uint32_t i = 0; i < kServeSessions; i++) acc[i] = 0;
+    for (uint32_t seg = 0; seg < words; seg += RW) {
+      // The sessions' query words of this segment into LDS (RW / 4 quads a session), once the
+      // last segment's (or item's) reads are done.
+      wave_sync();
+      for (uint32_t x = lane; x < ns * (RW / 4); x += kWave) {
+        const uint32_t i = x / (RW / 4), w = x % (RW / 4);
+        *(uint4 *)(qs + 4 * x) =
+            *(const uint4 *)(J.job_query + (uint64_t)list[i] * words + seg + 4 * w);
+      }
+      uint4 r[RW / 4];
+#pragma unroll
+      for (uint32_t w = 0; w < RW / 4; w++) r[w] = row[seg / 4 + w];
+      wave_sync();
+      // Four sessions at a time (four independent sums in flight), as many groups as the slice
+      // fills; a group's sessions past ns read words never staged and are not used.
+#pragma unroll
+      for (uint32_t i0 = 0; i0 < kServeSessions; i0 += 4) {
+        if (i0 < ns) {
+#pragma unroll
+          for (uint32_t w = 0; w < RW / 4; w++) {
+#pragma unroll
+            for (uint32_t i = i0; i < i0 + 4; i++) {
+              const uint4 q = *(const uint4 *)(qs + i * RW + 4 * w);
+              uint32_t a = acc[i];
+              a = sad2_u16(q.x, r[w].x, a);
+              a = sad2_u16(q.y, r[w].y, a);
+              a = sad2_u16(q.z, r[w].z, a);
+              a = sad2_u16(q.w, r[w].w, a);
+              acc[i] = a;
+            }
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < kServeSessions; i++) {
+      if (i < ns) {
+        const uint64_t v = valid ? ((uint64_t)acc[i] << 32) | tok : ~0ull;
+        const uint64_t best = wave_reduce64(v, OpMin());
+        if (lane == 0 && best != ~0ull) atomicMin(J.job_best + sid[i], (unsigned long long)best);
+      }
+    }
+  }
+}
+
+// Each job's token to the launch's output and to its slot cache's writer memory (the query and
+// kept drawers are there already); the drawer counts and job flags cleared for the next launch.
+__global__ __launch_bounds__(256) void fbs_serve_finish(DevModel M, ServeScan J) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (blockIdx.x == 0)
+    for (uint32_t c = threadIdx.x; c < M.D; c += blockDim.x) J.drawer_count[c] = 0;
+  if (i >= J.n || !J.job_flag[i]) return;
+  J.job_flag[i] = 0;
+  const uint32_t tok = (uint32_t)J.job_best[i];
+  J.out_tokens[(uint64_t)i * (J.gen + 1)] = tok;
+  if (J.cache) {
+    uint32_t *head = (uint32_t *)(J.cache + (uint64_t)J.slots[i] * J.cache_stride);
+    head[1] = M.writer_memory;
+    head[2] = tok;
+  }
+}
+
+// Sets n words to v (the job buffers' first state; no memset node in a captured launch).
+__global__ __launch_bounds__(256) void fbs_fill_u32(uint32_t *p, uint64_t n, uint32_t v) {
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (uint64_t)gridDim.x * blockDim.x)
+    p[i] = v;
+}
+
+// The plan (one block), then the scan over `blocks` wavefronts.
+hipError_t launch_fbs_serve_scan(const DevModel &M, const ServeScan &J, uint32_t blocks,
+                                 hipStream_t stream) {
+  const uint32_t words = M.d / 2;
+  if (words % 16 || blocks == 0) return hipErrorInvalidValue;  // widths are multiples of 32
+  DevModel m = M;
+  ServeScan j = J;
+  void *pargs[] = {&m, &j};
+  hipError_t e = hipLaunchKernel((const void *)fbs_serve_plan, dim3(1), dim3(1024), pargs, 0, stream);
+  if (e != hipSuccess) return e;
+  void *args[] = {&m, &j};
+  const void *f = words % 128 == 0  ? (const void *)fbs_serve_scan<128>
+                  : words % 64 == 0 ? (const void *)fbs_serve_scan<64>
+                  : words % 32 == 0 ? (const void *)fbs_serve_scan<32>
+                                    : (const void *)fbs_serve_scan<16>;
+  e = hipLaunchKernel(f, dim3(blocks), dim3(kWave), args, 0, stream);
+  return e != hipSuccess ? e : hipGetLastError();
+}
+
+hipError_t launch_fbs_serve_finish(const DevModel &M, const ServeScan &J, hipStream_t stream) {
+  DevModel m = M;
+  ServeScan j = J;
+  void *args[] = {&m, &j};
+  const uint32_t blocks = (J.n + 255) / 256;
+  hipError_t e = hipLaunchKernel((const void *)fbs_serve_finish, dim3(blocks ? blocks : 1), dim3(256),
+                                 args, 0, stream);
+  return e != hipSuccess ? e : hipGetLastError();
+}
+
+hipError_t launch_fbs_fill_u32(uint32_t *p, uint64_t n, uint32_t v, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  const uint64_t blocks = (n + 255) / 256;
+  fbs_fill_u32<<<dim3(blocks < 1024 ? (uint32_t)blocks : 1024u), dim3(256), 0, stream>>>(p, n, v);
+  return hipGetLastError();
+}
+
+}  // namespace fbs
