@@ -1136,7 +1136,7 @@ def main():
             "ms_per_launch": round(float(np.mean(serve_ms)), 4),
             "launches": K, "sessions": B,
             "kernel": (kernel.replace("fbs_decode", "fbs_prefill") +
-                       (" + fbs_serve_plan + fbs_serve_scan + fbs_serve_finish"
+                       (" + fbs_serve_scan + fbs_serve_finish"
                         if fused_out is not None and spec.table == "i16" else "")),
             "workload": f"{B} sessions in permuted device slots, one token each per launch, "
                         f"{K} launches from the prefilled state",

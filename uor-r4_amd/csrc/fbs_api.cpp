@@ -50,7 +50,6 @@ FBS_LAUNCHER(fbs_rows_pair_ham)
 // The deferred writer's drawer-major scan and hand-out (fbs_serve.hip).
 hipError_t launch_fbs_serve_scan(const DevModel &M, const ServeScan &J, uint32_t blocks,
                                  hipStream_t stream);
-hipError_t launch_fbs_serve_finish(const DevModel &M, const ServeScan &J, hipStream_t stream);
 hipError_t launch_fbs_fill_u32(uint32_t *p, uint64_t n, uint32_t v, hipStream_t stream);
 }
 
@@ -107,12 +106,12 @@ struct uor_fbs_handle {
   // This device's copy of the allocation-free decode's scratch array (null if its address could
   // not be read; that entry point then refuses).
   unsigned char *scratch = nullptr;
-  // The deferred writer of one-token serving launches (fbs_serve.hip): the (drawer, first
-  // member) chunks of 64 members, and the job buffers for `jobs_cap` sequences (grown, never
-  // shrunk). UOR_FBS_SERVE_SCAN=fused at model creation keeps the writer in the step.
+  // The deferred writer of one-token serving launches (fbs_serve.hip): the drawers' chunks of 64
+  // members (all, and the most of one drawer), and the job buffers for `jobs_cap` sequences
+  // (grown, never shrunk). UOR_FBS_SERVE_SCAN=fused at model creation keeps the writer in the
+  // step.
   bool serve_drawer_major = true;
-  const uint2 *serve_chunks = nullptr;
-  uint32_t serve_nchunks = 0, serve_max_chunks = 0;  // chunks, and the most of one drawer
+  uint32_t serve_nchunks = 0, serve_max_chunks = 0;
   uint32_t jobs_cap = 0, item_cap = 0;
   uint32_t *job_query = nullptr, *job_flag = nullptr, *drawer_count = nullptr,
            *drawer_list = nullptr, *item_count = nullptr;
@@ -164,7 +163,8 @@ struct uor_fbs_handle {
       return hip_fail(e, "hipMalloc(serving jobs)");
     }
     if ((e = launch_fbs_fill_u32(job_flag, n, 0, stream)) != hipSuccess ||
-        (e = launch_fbs_fill_u32(drawer_count, M.D, 0, stream)) != hipSuccess) {
+        (e = launch_fbs_fill_u32(drawer_count, M.D, 0, stream)) != hipSuccess ||
+        (e = launch_fbs_fill_u32(item_count, 1, 0, stream)) != hipSuccess) {
       free_jobs();
       return hip_fail(e, "kernel launch");
     }
@@ -797,14 +797,11 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
     if ((st = h->upload(off.data(), off.size(), &M.offsets))) return done(st);
     if ((st = h->upload(mem.data(), mem.size(), &M.members))) return done(st);
     // The deferred writer's scan chunks: each drawer's members, 64 at a time.
-    std::vector<uint2> chunks;
     for (uint32_t c = 0; c < r.D; c++) {
-      const uint32_t size = off[c + 1] - off[c], nch = (size + kServeRows - 1) / kServeRows;
-      for (uint32_t k0 = 0; k0 < size; k0 += kServeRows) chunks.push_back(make_uint2(c, k0));
+      const uint32_t nch = (off[c + 1] - off[c] + kServeRows - 1) / kServeRows;
+      h->serve_nchunks += nch;
       h->serve_max_chunks = nch > h->serve_max_chunks ? nch : h->serve_max_chunks;
     }
-    h->serve_nchunks = (uint32_t)chunks.size();
-    if ((st = h->upload(chunks.data(), chunks.size(), &h->serve_chunks))) return done(st);
   }
   if ((st = h->upload(m->icosian, 120 * 8, &M.icosian))) return done(st);
   if ((st = h->upload(m->keep_q31, 16, &M.keep_q31))) return done(st);
@@ -1354,7 +1351,8 @@ extern "C" int uor_fbs_serve_slots_async(uor_fbs_handle *h, const uint32_t *slot
   // stops at the drawer selection and the drawer-major scan (fbs_serve.hip) chooses the tokens.
   const bool deferred = h->serve_drawer_major && h->pair && !h->M.ham.heads && !h->M.table8 &&
                         h->M.head != 1 && h->M.d % 32 == 0 && prompt_len == 1 && gen == 0 &&
-                        !out_trace && sequences > 0;
+                        !out_trace && sequences > 0 &&
+                        (uint64_t)h->M.D * sequences < (1ull << 32);  // drawer-list indices
   hipStream_t st = (hipStream_t)stream;
   if (deferred) {
     int e = h->ensure_jobs(sequences, st);
@@ -1365,13 +1363,14 @@ extern "C" int uor_fbs_serve_slots_async(uor_fbs_handle *h, const uint32_t *slot
     A.drawer_count = h->drawer_count;
     A.drawer_list = h->drawer_list;
     A.list_stride = h->jobs_cap;
+    A.items = h->items;
+    A.item_count = h->item_count;
+    A.item_cap = h->item_cap;
   }
   // The trace is recorded by the one-wavefront kernels.
   int rc = launch(h, A, st, false, out_trace != nullptr);
   if (rc || !deferred) return rc;
   ServeScan J{};
-  J.chunks = h->serve_chunks;
-  J.nchunks = h->serve_nchunks;
   J.items = h->items;
   J.item_count = h->item_count;
   J.item_cap = h->item_cap;
@@ -1387,11 +1386,10 @@ extern "C" int uor_fbs_serve_slots_async(uor_fbs_handle *h, const uint32_t *slot
   J.slots = slots;
   J.cache = (uint8_t *)cache;
   J.cache_stride = A.cache_stride;
-  // The scan's wavefronts take the planned items in turn: two a SIMD, or one an item.
-  const uint32_t blocks = h->item_cap < 8 * h->cus ? h->item_cap : 8 * h->cus;
-  hipError_t e = hipSuccess;
-  if (h->serve_nchunks) e = launch_fbs_serve_scan(h->M, J, blocks, st);
-  if (e == hipSuccess) e = launch_fbs_serve_finish(h->M, J, st);
+  // The scan's wavefronts take the items in turn: two a SIMD, or one an item.
+  uint32_t blocks = h->item_cap < 8 * h->cus ? h->item_cap : 8 * h->cus;
+  blocks = blocks ? blocks : 1;
+  const hipError_t e = launch_fbs_serve_scan(h->M, J, blocks, st);
   return e != hipSuccess ? hip_fail(e, "kernel launch") : 0;
 }
 

@@ -256,29 +256,29 @@ struct RunArgs {
   // writer's remembered result ends at its drawer selection: sequence s's query goes to
   // job_query (d / 2 words of biased 16-bit pairs), each kept drawer c lists s in
   // drawer_list[c][.] (drawer_count[c] entries, list_stride a drawer), job_best[s] starts at
-  // the largest (L1, token) and job_flag[s] at 1; fbs_serve_scan and fbs_serve_finish finish it.
+  // the largest (L1, token) and job_flag[s] at 1. The session that opens a slice of 16 entries
+  // of c's list appends the slice's work items, one per 64 members of c (ServeScan::items).
   uint32_t *job_query;
   uint32_t *job_flag;
   unsigned long long *job_best;
   uint32_t *drawer_count;
   uint32_t *drawer_list;
   uint32_t list_stride;
+  uint4 *items;
+  uint32_t *item_count;
+  uint32_t item_cap;
 };
 
-// The drawer-major scan of the deferred writer's jobs (fbs_serve.hip): fbs_serve_plan lists the
-// launch's work items, one per (drawer, 64 members) chunk and slice of 16 sessions that kept the
-// drawer; fbs_serve_scan's blocks take the items in turn, score every member row against the
-// queries of the slice's sessions and combine each session's lowest (L1 << 32 | token) by a
-// 64-bit atomic minimum. Then fbs_serve_finish hands each job's token out (and to the slot
-// cache's writer memory) and clears the drawer counts and job flags.
+// The drawer-major scan of the deferred writer's jobs (fbs_serve.hip). A work item is one
+// (drawer, 64 members) chunk and one slice of 16 sessions that kept the drawer:
+// (first member index, rows, first drawer-list index, drawer). fbs_serve_scan's blocks take the
+// items in turn, score every member row against the queries of the slice's sessions and
+// combine each session's lowest (L1 << 32 | token) by a 64-bit atomic minimum; then
+// fbs_serve_finish hands each job's token out (and to the slot cache's writer memory) and clears
+// the drawer counts and the item count for the next launch.
 constexpr uint32_t kServeRows = 64;       // member rows a scan block holds, one per lane
 constexpr uint32_t kServeSessions = 16;   // sessions a scan block scores at once
 struct ServeScan {
-  const uint2 *chunks;                    // (drawer, first member) per chunk
-  uint32_t nchunks;
-  // The launch's work items, (first member index, rows, first drawer-list index, sessions)
-  // each, laid out by fbs_serve_plan from the drawer counts: item_count[0] of them (at most
-  // item_cap).
   uint4 *items;
   uint32_t *item_count;
   uint32_t item_cap;

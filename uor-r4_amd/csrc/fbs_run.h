@@ -2271,7 +2271,19 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
               if (lane < M.P) {
                 const uint32_t c = S.kept[lane];
                 const uint32_t at = atomicAdd(A.drawer_count + c, 1u);
-                if (at < A.list_stride) A.drawer_list[(uint64_t)c * A.list_stride + at] = s;
+                if (at < A.list_stride) {
+                  A.drawer_list[(uint64_t)c * A.list_stride + at] = s;
+                  if (at % kServeSessions == 0) {  // this session opens a slice: its items
+                    const uint32_t b = M.offsets[c], e = M.offsets[c + 1];
+                    const uint32_t nch = (e - b + kServeRows - 1) / kServeRows;
+                    const uint32_t i0 = nch ? atomicAdd(A.item_count, nch) : 0u;
+                    for (uint32_t k = 0; k < nch && i0 + k < A.item_cap; k++) {
+                      const uint32_t m0 = b + kServeRows * k;
+                      A.items[i0 + k] = make_uint4(m0, e - m0 < kServeRows ? e - m0 : kServeRows,
+                                                   c * A.list_stride + at, c);
+                    }
+                  }
+                }
               }
               if (lane == 0) {
                 A.job_best[s] = ~0ull;

@@ -3,7 +3,8 @@
 //
 // A serving launch steps every session by one token (serve_step, RS stack/session.rs:3405): the
 // paired prefill kernel runs the step up to the writer's drawer selection and leaves a job per
-// session (RunArgs::job_flag). The writer's choice is the lowest (L1, token) over the members of
+// session (RunArgs::job_flag), and the session that opens a slice of 16 entries of a drawer's
+// list appends that slice's work items. The writer's choice is the lowest (L1, token) over the members of
 // the session's kept drawers (session.rs:4100-4121, twin fbs_core.h:606-623); sessions that
 // keep the same drawer read the same member rows, so the scan here is laid out by drawer: a
 // block holds 64 member rows of one drawer in registers, one row a lane, and scores them against
@@ -19,62 +20,29 @@
 
 namespace fbs {
 
-// The launch's work items from the drawer counts: chunk i = (drawer c, members k0 ..) gets
-// ceil(n_c / 16) items, one per slice of 16 sessions of c's list, listed in chunk order at the
-// exclusive prefix sum of the counts (one block; each thread takes a run of consecutive chunks).
-// An item is (first member index, rows, first list index, sessions): what its scan loads first.
-__global__ __launch_bounds__(1024) void fbs_serve_plan(DevModel M, ServeScan J) {
-  __shared__ uint32_t part[1024];
-  const uint32_t t = threadIdx.x, T = blockDim.x;
-  const uint32_t per = (J.nchunks + T - 1) / T, c0 = t * per;
-  const uint32_t c1 = c0 + per < J.nchunks ? c0 + per : J.nchunks;
-  uint32_t mine = 0;
-  for (uint32_t i = c0; i < c1; i++) {
-    uint32_t nc = J.drawer_count[J.chunks[i].x];
-    nc = nc < J.list_stride ? nc : J.list_stride;
-    mine += (nc + kServeSessions - 1) / kServeSessions;
-  }
-  part[t] = mine;
-  __syncthreads();
-  for (uint32_t o = 1; o < T; o <<= 1) {  // inclusive prefix sums (Hillis-Steele)
-    const uint32_t v = t >= o ? part[t - o] : 0u;
-    __syncthreads();
-    part[t] += v;
-    __syncthreads();
-  }
-  uint32_t at = part[t] - mine;
-  for (uint32_t i = c0; i < c1; i++) {
-    const uint2 ch = J.chunks[i];
-    uint32_t nc = J.drawer_count[ch.x];
-    nc = nc < J.list_stride ? nc : J.list_stride;
-    const uint32_t beg = M.offsets[ch.x] + ch.y, end = M.offsets[ch.x + 1];
-    const uint32_t rows = end - beg < kServeRows ? end - beg : kServeRows;
-    for (uint32_t g = 0; g < nc; g += kServeSessions, at++) {
-      const uint32_t ns = nc - g < kServeSessions ? nc - g : kServeSessions;
-      if (at < J.item_cap)
-        J.items[at] = make_uint4(beg, rows, ch.x * J.list_stride + g, ns);
-    }
-  }
-  if (t == T - 1) J.item_count[0] = part[t] < J.item_cap ? part[t] : J.item_cap;
-}
-
-// The blocks (a wavefront each) take the planned items in turn: an item scores `rows` member
-// rows from its first member index (one a lane, in registers) against `ns` sessions of its
-// drawer's list, whose query words are staged in LDS and read as broadcasts (every lane reads
-// the same words), four sessions at a time. RW: the row words (biased 16-bit pairs) a lane holds
-// at once; rows of more words are scored in segments of RW, the sessions' sums carried across.
-// (Query words read as scalars straight from memory measured slower: each scalar load's wait
-// lands on the sums' path.)
+// The blocks (a wavefront each) take the launch's items in turn: an item scores `rows` member
+// rows from its first member index (one a lane, in registers) against the sessions of its
+// slice of the drawer's list (16, or the rest of the list), whose query words are staged in LDS
+// and read as broadcasts (every lane reads the same words), four sessions at a time. RW: the row
+// words (biased 16-bit pairs) a lane holds at once; rows of more words are scored in segments of
+// RW, the sessions' sums carried across. (Query words read as scalars straight from memory
+// measured slower: each scalar load's wait lands on the sums' path.)
 template <int RW>
 __global__ __launch_bounds__(64) void fbs_serve_scan(DevModel M, ServeScan J) {
   __shared__ __align__(16) uint32_t qs[kServeSessions * RW];
   const uint32_t lane = threadIdx.x;
-  const uint32_t total = uniform32(J.item_count[0]);
+  uint32_t total = uniform32(J.item_count[0]);
+  total = total < J.item_cap ? total : J.item_cap;
   const uint32_t words = M.d / 2;
   for (uint32_t it = blockIdx.x; it < total; it += gridDim.x) {
     const uint4 item = J.items[it];
     const uint32_t beg = uniform32(item.x), rows = uniform32(item.y);
-    const uint32_t lbeg = uniform32(item.z), ns = uniform32(item.w);
+    const uint32_t lbeg = uniform32(item.z), c = uniform32(item.w);
+    uint32_t nc = uniform32(J.drawer_count[c]);
+    nc = nc < J.list_stride ? nc : J.list_stride;  // a list holds at most list_stride sessions
+    const uint32_t g = lbeg - c * J.list_stride;
+    if (g >= nc) continue;
+    const uint32_t ns = nc - g < kServeSessions ? nc - g : kServeSessions;
     const bool valid = lane < rows;
     const uint32_t tok = valid ? M.members[beg + lane] : 0u;
     const uint4 *row = (const uint4 *)((const uint32_t *)M.table_b + (uint64_t)tok * words);
@@ -85,19 +53,31 @@ __global__ __launch_bounds__(64) void fbs_serve_scan(DevModel M, ServeScan J) {
     uint32_t acc[kServeSessions];
 #pragma unroll
     for (uint32_t i = 0; i < kServeSessions; i++) acc[i] = 0;
+    // The query quads this lane stages: 16-byte piece lane % (RW / 4) of session 64 j / (RW / 4)
+    // + lane / (RW / 4), for each of the slice's kStage groups of 64 pieces.
+    constexpr uint32_t kStage = kServeSessions * (RW / 4) / kWave;
+    uint32_t stage_sid[kStage];
+#pragma unroll
+    for (uint32_t j = 0; j < kStage; j++) {
+      const uint32_t i = (lane + kWave * j) / (RW / 4);
+      stage_sid[j] = i < ns ? list[i] : list[0];
+    }
     for (uint32_t seg = 0; seg < words; seg += RW) {
-      // The sessions' query words of this segment into LDS (RW / 4 quads a session), once the
-      // last segment's (or item's) reads are done.
+      // Once the last segment's (or item's) reads are done: the sessions' query words of this
+      // segment go to LDS by direct loads (no registers), the rows' words to registers, every
+      // load issued before the first is waited for.
       wave_sync();
-      for (uint32_t x = lane; x < ns * (RW / 4); x += kWave) {
-        const uint32_t i = x / (RW / 4), w = x % (RW / 4);
-        *(uint4 *)(qs + 4 * x) =
-            *(const uint4 *)(J.job_query + (uint64_t)list[i] * words + seg + 4 * w);
-      }
+#pragma unroll
+      for (uint32_t j = 0; j < kStage; j++)
+        if (kWave * j < ns * (RW / 4))
+          __builtin_amdgcn_global_load_lds(
+              (global_void *)(J.job_query + (uint64_t)stage_sid[j] * words + seg +
+                              4 * (lane % (RW / 4))),
+              (lds_void *)(qs + 4 * kWave * j), 16, 0, 0);
       uint4 r[RW / 4];
 #pragma unroll
       for (uint32_t w = 0; w < RW / 4; w++) r[w] = row[seg / 4 + w];
-      wave_sync();
+      wait_lds_dma();
       // Four sessions at a time (four independent sums in flight), as many groups as the slice
       // fills; a group's sessions past ns read words never staged and are not used.
 #pragma unroll
@@ -131,11 +111,15 @@ __global__ __launch_bounds__(64) void fbs_serve_scan(DevModel M, ServeScan J) {
 }
 
 // Each job's token to the launch's output and to its slot cache's writer memory (the query and
-// kept drawers are there already); the drawer counts and job flags cleared for the next launch.
+// kept drawers are there already); the drawer counts, the item count and the job flags cleared
+// for the next launch. (Run by the scan's last block instead, each block then ending with a
+// device-scope release fence before its count, the scan measured 2.6 times slower.)
 __global__ __launch_bounds__(256) void fbs_serve_finish(DevModel M, ServeScan J) {
   const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (blockIdx.x == 0)
+  if (blockIdx.x == 0) {
     for (uint32_t c = threadIdx.x; c < M.D; c += blockDim.x) J.drawer_count[c] = 0;
+    if (threadIdx.x == 0) J.item_count[0] = 0;
+  }
   if (i >= J.n || !J.job_flag[i]) return;
   J.job_flag[i] = 0;
   const uint32_t tok = (uint32_t)J.job_best[i];
@@ -154,32 +138,22 @@ __global__ __launch_bounds__(256) void fbs_fill_u32(uint32_t *p, uint64_t n, uin
     p[i] = v;
 }
 
-// The plan (one block), then the scan over `blocks` wavefronts.
+// The scan over `blocks` wavefronts, then the hand-out.
 hipError_t launch_fbs_serve_scan(const DevModel &M, const ServeScan &J, uint32_t blocks,
                                  hipStream_t stream) {
   const uint32_t words = M.d / 2;
   if (words % 16 || blocks == 0) return hipErrorInvalidValue;  // widths are multiples of 32
   DevModel m = M;
   ServeScan j = J;
-  void *pargs[] = {&m, &j};
-  hipError_t e = hipLaunchKernel((const void *)fbs_serve_plan, dim3(1), dim3(1024), pargs, 0, stream);
-  if (e != hipSuccess) return e;
   void *args[] = {&m, &j};
-  const void *f = words % 128 == 0  ? (const void *)fbs_serve_scan<128>
-                  : words % 64 == 0 ? (const void *)fbs_serve_scan<64>
+  const void *f = words % 64 == 0   ? (const void *)fbs_serve_scan<64>
                   : words % 32 == 0 ? (const void *)fbs_serve_scan<32>
                                     : (const void *)fbs_serve_scan<16>;
-  e = hipLaunchKernel(f, dim3(blocks), dim3(kWave), args, 0, stream);
-  return e != hipSuccess ? e : hipGetLastError();
-}
-
-hipError_t launch_fbs_serve_finish(const DevModel &M, const ServeScan &J, hipStream_t stream) {
-  DevModel m = M;
-  ServeScan j = J;
-  void *args[] = {&m, &j};
-  const uint32_t blocks = (J.n + 255) / 256;
-  hipError_t e = hipLaunchKernel((const void *)fbs_serve_finish, dim3(blocks ? blocks : 1), dim3(256),
-                                 args, 0, stream);
+  hipError_t e = hipLaunchKernel(f, dim3(blocks), dim3(kWave), args, 0, stream);
+  if (e == hipSuccess) e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const uint32_t fin = (J.n + 255) / 256;
+  e = hipLaunchKernel((const void *)fbs_serve_finish, dim3(fin ? fin : 1), dim3(256), args, 0, stream);
   return e != hipSuccess ? e : hipGetLastError();
 }
 
