@@ -187,10 +187,10 @@ constexpr uint64_t ce_isqrt64(uint64_t n) {
   return r;
 }
 
-struct Seed384 {
+struct alignas(16) Seed384 {
   uint32_t v[384];
 };
-struct Seed256 {
+struct alignas(16) Seed256 {
   uint32_t v[256];
 };
 

@@ -424,6 +424,7 @@ __device__ __forceinline__ void gate_mul(const DevModel &M, const int64_t (&g)[4
 // The writer.
 
 constexpr uint32_t kWindowChunk = 8; // window rows in flight per lane
+constexpr uint32_t kPrologueLayers = 8;  // layers whose state words a lane loads all at once
 constexpr int kScanUnroll = 4;       // row groups per pipeline stage
 
 typedef __attribute__((address_space(1))) void global_void;
@@ -434,6 +435,13 @@ typedef __attribute__((address_space(3))) void lds_void;
 __device__ __forceinline__ void lds_dma_words(const uint32_t *src, uint32_t *dst, uint32_t n,
                                               uint32_t lane) {
   if (lane < n) __builtin_amdgcn_global_load_lds((global_void *)(src + lane), (lds_void *)dst, 4, 0, 0);
+}
+// Copies n quads (16 bytes each, 16-byte aligned) from global src to LDS dst, lane i of the
+// wavefront taking quad i < min(n, 64) (global_load_lds_dwordx4: each lane's 16 bytes land at
+// dst + 16 i; dst uniform); complete after an s_waitcnt.
+__device__ __forceinline__ void lds_dma_quads(const uint32_t *src, uint32_t *dst, uint32_t n,
+                                              uint32_t lane) {
+  if (lane < n) __builtin_amdgcn_global_load_lds((global_void *)(src + 4 * lane), (lds_void *)dst, 16, 0, 0);
 }
 __device__ __forceinline__ void wait_lds_dma() {
   __builtin_amdgcn_s_waitcnt(0);
@@ -2036,14 +2044,16 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
       S.clk = (uint64_t *)(lds + at);
       at += 4 * kParts;
     }
+    // The seed tables by direct loads into LDS (16 bytes a lane, no registers), waited for with
+    // the first sequence's loads below.
+    // Wave w copies quads 64 w, 64 (w + NW), ... of each table (a copy's LDS base is the wave's).
     const uint32_t *rs = rsqrt_seed_table(), *rc = recip_seed_table();
-    for (uint32_t i = threadIdx.x; i < kRsqrtSeedWords; i += NW * kWave) seed_lds[i] = rs[i];
-    for (uint32_t i = threadIdx.x; i < kRecipSeedWords; i += NW * kWave) seed_lds[kRsqrtSeedWords + i] = rc[i];
+    const uint32_t wl = threadIdx.x % kWave, wv = uniform32(threadIdx.x / kWave);
+    for (uint32_t q = wv * kWave; q < kRsqrtSeedWords / 4; q += NW * kWave)
+      lds_dma_quads(rs + 4 * q, seed_lds + 4 * q, kRsqrtSeedWords / 4 - q, wl);
+    for (uint32_t q = wv * kWave; q < kRecipSeedWords / 4; q += NW * kWave)
+      lds_dma_quads(rc + 4 * q, seed_lds + kRsqrtSeedWords + 4 * q, kRecipSeedWords / 4 - q, wl);
     S.seeds = Seeds(seed_lds, seed_lds + kRsqrtSeedWords);
-    if (NW == 2)
-      pair_sync();
-    else
-      wave_sync();
   }
   // The wave index read as a scalar, so that the compiler treats the role branches as uniform.
   const uint32_t lane = threadIdx.x % kWave, wave = uniform32(threadIdx.x / kWave);
@@ -2093,30 +2103,44 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
     uint8_t *const ce = A.cache ? A.cache + (uint64_t)sl * A.cache_stride : nullptr;
     bool fresh = true;
     uint32_t fp_tag = 0;  // the fingerprint of the state the cached sums were formed beside
+    uint32_t fp_acc = 0;
     if (ce) {
       const SlotCacheLayout cl = slot_cache_layout(M);
       const uint32_t *head = (const uint32_t *)ce;
+      const uint4 h4 = *(const uint4 *)head;
       if (NW == 2) {
         hist = (int64_t *)(ce + cl.sums);
-        fresh = head[0] != pos + 1;
-        fp_tag = head[3];
+        fresh = h4.x != pos + 1;
+        fp_tag = h4.w;
       }
-      if (wave == 0 && head[1] && M.writer_memory) {
-        for (uint32_t i = lane; i < d; i += kWave) S.wq[i] = ((const int32_t *)(ce + cl.query))[i];
-        if (lane < kMaxProbes) S.kept[lane] = ((const uint32_t *)(ce + cl.kept))[lane];
+      if (wave == 0 && h4.y && M.writer_memory) {
+        // The remembered query and kept drawers by direct loads into LDS.
+        for (uint32_t q = 0; q < (d + 3) / 4; q += kWave)
+          lds_dma_quads((const uint32_t *)(ce + cl.query) + 4 * q, (uint32_t *)S.wq + 4 * q,
+                        (d + 3) / 4 - q, lane);
+        lds_dma_quads((const uint32_t *)(ce + cl.kept), S.kept, kMaxProbes / 4, lane);
         if (lane == 0) {
-          S.wmeta[0] = head[2];
+          S.wmeta[0] = h4.z;
           S.wmeta[1] = 1;
         }
       }
     }
-    uint32_t fp_acc = 0;
+    // The session's state: into LDS by direct loads where the state lives in LDS (its
+    // fingerprint is then read back after the prologue's wait), else word by word.
+    constexpr bool kStateLds = !(NW == 2 && kPairStateGlobal<Q, HM>);
+    const bool state_done = kStateLds && keeps_state && A.in_state;
+    if (state_done) {
+      const uint32_t *src = (const uint32_t *)(A.in_state + (uint64_t)sl * L * d);
+      const uint32_t quads = L * d / 2;  // L d i64
+      for (uint32_t q = 0; q < quads; q += kWave)
+        lds_dma_quads(src + 4 * q, (uint32_t *)stb + 4 * q, quads - q, lane);
+    }
     for (uint32_t l = 0; l < L; l++)
 #pragma unroll
       for (int k = 0; k < Q; k++)
         if (qv[k]) {
           uint32_t ch = 4 * qi[k];
-          if (keeps_state)
+          if (keeps_state && !state_done)
 #pragma unroll
             for (int c = 0; c < 4; c++) {
               const uint64_t at = (uint64_t)l * d + ch + c;
@@ -2171,7 +2195,7 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
     }
     // A serving slot's cached sums hold only beside the state they were formed with: a slot
     // whose state the host rewrote at the same position (a restore) sums its window afresh.
-    if (NW == 2 && ce && wave == 0) {
+    if (NW == 2 && ce && wave == 0 && !state_done) {
       const uint32_t fp = wave_reduce32(fp_acc, OpAdd());
       if (lane == 0) S.wmeta[3] = fp;
     }
@@ -2179,6 +2203,21 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
     if constexpr (CLK) {
       for (uint32_t i = lane; i < kParts; i += kWave) clk.acc[i] = 0;
       t_real = __builtin_amdgcn_s_memrealtime();
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the direct loads into LDS (seed tables, memory, state)
+    if (NW == 2 && ce && state_done) {  // wave 0: the loaded state's fingerprint
+      wave_sync();
+      for (uint32_t l = 0; l < L; l++)
+#pragma unroll
+        for (int k = 0; k < Q; k++)
+          if (qv[k])
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+              const uint64_t at = (uint64_t)l * d + 4 * qi[k] + c;
+              fp_acc += state_fp_word(stb[at], (uint32_t)at);
+            }
+      const uint32_t fp = wave_reduce32(fp_acc, OpAdd());
+      if (lane == 0) S.wmeta[3] = fp;
     }
     if (NW == 2)
       pair_sync();
@@ -2376,6 +2415,7 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
       wave_sync();
     }
   }
+  __builtin_amdgcn_s_waitcnt(0);  // no direct load into LDS outlives the block
 }
 
 // The (quaternions per lane, lanes per writer row) pairs widths 32..1024 produce:
