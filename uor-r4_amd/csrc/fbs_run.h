@@ -2113,15 +2113,17 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
         fresh = h4.x != pos + 1;
         fp_tag = h4.w;
       }
-      if (wave == 0 && h4.y && M.writer_memory) {
-        // The remembered query and kept drawers by direct loads into LDS.
+      if (wave == 0 && M.writer_memory) {
+        // The remembered query and kept drawers by direct loads into LDS, issued beside the
+        // head's load rather than after it: a slot without a memory then leaves the block with
+        // none (its last session's is overwritten).
         for (uint32_t q = 0; q < (d + 3) / 4; q += kWave)
           lds_dma_quads((const uint32_t *)(ce + cl.query) + 4 * q, (uint32_t *)S.wq + 4 * q,
                         (d + 3) / 4 - q, lane);
         lds_dma_quads((const uint32_t *)(ce + cl.kept), S.kept, kMaxProbes / 4, lane);
         if (lane == 0) {
           S.wmeta[0] = h4.z;
-          S.wmeta[1] = 1;
+          S.wmeta[1] = h4.y != 0;
         }
       }
     }
