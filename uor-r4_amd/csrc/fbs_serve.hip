@@ -120,12 +120,16 @@ __global__ __launch_bounds__(256) void fbs_serve_finish(DevModel M, ServeScan J)
     for (uint32_t c = threadIdx.x; c < M.D; c += blockDim.x) J.drawer_count[c] = 0;
     if (threadIdx.x == 0) J.item_count[0] = 0;
   }
-  if (i >= J.n || !J.job_flag[i]) return;
-  J.job_flag[i] = 0;
+  if (i >= J.n) return;
+  // The flag, the minimum and the slot loaded together (one wait), then used.
+  const uint32_t flag = J.job_flag[i];
   const uint32_t tok = (uint32_t)J.job_best[i];
+  const uint32_t slot = J.cache ? J.slots[i] : 0u;
+  if (!flag) return;
+  J.job_flag[i] = 0;
   J.out_tokens[(uint64_t)i * (J.gen + 1)] = tok;
   if (J.cache) {
-    uint32_t *head = (uint32_t *)(J.cache + (uint64_t)J.slots[i] * J.cache_stride);
+    uint32_t *head = (uint32_t *)(J.cache + (uint64_t)slot * J.cache_stride);
     head[1] = M.writer_memory;
     head[2] = tok;
   }
