@@ -1919,6 +1919,11 @@ __device__ __forceinline__ int step_window(const DevModel &M, const Lds &S, int3
       for (int c = 0; c < 4; c++) S.gq[ch + c] = gate[c];
     }
     clk.sync(kPartTransition, kPartSync2);  // 2: the window sums and the output gates' quaternions
+    // One-token serving launches (defer): the next step's window sums wait for nothing on the
+    // recurrence wave's path, so this wave yields the issue slots it shares with another
+    // block's recurrence wave until barrier 3 and takes them back for the MLP groups (in decode
+    // launches it keeps the low priority throughout: measured faster there, slower here).
+    if (defer) __builtin_amdgcn_s_setprio(0);
     // The next step's terms over earlier positions: tap 1 on this step's drive, taps
     // split+1..W from the ring (slots next - s, none of them the slot just written), added to
     // taps 2..split.
@@ -1934,6 +1939,7 @@ __device__ __forceinline__ int step_window(const DevModel &M, const Lds &S, int3
       hp[1] = make_longlong2(acc[2], acc[3]);
     }
     clk.sync(kPartTransport, kPartSync3);  // 3: the normed activations
+    if (defer) __builtin_amdgcn_s_setprio(3);  // the MLP groups, on both waves' path
     const uint64_t mbl = pair_mlp(M, S, ly, lane, 1, pg, pu);
     if (lane == 0) S.pair[1] = mbl;
     clk.sync(kPartMlp, kPartSync4);  // 4: both waves' MLP outputs and maxima
@@ -2068,8 +2074,10 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
   if constexpr (CLK) clk.acc = S.clk + wave * kParts;
   // The recurrence wave is the step's critical path (its instructions issue one after another,
   // each waiting for the last), while the ring wave's window sums have slack: the recurrence
-  // wave takes the issue slots first wherever waves on its SIMD compete for them.
-  if (NW == 2 && wave == 0) __builtin_amdgcn_s_setprio(3);
+  // wave takes the issue slots first wherever waves on its SIMD compete for them. In one-token
+  // serving launches the ring wave raises its priority too, but for its next-step window sums
+  // (step_window).
+  if (NW == 2 && (wave == 0 || defer)) __builtin_amdgcn_s_setprio(3);
   const uint32_t d = M.d, L = M.L, W = M.W;
   int32_t *const block_ring = A.ring + (uint64_t)blockIdx.x * L * W * d;
   int64_t *hist = NW == 2 ? A.hist + (uint64_t)blockIdx.x * L * d : nullptr;
