@@ -46,7 +46,7 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 TRAFFIC_SUMMARIES = {
     "c2": "fbs_decode_pair_c2_b1024_traffic.md", "c3": "fbs_decode_pair_c3_b1024_traffic.md",
     "c4": "fbs_rows_pair_c4_r1048576_traffic.md", "c5": "fbs_decode_pair8_c5_b16384_traffic.md",
-    "hamming": "fbs_decode_ham_c3_b1024_traffic.md"}
+    "hamming": "fbs_decode_pair_ham_c3_b1024_traffic.md"}
 D11_TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "d11_score_rows_m1_traffic.md")
 # BASELINE.json's configs at their full shapes: (sequences, prompt, decode steps); c4 is
 # teacher-forced scoring of (rows, row length).
@@ -767,6 +767,7 @@ def hamming_main(a, torch, oracle) -> dict:
     Sw = 1
     while Sw < spec.width // 32:
         Sw *= 2
+    ham_kernel = ("fbs_decode_pair_ham" if model.block_waves(B) == 2 else "fbs_decode_ham") + f"<{Q}, {Sw}>"
     out = {
         "metric": f"decoded tokens/sec at batch {B}, width {spec.width}, with Hamming reads (1 GPU)",
         "value": round(tokens / (ms_per_step / 1e3), 1), "unit": "tokens/s", "n_gpus": 1,
@@ -780,10 +781,10 @@ def hamming_main(a, torch, oracle) -> dict:
                    "vocab": spec.vocab, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(a, f"fbs_decode_ham<{Q}, {Sw}>"),
+                     "traffic": measured_traffic(a, ham_kernel),
                      "bytes_per_token": {k: round(v, 1) for k, v in bpt.items()},
                      "mean_candidate_rows": round(mean_cand, 1),
-                     "kernel": f"fbs_decode_ham<{Q}, {Sw}>",
+                     "kernel": ham_kernel,
                      "launch_ms": [round(x, 3) for x in launch_ms]},
         "prefill_tokens_per_s": round(B * a.prompt / prefill_s, 1),
     }
