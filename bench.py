@@ -78,13 +78,25 @@ def log(msg: str):
 
 
 def cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it, with the family, model and stepping numbers,
+    clock and cache the first processor reports (a VM's model name can be as short as
+    "AMD EPYC")."""
+    info = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if not line.strip():
+                break  # the first processor's block
+            k, _, v = line.partition(":")
+            info[k.strip()] = v.strip()
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = info.get("model name", "unknown")
+    extra = [f"{k} {info[k]}" for k in ("cpu family", "model", "stepping") if k in info]
+    if "cpu MHz" in info:
+        extra.append(f"{float(info['cpu MHz']):.0f} MHz")
+    if "cache size" in info:
+        extra.append(f"cache {info['cache size']}")
+    return f"{name} ({', '.join(extra)})" if extra else name
 
 
 def cpu_threads(a) -> tuple[int, dict]:
