@@ -25,6 +25,9 @@ SHAPES = {
     "c2": replace(synth.CONFIGS["c2"], context=64, layers=3),
     # Width 64 (the 32-word rows) over the reference's 256 cells (t mod 256).
     "w64": synth.Spec(vocab=4096, width=64, mlp=96, layers=2, context=64, kept=8, window=3),
+    # Width 32 (16-word rows, the smallest segment), Zipf drawers some of which are empty.
+    "w32": synth.Spec(vocab=2048, width=32, mlp=64, layers=2, context=64, kept=6, window=4,
+                      drawers=200, probes=6, zipf_drawers=1.3, max_drawer=150),
 }
 
 
@@ -80,7 +83,8 @@ def serve(model, prompts, slots, cap, K, cached, refuse=None):
 
 
 @pytest.mark.parametrize("name,n,cached", [("c3", 1100, True), ("c3", 300, False),
-                                           ("c2", 700, True), ("w64", 90, True)])
+                                           ("c2", 700, True), ("w64", 90, True),
+                                           ("w32", 257, True)])
 def test_drawer_major_serving_equals_the_fused_writer(name, n, cached):
     spec = SHAPES[name]
     art = synth.make_artifact(spec, 4242)
@@ -119,3 +123,32 @@ def test_a_refused_session_leaves_the_others_served():
     np.testing.assert_array_equal(got["status"], ref["status"])
     np.testing.assert_array_equal(got["reply"][ok], ref["reply"][ok])
     np.testing.assert_array_equal(got["state"], ref["state"])
+
+
+def test_job_buffers_grow_and_the_memory_off_equals_the_fused_writer():
+    """One model serving 40 sessions, then 600 (the job buffers grow between launches), then 40
+    again; and a model created with the writer's memory off (every step a job). Each against the
+    fused writer's launches from the same state."""
+    spec = SHAPES["c2"]
+    art = synth.make_artifact(spec, 4244)
+    P, K = 10, 4
+    print("serve scan: job buffers grow; writer memory off", flush=True)
+    deferred, fused = make_model(art, False), make_model(art, True)
+    for n in (40, 600, 40):
+        prompts = synth.uniform_prompts(spec.vocab, n, P, 90 + n)
+        slots = np.arange(n, dtype=np.uint32)[::-1].copy()
+        got = serve(deferred, prompts, slots, n, K, True)
+        ref = serve(fused, prompts, slots, n, K, True)
+        for key in ("reply", "kept", "query", "state", "status"):
+            np.testing.assert_array_equal(got[key], ref[key], err_msg=f"{n} {key}")
+    os.environ["UOR_FBS_WRITER_MEMORY"] = "0"
+    try:
+        no_memory = make_model(art, False)
+    finally:
+        del os.environ["UOR_FBS_WRITER_MEMORY"]
+    prompts = synth.uniform_prompts(spec.vocab, 64, P, 95)
+    slots = np.arange(64, dtype=np.uint32)
+    got = serve(no_memory, prompts, slots, 64, K, True)
+    ref = serve(fused, prompts, slots, 64, K, True)
+    for key in ("reply", "kept", "query", "state", "status"):
+        np.testing.assert_array_equal(got[key], ref[key], err_msg=key)

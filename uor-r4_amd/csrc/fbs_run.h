@@ -99,6 +99,20 @@ __device__ __forceinline__ uint64_t wave_reduce64(uint64_t v, Op op) {
   v = op(v, dpp64<kDppMirror>(v));
   return op(op(lane64(v, 0), lane64(v, 16)), op(lane64(v, 32), lane64(v, 48)));
 }
+// The wave's maximum of m and sum of s together, both returned uniform: each exchange step is
+// applied to both before the next, so one reduction's DPP waits are filled with the other's work.
+__device__ __forceinline__ void wave_max32_add64(uint32_t &m, uint64_t &s) {
+  m = OpMax()(m, dpp32<kDppXor1>(m));
+  s += dpp64<kDppXor1>(s);
+  m = OpMax()(m, dpp32<kDppXor2>(m));
+  s += dpp64<kDppXor2>(s);
+  m = OpMax()(m, dpp32<kDppHalfMirror>(m));
+  s += dpp64<kDppHalfMirror>(s);
+  m = OpMax()(m, dpp32<kDppMirror>(m));
+  s += dpp64<kDppMirror>(s);
+  m = OpMax()(OpMax()(lane32(m, 0), lane32(m, 16)), OpMax()(lane32(m, 32), lane32(m, 48)));
+  s = (lane64(s, 0) + lane64(s, 16)) + (lane64(s, 32) + lane64(s, 48));
+}
 // The bit length of the wave's largest magnitude from each lane's largest: the bit length of a
 // maximum is the maximum of the bit lengths, so a 32-bit reduction takes the place of a 64-bit one.
 __device__ __forceinline__ int32_t wave_bitlen_max(uint64_t v) {
@@ -211,29 +225,40 @@ __device__ __forceinline__ void norm_gain(const DevModel &M, const Seeds &sd,
                                           const int32_t (&x)[Q][4], const bool (&qv)[Q],
                                           const short4 (&gain)[Q], const ushort4 (&gdesc)[Q],
                                           int64_t (&out)[Q][4]) {
+  // The largest magnitude and, beside it, the sum of squares as if the pre-shift were 0 (it is
+  // wherever the largest magnitude is below 2^24, and then every square is below 2^48): both
+  // reductions run interleaved, and only a non-zero pre-shift sums the shifted values again.
   uint32_t mx = 0;
+  uint64_t sum = 0;
 #pragma unroll
   for (int k = 0; k < Q; k++)
     if (qv[k])
 #pragma unroll
       for (int c = 0; c < 4; c++) {
-        uint32_t a = uabs32(x[k][c]);
+        const uint32_t a = uabs32(x[k][c]);
         mx = a > mx ? a : mx;
+        sum += (uint64_t)a * a;  // used only when every a < 2^24
       }
-  mx = wave_reduce32(mx, OpMax());
+  wave_max32_add64(mx, sum);
   int32_t sh = bitlen64(mx) - 24;
   if (sh < 0) sh = 0;
-  uint64_t sum = 0;
 #pragma unroll
   for (int k = 0; k < Q; k++)
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-      int64_t y = qv[k] ? shift((int64_t)x[k][c], sh) : 0;
-      out[k][c] = y;
-      const uint32_t a = (uint32_t)uabs64(y);  // |y| <= 2^24: the shift leaves 24 bits
-      sum += (uint64_t)a * a;
-    }
-  sum = wave_reduce64(sum, OpAdd());
+    for (int c = 0; c < 4; c++) out[k][c] = qv[k] ? (int64_t)x[k][c] : 0;
+  if (sh > 0) {
+    sum = 0;
+#pragma unroll
+    for (int k = 0; k < Q; k++)
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const int64_t y = qv[k] ? shift((int64_t)x[k][c], sh) : 0;
+        out[k][c] = y;
+        const uint32_t a = (uint32_t)uabs64(y);  // |y| <= 2^24: the shift leaves 24 bits
+        sum += (uint64_t)a * a;
+      }
+    sum = wave_reduce64(sum, OpAdd());
+  }
   (void)sd;
   const NormFactor f = M.log2d != 0xffu ? norm_factor_lds(sum, M.log2d, M.eps_int[sh],
                                                           (lds_u32 *)sd.rsq_seed)
