@@ -97,6 +97,33 @@ FBS_HD uint32_t ham_nibble(const int64_t *unit, const int64_t (&p)[4]) {
          (uint32_t)(o[3] >= 0) << 3;
 }
 
+// A load made a global load: the read's tables are reached through pointers read from memory
+// (DevHamRead), which the compiler would otherwise load with flat instructions, and a flat load
+// counts against the LDS counter as well, so every later wait for an LDS read would wait for it.
+// 8- and 16-byte types load as plain integers and vectors (no constructor of a vector type takes
+// a global-space reference).
+template <class T>
+__device__ __forceinline__ T gload(const T *p) {
+  if constexpr (sizeof(T) == 8) {
+    typedef __attribute__((address_space(1))) const unsigned long long *G8;
+    return __builtin_bit_cast(T, *(G8)p);
+  } else if constexpr (sizeof(T) == 16) {
+    typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(1))) const v4u *G16;
+    return __builtin_bit_cast(T, *(G16)p);
+  } else {
+    typedef __attribute__((address_space(1))) const T *GP;
+    return *(GP)p;
+  }
+}
+
+// ham_nibble with the unit's words read by global loads (the read's tables are reached through
+// pointers read from memory, which the compiler would otherwise load as flat).
+__device__ __forceinline__ uint32_t ham_nibble_g(const int64_t *unit, const int64_t (&p)[4]) {
+  const int64_t u[4] = {gload(unit), gload(unit + 1), gload(unit + 2), gload(unit + 3)};
+  return ham_nibble(u, p);
+}
+
 // Head j's code word from the sign nibbles of its hw / 4 quaternions in LDS (uniform).
 __device__ __forceinline__ uint64_t ham_word(const uint32_t *nib, uint32_t j, uint32_t hw) {
   uint64_t word = 0;
@@ -106,7 +133,7 @@ __device__ __forceinline__ uint64_t ham_word(const uint32_t *nib, uint32_t j, ui
 
 __device__ __forceinline__ uint64_t ham_code(const DevHamRead &R, uint32_t heads, uint32_t token,
                                              uint32_t head) {
-  return R.codes[(uint64_t)token * heads + head];
+  return gload(R.codes + (uint64_t)token * heads + head);
 }
 
 // One token's biased table words on the lane's four channels of quaternion q, and their Q12
@@ -459,7 +486,7 @@ __device__ __forceinline__ uint32_t ham_type_part(const DevModel &M, const DevHa
     if (asks) {
       auto asked = [&](uint32_t v, int64_t (&o)[4]) {
         ham_point(M, v, q, o);
-        const short4 a = *(const short4 *)(R.ask + (uint64_t)v * d + 4 * q);
+        const short4 a = gload((const short4 *)(R.ask + (uint64_t)v * d + 4 * q));
         o[0] += a.x;
         o[1] += a.y;
         o[2] += a.z;
@@ -473,17 +500,18 @@ __device__ __forceinline__ uint32_t ham_type_part(const DevModel &M, const DevHa
         const uint32_t reach = R.carry_rows < t ? R.carry_rows : t;
         for (uint32_t s = 1; s <= reach; s++) {
           const uint32_t v = tk[t - s];
-          const int64_t gain = R.carry[v];
+          const int64_t gain = gload(R.carry + v);
           int64_t o[4];
           asked(v, o);
 #pragma unroll
           for (int c = 0; c < 4; c++) p[c] += gain * o[c];
         }
       }
-      S.hnib[q] = ham_nibble(R.ku + 4 * q, p);
+      S.hnib[q] = ham_nibble_g(R.ku + 4 * q, p);
     } else {
       i128 o[4];
-      const int64_t u[4] = {R.vu[4 * q], R.vu[4 * q + 1], R.vu[4 * q + 2], R.vu[4 * q + 3]};
+      const int64_t u[4] = {gload(R.vu + 4 * q), gload(R.vu + 4 * q + 1), gload(R.vu + 4 * q + 2),
+                            gload(R.vu + 4 * q + 3)};
       hamilton64(u, point[k], o);
       if (write_pay) {
         int64_t *dst = pay + (uint64_t)t * d + 4 * q;
@@ -492,7 +520,7 @@ __device__ __forceinline__ uint32_t ham_type_part(const DevModel &M, const DevHa
         *(longlong2 *)(dst + 2) = make_longlong2(clamp_i64(round_shift128(o[2], 31)),
                                                  clamp_i64(round_shift128(o[3], 31)));
       }
-      S.hnib[q] = ham_nibble(R.qu + 4 * q, point[k]);
+      S.hnib[q] = ham_nibble_g(R.qu + 4 * q, point[k]);
     }
   }
   wave_sync();
@@ -635,14 +663,14 @@ __device__ __forceinline__ uint32_t place_find(const DevModel &M, const Lds &S, 
       const uint32_t reach = H.p_carry_rows < t ? H.p_carry_rows : t;
       for (uint32_t s = 1; s <= reach; s++) {
         const uint32_t v = tk[t - s];
-        const int64_t gain = H.p_carry[v];
+        const int64_t gain = gload(H.p_carry + v);
         int64_t o[4];
         asked(v, o);
 #pragma unroll
         for (int c = 0; c < 4; c++) p[c] += gain * o[c];
       }
     }
-    S.hnib[q] = ham_nibble(R.ku + 4 * q, p);
+    S.hnib[q] = ham_nibble_g(R.ku + 4 * q, p);
   }
   wave_sync();
   const uint64_t first = (1ull << (H.hw / 2)) - 1;
