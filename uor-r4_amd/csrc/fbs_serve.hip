@@ -4,9 +4,10 @@
 // A serving launch steps every session by one token (serve_step, RS stack/session.rs:3405): the
 // paired prefill kernel runs the step up to the writer's drawer selection and leaves a job per
 // session (RunArgs::job_flag), and the session that opens a slice of 16 entries of a drawer's
-// list appends that slice's work items. The writer's choice is the lowest (L1, token) over the members of
-// the session's kept drawers (session.rs:4100-4121, twin fbs_core.h:606-623); sessions that
-// keep the same drawer read the same member rows, so the scan here is laid out by drawer: a
+// list appends that slice's work items. The writer's choice is the lowest (L1, token) over the
+// members of the session's kept drawers (session.rs:4100-4121, twin fbs_core.h:606-623);
+// sessions that keep the same drawer read the same member rows, so the scan here is laid out by
+// drawer: a
 // block holds 64 member rows of one drawer in registers, one row a lane, and scores them against
 // the queries of up to 16 sessions that kept the drawer at a time (staged in LDS and read as
 // broadcasts), each (row, session) L1 by packed v_sad_u16 over biased pairs. Each session's
