@@ -362,11 +362,12 @@ int uor_fbs_decode_stream(uor_fbs_handle *handle, const uint32_t *prompts, uint3
  *   selects root 0 there. Rows of steps a slot did not run are left as they were. NULL: no
  *   trace; otherwise the launch runs the one-wavefront kernels.
  * A launch of one token a session (prompt_len 1, gen 0) on a model with a 16-bit table and keyed
- * drawers queues three kernels on `stream`: the step up to the writer's drawer selection, a scan
- * of every kept drawer's members laid out by drawer over all the launch's sessions, and the
- * hand-out of each session's token (results those of the writer inside the step; the environment
- * variable UOR_FBS_SERVE_SCAN=fused at model creation keeps the writer in the step). Its job
- * buffers are the handle's, allocated on the first such launch of that many sessions.
+ * drawers of skewed sizes (the largest more than twice the mean) queues three kernels on
+ * `stream`: the step up to the writer's drawer selection, a scan of every kept drawer's members
+ * laid out by drawer over all the launch's sessions, and the hand-out of each session's token
+ * (results those of the writer inside the step; the environment variable UOR_FBS_SERVE_SCAN=fused
+ * or =drawer at model creation keeps the writer in the step or takes the scan whatever the sizes).
+ * Its job buffers are the handle's, allocated on the first such launch of that many sessions.
  * No counterpart beyond those: the reference's sessions keep their window sums implicitly (a CPU
  * session steps one token at a time). Device buffers. */
 uint64_t uor_fbs_slot_cache_bytes(const uor_fbs_handle *handle);

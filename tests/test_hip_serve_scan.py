@@ -2,7 +2,8 @@
 writer's drawer selection, a scan laid out by drawer scores every kept drawer's members against
 the queries of every session that kept it, and each session takes the lowest (L1, token),
 session.rs:4100-4121) against the writer inside the step (a model created with
-UOR_FBS_SERVE_SCAN=fused) and the batched decode: tokens, kept drawers, queries, states, window
+UOR_FBS_SERVE_SCAN=fused; the drawer-major models are created with =drawer, which takes the scan
+whatever the drawers' sizes) and the batched decode: tokens, kept drawers, queries, states, window
 rings, positions and statuses equal, at Zipf drawer sizes (several 64-member chunks a drawer,
 several 16-session slices), at more sessions than resident blocks, with permuted slots, with and
 without the slot cache, and with a refused session in a launch."""
@@ -32,8 +33,9 @@ SHAPES = {
 
 
 def make_model(art, fused: bool):
-    if fused:
-        os.environ["UOR_FBS_SERVE_SCAN"] = "fused"
+    """A model whose one-token launches take the drawer-major scan (whatever its drawers' sizes)
+    or keep the writer in the step."""
+    os.environ["UOR_FBS_SERVE_SCAN"] = "fused" if fused else "drawer"
     try:
         return hip.Model(art)
     finally:
@@ -152,3 +154,19 @@ def test_job_buffers_grow_and_the_memory_off_equals_the_fused_writer():
     ref = serve(fused, prompts, slots, 64, K, True)
     for key in ("reply", "kept", "query", "state", "status"):
         np.testing.assert_array_equal(got[key], ref[key], err_msg=key)
+
+
+def test_the_default_takes_the_scan_where_drawer_sizes_are_skewed():
+    """Without the environment switch the drawers' sizes choose: C3's Zipf drawers (largest 512
+    against a mean of 128) take the drawer-major scan, C2's uniform ones keep the writer in the
+    step; either way a serving launch equals the batched decode."""
+    for name in ("c3", "c2"):
+        spec = SHAPES[name]
+        art = synth.make_artifact(spec, 4245)
+        n, P, K = 64, 8, 3
+        prompts = (synth.zipf_prompts(spec.vocab, n, P, 79) if spec.zipf_drawers
+                   else synth.uniform_prompts(spec.vocab, n, P, 79))
+        model = hip.Model(art)
+        got = serve(model, prompts, np.arange(n, dtype=np.uint32), n, K, True)
+        want = model.decode(prompts, gen=K, want_state=False)["reply"]
+        np.testing.assert_array_equal(got["reply"], want, err_msg=name)

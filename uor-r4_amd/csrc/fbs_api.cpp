@@ -108,8 +108,10 @@ struct uor_fbs_handle {
   unsigned char *scratch = nullptr;
   // The deferred writer of one-token serving launches (fbs_serve.hip): the drawers' chunks of 64
   // members (all, and the most of one drawer), and the job buffers for `jobs_cap` sequences
-  // (grown, never shrunk). UOR_FBS_SERVE_SCAN=fused at model creation keeps the writer in the
-  // step.
+  // (grown, never shrunk). Taken where the drawers' sizes are skewed (the largest more than
+  // twice the mean), where a launch with the writer in the step waits for its sessions with the
+  // largest drawers; UOR_FBS_SERVE_SCAN=drawer or =fused at model creation takes or refuses it
+  // whatever the sizes.
   bool serve_drawer_major = true;
   uint32_t serve_nchunks = 0, serve_max_chunks = 0;
   uint32_t jobs_cap = 0, item_cap = 0;
@@ -658,10 +660,13 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
   // every step then scans its candidates; the results are the same either way).
   const char *wm = getenv("UOR_FBS_WRITER_MEMORY");
   M.writer_memory = (wm && wm[0] == '0' && !wm[1]) ? 0u : 1u;
-  // UOR_FBS_SERVE_SCAN=fused keeps the writer inside one-token serving launches (for
-  // measurement: the drawer-major scan is the default; the results are the same either way).
+  // UOR_FBS_SERVE_SCAN=fused keeps the writer inside one-token serving launches, =drawer takes
+  // the drawer-major scan; otherwise the drawers' sizes choose (below). The results are the same
+  // either way.
   const char *ss = getenv("UOR_FBS_SERVE_SCAN");
-  h->serve_drawer_major = !(ss && std::strcmp(ss, "fused") == 0);
+  const int serve_mode = ss && std::strcmp(ss, "fused") == 0    ? 2
+                         : ss && std::strcmp(ss, "drawer") == 0 ? 1
+                                                                 : 0;
   M.w_recip = (1ull << 32) / M.W;
   int64_t eps_int[9];
   for (int sh = 0; sh <= 8; sh++) eps_int[sh] = norm_eps(m->eps_mantissa, m->eps_exp, sh);
@@ -796,12 +801,19 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
     if (mem.empty()) mem.push_back(0);
     if ((st = h->upload(off.data(), off.size(), &M.offsets))) return done(st);
     if ((st = h->upload(mem.data(), mem.size(), &M.members))) return done(st);
-    // The deferred writer's scan chunks: each drawer's members, 64 at a time.
+    // The deferred writer's scan chunks: each drawer's members, 64 at a time; and whether the
+    // drawers' sizes are skewed enough for it (measured: C3's Zipf drawers, largest 512 against
+    // a mean of 128, 0.105 against 0.159 ms a serving launch; C2's uniform ones 0.095-0.115
+    // against 0.075-0.083 ms).
+    uint32_t largest = 0;
     for (uint32_t c = 0; c < r.D; c++) {
-      const uint32_t nch = (off[c + 1] - off[c] + kServeRows - 1) / kServeRows;
+      const uint32_t size = off[c + 1] - off[c], nch = (size + kServeRows - 1) / kServeRows;
       h->serve_nchunks += nch;
       h->serve_max_chunks = nch > h->serve_max_chunks ? nch : h->serve_max_chunks;
+      largest = size > largest ? size : largest;
     }
+    const bool skewed = (uint64_t)largest * r.D > 2ull * off[r.D];
+    h->serve_drawer_major = serve_mode == 1 || (serve_mode == 0 && skewed);
   }
   if ((st = h->upload(m->icosian, 120 * 8, &M.icosian))) return done(st);
   if ((st = h->upload(m->keep_q31, 16, &M.keep_q31))) return done(st);
