@@ -1128,16 +1128,16 @@ def main():
             return wall_, [ev[0].elapsed_time(ev[1]) / K], same_
 
         # The library takes the drawer-major scan for one-token launches where the drawers'
-        # sizes are skewed (the largest more than twice the mean) on a 16-bit table.
+        # sizes are skewed (the largest more than twice the mean).
         sizes_ = art.drawer_sizes()
-        drawer_major = (model.block_waves(B) == 2 and spec.table == "i16"
+        drawer_major = (model.block_waves(B) == 2
                         and int(sizes_.max()) * len(sizes_) > 2 * int(sizes_.sum()))
         bare_wall, bare_ms, bare_same = serve_loop(False)
         serve_wall, serve_ms, same_serve = serve_loop(True)
         # The same launches on the path the library did not choose (UOR_FBS_SERVE_SCAN at model
         # creation: the writer inside the step, or the drawer-major scan), for comparison.
         other = None
-        if model.block_waves(B) == 2 and spec.table == "i16":
+        if model.block_waves(B) == 2:
             os.environ["UOR_FBS_SERVE_SCAN"] = "fused" if drawer_major else "drawer"
             try:
                 model_o = hip.Model(art, device=0)

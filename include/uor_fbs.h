@@ -361,8 +361,8 @@ int uor_fbs_decode_stream(uor_fbs_handle *handle, const uint32_t *prompts, uint3
  *   transition roots (stack_lanes, session.rs:5097-5150); a zero raw quaternion, 255 here,
  *   selects root 0 there. Rows of steps a slot did not run are left as they were. NULL: no
  *   trace; otherwise the launch runs the one-wavefront kernels.
- * A launch of one token a session (prompt_len 1, gen 0) on a model with a 16-bit table and keyed
- * drawers of skewed sizes (the largest more than twice the mean) queues three kernels on
+ * A launch of one token a session (prompt_len 1, gen 0) on a model with keyed drawers of skewed
+ * sizes (the largest more than twice the mean) queues three kernels on
  * `stream`: the step up to the writer's drawer selection, a scan of every kept drawer's members
  * laid out by drawer over all the launch's sessions, and the hand-out of each session's token
  * (results those of the writer inside the step; the environment variable UOR_FBS_SERVE_SCAN=fused

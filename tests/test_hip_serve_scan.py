@@ -6,7 +6,7 @@ UOR_FBS_SERVE_SCAN=fused; the drawer-major models are created with =drawer, whic
 whatever the drawers' sizes) and the batched decode: tokens, kept drawers, queries, states, window
 rings, positions and statuses equal, at Zipf drawer sizes (several 64-member chunks a drawer,
 several 16-session slices), at more sessions than resident blocks, with permuted slots, with and
-without the slot cache, and with a refused session in a launch."""
+without the slot cache, with int8 tables, and with a refused session in a launch."""
 
 import os
 from dataclasses import replace
@@ -26,9 +26,14 @@ SHAPES = {
     "c2": replace(synth.CONFIGS["c2"], context=64, layers=3),
     # Width 64 (the 32-word rows) over the reference's 256 cells (t mod 256).
     "w64": synth.Spec(vocab=4096, width=64, mlp=96, layers=2, context=64, kept=8, window=3),
-    # Width 32 (16-word rows, the smallest segment), Zipf drawers some of which are empty.
+    # Width 32 (16-word rows, the smallest segment) over Zipf drawers.
     "w32": synth.Spec(vocab=2048, width=32, mlp=64, layers=2, context=64, kept=6, window=4,
                       drawers=200, probes=6, zipf_drawers=1.3, max_drawer=150),
+    # C5's int8 codes (two quaternions a lane, 1,024 Zipf drawers of up to 1,024 probing 16).
+    "c5": replace(synth.CONFIGS["c5"], context=64, layers=2),
+    # An int8 table at one quaternion a lane.
+    "w128i8": synth.Spec(vocab=8192, width=128, mlp=192, layers=2, context=64, kept=8, window=8,
+                         drawers=128, probes=8, zipf_drawers=1.1, max_drawer=400, table="i8"),
 }
 
 
@@ -86,7 +91,8 @@ def serve(model, prompts, slots, cap, K, cached, refuse=None):
 
 @pytest.mark.parametrize("name,n,cached", [("c3", 1100, True), ("c3", 300, False),
                                            ("c2", 700, True), ("w64", 90, True),
-                                           ("w32", 257, True)])
+                                           ("w32", 257, True), ("c5", 400, True),
+                                           ("w128i8", 500, False)])
 def test_drawer_major_serving_equals_the_fused_writer(name, n, cached):
     spec = SHAPES[name]
     art = synth.make_artifact(spec, 4242)

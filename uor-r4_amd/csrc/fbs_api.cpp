@@ -1359,9 +1359,10 @@ extern "C" int uor_fbs_serve_slots_async(uor_fbs_handle *h, const uint32_t *slot
   A.cache_stride = slot_cache_layout(h->M).bytes;
   A.slide = slide;
   A.out_trace = out_trace;
-  // One token a session on the paired kernels of a 16-bit table with keyed drawers: the step
-  // stops at the drawer selection and the drawer-major scan (fbs_serve.hip) chooses the tokens.
-  const bool deferred = h->serve_drawer_major && h->pair && !h->M.ham.heads && !h->M.table8 &&
+  // One token a session on the paired kernels with keyed drawers (of skewed sizes, or as the
+  // environment asked at model creation): the step stops at the drawer selection and the
+  // drawer-major scan (fbs_serve.hip) chooses the tokens.
+  const bool deferred = h->serve_drawer_major && h->pair && !h->M.ham.heads &&
                         h->M.head != 1 && h->M.d % 32 == 0 && prompt_len == 1 && gen == 0 &&
                         !out_trace && sequences > 0 &&
                         (uint64_t)h->M.D * sequences < (1ull << 32);  // drawer-list indices

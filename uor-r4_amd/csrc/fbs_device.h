@@ -251,10 +251,11 @@ struct RunArgs {
   const uint8_t *force_buckets;
   const uint64_t *force_codes;
   const uint8_t *force_mask;
-  // The deferred writer (one-token serving launches of the paired prefill kernels, i16 table,
-  // keyed drawers; null job_flag: the writer runs in the step). A step that does not take the
+  // The deferred writer (one-token serving launches of the paired prefill kernels, keyed
+  // drawers; null job_flag: the writer runs in the step). A step that does not take the
   // writer's remembered result ends at its drawer selection: sequence s's query goes to
-  // job_query (d / 2 words of biased 16-bit pairs), each kept drawer c lists s in
+  // job_query (d / 2 words of 16-bit pairs as the writer's scan packs them for the table),
+  // each kept drawer c lists s in
   // drawer_list[c][.] (drawer_count[c] entries, list_stride a drawer), job_best[s] starts at
   // the largest (L1, token) and job_flag[s] at 1. The session that opens a slice of 16 entries
   // of c's list appends the slice's work items, one per 64 members of c (ServeScan::items).

@@ -2090,9 +2090,9 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
   const uint32_t lane = threadIdx.x % kWave, wave = uniform32(threadIdx.x / kWave);
   // Paired blocks: wave 0 keeps the recurrence state, wave 1 the window ring.
   const bool keeps_state = NW == 1 || wave == 0, keeps_ring = NW == 1 || wave == 1;
-  // The deferred writer (RunArgs::job_flag): compiled into the paired prefill kernels of a
-  // 16-bit table only, the one-token serving launches' family.
-  constexpr bool kDefer = PH == kPhasePrefill && NW == 2 && !HM && !T8 && !CLK && !DT;
+  // The deferred writer (RunArgs::job_flag): compiled into the paired prefill kernels, the
+  // one-token serving launches' family.
+  constexpr bool kDefer = PH == kPhasePrefill && NW == 2 && !HM && !CLK && !DT;
   const bool defer = kDefer && A.job_flag != nullptr;
   const bool writes_out = wave == 0 && lane == 0;
   PartClock<CLK> clk;
@@ -2338,9 +2338,21 @@ __device__ __forceinline__ void run(const DevModel &M, const RunArgs &A) {
               for (int k = 0; k < Q; k++)
                 if (qv[k]) {
                   const int4 q = *(const int4 *)(S.xbar + 4 * qi[k]);
-                  *(uint2 *)(jq + 2 * qi[k]) =
-                      make_uint2((uint32_t)(q.x + 32768) | ((uint32_t)(q.y + 32768) << 16),
-                                 (uint32_t)(q.z + 32768) | ((uint32_t)(q.w + 32768) << 16));
+                  // As scan_setup packs it: biased 16-bit pairs, or for an int8 table the query
+                  // clamped to the table's range and scaled to meet its widened codes.
+                  uint32_t b[4];
+                  const int32_t qa[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+                  for (int c = 0; c < 4; c++) {
+                    if (T8) {
+                      const int32_t lo = -(128 << M.t8_shift), hi = 127 << M.t8_shift;
+                      const int32_t x = qa[c] < lo ? lo : qa[c] > hi ? hi : qa[c];
+                      b[c] = (uint32_t)(x - lo) << (8 - M.t8_shift);
+                    } else {
+                      b[c] = (uint32_t)(qa[c] + 32768);
+                    }
+                  }
+                  *(uint2 *)(jq + 2 * qi[k]) = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
                 }
               if (lane < M.P) {
                 const uint32_t c = S.kept[lane];

@@ -28,7 +28,9 @@ namespace fbs {
 // words (biased 16-bit pairs) a lane holds at once; rows of more words are scored in segments of
 // RW, the sessions' sums carried across. (Query words read as scalars straight from memory
 // measured slower: each scalar load's wait lands on the sums' path.)
-template <int RW>
+// T8: an int8 table, whose rows (code + 128 bytes) widen at the SADs as the fused writer's scan
+// widens them (widen8), against queries published in that scan's scaled form.
+template <int RW, bool T8>
 __global__ __launch_bounds__(64) void fbs_serve_scan(DevModel M, ServeScan J) {
   __shared__ __align__(16) uint32_t qs[kServeSessions * RW];
   const uint32_t lane = threadIdx.x;
@@ -46,7 +48,8 @@ __global__ __launch_bounds__(64) void fbs_serve_scan(DevModel M, ServeScan J) {
     const uint32_t ns = nc - g < kServeSessions ? nc - g : kServeSessions;
     const bool valid = lane < rows;
     const uint32_t tok = valid ? M.members[beg + lane] : 0u;
-    const uint4 *row = (const uint4 *)((const uint32_t *)M.table_b + (uint64_t)tok * words);
+    const uint4 *row = T8 ? (const uint4 *)(M.table8 + (uint64_t)tok * M.d)
+                          : (const uint4 *)((const uint32_t *)M.table_b + (uint64_t)tok * words);
     const uint32_t *list = J.drawer_list + lbeg;
     uint32_t sid[kServeSessions];
 #pragma unroll
@@ -75,26 +78,54 @@ __global__ __launch_bounds__(64) void fbs_serve_scan(DevModel M, ServeScan J) {
               (global_void *)(J.job_query + (uint64_t)stage_sid[j] * words + seg +
                               4 * (lane % (RW / 4))),
               (lds_void *)(qs + 4 * kWave * j), 16, 0, 0);
-      uint4 r[RW / 4];
+      // The row's quads of this segment: RW / 4 of biased 16-bit pairs, or RW / 8 of int8 codes.
+      constexpr uint32_t kRowQuads = T8 ? RW / 8 : RW / 4;
+      uint4 r[kRowQuads];
 #pragma unroll
-      for (uint32_t w = 0; w < RW / 4; w++) r[w] = row[seg / 4 + w];
+      for (uint32_t w = 0; w < kRowQuads; w++) r[w] = row[(T8 ? seg / 8 : seg / 4) + w];
       wait_lds_dma();
       // Four sessions at a time (four independent sums in flight), as many groups as the slice
       // fills; a group's sessions past ns read words never staged and are not used.
 #pragma unroll
       for (uint32_t i0 = 0; i0 < kServeSessions; i0 += 4) {
         if (i0 < ns) {
+          if constexpr (T8) {
 #pragma unroll
-          for (uint32_t w = 0; w < RW / 4; w++) {
+            for (uint32_t w = 0; w < kRowQuads; w++) {
+              uint32_t wd[8];  // the quad's 16 codes as eight widened words
+              widen8(r[w].x, wd[0], wd[1]);
+              widen8(r[w].y, wd[2], wd[3]);
+              widen8(r[w].z, wd[4], wd[5]);
+              widen8(r[w].w, wd[6], wd[7]);
 #pragma unroll
-            for (uint32_t i = i0; i < i0 + 4; i++) {
-              const uint4 q = *(const uint4 *)(qs + i * RW + 4 * w);
-              uint32_t a = acc[i];
-              a = sad2_u16(q.x, r[w].x, a);
-              a = sad2_u16(q.y, r[w].y, a);
-              a = sad2_u16(q.z, r[w].z, a);
-              a = sad2_u16(q.w, r[w].w, a);
-              acc[i] = a;
+              for (uint32_t i = i0; i < i0 + 4; i++) {
+                const uint4 qa = *(const uint4 *)(qs + i * RW + 8 * w);
+                const uint4 qb = *(const uint4 *)(qs + i * RW + 8 * w + 4);
+                uint32_t a = acc[i];
+                a = sad2_u16(qa.x, wd[0], a);
+                a = sad2_u16(qa.y, wd[1], a);
+                a = sad2_u16(qa.z, wd[2], a);
+                a = sad2_u16(qa.w, wd[3], a);
+                a = sad2_u16(qb.x, wd[4], a);
+                a = sad2_u16(qb.y, wd[5], a);
+                a = sad2_u16(qb.z, wd[6], a);
+                a = sad2_u16(qb.w, wd[7], a);
+                acc[i] = a;
+              }
+            }
+          } else {
+#pragma unroll
+            for (uint32_t w = 0; w < kRowQuads; w++) {
+#pragma unroll
+              for (uint32_t i = i0; i < i0 + 4; i++) {
+                const uint4 q = *(const uint4 *)(qs + i * RW + 4 * w);
+                uint32_t a = acc[i];
+                a = sad2_u16(q.x, r[w].x, a);
+                a = sad2_u16(q.y, r[w].y, a);
+                a = sad2_u16(q.z, r[w].z, a);
+                a = sad2_u16(q.w, r[w].w, a);
+                acc[i] = a;
+              }
             }
           }
         }
@@ -151,9 +182,13 @@ hipError_t launch_fbs_serve_scan(const DevModel &M, const ServeScan &J, uint32_t
   DevModel m = M;
   ServeScan j = J;
   void *args[] = {&m, &j};
-  const void *f = words % 64 == 0   ? (const void *)fbs_serve_scan<64>
-                  : words % 32 == 0 ? (const void *)fbs_serve_scan<32>
-                                    : (const void *)fbs_serve_scan<16>;
+  const bool t8 = M.table8 != nullptr;
+  const void *f = words % 64 == 0   ? (t8 ? (const void *)fbs_serve_scan<64, true>
+                                          : (const void *)fbs_serve_scan<64, false>)
+                  : words % 32 == 0 ? (t8 ? (const void *)fbs_serve_scan<32, true>
+                                          : (const void *)fbs_serve_scan<32, false>)
+                                    : (t8 ? (const void *)fbs_serve_scan<16, true>
+                                          : (const void *)fbs_serve_scan<16, false>);
   hipError_t e = hipLaunchKernel(f, dim3(blocks), dim3(kWave), args, 0, stream);
   if (e == hipSuccess) e = hipGetLastError();
   if (e != hipSuccess) return e;
