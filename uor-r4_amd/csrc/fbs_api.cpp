@@ -818,6 +818,7 @@ extern "C" int uor_fbs_model_create(const uor_fbs_model *m, const uor_fbs_ext *e
   if ((st = h->upload(m->icosian, 120 * 8, &M.icosian))) return done(st);
   if ((st = h->upload(m->keep_q31, 16, &M.keep_q31))) return done(st);
   if ((st = h->upload(eps_int, 9, &M.eps_int))) return done(st);
+  M.eps0 = eps_int[0];
 
   if (e && e->hamming && (st = upload_hamming(h, m, *e, *e->hamming))) return done(st);
 

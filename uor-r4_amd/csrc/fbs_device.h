@@ -126,6 +126,9 @@ struct DevModel {
   // Member ids the one-wavefront writer stages in LDS per scan segment: kListCap, or half of it
   // for a model with Hamming reads, so that four of their blocks share a CU's LDS at C3's shape.
   uint32_t list_cap;
+  // eps_int[0] as a kernel argument: the pre-shift is 0 for almost every norm, whose epsilon is
+  // then read from the argument segment instead of by a global load on the step's serial path.
+  int64_t eps0;
 };
 
 // LDS bytes per block (the layout the kernels carve): the gather crossbar, the MLP outputs, the

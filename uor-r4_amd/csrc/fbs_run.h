@@ -259,10 +259,9 @@ __device__ __forceinline__ void norm_gain(const DevModel &M, const Seeds &sd,
       }
     sum = wave_reduce64(sum, OpAdd());
   }
-  (void)sd;
-  const NormFactor f = M.log2d != 0xffu ? norm_factor_lds(sum, M.log2d, M.eps_int[sh],
-                                                          (lds_u32 *)sd.rsq_seed)
-                                         : norm_factor_slow(sum, M.d, M.eps_int[sh]);
+  const int64_t eps = sh == 0 ? M.eps0 : M.eps_int[sh];
+  const NormFactor f = M.log2d != 0xffu ? norm_factor_lds(sum, M.log2d, eps, (lds_u32 *)sd.rsq_seed)
+                                         : norm_factor_slow(sum, M.d, eps);
   if (!f.huge && M.gains_fast) {
     // The common case, one uniform branch: r < 2^62 and |y| <= 2^24 keep every normed value
     // below 2^48 in magnitude, where each gain's descriptor form is exact.
@@ -1364,6 +1363,19 @@ __device__ __forceinline__ void pair_requant(const DevModel &M, const Lds &S, ui
   }
 }
 
+// MLP group j's gather words (gate and up) for this lane, nothing past the last group; read by
+// global loads, which the LDS waits before their use do not wait for (a flat load's would).
+__device__ __forceinline__ void pair_mlp_words(const DevModel &M, const DevLayer &ly, uint32_t lane,
+                                               uint32_t j, uint32_t (&pg)[4], uint32_t (&pu)[4]) {
+  if (j < M.mpl) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      pg[c] = gload(ly.prog + (M.s_mlp_gate + 4 * j + c) * kWave + lane);
+      pu[c] = gload(ly.prog + (M.s_mlp_up + 4 * j + c) * kWave + lane);
+    }
+  }
+}
+
 // MLP quaternion groups j0, j0 + 2, ... of the feed-forward gate (session.rs:4005-4025) into
 // S.mlp_out; pg/pu hold group j0's gather words. Returns the bit length of the groups' largest
 // magnitude.
@@ -1380,13 +1392,7 @@ __device__ __forceinline__ uint64_t pair_mlp(const DevModel &M, const Lds &S, co
       gq[c] = S.xbar[pg[c]];
       up[c] = S.xbar[pu[c]];
     }
-    if (j + 2 < M.mpl) {
-#pragma unroll
-      for (int c = 0; c < 4; c++) {
-        pg[c] = prog_word(ly.prog, M.s_mlp_gate + 4 * (j + 2) + c, lane);
-        pu[c] = prog_word(ly.prog, M.s_mlp_up + 4 * (j + 2) + c, lane);
-      }
-    }
+    pair_mlp_words(M, ly, lane, j + 2, pg, pu);  // the next group's (none past the last)
     if (mq < M.nm) {
       int64_t mo[4];
       mlp_gate(M, S.seeds, gq, up, mo);
@@ -1401,16 +1407,6 @@ __device__ __forceinline__ uint64_t pair_mlp(const DevModel &M, const Lds &S, co
   return (uint64_t)wave_bitlen_max(mmx);
 }
 
-__device__ __forceinline__ void pair_mlp_words(const DevModel &M, const DevLayer &ly, uint32_t lane,
-                                               uint32_t j, uint32_t (&pg)[4], uint32_t (&pu)[4]) {
-  if (j < M.mpl) {
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-      pg[c] = prog_word(ly.prog, M.s_mlp_gate + 4 * j + c, lane);
-      pu[c] = prog_word(ly.prog, M.s_mlp_up + 4 * j + c, lane);
-    }
-  }
-}
 
 // The writer on both waves, after barrier 6 (the query is in the crossbar, wmeta[2] says whether
 // the step reuses the last result): wave 0 selects the drawers, each wave scans half of the
@@ -1683,6 +1679,11 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
         }
     }
     clk.lap(kPartTransport);
+    // The feed-forward block's gather words, loaded a phase ahead: the norm's factor is a call,
+    // whose entry waits for every load in flight, so loads issued just before it are waited for
+    // whole (global loads, so that the LDS waits in between do not wait for them).
+    uint32_t pg[4], pu[4];
+    pair_mlp_words(M, ly, lane, 0, pg, pu);
     // quantize16 over the d outputs (kernels.rs:545-553), then gather16 of rec_out.
     int32_t qs = wave_bitlen_max(mx) - 15;
     if (qs < 0) qs = 0;
@@ -1705,8 +1706,6 @@ __device__ __forceinline__ int step_main(const DevModel &M, const Lds &S, uint32
     clk.lap(kPartResidualRec);
     // ---- feed-forward block: wave 0 takes the even quaternion groups.
     if constexpr (Q != 1) load_ffn();
-    uint32_t pg[4], pu[4];
-    pair_mlp_words(M, ly, lane, 0, pg, pu);
     norm_gain<Q>(M, S.seeds, x, qv, g_mlp, gd_mlp, v);
     publish64<Q>(S.xbar, v, qv, qi);
     clk.sync(kPartNormMlp, kPartSync3);  // 3: the normed activations
