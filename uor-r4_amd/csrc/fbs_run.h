@@ -1876,12 +1876,12 @@ __device__ __forceinline__ int step_window(const DevModel &M, const Lds &S, int3
   if (tok >= M.vocab) return 1;
   const uint32_t d = M.d, W = M.W;
   const uint32_t next = base + 1 == W ? 0 : base + 1;  // the next step's ring slot
-  // Windows of 16 rows or more: the next step's taps 2..split (about a quarter) are summed
-  // before barrier 1, where this wave waits for the norm, and taps split+1..W after barrier 2
-  // (none of their ring rows is the one this step writes); shorter windows sum every tap after
-  // barrier 2. (W = 32: taps 2..8 first; a half first, or 3/8, measured slower. W = 16: taps
-  // 2..4 first measured 1.7 % faster than all after barrier 2, and taps 2..6 slower in serving.)
-  const uint32_t split = W >= 16 ? 1 + (W - 1) / 4 : 1;
+  // Windows of 16 rows or more: the next step's taps 2..split are summed before barrier 1, where
+  // this wave waits for the norm, and taps split+1..W after barrier 2 (none of their ring rows is
+  // the one this step writes); shorter windows sum every tap after barrier 2. Measured: W = 32,
+  // taps 2..16 first 2.9 % faster than 2..8 (2..12, 2..20 and 2..24 no better); W = 16, taps
+  // 2..4 first 1.7 % faster than none (2..6 slower in one-token serving launches).
+  const uint32_t split = W > 16 ? 1 + (W - 1) / 2 : W == 16 ? 1 + (W - 1) / 4 : 1;
   for (uint32_t l = 0; l < M.L; l++) {
     const DevLayer ly = M.layers[l];
     int32_t *ring_l = ring + (uint64_t)l * W * d;
